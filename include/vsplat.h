@@ -1,0 +1,226 @@
+/*
+ * vsplat.h -- C ABI of the MI355X (gfx950) Gaussian-splat rasterizer.
+ *
+ * This is the drop-in boundary for the reference's render / sort / scan call
+ * surface (voyager-so/vauss).  Every entry point names the reference
+ * interface it replaces.  Paths are relative to the reference repository.
+ *
+ * Conventions
+ *  - All array arguments are device pointers (HIP global memory) unless the
+ *    comment says "host".  Inputs are contiguous, row-major, fp32/u32.
+ *  - Outputs are caller-owned; intermediate state is library-owned and lives
+ *    in a `vs_fwd_state` until vs_fwd_state_free().
+ *  - Work is enqueued on the context's HIP stream.  Calls that must learn a
+ *    device-side count before sizing a buffer (the forward render after
+ *    projection) synchronise that stream once; everything else is
+ *    stream-ordered and returns without waiting.
+ *  - No C++ exception crosses this boundary.  Every call returns a
+ *    vs_status; vs_last_error() gives a human-readable message for the
+ *    calling thread.
+ *  - One context per host thread.  Contexts are independent.
+ */
+#ifndef VSPLAT_H
+#define VSPLAT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum vs_status {
+    VS_OK = 0,
+    VS_ERR_INVALID = 1,      /* bad argument (shape, size, null pointer, mode) */
+    VS_ERR_HIP = 2,          /* a HIP runtime call failed */
+    VS_ERR_OOM = 3,          /* device allocation failed */
+    VS_ERR_UNSUPPORTED = 4,  /* a mode the reference has that is not built here */
+    VS_ERR_CAPACITY = 5,     /* intersection count exceeds the u32 limit or the cap */
+    VS_ERR_NONFINITE = 6,    /* validation found NaN/Inf in an input */
+} vs_status;
+
+typedef struct vs_ctx vs_ctx;
+typedef struct vs_fwd_state vs_fwd_state;
+
+/* Camera models: crates/splat-train-render/src/kernels/camera_model/mod.rs:30-37
+ * (Pinhole and KannalaBrandt4; the RT8 and thin-prism models return
+ * VS_ERR_UNSUPPORTED). */
+typedef enum vs_camera_model { VS_CAMERA_PINHOLE = 0, VS_CAMERA_KB4 = 1 } vs_camera_model;
+
+/* Device-side projection uniforms, the fields of ProjectUniforms
+ * (crates/splat-train-render/src/kernels/types.rs:53-82) other than sizes.
+ * Built on the host by vs_camera_uniforms() exactly as render.rs:478-503
+ * builds them, or filled by the caller. */
+typedef struct vs_camera {
+    int32_t model;                  /* vs_camera_model */
+    float fx, fy, cx, cy;           /* PinholeParams */
+    float kb4[4];                   /* KannalaBrandt4Params k1..k4 */
+    float viewmat[12];              /* world->camera 3x4, column-major (col0,col1,col2,translation) */
+    float cam_pos[3];               /* view-direction origin for SH */
+    float half_max_render_fov;      /* fisheye angular cull */
+    float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y, lim_r; /* JacobianClampLimits */
+} vs_camera;
+
+/* Host camera description, crates/splat-train-render/src/camera.rs:11-23. */
+typedef struct vs_pose {
+    double fov_x, fov_y;            /* radians */
+    float center_uv[2];             /* principal point as a fraction of the image */
+    float position[3];              /* camera centre, world */
+    float rotation[4];              /* camera-to-world rotation quaternion, (x, y, z, w) */
+    int32_t model;                  /* vs_camera_model */
+    float kb4[4];
+} vs_pose;
+
+/* Parameters of N splats, crates/splat-train-render/src/gaussian_splats.rs:127-153. */
+typedef struct vs_splats {
+    const float* transforms;        /* [N,10]: mean xyz, quat w x y z, log-scale xyz */
+    const float* sh_coeffs;         /* [N,(d+1)^2,3] */
+    const float* raw_opacities;     /* [N] logits */
+    uint32_t num_splats;
+    uint32_t sh_degree;             /* 0..4 */
+    float log_scale_offset;         /* added to every log-scale (render.rs:325) */
+} vs_splats;
+
+/* RasterPass, crates/splat-train-render/src/gaussian_splats.rs:32-107. */
+typedef enum vs_pass {
+    VS_PASS_FORWARD = 0,            /* packed RGBA8 image [H,W] u32, no backward state */
+    VS_PASS_BACKWARD = 1,           /* float RGBA [H,W,4] + backward state */
+    VS_PASS_FLOAT = 2,              /* float RGBA [H,W,4], exact counts, not differentiated */
+    VS_PASS_BACKWARD_SMOOTH_CUTOFF = 3, /* Backward with the C^1 alpha cutoff (gradient checks) */
+    VS_PASS_GEOMETRY = 4,           /* float [H,W,12]: RGBA, sum(w z), median z, normal, distortion, median id */
+} vs_pass;
+
+/* SplatRenderMode, gaussian_splats.rs:19-26.  Only DEFAULT is built; MIP and
+ * SURFEL return VS_ERR_UNSUPPORTED. */
+typedef enum vs_render_mode { VS_MODE_DEFAULT = 0, VS_MODE_MIP = 1, VS_MODE_SURFEL = 2 } vs_render_mode;
+
+/* Forward outputs (RenderAux, crates/splat-train-render/src/render_aux.rs:74-100).
+ * Device arrays may be NULL when not wanted. */
+typedef struct vs_fwd_out {
+    void* out_img;                  /* [H,W,C] f32 (C = 4 or 12) or [H,W] u32 packed (FORWARD) */
+    float* visible;                 /* [N] 1 if the splat was blended into any pixel (bwd passes) */
+    float* max_radius;              /* [N] max(ex/W, ey/H), 0 if culled */
+    float* opacities;               /* [N] sigmoid(raw) for splats past the first culls, else 0 */
+    uint32_t* tile_offsets;         /* [ty,tx,2] start/end per tile (end shrunk on bwd passes) */
+    uint32_t num_visible;           /* host: splats that survived culling */
+    uint32_t num_intersections;     /* host: (tile, splat) pairs */
+} vs_fwd_out;
+
+/* Dense gradients per global splat (the reference's compact rows gathered
+ * through compact_from_global, bwd/burn_glue.rs:355-430). NULL skips one. */
+typedef struct vs_grads {
+    float* v_transforms;            /* [N,10] d/d(mean, quat wxyz, log-scale) */
+    float* v_sh_coeffs;             /* [N,(d+1)^2,3] */
+    float* v_raw_opacities;         /* [N] */
+    float* v_refine_weight;         /* [N] screen-space refine weight, clamped [0,1e32] */
+    float* v_combined;              /* [N,10] raster gradient rows (xy, conic, rgb, alpha, refine) */
+} vs_grads;
+
+/* ---- context --------------------------------------------------------------- */
+
+/* Create a context on `device` enqueueing on `hip_stream` (NULL: the null
+ * stream).  No reference counterpart: the reference's CubeCL client owns the
+ * device queue (crates/splat-train-cube/src/host.rs:12-38). */
+vs_status vs_ctx_create(int device, void* hip_stream, vs_ctx** out);
+void vs_ctx_destroy(vs_ctx* ctx);
+/* Switch the stream later work is enqueued on. */
+vs_status vs_ctx_set_stream(vs_ctx* ctx, void* hip_stream);
+/* Message of the last failing call on this host thread. */
+const char* vs_last_error(void);
+/* Library version string. */
+const char* vs_version(void);
+
+/* Per-stage HIP event timing (replaces the reference's tracing spans,
+ * render.rs:520-886).  While enabled, every stage of every call is bracketed
+ * by events on the context's stream; vs_ctx_stage_times() synchronises the
+ * stream once and returns the milliseconds summed over all calls since the
+ * previous query. */
+typedef struct vs_stage_times {
+    float project_ms, emit_ms, sort_ms, ranges_ms, raster_fwd_ms;
+    float raster_bwd_ms, project_bwd_ms, other_ms;
+} vs_stage_times;
+vs_status vs_ctx_enable_timing(vs_ctx* ctx, int enable);
+vs_status vs_ctx_stage_times(vs_ctx* ctx, vs_stage_times* out);
+
+/* ---- camera host math --------------------------------------------------------- */
+
+/* camera.rs:99-116 fov_to_focal / :118-134 focal_to_fov (host, f64). */
+double vs_fov_to_focal(double fov, uint32_t pixels, int32_t model, const float kb4[4]);
+double vs_focal_to_fov(double focal, uint32_t pixels, int32_t model, const float kb4[4]);
+/* camera.rs:166-172 max_render_theta (KB4 fold angle, pi otherwise). */
+double vs_max_render_theta(int32_t model, const float kb4[4]);
+/* render.rs:478-503 + camera.rs:55-96,305-374: uniforms of a pose at W x H (host). */
+vs_status vs_camera_uniforms(const vs_pose* pose, uint32_t img_w, uint32_t img_h, vs_camera* out);
+
+/* ---- render ------------------------------------------------------------------- */
+
+/* SplatOps::render (crates/splat-train-render/src/lib.rs:53-90; implementation
+ * render.rs:401-979).  Writes the image and aux outputs; for every pass but
+ * FORWARD also returns the state the backward needs in *state (free with
+ * vs_fwd_state_free).  `background` is host memory. */
+vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* splats,
+                            uint32_t img_w, uint32_t img_h, const float background[3],
+                            vs_pass pass, vs_render_mode mode,
+                            vs_fwd_out* out, vs_fwd_state** state);
+
+/* SplatBwdOps::rasterize_bwd + project_bwd (bwd/burn_glue.rs:70-111;
+ * bwd/render_bwd.rs:27-155 and 295-447).  `out_img` is the image the
+ * forward wrote (f32, C channels), `v_out` its cotangent [H,W,C].  The
+ * splat parameters must be the ones the forward saw. */
+vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* state, const vs_splats* splats,
+                             const float* out_img, const float* v_out, vs_grads* grads);
+
+void vs_fwd_state_free(vs_fwd_state* state);
+
+/* Read-only view of the forward's intermediate buffers (device pointers owned
+ * by the state), for parity checks of each stage against the reference
+ * semantics.  Projected rows are indexed by global splat id. */
+typedef struct vs_state_view {
+    uint32_t num_splats, num_visible, num_intersections, num_tiles, tile_bw, tile_bh;
+    uint32_t depth_shift;           /* sorted key = tile << depth_shift | (depth_bits - depth_min) */
+    uint32_t depth_min;
+    const uint64_t* isect_keys;     /* [I] sorted */
+    const uint32_t* isect_gids;     /* [I] sorted global splat ids */
+    const uint32_t* intersect_counts; /* [N] */
+    const float* proj_xy_conic;     /* [N,4] x, y, c00, c01 (valid for visible splats) */
+    const float* proj_c11_opac_rg;  /* [N,4] c11, opacity, r, g */
+    const float* proj_b;            /* [N] b */
+    const float* proj_aux;          /* [N,4] z, nx, ny, nz (GEOMETRY) or NULL */
+    const uint32_t* tile_ranges;    /* [T,2] before the forward shrank the ends */
+} vs_state_view;
+vs_status vs_fwd_state_view(const vs_fwd_state* state, vs_state_view* out);
+
+/* ---- sort / scan ---------------------------------------------------------------- */
+
+/* radix_argsort_skip_low_with_count (crates/splat-train-sort/src/lib.rs:40-189):
+ * stable LSD sort of (key, value) pairs by key bits [skip, skip+8*ceil(bits/8)).
+ * `n_dev` (device, may be NULL) holds the active count <= n; entries past it
+ * are not read or written.  Outputs must not alias inputs. */
+vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, const uint32_t* vals, uint32_t n,
+                               const uint32_t* n_dev, uint32_t skip_bits, uint32_t sorting_bits,
+                               uint32_t* out_keys, uint32_t* out_vals);
+/* The same sort on packed 64-bit keys (tile id above depth bits), bits
+ * [0, sorting_bits) with sorting_bits <= 64.  No reference counterpart as
+ * an API: it replaces the reference's two sorts of render.rs:689-694,792-794. */
+vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, const uint32_t* vals, uint32_t n,
+                               uint32_t sorting_bits, uint64_t* out_keys, uint32_t* out_vals);
+/* prefix_sum (crates/splat-train-scan/src/lib.rs:24-83): inclusive scan. */
+vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n);
+/* scan_in_place (crates/splat-train-scan/src/lib.rs:85-96). */
+vs_status vs_scan_in_place_u32(vs_ctx* ctx, uint32_t* data, uint32_t n);
+
+/* ---- loss cotangent ------------------------------------------------------------- */
+
+/* L1 image-loss cotangent used by the training step after the render
+ * (crates/splat-train-loss/src/lib.rs:786-811 sign, :1297-1300 weights):
+ * v[h,w,c] = sign(pred - gt) / (3 * count) for c < 3, 0 for alpha and for
+ * masked pixels; `count` is H*W, or the number of unmasked pixels when a
+ * circular mask of `mask_radius` > 0 px about (mask_cx, mask_cy) is given.
+ * pred is [H,W,C] f32, gt [H,W,3] f32. */
+vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const float* gt,
+                          uint32_t img_w, uint32_t img_h, float mask_cx, float mask_cy,
+                          float mask_radius, float* v_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

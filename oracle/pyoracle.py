@@ -1,0 +1,255 @@
+"""ctypes wrapper of oracle/liboracle.so.
+
+TEST INFRASTRUCTURE ONLY: a CPU restatement of the reference render path used
+as the parity checker by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg.  The product (vauss_amd) never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+FLAG_BWD_INFO, FLAG_GEOMETRY, FLAG_SMOOTH_CUTOFF = 1, 2, 4
+(F_INTERSECT_COUNTS, F_MAX_RADIUS, F_OPACITIES, F_GLOBAL_FROM_COMPACT, F_DEPTHS, F_PROJECTED, F_AUX, F_ISECT_TILE,
+ F_ISECT_GID, F_TILE_OFFSETS, F_TILE_OFFSETS_SHRUNK, F_VISIBLE, F_OUT_IMG) = range(13)
+
+
+class OrCamera(C.Structure):
+    """Same layout as vs_camera (include/vsplat.h)."""
+    _fields_ = [("model", C.c_int32), ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float),
+                ("kb4", C.c_float * 4), ("viewmat", C.c_float * 12), ("cam_pos", C.c_float * 3),
+                ("half_max_render_fov", C.c_float), ("lim_pos_x", C.c_float), ("lim_pos_y", C.c_float),
+                ("lim_neg_x", C.c_float), ("lim_neg_y", C.c_float), ("lim_r", C.c_float)]
+
+
+class OrFwdInfo(C.Structure):
+    _fields_ = [("num_splats", C.c_uint32), ("num_visible", C.c_uint32), ("num_intersections", C.c_uint32),
+                ("num_tiles", C.c_uint32), ("tile_bw", C.c_uint32), ("tile_bh", C.c_uint32),
+                ("img_w", C.c_uint32), ("img_h", C.c_uint32), ("out_channels", C.c_uint32),
+                ("num_evaluations", C.c_uint64)]
+
+
+_LIB = None
+_F = C.POINTER(C.c_float)
+_U = C.POINTER(C.c_uint32)
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def load() -> C.CDLL:
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        build()
+    lib = C.CDLL(os.fspath(LIB_PATH))
+    lib.or_render_forward.restype = C.c_int
+    lib.or_render_forward.argtypes = [C.POINTER(OrCamera), C.c_uint32, C.c_uint32, _F, _F, C.c_uint32, _F, C.c_uint32,
+                                      C.c_float, _F, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+    lib.or_fwd_get_info.argtypes = [C.c_void_p, C.POINTER(OrFwdInfo)]
+    lib.or_fwd_get.restype = C.c_int
+    lib.or_fwd_get.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+    lib.or_fwd_free.argtypes = [C.c_void_p]
+    lib.or_render_backward.restype = C.c_int
+    lib.or_render_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F, _F]
+    lib.or_radix_argsort_u32.argtypes = [_U, _U, C.c_uint32, C.c_uint32, C.c_uint32, _U, _U]
+    lib.or_prefix_sum_u32.argtypes = [_U, _U, C.c_uint32]
+    for name in ("or_expf", "or_logf"):
+        getattr(lib, name).restype = C.c_float
+        getattr(lib, name).argtypes = [C.c_float]
+    lib.or_atan2f.restype = C.c_float
+    lib.or_atan2f.argtypes = [C.c_float, C.c_float]
+    lib.or_expf_n.argtypes = [_F, _F, C.c_uint64]
+    lib.or_logf_n.argtypes = [_F, _F, C.c_uint64]
+    lib.or_atan2f_n.argtypes = [_F, _F, _F, C.c_uint64]
+    lib.or_sh_basis.argtypes = [C.c_uint32, _F, _F]
+    kb = C.POINTER(C.c_float)
+    for name, args in (("or_fov_to_focal", [C.c_double, C.c_uint32, C.c_int, kb]),
+                       ("or_focal_to_fov", [C.c_double, C.c_uint32, C.c_int, kb]),
+                       ("or_max_render_theta", [C.c_int, kb]), ("or_kb4_d", [C.c_double, kb]),
+                       ("or_kb4_dd_dtheta", [C.c_double, kb]), ("or_kb4_invert_d", [C.c_double, kb])):
+        getattr(lib, name).restype = C.c_double
+        getattr(lib, name).argtypes = args
+    lib.or_max_threads.restype = C.c_int
+    _LIB = lib
+    return lib
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_F)
+
+
+def _up(a: np.ndarray):
+    return a.ctypes.data_as(_U)
+
+
+def camera_struct(cam) -> OrCamera:
+    """Copy a vs_camera (or anything with the same fields) into an OrCamera."""
+    out = OrCamera()
+    C.memmove(C.byref(out), C.byref(cam), C.sizeof(OrCamera))
+    return out
+
+
+@dataclass
+class OracleForward:
+    handle: C.c_void_p
+    info: OrFwdInfo
+    num_splats: int
+    sh_degree: int
+    flags: int
+
+    def get(self, field: int) -> np.ndarray:
+        inf = self.info
+        n, v, i, t = inf.num_splats, inf.num_visible, inf.num_intersections, inf.num_tiles
+        shapes = {F_INTERSECT_COUNTS: ((n,), np.uint32), F_MAX_RADIUS: ((n,), np.float32),
+                  F_OPACITIES: ((n,), np.float32), F_GLOBAL_FROM_COMPACT: ((v,), np.uint32),
+                  F_DEPTHS: ((v,), np.float32), F_PROJECTED: ((v, 9), np.float32), F_AUX: ((v, 4), np.float32),
+                  F_ISECT_TILE: ((i,), np.uint32), F_ISECT_GID: ((i,), np.uint32),
+                  F_TILE_OFFSETS: ((inf.tile_bh, inf.tile_bw, 2), np.uint32),
+                  F_TILE_OFFSETS_SHRUNK: ((inf.tile_bh, inf.tile_bw, 2), np.uint32),
+                  F_VISIBLE: ((n,), np.float32)}
+        if field == F_OUT_IMG:
+            if self.flags & FLAG_BWD_INFO:
+                shape, dt = (inf.img_h, inf.img_w, inf.out_channels), np.float32
+            else:
+                shape, dt = (inf.img_h, inf.img_w), np.uint32
+        else:
+            shape, dt = shapes[field]
+        if field == F_AUX and not (self.flags & FLAG_GEOMETRY):
+            return np.zeros((0, 4), np.float32)
+        out = np.empty(shape, dt)
+        if out.size:
+            rc = load().or_fwd_get(self.handle, field, out.ctypes.data_as(C.c_void_p))
+            assert rc == 0
+        return out
+
+    def backward(self, v_out: np.ndarray, threads: int = 0):
+        n = self.num_splats
+        k = (self.sh_degree + 1) ** 2
+        v_out = np.ascontiguousarray(v_out, np.float32)
+        vc = np.zeros((n, 10), np.float32)
+        vt = np.zeros((n, 10), np.float32)
+        vs = np.zeros((n, k, 3), np.float32)
+        vo = np.zeros(n, np.float32)
+        vr = np.zeros(n, np.float32)
+        rc = load().or_render_backward(self.handle, _fp(v_out), threads, _fp(vc), _fp(vt), _fp(vs), _fp(vo), _fp(vr))
+        if rc != 0:
+            raise RuntimeError(f"oracle backward failed ({rc})")
+        return {"v_combined": vc, "v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+
+    def __del__(self):
+        try:
+            if self.handle:
+                load().or_fwd_free(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+def render_forward(cam, img_size, transforms, sh_coeffs, raw_opacities, background=(0, 0, 0), flags=FLAG_BWD_INFO,
+                   threads: int = 0, log_scale_offset: float = 0.0) -> OracleForward:
+    lib = load()
+    t = np.ascontiguousarray(transforms, np.float32)
+    s = np.ascontiguousarray(sh_coeffs, np.float32)
+    o = np.ascontiguousarray(raw_opacities, np.float32)
+    n = t.shape[0]
+    degree = int(round(np.sqrt(s.shape[1]))) - 1
+    bg = np.asarray(background, np.float32)
+    c = camera_struct(cam)
+    h = C.c_void_p()
+    rc = lib.or_render_forward(C.byref(c), int(img_size[0]), int(img_size[1]), _fp(t), _fp(s), degree, _fp(o), n,
+                               float(log_scale_offset), _fp(bg), flags, threads, C.byref(h))
+    if rc != 0:
+        raise RuntimeError(f"oracle forward failed ({rc})")
+    info = OrFwdInfo()
+    lib.or_fwd_get_info(h, C.byref(info))
+    return OracleForward(h, info, n, degree, flags)
+
+
+def radix_argsort_u32(keys, vals, skip_bits, sorting_bits):
+    k = np.ascontiguousarray(keys, np.uint32)
+    v = np.ascontiguousarray(vals, np.uint32)
+    ok, ov = np.empty_like(k), np.empty_like(v)
+    if k.size:
+        load().or_radix_argsort_u32(_up(k), _up(v), k.size, skip_bits, sorting_bits, _up(ok), _up(ov))
+    return ok, ov
+
+
+def prefix_sum_u32(x):
+    a = np.ascontiguousarray(x, np.uint32)
+    out = np.empty_like(a)
+    if a.size:
+        load().or_prefix_sum_u32(_up(a), _up(out), a.size)
+    return out
+
+
+def expf(x):
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    load().or_expf_n(_fp(a), _fp(out), a.size)
+    return out
+
+
+def logf(x):
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    load().or_logf_n(_fp(a), _fp(out), a.size)
+    return out
+
+
+def atan2f(y, x):
+    a = np.ascontiguousarray(y, np.float32)
+    b = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    load().or_atan2f_n(_fp(a), _fp(b), _fp(out), a.size)
+    return out
+
+
+def sh_basis(degree: int, v) -> np.ndarray:
+    vv = np.ascontiguousarray(v, np.float32)
+    out = np.zeros((degree + 1) ** 2, np.float32)
+    load().or_sh_basis(degree, _fp(vv), _fp(out))
+    return out
+
+
+def kb4_array(k):
+    return (C.c_float * 4)(*[float(v) for v in k])
+
+
+def fov_to_focal(fov, pixels, model=0, k=(0, 0, 0, 0)):
+    return load().or_fov_to_focal(fov, pixels, model, kb4_array(k))
+
+
+def focal_to_fov(focal, pixels, model=0, k=(0, 0, 0, 0)):
+    return load().or_focal_to_fov(focal, pixels, model, kb4_array(k))
+
+
+def max_render_theta(model=0, k=(0, 0, 0, 0)):
+    return load().or_max_render_theta(model, kb4_array(k))
+
+
+def kb4_d(theta, k):
+    return load().or_kb4_d(theta, kb4_array(k))
+
+
+def kb4_dd_dtheta(theta, k):
+    return load().or_kb4_dd_dtheta(theta, kb4_array(k))
+
+
+def kb4_invert_d(target, k):
+    return load().or_kb4_invert_d(target, kb4_array(k))
+
+
+def max_threads() -> int:
+    return load().or_max_threads()

@@ -1,0 +1,1135 @@
+// vs_oracle.cpp -- CPU restatement of the reference Gaussian-splat render path.
+//
+// TEST INFRASTRUCTURE ONLY.  Loaded by tests/, __graft_entry__.smoke() and the
+// cpu_baseline leg of bench.py as the checker; the product never links it.
+//
+// Each stage cites the reference function it restates (paths relative to
+// crates/splat-train-render/src unless they name another crate).  The stage
+// order follows render.rs:401-979 (`render_cube`):
+//   project_forward (cull + count, kernels/project_forward.rs:26-261)
+//   project_visible (kernels/project_visible.rs:97-174, aux 182-312)
+//   depth sort      (render.rs:689-694: stable, raw f32 bits)
+//   count scan      (kernels/map_gaussians.rs:215-269)
+//   map/emit        (kernels/map_gaussians.rs:23-174)
+//   tile sort       (render.rs:792-794: stable by tile id)
+//   tile offsets    (get_tile_offset.rs:11-59)
+//   rasterize       (kernels/rasterize.rs:109-420)
+//   raster VJP      (bwd/kernels/rasterize_backwards_planes.rs:112-682)
+//   projection VJP  (bwd/kernels/project_backwards.rs:132-424)
+//
+// The reference compacts visible splats with an atomic counter, so its
+// compaction order (and the order of exactly tied depths) is whatever the
+// atomics produced.  The oracle fixes that order to increasing global id, one
+// of the orders the reference can produce; every tie below is therefore
+// broken by global id.
+//
+// Arithmetic contract shared with the GPU kernels (both sides implement it
+// independently):
+//  * projection-side math: the reference's operation order, no contraction;
+//  * exp/log/atan2: the portable evaluations of or_math.h;
+//  * compositing: dx = px - x, dy = py - y,
+//      sigma = fma(fma(A, dx, B*dy), dx, (C*dy)*dy)   A = c00/2, B = c01, C = c11/2
+//    (equal to the reference's 0.5(c00 dx^2 + c11 dy^2) + c01 dx dy up to the
+//    contraction the reference's shader compiler is also free to apply),
+//    G = exp(-sigma), alpha = min(0.999, opac G), T' = T (1 - alpha),
+//    colour += max(c,0) * (alpha T) as an fma, final = fma(T, bg, colour).
+#include "vs_oracle.h"
+#include "or_math.h"
+
+#include <vector>
+#include <numeric>
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+using namespace orc;
+
+namespace {
+
+constexpr uint32_t TILE_W = 16;                 // kernels/helpers.rs:15-16
+constexpr float ALPHA_CUTOFF_MID = 1.0f / 255.0f;   // kernels/helpers.rs:23
+constexpr float ALPHA_CUTOFF_BAND = 1.0e-3f;        // kernels/helpers.rs:24
+constexpr float DIST_NEAR = 0.2f, DIST_FAR = 100.0f; // kernels/helpers.rs:93-94
+
+// kernels/helpers.rs:26-47
+float alpha_cutoff_weight(float alpha) {
+    const float t = clampf((alpha - (ALPHA_CUTOFF_MID - 0.5f * ALPHA_CUTOFF_BAND)) / ALPHA_CUTOFF_BAND, 0.0f, 1.0f);
+    return t * t * (3.0f - 2.0f * t);
+}
+float alpha_cutoff_weight_deriv(float alpha) {
+    const float low = ALPHA_CUTOFF_MID - 0.5f * ALPHA_CUTOFF_BAND;
+    const float high = ALPHA_CUTOFF_MID + 0.5f * ALPHA_CUTOFF_BAND;
+    const bool inside = alpha > low && alpha < high;
+    const float t = (alpha - low) / ALPHA_CUTOFF_BAND;
+    return inside ? (6.0f * t - 6.0f * t * t) / ALPHA_CUTOFF_BAND : 0.0f;
+}
+// kernels/helpers.rs:100-103
+float dist_depth(float z) { return DIST_FAR / (DIST_FAR - DIST_NEAR) * (1.0f - DIST_NEAR / fmax_(z, DIST_NEAR)); }
+
+M3 view_rot(const or_camera& u) {
+    return M3{V3{u.viewmat[0], u.viewmat[1], u.viewmat[2]},
+              V3{u.viewmat[3], u.viewmat[4], u.viewmat[5]},
+              V3{u.viewmat[6], u.viewmat[7], u.viewmat[8]}};
+}
+V3 view_trans(const or_camera& u) { return V3{u.viewmat[9], u.viewmat[10], u.viewmat[11]}; }
+// kernels/helpers.rs:472-475
+V3 world_to_cam(V3 mean, const or_camera& u) { return add(mul_vec3(view_rot(u), mean), view_trans(u)); }
+
+// --- camera models -----------------------------------------------------------
+// kernels/camera_model/pinhole.rs:165-171
+void project_pinhole(V3 p, const or_camera& u, float& ou, float& ov) {
+    const float inv_z = 1.0f / p.z;
+    ou = u.fx * p.x * inv_z + u.cx;
+    ov = u.fy * p.y * inv_z + u.cy;
+}
+// kernels/camera_model/kannala_brandt_4.rs:18-54
+void project_kb4(V3 p, const or_camera& u, float& ou, float& ov) {
+    const float x = p.x, y = p.y, z = p.z;
+    const float k1 = u.kb4[0], k2 = u.kb4[1], k3 = u.kb4[2], k4 = u.kb4[3];
+    const float inv_z = 1.0f / z;
+    const float pin_u = u.fx * x * inv_z + u.cx;
+    const float pin_v = u.fy * y * inv_z + u.cy;
+    const float r = std::sqrt(x * x + y * y);
+    const float theta = atan2f_c(r, z);
+    const float th2 = theta * theta, th4 = th2 * th2, th6 = th2 * th4, th8 = th4 * th4;
+    const float d = theta * (1.0f + k1 * th2 + k2 * th4 + k3 * th6 + k4 * th8);
+    const float inv_r = 1.0f / r;
+    const float fu = u.fx * (d * x * inv_r) + u.cx;
+    const float fv = u.fy * (d * y * inv_r) + u.cy;
+    const bool near_axis = r < 1e-6f;
+    ou = near_axis ? pin_u : fu;
+    ov = near_axis ? pin_v : fv;
+}
+void project(V3 p, const or_camera& u, float& ou, float& ov) {
+    if (u.model == OR_MODEL_KB4) project_kb4(p, u, ou, ov); else project_pinhole(p, u, ou, ov);
+}
+// kernels/camera_model/pinhole.rs:173-197
+M23 jac_pinhole(V3 p, const or_camera& u) {
+    const float inv_z = 1.0f / p.z;
+    const float dx = u.fx * inv_z;
+    const float dy = u.fy * inv_z;
+    const float cx = clampf(p.x * inv_z, u.lim_neg_x, u.lim_pos_x);
+    const float cy = clampf(p.y * inv_z, u.lim_neg_y, u.lim_pos_y);
+    return M23{V2{dx, 0.0f}, V2{0.0f, dy}, V2{-dx * cx, -dy * cy}};
+}
+// kernels/camera_model/kannala_brandt_4.rs:58-152
+M23 jac_kb4(V3 p, const or_camera& u) {
+    const float k1 = u.kb4[0], k2 = u.kb4[1], k3 = u.kb4[2], k4 = u.kb4[3];
+    const float x = p.x, y = p.y, z = p.z;
+    const float inv_z = 1.0f / z;
+    const float x2 = x * x, y2 = y * y, xy = x * y;
+    const float r2 = x2 + y2;
+    const float r = std::sqrt(r2);
+    const float inv_r = 1.0f / r;
+    const float inv_r3 = inv_r * inv_r * inv_r;
+    const float rho2 = r2 + z * z;
+    const float inv_rho2 = 1.0f / rho2;
+    const float inv_rho2_r = inv_rho2 * inv_r;
+    const float theta = atan2f_c(r, z);
+    const float th2 = theta * theta, th4 = th2 * th2, th6 = th4 * th2, th8 = th4 * th4;
+    const float d = theta * (1.0f + k1 * th2 + k2 * th4 + k3 * th6 + k4 * th8);
+    const float dd = 1.0f + 3.0f * k1 * th2 + 5.0f * k2 * th4 + 7.0f * k3 * th6 + 9.0f * k4 * th8;
+    const float dth_dx = x * z * inv_rho2_r;
+    const float dth_dy = y * z * inv_rho2_r;
+    const float dth_dz = -r * inv_rho2;
+    const float dd_dx = dd * dth_dx, dd_dy = dd * dth_dy, dd_dz = dd * dth_dz;
+    const float xr = x * inv_r;
+    const float dxr_dx = y2 * inv_r3;
+    const float dxr_dy = -xy * inv_r3;
+    const float du_dx = u.fx * (dd_dx * xr + d * dxr_dx);
+    const float du_dy = u.fx * (dd_dy * xr + d * dxr_dy);
+    const float du_dz = u.fx * (dd_dz * xr);
+    const float yr = y * inv_r;
+    const float dyr_dx = -xy * inv_r3;
+    const float dyr_dy = x2 * inv_r3;
+    const float dv_dx = u.fy * (dd_dx * yr + d * dyr_dx);
+    const float dv_dy = u.fy * (dd_dy * yr + d * dyr_dy);
+    const float dv_dz = u.fy * (dd_dz * yr);
+    const bool near_axis = r < 1e-6f;
+    const float pdx = u.fx * inv_z, pdy = u.fy * inv_z;
+    const float p_du_dz = -pdx * x * inv_z;
+    const float p_dv_dz = -pdy * y * inv_z;
+    return M23{V2{near_axis ? pdx : du_dx, near_axis ? 0.0f : dv_dx},
+               V2{near_axis ? 0.0f : du_dy, near_axis ? pdy : dv_dy},
+               V2{near_axis ? p_du_dz : du_dz, near_axis ? p_dv_dz : dv_dz}};
+}
+M23 project_jacobian(V3 p, const or_camera& u) {
+    return (u.model == OR_MODEL_KB4) ? jac_kb4(p, u) : jac_pinhole(p, u);
+}
+
+// kernels/camera_model/pinhole.rs:199-265
+V3 projection_vjp_pinhole(M23 J, V3 mc, S3 cov_c, const or_camera& u, S2 v_cov2d, V2 v_mean2d) {
+    const float fx = u.fx, fy = u.fy;
+    const float mx = mc.x, my = mc.y, mz = mc.z;
+    const float inv_z = 1.0f / mz;
+    const float mx_rz_raw = mx * inv_z, my_rz_raw = my * inv_z;
+    const float mx_rz = clampf(mx_rz_raw, u.lim_neg_x, u.lim_pos_x);
+    const float my_rz = clampf(my_rz_raw, u.lim_neg_y, u.lim_pos_y);
+    const bool in_x = mx_rz_raw <= u.lim_pos_x && mx_rz_raw >= u.lim_neg_x;
+    const bool in_y = my_rz_raw <= u.lim_pos_y && my_rz_raw >= u.lim_neg_y;
+    const float inv_z2 = inv_z * inv_z;
+    const float inv_z3 = inv_z2 * inv_z;
+    float v_mx = fx * inv_z * v_mean2d.x;
+    float v_my = fy * inv_z * v_mean2d.y;
+    float v_mz = -(fx * mx * v_mean2d.x + fy * my * v_mean2d.y) * inv_z2;
+    const M23 tmp = s2_mul_m23(v_cov2d, J);
+    const float vj00 = 2.0f * dot(m23_row0(tmp), s3_row0(cov_c));
+    const float vj11 = 2.0f * dot(m23_row1(tmp), s3_row1(cov_c));
+    const float vj20 = 2.0f * dot(m23_row0(tmp), s3_row2(cov_c));
+    const float vj21 = 2.0f * dot(m23_row1(tmp), s3_row2(cov_c));
+    const float tx = mz * mx_rz;
+    const float ty = mz * my_rz;
+    if (in_x) v_mx += -fx * inv_z2 * vj20; else v_mz += -fx * inv_z3 * vj20 * tx;
+    if (in_y) v_my += -fy * inv_z2 * vj21; else v_mz += -fy * inv_z3 * vj21 * ty;
+    v_mz += -fx * inv_z2 * vj00 - fy * inv_z2 * vj11 + 2.0f * fx * tx * inv_z3 * vj20 + 2.0f * fy * ty * inv_z3 * vj21;
+    return V3{v_mx, v_my, v_mz};
+}
+
+// kernels/camera_model/kannala_brandt_4.rs:154-337
+V3 projection_vjp_kb4(M23 J, V3 mc, S3 cov_c, const or_camera& u, S2 v_cov2d, V2 v_mean2d) {
+    const float fx = u.fx, fy = u.fy;
+    const float k1 = u.kb4[0], k2 = u.kb4[1], k3 = u.kb4[2], k4 = u.kb4[3];
+    const float mx = mc.x, my = mc.y, mz = mc.z;
+    const float r2 = mx * mx + my * my;
+    const float r = fmax_(std::sqrt(r2), 1.0e-8f);
+    const float rho2 = r2 + mz * mz;
+    const float theta = atan2f_c(r, mz);
+    const float th2 = theta * theta, th4 = th2 * th2, th6 = th4 * th2, th8 = th4 * th4;
+    const float theta_d = theta * (1.0f + k1 * th2 + k2 * th4 + k3 * th6 + k4 * th8);
+    const float p1 = 1.0f + 3.0f * k1 * th2 + 5.0f * k2 * th4 + 7.0f * k3 * th6 + 9.0f * k4 * th8;
+    const float p2 = 6.0f * k1 * theta + 20.0f * k2 * theta * th2 + 42.0f * k3 * theta * th4 + 72.0f * k4 * theta * th6;
+    const float inv_r = 1.0f / r;
+    const float inv_r3 = inv_r * inv_r * inv_r;
+    const float inv_r5 = inv_r3 * inv_r * inv_r;
+    const float inv_rho2 = 1.0f / rho2;
+    const float inv_rho2_sq = inv_rho2 * inv_rho2;
+    const float inv_rho2_r = inv_rho2 * inv_r;
+    const float dth_x = mx * mz * inv_rho2_r;
+    const float dth_y = my * mz * inv_rho2_r;
+    const float dth_z = -r * inv_rho2;
+    const float xr = mx * inv_r, yr = my * inv_r;
+    const float dxr_x = my * my * inv_r3;
+    const float dxr_y = -mx * my * inv_r3;
+    const float dyr_x = dxr_y;
+    const float dyr_y = mx * mx * inv_r3;
+    const float dg_x = p1 * dth_x, dg_y = p1 * dth_y, dg_z = p1 * dth_z;
+    float v_mx = dot2(v_mean2d, J.c0);
+    float v_my = dot2(v_mean2d, J.c1);
+    float v_mz = dot2(v_mean2d, J.c2);
+    const M23 tmp = s2_mul_m23(v_cov2d, J);
+    const float vj_u0 = 2.0f * dot(m23_row0(tmp), s3_row0(cov_c));
+    const float vj_u1 = 2.0f * dot(m23_row0(tmp), s3_row1(cov_c));
+    const float vj_u2 = 2.0f * dot(m23_row0(tmp), s3_row2(cov_c));
+    const float vj_v0 = 2.0f * dot(m23_row1(tmp), s3_row0(cov_c));
+    const float vj_v1 = 2.0f * dot(m23_row1(tmp), s3_row1(cov_c));
+    const float vj_v2 = 2.0f * dot(m23_row1(tmp), s3_row2(cov_c));
+    const float three_r2_z2 = 3.0f * r2 + mz * mz;
+    const float r2_minus_z2 = r2 - mz * mz;
+    const float h_th_00 = mz * (r2 * rho2 - mx * mx * three_r2_z2) * inv_r3 * inv_rho2_sq;
+    const float h_th_11 = mz * (r2 * rho2 - my * my * three_r2_z2) * inv_r3 * inv_rho2_sq;
+    const float h_th_01 = -mx * my * mz * three_r2_z2 * inv_r3 * inv_rho2_sq;
+    const float h_th_02 = mx * r2_minus_z2 * inv_r * inv_rho2_sq;
+    const float h_th_12 = my * r2_minus_z2 * inv_r * inv_rho2_sq;
+    const float h_th_22 = 2.0f * mz * r * inv_rho2_sq;
+    const float two_x2_my2 = 2.0f * mx * mx - my * my;
+    const float two_y2_mx2 = 2.0f * my * my - mx * mx;
+    const float h_xr_00 = -3.0f * mx * my * my * inv_r5;
+    const float h_xr_01 = my * two_x2_my2 * inv_r5;
+    const float h_xr_11 = mx * two_y2_mx2 * inv_r5;
+    const float h_yr_00 = my * two_x2_my2 * inv_r5;
+    const float h_yr_01 = mx * two_y2_mx2 * inv_r5;
+    const float h_yr_11 = -3.0f * mx * mx * my * inv_r5;
+    {
+        const float d2g = p2 * dth_x * dth_x + p1 * h_th_00;
+        const float d_ju = fx * (d2g * xr + dg_x * dxr_x + dg_x * dxr_x + theta_d * h_xr_00);
+        const float d_jv = fy * (d2g * yr + dg_x * dyr_x + dg_x * dyr_x + theta_d * h_yr_00);
+        v_mx += vj_u0 * d_ju + vj_v0 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_y * dth_x + p1 * h_th_01;
+        const float d_ju = fx * (d2g * xr + dg_y * dxr_x + dg_x * dxr_y + theta_d * h_xr_01);
+        const float d_jv = fy * (d2g * yr + dg_y * dyr_x + dg_x * dyr_y + theta_d * h_yr_01);
+        v_mx += vj_u1 * d_ju + vj_v1 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_z * dth_x + p1 * h_th_02;
+        const float d_ju = fx * (d2g * xr + dg_x * 0.0f + dg_z * dxr_x);
+        const float d_jv = fy * (d2g * yr + dg_x * 0.0f + dg_z * dyr_x);
+        v_mx += vj_u2 * d_ju + vj_v2 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_x * dth_y + p1 * h_th_01;
+        const float d_ju = fx * (d2g * xr + dg_x * dxr_y + dg_y * dxr_x + theta_d * h_xr_01);
+        const float d_jv = fy * (d2g * yr + dg_x * dyr_y + dg_y * dyr_x + theta_d * h_yr_01);
+        v_my += vj_u0 * d_ju + vj_v0 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_y * dth_y + p1 * h_th_11;
+        const float d_ju = fx * (d2g * xr + dg_y * dxr_y + dg_y * dxr_y + theta_d * h_xr_11);
+        const float d_jv = fy * (d2g * yr + dg_y * dyr_y + dg_y * dyr_y + theta_d * h_yr_11);
+        v_my += vj_u1 * d_ju + vj_v1 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_z * dth_y + p1 * h_th_12;
+        const float d_ju = fx * (d2g * xr + dg_y * 0.0f + dg_z * dxr_y);
+        const float d_jv = fy * (d2g * yr + dg_y * 0.0f + dg_z * dyr_y);
+        v_my += vj_u2 * d_ju + vj_v2 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_x * dth_z + p1 * h_th_02;
+        const float d_ju = fx * (d2g * xr + dg_z * dxr_x + dg_x * 0.0f);
+        const float d_jv = fy * (d2g * yr + dg_z * dyr_x + dg_x * 0.0f);
+        v_mz += vj_u0 * d_ju + vj_v0 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_y * dth_z + p1 * h_th_12;
+        const float d_ju = fx * (d2g * xr + dg_z * dxr_y + dg_y * 0.0f);
+        const float d_jv = fy * (d2g * yr + dg_z * dyr_y + dg_y * 0.0f);
+        v_mz += vj_u1 * d_ju + vj_v1 * d_jv;
+    }
+    {
+        const float d2g = p2 * dth_z * dth_z + p1 * h_th_22;
+        const float d_ju = fx * (d2g * xr);
+        const float d_jv = fy * (d2g * yr);
+        v_mz += vj_u2 * d_ju + vj_v2 * d_jv;
+    }
+    return V3{v_mx, v_my, v_mz};
+}
+
+// --- covariance ----------------------------------------------------------------
+// kernels/helpers.rs:195-225
+S2 calc_cov2d(V3 scale_, Q4 quat, V3 mean_c, const or_camera& u) {
+    const M3 ns = mul_diag(mul_mat3(view_rot(u), quat_to_mat3(quat)), scale_);
+    const M23 J = project_jacobian(mean_c, u);
+    const M23 v = m23_mul_mat3(J, ns);
+    const S2 raw = m23_gram(v);
+    const float lim = 1.0e18f;
+    const float max_abs = s2_max_abs(raw);
+    const float scale_down = (max_abs > lim) ? lim / max_abs : 1.0f;
+    return s2_scale(raw, scale_down);
+}
+// kernels/helpers.rs:230-245 (Default mode: +0.3 blur, no compensation)
+S2 compensate_cov2d(S2 c) { return S2{c.c00 + 0.3f, c.c01, c.c11 + 0.3f}; }
+
+// kernels/helpers.rs:133-144
+void bbox_extent(S2 conic, float power, float& ex, float& ey) {
+    const float det = conic.c00 * conic.c11 - conic.c01 * conic.c01;
+    const bool degenerate = det <= 0.0f;
+    const float inv_det = degenerate ? 0.0f : 1.0f / det;
+    const float ex_ = std::sqrt(2.0f * power * conic.c11 * inv_det);
+    const float ey_ = std::sqrt(2.0f * power * conic.c00 * inv_det);
+    ex = degenerate ? -1.0f : ex_;
+    ey = degenerate ? -1.0f : ey_;
+}
+struct TileBbox { uint32_t min_x, min_y, max_x, max_y; };
+// Rust's float -> u32 `as` cast: truncation, saturating, NaN -> 0.
+uint32_t f2u32_sat(float v) {
+    if (!(v > 0.0f)) return 0u;
+    if (v >= 4294967296.0f) return 0xFFFFFFFFu;
+    return (uint32_t)v;
+}
+// kernels/helpers.rs:160-190
+TileBbox tile_bbox(float cx, float cy, float ex, float ey, uint32_t bw, uint32_t bh) {
+    const float tw = (float)TILE_W;
+    const float x = cx / tw, y = cy / tw, dx = ex / tw, dy = ey / tw;
+    const float bwf = (float)bw, bhf = (float)bh;
+    return TileBbox{f2u32_sat(clampf(x - dx, 0.0f, bwf)), f2u32_sat(clampf(y - dy, 0.0f, bhf)),
+                    f2u32_sat(clampf(x + dx + 1.0f, 0.0f, bwf)), f2u32_sat(clampf(y + dy + 1.0f, 0.0f, bhf))};
+}
+// kernels/helpers.rs:275-314 (StopThePop conservative ellipse-rect test)
+bool will_contribute(uint32_t tx, uint32_t ty, float mx, float my, S2 conic, float power) {
+    const float min_x = (float)(tx * TILE_W), min_y = (float)(ty * TILE_W);
+    const float max_x = min_x + (float)TILE_W, max_y = min_y + (float)TILE_W;
+    const bool x_left = mx < min_x, x_right = mx > max_x;
+    const bool in_x = !(x_left || x_right);
+    const bool y_above = my < min_y, y_below = my > max_y;
+    const bool in_y = !(y_above || y_below);
+    bool hit = in_x && in_y;
+    if (!hit) {
+        const float corner_x = x_left ? min_x : max_x;
+        const float corner_y = y_above ? min_y : max_y;
+        const float width = max_x - min_x, height = max_y - min_y;
+        const float dxf = x_left ? width : -width;
+        const float dyf = y_above ? height : -height;
+        const float diff_x = mx - corner_x, diff_y = my - corner_y;
+        const float tx_raw = (dxf * conic.c00 * diff_x + dxf * conic.c01 * diff_y) / (dxf * conic.c00 * dxf);
+        const float ty_raw = (dyf * conic.c01 * diff_x + dyf * conic.c11 * diff_y) / (dyf * conic.c11 * dyf);
+        const float tx_ = in_y ? 0.0f : clampf(tx_raw, 0.0f, 1.0f);
+        const float ty_ = in_x ? 0.0f : clampf(ty_raw, 0.0f, 1.0f);
+        const float px = corner_x + tx_ * dxf;
+        const float py = corner_y + ty_ * dyf;
+        hit = calc_sigma(px, py, conic, mx, my) <= power;
+    }
+    return hit;
+}
+
+// --- SH -------------------------------------------------------------------------
+// kernels/sh.rs:51-140 basis values in the order the reference accumulates them.
+int sh_basis(uint32_t degree, V3 v, float* Y) {
+    Y[0] = 0.2820948f;
+    int n = 1;
+    if (degree >= 1) {
+        const float f0a = 0.4886025f;
+        Y[1] = -f0a * v.y; Y[2] = f0a * v.z; Y[3] = -f0a * v.x; n = 4;
+        if (degree >= 2) {
+            const float z2 = v.z * v.z;
+            const float f0b = -1.0925485f * v.z;
+            const float f1a = 0.54627424f;
+            const float fc1 = v.x * v.x - v.y * v.y;
+            const float fs1 = 2.0f * v.x * v.y;
+            Y[4] = f1a * fs1; Y[5] = f0b * v.y; Y[6] = 0.9461747f * z2 - 0.31539157f;
+            Y[7] = f0b * v.x; Y[8] = f1a * fc1; n = 9;
+            if (degree >= 3) {
+                const float f0c = -2.285229f * z2 + 0.4570458f;
+                const float f1b = 1.4453057f * v.z;
+                const float f2a = -0.5900436f;
+                const float fc2 = v.x * fc1 - v.y * fs1;
+                const float fs2 = v.x * fs1 + v.y * fc1;
+                const float p12 = v.z * (1.8658817f * z2 - 1.119529f);
+                Y[9] = f2a * fs2; Y[10] = f1b * fs1; Y[11] = f0c * v.y; Y[12] = p12;
+                Y[13] = f0c * v.x; Y[14] = f1b * fc1; Y[15] = f2a * fc2; n = 16;
+                if (degree >= 4) {
+                    const float f0d = v.z * (-4.683326f * z2 + 2.0071396f);
+                    const float f1c = 3.3116114f * z2 - 0.47308735f;
+                    const float f2b = -1.7701308f * v.z;
+                    const float f3a = 0.62583575f;
+                    const float fc3 = v.x * fc2 - v.y * fs2;
+                    const float fs3 = v.x * fs2 + v.y * fc2;
+                    const float p6 = Y[6];
+                    Y[16] = f3a * fs3; Y[17] = f2b * fs2; Y[18] = f1c * fs1; Y[19] = f0d * v.y;
+                    Y[20] = 1.9843135f * v.z * p12 - 1.0062306f * p6;
+                    Y[21] = f0d * v.x; Y[22] = f1c * fc1; Y[23] = f2b * fc2; Y[24] = f3a * fc3; n = 25;
+                }
+            }
+        }
+    }
+    return n;
+}
+// kernels/sh.rs:51-140: colour = C0 c0 + sum_k Y_k c_k, each term added in order.
+V3 sh_to_color(const float* coeffs, uint32_t degree, V3 v) {
+    float Y[25];
+    const int n = sh_basis(degree, v, Y);
+    V3 color = scale(v3(coeffs[0], coeffs[1], coeffs[2]), Y[0]);
+    for (int k = 1; k < n; ++k) color = add(color, scale(v3(coeffs[3 * k], coeffs[3 * k + 1], coeffs[3 * k + 2]), Y[k]));
+    return color;
+}
+// kernels/project_visible.rs:25-61 (SH branch)
+V3 splat_color(const float* coeffs, uint32_t degree, V3 mean, const or_camera& u) {
+    const V3 v = normalize(sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]}));
+    const V3 raw = sh_to_color(coeffs, degree, v);
+    const V3 c = V3{raw.x + 0.5f, raw.y + 0.5f, raw.z + 0.5f};
+    return V3{clampf(is_finite(c.x) ? c.x : 0.0f, -100.0f, 100.0f),
+              clampf(is_finite(c.y) ? c.y : 0.0f, -100.0f, 100.0f),
+              clampf(is_finite(c.z) ? c.z : 0.0f, -100.0f, 100.0f)};
+}
+// kernels/sh.rs:147-274
+V3 sh_viewdir_vjp(const float* cb, uint32_t degree, V3 v, V3 vc) {
+    auto co = [&](int k) { return v3(cb[3 * k], cb[3 * k + 1], cb[3 * k + 2]); };
+    float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+    if (degree >= 1) {
+        const float f0a = 0.4886025f;
+        const float s_n1 = dot(co(1), vc), s_z0 = dot(co(2), vc), s_p1 = dot(co(3), vc);
+        gx += -f0a * s_p1; gy += -f0a * s_n1; gz += f0a * s_z0;
+        if (degree >= 2) {
+            const float z = v.z, x = v.x, y = v.y;
+            const float c2 = -1.0925485f, f1a = 0.54627424f;
+            const float s_n2 = dot(co(4), vc), s_n1b = dot(co(5), vc), s_z0b = dot(co(6), vc), s_p1b = dot(co(7), vc), s_p2 = dot(co(8), vc);
+            gx += 2.0f * f1a * y * s_n2 + c2 * z * s_p1b + 2.0f * f1a * x * s_p2;
+            gy += 2.0f * f1a * x * s_n2 + c2 * z * s_n1b - 2.0f * f1a * y * s_p2;
+            gz += c2 * y * s_n1b + 2.0f * 0.9461747f * z * s_z0b + c2 * x * s_p1b;
+            if (degree >= 3) {
+                const float z2 = z * z, x2 = x * x, y2 = y * y;
+                const float f2a = -0.5900436f, c1b = 1.4453057f;
+                const float f1b = c1b * z;
+                const float c0c = -2.285229f;
+                const float f0c = c0c * z2 + 0.4570458f;
+                const float f0c_dz = 2.0f * c0c * z;
+                const float s_n3 = dot(co(9), vc), s_n2c = dot(co(10), vc), s_n1c = dot(co(11), vc), s_z0c = dot(co(12), vc);
+                const float s_p1c = dot(co(13), vc), s_p2c = dot(co(14), vc), s_p3 = dot(co(15), vc);
+                const float d12_z = 3.0f * 1.8658817f * z2 - 1.119529f;
+                gx += f2a * 6.0f * x * y * s_n3 + 2.0f * f1b * y * s_n2c + f0c * s_p1c + 2.0f * f1b * x * s_p2c + f2a * 3.0f * (x2 - y2) * s_p3;
+                gy += f2a * 3.0f * (x2 - y2) * s_n3 + 2.0f * f1b * x * s_n2c + f0c * s_n1c + (-2.0f) * f1b * y * s_p2c + f2a * (-6.0f) * x * y * s_p3;
+                gz += 2.0f * c1b * x * y * s_n2c + f0c_dz * y * s_n1c + d12_z * s_z0c + f0c_dz * x * s_p1c + c1b * (x2 - y2) * s_p2c;
+                if (degree >= 4) {
+                    const float fc1 = x2 - y2, fs1 = 2.0f * x * y;
+                    const float fc2 = x * fc1 - y * fs1, fs2 = x * fs1 + y * fc1;
+                    const float f0d = z * (-4.683326f * z2 + 2.0071396f);
+                    const float f0d_dz = -14.049978f * z2 + 2.0071396f;
+                    const float f1c = 3.3116114f * z2 - 0.47308735f;
+                    const float f1c_dz = 2.0f * 3.3116114f * z;
+                    const float f2b_c = -1.7701308f;
+                    const float f2b = f2b_c * z;
+                    const float f3a = 0.62583575f;
+                    const float p_sh12 = z * (1.8658817f * z2 - 1.119529f);
+                    const float dp12 = 3.0f * 1.8658817f * z2 - 1.119529f;
+                    const float dp6 = 2.0f * 0.9461747f * z;
+                    const float dp20 = 1.9843135f * (p_sh12 + z * dp12) - 1.0062306f * dp6;
+                    const float s_n4 = dot(co(16), vc), s_n3d = dot(co(17), vc), s_n2d = dot(co(18), vc), s_n1d = dot(co(19), vc);
+                    const float s_z0d = dot(co(20), vc), s_p1d = dot(co(21), vc), s_p2d = dot(co(22), vc), s_p3d = dot(co(23), vc), s_p4 = dot(co(24), vc);
+                    gx += f3a * 4.0f * fs2 * s_n4 + f2b * 3.0f * fs1 * s_n3d + f1c * 2.0f * y * s_n2d + f0d * s_p1d + f1c * 2.0f * x * s_p2d + f2b * 3.0f * fc1 * s_p3d + f3a * 4.0f * fc2 * s_p4;
+                    gy += f3a * 4.0f * fc2 * s_n4 + f2b * 3.0f * fc1 * s_n3d + f1c * 2.0f * x * s_n2d + f0d * s_n1d + f1c * (-2.0f) * y * s_p2d + f2b * (-3.0f) * fs1 * s_p3d + f3a * (-4.0f) * fs2 * s_p4;
+                    gz += f2b_c * fs2 * s_n3d + f1c_dz * fs1 * s_n2d + f0d_dz * y * s_n1d + dp20 * s_z0d + f0d_dz * x * s_p1d + f1c_dz * fc1 * s_p2d + f2b_c * fc2 * s_p3d;
+                }
+            }
+        }
+    }
+    return V3{gx, gy, gz};
+}
+
+// --- projection VJP helpers, bwd/kernels/project_backwards.rs:18-98 ----------
+Q4 apply_normalize_vjp(Q4 q, Q4 g) {
+    const float lsq = qdot(q, q);
+    const float l = std::sqrt(lsq);
+    const float inv = 1.0f / (l * lsq);
+    const float qw = q.w, qx = q.x, qy = q.y, qz = q.z;
+    const float gw = g.w, gx = g.x, gy = g.y, gz = g.z;
+    const float cc0 = -qw * qx, cc1 = -qx * qy, cc2 = -qy * qw;
+    const float cs0 = -qw * qz, cs1 = -qx * qz, cs2 = -qy * qz;
+    const float sw = qw * qw, sx = qx * qx, sy = qy * qy, sz = qz * qz;
+    return Q4{((lsq - sw) * gw + cc0 * gx + cc2 * gy + cs0 * gz) * inv,
+              (cc0 * gw + (lsq - sx) * gx + cc1 * gy + cs1 * gz) * inv,
+              (cc2 * gw + cc1 * gx + (lsq - sy) * gy + cs2 * gz) * inv,
+              (cs0 * gw + cs1 * gx + cs2 * gy + (lsq - sz) * gz) * inv};
+}
+Q4 quat_to_mat_vjp(Q4 q, M3 v) {
+    const float qw = q.w, qx = q.x, qy = q.y, qz = q.z;
+    const float w_grad = qx * (v.c1.z - v.c2.y) + qy * (v.c2.x - v.c0.z) + qz * (v.c0.y - v.c1.x);
+    const float x_grad = -2.0f * qx * (v.c1.y + v.c2.z) + qy * (v.c0.y + v.c1.x) + qz * (v.c0.z + v.c2.x) + qw * (v.c1.z - v.c2.y);
+    const float y_grad = qx * (v.c0.y + v.c1.x) - 2.0f * qy * (v.c0.x + v.c2.z) + qz * (v.c1.z + v.c2.y) + qw * (v.c2.x - v.c0.z);
+    const float z_grad = qx * (v.c0.z + v.c2.x) + qy * (v.c1.z + v.c2.y) - 2.0f * qz * (v.c0.x + v.c1.y) + qw * (v.c0.y - v.c1.x);
+    return Q4{2.0f * w_grad, 2.0f * x_grad, 2.0f * y_grad, 2.0f * z_grad};
+}
+S2 inverse2x2_vjp(S2 minv, S2 v) {
+    const float t00 = -minv.c00 * v.c00 + -minv.c01 * v.c01;
+    const float t01 = -minv.c01 * v.c00 + -minv.c11 * v.c01;
+    const float t10 = -minv.c00 * v.c01 + -minv.c01 * v.c11;
+    const float t11 = -minv.c01 * v.c01 + -minv.c11 * v.c11;
+    return S2{t00 * minv.c00 + t10 * minv.c01, t01 * minv.c00 + t11 * minv.c01, t01 * minv.c01 + t11 * minv.c11};
+}
+
+struct RasterSplat { float x, y, A, B, C, opac, r, g, b, c00, c01, c11; uint32_t gid; float z, nx, ny, nz; };
+
+} // namespace
+
+struct or_fwd {
+    or_camera cam;
+    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0;
+    float lso = 0.0f;
+    float bg[3] = {0, 0, 0};
+    int flags = 0;
+    uint32_t tbw = 0, tbh = 0, T = 0, out_ch = 4;
+    const float* transforms = nullptr;   // borrowed for the backward (caller keeps alive)
+    const float* sh = nullptr;
+    const float* raw_opac = nullptr;
+    std::vector<float> transforms_copy, sh_copy, opac_copy;
+    uint32_t V = 0;
+    uint64_t evals = 0;
+    std::vector<uint32_t> intersect_counts;
+    std::vector<float> max_radius, opacities, visible;
+    std::vector<uint32_t> global_from_compact;
+    std::vector<float> depths, projected, aux;
+    std::vector<uint32_t> isect_tile, isect_cid;   // sorted, sentinel-free prefix of length I
+    std::vector<uint32_t> tile_offsets, tile_offsets_shrunk;
+    std::vector<float> out_img;
+    std::vector<uint32_t> out_packed;
+};
+
+static int resolve_threads(int threads) {
+#ifdef _OPENMP
+    return threads > 0 ? threads : omp_get_max_threads();
+#else
+    (void)threads;
+    return 1;
+#endif
+}
+
+extern "C" int or_max_threads(void) { return resolve_threads(0); }
+
+extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H,
+                                 const float* transforms, const float* sh, uint32_t degree,
+                                 const float* raw_opac, uint32_t N, float lso,
+                                 const float bg[3], int flags, int threads, or_fwd** out) {
+    if (!cam_in || !out || W == 0 || H == 0 || degree > 4) return 1;
+    const int nthreads = resolve_threads(threads);
+    auto f = std::make_unique<or_fwd>();
+    f->cam = *cam_in;
+    const or_camera& u = f->cam;
+    f->W = W; f->H = H; f->N = N; f->degree = degree; f->K = (degree + 1) * (degree + 1); f->lso = lso;
+    f->bg[0] = bg[0]; f->bg[1] = bg[1]; f->bg[2] = bg[2];
+    f->flags = flags;
+    const bool bwd_info = flags & OR_FLAG_BWD_INFO;
+    const bool geometry = flags & OR_FLAG_GEOMETRY;
+    const bool smooth = flags & OR_FLAG_SMOOTH_CUTOFF;
+    f->tbw = (W + TILE_W - 1) / TILE_W; f->tbh = (H + TILE_W - 1) / TILE_W; f->T = f->tbw * f->tbh;
+    f->out_ch = geometry ? 12 : 4;
+    const uint32_t K = f->K;
+    // Keep private copies so the backward never depends on caller lifetimes.
+    f->transforms_copy.assign(transforms, transforms + (size_t)N * 10);
+    f->sh_copy.assign(sh, sh + (size_t)N * K * 3);
+    f->opac_copy.assign(raw_opac, raw_opac + N);
+    f->transforms = f->transforms_copy.data(); f->sh = f->sh_copy.data(); f->raw_opac = f->opac_copy.data();
+    transforms = f->transforms; sh = f->sh; raw_opac = f->raw_opac;
+
+    // ---- project_forward: cull + count, kernels/project_forward.rs:26-261 ----
+    f->intersect_counts.assign(N, 0u);
+    f->max_radius.assign(N, 0.0f);
+    f->opacities.assign(N, 0.0f);
+    std::vector<uint8_t> vis_flag(N, 0);
+    std::vector<float> depth_g(N, 0.0f);
+    const uint32_t tbw = f->tbw, tbh = f->tbh;
+    #pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int64_t gi = 0; gi < (int64_t)N; ++gi) {
+        const uint32_t g = (uint32_t)gi;
+        const float* t = transforms + (size_t)g * 10;
+        const V3 mean_c = world_to_cam(v3(t[0], t[1], t[2]), u);
+        if (!(finite3(mean_c) && mean_c.z <= 1.0e10f)) continue;
+        if (u.model == OR_MODEL_PINHOLE) {
+            if (mean_c.z < 0.01f) continue;
+        } else {
+            const float r = std::sqrt(mean_c.x * mean_c.x + mean_c.y * mean_c.y);
+            const float theta = atan2f_c(r, mean_c.z);
+            if (theta > u.half_max_render_fov) continue;
+        }
+        const V3 sc = v3(expf_c(t[7] + lso), expf_c(t[8] + lso), expf_c(t[9] + lso));
+        if (!finite3(sc)) continue;
+        const Q4 qu{t[3], t[4], t[5], t[6]};
+        const float qn = qdot(qu, qu);
+        if (!(qn >= 1.0e-6f && is_finite(qn))) continue;
+        const float ro = raw_opac[g];
+        if (!is_finite(ro)) continue;
+        const Q4 q = qnormalize(qu);
+        float opac = sigmoid(ro);
+        f->opacities[g] = opac;
+        const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
+        opac = opac * 1.0f;                       // filter_comp is 1 outside Mip mode
+        if (!s2_finite(cov)) continue;
+        float mx, my;
+        project(mean_c, u, mx, my);
+        if (!(opac >= 1.0f / 255.0f)) continue;
+        const float power = logf_c(opac * 255.0f);
+        const S2 conic = s2_inverse(cov);
+        float ex, ey;
+        bbox_extent(conic, power, ex, ey);
+        if (!(ex >= 0.0f && ey >= 0.0f)) continue;
+        const float wf = (float)W, hf = (float)H;
+        const bool on_screen = mx + ex > 0.0f && mx - ex < wf && my + ey > 0.0f && my - ey < hf;
+        if (!on_screen) continue;
+        const TileBbox bb = tile_bbox(mx, my, ex, ey, tbw, tbh);
+        const float radius = fmax_(ex / wf, ey / hf);
+        // count_contributing_tiles, kernels/helpers.rs:253-273
+        const uint32_t bw = bb.max_x - bb.min_x;
+        const uint32_t nb = (bb.max_y - bb.min_y) * bw;
+        uint32_t hits = 0;
+        for (uint32_t i = 0; i < nb; ++i) {
+            const uint32_t tx = i % bw + bb.min_x, ty = i / bw + bb.min_y;
+            if (will_contribute(tx, ty, mx, my, conic, power)) ++hits;
+        }
+        f->intersect_counts[g] = hits;
+        f->max_radius[g] = radius;
+        vis_flag[g] = 1;
+        depth_g[g] = mean_c.z;
+    }
+    // Compaction: increasing global id (see header).
+    for (uint32_t g = 0; g < N; ++g) if (vis_flag[g]) f->global_from_compact.push_back(g);
+    const uint32_t V = (uint32_t)f->global_from_compact.size();
+    f->V = V;
+    f->depths.resize(V);
+    for (uint32_t c = 0; c < V; ++c) f->depths[c] = depth_g[f->global_from_compact[c]];
+
+    // ---- project_visible, kernels/project_visible.rs:97-174 / 182-312 ----------
+    f->projected.assign((size_t)V * 9, 0.0f);
+    if (geometry) f->aux.assign((size_t)V * 4, 0.0f);
+    #pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int64_t ci = 0; ci < (int64_t)V; ++ci) {
+        const uint32_t c = (uint32_t)ci;
+        const uint32_t g = f->global_from_compact[c];
+        const float* t = transforms + (size_t)g * 10;
+        const V3 mean = v3(t[0], t[1], t[2]);
+        const V3 sc = v3(expf_c(t[7] + lso), expf_c(t[8] + lso), expf_c(t[9] + lso));
+        const Q4 q = qnormalize(Q4{t[3], t[4], t[5], t[6]});
+        const float opac_sig = sigmoid(raw_opac[g]);
+        const V3 mean_c = world_to_cam(mean, u);
+        const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
+        const float opac = opac_sig * 1.0f;
+        const S2 conic = s2_inverse(cov);
+        float mx, my;
+        project(mean_c, u, mx, my);
+        const V3 col = splat_color(sh + (size_t)g * K * 3, degree, mean, u);
+        float* row = &f->projected[(size_t)c * 9];
+        row[0] = mx; row[1] = my; row[2] = conic.c00; row[3] = conic.c01; row[4] = conic.c11;
+        row[5] = opac; row[6] = col.x; row[7] = col.y; row[8] = col.z;
+        if (geometry) {
+            const M3 rot = mul_mat3(view_rot(u), quat_to_mat3(q));
+            const bool x_min = sc.x <= sc.y && sc.x <= sc.z;
+            const bool y_min = !x_min && sc.y <= sc.z;
+            const V3 axis = x_min ? rot.c0 : (y_min ? rot.c1 : rot.c2);
+            const float flip = (dot(axis, mean_c) > 0.0f) ? -1.0f : 1.0f;
+            float* a = &f->aux[(size_t)c * 4];
+            a[0] = mean_c.z; a[1] = axis.x * flip; a[2] = axis.y * flip; a[3] = axis.z * flip;
+        }
+    }
+
+    // ---- depth sort: stable on raw f32 bits, render.rs:689-694 -------------------
+    std::vector<uint32_t> sorted(V);
+    std::iota(sorted.begin(), sorted.end(), 0u);
+    std::stable_sort(sorted.begin(), sorted.end(), [&](uint32_t a, uint32_t b) {
+        return f2u(f->depths[a]) < f2u(f->depths[b]);
+    });
+
+    // ---- count scan in depth order, kernels/map_gaussians.rs:215-269 -----------
+    std::vector<uint64_t> cum(V + 1, 0);
+    for (uint32_t j = 0; j < V; ++j) cum[j + 1] = cum[j] + f->intersect_counts[f->global_from_compact[sorted[j]]];
+    const uint64_t I = cum[V];
+    if (I > 0xFFFFFFFFull) return 2;
+
+    // ---- map: emit (tile, compact id) in depth order, kernels/map_gaussians.rs:23-174
+    std::vector<uint32_t> tile_of(I), cid_of(I);
+    const uint32_t sentinel = f->T;
+    #pragma omp parallel for schedule(dynamic, 256) num_threads(nthreads)
+    for (int64_t ji = 0; ji < (int64_t)V; ++ji) {
+        const uint32_t j = (uint32_t)ji;
+        const uint32_t c = sorted[j];
+        const float* row = &f->projected[(size_t)c * 9];
+        const S2 conic{row[2], row[3], row[4]};
+        const float power = logf_c(row[5] * 255.0f);
+        float ex, ey;
+        bbox_extent(conic, power, ex, ey);
+        const TileBbox bb = tile_bbox(row[0], row[1], ex, ey, tbw, tbh);
+        const uint64_t base = cum[j];
+        const uint32_t pf_count = (uint32_t)(cum[j + 1] - cum[j]);
+        const uint32_t bw = bb.max_x - bb.min_x;
+        const uint32_t nb = (bb.max_y - bb.min_y) * bw;
+        uint32_t hits = 0;
+        for (uint32_t i = 0; i < nb; ++i) {
+            const uint32_t tx = i % bw + bb.min_x, ty = i / bw + bb.min_y;
+            if (will_contribute(tx, ty, row[0], row[1], conic, power) && hits < pf_count) {
+                tile_of[base + hits] = tx + ty * tbw;
+                cid_of[base + hits] = c;
+                ++hits;
+            }
+        }
+        for (uint32_t p = hits; p < pf_count; ++p) { tile_of[base + p] = sentinel; cid_of[base + p] = c; }
+    }
+
+    // ---- tile sort: stable by tile id, render.rs:792-794 -----------------------
+    std::vector<uint32_t> perm(I);
+    std::iota(perm.begin(), perm.end(), 0u);
+    std::stable_sort(perm.begin(), perm.end(), [&](uint32_t a, uint32_t b) { return tile_of[a] < tile_of[b]; });
+    uint64_t I_valid = 0;
+    f->isect_tile.resize(I);
+    f->isect_cid.resize(I);
+    for (uint64_t i = 0; i < I; ++i) {
+        f->isect_tile[i] = tile_of[perm[i]];
+        f->isect_cid[i] = cid_of[perm[i]];
+        if (f->isect_tile[i] < sentinel) ++I_valid;
+    }
+    f->isect_tile.resize(I_valid);   // sentinels sort last and are never read
+    f->isect_cid.resize(I_valid);
+
+    // ---- tile offsets, get_tile_offset.rs:11-59 ---------------------------------
+    f->tile_offsets.assign((size_t)f->T * 2, 0u);
+    for (uint64_t i = 0; i < I_valid; ++i) {
+        const uint32_t tid = f->isect_tile[i];
+        if (i == 0 || f->isect_tile[i - 1] != tid) f->tile_offsets[(size_t)tid * 2] = (uint32_t)i;
+        if (i + 1 == I_valid || f->isect_tile[i + 1] != tid) f->tile_offsets[(size_t)tid * 2 + 1] = (uint32_t)(i + 1);
+    }
+    f->tile_offsets_shrunk = f->tile_offsets;
+
+    // ---- rasterize, kernels/rasterize.rs:109-420 --------------------------------
+    const uint32_t C = f->out_ch;
+    if (bwd_info) f->out_img.assign((size_t)W * H * C, 0.0f); else f->out_packed.assign((size_t)W * H, 0u);
+    f->visible.assign(N, 0.0f);
+    uint64_t evals_total = 0;
+    #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads) reduction(+ : evals_total)
+    for (int64_t ti = 0; ti < (int64_t)f->T; ++ti) {
+        const uint32_t tile = (uint32_t)ti;
+        const uint32_t tx = tile % tbw, ty = tile / tbw;
+        const uint32_t lo = f->tile_offsets[(size_t)tile * 2], hi = f->tile_offsets[(size_t)tile * 2 + 1];
+        std::vector<RasterSplat> list(hi - lo);
+        for (uint32_t i = lo; i < hi; ++i) {
+            const uint32_t c = f->isect_cid[i];
+            const float* row = &f->projected[(size_t)c * 9];
+            RasterSplat s;
+            s.x = row[0]; s.y = row[1]; s.c00 = row[2]; s.c01 = row[3]; s.c11 = row[4];
+            s.A = 0.5f * row[2]; s.B = row[3]; s.C = 0.5f * row[4];
+            s.opac = row[5]; s.r = row[6]; s.g = row[7]; s.b = row[8];
+            s.gid = f->global_from_compact[c];
+            if (geometry) { const float* a = &f->aux[(size_t)c * 4]; s.z = a[0]; s.nx = a[1]; s.ny = a[2]; s.nz = a[3]; }
+            else { s.z = s.nx = s.ny = s.nz = 0.0f; }
+            list[i - lo] = s;
+        }
+        uint32_t max_useful = lo;
+        for (uint32_t py = ty * TILE_W; py < ty * TILE_W + TILE_W; ++py) {
+            for (uint32_t px = tx * TILE_W; px < tx * TILE_W + TILE_W; ++px) {
+                if (px >= W || py >= H) continue;
+                const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+                float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+                float depth_acc = 0.0f, median = 0.0f, dist_b = 0.0f, dist_c = 0.0f, nx = 0.0f, ny = 0.0f, nz = 0.0f;
+                uint32_t median_id = 0xFFFFFFFFu;
+                uint32_t last_useful = lo;
+                for (uint32_t i = lo; i < hi; ++i) {
+                    const RasterSplat& s = list[i - lo];
+                    ++evals_total;
+                    const float dx = pcx - s.x, dy = pcy - s.y;
+                    const float sigma = std::fma(std::fma(s.A, dx, s.B * dy), dx, (s.C * dy) * dy);
+                    const float G = expf_c(-sigma);
+                    const float alpha = fmin_(0.999f, s.opac * G);
+                    const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
+                    if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
+                    const float alpha_eff = alpha * w_cut;
+                    const float next_t = T * (1.0f - alpha_eff);
+                    if (next_t <= 1.0e-4f) break;
+                    if (bwd_info) f->visible[s.gid] = 1.0f;   // benign race: every writer stores 1
+                    const float vis = alpha_eff * T;
+                    cr = std::fma(fmax_(s.r, 0.0f), vis, cr);
+                    cg = std::fma(fmax_(s.g, 0.0f), vis, cg);
+                    cb = std::fma(fmax_(s.b, 0.0f), vis, cb);
+                    if (geometry) {
+                        depth_acc = std::fma(s.z, vis, depth_acc);
+                        if (T > 0.5f) { median = s.z; median_id = i; }
+                        const float m = dist_depth(s.z);
+                        dist_b = std::fma(m, vis, dist_b);
+                        dist_c = std::fma(m * m, vis, dist_c);
+                        nx = std::fma(s.nx, vis, nx);
+                        ny = std::fma(s.ny, vis, ny);
+                        nz = std::fma(s.nz, vis, nz);
+                    }
+                    T = next_t;
+                    last_useful = i + 1;
+                }
+                max_useful = std::max(max_useful, last_useful);
+                const float fr = std::fma(T, f->bg[0], cr);
+                const float fg = std::fma(T, f->bg[1], cg);
+                const float fb = std::fma(T, f->bg[2], cb);
+                const float fa = 1.0f - T;
+                const size_t pid = (size_t)py * W + px;
+                if (bwd_info) {
+                    float* o = &f->out_img[pid * C];
+                    o[0] = fr; o[1] = fg; o[2] = fb; o[3] = fa;
+                    if (geometry) {
+                        o[4] = depth_acc; o[5] = median; o[6] = nx; o[7] = ny; o[8] = nz;
+                        o[9] = dist_b; o[10] = dist_c; o[11] = u2f(median_id);
+                    }
+                } else {
+                    const uint32_t r8 = f2u32_sat(clampf(fr * 255.0f, 0.0f, 255.0f));
+                    const uint32_t g8 = f2u32_sat(clampf(fg * 255.0f, 0.0f, 255.0f));
+                    const uint32_t b8 = f2u32_sat(clampf(fb * 255.0f, 0.0f, 255.0f));
+                    const uint32_t a8 = f2u32_sat(clampf(fa * 255.0f, 0.0f, 255.0f));
+                    f->out_packed[pid] = r8 | (g8 << 8) | (b8 << 16) | (a8 << 24);
+                }
+            }
+        }
+        if (bwd_info) f->tile_offsets_shrunk[(size_t)tile * 2 + 1] = max_useful;
+    }
+    f->evals = evals_total;
+    *out = f.release();
+    return 0;
+}
+
+extern "C" void or_fwd_get_info(const or_fwd* f, or_fwd_info* info) {
+    info->num_splats = f->N;
+    info->num_visible = f->V;
+    info->num_intersections = (uint32_t)f->isect_tile.size();
+    info->num_tiles = f->T;
+    info->tile_bw = f->tbw; info->tile_bh = f->tbh;
+    info->img_w = f->W; info->img_h = f->H;
+    info->out_channels = (f->flags & OR_FLAG_BWD_INFO) ? f->out_ch : 1;
+    info->num_evaluations = f->evals;
+}
+
+extern "C" int or_fwd_get(const or_fwd* f, int field, void* dst) {
+    auto cp = [&](const auto& v) { std::memcpy(dst, v.data(), v.size() * sizeof(v[0])); return 0; };
+    switch (field) {
+    case OR_F_INTERSECT_COUNTS: return cp(f->intersect_counts);
+    case OR_F_MAX_RADIUS: return cp(f->max_radius);
+    case OR_F_OPACITIES: return cp(f->opacities);
+    case OR_F_GLOBAL_FROM_COMPACT: return cp(f->global_from_compact);
+    case OR_F_DEPTHS: return cp(f->depths);
+    case OR_F_PROJECTED: return cp(f->projected);
+    case OR_F_AUX: return cp(f->aux);
+    case OR_F_ISECT_TILE: return cp(f->isect_tile);
+    case OR_F_ISECT_GID: {
+        uint32_t* d = (uint32_t*)dst;
+        for (size_t i = 0; i < f->isect_cid.size(); ++i) d[i] = f->global_from_compact[f->isect_cid[i]];
+        return 0;
+    }
+    case OR_F_TILE_OFFSETS: return cp(f->tile_offsets);
+    case OR_F_TILE_OFFSETS_SHRUNK: return cp(f->tile_offsets_shrunk);
+    case OR_F_VISIBLE: return cp(f->visible);
+    case OR_F_OUT_IMG: return (f->flags & OR_FLAG_BWD_INFO) ? cp(f->out_img) : cp(f->out_packed);
+    default: return 1;
+    }
+}
+
+extern "C" void or_fwd_free(or_fwd* f) { delete f; }
+
+extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threads,
+                                  float* v_combined_out, float* v_transforms, float* v_sh,
+                                  float* v_raw_opac, float* v_refine) {
+    if (!f || !v_out || !(f->flags & OR_FLAG_BWD_INFO)) return 1;
+    const int nthreads = resolve_threads(threads);
+    const or_camera& u = f->cam;
+    const uint32_t W = f->W, H = f->H, N = f->N, K = f->K, C = f->out_ch;
+    const bool smooth = f->flags & OR_FLAG_SMOOTH_CUTOFF;
+    const size_t I = f->isect_tile.size();
+    // Per-(tile, splat) partial sums of the raster VJP, one row per sorted
+    // intersection, summed afterwards in intersection order so the result
+    // does not depend on the thread count.
+    std::vector<double> part((size_t)I * 10, 0.0);
+    const float img_w = (float)W, img_h = (float)H;
+
+    // ---- raster VJP, bwd/kernels/rasterize_backwards_planes.rs:112-682 ----------
+    #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+    for (int64_t ti = 0; ti < (int64_t)f->T; ++ti) {
+        const uint32_t tile = (uint32_t)ti;
+        const uint32_t tx = tile % f->tbw, ty = tile / f->tbw;
+        const uint32_t lo = f->tile_offsets_shrunk[(size_t)tile * 2], hi = f->tile_offsets_shrunk[(size_t)tile * 2 + 1];
+        if (hi <= lo) continue;
+        for (uint32_t py = ty * TILE_W; py < ty * TILE_W + TILE_W; ++py) {
+            for (uint32_t px = tx * TILE_W; px < tx * TILE_W + TILE_W; ++px) {
+                if (px >= W || py >= H) continue;
+                const size_t base = ((size_t)py * W + px) * C;
+                const float final_a = f->out_img[base + 3];
+                const float t_final = 1.0f - final_a;
+                float sr = f->out_img[base] - t_final * f->bg[0];
+                float sg = f->out_img[base + 1] - t_final * f->bg[1];
+                float sb = f->out_img[base + 2] - t_final * f->bg[2];
+                float T = 1.0f;
+                const float vr = v_out[base], vg = v_out[base + 1], vb = v_out[base + 2];
+                const float v_t = (v_out[base + 3] - (f->bg[0] * vr + f->bg[1] * vg + f->bg[2] * vb)) * t_final;
+                const float refine_scale = 1.0f / fmax_(final_a, 1.0e-5f);
+                const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+                for (uint32_t i = lo; i < hi && T > 1.0e-4f; ++i) {
+                    const float* row = &f->projected[(size_t)f->isect_cid[i] * 9];
+                    const float x = row[0], y = row[1], c00 = row[2], c01 = row[3], c11 = row[4];
+                    const float opac = row[5], cr = row[6], cgc = row[7], cbc = row[8];
+                    const float dx = pcx - x, dy = pcy - y;
+                    const float sigma = std::fma(std::fma(0.5f * c00, dx, c01 * dy), dx, ((0.5f * c11) * dy) * dy);
+                    const float G = expf_c(-sigma);
+                    const float alpha = fmin_(0.999f, opac * G);
+                    const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
+                    if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
+                    const float alpha_eff = alpha * w_cut;
+                    const float next_t = T * (1.0f - alpha_eff);
+                    if (next_t <= 1.0e-4f) { T = 0.0f; break; }
+                    const float vis = alpha_eff * T;
+                    double* p = &part[(size_t)i * 10];
+                    const float clr = fmax_(cr, 0.0f), clg = fmax_(cgc, 0.0f), clb = fmax_(cbc, 0.0f);
+                    if (cr >= 0.0f) p[5] += (double)vis * vr;
+                    if (cgc >= 0.0f) p[6] += (double)vis * vg;
+                    if (cbc >= 0.0f) p[7] += (double)vis * vb;
+                    const double ra = 1.0 / (1.0 - (double)alpha_eff);
+                    const double dot_rgb = (((double)T * clr - sr) * vr + ((double)T * clg - sg) * vg + ((double)T * clb - sb) * vb) * ra;
+                    const double v_alpha_eff = dot_rgb + (double)v_t * ra;
+                    const double v_alpha = smooth ? v_alpha_eff * ((double)w_cut + (double)alpha * alpha_cutoff_weight_deriv(alpha)) : v_alpha_eff;
+                    const double v_sigma = -(double)alpha * v_alpha;
+                    const double bdx = -(double)dx, bdy = -(double)dy;   // x - pixel
+                    const double vxy_x = v_sigma * ((double)c00 * bdx + (double)c01 * bdy);
+                    const double vxy_y = v_sigma * ((double)c01 * bdx + (double)c11 * bdy);
+                    if (opac * G <= 0.999f) {
+                        p[2] += 0.5 * v_sigma * bdx * bdx;
+                        p[3] += v_sigma * bdx * bdy;
+                        p[4] += 0.5 * v_sigma * bdy * bdy;
+                        p[0] += vxy_x;
+                        p[1] += vxy_y;
+                        p[8] += v_alpha * (double)G;
+                        p[9] += std::sqrt(vxy_x * img_w * vxy_x * img_w + vxy_y * img_h * vxy_y * img_h) * (double)refine_scale;
+                    }
+                    sr = sr - vis * clr;
+                    sg = sg - vis * clg;
+                    sb = sb - vis * clb;
+                    T = next_t;
+                }
+            }
+        }
+    }
+    // Per-splat sums in sorted-intersection order.
+    std::vector<double> vc((size_t)N * 10, 0.0);
+    for (size_t i = 0; i < I; ++i) {
+        const uint32_t g = f->global_from_compact[f->isect_cid[i]];
+        for (int k = 0; k < 10; ++k) vc[(size_t)g * 10 + k] += part[i * 10 + k];
+    }
+    if (v_combined_out) for (size_t i = 0; i < (size_t)N * 10; ++i) v_combined_out[i] = (float)vc[i];
+
+    // ---- projection VJP, bwd/kernels/project_backwards.rs:132-424 ---------------
+    if (v_transforms) std::memset(v_transforms, 0, sizeof(float) * (size_t)N * 10);
+    if (v_sh) std::memset(v_sh, 0, sizeof(float) * (size_t)N * K * 3);
+    if (v_raw_opac) std::memset(v_raw_opac, 0, sizeof(float) * N);
+    if (v_refine) std::memset(v_refine, 0, sizeof(float) * N);
+    const uint32_t degree = f->degree;
+    #pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int64_t ci = 0; ci < (int64_t)f->V; ++ci) {
+        const uint32_t g = f->global_from_compact[(size_t)ci];
+        float rg[10];
+        bool any = false;
+        for (int k = 0; k < 10; ++k) { rg[k] = (float)vc[(size_t)g * 10 + k]; any = any || rg[k] != 0.0f; }
+        if (!any) continue;
+        const float* t = f->transforms + (size_t)g * 10;
+        const float* cb = f->sh + (size_t)g * K * 3;
+        const V3 mean = v3(t[0], t[1], t[2]);
+        const V3 sc = v3(expf_c(t[7] + f->lso), expf_c(t[8] + f->lso), expf_c(t[9] + f->lso));
+        const Q4 qu{t[3], t[4], t[5], t[6]};
+        const float raw = f->raw_opac[g];
+        const Q4 q = qnormalize(qu);
+        const float opac_sig = sigmoid(raw);
+        // SH + view-direction VJP
+        const V3 u_world = sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
+        const float u_len = length(u_world);
+        const V3 vdir = scale(u_world, 1.0f / u_len);
+        const V3 v_color = v3(rg[5], rg[6], rg[7]);
+        if (v_sh) {
+            float Y[25];
+            const int n = sh_basis(degree, vdir, Y);
+            float* o = v_sh + (size_t)g * K * 3;
+            for (int k = 0; k < n; ++k) { o[3 * k] = v_color.x * Y[k]; o[3 * k + 1] = v_color.y * Y[k]; o[3 * k + 2] = v_color.z * Y[k]; }
+        }
+        const V3 v_v_sh = sh_viewdir_vjp(cb, degree, vdir, v_color);
+        const float v_dot = dot(vdir, v_v_sh);
+        const V3 v_mean_sh = scale(sub(v_v_sh, scale(vdir, v_dot)), 1.0f / u_len);
+        const V3 mean_c = world_to_cam(mean, u);
+        const M3 R = quat_to_mat3(q);
+        const M3 Mm = mul_diag(R, sc);
+        const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
+        const float v_opac_base = 1.0f * rg[8];
+        const S2 conic_inv = s2_inverse(cov);
+        const S2 v_inv{rg[2], rg[3] * 0.5f, rg[4]};
+        const S2 v_cov2d = inverse2x2_vjp(conic_inv, v_inv);
+        const S3 covar = outer_self(Mm);
+        const M3 vrot = view_rot(u);
+        const S3 cov_c = s3_congruence(covar, vrot);
+        const M23 J = project_jacobian(mean_c, u);
+        const V3 v_mean_c = (u.model == OR_MODEL_KB4) ? projection_vjp_kb4(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]})
+                                                        : projection_vjp_pinhole(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]});
+        const S3 vcc = m23_tcongruence_s2(J, v_cov2d);
+        const V3 v_mean = add(tmul_vec3(vrot, v_mean_c), v_mean_sh);
+        const M3 v_m = s3_mul_mat3(s3_scale(s3_tcongruence(vcc, vrot), 2.0f), Mm);
+        const V3 v_log{dot(R.c0, v_m.c0) * sc.x, dot(R.c1, v_m.c1) * sc.y, dot(R.c2, v_m.c2) * sc.z};
+        // ratio_sq = 1 and floor.opac * (1 - 1) = 0 without a scale floor.
+        const V3 v_scale_exp{v_log.x * 1.0f + v_opac_base * opac_sig * 0.0f,
+                             v_log.y * 1.0f + v_opac_base * opac_sig * 0.0f,
+                             v_log.z * 1.0f + v_opac_base * opac_sig * 0.0f};
+        const Q4 q_grad = quat_to_mat_vjp(q, mul_diag(v_m, sc));
+        const Q4 v_q = apply_normalize_vjp(qu, q_grad);
+        const float v_raw = v_opac_base * 1.0f * opac_sig * (1.0f - opac_sig);
+        if (v_raw_opac) v_raw_opac[g] = v_raw;
+        if (v_refine) v_refine[g] = clampf(is_finite(rg[9]) ? rg[9] : 0.0f, 0.0f, 1.0e32f);
+        if (v_transforms) {
+            float* o = v_transforms + (size_t)g * 10;
+            o[0] = v_mean.x; o[1] = v_mean.y; o[2] = v_mean.z;
+            o[3] = v_q.w; o[4] = v_q.x; o[5] = v_q.y; o[6] = v_q.z;
+            o[7] = v_scale_exp.x; o[8] = v_scale_exp.y; o[9] = v_scale_exp.z;
+        }
+    }
+    return 0;
+}
+
+// ---- sort & scan ---------------------------------------------------------------
+extern "C" void or_radix_argsort_u32(const uint32_t* keys, const uint32_t* vals, uint32_t n,
+                                     uint32_t skip_bits, uint32_t sorting_bits,
+                                     uint32_t* out_keys, uint32_t* out_vals) {
+    if (n == 0) return;
+    if (sorting_bits == 0) {
+        std::memcpy(out_keys, keys, sizeof(uint32_t) * n);
+        std::memcpy(out_vals, vals, sizeof(uint32_t) * n);
+        return;
+    }
+    const uint32_t passes = (sorting_bits + 7) / 8;
+    const uint32_t width = passes * 8;
+    const uint64_t mask = (width >= 64) ? ~0ull : ((1ull << width) - 1ull);
+    std::vector<uint32_t> idx(n);
+    std::iota(idx.begin(), idx.end(), 0u);
+    std::stable_sort(idx.begin(), idx.end(), [&](uint32_t a, uint32_t b) {
+        return (((uint64_t)keys[a] >> skip_bits) & mask) < (((uint64_t)keys[b] >> skip_bits) & mask);
+    });
+    for (uint32_t i = 0; i < n; ++i) { out_keys[i] = keys[idx[i]]; out_vals[i] = vals[idx[i]]; }
+}
+
+extern "C" void or_prefix_sum_u32(const uint32_t* in, uint32_t* out, uint32_t n) {
+    uint32_t acc = 0;
+    for (uint32_t i = 0; i < n; ++i) { acc += in[i]; out[i] = acc; }
+}
+
+// ---- exported math -------------------------------------------------------------
+extern "C" float or_expf(float x) { return expf_c(x); }
+extern "C" float or_logf(float x) { return logf_c(x); }
+extern "C" float or_atan2f(float y, float x) { return atan2f_c(y, x); }
+extern "C" void or_expf_n(const float* x, float* y, uint64_t n) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; ++i) y[i] = expf_c(x[i]);
+}
+extern "C" void or_logf_n(const float* x, float* y, uint64_t n) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; ++i) y[i] = logf_c(x[i]);
+}
+extern "C" void or_atan2f_n(const float* y, const float* x, float* r, uint64_t n) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; ++i) r[i] = atan2f_c(y[i], x[i]);
+}
+extern "C" void or_sh_basis(uint32_t degree, const float v[3], float* out) {
+    sh_basis(degree, v3(v[0], v[1], v[2]), out);
+}
+
+// ---- camera host math, camera.rs:99-237 (f64) ----------------------------------
+namespace {
+double kb4_d(double th, const float* k) {
+    const double t2 = th * th, t3 = t2 * th, t5 = t3 * t2, t7 = t5 * t2, t9 = t7 * t2;
+    return th + (double)k[0] * t3 + (double)k[1] * t5 + (double)k[2] * t7 + (double)k[3] * t9;
+}
+double kb4_dd(double th, const float* k) {
+    const double t2 = th * th, t4 = t2 * t2, t6 = t4 * t2, t8 = t6 * t2;
+    return 1.0 + 3.0 * (double)k[0] * t2 + 5.0 * (double)k[1] * t4 + 7.0 * (double)k[2] * t6 + 9.0 * (double)k[3] * t8;
+}
+double kb4_fold(const float* k) {
+    const int STEPS = 128;
+    const double step = M_PI / STEPS;
+    double lo = 0.0, hi = M_PI;
+    bool found = false;
+    for (int i = 1; i <= STEPS; ++i) {
+        const double th = i * step;
+        if (kb4_dd(th, k) <= 0.0) { hi = th; found = true; break; }
+        lo = th;
+    }
+    if (!found) return M_PI;
+    for (int it = 0; it < 64; ++it) {
+        const double mid = 0.5 * (lo + hi);
+        if (kb4_dd(mid, k) > 0.0) lo = mid; else hi = mid;
+        if (hi - lo < 1e-12) break;
+    }
+    return 0.5 * (lo + hi);
+}
+double kb4_inv(double target, const float* k) {
+    if (target <= 0.0) return 0.0;
+    const double fold = kb4_fold(k);
+    if (target >= kb4_d(fold, k)) return fold;
+    double lo = 0.0, hi = fold;
+    for (int it = 0; it < 100; ++it) {
+        const double mid = 0.5 * (lo + hi);
+        if (kb4_d(mid, k) < target) lo = mid; else hi = mid;
+        if (hi - lo < 1e-14) break;
+    }
+    return 0.5 * (lo + hi);
+}
+} // namespace
+
+extern "C" double or_kb4_d(double theta, const float kb4[4]) { return kb4_d(theta, kb4); }
+extern "C" double or_kb4_dd_dtheta(double theta, const float kb4[4]) { return kb4_dd(theta, kb4); }
+extern "C" double or_kb4_invert_d(double target, const float kb4[4]) { return kb4_inv(target, kb4); }
+extern "C" double or_fov_to_focal(double fov, uint32_t pixels, int model, const float kb4[4]) {
+    const double half = fov / 2.0;
+    const double r_pix = (double)pixels / 2.0;
+    const double projected = (model == OR_MODEL_KB4) ? kb4_d(half, kb4) : std::tan(half);
+    return r_pix / projected;
+}
+extern "C" double or_focal_to_fov(double focal, uint32_t pixels, int model, const float kb4[4]) {
+    const double r_pix = (double)pixels / 2.0;
+    const double r_norm = r_pix / focal;
+    const double half = (model == OR_MODEL_KB4) ? kb4_inv(r_norm, kb4) : std::atan(r_norm);
+    return 2.0 * half;
+}
+extern "C" double or_max_render_theta(int model, const float kb4[4]) {
+    return (model == OR_MODEL_KB4) ? kb4_fold(kb4) : M_PI;
+}

@@ -1,0 +1,118 @@
+/*
+ * vs_oracle.h -- C ABI of the CPU oracle.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is a scalar/OpenMP CPU restatement
+ * of the reference Gaussian-splat render path (voyager-so/vauss,
+ * crates/splat-train-render, splat-train-sort, splat-train-scan).  It is
+ * loaded by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline
+ * leg only, as the checker.  Nothing in the product links or calls it.
+ *
+ * The camera struct below has the same field order and sizes as
+ * `vs_camera` in include/vsplat.h so one ctypes struct feeds both sides; it
+ * is declared here independently on purpose.
+ */
+#ifndef VS_ORACLE_H
+#define VS_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OR_MODEL_PINHOLE = 0, OR_MODEL_KB4 = 1 };
+
+/* Device-side ProjectUniforms of the reference
+ * (crates/splat-train-render/src/kernels/types.rs:53-82) minus the sizes. */
+typedef struct or_camera {
+    int32_t model;
+    float fx, fy, cx, cy;
+    float kb4[4];
+    float viewmat[12];          /* 3x4 column-major: col0, col1, col2, translation */
+    float cam_pos[3];
+    float half_max_render_fov;
+    float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y, lim_r;
+} or_camera;
+
+/* Render flags (RasterPass semantics, gaussian_splats.rs:32-107). */
+enum {
+    OR_FLAG_BWD_INFO = 1,       /* float RGBA image + visible marks + shrunk tile ends */
+    OR_FLAG_GEOMETRY = 2,       /* 12-channel output with depth/normal/distortion */
+    OR_FLAG_SMOOTH_CUTOFF = 4,  /* C^1 alpha cutoff (BackwardSmoothCutoff) */
+};
+
+typedef struct or_fwd or_fwd;
+
+/* Forward render.  `threads` <= 0 uses every OpenMP thread. */
+int or_render_forward(const or_camera* cam, uint32_t img_w, uint32_t img_h,
+                      const float* transforms, const float* sh_coeffs, uint32_t sh_degree,
+                      const float* raw_opacities, uint32_t num_splats, float log_scale_offset,
+                      const float background[3], int flags, int threads, or_fwd** out);
+
+/* Sizes of the result arrays. */
+typedef struct or_fwd_info {
+    uint32_t num_splats, num_visible, num_intersections, num_tiles;
+    uint32_t tile_bw, tile_bh, img_w, img_h, out_channels;
+    uint64_t num_evaluations;   /* pixel-splat evaluations actually performed */
+} or_fwd_info;
+void or_fwd_get_info(const or_fwd* f, or_fwd_info* info);
+
+/* Copy one result array out.  Fields: */
+enum {
+    OR_F_INTERSECT_COUNTS = 0,  /* u32 [N]   tiles hit per global splat (0 if culled) */
+    OR_F_MAX_RADIUS = 1,        /* f32 [N] */
+    OR_F_OPACITIES = 2,         /* f32 [N] */
+    OR_F_GLOBAL_FROM_COMPACT = 3, /* u32 [V] visible splats in compaction order */
+    OR_F_DEPTHS = 4,            /* f32 [V] view-space z, compaction order */
+    OR_F_PROJECTED = 5,         /* f32 [V,9] x,y,c00,c01,c11,opac,r,g,b */
+    OR_F_AUX = 6,               /* f32 [V,4] z,nx,ny,nz (geometry) */
+    OR_F_ISECT_TILE = 7,        /* u32 [I] tile id per sorted intersection */
+    OR_F_ISECT_GID = 8,         /* u32 [I] global splat id per sorted intersection */
+    OR_F_TILE_OFFSETS = 9,      /* u32 [T,2] before the raster shrinks the ends */
+    OR_F_TILE_OFFSETS_SHRUNK = 10, /* u32 [T,2] after it */
+    OR_F_VISIBLE = 11,          /* f32 [N] */
+    OR_F_OUT_IMG = 12,          /* f32 [H,W,C] (C=4 or 12) or u32 [H,W] packed */
+};
+int or_fwd_get(const or_fwd* f, int field, void* dst);
+void or_fwd_free(or_fwd* f);
+
+/* Backward of the same render: v_out is [H,W,C] (C as the forward image).
+ * All outputs dense per global splat; pass NULL to skip one. */
+int or_render_backward(const or_fwd* f, const float* v_out, int threads,
+                       float* v_combined /* [N,10] */, float* v_transforms /* [N,10] */,
+                       float* v_sh /* [N,K,3] */, float* v_raw_opac /* [N] */,
+                       float* v_refine /* [N] */);
+
+/* Stable LSD radix argsort restated (splat-train-sort/src/lib.rs:40-189):
+ * sorts by key bits [skip, skip + 8*ceil(bits/8)). */
+void or_radix_argsort_u32(const uint32_t* keys, const uint32_t* vals, uint32_t n,
+                          uint32_t skip_bits, uint32_t sorting_bits,
+                          uint32_t* out_keys, uint32_t* out_vals);
+/* Inclusive prefix sum (splat-train-scan/src/lib.rs:24-83). */
+void or_prefix_sum_u32(const uint32_t* in, uint32_t* out, uint32_t n);
+
+/* Arithmetic contract transcendentals, exported for the tests. */
+float or_expf(float x);
+float or_logf(float x);
+float or_atan2f(float y, float x);
+void or_expf_n(const float* x, float* y, uint64_t n);
+void or_logf_n(const float* x, float* y, uint64_t n);
+void or_atan2f_n(const float* y, const float* x, float* r, uint64_t n);
+
+/* SH basis values Y_k(v) for degree <= 4 (kernels/sh.rs:51-140), for tests. */
+void or_sh_basis(uint32_t degree, const float v[3], float* out /* [(d+1)^2] */);
+
+/* Camera host math restated from camera.rs (f64). model: 0 pinhole, 1 KB4. */
+double or_fov_to_focal(double fov, uint32_t pixels, int model, const float kb4[4]);
+double or_focal_to_fov(double focal, uint32_t pixels, int model, const float kb4[4]);
+double or_max_render_theta(int model, const float kb4[4]);
+double or_kb4_d(double theta, const float kb4[4]);
+double or_kb4_dd_dtheta(double theta, const float kb4[4]);
+double or_kb4_invert_d(double target, const float kb4[4]);
+
+int or_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

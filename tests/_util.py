@@ -1,0 +1,76 @@
+"""Shared helpers for the tests: device readback and scene upload."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+_HIP = None
+
+
+def _hip():
+    global _HIP
+    if _HIP is None:
+        import torch  # noqa: F401  (the HIP runtime torch loaded)
+        _HIP = C.CDLL("libamdhip64.so.7")
+        _HIP.hipMemcpy.restype = C.c_int
+        _HIP.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    return _HIP
+
+
+def dev_to_numpy(ptr, shape, dtype) -> np.ndarray:
+    """Copy `shape` elements of `dtype` from a device pointer the library owns."""
+    import torch
+    torch.cuda.synchronize()
+    out = np.empty(shape, dtype)
+    if out.size:
+        rc = _hip().hipMemcpy(out.ctypes.data_as(C.c_void_p), C.c_void_p(ptr), out.nbytes, 2)
+        assert rc == 0, f"hipMemcpy failed ({rc})"
+    return out
+
+
+def to_gpu(scene):
+    import torch
+    return (torch.from_numpy(scene.transforms).cuda(), torch.from_numpy(scene.sh_coeffs).cuda(),
+            torch.from_numpy(scene.raw_opacities).cuda())
+
+
+def l1_cotangent_np(img: np.ndarray, gt: np.ndarray, mask=None) -> np.ndarray:
+    """sign(pred - gt) / (3 * count) on rgb, 0 on the other channels (closed form)."""
+    v = np.zeros_like(img, dtype=np.float32)
+    h, w = img.shape[:2]
+    count = h * w if mask is None else int(mask.sum())
+    d = img[..., :3] - gt
+    s = np.sign(d).astype(np.float32) * np.float32(1.0 / (3.0 * count))
+    if mask is not None:
+        s = s * mask[..., None]
+    v[..., :3] = s
+    return v
+
+
+def circle_mask(img_size, center, radius) -> np.ndarray:
+    w, h = img_size
+    yy, xx = np.mgrid[0:h, 0:w]
+    dx = xx.astype(np.float32) + np.float32(0.5) - np.float32(center[0])
+    dy = yy.astype(np.float32) + np.float32(0.5) - np.float32(center[1])
+    return (dx * dx + dy * dy <= np.float32(radius) * np.float32(radius)).astype(np.float32)
+
+
+def gpu_state_arrays(out):
+    """Intermediate buffers of a GPU forward as numpy arrays keyed like the oracle's."""
+    v = out.state.view()
+    n, i = v.num_splats, v.num_intersections
+    keys = dev_to_numpy(v.isect_keys, (i,), np.uint64)
+    gids = dev_to_numpy(v.isect_gids, (i,), np.uint32)
+    return {
+        "view": v,
+        "tile": (keys >> np.uint64(v.depth_shift)).astype(np.uint32),
+        "depth_bits": ((keys & np.uint64((1 << v.depth_shift) - 1)) + np.uint64(v.depth_min)).astype(np.uint32),
+        "gid": gids,
+        "counts": dev_to_numpy(v.intersect_counts, (n,), np.uint32),
+        "proj_a": dev_to_numpy(v.proj_xy_conic, (n, 4), np.float32),
+        "proj_b": dev_to_numpy(v.proj_c11_opac_rg, (n, 4), np.float32),
+        "proj_c": dev_to_numpy(v.proj_b, (n,), np.float32),
+        "proj_aux": dev_to_numpy(v.proj_aux, (n, 4), np.float32) if v.proj_aux else None,
+        "ranges": dev_to_numpy(v.tile_ranges, (v.tile_bh, v.tile_bw, 2), np.uint32),
+    }

@@ -1,0 +1,148 @@
+"""GPU parity of the render path against the CPU oracle on identical seeded inputs.
+
+Bars (the contract of this build):
+  * tile-intersection counts, the sorted (tile, depth, splat) order, tile
+    ranges, projected rows and aux outputs: bit for bit;
+  * forward RGBA (and geometry channels): within 1e-4 absolute (expected
+    bit-exact: the kernels follow the oracle's arithmetic contract);
+  * per-splat gradients: within 1e-3 relative / 1e-5 absolute, and within
+    1e-3 of the largest gradient of the same parameter group (f32 atomics
+    reorder the per-splat sums).
+"""
+import numpy as np
+import pytest
+import torch
+
+import vauss_amd as va
+from vauss_amd import scenes
+from oracle import pyoracle as po
+from tests._util import circle_mask, gpu_state_arrays, l1_cotangent_np, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+CASES = [("c1", None, 0), ("c2", 20_000, 0), ("c3", 20_000, 3), ("c4", 20_000, 0), ("c5", 20_000, 0)]
+
+
+def _render_both(cfg, n, view, pass_=va.RasterPass.BACKWARD, background=(0.0, 0.0, 0.0)):
+    w = scenes.workload(cfg, n)
+    cam = w.cameras[view].uniforms(w.img_size)
+    t, s, o = to_gpu(w.scene)
+    print(f"[case] {cfg} n={w.scene.num_splats} view={view} pass={pass_.name}", flush=True)
+    out = va.render(cam, w.img_size, t, s, o, background=background, pass_=pass_)
+    flags = po.FLAG_BWD_INFO if pass_.bwd_info() else 0
+    if pass_ == va.RasterPass.GEOMETRY:
+        flags |= po.FLAG_GEOMETRY
+    if pass_ == va.RasterPass.BACKWARD_SMOOTH_CUTOFF:
+        flags |= po.FLAG_SMOOTH_CUTOFF
+    ref = po.render_forward(cam, w.img_size, w.scene.transforms, w.scene.sh_coeffs, w.scene.raw_opacities,
+                            background=background, flags=flags)
+    return w, (t, s, o), out, ref
+
+
+def _check_forward(out, ref, gpu):
+    info = ref.info
+    assert out.aux.num_visible == info.num_visible
+    assert out.aux.num_intersections == info.num_intersections
+    # per-splat tile counts, bit for bit
+    np.testing.assert_array_equal(gpu["counts"], ref.get(po.F_INTERSECT_COUNTS))
+    # sorted intersection order: tile, then raw depth bits, then splat id
+    np.testing.assert_array_equal(gpu["tile"], ref.get(po.F_ISECT_TILE))
+    np.testing.assert_array_equal(gpu["gid"], ref.get(po.F_ISECT_GID))
+    np.testing.assert_array_equal(gpu["ranges"], ref.get(po.F_TILE_OFFSETS))
+    # projected rows of the visible splats
+    gfc = ref.get(po.F_GLOBAL_FROM_COMPACT)
+    proj = ref.get(po.F_PROJECTED)
+    got = np.concatenate([gpu["proj_a"][gfc], gpu["proj_b"][gfc], gpu["proj_c"][gfc, None]], axis=1)
+    got = got[:, [0, 1, 2, 3, 4, 5, 6, 7, 8]]
+    np.testing.assert_array_equal(got.view(np.uint32), proj.view(np.uint32))
+    # the depth half of every packed key is the splat's raw view-z bits
+    depth_of = np.zeros(info.num_splats, np.uint32)
+    depth_of[gfc] = ref.get(po.F_DEPTHS).view(np.uint32)
+    np.testing.assert_array_equal(gpu["depth_bits"], depth_of[ref.get(po.F_ISECT_GID)])
+    # aux outputs
+    np.testing.assert_array_equal(out.aux.opacities.cpu().numpy().view(np.uint32), ref.get(po.F_OPACITIES).view(np.uint32))
+    np.testing.assert_array_equal(out.aux.max_radius.cpu().numpy().view(np.uint32), ref.get(po.F_MAX_RADIUS).view(np.uint32))
+
+
+@pytest.mark.parametrize("cfg,n,view", CASES)
+def test_forward_parity(cfg, n, view):
+    w, _, out, ref = _render_both(cfg, n, view)
+    gpu = gpu_state_arrays(out)
+    _check_forward(out, ref, gpu)
+    img = out.out_img.cpu().numpy()
+    rimg = ref.get(po.F_OUT_IMG)
+    diff = np.abs(img - rimg)
+    assert diff.max() <= 1e-4, f"max |rgba diff| {diff.max()}"
+    assert np.array_equal(img.view(np.uint32), rimg.view(np.uint32)), f"{(diff > 0).sum()} channels differ in the last bits"
+    np.testing.assert_array_equal(out.aux.visible.cpu().numpy(), ref.get(po.F_VISIBLE))
+    np.testing.assert_array_equal(out.aux.tile_offsets.cpu().numpy().view(np.uint32), ref.get(po.F_TILE_OFFSETS_SHRUNK))
+
+
+def _check_grads(got, want, name, rtol=1e-3, atol=1e-5, group_rtol=1e-3):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    bad = err > atol + rtol * np.abs(want)
+    assert not bad.any(), f"{name}: {bad.sum()} entries exceed 1e-3 rel / 1e-5 abs (max err {err.max():.3e})"
+    scale = np.abs(want).max(axis=0, keepdims=True) if want.ndim > 1 else np.abs(want).max()
+    tight = err > rtol * np.abs(want) + group_rtol * scale
+    assert not tight.any(), f"{name}: {tight.sum()} entries exceed 1e-3 of the group maximum (max err {err.max():.3e})"
+
+
+@pytest.mark.parametrize("cfg,n,view", [("c1", None, 0), ("c2", 20_000, 0), ("c3", 20_000, 5), ("c5", 20_000, 0)])
+def test_backward_parity(cfg, n, view):
+    w, (t, s, o), out, ref = _render_both(cfg, n, view)
+    img = out.out_img.cpu().numpy()
+    mask = circle_mask(w.img_size, w.mask_center, w.mask_radius) if w.mask_radius > 0 else None
+    v_out = l1_cotangent_np(img, scenes.loss_target(w.img_size), mask)
+    g = va.render_backward(out, t, s, o, torch.from_numpy(v_out).cuda())
+    rg = ref.backward(v_out)
+    vc = g.v_combined.cpu().numpy()
+    _check_grads(vc[:, 0:2], rg["v_combined"][:, 0:2], "v_xy")
+    _check_grads(vc[:, 2:5], rg["v_combined"][:, 2:5], "v_conic")
+    _check_grads(vc[:, 5:8], rg["v_combined"][:, 5:8], "v_rgb")
+    _check_grads(vc[:, 8], rg["v_combined"][:, 8], "v_opacity")
+    _check_grads(vc[:, 9], rg["v_combined"][:, 9], "v_refine")
+    vt = g.v_transforms.cpu().numpy()
+    _check_grads(vt[:, 0:3], rg["v_transforms"][:, 0:3], "v_means")
+    _check_grads(vt[:, 3:7], rg["v_transforms"][:, 3:7], "v_quats")
+    _check_grads(vt[:, 7:10], rg["v_transforms"][:, 7:10], "v_log_scales")
+    _check_grads(g.v_raw_opac.cpu().numpy(), rg["v_raw_opac"], "v_raw_opacity")
+    _check_grads(g.v_coeffs.cpu().numpy().reshape(len(vt), -1), rg["v_sh"].reshape(len(vt), -1), "v_sh")
+    _check_grads(g.v_refine_weight.cpu().numpy(), rg["v_refine"], "v_refine_weight")
+    assert np.isfinite(vt).all()
+
+
+def test_geometry_pass_parity():
+    w, _, out, ref = _render_both("c1", None, 0, pass_=va.RasterPass.GEOMETRY)
+    gpu = gpu_state_arrays(out)
+    _check_forward(out, ref, gpu)
+    gfc = ref.get(po.F_GLOBAL_FROM_COMPACT)
+    np.testing.assert_array_equal(gpu["proj_aux"][gfc].view(np.uint32), ref.get(po.F_AUX).view(np.uint32))
+    img = out.out_img.cpu().numpy()
+    rimg = ref.get(po.F_OUT_IMG)
+    assert img.shape == rimg.shape == (256, 256, 12)
+    assert np.abs(img[..., :11] - rimg[..., :11]).max() <= 1e-4
+    np.testing.assert_array_equal(img.view(np.uint32), rimg.view(np.uint32))
+
+
+def test_packed_forward_pass_parity():
+    w, _, out, ref = _render_both("c1", None, 0, pass_=va.RasterPass.FORWARD)
+    got = out.out_img.cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(got, ref.get(po.F_OUT_IMG))
+    assert out.state is None
+
+
+def test_smooth_cutoff_pass_parity():
+    w, (t, s, o), out, ref = _render_both("c1", None, 0, pass_=va.RasterPass.BACKWARD_SMOOTH_CUTOFF)
+    img = out.out_img.cpu().numpy()
+    np.testing.assert_array_equal(img.view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))
+    v_out = l1_cotangent_np(img, scenes.loss_target(w.img_size))
+    g = va.render_backward(out, t, s, o, torch.from_numpy(v_out).cuda())
+    rg = ref.backward(v_out)
+    _check_grads(g.v_transforms.cpu().numpy(), rg["v_transforms"], "v_transforms")
+
+
+def test_background_parity():
+    _, _, out, ref = _render_both("c1", 2000, 0, background=(0.7, 0.3, 0.1))
+    np.testing.assert_array_equal(out.out_img.cpu().numpy().view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))

@@ -1,0 +1,22 @@
+"""vauss_amd -- an MI355X (gfx950) Gaussian-splat rasterizer behind the
+splat-train-render / splat-train-sort call surface of voyager-so/vauss.
+
+The compute path is libvsplat.so (hand-written HIP kernels + C ABI,
+include/vsplat.h); this package is its host-side mirror.  Importing it
+loads torch first so the library shares torch's HIP runtime.
+"""
+from ._lib import VsError, load  # noqa: F401
+from .camera import Camera, KannalaBrandt4, PINHOLE, fov_to_focal, focal_to_fov, max_render_theta  # noqa: F401
+from .render import (  # noqa: F401
+    Context, ForwardState, RasterPass, RenderAux, RenderOutput, SplatGrads, SplatRenderMode,
+    l1_cotangent, prefix_sum, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
+    radix_argsort_with_count, render, render_backward, scan_in_place, sh_degree_from_coeffs, unpack_rgba8,
+)
+
+__all__ = [
+    "Camera", "KannalaBrandt4", "PINHOLE", "fov_to_focal", "focal_to_fov", "max_render_theta",
+    "Context", "ForwardState", "RasterPass", "RenderAux", "RenderOutput", "SplatGrads", "SplatRenderMode",
+    "VsError", "l1_cotangent", "load", "prefix_sum", "radix_argsort", "radix_argsort_skip_low_with_count",
+    "radix_argsort_u64", "radix_argsort_with_count", "render", "render_backward", "scan_in_place",
+    "sh_degree_from_coeffs", "unpack_rgba8",
+]

@@ -1,0 +1,492 @@
+// api.hip -- the C ABI of include/vsplat.h: argument checks, buffer planning,
+// the stage sequence of a render, and the sort / scan / loss entry points.
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+#include "vs_internal.h"
+
+using namespace vs;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+vs_status fail(vs_status st, const std::string& msg) {
+    g_last_error = msg;
+    return st;
+}
+vs_status hip_fail(hipError_t e, const char* what) {
+    return fail(e == hipErrorOutOfMemory ? VS_ERR_OOM : VS_ERR_HIP,
+                std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define VS_HIP(call, what)                                  \
+    do {                                                    \
+        hipError_t e_ = (call);                             \
+        if (e_ != hipSuccess) return hip_fail(e_, what);    \
+    } while (0)
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+uint32_t bit_length(uint64_t v) {
+    uint32_t b = 0;
+    while (v) { ++b; v >>= 1; }
+    return b;
+}
+
+enum Stage { ST_PROJECT, ST_EMIT, ST_SORT, ST_RANGES, ST_RASTER_FWD, ST_RASTER_BWD, ST_PROJECT_BWD, ST_OTHER, ST_N };
+
+} // namespace
+
+struct vs_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t* host_counters = nullptr;    // pinned readback of the projection counters
+    bool timing = false;
+    // Stage event pairs recorded since the last vs_ctx_stage_times(); the
+    // pool is reused, so timing many renders needs no extra synchronisation.
+    struct Rec { int stage; hipEvent_t b, e; };
+    std::vector<Rec> recs;
+    std::vector<hipEvent_t> pool;
+    hipEvent_t take() {
+        if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
+        hipEvent_t e = nullptr;
+        hipEventCreate(&e);
+        return e;
+    }
+};
+
+struct vs_fwd_state {
+    vs_ctx* ctx = nullptr;
+    vs_camera cam{};
+    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0;
+    float lso = 0.0f;
+    float bg[3] = {0, 0, 0};
+    vs_pass pass = VS_PASS_FORWARD;
+    uint32_t tbw = 0, tbh = 0, T = 0, V = 0, I = 0, shift = 0, dmin = 0;
+    void* arena = nullptr;        // per-splat buffers
+    void* isect_arena = nullptr;  // per-intersection buffers
+    uint32_t* counts = nullptr;
+    uint32_t* depth_bits = nullptr;
+    float4* proj_a = nullptr;
+    float4* proj_b = nullptr;
+    float* proj_c = nullptr;
+    float4* proj_aux = nullptr;
+    float* opacities = nullptr;
+    float* max_radius = nullptr;
+    float* visible = nullptr;
+    uint32_t* block_sums = nullptr;
+    uint32_t* counters = nullptr;
+    uint32_t* ranges = nullptr;
+    uint32_t* ranges_shrunk = nullptr;
+    float* v_combined = nullptr;
+    uint64_t* keys = nullptr;
+    uint32_t* gids = nullptr;
+};
+
+namespace {
+
+struct StageTimer {
+    vs_ctx* c;
+    Stage s;
+    hipEvent_t b = nullptr;
+    StageTimer(vs_ctx* ctx, Stage st) : c(ctx), s(st) {
+        if (c->timing) { b = c->take(); hipEventRecord(b, c->stream); }
+    }
+    ~StageTimer() {
+        if (c->timing) {
+            hipEvent_t e = c->take();
+            hipEventRecord(e, c->stream);
+            c->recs.push_back(vs_ctx::Rec{(int)s, b, e});
+        }
+    }
+};
+
+bool pass_bwd_info(vs_pass p) { return p != VS_PASS_FORWARD; }
+
+vs_status check_splats(const vs_splats* sp) {
+    if (!sp) return fail(VS_ERR_INVALID, "splats is null");
+    if (sp->sh_degree > 4) return fail(VS_ERR_INVALID, "SH degree must be 0..4 (1, 4, 9, 16 or 25 coefficients)");
+    if (sp->num_splats > 0 && (!sp->transforms || !sp->sh_coeffs || !sp->raw_opacities))
+        return fail(VS_ERR_INVALID, "splat parameter pointer is null");
+    if (((uintptr_t)sp->transforms & 7u) != 0) return fail(VS_ERR_INVALID, "transforms must be 8-byte aligned");
+    if (((uintptr_t)sp->sh_coeffs & 15u) != 0) return fail(VS_ERR_INVALID, "sh_coeffs must be 16-byte aligned");
+    if (((uintptr_t)sp->raw_opacities & 3u) != 0) return fail(VS_ERR_INVALID, "raw_opacities must be 4-byte aligned");
+    return VS_OK;
+}
+
+} // namespace
+
+extern "C" const char* vs_last_error(void) { return g_last_error.c_str(); }
+extern "C" const char* vs_version(void) { return "vsplat-gfx950 0.1"; }
+
+extern "C" vs_status vs_ctx_create(int device, void* hip_stream, vs_ctx** out) {
+    if (!out) return fail(VS_ERR_INVALID, "out is null");
+    *out = nullptr;
+    int count = 0;
+    VS_HIP(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device < 0 || device >= count) return fail(VS_ERR_INVALID, "device index out of range");
+    VS_HIP(hipSetDevice(device), "hipSetDevice");
+    vs_ctx* c = new (std::nothrow) vs_ctx();
+    if (!c) return fail(VS_ERR_OOM, "context allocation");
+    c->device = device;
+    c->stream = static_cast<hipStream_t>(hip_stream);
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&c->host_counters), CNT_COUNT * sizeof(uint32_t), hipHostMallocDefault);
+    if (e != hipSuccess) { delete c; return hip_fail(e, "hipHostMalloc"); }
+    // Keep freed stream-ordered allocations in the pool between renders.
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess) {
+        uint64_t thr = ~0ull;
+        hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &thr);
+    }
+    *out = c;
+    return VS_OK;
+}
+
+extern "C" void vs_ctx_destroy(vs_ctx* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    for (auto& r : c->recs) { hipEventDestroy(r.b); hipEventDestroy(r.e); }
+    for (auto e : c->pool) hipEventDestroy(e);
+    hipHostFree(c->host_counters);
+    delete c;
+}
+
+extern "C" vs_status vs_ctx_set_stream(vs_ctx* c, void* hip_stream) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    c->stream = static_cast<hipStream_t>(hip_stream);
+    return VS_OK;
+}
+
+extern "C" vs_status vs_ctx_enable_timing(vs_ctx* c, int enable) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    c->timing = enable != 0;
+    return VS_OK;
+}
+
+extern "C" vs_status vs_ctx_stage_times(vs_ctx* c, vs_stage_times* out) {
+    if (!c || !out) return fail(VS_ERR_INVALID, "null argument");
+    VS_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    float ms[ST_N] = {};
+    for (auto& r : c->recs) {
+        float v = 0.0f;
+        if (hipEventElapsedTime(&v, r.b, r.e) == hipSuccess) ms[r.stage] += v;
+        c->pool.push_back(r.b);
+        c->pool.push_back(r.e);
+    }
+    c->recs.clear();
+    out->project_ms = ms[ST_PROJECT];
+    out->emit_ms = ms[ST_EMIT];
+    out->sort_ms = ms[ST_SORT];
+    out->ranges_ms = ms[ST_RANGES];
+    out->raster_fwd_ms = ms[ST_RASTER_FWD];
+    out->raster_bwd_ms = ms[ST_RASTER_BWD];
+    out->project_bwd_ms = ms[ST_PROJECT_BWD];
+    out->other_ms = ms[ST_OTHER];
+    return VS_OK;
+}
+
+extern "C" void vs_fwd_state_free(vs_fwd_state* st) {
+    if (!st) return;
+    hipSetDevice(st->ctx->device);
+    if (st->isect_arena) hipFreeAsync(st->isect_arena, st->ctx->stream);
+    if (st->arena) hipFreeAsync(st->arena, st->ctx->stream);
+    delete st;
+}
+
+extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* sp, uint32_t W, uint32_t H,
+                                       const float background[3], vs_pass pass, vs_render_mode mode, vs_fwd_out* out,
+                                       vs_fwd_state** state_out) {
+    if (state_out) *state_out = nullptr;
+    if (!ctx || !cam || !out || !background) return fail(VS_ERR_INVALID, "null argument");
+    if (W == 0 || H == 0) return fail(VS_ERR_INVALID, "Can't render images with 0 size.");
+    if (mode != VS_MODE_DEFAULT) return fail(VS_ERR_UNSUPPORTED, "only the Default render mode is built (Mip and Surfel are not)");
+    if ((int)pass < 0 || (int)pass > (int)VS_PASS_GEOMETRY) return fail(VS_ERR_INVALID, "unknown pass");
+    if (cam->model != VS_CAMERA_PINHOLE && cam->model != VS_CAMERA_KB4)
+        return fail(VS_ERR_UNSUPPORTED, "camera model must be pinhole or Kannala-Brandt-4");
+    vs_status vst = check_splats(sp);
+    if (vst != VS_OK) return vst;
+    if (!out->out_img) return fail(VS_ERR_INVALID, "out_img is null");
+    if (pass_bwd_info(pass) && ((uintptr_t)out->out_img & 15u)) return fail(VS_ERR_INVALID, "out_img must be 16-byte aligned");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = ctx->stream;
+
+    vs_fwd_state* st = new (std::nothrow) vs_fwd_state();
+    if (!st) return fail(VS_ERR_OOM, "state allocation");
+    struct Guard { vs_fwd_state*& p; ~Guard() { if (p) vs_fwd_state_free(p); } } guard{st};
+    st->ctx = ctx;
+    st->cam = *cam;
+    st->W = W; st->H = H; st->N = sp->num_splats; st->degree = sp->sh_degree;
+    st->K = (sp->sh_degree + 1) * (sp->sh_degree + 1);
+    st->lso = sp->log_scale_offset;
+    st->bg[0] = background[0]; st->bg[1] = background[1]; st->bg[2] = background[2];
+    st->pass = pass;
+    st->tbw = (W + TILE_W_HOST_ - 1) / TILE_W_HOST_;
+    st->tbh = (H + TILE_W_HOST_ - 1) / TILE_W_HOST_;
+    const uint64_t T64 = (uint64_t)st->tbw * st->tbh;
+    if (T64 >= 0x7FFFFFFFull) return fail(VS_ERR_INVALID, "image too large");
+    st->T = (uint32_t)T64;
+    const uint32_t N = st->N, T = st->T;
+    const bool bwd_info = pass_bwd_info(pass);
+    const bool geometry = pass == VS_PASS_GEOMETRY;
+    const bool smooth = pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF;
+    const uint32_t nblocks = (N + 255) / 256;
+
+    // ---- per-splat arena -----------------------------------------------------
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
+    const size_t o_counts = take((size_t)N * 4), o_depth = take((size_t)N * 4);
+    const size_t o_pa = take((size_t)N * 16), o_pb = take((size_t)N * 16), o_pc = take((size_t)N * 4);
+    const size_t o_aux = geometry ? take((size_t)N * 16) : 0;
+    const size_t o_opac = out->opacities ? 0 : take((size_t)N * 4);
+    const size_t o_rad = out->max_radius ? 0 : take((size_t)N * 4);
+    const size_t o_vis = (bwd_info && !out->visible) ? take((size_t)N * 4) : 0;
+    const size_t o_bs = take((size_t)std::max(nblocks, 1u) * 4);
+    const size_t o_cnt = take(CNT_COUNT * 4);
+    const size_t o_rng = take((size_t)T * 8), o_rngs = take((size_t)T * 8);
+    VS_HIP(hipMallocAsync(&st->arena, off, s), "hipMallocAsync(splat arena)");
+    char* base = static_cast<char*>(st->arena);
+    st->counts = reinterpret_cast<uint32_t*>(base + o_counts);
+    st->depth_bits = reinterpret_cast<uint32_t*>(base + o_depth);
+    st->proj_a = reinterpret_cast<float4*>(base + o_pa);
+    st->proj_b = reinterpret_cast<float4*>(base + o_pb);
+    st->proj_c = reinterpret_cast<float*>(base + o_pc);
+    st->proj_aux = geometry ? reinterpret_cast<float4*>(base + o_aux) : nullptr;
+    st->opacities = out->opacities ? out->opacities : reinterpret_cast<float*>(base + o_opac);
+    st->max_radius = out->max_radius ? out->max_radius : reinterpret_cast<float*>(base + o_rad);
+    st->visible = bwd_info ? (out->visible ? out->visible : reinterpret_cast<float*>(base + o_vis)) : nullptr;
+    st->block_sums = reinterpret_cast<uint32_t*>(base + o_bs);
+    st->counters = reinterpret_cast<uint32_t*>(base + o_cnt);
+    st->ranges = reinterpret_cast<uint32_t*>(base + o_rng);
+    st->ranges_shrunk = reinterpret_cast<uint32_t*>(base + o_rngs);
+
+    // ---- projection --------------------------------------------------------------
+    {
+        StageTimer tm(ctx, ST_PROJECT);
+        VS_HIP(launch_init_counters(st->counters, s), "init counters");
+        ProjectArgs pa{};
+        pa.cam = *cam;
+        pa.img_w = W; pa.img_h = H; pa.tile_bw = st->tbw; pa.tile_bh = st->tbh;
+        pa.num_splats = N; pa.sh_degree = sp->sh_degree; pa.log_scale_offset = sp->log_scale_offset;
+        pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.raw_opac = sp->raw_opacities;
+        pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
+        pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
+        pa.proj_aux = st->proj_aux; pa.block_sums = st->block_sums; pa.counters = st->counters;
+        VS_HIP(launch_project(pa, s), "project kernel");
+        if (nblocks > 0) VS_HIP(scan_single_block(st->block_sums, nblocks, false, nullptr, s), "block offsets scan");
+        if (bwd_info) VS_HIP(launch_fill_f32(st->visible, 0.0f, N, s), "zero visible");
+        VS_HIP(launch_fill_u32(st->ranges, 0u, (uint64_t)T * 2, s), "zero ranges");
+    }
+    VS_HIP(hipMemcpyAsync(ctx->host_counters, st->counters, CNT_COUNT * 4, hipMemcpyDeviceToHost, s), "counter readback");
+    VS_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+    const uint32_t* hc = ctx->host_counters;
+    st->V = hc[CNT_VISIBLE];
+    uint64_t I64 = 0;
+    std::memcpy(&I64, hc + CNT_ISECT64, 8);
+    if (I64 > 0xFFFFFFFFull) return fail(VS_ERR_CAPACITY, "intersection count exceeds u32");
+    st->I = (uint32_t)I64;
+    st->dmin = (st->V > 0) ? hc[CNT_DEPTH_MIN] : 0u;
+    const uint32_t dmax = (st->V > 0) ? hc[CNT_DEPTH_MAX] : 0u;
+    st->shift = bit_length((uint64_t)(dmax - st->dmin));
+    const uint32_t tile_bits = bit_length(T);     // the sentinel tile id T must fit too
+    const uint32_t end_bit = st->shift + tile_bits;
+    const uint32_t I = st->I;
+
+    // ---- emission + sort ---------------------------------------------------------
+    if (I > 0) {
+        size_t ioff = 0;
+        auto itake = [&](size_t bytes) { const size_t o = ioff; ioff += align256(bytes); return o; };
+        const size_t o_ku = itake((size_t)I * 8), o_vu = itake((size_t)I * 4);
+        const size_t o_k = itake((size_t)I * 8), o_v = itake((size_t)I * 4);
+        const size_t o_tmp = itake(sort_tmp_bytes(I, true));
+        VS_HIP(hipMallocAsync(&st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
+        char* ib = static_cast<char*>(st->isect_arena);
+        uint64_t* keys_u = reinterpret_cast<uint64_t*>(ib + o_ku);
+        uint32_t* vals_u = reinterpret_cast<uint32_t*>(ib + o_vu);
+        st->keys = reinterpret_cast<uint64_t*>(ib + o_k);
+        st->gids = reinterpret_cast<uint32_t*>(ib + o_v);
+        {
+            StageTimer tm(ctx, ST_EMIT);
+            EmitArgs ea{};
+            ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
+            ea.depth_shift = st->shift; ea.depth_min = st->dmin;
+            ea.counts = st->counts; ea.block_offsets = st->block_sums; ea.depth_bits = st->depth_bits;
+            ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.keys = keys_u; ea.vals = vals_u;
+            VS_HIP(launch_emit(ea, s), "emit kernel");
+        }
+        {
+            StageTimer tm(ctx, ST_SORT);
+            VS_HIP(radix_sort_pairs(keys_u, vals_u, st->keys, st->gids, I, nullptr, true, 0, end_bit, ib + o_tmp, s),
+                   "tile/depth sort");
+        }
+        {
+            StageTimer tm(ctx, ST_RANGES);
+            VS_HIP(launch_tile_ranges(st->keys, I, st->shift, T, st->ranges, s), "tile ranges");
+        }
+    }
+
+    // ---- rasterize ---------------------------------------------------------------
+    {
+        StageTimer tm(ctx, ST_RASTER_FWD);
+        RasterArgs ra{};
+        ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T;
+        ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
+        ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;
+        ra.proj_a = st->proj_a; ra.proj_b = st->proj_b; ra.proj_c = st->proj_c; ra.proj_aux = st->proj_aux;
+        ra.out = out->out_img; ra.visible = st->visible;
+        VS_HIP(launch_raster_fwd(ra, bwd_info, geometry, smooth, s), "raster forward");
+    }
+    if (out->tile_offsets) {
+        const uint32_t* src = bwd_info ? st->ranges_shrunk : st->ranges;
+        VS_HIP(hipMemcpyAsync(out->tile_offsets, src, (size_t)T * 8, hipMemcpyDeviceToDevice, s), "tile offsets copy");
+    }
+    out->num_visible = st->V;
+    out->num_intersections = I;
+    if (bwd_info && state_out) {
+        *state_out = st;
+        st = nullptr;   // ownership passes to the caller
+    }
+    return VS_OK;
+}
+
+extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_splats* sp, const float* out_img,
+                                        const float* v_out, vs_grads* grads) {
+    if (!ctx || !st || !out_img || !v_out || !grads) return fail(VS_ERR_INVALID, "null argument");
+    if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
+    vs_status vst = check_splats(sp);
+    if (vst != VS_OK) return vst;
+    if (sp->num_splats != st->N || sp->sh_degree != st->degree) return fail(VS_ERR_INVALID, "splats differ from the forward's");
+    if (((uintptr_t)out_img & 15u) || ((uintptr_t)v_out & 15u)) return fail(VS_ERR_INVALID, "images must be 16-byte aligned");
+    if (grads->v_transforms && ((uintptr_t)grads->v_transforms & 7u)) return fail(VS_ERR_INVALID, "v_transforms must be 8-byte aligned");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = ctx->stream;
+    const uint32_t N = st->N;
+    float* vc = grads->v_combined;
+    void* vc_alloc = nullptr;
+    if (!vc && N > 0) {
+        VS_HIP(hipMallocAsync(&vc_alloc, (size_t)N * 40, s), "hipMallocAsync(v_combined)");
+        vc = static_cast<float*>(vc_alloc);
+    }
+    if (vc && ((uintptr_t)vc & 7u)) return fail(VS_ERR_INVALID, "v_combined must be 8-byte aligned");
+    {
+        VS_HIP(launch_fill_f32(vc, 0.0f, (uint64_t)N * 10, s), "zero v_combined");
+        StageTimer tm(ctx, ST_RASTER_BWD);
+        if (st->I > 0) {
+            RasterBwdArgs rb{};
+            rb.img_w = st->W; rb.img_h = st->H; rb.tile_bw = st->tbw; rb.tile_bh = st->tbh; rb.num_tiles = st->T;
+            rb.bg_r = st->bg[0]; rb.bg_g = st->bg[1]; rb.bg_b = st->bg[2];
+            rb.gids = st->gids; rb.ranges = st->ranges_shrunk;
+            rb.proj_a = st->proj_a; rb.proj_b = st->proj_b; rb.proj_c = st->proj_c;
+            rb.out_img = out_img; rb.v_out = v_out; rb.channels = (st->pass == VS_PASS_GEOMETRY) ? 12u : 4u;
+            rb.v_combined = vc;
+            VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s), "raster backward");
+        }
+    }
+    {
+        StageTimer tm(ctx, ST_PROJECT_BWD);
+        ProjectBwdArgs pb{};
+        pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = sp->log_scale_offset;
+        pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.raw_opac = sp->raw_opacities;
+        pb.counts = st->counts; pb.v_combined = vc;
+        pb.v_transforms = grads->v_transforms; pb.v_sh = grads->v_sh_coeffs;
+        pb.v_raw_opac = grads->v_raw_opacities; pb.v_refine = grads->v_refine_weight;
+        VS_HIP(launch_project_bwd(pb, s), "projection backward");
+    }
+    if (vc_alloc) VS_HIP(hipFreeAsync(vc_alloc, s), "hipFreeAsync(v_combined)");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_fwd_state_view(const vs_fwd_state* st, vs_state_view* o) {
+    if (!st || !o) return fail(VS_ERR_INVALID, "null argument");
+    o->num_splats = st->N; o->num_visible = st->V; o->num_intersections = st->I; o->num_tiles = st->T;
+    o->tile_bw = st->tbw; o->tile_bh = st->tbh; o->depth_shift = st->shift; o->depth_min = st->dmin;
+    o->isect_keys = st->keys; o->isect_gids = st->gids; o->intersect_counts = st->counts;
+    o->proj_xy_conic = reinterpret_cast<const float*>(st->proj_a);
+    o->proj_c11_opac_rg = reinterpret_cast<const float*>(st->proj_b);
+    o->proj_b = st->proj_c;
+    o->proj_aux = reinterpret_cast<const float*>(st->proj_aux);
+    o->tile_ranges = st->ranges;
+    return VS_OK;
+}
+
+extern "C" vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, const uint32_t* vals, uint32_t n,
+                                          const uint32_t* n_dev, uint32_t skip_bits, uint32_t sorting_bits,
+                                          uint32_t* out_keys, uint32_t* out_vals) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (skip_bits + sorting_bits > 32) return fail(VS_ERR_INVALID, "Can only sort up to 32 bits");
+    if (n == 0) return VS_OK;
+    if (!keys || !vals || !out_keys || !out_vals) return fail(VS_ERR_INVALID, "null buffer");
+    if (keys == out_keys || vals == out_vals) return fail(VS_ERR_INVALID, "outputs must not alias inputs");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    void* tmp = nullptr;
+    VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, false), ctx->stream), "hipMallocAsync(sort tmp)");
+    StageTimer tm(ctx, ST_OTHER);
+    hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, n_dev, false, skip_bits, skip_bits + sorting_bits,
+                                    tmp, ctx->stream);
+    hipFreeAsync(tmp, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "radix sort");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, const uint32_t* vals, uint32_t n,
+                                          uint32_t sorting_bits, uint64_t* out_keys, uint32_t* out_vals) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (sorting_bits > 64) return fail(VS_ERR_INVALID, "Can only sort up to 64 bits");
+    if (n == 0) return VS_OK;
+    if (!keys || !vals || !out_keys || !out_vals) return fail(VS_ERR_INVALID, "null buffer");
+    if (keys == out_keys || vals == out_vals) return fail(VS_ERR_INVALID, "outputs must not alias inputs");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    void* tmp = nullptr;
+    VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, true), ctx->stream), "hipMallocAsync(sort tmp)");
+    StageTimer tm(ctx, ST_OTHER);
+    hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, nullptr, true, 0, sorting_bits, tmp, ctx->stream);
+    hipFreeAsync(tmp, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "radix sort");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (n == 0) return VS_OK;
+    if (!in || !out) return fail(VS_ERR_INVALID, "null buffer");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    void* tmp = nullptr;
+    VS_HIP(hipMallocAsync(&tmp, scan_tmp_words(n) * 4, ctx->stream), "hipMallocAsync(scan tmp)");
+    hipError_t e = scan_u32(in, out, n, true, static_cast<uint32_t*>(tmp), nullptr, ctx->stream);
+    hipFreeAsync(tmp, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "prefix sum");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_scan_in_place_u32(vs_ctx* ctx, uint32_t* data, uint32_t n) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (n == 0) return VS_OK;
+    if (!data) return fail(VS_ERR_INVALID, "null buffer");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(scan_single_block(data, n, true, nullptr, ctx->stream), "scan in place");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const float* gt, uint32_t w,
+                                     uint32_t h, float mcx, float mcy, float mr, float* v_out) {
+    if (!ctx || !pred || !gt || !v_out) return fail(VS_ERR_INVALID, "null argument");
+    if (channels < 3) return fail(VS_ERR_INVALID, "prediction needs at least 3 channels");
+    uint64_t count = (uint64_t)w * h;
+    if (mr > 0.0f) {
+        count = 0;
+        for (uint32_t y = 0; y < h; ++y)
+            for (uint32_t x = 0; x < w; ++x) {
+                const float dx = (float)x + 0.5f - mcx, dy = (float)y + 0.5f - mcy;
+                if (dx * dx + dy * dy <= mr * mr) ++count;
+            }
+    }
+    const float inv = count ? 1.0f / (3.0f * (float)count) : 0.0f;
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_l1_cotangent(pred, channels, gt, w, h, mcx, mcy, mr, inv, v_out, ctx->stream), "l1 cotangent");
+    return VS_OK;
+}

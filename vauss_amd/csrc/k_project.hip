@@ -1,0 +1,382 @@
+// k_project.hip -- projection, culling, tile counting and intersection emission.
+//
+// One fused kernel replaces the reference's project_forward + project_visible
+// (crates/splat-train-render/src/kernels/project_forward.rs:26-261,
+// kernels/project_visible.rs:97-312): each lane owns one splat, culls it, and a
+// surviving splat reads its SH row, writes its projected row at its global id
+// (no compaction pass) and counts the tiles its ellipse touches.  Emission
+// writes one packed 64-bit (tile, depth) key per hit tile at offsets from a
+// scan over global-id order, so a stable sort by key yields per-tile depth
+// order with ties in global-id order.
+#include "vs_device.h"
+#include "vs_camera.h"
+#include "vs_sh.h"
+#include "vs_internal.h"
+
+namespace vs {
+
+constexpr int PROJ_BLOCK = 256;
+// Bounding boxes up to this many tiles are walked by their own lane; larger
+// ones by the whole wavefront (kernels/map_gaussians.rs:17-19 uses 16 for the
+// same split).
+constexpr uint32_t SMALL_BBOX = 16;
+
+struct TileBox { uint32_t x0, y0, x1, y1; };
+
+// kernels/helpers.rs:133-144
+VS_DEV void bbox_extent(S2 c, float power, float& ex, float& ey) {
+    const float det = c.c00 * c.c11 - c.c01 * c.c01;
+    const bool degenerate = det <= 0.0f;
+    const float inv_det = degenerate ? 0.0f : 1.0f / det;
+    const float ex_ = __builtin_sqrtf(2.0f * power * c.c11 * inv_det);
+    const float ey_ = __builtin_sqrtf(2.0f * power * c.c00 * inv_det);
+    ex = degenerate ? -1.0f : ex_;
+    ey = degenerate ? -1.0f : ey_;
+}
+// kernels/helpers.rs:160-190
+VS_DEV TileBox tile_box(float cx, float cy, float ex, float ey, uint32_t bw, uint32_t bh) {
+    const float x = cx / 16.0f, y = cy / 16.0f, dx = ex / 16.0f, dy = ey / 16.0f;
+    const float bwf = (float)bw, bhf = (float)bh;
+    return TileBox{f2u_sat(clampf(x - dx, 0.0f, bwf)), f2u_sat(clampf(y - dy, 0.0f, bhf)),
+                   f2u_sat(clampf(x + dx + 1.0f, 0.0f, bwf)), f2u_sat(clampf(y + dy + 1.0f, 0.0f, bhf))};
+}
+// kernels/helpers.rs:275-314 (StopThePop conservative ellipse-rectangle test)
+VS_DEV bool will_contribute(uint32_t tx, uint32_t ty, float mx_, float my_, S2 c, float power) {
+    const float x0 = (float)(tx * TILE_W), y0 = (float)(ty * TILE_W);
+    const float x1 = x0 + (float)TILE_W, y1 = y0 + (float)TILE_W;
+    const bool xl = mx_ < x0, xr = mx_ > x1;
+    const bool in_x = !(xl || xr);
+    const bool ya = my_ < y0, yb = my_ > y1;
+    const bool in_y = !(ya || yb);
+    if (in_x && in_y) return true;
+    const float cx = xl ? x0 : x1, cy = ya ? y0 : y1;
+    const float w = x1 - x0, h = y1 - y0;
+    const float dxf = xl ? w : -w, dyf = ya ? h : -h;
+    const float ddx = mx_ - cx, ddy = my_ - cy;
+    const float txr = (dxf * c.c00 * ddx + dxf * c.c01 * ddy) / (dxf * c.c00 * dxf);
+    const float tyr = (dyf * c.c01 * ddx + dyf * c.c11 * ddy) / (dyf * c.c11 * dyf);
+    const float tx_ = in_y ? 0.0f : clampf(txr, 0.0f, 1.0f);
+    const float ty_ = in_x ? 0.0f : clampf(tyr, 0.0f, 1.0f);
+    return calc_sigma(cx + tx_ * dxf, cy + ty_ * dyf, c, mx_, my_) <= power;
+}
+
+VS_DEV uint32_t lane_id() { return __lane_id(); }
+VS_DEV float rl(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
+VS_DEV uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+
+VS_DEV uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+VS_DEV uint32_t wave_min(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { const uint32_t w = __shfl_xor(v, o); v = w < v ? w : v; }
+    return v;
+}
+VS_DEV uint32_t wave_max(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { const uint32_t w = __shfl_xor(v, o); v = w > v ? w : v; }
+    return v;
+}
+
+__global__ void __launch_bounds__(64) init_counters_kernel(uint32_t* c) {
+    const uint32_t i = threadIdx.x;
+    if (i < CNT_COUNT) c[i] = (i == CNT_DEPTH_MIN) ? 0xFFFFFFFFu : 0u;
+}
+
+template <int DEG>
+VS_DEV F3 load_color(const float* __restrict__ sh, uint32_t g, F3 mean, const vs_camera& u) {
+    constexpr int K = sh_count<DEG>();
+    const float* row = sh + (size_t)g * (K * 3);
+    float c[K * 3];
+    if constexpr ((K * 3) % 4 == 0) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+        for (int i = 0; i < K * 3 / 4; ++i) {
+            const float4 q = r4[i];
+            c[4 * i] = q.x; c[4 * i + 1] = q.y; c[4 * i + 2] = q.z; c[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < K * 3; ++i) c[i] = row[i];
+    }
+    // kernels/project_visible.rs:25-61
+    const F3 v = normalize(mean - F3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
+    const F3 raw = sh_color<DEG>(c, v);
+    const float r = raw.x + 0.5f, gg = raw.y + 0.5f, b = raw.z + 0.5f;
+    return F3{clampf(finite(r) ? r : 0.0f, -100.0f, 100.0f),
+              clampf(finite(gg) ? gg : 0.0f, -100.0f, 100.0f),
+              clampf(finite(b) ? b : 0.0f, -100.0f, 100.0f)};
+}
+
+template <int DEG, int MODEL, bool GEOM>
+__global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
+    const vs_camera& u = a.cam;
+    const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+    bool visible = false;
+    float px = 0.0f, py = 0.0f, power = 0.0f, radius = 0.0f, opac_out = 0.0f;
+    S2 conic{0.0f, 0.0f, 0.0f};
+    TileBox bb{0, 0, 0, 0};
+    uint32_t dbits = 0;
+    if (g < a.num_splats) {
+        const float2* t2 = reinterpret_cast<const float2*>(a.transforms + (size_t)g * 10);
+        const float2 t01 = t2[0], t23 = t2[1], t45 = t2[2], t67 = t2[3], t89 = t2[4];
+        const float raw_op = a.raw_opac[g];
+        // kernels/project_forward.rs:62-194, culls in the reference's order.
+        do {
+            const F3 mean{t01.x, t01.y, t23.x};
+            const F3 mc = world_to_cam(mean, u);
+            if (!(finite(mc) && mc.z <= 1.0e10f)) break;
+            if constexpr (MODEL == VS_CAMERA_PINHOLE) {
+                if (mc.z < 0.01f) break;
+            } else {
+                const float r = __builtin_sqrtf(mc.x * mc.x + mc.y * mc.y);
+                if (atan2f_c(r, mc.z) > u.half_max_render_fov) break;
+            }
+            const float lso = a.log_scale_offset;
+            const F3 scl{expf_c(t67.y + lso), expf_c(t89.x + lso), expf_c(t89.y + lso)};
+            if (!finite(scl)) break;
+            const Qt qu{t23.y, t45.x, t45.y, t67.x};
+            const float qn = dot(qu, qu);
+            if (!(qn >= 1.0e-6f && finite(qn))) break;
+            if (!finite(raw_op)) break;
+            const Qt q = normalize(qu);
+            const float opac = sigmoid(raw_op);
+            opac_out = opac;
+            const S2 cov = cov2d_blurred<MODEL>(scl, q, mc, u);
+            if (!finite(cov)) break;
+            project_point<MODEL>(mc, u, px, py);
+            if (!(opac >= 1.0f / 255.0f)) break;
+            power = logf_c(opac * 255.0f);
+            conic = inverse(cov);
+            float ex, ey;
+            bbox_extent(conic, power, ex, ey);
+            if (!(ex >= 0.0f && ey >= 0.0f)) break;
+            const float wf = (float)a.img_w, hf = (float)a.img_h;
+            if (!(px + ex > 0.0f && px - ex < wf && py + ey > 0.0f && py - ey < hf)) break;
+            bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
+            radius = mx(ex / wf, ey / hf);
+            dbits = as_u(mc.z);
+            visible = true;
+            // Projected row (kernels/project_visible.rs:150-173), written at the global id.
+            const F3 col = load_color<DEG>(a.sh, g, mean, u);
+            a.proj_a[g] = make_float4(px, py, conic.c00, conic.c01);
+            a.proj_b[g] = make_float4(conic.c11, opac, col.x, col.y);
+            a.proj_c[g] = col.z;
+            if constexpr (GEOM) {
+                // kernels/project_visible.rs:271-289
+                const M3 rot = mul(view_rot(u), to_mat3(q));
+                const bool x_min = scl.x <= scl.y && scl.x <= scl.z;
+                const bool y_min = !x_min && scl.y <= scl.z;
+                const F3 axis = x_min ? rot.c0 : (y_min ? rot.c1 : rot.c2);
+                const float flip = (dot(axis, mc) > 0.0f) ? -1.0f : 1.0f;
+                a.proj_aux[g] = make_float4(mc.z, axis.x * flip, axis.y * flip, axis.z * flip);
+            }
+        } while (false);
+    }
+
+    // Tile counting (kernels/helpers.rs:253-273; wave-cooperative walk for
+    // big boxes as kernels/project_forward.rs:198-247 does per subgroup).
+    const uint32_t bw = bb.x1 - bb.x0;
+    const uint32_t nb = visible ? (bb.y1 - bb.y0) * bw : 0u;
+    uint32_t hits = 0;
+    if (visible && nb <= SMALL_BBOX) {
+        for (uint32_t i = 0; i < nb; ++i) {
+            const uint32_t tx = i % bw + bb.x0, ty = i / bw + bb.y0;
+            if (will_contribute(tx, ty, px, py, conic, power)) ++hits;
+        }
+    }
+    uint64_t pending = __ballot(visible && nb > SMALL_BBOX);
+    const uint32_t lane = lane_id();
+    while (pending) {
+        const int leader = __builtin_ctzll(pending);
+        const float lx = rl(px, leader), ly = rl(py, leader);
+        const S2 lc{rl(conic.c00, leader), rl(conic.c01, leader), rl(conic.c11, leader)};
+        const float lp = rl(power, leader);
+        const uint32_t lx0 = rl(bb.x0, leader), ly0 = rl(bb.y0, leader), lw = rl(bw, leader), ln = rl(nb, leader);
+        uint32_t total = 0;
+        for (uint32_t t0 = 0; t0 < ln; t0 += 64) {
+            const uint32_t t = t0 + lane;
+            const bool hit = t < ln && will_contribute(t % lw + lx0, t / lw + ly0, lx, ly, lc, lp);
+            total += (uint32_t)__popcll(__ballot(hit));
+        }
+        if ((int)lane == leader) hits = total;
+        pending &= pending - 1;
+    }
+
+    if (g < a.num_splats) {
+        a.opacities[g] = opac_out;
+        a.max_radius[g] = radius;
+        a.counts[g] = hits;
+        a.depth_bits[g] = dbits;
+    }
+
+    // Block totals: intersections for the emission scan; visible count and
+    // depth range through one atomic per wave.
+    __shared__ uint32_t s_sum[PROJ_BLOCK / 64];
+    const uint32_t wsum = wave_sum(hits);
+    const uint32_t wvis = (uint32_t)__popcll(__ballot(visible));
+    const uint32_t wmin = wave_min(visible ? dbits : 0xFFFFFFFFu);
+    const uint32_t wmax = wave_max(visible ? dbits : 0u);
+    const uint32_t wave = threadIdx.x / 64;
+    if (lane == 0) {
+        s_sum[wave] = wsum;
+        if (wvis) {
+            atomicAdd(&a.counters[CNT_VISIBLE], wvis);
+            atomicMin(&a.counters[CNT_DEPTH_MIN], wmin);
+            atomicMax(&a.counters[CNT_DEPTH_MAX], wmax);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t bs = 0;
+        uint64_t bs64 = 0;
+#pragma unroll
+        for (int w = 0; w < PROJ_BLOCK / 64; ++w) { bs += s_sum[w]; bs64 += s_sum[w]; }
+        a.block_sums[blockIdx.x] = bs;
+        if (bs64) atomicAdd(reinterpret_cast<unsigned long long*>(a.counters + CNT_ISECT64), (unsigned long long)bs64);
+    }
+}
+
+__global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
+    const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+    const uint32_t lane = lane_id(), wave = threadIdx.x / 64;
+    const uint32_t cnt = (g < a.num_splats) ? a.counts[g] : 0u;
+    // Block-exclusive scan of the counts (global-id order).
+    uint32_t incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o);
+        if ((int)lane >= o) incl += v;
+    }
+    __shared__ uint32_t s_w[PROJ_BLOCK / 64];
+    if (lane == 63) s_w[wave] = incl;
+    __syncthreads();
+    uint32_t wave_base = 0;
+    for (uint32_t w = 0; w < wave; ++w) wave_base += s_w[w];
+    const uint32_t base = a.block_offsets[blockIdx.x] + wave_base + incl - cnt;
+
+    float px = 0.0f, py = 0.0f, power = 0.0f;
+    S2 conic{0.0f, 0.0f, 0.0f};
+    TileBox bb{0, 0, 0, 0};
+    uint64_t key_lo = 0;
+    if (cnt > 0) {
+        // Recompute the box from the projected row as kernels/map_gaussians.rs:61-66 does.
+        const float4 pa = a.proj_a[g];
+        const float4 pb = a.proj_b[g];
+        px = pa.x; py = pa.y;
+        conic = S2{pa.z, pa.w, pb.x};
+        power = logf_c(pb.y * 255.0f);
+        float ex, ey;
+        bbox_extent(conic, power, ex, ey);
+        bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
+        key_lo = (uint64_t)(a.depth_bits[g] - a.depth_min);
+    }
+    const uint32_t bw = bb.x1 - bb.x0;
+    const uint32_t nb = (cnt > 0) ? (bb.y1 - bb.y0) * bw : 0u;
+    const uint32_t shift = a.depth_shift;
+    const uint64_t sentinel = (uint64_t)(a.tile_bw * a.tile_bh) << shift;
+    if (cnt > 0 && nb <= SMALL_BBOX) {
+        uint32_t k = 0;
+        for (uint32_t i = 0; i < nb; ++i) {
+            const uint32_t tx = i % bw + bb.x0, ty = i / bw + bb.y0;
+            if (k < cnt && will_contribute(tx, ty, px, py, conic, power)) {
+                a.keys[base + k] = ((uint64_t)(tx + ty * a.tile_bw) << shift) | key_lo;
+                a.vals[base + k] = g;
+                ++k;
+            }
+        }
+        for (; k < cnt; ++k) { a.keys[base + k] = sentinel; a.vals[base + k] = g; }
+    }
+    uint64_t pending = __ballot(cnt > 0 && nb > SMALL_BBOX);
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    while (pending) {
+        const int leader = __builtin_ctzll(pending);
+        const float lx = rl(px, leader), ly = rl(py, leader);
+        const S2 lc{rl(conic.c00, leader), rl(conic.c01, leader), rl(conic.c11, leader)};
+        const float lp = rl(power, leader);
+        const uint32_t lx0 = rl(bb.x0, leader), ly0 = rl(bb.y0, leader), lw = rl(bw, leader), ln = rl(nb, leader);
+        const uint32_t lbase = rl(base, leader), lcnt = rl(cnt, leader), lg = rl(g, leader);
+        const uint32_t lkey_lo = rl((uint32_t)key_lo, leader);
+        uint32_t emitted = 0;
+        for (uint32_t t0 = 0; t0 < ln; t0 += 64) {
+            const uint32_t t = t0 + lane;
+            const uint32_t tx = t % lw + lx0, ty = t / lw + ly0;
+            const bool hit = t < ln && will_contribute(tx, ty, lx, ly, lc, lp);
+            const uint64_t m = __ballot(hit);
+            const uint32_t slot = emitted + (uint32_t)__popcll(m & lt_mask);
+            if (hit && slot < lcnt) {
+                a.keys[lbase + slot] = ((uint64_t)(tx + ty * a.tile_bw) << shift) | (uint64_t)lkey_lo;
+                a.vals[lbase + slot] = lg;
+            }
+            emitted += (uint32_t)__popcll(m);
+        }
+        for (uint32_t p = (emitted < lcnt ? emitted : lcnt) + lane; p < lcnt; p += 64) {
+            a.keys[lbase + p] = sentinel;
+            a.vals[lbase + p] = lg;
+        }
+        pending &= pending - 1;
+    }
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) p[i] = v;
+}
+__global__ void fill_f32_kernel(float* p, float v, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+static uint32_t fill_grid(uint64_t n) {
+    const uint64_t b = (n + 255) / 256;
+    return (uint32_t)(b < 8192 ? (b ? b : 1) : 8192);
+}
+
+hipError_t launch_init_counters(uint32_t* counters, hipStream_t s) {
+    init_counters_kernel<<<1, 64, 0, s>>>(counters);
+    return hipGetLastError();
+}
+
+template <int DEG, int MODEL>
+static void launch_project_geom(const ProjectArgs& a, dim3 grid, hipStream_t s, bool geom) {
+    if (geom) project_kernel<DEG, MODEL, true><<<grid, PROJ_BLOCK, 0, s>>>(a);
+    else project_kernel<DEG, MODEL, false><<<grid, PROJ_BLOCK, 0, s>>>(a);
+}
+template <int DEG>
+static void launch_project_model(const ProjectArgs& a, dim3 grid, hipStream_t s, bool geom) {
+    if (a.cam.model == VS_CAMERA_KB4) launch_project_geom<DEG, VS_CAMERA_KB4>(a, grid, s, geom);
+    else launch_project_geom<DEG, VS_CAMERA_PINHOLE>(a, grid, s, geom);
+}
+
+hipError_t launch_project(const ProjectArgs& a, hipStream_t s) {
+    if (a.num_splats == 0) return hipSuccess;
+    const dim3 grid((a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK);
+    const bool geom = a.proj_aux != nullptr;
+    switch (a.sh_degree) {
+    case 0: launch_project_model<0>(a, grid, s, geom); break;
+    case 1: launch_project_model<1>(a, grid, s, geom); break;
+    case 2: launch_project_model<2>(a, grid, s, geom); break;
+    case 3: launch_project_model<3>(a, grid, s, geom); break;
+    default: launch_project_model<4>(a, grid, s, geom); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_emit(const EmitArgs& a, hipStream_t s) {
+    if (a.num_splats == 0) return hipSuccess;
+    emit_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    fill_u32_kernel<<<fill_grid(n), 256, 0, s>>>(p, value, n);
+    return hipGetLastError();
+}
+hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    fill_f32_kernel<<<fill_grid(n), 256, 0, s>>>(p, value, n);
+    return hipGetLastError();
+}
+
+} // namespace vs

@@ -1,0 +1,381 @@
+// k_raster.hip -- tile ranges, forward alpha compositing and its VJP.
+//
+// Forward: crates/splat-train-render/src/kernels/rasterize.rs:109-420.  One
+// 256-lane workgroup per 16x16 tile, one pixel per lane in Morton order so
+// each wavefront owns an 8x8 quadrant (kernels/helpers.rs:105-128); splats
+// are staged 256 at a time into LDS as float4 pairs that every lane reads as
+// a broadcast; the tile stops at the first batch boundary where every pixel
+// has reached T <= 1e-4.
+//
+// Backward: bwd/kernels/rasterize_backwards_planes.rs:112-682 redesigned for
+// 64-wide wavefronts.  Same tile/pixel mapping; splats staged 64 at a time;
+// each lane replays its pixel front to back with the forward's exact
+// arithmetic (so termination decisions agree bit for bit), the ten gradient
+// components of a splat are reduce-scattered across the wavefront in 13
+// shuffle-adds, the four wavefronts' partials are summed in LDS once per
+// batch, and each (tile, splat) pair issues at most ten f32 atomics.
+#include "vs_device.h"
+#include "vs_internal.h"
+
+namespace vs {
+
+constexpr int RASTER_BLOCK = 256;
+constexpr int BWD_BATCH = 64;
+
+// kernels/helpers.rs:105-113
+VS_DEV uint32_t compact_bits_16(uint32_t v) {
+    uint32_t x = v & 0x55555555u;
+    x = (x | (x >> 1)) & 0x33333333u;
+    x = (x | (x >> 2)) & 0x0F0F0F0Fu;
+    x = (x | (x >> 4)) & 0x00FF00FFu;
+    x = (x | (x >> 8)) & 0x0000FFFFu;
+    return x;
+}
+
+__global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, uint32_t n, uint32_t shift, uint32_t num_tiles,
+                                   uint32_t* __restrict__ ranges) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t tile = keys[i] >> shift;
+    if (tile >= num_tiles) return;   // sentinel rows sort last and own no tile
+    if (i == 0 || (keys[i - 1] >> shift) != tile) ranges[tile * 2] = i;
+    if (i + 1 == n || (keys[i + 1] >> shift) != tile) ranges[tile * 2 + 1] = i + 1;
+}
+
+// DIST_NEAR / DIST_FAR depth map, kernels/helpers.rs:91-103.
+VS_DEV float dist_depth(float z) { return 100.0f / (100.0f - 0.2f) * (1.0f - 0.2f / mx(z, 0.2f)); }
+
+template <bool BWD, bool GEOM, bool SMOOTH>
+__global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) {
+    __shared__ float4 s_a[RASTER_BLOCK];    // x, y, c00/2, c01
+    __shared__ float4 s_b[RASTER_BLOCK];    // c11/2, opacity, r, g
+    __shared__ float s_c[RASTER_BLOCK];     // b
+    __shared__ float4 s_d[GEOM ? RASTER_BLOCK : 1];
+    __shared__ uint32_t s_gid[BWD ? RASTER_BLOCK : 1];
+    __shared__ uint32_t s_hit[BWD ? RASTER_BLOCK : 1];
+    __shared__ uint32_t s_last;
+
+    const uint32_t tile = blockIdx.x;
+    const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
+    const uint32_t l = threadIdx.x;
+    const uint32_t px = tx * TILE_W + compact_bits_16(l);
+    const uint32_t py = ty * TILE_W + compact_bits_16(l >> 1);
+    const bool inside = px < a.img_w && py < a.img_h;
+    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+    const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
+    if (BWD && l == 0) s_last = lo;
+
+    float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+    float depth_acc = 0.0f, median = 0.0f, dist_b = 0.0f, dist_c = 0.0f, nx = 0.0f, ny = 0.0f, nz = 0.0f;
+    uint32_t median_id = 0xFFFFFFFFu;
+    bool done = !inside;
+    uint32_t last = lo;
+
+    for (uint32_t start = lo; start < hi; start += RASTER_BLOCK) {
+        // Barrier + vote: protects the previous batch's LDS reads and ends the
+        // tile once every pixel is done.
+        if (__syncthreads_count(!done) == 0) break;
+        const uint32_t rem = min((uint32_t)RASTER_BLOCK, hi - start);
+        if (l < rem) {
+            const uint32_t gid = a.gids[start + l];
+            const float4 pa = a.proj_a[gid];
+            const float4 pb = a.proj_b[gid];
+            s_a[l] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
+            s_b[l] = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
+            s_c[l] = a.proj_c[gid];
+            if constexpr (GEOM) s_d[l] = a.proj_aux[gid];
+            if constexpr (BWD) { s_gid[l] = gid; s_hit[l] = 0u; }
+        }
+        __syncthreads();
+        for (uint32_t t = 0; t < rem && !done; ++t) {
+            const float4 sa = s_a[t];
+            const float4 sb = s_b[t];
+            const float dx = pcx - sa.x, dy = pcy - sa.y;
+            const float sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);
+            const float G = expf_neg(-sigma);
+            const float alpha = mn(ALPHA_CAP, sb.y * G);
+            const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
+            if (sigma >= 0.0f && w_cut > 0.0f) {
+                const float ae = alpha * w_cut;
+                const float nt = T * (1.0f - ae);
+                if (nt <= T_STOP) {
+                    done = true;
+                } else {
+                    if constexpr (BWD) s_hit[t] = 1u;
+                    const float vis = ae * T;
+                    cr = __builtin_fmaf(mx(sb.z, 0.0f), vis, cr);
+                    cg = __builtin_fmaf(mx(sb.w, 0.0f), vis, cg);
+                    cb = __builtin_fmaf(mx(s_c[t], 0.0f), vis, cb);
+                    if constexpr (GEOM) {
+                        const float4 d = s_d[t];
+                        depth_acc = __builtin_fmaf(d.x, vis, depth_acc);
+                        if (T > 0.5f) { median = d.x; median_id = start + t; }
+                        const float m = dist_depth(d.x);
+                        dist_b = __builtin_fmaf(m, vis, dist_b);
+                        dist_c = __builtin_fmaf(m * m, vis, dist_c);
+                        nx = __builtin_fmaf(d.y, vis, nx);
+                        ny = __builtin_fmaf(d.z, vis, ny);
+                        nz = __builtin_fmaf(d.w, vis, nz);
+                    }
+                    T = nt;
+                    last = start + t + 1;
+                }
+            }
+        }
+        if constexpr (BWD) {
+            __syncthreads();
+            if (l < rem && s_hit[l]) a.visible[s_gid[l]] = 1.0f;
+        }
+    }
+
+    const float fr = __builtin_fmaf(T, a.bg_r, cr);
+    const float fg = __builtin_fmaf(T, a.bg_g, cg);
+    const float fb = __builtin_fmaf(T, a.bg_b, cb);
+    const float fa = 1.0f - T;
+    const size_t pid = (size_t)py * a.img_w + px;
+    if (inside) {
+        if constexpr (GEOM) {
+            float4* o = reinterpret_cast<float4*>(a.out) + pid * 3;
+            o[0] = make_float4(fr, fg, fb, fa);
+            o[1] = make_float4(depth_acc, median, nx, ny);
+            o[2] = make_float4(nz, dist_b, dist_c, as_f(median_id));
+        } else if constexpr (BWD) {
+            reinterpret_cast<float4*>(a.out)[pid] = make_float4(fr, fg, fb, fa);
+        } else {
+            const uint32_t r8 = f2u_sat(clampf(fr * 255.0f, 0.0f, 255.0f));
+            const uint32_t g8 = f2u_sat(clampf(fg * 255.0f, 0.0f, 255.0f));
+            const uint32_t b8 = f2u_sat(clampf(fb * 255.0f, 0.0f, 255.0f));
+            const uint32_t a8 = f2u_sat(clampf(fa * 255.0f, 0.0f, 255.0f));
+            reinterpret_cast<uint32_t*>(a.out)[pid] = r8 | (g8 << 8) | (b8 << 16) | (a8 << 24);
+        }
+    }
+    if constexpr (BWD) {
+        __syncthreads();
+        atomicMax(&s_last, last);
+        __syncthreads();
+        if (l == 0) {
+            a.ranges_shrunk[tile * 2] = lo;
+            a.ranges_shrunk[tile * 2 + 1] = s_last;
+        }
+    }
+}
+
+// 10-component reduce-scatter over a 64-lane wavefront.  After it, lane L
+// holds the wave sum of component 5*b5 + 3*b4 + 2*b3 + b2 (b = bits of L)
+// when that index is a real component; lanes with L & 3 == 0 write it.
+VS_DEV float reduce_scatter10(float v[10], uint32_t lane, int& comp) {
+    const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8, h4 = lane & 4;
+    float w[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const float keep = h32 ? v[i + 5] : v[i];
+        const float send = h32 ? v[i] : v[i + 5];
+        w[i] = keep + __shfl_xor(send, 32);
+    }
+    float x[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const float hiv = (i + 3 < 5) ? w[i + 3] : 0.0f;
+        const float keep = h16 ? hiv : w[i];
+        const float send = h16 ? w[i] : hiv;
+        x[i] = keep + __shfl_xor(send, 16);
+    }
+    float y[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float hiv = (i + 2 < 3) ? x[i + 2] : 0.0f;
+        const float keep = h8 ? hiv : x[i];
+        const float send = h8 ? x[i] : hiv;
+        y[i] = keep + __shfl_xor(send, 8);
+    }
+    float z = (h4 ? y[1] : y[0]) + __shfl_xor(h4 ? y[0] : y[1], 4);
+    z += __shfl_xor(z, 2);
+    z += __shfl_xor(z, 1);
+    const int i3 = (h8 ? 2 : 0) + (h4 ? 1 : 0);          // 0..3, 3 = padding
+    const int i5 = (h16 ? 3 : 0) + i3;                     // 0..5, 5 = padding
+    comp = (i3 < 3 && i5 < 5) ? (h32 ? 5 : 0) + i5 : -1;
+    return z;
+}
+
+template <bool SMOOTH>
+__global__ void __launch_bounds__(RASTER_BLOCK) raster_bwd_kernel(RasterBwdArgs a) {
+    __shared__ float4 s_a[BWD_BATCH];       // x, y, c00/2, c01
+    __shared__ float4 s_b[BWD_BATCH];       // c11/2, opacity, r, g
+    __shared__ float s_c[BWD_BATCH];        // b
+    __shared__ uint32_t s_gid[BWD_BATCH];
+    __shared__ float s_part[RASTER_BLOCK / 64][BWD_BATCH][10];
+    __shared__ uint32_t s_active[RASTER_BLOCK / 64];
+
+    const uint32_t tile = blockIdx.x;
+    const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
+    const uint32_t l = threadIdx.x, lane = l & 63, wave = l >> 6;
+    const uint32_t px = tx * TILE_W + compact_bits_16(l);
+    const uint32_t py = ty * TILE_W + compact_bits_16(l >> 1);
+    const bool inside = px < a.img_w && py < a.img_h;
+    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+    const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
+    if (lo >= hi) return;   // uniform per tile
+
+    // Pixel replay state, bwd/kernels/rasterize_backwards_planes.rs:194-209.
+    float sr = 0.0f, sg = 0.0f, sb = 0.0f, T = 0.0f, vr = 0.0f, vg = 0.0f, vb = 0.0f, vt = 0.0f, rscale = 0.0f;
+    if (inside) {
+        const size_t base = ((size_t)py * a.img_w + px) * a.channels;
+        const float4 o = *reinterpret_cast<const float4*>(a.out_img + base);
+        const float4 v = *reinterpret_cast<const float4*>(a.v_out + base);
+        const float t_final = 1.0f - o.w;
+        sr = o.x - t_final * a.bg_r;
+        sg = o.y - t_final * a.bg_g;
+        sb = o.z - t_final * a.bg_b;
+        T = 1.0f;
+        vr = v.x; vg = v.y; vb = v.z;
+        vt = (v.w - (a.bg_r * vr + a.bg_g * vg + a.bg_b * vb)) * t_final;
+        rscale = 1.0f / mx(o.w, 1.0e-5f);
+    }
+    const float img_w = (float)a.img_w, img_h = (float)a.img_h;
+
+    for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
+        const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
+        __syncthreads();
+        if (l < rem) {
+            const uint32_t gid = a.gids[start + l];
+            const float4 pa = a.proj_a[gid];
+            const float4 pb = a.proj_b[gid];
+            s_a[l] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
+            s_b[l] = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
+            s_c[l] = a.proj_c[gid];
+            s_gid[l] = gid;
+        }
+        const bool wave_active = __ballot(T > T_STOP) != 0ull;
+        if (lane == 0) s_active[wave] = wave_active ? 1u : 0u;
+        __syncthreads();
+        if (wave_active) {
+            for (uint32_t t = 0; t < rem; ++t) {
+                float g[10];
+#pragma unroll
+                for (int k = 0; k < 10; ++k) g[k] = 0.0f;
+                bool contrib = false;
+                if (T > T_STOP) {
+                    const float4 sa = s_a[t];
+                    const float4 sbv = s_b[t];
+                    const float dx = pcx - sa.x, dy = pcy - sa.y;
+                    const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);
+                    const float G = expf_neg(-sigma);
+                    const float opac = sbv.y;
+                    const float alpha = mn(ALPHA_CAP, opac * G);
+                    const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
+                    if (sigma >= 0.0f && w_cut > 0.0f) {
+                        const float ae = alpha * w_cut;
+                        const float nt = T * (1.0f - ae);
+                        if (nt <= T_STOP) {
+                            T = 0.0f;
+                        } else {
+                            contrib = true;
+                            const float c_r = sbv.z, c_g = sbv.w, c_b = s_c[t];
+                            const float cl_r = mx(c_r, 0.0f), cl_g = mx(c_g, 0.0f), cl_b = mx(c_b, 0.0f);
+                            const float vis = ae * T;
+                            g[5] = (c_r >= 0.0f) ? vis * vr : 0.0f;
+                            g[6] = (c_g >= 0.0f) ? vis * vg : 0.0f;
+                            g[7] = (c_b >= 0.0f) ? vis * vb : 0.0f;
+                            const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+                            const float dot_rgb = ((T * cl_r - sr) * vr + (T * cl_g - sg) * vg + (T * cl_b - sb) * vb) * ra;
+                            const float v_ae = dot_rgb + vt * ra;
+                            const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+                            const float v_sigma = -alpha * v_alpha;
+                            const float bdx = -dx, bdy = -dy;       // mean - pixel centre
+                            const float c00 = 2.0f * sa.z, c01 = sa.w, c11 = 2.0f * sbv.x;
+                            const float vxy_x = v_sigma * (c00 * bdx + c01 * bdy);
+                            const float vxy_y = v_sigma * (c01 * bdx + c11 * bdy);
+                            if (opac * G <= ALPHA_CAP) {
+                                g[2] = 0.5f * v_sigma * bdx * bdx;
+                                g[3] = v_sigma * bdx * bdy;
+                                g[4] = 0.5f * v_sigma * bdy * bdy;
+                                g[0] = vxy_x;
+                                g[1] = vxy_y;
+                                g[8] = v_alpha * G;
+                                const float ux = vxy_x * img_w, uy = vxy_y * img_h;
+                                g[9] = __builtin_sqrtf(ux * ux + uy * uy) * rscale;
+                            }
+                            sr = sr - vis * cl_r;
+                            sg = sg - vis * cl_g;
+                            sb = sb - vis * cl_b;
+                            T = nt;
+                        }
+                    }
+                }
+                int comp = -1;
+                float val = 0.0f;
+                if (__ballot(contrib) != 0ull) val = reduce_scatter10(g, lane, comp);
+                else {
+                    // keep the writer pattern identical: lanes 4k with a real component write zero
+                    const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8, h4 = lane & 4;
+                    const int i3 = (h8 ? 2 : 0) + (h4 ? 1 : 0), i5 = (h16 ? 3 : 0) + i3;
+                    comp = (i3 < 3 && i5 < 5) ? (h32 ? 5 : 0) + i5 : -1;
+                }
+                if ((lane & 3) == 0 && comp >= 0) s_part[wave][t][comp] = val;
+            }
+        }
+        __syncthreads();
+        for (uint32_t idx = l; idx < rem * 10; idx += RASTER_BLOCK) {
+            const uint32_t t = idx / 10, c = idx % 10;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < RASTER_BLOCK / 64; ++w)
+                if (s_active[w]) sum += s_part[w][t][c];
+            if (sum != 0.0f) atomicAdd(&a.v_combined[(size_t)s_gid[t] * 10 + c], sum);
+        }
+    }
+}
+
+__global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, const float* __restrict__ gt, uint32_t w,
+                                    uint32_t h, float mcx, float mcy, float mr, float inv_count, float* __restrict__ v) {
+    const uint32_t pid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (pid >= w * h) return;
+    const uint32_t x = pid % w, y = pid / w;
+    bool in_mask = true;
+    if (mr > 0.0f) {
+        const float dx = (float)x + 0.5f - mcx, dy = (float)y + 0.5f - mcy;
+        in_mask = dx * dx + dy * dy <= mr * mr;
+    }
+    for (uint32_t c = 0; c < C; ++c) {
+        float g = 0.0f;
+        if (c < 3 && in_mask) {
+            const float d = pred[(size_t)pid * C + c] - gt[(size_t)pid * 3 + c];
+            g = (d > 0.0f) ? inv_count : ((d < 0.0f) ? -inv_count : 0.0f);
+        }
+        v[(size_t)pid * C + c] = g;
+    }
+}
+
+hipError_t launch_tile_ranges(const uint64_t* keys, uint32_t n, uint32_t shift, uint32_t num_tiles, uint32_t* ranges,
+                              hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    tile_ranges_kernel<<<(n + 255) / 256, 256, 0, s>>>(keys, n, shift, num_tiles, ranges);
+    return hipGetLastError();
+}
+
+hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s) {
+    if (a.num_tiles == 0) return hipSuccess;
+    const dim3 grid(a.num_tiles);
+    if (!bwd_info) raster_fwd_kernel<false, false, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
+    else if (geometry) raster_fwd_kernel<true, true, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
+    else if (smooth) raster_fwd_kernel<true, false, true><<<grid, RASTER_BLOCK, 0, s>>>(a);
+    else raster_fwd_kernel<true, false, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s) {
+    if (a.num_tiles == 0) return hipSuccess;
+    if (smooth) raster_bwd_kernel<true><<<a.num_tiles, RASTER_BLOCK, 0, s>>>(a);
+    else raster_bwd_kernel<false><<<a.num_tiles, RASTER_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float* gt, uint32_t w, uint32_t h, float mcx,
+                               float mcy, float mr, float inv_count, float* v_out, hipStream_t s) {
+    const uint32_t n = w * h;
+    if (n == 0) return hipSuccess;
+    l1_cotangent_kernel<<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    return hipGetLastError();
+}
+
+} // namespace vs

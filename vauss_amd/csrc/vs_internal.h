@@ -1,0 +1,124 @@
+// vs_internal.h -- launch parameters and launcher declarations shared between
+// the kernel translation units and the C-ABI layer (api.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/vsplat.h"
+
+namespace vs {
+
+constexpr uint32_t TILE_W_HOST_ = 16;   // tile edge in pixels (kernels/helpers.rs:15)
+
+// Device counters written by the projection stage and read back once.
+enum : uint32_t {
+    CNT_VISIBLE = 0,      // splats surviving every cull
+    CNT_DEPTH_MIN = 1,    // min / max raw f32 bits of visible depths
+    CNT_DEPTH_MAX = 2,
+    CNT_ISECT64 = 4,      // words 4..5: total intersections as a u64
+    CNT_COUNT = 8,
+};
+
+struct ProjectArgs {
+    vs_camera cam;
+    uint32_t img_w, img_h, tile_bw, tile_bh;
+    uint32_t num_splats, sh_degree;
+    float log_scale_offset;
+    const float* transforms;
+    const float* sh;
+    const float* raw_opac;
+    // outputs, indexed by global splat id
+    float* opacities;           // [N]
+    float* max_radius;          // [N]
+    uint32_t* counts;           // [N] tiles hit
+    uint32_t* depth_bits;       // [N] raw f32 bits of view z
+    float4* proj_a;             // [N] x, y, c00, c01
+    float4* proj_b;             // [N] c11, opacity, r, g
+    float* proj_c;              // [N] b
+    float4* proj_aux;           // [N] z, nx, ny, nz (geometry) or null
+    uint32_t* block_sums;       // [ceil(N/256)] tiles hit per 256-splat block
+    uint32_t* counters;         // [CNT_COUNT]
+};
+
+struct EmitArgs {
+    uint32_t num_splats, tile_bw, tile_bh;
+    uint32_t depth_shift, depth_min;
+    const uint32_t* counts;
+    const uint32_t* block_offsets;   // exclusive scan of block_sums
+    const uint32_t* depth_bits;
+    const float4* proj_a;
+    const float4* proj_b;
+    uint64_t* keys;                  // [I]
+    uint32_t* vals;                  // [I]
+};
+
+struct RasterArgs {
+    uint32_t img_w, img_h, tile_bw, tile_bh, num_tiles;
+    float bg_r, bg_g, bg_b;
+    const uint32_t* gids;            // sorted intersections -> global splat id
+    const uint32_t* ranges;          // [T,2]
+    uint32_t* ranges_shrunk;         // [T,2] written by bwd-info passes (may alias nothing else)
+    const float4* proj_a;
+    const float4* proj_b;
+    const float* proj_c;
+    const float4* proj_aux;
+    void* out;                       // f32 [H,W,C] or u32 [H,W]
+    float* visible;                  // [N] or null
+};
+
+struct RasterBwdArgs {
+    uint32_t img_w, img_h, tile_bw, tile_bh, num_tiles;
+    float bg_r, bg_g, bg_b;
+    const uint32_t* gids;
+    const uint32_t* ranges;          // shrunk ranges
+    const float4* proj_a;
+    const float4* proj_b;
+    const float* proj_c;
+    const float* out_img;            // [H,W,C]
+    const float* v_out;              // [H,W,C]
+    uint32_t channels;
+    float* v_combined;               // [N,10]
+};
+
+struct ProjectBwdArgs {
+    vs_camera cam;
+    uint32_t num_splats, sh_degree;
+    float log_scale_offset;
+    const float* transforms;
+    const float* sh;
+    const float* raw_opac;
+    const uint32_t* counts;          // visible <=> counts defined; culled rows get zeros
+    const float* v_combined;         // [N,10]
+    float* v_transforms;
+    float* v_sh;
+    float* v_raw_opac;
+    float* v_refine;
+};
+
+// ---- launchers (return hipError_t of the launch) -------------------------------
+hipError_t launch_init_counters(uint32_t* counters, hipStream_t s);
+hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
+hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
+hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
+hipError_t launch_tile_ranges(const uint64_t* keys, uint32_t n, uint32_t shift, uint32_t num_tiles,
+                              uint32_t* ranges, hipStream_t s);
+hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
+hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s);
+hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s);
+hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float* gt, uint32_t w, uint32_t h,
+                               float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
+hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float mr, uint32_t* out, hipStream_t s);
+
+// Scans.  `tmp` needs scan_tmp_words(n) u32 words.
+size_t scan_tmp_words(uint64_t n);
+hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
+                    uint32_t* total_out, hipStream_t s);
+hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_t* total_out, hipStream_t s);
+
+// Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
+size_t sort_tmp_bytes(uint64_t n, bool key64);
+hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
+                            uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
+                            void* tmp, hipStream_t s);
+
+} // namespace vs

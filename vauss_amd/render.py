@@ -1,0 +1,359 @@
+"""Host-side mirror of the reference's render / sort / scan call surface.
+
+The functions keep the reference's names, argument meaning and error
+behaviour and drive the gfx950 kernels through the C ABI (include/vsplat.h):
+
+  render              SplatOps::render               crates/splat-train-render/src/lib.rs:53-90
+  render_backward     SplatBwdOps::rasterize_bwd +   bwd/burn_glue.rs:70-111
+                      project_bwd (dense gradients)
+  radix_argsort*      crates/splat-train-sort/src/lib.rs:15-189
+  prefix_sum          crates/splat-train-scan/src/lib.rs:24-83
+  scan_in_place       crates/splat-train-scan/src/lib.rs:85-96
+
+Tensors are torch tensors on a ROCm device; torch provides device memory and
+streams only.  u32 data travels in int32 tensors (same bits), u64 keys in
+int64 tensors.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from .camera import Camera
+
+
+class RasterPass(enum.IntEnum):
+    """RasterPass (gaussian_splats.rs:32-107) -- the passes built here."""
+    FORWARD = _lib.PASS_FORWARD
+    BACKWARD = _lib.PASS_BACKWARD
+    FLOAT = _lib.PASS_FLOAT
+    BACKWARD_SMOOTH_CUTOFF = _lib.PASS_BACKWARD_SMOOTH_CUTOFF
+    GEOMETRY = _lib.PASS_GEOMETRY
+
+    def bwd_info(self) -> bool:
+        return self is not RasterPass.FORWARD
+
+    def out_channels(self) -> int:
+        return 12 if self is RasterPass.GEOMETRY else (4 if self.bwd_info() else 1)
+
+
+class SplatRenderMode(enum.IntEnum):
+    """SplatRenderMode (gaussian_splats.rs:19-26); only DEFAULT is built."""
+    DEFAULT = _lib.MODE_DEFAULT
+    MIP = _lib.MODE_MIP
+    SURFEL = _lib.MODE_SURFEL
+
+
+def sh_degree_from_coeffs(n: int) -> int:
+    """crates/splat-train-render/src/sh.rs:10-19."""
+    table = {1: 0, 4: 1, 9: 2, 16: 3, 25: 4}
+    if n not in table:
+        raise ValueError(f"Unsupported SH coefficient count {n}: expected 1, 4, 9, 16 or 25")
+    return table[n]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+class Context:
+    """One vs_ctx per (device, stream); work goes on torch's current stream."""
+
+    _cache: dict = {}
+
+    def __init__(self, device: int):
+        self.lib = _lib.load()
+        h = C.c_void_p()
+        _lib.check(self.lib.vs_ctx_create(device, None, C.byref(h)))
+        self.handle = h
+        self.device = device
+
+    @classmethod
+    def get(cls, device: torch.device) -> "Context":
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        ctx = cls._cache.get(idx)
+        if ctx is None:
+            ctx = cls._cache[idx] = Context(idx)
+        stream = torch.cuda.current_stream(idx).cuda_stream
+        _lib.check(ctx.lib.vs_ctx_set_stream(ctx.handle, C.c_void_p(stream)))
+        return ctx
+
+    def enable_timing(self, on: bool = True) -> None:
+        _lib.check(self.lib.vs_ctx_enable_timing(self.handle, 1 if on else 0))
+
+    def stage_times(self) -> dict:
+        t = _lib.VsStageTimes()
+        _lib.check(self.lib.vs_ctx_stage_times(self.handle, C.byref(t)))
+        return {name: getattr(t, name) for name, _ in _lib.VsStageTimes._fields_}
+
+
+@dataclass
+class RenderAux:
+    """RenderAux, render_aux.rs:74-100."""
+    num_visible: int
+    num_intersections: int
+    visible: Optional[torch.Tensor]
+    max_radius: torch.Tensor
+    opacities: torch.Tensor
+    tile_offsets: torch.Tensor
+    img_size: tuple
+
+
+class ForwardState:
+    """Owner of the library's backward state (vs_fwd_state)."""
+
+    def __init__(self, handle: C.c_void_p, ctx: Context, pass_: RasterPass, num_splats: int, sh_degree: int):
+        self.handle = handle
+        self.ctx = ctx
+        self.pass_ = pass_
+        self.num_splats = num_splats
+        self.sh_degree = sh_degree
+
+    def view(self) -> _lib.VsStateView:
+        v = _lib.VsStateView()
+        _lib.check(self.ctx.lib.vs_fwd_state_view(self.handle, C.byref(v)))
+        return v
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx.lib.vs_fwd_state_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class RenderOutput:
+    """RenderOutput, render_aux.rs:17-42 (state is opaque here)."""
+    out_img: torch.Tensor
+    aux: RenderAux
+    state: Optional[ForwardState]
+    camera_uniforms: _lib.VsCamera
+    background: tuple
+
+
+@dataclass
+class SplatGrads:
+    """SplatGrads (bwd/burn_glue.rs:28-35), dense per global splat."""
+    v_transforms: torch.Tensor
+    v_coeffs: torch.Tensor
+    v_raw_opac: torch.Tensor
+    v_refine_weight: torch.Tensor
+    v_combined: torch.Tensor
+
+
+def _check_splats(transforms, sh_coeffs, raw_opacities):
+    if transforms.dim() != 2 or transforms.shape[1] != 10:
+        raise ValueError(f"transforms must be [N, 10], got {tuple(transforms.shape)}")
+    n = transforms.shape[0]
+    if sh_coeffs.dim() != 3 or sh_coeffs.shape[0] != n or sh_coeffs.shape[2] != 3:
+        raise ValueError(f"sh_coeffs must be [N, C, 3], got {tuple(sh_coeffs.shape)}")
+    if raw_opacities.dim() != 1 or raw_opacities.shape[0] != n:
+        raise ValueError(f"raw_opacities must be [N], got {tuple(raw_opacities.shape)}")
+    for name, t in (("transforms", transforms), ("sh_coeffs", sh_coeffs), ("raw_opacities", raw_opacities)):
+        if t.dtype != torch.float32:
+            raise TypeError(f"{name} must be float32, got {t.dtype}")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must live on the GPU")
+    return n, sh_degree_from_coeffs(sh_coeffs.shape[1])
+
+
+def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset) -> _lib.VsSplats:
+    s = _lib.VsSplats()
+    s.transforms = _ptr(transforms)
+    s.sh_coeffs = _ptr(sh_coeffs)
+    s.raw_opacities = _ptr(raw_opacities)
+    s.num_splats = transforms.shape[0]
+    s.sh_degree = degree
+    s.log_scale_offset = float(log_scale_offset)
+    return s
+
+
+def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs: torch.Tensor,
+           raw_opacities: torch.Tensor, background=(0.0, 0.0, 0.0), pass_: RasterPass = RasterPass.BACKWARD,
+           render_mode: SplatRenderMode = SplatRenderMode.DEFAULT, log_scale_offset: float = 0.0,
+           validate: bool = False) -> RenderOutput:
+    """SplatOps::render.  `camera` is a Camera or ready-made vs_camera uniforms.
+
+    Returns the image ([H,W,C] f32, or [H,W] int32-packed RGBA8 for
+    FORWARD), the aux outputs and, for every pass but FORWARD, the state the
+    backward needs."""
+    w, h = int(img_size[0]), int(img_size[1])
+    if w <= 0 or h <= 0:
+        raise ValueError("Can't render images with 0 size.")
+    pass_ = RasterPass(pass_)
+    transforms = transforms.contiguous()
+    sh_coeffs = sh_coeffs.contiguous()
+    raw_opacities = raw_opacities.contiguous()
+    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities)
+    if validate:
+        for name, t in (("transforms", transforms), ("sh_coeffs", sh_coeffs), ("raw_opacities", raw_opacities)):
+            if not bool(torch.isfinite(t).all()):
+                raise _lib.VsError(_lib.VS_ERR_NONFINITE, f"{name} holds NaN or Inf")
+    dev = transforms.device
+    ctx = Context.get(dev)
+    cam = camera.uniforms((w, h)) if isinstance(camera, Camera) else camera
+    tbw, tbh = (w + 15) // 16, (h + 15) // 16
+    ch = pass_.out_channels()
+    if ch == 1:
+        out_img = torch.empty((h, w), dtype=torch.int32, device=dev)
+    else:
+        out_img = torch.empty((h, w, ch), dtype=torch.float32, device=dev)
+    visible = torch.empty(n, dtype=torch.float32, device=dev) if pass_.bwd_info() else None
+    max_radius = torch.empty(n, dtype=torch.float32, device=dev)
+    opacities = torch.empty(n, dtype=torch.float32, device=dev)
+    tile_offsets = torch.empty((tbh, tbw, 2), dtype=torch.int32, device=dev)
+    out = _lib.VsFwdOut()
+    out.out_img = _ptr(out_img)
+    out.visible = _ptr(visible)
+    out.max_radius = _ptr(max_radius)
+    out.opacities = _ptr(opacities)
+    out.tile_offsets = _ptr(tile_offsets)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset)
+    bg = (C.c_float * 3)(*[float(v) for v in background])
+    st = C.c_void_p()
+    _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg, int(pass_),
+                                         int(render_mode), C.byref(out), C.byref(st)))
+    aux = RenderAux(out.num_visible, out.num_intersections, visible, max_radius, opacities, tile_offsets, (w, h))
+    state = ForwardState(st, ctx, pass_, n, degree) if st.value else None
+    return RenderOutput(out_img, aux, state, cam, tuple(float(v) for v in background))
+
+
+def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
+                    raw_opacities: torch.Tensor, v_output: torch.Tensor, log_scale_offset: float = 0.0) -> SplatGrads:
+    """rasterize_bwd followed by project_bwd, returning dense gradients."""
+    if output.state is None or output.state.handle is None:
+        raise ValueError("the forward pass kept no backward state (use a bwd-info pass)")
+    transforms = transforms.contiguous()
+    sh_coeffs = sh_coeffs.contiguous()
+    raw_opacities = raw_opacities.contiguous()
+    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities)
+    v_output = v_output.contiguous()
+    if v_output.shape != output.out_img.shape or v_output.dtype != torch.float32:
+        raise ValueError(f"v_output must be float32 {tuple(output.out_img.shape)}, got {tuple(v_output.shape)}")
+    dev = transforms.device
+    ctx = output.state.ctx
+    Context.get(dev)
+    k = (degree + 1) ** 2
+    g = SplatGrads(torch.empty((n, 10), dtype=torch.float32, device=dev),
+                   torch.empty((n, k, 3), dtype=torch.float32, device=dev),
+                   torch.empty(n, dtype=torch.float32, device=dev),
+                   torch.empty(n, dtype=torch.float32, device=dev),
+                   torch.empty((n, 10), dtype=torch.float32, device=dev))
+    grads = _lib.VsGrads()
+    grads.v_transforms = _ptr(g.v_transforms)
+    grads.v_sh_coeffs = _ptr(g.v_coeffs)
+    grads.v_raw_opacities = _ptr(g.v_raw_opac)
+    grads.v_refine_weight = _ptr(g.v_refine_weight)
+    grads.v_combined = _ptr(g.v_combined)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset)
+    _lib.check(ctx.lib.vs_render_backward(ctx.handle, output.state.handle, C.byref(splats), _ptr(output.out_img),
+                                          _ptr(v_output), C.byref(grads)))
+    return g
+
+
+def _u32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"{name} must hold u32 data (int32/uint32 tensor), got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"Please ensure {name} is contiguous")
+    return t
+
+
+def radix_argsort_skip_low_with_count(input_keys: torch.Tensor, input_values: torch.Tensor, skip_bits: int,
+                                      sorting_bits: int, num_keys: Optional[torch.Tensor]):
+    """Stable sort of (key, value) by key bits skip..skip+8*ceil(bits/8) of the
+    active prefix whose length is num_keys[0] (on the GPU)."""
+    _u32(input_keys, "input keys")
+    _u32(input_values, "input values")
+    if input_keys.shape[0] != input_values.shape[0]:
+        raise ValueError("Input keys and values must have the same number of elements")
+    if skip_bits + sorting_bits > 32:
+        raise ValueError("Can only sort up to 32 bits")
+    n = input_keys.shape[0]
+    if n == 0 or sorting_bits == 0:
+        return input_keys, input_values
+    ctx = Context.get(input_keys.device)
+    out_k = torch.empty_like(input_keys)
+    out_v = torch.empty_like(input_values)
+    if num_keys is not None:
+        _u32(num_keys, "num_keys")
+        # entries past the active prefix keep their input values
+        out_k.copy_(input_keys)
+        out_v.copy_(input_values)
+    _lib.check(ctx.lib.vs_radix_argsort_u32(ctx.handle, _ptr(input_keys), _ptr(input_values), n, _ptr(num_keys),
+                                            skip_bits, sorting_bits, _ptr(out_k), _ptr(out_v)))
+    return out_k, out_v
+
+
+def radix_argsort_with_count(input_keys, input_values, sorting_bits, num_keys):
+    """crates/splat-train-sort/src/lib.rs:28-35."""
+    return radix_argsort_skip_low_with_count(input_keys, input_values, 0, sorting_bits, num_keys)
+
+
+def radix_argsort(input_keys, input_values, sorting_bits):
+    """crates/splat-train-sort/src/lib.rs:15-24."""
+    return radix_argsort_skip_low_with_count(input_keys, input_values, 0, sorting_bits, None)
+
+
+def radix_argsort_u64(keys: torch.Tensor, values: torch.Tensor, sorting_bits: int):
+    """Stable sort of packed 64-bit keys (int64 tensor) by bits [0, sorting_bits)."""
+    if keys.dtype not in (torch.int64, torch.uint64) or not keys.is_contiguous():
+        raise TypeError("keys must be a contiguous int64/uint64 tensor")
+    _u32(values, "values")
+    n = keys.shape[0]
+    ctx = Context.get(keys.device)
+    out_k = torch.empty_like(keys)
+    out_v = torch.empty_like(values)
+    if n:
+        _lib.check(ctx.lib.vs_radix_argsort_u64(ctx.handle, _ptr(keys), _ptr(values), n, sorting_bits,
+                                                _ptr(out_k), _ptr(out_v)))
+    return out_k, out_v
+
+
+def prefix_sum(x: torch.Tensor) -> torch.Tensor:
+    """Inclusive prefix sum of a contiguous 1-D u32 tensor."""
+    _u32(x, "input")
+    if x.shape[0] == 0:
+        return x
+    ctx = Context.get(x.device)
+    out = torch.empty_like(x)
+    _lib.check(ctx.lib.vs_prefix_sum_u32(ctx.handle, _ptr(x), _ptr(out), x.shape[0]))
+    return out
+
+
+def scan_in_place(x: torch.Tensor) -> None:
+    """Inclusive prefix sum in place (one workgroup; meant for short arrays)."""
+    _u32(x, "values")
+    if x.shape[0] == 0:
+        return
+    ctx = Context.get(x.device)
+    _lib.check(ctx.lib.vs_scan_in_place_u32(ctx.handle, _ptr(x), x.shape[0]))
+
+
+def l1_cotangent(pred: torch.Tensor, gt: torch.Tensor, mask_center=(0.0, 0.0), mask_radius: float = 0.0) -> torch.Tensor:
+    """d(mean L1 over rgb)/d pred for an [H,W,C] prediction and [H,W,3] target."""
+    pred = pred.contiguous()
+    gt = gt.contiguous()
+    h, w, c = pred.shape
+    ctx = Context.get(pred.device)
+    v = torch.empty_like(pred)
+    _lib.check(ctx.lib.vs_l1_cotangent(ctx.handle, _ptr(pred), c, _ptr(gt), w, h, float(mask_center[0]),
+                                       float(mask_center[1]), float(mask_radius), _ptr(v)))
+    return v
+
+
+def unpack_rgba8(packed: torch.Tensor) -> torch.Tensor:
+    """[H,W] packed RGBA8 (FORWARD pass) -> [H,W,4] uint8."""
+    p = packed.to(torch.int64) & 0xFFFFFFFF
+    return torch.stack([(p >> s) & 0xFF for s in (0, 8, 16, 24)], dim=-1).to(torch.uint8)
