@@ -18,7 +18,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 
-FLAG_BWD_INFO, FLAG_GEOMETRY, FLAG_SMOOTH_CUTOFF = 1, 2, 4
+FLAG_BWD_INFO, FLAG_GEOMETRY, FLAG_SMOOTH_CUTOFF, FLAG_BRUTE_FORCE = 1, 2, 4, 8
 (F_INTERSECT_COUNTS, F_MAX_RADIUS, F_OPACITIES, F_GLOBAL_FROM_COMPACT, F_DEPTHS, F_PROJECTED, F_AUX, F_ISECT_TILE,
  F_ISECT_GID, F_TILE_OFFSETS, F_TILE_OFFSETS_SHRUNK, F_VISIBLE, F_OUT_IMG) = range(13)
 

@@ -564,6 +564,7 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
     const bool bwd_info = flags & OR_FLAG_BWD_INFO;
     const bool geometry = flags & OR_FLAG_GEOMETRY;
     const bool smooth = flags & OR_FLAG_SMOOTH_CUTOFF;
+    const bool brute = flags & OR_FLAG_BRUTE_FORCE;
     f->tbw = (W + TILE_W - 1) / TILE_W; f->tbh = (H + TILE_W - 1) / TILE_W; f->T = f->tbw * f->tbh;
     f->out_ch = geometry ? 12 : 4;
     const uint32_t K = f->K;
@@ -748,10 +749,11 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
     for (int64_t ti = 0; ti < (int64_t)f->T; ++ti) {
         const uint32_t tile = (uint32_t)ti;
         const uint32_t tx = tile % tbw, ty = tile / tbw;
-        const uint32_t lo = f->tile_offsets[(size_t)tile * 2], hi = f->tile_offsets[(size_t)tile * 2 + 1];
+        const uint32_t lo = brute ? 0u : f->tile_offsets[(size_t)tile * 2];
+        const uint32_t hi = brute ? V : f->tile_offsets[(size_t)tile * 2 + 1];
         std::vector<RasterSplat> list(hi - lo);
         for (uint32_t i = lo; i < hi; ++i) {
-            const uint32_t c = f->isect_cid[i];
+            const uint32_t c = brute ? sorted[i] : f->isect_cid[i];
             const float* row = &f->projected[(size_t)c * 9];
             RasterSplat s;
             s.x = row[0]; s.y = row[1]; s.c00 = row[2]; s.c01 = row[3]; s.c11 = row[4];
@@ -823,7 +825,7 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
                 }
             }
         }
-        if (bwd_info) f->tile_offsets_shrunk[(size_t)tile * 2 + 1] = max_useful;
+        if (bwd_info && !brute) f->tile_offsets_shrunk[(size_t)tile * 2 + 1] = max_useful;
     }
     f->evals = evals_total;
     *out = f.release();

@@ -39,6 +39,8 @@ enum {
     OR_FLAG_BWD_INFO = 1,       /* float RGBA image + visible marks + shrunk tile ends */
     OR_FLAG_GEOMETRY = 2,       /* 12-channel output with depth/normal/distortion */
     OR_FLAG_SMOOTH_CUTOFF = 4,  /* C^1 alpha cutoff (BackwardSmoothCutoff) */
+    OR_FLAG_BRUTE_FORCE = 8,    /* composite every pixel over the whole depth-sorted
+                                   visible list instead of its tile's list (checks binning) */
 };
 
 typedef struct or_fwd or_fwd;
