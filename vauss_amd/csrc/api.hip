@@ -79,7 +79,7 @@ struct vs_fwd_state {
     float* opacities = nullptr;
     float* max_radius = nullptr;
     float* visible = nullptr;
-    uint32_t* block_sums = nullptr;
+    uint32_t* block_stats = nullptr;
     uint32_t* counters = nullptr;
     uint32_t* ranges = nullptr;
     uint32_t* ranges_shrunk = nullptr;
@@ -246,7 +246,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     const size_t o_opac = out->opacities ? 0 : take((size_t)N * 4);
     const size_t o_rad = out->max_radius ? 0 : take((size_t)N * 4);
     const size_t o_vis = (bwd_info && !out->visible) ? take((size_t)N * 4) : 0;
-    const size_t o_bs = take((size_t)std::max(nblocks, 1u) * 4);
+    const size_t o_bs = take((size_t)std::max(nblocks, 1u) * 16);
     const size_t o_cnt = take(CNT_COUNT * 4);
     const size_t o_rng = take((size_t)T * 8), o_rngs = take((size_t)T * 8);
     VS_HIP(hipMallocAsync(&st->arena, off, s), "hipMallocAsync(splat arena)");
@@ -260,7 +260,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->opacities = out->opacities ? out->opacities : reinterpret_cast<float*>(base + o_opac);
     st->max_radius = out->max_radius ? out->max_radius : reinterpret_cast<float*>(base + o_rad);
     st->visible = bwd_info ? (out->visible ? out->visible : reinterpret_cast<float*>(base + o_vis)) : nullptr;
-    st->block_sums = reinterpret_cast<uint32_t*>(base + o_bs);
+    st->block_stats = reinterpret_cast<uint32_t*>(base + o_bs);
     st->counters = reinterpret_cast<uint32_t*>(base + o_cnt);
     st->ranges = reinterpret_cast<uint32_t*>(base + o_rng);
     st->ranges_shrunk = reinterpret_cast<uint32_t*>(base + o_rngs);
@@ -268,7 +268,6 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     // ---- projection --------------------------------------------------------------
     {
         StageTimer tm(ctx, ST_PROJECT);
-        VS_HIP(launch_init_counters(st->counters, s), "init counters");
         ProjectArgs pa{};
         pa.cam = *cam;
         pa.img_w = W; pa.img_h = H; pa.tile_bw = st->tbw; pa.tile_bh = st->tbh;
@@ -276,9 +275,9 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.raw_opac = sp->raw_opacities;
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
-        pa.proj_aux = st->proj_aux; pa.block_sums = st->block_sums; pa.counters = st->counters;
+        pa.proj_aux = st->proj_aux; pa.block_stats = st->block_stats;
         VS_HIP(launch_project(pa, s), "project kernel");
-        if (nblocks > 0) VS_HIP(scan_single_block(st->block_sums, nblocks, false, nullptr, s), "block offsets scan");
+        VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, s), "projection counts");
         if (bwd_info) VS_HIP(launch_fill_f32(st->visible, 0.0f, N, s), "zero visible");
         VS_HIP(launch_fill_u32(st->ranges, 0u, (uint64_t)T * 2, s), "zero ranges");
     }
@@ -315,7 +314,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
             ea.depth_shift = st->shift; ea.depth_min = st->dmin;
-            ea.counts = st->counts; ea.block_offsets = st->block_sums; ea.depth_bits = st->depth_bits;
+            ea.counts = st->counts; ea.block_offsets = st->block_stats; ea.depth_bits = st->depth_bits;
             ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.keys = keys_u; ea.vals = vals_u;
             VS_HIP(launch_emit(ea, s), "emit kernel");
         }

@@ -80,9 +80,57 @@ VS_DEV uint32_t wave_max(uint32_t v) {
     return v;
 }
 
-__global__ void __launch_bounds__(64) init_counters_kernel(uint32_t* c) {
-    const uint32_t i = threadIdx.x;
-    if (i < CNT_COUNT) c[i] = (i == CNT_DEPTH_MIN) ? 0xFFFFFFFFu : 0u;
+// One workgroup: exclusive scan of the block tile counts (in place) with a
+// 64-bit running total, plus the visible count and the depth-bit range.
+constexpr int FIN_BLOCK = 1024;
+__global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __restrict__ stats, uint32_t nb,
+                                                                   uint32_t* __restrict__ counters) {
+    __shared__ uint32_t s_w[FIN_BLOCK / 64];
+    __shared__ uint32_t s_vis[FIN_BLOCK / 64], s_min[FIN_BLOCK / 64], s_max[FIN_BLOCK / 64];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t* sums = stats;
+    const uint32_t* vis = stats + nb;
+    const uint32_t* dmin = stats + 2 * (size_t)nb;
+    const uint32_t* dmax = stats + 3 * (size_t)nb;
+    uint64_t carry = 0;
+    uint32_t v_acc = 0, mn_acc = 0xFFFFFFFFu, mx_acc = 0u;
+    for (uint32_t start = 0; start < nb; start += FIN_BLOCK) {
+        const uint32_t i = start + threadIdx.x;
+        const uint32_t x = (i < nb) ? sums[i] : 0u;
+        if (i < nb) {
+            v_acc += vis[i];
+            mn_acc = min(mn_acc, dmin[i]);
+            mx_acc = max(mx_acc, dmax[i]);
+        }
+        uint32_t incl = x;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o);
+            if ((int)lane >= o) incl += t;
+        }
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        uint64_t before = 0, chunk = 0;
+        for (uint32_t w = 0; w < FIN_BLOCK / 64; ++w) {
+            if (w < wave) before += s_w[w];
+            chunk += s_w[w];
+        }
+        if (i < nb) sums[i] = (uint32_t)(carry + before + incl - x);
+        carry += chunk;
+        __syncthreads();
+    }
+    const uint32_t wv = wave_sum(v_acc), wmn = wave_min(mn_acc), wmx = wave_max(mx_acc);
+    if (lane == 0) { s_vis[wave] = wv; s_min[wave] = wmn; s_max[wave] = wmx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t tv = 0, tmn = 0xFFFFFFFFu, tmx = 0u;
+        for (int w = 0; w < FIN_BLOCK / 64; ++w) { tv += s_vis[w]; tmn = min(tmn, s_min[w]); tmx = max(tmx, s_max[w]); }
+        counters[CNT_VISIBLE] = tv;
+        counters[CNT_DEPTH_MIN] = tmn;
+        counters[CNT_DEPTH_MAX] = tmx;
+        counters[CNT_ISECT64] = (uint32_t)carry;
+        counters[CNT_ISECT64 + 1] = (uint32_t)(carry >> 32);
+    }
 }
 
 template <int DEG>
@@ -212,30 +260,27 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
         a.depth_bits[g] = dbits;
     }
 
-    // Block totals: intersections for the emission scan; visible count and
-    // depth range through one atomic per wave.
-    __shared__ uint32_t s_sum[PROJ_BLOCK / 64];
+    // Block statistics, reduced by finalize_counts_kernel (no global atomics:
+    // a same-address atomic from every wave serialises across the XCDs).
+    __shared__ uint32_t s_sum[PROJ_BLOCK / 64], s_vis[PROJ_BLOCK / 64], s_min[PROJ_BLOCK / 64], s_max[PROJ_BLOCK / 64];
     const uint32_t wsum = wave_sum(hits);
     const uint32_t wvis = (uint32_t)__popcll(__ballot(visible));
     const uint32_t wmin = wave_min(visible ? dbits : 0xFFFFFFFFu);
     const uint32_t wmax = wave_max(visible ? dbits : 0u);
     const uint32_t wave = threadIdx.x / 64;
-    if (lane == 0) {
-        s_sum[wave] = wsum;
-        if (wvis) {
-            atomicAdd(&a.counters[CNT_VISIBLE], wvis);
-            atomicMin(&a.counters[CNT_DEPTH_MIN], wmin);
-            atomicMax(&a.counters[CNT_DEPTH_MAX], wmax);
-        }
-    }
+    if (lane == 0) { s_sum[wave] = wsum; s_vis[wave] = wvis; s_min[wave] = wmin; s_max[wave] = wmax; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t bs = 0;
-        uint64_t bs64 = 0;
+        uint32_t bs = 0, bv = 0, bmn = 0xFFFFFFFFu, bmx = 0u;
 #pragma unroll
-        for (int w = 0; w < PROJ_BLOCK / 64; ++w) { bs += s_sum[w]; bs64 += s_sum[w]; }
-        a.block_sums[blockIdx.x] = bs;
-        if (bs64) atomicAdd(reinterpret_cast<unsigned long long*>(a.counters + CNT_ISECT64), (unsigned long long)bs64);
+        for (int w = 0; w < PROJ_BLOCK / 64; ++w) {
+            bs += s_sum[w]; bv += s_vis[w]; bmn = min(bmn, s_min[w]); bmx = max(bmx, s_max[w]);
+        }
+        const uint32_t nb = gridDim.x;
+        a.block_stats[blockIdx.x] = bs;
+        a.block_stats[nb + blockIdx.x] = bv;
+        a.block_stats[2 * nb + blockIdx.x] = bmn;
+        a.block_stats[3 * nb + blockIdx.x] = bmx;
     }
 }
 
@@ -332,8 +377,8 @@ static uint32_t fill_grid(uint64_t n) {
     return (uint32_t)(b < 8192 ? (b ? b : 1) : 8192);
 }
 
-hipError_t launch_init_counters(uint32_t* counters, hipStream_t s) {
-    init_counters_kernel<<<1, 64, 0, s>>>(counters);
+hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, hipStream_t s) {
+    finalize_counts_kernel<<<1, FIN_BLOCK, 0, s>>>(block_stats, nblocks, counters);
     return hipGetLastError();
 }
 

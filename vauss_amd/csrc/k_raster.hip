@@ -11,9 +11,10 @@
 // 64-wide wavefronts.  Same tile/pixel mapping; splats staged 64 at a time;
 // each lane replays its pixel front to back with the forward's exact
 // arithmetic (so termination decisions agree bit for bit), the ten gradient
-// components of a splat are reduce-scattered across the wavefront in 13
-// shuffle-adds, the four wavefronts' partials are summed in LDS once per
-// batch, and each (tile, splat) pair issues at most ten f32 atomics.
+// components of a splat are reduce-scattered across the wavefront with
+// permlane swaps and DPP (no LDS traffic), the four wavefronts' partials are
+// summed in LDS once per batch, and each (tile, splat) pair issues at most
+// ten f32 atomics.
 #include "vs_device.h"
 #include "vs_internal.h"
 
@@ -160,40 +161,53 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
     }
 }
 
-// 10-component reduce-scatter over a 64-lane wavefront.  After it, lane L
-// holds the wave sum of component 5*b5 + 3*b4 + 2*b3 + b2 (b = bits of L)
-// when that index is a real component; lanes with L & 3 == 0 write it.
-VS_DEV float reduce_scatter10(float v[10], uint32_t lane, int& comp) {
-    const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8, h4 = lane & 4;
+// 10-component reduce-scatter over a 64-lane wavefront, built from gfx950's
+// cross-lane data paths instead of LDS permutes:
+//   bit 5: v_permlane32_swap (5 pairs)   bit 4: v_permlane16_swap (3 pairs)
+//   bit 3: DPP row_ror:8      (2 pairs)   bit 2: DPP row_half_mirror (1 pair)
+//   bits 1, 0: DPP quad_perm full sums.
+// A swap exchanges the upper lanes of its first operand with the lower lanes
+// of its second, so after it "first + second" is, in every lane, the pair
+// sum of the value that lane keeps.  Afterwards lane L holds the wave sum of
+// component 5*b5 + 3*b4 + 2*b3 + b2 (b = bits of L) when that is < 10 and the
+// sub-indices are not padding; lanes with L & 3 == 0 write it.
+VS_DEV float swap32_sum(float keep_lo, float keep_hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(keep_lo), __float_as_uint(keep_hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+VS_DEV float swap16_sum(float keep_lo, float keep_hi) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(keep_lo), __float_as_uint(keep_hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int CTRL>
+VS_DEV float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_ROR8 = 0x128;       // rotate a 16-lane row by 8 (= lane ^ 8)
+constexpr int DPP_ROW_HALF_MIRROR = 0x141; // lane i <-> 7 - i within each 8 lanes
+
+VS_DEV int scatter_component(uint32_t lane) {
+    const int i3 = ((lane & 8) ? 2 : 0) + ((lane & 4) ? 1 : 0);    // 3 = padding
+    const int i5 = ((lane & 16) ? 3 : 0) + i3;                      // 5 = padding
+    return (i3 < 3 && i5 < 5) ? ((lane & 32) ? 5 : 0) + i5 : -1;
+}
+
+VS_DEV float reduce_scatter10(const float v[10], uint32_t lane) {
     float w[5];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-        const float keep = h32 ? v[i + 5] : v[i];
-        const float send = h32 ? v[i] : v[i + 5];
-        w[i] = keep + __shfl_xor(send, 32);
-    }
+    for (int i = 0; i < 5; ++i) w[i] = swap32_sum(v[i], v[i + 5]);
     float x[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const float hiv = (i + 3 < 5) ? w[i + 3] : 0.0f;
-        const float keep = h16 ? hiv : w[i];
-        const float send = h16 ? w[i] : hiv;
-        x[i] = keep + __shfl_xor(send, 16);
-    }
-    float y[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float hiv = (i + 2 < 3) ? x[i + 2] : 0.0f;
-        const float keep = h8 ? hiv : x[i];
-        const float send = h8 ? x[i] : hiv;
-        y[i] = keep + __shfl_xor(send, 8);
-    }
-    float z = (h4 ? y[1] : y[0]) + __shfl_xor(h4 ? y[0] : y[1], 4);
-    z += __shfl_xor(z, 2);
-    z += __shfl_xor(z, 1);
-    const int i3 = (h8 ? 2 : 0) + (h4 ? 1 : 0);          // 0..3, 3 = padding
-    const int i5 = (h16 ? 3 : 0) + i3;                     // 0..5, 5 = padding
-    comp = (i3 < 3 && i5 < 5) ? (h32 ? 5 : 0) + i5 : -1;
+    x[0] = swap16_sum(w[0], w[3]);
+    x[1] = swap16_sum(w[1], w[4]);
+    x[2] = swap16_sum(w[2], 0.0f);
+    const bool h8 = lane & 8, h4 = lane & 4;
+    const float y0 = (h8 ? x[2] : x[0]) + dpp<DPP_ROW_ROR8>(h8 ? x[0] : x[2]);
+    const float y1 = (h8 ? 0.0f : x[1]) + dpp<DPP_ROW_ROR8>(h8 ? x[1] : 0.0f);
+    float z = (h4 ? y1 : y0) + dpp<DPP_ROW_HALF_MIRROR>(h4 ? y0 : y1);
+    z += dpp<DPP_QUAD_XOR2>(z);
+    z += dpp<DPP_QUAD_XOR1>(z);
     return z;
 }
 
@@ -232,6 +246,7 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_bwd_kernel(RasterBwdArgs 
         rscale = 1.0f / mx(o.w, 1.0e-5f);
     }
     const float img_w = (float)a.img_w, img_h = (float)a.img_h;
+    const int comp = scatter_component(lane);
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
         const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
@@ -302,15 +317,7 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_bwd_kernel(RasterBwdArgs 
                         }
                     }
                 }
-                int comp = -1;
-                float val = 0.0f;
-                if (__ballot(contrib) != 0ull) val = reduce_scatter10(g, lane, comp);
-                else {
-                    // keep the writer pattern identical: lanes 4k with a real component write zero
-                    const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8, h4 = lane & 4;
-                    const int i3 = (h8 ? 2 : 0) + (h4 ? 1 : 0), i5 = (h16 ? 3 : 0) + i3;
-                    comp = (i3 < 3 && i5 < 5) ? (h32 ? 5 : 0) + i5 : -1;
-                }
+                const float val = (__ballot(contrib) != 0ull) ? reduce_scatter10(g, lane) : 0.0f;
                 if ((lane & 3) == 0 && comp >= 0) s_part[wave][t][comp] = val;
             }
         }

@@ -35,8 +35,7 @@ struct ProjectArgs {
     float4* proj_b;             // [N] c11, opacity, r, g
     float* proj_c;              // [N] b
     float4* proj_aux;           // [N] z, nx, ny, nz (geometry) or null
-    uint32_t* block_sums;       // [ceil(N/256)] tiles hit per 256-splat block
-    uint32_t* counters;         // [CNT_COUNT]
+    uint32_t* block_stats;      // [4][ceil(N/256)]: tiles hit, visible count, min and max depth bits per block
 };
 
 struct EmitArgs {
@@ -95,8 +94,10 @@ struct ProjectBwdArgs {
 };
 
 // ---- launchers (return hipError_t of the launch) -------------------------------
-hipError_t launch_init_counters(uint32_t* counters, hipStream_t s);
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
+// Reduces the projection's block stats into `counters` and turns the block
+// tile counts (first row of block_stats) into exclusive offsets in place.
+hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, hipStream_t s);
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
