@@ -46,17 +46,34 @@ __global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, uint32_t n
 // DIST_NEAR / DIST_FAR depth map, kernels/helpers.rs:91-103.
 VS_DEV float dist_depth(float z) { return 100.0f / (100.0f - 0.2f) * (1.0f - 0.2f / mx(z, 0.2f)); }
 
+// Workgroups are dealt to the 8 XCDs round-robin; give XCD k the contiguous
+// band of tiles [k*per, (k+1)*per) so neighbouring tiles, which share most of
+// their splats, gather the same projected rows through the same L2.
+VS_DEV uint32_t xcd_tile(uint32_t block, uint32_t num_tiles) {
+    const uint32_t per = (num_tiles + 7) / 8;
+    return (block % 8) * per + block / 8;
+}
+static uint32_t xcd_grid(uint32_t num_tiles) { return 8 * ((num_tiles + 7) / 8); }
+
+// sigma beyond which alpha = opac * exp(-sigma) stays below the low edge of
+// the smooth cutoff band (1/255 - 5e-4) with a 1e-3 margin
+// (bwd/kernels/rasterize_backwards_planes.rs:512-515).  Skipping a wavefront
+// whose pixels all lie beyond it changes no result: every such pixel fails
+// the alpha test anyway.
+VS_DEV float sigma_skip(float opac) { return logf_c(opac / (ALPHA_MID - 0.5f * ALPHA_BAND)) + 1.0e-3f; }
+
 template <bool BWD, bool GEOM, bool SMOOTH>
 __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) {
     __shared__ float4 s_a[RASTER_BLOCK];    // x, y, c00/2, c01
-    __shared__ float4 s_b[RASTER_BLOCK];    // c11/2, opacity, r, g
-    __shared__ float s_c[RASTER_BLOCK];     // b
+    __shared__ float4 s_b[RASTER_BLOCK];    // c11/2, opacity, max(r,0), max(g,0)
+    __shared__ float2 s_c[RASTER_BLOCK];    // max(b,0), sigma skip threshold
     __shared__ float4 s_d[GEOM ? RASTER_BLOCK : 1];
     __shared__ uint32_t s_gid[BWD ? RASTER_BLOCK : 1];
     __shared__ uint32_t s_hit[BWD ? RASTER_BLOCK : 1];
     __shared__ uint32_t s_last;
 
-    const uint32_t tile = blockIdx.x;
+    const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
+    if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
     const uint32_t l = threadIdx.x;
     const uint32_t px = tx * TILE_W + compact_bits_16(l);
@@ -82,17 +99,21 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
             s_a[l] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
-            s_b[l] = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
-            s_c[l] = a.proj_c[gid];
+            s_b[l] = make_float4(0.5f * pb.x, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
+            s_c[l] = make_float2(mx(a.proj_c[gid], 0.0f), sigma_skip(pb.y));
             if constexpr (GEOM) s_d[l] = a.proj_aux[gid];
             if constexpr (BWD) { s_gid[l] = gid; s_hit[l] = 0u; }
         }
         __syncthreads();
-        for (uint32_t t = 0; t < rem && !done; ++t) {
+        for (uint32_t t = 0; t < rem; ++t) {
+            if (__ballot(!done) == 0ull) break;           // this wavefront's pixels are all done
             const float4 sa = s_a[t];
-            const float4 sb = s_b[t];
+            const float2 sc = s_c[t];
             const float dx = pcx - sa.x, dy = pcy - sa.y;
+            const float4 sb = s_b[t];
             const float sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);
+            if (__ballot(!done && sigma <= sc.y) == 0ull) continue;
+            if (done) continue;
             const float G = expf_neg(-sigma);
             const float alpha = mn(ALPHA_CAP, sb.y * G);
             const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
@@ -104,9 +125,9 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
                 } else {
                     if constexpr (BWD) s_hit[t] = 1u;
                     const float vis = ae * T;
-                    cr = __builtin_fmaf(mx(sb.z, 0.0f), vis, cr);
-                    cg = __builtin_fmaf(mx(sb.w, 0.0f), vis, cg);
-                    cb = __builtin_fmaf(mx(s_c[t], 0.0f), vis, cb);
+                    cr = __builtin_fmaf(sb.z, vis, cr);
+                    cg = __builtin_fmaf(sb.w, vis, cg);
+                    cb = __builtin_fmaf(sc.x, vis, cb);
                     if constexpr (GEOM) {
                         const float4 d = s_d[t];
                         depth_acc = __builtin_fmaf(d.x, vis, depth_acc);
@@ -215,12 +236,13 @@ template <bool SMOOTH>
 __global__ void __launch_bounds__(RASTER_BLOCK) raster_bwd_kernel(RasterBwdArgs a) {
     __shared__ float4 s_a[BWD_BATCH];       // x, y, c00/2, c01
     __shared__ float4 s_b[BWD_BATCH];       // c11/2, opacity, r, g
-    __shared__ float s_c[BWD_BATCH];        // b
+    __shared__ float2 s_c[BWD_BATCH];       // b, sigma skip threshold
     __shared__ uint32_t s_gid[BWD_BATCH];
     __shared__ float s_part[RASTER_BLOCK / 64][BWD_BATCH][10];
-    __shared__ uint32_t s_active[RASTER_BLOCK / 64];
+    __shared__ uint32_t s_flag[RASTER_BLOCK / 64][BWD_BATCH];
 
-    const uint32_t tile = blockIdx.x;
+    const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
+    if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
     const uint32_t l = threadIdx.x, lane = l & 63, wave = l >> 6;
     const uint32_t px = tx * TILE_W + compact_bits_16(l);
@@ -243,7 +265,7 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_bwd_kernel(RasterBwdArgs 
         T = 1.0f;
         vr = v.x; vg = v.y; vb = v.z;
         vt = (v.w - (a.bg_r * vr + a.bg_g * vg + a.bg_b * vb)) * t_final;
-        rscale = 1.0f / mx(o.w, 1.0e-5f);
+        rscale = __builtin_amdgcn_rcpf(mx(o.w, 1.0e-5f));
     }
     const float img_w = (float)a.img_w, img_h = (float)a.img_h;
     const int comp = scatter_component(lane);
@@ -257,78 +279,87 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_bwd_kernel(RasterBwdArgs 
             const float4 pb = a.proj_b[gid];
             s_a[l] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
             s_b[l] = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
-            s_c[l] = a.proj_c[gid];
+            s_c[l] = make_float2(a.proj_c[gid], sigma_skip(pb.y));
             s_gid[l] = gid;
         }
-        const bool wave_active = __ballot(T > T_STOP) != 0ull;
-        if (lane == 0) s_active[wave] = wave_active ? 1u : 0u;
         __syncthreads();
-        if (wave_active) {
-            for (uint32_t t = 0; t < rem; ++t) {
-                float g[10];
+        uint32_t t = 0;
+        for (; t < rem; ++t) {
+            if (__ballot(T > T_STOP) == 0ull) break;      // every pixel of this wavefront is done
+            const float4 sa = s_a[t];
+            const float4 sbv = s_b[t];
+            const float2 sc = s_c[t];
+            const float dx = pcx - sa.x, dy = pcy - sa.y;
+            const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);
+            if (__ballot(T > T_STOP && sigma <= sc.y) == 0ull) {
+                if (lane == 0) s_flag[wave][t] = 0u;
+                continue;
+            }
+            float g[10];
 #pragma unroll
-                for (int k = 0; k < 10; ++k) g[k] = 0.0f;
-                bool contrib = false;
-                if (T > T_STOP) {
-                    const float4 sa = s_a[t];
-                    const float4 sbv = s_b[t];
-                    const float dx = pcx - sa.x, dy = pcy - sa.y;
-                    const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);
-                    const float G = expf_neg(-sigma);
-                    const float opac = sbv.y;
-                    const float alpha = mn(ALPHA_CAP, opac * G);
-                    const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
-                    if (sigma >= 0.0f && w_cut > 0.0f) {
-                        const float ae = alpha * w_cut;
-                        const float nt = T * (1.0f - ae);
-                        if (nt <= T_STOP) {
-                            T = 0.0f;
-                        } else {
-                            contrib = true;
-                            const float c_r = sbv.z, c_g = sbv.w, c_b = s_c[t];
-                            const float cl_r = mx(c_r, 0.0f), cl_g = mx(c_g, 0.0f), cl_b = mx(c_b, 0.0f);
-                            const float vis = ae * T;
-                            g[5] = (c_r >= 0.0f) ? vis * vr : 0.0f;
-                            g[6] = (c_g >= 0.0f) ? vis * vg : 0.0f;
-                            g[7] = (c_b >= 0.0f) ? vis * vb : 0.0f;
-                            const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
-                            const float dot_rgb = ((T * cl_r - sr) * vr + (T * cl_g - sg) * vg + (T * cl_b - sb) * vb) * ra;
-                            const float v_ae = dot_rgb + vt * ra;
-                            const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
-                            const float v_sigma = -alpha * v_alpha;
-                            const float bdx = -dx, bdy = -dy;       // mean - pixel centre
-                            const float c00 = 2.0f * sa.z, c01 = sa.w, c11 = 2.0f * sbv.x;
-                            const float vxy_x = v_sigma * (c00 * bdx + c01 * bdy);
-                            const float vxy_y = v_sigma * (c01 * bdx + c11 * bdy);
-                            if (opac * G <= ALPHA_CAP) {
-                                g[2] = 0.5f * v_sigma * bdx * bdx;
-                                g[3] = v_sigma * bdx * bdy;
-                                g[4] = 0.5f * v_sigma * bdy * bdy;
-                                g[0] = vxy_x;
-                                g[1] = vxy_y;
-                                g[8] = v_alpha * G;
-                                const float ux = vxy_x * img_w, uy = vxy_y * img_h;
-                                g[9] = __builtin_sqrtf(ux * ux + uy * uy) * rscale;
-                            }
-                            sr = sr - vis * cl_r;
-                            sg = sg - vis * cl_g;
-                            sb = sb - vis * cl_b;
-                            T = nt;
+            for (int k = 0; k < 10; ++k) g[k] = 0.0f;
+            bool contrib = false;
+            if (T > T_STOP) {
+                const float G = expf_neg(-sigma);
+                const float opac = sbv.y;
+                const float alpha = mn(ALPHA_CAP, opac * G);
+                const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
+                if (sigma >= 0.0f && w_cut > 0.0f) {
+                    const float ae = alpha * w_cut;
+                    const float nt = T * (1.0f - ae);
+                    if (nt <= T_STOP) {
+                        T = 0.0f;
+                    } else {
+                        contrib = true;
+                        const float c_r = sbv.z, c_g = sbv.w, c_b = sc.x;
+                        const float cl_r = mx(c_r, 0.0f), cl_g = mx(c_g, 0.0f), cl_b = mx(c_b, 0.0f);
+                        const float vis = ae * T;
+                        g[5] = (c_r >= 0.0f) ? vis * vr : 0.0f;
+                        g[6] = (c_g >= 0.0f) ? vis * vg : 0.0f;
+                        g[7] = (c_b >= 0.0f) ? vis * vb : 0.0f;
+                        const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+                        const float dot_rgb = ((T * cl_r - sr) * vr + (T * cl_g - sg) * vg + (T * cl_b - sb) * vb) * ra;
+                        const float v_ae = dot_rgb + vt * ra;
+                        const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+                        const float v_sigma = -alpha * v_alpha;
+                        const float bdx = -dx, bdy = -dy;       // mean - pixel centre
+                        const float c00 = 2.0f * sa.z, c01 = sa.w, c11 = 2.0f * sbv.x;
+                        const float vxy_x = v_sigma * (c00 * bdx + c01 * bdy);
+                        const float vxy_y = v_sigma * (c01 * bdx + c11 * bdy);
+                        if (opac * G <= ALPHA_CAP) {
+                            g[2] = 0.5f * v_sigma * bdx * bdx;
+                            g[3] = v_sigma * bdx * bdy;
+                            g[4] = 0.5f * v_sigma * bdy * bdy;
+                            g[0] = vxy_x;
+                            g[1] = vxy_y;
+                            g[8] = v_alpha * G;
+                            const float ux = vxy_x * img_w, uy = vxy_y * img_h;
+                            g[9] = __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale;
                         }
+                        sr = sr - vis * cl_r;
+                        sg = sg - vis * cl_g;
+                        sb = sb - vis * cl_b;
+                        T = nt;
                     }
                 }
-                const float val = (__ballot(contrib) != 0ull) ? reduce_scatter10(g, lane) : 0.0f;
+            }
+            if (__ballot(contrib) != 0ull) {
+                const float val = reduce_scatter10(g, lane);
                 if ((lane & 3) == 0 && comp >= 0) s_part[wave][t][comp] = val;
+                if (lane == 0) s_flag[wave][t] = 1u;
+            } else if (lane == 0) {
+                s_flag[wave][t] = 0u;
             }
         }
+        for (uint32_t tt = t + lane; tt < rem; tt += 64) s_flag[wave][tt] = 0u;
         __syncthreads();
         for (uint32_t idx = l; idx < rem * 10; idx += RASTER_BLOCK) {
-            const uint32_t t = idx / 10, c = idx % 10;
+            const uint32_t ti = idx / 10, c = idx % 10;
             float sum = 0.0f;
 #pragma unroll
             for (int w = 0; w < RASTER_BLOCK / 64; ++w)
-                if (s_active[w]) sum += s_part[w][t][c];
-            if (sum != 0.0f) atomicAdd(&a.v_combined[(size_t)s_gid[t] * 10 + c], sum);
+                if (s_flag[w][ti]) sum += s_part[w][ti][c];
+            if (sum != 0.0f) atomicAdd(&a.v_combined[(size_t)s_gid[ti] * 10 + c], sum);
         }
     }
 }
@@ -362,7 +393,7 @@ hipError_t launch_tile_ranges(const uint64_t* keys, uint32_t n, uint32_t shift, 
 
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s) {
     if (a.num_tiles == 0) return hipSuccess;
-    const dim3 grid(a.num_tiles);
+    const dim3 grid(xcd_grid(a.num_tiles));
     if (!bwd_info) raster_fwd_kernel<false, false, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
     else if (geometry) raster_fwd_kernel<true, true, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
     else if (smooth) raster_fwd_kernel<true, false, true><<<grid, RASTER_BLOCK, 0, s>>>(a);
@@ -372,8 +403,9 @@ hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, 
 
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s) {
     if (a.num_tiles == 0) return hipSuccess;
-    if (smooth) raster_bwd_kernel<true><<<a.num_tiles, RASTER_BLOCK, 0, s>>>(a);
-    else raster_bwd_kernel<false><<<a.num_tiles, RASTER_BLOCK, 0, s>>>(a);
+    const dim3 grid(xcd_grid(a.num_tiles));
+    if (smooth) raster_bwd_kernel<true><<<grid, RASTER_BLOCK, 0, s>>>(a);
+    else raster_bwd_kernel<false><<<grid, RASTER_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
 
