@@ -60,6 +60,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB (counter calibration for HBM traffic)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the rasterizer runs one view per process on one device "
@@ -131,6 +133,15 @@ def main() -> int:
     roofline = {"bound": "hbm", "kernel": dom.replace("_ms", ""), "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None, "alg_bytes_per_launch": dom_bytes, "ms_per_launch": round(dom_ms, 4)}
+
+    if args.copy_calib:
+        src = torch.empty(args.copy_calib * (1 << 20) // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copy calibration: {args.copy_calib} MiB read + {args.copy_calib} MiB written per copy",
+              file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:

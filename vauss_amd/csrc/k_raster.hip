@@ -8,13 +8,12 @@
 // has reached T <= 1e-4.
 //
 // Backward: bwd/kernels/rasterize_backwards_planes.rs:112-682 redesigned for
-// 64-wide wavefronts.  Same tile/pixel mapping; splats staged 64 at a time;
-// each lane replays its pixel front to back with the forward's exact
-// arithmetic (so termination decisions agree bit for bit), the ten gradient
-// components of a splat are reduce-scattered across the wavefront with
-// permlane swaps and DPP (no LDS traffic), the four wavefronts' partials are
-// summed in LDS once per batch, and each (tile, splat) pair issues at most
-// ten f32 atomics.
+// 64-wide wavefronts: one wavefront per tile with four pixels per lane, splats
+// staged 64 at a time.  Each lane replays its pixels front to back with the
+// forward's exact arithmetic (so termination decisions agree bit for bit),
+// sums its pixels' ten gradient components in registers, and the wavefront
+// reduce-scatters them with permlane swaps and DPP (no LDS traffic) so each
+// (tile, splat) pair issues one atomic instruction of at most ten lanes.
 #include "vs_device.h"
 #include "vs_internal.h"
 
@@ -66,7 +65,7 @@ template <bool BWD, bool GEOM, bool SMOOTH>
 __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) {
     __shared__ float4 s_a[RASTER_BLOCK];    // x, y, c00/2, c01
     __shared__ float4 s_b[RASTER_BLOCK];    // c11/2, opacity, max(r,0), max(g,0)
-    __shared__ float2 s_c[RASTER_BLOCK];    // max(b,0), sigma skip threshold
+    __shared__ float s_c[RASTER_BLOCK];     // max(b,0)
     __shared__ float4 s_d[GEOM ? RASTER_BLOCK : 1];
     __shared__ uint32_t s_gid[BWD ? RASTER_BLOCK : 1];
     __shared__ uint32_t s_hit[BWD ? RASTER_BLOCK : 1];
@@ -100,20 +99,16 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
             const float4 pb = a.proj_b[gid];
             s_a[l] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
             s_b[l] = make_float4(0.5f * pb.x, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
-            s_c[l] = make_float2(mx(a.proj_c[gid], 0.0f), sigma_skip(pb.y));
+            s_c[l] = mx(a.proj_c[gid], 0.0f);
             if constexpr (GEOM) s_d[l] = a.proj_aux[gid];
             if constexpr (BWD) { s_gid[l] = gid; s_hit[l] = 0u; }
         }
         __syncthreads();
-        for (uint32_t t = 0; t < rem; ++t) {
-            if (__ballot(!done) == 0ull) break;           // this wavefront's pixels are all done
+        for (uint32_t t = 0; t < rem && !done; ++t) {
             const float4 sa = s_a[t];
-            const float2 sc = s_c[t];
-            const float dx = pcx - sa.x, dy = pcy - sa.y;
             const float4 sb = s_b[t];
+            const float dx = pcx - sa.x, dy = pcy - sa.y;
             const float sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);
-            if (__ballot(!done && sigma <= sc.y) == 0ull) continue;
-            if (done) continue;
             const float G = expf_neg(-sigma);
             const float alpha = mn(ALPHA_CAP, sb.y * G);
             const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
@@ -127,7 +122,7 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
                     const float vis = ae * T;
                     cr = __builtin_fmaf(sb.z, vis, cr);
                     cg = __builtin_fmaf(sb.w, vis, cg);
-                    cb = __builtin_fmaf(sc.x, vis, cb);
+                    cb = __builtin_fmaf(s_c[t], vis, cb);
                     if constexpr (GEOM) {
                         const float4 d = s_d[t];
                         depth_acc = __builtin_fmaf(d.x, vis, depth_acc);
@@ -232,134 +227,135 @@ VS_DEV float reduce_scatter10(const float v[10], uint32_t lane) {
     return z;
 }
 
+// One 64-lane wavefront per tile; lane L owns the pixel column x = L % 16,
+// rows y = L / 16 + 4k (k = 0..3), so a splat's dx is shared by the lane's
+// four pixels.  A lane sums its pixels' contributions in registers and the
+// wavefront reduces each splat once.
+constexpr int BWD_PX = 4;
+
 template <bool SMOOTH>
-__global__ void __launch_bounds__(RASTER_BLOCK) raster_bwd_kernel(RasterBwdArgs a) {
+__global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     __shared__ float4 s_a[BWD_BATCH];       // x, y, c00/2, c01
     __shared__ float4 s_b[BWD_BATCH];       // c11/2, opacity, r, g
     __shared__ float2 s_c[BWD_BATCH];       // b, sigma skip threshold
     __shared__ uint32_t s_gid[BWD_BATCH];
-    __shared__ float s_part[RASTER_BLOCK / 64][BWD_BATCH][10];
-    __shared__ uint32_t s_flag[RASTER_BLOCK / 64][BWD_BATCH];
 
     const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
-    const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
-    const uint32_t l = threadIdx.x, lane = l & 63, wave = l >> 6;
-    const uint32_t px = tx * TILE_W + compact_bits_16(l);
-    const uint32_t py = ty * TILE_W + compact_bits_16(l >> 1);
-    const bool inside = px < a.img_w && py < a.img_h;
-    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
     const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
     if (lo >= hi) return;   // uniform per tile
+    const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t px = tx * TILE_W + (lane & 15);
+    const float pcx = (float)px + 0.5f;
+    const float img_w = (float)a.img_w, img_h = (float)a.img_h;
 
     // Pixel replay state, bwd/kernels/rasterize_backwards_planes.rs:194-209.
-    float sr = 0.0f, sg = 0.0f, sb = 0.0f, T = 0.0f, vr = 0.0f, vg = 0.0f, vb = 0.0f, vt = 0.0f, rscale = 0.0f;
-    if (inside) {
-        const size_t base = ((size_t)py * a.img_w + px) * a.channels;
-        const float4 o = *reinterpret_cast<const float4*>(a.out_img + base);
-        const float4 v = *reinterpret_cast<const float4*>(a.v_out + base);
-        const float t_final = 1.0f - o.w;
-        sr = o.x - t_final * a.bg_r;
-        sg = o.y - t_final * a.bg_g;
-        sb = o.z - t_final * a.bg_b;
-        T = 1.0f;
-        vr = v.x; vg = v.y; vb = v.z;
-        vt = (v.w - (a.bg_r * vr + a.bg_g * vg + a.bg_b * vb)) * t_final;
-        rscale = __builtin_amdgcn_rcpf(mx(o.w, 1.0e-5f));
+    float pcy[BWD_PX], sr[BWD_PX], sg[BWD_PX], sb[BWD_PX], T[BWD_PX];
+    float vr[BWD_PX], vg[BWD_PX], vb[BWD_PX], vt[BWD_PX], rscale[BWD_PX];
+#pragma unroll
+    for (int k = 0; k < BWD_PX; ++k) {
+        const uint32_t py = ty * TILE_W + (lane >> 4) + 4 * k;
+        pcy[k] = (float)py + 0.5f;
+        sr[k] = sg[k] = sb[k] = T[k] = vr[k] = vg[k] = vb[k] = vt[k] = rscale[k] = 0.0f;
+        if (px < a.img_w && py < a.img_h) {
+            const size_t base = ((size_t)py * a.img_w + px) * a.channels;
+            const float4 o = *reinterpret_cast<const float4*>(a.out_img + base);
+            const float4 v = *reinterpret_cast<const float4*>(a.v_out + base);
+            const float t_final = 1.0f - o.w;
+            sr[k] = o.x - t_final * a.bg_r;
+            sg[k] = o.y - t_final * a.bg_g;
+            sb[k] = o.z - t_final * a.bg_b;
+            T[k] = 1.0f;
+            vr[k] = v.x; vg[k] = v.y; vb[k] = v.z;
+            vt[k] = (v.w - (a.bg_r * v.x + a.bg_g * v.y + a.bg_b * v.z)) * t_final;
+            rscale[k] = __builtin_amdgcn_rcpf(mx(o.w, 1.0e-5f));
+        }
     }
-    const float img_w = (float)a.img_w, img_h = (float)a.img_h;
     const int comp = scatter_component(lane);
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
+        bool alive = false;
+#pragma unroll
+        for (int k = 0; k < BWD_PX; ++k) alive = alive || T[k] > T_STOP;
+        if (__ballot(alive) == 0ull) break;                // every pixel of the tile is done
         const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
         __syncthreads();
-        if (l < rem) {
-            const uint32_t gid = a.gids[start + l];
+        if (lane < rem) {
+            const uint32_t gid = a.gids[start + lane];
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
-            s_a[l] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
-            s_b[l] = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
-            s_c[l] = make_float2(a.proj_c[gid], sigma_skip(pb.y));
-            s_gid[l] = gid;
+            s_a[lane] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
+            s_b[lane] = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
+            s_c[lane] = make_float2(a.proj_c[gid], sigma_skip(pb.y));
+            s_gid[lane] = gid;
         }
         __syncthreads();
-        uint32_t t = 0;
-        for (; t < rem; ++t) {
-            if (__ballot(T > T_STOP) == 0ull) break;      // every pixel of this wavefront is done
+        for (uint32_t t = 0; t < rem; ++t) {
             const float4 sa = s_a[t];
             const float4 sbv = s_b[t];
             const float2 sc = s_c[t];
-            const float dx = pcx - sa.x, dy = pcy - sa.y;
-            const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);
-            if (__ballot(T > T_STOP && sigma <= sc.y) == 0ull) {
-                if (lane == 0) s_flag[wave][t] = 0u;
-                continue;
+            const float dx = pcx - sa.x;
+            float sigma[BWD_PX];
+            bool near = false;
+#pragma unroll
+            for (int k = 0; k < BWD_PX; ++k) {
+                sigma[k] = raster_sigma(sa.z, sa.w, sbv.x, dx, pcy[k] - sa.y);
+                near = near || (T[k] > T_STOP && sigma[k] <= sc.y);
             }
+            if (__ballot(near) == 0ull) continue;         // no pixel of the tile reaches the cutoff
+            const float opac = sbv.y;
+            const float c00 = 2.0f * sa.z, c01 = sa.w, c11 = 2.0f * sbv.x;
+            const float c_r = sbv.z, c_g = sbv.w, c_b = sc.x;
+            const float cl_r = mx(c_r, 0.0f), cl_g = mx(c_g, 0.0f), cl_b = mx(c_b, 0.0f);
+            const float bdx = -dx;                           // mean - pixel centre
             float g[10];
 #pragma unroll
-            for (int k = 0; k < 10; ++k) g[k] = 0.0f;
+            for (int i = 0; i < 10; ++i) g[i] = 0.0f;
             bool contrib = false;
-            if (T > T_STOP) {
-                const float G = expf_neg(-sigma);
-                const float opac = sbv.y;
+#pragma unroll
+            for (int k = 0; k < BWD_PX; ++k) {
+                if (!(T[k] > T_STOP)) continue;
+                const float G = expf_neg(-sigma[k]);
                 const float alpha = mn(ALPHA_CAP, opac * G);
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
-                if (sigma >= 0.0f && w_cut > 0.0f) {
-                    const float ae = alpha * w_cut;
-                    const float nt = T * (1.0f - ae);
-                    if (nt <= T_STOP) {
-                        T = 0.0f;
-                    } else {
-                        contrib = true;
-                        const float c_r = sbv.z, c_g = sbv.w, c_b = sc.x;
-                        const float cl_r = mx(c_r, 0.0f), cl_g = mx(c_g, 0.0f), cl_b = mx(c_b, 0.0f);
-                        const float vis = ae * T;
-                        g[5] = (c_r >= 0.0f) ? vis * vr : 0.0f;
-                        g[6] = (c_g >= 0.0f) ? vis * vg : 0.0f;
-                        g[7] = (c_b >= 0.0f) ? vis * vb : 0.0f;
-                        const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
-                        const float dot_rgb = ((T * cl_r - sr) * vr + (T * cl_g - sg) * vg + (T * cl_b - sb) * vb) * ra;
-                        const float v_ae = dot_rgb + vt * ra;
-                        const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
-                        const float v_sigma = -alpha * v_alpha;
-                        const float bdx = -dx, bdy = -dy;       // mean - pixel centre
-                        const float c00 = 2.0f * sa.z, c01 = sa.w, c11 = 2.0f * sbv.x;
-                        const float vxy_x = v_sigma * (c00 * bdx + c01 * bdy);
-                        const float vxy_y = v_sigma * (c01 * bdx + c11 * bdy);
-                        if (opac * G <= ALPHA_CAP) {
-                            g[2] = 0.5f * v_sigma * bdx * bdx;
-                            g[3] = v_sigma * bdx * bdy;
-                            g[4] = 0.5f * v_sigma * bdy * bdy;
-                            g[0] = vxy_x;
-                            g[1] = vxy_y;
-                            g[8] = v_alpha * G;
-                            const float ux = vxy_x * img_w, uy = vxy_y * img_h;
-                            g[9] = __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale;
-                        }
-                        sr = sr - vis * cl_r;
-                        sg = sg - vis * cl_g;
-                        sb = sb - vis * cl_b;
-                        T = nt;
-                    }
+                if (!(sigma[k] >= 0.0f && w_cut > 0.0f)) continue;
+                const float ae = alpha * w_cut;
+                const float nt = T[k] * (1.0f - ae);
+                if (nt <= T_STOP) { T[k] = 0.0f; continue; }
+                contrib = true;
+                const float vis = ae * T[k];
+                if (c_r >= 0.0f) g[5] += vis * vr[k];
+                if (c_g >= 0.0f) g[6] += vis * vg[k];
+                if (c_b >= 0.0f) g[7] += vis * vb[k];
+                const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+                const float dot_rgb = ((T[k] * cl_r - sr[k]) * vr[k] + (T[k] * cl_g - sg[k]) * vg[k] +
+                                       (T[k] * cl_b - sb[k]) * vb[k]) * ra;
+                const float v_ae = dot_rgb + vt[k] * ra;
+                const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+                const float v_sigma = -alpha * v_alpha;
+                const float bdy = sa.y - pcy[k];
+                const float vxy_x = v_sigma * (c00 * bdx + c01 * bdy);
+                const float vxy_y = v_sigma * (c01 * bdx + c11 * bdy);
+                if (opac * G <= ALPHA_CAP) {
+                    g[2] += 0.5f * v_sigma * bdx * bdx;
+                    g[3] += v_sigma * bdx * bdy;
+                    g[4] += 0.5f * v_sigma * bdy * bdy;
+                    g[0] += vxy_x;
+                    g[1] += vxy_y;
+                    g[8] += v_alpha * G;
+                    const float ux = vxy_x * img_w, uy = vxy_y * img_h;
+                    g[9] += __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale[k];
                 }
+                sr[k] = sr[k] - vis * cl_r;
+                sg[k] = sg[k] - vis * cl_g;
+                sb[k] = sb[k] - vis * cl_b;
+                T[k] = nt;
             }
-            if (__ballot(contrib) != 0ull) {
-                const float val = reduce_scatter10(g, lane);
-                if ((lane & 3) == 0 && comp >= 0) s_part[wave][t][comp] = val;
-                if (lane == 0) s_flag[wave][t] = 1u;
-            } else if (lane == 0) {
-                s_flag[wave][t] = 0u;
-            }
-        }
-        for (uint32_t tt = t + lane; tt < rem; tt += 64) s_flag[wave][tt] = 0u;
-        __syncthreads();
-        for (uint32_t idx = l; idx < rem * 10; idx += RASTER_BLOCK) {
-            const uint32_t ti = idx / 10, c = idx % 10;
-            float sum = 0.0f;
-#pragma unroll
-            for (int w = 0; w < RASTER_BLOCK / 64; ++w)
-                if (s_flag[w][ti]) sum += s_part[w][ti][c];
-            if (sum != 0.0f) atomicAdd(&a.v_combined[(size_t)s_gid[ti] * 10 + c], sum);
+            if (__ballot(contrib) == 0ull) continue;
+            const float val = reduce_scatter10(g, lane);
+            if ((lane & 3) == 0 && comp >= 0 && val != 0.0f)
+                atomicAdd(&a.v_combined[(size_t)s_gid[t] * 10 + comp], val);
         }
     }
 }
@@ -404,8 +400,8 @@ hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, 
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s) {
     if (a.num_tiles == 0) return hipSuccess;
     const dim3 grid(xcd_grid(a.num_tiles));
-    if (smooth) raster_bwd_kernel<true><<<grid, RASTER_BLOCK, 0, s>>>(a);
-    else raster_bwd_kernel<false><<<grid, RASTER_BLOCK, 0, s>>>(a);
+    if (smooth) raster_bwd_kernel<true><<<grid, 64, 0, s>>>(a);
+    else raster_bwd_kernel<false><<<grid, 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
