@@ -2,18 +2,23 @@
 //
 // Forward: crates/splat-train-render/src/kernels/rasterize.rs:109-420.  One
 // 256-lane workgroup per 16x16 tile, one pixel per lane in Morton order so
-// each wavefront owns an 8x8 quadrant (kernels/helpers.rs:105-128); splats
+// each wavefront owns an 8x8 quadrant (kernels/helpers.rs:105-128).  Splats
 // are staged 256 at a time into LDS as float4 pairs that every lane reads as
-// a broadcast; the tile stops at the first batch boundary where every pixel
-// has reached T <= 1e-4.
+// a broadcast; while staging, each lane tests its splat against the four
+// quadrants and the workgroup compacts, per quadrant, the batch slots that
+// can reach the alpha cutoff there, so a wavefront walks only its own list.
+// The tile stops at the first batch boundary where every pixel has reached
+// T <= 1e-4.
 //
 // Backward: bwd/kernels/rasterize_backwards_planes.rs:112-682 redesigned for
-// 64-wide wavefronts: one wavefront per tile with four pixels per lane, splats
-// staged 64 at a time.  Each lane replays its pixels front to back with the
-// forward's exact arithmetic (so termination decisions agree bit for bit),
-// sums its pixels' ten gradient components in registers, and the wavefront
-// reduce-scatters them with permlane swaps and DPP (no LDS traffic) so each
-// (tile, splat) pair issues one atomic instruction of at most ten lanes.
+// 64-wide wavefronts: one wavefront per tile with four pixels per lane (one
+// per quadrant), splats staged 64 at a time with the same quadrant masks,
+// which become uniform branches.  Each lane replays its pixels front to back
+// with the forward's exact arithmetic (so termination decisions agree bit for
+// bit), sums its pixels' ten gradient components in registers, and the
+// wavefront reduce-scatters them with permlane swaps and DPP (no LDS traffic)
+// so each (tile, splat) pair issues one atomic instruction of at most ten
+// lanes.
 #include "vs_device.h"
 #include "vs_internal.h"
 
@@ -54,12 +59,56 @@ VS_DEV uint32_t xcd_tile(uint32_t block, uint32_t num_tiles) {
 }
 static uint32_t xcd_grid(uint32_t num_tiles) { return 8 * ((num_tiles + 7) / 8); }
 
-// sigma beyond which alpha = opac * exp(-sigma) stays below the low edge of
-// the smooth cutoff band (1/255 - 5e-4) with a 1e-3 margin
-// (bwd/kernels/rasterize_backwards_planes.rs:512-515).  Skipping a wavefront
-// whose pixels all lie beyond it changes no result: every such pixel fails
-// the alpha test anyway.
-VS_DEV float sigma_skip(float opac) { return logf_c(opac / (ALPHA_MID - 0.5f * ALPHA_BAND)) + 1.0e-3f; }
+// ---- quadrant culling -------------------------------------------------------
+// A tile is four 8x8 quadrants.  For each staged splat the kernels compute a
+// 4-bit mask of the quadrants in which some pixel centre may pass the alpha
+// cutoff, and a wavefront skips (splat, quadrant) pairs outside the mask.
+// The test is conservative, so skipping changes no result bit: a pixel that
+// is skipped would have failed `alpha >= 1/255` (or, with the smooth cutoff,
+// `alpha > 1/255 - 5e-4`: kernels/helpers.rs:23-47) and left every
+// accumulator untouched.
+//
+// alpha = min(0.999, opac e^-sigma) is below the cutoff c whenever
+// sigma > ln(opac / c).  A quadrant is dead when the minimum of
+// sigma = A dx^2 + B dx dy + C dy^2 over the rectangle spanned by its pixel
+// centres exceeds 1.01 ln(opac / c) + 0.01.  The 1% + 0.01 margin dwarfs the
+// f32 rounding of both this minimum and the per-pixel sigma, which is at most
+// a few ulp of (A dx^2 + |B dx dy| + C dy^2) <= 2 sigma / (1 - rho) with
+// rho = |B| / (2 sqrt(AC)); splats with 1 - rho^2 <= 0.01 (and any
+// non-positive-definite or non-finite conic) keep all four quadrants.
+constexpr float QUAD_MARGIN_REL = 1.01f;
+constexpr float QUAD_MARGIN_ABS = 0.01f;
+constexpr float QUAD_MIN_DECORR = 0.01f;
+
+// Minimum over t in [lo, hi] of sigma on the edge where the other offset is
+// fixed at u:  a u^2 + b u t + c t^2, minimised at t = k u (k = -b / 2c).
+VS_DEV float edge_min(float a, float b, float c, float k, float u, float lo, float hi) {
+    const float t = __builtin_fminf(__builtin_fmaxf(k * u, lo), hi);
+    return (a * u + b * t) * u + c * t * t;
+}
+
+// Bit q (q = qy * 2 + qx) set when quadrant q of the tile whose first pixel
+// centre is (x0, y0) may hold a pixel that passes the cutoff.
+VS_DEV uint32_t quadrant_mask(float x0, float y0, float mx_, float my_, float A, float B, float C, float opac,
+                              bool smooth) {
+    const float cut = smooth ? (ALPHA_MID - 0.5f * ALPHA_BAND) : ALPHA_MID;
+    const float thr = QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS;
+    const float four_ac = 4.0f * A * C;
+    if (!(A > 0.0f && C > 0.0f && four_ac - B * B > QUAD_MIN_DECORR * four_ac && thr < 3.0e38f)) return 0xFu;
+    const float kx = -B / (2.0f * C);   // vertical edges: dy* = kx dx
+    const float ky = -B / (2.0f * A);   // horizontal edges: dx* = ky dy
+    uint32_t mask = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float a0 = (x0 + (float)(8 * (q & 1))) - mx_, a1 = a0 + 7.0f;
+        const float b0 = (y0 + (float)(8 * (q >> 1))) - my_, b1 = b0 + 7.0f;
+        const bool inside = a0 <= 0.0f && a1 >= 0.0f && b0 <= 0.0f && b1 >= 0.0f;
+        float m = __builtin_fminf(edge_min(A, B, C, kx, a0, b0, b1), edge_min(A, B, C, kx, a1, b0, b1));
+        m = __builtin_fminf(m, __builtin_fminf(edge_min(C, B, A, ky, b0, a0, a1), edge_min(C, B, A, ky, b1, a0, a1)));
+        if (inside || !(m > thr)) mask |= 1u << q;
+    }
+    return mask;
+}
 
 template <bool BWD, bool GEOM, bool SMOOTH>
 __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) {
@@ -69,16 +118,21 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
     __shared__ float4 s_d[GEOM ? RASTER_BLOCK : 1];
     __shared__ uint32_t s_gid[BWD ? RASTER_BLOCK : 1];
     __shared__ uint32_t s_hit[BWD ? RASTER_BLOCK : 1];
+    __shared__ uint8_t s_list[4][RASTER_BLOCK];       // per-quadrant live batch slots
+    __shared__ uint32_t s_qcnt[4][4];                 // [wavefront][quadrant] live-slot counts
     __shared__ uint32_t s_last;
 
     const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
     const uint32_t l = threadIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(l >> 6);   // Morton order: wavefront w owns quadrant w
+    const uint64_t lt_mask = (1ull << (l & 63)) - 1ull;
     const uint32_t px = tx * TILE_W + compact_bits_16(l);
     const uint32_t py = ty * TILE_W + compact_bits_16(l >> 1);
     const bool inside = px < a.img_w && py < a.img_h;
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+    const float x0 = (float)(tx * TILE_W) + 0.5f, y0 = (float)(ty * TILE_W) + 0.5f;
     const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
     if (BWD && l == 0) s_last = lo;
 
@@ -93,24 +147,50 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
         // tile once every pixel is done.
         if (__syncthreads_count(!done) == 0) break;
         const uint32_t rem = min((uint32_t)RASTER_BLOCK, hi - start);
+        uint32_t qmask = 0;
         if (l < rem) {
             const uint32_t gid = a.gids[start + l];
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
-            s_a[l] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
-            s_b[l] = make_float4(0.5f * pb.x, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
+            const float4 sa = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
+            const float4 sb = make_float4(0.5f * pb.x, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
+            s_a[l] = sa;
+            s_b[l] = sb;
             s_c[l] = mx(a.proj_c[gid], 0.0f);
             if constexpr (GEOM) s_d[l] = a.proj_aux[gid];
             if constexpr (BWD) { s_gid[l] = gid; s_hit[l] = 0u; }
+            qmask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
+        }
+        // Per-quadrant compaction of the live slots, in slot (= depth) order.
+        uint32_t below[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint64_t b = __ballot((qmask >> q) & 1u);
+            below[q] = (uint32_t)__popcll(b & lt_mask);
+            if ((l & 63) == 0) s_qcnt[wave][q] = (uint32_t)__popcll(b);
         }
         __syncthreads();
-        for (uint32_t t = 0; t < rem && !done; ++t) {
+        uint32_t count = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t off = below[q];
+#pragma unroll
+            for (uint32_t w = 0; w < 3; ++w) off += (w < wave) ? s_qcnt[w][q] : 0u;
+            if ((qmask >> q) & 1u) s_list[q][off] = (uint8_t)l;
+            count += (q == (int)wave) ? s_qcnt[0][q] + s_qcnt[1][q] + s_qcnt[2][q] + s_qcnt[3][q] : 0u;
+        }
+        __syncthreads();
+        const uint8_t* list = s_list[wave];
+        for (uint32_t j = 0; j < count && !done; ++j) {
+            const uint32_t t = list[j];
             const float4 sa = s_a[t];
             const float4 sb = s_b[t];
             const float dx = pcx - sa.x, dy = pcy - sa.y;
             const float sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);
             const float G = expf_neg(-sigma);
-            const float alpha = mn(ALPHA_CAP, sb.y * G);
+            // min(0.999, .) of a product that is NaN only when sigma is
+            // (then the sigma test below rejects the pair): same value as mn().
+            const float alpha = __builtin_fminf(ALPHA_CAP, sb.y * G);
             const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
             if (sigma >= 0.0f && w_cut > 0.0f) {
                 const float ae = alpha * w_cut;
@@ -227,18 +307,19 @@ VS_DEV float reduce_scatter10(const float v[10], uint32_t lane) {
     return z;
 }
 
-// One 64-lane wavefront per tile; lane L owns the pixel column x = L % 16,
-// rows y = L / 16 + 4k (k = 0..3), so a splat's dx is shared by the lane's
-// four pixels.  A lane sums its pixels' contributions in registers and the
-// wavefront reduces each splat once.
+// One 64-lane wavefront per tile; lane L owns pixel (L % 8, L / 8) of each
+// 8x8 quadrant k (k = 0..3), so the quadrant masks turn into uniform branches.
+// A lane sums its pixels' contributions in registers and the wavefront
+// reduces each splat once.
 constexpr int BWD_PX = 4;
 
 template <bool SMOOTH>
 __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     __shared__ float4 s_a[BWD_BATCH];       // x, y, c00/2, c01
     __shared__ float4 s_b[BWD_BATCH];       // c11/2, opacity, r, g
-    __shared__ float2 s_c[BWD_BATCH];       // b, sigma skip threshold
+    __shared__ float s_c[BWD_BATCH];        // b
     __shared__ uint32_t s_gid[BWD_BATCH];
+    __shared__ uint32_t s_mask[BWD_BATCH];  // live quadrants
 
     const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
@@ -246,16 +327,17 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     if (lo >= hi) return;   // uniform per tile
     const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
     const uint32_t lane = threadIdx.x;
-    const uint32_t px = tx * TILE_W + (lane & 15);
-    const float pcx = (float)px + 0.5f;
     const float img_w = (float)a.img_w, img_h = (float)a.img_h;
+    const float x0 = (float)(tx * TILE_W) + 0.5f, y0 = (float)(ty * TILE_W) + 0.5f;
 
     // Pixel replay state, bwd/kernels/rasterize_backwards_planes.rs:194-209.
-    float pcy[BWD_PX], sr[BWD_PX], sg[BWD_PX], sb[BWD_PX], T[BWD_PX];
+    float pcx[BWD_PX], pcy[BWD_PX], sr[BWD_PX], sg[BWD_PX], sb[BWD_PX], T[BWD_PX];
     float vr[BWD_PX], vg[BWD_PX], vb[BWD_PX], vt[BWD_PX], rscale[BWD_PX];
 #pragma unroll
     for (int k = 0; k < BWD_PX; ++k) {
-        const uint32_t py = ty * TILE_W + (lane >> 4) + 4 * k;
+        const uint32_t px = tx * TILE_W + 8 * (k & 1) + (lane & 7);
+        const uint32_t py = ty * TILE_W + 8 * (k >> 1) + (lane >> 3);
+        pcx[k] = (float)px + 0.5f;
         pcy[k] = (float)py + 0.5f;
         sr[k] = sg[k] = sb[k] = T[k] = vr[k] = vg[k] = vb[k] = vt[k] = rscale[k] = 0.0f;
         if (px < a.img_w && py < a.img_h) {
@@ -275,51 +357,48 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     const int comp = scatter_component(lane);
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
-        bool alive = false;
+        uint32_t alive = 0;   // quadrants with a pixel still above T_STOP (uniform)
 #pragma unroll
-        for (int k = 0; k < BWD_PX; ++k) alive = alive || T[k] > T_STOP;
-        if (__ballot(alive) == 0ull) break;                // every pixel of the tile is done
+        for (int k = 0; k < BWD_PX; ++k) alive |= (__ballot(T[k] > T_STOP) != 0ull) ? (1u << k) : 0u;
+        if (alive == 0) break;                              // every pixel of the tile is done
         const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
         __syncthreads();
         if (lane < rem) {
             const uint32_t gid = a.gids[start + lane];
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
-            s_a[lane] = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
-            s_b[lane] = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
-            s_c[lane] = make_float2(a.proj_c[gid], sigma_skip(pb.y));
+            const float4 sa = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
+            const float4 sbv = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
+            s_a[lane] = sa;
+            s_b[lane] = sbv;
+            s_c[lane] = a.proj_c[gid];
             s_gid[lane] = gid;
+            s_mask[lane] = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, sbv.x, sbv.y, SMOOTH);
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {
+            const uint32_t live = __builtin_amdgcn_readfirstlane(s_mask[t]) & alive;
+            if (live == 0) continue;                        // uniform: no quadrant reaches the cutoff
             const float4 sa = s_a[t];
             const float4 sbv = s_b[t];
-            const float2 sc = s_c[t];
-            const float dx = pcx - sa.x;
-            float sigma[BWD_PX];
-            bool near = false;
-#pragma unroll
-            for (int k = 0; k < BWD_PX; ++k) {
-                sigma[k] = raster_sigma(sa.z, sa.w, sbv.x, dx, pcy[k] - sa.y);
-                near = near || (T[k] > T_STOP && sigma[k] <= sc.y);
-            }
-            if (__ballot(near) == 0ull) continue;         // no pixel of the tile reaches the cutoff
             const float opac = sbv.y;
             const float c00 = 2.0f * sa.z, c01 = sa.w, c11 = 2.0f * sbv.x;
-            const float c_r = sbv.z, c_g = sbv.w, c_b = sc.x;
+            const float c_r = sbv.z, c_g = sbv.w, c_b = s_c[t];
             const float cl_r = mx(c_r, 0.0f), cl_g = mx(c_g, 0.0f), cl_b = mx(c_b, 0.0f);
-            const float bdx = -dx;                           // mean - pixel centre
             float g[10];
 #pragma unroll
             for (int i = 0; i < 10; ++i) g[i] = 0.0f;
             bool contrib = false;
 #pragma unroll
             for (int k = 0; k < BWD_PX; ++k) {
+                if (!((live >> k) & 1u)) continue;          // uniform
                 if (!(T[k] > T_STOP)) continue;
-                const float G = expf_neg(-sigma[k]);
-                const float alpha = mn(ALPHA_CAP, opac * G);
+                const float dx = pcx[k] - sa.x, dy = pcy[k] - sa.y;
+                const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);
+                const float G = expf_neg(-sigma);
+                const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);   // == mn(): see the forward
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
-                if (!(sigma[k] >= 0.0f && w_cut > 0.0f)) continue;
+                if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
                 const float ae = alpha * w_cut;
                 const float nt = T[k] * (1.0f - ae);
                 if (nt <= T_STOP) { T[k] = 0.0f; continue; }
@@ -334,7 +413,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 const float v_ae = dot_rgb + vt[k] * ra;
                 const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
                 const float v_sigma = -alpha * v_alpha;
-                const float bdy = sa.y - pcy[k];
+                const float bdx = -dx, bdy = -dy;               // mean - pixel centre
                 const float vxy_x = v_sigma * (c00 * bdx + c01 * bdy);
                 const float vxy_y = v_sigma * (c01 * bdx + c11 * bdy);
                 if (opac * G <= ALPHA_CAP) {
