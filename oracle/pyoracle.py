@@ -16,7 +16,9 @@ from typing import Optional
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# ORACLE_LIB points the tests at another build of the oracle (a deliberately
+# mutated copy, to check that the tests catch the mistake).
+LIB_PATH = Path(os.environ.get("ORACLE_LIB", HERE / "liboracle.so"))
 
 FLAG_BWD_INFO, FLAG_GEOMETRY, FLAG_SMOOTH_CUTOFF, FLAG_BRUTE_FORCE = 1, 2, 4, 8
 (F_INTERSECT_COUNTS, F_MAX_RADIUS, F_OPACITIES, F_GLOBAL_FROM_COMPACT, F_DEPTHS, F_PROJECTED, F_AUX, F_ISECT_TILE,

@@ -146,3 +146,51 @@ def test_smooth_cutoff_pass_parity():
 def test_background_parity():
     _, _, out, ref = _render_both("c1", 2000, 0, background=(0.7, 0.3, 0.1))
     np.testing.assert_array_equal(out.out_img.cpu().numpy().view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))
+
+
+def _culling_stress_scene(n=1200, seed=0x0C0A):
+    """Splats centred on quadrant and tile boundaries, thin and rotated, some
+    barely above the alpha cutoff: the cases where the kernels' per-quadrant
+    skip test is tightest."""
+    rng = np.random.default_rng(seed)
+    w, h, f = 128, 96, 100.0
+    z = rng.uniform(2.0, 6.0, n)
+    u = 8.0 * rng.integers(0, w // 8 + 1, n) + rng.choice([-0.5, 0.0, 0.5, 0.25], n)
+    v = 8.0 * rng.integers(0, h // 8 + 1, n) + rng.choice([-0.5, 0.0, 0.5, 0.25], n)
+    means = np.stack([(u - w / 2) * z / f, (v - h / 2) * z / f, z], 1)
+    quats = rng.standard_normal((n, 4))
+    kind = rng.integers(0, 3, n)
+    ls = np.where(kind[:, None] == 0, np.stack([rng.uniform(-2.0, -1.0, n), rng.uniform(-7, -5, n),
+                                                rng.uniform(-7, -5, n)], 1),           # needles
+                  np.where(kind[:, None] == 1, rng.uniform(-3.5, -2.0, (n, 3)),          # blobs
+                           np.stack([rng.uniform(-2.5, -1.5, n), rng.uniform(-4.0, -3.0, n),
+                                     rng.uniform(-4.0, -3.0, n)], 1)))                  # ellipses
+    near_cut = rng.random(n) < 0.4
+    p = np.where(near_cut, (1.0 / 255.0) * (1.0 + rng.uniform(0.0, 0.05, n)), rng.uniform(0.05, 0.9, n))
+    logit = np.log(p / (1 - p))
+    t = np.concatenate([means, quats, ls], 1).astype(np.float32)
+    sh = rng.uniform(-0.5, 1.5, (n, 1, 3)).astype(np.float32)
+    return scenes.Scene(t, sh, logit.astype(np.float32)), (w, h), f
+
+
+@pytest.mark.parametrize("pass_", [va.RasterPass.BACKWARD, va.RasterPass.BACKWARD_SMOOTH_CUTOFF])
+def test_quadrant_culling_stress(pass_):
+    scene, img, f = _culling_stress_scene()
+    cam = va.Camera.from_focal(f, f, img).uniforms(img)
+    t, s, o = to_gpu(scene)
+    print(f"[case] culling stress pass={pass_.name}", flush=True)
+    out = va.render(cam, img, t, s, o, pass_=pass_)
+    flags = po.FLAG_BWD_INFO | (po.FLAG_SMOOTH_CUTOFF if pass_ == va.RasterPass.BACKWARD_SMOOTH_CUTOFF else 0)
+    ref = po.render_forward(cam, img, scene.transforms, scene.sh_coeffs, scene.raw_opacities, flags=flags)
+    _check_forward(out, ref, gpu_state_arrays(out))
+    gimg = out.out_img.cpu().numpy()
+    np.testing.assert_array_equal(gimg.view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))
+    np.testing.assert_array_equal(out.aux.tile_offsets.cpu().numpy().view(np.uint32), ref.get(po.F_TILE_OFFSETS_SHRUNK))
+    rng = np.random.default_rng(3)
+    v_out = (rng.standard_normal(gimg.shape) / gimg[..., 0].size).astype(np.float32)
+    g = va.render_backward(out, t, s, o, torch.from_numpy(v_out).cuda())
+    rg = ref.backward(v_out)
+    vc = g.v_combined.cpu().numpy()
+    _check_grads(vc[:, 0:5], rg["v_combined"][:, 0:5], "v_xy_conic")
+    _check_grads(vc[:, 5:9], rg["v_combined"][:, 5:9], "v_rgb_opacity")
+    _check_grads(vc[:, 9], rg["v_combined"][:, 9], "v_refine")
