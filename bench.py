@@ -62,7 +62,15 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (counter calibration for HBM traffic)")
+    ap.add_argument("--summarize-stats", metavar="CSV", help="summarise a rocprofv3 kernel_stats.csv as markdown")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc output directories (one counter group each) as markdown")
+    ap.add_argument("--summary-out", metavar="MD", help="where --summarize-* writes its markdown")
+    ap.add_argument("--traffic-out", metavar="JSON", help="where --summarize-pmc writes calibrated HBM bytes per kernel")
+    ap.add_argument("--command", default="", help="the profiling command, recorded in the summary")
     args = ap.parse_args()
+    if args.summarize_stats or args.summarize_pmc:
+        return summarize(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the rasterizer runs one view per process on one device "
               f"(--gpus {args.gpus} is not supported in this build)", file=sys.stderr)
@@ -130,9 +138,11 @@ def main() -> int:
     dom_bytes = algorithmic_bytes(dom, n, int(V), int(I), T, P, k)
     dom_ms = per_launch[dom]
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic, traffic_note = measured_traffic(args.workload, dom.replace("_ms", ""))
     roofline = {"bound": "hbm", "kernel": dom.replace("_ms", ""), "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": None, "alg_bytes_per_launch": dom_bytes, "ms_per_launch": round(dom_ms, 4)}
+                "traffic": traffic, "traffic_source": traffic_note, "alg_bytes_per_launch": dom_bytes,
+                "ms_per_launch": round(dom_ms, 4)}
 
     if args.copy_calib:
         src = torch.empty(args.copy_calib * (1 << 20) // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -170,6 +180,133 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+    return 0
+
+
+PROFILES = os.path.join(ROOT, "profiles")
+KERNEL_SOURCES = [os.path.join(ROOT, "vauss_amd", "csrc", f) for f in
+                  ("k_project.hip", "k_project_bwd.hip", "k_raster.hip", "k_scan.hip", "k_sort.hip", "api.hip",
+                   "vs_device.h", "vs_camera.h", "vs_sh.h", "vs_internal.h")]
+
+# rocprofv3 kernel names -> bench stage names
+STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "raster_fwd"),
+                   ("project_bwd_kernel", "project_bwd"), ("project_kernel", "project"), ("emit_kernel", "emit"),
+                   ("finalize_counts", "project"), ("sort_", "sort"), ("scan_", "sort"), ("tile_ranges", "ranges"),
+                   ("l1_cotangent", "loss"), ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
+
+
+# what the markdown summary lists (the traffic file keeps every kernel)
+SUMMARY_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VALU_TRANS_F32",
+                    "SQ_LDS_BANK_CONFLICT", "SQ_THREAD_CYCLES_VALU", "SQ_ACTIVE_INST_VALU", "TCC_ATOMIC_sum",
+                    "TCC_EA0_ATOMIC_sum", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE", "WRITE_SIZE")
+SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "copyBuffer")
+
+
+def source_digest() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary,
+    when it was measured on the kernel sources in this tree."""
+    path = os.path.join(PROFILES, f"hbm_traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None, "no counter summary for this workload"
+    with open(path) as fh:
+        data = json.load(fh)
+    if data.get("source_digest") != source_digest():
+        return None, f"{os.path.relpath(path, ROOT)} was measured on other kernel sources"
+    k = data["kernels"].get(kernel)
+    if not k:
+        return None, f"{kernel} missing from {os.path.relpath(path, ROOT)}"
+    return int(k["fetch_bytes"] + k["write_bytes"]), os.path.relpath(path, ROOT)
+
+
+def _short_kernel(name: str) -> str:
+    base = name.split("(")[0].replace("void ", "")
+    return base.replace("vs::", "")
+
+
+def summarize(args) -> int:
+    import csv
+    lines = []
+    if args.summarize_stats:
+        with open(args.summarize_stats) as fh:
+            rows = list(csv.DictReader(fh))
+        lines += ["| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
+        for r in rows:
+            lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                         f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.2f} |")
+    traffic = None
+    if args.summarize_pmc:
+        per = {}          # kernel -> counter -> {dispatch: value}
+        durs = {}         # kernel -> {dispatch: ns}
+        for d in args.summarize_pmc:
+            for f in os.listdir(d):
+                if not f.endswith("counter_collection.csv"):
+                    continue
+                with open(os.path.join(d, f)) as fh:
+                    for r in csv.DictReader(fh):
+                        k = _short_kernel(r["Kernel_Name"])
+                        key = (r["Dispatch_Id"], r["Grid_Size"])
+                        per.setdefault(k, {}).setdefault(r["Counter_Name"], {}).setdefault(key, 0.0)
+                        per[k][r["Counter_Name"]][key] += float(r["Counter_Value"])
+                        durs.setdefault(k, {})[key] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        dur = {k: sum(v.values()) / len(v) for k, v in durs.items()}
+        copy = per.get("__amd_rocclr_copyBuffer", {})
+        calib = args.copy_calib * (1 << 20) if args.copy_calib else 0
+        f_scale = w_scale = None
+        if calib and copy.get("FETCH_SIZE") and copy.get("WRITE_SIZE"):
+            f_scale = calib / (max(copy["FETCH_SIZE"].values()) * 1024.0)
+            w_scale = calib / (max(copy["WRITE_SIZE"].values()) * 1024.0)
+        lines += ["", f"Copy calibration ({args.copy_calib} MiB read + written): FETCH_SIZE x "
+                      f"{f_scale if f_scale is None else round(f_scale, 3)}, WRITE_SIZE x "
+                      f"{w_scale if w_scale is None else round(w_scale, 3)}", ""]
+        lines += ["| kernel | dispatches | counter | mean per dispatch | derived |", "|---|---|---|---|---|"]
+        traffic = {"source_digest": source_digest(), "calibration_mib": args.copy_calib,
+                   "fetch_scale": f_scale, "write_scale": w_scale, "kernels": {}}
+        nbwd = max(1, len(per.get("raster_bwd_kernel<false>", {}).get("FETCH_SIZE", {1: 0})))
+        for k, cs in sorted(per.items()):
+            n = max(len(v) for v in cs.values())
+            mean = {c: sum(v.values()) / len(v) for c, v in cs.items()}
+            dur_ns = dur.get(k)
+            for c in sorted(mean):
+                if c not in SUMMARY_COUNTERS or not any(x in k for x in SUMMARY_KERNELS):
+                    continue
+                derived = ""
+                if c == "SQ_INSTS_VALU" and dur_ns:
+                    derived = f"{mean[c] / dur_ns:.0f} G wave-instr/s over {dur_ns / 1e3:.1f} us"
+                elif c == "FETCH_SIZE" and f_scale:
+                    derived = f"{mean[c] * 1024 * f_scale / 1e6:.1f} MB calibrated"
+                elif c == "WRITE_SIZE" and w_scale:
+                    derived = f"{mean[c] * 1024 * w_scale / 1e6:.1f} MB calibrated"
+                lines.append(f"| `{k}` | {n} | {c} | {mean[c]:.5g} | {derived} |")
+            if f_scale and "FETCH_SIZE" in mean and "WRITE_SIZE" in mean:
+                stage = next((st for pat, st in STAGE_OF_KERNEL if pat in k), k)
+                if stage in ("copy", "torch", "fill"):
+                    continue
+                e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "kernels": []})
+                # a stage that launches a kernel several times per step (sort passes) adds them up
+                reps = n / nbwd if stage == "sort" else 1.0
+                e["fetch_bytes"] += mean["FETCH_SIZE"] * 1024.0 * f_scale * reps
+                e["write_bytes"] += mean["WRITE_SIZE"] * 1024.0 * w_scale * reps
+                e["kernels"].append(k)
+    text = "\n".join(lines) + "\n"
+    if args.command:
+        text = f"Command:\n\n```\n{args.command}\n```\n\n" + text
+    if args.summary_out:
+        with open(args.summary_out, "w") as fh:
+            fh.write(text)
+    else:
+        print(text)
+    if traffic is not None and args.traffic_out:
+        with open(args.traffic_out, "w") as fh:
+            json.dump(traffic, fh, indent=1)
     return 0
 
 
