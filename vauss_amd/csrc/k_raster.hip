@@ -331,7 +331,10 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     const float x0 = (float)(tx * TILE_W) + 0.5f, y0 = (float)(ty * TILE_W) + 0.5f;
 
     // Pixel replay state, bwd/kernels/rasterize_backwards_planes.rs:194-209.
-    float pcx[BWD_PX], pcy[BWD_PX], sr[BWD_PX], sg[BWD_PX], sb[BWD_PX], T[BWD_PX];
+    // The reference carries the remaining colour S (3 channels) to form
+    // sum_c (T max(c,0) - S_c) v_c; only its projection D = S . v enters
+    // that sum, so a lane carries D per pixel: D -= vis (max(c,0) . v).
+    float pcx[BWD_PX], pcy[BWD_PX], D[BWD_PX], T[BWD_PX];
     float vr[BWD_PX], vg[BWD_PX], vb[BWD_PX], vt[BWD_PX], rscale[BWD_PX];
 #pragma unroll
     for (int k = 0; k < BWD_PX; ++k) {
@@ -339,15 +342,16 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
         const uint32_t py = ty * TILE_W + 8 * (k >> 1) + (lane >> 3);
         pcx[k] = (float)px + 0.5f;
         pcy[k] = (float)py + 0.5f;
-        sr[k] = sg[k] = sb[k] = T[k] = vr[k] = vg[k] = vb[k] = vt[k] = rscale[k] = 0.0f;
+        D[k] = T[k] = vr[k] = vg[k] = vb[k] = vt[k] = rscale[k] = 0.0f;
         if (px < a.img_w && py < a.img_h) {
             const size_t base = ((size_t)py * a.img_w + px) * a.channels;
             const float4 o = *reinterpret_cast<const float4*>(a.out_img + base);
             const float4 v = *reinterpret_cast<const float4*>(a.v_out + base);
             const float t_final = 1.0f - o.w;
-            sr[k] = o.x - t_final * a.bg_r;
-            sg[k] = o.y - t_final * a.bg_g;
-            sb[k] = o.z - t_final * a.bg_b;
+            const float sr = o.x - t_final * a.bg_r;
+            const float sg = o.y - t_final * a.bg_g;
+            const float sb = o.z - t_final * a.bg_b;
+            D[k] = sr * v.x + sg * v.y + sb * v.z;
             T[k] = 1.0f;
             vr[k] = v.x; vg[k] = v.y; vb[k] = v.z;
             vt[k] = (v.w - (a.bg_r * v.x + a.bg_g * v.y + a.bg_b * v.z)) * t_final;
@@ -355,6 +359,10 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
         }
     }
     const int comp = scatter_component(lane);
+    // Per-lane factor applied to the reduced sum: the conic sums are carried
+    // as sum nv dx^2, nv dx dy, nv dy^2 with nv = alpha v_alpha = -v_sigma,
+    // so v_conic = (-1/2, -1, -1/2) times them (exact scalings).
+    const float comp_scale = (comp == 2 || comp == 4) ? -0.5f : ((comp == 3) ? -1.0f : 1.0f);
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
         uint32_t alive = 0;   // quadrants with a pixel still above T_STOP (uniform)
@@ -400,39 +408,41 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
                 if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
                 const float ae = alpha * w_cut;
-                const float nt = T[k] * (1.0f - ae);
+                const float one_m = 1.0f - ae;
+                const float nt = T[k] * one_m;
                 if (nt <= T_STOP) { T[k] = 0.0f; continue; }
                 contrib = true;
                 const float vis = ae * T[k];
-                if (c_r >= 0.0f) g[5] += vis * vr[k];
-                if (c_g >= 0.0f) g[6] += vis * vg[k];
-                if (c_b >= 0.0f) g[7] += vis * vb[k];
-                const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
-                const float dot_rgb = ((T[k] * cl_r - sr[k]) * vr[k] + (T[k] * cl_g - sg[k]) * vg[k] +
-                                       (T[k] * cl_b - sb[k]) * vb[k]) * ra;
-                const float v_ae = dot_rgb + vt[k] * ra;
+                // colour: the c >= 0 gate is per splat, applied after the reduction
+                g[5] = __builtin_fmaf(vis, vr[k], g[5]);
+                g[6] = __builtin_fmaf(vis, vg[k], g[6]);
+                g[7] = __builtin_fmaf(vis, vb[k], g[7]);
+                const float cv = __builtin_fmaf(cl_b, vb[k], __builtin_fmaf(cl_g, vg[k], cl_r * vr[k]));
+                const float ra = __builtin_amdgcn_rcpf(one_m);
+                const float v_ae = (__builtin_fmaf(T[k], cv, -D[k]) + vt[k]) * ra;
                 const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
-                const float v_sigma = -alpha * v_alpha;
-                const float bdx = -dx, bdy = -dy;               // mean - pixel centre
-                const float vxy_x = v_sigma * (c00 * bdx + c01 * bdy);
-                const float vxy_y = v_sigma * (c01 * bdx + c11 * bdy);
                 if (opac * G <= ALPHA_CAP) {
-                    g[2] += 0.5f * v_sigma * bdx * bdx;
-                    g[3] += v_sigma * bdx * bdy;
-                    g[4] += 0.5f * v_sigma * bdy * bdy;
-                    g[0] += vxy_x;
-                    g[1] += vxy_y;
-                    g[8] += v_alpha * G;
-                    const float ux = vxy_x * img_w, uy = vxy_y * img_h;
-                    g[9] += __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale[k];
+                    const float nv = alpha * v_alpha;                // = -v_sigma
+                    const float u = __builtin_fmaf(c01, dy, c00 * dx);
+                    const float w = __builtin_fmaf(c11, dy, c01 * dx);
+                    const float vx = nv * u, vy = nv * w;            // v_xy with dx = mean - pixel
+                    g[0] += vx;
+                    g[1] += vy;
+                    const float tx_ = nv * dx, ty_ = nv * dy;
+                    g[2] = __builtin_fmaf(tx_, dx, g[2]);
+                    g[3] = __builtin_fmaf(tx_, dy, g[3]);
+                    g[4] = __builtin_fmaf(ty_, dy, g[4]);
+                    g[8] = __builtin_fmaf(v_alpha, G, g[8]);
+                    const float ux = vx * img_w, uy = vy * img_h;
+                    g[9] = __builtin_fmaf(__builtin_amdgcn_sqrtf(__builtin_fmaf(ux, ux, uy * uy)), rscale[k], g[9]);
                 }
-                sr[k] = sr[k] - vis * cl_r;
-                sg[k] = sg[k] - vis * cl_g;
-                sb[k] = sb[k] - vis * cl_b;
+                D[k] = __builtin_fmaf(-vis, cv, D[k]);
                 T[k] = nt;
             }
             if (__ballot(contrib) == 0ull) continue;
-            const float val = reduce_scatter10(g, lane);
+            float val = reduce_scatter10(g, lane);
+            const bool gate = (comp == 5) ? (c_r >= 0.0f) : ((comp == 6) ? (c_g >= 0.0f) : ((comp == 7) ? (c_b >= 0.0f) : true));
+            val = gate ? val * comp_scale : 0.0f;
             if ((lane & 3) == 0 && comp >= 0 && val != 0.0f)
                 atomicAdd(&a.v_combined[(size_t)s_gid[t] * 10 + comp], val);
         }
