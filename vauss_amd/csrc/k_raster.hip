@@ -315,9 +315,11 @@ constexpr int BWD_PX = 4;
 
 template <bool SMOOTH>
 __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
+    // Per-splat values are formed once at staging, where one instruction
+    // serves the 64 splats of a batch, not per (splat, wavefront) in the loop.
     __shared__ float4 s_a[BWD_BATCH];       // x, y, c00/2, c01
-    __shared__ float4 s_b[BWD_BATCH];       // c11/2, opacity, r, g
-    __shared__ float s_c[BWD_BATCH];        // b
+    __shared__ float4 s_b[BWD_BATCH];       // c11/2, opacity, max(r,0), max(g,0)
+    __shared__ float4 s_c[BWD_BATCH];       // max(b,0), c00, c11, colour gates (bits r,g,b >= 0, bit 3 set)
     __shared__ uint32_t s_gid[BWD_BATCH];
     __shared__ uint32_t s_mask[BWD_BATCH];  // live quadrants
 
@@ -363,6 +365,11 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     // as sum nv dx^2, nv dx dy, nv dy^2 with nv = alpha v_alpha = -v_sigma,
     // so v_conic = (-1/2, -1, -1/2) times them (exact scalings).
     const float comp_scale = (comp == 2 || comp == 4) ? -0.5f : ((comp == 3) ? -1.0f : 1.0f);
+    // the colour rows (5, 6, 7) take the splat's c >= 0 gate, the rest bit 3 (always set)
+    const uint32_t gate_shift = (comp >= 5 && comp <= 7) ? (uint32_t)(comp - 5) : 3u;
+    float g[10];
+#pragma unroll
+    for (int i = 0; i < 10; ++i) g[i] = 0.0f;
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
         uint32_t alive = 0;   // quadrants with a pixel still above T_STOP (uniform)
@@ -376,12 +383,13 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
             const float4 sa = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
-            const float4 sbv = make_float4(0.5f * pb.x, pb.y, pb.z, pb.w);
+            const float cb = a.proj_c[gid];
+            const uint32_t gates = (pb.z >= 0.0f ? 1u : 0u) | (pb.w >= 0.0f ? 2u : 0u) | (cb >= 0.0f ? 4u : 0u) | 8u;
             s_a[lane] = sa;
-            s_b[lane] = sbv;
-            s_c[lane] = a.proj_c[gid];
+            s_b[lane] = make_float4(0.5f * pb.x, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
+            s_c[lane] = make_float4(mx(cb, 0.0f), pa.z, pb.x, as_f(gates));
             s_gid[lane] = gid;
-            s_mask[lane] = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, sbv.x, sbv.y, SMOOTH);
+            s_mask[lane] = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, 0.5f * pb.x, pb.y, SMOOTH);
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {
@@ -389,13 +397,10 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             if (live == 0) continue;                        // uniform: no quadrant reaches the cutoff
             const float4 sa = s_a[t];
             const float4 sbv = s_b[t];
+            const float4 scv = s_c[t];
             const float opac = sbv.y;
-            const float c00 = 2.0f * sa.z, c01 = sa.w, c11 = 2.0f * sbv.x;
-            const float c_r = sbv.z, c_g = sbv.w, c_b = s_c[t];
-            const float cl_r = mx(c_r, 0.0f), cl_g = mx(c_g, 0.0f), cl_b = mx(c_b, 0.0f);
-            float g[10];
-#pragma unroll
-            for (int i = 0; i < 10; ++i) g[i] = 0.0f;
+            const float c00 = scv.y, c01 = sa.w, c11 = scv.z;
+            const float cl_r = sbv.z, cl_g = sbv.w, cl_b = scv.x;
             bool contrib = false;
 #pragma unroll
             for (int k = 0; k < BWD_PX; ++k) {
@@ -439,10 +444,11 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 D[k] = __builtin_fmaf(-vis, cv, D[k]);
                 T[k] = nt;
             }
-            if (__ballot(contrib) == 0ull) continue;
+            if (__ballot(contrib) == 0ull) continue;          // g is still all zero
             float val = reduce_scatter10(g, lane);
-            const bool gate = (comp == 5) ? (c_r >= 0.0f) : ((comp == 6) ? (c_g >= 0.0f) : ((comp == 7) ? (c_b >= 0.0f) : true));
-            val = gate ? val * comp_scale : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 10; ++i) g[i] = 0.0f;
+            val = ((as_u(scv.w) >> gate_shift) & 1u) ? val * comp_scale : 0.0f;
             if ((lane & 3) == 0 && comp >= 0 && val != 0.0f)
                 atomicAdd(&a.v_combined[(size_t)s_gid[t] * 10 + comp], val);
         }
