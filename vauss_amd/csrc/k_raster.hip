@@ -1,41 +1,35 @@
 // k_raster.hip -- tile ranges, forward alpha compositing and its VJP.
 //
-// Forward: crates/splat-train-render/src/kernels/rasterize.rs:109-420.  One
-// 256-lane workgroup per 16x16 tile, one pixel per lane in Morton order so
-// each wavefront owns an 8x8 quadrant (kernels/helpers.rs:105-128).  Splats
-// are staged 256 at a time into LDS as float4 pairs that every lane reads as
-// a broadcast; while staging, each lane tests its splat against the four
-// quadrants and the workgroup compacts, per quadrant, the batch slots that
-// can reach the alpha cutoff there, so a wavefront walks only its own list.
-// The tile stops at the first batch boundary where every pixel has reached
-// T <= 1e-4.
+// Both kernels split a 16x16 tile into four 8x8 quadrants and stage the
+// tile's depth-sorted splats into LDS in batches.  While staging, each lane
+// tests its splat against the four quadrants (quadrant_mask), so no cycle is
+// spent on a (splat, quadrant) pair whose every pixel stays below the alpha
+// cutoff.
 //
-// Backward: bwd/kernels/rasterize_backwards_planes.rs:112-682 redesigned for
-// 64-wide wavefronts: one wavefront per tile with four pixels per lane (one
-// per quadrant), splats staged 64 at a time with the same quadrant masks,
-// which become uniform branches.  Each lane replays its pixels front to back
-// with the forward's exact arithmetic (so termination decisions agree bit for
-// bit), sums its pixels' ten gradient components in registers, and the
-// wavefront reduce-scatters them with permlane swaps and DPP (no LDS traffic)
-// so each (tile, splat) pair issues one atomic instruction of at most ten
-// lanes.
+// Forward: crates/splat-train-render/src/kernels/rasterize.rs:109-420.  One
+// 256-lane workgroup per tile, one pixel per lane in Morton order so each
+// wavefront owns one quadrant (kernels/helpers.rs:105-128).  Batches of 256
+// splats are staged as float4 pairs that lanes read as broadcasts; the
+// workgroup compacts, per quadrant, the live batch slots, and each wavefront
+// walks its own list.  The tile stops at the first batch boundary where every
+// pixel has reached T <= 1e-4.  (Four wavefronts per tile hide the long exp
+// dependency chain better than one wavefront with four pixels per lane.)
+//
+// Backward: bwd/kernels/rasterize_backwards_planes.rs:112-682.  One 64-lane
+// wavefront per tile; lane L owns pixel (L % 8, L / 8) of each quadrant, so
+// the quadrant masks become uniform branches and the per-splat work (one
+// reduction, one atomic instruction) is shared by the whole tile.  Each lane
+// replays its pixels front to back with the forward's exact arithmetic (so
+// termination decisions agree bit for bit), sums its pixels' ten gradient
+// components in registers, and the wavefront reduce-scatters them with
+// permlane swaps and DPP (no LDS traffic), so each (tile, splat) pair issues
+// one atomic instruction of at most ten lanes.
 #include "vs_device.h"
 #include "vs_internal.h"
 
 namespace vs {
 
-constexpr int RASTER_BLOCK = 256;
 constexpr int BWD_BATCH = 64;
-
-// kernels/helpers.rs:105-113
-VS_DEV uint32_t compact_bits_16(uint32_t v) {
-    uint32_t x = v & 0x55555555u;
-    x = (x | (x >> 1)) & 0x33333333u;
-    x = (x | (x >> 2)) & 0x0F0F0F0Fu;
-    x = (x | (x >> 4)) & 0x00FF00FFu;
-    x = (x | (x >> 8)) & 0x0000FFFFu;
-    return x;
-}
 
 __global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, uint32_t n, uint32_t shift, uint32_t num_tiles,
                                    uint32_t* __restrict__ ranges) {
@@ -110,15 +104,28 @@ VS_DEV uint32_t quadrant_mask(float x0, float y0, float mx_, float my_, float A,
     return mask;
 }
 
+// kernels/helpers.rs:105-113: pixel of lane l in a 256-lane tile in Morton
+// order, so wavefront w = l / 64 owns the 8x8 quadrant w.
+VS_DEV uint32_t compact_bits_16(uint32_t v) {
+    uint32_t x = v & 0x55555555u;
+    x = (x | (x >> 1)) & 0x33333333u;
+    x = (x | (x >> 2)) & 0x0F0F0F0Fu;
+    x = (x | (x >> 4)) & 0x00FF00FFu;
+    x = (x | (x >> 8)) & 0x0000FFFFu;
+    return x;
+}
+
+constexpr int FWD_BLOCK = 256;
+
 template <bool BWD, bool GEOM, bool SMOOTH>
-__global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) {
-    __shared__ float4 s_a[RASTER_BLOCK];    // x, y, c00/2, c01
-    __shared__ float4 s_b[RASTER_BLOCK];    // c11/2, opacity, max(r,0), max(g,0)
-    __shared__ float s_c[RASTER_BLOCK];     // max(b,0)
-    __shared__ float4 s_d[GEOM ? RASTER_BLOCK : 1];
-    __shared__ uint32_t s_gid[BWD ? RASTER_BLOCK : 1];
-    __shared__ uint32_t s_hit[BWD ? RASTER_BLOCK : 1];
-    __shared__ uint8_t s_list[4][RASTER_BLOCK];       // per-quadrant live batch slots
+__global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
+    __shared__ float4 s_a[FWD_BLOCK];    // x, y, c00/2, c01
+    __shared__ float4 s_b[FWD_BLOCK];    // c11/2, opacity, max(r,0), max(g,0)
+    __shared__ float s_c[FWD_BLOCK];     // max(b,0)
+    __shared__ float4 s_d[GEOM ? FWD_BLOCK : 1];
+    __shared__ uint32_t s_gid[BWD ? FWD_BLOCK : 1];
+    __shared__ uint32_t s_hit[BWD ? FWD_BLOCK : 1];
+    __shared__ uint8_t s_list[4][FWD_BLOCK];       // per-quadrant live batch slots
     __shared__ uint32_t s_qcnt[4][4];                 // [wavefront][quadrant] live-slot counts
     __shared__ uint32_t s_last;
 
@@ -142,11 +149,11 @@ __global__ void __launch_bounds__(RASTER_BLOCK) raster_fwd_kernel(RasterArgs a) 
     bool done = !inside;
     uint32_t last = lo;
 
-    for (uint32_t start = lo; start < hi; start += RASTER_BLOCK) {
+    for (uint32_t start = lo; start < hi; start += FWD_BLOCK) {
         // Barrier + vote: protects the previous batch's LDS reads and ends the
         // tile once every pixel is done.
         if (__syncthreads_count(!done) == 0) break;
-        const uint32_t rem = min((uint32_t)RASTER_BLOCK, hi - start);
+        const uint32_t rem = min((uint32_t)FWD_BLOCK, hi - start);
         uint32_t qmask = 0;
         if (l < rem) {
             const uint32_t gid = a.gids[start + l];
@@ -485,10 +492,10 @@ hipError_t launch_tile_ranges(const uint64_t* keys, uint32_t n, uint32_t shift, 
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s) {
     if (a.num_tiles == 0) return hipSuccess;
     const dim3 grid(xcd_grid(a.num_tiles));
-    if (!bwd_info) raster_fwd_kernel<false, false, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
-    else if (geometry) raster_fwd_kernel<true, true, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
-    else if (smooth) raster_fwd_kernel<true, false, true><<<grid, RASTER_BLOCK, 0, s>>>(a);
-    else raster_fwd_kernel<true, false, false><<<grid, RASTER_BLOCK, 0, s>>>(a);
+    if (!bwd_info) raster_fwd_kernel<false, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
+    else if (geometry) raster_fwd_kernel<true, true, false><<<grid, FWD_BLOCK, 0, s>>>(a);
+    else if (smooth) raster_fwd_kernel<true, false, true><<<grid, FWD_BLOCK, 0, s>>>(a);
+    else raster_fwd_kernel<true, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
 
