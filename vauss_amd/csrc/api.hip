@@ -45,7 +45,8 @@ enum Stage { ST_PROJECT, ST_EMIT, ST_SORT, ST_RANGES, ST_RASTER_FWD, ST_RASTER_B
 struct vs_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
-    uint32_t* host_counters = nullptr;    // pinned readback of the projection counters
+    uint32_t* host_counters = nullptr;    // pinned readback of the projection counters (+ CTX_FLAGS words)
+    uint32_t* dev_flags = nullptr;        // device: [0] set when a sort look-back gave up waiting
     bool timing = false;
     // Stage event pairs recorded since the last vs_ctx_stage_times(); the
     // pool is reused, so timing many renders needs no extra synchronisation.
@@ -135,8 +136,12 @@ extern "C" vs_status vs_ctx_create(int device, void* hip_stream, vs_ctx** out) {
     if (!c) return fail(VS_ERR_OOM, "context allocation");
     c->device = device;
     c->stream = static_cast<hipStream_t>(hip_stream);
-    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&c->host_counters), CNT_COUNT * sizeof(uint32_t), hipHostMallocDefault);
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&c->host_counters), (CNT_COUNT + CTX_FLAGS) * sizeof(uint32_t),
+                                 hipHostMallocDefault);
     if (e != hipSuccess) { delete c; return hip_fail(e, "hipHostMalloc"); }
+    e = hipMalloc(reinterpret_cast<void**>(&c->dev_flags), CTX_FLAGS * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c->dev_flags, 0, CTX_FLAGS * sizeof(uint32_t));
+    if (e != hipSuccess) { hipHostFree(c->host_counters); if (c->dev_flags) hipFree(c->dev_flags); delete c; return hip_fail(e, "context flags"); }
     // Keep freed stream-ordered allocations in the pool between renders.
     hipMemPool_t pool;
     if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess) {
@@ -154,6 +159,7 @@ extern "C" void vs_ctx_destroy(vs_ctx* c) {
     for (auto& r : c->recs) { hipEventDestroy(r.b); hipEventDestroy(r.e); }
     for (auto e : c->pool) hipEventDestroy(e);
     hipHostFree(c->host_counters);
+    hipFree(c->dev_flags);
     delete c;
 }
 
@@ -282,8 +288,14 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         VS_HIP(launch_fill_u32(st->ranges, 0u, (uint64_t)T * 2, s), "zero ranges");
     }
     VS_HIP(hipMemcpyAsync(ctx->host_counters, st->counters, CNT_COUNT * 4, hipMemcpyDeviceToHost, s), "counter readback");
+    VS_HIP(hipMemcpyAsync(ctx->host_counters + CNT_COUNT, ctx->dev_flags, CTX_FLAGS * 4, hipMemcpyDeviceToHost, s),
+           "flag readback");
     VS_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
     const uint32_t* hc = ctx->host_counters;
+    if (hc[CNT_COUNT + FLAG_SORT_STALL] != 0u) {
+        VS_HIP(launch_fill_u32(ctx->dev_flags, 0u, CTX_FLAGS, s), "flag reset");
+        return fail(VS_ERR_HIP, "an earlier radix sort on this context gave up waiting in its look-back; its output was wrong");
+    }
     st->V = hc[CNT_VISIBLE];
     uint64_t I64 = 0;
     std::memcpy(&I64, hc + CNT_ISECT64, 8);
@@ -320,7 +332,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         }
         {
             StageTimer tm(ctx, ST_SORT);
-            VS_HIP(radix_sort_pairs(keys_u, vals_u, st->keys, st->gids, I, nullptr, true, 0, end_bit, ib + o_tmp, s),
+            VS_HIP(radix_sort_pairs(keys_u, vals_u, st->keys, st->gids, I, nullptr, true, 0, end_bit, ib + o_tmp,
+                                    ctx->dev_flags + FLAG_SORT_STALL, s),
                    "tile/depth sort");
         }
         {
@@ -426,7 +439,7 @@ extern "C" vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, con
     VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, false), ctx->stream), "hipMallocAsync(sort tmp)");
     StageTimer tm(ctx, ST_OTHER);
     hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, n_dev, false, skip_bits, skip_bits + sorting_bits,
-                                    tmp, ctx->stream);
+                                    tmp, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream);
     hipFreeAsync(tmp, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
     return VS_OK;
@@ -443,7 +456,8 @@ extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, con
     void* tmp = nullptr;
     VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, true), ctx->stream), "hipMallocAsync(sort tmp)");
     StageTimer tm(ctx, ST_OTHER);
-    hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, nullptr, true, 0, sorting_bits, tmp, ctx->stream);
+    hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, nullptr, true, 0, sorting_bits, tmp,
+                                    ctx->dev_flags + FLAG_SORT_STALL, ctx->stream);
     hipFreeAsync(tmp, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
     return VS_OK;

@@ -2,15 +2,22 @@
 // u32 or u64 keys.
 //
 // Replaces crates/splat-train-sort (radix_argsort*, lib.rs:15-189;
-// kernels.rs:35-341).  One pass per digit:
-//   upsweep  -- per 2048-key block, an LDS digit histogram written digit-major
-//               into a [256 x blocks] table;
-//   scan     -- exclusive scan of the table (k_scan.hip) = each block's
-//               first output slot per digit;
-//   scatter  -- each wavefront ranks its keys in input order with ballot-based
-//               digit matching (8 ballots per step, no atomics), the block
-//               reorders keys by digit in LDS, and the reordered tile is
-//               written out so equal digits land in consecutive addresses.
+// kernels.rs:35-341).  Two schedules share one block-level ranking step, in
+// which each wavefront ranks its keys in input order with ballot-based digit
+// matching (8 ballots per step, no atomics) and the block reorders its tile by
+// digit in LDS so that equal digits leave in consecutive addresses:
+//
+//  * one-sweep (n >= ONESWEEP_MIN): one histogram kernel counts the digits of
+//    every pass in a single read of the keys; each pass is then a single
+//    kernel in which each block publishes its tile's per-digit counts and sums
+//    its predecessors' counts by decoupled look-back (a block only waits on
+//    lower-indexed blocks, which are dispatched first and publish before they
+//    wait, so the chain drains; a bounded spin turns anything else into a
+//    reported error, not a hang);
+//  * three kernels per pass for small or device-counted inputs: upsweep
+//    (per-tile digit histograms into a [256 x blocks] table), an exclusive
+//    scan of that table (k_scan.hip), and the scatter.
+//
 // Ranking in (wave, step, lane) order with waves owning consecutive key
 // ranges keeps every pass stable, so the sort is stable.
 #include "vs_internal.h"
@@ -49,22 +56,17 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_upsweep_kernel(const K* __res
     table[(size_t)d * nblocks + blockIdx.x] = c;
 }
 
-template <typename K>
-__global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
-                                                                  K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
-                                                                  uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
-                                                                  const uint32_t* __restrict__ offsets, uint32_t nblocks) {
-    __shared__ uint32_t wave_hist[SORT_WAVES][256];
-    __shared__ uint32_t digit_start[256];
-    __shared__ uint32_t s_tot[8];
-    __shared__ K s_keys[SORT_TILE];
-    __shared__ uint32_t s_vals[SORT_TILE];
-
-    const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
+// Block-level ranking of one tile of up to SORT_TILE keys.  On return the tile
+// sits digit-ordered (and stable) in s_keys/s_vals, digit_start[d] is the
+// first LDS slot of digit d and d_count[d] (thread d) its count in the tile.
+template <typename K, int BLOCK>
+__device__ __forceinline__ uint32_t rank_tile(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+                                              uint32_t base, uint32_t n, uint32_t shift,
+                                              uint32_t (*wave_hist)[256], uint32_t* digit_start, uint32_t* s_tot,
+                                              K* s_keys, uint32_t* s_vals) {
+    constexpr int WAVES = BLOCK / 64;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t base = blockIdx.x * SORT_TILE;
-    if (base >= n) return;   // uniform per block
-    for (uint32_t i = threadIdx.x; i < SORT_WAVES * 256; i += SORT_BLOCK) (&wave_hist[0][0])[i] = 0;
+    for (uint32_t i = threadIdx.x; i < WAVES * 256; i += BLOCK) (&wave_hist[0][0])[i] = 0;
     __syncthreads();
 
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -95,28 +97,33 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __res
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    // Per-digit totals, wave offsets and the block's digit starts.
+    // Per-digit totals, wave offsets and the block's digit starts (threads 0..255, one digit each).
+    uint32_t run = 0;
     {
         const uint32_t d = threadIdx.x;
-        uint32_t run = 0;
+        uint32_t incl = 0;
+        if (d < 256) {
 #pragma unroll
-        for (int w = 0; w < SORT_WAVES; ++w) {
-            const uint32_t c = wave_hist[w][d];
-            wave_hist[w][d] = run;     // becomes the wave's exclusive offset within digit d
-            run += c;
-        }
-        // exclusive scan of run over the 256 digits
-        uint32_t incl = run;
+            for (int w = 0; w < WAVES; ++w) {
+                const uint32_t c = wave_hist[w][d];
+                wave_hist[w][d] = run;     // becomes the wave's exclusive offset within digit d
+                run += c;
+            }
+            // exclusive scan of run over the 256 digits
+            incl = run;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t t = __shfl_up(incl, o);
-            if ((int)lane >= o) incl += t;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_up(incl, o);
+                if ((int)lane >= o) incl += t;
+            }
+            if (lane == 63) s_tot[wave] = incl;
         }
-        if (lane == 63) s_tot[wave] = incl;
         __syncthreads();
-        uint32_t wo = 0;
-        for (uint32_t w = 0; w < wave; ++w) wo += s_tot[w];
-        digit_start[d] = wo + incl - run;
+        if (d < 256) {
+            uint32_t wo = 0;
+            for (uint32_t w = 0; w < wave; ++w) wo += s_tot[w];
+            digit_start[d] = wo + incl - run;
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -128,6 +135,24 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __res
         }
     }
     __syncthreads();
+    return run;
+}
+
+template <typename K>
+__global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+                                                                  K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
+                                                                  uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
+                                                                  const uint32_t* __restrict__ offsets, uint32_t nblocks) {
+    __shared__ uint32_t wave_hist[SORT_WAVES][256];
+    __shared__ uint32_t digit_start[256];
+    __shared__ uint32_t s_tot[8];
+    __shared__ K s_keys[SORT_TILE];
+    __shared__ uint32_t s_vals[SORT_TILE];
+
+    const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
+    const uint32_t base = blockIdx.x * SORT_TILE;
+    if (base >= n) return;   // uniform per block
+    rank_tile<K, SORT_BLOCK>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
     const uint32_t count = min(SORT_TILE, n - base);
     for (uint32_t i = threadIdx.x; i < count; i += SORT_BLOCK) {
         const K k = s_keys[i];
@@ -140,22 +165,166 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __res
     }
 }
 
+// ---- one-sweep schedule ---------------------------------------------------------
+constexpr uint32_t ONESWEEP_MIN = 1u << 16;
+constexpr int OS_BLOCK = 512;
+constexpr uint32_t OS_TILE = OS_BLOCK * SORT_ITEMS;        // 4096 keys per one-sweep tile
+constexpr uint32_t ONESWEEP_MAX_KEYS = 1u << 30;       // counts fit the 30-bit status payload
+constexpr uint32_t OS_AGGREGATE = 1u << 30;            // status: this tile's own count
+constexpr uint32_t OS_PREFIX = 2u << 30;               // status: count of this tile and all before it
+constexpr uint32_t OS_VALUE = (1u << 30) - 1u;
+constexpr uint32_t OS_SPIN_LIMIT = 1u << 18;           // polls before a look-back gives up
+constexpr int MAX_PASSES = 8;
+constexpr int LOOKBACK = 16;                           // predecessor statuses read per look-back step
+constexpr uint32_t HIST_BLOCKS = 512;
+
+// Digit histograms of every pass in one read: ghist[p][d] (zeroed by the caller).
+template <typename K>
+__global__ void __launch_bounds__(SORT_BLOCK) sort_histogram_kernel(const K* __restrict__ keys, uint32_t n_cap,
+                                                                    const uint32_t* __restrict__ n_dev, uint32_t first_bit,
+                                                                    uint32_t passes, uint32_t* __restrict__ ghist) {
+    __shared__ uint32_t h[SORT_WAVES][MAX_PASSES][256];
+    const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
+    const uint32_t wave = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < SORT_WAVES * MAX_PASSES * 256; i += SORT_BLOCK) (&h[0][0][0])[i] = 0;
+    __syncthreads();
+    for (uint32_t i = blockIdx.x * SORT_BLOCK + threadIdx.x; i < n; i += gridDim.x * SORT_BLOCK) {
+        const K k = keys[i];
+        for (uint32_t p = 0; p < passes; ++p) atomicAdd(&h[wave][p][digit_of(k, first_bit + 8 * p)], 1u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < passes * 256; i += SORT_BLOCK) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < SORT_WAVES; ++w) c += (&h[w][0][0])[i];
+        if (c) atomicAdd(&ghist[i], c);
+    }
+}
+
+__device__ __forceinline__ uint32_t status_load(uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void status_store(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One pass: rank a tile, find its digits' global offsets by look-back, scatter.
+// `status` is [nblocks][256], zeroed before the pass.
+template <typename K>
+__global__ void __launch_bounds__(OS_BLOCK) sort_onesweep_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+                                                                   K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
+                                                                   uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
+                                                                   const uint32_t* __restrict__ ghist, uint32_t* status,
+                                                                   uint32_t* err) {
+    __shared__ uint32_t wave_hist[OS_BLOCK / 64][256];
+    __shared__ uint32_t digit_start[256];
+    __shared__ uint32_t s_tot[8];
+    __shared__ uint32_t s_gstart[256];      // where this tile's digit d starts in the output
+    __shared__ K s_keys[OS_TILE];
+    __shared__ uint32_t s_vals[OS_TILE];
+
+    // Tile = block index.  Workgroups are dispatched in index order on each
+    // XCD, so every block this one waits on (lower indices) is already
+    // running or finished and never waits on a higher one: the chain drains.
+    // (A global ticket counter would serialise ~2k same-address atomics per
+    // pass across the XCDs.)
+    const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
+    const uint32_t tile = blockIdx.x;
+    const uint32_t base = tile * OS_TILE;
+    // A tile past the end has no successor with keys.
+    if (base >= n) return;
+    const uint32_t cnt = rank_tile<K, OS_BLOCK>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
+
+    const uint32_t d = threadIdx.x;
+    if (d < 256) {
+        uint32_t* my = status + (size_t)tile * 256 + d;
+        status_store(my, (tile == 0 ? OS_PREFIX : OS_AGGREGATE) | cnt);
+        uint32_t excl = 0;
+        if (tile > 0) {
+            // Look back over predecessors LOOKBACK at a time (independent loads),
+            // newest first, summing aggregates until a prefix; a not-yet-published
+            // tile is polled again.
+            int j = (int)tile - 1;
+            uint32_t spins = 0;
+            while (true) {
+                uint32_t st[LOOKBACK];
+    #pragma unroll
+                for (int i = 0; i < LOOKBACK; ++i)
+                    st[i] = (j - i >= 0) ? status_load(status + (size_t)(j - i) * 256 + d) : OS_PREFIX;
+                int used = 0;
+                bool found = false, stalled = false;
+    #pragma unroll
+                for (int i = 0; i < LOOKBACK; ++i) {
+                    if (found || stalled) continue;
+                    const uint32_t flag = st[i] & ~OS_VALUE;
+                    if (flag == 0u) { stalled = true; continue; }
+                    excl += st[i] & OS_VALUE;
+                    ++used;
+                    found = flag == OS_PREFIX;
+                }
+                if (found) break;
+                j -= used;
+                if (stalled) {
+                    if (++spins > OS_SPIN_LIMIT) { atomicOr(err, 1u); break; }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            status_store(my, OS_PREFIX | (excl + cnt));
+        }
+        s_gstart[d] = excl;
+    }
+    // global exclusive start of digit d: sum of ghist[0..d) (block scan over 256)
+    {
+        const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const uint32_t c = d < 256 ? ghist[d] : 0u;
+        uint32_t incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o);
+            if ((int)lane >= o) incl += t;
+        }
+        __syncthreads();                    // s_tot is reused
+        if (lane == 63 && d < 256) s_tot[wave] = incl;
+        __syncthreads();
+        if (d < 256) {
+            uint32_t wo = 0;
+            for (uint32_t w = 0; w < wave; ++w) wo += s_tot[w];
+            s_gstart[d] += wo + incl - c;
+        }
+    }
+    __syncthreads();
+    const uint32_t count = min(OS_TILE, n - base);
+    for (uint32_t i = threadIdx.x; i < count; i += OS_BLOCK) {
+        const K k = s_keys[i];
+        const uint32_t dd = digit_of(k, shift);
+        const uint32_t gpos = s_gstart[dd] + (i - digit_start[dd]);
+        if (gpos < n) {   // always true for consistent counts; keeps a bad count from writing out of bounds
+            keys_out[gpos] = k;
+            vals_out[gpos] = s_vals[i];
+        }
+    }
+}
+
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 size_t sort_tmp_bytes(uint64_t n, bool key64) {
     const uint64_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;
     const size_t ks = key64 ? 8 : 4;
+    const int max_passes = key64 ? 8 : 4;
     size_t b = 0;
     b += align_up(n * ks, 256);                 // ping-pong keys
     b += align_up(n * 4, 256);                  // ping-pong values
     b += align_up(nblocks * 256 * 4, 256);      // digit table
     b += align_up(scan_tmp_words(nblocks * 256) * 4, 256);
+    // one-sweep: histograms, tickets and per-pass tile status
+    b += align_up((size_t)max_passes * 256 * 4 + 64 + (size_t)max_passes * nblocks * 256 * 4, 256);
     return b + 256;
 }
 
 template <typename K>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_out, uint32_t* vals_out, uint32_t n,
-                            const uint32_t* n_dev, uint32_t first_bit, uint32_t end_bit, void* tmp, hipStream_t s) {
+                            const uint32_t* n_dev, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t* err,
+                            hipStream_t s) {
     if (n == 0) return hipSuccess;
     const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
     const uint32_t passes = (bits + 7) / 8;
@@ -169,7 +338,18 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
     K* tk = reinterpret_cast<K*>(p); p += align_up((size_t)n * sizeof(K), 256);
     uint32_t* tv = reinterpret_cast<uint32_t*>(p); p += align_up((size_t)n * 4, 256);
     uint32_t* table = reinterpret_cast<uint32_t*>(p); p += align_up((size_t)nblocks * 256 * 4, 256);
-    uint32_t* stmp = reinterpret_cast<uint32_t*>(p);
+    uint32_t* stmp = reinterpret_cast<uint32_t*>(p); p += align_up(scan_tmp_words((uint64_t)nblocks * 256) * 4, 256);
+    const bool onesweep = n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS && err != nullptr;
+    const uint32_t os_tiles = (n + OS_TILE - 1) / OS_TILE;
+    uint32_t* ghist = reinterpret_cast<uint32_t*>(p);          // [passes][256]
+    uint32_t* status = ghist + passes * 256 + 16;              // [passes][os_tiles][256]
+    if (onesweep) {
+        hipError_t e = launch_fill_u32(ghist, 0u, (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
+        if (e != hipSuccess) return e;
+        sort_histogram_kernel<K><<<min(nblocks, HIST_BLOCKS), SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     const K* src_k = keys_in;
     const uint32_t* src_v = vals_in;
     for (uint32_t pass = 0; pass < passes; ++pass) {
@@ -177,14 +357,22 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         K* dk = to_out ? keys_out : tk;
         uint32_t* dv = to_out ? vals_out : tv;
         const uint32_t shift = first_bit + 8 * pass;
-        sort_upsweep_kernel<K><<<nblocks, SORT_BLOCK, 0, s>>>(src_k, n, n_dev, shift, table, nblocks);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        e = scan_u32(table, table, (uint64_t)nblocks * 256, false, stmp, nullptr, s);
-        if (e != hipSuccess) return e;
-        sort_scatter_kernel<K><<<nblocks, SORT_BLOCK, 0, s>>>(src_k, src_v, dk, dv, n, n_dev, shift, table, nblocks);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        hipError_t e;
+        if (onesweep) {
+            sort_onesweep_kernel<K><<<os_tiles, OS_BLOCK, 0, s>>>(src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256,
+                                                                  status + (size_t)pass * os_tiles * 256, err);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        } else {
+            sort_upsweep_kernel<K><<<nblocks, SORT_BLOCK, 0, s>>>(src_k, n, n_dev, shift, table, nblocks);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            e = scan_u32(table, table, (uint64_t)nblocks * 256, false, stmp, nullptr, s);
+            if (e != hipSuccess) return e;
+            sort_scatter_kernel<K><<<nblocks, SORT_BLOCK, 0, s>>>(src_k, src_v, dk, dv, n, n_dev, shift, table, nblocks);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
         src_k = dk;
         src_v = dv;
     }
@@ -193,12 +381,12 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
 
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
-                            void* tmp, hipStream_t s) {
+                            void* tmp, uint32_t* err, hipStream_t s) {
     if (key64)
         return sort_impl<uint64_t>(static_cast<const uint64_t*>(keys_in), vals_in, static_cast<uint64_t*>(keys_out),
-                                   vals_out, n, n_dev, first_bit, end_bit, tmp, s);
+                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s);
     return sort_impl<uint32_t>(static_cast<const uint32_t*>(keys_in), vals_in, static_cast<uint32_t*>(keys_out),
-                               vals_out, n, n_dev, first_bit, end_bit, tmp, s);
+                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s);
 }
 
 } // namespace vs

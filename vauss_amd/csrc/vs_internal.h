@@ -18,6 +18,12 @@ enum : uint32_t {
     CNT_COUNT = 8,
 };
 
+// Per-context device flags (read back with the projection counters).
+enum : uint32_t {
+    FLAG_SORT_STALL = 0,  // a one-sweep look-back gave up waiting
+    CTX_FLAGS = 4,
+};
+
 struct ProjectArgs {
     vs_camera cam;
     uint32_t img_w, img_h, tile_bw, tile_bh;
@@ -118,8 +124,10 @@ hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
 size_t sort_tmp_bytes(uint64_t n, bool key64);
+// `err` (device word, may be null: then the one-sweep schedule is not used)
+// is or-ed with 1 if a one-sweep look-back gave up waiting.
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
-                            void* tmp, hipStream_t s);
+                            void* tmp, uint32_t* err, hipStream_t s);
 
 } // namespace vs
