@@ -176,11 +176,10 @@ void vs_fwd_state_free(vs_fwd_state* state);
  * semantics.  Projected rows are indexed by global splat id. */
 typedef struct vs_state_view {
     uint32_t num_splats, num_visible, num_intersections, num_tiles, tile_bw, tile_bh;
-    uint32_t depth_shift;           /* sorted key = tile << depth_shift | (depth_bits - depth_min) */
-    uint32_t depth_min;
-    const uint64_t* isect_keys;     /* [I] sorted */
+    const uint32_t* isect_tiles;    /* [I] sorted tile ids (T = sentinel, sorts last) */
     const uint32_t* isect_gids;     /* [I] sorted global splat ids */
     const uint32_t* intersect_counts; /* [N] */
+    const uint32_t* depth_bits;     /* [N] raw f32 bits of view z (the depth key) */
     const float* proj_xy_conic;     /* [N,4] x, y, c00, c01 (valid for visible splats) */
     const float* proj_c11_opac_rg;  /* [N,4] c11, opacity, r, g */
     const float* proj_b;            /* [N] b */
@@ -198,9 +197,9 @@ vs_status vs_fwd_state_view(const vs_fwd_state* state, vs_state_view* out);
 vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, const uint32_t* vals, uint32_t n,
                                const uint32_t* n_dev, uint32_t skip_bits, uint32_t sorting_bits,
                                uint32_t* out_keys, uint32_t* out_vals);
-/* The same sort on packed 64-bit keys (tile id above depth bits), bits
- * [0, sorting_bits) with sorting_bits <= 64.  No reference counterpart as
- * an API: it replaces the reference's two sorts of render.rs:689-694,792-794. */
+/* The same sort on 64-bit keys, bits [0, sorting_bits) with sorting_bits <= 64
+ * (e.g. a packed (tile, depth) key).  No reference counterpart: the
+ * reference's sort crate takes u32 keys only. */
 vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, const uint32_t* vals, uint32_t n,
                                uint32_t sorting_bits, uint64_t* out_keys, uint32_t* out_vals);
 /* prefix_sum (crates/splat-train-scan/src/lib.rs:24-83): inclusive scan. */

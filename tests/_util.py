@@ -60,13 +60,11 @@ def gpu_state_arrays(out):
     """Intermediate buffers of a GPU forward as numpy arrays keyed like the oracle's."""
     v = out.state.view()
     n, i = v.num_splats, v.num_intersections
-    keys = dev_to_numpy(v.isect_keys, (i,), np.uint64)
-    gids = dev_to_numpy(v.isect_gids, (i,), np.uint32)
     return {
         "view": v,
-        "tile": (keys >> np.uint64(v.depth_shift)).astype(np.uint32),
-        "depth_bits": ((keys & np.uint64((1 << v.depth_shift) - 1)) + np.uint64(v.depth_min)).astype(np.uint32),
-        "gid": gids,
+        "tile": dev_to_numpy(v.isect_tiles, (i,), np.uint32),
+        "depth_bits": dev_to_numpy(v.depth_bits, (n,), np.uint32),
+        "gid": dev_to_numpy(v.isect_gids, (i,), np.uint32),
         "counts": dev_to_numpy(v.intersect_counts, (n,), np.uint32),
         "proj_a": dev_to_numpy(v.proj_xy_conic, (n, 4), np.float32),
         "proj_b": dev_to_numpy(v.proj_c11_opac_rg, (n, 4), np.float32),

@@ -55,10 +55,8 @@ def _check_forward(out, ref, gpu):
     got = np.concatenate([gpu["proj_a"][gfc], gpu["proj_b"][gfc], gpu["proj_c"][gfc, None]], axis=1)
     got = got[:, [0, 1, 2, 3, 4, 5, 6, 7, 8]]
     np.testing.assert_array_equal(got.view(np.uint32), proj.view(np.uint32))
-    # the depth half of every packed key is the splat's raw view-z bits
-    depth_of = np.zeros(info.num_splats, np.uint32)
-    depth_of[gfc] = ref.get(po.F_DEPTHS).view(np.uint32)
-    np.testing.assert_array_equal(gpu["depth_bits"], depth_of[ref.get(po.F_ISECT_GID)])
+    # the depth key of every visible splat is its raw view-z bits
+    np.testing.assert_array_equal(gpu["depth_bits"][gfc], ref.get(po.F_DEPTHS).view(np.uint32))
     # aux outputs
     np.testing.assert_array_equal(out.aux.opacities.cpu().numpy().view(np.uint32), ref.get(po.F_OPACITIES).view(np.uint32))
     np.testing.assert_array_equal(out.aux.max_radius.cpu().numpy().view(np.uint32), ref.get(po.F_MAX_RADIUS).view(np.uint32))

@@ -59,8 +59,8 @@ class VsStageTimes(C.Structure):
 class VsStateView(C.Structure):
     _fields_ = [("num_splats", C.c_uint32), ("num_visible", C.c_uint32), ("num_intersections", C.c_uint32),
                 ("num_tiles", C.c_uint32), ("tile_bw", C.c_uint32), ("tile_bh", C.c_uint32),
-                ("depth_shift", C.c_uint32), ("depth_min", C.c_uint32),
-                ("isect_keys", C.c_void_p), ("isect_gids", C.c_void_p), ("intersect_counts", C.c_void_p),
+                ("isect_tiles", C.c_void_p), ("isect_gids", C.c_void_p), ("intersect_counts", C.c_void_p),
+                ("depth_bits", C.c_void_p),
                 ("proj_xy_conic", C.c_void_p), ("proj_c11_opac_rg", C.c_void_p), ("proj_b", C.c_void_p),
                 ("proj_aux", C.c_void_p), ("tile_ranges", C.c_void_p)]
 

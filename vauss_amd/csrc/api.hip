@@ -68,7 +68,7 @@ struct vs_fwd_state {
     float lso = 0.0f;
     float bg[3] = {0, 0, 0};
     vs_pass pass = VS_PASS_FORWARD;
-    uint32_t tbw = 0, tbh = 0, T = 0, V = 0, I = 0, shift = 0, dmin = 0;
+    uint32_t tbw = 0, tbh = 0, T = 0, V = 0, I = 0, M = 0;
     void* arena = nullptr;        // per-splat buffers
     void* isect_arena = nullptr;  // per-intersection buffers
     uint32_t* counts = nullptr;
@@ -85,8 +85,8 @@ struct vs_fwd_state {
     uint32_t* ranges = nullptr;
     uint32_t* ranges_shrunk = nullptr;
     float* v_combined = nullptr;
-    uint64_t* keys = nullptr;
-    uint32_t* gids = nullptr;
+    uint32_t* tiles = nullptr;    // [I] sorted tile ids
+    uint32_t* gids = nullptr;     // [I] sorted global ids
 };
 
 namespace {
@@ -252,7 +252,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     const size_t o_opac = out->opacities ? 0 : take((size_t)N * 4);
     const size_t o_rad = out->max_radius ? 0 : take((size_t)N * 4);
     const size_t o_vis = (bwd_info && !out->visible) ? take((size_t)N * 4) : 0;
-    const size_t o_bs = take((size_t)std::max(nblocks, 1u) * 16);
+    const size_t o_bs = take((size_t)std::max(nblocks, 1u) * 4 * BS_ROWS);
     const size_t o_cnt = take(CNT_COUNT * 4);
     const size_t o_rng = take((size_t)T * 8), o_rngs = take((size_t)T * 8);
     VS_HIP(hipMallocAsync(&st->arena, off, s), "hipMallocAsync(splat arena)");
@@ -297,48 +297,72 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         return fail(VS_ERR_HIP, "an earlier radix sort on this context gave up waiting in its look-back; its output was wrong");
     }
     st->V = hc[CNT_VISIBLE];
+    st->M = hc[CNT_EMITTERS];
     uint64_t I64 = 0;
     std::memcpy(&I64, hc + CNT_ISECT64, 8);
     if (I64 > 0xFFFFFFFFull) return fail(VS_ERR_CAPACITY, "intersection count exceeds u32");
     st->I = (uint32_t)I64;
-    st->dmin = (st->V > 0) ? hc[CNT_DEPTH_MIN] : 0u;
+    const uint32_t dmin = (st->V > 0) ? hc[CNT_DEPTH_MIN] : 0u;
     const uint32_t dmax = (st->V > 0) ? hc[CNT_DEPTH_MAX] : 0u;
-    st->shift = bit_length((uint64_t)(dmax - st->dmin));
+    const uint32_t depth_bits = bit_length((uint64_t)(dmax - dmin));
     const uint32_t tile_bits = bit_length(T);     // the sentinel tile id T must fit too
-    const uint32_t end_bit = st->shift + tile_bits;
-    const uint32_t I = st->I;
+    const uint32_t I = st->I, M = st->M;
 
-    // ---- emission + sort ---------------------------------------------------------
+    // ---- binning: compaction, depth sort, slot scan, emission, tile sort ------------
     if (I > 0) {
         size_t ioff = 0;
         auto itake = [&](size_t bytes) { const size_t o = ioff; ioff += align256(bytes); return o; };
-        const size_t o_ku = itake((size_t)I * 8), o_vu = itake((size_t)I * 4);
-        const size_t o_k = itake((size_t)I * 8), o_v = itake((size_t)I * 4);
-        const size_t o_tmp = itake(sort_tmp_bytes(I, true));
+        const size_t o_tu = itake((size_t)I * 4), o_vu = itake((size_t)I * 4);
+        const size_t o_t = itake((size_t)I * 4), o_v = itake((size_t)I * 4);
+        const size_t o_dk = itake((size_t)M * 4), o_dv = itake((size_t)M * 4);
+        const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)N * 4);
+        const size_t o_scan = itake(scan_tmp_words(M) * 4);
+        const size_t o_tmp = itake(sort_tmp_bytes(I, false));     // M <= I: serves both sorts
         VS_HIP(hipMallocAsync(&st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
         char* ib = static_cast<char*>(st->isect_arena);
-        uint64_t* keys_u = reinterpret_cast<uint64_t*>(ib + o_ku);
+        uint32_t* tiles_u = reinterpret_cast<uint32_t*>(ib + o_tu);
         uint32_t* vals_u = reinterpret_cast<uint32_t*>(ib + o_vu);
-        st->keys = reinterpret_cast<uint64_t*>(ib + o_k);
+        st->tiles = reinterpret_cast<uint32_t*>(ib + o_t);
         st->gids = reinterpret_cast<uint32_t*>(ib + o_v);
+        uint32_t* dkeys = reinterpret_cast<uint32_t*>(ib + o_dk);
+        uint32_t* dvals = reinterpret_cast<uint32_t*>(ib + o_dv);
+        uint32_t* dkeys_sorted = reinterpret_cast<uint32_t*>(ib + o_dks);
+        uint32_t* order = reinterpret_cast<uint32_t*>(ib + o_ord);
+        uint32_t* slot_base = reinterpret_cast<uint32_t*>(ib + o_base);   // written for splats with hits only
+        uint32_t* scan_tmp = reinterpret_cast<uint32_t*>(ib + o_scan);
+        uint32_t* err = ctx->dev_flags + FLAG_SORT_STALL;
         {
             StageTimer tm(ctx, ST_EMIT);
+            CompactArgs ca{};
+            ca.num_splats = N; ca.counts = st->counts; ca.depth_bits = st->depth_bits;
+            ca.block_offsets = st->block_stats + (size_t)BS_EMIT * nblocks; ca.counters = st->counters;
+            ca.keys = dkeys; ca.vals = dvals;
+            VS_HIP(launch_compact(ca, s), "compaction");
+        }
+        {
+            StageTimer tm(ctx, ST_SORT);
+            VS_HIP(radix_sort_pairs(dkeys, dvals, dkeys_sorted, order, M, nullptr, false, 0, depth_bits, ib + o_tmp,
+                                    err, s),
+                   "depth sort");
+        }
+        {
+            StageTimer tm(ctx, ST_EMIT);
+            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order), "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
-            ea.depth_shift = st->shift; ea.depth_min = st->dmin;
-            ea.counts = st->counts; ea.block_offsets = st->block_stats; ea.depth_bits = st->depth_bits;
-            ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.keys = keys_u; ea.vals = vals_u;
+            ea.counts = st->counts; ea.slot_base = slot_base;
+            ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u;
             VS_HIP(launch_emit(ea, s), "emit kernel");
         }
         {
             StageTimer tm(ctx, ST_SORT);
-            VS_HIP(radix_sort_pairs(keys_u, vals_u, st->keys, st->gids, I, nullptr, true, 0, end_bit, ib + o_tmp,
-                                    ctx->dev_flags + FLAG_SORT_STALL, s),
-                   "tile/depth sort");
+            VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, nullptr, false, 0, tile_bits, ib + o_tmp,
+                                    err, s),
+                   "tile sort");
         }
         {
             StageTimer tm(ctx, ST_RANGES);
-            VS_HIP(launch_tile_ranges(st->keys, I, st->shift, T, st->ranges, s), "tile ranges");
+            VS_HIP(launch_tile_ranges(st->tiles, I, T, st->ranges, s), "tile ranges");
         }
     }
 
@@ -416,8 +440,9 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
 extern "C" vs_status vs_fwd_state_view(const vs_fwd_state* st, vs_state_view* o) {
     if (!st || !o) return fail(VS_ERR_INVALID, "null argument");
     o->num_splats = st->N; o->num_visible = st->V; o->num_intersections = st->I; o->num_tiles = st->T;
-    o->tile_bw = st->tbw; o->tile_bh = st->tbh; o->depth_shift = st->shift; o->depth_min = st->dmin;
-    o->isect_keys = st->keys; o->isect_gids = st->gids; o->intersect_counts = st->counts;
+    o->tile_bw = st->tbw; o->tile_bh = st->tbh;
+    o->isect_tiles = st->tiles; o->isect_gids = st->gids; o->intersect_counts = st->counts;
+    o->depth_bits = st->depth_bits;
     o->proj_xy_conic = reinterpret_cast<const float*>(st->proj_a);
     o->proj_c11_opac_rg = reinterpret_cast<const float*>(st->proj_b);
     o->proj_b = st->proj_c;

@@ -4,10 +4,16 @@
 // (crates/splat-train-render/src/kernels/project_forward.rs:26-261,
 // kernels/project_visible.rs:97-312): each lane owns one splat, culls it, and a
 // surviving splat reads its SH row, writes its projected row at its global id
-// (no compaction pass) and counts the tiles its ellipse touches.  Emission
-// writes one packed 64-bit (tile, depth) key per hit tile at offsets from a
-// scan over global-id order, so a stable sort by key yields per-tile depth
-// order with ties in global-id order.
+// (no compaction of the rows) and counts the tiles its ellipse touches.
+//
+// Binning then follows the reference's order of work (render.rs:689-794) on
+// smaller keys: the splats that hit a tile are compacted in global-id order
+// with their depth bits (less the minimum) as u32 keys, a stable radix sort
+// puts them in depth order (ties in global-id order), a scan of their tile
+// counts in that order gives each one its slot range, and emission (in
+// global-id order) writes one u32 tile id per hit tile into that range.  A
+// stable sort by tile id then yields each tile's list in (depth bits, global
+// id) order.
 #include "vs_device.h"
 #include "vs_camera.h"
 #include "vs_sh.h"
@@ -80,24 +86,30 @@ VS_DEV uint32_t wave_max(uint32_t v) {
     return v;
 }
 
-// One workgroup: exclusive scan of the block tile counts (in place) with a
-// 64-bit running total, plus the visible count and the depth-bit range.
+// One workgroup reduces the projection's block statistics: the 64-bit total of
+// tile hits, the visible count, the depth-bit range, and the exclusive scan
+// (in place) of the per-block counts of splats that hit at least one tile,
+// which are the compaction offsets of those splats.
 constexpr int FIN_BLOCK = 1024;
 __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __restrict__ stats, uint32_t nb,
                                                                    uint32_t* __restrict__ counters) {
     __shared__ uint32_t s_w[FIN_BLOCK / 64];
     __shared__ uint32_t s_vis[FIN_BLOCK / 64], s_min[FIN_BLOCK / 64], s_max[FIN_BLOCK / 64];
+    __shared__ unsigned long long s_hits[FIN_BLOCK / 64];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t* sums = stats;
-    const uint32_t* vis = stats + nb;
-    const uint32_t* dmin = stats + 2 * (size_t)nb;
-    const uint32_t* dmax = stats + 3 * (size_t)nb;
-    uint64_t carry = 0;
+    const uint32_t* hits = stats + (size_t)BS_HITS * nb;
+    const uint32_t* vis = stats + (size_t)BS_VISIBLE * nb;
+    const uint32_t* dmin = stats + (size_t)BS_DMIN * nb;
+    const uint32_t* dmax = stats + (size_t)BS_DMAX * nb;
+    uint32_t* emit = stats + (size_t)BS_EMIT * nb;
+    uint32_t carry = 0;
+    unsigned long long h_acc = 0;
     uint32_t v_acc = 0, mn_acc = 0xFFFFFFFFu, mx_acc = 0u;
     for (uint32_t start = 0; start < nb; start += FIN_BLOCK) {
         const uint32_t i = start + threadIdx.x;
-        const uint32_t x = (i < nb) ? sums[i] : 0u;
+        const uint32_t x = (i < nb) ? emit[i] : 0u;
         if (i < nb) {
+            h_acc += hits[i];
             v_acc += vis[i];
             mn_acc = min(mn_acc, dmin[i]);
             mx_acc = max(mx_acc, dmax[i]);
@@ -110,26 +122,32 @@ __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __
         }
         if (lane == 63) s_w[wave] = incl;
         __syncthreads();
-        uint64_t before = 0, chunk = 0;
+        uint32_t before = 0, chunk = 0;
         for (uint32_t w = 0; w < FIN_BLOCK / 64; ++w) {
             if (w < wave) before += s_w[w];
             chunk += s_w[w];
         }
-        if (i < nb) sums[i] = (uint32_t)(carry + before + incl - x);
+        if (i < nb) emit[i] = carry + before + incl - x;
         carry += chunk;
         __syncthreads();
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) h_acc += __shfl_xor(h_acc, o);
     const uint32_t wv = wave_sum(v_acc), wmn = wave_min(mn_acc), wmx = wave_max(mx_acc);
-    if (lane == 0) { s_vis[wave] = wv; s_min[wave] = wmn; s_max[wave] = wmx; }
+    if (lane == 0) { s_vis[wave] = wv; s_min[wave] = wmn; s_max[wave] = wmx; s_hits[wave] = h_acc; }
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t tv = 0, tmn = 0xFFFFFFFFu, tmx = 0u;
-        for (int w = 0; w < FIN_BLOCK / 64; ++w) { tv += s_vis[w]; tmn = min(tmn, s_min[w]); tmx = max(tmx, s_max[w]); }
+        unsigned long long th = 0;
+        for (int w = 0; w < FIN_BLOCK / 64; ++w) {
+            tv += s_vis[w]; tmn = min(tmn, s_min[w]); tmx = max(tmx, s_max[w]); th += s_hits[w];
+        }
         counters[CNT_VISIBLE] = tv;
         counters[CNT_DEPTH_MIN] = tmn;
         counters[CNT_DEPTH_MAX] = tmx;
-        counters[CNT_ISECT64] = (uint32_t)carry;
-        counters[CNT_ISECT64 + 1] = (uint32_t)(carry >> 32);
+        counters[CNT_EMITTERS] = carry;
+        counters[CNT_ISECT64] = (uint32_t)th;
+        counters[CNT_ISECT64 + 1] = (uint32_t)(th >> 32);
     }
 }
 
@@ -263,49 +281,67 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
     // Block statistics, reduced by finalize_counts_kernel (no global atomics:
     // a same-address atomic from every wave serialises across the XCDs).
     __shared__ uint32_t s_sum[PROJ_BLOCK / 64], s_vis[PROJ_BLOCK / 64], s_min[PROJ_BLOCK / 64], s_max[PROJ_BLOCK / 64];
+    __shared__ uint32_t s_emit[PROJ_BLOCK / 64];
     const uint32_t wsum = wave_sum(hits);
     const uint32_t wvis = (uint32_t)__popcll(__ballot(visible));
+    const uint32_t wemit = (uint32_t)__popcll(__ballot(hits > 0u));
     const uint32_t wmin = wave_min(visible ? dbits : 0xFFFFFFFFu);
     const uint32_t wmax = wave_max(visible ? dbits : 0u);
     const uint32_t wave = threadIdx.x / 64;
-    if (lane == 0) { s_sum[wave] = wsum; s_vis[wave] = wvis; s_min[wave] = wmin; s_max[wave] = wmax; }
+    if (lane == 0) { s_sum[wave] = wsum; s_vis[wave] = wvis; s_min[wave] = wmin; s_max[wave] = wmax; s_emit[wave] = wemit; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t bs = 0, bv = 0, bmn = 0xFFFFFFFFu, bmx = 0u;
+        uint32_t bs = 0, bv = 0, bmn = 0xFFFFFFFFu, bmx = 0u, be = 0;
 #pragma unroll
         for (int w = 0; w < PROJ_BLOCK / 64; ++w) {
-            bs += s_sum[w]; bv += s_vis[w]; bmn = min(bmn, s_min[w]); bmx = max(bmx, s_max[w]);
+            bs += s_sum[w]; bv += s_vis[w]; bmn = min(bmn, s_min[w]); bmx = max(bmx, s_max[w]); be += s_emit[w];
         }
         const uint32_t nb = gridDim.x;
-        a.block_stats[blockIdx.x] = bs;
-        a.block_stats[nb + blockIdx.x] = bv;
-        a.block_stats[2 * nb + blockIdx.x] = bmn;
-        a.block_stats[3 * nb + blockIdx.x] = bmx;
+        a.block_stats[BS_HITS * nb + blockIdx.x] = bs;
+        a.block_stats[BS_VISIBLE * nb + blockIdx.x] = bv;
+        a.block_stats[BS_DMIN * nb + blockIdx.x] = bmn;
+        a.block_stats[BS_DMAX * nb + blockIdx.x] = bmx;
+        a.block_stats[BS_EMIT * nb + blockIdx.x] = be;
     }
 }
 
-__global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
+// Compaction of the splats that hit a tile, in global-id order, as (depth
+// bits - minimum, global id) pairs: the input of the depth sort (the
+// reference's depth argsort of render.rs:689-694, keyed on raw f32 bits).
+// Blocks match the projection's, whose scanned emitter counts give the base.
+__global__ void __launch_bounds__(PROJ_BLOCK) compact_kernel(CompactArgs a) {
     const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
     const uint32_t lane = lane_id(), wave = threadIdx.x / 64;
-    const uint32_t cnt = (g < a.num_splats) ? a.counts[g] : 0u;
-    // Block-exclusive scan of the counts (global-id order).
-    uint32_t incl = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o);
-        if ((int)lane >= o) incl += v;
-    }
+    const bool e = g < a.num_splats && a.counts[g] > 0u;
+    const uint64_t m = __ballot(e);
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     __shared__ uint32_t s_w[PROJ_BLOCK / 64];
-    if (lane == 63) s_w[wave] = incl;
+    if (lane == 0) s_w[wave] = (uint32_t)__popcll(m);
     __syncthreads();
-    uint32_t wave_base = 0;
-    for (uint32_t w = 0; w < wave; ++w) wave_base += s_w[w];
-    const uint32_t base = a.block_offsets[blockIdx.x] + wave_base + incl - cnt;
+    uint32_t base = a.block_offsets[blockIdx.x];
+    for (uint32_t w = 0; w < wave; ++w) base += s_w[w];
+    if (e) {
+        const uint32_t o = base + (uint32_t)__popcll(m & lt_mask);
+        a.keys[o] = a.depth_bits[g] - a.counters[CNT_DEPTH_MIN];
+        a.vals[o] = g;
+    }
+}
 
+// Emission (kernels/map_gaussians.rs:23-174), one lane per splat in global-id
+// order so the projected rows are read coalesced: a splat with hits owns the
+// slots [slot_base, slot_base + count), which a scan in depth order assigned,
+// and writes there the ids of the tiles that pass the tile test, in row-major
+// box order; if the recomputed test finds fewer tiles than the projection
+// counted, the rest of its slots get the sentinel tile id T, which sorts last
+// and owns no range.
+__global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
+    const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t cnt = (g < a.num_splats) ? a.counts[g] : 0u;
+    const uint32_t base = (cnt > 0) ? a.slot_base[g] : 0u;
     float px = 0.0f, py = 0.0f, power = 0.0f;
     S2 conic{0.0f, 0.0f, 0.0f};
     TileBox bb{0, 0, 0, 0};
-    uint64_t key_lo = 0;
     if (cnt > 0) {
         // Recompute the box from the projected row as kernels/map_gaussians.rs:61-66 does.
         const float4 pa = a.proj_a[g];
@@ -316,23 +352,21 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
         float ex, ey;
         bbox_extent(conic, power, ex, ey);
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
-        key_lo = (uint64_t)(a.depth_bits[g] - a.depth_min);
     }
     const uint32_t bw = bb.x1 - bb.x0;
     const uint32_t nb = (cnt > 0) ? (bb.y1 - bb.y0) * bw : 0u;
-    const uint32_t shift = a.depth_shift;
-    const uint64_t sentinel = (uint64_t)(a.tile_bw * a.tile_bh) << shift;
+    const uint32_t sentinel = a.tile_bw * a.tile_bh;
     if (cnt > 0 && nb <= SMALL_BBOX) {
         uint32_t k = 0;
         for (uint32_t i = 0; i < nb; ++i) {
             const uint32_t tx = i % bw + bb.x0, ty = i / bw + bb.y0;
             if (k < cnt && will_contribute(tx, ty, px, py, conic, power)) {
-                a.keys[base + k] = ((uint64_t)(tx + ty * a.tile_bw) << shift) | key_lo;
+                a.tiles[base + k] = tx + ty * a.tile_bw;
                 a.vals[base + k] = g;
                 ++k;
             }
         }
-        for (; k < cnt; ++k) { a.keys[base + k] = sentinel; a.vals[base + k] = g; }
+        for (; k < cnt; ++k) { a.tiles[base + k] = sentinel; a.vals[base + k] = g; }
     }
     uint64_t pending = __ballot(cnt > 0 && nb > SMALL_BBOX);
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -343,7 +377,6 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
         const float lp = rl(power, leader);
         const uint32_t lx0 = rl(bb.x0, leader), ly0 = rl(bb.y0, leader), lw = rl(bw, leader), ln = rl(nb, leader);
         const uint32_t lbase = rl(base, leader), lcnt = rl(cnt, leader), lg = rl(g, leader);
-        const uint32_t lkey_lo = rl((uint32_t)key_lo, leader);
         uint32_t emitted = 0;
         for (uint32_t t0 = 0; t0 < ln; t0 += 64) {
             const uint32_t t = t0 + lane;
@@ -352,13 +385,13 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
             const uint64_t m = __ballot(hit);
             const uint32_t slot = emitted + (uint32_t)__popcll(m & lt_mask);
             if (hit && slot < lcnt) {
-                a.keys[lbase + slot] = ((uint64_t)(tx + ty * a.tile_bw) << shift) | (uint64_t)lkey_lo;
+                a.tiles[lbase + slot] = tx + ty * a.tile_bw;
                 a.vals[lbase + slot] = lg;
             }
             emitted += (uint32_t)__popcll(m);
         }
         for (uint32_t p = (emitted < lcnt ? emitted : lcnt) + lane; p < lcnt; p += 64) {
-            a.keys[lbase + p] = sentinel;
+            a.tiles[lbase + p] = sentinel;
             a.vals[lbase + p] = lg;
         }
         pending &= pending - 1;
@@ -404,6 +437,12 @@ hipError_t launch_project(const ProjectArgs& a, hipStream_t s) {
     case 3: launch_project_model<3>(a, grid, s, geom); break;
     default: launch_project_model<4>(a, grid, s, geom); break;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_compact(const CompactArgs& a, hipStream_t s) {
+    if (a.num_splats == 0) return hipSuccess;
+    compact_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
 

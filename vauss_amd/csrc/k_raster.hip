@@ -31,14 +31,15 @@ namespace vs {
 
 constexpr int BWD_BATCH = 64;
 
-__global__ void tile_ranges_kernel(const uint64_t* __restrict__ keys, uint32_t n, uint32_t shift, uint32_t num_tiles,
+// get_tile_offset.rs:11-59: [start, end) of each tile in the sorted ids.
+__global__ void tile_ranges_kernel(const uint32_t* __restrict__ tiles, uint32_t n, uint32_t num_tiles,
                                    uint32_t* __restrict__ ranges) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const uint64_t tile = keys[i] >> shift;
+    const uint32_t tile = tiles[i];
     if (tile >= num_tiles) return;   // sentinel rows sort last and own no tile
-    if (i == 0 || (keys[i - 1] >> shift) != tile) ranges[tile * 2] = i;
-    if (i + 1 == n || (keys[i + 1] >> shift) != tile) ranges[tile * 2 + 1] = i + 1;
+    if (i == 0 || tiles[i - 1] != tile) ranges[tile * 2] = i;
+    if (i + 1 == n || tiles[i + 1] != tile) ranges[tile * 2 + 1] = i + 1;
 }
 
 // DIST_NEAR / DIST_FAR depth map, kernels/helpers.rs:91-103.
@@ -482,10 +483,9 @@ __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, 
     }
 }
 
-hipError_t launch_tile_ranges(const uint64_t* keys, uint32_t n, uint32_t shift, uint32_t num_tiles, uint32_t* ranges,
-                              hipStream_t s) {
+hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    tile_ranges_kernel<<<(n + 255) / 256, 256, 0, s>>>(keys, n, shift, num_tiles, ranges);
+    tile_ranges_kernel<<<(n + 255) / 256, 256, 0, s>>>(tiles, n, num_tiles, ranges);
     return hipGetLastError();
 }
 

@@ -24,14 +24,33 @@
 
 namespace vs {
 
+#ifndef VS_SORT_ITEMS
+#define VS_SORT_ITEMS 8
+#endif
+#ifndef VS_ONESWEEP_MIN
+#define VS_ONESWEEP_MIN (1u << 16)
+#endif
 constexpr int SORT_BLOCK = 256;
-constexpr int SORT_ITEMS = 8;
-constexpr uint32_t SORT_TILE = SORT_BLOCK * SORT_ITEMS;   // 2048 keys per block
+constexpr int SORT_ITEMS = VS_SORT_ITEMS;
+constexpr uint32_t SORT_TILE = SORT_BLOCK * SORT_ITEMS;   // keys per block of the three-kernel schedule
 constexpr int SORT_WAVES = SORT_BLOCK / 64;
-constexpr uint32_t KEYS_PER_WAVE = 64 * SORT_ITEMS;
 
 template <typename K>
 __device__ __forceinline__ uint32_t digit_of(K k, uint32_t shift) { return (uint32_t)(k >> shift) & 0xFFu; }
+
+// Adds the digits of 64 consecutive keys (one per lane, the first `nvalid`
+// valid) to a wavefront's LDS histogram: only the first lane of each run of
+// equal digits adds, with the run's length, so runs (a splat's tiles along a
+// row share the high digit of the tile id) cost one LDS atomic, not one per
+// key on the same address.
+__device__ __forceinline__ void hist_add_runs(uint32_t* hist, uint32_t d, uint32_t lane, uint32_t nvalid) {
+    const uint64_t above_me = ~((2ull << lane) - 1ull);   // lanes above this one (none for lane 63)
+    const uint32_t prev = __shfl_up(d, 1);
+    const bool head = lane < nvalid && (lane == 0 || prev != d);
+    const uint64_t nxt = __ballot(head) & above_me;
+    const uint32_t end = nxt ? (uint32_t)__builtin_ctzll(nxt) : nvalid;
+    if (head) atomicAdd(&hist[d], end - lane);
+}
 
 template <typename K>
 __global__ void __launch_bounds__(SORT_BLOCK) sort_upsweep_kernel(const K* __restrict__ keys, uint32_t n_cap,
@@ -39,14 +58,23 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_upsweep_kernel(const K* __res
                                                                   uint32_t* __restrict__ table, uint32_t nblocks) {
     __shared__ uint32_t hist[SORT_WAVES][256];
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
-    const uint32_t wave = threadIdx.x >> 6;
-    for (uint32_t i = threadIdx.x; i < SORT_WAVES * 256; i += SORT_BLOCK) (&hist[0][0])[i] = 0;
-    __syncthreads();
-    const uint32_t base = blockIdx.x * SORT_TILE;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Wavefront w counts keys [base + w*64*ITEMS, ...), the same keys its
+    // wavefront ranks in the scatter kernel.
+    const uint32_t wbase = blockIdx.x * SORT_TILE + wave * (64 * SORT_ITEMS);
+    K k[SORT_ITEMS];
 #pragma unroll
     for (int i = 0; i < SORT_ITEMS; ++i) {
-        const uint32_t idx = base + i * SORT_BLOCK + threadIdx.x;
-        if (idx < n) atomicAdd(&hist[wave][digit_of(keys[idx], shift)], 1u);
+        const uint32_t idx = wbase + i * 64 + lane;
+        k[i] = idx < n ? keys[idx] : (K)0;
+    }
+    for (uint32_t i = threadIdx.x; i < SORT_WAVES * 256; i += SORT_BLOCK) (&hist[0][0])[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < SORT_ITEMS; ++i) {
+        const uint32_t b = wbase + i * 64;
+        const uint32_t nvalid = b < n ? min(64u, n - b) : 0u;
+        if (nvalid) hist_add_runs(hist[wave], digit_of(k[i], shift), lane, nvalid);
     }
     __syncthreads();
     const uint32_t d = threadIdx.x;
@@ -56,29 +84,40 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_upsweep_kernel(const K* __res
     table[(size_t)d * nblocks + blockIdx.x] = c;
 }
 
-// Block-level ranking of one tile of up to SORT_TILE keys.  On return the tile
+// Block-level ranking of one tile of up to BLOCK * ITEMS keys.  On return the tile
 // sits digit-ordered (and stable) in s_keys/s_vals, digit_start[d] is the
 // first LDS slot of digit d and d_count[d] (thread d) its count in the tile.
-template <typename K, int BLOCK>
+template <typename K, int BLOCK, int ITEMS>
 __device__ __forceinline__ uint32_t rank_tile(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                                               uint32_t base, uint32_t n, uint32_t shift,
                                               uint32_t (*wave_hist)[256], uint32_t* digit_start, uint32_t* s_tot,
                                               K* s_keys, uint32_t* s_vals) {
+    static_assert(BLOCK >= 256 && BLOCK % 64 == 0, "one thread per digit");
     constexpr int WAVES = BLOCK / 64;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Issue every load of the tile before any ranking step, so a wavefront
+    // waits for memory once rather than once per step.
+    K key[ITEMS];
+    uint32_t val[ITEMS], dig[ITEMS], rank[ITEMS];
+    const uint32_t wbase = base + wave * (64 * ITEMS);
+#pragma unroll
+    for (int s = 0; s < ITEMS; ++s) {
+        const uint32_t idx = wbase + s * 64 + lane;
+        key[s] = idx < n ? keys_in[idx] : (K)0;
+    }
+#pragma unroll
+    for (int s = 0; s < ITEMS; ++s) {
+        const uint32_t idx = wbase + s * 64 + lane;
+        val[s] = idx < n ? vals_in[idx] : 0u;
+    }
     for (uint32_t i = threadIdx.x; i < WAVES * 256; i += BLOCK) (&wave_hist[0][0])[i] = 0;
     __syncthreads();
 
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    K key[SORT_ITEMS];
-    uint32_t val[SORT_ITEMS], dig[SORT_ITEMS], rank[SORT_ITEMS];
-    const uint32_t wbase = base + wave * KEYS_PER_WAVE;
 #pragma unroll
-    for (int s = 0; s < SORT_ITEMS; ++s) {
+    for (int s = 0; s < ITEMS; ++s) {
         const uint32_t idx = wbase + s * 64 + lane;
         const bool valid = idx < n;
-        key[s] = valid ? keys_in[idx] : (K)0;
-        val[s] = valid ? vals_in[idx] : 0u;
         const uint32_t d = digit_of(key[s], shift);
         dig[s] = valid ? d : 256u;
         uint64_t peers = __ballot(valid);
@@ -127,7 +166,7 @@ __device__ __forceinline__ uint32_t rank_tile(const K* __restrict__ keys_in, con
     }
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < SORT_ITEMS; ++s) {
+    for (int s = 0; s < ITEMS; ++s) {
         if (dig[s] < 256u) {
             const uint32_t pos = digit_start[dig[s]] + wave_hist[wave][dig[s]] + rank[s];
             s_keys[pos] = key[s];
@@ -145,19 +184,23 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __res
                                                                   const uint32_t* __restrict__ offsets, uint32_t nblocks) {
     __shared__ uint32_t wave_hist[SORT_WAVES][256];
     __shared__ uint32_t digit_start[256];
-    __shared__ uint32_t s_tot[8];
+    __shared__ uint32_t s_tot[SORT_WAVES];
     __shared__ K s_keys[SORT_TILE];
     __shared__ uint32_t s_vals[SORT_TILE];
+
+    __shared__ uint32_t s_gstart[256];
 
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
     const uint32_t base = blockIdx.x * SORT_TILE;
     if (base >= n) return;   // uniform per block
-    rank_tile<K, SORT_BLOCK>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
+    rank_tile<K, SORT_BLOCK, SORT_ITEMS>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
+    if (threadIdx.x < 256) s_gstart[threadIdx.x] = offsets[(size_t)threadIdx.x * nblocks + blockIdx.x];
+    __syncthreads();
     const uint32_t count = min(SORT_TILE, n - base);
     for (uint32_t i = threadIdx.x; i < count; i += SORT_BLOCK) {
         const K k = s_keys[i];
         const uint32_t d = digit_of(k, shift);
-        const uint32_t gpos = offsets[(size_t)d * nblocks + blockIdx.x] + (i - digit_start[d]);
+        const uint32_t gpos = s_gstart[d] + (i - digit_start[d]);
         if (gpos < n) {   // always true for a consistent table; keeps a bad rank from writing out of bounds
             keys_out[gpos] = k;
             vals_out[gpos] = s_vals[i];
@@ -166,31 +209,79 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __res
 }
 
 // ---- one-sweep schedule ---------------------------------------------------------
-constexpr uint32_t ONESWEEP_MIN = 1u << 16;
-constexpr int OS_BLOCK = 512;
-constexpr uint32_t OS_TILE = OS_BLOCK * SORT_ITEMS;        // 4096 keys per one-sweep tile
+// Tile shapes: inputs of OS_SMALL_N keys or more use OS_BLOCK x OS_ITEMS
+// (8192) keys per block, which halves the look-back chain, the bound of a
+// pass over a long array; shorter inputs use OS_SMALL_BLOCK x OS_SMALL_ITEMS
+// (4096), which spreads them over more blocks (a pass there costs about the
+// latency of one block).  Measured on MI355X (u32 pairs, 4 passes over 30M
+// random keys): 8192-key tiles 0.86 ms, 4096 1.16 ms; a look-back window of
+// 8 predecessors per step beat 16 and 32.
+#ifndef VS_OS_BLOCK
+#define VS_OS_BLOCK 512
+#endif
+#ifndef VS_OS_ITEMS
+#define VS_OS_ITEMS 16
+#endif
+#ifndef VS_OS_SMALL_BLOCK
+#define VS_OS_SMALL_BLOCK 512
+#endif
+#ifndef VS_OS_SMALL_ITEMS
+#define VS_OS_SMALL_ITEMS 8
+#endif
+#ifndef VS_OS_SMALL_N
+#define VS_OS_SMALL_N (2u << 20)
+#endif
+#ifndef VS_LOOKBACK
+#define VS_LOOKBACK 8
+#endif
+#ifndef VS_HIST_BLOCKS
+#define VS_HIST_BLOCKS 1024
+#endif
+constexpr uint32_t ONESWEEP_MIN = VS_ONESWEEP_MIN;
+constexpr int OS_BLOCK = VS_OS_BLOCK;
+constexpr int OS_ITEMS = VS_OS_ITEMS;
+constexpr uint32_t OS_TILE = OS_BLOCK * OS_ITEMS;
+constexpr int OS_SMALL_BLOCK = VS_OS_SMALL_BLOCK;
+constexpr int OS_SMALL_ITEMS = VS_OS_SMALL_ITEMS;
+constexpr uint32_t OS_SMALL_TILE = OS_SMALL_BLOCK * OS_SMALL_ITEMS;
+constexpr uint32_t OS_SMALL_N = VS_OS_SMALL_N;
+constexpr uint32_t OS_MIN_TILE = OS_TILE < OS_SMALL_TILE ? OS_TILE : OS_SMALL_TILE;
 constexpr uint32_t ONESWEEP_MAX_KEYS = 1u << 30;       // counts fit the 30-bit status payload
 constexpr uint32_t OS_AGGREGATE = 1u << 30;            // status: this tile's own count
 constexpr uint32_t OS_PREFIX = 2u << 30;               // status: count of this tile and all before it
 constexpr uint32_t OS_VALUE = (1u << 30) - 1u;
 constexpr uint32_t OS_SPIN_LIMIT = 1u << 18;           // polls before a look-back gives up
 constexpr int MAX_PASSES = 8;
-constexpr int LOOKBACK = 16;                           // predecessor statuses read per look-back step
-constexpr uint32_t HIST_BLOCKS = 512;
+constexpr int LOOKBACK = VS_LOOKBACK;                  // predecessor statuses read per look-back step
+constexpr uint32_t HIST_BLOCKS = VS_HIST_BLOCKS;
+constexpr int HIST_ITEMS = 4;
 
 // Digit histograms of every pass in one read: ghist[p][d] (zeroed by the caller).
+// Each wavefront takes chunks of HIST_ITEMS x 64 consecutive keys.
 template <typename K>
 __global__ void __launch_bounds__(SORT_BLOCK) sort_histogram_kernel(const K* __restrict__ keys, uint32_t n_cap,
                                                                     const uint32_t* __restrict__ n_dev, uint32_t first_bit,
                                                                     uint32_t passes, uint32_t* __restrict__ ghist) {
     __shared__ uint32_t h[SORT_WAVES][MAX_PASSES][256];
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (uint32_t i = threadIdx.x; i < SORT_WAVES * MAX_PASSES * 256; i += SORT_BLOCK) (&h[0][0][0])[i] = 0;
     __syncthreads();
-    for (uint32_t i = blockIdx.x * SORT_BLOCK + threadIdx.x; i < n; i += gridDim.x * SORT_BLOCK) {
-        const K k = keys[i];
-        for (uint32_t p = 0; p < passes; ++p) atomicAdd(&h[wave][p][digit_of(k, first_bit + 8 * p)], 1u);
+    const uint64_t stride = (uint64_t)gridDim.x * SORT_WAVES * 64 * HIST_ITEMS;
+    for (uint64_t c = ((uint64_t)blockIdx.x * SORT_WAVES + wave) * 64 * HIST_ITEMS; c < n; c += stride) {
+        K k[HIST_ITEMS];
+#pragma unroll
+        for (int s = 0; s < HIST_ITEMS; ++s) {
+            const uint64_t idx = c + (uint64_t)s * 64 + lane;
+            k[s] = idx < n ? keys[idx] : (K)0;
+        }
+#pragma unroll
+        for (int s = 0; s < HIST_ITEMS; ++s) {
+            const uint64_t b = c + (uint64_t)s * 64;
+            if (b >= n) break;                                   // uniform across the wavefront
+            const uint32_t nvalid = (uint32_t)min((uint64_t)64, (uint64_t)n - b);
+            for (uint32_t p = 0; p < passes; ++p) hist_add_runs(h[wave][p], digit_of(k[s], first_bit + 8 * p), lane, nvalid);
+        }
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < passes * 256; i += SORT_BLOCK) {
@@ -210,18 +301,19 @@ __device__ __forceinline__ void status_store(uint32_t* p, uint32_t v) {
 
 // One pass: rank a tile, find its digits' global offsets by look-back, scatter.
 // `status` is [nblocks][256], zeroed before the pass.
-template <typename K>
-__global__ void __launch_bounds__(OS_BLOCK) sort_onesweep_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+template <typename K, int BLOCK, int ITEMS>
+__global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                                                                    K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
                                                                    uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
                                                                    const uint32_t* __restrict__ ghist, uint32_t* status,
                                                                    uint32_t* err) {
-    __shared__ uint32_t wave_hist[OS_BLOCK / 64][256];
+    constexpr uint32_t TILE = BLOCK * ITEMS;
+    __shared__ uint32_t wave_hist[BLOCK / 64][256];
     __shared__ uint32_t digit_start[256];
-    __shared__ uint32_t s_tot[8];
+    __shared__ uint32_t s_tot[BLOCK / 64];
     __shared__ uint32_t s_gstart[256];      // where this tile's digit d starts in the output
-    __shared__ K s_keys[OS_TILE];
-    __shared__ uint32_t s_vals[OS_TILE];
+    __shared__ K s_keys[TILE];
+    __shared__ uint32_t s_vals[TILE];
 
     // Tile = block index.  Workgroups are dispatched in index order on each
     // XCD, so every block this one waits on (lower indices) is already
@@ -230,10 +322,10 @@ __global__ void __launch_bounds__(OS_BLOCK) sort_onesweep_kernel(const K* __rest
     // pass across the XCDs.)
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
     const uint32_t tile = blockIdx.x;
-    const uint32_t base = tile * OS_TILE;
+    const uint32_t base = tile * TILE;
     // A tile past the end has no successor with keys.
     if (base >= n) return;
-    const uint32_t cnt = rank_tile<K, OS_BLOCK>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
+    const uint32_t cnt = rank_tile<K, BLOCK, ITEMS>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
 
     const uint32_t d = threadIdx.x;
     if (d < 256) {
@@ -293,8 +385,8 @@ __global__ void __launch_bounds__(OS_BLOCK) sort_onesweep_kernel(const K* __rest
         }
     }
     __syncthreads();
-    const uint32_t count = min(OS_TILE, n - base);
-    for (uint32_t i = threadIdx.x; i < count; i += OS_BLOCK) {
+    const uint32_t count = min(TILE, n - base);
+    for (uint32_t i = threadIdx.x; i < count; i += BLOCK) {
         const K k = s_keys[i];
         const uint32_t dd = digit_of(k, shift);
         const uint32_t gpos = s_gstart[dd] + (i - digit_start[dd]);
@@ -316,8 +408,9 @@ size_t sort_tmp_bytes(uint64_t n, bool key64) {
     b += align_up(n * 4, 256);                  // ping-pong values
     b += align_up(nblocks * 256 * 4, 256);      // digit table
     b += align_up(scan_tmp_words(nblocks * 256) * 4, 256);
-    // one-sweep: histograms, tickets and per-pass tile status
-    b += align_up((size_t)max_passes * 256 * 4 + 64 + (size_t)max_passes * nblocks * 256 * 4, 256);
+    // one-sweep: histograms and per-pass tile status
+    const uint64_t os_tiles = (n + OS_MIN_TILE - 1) / OS_MIN_TILE;
+    b += align_up((size_t)max_passes * 256 * 4 + 64 + (size_t)max_passes * os_tiles * 256 * 4, 256);
     return b + 256;
 }
 
@@ -340,13 +433,16 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
     uint32_t* table = reinterpret_cast<uint32_t*>(p); p += align_up((size_t)nblocks * 256 * 4, 256);
     uint32_t* stmp = reinterpret_cast<uint32_t*>(p); p += align_up(scan_tmp_words((uint64_t)nblocks * 256) * 4, 256);
     const bool onesweep = n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS && err != nullptr;
-    const uint32_t os_tiles = (n + OS_TILE - 1) / OS_TILE;
+    const bool small = n < OS_SMALL_N;
+    const uint32_t os_tile = small ? OS_SMALL_TILE : OS_TILE;
+    const uint32_t os_tiles = (n + os_tile - 1) / os_tile;
     uint32_t* ghist = reinterpret_cast<uint32_t*>(p);          // [passes][256]
     uint32_t* status = ghist + passes * 256 + 16;              // [passes][os_tiles][256]
     if (onesweep) {
         hipError_t e = launch_fill_u32(ghist, 0u, (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
         if (e != hipSuccess) return e;
-        sort_histogram_kernel<K><<<min(nblocks, HIST_BLOCKS), SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+        const uint32_t hist_blocks = (uint32_t)min((uint64_t)HIST_BLOCKS, ((uint64_t)n + SORT_BLOCK * HIST_ITEMS - 1) / (SORT_BLOCK * HIST_ITEMS));
+        sort_histogram_kernel<K><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -359,8 +455,12 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         const uint32_t shift = first_bit + 8 * pass;
         hipError_t e;
         if (onesweep) {
-            sort_onesweep_kernel<K><<<os_tiles, OS_BLOCK, 0, s>>>(src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256,
-                                                                  status + (size_t)pass * os_tiles * 256, err);
+            if (small)
+                sort_onesweep_kernel<K, OS_SMALL_BLOCK, OS_SMALL_ITEMS><<<os_tiles, OS_SMALL_BLOCK, 0, s>>>(
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err);
+            else
+                sort_onesweep_kernel<K, OS_BLOCK, OS_ITEMS><<<os_tiles, OS_BLOCK, 0, s>>>(
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         } else {

@@ -14,8 +14,19 @@ enum : uint32_t {
     CNT_VISIBLE = 0,      // splats surviving every cull
     CNT_DEPTH_MIN = 1,    // min / max raw f32 bits of visible depths
     CNT_DEPTH_MAX = 2,
+    CNT_EMITTERS = 3,     // splats that hit at least one tile
     CNT_ISECT64 = 4,      // words 4..5: total intersections as a u64
     CNT_COUNT = 8,
+};
+
+// Rows of the projection's per-block statistics, [BS_ROWS][ceil(N/256)].
+enum : uint32_t {
+    BS_HITS = 0,          // tiles hit
+    BS_VISIBLE = 1,       // splats surviving the culls
+    BS_DMIN = 2,          // min / max raw depth bits of the visible splats
+    BS_DMAX = 3,
+    BS_EMIT = 4,          // splats with at least one hit; exclusive offsets after finalize
+    BS_ROWS = 5,
 };
 
 // Per-context device flags (read back with the projection counters).
@@ -41,19 +52,27 @@ struct ProjectArgs {
     float4* proj_b;             // [N] c11, opacity, r, g
     float* proj_c;              // [N] b
     float4* proj_aux;           // [N] z, nx, ny, nz (geometry) or null
-    uint32_t* block_stats;      // [4][ceil(N/256)]: tiles hit, visible count, min and max depth bits per block
+    uint32_t* block_stats;      // [BS_ROWS][ceil(N/256)]
+};
+
+struct CompactArgs {
+    uint32_t num_splats;
+    const uint32_t* counts;          // [N]
+    const uint32_t* depth_bits;      // [N]
+    const uint32_t* block_offsets;   // row BS_EMIT of the block stats after finalize
+    const uint32_t* counters;        // device counters (CNT_DEPTH_MIN)
+    uint32_t* keys;                  // [M] depth bits - min
+    uint32_t* vals;                  // [M] global ids
 };
 
 struct EmitArgs {
     uint32_t num_splats, tile_bw, tile_bh;
-    uint32_t depth_shift, depth_min;
-    const uint32_t* counts;
-    const uint32_t* block_offsets;   // exclusive scan of block_sums
-    const uint32_t* depth_bits;
+    const uint32_t* counts;          // [N]
+    const uint32_t* slot_base;       // [N] first slot of each splat with hits (scan in depth order)
     const float4* proj_a;
     const float4* proj_b;
-    uint64_t* keys;                  // [I]
-    uint32_t* vals;                  // [I]
+    uint32_t* tiles;                 // [I] tile id (T = sentinel)
+    uint32_t* vals;                  // [I] global id
 };
 
 struct RasterArgs {
@@ -102,13 +121,13 @@ struct ProjectBwdArgs {
 // ---- launchers (return hipError_t of the launch) -------------------------------
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
 // Reduces the projection's block stats into `counters` and turns the block
-// tile counts (first row of block_stats) into exclusive offsets in place.
+// emitter counts (row BS_EMIT) into exclusive offsets in place.
 hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, hipStream_t s);
+hipError_t launch_compact(const CompactArgs& a, hipStream_t s);
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
-hipError_t launch_tile_ranges(const uint64_t* keys, uint32_t n, uint32_t shift, uint32_t num_tiles,
-                              uint32_t* ranges, hipStream_t s);
+hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s);
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s);
@@ -116,10 +135,12 @@ hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float
                                float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
 hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float mr, uint32_t* out, hipStream_t s);
 
-// Scans.  `tmp` needs scan_tmp_words(n) u32 words.
+// Scans.  `tmp` needs scan_tmp_words(n) u32 words.  With a permutation `perm`
+// (n distinct indices) the scan runs along it: element i of the sequence is
+// in[perm[i]] and its result goes to out[perm[i]].
 size_t scan_tmp_words(uint64_t n);
 hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
-                    uint32_t* total_out, hipStream_t s);
+                    uint32_t* total_out, hipStream_t s, const uint32_t* perm = nullptr);
 hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_t* total_out, hipStream_t s);
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
