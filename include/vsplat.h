@@ -130,15 +130,23 @@ const char* vs_last_error(void);
 const char* vs_version(void);
 
 /* Per-stage HIP event timing (replaces the reference's tracing spans,
- * render.rs:520-886).  While enabled, every stage of every call is bracketed
- * by events on the context's stream; vs_ctx_stage_times() synchronises the
- * stream once and returns the milliseconds summed over all calls since the
- * previous query. */
+ * render.rs:520-886).  `stages` is a bitmask of the stages to bracket with
+ * events on the context's stream (bit i = field i of vs_stage_times, in
+ * order; VS_TIME_ALL for every stage, 0 to stop); vs_ctx_stage_times()
+ * synchronises the stream once and returns the milliseconds summed over all
+ * calls since the previous query.  Each bracket costs a few microseconds of
+ * stream time, so timing only the stage of interest keeps the rest of a
+ * render's timeline as it runs untimed. */
 typedef struct vs_stage_times {
     float project_ms, emit_ms, sort_ms, ranges_ms, raster_fwd_ms;
     float raster_bwd_ms, project_bwd_ms, other_ms;
 } vs_stage_times;
-vs_status vs_ctx_enable_timing(vs_ctx* ctx, int enable);
+enum {
+    VS_TIME_PROJECT = 1u << 0, VS_TIME_EMIT = 1u << 1, VS_TIME_SORT = 1u << 2, VS_TIME_RANGES = 1u << 3,
+    VS_TIME_RASTER_FWD = 1u << 4, VS_TIME_RASTER_BWD = 1u << 5, VS_TIME_PROJECT_BWD = 1u << 6,
+    VS_TIME_OTHER = 1u << 7, VS_TIME_ALL = 0xFFu
+};
+vs_status vs_ctx_enable_timing(vs_ctx* ctx, uint32_t stages);
 vs_status vs_ctx_stage_times(vs_ctx* ctx, vs_stage_times* out);
 
 /* ---- camera host math --------------------------------------------------------- */

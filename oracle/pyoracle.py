@@ -65,6 +65,8 @@ def load() -> C.CDLL:
     lib.or_fwd_free.argtypes = [C.c_void_p]
     lib.or_render_backward.restype = C.c_int
     lib.or_render_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F, _F]
+    lib.or_project_backward.restype = C.c_int
+    lib.or_project_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F]
     lib.or_radix_argsort_u32.argtypes = [_U, _U, C.c_uint32, C.c_uint32, C.c_uint32, _U, _U]
     lib.or_prefix_sum_u32.argtypes = [_U, _U, C.c_uint32]
     for name in ("or_expf", "or_logf"):
@@ -149,6 +151,21 @@ class OracleForward:
         if rc != 0:
             raise RuntimeError(f"oracle backward failed ({rc})")
         return {"v_combined": vc, "v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+
+    def project_backward(self, v_combined: np.ndarray, threads: int = 0):
+        """The projection VJP alone, applied to the given v_combined [N,10]."""
+        n = self.num_splats
+        k = (self.sh_degree + 1) ** 2
+        vc = np.ascontiguousarray(v_combined, np.float32)
+        assert vc.shape == (n, 10)
+        vt = np.zeros((n, 10), np.float32)
+        vs = np.zeros((n, k, 3), np.float32)
+        vo = np.zeros(n, np.float32)
+        vr = np.zeros(n, np.float32)
+        rc = load().or_project_backward(self.handle, _fp(vc), threads, _fp(vt), _fp(vs), _fp(vo), _fp(vr))
+        if rc != 0:
+            raise RuntimeError(f"oracle projection backward failed ({rc})")
+        return {"v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
 
     def __del__(self):
         try:

@@ -717,19 +717,21 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
     }
 
     // ---- tile sort: stable by tile id, render.rs:792-794 -----------------------
-    std::vector<uint32_t> perm(I);
-    std::iota(perm.begin(), perm.end(), 0u);
-    std::stable_sort(perm.begin(), perm.end(), [&](uint32_t a, uint32_t b) { return tile_of[a] < tile_of[b]; });
-    uint64_t I_valid = 0;
-    f->isect_tile.resize(I);
-    f->isect_cid.resize(I);
-    for (uint64_t i = 0; i < I; ++i) {
-        f->isect_tile[i] = tile_of[perm[i]];
-        f->isect_cid[i] = cid_of[perm[i]];
-        if (f->isect_tile[i] < sentinel) ++I_valid;
-    }
-    f->isect_tile.resize(I_valid);   // sentinels sort last and are never read
+    // A counting sort: tile ids are < T + 1, and scattering in input order
+    // into each tile's bucket keeps equal ids in emission (depth) order.
+    std::vector<uint64_t> bucket((size_t)f->T + 2, 0);
+    for (uint64_t i = 0; i < I; ++i) ++bucket[(size_t)tile_of[i] + 1];
+    for (size_t t = 1; t < bucket.size(); ++t) bucket[t] += bucket[t - 1];
+    const uint64_t I_valid = bucket[sentinel];    // sentinels sort last and are never read
+    f->isect_tile.resize(I_valid);
     f->isect_cid.resize(I_valid);
+    for (uint64_t i = 0; i < I; ++i) {
+        const uint32_t t = tile_of[i];
+        if (t >= sentinel) continue;
+        const uint64_t o = bucket[t]++;
+        f->isect_tile[o] = t;
+        f->isect_cid[o] = cid_of[i];
+    }
 
     // ---- tile offsets, get_tile_offset.rs:11-59 ---------------------------------
     f->tile_offsets.assign((size_t)f->T * 2, 0u);
@@ -869,19 +871,26 @@ extern "C" int or_fwd_get(const or_fwd* f, int field, void* dst) {
 
 extern "C" void or_fwd_free(or_fwd* f) { delete f; }
 
+static int project_vjp(const or_fwd* f, const float* vcf, int nthreads, float* v_transforms, float* v_sh,
+                       float* v_raw_opac, float* v_refine);
+
 extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threads,
                                   float* v_combined_out, float* v_transforms, float* v_sh,
                                   float* v_raw_opac, float* v_refine) {
     if (!f || !v_out || !(f->flags & OR_FLAG_BWD_INFO)) return 1;
     const int nthreads = resolve_threads(threads);
-    const or_camera& u = f->cam;
-    const uint32_t W = f->W, H = f->H, N = f->N, K = f->K, C = f->out_ch;
+    const uint32_t W = f->W, H = f->H, N = f->N, C = f->out_ch;
     const bool smooth = f->flags & OR_FLAG_SMOOTH_CUTOFF;
-    const size_t I = f->isect_tile.size();
     // Per-(tile, splat) partial sums of the raster VJP, one row per sorted
-    // intersection, summed afterwards in intersection order so the result
-    // does not depend on the thread count.
-    std::vector<double> part((size_t)I * 10, 0.0);
+    // intersection inside the shrunk tile ranges (the only ones a pixel
+    // evaluates), summed afterwards in intersection order so the result does
+    // not depend on the thread count.  row_of[tile] + (i - lo) is the row.
+    std::vector<uint64_t> row_of((size_t)f->T + 1, 0);
+    for (uint32_t t = 0; t < f->T; ++t) {
+        const uint32_t lo = f->tile_offsets_shrunk[(size_t)t * 2], hi = f->tile_offsets_shrunk[(size_t)t * 2 + 1];
+        row_of[t + 1] = row_of[t] + (hi > lo ? hi - lo : 0);
+    }
+    std::vector<double> part((size_t)row_of[f->T] * 10, 0.0);
     const float img_w = (float)W, img_h = (float)H;
 
     // ---- raster VJP, bwd/kernels/rasterize_backwards_planes.rs:112-682 ----------
@@ -919,7 +928,7 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
                     const float next_t = T * (1.0f - alpha_eff);
                     if (next_t <= 1.0e-4f) { T = 0.0f; break; }
                     const float vis = alpha_eff * T;
-                    double* p = &part[(size_t)i * 10];
+                    double* p = &part[(size_t)(row_of[tile] + (i - lo)) * 10];
                     const float clr = fmax_(cr, 0.0f), clg = fmax_(cgc, 0.0f), clb = fmax_(cbc, 0.0f);
                     if (cr >= 0.0f) p[5] += (double)vis * vr;
                     if (cgc >= 0.0f) p[6] += (double)vis * vg;
@@ -951,13 +960,28 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
     }
     // Per-splat sums in sorted-intersection order.
     std::vector<double> vc((size_t)N * 10, 0.0);
-    for (size_t i = 0; i < I; ++i) {
-        const uint32_t g = f->global_from_compact[f->isect_cid[i]];
-        for (int k = 0; k < 10; ++k) vc[(size_t)g * 10 + k] += part[i * 10 + k];
+    for (uint32_t t = 0; t < f->T; ++t) {
+        const uint32_t lo = f->tile_offsets_shrunk[(size_t)t * 2], hi = f->tile_offsets_shrunk[(size_t)t * 2 + 1];
+        for (uint32_t i = lo; i < hi; ++i) {
+            const uint32_t g = f->global_from_compact[f->isect_cid[i]];
+            const double* p = &part[(size_t)(row_of[t] + (i - lo)) * 10];
+            for (int k = 0; k < 10; ++k) vc[(size_t)g * 10 + k] += p[k];
+        }
     }
-    if (v_combined_out) for (size_t i = 0; i < (size_t)N * 10; ++i) v_combined_out[i] = (float)vc[i];
+    std::vector<float> vcf((size_t)N * 10);
+    for (size_t i = 0; i < (size_t)N * 10; ++i) vcf[i] = (float)vc[i];
+    if (v_combined_out) std::memcpy(v_combined_out, vcf.data(), sizeof(float) * vcf.size());
+    return project_vjp(f, vcf.data(), nthreads, v_transforms, v_sh, v_raw_opac, v_refine);
+}
 
-    // ---- projection VJP, bwd/kernels/project_backwards.rs:132-424 ---------------
+// ---- projection VJP, bwd/kernels/project_backwards.rs:132-424 -------------------
+// Dense per-splat gradients from the raster VJP's v_combined [N,10]; rows of
+// splats that were culled, or whose v_combined row is all zero, stay zero
+// (bwd/kernels/project_backwards.rs:311-382).
+static int project_vjp(const or_fwd* f, const float* vcf, int nthreads, float* v_transforms, float* v_sh,
+                       float* v_raw_opac, float* v_refine) {
+    const or_camera& u = f->cam;
+    const uint32_t N = f->N, K = f->K;
     if (v_transforms) std::memset(v_transforms, 0, sizeof(float) * (size_t)N * 10);
     if (v_sh) std::memset(v_sh, 0, sizeof(float) * (size_t)N * K * 3);
     if (v_raw_opac) std::memset(v_raw_opac, 0, sizeof(float) * N);
@@ -968,7 +992,7 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
         const uint32_t g = f->global_from_compact[(size_t)ci];
         float rg[10];
         bool any = false;
-        for (int k = 0; k < 10; ++k) { rg[k] = (float)vc[(size_t)g * 10 + k]; any = any || rg[k] != 0.0f; }
+        for (int k = 0; k < 10; ++k) { rg[k] = vcf[(size_t)g * 10 + k]; any = any || rg[k] != 0.0f; }
         if (!any) continue;
         const float* t = f->transforms + (size_t)g * 10;
         const float* cb = f->sh + (size_t)g * K * 3;
@@ -1027,6 +1051,12 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
         }
     }
     return 0;
+}
+
+extern "C" int or_project_backward(const or_fwd* f, const float* v_combined, int threads, float* v_transforms,
+                                   float* v_sh, float* v_raw_opac, float* v_refine) {
+    if (!f || !v_combined || !(f->flags & OR_FLAG_BWD_INFO)) return 1;
+    return project_vjp(f, v_combined, resolve_threads(threads), v_transforms, v_sh, v_raw_opac, v_refine);
 }
 
 // ---- sort & scan ---------------------------------------------------------------

@@ -85,6 +85,12 @@ int or_render_backward(const or_fwd* f, const float* v_out, int threads,
                        float* v_sh /* [N,K,3] */, float* v_raw_opac /* [N] */,
                        float* v_refine /* [N] */);
 
+/* The projection VJP alone (bwd/kernels/project_backwards.rs:132-424) applied
+ * to a given v_combined [N,10]: checks a projection backward on the exact
+ * raster gradients it was fed. */
+int or_project_backward(const or_fwd* f, const float* v_combined, int threads,
+                        float* v_transforms, float* v_sh, float* v_raw_opac, float* v_refine);
+
 /* Stable LSD radix argsort restated (splat-train-sort/src/lib.rs:40-189):
  * sorts by key bits [skip, skip + 8*ceil(bits/8)). */
 void or_radix_argsort_u32(const uint32_t* keys, const uint32_t* vals, uint32_t n,

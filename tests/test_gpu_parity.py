@@ -81,10 +81,44 @@ def _check_grads(got, want, name, rtol=1e-3, atol=1e-5, group_rtol=1e-3):
     want = np.asarray(want, np.float64)
     err = np.abs(got - want)
     bad = err > atol + rtol * np.abs(want)
-    assert not bad.any(), f"{name}: {bad.sum()} entries exceed 1e-3 rel / 1e-5 abs (max err {err.max():.3e})"
+    assert not bad.any(), f"{name}: {bad.sum()} entries exceed {rtol:g} rel / {atol:g} abs (max err {err.max():.3e})"
+    if group_rtol is None:
+        return
     scale = np.abs(want).max(axis=0, keepdims=True) if want.ndim > 1 else np.abs(want).max()
     tight = err > rtol * np.abs(want) + group_rtol * scale
-    assert not tight.any(), f"{name}: {tight.sum()} entries exceed 1e-3 of the group maximum (max err {err.max():.3e})"
+    assert not tight.any(), f"{name}: {tight.sum()} entries exceed {group_rtol:g} of the group maximum (max err {err.max():.3e})"
+
+
+def _check_param_grads(g, rg, ref, vc):
+    """Dense parameter gradients, end to end and per stage.
+
+    End to end (GPU raster + projection VJPs vs the oracle's) at the contract
+    bar, 1e-3 relative / 1e-5 absolute.  The projection VJP can amplify the
+    ~1e-6 relative atomic-order differences of v_combined by orders of
+    magnitude where its terms cancel (a splat with |v_conic| ~ 1 and
+    |v_quat| ~ 1e-6), so the projection stage is also checked on its own: the
+    oracle's projection VJP applied to the GPU's own v_combined must agree to
+    1e-5 relative / 1e-3 of the group maximum."""
+    vt = g.v_transforms.cpu().numpy()
+    vs = g.v_coeffs.cpu().numpy().reshape(len(vt), -1)
+    vo = g.v_raw_opac.cpu().numpy()
+    vr = g.v_refine_weight.cpu().numpy()
+    assert np.isfinite(vt).all() and np.isfinite(vs).all()
+    for got, want, name in ((vt[:, 0:3], rg["v_transforms"][:, 0:3], "v_means"),
+                            (vt[:, 3:7], rg["v_transforms"][:, 3:7], "v_quats"),
+                            (vt[:, 7:10], rg["v_transforms"][:, 7:10], "v_log_scales"),
+                            (vo, rg["v_raw_opac"], "v_raw_opacity"),
+                            (vs, rg["v_sh"].reshape(len(vt), -1), "v_sh"),
+                            (vr, rg["v_refine"], "v_refine_weight")):
+        _check_grads(got, want, name, group_rtol=None)
+    pg = ref.project_backward(vc)
+    for got, want, name in ((vt[:, 0:3], pg["v_transforms"][:, 0:3], "v_means (projection stage)"),
+                            (vt[:, 3:7], pg["v_transforms"][:, 3:7], "v_quats (projection stage)"),
+                            (vt[:, 7:10], pg["v_transforms"][:, 7:10], "v_log_scales (projection stage)"),
+                            (vo, pg["v_raw_opac"], "v_raw_opacity (projection stage)"),
+                            (vs, pg["v_sh"].reshape(len(vt), -1), "v_sh (projection stage)"),
+                            (vr, pg["v_refine"], "v_refine_weight (projection stage)")):
+        _check_grads(got, want, name, rtol=1e-5, atol=0.0, group_rtol=1e-3)
 
 
 @pytest.mark.parametrize("cfg,n,view", [("c1", None, 0), ("c2", 20_000, 0), ("c3", 20_000, 5), ("c5", 20_000, 0)])
@@ -101,14 +135,7 @@ def test_backward_parity(cfg, n, view):
     _check_grads(vc[:, 5:8], rg["v_combined"][:, 5:8], "v_rgb")
     _check_grads(vc[:, 8], rg["v_combined"][:, 8], "v_opacity")
     _check_grads(vc[:, 9], rg["v_combined"][:, 9], "v_refine")
-    vt = g.v_transforms.cpu().numpy()
-    _check_grads(vt[:, 0:3], rg["v_transforms"][:, 0:3], "v_means")
-    _check_grads(vt[:, 3:7], rg["v_transforms"][:, 3:7], "v_quats")
-    _check_grads(vt[:, 7:10], rg["v_transforms"][:, 7:10], "v_log_scales")
-    _check_grads(g.v_raw_opac.cpu().numpy(), rg["v_raw_opac"], "v_raw_opacity")
-    _check_grads(g.v_coeffs.cpu().numpy().reshape(len(vt), -1), rg["v_sh"].reshape(len(vt), -1), "v_sh")
-    _check_grads(g.v_refine_weight.cpu().numpy(), rg["v_refine"], "v_refine_weight")
-    assert np.isfinite(vt).all()
+    _check_param_grads(g, rg, ref, vc)
 
 
 def test_geometry_pass_parity():

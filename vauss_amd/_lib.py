@@ -21,6 +21,9 @@ STATUS_NAMES = ["VS_OK", "VS_ERR_INVALID", "VS_ERR_HIP", "VS_ERR_OOM", "VS_ERR_U
 CAMERA_PINHOLE, CAMERA_KB4 = 0, 1
 PASS_FORWARD, PASS_BACKWARD, PASS_FLOAT, PASS_BACKWARD_SMOOTH_CUTOFF, PASS_GEOMETRY = range(5)
 MODE_DEFAULT, MODE_MIP, MODE_SURFEL = range(3)
+# stage bits of vs_ctx_enable_timing, in vs_stage_times field order
+TIME_STAGES = ("project", "emit", "sort", "ranges", "raster_fwd", "raster_bwd", "project_bwd", "other")
+TIME_ALL = (1 << len(TIME_STAGES)) - 1
 
 
 class VsCamera(C.Structure):
@@ -72,7 +75,7 @@ SIGNATURES = {
     "vs_ctx_set_stream": (C.c_int, [C.c_void_p, C.c_void_p]),
     "vs_last_error": (C.c_char_p, []),
     "vs_version": (C.c_char_p, []),
-    "vs_ctx_enable_timing": (C.c_int, [C.c_void_p, C.c_int]),
+    "vs_ctx_enable_timing": (C.c_int, [C.c_void_p, C.c_uint32]),
     "vs_ctx_stage_times": (C.c_int, [C.c_void_p, C.POINTER(VsStageTimes)]),
     "vs_fov_to_focal": (C.c_double, [C.c_double, C.c_uint32, C.c_int32, C.POINTER(C.c_float)]),
     "vs_focal_to_fov": (C.c_double, [C.c_double, C.c_uint32, C.c_int32, C.POINTER(C.c_float)]),

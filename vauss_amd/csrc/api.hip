@@ -47,7 +47,7 @@ struct vs_ctx {
     hipStream_t stream = nullptr;
     uint32_t* host_counters = nullptr;    // pinned readback of the projection counters (+ CTX_FLAGS words)
     uint32_t* dev_flags = nullptr;        // device: [0] set when a sort look-back gave up waiting
-    bool timing = false;
+    uint32_t timing = 0;                  // bitmask of timed stages (VS_TIME_*)
     // Stage event pairs recorded since the last vs_ctx_stage_times(); the
     // pool is reused, so timing many renders needs no extra synchronisation.
     struct Rec { int stage; hipEvent_t b, e; };
@@ -96,10 +96,10 @@ struct StageTimer {
     Stage s;
     hipEvent_t b = nullptr;
     StageTimer(vs_ctx* ctx, Stage st) : c(ctx), s(st) {
-        if (c->timing) { b = c->take(); hipEventRecord(b, c->stream); }
+        if (c->timing & (1u << s)) { b = c->take(); hipEventRecord(b, c->stream); }
     }
     ~StageTimer() {
-        if (c->timing) {
+        if (b) {
             hipEvent_t e = c->take();
             hipEventRecord(e, c->stream);
             c->recs.push_back(vs_ctx::Rec{(int)s, b, e});
@@ -169,9 +169,10 @@ extern "C" vs_status vs_ctx_set_stream(vs_ctx* c, void* hip_stream) {
     return VS_OK;
 }
 
-extern "C" vs_status vs_ctx_enable_timing(vs_ctx* c, int enable) {
+extern "C" vs_status vs_ctx_enable_timing(vs_ctx* c, uint32_t stages) {
     if (!c) return fail(VS_ERR_INVALID, "ctx is null");
-    c->timing = enable != 0;
+    if (stages & ~(uint32_t)VS_TIME_ALL) return fail(VS_ERR_INVALID, "unknown stage bit in the timing mask");
+    c->timing = stages;
     return VS_OK;
 }
 

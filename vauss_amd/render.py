@@ -84,8 +84,14 @@ class Context:
         _lib.check(ctx.lib.vs_ctx_set_stream(ctx.handle, C.c_void_p(stream)))
         return ctx
 
-    def enable_timing(self, on: bool = True) -> None:
-        _lib.check(self.lib.vs_ctx_enable_timing(self.handle, 1 if on else 0))
+    def enable_timing(self, on: bool = True, stages: Optional[Sequence[str]] = None) -> None:
+        """Bracket the named stages (all when `stages` is None) with HIP events."""
+        mask = 0
+        if on:
+            names = _lib.TIME_STAGES if stages is None else stages
+            for name in names:
+                mask |= 1 << _lib.TIME_STAGES.index(name)
+        _lib.check(self.lib.vs_ctx_enable_timing(self.handle, mask))
 
     def stage_times(self) -> dict:
         t = _lib.VsStageTimes()

@@ -52,7 +52,8 @@ class SplitMix64:
 
     def normal(self, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
         m = (n + 1) // 2
-        u1 = 1.0 - self.unit(m).astype(np.float64)     # (0, 1]
+        # u1 in (0, 1] from the top 53 bits, so log(u1) is always finite
+        u1 = ((self.next_u64(m) >> np.uint64(11)).astype(np.float64) + 1.0) * 2.0 ** -53
         u2 = self.unit(m).astype(np.float64)
         r = np.sqrt(-2.0 * np.log(u1))
         z = np.concatenate([r * np.cos(2 * np.pi * u2), r * np.sin(2 * np.pi * u2)])[:n]
