@@ -53,6 +53,21 @@ def algorithmic_bytes(stage: str, n: int, v: int, i: int, t: int, p: int, k: int
     return 0
 
 
+def list_length_histogram(ranges) -> dict:
+    """Per-tile list lengths from tile ranges [.., 2] (before the forward
+    shrinks their ends) as a power-of-two histogram."""
+    import numpy as np
+    import torch
+    r = ranges.to(torch.int64).reshape(-1, 2)
+    lens = (r[:, 1] - r[:, 0]).clamp_min(0).cpu().numpy()
+    top = max(int(lens.max()), 1)
+    edges = [0, 1] + [1 << e for e in range(1, 32) if (1 << (e - 1)) <= top]
+    counts, _ = np.histogram(lens, bins=edges + [edges[-1] * 2])
+    return {"tiles": int(lens.size), "mean": round(float(lens.mean()), 1), "max": int(lens.max()),
+            "p50": int(np.percentile(lens, 50)), "p99": int(np.percentile(lens, 99)),
+            "hist_lower_edges": edges, "hist_counts": [int(c) for c in counts]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,11 +113,16 @@ def main() -> int:
     T = ((w + 15) // 16) * ((h + 15) // 16)
     P = w * h
 
-    def step(view: int):
+    tile_lists = None
+
+    def step(view: int, list_histogram: bool = False):
+        nonlocal tile_lists
         out = va.render(cams[view], wl.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
         v = va.l1_cotangent(out.out_img, gt, mc, mr)
         g = va.render_backward(out, t, s, o, v)
         aux = (out.aux.num_visible, out.aux.num_intersections)
+        if list_histogram:
+            tile_lists = list_length_histogram(out.state.tile_ranges(dev))
         out.state.free()
         return g, aux
 
@@ -119,7 +139,7 @@ def main() -> int:
     counts = []
     nb = len(cams)
     for i in range(nb):
-        _, aux = step(i % len(cams))
+        _, aux = step(i % len(cams), list_histogram=(i == 0))
         counts.append(aux)
     stages = ctx.stage_times()
     per_launch = {name: ms / nb for name, ms in stages.items()}
@@ -166,7 +186,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(wl, cams[0])
+        cpu = cpu_baseline(wl, cams)
 
     line = {
         "metric": METRIC,
@@ -189,6 +209,7 @@ def main() -> int:
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "tile_lists": tile_lists,
     }
     print(json.dumps(line))
     return 0
@@ -202,7 +223,8 @@ KERNEL_SOURCES = [os.path.join(ROOT, "vauss_amd", "csrc", f) for f in
 # rocprofv3 kernel names -> bench stage names
 STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "raster_fwd"),
                    ("project_bwd_kernel", "project_bwd"), ("project_kernel", "project"), ("emit_kernel", "emit"),
-                   ("finalize_counts", "project"), ("sort_", "sort"), ("scan_", "sort"), ("tile_ranges", "ranges"),
+                   ("finalize_counts", "project"), ("compact_kernel", "emit"), ("scan_", "emit"), ("sort_", "sort"),
+                   ("tile_ranges", "ranges"),
                    ("l1_cotangent", "loss"), ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
 
 
@@ -302,8 +324,8 @@ def summarize(args) -> int:
                 if stage in ("copy", "torch", "fill"):
                     continue
                 e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "kernels": []})
-                # a stage that launches a kernel several times per step (sort passes) adds them up
-                reps = n / nbwd if stage == "sort" else 1.0
+                # per step: a kernel launched several times a step (sort passes) adds up
+                reps = n / nbwd
                 e["fetch_bytes"] += mean["FETCH_SIZE"] * 1024.0 * f_scale * reps
                 e["write_bytes"] += mean["WRITE_SIZE"] * 1024.0 * w_scale * reps
                 e["kernels"].append(k)
@@ -321,28 +343,39 @@ def summarize(args) -> int:
     return 0
 
 
-def cpu_baseline(wl, cam):
-    """The oracle (CPU restatement of the reference path) on one view, all host threads."""
+def cpu_baseline(wl, cams, min_seconds: float = 10.0):
+    """The oracle (CPU restatement of the reference path) on all host threads:
+    full training renders (forward + L1 cotangent + backward) of consecutive
+    views until at least `min_seconds` of CPU work or every view is done."""
     import numpy as np
     from oracle import pyoracle as po
     from vauss_amd import scenes
     sc = wl.scene
     threads = po.max_threads()
-    t0 = time.perf_counter()
-    f = po.render_forward(cam, wl.img_size, sc.transforms, sc.sh_coeffs, sc.raw_opacities, flags=po.FLAG_BWD_INFO,
-                          threads=threads)
-    img = f.get(po.F_OUT_IMG)
-    v = np.zeros_like(img)
-    hh, ww = img.shape[:2]
-    v[..., :3] = np.sign(img[..., :3] - scenes.loss_target(wl.img_size)) / np.float32(3 * hh * ww)
-    t1 = time.perf_counter()
-    f.backward(v, threads=threads)
-    t2 = time.perf_counter()
-    ms = (t2 - t0) * 1000.0
+    gt = scenes.loss_target(wl.img_size)
+    fwd_ms, bwd_ms = [], []
+    t_start = time.perf_counter()
+    for cam in cams:
+        t0 = time.perf_counter()
+        f = po.render_forward(cam, wl.img_size, sc.transforms, sc.sh_coeffs, sc.raw_opacities, flags=po.FLAG_BWD_INFO,
+                              threads=threads)
+        img = f.get(po.F_OUT_IMG)
+        v = np.zeros_like(img)
+        hh, ww = img.shape[:2]
+        v[..., :3] = np.sign(img[..., :3] - gt) / np.float32(3 * hh * ww)
+        t1 = time.perf_counter()
+        f.backward(v, threads=threads)
+        t2 = time.perf_counter()
+        fwd_ms.append(1000 * (t1 - t0))
+        bwd_ms.append(1000 * (t2 - t1))
+        if t2 - t_start >= min_seconds:
+            break
+    k = len(fwd_ms)
+    ms = (sum(fwd_ms) + sum(bwd_ms)) / k
     return {"value": round(ms, 1), "unit": "ms/view", "cores": threads, "kind": "port",
-            "sample": f"one full view (view 0) of {wl.name}: fwd {1000 * (t1 - t0):.0f} ms + bwd {1000 * (t2 - t1):.0f} ms, "
-                      f"OpenMP over {threads} threads",
-            "evaluations": int(f.info.num_evaluations)}
+            "sample": f"{k} full view(s) of {wl.name} (views 0..{k - 1}), mean fwd {sum(fwd_ms) / k:.0f} ms + "
+                      f"bwd {sum(bwd_ms) / k:.0f} ms per view, OpenMP over {threads} threads, "
+                      f"{(time.perf_counter() - t_start):.1f} s in total"}
 
 
 if __name__ == "__main__":

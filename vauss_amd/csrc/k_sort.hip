@@ -441,7 +441,10 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
     if (onesweep) {
         hipError_t e = launch_fill_u32(ghist, 0u, (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
         if (e != hipSuccess) return e;
-        const uint32_t hist_blocks = (uint32_t)min((uint64_t)HIST_BLOCKS, ((uint64_t)n + SORT_BLOCK * HIST_ITEMS - 1) / (SORT_BLOCK * HIST_ITEMS));
+        // ~4k keys per block up to HIST_BLOCKS blocks: each block ends with
+        // passes x 256 global atomics, so a grid much wider than the data
+        // only adds atomics (16k keys per block starves short inputs).
+        const uint32_t hist_blocks = (uint32_t)max((uint64_t)1, min((uint64_t)HIST_BLOCKS, ((uint64_t)n + 4095) / 4096));
         sort_histogram_kernel<K><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
         e = hipGetLastError();
         if (e != hipSuccess) return e;

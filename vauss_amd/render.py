@@ -126,6 +126,16 @@ class ForwardState:
         _lib.check(self.ctx.lib.vs_fwd_state_view(self.handle, C.byref(v)))
         return v
 
+    def tile_ranges(self, device: torch.device) -> torch.Tensor:
+        """A copy of the tile ranges before the forward shrank their ends, [ty, tx, 2] (u32 bits in int32)."""
+        v = self.view()
+
+        class _Dev:   # a borrowed device array, copied at once
+            __cuda_array_interface__ = {"shape": (v.tile_bh, v.tile_bw, 2), "typestr": "<i4",
+                                        "data": (v.tile_ranges, False), "version": 2, "strides": None}
+        with torch.cuda.device(device):
+            return torch.as_tensor(_Dev(), device=device).clone()
+
     def free(self) -> None:
         if self.handle:
             self.ctx.lib.vs_fwd_state_free(self.handle)
