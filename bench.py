@@ -24,6 +24,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
 FP32_VALU_PEAK_TFLOPS = 157.3    # MI355X vector fp32 (packed) peak
+VALU_ISSUE_PEAK_G = 256 * 4 * 2.4 / 4   # G wave64 VALU instructions/s without packed fp32 (614.4)
 
 METRIC = "fwd+bwd raster ms/view, 1M Gaussians SH3 1080p; achieved HBM GB/s vs peak"
 
@@ -170,10 +171,20 @@ def main() -> int:
     dom_bytes = algorithmic_bytes(dom, n, int(V), int(I), T, P, k)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic, traffic_note = measured_traffic(args.workload, dom.replace("_ms", ""))
+    valu = measured_valu_insts(args.workload, dom.replace("_ms", ""))
     roofline = {"bound": "hbm", "kernel": dom.replace("_ms", ""), "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "traffic_source": traffic_note, "alg_bytes_per_launch": dom_bytes,
                 "ms_per_launch": round(dom_ms, 4)}
+    # The raster kernels are bound by VALU instruction issue, not HBM: their
+    # wave instructions per launch (counter summary) over the live launch
+    # time, against MI355X's issue ceiling without packed FP32 (256 CUs x 4
+    # SIMDs x 2.4 GHz / 4 cycles per wave64 instruction).
+    if valu:
+        rate = valu / (dom_ms * 1e-3) / 1e9
+        roofline["valu_issue"] = {"achieved": round(rate, 1), "peak": VALU_ISSUE_PEAK_G, "unit": "G wave-instr/s",
+                                  "frac": round(rate / VALU_ISSUE_PEAK_G, 4), "insts_per_launch": int(valu),
+                                  "source": traffic_note}
 
     if args.copy_calib:
         src = torch.empty(args.copy_calib * (1 << 20) // 4, dtype=torch.float32, device=dev).fill_(1.0)
@@ -260,6 +271,19 @@ def measured_traffic(workload: str, kernel: str):
     return int(k["fetch_bytes"] + k["write_bytes"]), os.path.relpath(path, ROOT)
 
 
+def measured_valu_insts(workload: str, kernel: str):
+    """Wave-level VALU instructions per launch of `kernel` (SQ_INSTS_VALU)
+    from the committed counter summary, when measured on these sources."""
+    path = os.path.join(PROFILES, f"hbm_traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        data = json.load(fh)
+    if data.get("source_digest") != source_digest():
+        return None
+    return data["kernels"].get(kernel, {}).get("valu_insts")
+
+
 def _short_kernel(name: str) -> str:
     base = name.split("(")[0].replace("void ", "")
     return base.replace("vs::", "")
@@ -323,11 +347,13 @@ def summarize(args) -> int:
                 stage = next((st for pat, st in STAGE_OF_KERNEL if pat in k), k)
                 if stage in ("copy", "torch", "fill"):
                     continue
-                e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "kernels": []})
+                e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "valu_insts": 0.0,
+                                                          "kernels": []})
                 # per step: a kernel launched several times a step (sort passes) adds up
                 reps = n / nbwd
                 e["fetch_bytes"] += mean["FETCH_SIZE"] * 1024.0 * f_scale * reps
                 e["write_bytes"] += mean["WRITE_SIZE"] * 1024.0 * w_scale * reps
+                e["valu_insts"] += mean.get("SQ_INSTS_VALU", 0.0) * reps
                 e["kernels"].append(k)
     text = "\n".join(lines) + "\n"
     if args.command:
