@@ -228,8 +228,9 @@ def main() -> int:
 
 PROFILES = os.path.join(ROOT, "profiles")
 KERNEL_SOURCES = [os.path.join(ROOT, "vauss_amd", "csrc", f) for f in
-                  ("k_project.hip", "k_project_bwd.hip", "k_raster.hip", "k_scan.hip", "k_sort.hip", "api.hip",
-                   "vs_device.h", "vs_camera.h", "vs_sh.h", "vs_internal.h")]
+                  ("k_project.hip", "k_project_bwd.hip", "k_project_update.hip", "k_raster.hip", "k_scan.hip",
+                   "k_sort.hip", "api.hip", "vs_device.h", "vs_camera.h", "vs_sh.h", "vs_vjp.h", "vs_adam.h",
+                   "vs_internal.h")]
 
 # rocprofv3 kernel names -> bench stage names
 STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "raster_fwd"),

@@ -173,7 +173,10 @@ vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* 
 /* SplatBwdOps::rasterize_bwd + project_bwd (bwd/burn_glue.rs:70-111;
  * bwd/render_bwd.rs:27-155 and 295-447).  `out_img` is the image the
  * forward wrote (f32, C channels), `v_out` its cotangent [H,W,C].  The
- * splat parameters must be the ones the forward saw. */
+ * splat parameters must be the ones the forward saw.  When every dense
+ * output of `grads` is NULL the call stops at the raster gradients
+ * (grads->v_combined), as the reference's BackwardFusedUpdate pass does
+ * (gaussian_splats.rs:95); vs_project_update then consumes them. */
 vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* state, const vs_splats* splats,
                              const float* out_img, const float* v_out, vs_grads* grads);
 
@@ -188,6 +191,9 @@ typedef struct vs_state_view {
     const uint32_t* isect_gids;     /* [I] sorted global splat ids */
     const uint32_t* intersect_counts; /* [N] */
     const uint32_t* depth_bits;     /* [N] raw f32 bits of view z (the depth key) */
+    const uint32_t* compact_from_global; /* [N] g + 1 for splats past every cull, 0 if culled
+                                       (RenderOutput state, render_aux.rs:36-41: the rows of
+                                       vs_project_update's color_dir) */
     const float* proj_xy_conic;     /* [N,4] x, y, c00, c01 (valid for visible splats) */
     const float* proj_c11_opac_rg;  /* [N,4] c11, opacity, r, g */
     const float* proj_b;            /* [N] b */
@@ -195,6 +201,52 @@ typedef struct vs_state_view {
     const uint32_t* tile_ranges;    /* [T,2] before the forward shrank the ends */
 } vs_state_view;
 vs_status vs_fwd_state_view(const vs_fwd_state* state, vs_state_view* out);
+
+/* ---- fused projection backward + Adam ------------------------------------------- */
+
+/* FusedAdam (bwd/project_update.rs:232-250): the Adam step shared by the
+ * transforms and raw opacities. */
+typedef struct vs_adam_step {
+    float beta1, beta2;             /* moment decays */
+    float inv1, inv2;               /* 1 / (1 - beta1^t), 1 / (1 - beta2^t) */
+    float epsilon;                  /* Adam epsilon, also the moment codec's scale */
+    float lr_opac;                  /* raw-opacity learning rate */
+    float opac_reg;                 /* opacity regulariser gradient weight (w / N), 0 = off */
+    uint32_t round_seed;            /* stochastic-rounding stream (the step count) */
+} vs_adam_step;
+
+/* ProjectUpdateOut minus the stepped tensors (bwd/project_update.rs:25-40).
+ * NULL skips an output. */
+typedef struct vs_update_out {
+    float* color_dir;               /* [N+1,6]: row compact_from_global[g] = colour gradient, view
+                                       direction; row 0, rows without gradient and the rows g + 1
+                                       of culled splats zero */
+    float* v_refine_weight;         /* [N] clamped to [0,1e32], 0 for culled splats */
+    float* coeffs_grad_sq;          /* [N] mean square of the SH gradient row, from its DC entries */
+} vs_update_out;
+
+/* ProjectUpdateOps::project_update (bwd/project_update.rs:80-220; kernel
+ * bwd/kernels/project_update.rs:40-178): the projection VJP of a backward
+ * pass's raster gradients `v_combined` [N,10] fused with one Adam step of
+ * `transforms` [N,10] and `raw_opacities` [N], both updated in place, whose
+ * moments are packed one u32 per value in `w_t` [N,10] and `w_o` [N]
+ * (geo_moments.rs codec; zero words are reset moments).  `lr_scale` is the
+ * per-column transforms learning rate [10] (device).  The parameters must be
+ * the pre-step values the forward of `state` saw.  Every splat steps: culled
+ * ones decay their moments with a zero gradient plus the opacity regulariser. */
+vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* state, float* transforms, const float* sh_coeffs,
+                            float* raw_opacities, const float* v_combined, uint32_t* w_t,
+                            const float* lr_scale, uint32_t* w_o, const vs_adam_step* adam,
+                            vs_update_out* out);
+
+/* GeoMomentOps (bwd/geo_moments.rs:25-60, kernels geo_moments.rs:104-137):
+ * pack f32 (m, v) pairs into words rounding to nearest, unpack words, and
+ * zero `row_width` words of each listed row (a reset moment; rows past
+ * num_words are ignored). */
+vs_status vs_geo_encode(vs_ctx* ctx, const float* m, const float* v, uint32_t n, float epsilon, uint32_t* words);
+vs_status vs_geo_decode(vs_ctx* ctx, const uint32_t* words, uint32_t n, float epsilon, float* m, float* v);
+vs_status vs_geo_zero_rows(vs_ctx* ctx, uint32_t* words, uint64_t num_words, const uint32_t* rows,
+                           uint32_t num_rows, uint32_t row_width);
 
 /* ---- sort / scan ---------------------------------------------------------------- */
 

@@ -33,6 +33,12 @@ class OrCamera(C.Structure):
                 ("lim_neg_x", C.c_float), ("lim_neg_y", C.c_float), ("lim_r", C.c_float)]
 
 
+class OrAdam(C.Structure):
+    """Same layout as vs_adam_step (include/vsplat.h)."""
+    _fields_ = [("beta1", C.c_float), ("beta2", C.c_float), ("inv1", C.c_float), ("inv2", C.c_float),
+                ("epsilon", C.c_float), ("lr_opac", C.c_float), ("opac_reg", C.c_float), ("round_seed", C.c_uint32)]
+
+
 class OrFwdInfo(C.Structure):
     _fields_ = [("num_splats", C.c_uint32), ("num_visible", C.c_uint32), ("num_intersections", C.c_uint32),
                 ("num_tiles", C.c_uint32), ("tile_bw", C.c_uint32), ("tile_bh", C.c_uint32),
@@ -67,6 +73,17 @@ def load() -> C.CDLL:
     lib.or_render_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F, _F]
     lib.or_project_backward.restype = C.c_int
     lib.or_project_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F]
+    lib.or_project_update.restype = C.c_int
+    lib.or_project_update.argtypes = [C.c_void_p, _F, _F, _F, _U, _F, _U, C.POINTER(OrAdam), _F, _F, _F, C.c_int]
+    lib.or_geo_encode.restype = C.c_uint32
+    lib.or_geo_encode.argtypes = [C.c_float, C.c_float, C.c_float]
+    lib.or_geo_decode.argtypes = [C.c_uint32, C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]
+    lib.or_geo_pack.restype = C.c_uint32
+    lib.or_geo_pack.argtypes = [C.c_float, C.c_float, C.c_float, C.c_float, C.c_float]
+    lib.or_mix_hash.restype = C.c_uint32
+    lib.or_mix_hash.argtypes = [C.c_uint32, C.c_uint32]
+    lib.or_adam_packed.argtypes = [C.POINTER(C.c_float), C.POINTER(C.c_uint32), C.c_uint32, C.c_float, C.c_float,
+                                   C.POINTER(OrAdam), C.c_uint32]
     lib.or_radix_argsort_u32.argtypes = [_U, _U, C.c_uint32, C.c_uint32, C.c_uint32, _U, _U]
     lib.or_prefix_sum_u32.argtypes = [_U, _U, C.c_uint32]
     for name in ("or_expf", "or_logf"):
@@ -151,6 +168,25 @@ class OracleForward:
         if rc != 0:
             raise RuntimeError(f"oracle backward failed ({rc})")
         return {"v_combined": vc, "v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+
+    def project_update(self, v_combined, transforms, raw_opac, w_t, lr_scale, w_o, adam: "OrAdam", threads: int = 0):
+        """project_update on copies of the host arrays; returns the stepped
+        parameters and moments plus color_dir [N+1,6], v_refine, grad_sq."""
+        n = self.num_splats
+        vc = np.ascontiguousarray(v_combined, np.float32)
+        t = np.array(transforms, np.float32, copy=True)
+        o = np.array(raw_opac, np.float32, copy=True)
+        wt = np.array(w_t, np.uint32, copy=True)
+        wo = np.array(w_o, np.uint32, copy=True)
+        lr = np.ascontiguousarray(lr_scale, np.float32)
+        cd = np.zeros((n + 1, 6), np.float32)
+        vr = np.zeros(n, np.float32)
+        gs = np.zeros(n, np.float32)
+        rc = load().or_project_update(self.handle, _fp(vc), _fp(t), _fp(o), _up(wt), _fp(lr), _up(wo), C.byref(adam),
+                                      _fp(cd), _fp(vr), _fp(gs), threads)
+        if rc != 0:
+            raise RuntimeError(f"oracle project_update failed ({rc})")
+        return {"transforms": t, "raw_opac": o, "w_t": wt, "w_o": wo, "color_dir": cd, "v_refine": vr, "grad_sq": gs}
 
     def project_backward(self, v_combined: np.ndarray, threads: int = 0):
         """The projection VJP alone, applied to the given v_combined [N,10]."""
@@ -272,3 +308,27 @@ def kb4_invert_d(target, k):
 
 def max_threads() -> int:
     return load().or_max_threads()
+
+
+def geo_encode(m: float, v: float, epsilon: float) -> int:
+    return int(load().or_geo_encode(m, v, epsilon))
+
+
+def geo_pack(m: float, v: float, epsilon: float, round_l: float, round_u: float) -> int:
+    return int(load().or_geo_pack(m, v, epsilon, round_l, round_u))
+
+
+def geo_decode(word: int, epsilon: float):
+    m, v = C.c_float(), C.c_float()
+    load().or_geo_decode(word & 0xFFFFFFFF, epsilon, C.byref(m), C.byref(v))
+    return m.value, v.value
+
+
+def mix_hash(index: int, step: int) -> int:
+    return int(load().or_mix_hash(index & 0xFFFFFFFF, step & 0xFFFFFFFF))
+
+
+def adam_packed(param: float, word: int, index: int, g: float, lr: float, adam: OrAdam, seed: int):
+    p, w = C.c_float(param), C.c_uint32(word & 0xFFFFFFFF)
+    load().or_adam_packed(C.byref(p), C.byref(w), index & 0xFFFFFFFF, g, lr, C.byref(adam), seed & 0xFFFFFFFF)
+    return p.value, w.value

@@ -975,12 +975,62 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
 }
 
 // ---- projection VJP, bwd/kernels/project_backwards.rs:132-424 -------------------
+struct SplatVjp { V3 v_mean; Q4 v_q; V3 v_log; float v_raw; V3 vdir; };
+
+// splat_vjp (project_backwards.rs:132-274) of global splat g with parameters
+// row t [10] and raw opacity `raw` on its raster gradients rg [10].
+static SplatVjp splat_vjp(const or_fwd* f, uint32_t g, const float* t, float raw, const float rg[10]) {
+    const or_camera& u = f->cam;
+    const uint32_t K = f->K, degree = f->degree;
+    const float* cb = f->sh + (size_t)g * K * 3;
+    const V3 mean = v3(t[0], t[1], t[2]);
+    const V3 sc = v3(expf_c(t[7] + f->lso), expf_c(t[8] + f->lso), expf_c(t[9] + f->lso));
+    const Q4 qu{t[3], t[4], t[5], t[6]};
+    const Q4 q = qnormalize(qu);
+    const float opac_sig = sigmoid(raw);
+    // SH + view-direction VJP
+    const V3 u_world = sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
+    const float u_len = length(u_world);
+    const V3 vdir = scale(u_world, 1.0f / u_len);
+    const V3 v_color = v3(rg[5], rg[6], rg[7]);
+    const V3 v_v_sh = sh_viewdir_vjp(cb, degree, vdir, v_color);
+    const float v_dot = dot(vdir, v_v_sh);
+    const V3 v_mean_sh = scale(sub(v_v_sh, scale(vdir, v_dot)), 1.0f / u_len);
+    const V3 mean_c = world_to_cam(mean, u);
+    const M3 R = quat_to_mat3(q);
+    const M3 Mm = mul_diag(R, sc);
+    const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
+    const float v_opac_base = 1.0f * rg[8];
+    const S2 conic_inv = s2_inverse(cov);
+    const S2 v_inv{rg[2], rg[3] * 0.5f, rg[4]};
+    const S2 v_cov2d = inverse2x2_vjp(conic_inv, v_inv);
+    const S3 covar = outer_self(Mm);
+    const M3 vrot = view_rot(u);
+    const S3 cov_c = s3_congruence(covar, vrot);
+    const M23 J = project_jacobian(mean_c, u);
+    const V3 v_mean_c = (u.model == OR_MODEL_KB4) ? projection_vjp_kb4(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]})
+                                                    : projection_vjp_pinhole(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]});
+    const S3 vcc = m23_tcongruence_s2(J, v_cov2d);
+    SplatVjp r;
+    r.v_mean = add(tmul_vec3(vrot, v_mean_c), v_mean_sh);
+    const M3 v_m = s3_mul_mat3(s3_scale(s3_tcongruence(vcc, vrot), 2.0f), Mm);
+    const V3 v_log{dot(R.c0, v_m.c0) * sc.x, dot(R.c1, v_m.c1) * sc.y, dot(R.c2, v_m.c2) * sc.z};
+    // ratio_sq = 1 and floor.opac * (1 - 1) = 0 without a scale floor.
+    r.v_log = V3{v_log.x * 1.0f + v_opac_base * opac_sig * 0.0f,
+                 v_log.y * 1.0f + v_opac_base * opac_sig * 0.0f,
+                 v_log.z * 1.0f + v_opac_base * opac_sig * 0.0f};
+    const Q4 q_grad = quat_to_mat_vjp(q, mul_diag(v_m, sc));
+    r.v_q = apply_normalize_vjp(qu, q_grad);
+    r.v_raw = v_opac_base * 1.0f * opac_sig * (1.0f - opac_sig);
+    r.vdir = vdir;
+    return r;
+}
+
 // Dense per-splat gradients from the raster VJP's v_combined [N,10]; rows of
 // splats that were culled, or whose v_combined row is all zero, stay zero
 // (bwd/kernels/project_backwards.rs:311-382).
 static int project_vjp(const or_fwd* f, const float* vcf, int nthreads, float* v_transforms, float* v_sh,
                        float* v_raw_opac, float* v_refine) {
-    const or_camera& u = f->cam;
     const uint32_t N = f->N, K = f->K;
     if (v_transforms) std::memset(v_transforms, 0, sizeof(float) * (size_t)N * 10);
     if (v_sh) std::memset(v_sh, 0, sizeof(float) * (size_t)N * K * 3);
@@ -994,61 +1044,131 @@ static int project_vjp(const or_fwd* f, const float* vcf, int nthreads, float* v
         bool any = false;
         for (int k = 0; k < 10; ++k) { rg[k] = vcf[(size_t)g * 10 + k]; any = any || rg[k] != 0.0f; }
         if (!any) continue;
-        const float* t = f->transforms + (size_t)g * 10;
-        const float* cb = f->sh + (size_t)g * K * 3;
-        const V3 mean = v3(t[0], t[1], t[2]);
-        const V3 sc = v3(expf_c(t[7] + f->lso), expf_c(t[8] + f->lso), expf_c(t[9] + f->lso));
-        const Q4 qu{t[3], t[4], t[5], t[6]};
-        const float raw = f->raw_opac[g];
-        const Q4 q = qnormalize(qu);
-        const float opac_sig = sigmoid(raw);
-        // SH + view-direction VJP
-        const V3 u_world = sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
-        const float u_len = length(u_world);
-        const V3 vdir = scale(u_world, 1.0f / u_len);
-        const V3 v_color = v3(rg[5], rg[6], rg[7]);
+        const SplatVjp r = splat_vjp(f, g, f->transforms + (size_t)g * 10, f->raw_opac[g], rg);
         if (v_sh) {
+            // sh.rs:281-359: v_coeff_k = Y_k(v) v_colour
             float Y[25];
-            const int n = sh_basis(degree, vdir, Y);
+            const int n = sh_basis(degree, r.vdir, Y);
             float* o = v_sh + (size_t)g * K * 3;
-            for (int k = 0; k < n; ++k) { o[3 * k] = v_color.x * Y[k]; o[3 * k + 1] = v_color.y * Y[k]; o[3 * k + 2] = v_color.z * Y[k]; }
+            for (int k = 0; k < n; ++k) { o[3 * k] = rg[5] * Y[k]; o[3 * k + 1] = rg[6] * Y[k]; o[3 * k + 2] = rg[7] * Y[k]; }
         }
-        const V3 v_v_sh = sh_viewdir_vjp(cb, degree, vdir, v_color);
-        const float v_dot = dot(vdir, v_v_sh);
-        const V3 v_mean_sh = scale(sub(v_v_sh, scale(vdir, v_dot)), 1.0f / u_len);
-        const V3 mean_c = world_to_cam(mean, u);
-        const M3 R = quat_to_mat3(q);
-        const M3 Mm = mul_diag(R, sc);
-        const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
-        const float v_opac_base = 1.0f * rg[8];
-        const S2 conic_inv = s2_inverse(cov);
-        const S2 v_inv{rg[2], rg[3] * 0.5f, rg[4]};
-        const S2 v_cov2d = inverse2x2_vjp(conic_inv, v_inv);
-        const S3 covar = outer_self(Mm);
-        const M3 vrot = view_rot(u);
-        const S3 cov_c = s3_congruence(covar, vrot);
-        const M23 J = project_jacobian(mean_c, u);
-        const V3 v_mean_c = (u.model == OR_MODEL_KB4) ? projection_vjp_kb4(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]})
-                                                        : projection_vjp_pinhole(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]});
-        const S3 vcc = m23_tcongruence_s2(J, v_cov2d);
-        const V3 v_mean = add(tmul_vec3(vrot, v_mean_c), v_mean_sh);
-        const M3 v_m = s3_mul_mat3(s3_scale(s3_tcongruence(vcc, vrot), 2.0f), Mm);
-        const V3 v_log{dot(R.c0, v_m.c0) * sc.x, dot(R.c1, v_m.c1) * sc.y, dot(R.c2, v_m.c2) * sc.z};
-        // ratio_sq = 1 and floor.opac * (1 - 1) = 0 without a scale floor.
-        const V3 v_scale_exp{v_log.x * 1.0f + v_opac_base * opac_sig * 0.0f,
-                             v_log.y * 1.0f + v_opac_base * opac_sig * 0.0f,
-                             v_log.z * 1.0f + v_opac_base * opac_sig * 0.0f};
-        const Q4 q_grad = quat_to_mat_vjp(q, mul_diag(v_m, sc));
-        const Q4 v_q = apply_normalize_vjp(qu, q_grad);
-        const float v_raw = v_opac_base * 1.0f * opac_sig * (1.0f - opac_sig);
-        if (v_raw_opac) v_raw_opac[g] = v_raw;
+        if (v_raw_opac) v_raw_opac[g] = r.v_raw;
         if (v_refine) v_refine[g] = clampf(is_finite(rg[9]) ? rg[9] : 0.0f, 0.0f, 1.0e32f);
         if (v_transforms) {
             float* o = v_transforms + (size_t)g * 10;
-            o[0] = v_mean.x; o[1] = v_mean.y; o[2] = v_mean.z;
-            o[3] = v_q.w; o[4] = v_q.x; o[5] = v_q.y; o[6] = v_q.z;
-            o[7] = v_scale_exp.x; o[8] = v_scale_exp.y; o[9] = v_scale_exp.z;
+            o[0] = r.v_mean.x; o[1] = r.v_mean.y; o[2] = r.v_mean.z;
+            o[3] = r.v_q.w; o[4] = r.v_q.x; o[5] = r.v_q.y; o[6] = r.v_q.z;
+            o[7] = r.v_log.x; o[8] = r.v_log.y; o[9] = r.v_log.z;
         }
+    }
+    return 0;
+}
+
+// ---- packed Adam moments, bwd/kernels/geo_moments.rs:1-127 ----------------------
+// With Adam's epsilon e: u = m / (sqrt(v) + e) in the low 16 bits (sign +
+// 15-bit magnitude over [0, 8]), l = ln(1 + sqrt(v) / e) as a 16-bit code over
+// [0, 64] in the high half; sqrt(v) = e (exp(l) - 1), m = u e exp(l).
+static const float GEO_U_CODES = 32767.0f, GEO_U_STEP = 8.0f / 32767.0f, GEO_U_PER_UNIT = 32767.0f / 8.0f;
+static const float GEO_L_CODES = 65535.0f, GEO_L_STEP = 64.0f / 65535.0f, GEO_L_PER_UNIT = 65535.0f / 64.0f;
+
+static float geo_growth(uint32_t word) { return expf_c((float)(word >> 16) * GEO_L_STEP); }      // :24-28
+static float geo_normalized(uint32_t word) {                                                   // :30-35
+    const float magnitude = (float)(word & 0x7fffu) * GEO_U_STEP;
+    return (word & 0x8000u) ? -magnitude : magnitude;
+}
+static uint32_t pack_geo(float m, float v, float epsilon, float round_l, float round_u) {      // :37-56
+    const float l = logf_c(1.0f + std::sqrt(fmax_(v, 0.0f)) / epsilon) * GEO_L_PER_UNIT;
+    const float l_code = std::floor(clampf(l + round_l, 0.0f, GEO_L_CODES));
+    const float sc = epsilon * expf_c(l_code * GEO_L_STEP);
+    const float uu = std::fabs(m) / sc * GEO_U_PER_UNIT;
+    const uint32_t u_code = (uint32_t)std::floor(clampf(uu + round_u, 0.0f, GEO_U_CODES));
+    const uint32_t sign = (m < 0.0f) ? 0x8000u : 0u;
+    return ((uint32_t)l_code << 16) | sign | u_code;
+}
+static uint32_t mix_hash(uint32_t index, uint32_t step) {                                      // :58-66
+    uint32_t h = index ^ (step * 0x9e3779b9u);
+    h = (h ^ (h >> 16)) * 0x7feb352du;
+    h = (h ^ (h >> 15)) * 0x846ca68bu;
+    return h ^ (h >> 16);
+}
+static void adam_packed(float& param, uint32_t& word, uint32_t index, float g, float lr, const or_adam& a,
+                        uint32_t seed) {                                                          // :68-101
+    const float growth = geo_growth(word);
+    const float root = a.epsilon * (growth - 1.0f);
+    const float m1 = geo_normalized(word) * (a.epsilon * growth) * a.beta1 + g * (1.0f - a.beta1);
+    const float v1 = root * root * a.beta2 + g * g * (1.0f - a.beta2);
+    const float step = (m1 * a.inv1) / (std::sqrt(v1 * a.inv2) + a.epsilon);
+    param = param - step * lr;
+    const uint32_t h = mix_hash(index, seed);
+    word = pack_geo(m1, v1, a.epsilon, (float)(h >> 16) / 65536.0f, (float)(h & 0xffffu) / 65536.0f);
+}
+
+extern "C" uint32_t or_geo_encode(float m, float v, float epsilon) { return pack_geo(m, v, epsilon, 0.5f, 0.5f); }
+extern "C" void or_geo_decode(uint32_t word, float epsilon, float* m, float* v) {
+    const float growth = geo_growth(word);
+    const float root = epsilon * (growth - 1.0f);
+    *m = geo_normalized(word) * (epsilon * growth);
+    *v = root * root;
+}
+extern "C" uint32_t or_geo_pack(float m, float v, float epsilon, float round_l, float round_u) {
+    return pack_geo(m, v, epsilon, round_l, round_u);
+}
+extern "C" uint32_t or_mix_hash(uint32_t index, uint32_t step) { return mix_hash(index, step); }
+extern "C" void or_adam_packed(float* param, uint32_t* word, uint32_t index, float g, float lr, const or_adam* a,
+                               uint32_t seed) {
+    adam_packed(*param, *word, index, g, lr, *a, seed);
+}
+
+// ---- fused projection VJP + Adam, bwd/kernels/project_update.rs:40-178 ------------
+extern "C" int or_project_update(const or_fwd* f, const float* v_combined, float* transforms, float* raw_opac,
+                                 uint32_t* w_t, const float* lr_scale, uint32_t* w_o, const or_adam* a,
+                                 float* color_dir, float* v_refine, float* grad_sq, int threads) {
+    if (!f || !v_combined || !transforms || !raw_opac || !w_t || !lr_scale || !w_o || !a ||
+        !(f->flags & OR_FLAG_BWD_INFO))
+        return 1;
+    const uint32_t N = f->N;
+    std::vector<uint8_t> visible(N, 0);
+    for (uint32_t c = 0; c < f->V; ++c) visible[f->global_from_compact[c]] = 1;
+    if (color_dir) for (int k = 0; k < 6; ++k) color_dir[k] = 0.0f;
+    const uint32_t seed_t = a->round_seed ^ (10u << 24), seed_o = a->round_seed ^ (1u << 24);
+    #pragma omp parallel for schedule(static) num_threads(resolve_threads(threads))
+    for (int64_t gi = 0; gi < (int64_t)N; ++gi) {
+        const uint32_t g = (uint32_t)gi;
+        float* t = transforms + (size_t)g * 10;
+        float grad[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        float g_opac = 0.0f, refine = 0.0f, gsq = 0.0f;
+        if (visible[g]) {
+            const float* rg = v_combined + (size_t)g * 10;
+            bool any = false;
+            for (int k = 0; k < 10; ++k) any = any || rg[k] != 0.0f;
+            float* cd = color_dir ? color_dir + (size_t)(g + 1) * 6 : nullptr;
+            if (any) {
+                const SplatVjp r = splat_vjp(f, g, t, raw_opac[g], rg);
+                if (cd) { cd[0] = rg[5]; cd[1] = rg[6]; cd[2] = rg[7]; cd[3] = r.vdir.x; cd[4] = r.vdir.y; cd[5] = r.vdir.z; }
+                grad[0] = r.v_mean.x; grad[1] = r.v_mean.y; grad[2] = r.v_mean.z;
+                grad[3] = r.v_q.w; grad[4] = r.v_q.x; grad[5] = r.v_q.y; grad[6] = r.v_q.z;
+                grad[7] = r.v_log.x; grad[8] = r.v_log.y; grad[9] = r.v_log.z;
+                g_opac = r.v_raw;
+                refine = clampf(is_finite(rg[9]) ? rg[9] : 0.0f, 0.0f, 1.0e32f);
+                // project_update.rs:133-140: the SH row's mean square from its DC
+                // entries (SH C0 = 0.2820948, kernels/sh.rs:17)
+                const float c0 = 0.2820948f * rg[5], c1 = 0.2820948f * rg[6], c2 = 0.2820948f * rg[7];
+                gsq = (c0 * c0 + c1 * c1 + c2 * c2) / 3.0f;
+            } else if (cd) {
+                for (int k = 0; k < 6; ++k) cd[k] = 0.0f;
+            }
+        } else if (color_dir) {
+            for (int k = 0; k < 6; ++k) color_dir[(size_t)(g + 1) * 6 + k] = 0.0f;
+        }
+        if (v_refine) v_refine[g] = refine;
+        if (grad_sq) grad_sq[g] = gsq;
+        float raw = raw_opac[g];
+        const float o = 1.0f / (1.0f + expf_c(-raw));
+        g_opac += a->opac_reg * o * (1.0f - o);
+        for (int k = 0; k < 10; ++k)
+            adam_packed(t[k], w_t[(size_t)g * 10 + k], g * 10u + (uint32_t)k, grad[k], lr_scale[k], *a, seed_t);
+        adam_packed(raw, w_o[g], g, g_opac, a->lr_opac, *a, seed_o);
+        raw_opac[g] = raw;
     }
     return 0;
 }

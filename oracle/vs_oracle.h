@@ -91,6 +91,29 @@ int or_render_backward(const or_fwd* f, const float* v_out, int threads,
 int or_project_backward(const or_fwd* f, const float* v_combined, int threads,
                         float* v_transforms, float* v_sh, float* v_raw_opac, float* v_refine);
 
+/* FusedAdam (bwd/project_update.rs:232-250). */
+typedef struct or_adam {
+    float beta1, beta2, inv1, inv2, epsilon, lr_opac, opac_reg;
+    uint32_t round_seed;
+} or_adam;
+
+/* project_update (bwd/kernels/project_update.rs:40-178) on host arrays: the
+ * projection VJP of `v_combined` [N,10] fused with one Adam step of
+ * `transforms` [N,10] and `raw_opac` [N] (updated in place, and read as the
+ * pre-step values the forward saw), packed moments `w_t` [N,10], `w_o` [N].
+ * color_dir is [N+1,6] with row g + 1 for splat g (NULL skips an output). */
+int or_project_update(const or_fwd* f, const float* v_combined, float* transforms, float* raw_opac,
+                      uint32_t* w_t, const float* lr_scale, uint32_t* w_o, const or_adam* adam,
+                      float* color_dir, float* v_refine, float* grad_sq, int threads);
+
+/* The packed-moment codec (bwd/kernels/geo_moments.rs), one value at a time. */
+uint32_t or_geo_encode(float m, float v, float epsilon);               /* round to nearest */
+void or_geo_decode(uint32_t word, float epsilon, float* m, float* v);
+uint32_t or_geo_pack(float m, float v, float epsilon, float round_l, float round_u);
+uint32_t or_mix_hash(uint32_t index, uint32_t step);
+void or_adam_packed(float* param, uint32_t* word, uint32_t index, float g, float lr, const or_adam* adam,
+                    uint32_t seed);
+
 /* Stable LSD radix argsort restated (splat-train-sort/src/lib.rs:40-189):
  * sorts by key bits [skip, skip + 8*ceil(bits/8)). */
 void or_radix_argsort_u32(const uint32_t* keys, const uint32_t* vals, uint32_t n,

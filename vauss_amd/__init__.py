@@ -8,15 +8,16 @@ loads torch first so the library shares torch's HIP runtime.
 from ._lib import VsError, load  # noqa: F401
 from .camera import Camera, KannalaBrandt4, PINHOLE, fov_to_focal, focal_to_fov, max_render_theta  # noqa: F401
 from .render import (  # noqa: F401
-    Context, ForwardState, RasterPass, RenderAux, RenderOutput, SplatGrads, SplatRenderMode,
-    l1_cotangent, prefix_sum, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
+    Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput, SplatGrads,
+    SplatRenderMode, geo_decode, geo_encode, geo_zero_rows, l1_cotangent, prefix_sum, project_update, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
     radix_argsort_with_count, render, render_backward, scan_in_place, sh_degree_from_coeffs, unpack_rgba8,
 )
 
 __all__ = [
     "Camera", "KannalaBrandt4", "PINHOLE", "fov_to_focal", "focal_to_fov", "max_render_theta",
-    "Context", "ForwardState", "RasterPass", "RenderAux", "RenderOutput", "SplatGrads", "SplatRenderMode",
-    "VsError", "l1_cotangent", "load", "prefix_sum", "radix_argsort", "radix_argsort_skip_low_with_count",
+    "Context", "ForwardState", "FusedAdam", "ProjectUpdateResult", "RasterPass", "RenderAux", "RenderOutput",
+    "SplatGrads", "SplatRenderMode", "VsError", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",
+    "prefix_sum", "project_update", "radix_argsort", "radix_argsort_skip_low_with_count",
     "radix_argsort_u64", "radix_argsort_with_count", "render", "render_backward", "scan_in_place",
     "sh_degree_from_coeffs", "unpack_rgba8",
 ]

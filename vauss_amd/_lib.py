@@ -63,9 +63,18 @@ class VsStateView(C.Structure):
     _fields_ = [("num_splats", C.c_uint32), ("num_visible", C.c_uint32), ("num_intersections", C.c_uint32),
                 ("num_tiles", C.c_uint32), ("tile_bw", C.c_uint32), ("tile_bh", C.c_uint32),
                 ("isect_tiles", C.c_void_p), ("isect_gids", C.c_void_p), ("intersect_counts", C.c_void_p),
-                ("depth_bits", C.c_void_p),
+                ("depth_bits", C.c_void_p), ("compact_from_global", C.c_void_p),
                 ("proj_xy_conic", C.c_void_p), ("proj_c11_opac_rg", C.c_void_p), ("proj_b", C.c_void_p),
                 ("proj_aux", C.c_void_p), ("tile_ranges", C.c_void_p)]
+
+
+class VsAdamStep(C.Structure):
+    _fields_ = [("beta1", C.c_float), ("beta2", C.c_float), ("inv1", C.c_float), ("inv2", C.c_float),
+                ("epsilon", C.c_float), ("lr_opac", C.c_float), ("opac_reg", C.c_float), ("round_seed", C.c_uint32)]
+
+
+class VsUpdateOut(C.Structure):
+    _fields_ = [("color_dir", C.c_void_p), ("v_refine_weight", C.c_void_p), ("coeffs_grad_sq", C.c_void_p)]
 
 
 # name -> (restype, argtypes); the list is the ABI surface the tests check.
@@ -88,6 +97,12 @@ SIGNATURES = {
                                      C.POINTER(VsGrads)]),
     "vs_fwd_state_free": (None, [C.c_void_p]),
     "vs_fwd_state_view": (C.c_int, [C.c_void_p, C.POINTER(VsStateView)]),
+    "vs_project_update": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(VsAdamStep),
+                                    C.POINTER(VsUpdateOut)]),
+    "vs_geo_encode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_float, C.c_void_p]),
+    "vs_geo_decode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_float, C.c_void_p, C.c_void_p]),
+    "vs_geo_zero_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32]),
     "vs_radix_argsort_u32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32,
                                        C.c_uint32, C.c_void_p, C.c_void_p]),
     "vs_radix_argsort_u64": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,

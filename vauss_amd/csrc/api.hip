@@ -73,6 +73,7 @@ struct vs_fwd_state {
     void* isect_arena = nullptr;  // per-intersection buffers
     uint32_t* counts = nullptr;
     uint32_t* depth_bits = nullptr;
+    uint32_t* compact = nullptr;  // [N] g + 1 past every cull, else 0
     float4* proj_a = nullptr;
     float4* proj_b = nullptr;
     float* proj_c = nullptr;
@@ -247,7 +248,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     // ---- per-splat arena -----------------------------------------------------
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
-    const size_t o_counts = take((size_t)N * 4), o_depth = take((size_t)N * 4);
+    const size_t o_counts = take((size_t)N * 4), o_depth = take((size_t)N * 4), o_compact = take((size_t)N * 4);
     const size_t o_pa = take((size_t)N * 16), o_pb = take((size_t)N * 16), o_pc = take((size_t)N * 4);
     const size_t o_aux = geometry ? take((size_t)N * 16) : 0;
     const size_t o_opac = out->opacities ? 0 : take((size_t)N * 4);
@@ -260,6 +261,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     char* base = static_cast<char*>(st->arena);
     st->counts = reinterpret_cast<uint32_t*>(base + o_counts);
     st->depth_bits = reinterpret_cast<uint32_t*>(base + o_depth);
+    st->compact = reinterpret_cast<uint32_t*>(base + o_compact);
     st->proj_a = reinterpret_cast<float4*>(base + o_pa);
     st->proj_b = reinterpret_cast<float4*>(base + o_pb);
     st->proj_c = reinterpret_cast<float*>(base + o_pc);
@@ -282,7 +284,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.raw_opac = sp->raw_opacities;
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
-        pa.proj_aux = st->proj_aux; pa.block_stats = st->block_stats;
+        pa.proj_aux = st->proj_aux; pa.compact = st->compact; pa.block_stats = st->block_stats;
         VS_HIP(launch_project(pa, s), "project kernel");
         VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, s), "projection counts");
         if (bwd_info) VS_HIP(launch_fill_f32(st->visible, 0.0f, N, s), "zero visible");
@@ -424,7 +426,11 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s), "raster backward");
         }
     }
-    {
+    // With no dense gradient requested the backward stops at the raster
+    // gradients (the reference's BackwardFusedUpdate pass: vs_project_update
+    // then takes v_combined).
+    const bool dense = grads->v_transforms || grads->v_sh_coeffs || grads->v_raw_opacities || grads->v_refine_weight;
+    if (dense) {
         StageTimer tm(ctx, ST_PROJECT_BWD);
         ProjectBwdArgs pb{};
         pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = sp->log_scale_offset;
@@ -438,12 +444,70 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     return VS_OK;
 }
 
+extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* transforms, const float* sh_coeffs,
+                                       float* raw_opacities, const float* v_combined, uint32_t* w_t,
+                                       const float* lr_scale, uint32_t* w_o, const vs_adam_step* adam,
+                                       vs_update_out* out) {
+    if (!ctx || !st || !adam || !out) return fail(VS_ERR_INVALID, "null argument");
+    if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
+    const uint32_t N = st->N;
+    if (N > 0 && (!transforms || !sh_coeffs || !raw_opacities || !v_combined || !w_t || !lr_scale || !w_o))
+        return fail(VS_ERR_INVALID, "parameter, gradient or moment pointer is null");
+    if (((uintptr_t)transforms & 7u) || ((uintptr_t)v_combined & 7u))
+        return fail(VS_ERR_INVALID, "transforms and v_combined must be 8-byte aligned");
+    if (((uintptr_t)sh_coeffs & 15u)) return fail(VS_ERR_INVALID, "sh_coeffs must be 16-byte aligned");
+    if (!(adam->epsilon > 0.0f)) return fail(VS_ERR_INVALID, "Adam epsilon must be positive (it scales the moment codec)");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    StageTimer tm(ctx, ST_PROJECT_BWD);
+    ProjectUpdateArgs pu{};
+    pu.cam = st->cam; pu.num_splats = N; pu.sh_degree = st->degree; pu.log_scale_offset = st->lso;
+    pu.transforms = transforms; pu.sh = sh_coeffs; pu.raw_opac = raw_opacities; pu.compact = st->compact;
+    pu.v_combined = v_combined; pu.w_t = w_t; pu.lr_scale = lr_scale; pu.w_o = w_o;
+    pu.beta1 = adam->beta1; pu.beta2 = adam->beta2; pu.inv1 = adam->inv1; pu.inv2 = adam->inv2;
+    pu.epsilon = adam->epsilon; pu.lr_opac = adam->lr_opac; pu.opac_reg = adam->opac_reg; pu.round_seed = adam->round_seed;
+    pu.color_dir = out->color_dir; pu.v_refine = out->v_refine_weight; pu.grad_sq = out->coeffs_grad_sq;
+    VS_HIP(launch_project_update(pu, ctx->stream), "project update");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_geo_encode(vs_ctx* ctx, const float* m, const float* v, uint32_t n, float epsilon,
+                                   uint32_t* words) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (n == 0) return VS_OK;
+    if (!m || !v || !words) return fail(VS_ERR_INVALID, "null buffer");
+    if (!(epsilon > 0.0f)) return fail(VS_ERR_INVALID, "epsilon must be positive");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_geo_encode(m, v, n, epsilon, words, ctx->stream), "geo encode");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_geo_decode(vs_ctx* ctx, const uint32_t* words, uint32_t n, float epsilon, float* m, float* v) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (n == 0) return VS_OK;
+    if (!m || !v || !words) return fail(VS_ERR_INVALID, "null buffer");
+    if (!(epsilon > 0.0f)) return fail(VS_ERR_INVALID, "epsilon must be positive");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_geo_decode(words, n, epsilon, m, v, ctx->stream), "geo decode");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_geo_zero_rows(vs_ctx* ctx, uint32_t* words, uint64_t num_words, const uint32_t* rows,
+                                      uint32_t num_rows, uint32_t row_width) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if ((uint64_t)num_rows * row_width == 0) return VS_OK;
+    if (!words || !rows) return fail(VS_ERR_INVALID, "null buffer");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_geo_zero_rows(words, rows, num_rows, row_width, num_words, ctx->stream), "geo zero rows");
+    return VS_OK;
+}
+
 extern "C" vs_status vs_fwd_state_view(const vs_fwd_state* st, vs_state_view* o) {
     if (!st || !o) return fail(VS_ERR_INVALID, "null argument");
     o->num_splats = st->N; o->num_visible = st->V; o->num_intersections = st->I; o->num_tiles = st->T;
     o->tile_bw = st->tbw; o->tile_bh = st->tbh;
     o->isect_tiles = st->tiles; o->isect_gids = st->gids; o->intersect_counts = st->counts;
     o->depth_bits = st->depth_bits;
+    o->compact_from_global = st->compact;
     o->proj_xy_conic = reinterpret_cast<const float*>(st->proj_a);
     o->proj_c11_opac_rg = reinterpret_cast<const float*>(st->proj_b);
     o->proj_b = st->proj_c;

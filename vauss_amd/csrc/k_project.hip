@@ -276,6 +276,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
         a.max_radius[g] = radius;
         a.counts[g] = hits;
         a.depth_bits[g] = dbits;
+        a.compact[g] = visible ? g + 1u : 0u;
     }
 
     // Block statistics, reduced by finalize_counts_kernel (no global atomics:

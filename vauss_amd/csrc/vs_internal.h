@@ -52,6 +52,7 @@ struct ProjectArgs {
     float4* proj_b;             // [N] c11, opacity, r, g
     float* proj_c;              // [N] b
     float4* proj_aux;           // [N] z, nx, ny, nz (geometry) or null
+    uint32_t* compact;          // [N] g + 1 for splats past every cull, else 0 (compact_from_global)
     uint32_t* block_stats;      // [BS_ROWS][ceil(N/256)]
 };
 
@@ -118,6 +119,25 @@ struct ProjectBwdArgs {
     float* v_refine;
 };
 
+struct ProjectUpdateArgs {
+    vs_camera cam;
+    uint32_t num_splats, sh_degree;
+    float log_scale_offset;
+    float* transforms;               // [N,10] stepped in place
+    const float* sh;
+    float* raw_opac;                 // [N] stepped in place
+    const uint32_t* compact;         // [N] g + 1 if visible, else 0
+    const float* v_combined;         // [N,10]
+    uint32_t* w_t;                   // [N,10] packed moments
+    const float* lr_scale;           // [10] device
+    uint32_t* w_o;                   // [N] packed moments
+    float beta1, beta2, inv1, inv2, epsilon, lr_opac, opac_reg;
+    uint32_t round_seed;
+    float* color_dir;                // [N+1,6] or null
+    float* v_refine;                 // [N] or null
+    float* grad_sq;                  // [N] or null
+};
+
 // ---- launchers (return hipError_t of the launch) -------------------------------
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
 // Reduces the projection's block stats into `counters` and turns the block
@@ -131,6 +151,11 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s);
+hipError_t launch_project_update(const ProjectUpdateArgs& a, hipStream_t s);
+hipError_t launch_geo_encode(const float* m, const float* v, uint32_t n, float epsilon, uint32_t* words, hipStream_t s);
+hipError_t launch_geo_decode(const uint32_t* words, uint32_t n, float epsilon, float* m, float* v, hipStream_t s);
+hipError_t launch_geo_zero_rows(uint32_t* words, const uint32_t* rows, uint32_t num_rows, uint32_t row_width,
+                                uint64_t num_words, hipStream_t s);
 hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float* gt, uint32_t w, uint32_t h,
                                float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
 hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float mr, uint32_t* out, hipStream_t s);

@@ -126,6 +126,16 @@ class ForwardState:
         _lib.check(self.ctx.lib.vs_fwd_state_view(self.handle, C.byref(v)))
         return v
 
+    def compact_from_global(self, device: torch.device) -> torch.Tensor:
+        """A copy of compact_from_global [N]: g + 1 for splats past every cull, 0 if culled."""
+        v = self.view()
+
+        class _Dev:
+            __cuda_array_interface__ = {"shape": (v.num_splats,), "typestr": "<i4",
+                                        "data": (v.compact_from_global, False), "version": 2, "strides": None}
+        with torch.cuda.device(device):
+            return torch.as_tensor(_Dev(), device=device).clone()
+
     def tile_ranges(self, device: torch.device) -> torch.Tensor:
         """A copy of the tile ranges before the forward shrank their ends, [ty, tx, 2] (u32 bits in int32)."""
         v = self.view()
@@ -246,8 +256,13 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
 
 
 def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
-                    raw_opacities: torch.Tensor, v_output: torch.Tensor, log_scale_offset: float = 0.0) -> SplatGrads:
-    """rasterize_bwd followed by project_bwd, returning dense gradients."""
+                    raw_opacities: torch.Tensor, v_output: torch.Tensor, log_scale_offset: float = 0.0,
+                    fused: bool = False) -> SplatGrads:
+    """rasterize_bwd followed by project_bwd, returning dense gradients.
+
+    With `fused` the backward stops at the raster gradients (the
+    BackwardFusedUpdate pass): only `v_combined` is filled, for
+    project_update; the other fields are None."""
     if output.state is None or output.state.handle is None:
         raise ValueError("the forward pass kept no backward state (use a bwd-info pass)")
     transforms = transforms.contiguous()
@@ -261,11 +276,14 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     ctx = output.state.ctx
     Context.get(dev)
     k = (degree + 1) ** 2
-    g = SplatGrads(torch.empty((n, 10), dtype=torch.float32, device=dev),
-                   torch.empty((n, k, 3), dtype=torch.float32, device=dev),
-                   torch.empty(n, dtype=torch.float32, device=dev),
-                   torch.empty(n, dtype=torch.float32, device=dev),
-                   torch.empty((n, 10), dtype=torch.float32, device=dev))
+    if fused:
+        g = SplatGrads(None, None, None, None, torch.empty((n, 10), dtype=torch.float32, device=dev))
+    else:
+        g = SplatGrads(torch.empty((n, 10), dtype=torch.float32, device=dev),
+                       torch.empty((n, k, 3), dtype=torch.float32, device=dev),
+                       torch.empty(n, dtype=torch.float32, device=dev),
+                       torch.empty(n, dtype=torch.float32, device=dev),
+                       torch.empty((n, 10), dtype=torch.float32, device=dev))
     grads = _lib.VsGrads()
     grads.v_transforms = _ptr(g.v_transforms)
     grads.v_sh_coeffs = _ptr(g.v_coeffs)
@@ -276,6 +294,103 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     _lib.check(ctx.lib.vs_render_backward(ctx.handle, output.state.handle, C.byref(splats), _ptr(output.out_img),
                                           _ptr(v_output), C.byref(grads)))
     return g
+
+
+@dataclass
+class FusedAdam:
+    """FusedAdam, bwd/project_update.rs:232-250."""
+    beta1: float
+    beta2: float
+    inv1: float
+    inv2: float
+    epsilon: float
+    lr_opac: float
+    opac_reg: float = 0.0
+    round_seed: int = 0
+
+    @classmethod
+    def at_step(cls, step: int, lr_opac: float, beta1: float = 0.9, beta2: float = 0.999, epsilon: float = 1e-15,
+                opac_reg: float = 0.0) -> "FusedAdam":
+        """Bias corrections of Adam step `step` (1-based); the step count seeds the rounding."""
+        return cls(beta1, beta2, 1.0 / (1.0 - beta1 ** step), 1.0 / (1.0 - beta2 ** step), epsilon, lr_opac,
+                   opac_reg, step)
+
+
+@dataclass
+class ProjectUpdateResult:
+    """ProjectUpdateResult minus the tensors stepped in place (bwd/project_update.rs:252-262)."""
+    color_dir: torch.Tensor        # [N+1, 6]
+    v_refine_weight: torch.Tensor  # [N]
+    coeffs_grad_sq: torch.Tensor   # [N, 1, 1]
+    compact_from_global: torch.Tensor  # [N] rows of color_dir (g + 1), 0 for culled splats
+
+
+def project_update(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
+                   raw_opacities: torch.Tensor, v_combined: torch.Tensor, w_t: torch.Tensor, lr_scale: torch.Tensor,
+                   w_o: torch.Tensor, adam: FusedAdam) -> ProjectUpdateResult:
+    """project_update (bwd/project_update.rs:264-322): projection VJP + one
+    Adam step; `transforms`, `raw_opacities`, `w_t` and `w_o` are updated in
+    place.  `w_t` [N,10] and `w_o` [N] hold packed moments (int32 tensors)."""
+    if output.state is None or output.state.handle is None:
+        raise ValueError("the forward pass kept no backward state (use a bwd-info pass)")
+    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities)
+    for name, t in (("transforms", transforms), ("raw_opacities", raw_opacities), ("w_t", w_t), ("w_o", w_o),
+                    ("v_combined", v_combined), ("lr_scale", lr_scale)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous (it is read or updated in place)")
+    _u32(w_t, "w_t")
+    _u32(w_o, "w_o")
+    if tuple(w_t.shape) != (n, 10) or tuple(w_o.shape) != (n,):
+        raise ValueError("packed moments must be [N, 10] and [N]")
+    if tuple(v_combined.shape) != (n, 10) or lr_scale.numel() != 10 or lr_scale.dtype != torch.float32:
+        raise ValueError("v_combined must be [N, 10] and lr_scale [10] float32")
+    sh_coeffs = sh_coeffs.contiguous()
+    dev = transforms.device
+    ctx = output.state.ctx
+    Context.get(dev)
+    res = ProjectUpdateResult(torch.empty((n + 1, 6), dtype=torch.float32, device=dev),
+                              torch.empty(n, dtype=torch.float32, device=dev),
+                              torch.empty((n, 1, 1), dtype=torch.float32, device=dev),
+                              output.state.compact_from_global(dev))
+    a = _lib.VsAdamStep(adam.beta1, adam.beta2, adam.inv1, adam.inv2, adam.epsilon, adam.lr_opac, adam.opac_reg,
+                        adam.round_seed & 0xFFFFFFFF)
+    out = _lib.VsUpdateOut(_ptr(res.color_dir), _ptr(res.v_refine_weight), _ptr(res.coeffs_grad_sq))
+    _lib.check(ctx.lib.vs_project_update(ctx.handle, output.state.handle, _ptr(transforms), _ptr(sh_coeffs),
+                                         _ptr(raw_opacities), _ptr(v_combined), _ptr(w_t), _ptr(lr_scale),
+                                         _ptr(w_o), C.byref(a), C.byref(out)))
+    return res
+
+
+def geo_encode(m: torch.Tensor, v: torch.Tensor, epsilon: float) -> torch.Tensor:
+    """encode_geo (bwd/geo_moments.rs:33-39): f32 (m, v) -> packed words, rounding to nearest."""
+    m = m.contiguous().float()
+    v = v.contiguous().float()
+    if m.shape != v.shape:
+        raise ValueError("m and v must have the same shape")
+    words = torch.empty(m.shape, dtype=torch.int32, device=m.device)
+    ctx = Context.get(m.device)
+    _lib.check(ctx.lib.vs_geo_encode(ctx.handle, _ptr(m), _ptr(v), m.numel(), float(epsilon), _ptr(words)))
+    return words
+
+
+def geo_decode(words: torch.Tensor, epsilon: float):
+    """decode_geo (bwd/geo_moments.rs:41-48): packed words -> f32 (m, v)."""
+    words = _u32(words.contiguous(), "words")
+    m = torch.empty(words.shape, dtype=torch.float32, device=words.device)
+    v = torch.empty_like(m)
+    ctx = Context.get(words.device)
+    _lib.check(ctx.lib.vs_geo_decode(ctx.handle, _ptr(words), words.numel(), float(epsilon), _ptr(m), _ptr(v)))
+    return m, v
+
+
+def geo_zero_rows(words: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """zero_geo_rows (bwd/geo_moments.rs:50-58): reset the moments of `rows` in place."""
+    _u32(words, "words")
+    rows = _u32(rows.contiguous(), "rows")
+    width = words.shape[1] if words.dim() > 1 else 1
+    ctx = Context.get(words.device)
+    _lib.check(ctx.lib.vs_geo_zero_rows(ctx.handle, _ptr(words), words.numel(), _ptr(rows), rows.numel(), width))
+    return words
 
 
 def _u32(t: torch.Tensor, name: str) -> torch.Tensor:
