@@ -39,6 +39,18 @@ class OrAdam(C.Structure):
                 ("epsilon", C.c_float), ("lr_opac", C.c_float), ("opac_reg", C.c_float), ("round_seed", C.c_uint32)]
 
 
+class OrLossCfg(C.Structure):
+    """Same layout as vs_loss_cfg (include/vsplat.h)."""
+    _fields_ = [("l1_weight", C.c_float), ("ssim_weight", C.c_float), ("alpha_weight", C.c_float),
+                ("composite", C.c_int32), ("bg", C.c_float * 3), ("mask", C.c_int32)]
+
+
+def loss_cfg(l1_weight=0.8, ssim_weight=-0.2, alpha_weight=0.0, composite_bg=None, mask=False) -> OrLossCfg:
+    bg = composite_bg if composite_bg is not None else (0.0, 0.0, 0.0)
+    return OrLossCfg(l1_weight, ssim_weight, alpha_weight, 1 if composite_bg is not None else 0,
+                     (C.c_float * 3)(*bg), 1 if mask else 0)
+
+
 class OrFwdInfo(C.Structure):
     _fields_ = [("num_splats", C.c_uint32), ("num_visible", C.c_uint32), ("num_intersections", C.c_uint32),
                 ("num_tiles", C.c_uint32), ("tile_bw", C.c_uint32), ("tile_bh", C.c_uint32),
@@ -75,6 +87,11 @@ def load() -> C.CDLL:
     lib.or_project_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F]
     lib.or_project_update.restype = C.c_int
     lib.or_project_update.argtypes = [C.c_void_p, _F, _F, _F, _U, _F, _U, C.POINTER(OrAdam), _F, _F, _F, C.c_int]
+    lib.or_image_loss_forward.restype = C.c_int
+    lib.or_image_loss_forward.argtypes = [_F, C.c_uint32, _U, C.c_uint32, C.c_uint32, C.POINTER(OrLossCfg), _F, _F, _F]
+    lib.or_image_loss_backward.restype = C.c_int
+    lib.or_image_loss_backward.argtypes = [_F, C.c_uint32, _U, C.c_uint32, C.c_uint32, C.POINTER(OrLossCfg), _F,
+                                           C.c_int, _F, _F]
     lib.or_geo_encode.restype = C.c_uint32
     lib.or_geo_encode.argtypes = [C.c_float, C.c_float, C.c_float]
     lib.or_geo_decode.argtypes = [C.c_uint32, C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]
@@ -332,3 +349,34 @@ def adam_packed(param: float, word: int, index: int, g: float, lr: float, adam: 
     p, w = C.c_float(param), C.c_uint32(word & 0xFFFFFFFF)
     load().or_adam_packed(C.byref(p), C.byref(w), index & 0xFFFFFFFF, g, lr, C.byref(adam), seed & 0xFFFFFFFF)
     return p.value, w.value
+
+
+def image_loss_forward(pred: np.ndarray, gt_packed: np.ndarray, cfg: OrLossCfg):
+    """(partials [planes, tiles], coeffs [3,3,H,W], loss_map [H,W,C])."""
+    pred = np.ascontiguousarray(pred, np.float32)
+    gt = np.ascontiguousarray(gt_packed, np.uint32)
+    h, w, cn = pred.shape
+    tiles = ((w + 15) // 16) * ((h + 15) // 16)
+    planes = 4 if (cfg.alpha_weight > 0 and cn == 4) else 3
+    partials = np.zeros((planes, tiles), np.float32)
+    coeffs = np.zeros((3, 3, h, w), np.float32)
+    lmap = np.zeros((h, w, cn), np.float32)
+    rc = load().or_image_loss_forward(_fp(pred), cn, _up(gt), w, h, C.byref(cfg), _fp(partials), _fp(coeffs), _fp(lmap))
+    if rc != 0:
+        raise RuntimeError(f"oracle image loss failed ({rc})")
+    return partials, coeffs, lmap
+
+
+def image_loss_backward(pred: np.ndarray, gt_packed: np.ndarray, cfg: OrLossCfg, dl_dpartials: np.ndarray,
+                        coeffs: np.ndarray) -> np.ndarray:
+    pred = np.ascontiguousarray(pred, np.float32)
+    gt = np.ascontiguousarray(gt_packed, np.uint32)
+    dl = np.ascontiguousarray(dl_dpartials, np.float32)
+    co = np.ascontiguousarray(coeffs, np.float32)
+    h, w, cn = pred.shape
+    out = np.zeros_like(pred)
+    rc = load().or_image_loss_backward(_fp(pred), cn, _up(gt), w, h, C.byref(cfg), _fp(dl), 1 if dl.size == 1 else 0,
+                                       _fp(co), _fp(out))
+    if rc != 0:
+        raise RuntimeError(f"oracle image loss backward failed ({rc})")
+    return out

@@ -1285,3 +1285,218 @@ extern "C" double or_focal_to_fov(double focal, uint32_t pixels, int model, cons
 extern "C" double or_max_render_theta(int model, const float kb4[4]) {
     return (model == OR_MODEL_KB4) ? kb4_fold(kb4) : M_PI;
 }
+
+// ---- image loss: L1 + SSIM, crates/splat-train-loss/src/lib.rs:226-1306 ------------
+// gauss_taps() (lib.rs:48-62): exp(-x^2 / 4.5), x = -5..5, in f32, normalised
+// by their f32 sum; the literals are those f32 values.
+static const float LOSS_GW[11] = {0x1.0d957p-10f, 0x1.f1fe04p-8f, 0x1.26eb18p-5f, 0x1.bff1p-4f, 0x1.b43c4p-3f,
+                                  0x1.106562p-2f, 0x1.b43c4p-3f, 0x1.bff1p-4f, 0x1.26eb18p-5f, 0x1.f1fe04p-8f,
+                                  0x1.0d957p-10f};
+static const float LOSS_C1 = 0.01f * 0.01f, LOSS_C2 = 0.03f * 0.03f, LOSS_INV_255 = 1.0f / 255.0f;
+static const uint32_t LOSS_TILE = 16;
+
+namespace {
+struct LossImg {
+    uint32_t h, w, cn;
+    const float* pred;
+    const uint32_t* gt;
+    const or_loss_cfg* cfg;
+    float gt_c(uint32_t y, uint32_t x, uint32_t c) const { return (float)((gt[(size_t)y * w + x] >> (c * 8)) & 0xffu) * LOSS_INV_255; }
+    float gt_a(uint32_t y, uint32_t x) const { return (float)((gt[(size_t)y * w + x] >> 24) & 0xffu) * LOSS_INV_255; }
+    // read_gt + compositing (lib.rs:161-183, 318-323)
+    float gt_eff(uint32_t y, uint32_t x, uint32_t c) const {
+        const float g = gt_c(y, x, c);
+        return cfg->composite ? g + (1.0f - gt_a(y, x)) * cfg->bg[c] : g;
+    }
+    float p(uint32_t y, uint32_t x, uint32_t c) const { return pred[((size_t)y * w + x) * cn + c]; }
+    uint32_t tiles_x() const { return (w + LOSS_TILE - 1) / LOSS_TILE; }
+    uint32_t tiles() const { return tiles_x() * ((h + LOSS_TILE - 1) / LOSS_TILE); }
+    uint32_t tile_of(uint32_t y, uint32_t x) const { return (y / LOSS_TILE) * tiles_x() + x / LOSS_TILE; }
+};
+
+// Separable 11-tap blur of `n` per-pixel values with zero outside the image,
+// in the kernels' order: per tap distance d = 1..5, sum += (left + right) * w,
+// then the centre tap; rows first, then columns (lib.rs:326-414).
+// src(y, x, k) gives value k at an in-image pixel; out is [h][w][n].
+template <typename F>
+void blur(const LossImg& im, int n, F src, std::vector<float>& out) {
+    const uint32_t h = im.h, w = im.w;
+    std::vector<float> hs((size_t)h * w * n);
+    std::vector<float> row((size_t)(w + 10) * n);
+    for (uint32_t y = 0; y < h; ++y) {
+        std::fill(row.begin(), row.end(), 0.0f);
+        for (uint32_t x = 0; x < w; ++x)
+            for (int k = 0; k < n; ++k) row[(size_t)(x + 5) * n + k] = src(y, x, k);
+        for (uint32_t x = 0; x < w; ++x)
+            for (int k = 0; k < n; ++k) {
+                float s = 0.0f;
+                for (int d = 1; d <= 5; ++d) s += (row[(size_t)(x + 5 - d) * n + k] + row[(size_t)(x + 5 + d) * n + k]) * LOSS_GW[5 - d];
+                s += row[(size_t)(x + 5) * n + k] * LOSS_GW[5];
+                hs[((size_t)y * w + x) * n + k] = s;
+            }
+    }
+    out.assign((size_t)h * w * n, 0.0f);
+    auto hv = [&](int64_t y, uint32_t x, int k) { return (y < 0 || y >= (int64_t)h) ? 0.0f : hs[((size_t)y * w + x) * n + k]; };
+    for (uint32_t y = 0; y < h; ++y)
+        for (uint32_t x = 0; x < w; ++x)
+            for (int k = 0; k < n; ++k) {
+                float s = 0.0f;
+                for (int d = 1; d <= 5; ++d) s += (hv((int64_t)y - d, x, k) + hv((int64_t)y + d, x, k)) * LOSS_GW[5 - d];
+                s += hv(y, x, k) * LOSS_GW[5];
+                out[((size_t)y * w + x) * n + k] = s;
+            }
+}
+
+// Sum of a 16x16 tile's 256 values (tid = row * 16 + col, zero past the
+// image) by the halving tree tile_sum (lib.rs:112-128) uses.
+float tile_tree_sum(float* v) {
+    for (uint32_t stride = 128; stride >= 1; stride >>= 1)
+        for (uint32_t t = 0; t < stride; ++t) v[t] += v[t + stride];
+    return v[0];
+}
+} // namespace
+
+// image_loss_forward_kernel (lib.rs:238-478) for every plane, writing the
+// reduced partials [planes, tiles], the per-pixel SSIM coefficients [3][3][H,W]
+// (dmu1, dsigma1, dsigma12 per channel) and the loss map [H,W,cn]; NULL skips.
+extern "C" int or_image_loss_forward(const float* pred, uint32_t cn, const uint32_t* gt, uint32_t w, uint32_t h,
+                                     const or_loss_cfg* cfg, float* partials, float* coeffs, float* loss_map) {
+    if (!pred || !gt || !cfg || (cn != 3 && cn != 4) || w == 0 || h == 0) return 1;
+    const LossImg im{h, w, cn, pred, gt, cfg};
+    const bool alpha_match = cfg->alpha_weight > 0.0f && cn == 4;
+    const float pixels = (float)(h * w);
+    const float rgb_weight = 1.0f / (3.0f * pixels);
+    const float alpha_weight = cfg->alpha_weight / pixels;
+    const uint32_t T = im.tiles();
+    std::vector<float> lossv((size_t)h * w);
+    std::vector<float> bl;
+    for (uint32_t c = 0; c < 3; ++c) {
+        blur(im, 5, [&](uint32_t y, uint32_t x, int k) {
+            const float xv = im.p(y, x, c), yv = im.gt_eff(y, x, c);
+            switch (k) {
+            case 0: return xv;
+            case 1: return xv * xv;
+            case 2: return yv;
+            case 3: return yv * yv;
+            default: return xv * yv;
+            }
+        }, bl);
+        for (uint32_t y = 0; y < h; ++y)
+            for (uint32_t x = 0; x < w; ++x) {
+                const float* o = &bl[((size_t)y * w + x) * 5];
+                const float mu1 = o[0], mu2 = o[2];
+                const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
+                const float sigma1_sq = fmax_(0.0f, o[1] - mu1_sq);
+                const float sigma2_sq = fmax_(0.0f, o[3] - mu2_sq);
+                const float sigma12 = o[4] - mu1 * mu2;
+                const float a = mu1_sq + mu2_sq + LOSS_C1;
+                const float b = sigma1_sq + sigma2_sq + LOSS_C2;
+                const float c_top = 2.0f * mu1 * mu2 + LOSS_C1;
+                const float d_top = 2.0f * sigma12 + LOSS_C2;
+                const float raw = (c_top * d_top) / (a * b);
+                const float val = clampf(raw, -1.0f, 1.0f);
+                if (coeffs) {
+                    const float inv_b = 1.0f / b;
+                    const float inv_ab = 1.0f / (a * b);
+                    const float cd = c_top * d_top * inv_ab;
+                    const bool clamped = cd < -1.0f || cd > 1.0f;
+                    const size_t plane = (size_t)h * w, at = (size_t)c * 3 * plane + (size_t)y * w + x;
+                    coeffs[at] = clamped ? 0.0f : 2.0f * inv_ab * (mu2 * (d_top - c_top) - mu1 * cd * (b - a));
+                    coeffs[at + plane] = clamped ? 0.0f : -cd * inv_b;
+                    coeffs[at + 2 * plane] = clamped ? 0.0f : 2.0f * c_top * inv_ab;
+                }
+                const float l1 = std::fabs(im.p(y, x, c) - im.gt_eff(y, x, c));
+                float lv = cfg->l1_weight * l1 + cfg->ssim_weight * val;
+                if (cfg->mask) lv = lv * im.gt_a(y, x);
+                lossv[(size_t)y * w + x] = lv;
+                if (loss_map) loss_map[((size_t)y * w + x) * cn + c] = lv;
+            }
+        if (partials)
+            for (uint32_t t = 0; t < T; ++t) {
+                float v[256];
+                const uint32_t ty = t / im.tiles_x(), tx = t % im.tiles_x();
+                for (uint32_t i = 0; i < 256; ++i) {
+                    const uint32_t y = ty * 16 + i / 16, x = tx * 16 + i % 16;
+                    v[i] = (y < h && x < w) ? lossv[(size_t)y * w + x] : 0.0f;
+                }
+                partials[(size_t)c * T + t] = tile_tree_sum(v) * rgb_weight;
+            }
+    }
+    if (alpha_match) {
+        // lib.rs:266-285: |pred.a - gt.a| (times gt.a when masking), no blur
+        for (uint32_t y = 0; y < h; ++y)
+            for (uint32_t x = 0; x < w; ++x) {
+                const float ga = im.gt_a(y, x);
+                float v = std::fabs(im.p(y, x, 3) - ga);
+                if (cfg->mask) v = v * ga;
+                lossv[(size_t)y * w + x] = v;
+                if (loss_map) loss_map[((size_t)y * w + x) * cn + 3] = v;
+            }
+        if (partials)
+            for (uint32_t t = 0; t < T; ++t) {
+                float v[256];
+                const uint32_t ty = t / im.tiles_x(), tx = t % im.tiles_x();
+                for (uint32_t i = 0; i < 256; ++i) {
+                    const uint32_t y = ty * 16 + i / 16, x = tx * 16 + i % 16;
+                    v[i] = (y < h && x < w) ? lossv[(size_t)y * w + x] : 0.0f;
+                }
+                partials[(size_t)3 * T + t] = tile_tree_sum(v) * alpha_weight;
+            }
+    }
+    return 0;
+}
+
+// image_loss_backward_coeffs_kernel (lib.rs:821-1020): dL/dpred [H,W,cn] from
+// the forward's coefficients and dl_dpartials ([1] gradient of the total when
+// scalar_grad, else one per partial [planes, tiles]).
+extern "C" int or_image_loss_backward(const float* pred, uint32_t cn, const uint32_t* gt, uint32_t w, uint32_t h,
+                                      const or_loss_cfg* cfg, const float* dl_dpartials, int scalar_grad,
+                                      const float* coeffs, float* dl_dpred) {
+    if (!pred || !gt || !cfg || !dl_dpartials || !coeffs || !dl_dpred || (cn != 3 && cn != 4)) return 1;
+    const LossImg im{h, w, cn, pred, gt, cfg};
+    const bool alpha_match = cfg->alpha_weight > 0.0f && cn == 4;
+    const float pixels = (float)(h * w);
+    const float rgb_weight = 1.0f / (3.0f * pixels);
+    const float alpha_weight = cfg->alpha_weight / pixels;
+    const uint32_t T = im.tiles();
+    const size_t plane = (size_t)h * w;
+    // chain_at (lib.rs:141-159)
+    auto chain_at = [&](uint32_t c, uint32_t y, uint32_t x, float weight) {
+        const float g = scalar_grad ? dl_dpartials[0] : dl_dpartials[(size_t)c * T + im.tile_of(y, x)];
+        return g * weight;
+    };
+    std::vector<float> bl;
+    for (uint32_t c = 0; c < 3; ++c) {
+        blur(im, 3, [&](uint32_t y, uint32_t x, int k) {
+            float chain = chain_at(c, y, x, rgb_weight);
+            if (cfg->mask) chain = chain * im.gt_a(y, x);
+            return coeffs[(size_t)c * 3 * plane + (size_t)k * plane + (size_t)y * w + x] * chain;
+        }, bl);
+        for (uint32_t y = 0; y < h; ++y)
+            for (uint32_t x = 0; x < w; ++x) {
+                const float* s = &bl[((size_t)y * w + x) * 3];
+                const float p1 = im.p(y, x, c), ge = im.gt_eff(y, x, c);
+                const float ssim_grad = s[0] + (2.0f * p1) * s[1] + ge * s[2];
+                const float diff = p1 - ge;
+                const float sign = diff > 0.0f ? 1.0f : (diff < 0.0f ? -1.0f : 0.0f);
+                float cc = chain_at(c, y, x, rgb_weight);
+                if (cfg->mask) cc = cc * im.gt_a(y, x);
+                dl_dpred[((size_t)y * w + x) * cn + c] = cfg->ssim_weight * ssim_grad + cfg->l1_weight * sign * cc;
+            }
+    }
+    if (cn == 4)
+        for (uint32_t y = 0; y < h; ++y)
+            for (uint32_t x = 0; x < w; ++x) {
+                float g = 0.0f;
+                if (alpha_match) {
+                    const float ga = im.gt_a(y, x);
+                    const float diff = im.p(y, x, 3) - ga;
+                    const float sign = diff > 0.0f ? 1.0f : (diff < 0.0f ? -1.0f : 0.0f);
+                    float chain = chain_at(3, y, x, alpha_weight);
+                    if (cfg->mask) chain = chain * ga;
+                    g = sign * chain;
+                }
+                dl_dpred[((size_t)y * w + x) * cn + 3] = g;
+            }
+    return 0;
+}

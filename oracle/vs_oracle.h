@@ -114,6 +114,26 @@ uint32_t or_mix_hash(uint32_t index, uint32_t step);
 void or_adam_packed(float* param, uint32_t* word, uint32_t index, float g, float lr, const or_adam* adam,
                     uint32_t seed);
 
+/* ImageLossConfig (crates/splat-train-loss/src/lib.rs:1227-1260). ssim_weight
+ * multiplies SSIM itself (negative for a training loss). */
+typedef struct or_loss_cfg {
+    float l1_weight, ssim_weight, alpha_weight;
+    int32_t composite;          /* composite gt over bg: gt + (1 - gt.a) bg */
+    float bg[3];
+    int32_t mask;               /* multiply each loss pixel by gt.a */
+} or_loss_cfg;
+
+/* image_loss_forward_kernel (lib.rs:238-478) over an [H,W,cn] f32 prediction
+ * and [H,W] RGBA8-packed ground truth: per-16x16-tile weighted partial sums
+ * [planes, tiles] (planes = 3, or 4 with the alpha-match term), the SSIM
+ * coefficients [3][3][H,W] and the per-pixel loss map [H,W,cn]; NULL skips. */
+int or_image_loss_forward(const float* pred, uint32_t cn, const uint32_t* gt, uint32_t w, uint32_t h,
+                          const or_loss_cfg* cfg, float* partials, float* coeffs, float* loss_map);
+/* image_loss_backward_coeffs_kernel (lib.rs:821-1020): dL/dpred [H,W,cn]. */
+int or_image_loss_backward(const float* pred, uint32_t cn, const uint32_t* gt, uint32_t w, uint32_t h,
+                           const or_loss_cfg* cfg, const float* dl_dpartials, int scalar_grad,
+                           const float* coeffs, float* dl_dpred);
+
 /* Stable LSD radix argsort restated (splat-train-sort/src/lib.rs:40-189):
  * sorts by key bits [skip, skip + 8*ceil(bits/8)). */
 void or_radix_argsort_u32(const uint32_t* keys, const uint32_t* vals, uint32_t n,
