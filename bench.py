@@ -228,7 +228,7 @@ def main() -> int:
 
 PROFILES = os.path.join(ROOT, "profiles")
 KERNEL_SOURCES = [os.path.join(ROOT, "vauss_amd", "csrc", f) for f in
-                  ("k_project.hip", "k_project_bwd.hip", "k_project_update.hip", "k_raster.hip", "k_scan.hip",
+                  ("k_project.hip", "k_project_bwd.hip", "k_project_update.hip", "k_raster.hip", "k_loss.hip", "k_scan.hip",
                    "k_sort.hip", "api.hip", "vs_device.h", "vs_camera.h", "vs_sh.h", "vs_vjp.h", "vs_adam.h",
                    "vs_internal.h")]
 

@@ -279,6 +279,41 @@ vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, con
                           uint32_t img_w, uint32_t img_h, float mask_cx, float mask_cy,
                           float mask_radius, float* v_out);
 
+/* ---- image loss: L1 + SSIM ------------------------------------------------------- */
+
+/* ImageLossConfig (crates/splat-train-loss/src/lib.rs:1227-1260).  The
+ * per-pixel loss is l1_weight |pred - gt| + ssim_weight SSIM(pred, gt) per
+ * colour channel (ssim_weight multiplies SSIM itself: a training loss passes
+ * it negative, e.g. l1_dssim(w) = {1 - w, -w}), times gt.a when `mask`, with
+ * gt composited over `bg` (gt + (1 - gt.a) bg) when `composite`; an
+ * alpha-match term alpha_weight |pred.a - gt.a| joins with a 4-channel pred. */
+typedef struct vs_loss_cfg {
+    float l1_weight, ssim_weight, alpha_weight;
+    int32_t composite;
+    float bg[3];
+    int32_t mask;
+} vs_loss_cfg;
+
+/* LossOps::image_loss_forward / image_loss_forward_train (lib.rs:1312-1380;
+ * kernel :238-478) over pred [H,W,C] f32 (C = 3 or 4) and gt_packed [H,W]
+ * u32 RGBA8 (r in the low byte).  Writes (NULL skips each): the weighted
+ * 16x16-tile partial sums [planes, tiles] (planes 3, or 4 with alpha
+ * matching; tiles row-major) whose sum is the loss, the SSIM coefficients
+ * [3][3][H,W] the backward blurs, the per-pixel loss map [H,W,C], and the
+ * loss `total` [1] (needs `partials`). */
+vs_status vs_image_loss_forward(vs_ctx* ctx, const float* pred, uint32_t channels, const uint32_t* gt_packed,
+                                uint32_t img_w, uint32_t img_h, const vs_loss_cfg* cfg, float* partials,
+                                float* coeffs, float* loss_map, float* total);
+/* LossOps::image_loss_backward / image_loss_backward_coeffs (lib.rs:1335-1380;
+ * kernels :481-1020): dL/dpred [H,W,C] (16-byte aligned when C = 4) from
+ * dl_dpartials, the [1] gradient of the total (dl_count 1) or one per
+ * partial (dl_count = planes x tiles).  `coeffs` from the forward, or NULL to
+ * recompute them (same values). */
+vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint32_t channels, const uint32_t* gt_packed,
+                                 uint32_t img_w, uint32_t img_h, const vs_loss_cfg* cfg,
+                                 const float* dl_dpartials, uint32_t dl_count, const float* coeffs,
+                                 float* dl_dpred);
+
 #ifdef __cplusplus
 }
 #endif

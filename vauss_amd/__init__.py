@@ -6,6 +6,10 @@ include/vsplat.h); this package is its host-side mirror.  Importing it
 loads torch first so the library shares torch's HIP runtime.
 """
 from ._lib import VsError, load  # noqa: F401
+from .loss import (  # noqa: F401
+    ImageLossConfig, image_loss, image_loss_backward, image_loss_eval, image_loss_forward_train,
+    image_loss_partials, pack_rgba8,
+)
 from .camera import Camera, KannalaBrandt4, PINHOLE, fov_to_focal, focal_to_fov, max_render_theta  # noqa: F401
 from .render import (  # noqa: F401
     Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput, SplatGrads,
@@ -14,6 +18,8 @@ from .render import (  # noqa: F401
 )
 
 __all__ = [
+    "ImageLossConfig", "image_loss", "image_loss_backward", "image_loss_eval", "image_loss_forward_train",
+    "image_loss_partials", "pack_rgba8",
     "Camera", "KannalaBrandt4", "PINHOLE", "fov_to_focal", "focal_to_fov", "max_render_theta",
     "Context", "ForwardState", "FusedAdam", "ProjectUpdateResult", "RasterPass", "RenderAux", "RenderOutput",
     "SplatGrads", "SplatRenderMode", "VsError", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",

@@ -68,6 +68,11 @@ class VsStateView(C.Structure):
                 ("proj_aux", C.c_void_p), ("tile_ranges", C.c_void_p)]
 
 
+class VsLossCfg(C.Structure):
+    _fields_ = [("l1_weight", C.c_float), ("ssim_weight", C.c_float), ("alpha_weight", C.c_float),
+                ("composite", C.c_int32), ("bg", C.c_float * 3), ("mask", C.c_int32)]
+
+
 class VsAdamStep(C.Structure):
     _fields_ = [("beta1", C.c_float), ("beta2", C.c_float), ("inv1", C.c_float), ("inv2", C.c_float),
                 ("epsilon", C.c_float), ("lr_opac", C.c_float), ("opac_reg", C.c_float), ("round_seed", C.c_uint32)]
@@ -109,6 +114,10 @@ SIGNATURES = {
                                        C.c_void_p]),
     "vs_prefix_sum_u32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]),
     "vs_scan_in_place_u32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32]),
+    "vs_image_loss_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
+                                        C.POINTER(VsLossCfg), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "vs_image_loss_backward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
+                                         C.POINTER(VsLossCfg), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
     "vs_l1_cotangent": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
                                   C.c_float, C.c_float, C.c_float, C.c_void_p]),
 }

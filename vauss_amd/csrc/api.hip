@@ -575,6 +575,79 @@ extern "C" vs_status vs_scan_in_place_u32(vs_ctx* ctx, uint32_t* data, uint32_t 
     return VS_OK;
 }
 
+namespace {
+vs_status loss_args(const float* pred, uint32_t channels, const uint32_t* gt, uint32_t w, uint32_t h,
+                    const vs_loss_cfg* cfg, LossArgs& a) {
+    if (!pred || !gt || !cfg) return fail(VS_ERR_INVALID, "null argument");
+    if (channels != 3 && channels != 4) return fail(VS_ERR_INVALID, "image loss expects 3 or 4 channels");
+    if (w == 0 || h == 0) return fail(VS_ERR_INVALID, "empty image");
+    a = LossArgs{};
+    a.img_w = w; a.img_h = h; a.channels = channels; a.pred = pred; a.gt = gt;
+    a.l1_weight = cfg->l1_weight; a.ssim_weight = cfg->ssim_weight; a.alpha_weight_cfg = cfg->alpha_weight;
+    a.composite = cfg->composite != 0; a.mask = cfg->mask != 0;
+    a.bg[0] = cfg->bg[0]; a.bg[1] = cfg->bg[1]; a.bg[2] = cfg->bg[2];
+    // channel_weights (lib.rs:1297-1300)
+    const float pixels = (float)(h * w);
+    a.rgb_weight = 1.0f / (3.0f * pixels);
+    a.alpha_weight = cfg->alpha_weight / pixels;
+    return VS_OK;
+}
+uint32_t loss_planes(const vs_loss_cfg* cfg, uint32_t channels) { return (cfg->alpha_weight > 0.0f && channels == 4) ? 4u : 3u; }
+uint32_t loss_tiles(uint32_t w, uint32_t h) { return ((w + 15) / 16) * ((h + 15) / 16); }
+} // namespace
+
+extern "C" vs_status vs_image_loss_forward(vs_ctx* ctx, const float* pred, uint32_t channels, const uint32_t* gt_packed,
+                                           uint32_t img_w, uint32_t img_h, const vs_loss_cfg* cfg, float* partials,
+                                           float* coeffs, float* loss_map, float* total) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    LossArgs a;
+    vs_status st = loss_args(pred, channels, gt_packed, img_w, img_h, cfg, a);
+    if (st != VS_OK) return st;
+    if (total && !partials) return fail(VS_ERR_INVALID, "the total needs the partials buffer");
+    a.partials = partials; a.coeffs = coeffs; a.loss_map = loss_map; a.total = total;
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    StageTimer tm(ctx, ST_OTHER);
+    VS_HIP(launch_loss_forward(a, ctx->stream), "image loss forward");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint32_t channels, const uint32_t* gt_packed,
+                                            uint32_t img_w, uint32_t img_h, const vs_loss_cfg* cfg,
+                                            const float* dl_dpartials, uint32_t dl_count, const float* coeffs,
+                                            float* dl_dpred) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    LossArgs a;
+    vs_status st = loss_args(pred, channels, gt_packed, img_w, img_h, cfg, a);
+    if (st != VS_OK) return st;
+    if (!dl_dpartials || !dl_dpred) return fail(VS_ERR_INVALID, "null argument");
+    const uint32_t n_partials = loss_planes(cfg, channels) * loss_tiles(img_w, img_h);
+    if (dl_count != 1 && dl_count != n_partials)
+        return fail(VS_ERR_INVALID, "dl_dpartials must be [1] or [planes, tiles]");
+    if (channels == 4 && ((uintptr_t)dl_dpred & 15u)) return fail(VS_ERR_INVALID, "dl_dpred must be 16-byte aligned");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = ctx->stream;
+    StageTimer tm(ctx, ST_OTHER);
+    void* tmp = nullptr;
+    if (!coeffs) {
+        // No stored coefficients: the forward recomputes them (the reference's
+        // recomputing backward blurs the same quantities in the same order).
+        VS_HIP(hipMallocAsync(&tmp, (size_t)9 * img_w * img_h * 4, s), "hipMallocAsync(loss coefficients)");
+        LossArgs f = a;
+        f.coeffs = static_cast<float*>(tmp);
+        hipError_t e = launch_loss_forward(f, s);
+        if (e != hipSuccess) { hipFreeAsync(tmp, s); return hip_fail(e, "image loss coefficients"); }
+        coeffs = static_cast<const float*>(tmp);
+    }
+    LossBwdArgs b{};
+    b.fwd = a; b.img_w = img_w; b.img_h = img_h; b.channels = channels; b.pred = pred; b.gt = gt_packed;
+    b.dl = dl_dpartials; b.coeffs = coeffs; b.dl_dpred = dl_dpred; b.rgb_weight = a.rgb_weight;
+    b.alpha_weight = a.alpha_weight;
+    hipError_t e = launch_loss_backward(b, dl_count == 1, s);
+    if (tmp) hipFreeAsync(tmp, s);
+    if (e != hipSuccess) return hip_fail(e, "image loss backward");
+    return VS_OK;
+}
+
 extern "C" vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const float* gt, uint32_t w,
                                      uint32_t h, float mcx, float mcy, float mr, float* v_out) {
     if (!ctx || !pred || !gt || !v_out) return fail(VS_ERR_INVALID, "null argument");

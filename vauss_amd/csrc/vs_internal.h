@@ -138,6 +138,31 @@ struct ProjectUpdateArgs {
     float* grad_sq;                  // [N] or null
 };
 
+struct LossArgs {
+    uint32_t img_w, img_h, channels;     // channels 3 or 4
+    const float* pred;                   // [H,W,C]
+    const uint32_t* gt;                  // [H,W] RGBA8 packed
+    float l1_weight, ssim_weight, alpha_weight_cfg;
+    int32_t composite, mask;
+    float bg[3];
+    float rgb_weight, alpha_weight;      // 1 / (3 H W), alpha_weight_cfg / (H W)
+    float* partials;                     // [planes, tiles] or null
+    float* coeffs;                       // [3][3][H,W] or null
+    float* loss_map;                     // [H,W,C] or null
+    float* total;                        // [1] or null (needs partials)
+};
+
+struct LossBwdArgs {
+    LossArgs fwd;                        // configuration
+    uint32_t img_w, img_h, channels;
+    const float* pred;
+    const uint32_t* gt;
+    const float* dl;                     // [1] or [planes, tiles]
+    const float* coeffs;                 // [3][3][H,W] from the forward
+    float* dl_dpred;                     // [H,W,C]
+    float rgb_weight, alpha_weight;
+};
+
 // ---- launchers (return hipError_t of the launch) -------------------------------
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
 // Reduces the projection's block stats into `counters` and turns the block
@@ -158,6 +183,8 @@ hipError_t launch_geo_zero_rows(uint32_t* words, const uint32_t* rows, uint32_t 
                                 uint64_t num_words, hipStream_t s);
 hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float* gt, uint32_t w, uint32_t h,
                                float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
+hipError_t launch_loss_forward(const LossArgs& a, hipStream_t s);
+hipError_t launch_loss_backward(const LossBwdArgs& a, bool scalar, hipStream_t s);
 hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float mr, uint32_t* out, hipStream_t s);
 
 // Scans.  `tmp` needs scan_tmp_words(n) u32 words.  With a permutation `perm`
