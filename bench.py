@@ -54,6 +54,78 @@ def algorithmic_bytes(stage: str, n: int, v: int, i: int, t: int, p: int, k: int
     return 0
 
 
+def measure_next_rows(va, wl, cam, t, s, o, gt, dev, reps: int = 10) -> dict:
+    """Kernel times (HIP events on the library's stream, outside the timed
+    region) of the rows after the render: the L1 + SSIM loss (training
+    forward with SSIM coefficients, and its backward) on the view's image, and
+    the fused projection backward + packed-moment Adam on its raster
+    gradients.  Algorithmic bytes: loss forward 20 B/px in + 36 B/px of
+    coefficients out; backward 56 B/px in + 16 B/px out; update per splat
+    40 + 4 + 4 + 40 + 40 + 4 B in and 40 + 4 + 40 + 4 + 24 + 8 B out, plus the
+    192 B SH row of each splat with gradients."""
+    import torch
+
+    def timed(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sorted(ts)[len(ts) // 2]
+
+    out = va.render(cam, wl.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
+    h, w = out.out_img.shape[:2]
+    gt_rgba = torch.cat([gt, torch.ones((h, w, 1), device=dev)], dim=-1)
+    gtp = va.pack_rgba8(gt_rgba.cpu()).to(dev)
+    cfg = va.ImageLossConfig.l1_dssim(0.2)
+    box = {}
+
+    def fwd():
+        box["p"], box["c"], box["t"] = va.image_loss_forward_train(out.out_img, gtp, cfg)
+    f_ms = timed(fwd)
+    one = torch.ones(1, device=dev)
+    b_ms = timed(lambda: va.image_loss_backward(out.out_img, gtp, one, cfg, box["c"]))
+    px = h * w
+    v = va.l1_cotangent(out.out_img, gt, (0.0, 0.0), 0.0)
+    g = va.render_backward(out, t, s, o, v, fused=True)
+    n = t.shape[0]
+    tw, ow = t.clone(), o.clone()
+    w_t = torch.zeros((n, 10), dtype=torch.int32, device=dev)
+    w_o = torch.zeros(n, dtype=torch.int32, device=dev)
+    lr = torch.full((10,), 1e-4, device=dev)
+    adam = va.FusedAdam.at_step(1, lr_opac=0.05)
+    res = va.project_update(out, tw, s, ow, g.v_combined, w_t, lr, w_o, adam)
+    u_ms = timed(lambda: va.project_update(out, tw, s, ow, g.v_combined, w_t, lr, w_o, adam))
+    with_grad = int((g.v_combined.abs().sum(dim=1) > 0).sum().item())
+    u_bytes = n * (132 + 120) + with_grad * 192
+    # SH step on f16 coefficients: every block holding a value of a splat with
+    # a gradient row reads and writes 128 x (2 B coefficient + 1 B code) and
+    # its scale; per splat 4 B row + 4 B grad_sq + 4 + 4 B variance, per
+    # visible splat its 24 B colour row.
+    sh16 = s.half()
+    k3 = sh16.shape[1] * 3
+    st = va.ShStepState.fresh(n, wl.scene.sh_degree, dev)
+    rows = res.compact_from_global
+    sh_ms = timed(lambda: va.sh_step(sh16, res.color_dir, rows, res.coeffs_grad_sq, st, 1e-3))
+    vis_vals = (rows != 0).repeat_interleave(k3)
+    pad = (-vis_vals.numel()) % 128
+    touched = int(torch.nn.functional.pad(vis_vals, (0, pad)).view(-1, 128).any(dim=1).sum().item())
+    nvis = int((rows != 0).sum().item())
+    sh_bytes = touched * (128 * 6 + 8) + n * 16 + nvis * 24
+    out.state.free()
+    return {"image_loss_l1_ssim": {"img": [w, h], "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+                                   "fwd_alg_GBs": round(56 * px / (f_ms * 1e-3) / 1e9, 1),
+                                   "bwd_alg_GBs": round(72 * px / (b_ms * 1e-3) / 1e9, 1)},
+            "project_update": {"ms": round(u_ms, 4), "splats": n, "with_gradient": with_grad,
+                               "alg_GBs": round(u_bytes / (u_ms * 1e-3) / 1e9, 1)},
+            "sh_step": {"ms": round(sh_ms, 4), "blocks_stepped": touched, "coeff_dtype": "f16",
+                        "alg_GBs": round(sh_bytes / (sh_ms * 1e-3) / 1e9, 1)}}
+
+
 def list_length_histogram(ranges) -> dict:
     """Per-tile list lengths from tile ranges [.., 2] (before the forward
     shrinks their ends) as a power-of-two histogram."""
@@ -195,6 +267,8 @@ def main() -> int:
         print(f"[bench] copy calibration: {args.copy_calib} MiB read + {args.copy_calib} MiB written per copy",
               file=sys.stderr, flush=True)
 
+    next_rows = measure_next_rows(va, wl, cams[0], t, s, o, gt, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(wl, cams)
@@ -221,23 +295,28 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "tile_lists": tile_lists,
+        "next_rows": next_rows,
     }
     print(json.dumps(line))
     return 0
 
 
 PROFILES = os.path.join(ROOT, "profiles")
-KERNEL_SOURCES = [os.path.join(ROOT, "vauss_amd", "csrc", f) for f in
-                  ("k_project.hip", "k_project_bwd.hip", "k_project_update.hip", "k_raster.hip", "k_loss.hip", "k_scan.hip",
-                   "k_sort.hip", "api.hip", "vs_device.h", "vs_camera.h", "vs_sh.h", "vs_vjp.h", "vs_adam.h",
-                   "vs_internal.h")]
+def _kernel_sources():
+    from vauss_amd.build import HEADERS, SOURCES
+    return [os.path.join(ROOT, "vauss_amd", "csrc", f) for f in SOURCES + HEADERS if not f.endswith(".cpp")]
+
+
+KERNEL_SOURCES = _kernel_sources()
 
 # rocprofv3 kernel names -> bench stage names
 STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "raster_fwd"),
                    ("project_bwd_kernel", "project_bwd"), ("project_kernel", "project"), ("emit_kernel", "emit"),
                    ("finalize_counts", "project"), ("compact_kernel", "emit"), ("scan_", "emit"), ("sort_", "sort"),
                    ("tile_ranges", "ranges"),
-                   ("l1_cotangent", "loss"), ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
+                   ("l1_cotangent", "loss"), ("loss_", "image_loss"), ("project_update", "project_update"),
+                   ("sh_step", "sh_step"), ("sh_variance", "sh_step"), ("b8_", "sh_step"),
+                   ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
 
 
 # what the markdown summary lists (the traffic file keeps every kernel)

@@ -70,14 +70,19 @@ typedef struct vs_pose {
     float kb4[4];
 } vs_pose;
 
+/* Element type of the SH coefficients (render.rs:683-687: f32 or f16; the
+ * trainer's SH step keeps them in f16).  Gradients are always f32. */
+typedef enum vs_sh_dtype { VS_SH_F32 = 0, VS_SH_F16 = 1 } vs_sh_dtype;
+
 /* Parameters of N splats, crates/splat-train-render/src/gaussian_splats.rs:127-153. */
 typedef struct vs_splats {
     const float* transforms;        /* [N,10]: mean xyz, quat w x y z, log-scale xyz */
-    const float* sh_coeffs;         /* [N,(d+1)^2,3] */
+    const void* sh_coeffs;          /* [N,(d+1)^2,3] f32, or IEEE binary16 when sh_dtype = VS_SH_F16 */
     const float* raw_opacities;     /* [N] logits */
     uint32_t num_splats;
     uint32_t sh_degree;             /* 0..4 */
     float log_scale_offset;         /* added to every log-scale (render.rs:325) */
+    uint32_t sh_dtype;              /* vs_sh_dtype */
 } vs_splats;
 
 /* RasterPass, crates/splat-train-render/src/gaussian_splats.rs:32-107. */
@@ -232,9 +237,10 @@ typedef struct vs_update_out {
  * moments are packed one u32 per value in `w_t` [N,10] and `w_o` [N]
  * (geo_moments.rs codec; zero words are reset moments).  `lr_scale` is the
  * per-column transforms learning rate [10] (device).  The parameters must be
- * the pre-step values the forward of `state` saw.  Every splat steps: culled
- * ones decay their moments with a zero gradient plus the opacity regulariser. */
-vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* state, float* transforms, const float* sh_coeffs,
+ * the pre-step values the forward of `state` saw (`sh_coeffs` in the
+ * forward's dtype).  Every splat steps: culled ones decay their moments with a
+ * zero gradient plus the opacity regulariser. */
+vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* state, float* transforms, const void* sh_coeffs,
                             float* raw_opacities, const float* v_combined, uint32_t* w_t,
                             const float* lr_scale, uint32_t* w_o, const vs_adam_step* adam,
                             vs_update_out* out);
@@ -247,6 +253,47 @@ vs_status vs_geo_encode(vs_ctx* ctx, const float* m, const float* v, uint32_t n,
 vs_status vs_geo_decode(vs_ctx* ctx, const uint32_t* words, uint32_t n, float epsilon, float* m, float* v);
 vs_status vs_geo_zero_rows(vs_ctx* ctx, uint32_t* words, uint64_t num_words, const uint32_t* rows,
                            uint32_t num_rows, uint32_t row_width);
+
+/* Block-scaled 8-bit moment (BlockMoment, crates/splat-train/src/quant.rs:30-160;
+ * kernels quant_kernels.rs:438-498, 911-925).  n values in blocks of 128: block
+ * b has scales[b] = absmax / 127 and codes round(clamp(v / scale, -127, 127)) +
+ * 128 (128 for a zero scale), four per u32 word, value 4w+j in byte j of word
+ * w; `codes` holds ceil(n/128)*32 words, `scales` ceil(n/128) floats.  All-zero
+ * codes and scales are a fresh moment (BlockMoment::zeros).  zero_rows sets the
+ * codes of each listed row of `row_width` values to 128 (values past n are
+ * ignored); growing the moment for new rows (BlockMoment::reset_rows' extra
+ * blocks) is the caller's allocation: new words 0x80808080, new scales 0. */
+vs_status vs_block8_encode(vs_ctx* ctx, const float* values, uint32_t n, uint32_t* codes, float* scales);
+vs_status vs_block8_decode(vs_ctx* ctx, const uint32_t* codes, const float* scales, uint32_t n, float* values);
+vs_status vs_block8_zero_rows(vs_ctx* ctx, uint32_t* codes, uint32_t n, const uint32_t* rows, uint32_t num_rows,
+                              uint32_t row_width);
+
+/* Step constants of the SH step (MomentUpdate, quant.rs:19-28, with beta2). */
+typedef struct vs_sh_step_params {
+    float beta1, beta2;
+    float inv1, inv2;               /* 1 / (1 - beta1^t), 1 / (1 - beta2^t) */
+    float epsilon, lr;              /* lr = the DC learning rate; lr_scale scales it per column */
+    uint32_t round_seed;            /* the step count t: seeds the stochastic f16 rounding */
+    uint32_t first;                 /* 1 on the first step (no moments yet) */
+} vs_sh_step_params;
+
+/* AdamScaled::step_sh_color (crates/splat-train/src/optim.rs:391-498;
+ * BlockMoment::step quant.rs:121-161; step_kernel_w4 quant_kernels.rs:582-727).
+ * One lazy Adam step of the f16 SH coefficients `sh_coeffs` [N,K,3] (IEEE
+ * binary16, in place) from vs_project_update's `color_dir` [rows,6]: the
+ * coefficient gradient Y_k(dir) colour_c is rebuilt per value.  `grad_rows`
+ * [N] is the forward's compact_from_global (row of color_dir, 0 = culled),
+ * `grad_sq` [N] vs_project_update's coeffs_grad_sq.  The second moment
+ * `variance` [N] first becomes v beta2 + grad_sq (1 - beta2) for splats with a
+ * row (grad_sq (1 - beta2) for every splat when p->first); then each value of
+ * a splat with a row steps m = m beta1 + g (1 - beta1), c -= (m inv1 /
+ * (sqrt(v inv2) + eps)) lr_scale[col] lr, rounded stochastically to f16;
+ * values of culled splats keep coefficient and moment; blocks holding a
+ * value of a splat with a row are re-packed, others are left as they are.
+ * `lr_scale` [K*3] (device). */
+vs_status vs_sh_step(vs_ctx* ctx, uint16_t* sh_coeffs, uint32_t num_splats, uint32_t sh_degree,
+                     const float* color_dir, const uint32_t* grad_rows, const float* grad_sq, float* variance,
+                     uint32_t* codes, float* scales, const float* lr_scale, const vs_sh_step_params* p);
 
 /* ---- sort / scan ---------------------------------------------------------------- */
 

@@ -101,6 +101,18 @@ def load() -> C.CDLL:
     lib.or_mix_hash.argtypes = [C.c_uint32, C.c_uint32]
     lib.or_adam_packed.argtypes = [C.POINTER(C.c_float), C.POINTER(C.c_uint32), C.c_uint32, C.c_float, C.c_float,
                                    C.POINTER(OrAdam), C.c_uint32]
+    lib.or_f32_to_f16.restype = C.c_uint16
+    lib.or_f32_to_f16.argtypes = [C.c_float]
+    lib.or_f16_to_f32.restype = C.c_float
+    lib.or_f16_to_f32.argtypes = [C.c_uint16]
+    lib.or_stochastic_half.restype = C.c_float
+    lib.or_stochastic_half.argtypes = [C.c_float, C.c_uint32, C.c_uint32]
+    lib.or_block8_encode.argtypes = [_F, C.c_uint64, _U, _F]
+    lib.or_block8_decode.argtypes = [_U, _F, C.c_uint64, _F]
+    lib.or_block8_zero_rows.argtypes = [_U, C.c_uint64, _U, C.c_uint32, C.c_uint32]
+    lib.or_sh_step.restype = C.c_int
+    lib.or_sh_step.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, _F, _U, _F, _F, _U, _F, _F, C.c_float, C.c_float,
+                               C.c_float, C.c_float, C.c_float, C.c_float, C.c_uint32, C.c_int]
     lib.or_radix_argsort_u32.argtypes = [_U, _U, C.c_uint32, C.c_uint32, C.c_uint32, _U, _U]
     lib.or_prefix_sum_u32.argtypes = [_U, _U, C.c_uint32]
     for name in ("or_expf", "or_logf"):
@@ -380,3 +392,61 @@ def image_loss_backward(pred: np.ndarray, gt_packed: np.ndarray, cfg: OrLossCfg,
     if rc != 0:
         raise RuntimeError(f"oracle image loss backward failed ({rc})")
     return out
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(load().or_f32_to_f16(x))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(load().or_f16_to_f32(h & 0xFFFF))
+
+
+def stochastic_half(value: float, index: int, step: int) -> float:
+    return float(load().or_stochastic_half(value, index & 0xFFFFFFFF, step & 0xFFFFFFFF))
+
+
+def block8_encode(values: np.ndarray):
+    """(codes [ceil(n/128)*32] u32, scales [ceil(n/128)] f32)."""
+    v = np.ascontiguousarray(values, np.float32).reshape(-1)
+    blocks = (v.size + 127) // 128
+    codes = np.zeros(blocks * 32, np.uint32)
+    scales = np.zeros(blocks, np.float32)
+    load().or_block8_encode(_fp(v), v.size, _up(codes), _fp(scales))
+    return codes, scales
+
+
+def block8_decode(codes: np.ndarray, scales: np.ndarray, n: int) -> np.ndarray:
+    out = np.zeros(n, np.float32)
+    load().or_block8_decode(_up(np.ascontiguousarray(codes, np.uint32)), _fp(np.ascontiguousarray(scales, np.float32)),
+                            n, _fp(out))
+    return out
+
+
+def block8_zero_rows(codes: np.ndarray, n: int, rows: np.ndarray, row_width: int) -> np.ndarray:
+    out = np.ascontiguousarray(codes, np.uint32).copy()
+    r = np.ascontiguousarray(rows, np.uint32)
+    load().or_block8_zero_rows(_up(out), n, _up(r), r.size, row_width)
+    return out
+
+
+def sh_step(sh_half: np.ndarray, color_dir: np.ndarray, grad_rows: np.ndarray, grad_sq: np.ndarray,
+            variance: np.ndarray, codes: np.ndarray, scales: np.ndarray, lr_scale: np.ndarray, *, beta1: float,
+            beta2: float, inv1: float, inv2: float, epsilon: float, lr: float, round_seed: int, first: bool):
+    """One SH step on copies: returns (sh [N,K,3] f16, variance, codes, scales)."""
+    sh = np.ascontiguousarray(sh_half, np.float16).copy()
+    n, k = sh.shape[0], sh.shape[1]
+    degree = int(round(k ** 0.5)) - 1
+    var = np.ascontiguousarray(variance, np.float32).copy()
+    co = np.ascontiguousarray(codes, np.uint32).copy()
+    sc = np.ascontiguousarray(scales, np.float32).copy()
+    cd = np.ascontiguousarray(color_dir, np.float32)
+    gr = np.ascontiguousarray(grad_rows, np.uint32)
+    gs = np.ascontiguousarray(grad_sq, np.float32)
+    ls = np.ascontiguousarray(lr_scale, np.float32)
+    rc = load().or_sh_step(sh.ctypes.data_as(C.c_void_p), n, degree, _fp(cd), _up(gr), _fp(gs), _fp(var), _up(co),
+                           _fp(sc), _fp(ls), beta1, beta2, inv1, inv2, epsilon, lr, round_seed & 0xFFFFFFFF,
+                           1 if first else 0)
+    if rc != 0:
+        raise RuntimeError(f"oracle SH step failed ({rc})")
+    return sh, var, co, sc

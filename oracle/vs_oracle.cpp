@@ -1119,6 +1119,151 @@ extern "C" void or_adam_packed(float* param, uint32_t* word, uint32_t index, flo
     adam_packed(*param, *word, index, g, lr, *a, seed);
 }
 
+// ---- IEEE binary16, the SH step's coefficient storage ------------------------------
+namespace {
+float f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+    if (e == 0) {
+        const float v = (float)man * 5.9604644775390625e-08f;      // man * 2^-24, exact
+        return (h & 0x8000u) ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7F800000u | (man << 13));
+    return u2f(sign | ((e + 112u) << 23) | (man << 13));
+}
+// Round to nearest even; subnormals kept; >= 65520 in magnitude -> infinity.
+uint16_t f32_to_f16(float f) {
+    const uint32_t x = f2u(f), sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (ax < 0x38800000u) return (uint16_t)(sign | (uint32_t)std::nearbyint(u2f(ax) * 16777216.0f));
+    const uint32_t r = ax - 0x38000000u;
+    return (uint16_t)(sign | ((r + 0x0FFFu + ((r >> 13) & 1u)) >> 13));
+}
+
+// quant_kernels.rs:866-894.
+float stochastic_half(float value, uint32_t index, uint32_t step) {
+    const float magnitude = std::fabs(value);
+    if (!(magnitude <= 65504.0f)) return value;
+    float lower, upper;
+    if (magnitude < 6.103515625e-05f) {
+        lower = std::floor(magnitude * 16777216.0f) / 16777216.0f;
+        upper = lower + 5.9604644775390625e-08f;
+    } else {
+        const uint32_t bits = f2u(magnitude) & 0xffffe000u;
+        lower = u2f(bits);
+        upper = u2f(bits + 8192u);
+    }
+    uint32_t h = index ^ (step * 0x9e3779b9u);
+    h = (h ^ (h >> 16)) * 0x7feb352du;
+    h = (h ^ (h >> 15)) * 0x846ca68bu;
+    h = h ^ (h >> 16);
+    const float uniform = (float)(h >> 8) / 16777216.0f;
+    const float probability = (magnitude - lower) / (upper - lower);
+    const float r = uniform < probability ? upper : lower;
+    return value < 0.0f ? -r : r;
+}
+
+// Block-scaled 8-bit moment (quant.rs; pack_block / unpack, quant_kernels.rs:438-484).
+constexpr uint32_t B8 = 128;
+float b8_get(const uint32_t* codes, const float* scales, uint64_t i) {
+    const uint32_t code = (codes[i / 4] >> ((i % 4) * 8)) & 255u;
+    return ((float)code - 128.0f) * scales[i / B8];
+}
+// Pack one block's 128 moments (values past the end are 0).
+void b8_pack(const float* m, uint64_t block, uint32_t* codes, float* scales) {
+    float absmax = 0.0f;
+    for (uint32_t i = 0; i < B8; ++i) absmax = fmax_(absmax, std::fabs(m[i]));
+    const float scale = absmax / 127.0f;
+    scales[block] = scale;
+    for (uint32_t w = 0; w < B8 / 4; ++w) {
+        uint32_t word = 0;
+        for (uint32_t j = 0; j < 4; ++j) {
+            uint32_t code = 128u;
+            if (scale > 0.0f) code = (uint32_t)(std::nearbyint(clampf(m[4 * w + j] / scale, -127.0f, 127.0f)) + 128.0f);
+            word |= code << (8 * j);
+        }
+        codes[block * (B8 / 4) + w] = word;
+    }
+}
+} // namespace
+
+extern "C" uint16_t or_f32_to_f16(float f) { return f32_to_f16(f); }
+extern "C" float or_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
+extern "C" float or_stochastic_half(float value, uint32_t index, uint32_t step) {
+    return stochastic_half(value, index, step);
+}
+extern "C" void or_block8_encode(const float* values, uint64_t n, uint32_t* codes, float* scales) {
+    const uint64_t blocks = (n + B8 - 1) / B8;
+    float m[B8];
+    for (uint64_t b = 0; b < blocks; ++b) {
+        for (uint32_t i = 0; i < B8; ++i) m[i] = b * B8 + i < n ? values[b * B8 + i] : 0.0f;
+        b8_pack(m, b, codes, scales);
+    }
+}
+extern "C" void or_block8_decode(const uint32_t* codes, const float* scales, uint64_t n, float* values) {
+    for (uint64_t i = 0; i < n; ++i) values[i] = b8_get(codes, scales, i);
+}
+extern "C" void or_block8_zero_rows(uint32_t* codes, uint64_t n, const uint32_t* rows, uint32_t num_rows,
+                                    uint32_t row_width) {
+    for (uint32_t r = 0; r < num_rows; ++r)
+        for (uint32_t c = 0; c < row_width; ++c) {
+            const uint64_t i = (uint64_t)rows[r] * row_width + c;
+            if (i >= n) continue;
+            const uint32_t shift = (uint32_t)(i % 4) * 8;
+            codes[i / 4] = (codes[i / 4] & ~(255u << shift)) | (128u << shift);
+        }
+}
+
+// AdamScaled::step_sh_color (crates/splat-train/src/optim.rs:391-498) with
+// the moment step of quant_kernels.rs:582-727, block by block: the second
+// moment first (optim.rs:447-469), then each block holding a value of a splat
+// with a gradient row is decoded, its values of such splats stepped (the
+// coefficient gradient rebuilt as Y_k(dir) colour_c, quant_kernels.rs:569-577
+// and 673-700) and the block re-packed; other blocks stay as they are.
+extern "C" int or_sh_step(uint16_t* sh, uint32_t N, uint32_t degree, const float* color_dir, const uint32_t* grad_rows,
+                          const float* grad_sq, float* variance, uint32_t* codes, float* scales, const float* lr_scale,
+                          float beta1, float beta2, float inv1, float inv2, float epsilon, float lr,
+                          uint32_t round_seed, int first) {
+    if (degree > 4) return 1;
+    const uint32_t K = (degree + 1) * (degree + 1), RW = K * 3;
+    const uint64_t n = (uint64_t)N * RW, blocks = (n + B8 - 1) / B8;
+    const float c2 = 1.0f - beta2;
+    for (uint32_t g = 0; g < N; ++g) {
+        if (first) variance[g] = grad_sq[g] * c2;
+        else if (grad_rows[g] != 0u) variance[g] = variance[g] * beta2 + grad_sq[g] * c2;
+    }
+    const float factor = 1.0f - beta1;
+    float m[B8];
+    float Y[25];
+    for (uint64_t b = 0; b < blocks; ++b) {
+        bool any = false;
+        for (uint32_t i = 0; i < B8 && !any; ++i) {
+            const uint64_t idx = b * B8 + i;
+            any = idx < n && grad_rows[idx / RW] != 0u;
+        }
+        if (!any) continue;
+        for (uint32_t i = 0; i < B8; ++i) {
+            const uint64_t idx = b * B8 + i;
+            m[i] = idx < n ? b8_get(codes, scales, idx) : 0.0f;
+            if (idx >= n) continue;
+            const uint64_t row = idx / RW;
+            const uint32_t gr = grad_rows[row];
+            if (gr == 0u) continue;
+            const uint32_t col = (uint32_t)(idx % RW), k = col / 3, c = col % 3;
+            const float* cd = color_dir + (uint64_t)gr * 6;
+            sh_basis(degree, v3(cd[3], cd[4], cd[5]), Y);
+            const float gv = Y[k] * cd[c];
+            const float moment = m[i] * beta1 + gv * factor;
+            const float denom = std::sqrt(variance[row] * inv2) + epsilon;
+            const float delta = (moment * inv1 / denom) * (lr_scale[col] * lr);
+            sh[idx] = f32_to_f16(stochastic_half(f16_to_f32(sh[idx]) - delta, (uint32_t)idx, round_seed));
+            m[i] = moment;
+        }
+        b8_pack(m, b, codes, scales);
+    }
+    return 0;
+}
+
 // ---- fused projection VJP + Adam, bwd/kernels/project_update.rs:40-178 ------------
 extern "C" int or_project_update(const or_fwd* f, const float* v_combined, float* transforms, float* raw_opac,
                                  uint32_t* w_t, const float* lr_scale, uint32_t* w_o, const or_adam* a,

@@ -114,6 +114,24 @@ uint32_t or_mix_hash(uint32_t index, uint32_t step);
 void or_adam_packed(float* param, uint32_t* word, uint32_t index, float g, float lr, const or_adam* adam,
                     uint32_t seed);
 
+/* IEEE binary16 conversions (round to nearest even) and the SH step's
+ * stochastic f16 rounding (crates/splat-train/src/quant_kernels.rs:866-894). */
+uint16_t or_f32_to_f16(float f);
+float or_f16_to_f32(uint16_t h);
+float or_stochastic_half(float value, uint32_t index, uint32_t step);
+/* Block-scaled 8-bit moment codec (crates/splat-train/src/quant.rs,
+ * quant_kernels.rs:438-498, 911-925): ceil(n/128) scales, ceil(n/128)*32 words. */
+void or_block8_encode(const float* values, uint64_t n, uint32_t* codes, float* scales);
+void or_block8_decode(const uint32_t* codes, const float* scales, uint64_t n, float* values);
+void or_block8_zero_rows(uint32_t* codes, uint64_t n, const uint32_t* rows, uint32_t num_rows, uint32_t row_width);
+/* The trainer's SH step (optim.rs:391-498, quant_kernels.rs:582-727) on f16
+ * coefficients sh [N,K,3] from color_dir [rows,6]; grad_rows [N] (0 = culled),
+ * grad_sq [N]; variance [N], codes and scales updated in place. */
+int or_sh_step(uint16_t* sh, uint32_t N, uint32_t degree, const float* color_dir, const uint32_t* grad_rows,
+               const float* grad_sq, float* variance, uint32_t* codes, float* scales, const float* lr_scale,
+               float beta1, float beta2, float inv1, float inv2, float epsilon, float lr,
+               uint32_t round_seed, int first);
+
 /* ImageLossConfig (crates/splat-train-loss/src/lib.rs:1227-1260). ssim_weight
  * multiplies SSIM itself (negative for a training loss). */
 typedef struct or_loss_cfg {

@@ -12,15 +12,17 @@ from .loss import (  # noqa: F401
 )
 from .camera import Camera, KannalaBrandt4, PINHOLE, fov_to_focal, focal_to_fov, max_render_theta  # noqa: F401
 from .render import (  # noqa: F401
-    Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput, SplatGrads,
-    SplatRenderMode, geo_decode, geo_encode, geo_zero_rows, l1_cotangent, prefix_sum, project_update, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
-    radix_argsort_with_count, render, render_backward, scan_in_place, sh_degree_from_coeffs, unpack_rgba8,
+    Block8Moment, Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput,
+    ShStepState, SplatGrads, SplatRenderMode, adam_bias_corrections, geo_decode, geo_encode, geo_zero_rows,
+    l1_cotangent, prefix_sum, project_update, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
+    radix_argsort_with_count, render, render_backward, scan_in_place, sh_degree_from_coeffs, sh_step, unpack_rgba8,
 )
 
 __all__ = [
     "ImageLossConfig", "image_loss", "image_loss_backward", "image_loss_eval", "image_loss_forward_train",
     "image_loss_partials", "pack_rgba8",
     "Camera", "KannalaBrandt4", "PINHOLE", "fov_to_focal", "focal_to_fov", "max_render_theta",
+    "Block8Moment", "ShStepState", "adam_bias_corrections", "sh_step",
     "Context", "ForwardState", "FusedAdam", "ProjectUpdateResult", "RasterPass", "RenderAux", "RenderOutput",
     "SplatGrads", "SplatRenderMode", "VsError", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",
     "prefix_sum", "project_update", "radix_argsort", "radix_argsort_skip_low_with_count",

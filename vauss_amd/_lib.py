@@ -15,6 +15,7 @@ import torch  # noqa: F401  (loads the HIP runtime torch was built with first)
 LIB_PATH = Path(__file__).resolve().parent / "libvsplat.so"
 
 VS_OK, VS_ERR_INVALID, VS_ERR_HIP, VS_ERR_OOM, VS_ERR_UNSUPPORTED, VS_ERR_CAPACITY, VS_ERR_NONFINITE = range(7)
+VS_SH_F32, VS_SH_F16 = 0, 1
 STATUS_NAMES = ["VS_OK", "VS_ERR_INVALID", "VS_ERR_HIP", "VS_ERR_OOM", "VS_ERR_UNSUPPORTED",
                 "VS_ERR_CAPACITY", "VS_ERR_NONFINITE"]
 
@@ -40,7 +41,13 @@ class VsPose(C.Structure):
 
 class VsSplats(C.Structure):
     _fields_ = [("transforms", C.c_void_p), ("sh_coeffs", C.c_void_p), ("raw_opacities", C.c_void_p),
-                ("num_splats", C.c_uint32), ("sh_degree", C.c_uint32), ("log_scale_offset", C.c_float)]
+                ("num_splats", C.c_uint32), ("sh_degree", C.c_uint32), ("log_scale_offset", C.c_float),
+                ("sh_dtype", C.c_uint32)]
+
+
+class VsShStepParams(C.Structure):
+    _fields_ = [("beta1", C.c_float), ("beta2", C.c_float), ("inv1", C.c_float), ("inv2", C.c_float),
+                ("epsilon", C.c_float), ("lr", C.c_float), ("round_seed", C.c_uint32), ("first", C.c_uint32)]
 
 
 class VsFwdOut(C.Structure):
@@ -108,6 +115,11 @@ SIGNATURES = {
     "vs_geo_encode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_float, C.c_void_p]),
     "vs_geo_decode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_float, C.c_void_p, C.c_void_p]),
     "vs_geo_zero_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint32, C.c_uint32]),
+    "vs_block8_encode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
+    "vs_block8_decode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
+    "vs_block8_zero_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32]),
+    "vs_sh_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(VsShStepParams)]),
     "vs_radix_argsort_u32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32,
                                        C.c_uint32, C.c_void_p, C.c_void_p]),
     "vs_radix_argsort_u64": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,

@@ -64,7 +64,7 @@ struct vs_ctx {
 struct vs_fwd_state {
     vs_ctx* ctx = nullptr;
     vs_camera cam{};
-    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0;
+    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0, sh_half = 0;
     float lso = 0.0f;
     float bg[3] = {0, 0, 0};
     vs_pass pass = VS_PASS_FORWARD;
@@ -113,6 +113,8 @@ bool pass_bwd_info(vs_pass p) { return p != VS_PASS_FORWARD; }
 vs_status check_splats(const vs_splats* sp) {
     if (!sp) return fail(VS_ERR_INVALID, "splats is null");
     if (sp->sh_degree > 4) return fail(VS_ERR_INVALID, "SH degree must be 0..4 (1, 4, 9, 16 or 25 coefficients)");
+    if (sp->sh_dtype != VS_SH_F32 && sp->sh_dtype != VS_SH_F16)
+        return fail(VS_ERR_INVALID, "SH coefficients must use f16 or f32");
     if (sp->num_splats > 0 && (!sp->transforms || !sp->sh_coeffs || !sp->raw_opacities))
         return fail(VS_ERR_INVALID, "splat parameter pointer is null");
     if (((uintptr_t)sp->transforms & 7u) != 0) return fail(VS_ERR_INVALID, "transforms must be 8-byte aligned");
@@ -231,6 +233,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->cam = *cam;
     st->W = W; st->H = H; st->N = sp->num_splats; st->degree = sp->sh_degree;
     st->K = (sp->sh_degree + 1) * (sp->sh_degree + 1);
+    st->sh_half = sp->sh_dtype == VS_SH_F16 ? 1u : 0u;
     st->lso = sp->log_scale_offset;
     st->bg[0] = background[0]; st->bg[1] = background[1]; st->bg[2] = background[2];
     st->pass = pass;
@@ -281,7 +284,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.cam = *cam;
         pa.img_w = W; pa.img_h = H; pa.tile_bw = st->tbw; pa.tile_bh = st->tbh;
         pa.num_splats = N; pa.sh_degree = sp->sh_degree; pa.log_scale_offset = sp->log_scale_offset;
-        pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.raw_opac = sp->raw_opacities;
+        pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.raw_opac = sp->raw_opacities;
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
         pa.proj_aux = st->proj_aux; pa.compact = st->compact; pa.block_stats = st->block_stats;
@@ -399,7 +402,8 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
     vs_status vst = check_splats(sp);
     if (vst != VS_OK) return vst;
-    if (sp->num_splats != st->N || sp->sh_degree != st->degree) return fail(VS_ERR_INVALID, "splats differ from the forward's");
+    if (sp->num_splats != st->N || sp->sh_degree != st->degree || (sp->sh_dtype == VS_SH_F16) != (st->sh_half != 0))
+        return fail(VS_ERR_INVALID, "splats differ from the forward's");
     if (((uintptr_t)out_img & 15u) || ((uintptr_t)v_out & 15u)) return fail(VS_ERR_INVALID, "images must be 16-byte aligned");
     if (grads->v_transforms && ((uintptr_t)grads->v_transforms & 7u)) return fail(VS_ERR_INVALID, "v_transforms must be 8-byte aligned");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
@@ -434,7 +438,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
         StageTimer tm(ctx, ST_PROJECT_BWD);
         ProjectBwdArgs pb{};
         pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = sp->log_scale_offset;
-        pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.raw_opac = sp->raw_opacities;
+        pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.sh_half = st->sh_half; pb.raw_opac = sp->raw_opacities;
         pb.counts = st->counts; pb.v_combined = vc;
         pb.v_transforms = grads->v_transforms; pb.v_sh = grads->v_sh_coeffs;
         pb.v_raw_opac = grads->v_raw_opacities; pb.v_refine = grads->v_refine_weight;
@@ -444,7 +448,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     return VS_OK;
 }
 
-extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* transforms, const float* sh_coeffs,
+extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* transforms, const void* sh_coeffs,
                                        float* raw_opacities, const float* v_combined, uint32_t* w_t,
                                        const float* lr_scale, uint32_t* w_o, const vs_adam_step* adam,
                                        vs_update_out* out) {
@@ -461,12 +465,68 @@ extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* tra
     StageTimer tm(ctx, ST_PROJECT_BWD);
     ProjectUpdateArgs pu{};
     pu.cam = st->cam; pu.num_splats = N; pu.sh_degree = st->degree; pu.log_scale_offset = st->lso;
-    pu.transforms = transforms; pu.sh = sh_coeffs; pu.raw_opac = raw_opacities; pu.compact = st->compact;
+    pu.transforms = transforms; pu.sh = sh_coeffs; pu.sh_half = st->sh_half; pu.raw_opac = raw_opacities; pu.compact = st->compact;
     pu.v_combined = v_combined; pu.w_t = w_t; pu.lr_scale = lr_scale; pu.w_o = w_o;
     pu.beta1 = adam->beta1; pu.beta2 = adam->beta2; pu.inv1 = adam->inv1; pu.inv2 = adam->inv2;
     pu.epsilon = adam->epsilon; pu.lr_opac = adam->lr_opac; pu.opac_reg = adam->opac_reg; pu.round_seed = adam->round_seed;
     pu.color_dir = out->color_dir; pu.v_refine = out->v_refine_weight; pu.grad_sq = out->coeffs_grad_sq;
     VS_HIP(launch_project_update(pu, ctx->stream), "project update");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_block8_encode(vs_ctx* ctx, const float* values, uint32_t n, uint32_t* codes, float* scales) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (n == 0) return VS_OK;
+    if (!values || !codes || !scales) return fail(VS_ERR_INVALID, "null buffer");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_b8_encode(values, n, codes, scales, ctx->stream), "block8 encode");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_block8_decode(vs_ctx* ctx, const uint32_t* codes, const float* scales, uint32_t n,
+                                      float* values) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (n == 0) return VS_OK;
+    if (!values || !codes || !scales) return fail(VS_ERR_INVALID, "null buffer");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_b8_decode(codes, scales, n, values, ctx->stream), "block8 decode");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_block8_zero_rows(vs_ctx* ctx, uint32_t* codes, uint32_t n, const uint32_t* rows,
+                                         uint32_t num_rows, uint32_t row_width) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if ((uint64_t)num_rows * row_width == 0 || n == 0) return VS_OK;
+    if (!codes || !rows) return fail(VS_ERR_INVALID, "null buffer");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_b8_zero_rows(codes, n, rows, num_rows, row_width, ctx->stream), "block8 zero rows");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_sh_step(vs_ctx* ctx, uint16_t* sh_coeffs, uint32_t num_splats, uint32_t sh_degree,
+                                const float* color_dir, const uint32_t* grad_rows, const float* grad_sq,
+                                float* variance, uint32_t* codes, float* scales, const float* lr_scale,
+                                const vs_sh_step_params* p) {
+    if (!ctx || !p) return fail(VS_ERR_INVALID, "null argument");
+    if (sh_degree > 4) return fail(VS_ERR_INVALID, "SH degree must be 0..4 (1, 4, 9, 16 or 25 coefficients)");
+    if (num_splats == 0) return VS_OK;
+    const uint64_t values = (uint64_t)num_splats * (sh_degree + 1) * (sh_degree + 1) * 3;
+    if (values > 0xFFFFFF00ull) return fail(VS_ERR_INVALID, "too many SH values for 32-bit value indices");
+    if (!sh_coeffs || !color_dir || !grad_rows || !grad_sq || !variance || !codes || !scales || !lr_scale)
+        return fail(VS_ERR_INVALID, "null buffer");
+    if (((uintptr_t)sh_coeffs & 7u) || ((uintptr_t)codes & 3u) || ((uintptr_t)scales & 3u))
+        return fail(VS_ERR_INVALID, "sh_coeffs must be 8-byte aligned, codes and scales 4-byte aligned");
+    if (!(p->epsilon > 0.0f)) return fail(VS_ERR_INVALID, "Adam epsilon must be positive");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    StageTimer tm(ctx, ST_OTHER);
+    ShStepArgs a{};
+    a.num_splats = num_splats; a.sh_degree = sh_degree;
+    a.num_values = (uint32_t)values; a.num_blocks = (uint32_t)((values + 127) / 128);
+    a.sh = sh_coeffs; a.color_dir = color_dir; a.grad_rows = grad_rows; a.grad_sq = grad_sq;
+    a.variance = variance; a.codes = codes; a.scales = scales; a.lr_scale = lr_scale;
+    a.beta1 = p->beta1; a.beta2 = p->beta2; a.inv1 = p->inv1; a.inv2 = p->inv2; a.epsilon = p->epsilon; a.lr = p->lr;
+    a.round_seed = p->round_seed; a.first = p->first ? 1u : 0u;
+    VS_HIP(launch_sh_step(a, ctx->stream), "SH step");
     return VS_OK;
 }
 

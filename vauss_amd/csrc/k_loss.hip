@@ -283,15 +283,34 @@ __global__ void __launch_bounds__(LBLOCK) loss_bwd_kernel(LossBwdArgs a) {
 }
 
 // Sum of the partials in one fixed order (per-lane strided sums, then a tree).
-__global__ void __launch_bounds__(LBLOCK) loss_total_kernel(const float* __restrict__ partials, uint32_t n,
-                                                            float* __restrict__ total) {
-    __shared__ float s[LBLOCK];
-    float acc = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += LBLOCK) acc += partials[i];
-    s[threadIdx.x] = acc;
+// The total of the weighted tile partials: one 1024-lane block, four
+// independent loads in flight per lane, then a wave64 butterfly and a
+// 16-entry LDS sum.  The summation order is fixed but differs from the tile
+// tree's; the total is a convenience (the partials are the exact outputs).
+constexpr int TOTAL_BLOCK = 1024;
+__global__ void __launch_bounds__(TOTAL_BLOCK) loss_total_kernel(const float* __restrict__ partials, uint32_t n,
+                                                                 float* __restrict__ total) {
+    __shared__ float s[TOTAL_BLOCK / 64];
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    uint32_t i = threadIdx.x;
+    for (; i + 3u * TOTAL_BLOCK < n; i += 4u * TOTAL_BLOCK) {
+        a0 += partials[i];
+        a1 += partials[i + TOTAL_BLOCK];
+        a2 += partials[i + 2u * TOTAL_BLOCK];
+        a3 += partials[i + 3u * TOTAL_BLOCK];
+    }
+    for (; i < n; i += TOTAL_BLOCK) a0 += partials[i];
+    float v = (a0 + a1) + (a2 + a3);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63u) == 0u) s[threadIdx.x >> 6] = v;
     __syncthreads();
-    const float t = tile_tree(s);
-    if (threadIdx.x == 0) *total = t;
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < TOTAL_BLOCK / 64; ++w) t += s[w];
+        *total = t;
+    }
 }
 
 template <bool C, bool M, bool A>
@@ -315,7 +334,7 @@ hipError_t launch_loss_forward(const LossArgs& a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !a.total || !a.partials) return e;
     const uint32_t planes = alpha ? 4u : 3u;
-    loss_total_kernel<<<1, LBLOCK, 0, s>>>(a.partials, planes * grid.x * grid.y, a.total);
+    loss_total_kernel<<<1, TOTAL_BLOCK, 0, s>>>(a.partials, planes * grid.x * grid.y, a.total);
     return hipGetLastError();
 }
 

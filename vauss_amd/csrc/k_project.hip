@@ -151,11 +151,41 @@ __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __
     }
 }
 
+// A splat's SH row as f32: f32 rows in float4 loads where the row size
+// allows; f16 rows (raw binary16) in 16- or 8-byte loads where it allows.
 template <int DEG>
-VS_DEV F3 load_color(const float* __restrict__ sh, uint32_t g, F3 mean, const vs_camera& u) {
+VS_DEV void load_sh_row(const uint16_t* __restrict__ sh, uint32_t g, float* c) {
+    constexpr int N = sh_count<DEG>() * 3;
+    const uint16_t* row = sh + (size_t)g * N;
+    if constexpr (N % 8 == 0) {
+        const uint4* r = reinterpret_cast<const uint4*>(row);
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) {
+            const uint4 q = r[i];
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                c[8 * i + 2 * j] = h2f((uint16_t)(w[j] & 0xFFFFu));
+                c[8 * i + 2 * j + 1] = h2f((uint16_t)(w[j] >> 16));
+            }
+        }
+    } else if constexpr (N % 4 == 0) {
+        const uint2* r = reinterpret_cast<const uint2*>(row);
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const uint2 q = r[i];
+            c[4 * i] = h2f((uint16_t)(q.x & 0xFFFFu)); c[4 * i + 1] = h2f((uint16_t)(q.x >> 16));
+            c[4 * i + 2] = h2f((uint16_t)(q.y & 0xFFFFu)); c[4 * i + 3] = h2f((uint16_t)(q.y >> 16));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) c[i] = h2f(row[i]);
+    }
+}
+template <int DEG>
+VS_DEV void load_sh_row(const float* __restrict__ sh, uint32_t g, float* c) {
     constexpr int K = sh_count<DEG>();
     const float* row = sh + (size_t)g * (K * 3);
-    float c[K * 3];
     if constexpr ((K * 3) % 4 == 0) {
         const float4* r4 = reinterpret_cast<const float4*>(row);
 #pragma unroll
@@ -167,6 +197,12 @@ VS_DEV F3 load_color(const float* __restrict__ sh, uint32_t g, F3 mean, const vs
 #pragma unroll
         for (int i = 0; i < K * 3; ++i) c[i] = row[i];
     }
+}
+
+template <int DEG, typename SHT>
+VS_DEV F3 load_color(const SHT* __restrict__ sh, uint32_t g, F3 mean, const vs_camera& u) {
+    float c[sh_count<DEG>() * 3];
+    load_sh_row<DEG>(sh, g, c);
     // kernels/project_visible.rs:25-61
     const F3 v = normalize(mean - F3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
     const F3 raw = sh_color<DEG>(c, v);
@@ -176,7 +212,7 @@ VS_DEV F3 load_color(const float* __restrict__ sh, uint32_t g, F3 mean, const vs
               clampf(finite(b) ? b : 0.0f, -100.0f, 100.0f)};
 }
 
-template <int DEG, int MODEL, bool GEOM>
+template <int DEG, int MODEL, bool GEOM, typename SHT>
 __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
     const vs_camera& u = a.cam;
     const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
@@ -226,7 +262,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             dbits = as_u(mc.z);
             visible = true;
             // Projected row (kernels/project_visible.rs:150-173), written at the global id.
-            const F3 col = load_color<DEG>(a.sh, g, mean, u);
+            const F3 col = load_color<DEG>(static_cast<const SHT*>(a.sh), g, mean, u);
             a.proj_a[g] = make_float4(px, py, conic.c00, conic.c01);
             a.proj_b[g] = make_float4(conic.c11, opac, col.x, col.y);
             a.proj_c[g] = col.z;
@@ -416,15 +452,20 @@ hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint3
     return hipGetLastError();
 }
 
-template <int DEG, int MODEL>
+template <int DEG, int MODEL, typename SHT>
 static void launch_project_geom(const ProjectArgs& a, dim3 grid, hipStream_t s, bool geom) {
-    if (geom) project_kernel<DEG, MODEL, true><<<grid, PROJ_BLOCK, 0, s>>>(a);
-    else project_kernel<DEG, MODEL, false><<<grid, PROJ_BLOCK, 0, s>>>(a);
+    if (geom) project_kernel<DEG, MODEL, true, SHT><<<grid, PROJ_BLOCK, 0, s>>>(a);
+    else project_kernel<DEG, MODEL, false, SHT><<<grid, PROJ_BLOCK, 0, s>>>(a);
+}
+template <int DEG, int MODEL>
+static void launch_project_type(const ProjectArgs& a, dim3 grid, hipStream_t s, bool geom) {
+    if (a.sh_half) launch_project_geom<DEG, MODEL, uint16_t>(a, grid, s, geom);
+    else launch_project_geom<DEG, MODEL, float>(a, grid, s, geom);
 }
 template <int DEG>
 static void launch_project_model(const ProjectArgs& a, dim3 grid, hipStream_t s, bool geom) {
-    if (a.cam.model == VS_CAMERA_KB4) launch_project_geom<DEG, VS_CAMERA_KB4>(a, grid, s, geom);
-    else launch_project_geom<DEG, VS_CAMERA_PINHOLE>(a, grid, s, geom);
+    if (a.cam.model == VS_CAMERA_KB4) launch_project_type<DEG, VS_CAMERA_KB4>(a, grid, s, geom);
+    else launch_project_type<DEG, VS_CAMERA_PINHOLE>(a, grid, s, geom);
 }
 
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s) {

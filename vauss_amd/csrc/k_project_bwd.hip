@@ -14,7 +14,7 @@ namespace vs {
 
 constexpr int PBWD_BLOCK = 256;
 
-template <int DEG, int MODEL>
+template <int DEG, int MODEL, typename SHT>
 __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs a) {
     constexpr int K = sh_count<DEG>();
     const uint32_t g = blockIdx.x * PBWD_BLOCK + threadIdx.x;
@@ -47,7 +47,7 @@ __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs 
     const F3 mean{t01.x, t01.y, t23.x};
     const F3 scl{expf_c(t67.y + lso), expf_c(t89.x + lso), expf_c(t89.y + lso)};
     const Qt qu{t23.y, t45.x, t45.y, t67.x};
-    const SplatVjp r = splat_vjp<DEG, MODEL>(u, a.sh + (size_t)g * K * 3, mean, scl, qu, a.raw_opac[g], rg);
+    const SplatVjp r = splat_vjp<DEG, MODEL>(u, static_cast<const SHT*>(a.sh) + (size_t)g * K * 3, mean, scl, qu, a.raw_opac[g], rg);
     if (vsh) {
         // sh.rs:281-359: v_coeff_k = Y_k(v) v_colour
         float Y[K];
@@ -71,10 +71,15 @@ __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs 
     }
 }
 
+template <int DEG, typename SHT>
+static void launch_pbwd_type(const ProjectBwdArgs& a, dim3 grid, hipStream_t s) {
+    if (a.cam.model == VS_CAMERA_KB4) project_bwd_kernel<DEG, VS_CAMERA_KB4, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a);
+    else project_bwd_kernel<DEG, VS_CAMERA_PINHOLE, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a);
+}
 template <int DEG>
 static void launch_pbwd_model(const ProjectBwdArgs& a, dim3 grid, hipStream_t s) {
-    if (a.cam.model == VS_CAMERA_KB4) project_bwd_kernel<DEG, VS_CAMERA_KB4><<<grid, PBWD_BLOCK, 0, s>>>(a);
-    else project_bwd_kernel<DEG, VS_CAMERA_PINHOLE><<<grid, PBWD_BLOCK, 0, s>>>(a);
+    if (a.sh_half) launch_pbwd_type<DEG, uint16_t>(a, grid, s);
+    else launch_pbwd_type<DEG, float>(a, grid, s);
 }
 
 hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s) {

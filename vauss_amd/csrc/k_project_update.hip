@@ -18,7 +18,7 @@ namespace vs {
 
 constexpr int PUPD_BLOCK = 256;
 
-template <int DEG, int MODEL>
+template <int DEG, int MODEL, typename SHT>
 __global__ void __launch_bounds__(PUPD_BLOCK) project_update_kernel(ProjectUpdateArgs a) {
     constexpr int K = sh_count<DEG>();
     const uint32_t g = blockIdx.x * PUPD_BLOCK + threadIdx.x;
@@ -50,7 +50,7 @@ __global__ void __launch_bounds__(PUPD_BLOCK) project_update_kernel(ProjectUpdat
             const F3 mean{t[0], t[1], t[2]};
             const F3 scl{expf_c(t[7] + lso), expf_c(t[8] + lso), expf_c(t[9] + lso)};
             const Qt qu{t[3], t[4], t[5], t[6]};
-            const SplatVjp r = splat_vjp<DEG, MODEL>(a.cam, a.sh + (size_t)g * K * 3, mean, scl, qu, raw, rg);
+            const SplatVjp r = splat_vjp<DEG, MODEL>(a.cam, static_cast<const SHT*>(a.sh) + (size_t)g * K * 3, mean, scl, qu, raw, rg);
             if (cd) {
                 cd[0] = rg[5]; cd[1] = rg[6]; cd[2] = rg[7];
                 cd[3] = r.vdir.x; cd[4] = r.vdir.y; cd[5] = r.vdir.z;
@@ -127,10 +127,15 @@ __global__ void geo_zero_rows_kernel(uint32_t* __restrict__ words, const uint32_
     if (idx < num_words) words[idx] = 0u;
 }
 
+template <int DEG, typename SHT>
+static void launch_pupd_type(const ProjectUpdateArgs& a, dim3 grid, hipStream_t s) {
+    if (a.cam.model == VS_CAMERA_KB4) project_update_kernel<DEG, VS_CAMERA_KB4, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a);
+    else project_update_kernel<DEG, VS_CAMERA_PINHOLE, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a);
+}
 template <int DEG>
 static void launch_pupd_model(const ProjectUpdateArgs& a, dim3 grid, hipStream_t s) {
-    if (a.cam.model == VS_CAMERA_KB4) project_update_kernel<DEG, VS_CAMERA_KB4><<<grid, PUPD_BLOCK, 0, s>>>(a);
-    else project_update_kernel<DEG, VS_CAMERA_PINHOLE><<<grid, PUPD_BLOCK, 0, s>>>(a);
+    if (a.sh_half) launch_pupd_type<DEG, uint16_t>(a, grid, s);
+    else launch_pupd_type<DEG, float>(a, grid, s);
 }
 
 hipError_t launch_project_update(const ProjectUpdateArgs& a, hipStream_t s) {

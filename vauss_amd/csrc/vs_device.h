@@ -24,6 +24,10 @@ constexpr float ALPHA_CAP = 0.999f;             // kernels/rasterize.rs:313
 VS_DEV uint32_t as_u(float x) { return __float_as_uint(x); }
 VS_DEV float as_f(uint32_t u) { return __uint_as_float(u); }
 VS_DEV bool finite(float x) { return ((as_u(x) >> 23) & 0xFFu) != 0xFFu; }
+// IEEE binary16 <-> f32: widening is exact; narrowing rounds to nearest even
+// (f16 subnormals kept, overflow to infinity).
+VS_DEV float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+VS_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 // Min/max/clamp with the semantics of Rust's f32::min/max on NaN (return
 // the other operand), written out so the result never depends on the

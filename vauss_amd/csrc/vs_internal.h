@@ -41,7 +41,8 @@ struct ProjectArgs {
     uint32_t num_splats, sh_degree;
     float log_scale_offset;
     const float* transforms;
-    const float* sh;
+    const void* sh;                  // [N,K,3] f32, or f16 bits when sh_half
+    uint32_t sh_half;
     const float* raw_opac;
     // outputs, indexed by global splat id
     float* opacities;           // [N]
@@ -109,7 +110,8 @@ struct ProjectBwdArgs {
     uint32_t num_splats, sh_degree;
     float log_scale_offset;
     const float* transforms;
-    const float* sh;
+    const void* sh;                  // [N,K,3] f32, or f16 bits when sh_half
+    uint32_t sh_half;
     const float* raw_opac;
     const uint32_t* counts;          // visible <=> counts defined; culled rows get zeros
     const float* v_combined;         // [N,10]
@@ -124,7 +126,8 @@ struct ProjectUpdateArgs {
     uint32_t num_splats, sh_degree;
     float log_scale_offset;
     float* transforms;               // [N,10] stepped in place
-    const float* sh;
+    const void* sh;                  // [N,K,3] f32, or f16 bits when sh_half
+    uint32_t sh_half;
     float* raw_opac;                 // [N] stepped in place
     const uint32_t* compact;         // [N] g + 1 if visible, else 0
     const float* v_combined;         // [N,10]
@@ -163,6 +166,21 @@ struct LossBwdArgs {
     float rgb_weight, alpha_weight;
 };
 
+struct ShStepArgs {
+    uint32_t num_splats, sh_degree;
+    uint32_t num_values, num_blocks;     // N*K*3 and ceil(num_values / 128)
+    uint16_t* sh;                        // [N,K,3] f16 bits, stepped in place
+    const float* color_dir;              // [rows,6] colour gradient + view direction, row 0 zero
+    const uint32_t* grad_rows;           // [N] row of color_dir per splat, 0 = culled
+    const float* grad_sq;                // [N]
+    float* variance;                     // [N] second moment, updated in place
+    uint32_t* codes;                     // [num_blocks*32] biased 8-bit first-moment codes
+    float* scales;                       // [num_blocks]
+    const float* lr_scale;               // [K*3]
+    float beta1, beta2, inv1, inv2, epsilon, lr;
+    uint32_t round_seed, first;
+};
+
 // ---- launchers (return hipError_t of the launch) -------------------------------
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
 // Reduces the projection's block stats into `counters` and turns the block
@@ -185,6 +203,11 @@ hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float
                                float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
 hipError_t launch_loss_forward(const LossArgs& a, hipStream_t s);
 hipError_t launch_loss_backward(const LossBwdArgs& a, bool scalar, hipStream_t s);
+hipError_t launch_sh_step(const ShStepArgs& a, hipStream_t s);
+hipError_t launch_b8_encode(const float* values, uint32_t n, uint32_t* codes, float* scales, hipStream_t s);
+hipError_t launch_b8_decode(const uint32_t* codes, const float* scales, uint32_t n, float* values, hipStream_t s);
+hipError_t launch_b8_zero_rows(uint32_t* codes, uint32_t n, const uint32_t* rows, uint32_t num_rows,
+                               uint32_t row_width, hipStream_t s);
 hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float mr, uint32_t* out, hipStream_t s);
 
 // Scans.  `tmp` needs scan_tmp_words(n) u32 words.  With a permutation `perm`

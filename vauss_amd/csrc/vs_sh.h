@@ -51,6 +51,10 @@ VS_DEV void sh_basis(F3 v, float* Y) {
 
 template <int DEG> constexpr int sh_count() { return (DEG + 1) * (DEG + 1); }
 
+// One coefficient of an f32 or f16 (raw binary16 bits) row, as f32.
+VS_DEV float sh_ld(const float* __restrict__ p, int i) { return p[i]; }
+VS_DEV float sh_ld(const uint16_t* __restrict__ p, int i) { return h2f(p[i]); }
+
 // sh.rs:51-140 -- colour = c_0 C0 + sum_k c_k Y_k, terms added in order.
 template <int DEG>
 VS_DEV F3 sh_color(const float* __restrict__ c, F3 v) {
@@ -63,9 +67,9 @@ VS_DEV F3 sh_color(const float* __restrict__ c, F3 v) {
 }
 
 // sh.rs:147-274 -- d colour . vc / d v.
-template <int DEG>
-VS_DEV F3 sh_viewdir_vjp(const float* __restrict__ cb, F3 v, F3 vc) {
-    auto co = [&](int k) { return F3{cb[3 * k], cb[3 * k + 1], cb[3 * k + 2]}; };
+template <int DEG, typename T>
+VS_DEV F3 sh_viewdir_vjp(const T* __restrict__ cb, F3 v, F3 vc) {
+    auto co = [&](int k) { return F3{sh_ld(cb, 3 * k), sh_ld(cb, 3 * k + 1), sh_ld(cb, 3 * k + 2)}; };
     float gx = 0.0f, gy = 0.0f, gz = 0.0f;
     if constexpr (DEG >= 1) {
         const float f0a = 0.4886025f;

@@ -51,8 +51,8 @@ struct SplatVjp {
 };
 
 // rg: the splat's raster gradients [xy(2), conic(3), rgb(3), opacity, refine].
-template <int DEG, int MODEL>
-VS_DEV SplatVjp splat_vjp(const vs_camera& u, const float* __restrict__ sh_row, F3 mean, F3 scl, Qt qu, float raw,
+template <int DEG, int MODEL, typename SHT>
+VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3 mean, F3 scl, Qt qu, float raw,
                           const float rg[10]) {
     const Qt q = normalize(qu);
     const float opac_sig = sigmoid(raw);

@@ -22,6 +22,7 @@ import math
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -186,9 +187,13 @@ def _check_splats(transforms, sh_coeffs, raw_opacities):
         raise ValueError(f"sh_coeffs must be [N, C, 3], got {tuple(sh_coeffs.shape)}")
     if raw_opacities.dim() != 1 or raw_opacities.shape[0] != n:
         raise ValueError(f"raw_opacities must be [N], got {tuple(raw_opacities.shape)}")
-    for name, t in (("transforms", transforms), ("sh_coeffs", sh_coeffs), ("raw_opacities", raw_opacities)):
+    for name, t in (("transforms", transforms), ("raw_opacities", raw_opacities)):
         if t.dtype != torch.float32:
             raise TypeError(f"{name} must be float32, got {t.dtype}")
+    # render.rs:683-687: SH coefficients in f32 or f16.
+    if sh_coeffs.dtype not in (torch.float32, torch.float16):
+        raise TypeError(f"SH coefficients must use f16 or f32, got {sh_coeffs.dtype}")
+    for name, t in (("transforms", transforms), ("sh_coeffs", sh_coeffs), ("raw_opacities", raw_opacities)):
         if not t.is_cuda:
             raise ValueError(f"{name} must live on the GPU")
     return n, sh_degree_from_coeffs(sh_coeffs.shape[1])
@@ -202,6 +207,7 @@ def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offse
     s.num_splats = transforms.shape[0]
     s.sh_degree = degree
     s.log_scale_offset = float(log_scale_offset)
+    s.sh_dtype = _lib.VS_SH_F16 if sh_coeffs.dtype == torch.float16 else _lib.VS_SH_F32
     return s
 
 
@@ -296,6 +302,27 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     return g
 
 
+def _powi_f32(a: float, b: int) -> np.float32:
+    """f32 a^b by binary exponentiation (Rust's f32::powi, lowered to
+    compiler-rt's __powisf2)."""
+    x, r, recip, b = np.float32(a), np.float32(1.0), b < 0, abs(b)
+    while True:
+        if b & 1:
+            r = np.float32(r * x)
+        b >>= 1
+        if b == 0:
+            break
+        x = np.float32(x * x)
+    return np.float32(1.0) / r if recip else r
+
+
+def adam_bias_corrections(step: int, beta1: float, beta2: float):
+    """AdamScaled::coefficients (crates/splat-train/src/optim.rs:269-277), in
+    f32: (1 / (1 - beta1^t), 1 / (1 - beta2^t))."""
+    one = np.float32(1.0)
+    return (float(one / (one - _powi_f32(beta1, step))), float(one / (one - _powi_f32(beta2, step))))
+
+
 @dataclass
 class FusedAdam:
     """FusedAdam, bwd/project_update.rs:232-250."""
@@ -312,8 +339,8 @@ class FusedAdam:
     def at_step(cls, step: int, lr_opac: float, beta1: float = 0.9, beta2: float = 0.999, epsilon: float = 1e-15,
                 opac_reg: float = 0.0) -> "FusedAdam":
         """Bias corrections of Adam step `step` (1-based); the step count seeds the rounding."""
-        return cls(beta1, beta2, 1.0 / (1.0 - beta1 ** step), 1.0 / (1.0 - beta2 ** step), epsilon, lr_opac,
-                   opac_reg, step)
+        inv1, inv2 = adam_bias_corrections(step, beta1, beta2)
+        return cls(beta1, beta2, inv1, inv2, epsilon, lr_opac, opac_reg, step)
 
 
 @dataclass
@@ -488,3 +515,109 @@ def unpack_rgba8(packed: torch.Tensor) -> torch.Tensor:
     """[H,W] packed RGBA8 (FORWARD pass) -> [H,W,4] uint8."""
     p = packed.to(torch.int64) & 0xFFFFFFFF
     return torch.stack([(p >> s) & 0xFF for s in (0, 8, 16, 24)], dim=-1).to(torch.uint8)
+
+
+# ---- the trainer's SH step: f16 coefficients, block-scaled 8-bit first moment ------
+
+BLOCK8_VALUES = 128
+
+
+@dataclass
+class Block8Moment:
+    """BlockMoment (crates/splat-train/src/quant.rs:30-160): `codes` [blocks*32]
+    int32 words of four biased 8-bit codes, `scales` [blocks] f32, for `n`
+    values in blocks of 128."""
+    codes: torch.Tensor
+    scales: torch.Tensor
+    n: int
+
+    @classmethod
+    def zeros(cls, n: int, device) -> "Block8Moment":
+        if n <= 0:
+            raise ValueError("cannot quantize an empty moment")
+        blocks = (n + BLOCK8_VALUES - 1) // BLOCK8_VALUES
+        return cls(torch.zeros(blocks * 32, dtype=torch.int32, device=device),
+                   torch.zeros(blocks, dtype=torch.float32, device=device), n)
+
+    @classmethod
+    def encode(cls, values: torch.Tensor) -> "Block8Moment":
+        v = values.contiguous().float().reshape(-1)
+        if v.numel() == 0:
+            raise ValueError("cannot quantize an empty moment")
+        m = cls.zeros(v.numel(), v.device)
+        ctx = Context.get(v.device)
+        _lib.check(ctx.lib.vs_block8_encode(ctx.handle, _ptr(v), v.numel(), _ptr(m.codes), _ptr(m.scales)))
+        return m
+
+    def decode(self) -> torch.Tensor:
+        out = torch.empty(self.n, dtype=torch.float32, device=self.codes.device)
+        ctx = Context.get(self.codes.device)
+        _lib.check(ctx.lib.vs_block8_decode(ctx.handle, _ptr(self.codes), _ptr(self.scales), self.n, _ptr(out)))
+        return out
+
+    def zero_rows(self, rows: torch.Tensor, row_width: int) -> "Block8Moment":
+        """reset_rows' zeroing (quant.rs:93-111): the listed rows' moments become 0, in place."""
+        rows = _u32(rows.contiguous(), "rows")
+        ctx = Context.get(self.codes.device)
+        _lib.check(ctx.lib.vs_block8_zero_rows(ctx.handle, _ptr(self.codes), self.n, _ptr(rows), rows.numel(),
+                                               int(row_width)))
+        return self
+
+
+@dataclass
+class ShStepState:
+    """The SH coefficients' optimizer state (MomentumState with split moments,
+    optim.rs:413-498): the Block8 first moment, the per-splat f32 variance and
+    the step count t (0 before the first step)."""
+    moment: Block8Moment
+    variance: torch.Tensor
+    time: int = 0
+
+    @classmethod
+    def fresh(cls, num_splats: int, sh_degree: int, device) -> "ShStepState":
+        k = (sh_degree + 1) ** 2
+        return cls(Block8Moment.zeros(num_splats * k * 3, device),
+                   torch.zeros(num_splats, dtype=torch.float32, device=device), 0)
+
+
+def sh_step(sh_coeffs: torch.Tensor, color_dir: torch.Tensor, compact_from_global: torch.Tensor,
+            grad_sq: torch.Tensor, state: ShStepState, lr: float, lr_scale: Optional[torch.Tensor] = None,
+            beta1: float = 0.9, beta2: float = 0.999, epsilon: float = 1e-15) -> torch.Tensor:
+    """AdamScaled::step_sh_color (optim.rs:391-498): one lazy Adam step of the
+    SH coefficients from project_update's `color_dir` and `coeffs_grad_sq`.
+    `sh_coeffs` [N,K,3] is f16 (stepped in place; an f32 tensor is first cast
+    to f16, as the reference's canonical half storage, and the f16 tensor is
+    returned).  `state` advances one step."""
+    if sh_coeffs.dim() != 3 or sh_coeffs.shape[2] != 3:
+        raise ValueError(f"sh_coeffs must be [N, C, 3], got {tuple(sh_coeffs.shape)}")
+    n, k = sh_coeffs.shape[0], sh_coeffs.shape[1]
+    degree = sh_degree_from_coeffs(k)
+    if sh_coeffs.dtype == torch.float32:
+        sh_coeffs = sh_coeffs.half()
+    elif sh_coeffs.dtype != torch.float16:
+        raise TypeError(f"SH coefficients must use f16 or f32, got {sh_coeffs.dtype}")
+    if not sh_coeffs.is_contiguous():
+        raise ValueError("sh_coeffs must be contiguous (it is stepped in place)")
+    dev = sh_coeffs.device
+    if color_dir.dim() != 2 or color_dir.shape[1] != 6 or color_dir.dtype != torch.float32:
+        raise ValueError("color_dir must be [rows, 6] float32")
+    rows = _u32(compact_from_global.contiguous(), "compact_from_global")
+    gsq = grad_sq.contiguous().float().reshape(-1)
+    if rows.numel() != n or gsq.numel() != n:
+        raise ValueError("compact_from_global and grad_sq must have one entry per splat")
+    if state.moment.n != n * k * 3 or state.variance.numel() != n:
+        raise ValueError("optimizer state does not match the coefficients")
+    if lr_scale is None:
+        lr_scale = torch.ones(k * 3, dtype=torch.float32, device=dev)
+    lr_scale = lr_scale.contiguous().float().reshape(-1)
+    if lr_scale.numel() != k * 3:
+        raise ValueError("lr_scale must hold one factor per coefficient value [K*3]")
+    t = state.time + 1
+    inv1, inv2 = adam_bias_corrections(t, beta1, beta2)
+    p = _lib.VsShStepParams(beta1, beta2, inv1, inv2, epsilon, lr, t & 0xFFFFFFFF, 1 if state.time == 0 else 0)
+    ctx = Context.get(dev)
+    _lib.check(ctx.lib.vs_sh_step(ctx.handle, _ptr(sh_coeffs), n, degree, _ptr(color_dir.contiguous()), _ptr(rows),
+                                  _ptr(gsq), _ptr(state.variance), _ptr(state.moment.codes),
+                                  _ptr(state.moment.scales), _ptr(lr_scale), C.byref(p)))
+    state.time = t
+    return sh_coeffs
