@@ -323,7 +323,7 @@ STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "r
 SUMMARY_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VALU_TRANS_F32",
                     "SQ_LDS_BANK_CONFLICT", "SQ_THREAD_CYCLES_VALU", "SQ_ACTIVE_INST_VALU", "TCC_ATOMIC_sum",
                     "TCC_EA0_ATOMIC_sum", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE", "WRITE_SIZE")
-SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "copyBuffer")
+SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "copyBuffer")
 
 
 def source_digest() -> str:

@@ -120,6 +120,20 @@ def test_forward_matches_float64(opts):
         assert abs(partials[1, t] - s) <= 1e-6 * abs(s) + 1e-9
 
 
+def test_anticorrelated_images_give_negative_ssim():
+    """pred = 1 - gt: SSIM is negative wherever the window has texture, and
+    the map follows the float64 SSIM with its [-1, 1] clamp."""
+    _, gt = make_case(seed=7, cn=3)
+    g = decode_gt(gt)[..., :3]
+    pred = (1.0 - g).astype(np.float32)
+    cfg = po.loss_cfg(0.0, 1.0)
+    _, _, lmap = po.image_loss_forward(pred, gt, cfg)
+    for c in range(3):
+        want = ssim64(pred[..., c].astype(np.float64), g[..., c])
+        np.testing.assert_allclose(lmap[..., c], want, rtol=0, atol=2e-5)
+    assert (lmap < -0.5).mean() > 0.5
+
+
 def test_ssim_of_identical_images_is_one():
     pred, gt = make_case(seed=2, cn=3)
     exact = (decode_gt(gt)[..., :3]).astype(np.float32)
