@@ -83,6 +83,9 @@ typedef struct vs_splats {
     uint32_t sh_degree;             /* 0..4 */
     float log_scale_offset;         /* added to every log-scale (render.rs:325) */
     uint32_t sh_dtype;              /* vs_sh_dtype */
+    const float* min_scale;         /* [N] scale floor (the Mip-Splatting 3D filter,
+                                       kernels/helpers.rs:497-553) or NULL for none
+                                       (render's min_scale / has_min_scale) */
 } vs_splats;
 
 /* RasterPass, crates/splat-train-render/src/gaussian_splats.rs:32-107. */
@@ -94,8 +97,9 @@ typedef enum vs_pass {
     VS_PASS_GEOMETRY = 4,           /* float [H,W,12]: RGBA, sum(w z), median z, normal, distortion, median id */
 } vs_pass;
 
-/* SplatRenderMode, gaussian_splats.rs:19-26.  Only DEFAULT is built; MIP and
- * SURFEL return VS_ERR_UNSUPPORTED. */
+/* SplatRenderMode, gaussian_splats.rs:19-26.  DEFAULT (+0.3 2-D blur) and MIP
+ * (+0.1 blur with opacity compensation, kernels/helpers.rs:227-245) are
+ * built; SURFEL returns VS_ERR_UNSUPPORTED. */
 typedef enum vs_render_mode { VS_MODE_DEFAULT = 0, VS_MODE_MIP = 1, VS_MODE_SURFEL = 2 } vs_render_mode;
 
 /* Forward outputs (RenderAux, crates/splat-train-render/src/render_aux.rs:74-100).
@@ -238,7 +242,8 @@ typedef struct vs_update_out {
  * (geo_moments.rs codec; zero words are reset moments).  `lr_scale` is the
  * per-column transforms learning rate [10] (device).  The parameters must be
  * the pre-step values the forward of `state` saw (`sh_coeffs` in the
- * forward's dtype).  Every splat steps: culled ones decay their moments with a
+ * forward's dtype; the render mode and the forward's `min_scale` array, which
+ * must still hold the same floors, apply).  Every splat steps: culled ones decay their moments with a
  * zero gradient plus the opacity regulariser. */
 vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* state, float* transforms, const void* sh_coeffs,
                             float* raw_opacities, const float* v_combined, uint32_t* w_t,

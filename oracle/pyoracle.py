@@ -20,7 +20,7 @@ HERE = Path(__file__).resolve().parent
 # mutated copy, to check that the tests catch the mistake).
 LIB_PATH = Path(os.environ.get("ORACLE_LIB", HERE / "liboracle.so"))
 
-FLAG_BWD_INFO, FLAG_GEOMETRY, FLAG_SMOOTH_CUTOFF, FLAG_BRUTE_FORCE = 1, 2, 4, 8
+FLAG_BWD_INFO, FLAG_GEOMETRY, FLAG_SMOOTH_CUTOFF, FLAG_BRUTE_FORCE, FLAG_MIP = 1, 2, 4, 8, 16
 (F_INTERSECT_COUNTS, F_MAX_RADIUS, F_OPACITIES, F_GLOBAL_FROM_COMPACT, F_DEPTHS, F_PROJECTED, F_AUX, F_ISECT_TILE,
  F_ISECT_GID, F_TILE_OFFSETS, F_TILE_OFFSETS_SHRUNK, F_VISIBLE, F_OUT_IMG) = range(13)
 
@@ -76,7 +76,7 @@ def load() -> C.CDLL:
     lib = C.CDLL(os.fspath(LIB_PATH))
     lib.or_render_forward.restype = C.c_int
     lib.or_render_forward.argtypes = [C.POINTER(OrCamera), C.c_uint32, C.c_uint32, _F, _F, C.c_uint32, _F, C.c_uint32,
-                                      C.c_float, _F, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+                                      C.c_float, _F, _F, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
     lib.or_fwd_get_info.argtypes = [C.c_void_p, C.POINTER(OrFwdInfo)]
     lib.or_fwd_get.restype = C.c_int
     lib.or_fwd_get.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
@@ -242,7 +242,8 @@ class OracleForward:
 
 
 def render_forward(cam, img_size, transforms, sh_coeffs, raw_opacities, background=(0, 0, 0), flags=FLAG_BWD_INFO,
-                   threads: int = 0, log_scale_offset: float = 0.0) -> OracleForward:
+                   threads: int = 0, log_scale_offset: float = 0.0, min_scale=None) -> OracleForward:
+    """`flags` may add FLAG_MIP (SplatRenderMode::Mip); `min_scale` [N] is the scale floor (None: none)."""
     lib = load()
     t = np.ascontiguousarray(transforms, np.float32)
     s = np.ascontiguousarray(sh_coeffs, np.float32)
@@ -252,8 +253,12 @@ def render_forward(cam, img_size, transforms, sh_coeffs, raw_opacities, backgrou
     bg = np.asarray(background, np.float32)
     c = camera_struct(cam)
     h = C.c_void_p()
+    ms = None if min_scale is None else np.ascontiguousarray(min_scale, np.float32)
+    if ms is not None and ms.shape != (n,):
+        raise ValueError("min_scale must hold one floor per splat")
     rc = lib.or_render_forward(C.byref(c), int(img_size[0]), int(img_size[1]), _fp(t), _fp(s), degree, _fp(o), n,
-                               float(log_scale_offset), _fp(bg), flags, threads, C.byref(h))
+                               float(log_scale_offset), None if ms is None else _fp(ms), _fp(bg), flags, threads,
+                               C.byref(h))
     if rc != 0:
         raise RuntimeError(f"oracle forward failed ({rc})")
     info = OrFwdInfo()

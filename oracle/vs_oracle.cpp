@@ -312,8 +312,37 @@ S2 calc_cov2d(V3 scale_, Q4 quat, V3 mean_c, const or_camera& u) {
     const float scale_down = (max_abs > lim) ? lim / max_abs : 1.0f;
     return s2_scale(raw, scale_down);
 }
-// kernels/helpers.rs:230-245 (Default mode: +0.3 blur, no compensation)
-S2 compensate_cov2d(S2 c) { return S2{c.c00 + 0.3f, c.c01, c.c11 + 0.3f}; }
+// compensate_cov2d, kernels/helpers.rs:227-245: +0.3 on the diagonal (Default)
+// or +0.1 with the compensation sqrt(max(det, 0) / det_blurred) (Mip).
+S2 compensate_cov2d(S2 c, bool mip, float& filter_comp) {
+    const float blur = mip ? 0.1f : 0.3f;
+    const S2 b{c.c00 + blur, c.c01, c.c11 + blur};
+    filter_comp = 1.0f;
+    if (mip) {
+        const float det_raw = fmax_(c.c00 * c.c11 - c.c01 * c.c01, 0.0f);
+        const float det_blurred = b.c00 * b.c11 - b.c01 * b.c01;
+        filter_comp = std::sqrt(det_raw / det_blurred);
+    }
+    return b;
+}
+
+// apply_scale_floor, kernels/helpers.rs:497-553: s' = sqrt(s^2 + f^2) per
+// axis, opacity sigmoid(raw) prod(s / s') clamped to [1e-6, 1 - 1e-6].
+struct ScaleFloor { V3 scale; float opac, coef; V3 ratio_sq; bool opac_open; };
+ScaleFloor apply_scale_floor(V3 s, float opac_sig, const float* min_scale, uint32_t g) {
+    ScaleFloor r{s, opac_sig, 1.0f, v3(1.0f, 1.0f, 1.0f), true};
+    if (min_scale) {
+        const float f = min_scale[g], f2 = f * f;
+        r.scale = v3(std::sqrt(s.x * s.x + f2), std::sqrt(s.y * s.y + f2), std::sqrt(s.z * s.z + f2));
+        const float rx = s.x / r.scale.x, ry = s.y / r.scale.y, rz = s.z / r.scale.z;
+        r.coef = rx * ry * rz;
+        r.ratio_sq = v3(rx * rx, ry * ry, rz * rz);
+        const float o = opac_sig * r.coef;
+        r.opac_open = o > 1.0e-6f && o < 1.0f - 1.0e-6f;
+        r.opac = clampf(o, 1.0e-6f, 1.0f - 1.0e-6f);
+    }
+    return r;
+}
 
 // kernels/helpers.rs:133-144
 void bbox_extent(S2 conic, float power, float& ex, float& ey) {
@@ -525,7 +554,9 @@ struct or_fwd {
     const float* transforms = nullptr;   // borrowed for the backward (caller keeps alive)
     const float* sh = nullptr;
     const float* raw_opac = nullptr;
-    std::vector<float> transforms_copy, sh_copy, opac_copy;
+    const float* min_scale = nullptr;    // NULL: no scale floor
+    bool mip = false;
+    std::vector<float> transforms_copy, sh_copy, opac_copy, min_scale_copy;
     uint32_t V = 0;
     uint64_t evals = 0;
     std::vector<uint32_t> intersect_counts;
@@ -551,7 +582,7 @@ extern "C" int or_max_threads(void) { return resolve_threads(0); }
 
 extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H,
                                  const float* transforms, const float* sh, uint32_t degree,
-                                 const float* raw_opac, uint32_t N, float lso,
+                                 const float* raw_opac, uint32_t N, float lso, const float* min_scale,
                                  const float bg[3], int flags, int threads, or_fwd** out) {
     if (!cam_in || !out || W == 0 || H == 0 || degree > 4) return 1;
     const int nthreads = resolve_threads(threads);
@@ -574,6 +605,12 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
     f->opac_copy.assign(raw_opac, raw_opac + N);
     f->transforms = f->transforms_copy.data(); f->sh = f->sh_copy.data(); f->raw_opac = f->opac_copy.data();
     transforms = f->transforms; sh = f->sh; raw_opac = f->raw_opac;
+    if (min_scale) {
+        f->min_scale_copy.assign(min_scale, min_scale + N);
+        f->min_scale = f->min_scale_copy.data();
+    }
+    f->mip = (flags & OR_FLAG_MIP) != 0;
+    const bool mip = f->mip;
 
     // ---- project_forward: cull + count, kernels/project_forward.rs:26-261 ----
     f->intersect_counts.assign(N, 0u);
@@ -603,10 +640,11 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         const float ro = raw_opac[g];
         if (!is_finite(ro)) continue;
         const Q4 q = qnormalize(qu);
-        float opac = sigmoid(ro);
-        f->opacities[g] = opac;
-        const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
-        opac = opac * 1.0f;                       // filter_comp is 1 outside Mip mode
+        const ScaleFloor fl = apply_scale_floor(sc, sigmoid(ro), f->min_scale, g);
+        f->opacities[g] = fl.opac;
+        float filter_comp;
+        const S2 cov = compensate_cov2d(calc_cov2d(fl.scale, q, mean_c, u), mip, filter_comp);
+        const float opac = fl.opac * filter_comp;
         if (!s2_finite(cov)) continue;
         float mx, my;
         project(mean_c, u, mx, my);
@@ -652,10 +690,11 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         const V3 mean = v3(t[0], t[1], t[2]);
         const V3 sc = v3(expf_c(t[7] + lso), expf_c(t[8] + lso), expf_c(t[9] + lso));
         const Q4 q = qnormalize(Q4{t[3], t[4], t[5], t[6]});
-        const float opac_sig = sigmoid(raw_opac[g]);
+        const ScaleFloor fl = apply_scale_floor(sc, sigmoid(raw_opac[g]), f->min_scale, g);
         const V3 mean_c = world_to_cam(mean, u);
-        const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
-        const float opac = opac_sig * 1.0f;
+        float filter_comp;
+        const S2 cov = compensate_cov2d(calc_cov2d(fl.scale, q, mean_c, u), mip, filter_comp);
+        const float opac = fl.opac * filter_comp;
         const S2 conic = s2_inverse(cov);
         float mx, my;
         project(mean_c, u, mx, my);
@@ -665,8 +704,9 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         row[5] = opac; row[6] = col.x; row[7] = col.y; row[8] = col.z;
         if (geometry) {
             const M3 rot = mul_mat3(view_rot(u), quat_to_mat3(q));
-            const bool x_min = sc.x <= sc.y && sc.x <= sc.z;
-            const bool y_min = !x_min && sc.y <= sc.z;
+            const V3 fs = fl.scale;               // the normal's axis is the floored scales' smallest
+            const bool x_min = fs.x <= fs.y && fs.x <= fs.z;
+            const bool y_min = !x_min && fs.y <= fs.z;
             const V3 axis = x_min ? rot.c0 : (y_min ? rot.c1 : rot.c2);
             const float flip = (dot(axis, mean_c) > 0.0f) ? -1.0f : 1.0f;
             float* a = &f->aux[(size_t)c * 4];
@@ -984,10 +1024,12 @@ static SplatVjp splat_vjp(const or_fwd* f, uint32_t g, const float* t, float raw
     const uint32_t K = f->K, degree = f->degree;
     const float* cb = f->sh + (size_t)g * K * 3;
     const V3 mean = v3(t[0], t[1], t[2]);
-    const V3 sc = v3(expf_c(t[7] + f->lso), expf_c(t[8] + f->lso), expf_c(t[9] + f->lso));
+    const V3 sc_raw = v3(expf_c(t[7] + f->lso), expf_c(t[8] + f->lso), expf_c(t[9] + f->lso));
     const Q4 qu{t[3], t[4], t[5], t[6]};
     const Q4 q = qnormalize(qu);
     const float opac_sig = sigmoid(raw);
+    const ScaleFloor fl = apply_scale_floor(sc_raw, opac_sig, f->min_scale, g);
+    const V3 sc = fl.scale;
     // SH + view-direction VJP
     const V3 u_world = sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
     const float u_len = length(u_world);
@@ -999,8 +1041,10 @@ static SplatVjp splat_vjp(const or_fwd* f, uint32_t g, const float* t, float raw
     const V3 mean_c = world_to_cam(mean, u);
     const M3 R = quat_to_mat3(q);
     const M3 Mm = mul_diag(R, sc);
-    const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u));
-    const float v_opac_base = 1.0f * rg[8];
+    float filter_comp;
+    const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u), f->mip, filter_comp);
+    // the compensated opacity's gradient (no path through filter_comp), 0 where the floor clamps
+    const float v_opac_base = fl.opac_open ? filter_comp * rg[8] : 0.0f;
     const S2 conic_inv = s2_inverse(cov);
     const S2 v_inv{rg[2], rg[3] * 0.5f, rg[4]};
     const S2 v_cov2d = inverse2x2_vjp(conic_inv, v_inv);
@@ -1015,13 +1059,14 @@ static SplatVjp splat_vjp(const or_fwd* f, uint32_t g, const float* t, float raw
     r.v_mean = add(tmul_vec3(vrot, v_mean_c), v_mean_sh);
     const M3 v_m = s3_mul_mat3(s3_scale(s3_tcongruence(vcc, vrot), 2.0f), Mm);
     const V3 v_log{dot(R.c0, v_m.c0) * sc.x, dot(R.c1, v_m.c1) * sc.y, dot(R.c2, v_m.c2) * sc.z};
-    // ratio_sq = 1 and floor.opac * (1 - 1) = 0 without a scale floor.
-    r.v_log = V3{v_log.x * 1.0f + v_opac_base * opac_sig * 0.0f,
-                 v_log.y * 1.0f + v_opac_base * opac_sig * 0.0f,
-                 v_log.z * 1.0f + v_opac_base * opac_sig * 0.0f};
+    // through the floor: d log s' / d log s = ratio_sq, plus the opacity
+    // compensation's d(opac) / d(log s_i) = opac (1 - ratio_sq_i)
+    r.v_log = V3{v_log.x * fl.ratio_sq.x + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.x),
+                 v_log.y * fl.ratio_sq.y + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.y),
+                 v_log.z * fl.ratio_sq.z + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.z)};
     const Q4 q_grad = quat_to_mat_vjp(q, mul_diag(v_m, sc));
     r.v_q = apply_normalize_vjp(qu, q_grad);
-    r.v_raw = v_opac_base * 1.0f * opac_sig * (1.0f - opac_sig);
+    r.v_raw = v_opac_base * fl.coef * opac_sig * (1.0f - opac_sig);
     r.vdir = vdir;
     return r;
 }

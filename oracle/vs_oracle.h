@@ -41,6 +41,7 @@ enum {
     OR_FLAG_SMOOTH_CUTOFF = 4,  /* C^1 alpha cutoff (BackwardSmoothCutoff) */
     OR_FLAG_BRUTE_FORCE = 8,    /* composite every pixel over the whole depth-sorted
                                    visible list instead of its tile's list (checks binning) */
+    OR_FLAG_MIP = 16,           /* SplatRenderMode::Mip: 0.1 blur with opacity compensation */
 };
 
 typedef struct or_fwd or_fwd;
@@ -49,6 +50,7 @@ typedef struct or_fwd or_fwd;
 int or_render_forward(const or_camera* cam, uint32_t img_w, uint32_t img_h,
                       const float* transforms, const float* sh_coeffs, uint32_t sh_degree,
                       const float* raw_opacities, uint32_t num_splats, float log_scale_offset,
+                      const float* min_scale /* [N] scale floor or NULL */,
                       const float background[3], int flags, int threads, or_fwd** out);
 
 /* Sizes of the result arrays. */

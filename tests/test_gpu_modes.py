@@ -1,0 +1,80 @@
+"""GPU parity of the Mip render mode and the scale floor (min_scale) against
+the CPU oracle: forward bit for bit (counts, sorted order, projected rows,
+image, floored opacities), dense gradients at the contract bar with the
+projection stage checked on its own, and the fused update bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import vauss_amd as va
+from oracle import pyoracle as po
+from tests._util import circle_mask, gpu_state_arrays, l1_cotangent_np, to_gpu
+from tests.test_gpu_parity import _check_forward, _check_grads, _check_param_grads
+from vauss_amd import scenes
+
+pytestmark = pytest.mark.gpu
+
+CASES = [("c2", 20_000, 0, True, False), ("c2", 20_000, 0, False, True), ("c5", 20_000, 0, True, True),
+         ("c3", 20_000, 3, True, True)]
+
+
+@pytest.mark.parametrize("cfg,n,view,mip,use_floor", CASES)
+def test_mode_parity(cfg, n, view, mip, use_floor):
+    w = scenes.workload(cfg, n)
+    sc = w.scene
+    cam = w.cameras[view].uniforms(w.img_size)
+    t, s, o = to_gpu(sc)
+    floor = np.random.default_rng(17).uniform(0.0, 0.02, sc.num_splats).astype(np.float32) if use_floor else None
+    floor_gpu = torch.from_numpy(floor).cuda() if use_floor else None
+    mode = va.SplatRenderMode.MIP if mip else va.SplatRenderMode.DEFAULT
+    print(f"[case] {cfg} n={sc.num_splats} view={view} mip={mip} floor={use_floor}", flush=True)
+    out = va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD, render_mode=mode, min_scale=floor_gpu)
+    flags = po.FLAG_BWD_INFO | (po.FLAG_MIP if mip else 0)
+    ref = po.render_forward(cam, w.img_size, sc.transforms, sc.sh_coeffs, sc.raw_opacities, flags=flags,
+                            min_scale=floor)
+    _check_forward(out, ref, gpu_state_arrays(out))
+    img = out.out_img.cpu().numpy()
+    np.testing.assert_array_equal(img.view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))
+    np.testing.assert_array_equal(out.aux.visible.cpu().numpy(), ref.get(po.F_VISIBLE))
+
+    mask = circle_mask(w.img_size, w.mask_center, w.mask_radius) if w.mask_radius > 0 else None
+    v_out = l1_cotangent_np(img, scenes.loss_target(w.img_size), mask)
+    g = va.render_backward(out, t, s, o, torch.from_numpy(v_out).cuda(), min_scale=floor_gpu)
+    rg = ref.backward(v_out)
+    vc = g.v_combined.cpu().numpy()
+    _check_grads(vc[:, 0:5], rg["v_combined"][:, 0:5], "v_xy_conic")
+    _check_grads(vc[:, 5:9], rg["v_combined"][:, 5:9], "v_rgb_opacity")
+    _check_param_grads(g, rg, ref, vc)
+
+    nn = sc.num_splats
+    rng = np.random.default_rng(2)
+    w_t = rng.integers(0, 1 << 32, (nn, 10), dtype=np.uint64).astype(np.uint32) & np.uint32(0x4FFF7FFF)
+    w_o = rng.integers(0, 1 << 32, nn, dtype=np.uint64).astype(np.uint32) & np.uint32(0x4FFF7FFF)
+    lr_scale = np.full(10, 1e-3, np.float32)
+    adam = va.FusedAdam.at_step(5, lr_opac=0.05, opac_reg=1e-6)
+    tg, og = t.clone(), o.clone()
+    wtg = torch.from_numpy(w_t.view(np.int32).copy()).cuda()
+    wog = torch.from_numpy(w_o.view(np.int32).copy()).cuda()
+    res = va.project_update(out, tg, s, og, g.v_combined, wtg, torch.from_numpy(lr_scale).cuda(), wog, adam)
+    oa = po.OrAdam(adam.beta1, adam.beta2, adam.inv1, adam.inv2, adam.epsilon, adam.lr_opac, adam.opac_reg,
+                   adam.round_seed)
+    want = ref.project_update(vc, sc.transforms, sc.raw_opacities, w_t, lr_scale, w_o, oa)
+    np.testing.assert_array_equal(res.color_dir.cpu().numpy(), want["color_dir"])
+    np.testing.assert_array_equal(tg.cpu().numpy().view(np.uint32), want["transforms"].view(np.uint32))
+    np.testing.assert_array_equal(og.cpu().numpy().view(np.uint32), want["raw_opac"].view(np.uint32))
+    np.testing.assert_array_equal(wtg.cpu().numpy().view(np.uint32), want["w_t"])
+    np.testing.assert_array_equal(wog.cpu().numpy().view(np.uint32), want["w_o"])
+    out.state.free()
+
+
+def test_mode_errors():
+    w = scenes.workload("c1", 500)
+    cam = w.cameras[0].uniforms(w.img_size)
+    t, s, o = to_gpu(w.scene)
+    with pytest.raises(va.VsError):
+        va.render(cam, w.img_size, t, s, o, render_mode=va.SplatRenderMode.SURFEL)
+    out = va.render(cam, w.img_size, t, s, o, min_scale=torch.full((500,), 0.01, device="cuda"))
+    v = torch.zeros_like(out.out_img)
+    with pytest.raises(va.VsError):                 # the backward must see the forward's floor
+        va.render_backward(out, t, s, o, v)
+    out.state.free()

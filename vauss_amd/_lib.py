@@ -42,7 +42,7 @@ class VsPose(C.Structure):
 class VsSplats(C.Structure):
     _fields_ = [("transforms", C.c_void_p), ("sh_coeffs", C.c_void_p), ("raw_opacities", C.c_void_p),
                 ("num_splats", C.c_uint32), ("sh_degree", C.c_uint32), ("log_scale_offset", C.c_float),
-                ("sh_dtype", C.c_uint32)]
+                ("sh_dtype", C.c_uint32), ("min_scale", C.c_void_p)]
 
 
 class VsShStepParams(C.Structure):

@@ -64,7 +64,8 @@ struct vs_ctx {
 struct vs_fwd_state {
     vs_ctx* ctx = nullptr;
     vs_camera cam{};
-    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0, sh_half = 0;
+    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0, sh_half = 0, mip = 0;
+    const float* min_scale = nullptr;   // the forward's scale floor (borrowed), or null
     float lso = 0.0f;
     float bg[3] = {0, 0, 0};
     vs_pass pass = VS_PASS_FORWARD;
@@ -120,6 +121,7 @@ vs_status check_splats(const vs_splats* sp) {
     if (((uintptr_t)sp->transforms & 7u) != 0) return fail(VS_ERR_INVALID, "transforms must be 8-byte aligned");
     if (((uintptr_t)sp->sh_coeffs & 15u) != 0) return fail(VS_ERR_INVALID, "sh_coeffs must be 16-byte aligned");
     if (((uintptr_t)sp->raw_opacities & 3u) != 0) return fail(VS_ERR_INVALID, "raw_opacities must be 4-byte aligned");
+    if (((uintptr_t)sp->min_scale & 3u) != 0) return fail(VS_ERR_INVALID, "min_scale must be 4-byte aligned");
     return VS_OK;
 }
 
@@ -215,7 +217,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     if (state_out) *state_out = nullptr;
     if (!ctx || !cam || !out || !background) return fail(VS_ERR_INVALID, "null argument");
     if (W == 0 || H == 0) return fail(VS_ERR_INVALID, "Can't render images with 0 size.");
-    if (mode != VS_MODE_DEFAULT) return fail(VS_ERR_UNSUPPORTED, "only the Default render mode is built (Mip and Surfel are not)");
+    if (mode != VS_MODE_DEFAULT && mode != VS_MODE_MIP)
+        return fail(VS_ERR_UNSUPPORTED, "the Surfel render mode is not built (Default and Mip are)");
     if ((int)pass < 0 || (int)pass > (int)VS_PASS_GEOMETRY) return fail(VS_ERR_INVALID, "unknown pass");
     if (cam->model != VS_CAMERA_PINHOLE && cam->model != VS_CAMERA_KB4)
         return fail(VS_ERR_UNSUPPORTED, "camera model must be pinhole or Kannala-Brandt-4");
@@ -234,6 +237,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->W = W; st->H = H; st->N = sp->num_splats; st->degree = sp->sh_degree;
     st->K = (sp->sh_degree + 1) * (sp->sh_degree + 1);
     st->sh_half = sp->sh_dtype == VS_SH_F16 ? 1u : 0u;
+    st->mip = mode == VS_MODE_MIP ? 1u : 0u;
+    st->min_scale = sp->min_scale;
     st->lso = sp->log_scale_offset;
     st->bg[0] = background[0]; st->bg[1] = background[1]; st->bg[2] = background[2];
     st->pass = pass;
@@ -284,7 +289,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.cam = *cam;
         pa.img_w = W; pa.img_h = H; pa.tile_bw = st->tbw; pa.tile_bh = st->tbh;
         pa.num_splats = N; pa.sh_degree = sp->sh_degree; pa.log_scale_offset = sp->log_scale_offset;
-        pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.raw_opac = sp->raw_opacities;
+        pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.min_scale = st->min_scale; pa.mip = st->mip; pa.raw_opac = sp->raw_opacities;
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
         pa.proj_aux = st->proj_aux; pa.compact = st->compact; pa.block_stats = st->block_stats;
@@ -404,6 +409,8 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     if (vst != VS_OK) return vst;
     if (sp->num_splats != st->N || sp->sh_degree != st->degree || (sp->sh_dtype == VS_SH_F16) != (st->sh_half != 0))
         return fail(VS_ERR_INVALID, "splats differ from the forward's");
+    if ((sp->min_scale != nullptr) != (st->min_scale != nullptr))
+        return fail(VS_ERR_INVALID, "the backward's scale floor must match the forward's (both set or both null)");
     if (((uintptr_t)out_img & 15u) || ((uintptr_t)v_out & 15u)) return fail(VS_ERR_INVALID, "images must be 16-byte aligned");
     if (grads->v_transforms && ((uintptr_t)grads->v_transforms & 7u)) return fail(VS_ERR_INVALID, "v_transforms must be 8-byte aligned");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
@@ -438,7 +445,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
         StageTimer tm(ctx, ST_PROJECT_BWD);
         ProjectBwdArgs pb{};
         pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = sp->log_scale_offset;
-        pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.sh_half = st->sh_half; pb.raw_opac = sp->raw_opacities;
+        pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.sh_half = st->sh_half; pb.min_scale = sp->min_scale; pb.mip = st->mip; pb.raw_opac = sp->raw_opacities;
         pb.counts = st->counts; pb.v_combined = vc;
         pb.v_transforms = grads->v_transforms; pb.v_sh = grads->v_sh_coeffs;
         pb.v_raw_opac = grads->v_raw_opacities; pb.v_refine = grads->v_refine_weight;
@@ -465,7 +472,7 @@ extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* tra
     StageTimer tm(ctx, ST_PROJECT_BWD);
     ProjectUpdateArgs pu{};
     pu.cam = st->cam; pu.num_splats = N; pu.sh_degree = st->degree; pu.log_scale_offset = st->lso;
-    pu.transforms = transforms; pu.sh = sh_coeffs; pu.sh_half = st->sh_half; pu.raw_opac = raw_opacities; pu.compact = st->compact;
+    pu.transforms = transforms; pu.sh = sh_coeffs; pu.sh_half = st->sh_half; pu.min_scale = st->min_scale; pu.mip = st->mip; pu.raw_opac = raw_opacities; pu.compact = st->compact;
     pu.v_combined = v_combined; pu.w_t = w_t; pu.lr_scale = lr_scale; pu.w_o = w_o;
     pu.beta1 = adam->beta1; pu.beta2 = adam->beta2; pu.inv1 = adam->inv1; pu.inv2 = adam->inv2;
     pu.epsilon = adam->epsilon; pu.lr_opac = adam->lr_opac; pu.opac_reg = adam->opac_reg; pu.round_seed = adam->round_seed;

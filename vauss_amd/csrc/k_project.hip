@@ -221,6 +221,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
     S2 conic{0.0f, 0.0f, 0.0f};
     TileBox bb{0, 0, 0, 0};
     uint32_t dbits = 0;
+    F3 fscl{0.0f, 0.0f, 0.0f};      // floored scale (the geometry normal picks its smallest axis)
     if (g < a.num_splats) {
         const float2* t2 = reinterpret_cast<const float2*>(a.transforms + (size_t)g * 10);
         const float2 t01 = t2[0], t23 = t2[1], t45 = t2[2], t67 = t2[3], t89 = t2[4];
@@ -244,9 +245,12 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             if (!(qn >= 1.0e-6f && finite(qn))) break;
             if (!finite(raw_op)) break;
             const Qt q = normalize(qu);
-            const float opac = sigmoid(raw_op);
-            opac_out = opac;
-            const S2 cov = cov2d_blurred<MODEL>(scl, q, mc, u);
+            const ScaleFloor fl = apply_scale_floor(scl, sigmoid(raw_op), a.min_scale, g);
+            opac_out = fl.opac;
+            float filter_comp;
+            const S2 cov = compensate_cov2d(cov2d_raw<MODEL>(fl.scale, q, mc, u), a.mip != 0u, filter_comp);
+            const float opac = fl.opac * filter_comp;
+            fscl = fl.scale;
             if (!finite(cov)) break;
             project_point<MODEL>(mc, u, px, py);
             if (!(opac >= 1.0f / 255.0f)) break;
@@ -269,8 +273,8 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             if constexpr (GEOM) {
                 // kernels/project_visible.rs:271-289
                 const M3 rot = mul(view_rot(u), to_mat3(q));
-                const bool x_min = scl.x <= scl.y && scl.x <= scl.z;
-                const bool y_min = !x_min && scl.y <= scl.z;
+                const bool x_min = fscl.x <= fscl.y && fscl.x <= fscl.z;
+                const bool y_min = !x_min && fscl.y <= fscl.z;
                 const F3 axis = x_min ? rot.c0 : (y_min ? rot.c1 : rot.c2);
                 const float flip = (dot(axis, mc) > 0.0f) ? -1.0f : 1.0f;
                 a.proj_aux[g] = make_float4(mc.z, axis.x * flip, axis.y * flip, axis.z * flip);

@@ -47,7 +47,8 @@ __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs 
     const F3 mean{t01.x, t01.y, t23.x};
     const F3 scl{expf_c(t67.y + lso), expf_c(t89.x + lso), expf_c(t89.y + lso)};
     const Qt qu{t23.y, t45.x, t45.y, t67.x};
-    const SplatVjp r = splat_vjp<DEG, MODEL>(u, static_cast<const SHT*>(a.sh) + (size_t)g * K * 3, mean, scl, qu, a.raw_opac[g], rg);
+    const SplatVjp r = splat_vjp<DEG, MODEL>(u, static_cast<const SHT*>(a.sh) + (size_t)g * K * 3, mean, scl, qu, a.raw_opac[g], rg,
+                                              a.min_scale, g, a.mip != 0u);
     if (vsh) {
         // sh.rs:281-359: v_coeff_k = Y_k(v) v_colour
         float Y[K];

@@ -50,7 +50,8 @@ __global__ void __launch_bounds__(PUPD_BLOCK) project_update_kernel(ProjectUpdat
             const F3 mean{t[0], t[1], t[2]};
             const F3 scl{expf_c(t[7] + lso), expf_c(t[8] + lso), expf_c(t[9] + lso)};
             const Qt qu{t[3], t[4], t[5], t[6]};
-            const SplatVjp r = splat_vjp<DEG, MODEL>(a.cam, static_cast<const SHT*>(a.sh) + (size_t)g * K * 3, mean, scl, qu, raw, rg);
+            const SplatVjp r = splat_vjp<DEG, MODEL>(a.cam, static_cast<const SHT*>(a.sh) + (size_t)g * K * 3, mean,
+                                                     scl, qu, raw, rg, a.min_scale, g, a.mip != 0u);
             if (cd) {
                 cd[0] = rg[5]; cd[1] = rg[6]; cd[2] = rg[7];
                 cd[3] = r.vdir.x; cd[4] = r.vdir.y; cd[5] = r.vdir.z;

@@ -199,16 +199,56 @@ VS_DEV F3 projection_vjp_kb4(M23 J, F3 mc, S3 cov_c, const vs_camera& u, S2 v_co
     return F3{v_mx, v_my, v_mz};
 }
 
-// kernels/helpers.rs:195-225 + 230-245 (Default mode: +0.3 on the diagonal).
+// calc_cov2d, kernels/helpers.rs:195-225: (J W R S)(J W R S)^T, scaled so no
+// entry exceeds 1e18.
 template <int MODEL>
-VS_DEV S2 cov2d_blurred(F3 scl, Qt q, F3 mean_c, const vs_camera& u) {
+VS_DEV S2 cov2d_raw(F3 scl, Qt q, F3 mean_c, const vs_camera& u) {
     const M3 ns = mul_diag(mul(view_rot(u), to_mat3(q)), scl);
     const M23 J = project_jacobian<MODEL>(mean_c, u);
     const S2 raw = gram(mul(J, ns));
     const float ma = max_abs(raw);
     const float sd = (ma > 1.0e18f) ? 1.0e18f / ma : 1.0f;
-    const S2 c = scale(raw, sd);
-    return S2{c.c00 + 0.3f, c.c01, c.c11 + 0.3f};
+    return scale(raw, sd);
+}
+
+// compensate_cov2d, kernels/helpers.rs:227-245: +0.3 on the diagonal
+// (Default), or +0.1 and the opacity factor sqrt(max(det, 0) / det_blurred)
+// (Mip).
+VS_DEV S2 compensate_cov2d(S2 c, bool mip, float& filter_comp) {
+    const float blur = mip ? 0.1f : 0.3f;
+    const S2 b{c.c00 + blur, c.c01, c.c11 + blur};
+    filter_comp = 1.0f;
+    if (mip) {
+        const float det_raw = mx(c.c00 * c.c11 - c.c01 * c.c01, 0.0f);
+        const float det_blurred = b.c00 * b.c11 - b.c01 * b.c01;
+        filter_comp = __builtin_sqrtf(det_raw / det_blurred);
+    }
+    return b;
+}
+
+// apply_scale_floor, kernels/helpers.rs:497-553 (the Mip-Splatting 3D
+// filter): s' = sqrt(s^2 + f^2) per axis; the opacity keeps the splat's mass,
+// sigmoid(raw) prod(s / s'), clamped to [1e-6, 1 - 1e-6].  Without a floor
+// (min_scale NULL) the identity.
+struct ScaleFloor {
+    F3 scale;
+    float opac, coef;
+    F3 ratio_sq;          // d log s' / d log s
+    bool opac_open;       // the clamp passes gradient
+};
+VS_DEV ScaleFloor apply_scale_floor(F3 s, float opac_sig, const float* __restrict__ min_scale, uint32_t g) {
+    ScaleFloor r{s, opac_sig, 1.0f, F3{1.0f, 1.0f, 1.0f}, true};
+    if (min_scale) {
+        const float f = min_scale[g], f2 = f * f;
+        r.scale = F3{__builtin_sqrtf(s.x * s.x + f2), __builtin_sqrtf(s.y * s.y + f2), __builtin_sqrtf(s.z * s.z + f2)};
+        const float rx = s.x / r.scale.x, ry = s.y / r.scale.y, rz = s.z / r.scale.z;
+        r.coef = rx * ry * rz;
+        r.ratio_sq = F3{rx * rx, ry * ry, rz * rz};
+        const float o = opac_sig * r.coef;
+        r.opac_open = o > 1.0e-6f && o < 1.0f - 1.0e-6f;
+        r.opac = clampf(o, 1.0e-6f, 1.0f - 1.0e-6f);
+    }
+    return r;
 }
 
 } // namespace vs

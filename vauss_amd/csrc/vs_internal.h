@@ -43,6 +43,8 @@ struct ProjectArgs {
     const float* transforms;
     const void* sh;                  // [N,K,3] f32, or f16 bits when sh_half
     uint32_t sh_half;
+    const float* min_scale;          // [N] scale floor (apply_scale_floor) or null
+    uint32_t mip;                    // SplatRenderMode::Mip
     const float* raw_opac;
     // outputs, indexed by global splat id
     float* opacities;           // [N]
@@ -112,6 +114,8 @@ struct ProjectBwdArgs {
     const float* transforms;
     const void* sh;                  // [N,K,3] f32, or f16 bits when sh_half
     uint32_t sh_half;
+    const float* min_scale;          // [N] scale floor (apply_scale_floor) or null
+    uint32_t mip;                    // SplatRenderMode::Mip
     const float* raw_opac;
     const uint32_t* counts;          // visible <=> counts defined; culled rows get zeros
     const float* v_combined;         // [N,10]
@@ -128,6 +132,8 @@ struct ProjectUpdateArgs {
     float* transforms;               // [N,10] stepped in place
     const void* sh;                  // [N,K,3] f32, or f16 bits when sh_half
     uint32_t sh_half;
+    const float* min_scale;          // [N] scale floor (apply_scale_floor) or null
+    uint32_t mip;                    // SplatRenderMode::Mip
     float* raw_opac;                 // [N] stepped in place
     const uint32_t* compact;         // [N] g + 1 if visible, else 0
     const float* v_combined;         // [N,10]

@@ -3,7 +3,8 @@
 // (k_project_update.hip).
 //
 // Restates crates/splat-train-render/src/bwd/kernels/project_backwards.rs
-// (splat_vjp :132-274) for the Default render mode without a scale floor.
+// (splat_vjp :132-274) for the Default and Mip render modes, with or without
+// the scale floor.
 #pragma once
 #include "vs_device.h"
 #include "vs_camera.h"
@@ -51,11 +52,15 @@ struct SplatVjp {
 };
 
 // rg: the splat's raster gradients [xy(2), conic(3), rgb(3), opacity, refine].
+// `scl_raw` is exp(log-scale + offset); `min_scale` (NULL: no floor) and
+// `mip` select the render mode's forward, as in the projection.
 template <int DEG, int MODEL, typename SHT>
-VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3 mean, F3 scl, Qt qu, float raw,
-                          const float rg[10]) {
+VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3 mean, F3 scl_raw, Qt qu, float raw,
+                          const float rg[10], const float* __restrict__ min_scale, uint32_t g, bool mip) {
     const Qt q = normalize(qu);
     const float opac_sig = sigmoid(raw);
+    const ScaleFloor fl = apply_scale_floor(scl_raw, opac_sig, min_scale, g);
+    const F3 scl = fl.scale;
 
     // SH and view-direction VJP, project_backwards.rs:174-201
     const F3 u_world = mean - F3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]};
@@ -70,8 +75,10 @@ VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3
     const F3 mc = world_to_cam(mean, u);
     const M3 R = to_mat3(q);
     const M3 Mm = mul_diag(R, scl);
-    const S2 cov = cov2d_blurred<MODEL>(scl, q, mc, u);
-    const float v_opac_base = 1.0f * rg[8];
+    float filter_comp;
+    const S2 cov = compensate_cov2d(cov2d_raw<MODEL>(scl, q, mc, u), mip, filter_comp);
+    // the compensated opacity's gradient (no path through filter_comp), 0 where the floor clamps
+    const float v_opac_base = fl.opac_open ? filter_comp * rg[8] : 0.0f;
     const S2 conic = inverse(cov);
     const S2 v_cov2d = inverse_vjp(conic, S2{rg[2], rg[3] * 0.5f, rg[4]});
     const S3 covar = outer_self(Mm);
@@ -85,10 +92,15 @@ VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3
     SplatVjp r;
     r.v_mean = tmul(vrot, v_mean_c) + v_mean_sh;
     const M3 v_m = mul(scale(tcongruence(vcc, vrot), 2.0f), Mm);
-    r.v_log = F3{dot(R.c0, v_m.c0) * scl.x, dot(R.c1, v_m.c1) * scl.y, dot(R.c2, v_m.c2) * scl.z};
+    // project_backwards.rs:256-265: through the floor (ratio_sq) plus the
+    // opacity compensation's d(opac) / d(log s_i) = opac (1 - ratio_sq_i)
+    const F3 v_lf{dot(R.c0, v_m.c0) * scl.x, dot(R.c1, v_m.c1) * scl.y, dot(R.c2, v_m.c2) * scl.z};
+    r.v_log = F3{v_lf.x * fl.ratio_sq.x + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.x),
+                 v_lf.y * fl.ratio_sq.y + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.y),
+                 v_lf.z * fl.ratio_sq.z + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.z)};
     const Qt q_grad = quat_to_mat_vjp(q, mul_diag(v_m, scl));
     r.v_q = normalize_vjp(qu, q_grad);
-    r.v_raw = v_opac_base * 1.0f * opac_sig * (1.0f - opac_sig);
+    r.v_raw = v_opac_base * fl.coef * opac_sig * (1.0f - opac_sig);
     r.vdir = vdir;
     return r;
 }

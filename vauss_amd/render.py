@@ -45,7 +45,7 @@ class RasterPass(enum.IntEnum):
 
 
 class SplatRenderMode(enum.IntEnum):
-    """SplatRenderMode (gaussian_splats.rs:19-26); only DEFAULT is built."""
+    """SplatRenderMode (gaussian_splats.rs:19-26); DEFAULT and MIP are built, SURFEL raises VsError."""
     DEFAULT = _lib.MODE_DEFAULT
     MIP = _lib.MODE_MIP
     SURFEL = _lib.MODE_SURFEL
@@ -121,6 +121,7 @@ class ForwardState:
         self.pass_ = pass_
         self.num_splats = num_splats
         self.sh_degree = sh_degree
+        self.keep = None                # tensors the library state borrows (the scale floor)
 
     def view(self) -> _lib.VsStateView:
         v = _lib.VsStateView()
@@ -199,7 +200,15 @@ def _check_splats(transforms, sh_coeffs, raw_opacities):
     return n, sh_degree_from_coeffs(sh_coeffs.shape[1])
 
 
-def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset) -> _lib.VsSplats:
+def _min_scale(min_scale: Optional[torch.Tensor], n: int) -> Optional[torch.Tensor]:
+    if min_scale is None:
+        return None
+    if min_scale.dtype != torch.float32 or min_scale.numel() != n or not min_scale.is_cuda:
+        raise ValueError("min_scale must be a float32 [N] GPU tensor")
+    return min_scale.contiguous().reshape(n)
+
+
+def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale=None) -> _lib.VsSplats:
     s = _lib.VsSplats()
     s.transforms = _ptr(transforms)
     s.sh_coeffs = _ptr(sh_coeffs)
@@ -208,14 +217,17 @@ def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offse
     s.sh_degree = degree
     s.log_scale_offset = float(log_scale_offset)
     s.sh_dtype = _lib.VS_SH_F16 if sh_coeffs.dtype == torch.float16 else _lib.VS_SH_F32
+    s.min_scale = _ptr(min_scale)
     return s
 
 
 def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs: torch.Tensor,
            raw_opacities: torch.Tensor, background=(0.0, 0.0, 0.0), pass_: RasterPass = RasterPass.BACKWARD,
            render_mode: SplatRenderMode = SplatRenderMode.DEFAULT, log_scale_offset: float = 0.0,
-           validate: bool = False) -> RenderOutput:
+           validate: bool = False, min_scale: Optional[torch.Tensor] = None) -> RenderOutput:
     """SplatOps::render.  `camera` is a Camera or ready-made vs_camera uniforms.
+    `render_mode` DEFAULT or MIP; `min_scale` [N] is the scale floor
+    (render's min_scale with has_min_scale), None for none.
 
     Returns the image ([H,W,C] f32, or [H,W] int32-packed RGBA8 for
     FORWARD), the aux outputs and, for every pass but FORWARD, the state the
@@ -251,19 +263,22 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     out.max_radius = _ptr(max_radius)
     out.opacities = _ptr(opacities)
     out.tile_offsets = _ptr(tile_offsets)
-    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset)
+    min_scale = _min_scale(min_scale, n)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale)
     bg = (C.c_float * 3)(*[float(v) for v in background])
     st = C.c_void_p()
     _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg, int(pass_),
                                          int(render_mode), C.byref(out), C.byref(st)))
     aux = RenderAux(out.num_visible, out.num_intersections, visible, max_radius, opacities, tile_offsets, (w, h))
     state = ForwardState(st, ctx, pass_, n, degree) if st.value else None
+    if state is not None:
+        state.keep = min_scale          # the state borrows the floor for project_update
     return RenderOutput(out_img, aux, state, cam, tuple(float(v) for v in background))
 
 
 def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
                     raw_opacities: torch.Tensor, v_output: torch.Tensor, log_scale_offset: float = 0.0,
-                    fused: bool = False) -> SplatGrads:
+                    fused: bool = False, min_scale: Optional[torch.Tensor] = None) -> SplatGrads:
     """rasterize_bwd followed by project_bwd, returning dense gradients.
 
     With `fused` the backward stops at the raster gradients (the
@@ -296,7 +311,7 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     grads.v_raw_opacities = _ptr(g.v_raw_opac)
     grads.v_refine_weight = _ptr(g.v_refine_weight)
     grads.v_combined = _ptr(g.v_combined)
-    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, _min_scale(min_scale, n))
     _lib.check(ctx.lib.vs_render_backward(ctx.handle, output.state.handle, C.byref(splats), _ptr(output.out_img),
                                           _ptr(v_output), C.byref(grads)))
     return g
