@@ -41,10 +41,14 @@ typedef enum vs_status {
 typedef struct vs_ctx vs_ctx;
 typedef struct vs_fwd_state vs_fwd_state;
 
-/* Camera models: crates/splat-train-render/src/kernels/camera_model/mod.rs:30-37
- * (Pinhole and KannalaBrandt4; the RT8 and thin-prism models return
- * VS_ERR_UNSUPPORTED). */
-typedef enum vs_camera_model { VS_CAMERA_PINHOLE = 0, VS_CAMERA_KB4 = 1 } vs_camera_model;
+/* Camera models: crates/splat-train-render/src/kernels/camera_model/mod.rs:30-37.
+ * Distortion parameters: KB4 k1..k4 in kb4[]; RT8 (OpenCV rational +
+ * tangential) k1..k6, p1, p2 in dist[0..7]; thin-prism fisheye (COLMAP
+ * THIN_PRISM_FISHEYE) its KB4 part in kb4[] and p1, p2, sx1, sy1 in
+ * dist[0..3]. */
+typedef enum vs_camera_model {
+    VS_CAMERA_PINHOLE = 0, VS_CAMERA_KB4 = 1, VS_CAMERA_RT8 = 2, VS_CAMERA_TPF = 3
+} vs_camera_model;
 
 /* Device-side projection uniforms, the fields of ProjectUniforms
  * (crates/splat-train-render/src/kernels/types.rs:53-82) other than sizes.
@@ -58,6 +62,7 @@ typedef struct vs_camera {
     float cam_pos[3];               /* view-direction origin for SH */
     float half_max_render_fov;      /* fisheye angular cull */
     float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y, lim_r; /* JacobianClampLimits */
+    float dist[8];                  /* RT8 / thin-prism parameters (see vs_camera_model) */
 } vs_camera;
 
 /* Host camera description, crates/splat-train-render/src/camera.rs:11-23. */
@@ -68,6 +73,7 @@ typedef struct vs_pose {
     float rotation[4];              /* camera-to-world rotation quaternion, (x, y, z, w) */
     int32_t model;                  /* vs_camera_model */
     float kb4[4];
+    float dist[8];                  /* RT8 / thin-prism parameters */
 } vs_pose;
 
 /* Element type of the SH coefficients (render.rs:683-687: f32 or f16; the
@@ -160,11 +166,12 @@ vs_status vs_ctx_stage_times(vs_ctx* ctx, vs_stage_times* out);
 
 /* ---- camera host math --------------------------------------------------------- */
 
-/* camera.rs:99-116 fov_to_focal / :118-134 focal_to_fov (host, f64). */
-double vs_fov_to_focal(double fov, uint32_t pixels, int32_t model, const float kb4[4]);
-double vs_focal_to_fov(double focal, uint32_t pixels, int32_t model, const float kb4[4]);
-/* camera.rs:166-172 max_render_theta (KB4 fold angle, pi otherwise). */
-double vs_max_render_theta(int32_t model, const float kb4[4]);
+/* camera.rs:99-116 fov_to_focal / :118-134 focal_to_fov (host, f64).
+ * `params` holds 12 floats: kb4 k1..k4 then dist[8] (NULL for pinhole). */
+double vs_fov_to_focal(double fov, uint32_t pixels, int32_t model, const float* params);
+double vs_focal_to_fov(double focal, uint32_t pixels, int32_t model, const float* params);
+/* camera.rs:166-172 max_render_theta (the KB4 / thin-prism fold angle, pi otherwise). */
+double vs_max_render_theta(int32_t model, const float* params);
 /* render.rs:478-503 + camera.rs:55-96,305-374: uniforms of a pose at W x H (host). */
 vs_status vs_camera_uniforms(const vs_pose* pose, uint32_t img_w, uint32_t img_h, vs_camera* out);
 

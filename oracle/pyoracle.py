@@ -30,7 +30,7 @@ class OrCamera(C.Structure):
     _fields_ = [("model", C.c_int32), ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float),
                 ("kb4", C.c_float * 4), ("viewmat", C.c_float * 12), ("cam_pos", C.c_float * 3),
                 ("half_max_render_fov", C.c_float), ("lim_pos_x", C.c_float), ("lim_pos_y", C.c_float),
-                ("lim_neg_x", C.c_float), ("lim_neg_y", C.c_float), ("lim_r", C.c_float)]
+                ("lim_neg_x", C.c_float), ("lim_neg_y", C.c_float), ("lim_r", C.c_float), ("dist", C.c_float * 8)]
 
 
 class OrAdam(C.Structure):
@@ -125,6 +125,10 @@ def load() -> C.CDLL:
     lib.or_atan2f_n.argtypes = [_F, _F, _F, C.c_uint64]
     lib.or_sh_basis.argtypes = [C.c_uint32, _F, _F]
     kb = C.POINTER(C.c_float)
+    for name in ("or_rt8_radial", "or_rt8_undistort_radius", "or_rt8_undistort_corner_radius"):
+        getattr(lib, name).restype = C.c_double
+        getattr(lib, name).argtypes = [C.c_double, kb]
+    lib.or_clamp_limits.argtypes = [C.c_int, C.c_uint32, C.c_uint32, C.c_float, C.c_float, C.c_float, C.c_float, kb, kb]
     for name, args in (("or_fov_to_focal", [C.c_double, C.c_uint32, C.c_int, kb]),
                        ("or_focal_to_fov", [C.c_double, C.c_uint32, C.c_int, kb]),
                        ("or_max_render_theta", [C.c_int, kb]), ("or_kb4_d", [C.c_double, kb]),
@@ -316,16 +320,41 @@ def kb4_array(k):
     return (C.c_float * 4)(*[float(v) for v in k])
 
 
-def fov_to_focal(fov, pixels, model=0, k=(0, 0, 0, 0)):
-    return load().or_fov_to_focal(fov, pixels, model, kb4_array(k))
+MODEL_PINHOLE, MODEL_KB4, MODEL_RT8, MODEL_TPF = 0, 1, 2, 3
 
 
-def focal_to_fov(focal, pixels, model=0, k=(0, 0, 0, 0)):
-    return load().or_focal_to_fov(focal, pixels, model, kb4_array(k))
+def _params12(k, dist):
+    return (C.c_float * 12)(*([float(v) for v in k] + [float(v) for v in dist] + [0.0] * (8 - len(dist))))
 
 
-def max_render_theta(model=0, k=(0, 0, 0, 0)):
-    return load().or_max_render_theta(model, kb4_array(k))
+def fov_to_focal(fov, pixels, model=0, k=(0, 0, 0, 0), dist=()):
+    """`k`: KB4 k1..k4 (KB4, thin-prism); `dist`: RT8 k1..k6, p1, p2 or thin-prism p1, p2, sx1, sy1."""
+    return load().or_fov_to_focal(fov, pixels, model, _params12(k, dist))
+
+
+def focal_to_fov(focal, pixels, model=0, k=(0, 0, 0, 0), dist=()):
+    return load().or_focal_to_fov(focal, pixels, model, _params12(k, dist))
+
+
+def max_render_theta(model=0, k=(0, 0, 0, 0), dist=()):
+    return load().or_max_render_theta(model, _params12(k, dist))
+
+
+def rt8_radial(r, dist):
+    return load().or_rt8_radial(r, (C.c_float * 8)(*dist))
+
+
+def rt8_undistort_corner_radius(r_d, dist):
+    """None when r radial(r) never reaches r_d below r = 16."""
+    v = load().or_rt8_undistort_corner_radius(r_d, (C.c_float * 8)(*dist))
+    return None if v < 0 else v
+
+
+def clamp_limits(model, img, fx, fy, cx, cy, dist=(0,) * 8):
+    """(lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y, lim_r)."""
+    out = (C.c_float * 5)()
+    load().or_clamp_limits(model, img[0], img[1], fx, fy, cx, cy, (C.c_float * 8)(*dist), out)
+    return tuple(out)
 
 
 def kb4_d(theta, k):

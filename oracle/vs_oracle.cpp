@@ -104,8 +104,52 @@ void project_kb4(V3 p, const or_camera& u, float& ou, float& ov) {
     ou = near_axis ? pin_u : fu;
     ov = near_axis ? pin_v : fv;
 }
+// kernels/camera_model/thin_prism_fisheye.rs:37-63: N_u, N_v (delta = N / z^2)
+// and their (x, y) derivatives, in camera-space x, y.
+struct TpPolys { float nu, nv, dnu_dx, dnu_dy, dnv_dx, dnv_dy; };
+TpPolys thin_prism_polys(float x, float y, const or_camera& u) {
+    const float p1 = u.dist[0], p2 = u.dist[1], sx1 = u.dist[2], sy1 = u.dist[3];
+    const float x2 = x * x, y2 = y * y, xy = x * y, r2 = x2 + y2;
+    TpPolys t;
+    t.nu = 2.0f * p1 * xy + p2 * (3.0f * x2 + y2) + sx1 * r2;
+    t.nv = 2.0f * p2 * xy + p1 * (x2 + 3.0f * y2) + sy1 * r2;
+    t.dnu_dx = 2.0f * (p1 * y + (3.0f * p2 + sx1) * x);
+    t.dnu_dy = 2.0f * (p1 * x + (p2 + sx1) * y);
+    t.dnv_dx = 2.0f * (p2 * y + (p1 + sy1) * x);
+    t.dnv_dy = 2.0f * (p2 * x + (3.0f * p1 + sy1) * y);
+    return t;
+}
+
+// kernels/camera_model/radial_tangential_8.rs:23-62
+void project_rt8(V3 p, const or_camera& u, float& ou, float& ov) {
+    const float k1 = u.dist[0], k2 = u.dist[1], k3 = u.dist[2], k4 = u.dist[3], k5 = u.dist[4], k6 = u.dist[5];
+    const float p1 = u.dist[6], p2 = u.dist[7];
+    const float xn = p.x / p.z, yn = p.y / p.z;
+    const float xn2 = xn * xn, yn2 = yn * yn;
+    const float r2 = xn2 + yn2, r4 = r2 * r2, r6 = r4 * r2;
+    const float radial = (1.0f + k1 * r2 + k2 * r4 + k3 * r6) / (1.0f + k4 * r2 + k5 * r4 + k6 * r6);
+    const float xyn = xn * yn;
+    const float xd = xn * radial + 2.0f * p1 * xyn + p2 * (r2 + 2.0f * xn2);
+    const float yd = yn * radial + 2.0f * p2 * xyn + p1 * (r2 + 2.0f * yn2);
+    ou = u.fx * xd + u.cx;
+    ov = u.fy * yd + u.cy;
+}
+// kernels/camera_model/thin_prism_fisheye.rs:65-82
+void project_tpf(V3 p, const or_camera& u, float& ou, float& ov) {
+    float ku, kv;
+    project_kb4(p, u, ku, kv);
+    const float inv_z = 1.0f / p.z, inv_z2 = inv_z * inv_z;
+    const TpPolys t = thin_prism_polys(p.x, p.y, u);
+    ou = ku + u.fx * t.nu * inv_z2;
+    ov = kv + u.fy * t.nv * inv_z2;
+}
 void project(V3 p, const or_camera& u, float& ou, float& ov) {
-    if (u.model == OR_MODEL_KB4) project_kb4(p, u, ou, ov); else project_pinhole(p, u, ou, ov);
+    switch (u.model) {
+    case OR_MODEL_KB4: project_kb4(p, u, ou, ov); break;
+    case OR_MODEL_RT8: project_rt8(p, u, ou, ov); break;
+    case OR_MODEL_TPF: project_tpf(p, u, ou, ov); break;
+    default: project_pinhole(p, u, ou, ov); break;
+    }
 }
 // kernels/camera_model/pinhole.rs:173-197
 M23 jac_pinhole(V3 p, const or_camera& u) {
@@ -157,8 +201,48 @@ M23 jac_kb4(V3 p, const or_camera& u) {
                V2{near_axis ? 0.0f : du_dy, near_axis ? pdy : dv_dy},
                V2{near_axis ? p_du_dz : du_dz, near_axis ? p_dv_dz : dv_dz}};
 }
+// kernels/camera_model/radial_tangential_8.rs:64-149
+M23 jac_rt8(V3 p, const or_camera& u) {
+    const float k1 = u.dist[0], k2 = u.dist[1], k3 = u.dist[2], k4 = u.dist[3], k5 = u.dist[4], k6 = u.dist[5];
+    const float p1 = u.dist[6], p2 = u.dist[7];
+    const float z = p.z, inv_z = 1.0f / z, inv_z2 = inv_z * inv_z;
+    const float xb = clampf(p.x * inv_z, u.lim_neg_x, u.lim_pos_x);
+    const float yb = clampf(p.y * inv_z, u.lim_neg_y, u.lim_pos_y);
+    const float rb = std::sqrt(xb * xb + yb * yb);
+    const float sc = rb > u.lim_r ? u.lim_r / rb : 1.0f;
+    const float xn = xb * sc, yn = yb * sc;
+    const float xc = xn * z, yc = yn * z;
+    const float r2 = xn * xn + yn * yn, r4 = r2 * r2, r6 = r4 * r2;
+    const float N = 1.0f + k1 * r2 + k2 * r4 + k3 * r6;
+    const float D = 1.0f + k4 * r2 + k5 * r4 + k6 * r6;
+    const float Np = k1 + 2.0f * k2 * r2 + 3.0f * k3 * r4;
+    const float Dp = k4 + 2.0f * k5 * r2 + 3.0f * k6 * r4;
+    const float iD = 1.0f / D, iD2 = iD * iD;
+    const float R0 = N * iD, R1 = (Np * D - N * Dp) * iD2;
+    const float a00 = R0 + 2.0f * xn * xn * R1 + 2.0f * p1 * yn + 6.0f * p2 * xn;
+    const float a01 = 2.0f * xn * yn * R1 + 2.0f * p1 * xn + 2.0f * p2 * yn;
+    const float a10 = a01;
+    const float a11 = R0 + 2.0f * yn * yn * R1 + 6.0f * p1 * yn + 2.0f * p2 * xn;
+    return M23{V2{u.fx * a00 * inv_z, u.fy * a10 * inv_z},
+               V2{u.fx * a01 * inv_z, u.fy * a11 * inv_z},
+               V2{-u.fx * (a00 * xc + a01 * yc) * inv_z2, -u.fy * (a10 * xc + a11 * yc) * inv_z2}};
+}
+// kernels/camera_model/thin_prism_fisheye.rs:84-116
+M23 jac_tpf(V3 p, const or_camera& u) {
+    const M23 k = jac_kb4(p, u);
+    const float inv_z = 1.0f / p.z, inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z;
+    const TpPolys t = thin_prism_polys(p.x, p.y, u);
+    return M23{V2{k.c0.x + u.fx * t.dnu_dx * inv_z2, k.c0.y + u.fy * t.dnv_dx * inv_z2},
+               V2{k.c1.x + u.fx * t.dnu_dy * inv_z2, k.c1.y + u.fy * t.dnv_dy * inv_z2},
+               V2{k.c2.x + -2.0f * u.fx * t.nu * inv_z3, k.c2.y + -2.0f * u.fy * t.nv * inv_z3}};
+}
 M23 project_jacobian(V3 p, const or_camera& u) {
-    return (u.model == OR_MODEL_KB4) ? jac_kb4(p, u) : jac_pinhole(p, u);
+    switch (u.model) {
+    case OR_MODEL_KB4: return jac_kb4(p, u);
+    case OR_MODEL_RT8: return jac_rt8(p, u);
+    case OR_MODEL_TPF: return jac_tpf(p, u);
+    default: return jac_pinhole(p, u);
+    }
 }
 
 // kernels/camera_model/pinhole.rs:199-265
@@ -298,6 +382,127 @@ V3 projection_vjp_kb4(M23 J, V3 mc, S3 cov_c, const or_camera& u, S2 v_cov2d, V2
         v_mz += vj_u2 * d_ju + vj_v2 * d_jv;
     }
     return V3{v_mx, v_my, v_mz};
+}
+
+// kernels/camera_model/radial_tangential_8.rs:151-393: the Jacobian at the
+// clamped, radially capped surrogate point and its derivative; clamped or
+// capped coordinates act as constants of the mean.
+V3 projection_vjp_rt8(V3 mc, S3 cov_c, const or_camera& u, S2 v_cov2d, V2 v_mean2d) {
+    const float fx = u.fx, fy = u.fy;
+    const float k1 = u.dist[0], k2 = u.dist[1], k3 = u.dist[2], k4 = u.dist[3], k5 = u.dist[4], k6 = u.dist[5];
+    const float p1 = u.dist[6], p2 = u.dist[7];
+    const float mz = mc.z, inv_z = 1.0f / mz;
+    const float xr_raw = mc.x * inv_z, yr_raw = mc.y * inv_z;
+    const float xr_box = clampf(xr_raw, u.lim_neg_x, u.lim_pos_x);
+    const float yr_box = clampf(yr_raw, u.lim_neg_y, u.lim_pos_y);
+    const float r_box = std::sqrt(xr_box * xr_box + yr_box * yr_box);
+    const bool capped = r_box > u.lim_r;
+    const float r_scale = capped ? u.lim_r / r_box : 1.0f;
+    const float xr = xr_box * r_scale, yr = yr_box * r_scale;
+    const bool in_x = xr_raw <= u.lim_pos_x && xr_raw >= u.lim_neg_x && !capped;
+    const bool in_y = yr_raw <= u.lim_pos_y && yr_raw >= u.lim_neg_y && !capped;
+    const float xc = xr * mz, yc = yr * mz;
+    const float inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z;
+    const float x = xc * inv_z, y = yc * inv_z;
+    const float r2 = x * x + y * y, r4 = r2 * r2;
+    const float N = 1.0f + k1 * r2 + k2 * r4 + k3 * r2 * r4;
+    const float D = 1.0f + k4 * r2 + k5 * r4 + k6 * r2 * r4;
+    const float Np = k1 + 2.0f * k2 * r2 + 3.0f * k3 * r4;
+    const float Dp = k4 + 2.0f * k5 * r2 + 3.0f * k6 * r4;
+    const float Npp = 2.0f * k2 + 6.0f * k3 * r2;
+    const float Dpp = 2.0f * k5 + 6.0f * k6 * r2;
+    const float iD = 1.0f / D, iD2 = iD * iD, iD3 = iD2 * iD;
+    const float R0 = N * iD;
+    const float R1 = (Np * D - N * Dp) * iD2;
+    const float R2 = (Npp * D * D - 2.0f * Np * D * Dp - N * Dpp * D + 2.0f * N * Dp * Dp) * iD3;
+    const float Rx = 2.0f * x * R1, Ry = 2.0f * y * R1;
+    const float R1x = 2.0f * x * R2, R1y = 2.0f * y * R2;
+    const float a00 = R0 + 2.0f * x * x * R1 + 2.0f * p1 * y + 6.0f * p2 * x;
+    const float a01 = 2.0f * x * y * R1 + 2.0f * p1 * x + 2.0f * p2 * y;
+    const float a10 = a01;
+    const float a11 = R0 + 2.0f * y * y * R1 + 6.0f * p1 * y + 2.0f * p2 * x;
+    const float s00 = fx * a00 * inv_z, s01 = fx * a01 * inv_z, s02 = -fx * (a00 * xc + a01 * yc) * inv_z2;
+    const float s10 = fy * a10 * inv_z, s11 = fy * a11 * inv_z, s12 = -fy * (a10 * xc + a11 * yc) * inv_z2;
+    const float e00 = in_x ? s00 : 0.0f, e10 = in_x ? s10 : 0.0f;
+    const float e01 = in_y ? s01 : 0.0f, e11 = in_y ? s11 : 0.0f;
+    const float e02 = ((in_x ? 0.0f : xr * s00) + (in_y ? 0.0f : yr * s01)) + s02;
+    const float e12 = ((in_x ? 0.0f : xr * s10) + (in_y ? 0.0f : yr * s11)) + s12;
+    float v_x = e00 * v_mean2d.x + e10 * v_mean2d.y;
+    float v_y = e01 * v_mean2d.x + e11 * v_mean2d.y;
+    float v_z = e02 * v_mean2d.x + e12 * v_mean2d.y;
+    const M23 tmp = s2_mul_m23(v_cov2d, M23{V2{e00, e10}, V2{e01, e11}, V2{e02, e12}});
+    const float gu0 = 2.0f * dot(m23_row0(tmp), s3_row0(cov_c)), gu1 = 2.0f * dot(m23_row0(tmp), s3_row1(cov_c));
+    const float gu2 = 2.0f * dot(m23_row0(tmp), s3_row2(cov_c));
+    const float gv0 = 2.0f * dot(m23_row1(tmp), s3_row0(cov_c)), gv1 = 2.0f * dot(m23_row1(tmp), s3_row1(cov_c));
+    const float gv2 = 2.0f * dot(m23_row1(tmp), s3_row2(cov_c));
+    const float wu0 = in_x ? gu0 : xr * gu2, wv0 = in_x ? gv0 : xr * gv2;
+    const float wu1 = in_y ? gu1 : yr * gu2, wv1 = in_y ? gv1 : yr * gv2;
+    const float wu2 = gu2, wv2 = gv2;
+    // derivatives of the distortion Jacobian entries in (x, y)
+    const float a00x = Rx + 4.0f * x * R1 + 2.0f * x * x * R1x + 6.0f * p2;
+    const float a00y = Ry + 2.0f * x * x * R1y + 2.0f * p1;
+    const float a01x = 2.0f * y * R1 + 2.0f * x * y * R1x + 2.0f * p1;
+    const float a01y = 2.0f * x * R1 + 2.0f * x * y * R1y + 2.0f * p2;
+    const float a10x = a01x, a10y = a01y;
+    const float a11x = Rx + 2.0f * y * y * R1x + 2.0f * p2;
+    const float a11y = Ry + 4.0f * y * R1 + 2.0f * y * y * R1y + 6.0f * p1;
+    // ... in (xc, yc, Z)
+    const float a00_xc = a00x * inv_z, a00_yc = a00y * inv_z, a00_z = -(xc * a00x + yc * a00y) * inv_z2;
+    const float a01_xc = a01x * inv_z, a01_yc = a01y * inv_z, a01_z = -(xc * a01x + yc * a01y) * inv_z2;
+    const float a10_xc = a10x * inv_z, a10_yc = a10y * inv_z, a10_z = -(xc * a10x + yc * a10y) * inv_z2;
+    const float a11_xc = a11x * inv_z, a11_yc = a11y * inv_z, a11_z = -(xc * a11x + yc * a11y) * inv_z2;
+    const float s00_xc = fx * a00_xc * inv_z, s00_yc = fx * a00_yc * inv_z, s00_z = fx * (a00_z * inv_z - a00 * inv_z2);
+    const float s01_xc = fx * a01_xc * inv_z, s01_yc = fx * a01_yc * inv_z, s01_z = fx * (a01_z * inv_z - a01 * inv_z2);
+    const float s10_xc = fy * a10_xc * inv_z, s10_yc = fy * a10_yc * inv_z, s10_z = fy * (a10_z * inv_z - a10 * inv_z2);
+    const float s11_xc = fy * a11_xc * inv_z, s11_yc = fy * a11_yc * inv_z, s11_z = fy * (a11_z * inv_z - a11 * inv_z2);
+    const float s02_xc = -fx * (a00_xc * xc + a00 + a01_xc * yc) * inv_z2;
+    const float s02_yc = -fx * (a00_yc * xc + a01_yc * yc + a01) * inv_z2;
+    const float s02_z = -fx * ((a00_z * xc + a01_z * yc) * inv_z2 - 2.0f * (a00 * xc + a01 * yc) * inv_z3);
+    const float s12_xc = -fy * (a10_xc * xc + a10 + a11_xc * yc) * inv_z2;
+    const float s12_yc = -fy * (a10_yc * xc + a11_yc * yc + a11) * inv_z2;
+    const float s12_z = -fy * ((a10_z * xc + a11_z * yc) * inv_z2 - 2.0f * (a10 * xc + a11 * yc) * inv_z3);
+    const float c_xc = wu0 * s00_xc + wu1 * s01_xc + wu2 * s02_xc + wv0 * s10_xc + wv1 * s11_xc + wv2 * s12_xc;
+    const float c_yc = wu0 * s00_yc + wu1 * s01_yc + wu2 * s02_yc + wv0 * s10_yc + wv1 * s11_yc + wv2 * s12_yc;
+    const float c_z = wu0 * s00_z + wu1 * s01_z + wu2 * s02_z + wv0 * s10_z + wv1 * s11_z + wv2 * s12_z;
+    if (in_x) v_x += c_xc;
+    if (in_y) v_y += c_yc;
+    v_z += c_z;
+    if (!in_x) v_z += xr * c_xc;
+    if (!in_y) v_z += yr * c_yc;
+    return V3{v_x, v_y, v_z};
+}
+
+// kernels/camera_model/thin_prism_fisheye.rs:118-203
+V3 projection_vjp_tpf(M23 J, V3 mc, S3 cov_c, const or_camera& u, S2 v_cov2d, V2 v_mean2d) {
+    const V3 kg = projection_vjp_kb4(J, mc, cov_c, u, v_cov2d, v_mean2d);
+    const float fx = u.fx, fy = u.fy;
+    const float p1 = u.dist[0], p2 = u.dist[1], sx1 = u.dist[2], sy1 = u.dist[3];
+    const float inv_z = 1.0f / mc.z, inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z, inv_z4 = inv_z2 * inv_z2;
+    const TpPolys t = thin_prism_polys(mc.x, mc.y, u);
+    const float nu_xx = 6.0f * p2 + 2.0f * sx1, nu_yy = 2.0f * p2 + 2.0f * sx1, nu_xy = 2.0f * p1;
+    const float nv_xx = 2.0f * p1 + 2.0f * sy1, nv_yy = 6.0f * p1 + 2.0f * sy1, nv_xy = 2.0f * p2;
+    const float hu00 = nu_xx * inv_z2, hu01 = nu_xy * inv_z2, hu11 = nu_yy * inv_z2;
+    const float hu02 = -2.0f * t.dnu_dx * inv_z3, hu12 = -2.0f * t.dnu_dy * inv_z3, hu22 = 6.0f * t.nu * inv_z4;
+    const float hv00 = nv_xx * inv_z2, hv01 = nv_xy * inv_z2, hv11 = nv_yy * inv_z2;
+    const float hv02 = -2.0f * t.dnv_dx * inv_z3, hv12 = -2.0f * t.dnv_dy * inv_z3, hv22 = 6.0f * t.nv * inv_z4;
+    const M23 tmp = s2_mul_m23(v_cov2d, J);
+    const float gu0 = 2.0f * dot(m23_row0(tmp), s3_row0(cov_c)), gu1 = 2.0f * dot(m23_row0(tmp), s3_row1(cov_c));
+    const float gu2 = 2.0f * dot(m23_row0(tmp), s3_row2(cov_c));
+    const float gv0 = 2.0f * dot(m23_row1(tmp), s3_row0(cov_c)), gv1 = 2.0f * dot(m23_row1(tmp), s3_row1(cov_c));
+    const float gv2 = 2.0f * dot(m23_row1(tmp), s3_row2(cov_c));
+    const float ax = fx * (gu0 * hu00 + gu1 * hu01 + gu2 * hu02) + fy * (gv0 * hv00 + gv1 * hv01 + gv2 * hv02);
+    const float ay = fx * (gu0 * hu01 + gu1 * hu11 + gu2 * hu12) + fy * (gv0 * hv01 + gv1 * hv11 + gv2 * hv12);
+    const float az = fx * (gu0 * hu02 + gu1 * hu12 + gu2 * hu22) + fy * (gv0 * hv02 + gv1 * hv12 + gv2 * hv22);
+    return V3{kg.x + ax, kg.y + ay, kg.z + az};
+}
+
+V3 projection_vjp(M23 J, V3 mc, S3 cov_c, const or_camera& u, S2 v_cov2d, V2 v_mean2d) {
+    switch (u.model) {
+    case OR_MODEL_KB4: return projection_vjp_kb4(J, mc, cov_c, u, v_cov2d, v_mean2d);
+    case OR_MODEL_RT8: return projection_vjp_rt8(mc, cov_c, u, v_cov2d, v_mean2d);
+    case OR_MODEL_TPF: return projection_vjp_tpf(J, mc, cov_c, u, v_cov2d, v_mean2d);
+    default: return projection_vjp_pinhole(J, mc, cov_c, u, v_cov2d, v_mean2d);
+    }
 }
 
 // --- covariance ----------------------------------------------------------------
@@ -625,7 +830,7 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         const float* t = transforms + (size_t)g * 10;
         const V3 mean_c = world_to_cam(v3(t[0], t[1], t[2]), u);
         if (!(finite3(mean_c) && mean_c.z <= 1.0e10f)) continue;
-        if (u.model == OR_MODEL_PINHOLE) {
+        if (u.model == OR_MODEL_PINHOLE) {             // the fisheye models cull by angle
             if (mean_c.z < 0.01f) continue;
         } else {
             const float r = std::sqrt(mean_c.x * mean_c.x + mean_c.y * mean_c.y);
@@ -1052,8 +1257,7 @@ static SplatVjp splat_vjp(const or_fwd* f, uint32_t g, const float* t, float raw
     const M3 vrot = view_rot(u);
     const S3 cov_c = s3_congruence(covar, vrot);
     const M23 J = project_jacobian(mean_c, u);
-    const V3 v_mean_c = (u.model == OR_MODEL_KB4) ? projection_vjp_kb4(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]})
-                                                    : projection_vjp_pinhole(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]});
+    const V3 v_mean_c = projection_vjp(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]});
     const S3 vcc = m23_tcongruence_s2(J, v_cov2d);
     SplatVjp r;
     r.v_mean = add(tmul_vec3(vrot, v_mean_c), v_mean_sh);
@@ -1455,25 +1659,92 @@ double kb4_inv(double target, const float* k) {
     }
     return 0.5 * (lo + hi);
 }
+// camera.rs:238-303: the RT8 radial factor and its two inverses.
+double rt8_radial(double r, const float* k) {
+    const double r2 = r * r, r4 = r2 * r2, r6 = r4 * r2;
+    return (1.0 + (double)k[0] * r2 + (double)k[1] * r4 + (double)k[2] * r6) /
+           (1.0 + (double)k[3] * r2 + (double)k[4] * r4 + (double)k[5] * r6);
+}
+double rt8_undistort(double r_d, const float* k) {
+    double r = r_d;
+    for (int it = 0; it < 30; ++it) {
+        const double f = rt8_radial(r, k);
+        if (std::fabs(f) < 1e-12) break;
+        const double nr = r_d / f;
+        if (std::fabs(nr - r) < 1e-12) { r = nr; break; }
+        r = nr;
+    }
+    return r;
+}
+double rt8_corner(double r_d, const float* k) {     // < 0: no crossing below r = 16
+    const double step = 16.0 / 4096;
+    double lo = 0.0, hi = -1.0;
+    for (int i = 1; i <= 4096; ++i) {
+        const double r = i * step;
+        if (r * rt8_radial(r, k) >= r_d) { hi = r; break; }
+        lo = r;
+    }
+    if (hi < 0.0) return -1.0;
+    for (int it = 0; it < 64; ++it) {
+        const double mid = 0.5 * (lo + hi);
+        if (mid * rt8_radial(mid, k) < r_d) lo = mid; else hi = mid;
+        if (hi - lo < 1e-12) break;
+    }
+    return 0.5 * (lo + hi);
+}
 } // namespace
+
+extern "C" double or_rt8_radial(double r, const float dist[8]) { return rt8_radial(r, dist); }
+extern "C" double or_rt8_undistort_radius(double r_d, const float dist[8]) { return rt8_undistort(r_d, dist); }
+extern "C" double or_rt8_undistort_corner_radius(double r_d, const float dist[8]) { return rt8_corner(r_d, dist); }
+// calculate_jacobian_clamp_limits (camera.rs:305-374) for a model and pinhole
+// parameters: out = lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y, lim_r.
+extern "C" void or_clamp_limits(int model, uint32_t img_w, uint32_t img_h, float fx, float fy, float cx, float cy,
+                                const float dist[8], float out[5]) {
+    const float w = (float)img_w, h = (float)img_h;
+    out[0] = out[1] = out[2] = out[3] = 0.0f;
+    out[4] = 3.40282347e+38f;
+    const float epx = (1.15f * w - cx) / fx, epy = (1.15f * h - cy) / fy;
+    const float enx = (-0.15f * w - cx) / fx, eny = (-0.15f * h - cy) / fy;
+    if (model == OR_MODEL_PINHOLE) {
+        out[0] = epx; out[1] = epy; out[2] = enx; out[3] = eny;
+    } else if (model == OR_MODEL_RT8) {
+        auto und = [&](float e) {
+            const float sgn = std::signbit(e) ? -1.0f : 1.0f;
+            return (float)rt8_undistort((double)std::fabs(e), dist) * sgn;
+        };
+        out[0] = und(epx); out[1] = und(epy); out[2] = und(enx); out[3] = und(eny);
+        const double cd = std::hypot((double)fmax_(std::fabs(epx), std::fabs(enx)),
+                                     (double)fmax_(std::fabs(epy), std::fabs(eny)));
+        const double r = rt8_corner(cd, dist);
+        if (r >= 0.0) out[4] = (float)r;
+    }
+}
 
 extern "C" double or_kb4_d(double theta, const float kb4[4]) { return kb4_d(theta, kb4); }
 extern "C" double or_kb4_dd_dtheta(double theta, const float kb4[4]) { return kb4_dd(theta, kb4); }
 extern "C" double or_kb4_invert_d(double target, const float kb4[4]) { return kb4_inv(target, kb4); }
-extern "C" double or_fov_to_focal(double fov, uint32_t pixels, int model, const float kb4[4]) {
+// params: kb4 k1..k4 then dist[8]
+extern "C" double or_fov_to_focal(double fov, uint32_t pixels, int model, const float params[12]) {
     const double half = fov / 2.0;
     const double r_pix = (double)pixels / 2.0;
-    const double projected = (model == OR_MODEL_KB4) ? kb4_d(half, kb4) : std::tan(half);
+    double projected;
+    if (model == OR_MODEL_KB4 || model == OR_MODEL_TPF) projected = kb4_d(half, params);
+    else if (model == OR_MODEL_RT8) { const double r = std::tan(half); projected = r * rt8_radial(r, params + 4); }
+    else projected = std::tan(half);
     return r_pix / projected;
 }
-extern "C" double or_focal_to_fov(double focal, uint32_t pixels, int model, const float kb4[4]) {
+extern "C" double or_focal_to_fov(double focal, uint32_t pixels, int model, const float params[12]) {
     const double r_pix = (double)pixels / 2.0;
     const double r_norm = r_pix / focal;
-    const double half = (model == OR_MODEL_KB4) ? kb4_inv(r_norm, kb4) : std::atan(r_norm);
+    double half;
+    if (model == OR_MODEL_KB4 || model == OR_MODEL_TPF) half = kb4_inv(r_norm, params);
+    else if (model == OR_MODEL_RT8) half = std::atan(rt8_undistort(r_norm, params + 4));
+    else half = std::atan(r_norm);
     return 2.0 * half;
 }
-extern "C" double or_max_render_theta(int model, const float kb4[4]) {
-    return (model == OR_MODEL_KB4) ? kb4_fold(kb4) : M_PI;
+extern "C" double or_max_render_theta(int model, const float params[12]) {
+    return (model == OR_MODEL_KB4 || model == OR_MODEL_TPF) ? kb4_fold(params) : M_PI;
 }
 
 // ---- image loss: L1 + SSIM, crates/splat-train-loss/src/lib.rs:226-1306 ------------

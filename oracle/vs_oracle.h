@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-enum { OR_MODEL_PINHOLE = 0, OR_MODEL_KB4 = 1 };
+enum { OR_MODEL_PINHOLE = 0, OR_MODEL_KB4 = 1, OR_MODEL_RT8 = 2, OR_MODEL_TPF = 3 };
 
 /* Device-side ProjectUniforms of the reference
  * (crates/splat-train-render/src/kernels/types.rs:53-82) minus the sizes. */
@@ -32,6 +32,7 @@ typedef struct or_camera {
     float cam_pos[3];
     float half_max_render_fov;
     float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y, lim_r;
+    float dist[8];              /* RT8: k1..k6, p1, p2; thin-prism: p1, p2, sx1, sy1 */
 } or_camera;
 
 /* Render flags (RasterPass semantics, gaussian_splats.rs:32-107). */

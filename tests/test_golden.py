@@ -21,11 +21,20 @@ def _load(path):
         return {k: z[k] for k in z.files}
 
 
-def _camera(fx):
+def _camera_bytes(fx):
+    """The fixture's vs_camera bytes.  Fixtures written before the struct grew
+    its distortion block (dist[8], appended) hold the first 120 bytes; the
+    block is zero for their pinhole and KB4 cameras."""
     from vauss_amd import _lib
     raw = fx["camera"].tobytes()
-    assert len(raw) == C.sizeof(_lib.VsCamera)
-    return _lib.VsCamera.from_buffer_copy(raw)
+    full = C.sizeof(_lib.VsCamera)
+    assert len(raw) in (120, full)
+    return raw + bytes(full - len(raw))
+
+
+def _camera(fx):
+    from vauss_amd import _lib
+    return _lib.VsCamera.from_buffer_copy(_camera_bytes(fx))
 
 
 def test_fixtures_present():
@@ -36,7 +45,7 @@ def test_fixtures_present():
 def test_oracle_reproduces_fixture(path):
     from oracle import pyoracle as po
     fx = _load(path)
-    cam = po.OrCamera.from_buffer_copy(fx["camera"].tobytes())
+    cam = po.OrCamera.from_buffer_copy(_camera_bytes(fx))
     img = tuple(int(v) for v in fx["img_size"])
     f = po.render_forward(cam, img, fx["transforms"], fx["sh_coeffs"], fx["raw_opacities"],
                           background=tuple(fx["background"]), flags=int(fx["flags"]))

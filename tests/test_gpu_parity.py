@@ -89,7 +89,7 @@ def _check_grads(got, want, name, rtol=1e-3, atol=1e-5, group_rtol=1e-3):
     assert not tight.any(), f"{name}: {tight.sum()} entries exceed {group_rtol:g} of the group maximum (max err {err.max():.3e})"
 
 
-def _check_param_grads(g, rg, ref, vc):
+def _check_param_grads(g, rg, ref, vc, exclude=None):
     """Dense parameter gradients, end to end and per stage.
 
     End to end (GPU raster + projection VJPs vs the oracle's) at the contract
@@ -98,19 +98,23 @@ def _check_param_grads(g, rg, ref, vc):
     magnitude where its terms cancel (a splat with |v_conic| ~ 1 and
     |v_quat| ~ 1e-6), so the projection stage is also checked on its own: the
     oracle's projection VJP applied to the GPU's own v_combined must agree to
-    1e-5 relative / 1e-3 of the group maximum."""
+    1e-5 relative / 1e-3 of the group maximum.  `exclude` (a boolean row mask)
+    drops rows from the end-to-end check only: rows whose gradients the
+    oracle itself moves past the bar under 1e-6 relative noise in v_combined
+    (see ill_conditioned_rows)."""
     vt = g.v_transforms.cpu().numpy()
     vs = g.v_coeffs.cpu().numpy().reshape(len(vt), -1)
     vo = g.v_raw_opac.cpu().numpy()
     vr = g.v_refine_weight.cpu().numpy()
     assert np.isfinite(vt).all() and np.isfinite(vs).all()
+    keep = slice(None) if exclude is None else ~exclude
     for got, want, name in ((vt[:, 0:3], rg["v_transforms"][:, 0:3], "v_means"),
                             (vt[:, 3:7], rg["v_transforms"][:, 3:7], "v_quats"),
                             (vt[:, 7:10], rg["v_transforms"][:, 7:10], "v_log_scales"),
                             (vo, rg["v_raw_opac"], "v_raw_opacity"),
                             (vs, rg["v_sh"].reshape(len(vt), -1), "v_sh"),
                             (vr, rg["v_refine"], "v_refine_weight")):
-        _check_grads(got, want, name, group_rtol=None)
+        _check_grads(got[keep], want[keep], name, group_rtol=None)
     pg = ref.project_backward(vc)
     for got, want, name in ((vt[:, 0:3], pg["v_transforms"][:, 0:3], "v_means (projection stage)"),
                             (vt[:, 3:7], pg["v_transforms"][:, 3:7], "v_quats (projection stage)"),
@@ -219,3 +223,19 @@ def test_quadrant_culling_stress(pass_):
     _check_grads(vc[:, 0:5], rg["v_combined"][:, 0:5], "v_xy_conic")
     _check_grads(vc[:, 5:9], rg["v_combined"][:, 5:9], "v_rgb_opacity")
     _check_grads(vc[:, 9], rg["v_combined"][:, 9], "v_refine")
+
+
+def ill_conditioned_rows(ref, vc, seed=1):
+    """Rows whose projection-VJP output the oracle itself moves past the
+    end-to-end bar (1e-3 relative / 1e-5 absolute) when v_combined carries
+    1e-6 relative noise, the size of the f32 atomic-order differences between
+    two correct raster backwards."""
+    rng = np.random.default_rng(seed)
+    noisy = (vc.astype(np.float64) * (1 + 1e-6 * rng.standard_normal(vc.shape))).astype(np.float32)
+    a, b = ref.project_backward(vc), ref.project_backward(noisy)
+    bad = np.zeros(vc.shape[0], bool)
+    for key in ("v_transforms", "v_sh", "v_raw_opac"):
+        x = a[key].reshape(vc.shape[0], -1).astype(np.float64)
+        y = b[key].reshape(vc.shape[0], -1).astype(np.float64)
+        bad |= (np.abs(x - y) > 1e-5 + 1e-3 * np.abs(x)).any(axis=1)
+    return bad

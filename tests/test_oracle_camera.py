@@ -180,3 +180,89 @@ def test_camera_uniforms_agree_between_oracle_and_library(model):
     if model is None:   # camera.rs:327-332
         assert abs(u.lim_pos_x - (1.15 * 640 - u.cx) / u.fx) < 1e-6
         assert abs(u.lim_neg_y - (-0.15 * 480 - u.cy) / u.fy) < 1e-6
+
+
+# ---- RT8 and thin-prism fisheye (camera.rs:425-431, 494-575; tests/mod.rs:844-883) ----
+
+RT8_PINCUSHION = (0.15, 0.08, 0.02, 0.03, 0.0, 0.0, 0.001, -0.002)   # k1..k6, p1, p2
+KB4_MILD = (-0.01, 0.003, -0.0005, 0.00002)
+
+
+def _library_limits(model, img, f, c):
+    """Clamp limits from vs_camera_uniforms for a camera of focal f (both axes)."""
+    cam = vcam.Camera.from_focal(f, f, img, center=c, model=model)
+    u = cam.uniforms(img)
+    return (u.lim_pos_x, u.lim_pos_y, u.lim_neg_x, u.lim_neg_y, u.lim_r), u
+
+
+def test_rt8_radial_cap_matches_image_corner():
+    img = (1920, 1080)
+    corner_d = math.hypot((1.15 * 1920.0 - 960.0) / 800.0, (1.15 * 1080.0 - 540.0) / 800.0)
+    lims = [po.clamp_limits(po.MODEL_RT8, img, 800.0, 800.0, 960.0, 540.0, RT8_PINCUSHION)]
+    lib_lims, u = _library_limits(vcam.RadialTangential8(*RT8_PINCUSHION), img, 800.0, (960.0, 540.0))
+    assert abs(u.fx - 800.0) < 1e-3
+    lims.append(lib_lims)
+    for (lim_pos_x, lim_pos_y, _, _, lim_r), tol in zip(lims, (1e-5, 1e-4)):   # the library's fx is f32 of a round trip
+        assert abs(lim_r * po.rt8_radial(lim_r, RT8_PINCUSHION) - corner_d) < tol
+        assert lim_r < math.hypot(lim_pos_x, lim_pos_y)
+        assert lim_pos_x < lim_r and lim_pos_y < lim_r
+    np.testing.assert_allclose(lims[0], lims[1], rtol=1e-5)
+
+
+def test_rt8_radial_cap_is_unbounded_when_the_polynomial_folds():
+    img = (1920, 1080)
+    barrel = (-0.5, 0, 0, 0, 0, 0, 0, 0)
+    assert po.clamp_limits(po.MODEL_RT8, img, 500.0, 500.0, 960.0, 540.0, barrel)[4] == np.float32(3.40282347e38)
+    lib_lims, _ = _library_limits(vcam.RadialTangential8(*barrel), img, 500.0, (960.0, 540.0))
+    assert lib_lims[4] == np.float32(3.40282347e38)
+    assert po.rt8_undistort_corner_radius(10.0, barrel) is None
+    for model, m in ((po.MODEL_PINHOLE, None), (po.MODEL_KB4, vcam.KannalaBrandt4(*ULTRAWIDE))):
+        assert po.clamp_limits(model, img, 500.0, 500.0, 960.0, 540.0)[4] == np.float32(3.40282347e38)
+        assert _library_limits(m, img, 500.0, (960.0, 540.0))[0][4] == np.float32(3.40282347e38)
+    # the fisheye models leave the per-axis limits at zero
+    assert _library_limits(vcam.KannalaBrandt4(*ULTRAWIDE), img, 500.0, (960.0, 540.0))[0][:4] == (0.0,) * 4
+
+
+def test_rt8_focal_to_fov_and_back():
+    rt8 = (-0.2, 0.05, -0.001, 0.0, 0.0, 0.0, 0.0, 0.0)
+    fov = po.focal_to_fov(900.0, 1920, po.MODEL_RT8, dist=rt8)
+    assert abs(po.fov_to_focal(fov, 1920, po.MODEL_RT8, dist=rt8) - 900.0) < 1e-6
+    m = vcam.RadialTangential8(*rt8)
+    fov_l = vcam.focal_to_fov(900.0, 1920, m)
+    assert abs(vcam.fov_to_focal(fov_l, 1920, m) - 900.0) < 1e-6
+    assert abs(fov - fov_l) < 1e-12
+    # a radial factor below 1 (barrel) widens the fov past the pinhole's
+    assert fov > po.focal_to_fov(900.0, 1920)
+
+
+def test_tpf_focal_to_fov_and_back_follows_kb4():
+    tp = (1e-3, -2e-3, 5e-4, -5e-4)
+    for impl_fov, impl_focal, impl_theta in (
+            (lambda f, px: po.focal_to_fov(f, px, po.MODEL_TPF, KB4_MILD, tp),
+             lambda v, px: po.fov_to_focal(v, px, po.MODEL_TPF, KB4_MILD, tp),
+             lambda k: po.max_render_theta(po.MODEL_TPF, k, tp)),
+            (lambda f, px: vcam.focal_to_fov(f, px, vcam.ThinPrismFisheye(vcam.KannalaBrandt4(*KB4_MILD), *tp)),
+             lambda v, px: vcam.fov_to_focal(v, px, vcam.ThinPrismFisheye(vcam.KannalaBrandt4(*KB4_MILD), *tp)),
+             lambda k: vcam.max_render_theta(vcam.ThinPrismFisheye(vcam.KannalaBrandt4(*k), *tp)))):
+        fov = impl_fov(280.0, 1024)
+        assert abs(impl_focal(fov, 1024) - 280.0) < 1e-6
+        assert abs(fov - po.focal_to_fov(280.0, 1024, po.MODEL_KB4, KB4_MILD)) < 1e-12
+        # camera.rs:505-514: the thin-prism model folds where its KB4 part does
+        assert impl_theta(ULTRAWIDE) == po.max_render_theta(po.MODEL_KB4, ULTRAWIDE)
+
+
+def test_rt8_and_tpf_uniforms():
+    img = (640, 480)
+    rt8 = vcam.RadialTangential8(-0.05, 0.01, 0.0, 0.0, 0.0, 0.0, 1e-3, -1e-3)
+    u = vcam.Camera(0.9, 0.7, (0.5, 0.5), (0.0, 0.0, -4.0), (0.0, 0.0, 0.0, 1.0), rt8).uniforms(img)
+    assert u.model == 2 and tuple(u.dist) == tuple(np.float32(v) for v in (-0.05, 0.01, 0, 0, 0, 0, 1e-3, -1e-3))
+    assert tuple(u.kb4) == (0.0,) * 4 and abs(u.half_max_render_fov - math.hypot(0.9, 0.7) * 1.05 / 2) < 1e-6
+    want = po.clamp_limits(po.MODEL_RT8, img, u.fx, u.fy, u.cx, u.cy, list(u.dist))
+    np.testing.assert_array_equal(np.array([u.lim_pos_x, u.lim_pos_y, u.lim_neg_x, u.lim_neg_y, u.lim_r], np.float32),
+                                  np.array(want, np.float32))
+    tpf = vcam.ThinPrismFisheye(vcam.KannalaBrandt4(*ULTRAWIDE), 1e-3, -2e-3, 5e-4, -5e-4)
+    u = vcam.Camera(1.2, 1.0, (0.5, 0.5), (0.0, 0.0, -4.0), (0.0, 0.0, 0.0, 1.0), tpf).uniforms(img)
+    assert u.model == 3 and tuple(u.kb4) == tuple(np.float32(v) for v in ULTRAWIDE)
+    assert tuple(u.dist)[:4] == tuple(np.float32(v) for v in (1e-3, -2e-3, 5e-4, -5e-4))
+    assert abs(u.half_max_render_fov - min(math.hypot(1.2, 1.0) * 1.05 / 2,
+                                           po.max_render_theta(po.MODEL_KB4, ULTRAWIDE))) < 1e-6

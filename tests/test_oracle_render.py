@@ -263,7 +263,11 @@ def _fd_check(model, seed):
     assert checked >= 20
 
 
-@pytest.mark.parametrize("model", [None, vcam.KannalaBrandt4(0.08, -0.05, 0.03, -0.02)], ids=["pinhole", "kb4"])
+@pytest.mark.parametrize("model", [None, vcam.KannalaBrandt4(0.08, -0.05, 0.03, -0.02),
+                                   vcam.RadialTangential8(-0.15, 0.06, -0.01, 0.05, 0.02, -0.005, 0.03, -0.02),
+                                   vcam.ThinPrismFisheye(vcam.KannalaBrandt4(0.08, -0.05, 0.03, -0.02),
+                                                         0.03, -0.02, 0.015, -0.015)],
+                         ids=["pinhole", "kb4", "rt8", "tpf"])
 @pytest.mark.parametrize("seed", [0x1234, 2])
 def test_gradients_match_central_differences(model, seed):
     _fd_check(model, seed)
@@ -297,20 +301,43 @@ def _quat_to_mat(q):
 
 
 def _project_closed_form(p, model, fx, fy, cx, cy):
-    """Pixel position of a camera-space point: pinhole, or Kannala-Brandt-4
-    d(theta) = theta (1 + k1 theta^2 + k2 theta^4 + k3 theta^6 + k4 theta^8)."""
+    """Pixel position of a camera-space point: pinhole; Kannala-Brandt-4
+    d(theta) = theta (1 + k1 theta^2 + k2 theta^4 + k3 theta^6 + k4 theta^8);
+    OpenCV's rational radial + tangential model on (x/z, y/z); COLMAP's thin
+    prism fisheye = KB4 + (2 p1 uv + p2 (r^2 + 2u^2) + sx1 r^2, ...) on (u, v) =
+    (x/z, y/z)."""
     x, y, z = p
     if model is None:
         return np.array([fx * x / z + cx, fy * y / z + cy])
+    if isinstance(model, vcam.RadialTangential8):
+        m = model
+        u, v = x / z, y / z
+        r2 = u * u + v * v
+        rad = (1 + m.k1 * r2 + m.k2 * r2 ** 2 + m.k3 * r2 ** 3) / (1 + m.k4 * r2 + m.k5 * r2 ** 2 + m.k6 * r2 ** 3)
+        ud = u * rad + 2 * m.p1 * u * v + m.p2 * (r2 + 2 * u * u)
+        vd = v * rad + 2 * m.p2 * u * v + m.p1 * (r2 + 2 * v * v)
+        return np.array([fx * ud + cx, fy * vd + cy])
+    kb = model.kb4 if isinstance(model, vcam.ThinPrismFisheye) else model
     r = np.hypot(x, y)
     th = np.arctan2(r, z)
-    k = (model.k1, model.k2, model.k3, model.k4)
+    k = (kb.k1, kb.k2, kb.k3, kb.k4)
     t2 = th * th
     d = th * (1 + k[0] * t2 + k[1] * t2 ** 2 + k[2] * t2 ** 3 + k[3] * t2 ** 4)
-    return np.array([fx * d * x / r + cx, fy * d * y / r + cy])
+    out = np.array([fx * d * x / r + cx, fy * d * y / r + cy])
+    if isinstance(model, vcam.ThinPrismFisheye):
+        m = model
+        u, v = x / z, y / z
+        r2 = u * u + v * v
+        out += np.array([fx * (2 * m.p1 * u * v + m.p2 * (r2 + 2 * u * u) + m.sx1 * r2),
+                         fy * (2 * m.p2 * u * v + m.p1 * (r2 + 2 * v * v) + m.sy1 * r2)])
+    return out
 
 
-@pytest.mark.parametrize("model", [None, KB4_MODEL], ids=["pinhole", "kb4"])
+RT8_MODEL = vcam.RadialTangential8(-0.15, 0.06, -0.01, 0.05, 0.02, -0.005, 0.03, -0.02)
+TPF_MODEL = vcam.ThinPrismFisheye(vcam.KannalaBrandt4(0.02, -0.01, 0.005, -0.001), 0.03, -0.02, 0.015, -0.015)
+
+
+@pytest.mark.parametrize("model", [None, KB4_MODEL, RT8_MODEL, TPF_MODEL], ids=["pinhole", "kb4", "rt8", "tpf"])
 def test_projection_matches_closed_form(model):
     """Mean, conic, opacity and colour of each projected row against float64
     closed forms: mean = proj(W x + t); Sigma2D = J R S^2 R^T J^T + 0.3 I with J
@@ -353,3 +380,48 @@ def test_projection_matches_closed_form(model):
         basis = po.sh_basis(3, (v / np.linalg.norm(v)).astype(np.float32)).astype(np.float64)
         color = basis @ sh[g].astype(np.float64) + 0.5
         np.testing.assert_allclose(row[6:9], color, rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("model", [None, KB4_MODEL, vcam.RadialTangential8(-0.1, 0.15, -0.02, 0.05, 0.1, -0.01, 0.03, -0.02),
+                                   TPF_MODEL], ids=["pinhole", "kb4", "rt8", "tpf"])
+def test_covariance_path_of_the_mean_gradient(model):
+    """The mean gradient carried by the conic alone (v_xy = 0): the derivative
+    of the projection Jacobian in the EWA covariance, which each camera model's
+    VJP writes out by hand (second derivatives of the distortion).  Checked
+    against central differences of a float64 conic whose Jacobian is itself a
+    central difference of the closed-form projection."""
+    img = (96, 80)
+    cam_obj = scenes.test_camera(img, fov=1.5, position=(0.0, 0.0, -4.0), model=model)
+    cam = cam_obj.uniforms(img)
+    fx, fy, cx, cy = (float(v) for v in (cam.fx, cam.fy, cam.cx, cam.cy))
+    rng = np.random.default_rng(12)
+    n = 24
+    means = np.stack([rng.uniform(-2.0, 2.0, n), rng.uniform(-1.6, 1.6, n), rng.uniform(-0.5, 0.5, n)], 1)
+    t = np.concatenate([means, rng.standard_normal((n, 4)), rng.uniform(-2.5, -1.5, (n, 3))], 1).astype(np.float32)
+    f = po.render_forward(cam, img, t, np.zeros((n, 1, 3), np.float32), np.full(n, 2.0, np.float32))
+    gfc = f.get(po.F_GLOBAL_FROM_COMPACT)
+    vc = np.zeros((n, 10), np.float32)
+    vc[:, 2:5] = rng.standard_normal((n, 3)).astype(np.float32)
+    g = f.project_backward(vc)["v_transforms"][:, 0:3].astype(np.float64)
+
+    def conic(g_, mean):
+        pc = mean + np.array([0.0, 0.0, 4.0])
+        J = np.zeros((2, 3))
+        for i in range(3):
+            h = np.zeros(3)
+            h[i] = 1e-6
+            J[:, i] = (_project_closed_form(pc + h, model, fx, fy, cx, cy) -
+                       _project_closed_form(pc - h, model, fx, fy, cx, cy)) / 2e-6
+        M = _quat_to_mat(t[g_, 3:7].astype(np.float64)) @ np.diag(np.exp(t[g_, 7:10].astype(np.float64)))
+        c = np.linalg.inv(J @ M @ M.T @ J.T + 0.3 * np.eye(2))
+        return np.array([c[0, 0], c[0, 1], c[1, 1]])
+
+    assert len(gfc) >= 16
+    for gi in gfc:
+        m0 = t[gi, :3].astype(np.float64)
+        num = np.zeros(3)
+        for i in range(3):
+            e = np.zeros(3)
+            e[i] = 1e-4
+            num[i] = vc[gi, 2:5].astype(np.float64) @ (conic(gi, m0 + e) - conic(gi, m0 - e)) / 2e-4
+        assert np.all(np.abs(g[gi] - num) <= 3e-4 * np.abs(num).max() + 1e-6), (gi, g[gi], num)

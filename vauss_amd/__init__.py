@@ -10,7 +10,9 @@ from .loss import (  # noqa: F401
     ImageLossConfig, image_loss, image_loss_backward, image_loss_eval, image_loss_forward_train,
     image_loss_partials, pack_rgba8,
 )
-from .camera import Camera, KannalaBrandt4, PINHOLE, fov_to_focal, focal_to_fov, max_render_theta  # noqa: F401
+from .camera import (  # noqa: F401
+    PINHOLE, Camera, KannalaBrandt4, RadialTangential8, ThinPrismFisheye, fov_to_focal, focal_to_fov, max_render_theta,
+)
 from .render import (  # noqa: F401
     Block8Moment, Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput,
     ShStepState, SplatGrads, SplatRenderMode, adam_bias_corrections, geo_decode, geo_encode, geo_zero_rows,
@@ -21,7 +23,7 @@ from .render import (  # noqa: F401
 __all__ = [
     "ImageLossConfig", "image_loss", "image_loss_backward", "image_loss_eval", "image_loss_forward_train",
     "image_loss_partials", "pack_rgba8",
-    "Camera", "KannalaBrandt4", "PINHOLE", "fov_to_focal", "focal_to_fov", "max_render_theta",
+    "Camera", "KannalaBrandt4", "RadialTangential8", "ThinPrismFisheye", "PINHOLE", "fov_to_focal", "focal_to_fov", "max_render_theta",
     "Block8Moment", "ShStepState", "adam_bias_corrections", "sh_step",
     "Context", "ForwardState", "FusedAdam", "ProjectUpdateResult", "RasterPass", "RenderAux", "RenderOutput",
     "SplatGrads", "SplatRenderMode", "VsError", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",

@@ -19,7 +19,7 @@ VS_SH_F32, VS_SH_F16 = 0, 1
 STATUS_NAMES = ["VS_OK", "VS_ERR_INVALID", "VS_ERR_HIP", "VS_ERR_OOM", "VS_ERR_UNSUPPORTED",
                 "VS_ERR_CAPACITY", "VS_ERR_NONFINITE"]
 
-CAMERA_PINHOLE, CAMERA_KB4 = 0, 1
+CAMERA_PINHOLE, CAMERA_KB4, CAMERA_RT8, CAMERA_TPF = 0, 1, 2, 3
 PASS_FORWARD, PASS_BACKWARD, PASS_FLOAT, PASS_BACKWARD_SMOOTH_CUTOFF, PASS_GEOMETRY = range(5)
 MODE_DEFAULT, MODE_MIP, MODE_SURFEL = range(3)
 # stage bits of vs_ctx_enable_timing, in vs_stage_times field order
@@ -31,12 +31,13 @@ class VsCamera(C.Structure):
     _fields_ = [("model", C.c_int32), ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float),
                 ("kb4", C.c_float * 4), ("viewmat", C.c_float * 12), ("cam_pos", C.c_float * 3),
                 ("half_max_render_fov", C.c_float), ("lim_pos_x", C.c_float), ("lim_pos_y", C.c_float),
-                ("lim_neg_x", C.c_float), ("lim_neg_y", C.c_float), ("lim_r", C.c_float)]
+                ("lim_neg_x", C.c_float), ("lim_neg_y", C.c_float), ("lim_r", C.c_float), ("dist", C.c_float * 8)]
 
 
 class VsPose(C.Structure):
     _fields_ = [("fov_x", C.c_double), ("fov_y", C.c_double), ("center_uv", C.c_float * 2),
-                ("position", C.c_float * 3), ("rotation", C.c_float * 4), ("model", C.c_int32), ("kb4", C.c_float * 4)]
+                ("position", C.c_float * 3), ("rotation", C.c_float * 4), ("model", C.c_int32), ("kb4", C.c_float * 4),
+                ("dist", C.c_float * 8)]
 
 
 class VsSplats(C.Structure):

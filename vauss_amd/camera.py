@@ -28,32 +28,69 @@ class KannalaBrandt4:
         return (C.c_float * 4)(self.k1, self.k2, self.k3, self.k4)
 
 
+@dataclass(frozen=True)
+class RadialTangential8:
+    """RadialTangential8Params (kernels/camera_model/radial_tangential_8.rs:9-21):
+    OpenCV's rational radial (k1..k6) plus tangential (p1, p2) model."""
+    k1: float = 0.0
+    k2: float = 0.0
+    k3: float = 0.0
+    k4: float = 0.0
+    k5: float = 0.0
+    k6: float = 0.0
+    p1: float = 0.0
+    p2: float = 0.0
+
+
+@dataclass(frozen=True)
+class ThinPrismFisheye:
+    """ThinPrismFisheyeParams (kernels/camera_model/thin_prism_fisheye.rs:21-29):
+    KB4 radial plus tangential (p1, p2) plus thin-prism (sx1, sy1)."""
+    kb4: KannalaBrandt4 = KannalaBrandt4()
+    p1: float = 0.0
+    p2: float = 0.0
+    sx1: float = 0.0
+    sy1: float = 0.0
+
+
 PINHOLE = None   # CameraModel::Pinhole
 
 
 def _model_args(model):
+    """(vs_camera_model, kb4[4], dist[8])."""
+    zero4, zero8 = [0.0] * 4, [0.0] * 8
     if model is None:
-        return _lib.CAMERA_PINHOLE, (C.c_float * 4)(0, 0, 0, 0)
+        return _lib.CAMERA_PINHOLE, zero4, zero8
     if isinstance(model, KannalaBrandt4):
-        return _lib.CAMERA_KB4, model.as_array()
-    raise ValueError(f"unsupported camera model {model!r} (pinhole or KannalaBrandt4)")
+        return _lib.CAMERA_KB4, [model.k1, model.k2, model.k3, model.k4], zero8
+    if isinstance(model, RadialTangential8):
+        return _lib.CAMERA_RT8, zero4, [model.k1, model.k2, model.k3, model.k4, model.k5, model.k6, model.p1, model.p2]
+    if isinstance(model, ThinPrismFisheye):
+        k = model.kb4
+        return _lib.CAMERA_TPF, [k.k1, k.k2, k.k3, k.k4], [model.p1, model.p2, model.sx1, model.sy1, 0.0, 0.0, 0.0, 0.0]
+    raise ValueError(f"unsupported camera model {model!r}")
+
+
+def _params(model):
+    m, k, d = _model_args(model)
+    return m, (C.c_float * 12)(*(k + d))
 
 
 def fov_to_focal(fov: float, pixels: int, model=PINHOLE) -> float:
     """camera.rs:99-116."""
-    m, k = _model_args(model)
+    m, k = _params(model)
     return _lib.load().vs_fov_to_focal(float(fov), int(pixels), m, k)
 
 
 def focal_to_fov(focal: float, pixels: int, model=PINHOLE) -> float:
     """camera.rs:118-134."""
-    m, k = _model_args(model)
+    m, k = _params(model)
     return _lib.load().vs_focal_to_fov(float(focal), int(pixels), m, k)
 
 
 def max_render_theta(model=PINHOLE) -> float:
     """camera.rs:166-172."""
-    m, k = _model_args(model)
+    m, k = _params(model)
     return _lib.load().vs_max_render_theta(m, k)
 
 
@@ -78,7 +115,7 @@ class Camera:
         return cls(focal_to_fov(fx, w, model), focal_to_fov(fy, h, model), cuv, tuple(position), tuple(rotation), model)
 
     def pose(self) -> _lib.VsPose:
-        m, k = _model_args(self.model)
+        m, k, d = _model_args(self.model)
         p = _lib.VsPose()
         p.fov_x, p.fov_y = float(self.fov_x), float(self.fov_y)
         p.center_uv[:] = [float(v) for v in self.center_uv]
@@ -86,6 +123,7 @@ class Camera:
         p.rotation[:] = [float(v) for v in self.rotation]
         p.model = m
         p.kb4[:] = list(k)
+        p.dist[:] = list(d)
         return p
 
     def uniforms(self, img_size) -> _lib.VsCamera:

@@ -220,8 +220,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     if (mode != VS_MODE_DEFAULT && mode != VS_MODE_MIP)
         return fail(VS_ERR_UNSUPPORTED, "the Surfel render mode is not built (Default and Mip are)");
     if ((int)pass < 0 || (int)pass > (int)VS_PASS_GEOMETRY) return fail(VS_ERR_INVALID, "unknown pass");
-    if (cam->model != VS_CAMERA_PINHOLE && cam->model != VS_CAMERA_KB4)
-        return fail(VS_ERR_UNSUPPORTED, "camera model must be pinhole or Kannala-Brandt-4");
+    if (cam->model < VS_CAMERA_PINHOLE || cam->model > VS_CAMERA_TPF)
+        return fail(VS_ERR_INVALID, "unknown camera model");
     vs_status vst = check_splats(sp);
     if (vst != VS_OK) return vst;
     if (!out->out_img) return fail(VS_ERR_INVALID, "out_img is null");

@@ -468,8 +468,12 @@ static void launch_project_type(const ProjectArgs& a, dim3 grid, hipStream_t s, 
 }
 template <int DEG>
 static void launch_project_model(const ProjectArgs& a, dim3 grid, hipStream_t s, bool geom) {
-    if (a.cam.model == VS_CAMERA_KB4) launch_project_type<DEG, VS_CAMERA_KB4>(a, grid, s, geom);
-    else launch_project_type<DEG, VS_CAMERA_PINHOLE>(a, grid, s, geom);
+    switch (a.cam.model) {
+    case VS_CAMERA_KB4: launch_project_type<DEG, VS_CAMERA_KB4>(a, grid, s, geom); break;
+    case VS_CAMERA_RT8: launch_project_type<DEG, VS_CAMERA_RT8>(a, grid, s, geom); break;
+    case VS_CAMERA_TPF: launch_project_type<DEG, VS_CAMERA_TPF>(a, grid, s, geom); break;
+    default: launch_project_type<DEG, VS_CAMERA_PINHOLE>(a, grid, s, geom); break;
+    }
 }
 
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s) {

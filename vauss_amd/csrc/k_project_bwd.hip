@@ -74,8 +74,12 @@ __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs 
 
 template <int DEG, typename SHT>
 static void launch_pbwd_type(const ProjectBwdArgs& a, dim3 grid, hipStream_t s) {
-    if (a.cam.model == VS_CAMERA_KB4) project_bwd_kernel<DEG, VS_CAMERA_KB4, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a);
-    else project_bwd_kernel<DEG, VS_CAMERA_PINHOLE, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a);
+    switch (a.cam.model) {
+    case VS_CAMERA_KB4: project_bwd_kernel<DEG, VS_CAMERA_KB4, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a); break;
+    case VS_CAMERA_RT8: project_bwd_kernel<DEG, VS_CAMERA_RT8, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a); break;
+    case VS_CAMERA_TPF: project_bwd_kernel<DEG, VS_CAMERA_TPF, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a); break;
+    default: project_bwd_kernel<DEG, VS_CAMERA_PINHOLE, SHT><<<grid, PBWD_BLOCK, 0, s>>>(a); break;
+    }
 }
 template <int DEG>
 static void launch_pbwd_model(const ProjectBwdArgs& a, dim3 grid, hipStream_t s) {

@@ -130,8 +130,12 @@ __global__ void geo_zero_rows_kernel(uint32_t* __restrict__ words, const uint32_
 
 template <int DEG, typename SHT>
 static void launch_pupd_type(const ProjectUpdateArgs& a, dim3 grid, hipStream_t s) {
-    if (a.cam.model == VS_CAMERA_KB4) project_update_kernel<DEG, VS_CAMERA_KB4, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a);
-    else project_update_kernel<DEG, VS_CAMERA_PINHOLE, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a);
+    switch (a.cam.model) {
+    case VS_CAMERA_KB4: project_update_kernel<DEG, VS_CAMERA_KB4, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a); break;
+    case VS_CAMERA_RT8: project_update_kernel<DEG, VS_CAMERA_RT8, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a); break;
+    case VS_CAMERA_TPF: project_update_kernel<DEG, VS_CAMERA_TPF, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a); break;
+    default: project_update_kernel<DEG, VS_CAMERA_PINHOLE, SHT><<<grid, PUPD_BLOCK, 0, s>>>(a); break;
+    }
 }
 template <int DEG>
 static void launch_pupd_model(const ProjectUpdateArgs& a, dim3 grid, hipStream_t s) {

@@ -86,8 +86,7 @@ VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3
     const S3 cov_c = congruence(covar, vrot);
     const M23 J = project_jacobian<MODEL>(mc, u);
     F3 v_mean_c;
-    if constexpr (MODEL == VS_CAMERA_KB4) v_mean_c = projection_vjp_kb4(J, mc, cov_c, u, v_cov2d, F2{rg[0], rg[1]});
-    else v_mean_c = projection_vjp_pinhole(J, mc, cov_c, u, v_cov2d, F2{rg[0], rg[1]});
+    v_mean_c = projection_vjp<MODEL>(J, mc, cov_c, u, v_cov2d, F2{rg[0], rg[1]});
     const S3 vcc = tcongruence(J, v_cov2d);
     SplatVjp r;
     r.v_mean = tmul(vrot, v_mean_c) + v_mean_sh;
