@@ -25,6 +25,14 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
 FP32_VALU_PEAK_TFLOPS = 157.3    # MI355X vector fp32 (packed) peak
 VALU_ISSUE_PEAK_G = 256 * 4 * 2.4 / 4   # G wave64 VALU instructions/s without packed fp32 (614.4)
+SIMD_CYCLES_G = 256 * 4 * 2.4           # G SIMD cycles/s across the chip
+# Cycles per wave64 instruction by counter class, relative to FP32 add at 4,
+# as vauss_amd/valu_rates measures them on gfx950: FP32 add/mul/fma 4,
+# int32 2, conversions 4, transcendentals 8.  The remainder (moves 2;
+# max/min, compares, selects 4) is bracketed by its two rates.
+VALU_CLASS_CYCLES = {"SQ_INSTS_VALU_ADD_F32": 4, "SQ_INSTS_VALU_MUL_F32": 4, "SQ_INSTS_VALU_FMA_F32": 4,
+                     "SQ_INSTS_VALU_TRANS_F32": 8, "SQ_INSTS_VALU_INT32": 2, "SQ_INSTS_VALU_CVT": 4,
+                     "SQ_INSTS_VALU_INT64": 4}
 
 METRIC = "fwd+bwd raster ms/view, 1M Gaussians SH3 1080p; achieved HBM GB/s vs peak"
 
@@ -243,19 +251,23 @@ def main() -> int:
     dom_bytes = algorithmic_bytes(dom, n, int(V), int(I), T, P, k)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic, traffic_note = measured_traffic(args.workload, dom.replace("_ms", ""))
-    valu = measured_valu_insts(args.workload, dom.replace("_ms", ""))
+    valu, valu_classes = measured_valu_insts(args.workload, dom.replace("_ms", "")) or (None, None)
     roofline = {"bound": "hbm", "kernel": dom.replace("_ms", ""), "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "traffic_source": traffic_note, "alg_bytes_per_launch": dom_bytes,
                 "ms_per_launch": round(dom_ms, 4)}
     # The raster kernels are bound by VALU instruction issue, not HBM: their
     # wave instructions per launch (counter summary) over the live launch
-    # time, against MI355X's issue ceiling without packed FP32 (256 CUs x 4
-    # SIMDs x 2.4 GHz / 4 cycles per wave64 instruction).
+    # time, against MI355X's FP32 issue rate (256 CUs x 4 SIMDs x 2.4 GHz / 4
+    # cycles per wave64 instruction).  Integer, move and conversion
+    # instructions issue in 2 cycles, so "frac" is not a bound by itself:
+    # "utilization" weighs the counter classes by their measured cycles
+    # (the unclassified remainder between 2 and 4) against the SIMD cycles.
     if valu:
         rate = valu / (dom_ms * 1e-3) / 1e9
         roofline["valu_issue"] = {"achieved": round(rate, 1), "peak": VALU_ISSUE_PEAK_G, "unit": "G wave-instr/s",
                                   "frac": round(rate / VALU_ISSUE_PEAK_G, 4), "insts_per_launch": int(valu),
+                                  "utilization": issue_utilization(valu, valu_classes, dom_ms),
                                   "source": traffic_note}
 
     if args.copy_calib:
@@ -322,7 +334,9 @@ STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "r
 # what the markdown summary lists (the traffic file keeps every kernel)
 SUMMARY_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VALU_TRANS_F32",
                     "SQ_LDS_BANK_CONFLICT", "SQ_THREAD_CYCLES_VALU", "SQ_ACTIVE_INST_VALU", "TCC_ATOMIC_sum",
-                    "TCC_EA0_ATOMIC_sum", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE", "WRITE_SIZE")
+                    "TCC_EA0_ATOMIC_sum", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE", "WRITE_SIZE",
+                    "SQ_INSTS_VALU_ADD_F32", "SQ_INSTS_VALU_MUL_F32", "SQ_INSTS_VALU_FMA_F32", "SQ_INSTS_VALU_INT32",
+                    "SQ_INSTS_VALU_CVT", "SQ_INSTS_VALU_INT64")
 SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "copyBuffer")
 
 
@@ -361,7 +375,19 @@ def measured_valu_insts(workload: str, kernel: str):
         data = json.load(fh)
     if data.get("source_digest") != source_digest():
         return None
-    return data["kernels"].get(kernel, {}).get("valu_insts")
+    k = data["kernels"].get(kernel, {})
+    return k.get("valu_insts"), k.get("valu_classes")
+
+
+def issue_utilization(insts: float, classes: dict, ms: float):
+    """Fraction of the SIMDs' cycles the kernel's VALU instructions occupy,
+    [low, high] with the unclassified remainder at 2 and 4 cycles."""
+    if not classes or not insts:
+        return None
+    known = sum(classes.get(c, 0.0) * cyc for c, cyc in VALU_CLASS_CYCLES.items())
+    rest = max(0.0, insts - sum(classes.get(c, 0.0) for c in VALU_CLASS_CYCLES))
+    avail = SIMD_CYCLES_G * 1e9 * ms * 1e-3
+    return [round((known + 2 * rest) / avail, 3), round((known + 4 * rest) / avail, 3)]
 
 
 def _short_kernel(name: str) -> str:
@@ -390,7 +416,9 @@ def summarize(args) -> int:
                 with open(os.path.join(d, f)) as fh:
                     for r in csv.DictReader(fh):
                         k = _short_kernel(r["Kernel_Name"])
-                        key = (r["Dispatch_Id"], r["Grid_Size"])
+                        # rows of one dispatch (one per counter instance) add up; the same
+                        # counter collected in two runs averages over both
+                        key = (d, r["Dispatch_Id"], r["Grid_Size"])
                         per.setdefault(k, {}).setdefault(r["Counter_Name"], {}).setdefault(key, 0.0)
                         per[k][r["Counter_Name"]][key] += float(r["Counter_Value"])
                         durs.setdefault(k, {})[key] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
@@ -407,9 +435,12 @@ def summarize(args) -> int:
         lines += ["| kernel | dispatches | counter | mean per dispatch | derived |", "|---|---|---|---|---|"]
         traffic = {"source_digest": source_digest(), "calibration_mib": args.copy_calib,
                    "fetch_scale": f_scale, "write_scale": w_scale, "kernels": {}}
-        nbwd = max(1, len(per.get("raster_bwd_kernel<false>", {}).get("FETCH_SIZE", {1: 0})))
+        def per_run(v):        # dispatches of one run (the same counter may come from two runs)
+            runs = {key[0] for key in v}
+            return max(sum(1 for key in v if key[0] == r) for r in runs) if v else 0
+        nbwd = max(1, per_run(per.get("raster_bwd_kernel<false>", {}).get("FETCH_SIZE", {})))
         for k, cs in sorted(per.items()):
-            n = max(len(v) for v in cs.values())
+            n = max(per_run(v) for v in cs.values())
             mean = {c: sum(v.values()) / len(v) for c, v in cs.items()}
             dur_ns = dur.get(k)
             for c in sorted(mean):
@@ -428,12 +459,15 @@ def summarize(args) -> int:
                 if stage in ("copy", "torch", "fill"):
                     continue
                 e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "valu_insts": 0.0,
-                                                          "kernels": []})
+                                                          "valu_classes": {}, "kernels": []})
                 # per step: a kernel launched several times a step (sort passes) adds up
                 reps = n / nbwd
                 e["fetch_bytes"] += mean["FETCH_SIZE"] * 1024.0 * f_scale * reps
                 e["write_bytes"] += mean["WRITE_SIZE"] * 1024.0 * w_scale * reps
                 e["valu_insts"] += mean.get("SQ_INSTS_VALU", 0.0) * reps
+                for c in VALU_CLASS_CYCLES:
+                    if c in mean:
+                        e["valu_classes"][c] = e["valu_classes"].get(c, 0.0) + mean[c] * reps
                 e["kernels"].append(k)
     text = "\n".join(lines) + "\n"
     if args.command:

@@ -61,7 +61,24 @@ def build(verbose: bool = True) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}", file=sys.stderr)
+    build_valu_rates(verbose)
     return LIB
+
+
+VALU_RATES = PKG / "valu_rates"
+
+
+def build_valu_rates(verbose: bool = True) -> Path:
+    """The VALU issue-rate calibration (csrc/valu_rates.hip), a standalone
+    executable: `vauss_amd/valu_rates` prints the rate of each instruction
+    class, the ceiling bench.py's instruction-issue roofline is built on."""
+    cmd = [HIPCC, "-O3", "-std=c++17", *DEVICE, "-o", str(VALU_RATES), str(CSRC / "valu_rates.hip")]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compiling valu_rates failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    if verbose:
+        print(f"built {VALU_RATES}", file=sys.stderr)
+    return VALU_RATES
 
 
 def build_oracle(verbose: bool = True) -> None:
