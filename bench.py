@@ -156,6 +156,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--exact-counts", action="store_true",
+                    help="time training renders that wait for their own counts (the default times lagged counts, "
+                         "as the reference's training renders run)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (counter calibration for HBM traffic)")
     ap.add_argument("--summarize-stats", metavar="CSV", help="summarise a rocprofv3 kernel_stats.csv as markdown")
@@ -207,14 +210,17 @@ def main() -> int:
         out.state.free()
         return g, aux
 
+    ctx = va.Context.get(dev)
+    lagged = not args.exact_counts
+    ctx.set_lagged_counts(lagged)
     for i in range(args.warmup):
         step(i % len(cams))
     torch.cuda.synchronize()
 
     # Stage breakdown: one pass over the views with every stage bracketed by
     # HIP events (each bracket adds a few microseconds of stream time, so this
-    # pass is not the timed one).
-    ctx = va.Context.get(dev)
+    # pass is not the timed one), on exact counts so each view's counts are its own.
+    ctx.set_lagged_counts(False)
     ctx.enable_timing(True)
     ctx.stage_times()                # drop anything recorded before
     counts = []
@@ -227,19 +233,33 @@ def main() -> int:
     dom = max(("raster_bwd_ms", "raster_fwd_ms", "project_ms", "project_bwd_ms", "sort_ms"), key=lambda x: per_launch[x])
 
     # Timed region: K steps; only the dominant kernel's stage is bracketed by
-    # events (its live launch time is the roofline's denominator).
-    ctx.enable_timing(True, stages=[dom.replace("_ms", "")])
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        _, aux = step(i % len(cams))
-        counts.append(aux)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    dom_ms = ctx.stage_times()[dom] / args.steps
-    ctx.enable_timing(False)
-    ms_per_step = (t1 - t0) * 1000.0 / args.steps
-    print(f"[bench] {args.steps} steps, {ms_per_step:.3f} ms/view", file=sys.stderr, flush=True)
+    # events (its live launch time is the roofline's denominator).  With
+    # lagged counts a render that overflowed its capacity would drop work, so
+    # the overflow count is read before and after and must not move.
+    def timed_steps(lagged_counts: bool):
+        ctx.set_lagged_counts(lagged_counts)
+        for i in range(len(cams)):          # settle the hints on this mode
+            step(i % len(cams))
+        before = ctx.settle_lagged_counts()[1]
+        ctx.enable_timing(True, stages=[dom.replace("_ms", "")])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i % len(cams))
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        launch_ms = ctx.stage_times()[dom] / args.steps
+        ctx.enable_timing(False)
+        overflows = ctx.settle_lagged_counts()[1] - before
+        ctx.set_lagged_counts(False)
+        if overflows:
+            raise SystemExit(f"bench: {overflows} lagged renders overflowed their capacity in the timed region")
+        return (t1 - t0) * 1000.0 / args.steps, launch_ms
+
+    ms_per_step, dom_ms = timed_steps(lagged)
+    other_ms = timed_steps(not lagged)[0]
+    print(f"[bench] {args.steps} steps, {ms_per_step:.3f} ms/view ({'lagged' if lagged else 'exact'} counts; "
+          f"{other_ms:.3f} with {'exact' if lagged else 'lagged'} counts)", file=sys.stderr, flush=True)
 
     V = float(np.mean([c[0] for c in counts]))
     I = float(np.mean([c[1] for c in counts]))
@@ -300,7 +320,9 @@ def main() -> int:
         "data": "synthetic (seeded SplitMix64 cloud, random-init parameters)",
         "config": {"workload": f"{args.workload}: {WORKLOAD_DESC[args.workload]}", "num_splats": n,
                    "sh_degree": sc.sh_degree, "img": [w, h], "tile": 16, "views": len(cams),
-                   "mean_visible": round(V), "mean_intersections": round(I)},
+                   "mean_visible": round(V), "mean_intersections": round(I),
+                   "counts": "lagged" if lagged else "exact"},
+        ("ms_per_view_exact_counts" if lagged else "ms_per_view_lagged_counts"): round(other_ms, 4),
         "gaussians_per_s": round(n / (ms_per_step * 1e-3)),
         "stage_ms": {k2: v2["ms"] for k2, v2 in kernels.items()},
         "kernels": kernels,

@@ -164,6 +164,26 @@ enum {
 vs_status vs_ctx_enable_timing(vs_ctx* ctx, uint32_t stages);
 vs_status vs_ctx_stage_times(vs_ctx* ctx, vs_stage_times* out);
 
+/* Lagged counts for training renders (render.rs:38-304, 741-768, 887-915).
+ * With `enable` set, a VS_PASS_BACKWARD forward at an image size this context
+ * has already rendered sizes its intersection arena from a capacity hint kept
+ * per (width, height) and runs every stage after projection on device-resident
+ * counts: it never waits for the GPU.  Its vs_render_out counts are then the
+ * previous lagged render's at that size (0, 0 for the first), and its own are
+ * read by the next one.  A render needing more intersections than the hint
+ * keeps the first `capacity` of the depth-ordered list (the farthest splats'
+ * tiles are dropped), logs to stderr and grows the hint.  The hint follows
+ * the reference's policy: 200-render windows sized to the p99 intersections
+ * per splat with 25% headroom, never below the window's largest render + 5%,
+ * 1.5x growth before the first full window.  Other passes, and every render
+ * with `enable` clear (the default), stay exact and refine the hint.  The
+ * reference enables this for every training render; it is opt-in here. */
+vs_status vs_ctx_set_lagged_counts(vs_ctx* ctx, int enable);
+/* Wait for every pending lagged render's counts, fold them into the hints
+ * and return the number of lagged renders settled so far and how many of
+ * them overflowed their capacity (either pointer may be NULL). */
+vs_status vs_ctx_settle_lagged_counts(vs_ctx* ctx, uint64_t* renders, uint64_t* overflows);
+
 /* ---- camera host math --------------------------------------------------------- */
 
 /* camera.rs:99-116 fov_to_focal / :118-134 focal_to_fov (host, f64).

@@ -99,6 +99,8 @@ SIGNATURES = {
     "vs_version": (C.c_char_p, []),
     "vs_ctx_enable_timing": (C.c_int, [C.c_void_p, C.c_uint32]),
     "vs_ctx_stage_times": (C.c_int, [C.c_void_p, C.POINTER(VsStageTimes)]),
+    "vs_ctx_set_lagged_counts": (C.c_int, [C.c_void_p, C.c_int]),
+    "vs_ctx_settle_lagged_counts": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "vs_fov_to_focal": (C.c_double, [C.c_double, C.c_uint32, C.c_int32, C.POINTER(C.c_float)]),
     "vs_focal_to_fov": (C.c_double, [C.c_double, C.c_uint32, C.c_int32, C.POINTER(C.c_float)]),
     "vs_max_render_theta": (C.c_double, [C.c_int32, C.POINTER(C.c_float)]),

@@ -4,10 +4,12 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <new>
 #include <string>
 #include <vector>
 #include "vs_internal.h"
+#include "vs_capacity.h"
 
 using namespace vs;
 
@@ -53,6 +55,15 @@ struct vs_ctx {
     struct Rec { int stage; hipEvent_t b, e; };
     std::vector<Rec> recs;
     std::vector<hipEvent_t> pool;
+    // Lagged training renders (render.rs:57-304): capacity hints per
+    // (image size, count slot) and the not-yet-read counts of the last lagged
+    // render at each key, copied to pinned memory behind an event.
+    bool lagged = false;
+    CapacityTable caps;
+    struct Pending { uint32_t* host = nullptr; hipEvent_t ev = nullptr; size_t capacity = 0; uint32_t splats = 0;
+                     size_t limit = 0; bool live = false; };
+    std::map<CapacityKey, Pending> pending;
+    uint64_t lagged_renders = 0, lagged_overflows = 0;
     hipEvent_t take() {
         if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
         hipEvent_t e = nullptr;
@@ -163,6 +174,10 @@ extern "C" void vs_ctx_destroy(vs_ctx* c) {
     hipStreamSynchronize(c->stream);
     for (auto& r : c->recs) { hipEventDestroy(r.b); hipEventDestroy(r.e); }
     for (auto e : c->pool) hipEventDestroy(e);
+    for (auto& kv : c->pending) {
+        if (kv.second.ev) hipEventDestroy(kv.second.ev);
+        if (kv.second.host) hipHostFree(kv.second.host);
+    }
     hipHostFree(c->host_counters);
     hipFree(c->dev_flags);
     delete c;
@@ -211,6 +226,77 @@ extern "C" void vs_fwd_state_free(vs_fwd_state* st) {
     delete st;
 }
 
+namespace {
+
+// settle_pending (render.rs:254-282): wait for the last lagged render at `k`
+// (long finished by now), fold its count into the hint and report it.
+vs_status settle(vs_ctx* ctx, const CapacityKey& k, bool& have, uint32_t& vis, uint32_t& isects) {
+    have = false;
+    auto it = ctx->pending.find(k);
+    if (it == ctx->pending.end() || !it->second.live) return VS_OK;
+    vs_ctx::Pending& p = it->second;
+    VS_HIP(hipEventSynchronize(p.ev), "hipEventSynchronize(lagged counts)");
+    p.live = false;
+    const uint32_t* hc = p.host;
+    if (hc[CNT_COUNT + FLAG_SORT_STALL] != 0u) {
+        VS_HIP(launch_fill_u32(ctx->dev_flags, 0u, CTX_FLAGS, ctx->stream), "flag reset");
+        return fail(VS_ERR_HIP, "an earlier radix sort on this context gave up waiting in its look-back; its output was wrong");
+    }
+    uint64_t I64 = 0;
+    std::memcpy(&I64, hc + CNT_ISECT64, 8);
+    ctx->lagged_renders += 1;
+    if (I64 > p.capacity) {
+        ctx->lagged_overflows += 1;
+        std::fprintf(stderr, "vsplat: intersection capacity overflow: required=%llu, capacity=%zu, dropped=%.3f%% "
+                     "(farthest splats), overflows=%llu/%llu renders\n", (unsigned long long)I64, p.capacity,
+                     100.0 * (1.0 - (double)p.capacity / (double)I64), (unsigned long long)ctx->lagged_overflows,
+                     (unsigned long long)ctx->lagged_renders);
+    }
+    ctx->caps.record(k, (size_t)I64, p.splats, p.limit);
+    have = true;
+    vis = hc[CNT_VISIBLE];
+    isects = (uint32_t)std::min<uint64_t>(I64, 0xFFFFFFFFull);
+    return VS_OK;
+}
+
+// intersection_ceiling (render.rs:197-216): the most intersections one render
+// may allocate, consulting free device memory only for arenas big enough to
+// matter (24 bytes per intersection at the arena's peak).
+size_t isect_ceiling(size_t wanted, size_t limit) {
+    size_t cap = limit;
+    size_t free_b = 0, total_b = 0;
+    if (wanted * 24 > (size_t)1 << 30 && hipMemGetInfo(&free_b, &total_b) == hipSuccess && wanted * 24 > free_b / 4)
+        cap = std::min(cap, free_b / 24);
+    return std::min(std::max<size_t>(cap, (size_t)1 << 16), limit);
+}
+
+} // namespace
+
+extern "C" vs_status vs_ctx_set_lagged_counts(vs_ctx* c, int enable) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    c->lagged = enable != 0;
+    return VS_OK;
+}
+
+extern "C" vs_status vs_ctx_settle_lagged_counts(vs_ctx* c, uint64_t* renders, uint64_t* overflows) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    VS_HIP(hipSetDevice(c->device), "hipSetDevice");
+    std::vector<CapacityKey> keys;
+    for (auto& kv : c->pending) keys.push_back(kv.first);
+    for (auto& k : keys) {
+        bool have = false;
+        uint32_t v = 0, i = 0;
+        vs_status st = settle(c, k, have, v, i);
+        if (st != VS_OK) return st;
+    }
+    // One line per settle so a clamped render shows in any log.
+    std::fprintf(stderr, "vsplat: lagged render counts: %llu overflows / %llu renders\n",
+                 (unsigned long long)c->lagged_overflows, (unsigned long long)c->lagged_renders);
+    if (renders) *renders = c->lagged_renders;
+    if (overflows) *overflows = c->lagged_overflows;
+    return VS_OK;
+}
+
 extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* sp, uint32_t W, uint32_t H,
                                        const float background[3], vs_pass pass, vs_render_mode mode, vs_fwd_out* out,
                                        vs_fwd_state** state_out) {
@@ -253,6 +339,23 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     const bool smooth = pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF;
     const uint32_t nblocks = (N + 255) / 256;
 
+    // ---- lagged training renders (render.rs:741-768) ------------------------------
+    // A training render at a size with a capacity hint sizes its intersection
+    // arena from it and does not wait for its own counts; it reports the
+    // previous training render's at this size.  Other renders stay exact.
+    const CapacityKey key{W, H, 0u};
+    const size_t limit = (size_t)std::max<uint64_t>(std::min<uint64_t>((uint64_t)N * T, 0xFFFFFFFFull), 1);
+    const bool training = pass == VS_PASS_BACKWARD;
+    bool have_lag = false;
+    uint32_t lag_vis = 0, lag_isects = 0;
+    if (ctx->lagged && training) {
+        vs_status se = settle(ctx, key, have_lag, lag_vis, lag_isects);
+        if (se != VS_OK) return se;
+    }
+    size_t hint = 0;
+    const bool lagged = ctx->lagged && training && N > 0 && ctx->caps.hint(key, N, limit, hint);
+    const uint32_t isect_cap = lagged ? (uint32_t)std::min(hint, isect_ceiling(hint, limit)) : 0xFFFFFFFFu;
+
     // ---- per-splat arena -----------------------------------------------------
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
@@ -294,29 +397,43 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
         pa.proj_aux = st->proj_aux; pa.compact = st->compact; pa.block_stats = st->block_stats;
         VS_HIP(launch_project(pa, s), "project kernel");
-        VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, s), "projection counts");
+        VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, isect_cap, s), "projection counts");
         if (bwd_info) VS_HIP(launch_fill_f32(st->visible, 0.0f, N, s), "zero visible");
         VS_HIP(launch_fill_u32(st->ranges, 0u, (uint64_t)T * 2, s), "zero ranges");
     }
-    VS_HIP(hipMemcpyAsync(ctx->host_counters, st->counters, CNT_COUNT * 4, hipMemcpyDeviceToHost, s), "counter readback");
-    VS_HIP(hipMemcpyAsync(ctx->host_counters + CNT_COUNT, ctx->dev_flags, CTX_FLAGS * 4, hipMemcpyDeviceToHost, s),
-           "flag readback");
-    VS_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
-    const uint32_t* hc = ctx->host_counters;
-    if (hc[CNT_COUNT + FLAG_SORT_STALL] != 0u) {
-        VS_HIP(launch_fill_u32(ctx->dev_flags, 0u, CTX_FLAGS, s), "flag reset");
-        return fail(VS_ERR_HIP, "an earlier radix sort on this context gave up waiting in its look-back; its output was wrong");
-    }
-    st->V = hc[CNT_VISIBLE];
-    st->M = hc[CNT_EMITTERS];
-    uint64_t I64 = 0;
-    std::memcpy(&I64, hc + CNT_ISECT64, 8);
-    if (I64 > 0xFFFFFFFFull) return fail(VS_ERR_CAPACITY, "intersection count exceeds u32");
-    st->I = (uint32_t)I64;
-    const uint32_t dmin = (st->V > 0) ? hc[CNT_DEPTH_MIN] : 0u;
-    const uint32_t dmax = (st->V > 0) ? hc[CNT_DEPTH_MAX] : 0u;
-    const uint32_t depth_bits = bit_length((uint64_t)(dmax - dmin));
     const uint32_t tile_bits = bit_length(T);     // the sentinel tile id T must fit too
+    uint32_t depth_bits = 32;
+    // Device-resident counts for the lagged path (null: the exact host counts).
+    const uint32_t* m_dev = nullptr;
+    const uint32_t* i_dev = nullptr;
+    if (!lagged) {
+        VS_HIP(hipMemcpyAsync(ctx->host_counters, st->counters, CNT_COUNT * 4, hipMemcpyDeviceToHost, s), "counter readback");
+        VS_HIP(hipMemcpyAsync(ctx->host_counters + CNT_COUNT, ctx->dev_flags, CTX_FLAGS * 4, hipMemcpyDeviceToHost, s),
+               "flag readback");
+        VS_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+        const uint32_t* hc = ctx->host_counters;
+        if (hc[CNT_COUNT + FLAG_SORT_STALL] != 0u) {
+            VS_HIP(launch_fill_u32(ctx->dev_flags, 0u, CTX_FLAGS, s), "flag reset");
+            return fail(VS_ERR_HIP, "an earlier radix sort on this context gave up waiting in its look-back; its output was wrong");
+        }
+        st->V = hc[CNT_VISIBLE];
+        st->M = hc[CNT_EMITTERS];
+        uint64_t I64 = 0;
+        std::memcpy(&I64, hc + CNT_ISECT64, 8);
+        if (I64 > 0xFFFFFFFFull) return fail(VS_ERR_CAPACITY, "intersection count exceeds u32");
+        st->I = (uint32_t)I64;
+        const uint32_t dmin = (st->V > 0) ? hc[CNT_DEPTH_MIN] : 0u;
+        const uint32_t dmax = (st->V > 0) ? hc[CNT_DEPTH_MAX] : 0u;
+        depth_bits = bit_length((uint64_t)(dmax - dmin));
+        ctx->caps.record(key, (size_t)I64, N, limit);   // every exact render refines the hint
+    } else {
+        // Capacities: every splat may emit; the arena holds isect_cap pairs.
+        st->V = N;
+        st->M = N;
+        st->I = isect_cap;
+        m_dev = st->counters + CNT_EMITTERS;
+        i_dev = st->counters + CNT_BOUNDED;
+    }
     const uint32_t I = st->I, M = st->M;
 
     // ---- binning: compaction, depth sort, slot scan, emission, tile sort ------------
@@ -328,7 +445,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const size_t o_dk = itake((size_t)M * 4), o_dv = itake((size_t)M * 4);
         const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)N * 4);
         const size_t o_scan = itake(scan_tmp_words(M) * 4);
-        const size_t o_tmp = itake(sort_tmp_bytes(I, false));     // M <= I: serves both sorts
+        const size_t o_tmp = itake(sort_tmp_bytes(std::max(I, M), false));   // serves both sorts
         VS_HIP(hipMallocAsync(&st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
         char* ib = static_cast<char*>(st->isect_arena);
         uint32_t* tiles_u = reinterpret_cast<uint32_t*>(ib + o_tu);
@@ -352,28 +469,28 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         }
         {
             StageTimer tm(ctx, ST_SORT);
-            VS_HIP(radix_sort_pairs(dkeys, dvals, dkeys_sorted, order, M, nullptr, false, 0, depth_bits, ib + o_tmp,
+            VS_HIP(radix_sort_pairs(dkeys, dvals, dkeys_sorted, order, M, m_dev, false, 0, depth_bits, ib + o_tmp,
                                     err, s),
                    "depth sort");
         }
         {
             StageTimer tm(ctx, ST_EMIT);
-            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order), "slot scan");
+            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order, m_dev), "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
             ea.counts = st->counts; ea.slot_base = slot_base;
-            ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u;
+            ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u; ea.capacity = I;
             VS_HIP(launch_emit(ea, s), "emit kernel");
         }
         {
             StageTimer tm(ctx, ST_SORT);
-            VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, nullptr, false, 0, tile_bits, ib + o_tmp,
+            VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, i_dev, false, 0, tile_bits, ib + o_tmp,
                                     err, s),
                    "tile sort");
         }
         {
             StageTimer tm(ctx, ST_RANGES);
-            VS_HIP(launch_tile_ranges(st->tiles, I, T, st->ranges, s), "tile ranges");
+            VS_HIP(launch_tile_ranges(st->tiles, I, T, st->ranges, s, i_dev), "tile ranges");
         }
     }
 
@@ -392,8 +509,26 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const uint32_t* src = bwd_info ? st->ranges_shrunk : st->ranges;
         VS_HIP(hipMemcpyAsync(out->tile_offsets, src, (size_t)T * 8, hipMemcpyDeviceToDevice, s), "tile offsets copy");
     }
-    out->num_visible = st->V;
-    out->num_intersections = I;
+    if (lagged) {
+        // Counts leave behind an event; the next training render at this size
+        // (or vs_ctx_settle_lagged_counts) reads them.
+        vs_ctx::Pending& p = ctx->pending[key];
+        if (!p.host) {
+            VS_HIP(hipHostMalloc(reinterpret_cast<void**>(&p.host), (CNT_COUNT + CTX_FLAGS) * sizeof(uint32_t),
+                                 hipHostMallocDefault), "hipHostMalloc(lagged counts)");
+            VS_HIP(hipEventCreateWithFlags(&p.ev, hipEventDisableTiming), "hipEventCreate(lagged counts)");
+        }
+        VS_HIP(hipMemcpyAsync(p.host, st->counters, CNT_COUNT * 4, hipMemcpyDeviceToHost, s), "lagged counter copy");
+        VS_HIP(hipMemcpyAsync(p.host + CNT_COUNT, ctx->dev_flags, CTX_FLAGS * 4, hipMemcpyDeviceToHost, s),
+               "lagged flag copy");
+        VS_HIP(hipEventRecord(p.ev, s), "hipEventRecord(lagged counts)");
+        p.capacity = isect_cap; p.splats = N; p.limit = limit; p.live = true;
+        out->num_visible = have_lag ? std::min(lag_vis, N) : 0u;
+        out->num_intersections = have_lag ? lag_isects : 0u;
+    } else {
+        out->num_visible = st->V;
+        out->num_intersections = I;
+    }
     if (bwd_info && state_out) {
         *state_out = st;
         st = nullptr;   // ownership passes to the caller

@@ -92,7 +92,8 @@ VS_DEV uint32_t wave_max(uint32_t v) {
 // which are the compaction offsets of those splats.
 constexpr int FIN_BLOCK = 1024;
 __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __restrict__ stats, uint32_t nb,
-                                                                   uint32_t* __restrict__ counters) {
+                                                                   uint32_t* __restrict__ counters,
+                                                                   uint32_t isect_capacity) {
     __shared__ uint32_t s_w[FIN_BLOCK / 64];
     __shared__ uint32_t s_vis[FIN_BLOCK / 64], s_min[FIN_BLOCK / 64], s_max[FIN_BLOCK / 64];
     __shared__ unsigned long long s_hits[FIN_BLOCK / 64];
@@ -148,6 +149,7 @@ __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __
         counters[CNT_EMITTERS] = carry;
         counters[CNT_ISECT64] = (uint32_t)th;
         counters[CNT_ISECT64 + 1] = (uint32_t)(th >> 32);
+        counters[CNT_BOUNDED] = th < (unsigned long long)isect_capacity ? (uint32_t)th : isect_capacity;
     }
 }
 
@@ -402,12 +404,14 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
         for (uint32_t i = 0; i < nb; ++i) {
             const uint32_t tx = i % bw + bb.x0, ty = i / bw + bb.y0;
             if (k < cnt && will_contribute(tx, ty, px, py, conic, power)) {
-                a.tiles[base + k] = tx + ty * a.tile_bw;
-                a.vals[base + k] = g;
+                if (base + k < a.capacity) {
+                    a.tiles[base + k] = tx + ty * a.tile_bw;
+                    a.vals[base + k] = g;
+                }
                 ++k;
             }
         }
-        for (; k < cnt; ++k) { a.tiles[base + k] = sentinel; a.vals[base + k] = g; }
+        for (; k < cnt && base + k < a.capacity; ++k) { a.tiles[base + k] = sentinel; a.vals[base + k] = g; }
     }
     uint64_t pending = __ballot(cnt > 0 && nb > SMALL_BBOX);
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -425,13 +429,13 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
             const bool hit = t < ln && will_contribute(tx, ty, lx, ly, lc, lp);
             const uint64_t m = __ballot(hit);
             const uint32_t slot = emitted + (uint32_t)__popcll(m & lt_mask);
-            if (hit && slot < lcnt) {
+            if (hit && slot < lcnt && lbase + slot < a.capacity) {
                 a.tiles[lbase + slot] = tx + ty * a.tile_bw;
                 a.vals[lbase + slot] = lg;
             }
             emitted += (uint32_t)__popcll(m);
         }
-        for (uint32_t p = (emitted < lcnt ? emitted : lcnt) + lane; p < lcnt; p += 64) {
+        for (uint32_t p = (emitted < lcnt ? emitted : lcnt) + lane; p < lcnt && lbase + p < a.capacity; p += 64) {
             a.tiles[lbase + p] = sentinel;
             a.vals[lbase + p] = lg;
         }
@@ -451,8 +455,9 @@ static uint32_t fill_grid(uint64_t n) {
     return (uint32_t)(b < 8192 ? (b ? b : 1) : 8192);
 }
 
-hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, hipStream_t s) {
-    finalize_counts_kernel<<<1, FIN_BLOCK, 0, s>>>(block_stats, nblocks, counters);
+hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, uint32_t isect_capacity,
+                                  hipStream_t s) {
+    finalize_counts_kernel<<<1, FIN_BLOCK, 0, s>>>(block_stats, nblocks, counters, isect_capacity);
     return hipGetLastError();
 }
 

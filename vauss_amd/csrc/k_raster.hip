@@ -32,8 +32,9 @@ namespace vs {
 constexpr int BWD_BATCH = 64;
 
 // get_tile_offset.rs:11-59: [start, end) of each tile in the sorted ids.
-__global__ void tile_ranges_kernel(const uint32_t* __restrict__ tiles, uint32_t n, uint32_t num_tiles,
-                                   uint32_t* __restrict__ ranges) {
+__global__ void tile_ranges_kernel(const uint32_t* __restrict__ tiles, uint32_t n_cap, uint32_t num_tiles,
+                                   uint32_t* __restrict__ ranges, const uint32_t* __restrict__ n_dev) {
+    const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const uint32_t tile = tiles[i];
@@ -483,9 +484,10 @@ __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, 
     }
 }
 
-hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s) {
+hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
+                              const uint32_t* n_dev) {
     if (n == 0) return hipSuccess;
-    tile_ranges_kernel<<<(n + 255) / 256, 256, 0, s>>>(tiles, n, num_tiles, ranges);
+    tile_ranges_kernel<<<(n + 255) / 256, 256, 0, s>>>(tiles, n, num_tiles, ranges, n_dev);
     return hipGetLastError();
 }
 

@@ -50,9 +50,16 @@ __device__ __forceinline__ uint32_t scan_load(const uint32_t* __restrict__ in, c
     return perm ? in[perm[idx]] : in[idx];
 }
 
-__global__ void __launch_bounds__(SCAN_BLOCK) scan_reduce_kernel(const uint32_t* __restrict__ in, uint64_t n,
+// Element count: n, or min(*n_dev, n) when a device count is given.
+__device__ __forceinline__ uint64_t scan_count(uint64_t n, const uint32_t* __restrict__ n_dev) {
+    return n_dev ? (*n_dev < n ? (uint64_t)*n_dev : n) : n;
+}
+
+__global__ void __launch_bounds__(SCAN_BLOCK) scan_reduce_kernel(const uint32_t* __restrict__ in, uint64_t n_cap,
                                                                  uint32_t* __restrict__ sums,
-                                                                 const uint32_t* __restrict__ perm) {
+                                                                 const uint32_t* __restrict__ perm,
+                                                                 const uint32_t* __restrict__ n_dev) {
+    const uint64_t n = scan_count(n_cap, n_dev);
     const uint64_t base = (uint64_t)blockIdx.x * SCAN_TILE;
     uint32_t acc = 0;
 #pragma unroll
@@ -67,8 +74,10 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_reduce_kernel(const uint32_t*
 }
 
 __global__ void __launch_bounds__(SCAN_BLOCK) scan_block_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
-                                                                uint64_t n, const uint32_t* __restrict__ offsets,
-                                                                int inclusive, const uint32_t* __restrict__ perm) {
+                                                                uint64_t n_cap, const uint32_t* __restrict__ offsets,
+                                                                int inclusive, const uint32_t* __restrict__ perm,
+                                                                const uint32_t* __restrict__ n_dev) {
+    const uint64_t n = scan_count(n_cap, n_dev);
     __shared__ uint32_t s_data[SCAN_TILE];
     __shared__ uint32_t s_w[48];
     const uint64_t base = (uint64_t)blockIdx.x * SCAN_TILE;
@@ -129,28 +138,28 @@ hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_
 }
 
 hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
-                    uint32_t* total_out, hipStream_t s, const uint32_t* perm) {
+                    uint32_t* total_out, hipStream_t s, const uint32_t* perm, const uint32_t* n_dev) {
     if (n == 0) {
         if (total_out) return scan_single_block(tmp, 0, false, total_out, s);
         return hipSuccess;
     }
     const uint64_t blocks = (n + SCAN_TILE - 1) / SCAN_TILE;
     if (blocks == 1) {
-        scan_block_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, out, n, nullptr, inclusive ? 1 : 0, perm);
+        scan_block_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, out, n, nullptr, inclusive ? 1 : 0, perm, n_dev);
         if (total_out) {
-            scan_reduce_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm);
+            scan_reduce_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm, n_dev);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
             return scan_single_block(tmp, 1, true, total_out, s);
         }
         return hipGetLastError();
     }
-    scan_reduce_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm);
+    scan_reduce_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm, n_dev);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     e = scan_single_block(tmp, (uint32_t)blocks, false, total_out, s);
     if (e != hipSuccess) return e;
-    scan_block_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, tmp, inclusive ? 1 : 0, perm);
+    scan_block_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, tmp, inclusive ? 1 : 0, perm, n_dev);
     return hipGetLastError();
 }
 

@@ -16,6 +16,7 @@ enum : uint32_t {
     CNT_DEPTH_MAX = 2,
     CNT_EMITTERS = 3,     // splats that hit at least one tile
     CNT_ISECT64 = 4,      // words 4..5: total intersections as a u64
+    CNT_BOUNDED = 6,      // min(total intersections, the arena's capacity): the pairs emitted
     CNT_COUNT = 8,
 };
 
@@ -75,8 +76,9 @@ struct EmitArgs {
     const uint32_t* slot_base;       // [N] first slot of each splat with hits (scan in depth order)
     const float4* proj_a;
     const float4* proj_b;
-    uint32_t* tiles;                 // [I] tile id (T = sentinel)
-    uint32_t* vals;                  // [I] global id
+    uint32_t* tiles;                 // [capacity] tile id (T = sentinel)
+    uint32_t* vals;                  // [capacity] global id
+    uint32_t capacity;               // slots at or past it are dropped (the farthest splats' pairs)
 };
 
 struct RasterArgs {
@@ -191,12 +193,15 @@ struct ShStepArgs {
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
 // Reduces the projection's block stats into `counters` and turns the block
 // emitter counts (row BS_EMIT) into exclusive offsets in place.
-hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, hipStream_t s);
+hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, uint32_t isect_capacity,
+                                  hipStream_t s);
 hipError_t launch_compact(const CompactArgs& a, hipStream_t s);
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
-hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s);
+// Ranges of the first min(*n_dev, n) sorted tile ids (all n when n_dev is null).
+hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
+                              const uint32_t* n_dev = nullptr);
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s);
@@ -220,8 +225,11 @@ hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float
 // (n distinct indices) the scan runs along it: element i of the sequence is
 // in[perm[i]] and its result goes to out[perm[i]].
 size_t scan_tmp_words(uint64_t n);
+// `n_dev` (device, may be null): only the first min(*n_dev, n) elements are
+// scanned, read and written.
 hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
-                    uint32_t* total_out, hipStream_t s, const uint32_t* perm = nullptr);
+                    uint32_t* total_out, hipStream_t s, const uint32_t* perm = nullptr,
+                    const uint32_t* n_dev = nullptr);
 hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_t* total_out, hipStream_t s);
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.

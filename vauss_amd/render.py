@@ -99,6 +99,18 @@ class Context:
         _lib.check(self.lib.vs_ctx_stage_times(self.handle, C.byref(t)))
         return {name: getattr(t, name) for name, _ in _lib.VsStageTimes._fields_}
 
+    def set_lagged_counts(self, on: bool = True) -> None:
+        """Training renders (RasterPass.BACKWARD) at an already-seen image size
+        run on a capacity hint and device counts without waiting for the GPU;
+        their aux counts are the previous such render's (render.rs:741-768)."""
+        _lib.check(self.lib.vs_ctx_set_lagged_counts(self.handle, 1 if on else 0))
+
+    def settle_lagged_counts(self) -> tuple:
+        """(lagged renders settled, of which overflowed their capacity)."""
+        r, o = C.c_uint64(), C.c_uint64()
+        _lib.check(self.lib.vs_ctx_settle_lagged_counts(self.handle, C.byref(r), C.byref(o)))
+        return int(r.value), int(o.value)
+
 
 @dataclass
 class RenderAux:
