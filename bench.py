@@ -70,7 +70,8 @@ def measure_next_rows(va, wl, cam, t, s, o, gt, dev, reps: int = 10) -> dict:
     gradients.  Algorithmic bytes: loss forward 20 B/px in + 36 B/px of
     coefficients out; backward 56 B/px in + 16 B/px out; update per splat
     40 + 4 + 4 + 40 + 40 + 4 B in and 40 + 4 + 40 + 4 + 24 + 8 B out, plus the
-    192 B SH row of each splat with gradients."""
+    192 B SH row of each splat with gradients; the camera gradient as noted
+    where it is timed."""
     import torch
 
     def timed(fn):
@@ -110,6 +111,11 @@ def measure_next_rows(va, wl, cam, t, s, o, gt, dev, reps: int = 10) -> dict:
     u_ms = timed(lambda: va.project_update(out, tw, s, ow, g.v_combined, w_t, lr, w_o, adam))
     with_grad = int((g.v_combined.abs().sum(dim=1) > 0).sum().item())
     u_bytes = n * (132 + 120) + with_grad * 192
+    # camera gradient: 32 B of raster gradients per splat, the 44 B parameters
+    # and the SH row of each splat with position, conic or colour gradients
+    p_ms = timed(lambda: va.pose_backward(out, t, s, o, g.v_combined))
+    pose_rows = int((g.v_combined[:, :8].abs().sum(dim=1) > 0).sum().item())
+    p_bytes = 32 * n + pose_rows * (44 + 12 * s.shape[1])
     # SH step on f16 coefficients: every block holding a value of a splat with
     # a gradient row reads and writes 128 x (2 B coefficient + 1 B code) and
     # its scale; per splat 4 B row + 4 B grad_sq + 4 + 4 B variance, per
@@ -131,7 +137,9 @@ def measure_next_rows(va, wl, cam, t, s, o, gt, dev, reps: int = 10) -> dict:
             "project_update": {"ms": round(u_ms, 4), "splats": n, "with_gradient": with_grad,
                                "alg_GBs": round(u_bytes / (u_ms * 1e-3) / 1e9, 1)},
             "sh_step": {"ms": round(sh_ms, 4), "blocks_stepped": touched, "coeff_dtype": "f16",
-                        "alg_GBs": round(sh_bytes / (sh_ms * 1e-3) / 1e9, 1)}}
+                        "alg_GBs": round(sh_bytes / (sh_ms * 1e-3) / 1e9, 1)},
+            "pose_backward": {"ms": round(p_ms, 4), "rows": pose_rows,
+                              "alg_GBs": round(p_bytes / (p_ms * 1e-3) / 1e9, 1)}}
 
 
 def list_length_histogram(ranges) -> dict:
@@ -350,6 +358,7 @@ STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "r
                    ("tile_ranges", "ranges"),
                    ("l1_cotangent", "loss"), ("loss_", "image_loss"), ("project_update", "project_update"),
                    ("sh_step", "sh_step"), ("sh_variance", "sh_step"), ("b8_", "sh_step"),
+                   ("pose_", "pose_backward"),
                    ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
 
 
@@ -359,7 +368,7 @@ SUMMARY_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS"
                     "TCC_EA0_ATOMIC_sum", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE", "WRITE_SIZE",
                     "SQ_INSTS_VALU_ADD_F32", "SQ_INSTS_VALU_MUL_F32", "SQ_INSTS_VALU_FMA_F32", "SQ_INSTS_VALU_INT32",
                     "SQ_INSTS_VALU_CVT", "SQ_INSTS_VALU_INT64")
-SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "copyBuffer")
+SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "pose_", "copyBuffer")
 
 
 def source_digest() -> str:

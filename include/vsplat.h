@@ -12,8 +12,8 @@
  *    in a `vs_fwd_state` until vs_fwd_state_free().
  *  - Work is enqueued on the context's HIP stream.  Calls that must learn a
  *    device-side count before sizing a buffer (the forward render after
- *    projection) synchronise that stream once; everything else is
- *    stream-ordered and returns without waiting.
+ *    projection, unless lagged counts apply) synchronise that stream once;
+ *    everything else is stream-ordered and returns without waiting.
  *  - No C++ exception crosses this boundary.  Every call returns a
  *    vs_status; vs_last_error() gives a human-readable message for the
  *    calling thread.
@@ -260,6 +260,18 @@ typedef struct vs_update_out {
     float* v_refine_weight;         /* [N] clamped to [0,1e32], 0 for culled splats */
     float* coeffs_grad_sq;          /* [N] mean square of the SH gradient row, from its DC entries */
 } vs_update_out;
+
+/* SplatBwdOps::pose_bwd (bwd/render_bwd.rs:224-288, kernel
+ * bwd/kernels/pose_backwards.rs:88-191): the camera gradient.  The camera is
+ * perturbed by x_c' = (I + A) x_c + b after the world-to-camera transform, A
+ * pivoting on the camera centre (which b moves by -M^-1 b, all the SH view
+ * direction sees); v_pose [12] (device) receives d loss / d [A row-major,
+ * b], summed over the splats with position, conic or colour gradients in
+ * `v_combined` [N,10] (vs_render_backward's raster rows for `state`).  A
+ * rigid twist [rho, w] is A = [w]x, b = rho.  `splats` must be the forward's
+ * (same floor).  Stream-ordered; the sum is deterministic. */
+vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* state, const vs_splats* splats, const float* v_combined,
+                           float* v_pose);
 
 /* ProjectUpdateOps::project_update (bwd/project_update.rs:80-220; kernel
  * bwd/kernels/project_update.rs:40-178): the projection VJP of a backward

@@ -85,6 +85,8 @@ def load() -> C.CDLL:
     lib.or_render_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F, _F]
     lib.or_project_backward.restype = C.c_int
     lib.or_project_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F]
+    lib.or_pose_backward.restype = C.c_int
+    lib.or_pose_backward.argtypes = [C.c_void_p, _F, C.c_int, C.POINTER(C.c_double), _F]
     lib.or_project_update.restype = C.c_int
     lib.or_project_update.argtypes = [C.c_void_p, _F, _F, _F, _U, _F, _U, C.POINTER(OrAdam), _F, _F, _F, C.c_int]
     lib.or_image_loss_forward.restype = C.c_int
@@ -235,6 +237,18 @@ class OracleForward:
         if rc != 0:
             raise RuntimeError(f"oracle projection backward failed ({rc})")
         return {"v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+
+    def pose_backward(self, v_combined: np.ndarray, threads: int = 0):
+        """The camera gradient [dA (row-major 3x3), db] (f64 sum) and the per-splat rows [N,12]."""
+        n = self.num_splats
+        vc = np.ascontiguousarray(v_combined, np.float32)
+        assert vc.shape == (n, 10)
+        total = (C.c_double * 12)()
+        rows = np.zeros((n, 12), np.float32)
+        rc = load().or_pose_backward(self.handle, _fp(vc), threads, total, _fp(rows))
+        if rc != 0:
+            raise RuntimeError(f"oracle pose backward failed ({rc})")
+        return np.array(total[:], np.float64), rows
 
     def __del__(self):
         try:

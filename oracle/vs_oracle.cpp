@@ -1567,6 +1567,78 @@ extern "C" int or_project_update(const or_fwd* f, const float* v_combined, float
     return 0;
 }
 
+// ---- camera gradient, bwd/kernels/pose_backwards.rs:1-191 -------------------------
+// The camera is perturbed by x_c' = (I + A) x_c + b after the world-to-camera
+// transform; A pivots on the camera centre, which b moves by -M^-1 b.
+static V3 cross3(V3 a, V3 b) {
+    return V3{a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+// pose_backwards.rs:61-74: M^-T g from the column cross products over det M.
+static V3 inverse_transpose_mul(M3 m, V3 g) {
+    const V3 k0 = cross3(m.c1, m.c2), k1 = cross3(m.c2, m.c0), k2 = cross3(m.c0, m.c1);
+    return scale(add(add(scale(k0, g.x), scale(k1, g.y)), scale(k2, g.z)), 1.0f / dot(m.c0, k0));
+}
+// pose_backwards_kernel (pose_backwards.rs:88-191) for global splat g: the row
+// [v x^T + 2 V S (row-major 3x3), db]; false (zero row) when the raster
+// gradients of position, conic and colour are all zero.
+static bool pose_row(const or_fwd* f, uint32_t g, const float rg[10], float row[12]) {
+    for (int k = 0; k < 12; ++k) row[k] = 0.0f;
+    bool any = false;
+    for (int k = 0; k < 8; ++k) any = any || rg[k] != 0.0f;
+    if (!any) return false;
+    const or_camera& u = f->cam;
+    const float* t = f->transforms + (size_t)g * 10;
+    const V3 mean = v3(t[0], t[1], t[2]);
+    const V3 sc_raw = v3(expf_c(t[7] + f->lso), expf_c(t[8] + f->lso), expf_c(t[9] + f->lso));
+    const Q4 q = qnormalize(Q4{t[3], t[4], t[5], t[6]});
+    const V3 sc = apply_scale_floor(sc_raw, sigmoid(f->raw_opac[g]), f->min_scale, g).scale;
+    // SH view direction: only the camera centre moves it.
+    const V3 u_world = sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
+    const float u_len = length(u_world);
+    const V3 dir = scale(u_world, 1.0f / u_len);
+    const V3 v_dir = sh_viewdir_vjp(f->sh + (size_t)g * f->K * 3, f->degree, dir, v3(rg[5], rg[6], rg[7]));
+    const V3 v_mean_sh = scale(sub(v_dir, scale(dir, dot(dir, v_dir))), 1.0f / u_len);
+    const V3 mean_c = world_to_cam(mean, u);
+    float filter_comp;
+    const S2 cov = compensate_cov2d(calc_cov2d(sc, q, mean_c, u), f->mip, filter_comp);
+    const S2 v_cov2d = inverse2x2_vjp(s2_inverse(cov), S2{rg[2], rg[3] * 0.5f, rg[4]});
+    const M3 vrot = view_rot(u);
+    const S3 cov_c = s3_congruence(outer_self(mul_diag(quat_to_mat3(q), sc)), vrot);
+    const M23 J = project_jacobian(mean_c, u);
+    const V3 v = projection_vjp(J, mean_c, cov_c, u, v_cov2d, V2{rg[0], rg[1]});
+    const S3 V = m23_tcongruence_s2(J, v_cov2d);
+    const V3 vb = add(v, inverse_transpose_mul(vrot, v_mean_sh));
+    const V3 vr[3] = {V3{V.c00, V.c01, V.c02}, V3{V.c01, V.c11, V.c12}, V3{V.c02, V.c12, V.c22}};
+    const V3 sr[3] = {V3{cov_c.c00, cov_c.c01, cov_c.c02}, V3{cov_c.c01, cov_c.c11, cov_c.c12},
+                      V3{cov_c.c02, cov_c.c12, cov_c.c22}};
+    const float vv[3] = {v.x, v.y, v.z}, xx[3] = {mean_c.x, mean_c.y, mean_c.z};
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j) row[3 * i + j] = vv[i] * xx[j] + 2.0f * dot(vr[i], sr[j]);
+    row[9] = vb.x; row[10] = vb.y; row[11] = vb.z;
+    return true;
+}
+
+// SplatBwdOps::pose_bwd (bwd/render_bwd.rs:224-288): the rows summed over the
+// visible splats in f64; `rows` [N,12] (optional) receives each splat's row.
+extern "C" int or_pose_backward(const or_fwd* f, const float* v_combined, int threads, double* v_pose, float* rows) {
+    if (!f || !v_combined || !v_pose || !(f->flags & OR_FLAG_BWD_INFO)) return 1;
+    const uint32_t N = f->N;
+    std::vector<float> all((size_t)N * 12, 0.0f);
+    const int nthreads = resolve_threads(threads);
+    #pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int64_t ci = 0; ci < (int64_t)f->V; ++ci) {
+        const uint32_t g = f->global_from_compact[(size_t)ci];
+        pose_row(f, g, v_combined + (size_t)g * 10, &all[(size_t)g * 12]);
+    }
+    for (int k = 0; k < 12; ++k) v_pose[k] = 0.0;
+    for (uint32_t ci = 0; ci < f->V; ++ci) {
+        const uint32_t g = f->global_from_compact[ci];
+        for (int k = 0; k < 12; ++k) v_pose[k] += (double)all[(size_t)g * 12 + k];
+    }
+    if (rows) std::memcpy(rows, all.data(), sizeof(float) * all.size());
+    return 0;
+}
+
 extern "C" int or_project_backward(const or_fwd* f, const float* v_combined, int threads, float* v_transforms,
                                    float* v_sh, float* v_raw_opac, float* v_refine) {
     if (!f || !v_combined || !(f->flags & OR_FLAG_BWD_INFO)) return 1;

@@ -94,6 +94,14 @@ int or_render_backward(const or_fwd* f, const float* v_out, int threads,
 int or_project_backward(const or_fwd* f, const float* v_combined, int threads,
                         float* v_transforms, float* v_sh, float* v_raw_opac, float* v_refine);
 
+/* The camera gradient (bwd/render_bwd.rs:224-288, bwd/kernels/pose_backwards.rs):
+ * d loss / d [A (row-major 3x3), b] of the camera-space perturbation
+ * x_c' = (I + A) x_c + b, summed in f64 over the visible splats; `rows`
+ * [N,12] (may be NULL) receives each splat's row (zero for culled splats and
+ * rows without position, conic or colour gradients). */
+int or_pose_backward(const or_fwd* f, const float* v_combined, int threads, double* v_pose /* [12] */,
+                     float* rows /* [N,12] */);
+
 /* FusedAdam (bwd/project_update.rs:232-250). */
 typedef struct or_adam {
     float beta1, beta2, inv1, inv2, epsilon, lr_opac, opac_reg;

@@ -16,7 +16,7 @@ from .camera import (  # noqa: F401
 from .render import (  # noqa: F401
     Block8Moment, Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput,
     ShStepState, SplatGrads, SplatRenderMode, adam_bias_corrections, geo_decode, geo_encode, geo_zero_rows,
-    l1_cotangent, prefix_sum, project_update, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
+    l1_cotangent, pose_backward, prefix_sum, project_update, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
     radix_argsort_with_count, render, render_backward, scan_in_place, sh_degree_from_coeffs, sh_step, unpack_rgba8,
 )
 
@@ -27,7 +27,7 @@ __all__ = [
     "Block8Moment", "ShStepState", "adam_bias_corrections", "sh_step",
     "Context", "ForwardState", "FusedAdam", "ProjectUpdateResult", "RasterPass", "RenderAux", "RenderOutput",
     "SplatGrads", "SplatRenderMode", "VsError", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",
-    "prefix_sum", "project_update", "radix_argsort", "radix_argsort_skip_low_with_count",
+    "pose_backward", "prefix_sum", "project_update", "radix_argsort", "radix_argsort_skip_low_with_count",
     "radix_argsort_u64", "radix_argsort_with_count", "render", "render_backward", "scan_in_place",
     "sh_degree_from_coeffs", "unpack_rgba8",
 ]

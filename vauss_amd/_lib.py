@@ -112,6 +112,7 @@ SIGNATURES = {
                                      C.POINTER(VsGrads)]),
     "vs_fwd_state_free": (None, [C.c_void_p]),
     "vs_fwd_state_view": (C.c_int, [C.c_void_p, C.POINTER(VsStateView)]),
+    "vs_pose_backward": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(VsSplats), C.c_void_p, C.c_void_p]),
     "vs_project_update": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(VsAdamStep),
                                     C.POINTER(VsUpdateOut)]),

@@ -590,6 +590,34 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     return VS_OK;
 }
 
+extern "C" vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_splats* sp, const float* v_combined,
+                                      float* v_pose) {
+    if (!ctx || !st || !v_combined || !v_pose) return fail(VS_ERR_INVALID, "null argument");
+    if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
+    vs_status vst = check_splats(sp);
+    if (vst != VS_OK) return vst;
+    if (sp->num_splats != st->N || sp->sh_degree != st->degree || (sp->sh_dtype == VS_SH_F16) != (st->sh_half != 0))
+        return fail(VS_ERR_INVALID, "splats differ from the forward's");
+    if ((sp->min_scale != nullptr) != (st->min_scale != nullptr))
+        return fail(VS_ERR_INVALID, "the scale floor must match the forward's (both set or both null)");
+    if ((uintptr_t)v_combined & 7u) return fail(VS_ERR_INVALID, "v_combined must be 8-byte aligned");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    hipStream_t s = ctx->stream;
+    StageTimer tm(ctx, ST_PROJECT_BWD);
+    PoseBwdArgs pa{};
+    pa.cam = st->cam; pa.num_splats = st->N; pa.sh_degree = st->degree; pa.log_scale_offset = sp->log_scale_offset;
+    pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.min_scale = sp->min_scale;
+    pa.mip = st->mip; pa.raw_opac = sp->raw_opacities; pa.v_combined = v_combined; pa.v_pose = v_pose;
+    void* part = nullptr;
+    const uint32_t nb = pose_bwd_blocks(st->N);
+    if (nb > 0) VS_HIP(hipMallocAsync(&part, (size_t)nb * 12 * sizeof(float), s), "hipMallocAsync(pose partials)");
+    pa.partials = static_cast<float*>(part);
+    const hipError_t e = launch_pose_bwd(pa, s);
+    if (part) hipFreeAsync(part, s);
+    VS_HIP(e, "pose backward");
+    return VS_OK;
+}
+
 extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* transforms, const void* sh_coeffs,
                                        float* raw_opacities, const float* v_combined, uint32_t* w_t,
                                        const float* lr_scale, uint32_t* w_o, const vs_adam_step* adam,

@@ -127,6 +127,21 @@ struct ProjectBwdArgs {
     float* v_refine;
 };
 
+struct PoseBwdArgs {
+    vs_camera cam;
+    uint32_t num_splats, sh_degree;
+    float log_scale_offset;
+    const float* transforms;
+    const void* sh;                  // [N,K,3] f32, or f16 bits when sh_half
+    uint32_t sh_half;
+    const float* min_scale;          // [N] scale floor or null
+    uint32_t mip;
+    const float* raw_opac;
+    const float* v_combined;         // [N,10]
+    float* partials;                 // [ceil(N/256), 12] block sums
+    float* v_pose;                   // [12]
+};
+
 struct ProjectUpdateArgs {
     vs_camera cam;
     uint32_t num_splats, sh_degree;
@@ -206,6 +221,9 @@ hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, 
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s);
 hipError_t launch_project_update(const ProjectUpdateArgs& a, hipStream_t s);
+// Camera gradient: per-splat rows summed per 256-splat block, then the blocks (in order).
+hipError_t launch_pose_bwd(const PoseBwdArgs& a, hipStream_t s);
+uint32_t pose_bwd_blocks(uint32_t num_splats);
 hipError_t launch_geo_encode(const float* m, const float* v, uint32_t n, float epsilon, uint32_t* words, hipStream_t s);
 hipError_t launch_geo_decode(const uint32_t* words, uint32_t n, float epsilon, float* m, float* v, hipStream_t s);
 hipError_t launch_geo_zero_rows(uint32_t* words, const uint32_t* rows, uint32_t num_rows, uint32_t row_width,

@@ -104,4 +104,49 @@ VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3
     return r;
 }
 
+// ---- camera gradient, bwd/kernels/pose_backwards.rs ------------------------------
+// The camera is perturbed by x_c' = (I + A) x_c + b after the world-to-camera
+// transform; A pivots on the camera centre, which b moves by -M^-1 b.
+VS_DEV F3 cross(F3 a, F3 b) { return F3{a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x}; }
+// pose_backwards.rs:61-74: M^-T g from the column cross products over det M.
+VS_DEV F3 inverse_transpose_mul(M3 m, F3 g) {
+    const F3 k0 = cross(m.c1, m.c2), k1 = cross(m.c2, m.c0), k2 = cross(m.c0, m.c1);
+    return ((k0 * g.x + k1 * g.y) + k2 * g.z) * (1.0f / dot(m.c0, k0));
+}
+
+// pose_backwards_kernel (pose_backwards.rs:88-191) for one splat whose raster
+// gradients of position, conic or colour are not all zero: the row
+// [v x^T + 2 V S (row-major 3x3), db] with v, V the camera-space mean and
+// covariance gradients and x, S the camera-space mean and covariance.
+template <int DEG, int MODEL, typename SHT>
+VS_DEV void pose_row(const vs_camera& u, const SHT* __restrict__ sh_row, F3 mean, F3 scl_raw, Qt qu, float raw,
+                     const float rg[10], const float* __restrict__ min_scale, uint32_t g, bool mip, float row[12]) {
+    const Qt q = normalize(qu);
+    const F3 scl = apply_scale_floor(scl_raw, sigmoid(raw), min_scale, g).scale;
+    // SH view direction: only the camera centre moves it.
+    const F3 u_world = mean - F3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]};
+    const float u_len = length(u_world);
+    const F3 dir = u_world * (1.0f / u_len);
+    const F3 v_dir = sh_viewdir_vjp<DEG>(sh_row, dir, F3{rg[5], rg[6], rg[7]});
+    const F3 v_mean_sh = (v_dir - dir * dot(dir, v_dir)) * (1.0f / u_len);
+    const F3 mc = world_to_cam(mean, u);
+    float filter_comp;
+    const S2 cov = compensate_cov2d(cov2d_raw<MODEL>(scl, q, mc, u), mip, filter_comp);
+    const S2 v_cov2d = inverse_vjp(inverse(cov), S2{rg[2], rg[3] * 0.5f, rg[4]});
+    const M3 vrot = view_rot(u);
+    const S3 S = congruence(outer_self(mul_diag(to_mat3(q), scl)), vrot);
+    const M23 J = project_jacobian<MODEL>(mc, u);
+    const F3 v = projection_vjp<MODEL>(J, mc, S, u, v_cov2d, F2{rg[0], rg[1]});
+    const S3 V = tcongruence(J, v_cov2d);
+    const F3 vb = v + inverse_transpose_mul(vrot, v_mean_sh);
+    const F3 vr[3] = {srow0(V), srow1(V), srow2(V)};
+    const F3 sr[3] = {srow0(S), srow1(S), srow2(S)};
+    const float vv[3] = {v.x, v.y, v.z}, xx[3] = {mc.x, mc.y, mc.z};
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) row[3 * i + j] = vv[i] * xx[j] + 2.0f * dot(vr[i], sr[j]);
+    row[9] = vb.x; row[10] = vb.y; row[11] = vb.z;
+}
+
 } // namespace vs

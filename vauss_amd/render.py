@@ -329,6 +329,31 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     return g
 
 
+def pose_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
+                  raw_opacities: torch.Tensor, v_combined: torch.Tensor, log_scale_offset: float = 0.0,
+                  min_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """pose_bwd (bwd/render_bwd.rs:224-288): the camera gradient [12] =
+    d loss / d [A (row-major 3x3), b] of x_c' = (I + A) x_c + b, from the raster
+    gradient rows `v_combined` [N,10] of render_backward on `output`."""
+    if output.state is None or output.state.handle is None:
+        raise ValueError("the forward pass kept no backward state (use a bwd-info pass)")
+    transforms = transforms.contiguous()
+    sh_coeffs = sh_coeffs.contiguous()
+    raw_opacities = raw_opacities.contiguous()
+    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities)
+    v_combined = v_combined.contiguous()
+    if tuple(v_combined.shape) != (n, 10) or v_combined.dtype != torch.float32:
+        raise ValueError("v_combined must be float32 [N, 10]")
+    dev = transforms.device
+    ctx = output.state.ctx
+    Context.get(dev)
+    v_pose = torch.empty(12, dtype=torch.float32, device=dev)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, _min_scale(min_scale, n))
+    _lib.check(ctx.lib.vs_pose_backward(ctx.handle, output.state.handle, C.byref(splats), _ptr(v_combined),
+                                        _ptr(v_pose)))
+    return v_pose
+
+
 def _powi_f32(a: float, b: int) -> np.float32:
     """f32 a^b by binary exponentiation (Rust's f32::powi, lowered to
     compiler-rt's __powisf2)."""
