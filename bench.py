@@ -131,7 +131,32 @@ def measure_next_rows(va, wl, cam, t, s, o, gt, dev, reps: int = 10) -> dict:
     nvis = int((rows != 0).sum().item())
     sh_bytes = touched * (128 * 6 + 8) + n * 16 + nvis * 24
     out.state.free()
-    return {"image_loss_l1_ssim": {"img": [w, h], "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+    # neural appearance (render_neural): the same view with random [N,4,3]
+    # rows and an [816] decoder at direction band 3; one training view
+    # (render, L1 cotangent, dense backward incl. the decoder gradient), with
+    # the projection and projection + neural backward stages from HIP events.
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    nrows = torch.rand((n, 4, 3), generator=gen, device=dev) * 3.0 - 1.5
+    dec = torch.randn(816, generator=gen, device=dev) * 0.35
+
+    def neural_step():
+        o2 = va.render(cam, wl.img_size, t, nrows, o, pass_=va.RasterPass.BACKWARD, decoder=dec, neural_degree=3)
+        v2 = va.l1_cotangent(o2.out_img, gt, (0.0, 0.0), 0.0)
+        va.render_backward(o2, t, nrows, o, v2, decoder=dec)
+        o2.state.free()
+    n_ms = timed(neural_step)
+    ctx = va.Context.get(dev)
+    ctx.enable_timing(True, stages=["project", "project_bwd"])
+    ctx.stage_times()
+    for _ in range(reps):
+        neural_step()
+    st_ms = ctx.stage_times()
+    ctx.enable_timing(False)
+    return {"neural_appearance": {"view_ms": round(n_ms, 4), "band": 3,
+                                  "project_ms": round(st_ms["project_ms"] / reps, 4),
+                                  "project_bwd_with_neural_ms": round(st_ms["project_bwd_ms"] / reps, 4)},
+            "image_loss_l1_ssim": {"img": [w, h], "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
                                    "fwd_alg_GBs": round(56 * px / (f_ms * 1e-3) / 1e9, 1),
                                    "bwd_alg_GBs": round(72 * px / (b_ms * 1e-3) / 1e9, 1)},
             "project_update": {"ms": round(u_ms, 4), "splats": n, "with_gradient": with_grad,
@@ -358,7 +383,7 @@ STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "r
                    ("tile_ranges", "ranges"),
                    ("l1_cotangent", "loss"), ("loss_", "image_loss"), ("project_update", "project_update"),
                    ("sh_step", "sh_step"), ("sh_variance", "sh_step"), ("b8_", "sh_step"),
-                   ("pose_", "pose_backward"),
+                   ("pose_", "pose_backward"), ("neural_", "neural"),
                    ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
 
 
@@ -368,7 +393,7 @@ SUMMARY_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS"
                     "TCC_EA0_ATOMIC_sum", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE", "WRITE_SIZE",
                     "SQ_INSTS_VALU_ADD_F32", "SQ_INSTS_VALU_MUL_F32", "SQ_INSTS_VALU_FMA_F32", "SQ_INSTS_VALU_INT32",
                     "SQ_INSTS_VALU_CVT", "SQ_INSTS_VALU_INT64")
-SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "pose_", "copyBuffer")
+SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "pose_", "neural_", "copyBuffer")
 
 
 def source_digest() -> str:

@@ -92,6 +92,12 @@ typedef struct vs_splats {
     const float* min_scale;         /* [N] scale floor (the Mip-Splatting 3D filter,
                                        kernels/helpers.rs:497-553) or NULL for none
                                        (render's min_scale / has_min_scale) */
+    const float* decoder;           /* [816] compact neural appearance (kernels/neural.rs,
+                                       SplatOps::render_neural, render.rs:352-397) or NULL
+                                       for SH colour.  With a decoder, sh_coeffs holds
+                                       [N,4,3] rows (base colour as a DC coefficient, an
+                                       8-value latent, a pad) and sh_degree is the
+                                       decoder's direction band, 0..3. */
 } vs_splats;
 
 /* RasterPass, crates/splat-train-render/src/gaussian_splats.rs:32-107. */
@@ -124,10 +130,12 @@ typedef struct vs_fwd_out {
  * through compact_from_global, bwd/burn_glue.rs:355-430). NULL skips one. */
 typedef struct vs_grads {
     float* v_transforms;            /* [N,10] d/d(mean, quat wxyz, log-scale) */
-    float* v_sh_coeffs;             /* [N,(d+1)^2,3] */
+    float* v_sh_coeffs;             /* [N,(d+1)^2,3], or the neural rows [N,4,3] */
     float* v_raw_opacities;         /* [N] */
     float* v_refine_weight;         /* [N] screen-space refine weight, clamped [0,1e32] */
     float* v_combined;              /* [N,10] raster gradient rows (xy, conic, rgb, alpha, refine) */
+    float* v_decoder;               /* [816] neural appearance: decoder gradient summed over splats */
+    float* v_coeffs_sq;             /* [N] neural appearance: mean square of each row's gradient */
 } vs_grads;
 
 /* ---- context --------------------------------------------------------------- */

@@ -114,6 +114,55 @@ static inline float atan2f_c(float y, float x) {
     return std::copysign(r, y);
 }
 
+// sin and cos of one argument: j = rint(x 2/pi); r = x - j pi/2 in three fma
+// steps (pi/2 split into three f32 parts), |r| <= pi/4 plus rounding; Taylor
+// polynomials of sin r (through r^11) and cos r (through r^12) in Horner
+// form; the quadrant j mod 4 picks and signs them.  Non-finite x -> NaN.
+static inline void sincosf_c(float x, float& s, float& c) {
+    if (!is_finite(x)) { s = c = NAN; return; }
+    const float j = std::rint(x * 0x1.45f306p-1f);
+    float r = std::fma(-j, 0x1.921fb6p+0f, x);
+    r = std::fma(-j, -0x1.777a5cp-25f, r);
+    r = std::fma(-j, -0x1.ee59dap-50f, r);
+    const float z = r * r;
+    float ps = std::fma(z, -0x1.ae6456p-26f, 0x1.71de3ap-19f);
+    ps = std::fma(ps, z, -0x1.a01a02p-13f);
+    ps = std::fma(ps, z, 0x1.111112p-7f);
+    ps = std::fma(ps, z, -0x1.555556p-3f);
+    const float sr = std::fma(r * z, ps, r);
+    float pc = std::fma(z, 0x1.1eed8ep-29f, -0x1.27e4fcp-22f);
+    pc = std::fma(pc, z, 0x1.a01a02p-16f);
+    pc = std::fma(pc, z, -0x1.6c16c2p-10f);
+    pc = std::fma(pc, z, 0x1.555556p-5f);
+    pc = std::fma(pc, z, -0.5f);
+    const float cr = std::fma(z, pc, 1.0f);
+    const int q = (int)(j - 4.0f * std::floor(j * 0.25f));
+    s = (q == 0) ? sr : (q == 1) ? cr : (q == 2) ? -sr : -cr;
+    c = (q == 0) ? cr : (q == 1) ? -sr : (q == 2) ? -cr : sr;
+}
+
+// tanh: |x| < 0.5625 -> x + x^3 P(x^2), P the Taylor series of (tanh x - x)/x^3
+// through x^16; otherwise 1 - 2 / (exp(2|x|) + 1) with the sign of x (1 once
+// exp overflows); signed zeros pass through.
+static inline float tanhf_c(float x) {
+    if (x != x || x == 0.0f) return x;
+    const float a = std::fabs(x);
+    if (a < 0.5625f) {
+        const float z = x * x;
+        float p = std::fma(z, -0x1.f57d78p-13f, 0x1.355824p-11f);
+        p = std::fma(p, z, -0x1.7da364p-10f);
+        p = std::fma(p, z, 0x1.d6d3d0p-9f);
+        p = std::fma(p, z, -0x1.226e36p-7f);
+        p = std::fma(p, z, 0x1.664f48p-6f);
+        p = std::fma(p, z, -0x1.ba1ba2p-5f);
+        p = std::fma(p, z, 0x1.111112p-3f);
+        p = std::fma(p, z, -0x1.555556p-2f);
+        return std::fma(x * z, p, x);
+    }
+    const float t = 1.0f - 2.0f / (expf_c(2.0f * a) + 1.0f);
+    return std::copysign(t, x);
+}
+
 // sigmoid, crates/splat-train-cube/src/lib.rs:561-564.
 static inline float sigmoid(float x) { return 1.0f / (1.0f + expf_c(-x)); }
 

@@ -76,7 +76,7 @@ def load() -> C.CDLL:
     lib = C.CDLL(os.fspath(LIB_PATH))
     lib.or_render_forward.restype = C.c_int
     lib.or_render_forward.argtypes = [C.POINTER(OrCamera), C.c_uint32, C.c_uint32, _F, _F, C.c_uint32, _F, C.c_uint32,
-                                      C.c_float, _F, _F, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+                                      C.c_float, _F, _F, _F, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
     lib.or_fwd_get_info.argtypes = [C.c_void_p, C.POINTER(OrFwdInfo)]
     lib.or_fwd_get.restype = C.c_int
     lib.or_fwd_get.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
@@ -85,6 +85,11 @@ def load() -> C.CDLL:
     lib.or_render_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F, _F]
     lib.or_project_backward.restype = C.c_int
     lib.or_project_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F]
+    lib.or_neural_backward.restype = C.c_int
+    lib.or_neural_backward.argtypes = [C.c_void_p, _F, C.c_int, _F, _F, _F, _F, C.POINTER(C.c_double)]
+    lib.or_sincosf_n.argtypes = [_F, _F, _F, C.c_uint64]
+    lib.or_tanhf_n.argtypes = [_F, _F, C.c_uint64]
+    lib.or_neural_color.argtypes = [_F, _F, _F, C.c_uint32, _F]
     lib.or_pose_backward.restype = C.c_int
     lib.or_pose_backward.argtypes = [C.c_void_p, _F, C.c_int, C.POINTER(C.c_double), _F]
     lib.or_project_update.restype = C.c_int
@@ -164,6 +169,24 @@ class OracleForward:
     num_splats: int
     sh_degree: int
     flags: int
+    neural: bool = False
+
+    @property
+    def coeffs_per_row(self) -> int:
+        return 4 if self.neural else (self.sh_degree + 1) ** 2
+
+    def _neural(self, vc, vt, vs, threads):
+        """Neural rows into vs [N,4,3], the view-direction term into vt; (v_decoder, v_coeffs_sq).
+        The decoder gradient's sums of |products| land in self.decoder_abs [816]."""
+        sq = np.zeros(self.num_splats, np.float32)
+        dec = np.zeros(816, np.float32)
+        dabs = np.zeros(816, np.float64)
+        rc = load().or_neural_backward(self.handle, _fp(vc), threads, _fp(vt), _fp(vs), _fp(sq), _fp(dec),
+                                       dabs.ctypes.data_as(C.POINTER(C.c_double)))
+        if rc != 0:
+            raise RuntimeError(f"oracle neural backward failed ({rc})")
+        self.decoder_abs = dabs
+        return dec, sq
 
     def get(self, field: int) -> np.ndarray:
         inf = self.info
@@ -192,7 +215,7 @@ class OracleForward:
 
     def backward(self, v_out: np.ndarray, threads: int = 0):
         n = self.num_splats
-        k = (self.sh_degree + 1) ** 2
+        k = self.coeffs_per_row
         v_out = np.ascontiguousarray(v_out, np.float32)
         vc = np.zeros((n, 10), np.float32)
         vt = np.zeros((n, 10), np.float32)
@@ -202,7 +225,10 @@ class OracleForward:
         rc = load().or_render_backward(self.handle, _fp(v_out), threads, _fp(vc), _fp(vt), _fp(vs), _fp(vo), _fp(vr))
         if rc != 0:
             raise RuntimeError(f"oracle backward failed ({rc})")
-        return {"v_combined": vc, "v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+        out = {"v_combined": vc, "v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+        if self.neural:
+            out["v_decoder"], out["v_coeffs_sq"] = self._neural(vc, vt, vs, threads)
+        return out
 
     def project_update(self, v_combined, transforms, raw_opac, w_t, lr_scale, w_o, adam: "OrAdam", threads: int = 0):
         """project_update on copies of the host arrays; returns the stepped
@@ -224,9 +250,10 @@ class OracleForward:
         return {"transforms": t, "raw_opac": o, "w_t": wt, "w_o": wo, "color_dir": cd, "v_refine": vr, "grad_sq": gs}
 
     def project_backward(self, v_combined: np.ndarray, threads: int = 0):
-        """The projection VJP alone, applied to the given v_combined [N,10]."""
+        """The projection VJP alone (and the neural backward in neural mode),
+        applied to the given v_combined [N,10]."""
         n = self.num_splats
-        k = (self.sh_degree + 1) ** 2
+        k = self.coeffs_per_row
         vc = np.ascontiguousarray(v_combined, np.float32)
         assert vc.shape == (n, 10)
         vt = np.zeros((n, 10), np.float32)
@@ -236,7 +263,10 @@ class OracleForward:
         rc = load().or_project_backward(self.handle, _fp(vc), threads, _fp(vt), _fp(vs), _fp(vo), _fp(vr))
         if rc != 0:
             raise RuntimeError(f"oracle projection backward failed ({rc})")
-        return {"v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+        out = {"v_transforms": vt, "v_sh": vs, "v_raw_opac": vo, "v_refine": vr}
+        if self.neural:
+            out["v_decoder"], out["v_coeffs_sq"] = self._neural(vc, vt, vs, threads)
+        return out
 
     def pose_backward(self, v_combined: np.ndarray, threads: int = 0):
         """The camera gradient [dA (row-major 3x3), db] (f64 sum) and the per-splat rows [N,12]."""
@@ -260,14 +290,23 @@ class OracleForward:
 
 
 def render_forward(cam, img_size, transforms, sh_coeffs, raw_opacities, background=(0, 0, 0), flags=FLAG_BWD_INFO,
-                   threads: int = 0, log_scale_offset: float = 0.0, min_scale=None) -> OracleForward:
-    """`flags` may add FLAG_MIP (SplatRenderMode::Mip); `min_scale` [N] is the scale floor (None: none)."""
+                   threads: int = 0, log_scale_offset: float = 0.0, min_scale=None, decoder=None,
+                   neural_degree: int = 0) -> OracleForward:
+    """`flags` may add FLAG_MIP (SplatRenderMode::Mip); `min_scale` [N] is the scale floor (None: none).
+    With `decoder` [816] the colour is the neural appearance's: `sh_coeffs` holds [N,4,3] rows
+    (base, latents, pad) and `neural_degree` (0..3) is the decoder's direction band."""
     lib = load()
     t = np.ascontiguousarray(transforms, np.float32)
     s = np.ascontiguousarray(sh_coeffs, np.float32)
     o = np.ascontiguousarray(raw_opacities, np.float32)
     n = t.shape[0]
     degree = int(round(np.sqrt(s.shape[1]))) - 1
+    dec = None
+    if decoder is not None:
+        dec = np.ascontiguousarray(decoder, np.float32)
+        if dec.shape != (816,) or s.shape[1:] != (4, 3):
+            raise ValueError("neural mode takes a [816] decoder and [N,4,3] rows")
+        degree = int(neural_degree)
     bg = np.asarray(background, np.float32)
     c = camera_struct(cam)
     h = C.c_void_p()
@@ -275,13 +314,13 @@ def render_forward(cam, img_size, transforms, sh_coeffs, raw_opacities, backgrou
     if ms is not None and ms.shape != (n,):
         raise ValueError("min_scale must hold one floor per splat")
     rc = lib.or_render_forward(C.byref(c), int(img_size[0]), int(img_size[1]), _fp(t), _fp(s), degree, _fp(o), n,
-                               float(log_scale_offset), None if ms is None else _fp(ms), _fp(bg), flags, threads,
-                               C.byref(h))
+                               float(log_scale_offset), None if ms is None else _fp(ms),
+                               None if dec is None else _fp(dec), _fp(bg), flags, threads, C.byref(h))
     if rc != 0:
         raise RuntimeError(f"oracle forward failed ({rc})")
     info = OrFwdInfo()
     lib.or_fwd_get_info(h, C.byref(info))
-    return OracleForward(h, info, n, degree, flags)
+    return OracleForward(h, info, n, degree, flags, dec is not None)
 
 
 def radix_argsort_u32(keys, vals, skip_bits, sorting_bits):
@@ -320,6 +359,29 @@ def atan2f(y, x):
     b = np.ascontiguousarray(x, np.float32)
     out = np.empty_like(a)
     load().or_atan2f_n(_fp(a), _fp(b), _fp(out), a.size)
+    return out
+
+
+def sincosf(x):
+    a = np.ascontiguousarray(x, np.float32)
+    s, c = np.empty_like(a), np.empty_like(a)
+    load().or_sincosf_n(_fp(a), _fp(s), _fp(c), a.size)
+    return s, c
+
+
+def tanhf(x):
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    load().or_tanhf_n(_fp(a), _fp(out), a.size)
+    return out
+
+
+def neural_color(row, decoder, direction, degree: int) -> np.ndarray:
+    r = np.ascontiguousarray(row, np.float32)
+    d = np.ascontiguousarray(decoder, np.float32)
+    v = np.ascontiguousarray(direction, np.float32)
+    out = np.zeros(3, np.float32)
+    load().or_neural_color(_fp(r), _fp(d), _fp(v), degree, _fp(out))
     return out
 
 

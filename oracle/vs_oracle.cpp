@@ -745,6 +745,115 @@ S2 inverse2x2_vjp(S2 minv, S2 v) {
     return S2{t00 * minv.c00 + t10 * minv.c01, t01 * minv.c00 + t11 * minv.c01, t01 * minv.c01 + t11 * minv.c11};
 }
 
+// ---- compact neural appearance, kernels/neural.rs:1-161 -------------------------
+// Row of 12 floats per splat: base colour as an SH DC coefficient (3), latent
+// f (8), pad.  x = [sin f0, cos f0, ..., sin f7, cos f7, Y0(d) .. Y15(d)],
+// h1 = ReLU(W1 x), h2 = ReLU(W2 h1), colour = ReLU(C0 base + tanh(W3 h2) + 0.5);
+// W1 16x32, W2 16x16, W3 3x16 row-major [out][in], packed in one [816].
+constexpr int NEURAL_LATENTS = 8, NEURAL_INPUTS = 32, NEURAL_HIDDEN = 16;
+constexpr int NEURAL_W1 = 0, NEURAL_W2 = 512, NEURAL_W3 = 768, NEURAL_LEN = 816, NEURAL_ROW = 12;
+constexpr float SH_C0 = 0.2820948f;
+
+// write_direction_basis (neural.rs:64-98): real SH bands 0..3 of the unit
+// direction into x[16..32); bands above `deg` are 0.
+static void direction_basis(float* x, V3 v, uint32_t deg) {
+    const float vx = v.x, vy = v.y, vz = v.z;
+    const float xy = vx * vy, xz = vx * vz, yz = vy * vz, x2 = vx * vx, y2 = vy * vy, z2 = vz * vz;
+    const float m1 = deg >= 1 ? 1.0f : 0.0f, m2 = deg >= 2 ? 1.0f : 0.0f, m3 = deg >= 3 ? 1.0f : 0.0f;
+    x[16] = 0.2820948f;
+    x[17] = m1 * (-0.4886025f * vy);
+    x[18] = m1 * (0.4886025f * vz);
+    x[19] = m1 * (-0.4886025f * vx);
+    x[20] = m2 * (1.0925484f * xy);
+    x[21] = m2 * (-1.0925484f * yz);
+    x[22] = m2 * (0.9461747f * z2 - 0.31539157f);
+    x[23] = m2 * (-1.0925484f * xz);
+    x[24] = m2 * (0.5462742f * x2 - 0.5462742f * y2);
+    x[25] = m3 * (0.5900436f * vy * (-3.0f * x2 + y2));
+    x[26] = m3 * (2.8906114f * xy * vz);
+    x[27] = m3 * (0.4570458f * vy * (1.0f - 5.0f * z2));
+    x[28] = m3 * (0.37317633f * vz * (5.0f * z2 - 3.0f));
+    x[29] = m3 * (0.4570458f * vx * (1.0f - 5.0f * z2));
+    x[30] = m3 * (1.4453057f * vz * (x2 - y2));
+    x[31] = m3 * (0.5900436f * vx * (-x2 + 3.0f * y2));
+}
+
+// direction_basis_vjp (neural_backwards.rs:82-133): d x[17..32) / d v applied to dx.
+static V3 direction_basis_vjp(const float* dx, V3 v, uint32_t deg) {
+    const float x = v.x, y = v.y, z = v.z;
+    float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+    if (deg >= 1) {
+        const float c1 = 0.4886025f;
+        gy += -c1 * dx[17];
+        gz += c1 * dx[18];
+        gx += -c1 * dx[19];
+    }
+    if (deg >= 2) {
+        const float a = 1.0925484f;
+        gx += a * y * dx[20];
+        gy += a * x * dx[20];
+        gy += -a * z * dx[21];
+        gz += -a * y * dx[21];
+        gz += 1.8923494f * z * dx[22];
+        gx += -a * z * dx[23];
+        gz += -a * x * dx[23];
+        gx += a * x * dx[24];
+        gy += -a * y * dx[24];
+    }
+    if (deg >= 3) {
+        const float x2 = x * x, y2 = y * y, z2 = z * z;
+        const float b = 1.7701308f, c = 2.8906114f, e = 0.4570458f, f = 4.570458f;
+        gx += -3.5402615f * x * y * dx[25];
+        gy += (b * y2 - b * x2) * dx[25];
+        gx += c * y * z * dx[26];
+        gy += c * x * z * dx[26];
+        gz += c * x * y * dx[26];
+        gy += (e - 2.285229f * z2) * dx[27];
+        gz += -f * y * z * dx[27];
+        gz += (5.597645f * z2 - 1.119529f) * dx[28];
+        gx += (e - 2.285229f * z2) * dx[29];
+        gz += -f * x * z * dx[29];
+        gx += c * x * z * dx[30];
+        gy += -c * y * z * dx[30];
+        gz += 1.4453057f * (x2 - y2) * dx[30];
+        gx += (b * y2 - b * x2) * dx[31];
+        gy += 3.5402615f * x * y * dx[31];
+    }
+    return V3{gx, gy, gz};
+}
+
+struct NeuralAct { float x[NEURAL_INPUTS], h1[NEURAL_HIDDEN], h2[NEURAL_HIDDEN], o[3]; };
+
+// The decoder's forward for one row (neural.rs:100-151); sums run in input order.
+static void neural_forward(const float* row, const float* W, V3 v, uint32_t deg, NeuralAct& a) {
+    for (int i = 0; i < NEURAL_LATENTS; ++i) sincosf_c(row[3 + i], a.x[2 * i], a.x[2 * i + 1]);
+    direction_basis(a.x, v, deg);
+    for (int j = 0; j < NEURAL_HIDDEN; ++j) {
+        float acc = 0.0f;
+        for (int k = 0; k < NEURAL_INPUTS; ++k) acc += W[NEURAL_W1 + j * NEURAL_INPUTS + k] * a.x[k];
+        a.h1[j] = fmax_(acc, 0.0f);
+    }
+    for (int j = 0; j < NEURAL_HIDDEN; ++j) {
+        float acc = 0.0f;
+        for (int k = 0; k < NEURAL_HIDDEN; ++k) acc += W[NEURAL_W2 + j * NEURAL_HIDDEN + k] * a.h1[k];
+        a.h2[j] = fmax_(acc, 0.0f);
+    }
+    for (int c = 0; c < 3; ++c) {
+        float acc = 0.0f;
+        for (int k = 0; k < NEURAL_HIDDEN; ++k) acc += W[NEURAL_W3 + c * NEURAL_HIDDEN + k] * a.h2[k];
+        a.o[c] = acc;
+    }
+}
+
+// neural_color (neural.rs:100-161).
+static V3 neural_color(const float* row, const float* W, V3 v, uint32_t deg) {
+    NeuralAct a;
+    neural_forward(row, W, v, deg, a);
+    return V3{fmax_(row[0] * SH_C0 + tanhf_c(a.o[0]) + 0.5f, 0.0f),
+              fmax_(row[1] * SH_C0 + tanhf_c(a.o[1]) + 0.5f, 0.0f),
+              fmax_(row[2] * SH_C0 + tanhf_c(a.o[2]) + 0.5f, 0.0f)};
+}
+
 struct RasterSplat { float x, y, A, B, C, opac, r, g, b, c00, c01, c11; uint32_t gid; float z, nx, ny, nz; };
 
 } // namespace
@@ -761,7 +870,8 @@ struct or_fwd {
     const float* raw_opac = nullptr;
     const float* min_scale = nullptr;    // NULL: no scale floor
     bool mip = false;
-    std::vector<float> transforms_copy, sh_copy, opac_copy, min_scale_copy;
+    const float* decoder = nullptr;      // [816] neural appearance, NULL: SH colour
+    std::vector<float> transforms_copy, sh_copy, opac_copy, min_scale_copy, decoder_copy;
     uint32_t V = 0;
     uint64_t evals = 0;
     std::vector<uint32_t> intersect_counts;
@@ -788,13 +898,14 @@ extern "C" int or_max_threads(void) { return resolve_threads(0); }
 extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H,
                                  const float* transforms, const float* sh, uint32_t degree,
                                  const float* raw_opac, uint32_t N, float lso, const float* min_scale,
-                                 const float bg[3], int flags, int threads, or_fwd** out) {
-    if (!cam_in || !out || W == 0 || H == 0 || degree > 4) return 1;
+                                 const float* decoder, const float bg[3], int flags, int threads, or_fwd** out) {
+    if (!cam_in || !out || W == 0 || H == 0 || degree > 4 || (decoder && degree > 3)) return 1;
     const int nthreads = resolve_threads(threads);
     auto f = std::make_unique<or_fwd>();
     f->cam = *cam_in;
     const or_camera& u = f->cam;
-    f->W = W; f->H = H; f->N = N; f->degree = degree; f->K = (degree + 1) * (degree + 1); f->lso = lso;
+    // Neural rows hold 4 coefficients; `degree` is then the decoder's direction band.
+    f->W = W; f->H = H; f->N = N; f->degree = degree; f->K = decoder ? 4u : (degree + 1) * (degree + 1); f->lso = lso;
     f->bg[0] = bg[0]; f->bg[1] = bg[1]; f->bg[2] = bg[2];
     f->flags = flags;
     const bool bwd_info = flags & OR_FLAG_BWD_INFO;
@@ -813,6 +924,10 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
     if (min_scale) {
         f->min_scale_copy.assign(min_scale, min_scale + N);
         f->min_scale = f->min_scale_copy.data();
+    }
+    if (decoder) {
+        f->decoder_copy.assign(decoder, decoder + NEURAL_LEN);
+        f->decoder = f->decoder_copy.data();
     }
     f->mip = (flags & OR_FLAG_MIP) != 0;
     const bool mip = f->mip;
@@ -903,7 +1018,17 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         const S2 conic = s2_inverse(cov);
         float mx, my;
         project(mean_c, u, mx, my);
-        const V3 col = splat_color(sh + (size_t)g * K * 3, degree, mean, u);
+        V3 col;
+        if (f->decoder) {
+            // kernels/project_visible.rs:25-61, neural branch: the same scrub and clamp
+            const V3 c3 = neural_color(sh + (size_t)g * NEURAL_ROW, f->decoder,
+                                       normalize(sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]})), degree);
+            col = V3{clampf(is_finite(c3.x) ? c3.x : 0.0f, -100.0f, 100.0f),
+                     clampf(is_finite(c3.y) ? c3.y : 0.0f, -100.0f, 100.0f),
+                     clampf(is_finite(c3.z) ? c3.z : 0.0f, -100.0f, 100.0f)};
+        } else {
+            col = splat_color(sh + (size_t)g * K * 3, degree, mean, u);
+        }
         float* row = &f->projected[(size_t)c * 9];
         row[0] = mx; row[1] = my; row[2] = conic.c00; row[3] = conic.c01; row[4] = conic.c11;
         row[5] = opac; row[6] = col.x; row[7] = col.y; row[8] = col.z;
@@ -1240,9 +1365,10 @@ static SplatVjp splat_vjp(const or_fwd* f, uint32_t g, const float* t, float raw
     const float u_len = length(u_world);
     const V3 vdir = scale(u_world, 1.0f / u_len);
     const V3 v_color = v3(rg[5], rg[6], rg[7]);
-    const V3 v_v_sh = sh_viewdir_vjp(cb, degree, vdir, v_color);
+    // Neural appearance adds its own view-direction term after (neural_backwards.rs).
+    const V3 v_v_sh = f->decoder ? V3{0.0f, 0.0f, 0.0f} : sh_viewdir_vjp(cb, degree, vdir, v_color);
     const float v_dot = dot(vdir, v_v_sh);
-    const V3 v_mean_sh = scale(sub(v_v_sh, scale(vdir, v_dot)), 1.0f / u_len);
+    const V3 v_mean_sh = f->decoder ? V3{0.0f, 0.0f, 0.0f} : scale(sub(v_v_sh, scale(vdir, v_dot)), 1.0f / u_len);
     const V3 mean_c = world_to_cam(mean, u);
     const M3 R = quat_to_mat3(q);
     const M3 Mm = mul_diag(R, sc);
@@ -1294,7 +1420,7 @@ static int project_vjp(const or_fwd* f, const float* vcf, int nthreads, float* v
         for (int k = 0; k < 10; ++k) { rg[k] = vcf[(size_t)g * 10 + k]; any = any || rg[k] != 0.0f; }
         if (!any) continue;
         const SplatVjp r = splat_vjp(f, g, f->transforms + (size_t)g * 10, f->raw_opac[g], rg);
-        if (v_sh) {
+        if (v_sh && !f->decoder) {
             // sh.rs:281-359: v_coeff_k = Y_k(v) v_colour
             float Y[25];
             const int n = sh_basis(degree, r.vdir, Y);
@@ -1567,6 +1693,122 @@ extern "C" int or_project_update(const or_fwd* f, const float* v_combined, float
     return 0;
 }
 
+// ---- neural appearance backward, bwd/kernels/neural_backwards.rs:141-283 ---------
+// One visible splat with a colour gradient: its row gradient [base (DC
+// units), latents, 0] and the row's mean square, its view-direction mean
+// gradient, and its decoder weight products added to dW (f64).
+static void neural_row_backward(const or_fwd* f, uint32_t g, V3 vc, float* v_row, float& sq_out, V3& v_mean,
+                                double* dW, double* dW_abs) {
+    const or_camera& u = f->cam;
+    const float* W = f->decoder;
+    const float* row = f->sh + (size_t)g * NEURAL_ROW;
+    const float* t = f->transforms + (size_t)g * 10;
+    const V3 u_world = sub(v3(t[0], t[1], t[2]), V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
+    const float u_len = length(u_world);
+    const V3 dir = scale(u_world, 1.0f / u_len);
+    NeuralAct a;
+    neural_forward(row, W, dir, f->degree, a);
+    const float gc3[3] = {vc.x, vc.y, vc.z};
+    float sq = 0.0f, go[3];
+    for (int c = 0; c < 3; ++c) {
+        const float th = tanhf_c(a.o[c]);
+        const float base = row[c] * SH_C0;
+        const float gcol = (base + th + 0.5f > 0.0f) ? gc3[c] : 0.0f;     // ReLU of the colour
+        v_row[c] = gcol * SH_C0;
+        sq += (gcol * SH_C0) * (gcol * SH_C0);
+        go[c] = gcol * (1.0f - th * th);
+    }
+    float d2[NEURAL_HIDDEN], d1[NEURAL_HIDDEN], dx[NEURAL_INPUTS];
+    for (int k = 0; k < NEURAL_HIDDEN; ++k) {
+        float acc = 0.0f;
+        for (int c = 0; c < 3; ++c) acc += W[NEURAL_W3 + c * NEURAL_HIDDEN + k] * go[c];
+        d2[k] = (a.h2[k] > 0.0f) ? acc : 0.0f;
+    }
+    for (int k = 0; k < NEURAL_HIDDEN; ++k) {
+        float acc = 0.0f;
+        for (int j = 0; j < NEURAL_HIDDEN; ++j) acc += W[NEURAL_W2 + j * NEURAL_HIDDEN + k] * d2[j];
+        d1[k] = (a.h1[k] > 0.0f) ? acc : 0.0f;
+    }
+    for (int k = 0; k < NEURAL_INPUTS; ++k) {
+        float acc = 0.0f;
+        for (int j = 0; j < NEURAL_HIDDEN; ++j) acc += W[NEURAL_W1 + j * NEURAL_INPUTS + k] * d1[j];
+        dx[k] = acc;
+    }
+    // latents through sin / cos
+    for (int i = 0; i < NEURAL_LATENTS; ++i) {
+        const float gl = dx[2 * i] * a.x[2 * i + 1] - dx[2 * i + 1] * a.x[2 * i];
+        v_row[3 + i] = gl;
+        sq += gl * gl;
+    }
+    v_row[11] = 0.0f;
+    sq_out = sq / (float)NEURAL_ROW;
+    const V3 g_dir = direction_basis_vjp(dx, dir, f->degree);
+    v_mean = scale(sub(g_dir, scale(dir, dot(dir, g_dir))), 1.0f / u_len);
+    auto add = [&](int w, float p) { dW[w] += (double)p; dW_abs[w] += std::fabs((double)p); };
+    for (int j = 0; j < NEURAL_HIDDEN; ++j)
+        for (int k = 0; k < NEURAL_INPUTS; ++k) add(NEURAL_W1 + j * NEURAL_INPUTS + k, d1[j] * a.x[k]);
+    for (int j = 0; j < NEURAL_HIDDEN; ++j)
+        for (int k = 0; k < NEURAL_HIDDEN; ++k) add(NEURAL_W2 + j * NEURAL_HIDDEN + k, d2[j] * a.h1[k]);
+    for (int c = 0; c < 3; ++c)
+        for (int k = 0; k < NEURAL_HIDDEN; ++k) add(NEURAL_W3 + c * NEURAL_HIDDEN + k, go[c] * a.h2[k]);
+}
+
+// project_bwd_neural's neural half (bwd/render_bwd.rs:390-435): rows [N,12],
+// their mean squares [N], the decoder gradient [816] summed in f64, and each
+// row's view-direction term added to v_transforms' mean (in/out; may be NULL).
+extern "C" int or_neural_backward(const or_fwd* f, const float* v_combined, int threads, float* v_transforms,
+                                  float* v_rows, float* v_rows_sq, float* v_decoder, double* v_decoder_abs) {
+    if (!f || !v_combined || !f->decoder || !(f->flags & OR_FLAG_BWD_INFO)) return 1;
+    const uint32_t N = f->N;
+    if (v_rows) std::memset(v_rows, 0, sizeof(float) * (size_t)N * NEURAL_ROW);
+    if (v_rows_sq) std::memset(v_rows_sq, 0, sizeof(float) * N);
+    const int nthreads = resolve_threads(threads);
+    std::vector<double> dW((size_t)nthreads * NEURAL_LEN, 0.0), dW_abs((size_t)nthreads * NEURAL_LEN, 0.0);
+    std::vector<float> means((size_t)N * 3, 0.0f);
+    std::vector<uint8_t> active(N, 0);
+    #pragma omp parallel num_threads(nthreads)
+    {
+#ifdef _OPENMP
+        double* mine = &dW[(size_t)omp_get_thread_num() * NEURAL_LEN];
+        double* mine_abs = &dW_abs[(size_t)omp_get_thread_num() * NEURAL_LEN];
+#else
+        double* mine = dW.data();
+        double* mine_abs = dW_abs.data();
+#endif
+        #pragma omp for schedule(static)
+        for (int64_t ci = 0; ci < (int64_t)f->V; ++ci) {
+            const uint32_t g = f->global_from_compact[(size_t)ci];
+            const float* rg = v_combined + (size_t)g * 10;
+            const V3 vc = v3(rg[5], rg[6], rg[7]);
+            if (vc.x == 0.0f && vc.y == 0.0f && vc.z == 0.0f) continue;
+            float row[NEURAL_ROW], sq;
+            V3 vm;
+            neural_row_backward(f, g, vc, row, sq, vm, mine, mine_abs);
+            if (v_rows) std::memcpy(v_rows + (size_t)g * NEURAL_ROW, row, sizeof(row));
+            if (v_rows_sq) v_rows_sq[g] = sq;
+            means[(size_t)g * 3] = vm.x; means[(size_t)g * 3 + 1] = vm.y; means[(size_t)g * 3 + 2] = vm.z;
+            active[g] = 1;
+        }
+    }
+    if (v_transforms)
+        for (uint32_t g = 0; g < N; ++g)
+            if (active[g])
+                for (int k = 0; k < 3; ++k) v_transforms[(size_t)g * 10 + k] += means[(size_t)g * 3 + k];
+    if (v_decoder)
+        for (int w = 0; w < NEURAL_LEN; ++w) {
+            double acc = 0.0;
+            for (int t = 0; t < nthreads; ++t) acc += dW[(size_t)t * NEURAL_LEN + w];
+            v_decoder[w] = (float)acc;
+        }
+    if (v_decoder_abs)
+        for (int w = 0; w < NEURAL_LEN; ++w) {
+            double acc = 0.0;
+            for (int t = 0; t < nthreads; ++t) acc += dW_abs[(size_t)t * NEURAL_LEN + w];
+            v_decoder_abs[w] = acc;
+        }
+    return 0;
+}
+
 // ---- camera gradient, bwd/kernels/pose_backwards.rs:1-191 -------------------------
 // The camera is perturbed by x_c' = (I + A) x_c + b after the world-to-camera
 // transform; A pivots on the camera centre, which b moves by -M^-1 b.
@@ -1682,6 +1924,18 @@ extern "C" void or_expf_n(const float* x, float* y, uint64_t n) {
 extern "C" void or_logf_n(const float* x, float* y, uint64_t n) {
     #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < (int64_t)n; ++i) y[i] = logf_c(x[i]);
+}
+extern "C" void or_sincosf_n(const float* x, float* s, float* c, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) sincosf_c(x[i], s[i], c[i]);
+}
+extern "C" void or_tanhf_n(const float* x, float* y, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) y[i] = tanhf_c(x[i]);
+}
+// The neural decoder's colour for one row and direction (test hook).
+extern "C" void or_neural_color(const float row[12], const float decoder[816], const float dir[3], uint32_t degree,
+                                float out[3]) {
+    const V3 c = neural_color(row, decoder, V3{dir[0], dir[1], dir[2]}, degree);
+    out[0] = c.x; out[1] = c.y; out[2] = c.z;
 }
 extern "C" void or_atan2f_n(const float* y, const float* x, float* r, uint64_t n) {
     #pragma omp parallel for schedule(static)

@@ -52,6 +52,7 @@ int or_render_forward(const or_camera* cam, uint32_t img_w, uint32_t img_h,
                       const float* transforms, const float* sh_coeffs, uint32_t sh_degree,
                       const float* raw_opacities, uint32_t num_splats, float log_scale_offset,
                       const float* min_scale /* [N] scale floor or NULL */,
+                      const float* decoder /* [816] neural appearance or NULL */,
                       const float background[3], int flags, int threads, or_fwd** out);
 
 /* Sizes of the result arrays. */
@@ -93,6 +94,21 @@ int or_render_backward(const or_fwd* f, const float* v_out, int threads,
  * raster gradients it was fed. */
 int or_project_backward(const or_fwd* f, const float* v_combined, int threads,
                         float* v_transforms, float* v_sh, float* v_raw_opac, float* v_refine);
+
+/* Neural appearance backward (bwd/kernels/neural_backwards.rs, bwd/render_bwd.rs:
+ * 390-435) of a forward rendered with a decoder: per-splat row gradients
+ * [N,12] (base in DC units, latents, 0), their mean squares [N], the decoder
+ * gradient [816] (f64 sum), and each row's view-direction term added to
+ * v_transforms [N,10] (in/out, as or_render_backward wrote it; NULL skips). */
+int or_neural_backward(const or_fwd* f, const float* v_combined, int threads, float* v_transforms,
+                       float* v_rows, float* v_rows_sq, float* v_decoder,
+                       double* v_decoder_abs /* [816] sum of |products| (a bound for summation error) or NULL */);
+
+/* Shared transcendentals and the neural colour, for the oracle's own tests. */
+void or_sincosf_n(const float* x, float* s, float* c, uint64_t n);
+void or_tanhf_n(const float* x, float* y, uint64_t n);
+void or_neural_color(const float row[12], const float decoder[816], const float dir[3], uint32_t degree,
+                     float out[3]);
 
 /* The camera gradient (bwd/render_bwd.rs:224-288, bwd/kernels/pose_backwards.rs):
  * d loss / d [A (row-major 3x3), b] of the camera-space perturbation

@@ -43,7 +43,7 @@ class VsPose(C.Structure):
 class VsSplats(C.Structure):
     _fields_ = [("transforms", C.c_void_p), ("sh_coeffs", C.c_void_p), ("raw_opacities", C.c_void_p),
                 ("num_splats", C.c_uint32), ("sh_degree", C.c_uint32), ("log_scale_offset", C.c_float),
-                ("sh_dtype", C.c_uint32), ("min_scale", C.c_void_p)]
+                ("sh_dtype", C.c_uint32), ("min_scale", C.c_void_p), ("decoder", C.c_void_p)]
 
 
 class VsShStepParams(C.Structure):
@@ -59,7 +59,8 @@ class VsFwdOut(C.Structure):
 
 class VsGrads(C.Structure):
     _fields_ = [("v_transforms", C.c_void_p), ("v_sh_coeffs", C.c_void_p), ("v_raw_opacities", C.c_void_p),
-                ("v_refine_weight", C.c_void_p), ("v_combined", C.c_void_p)]
+                ("v_refine_weight", C.c_void_p), ("v_combined", C.c_void_p), ("v_decoder", C.c_void_p),
+                ("v_coeffs_sq", C.c_void_p)]
 
 
 class VsStageTimes(C.Structure):

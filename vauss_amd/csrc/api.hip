@@ -75,7 +75,7 @@ struct vs_ctx {
 struct vs_fwd_state {
     vs_ctx* ctx = nullptr;
     vs_camera cam{};
-    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0, sh_half = 0, mip = 0;
+    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0, sh_half = 0, mip = 0, neural = 0;
     const float* min_scale = nullptr;   // the forward's scale floor (borrowed), or null
     float lso = 0.0f;
     float bg[3] = {0, 0, 0};
@@ -133,6 +133,9 @@ vs_status check_splats(const vs_splats* sp) {
     if (((uintptr_t)sp->sh_coeffs & 15u) != 0) return fail(VS_ERR_INVALID, "sh_coeffs must be 16-byte aligned");
     if (((uintptr_t)sp->raw_opacities & 3u) != 0) return fail(VS_ERR_INVALID, "raw_opacities must be 4-byte aligned");
     if (((uintptr_t)sp->min_scale & 3u) != 0) return fail(VS_ERR_INVALID, "min_scale must be 4-byte aligned");
+    if (sp->decoder && sp->sh_degree > 3)
+        return fail(VS_ERR_INVALID, "neural appearance: sh_degree is the decoder's direction band, 0..3");
+    if (((uintptr_t)sp->decoder & 3u) != 0) return fail(VS_ERR_INVALID, "decoder must be 4-byte aligned");
     return VS_OK;
 }
 
@@ -321,7 +324,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->ctx = ctx;
     st->cam = *cam;
     st->W = W; st->H = H; st->N = sp->num_splats; st->degree = sp->sh_degree;
-    st->K = (sp->sh_degree + 1) * (sp->sh_degree + 1);
+    st->neural = sp->decoder ? 1u : 0u;
+    st->K = sp->decoder ? 4u : (sp->sh_degree + 1) * (sp->sh_degree + 1);
     st->sh_half = sp->sh_dtype == VS_SH_F16 ? 1u : 0u;
     st->mip = mode == VS_MODE_MIP ? 1u : 0u;
     st->min_scale = sp->min_scale;
@@ -392,7 +396,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.cam = *cam;
         pa.img_w = W; pa.img_h = H; pa.tile_bw = st->tbw; pa.tile_bh = st->tbh;
         pa.num_splats = N; pa.sh_degree = sp->sh_degree; pa.log_scale_offset = sp->log_scale_offset;
-        pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.min_scale = st->min_scale; pa.mip = st->mip; pa.raw_opac = sp->raw_opacities;
+        pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.min_scale = st->min_scale; pa.mip = st->mip; pa.decoder = sp->decoder; pa.raw_opac = sp->raw_opacities;
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
         pa.proj_aux = st->proj_aux; pa.compact = st->compact; pa.block_stats = st->block_stats;
@@ -546,6 +550,10 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
         return fail(VS_ERR_INVALID, "splats differ from the forward's");
     if ((sp->min_scale != nullptr) != (st->min_scale != nullptr))
         return fail(VS_ERR_INVALID, "the backward's scale floor must match the forward's (both set or both null)");
+    if ((sp->decoder != nullptr) != (st->neural != 0u))
+        return fail(VS_ERR_INVALID, "the backward's decoder must match the forward's (both set or both null)");
+    if (st->neural && grads->v_sh_coeffs && ((uintptr_t)grads->v_sh_coeffs & 15u))
+        return fail(VS_ERR_INVALID, "neural row gradients must be 16-byte aligned");
     if (((uintptr_t)out_img & 15u) || ((uintptr_t)v_out & 15u)) return fail(VS_ERR_INVALID, "images must be 16-byte aligned");
     if (grads->v_transforms && ((uintptr_t)grads->v_transforms & 7u)) return fail(VS_ERR_INVALID, "v_transforms must be 8-byte aligned");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
@@ -575,16 +583,33 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     // With no dense gradient requested the backward stops at the raster
     // gradients (the reference's BackwardFusedUpdate pass: vs_project_update
     // then takes v_combined).
-    const bool dense = grads->v_transforms || grads->v_sh_coeffs || grads->v_raw_opacities || grads->v_refine_weight;
+    const bool dense = grads->v_transforms || grads->v_sh_coeffs || grads->v_raw_opacities || grads->v_refine_weight ||
+                       grads->v_decoder || grads->v_coeffs_sq;
     if (dense) {
         StageTimer tm(ctx, ST_PROJECT_BWD);
         ProjectBwdArgs pb{};
         pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = sp->log_scale_offset;
         pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.sh_half = st->sh_half; pb.min_scale = sp->min_scale; pb.mip = st->mip; pb.raw_opac = sp->raw_opacities;
+        pb.decoder = sp->decoder;
         pb.counts = st->counts; pb.v_combined = vc;
         pb.v_transforms = grads->v_transforms; pb.v_sh = grads->v_sh_coeffs;
         pb.v_raw_opac = grads->v_raw_opacities; pb.v_refine = grads->v_refine_weight;
         VS_HIP(launch_project_bwd(pb, s), "projection backward");
+        if (st->neural) {
+            // project_bwd_neural's second half (bwd/render_bwd.rs:390-435)
+            NeuralBwdArgs nb{};
+            nb.cam = st->cam; nb.num_splats = N; nb.degree = st->degree; nb.transforms = sp->transforms;
+            nb.rows = sp->sh_coeffs; nb.half = st->sh_half; nb.decoder = sp->decoder; nb.v_combined = vc;
+            nb.v_transforms = grads->v_transforms; nb.v_rows = grads->v_sh_coeffs; nb.v_rows_sq = grads->v_coeffs_sq;
+            nb.v_decoder = grads->v_decoder;
+            void* part = nullptr;
+            VS_HIP(hipMallocAsync(&part, (size_t)neural_bwd_blocks(N) * 816 * sizeof(float), s),
+                   "hipMallocAsync(decoder partials)");
+            nb.partials = static_cast<float*>(part);
+            const hipError_t e = launch_neural_bwd(nb, s);
+            hipFreeAsync(part, s);
+            VS_HIP(e, "neural backward");
+        }
     }
     if (vc_alloc) VS_HIP(hipFreeAsync(vc_alloc, s), "hipFreeAsync(v_combined)");
     return VS_OK;
@@ -594,6 +619,7 @@ extern "C" vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_sp
                                       float* v_pose) {
     if (!ctx || !st || !v_combined || !v_pose) return fail(VS_ERR_INVALID, "null argument");
     if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
+    if (st->neural) return fail(VS_ERR_UNSUPPORTED, "the camera gradient follows the SH colour path (no neural appearance)");
     vs_status vst = check_splats(sp);
     if (vst != VS_OK) return vst;
     if (sp->num_splats != st->N || sp->sh_degree != st->degree || (sp->sh_dtype == VS_SH_F16) != (st->sh_half != 0))
@@ -624,6 +650,7 @@ extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* tra
                                        vs_update_out* out) {
     if (!ctx || !st || !adam || !out) return fail(VS_ERR_INVALID, "null argument");
     if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
+    if (st->neural) return fail(VS_ERR_UNSUPPORTED, "the fused update takes SH colour (neural appearance trains unfused)");
     const uint32_t N = st->N;
     if (N > 0 && (!transforms || !sh_coeffs || !raw_opacities || !v_combined || !w_t || !lr_scale || !w_o))
         return fail(VS_ERR_INVALID, "parameter, gradient or moment pointer is null");

@@ -17,6 +17,7 @@
 #include "vs_device.h"
 #include "vs_camera.h"
 #include "vs_sh.h"
+#include "vs_neural.h"
 #include "vs_internal.h"
 
 namespace vs {
@@ -268,7 +269,18 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             dbits = as_u(mc.z);
             visible = true;
             // Projected row (kernels/project_visible.rs:150-173), written at the global id.
-            const F3 col = load_color<DEG>(static_cast<const SHT*>(a.sh), g, mean, u);
+            F3 col;
+            if constexpr (DEG == NEURAL_DEG) {
+                // kernels/project_visible.rs:25-61, neural branch: the same scrub and clamp
+                const F3 vd = normalize(mean - F3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
+                const F3 c3 = neural_color(static_cast<const SHT*>(a.sh) + (size_t)g * NEURAL_ROW, a.decoder, vd,
+                                           a.sh_degree);
+                col = F3{clampf(finite(c3.x) ? c3.x : 0.0f, -100.0f, 100.0f),
+                         clampf(finite(c3.y) ? c3.y : 0.0f, -100.0f, 100.0f),
+                         clampf(finite(c3.z) ? c3.z : 0.0f, -100.0f, 100.0f)};
+            } else {
+                col = load_color<DEG>(static_cast<const SHT*>(a.sh), g, mean, u);
+            }
             a.proj_a[g] = make_float4(px, py, conic.c00, conic.c01);
             a.proj_b[g] = make_float4(conic.c11, opac, col.x, col.y);
             a.proj_c[g] = col.z;
@@ -485,6 +497,10 @@ hipError_t launch_project(const ProjectArgs& a, hipStream_t s) {
     if (a.num_splats == 0) return hipSuccess;
     const dim3 grid((a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK);
     const bool geom = a.proj_aux != nullptr;
+    if (a.decoder) {
+        launch_project_model<NEURAL_DEG>(a, grid, s, geom);
+        return hipGetLastError();
+    }
     switch (a.sh_degree) {
     case 0: launch_project_model<0>(a, grid, s, geom); break;
     case 1: launch_project_model<1>(a, grid, s, geom); break;

@@ -8,6 +8,7 @@
 // gradients, which is the reference's dense result after gathering its compact
 // rows through compact_from_global (bwd/burn_glue.rs:355-395).
 #include "vs_vjp.h"
+#include "vs_neural.h"
 #include "vs_internal.h"
 
 namespace vs {
@@ -16,7 +17,8 @@ constexpr int PBWD_BLOCK = 256;
 
 template <int DEG, int MODEL, typename SHT>
 __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs a) {
-    constexpr int K = sh_count<DEG>();
+    // Neural rows (DEG < 0) and their gradients belong to the neural backward.
+    constexpr int K = DEG >= 0 ? sh_count<DEG>() : 0;
     const uint32_t g = blockIdx.x * PBWD_BLOCK + threadIdx.x;
     if (g >= a.num_splats) return;
     const vs_camera& u = a.cam;
@@ -26,7 +28,7 @@ __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs 
     bool any = false;
 #pragma unroll
     for (int k = 0; k < 10; ++k) any = any || rg[k] != 0.0f;
-    float* vsh = a.v_sh ? a.v_sh + (size_t)g * K * 3 : nullptr;
+    float* vsh = (DEG >= 0 && a.v_sh) ? a.v_sh + (size_t)g * K * 3 : nullptr;
     if (!any) {
         if (a.v_transforms) {
             float2* o = reinterpret_cast<float2*>(a.v_transforms + (size_t)g * 10);
@@ -49,15 +51,17 @@ __global__ void __launch_bounds__(PBWD_BLOCK) project_bwd_kernel(ProjectBwdArgs 
     const Qt qu{t23.y, t45.x, t45.y, t67.x};
     const SplatVjp r = splat_vjp<DEG, MODEL>(u, static_cast<const SHT*>(a.sh) + (size_t)g * K * 3, mean, scl, qu, a.raw_opac[g], rg,
                                               a.min_scale, g, a.mip != 0u);
-    if (vsh) {
-        // sh.rs:281-359: v_coeff_k = Y_k(v) v_colour
-        float Y[K];
-        sh_basis<DEG>(r.vdir, Y);
+    if constexpr (DEG >= 0) {
+        if (vsh) {
+            // sh.rs:281-359: v_coeff_k = Y_k(v) v_colour
+            float Y[K];
+            sh_basis<DEG>(r.vdir, Y);
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            vsh[3 * k] = rg[5] * Y[k];
-            vsh[3 * k + 1] = rg[6] * Y[k];
-            vsh[3 * k + 2] = rg[7] * Y[k];
+            for (int k = 0; k < K; ++k) {
+                vsh[3 * k] = rg[5] * Y[k];
+                vsh[3 * k + 1] = rg[6] * Y[k];
+                vsh[3 * k + 2] = rg[7] * Y[k];
+            }
         }
     }
     if (a.v_raw_opac) a.v_raw_opac[g] = r.v_raw;
@@ -90,6 +94,10 @@ static void launch_pbwd_model(const ProjectBwdArgs& a, dim3 grid, hipStream_t s)
 hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s) {
     if (a.num_splats == 0) return hipSuccess;
     const dim3 grid((a.num_splats + PBWD_BLOCK - 1) / PBWD_BLOCK);
+    if (a.decoder) {
+        launch_pbwd_model<NEURAL_DEG>(a, grid, s);
+        return hipGetLastError();
+    }
     switch (a.sh_degree) {
     case 0: launch_pbwd_model<0>(a, grid, s); break;
     case 1: launch_pbwd_model<1>(a, grid, s); break;

@@ -46,6 +46,7 @@ struct ProjectArgs {
     uint32_t sh_half;
     const float* min_scale;          // [N] scale floor (apply_scale_floor) or null
     uint32_t mip;                    // SplatRenderMode::Mip
+    const float* decoder;            // [816] neural appearance (rows of 12, sh_degree = direction band) or null
     const float* raw_opac;
     // outputs, indexed by global splat id
     float* opacities;           // [N]
@@ -118,6 +119,7 @@ struct ProjectBwdArgs {
     uint32_t sh_half;
     const float* min_scale;          // [N] scale floor (apply_scale_floor) or null
     uint32_t mip;                    // SplatRenderMode::Mip
+    const float* decoder;            // neural appearance: no SH term here (the neural backward adds it)
     const float* raw_opac;
     const uint32_t* counts;          // visible <=> counts defined; culled rows get zeros
     const float* v_combined;         // [N,10]
@@ -125,6 +127,21 @@ struct ProjectBwdArgs {
     float* v_sh;
     float* v_raw_opac;
     float* v_refine;
+};
+
+struct NeuralBwdArgs {
+    vs_camera cam;
+    uint32_t num_splats, degree;     // degree: the decoder's direction band
+    const float* transforms;
+    const void* rows;                // [N,12] f32, or f16 bits when half
+    uint32_t half;
+    const float* decoder;            // [816]
+    const float* v_combined;         // [N,10]
+    float* v_transforms;             // [N,10] mean += view-direction term, or null
+    float* v_rows;                   // [N,12] or null
+    float* v_rows_sq;                // [N] or null
+    float* partials;                 // [gridDim, 816]
+    float* v_decoder;                // [816] or null
 };
 
 struct PoseBwdArgs {
@@ -223,6 +240,9 @@ hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s);
 hipError_t launch_project_update(const ProjectUpdateArgs& a, hipStream_t s);
 // Camera gradient: per-splat rows summed per 256-splat block, then the blocks (in order).
 hipError_t launch_pose_bwd(const PoseBwdArgs& a, hipStream_t s);
+// Neural appearance backward: rows, mean term, per-block decoder partials, then their sum.
+hipError_t launch_neural_bwd(const NeuralBwdArgs& a, hipStream_t s);
+uint32_t neural_bwd_blocks(uint32_t num_splats);
 uint32_t pose_bwd_blocks(uint32_t num_splats);
 hipError_t launch_geo_encode(const float* m, const float* v, uint32_t n, float epsilon, uint32_t* words, hipStream_t s);
 hipError_t launch_geo_decode(const uint32_t* words, uint32_t n, float epsilon, float* m, float* v, hipStream_t s);

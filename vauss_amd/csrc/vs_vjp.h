@@ -67,9 +67,12 @@ VS_DEV SplatVjp splat_vjp(const vs_camera& u, const SHT* __restrict__ sh_row, F3
     const float u_len = length(u_world);
     const F3 vdir = u_world * (1.0f / u_len);
     const F3 v_color{rg[5], rg[6], rg[7]};
-    const F3 v_v_sh = sh_viewdir_vjp<DEG>(sh_row, vdir, v_color);
-    const float v_dot = dot(vdir, v_v_sh);
-    const F3 v_mean_sh = (v_v_sh - vdir * v_dot) * (1.0f / u_len);
+    F3 v_mean_sh{0.0f, 0.0f, 0.0f};   // neural appearance (DEG < 0) adds its own term after
+    if constexpr (DEG >= 0) {
+        const F3 v_v_sh = sh_viewdir_vjp<DEG>(sh_row, vdir, v_color);
+        const float v_dot = dot(vdir, v_v_sh);
+        v_mean_sh = (v_v_sh - vdir * v_dot) * (1.0f / u_len);
+    }
 
     // Covariance / projection VJP, project_backwards.rs:203-274
     const F3 mc = world_to_cam(mean, u);

@@ -190,9 +190,24 @@ class SplatGrads:
     v_raw_opac: torch.Tensor
     v_refine_weight: torch.Tensor
     v_combined: torch.Tensor
+    v_decoder: Optional[torch.Tensor] = None     # neural appearance: [816]
+    v_coeffs_sq: Optional[torch.Tensor] = None   # neural appearance: [N] mean square of each row gradient
 
 
-def _check_splats(transforms, sh_coeffs, raw_opacities):
+NEURAL_DECODER_LEN = 816     # kernels/neural.rs:42-49: W1 16x32, W2 16x16, W3 3x16
+
+
+def _check_decoder(decoder: Optional[torch.Tensor], neural_degree: int) -> Optional[torch.Tensor]:
+    if decoder is None:
+        return None
+    if decoder.dtype != torch.float32 or decoder.numel() != NEURAL_DECODER_LEN or not decoder.is_cuda:
+        raise ValueError("decoder must be a float32 GPU tensor of 816 weights")
+    if not 0 <= int(neural_degree) <= 3:
+        raise ValueError("neural_degree (the decoder's direction band) must be 0..3")
+    return decoder.contiguous()
+
+
+def _check_splats(transforms, sh_coeffs, raw_opacities, neural_degree: Optional[int] = None):
     if transforms.dim() != 2 or transforms.shape[1] != 10:
         raise ValueError(f"transforms must be [N, 10], got {tuple(transforms.shape)}")
     n = transforms.shape[0]
@@ -209,6 +224,11 @@ def _check_splats(transforms, sh_coeffs, raw_opacities):
     for name, t in (("transforms", transforms), ("sh_coeffs", sh_coeffs), ("raw_opacities", raw_opacities)):
         if not t.is_cuda:
             raise ValueError(f"{name} must live on the GPU")
+    if neural_degree is not None:
+        # neural appearance rows: base (3), latent (8), pad as 4 coefficients (kernels/neural.rs:37-40)
+        if sh_coeffs.shape[1] != 4:
+            raise ValueError("neural appearance rows must be [N, 4, 3]")
+        return n, int(neural_degree)
     return n, sh_degree_from_coeffs(sh_coeffs.shape[1])
 
 
@@ -220,7 +240,8 @@ def _min_scale(min_scale: Optional[torch.Tensor], n: int) -> Optional[torch.Tens
     return min_scale.contiguous().reshape(n)
 
 
-def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale=None) -> _lib.VsSplats:
+def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale=None,
+                   decoder=None) -> _lib.VsSplats:
     s = _lib.VsSplats()
     s.transforms = _ptr(transforms)
     s.sh_coeffs = _ptr(sh_coeffs)
@@ -230,16 +251,21 @@ def _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offse
     s.log_scale_offset = float(log_scale_offset)
     s.sh_dtype = _lib.VS_SH_F16 if sh_coeffs.dtype == torch.float16 else _lib.VS_SH_F32
     s.min_scale = _ptr(min_scale)
+    s.decoder = _ptr(decoder)
     return s
 
 
 def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs: torch.Tensor,
            raw_opacities: torch.Tensor, background=(0.0, 0.0, 0.0), pass_: RasterPass = RasterPass.BACKWARD,
            render_mode: SplatRenderMode = SplatRenderMode.DEFAULT, log_scale_offset: float = 0.0,
-           validate: bool = False, min_scale: Optional[torch.Tensor] = None) -> RenderOutput:
-    """SplatOps::render.  `camera` is a Camera or ready-made vs_camera uniforms.
-    `render_mode` DEFAULT or MIP; `min_scale` [N] is the scale floor
-    (render's min_scale with has_min_scale), None for none.
+           validate: bool = False, min_scale: Optional[torch.Tensor] = None,
+           decoder: Optional[torch.Tensor] = None, neural_degree: int = 0) -> RenderOutput:
+    """SplatOps::render (SplatOps::render_neural with `decoder`).  `camera` is
+    a Camera or ready-made vs_camera uniforms.  `render_mode` DEFAULT or MIP;
+    `min_scale` [N] is the scale floor (render's min_scale with
+    has_min_scale), None for none.  With `decoder` [816] the colour comes from
+    the compact neural appearance: `sh_coeffs` holds [N,4,3] rows (base,
+    latent, pad) and `neural_degree` (0..3) is its direction band.
 
     Returns the image ([H,W,C] f32, or [H,W] int32-packed RGBA8 for
     FORWARD), the aux outputs and, for every pass but FORWARD, the state the
@@ -251,7 +277,8 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     transforms = transforms.contiguous()
     sh_coeffs = sh_coeffs.contiguous()
     raw_opacities = raw_opacities.contiguous()
-    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities)
+    decoder = _check_decoder(decoder, neural_degree)
+    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities, None if decoder is None else neural_degree)
     if validate:
         for name, t in (("transforms", transforms), ("sh_coeffs", sh_coeffs), ("raw_opacities", raw_opacities)):
             if not bool(torch.isfinite(t).all()):
@@ -276,7 +303,7 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     out.opacities = _ptr(opacities)
     out.tile_offsets = _ptr(tile_offsets)
     min_scale = _min_scale(min_scale, n)
-    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale, decoder)
     bg = (C.c_float * 3)(*[float(v) for v in background])
     st = C.c_void_p()
     _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg, int(pass_),
@@ -290,25 +317,31 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
 
 def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
                     raw_opacities: torch.Tensor, v_output: torch.Tensor, log_scale_offset: float = 0.0,
-                    fused: bool = False, min_scale: Optional[torch.Tensor] = None) -> SplatGrads:
-    """rasterize_bwd followed by project_bwd, returning dense gradients.
+                    fused: bool = False, min_scale: Optional[torch.Tensor] = None,
+                    decoder: Optional[torch.Tensor] = None) -> SplatGrads:
+    """rasterize_bwd followed by project_bwd (project_bwd_neural with
+    `decoder`, the forward's), returning dense gradients.
 
     With `fused` the backward stops at the raster gradients (the
     BackwardFusedUpdate pass): only `v_combined` is filled, for
-    project_update; the other fields are None."""
+    project_update; the other fields are None.  In neural mode `v_coeffs`
+    holds the [N,4,3] row gradients, and `v_decoder` [816] and `v_coeffs_sq`
+    [N] are filled."""
     if output.state is None or output.state.handle is None:
         raise ValueError("the forward pass kept no backward state (use a bwd-info pass)")
     transforms = transforms.contiguous()
     sh_coeffs = sh_coeffs.contiguous()
     raw_opacities = raw_opacities.contiguous()
-    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities)
+    decoder = _check_decoder(decoder, output.state.sh_degree if decoder is not None else 0)
+    n, degree = _check_splats(transforms, sh_coeffs, raw_opacities,
+                              None if decoder is None else output.state.sh_degree)
     v_output = v_output.contiguous()
     if v_output.shape != output.out_img.shape or v_output.dtype != torch.float32:
         raise ValueError(f"v_output must be float32 {tuple(output.out_img.shape)}, got {tuple(v_output.shape)}")
     dev = transforms.device
     ctx = output.state.ctx
     Context.get(dev)
-    k = (degree + 1) ** 2
+    k = 4 if decoder is not None else (degree + 1) ** 2
     if fused:
         g = SplatGrads(None, None, None, None, torch.empty((n, 10), dtype=torch.float32, device=dev))
     else:
@@ -317,13 +350,19 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
                        torch.empty(n, dtype=torch.float32, device=dev),
                        torch.empty(n, dtype=torch.float32, device=dev),
                        torch.empty((n, 10), dtype=torch.float32, device=dev))
+        if decoder is not None:
+            g.v_decoder = torch.empty(NEURAL_DECODER_LEN, dtype=torch.float32, device=dev)
+            g.v_coeffs_sq = torch.empty(n, dtype=torch.float32, device=dev)
     grads = _lib.VsGrads()
     grads.v_transforms = _ptr(g.v_transforms)
     grads.v_sh_coeffs = _ptr(g.v_coeffs)
     grads.v_raw_opacities = _ptr(g.v_raw_opac)
     grads.v_refine_weight = _ptr(g.v_refine_weight)
     grads.v_combined = _ptr(g.v_combined)
-    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, _min_scale(min_scale, n))
+    grads.v_decoder = _ptr(g.v_decoder)
+    grads.v_coeffs_sq = _ptr(g.v_coeffs_sq)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, _min_scale(min_scale, n),
+                            decoder)
     _lib.check(ctx.lib.vs_render_backward(ctx.handle, output.state.handle, C.byref(splats), _ptr(output.out_img),
                                           _ptr(v_output), C.byref(grads)))
     return g
