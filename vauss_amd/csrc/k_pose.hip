@@ -6,8 +6,8 @@
 // [dA (row-major 3x3), db] of a splat whose position, conic or colour
 // gradients are not all zero (culled splats have none), zero otherwise; each
 // 256-splat block sums its rows (wave butterflies, then the four waves in
-// order) into one partial, and a single block sums the partials in f64, in
-// block order, so the result does not depend on scheduling.
+// order) into one partial, and a single block sums the partials in f64 in a
+// fixed order, so the result does not depend on scheduling.
 #include "vs_vjp.h"
 #include "vs_internal.h"
 
@@ -59,25 +59,23 @@ __global__ void __launch_bounds__(POSE_BLOCK) pose_bwd_kernel(PoseBwdArgs a) {
     }
 }
 
-// One block: column k of the [nblocks, 12] partials, strided over the lanes
-// and reduced in f64.
-__global__ void __launch_bounds__(POSE_BLOCK) pose_sum_kernel(const float* __restrict__ partials, uint32_t nblocks,
-                                                              float* __restrict__ out) {
-    __shared__ double s_w[POSE_BLOCK / 64];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    for (int k = 0; k < POSE_DIM; ++k) {
-        double v = 0.0;
-        for (uint32_t b = threadIdx.x; b < nblocks; b += POSE_BLOCK) v += (double)partials[(size_t)b * POSE_DIM + k];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane == 0) s_w[wave] = v;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double t = s_w[0];
-            for (int w = 1; w < POSE_BLOCK / 64; ++w) t += s_w[w];
-            out[k] = (float)t;
-        }
-        __syncthreads();
+// One block of 192 lanes: 16 lanes per component stride the [nblocks, 12]
+// partials in f64 (independent loads, so the pass is not one long chain),
+// then each component adds its 16 sums in a fixed order.
+constexpr int POSE_SUM_PARTS = 16;
+__global__ void __launch_bounds__(POSE_DIM * POSE_SUM_PARTS) pose_sum_kernel(const float* __restrict__ partials,
+                                                                            uint32_t nblocks, float* __restrict__ out) {
+    __shared__ double s_part[POSE_SUM_PARTS][POSE_DIM];
+    const uint32_t k = threadIdx.x % POSE_DIM, part = threadIdx.x / POSE_DIM;
+    double v = 0.0;
+#pragma unroll 8
+    for (uint32_t b = part; b < nblocks; b += POSE_SUM_PARTS) v += (double)partials[(size_t)b * POSE_DIM + k];
+    s_part[part][k] = v;
+    __syncthreads();
+    if (threadIdx.x < POSE_DIM) {
+        double t = s_part[0][k];
+        for (int p = 1; p < POSE_SUM_PARTS; ++p) t += s_part[p][k];
+        out[k] = (float)t;
     }
 }
 
@@ -110,7 +108,7 @@ hipError_t launch_pose_bwd(const PoseBwdArgs& a, hipStream_t s) {
         default: launch_pose_model<4>(a, grid, s); break;
         }
     }
-    pose_sum_kernel<<<1, POSE_BLOCK, 0, s>>>(a.partials, nb, a.v_pose);
+    pose_sum_kernel<<<1, POSE_DIM * POSE_SUM_PARTS, 0, s>>>(a.partials, nb, a.v_pose);
     return hipGetLastError();
 }
 
