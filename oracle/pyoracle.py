@@ -21,8 +21,10 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("ORACLE_LIB", HERE / "liboracle.so"))
 
 FLAG_BWD_INFO, FLAG_GEOMETRY, FLAG_SMOOTH_CUTOFF, FLAG_BRUTE_FORCE, FLAG_MIP = 1, 2, 4, 8, 16
+FLAG_SURFEL, FLAG_SURFACE = 32, 64
 (F_INTERSECT_COUNTS, F_MAX_RADIUS, F_OPACITIES, F_GLOBAL_FROM_COMPACT, F_DEPTHS, F_PROJECTED, F_AUX, F_ISECT_TILE,
- F_ISECT_GID, F_TILE_OFFSETS, F_TILE_OFFSETS_SHRUNK, F_VISIBLE, F_OUT_IMG) = range(13)
+ F_ISECT_GID, F_TILE_OFFSETS, F_TILE_OFFSETS_SHRUNK, F_VISIBLE, F_OUT_IMG, F_SURFEL_AUX) = range(14)
+SURFEL_GRADS = 17
 
 
 class OrCamera(C.Structure):
@@ -197,7 +199,7 @@ class OracleForward:
                   F_ISECT_TILE: ((i,), np.uint32), F_ISECT_GID: ((i,), np.uint32),
                   F_TILE_OFFSETS: ((inf.tile_bh, inf.tile_bw, 2), np.uint32),
                   F_TILE_OFFSETS_SHRUNK: ((inf.tile_bh, inf.tile_bw, 2), np.uint32),
-                  F_VISIBLE: ((n,), np.float32)}
+                  F_VISIBLE: ((n,), np.float32), F_SURFEL_AUX: ((v, 14), np.float32)}
         if field == F_OUT_IMG:
             if self.flags & FLAG_BWD_INFO:
                 shape, dt = (inf.img_h, inf.img_w, inf.out_channels), np.float32
@@ -205,8 +207,10 @@ class OracleForward:
                 shape, dt = (inf.img_h, inf.img_w), np.uint32
         else:
             shape, dt = shapes[field]
-        if field == F_AUX and not (self.flags & FLAG_GEOMETRY):
+        if field == F_AUX and (not (self.flags & FLAG_GEOMETRY) or self.flags & FLAG_SURFEL):
             return np.zeros((0, 4), np.float32)
+        if field == F_SURFEL_AUX and not (self.flags & FLAG_SURFEL):
+            return np.zeros((0, 14), np.float32)
         out = np.empty(shape, dt)
         if out.size:
             rc = load().or_fwd_get(self.handle, field, out.ctypes.data_as(C.c_void_p))
@@ -217,7 +221,7 @@ class OracleForward:
         n = self.num_splats
         k = self.coeffs_per_row
         v_out = np.ascontiguousarray(v_out, np.float32)
-        vc = np.zeros((n, 10), np.float32)
+        vc = np.zeros((n, SURFEL_GRADS if self.flags & FLAG_SURFEL else 10), np.float32)
         vt = np.zeros((n, 10), np.float32)
         vs = np.zeros((n, k, 3), np.float32)
         vo = np.zeros(n, np.float32)
@@ -255,7 +259,7 @@ class OracleForward:
         n = self.num_splats
         k = self.coeffs_per_row
         vc = np.ascontiguousarray(v_combined, np.float32)
-        assert vc.shape == (n, 10)
+        assert vc.shape == (n, SURFEL_GRADS if self.flags & FLAG_SURFEL else 10)
         vt = np.zeros((n, 10), np.float32)
         vs = np.zeros((n, k, 3), np.float32)
         vo = np.zeros(n, np.float32)

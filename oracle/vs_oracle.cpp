@@ -854,7 +854,79 @@ static V3 neural_color(const float* row, const float* W, V3 v, uint32_t deg) {
               fmax_(row[2] * SH_C0 + tanhf_c(a.o[2]) + 0.5f, 0.0f)};
 }
 
-struct RasterSplat { float x, y, A, B, C, opac, r, g, b, c00, c01, c11; uint32_t gid; float z, nx, ny, nz; };
+// ---- surfels (2DGS), kernels/helpers.rs:56-69,316-423 ---------------------------
+constexpr float SURFEL_NEAR = 0.01f;
+constexpr int SURFEL_AUX = 14;          // M rows (9), low-pass centre (2), normal (3)
+constexpr int SURFEL_GRADS = 17;        // M rows (9), normal (3), rgb (3), alpha, refine
+struct SurfelProj { V3 r0, r1, r2; float bin_x, bin_y; S2 bin_conic; bool valid; };
+
+// surfel_project (helpers.rs:331-412): M = K [s_u W R e0, s_v W R e1, p_c]
+// (rows r0..r2) and the screen ellipse covering the opacity cutoff footprint
+// u^2 + v^2 <= 2 power and the low-pass disk of radius sqrt(power).
+static SurfelProj surfel_project(V3 sc, Q4 q, V3 mc, const or_camera& u, float power) {
+    const M3 rot = mul_mat3(view_rot(u), quat_to_mat3(q));
+    const V3 a = scale(rot.c0, sc.x), b = scale(rot.c1, sc.y);
+    const V3 ka{u.fx * a.x + u.cx * a.z, u.fy * a.y + u.cy * a.z, a.z};
+    const V3 kb{u.fx * b.x + u.cx * b.z, u.fy * b.y + u.cy * b.z, b.z};
+    const V3 kc{u.fx * mc.x + u.cx * mc.z, u.fy * mc.y + u.cy * mc.z, mc.z};
+    SurfelProj p;
+    p.r0 = V3{ka.x, kb.x, kc.x};
+    p.r1 = V3{ka.y, kb.y, kc.y};
+    p.r2 = V3{ka.z, kb.z, kc.z};
+    const V3 r0 = p.r0, r1 = p.r1, r2 = p.r2;
+    const float k2 = 2.0f * power;
+    const float d00 = k2 * (r0.x * r0.x + r0.y * r0.y) - r0.z * r0.z;
+    const float d01 = k2 * (r0.x * r1.x + r0.y * r1.y) - r0.z * r1.z;
+    const float d11 = k2 * (r1.x * r1.x + r1.y * r1.y) - r1.z * r1.z;
+    const float d02 = k2 * (r0.x * r2.x + r0.y * r2.y) - r0.z * r2.z;
+    const float d12 = k2 * (r1.x * r2.x + r1.y * r2.y) - r1.z * r2.z;
+    const float d22 = k2 * (r2.x * r2.x + r2.y * r2.y) - r2.z * r2.z;
+    const float n = -d22;
+    const bool front = n > 1.0e-12f;                     // the ellipse lies in front of the camera
+    const float inv_n = front ? 1.0f / n : 0.0f;
+    const float x0 = -d02 * inv_n, y0 = -d12 * inv_n;
+    const float s00 = d00 * inv_n + x0 * x0, s01 = d01 * inv_n + x0 * y0, s11 = d11 * inv_n + y0 * y0;
+    const float r2f = fmax_(power, 0.0f);
+    const float half_tr = fmax_(0.5f * (s00 + s11), 1.0e-12f);
+    const float t = clampf(std::sqrt(half_tr / fmax_(r2f, 1.0e-12f)), 1.0e-3f, 1.0e3f);
+    const float ga = 1.0f + 1.0f / t, gb = (1.0f + t) * r2f;
+    const S2 grown{ga * s00 + gb, ga * s01, ga * s11 + gb};
+    const float det = grown.c00 * grown.c11 - grown.c01 * grown.c01;
+    const S2 inv = s2_inverse(grown);
+    p.bin_conic = S2{inv.c00 * k2, inv.c01 * k2, inv.c11 * k2};
+    p.bin_x = x0; p.bin_y = y0;
+    p.valid = front && det > 0.0f && is_finite(x0) && is_finite(y0) && s2_finite(p.bin_conic);
+    return p;
+}
+// surfel_normal (helpers.rs:414-419): the rotated local +Z, facing the camera.
+static V3 surfel_normal(Q4 q, V3 mc, const or_camera& u) {
+    const V3 n = mul_mat3(view_rot(u), quat_to_mat3(q)).c2;
+    return scale(n, dot(n, mc) > 0.0f ? -1.0f : 1.0f);
+}
+// The ray-plane sample of a pixel (rasterize.rs:267-301): (u, v), the
+// intersection depth z, the low-pass offsets and sigma = min(s3d, s2d) / 2;
+// false when the ray misses or meets the plane before the near limit.
+struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
+static SurfelHit surfel_hit(const float* a, float px, float py) {
+    SurfelHit h;
+    const float m20 = a[6], m21 = a[7], m22 = a[8];
+    h.hux = a[0] - px * m20; h.huy = a[1] - px * m21; h.huz = a[2] - px * m22;
+    h.hvx = a[3] - py * m20; h.hvy = a[4] - py * m21; h.hvz = a[5] - py * m22;
+    const float qx = h.huy * h.hvz - h.huz * h.hvy;
+    const float qy = h.huz * h.hvx - h.hux * h.hvz;
+    h.qz = h.hux * h.hvy - h.huy * h.hvx;
+    h.su = qx / h.qz;
+    h.sv = qy / h.qz;
+    h.s3d = h.su * h.su + h.sv * h.sv;
+    h.z = m20 * h.su + m21 * h.sv + m22;
+    h.dxs = px - a[9]; h.dys = py - a[10];
+    h.s2d = 2.0f * (h.dxs * h.dxs + h.dys * h.dys);
+    h.sigma = 0.5f * fmin_(h.s3d, h.s2d);
+    h.valid = is_finite(h.z) && h.z >= SURFEL_NEAR;
+    return h;
+}
+
+struct RasterSplat { float x, y, A, B, C, opac, r, g, b, c00, c01, c11; uint32_t gid; float z, nx, ny, nz; const float* surf; };
 
 } // namespace
 
@@ -877,7 +949,8 @@ struct or_fwd {
     std::vector<uint32_t> intersect_counts;
     std::vector<float> max_radius, opacities, visible;
     std::vector<uint32_t> global_from_compact;
-    std::vector<float> depths, projected, aux;
+    std::vector<float> depths, projected, aux, surf;   // surf: [V,14] surfel aux (M rows, centre, normal)
+    bool surfel = false;
     std::vector<uint32_t> isect_tile, isect_cid;   // sorted, sentinel-free prefix of length I
     std::vector<uint32_t> tile_offsets, tile_offsets_shrunk;
     std::vector<float> out_img;
@@ -909,7 +982,10 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
     f->bg[0] = bg[0]; f->bg[1] = bg[1]; f->bg[2] = bg[2];
     f->flags = flags;
     const bool bwd_info = flags & OR_FLAG_BWD_INFO;
-    const bool geometry = flags & OR_FLAG_GEOMETRY;
+    const bool surfel = flags & OR_FLAG_SURFEL;
+    // Surfel training renders always carry the geometry channels (render.rs:471-473).
+    const bool geometry = (flags & OR_FLAG_GEOMETRY) || (surfel && bwd_info);
+    const bool surf_crit = surfel && (flags & OR_FLAG_SURFACE);
     const bool smooth = flags & OR_FLAG_SMOOTH_CUTOFF;
     const bool brute = flags & OR_FLAG_BRUTE_FORCE;
     f->tbw = (W + TILE_W - 1) / TILE_W; f->tbh = (H + TILE_W - 1) / TILE_W; f->T = f->tbw * f->tbh;
@@ -930,6 +1006,7 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         f->decoder = f->decoder_copy.data();
     }
     f->mip = (flags & OR_FLAG_MIP) != 0;
+    f->surfel = surfel;
     const bool mip = f->mip;
 
     // ---- project_forward: cull + count, kernels/project_forward.rs:26-261 ----
@@ -945,7 +1022,7 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         const float* t = transforms + (size_t)g * 10;
         const V3 mean_c = world_to_cam(v3(t[0], t[1], t[2]), u);
         if (!(finite3(mean_c) && mean_c.z <= 1.0e10f)) continue;
-        if (u.model == OR_MODEL_PINHOLE) {             // the fisheye models cull by angle
+        if (u.model == OR_MODEL_PINHOLE || surfel) {   // the fisheye models cull by angle; surfels are pinhole
             if (mean_c.z < 0.01f) continue;
         } else {
             const float r = std::sqrt(mean_c.x * mean_c.x + mean_c.y * mean_c.y);
@@ -962,15 +1039,26 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
         const Q4 q = qnormalize(qu);
         const ScaleFloor fl = apply_scale_floor(sc, sigmoid(ro), f->min_scale, g);
         f->opacities[g] = fl.opac;
-        float filter_comp;
-        const S2 cov = compensate_cov2d(calc_cov2d(fl.scale, q, mean_c, u), mip, filter_comp);
-        const float opac = fl.opac * filter_comp;
-        if (!s2_finite(cov)) continue;
-        float mx, my;
-        project(mean_c, u, mx, my);
-        if (!(opac >= 1.0f / 255.0f)) continue;
-        const float power = logf_c(opac * 255.0f);
-        const S2 conic = s2_inverse(cov);
+        float mx, my, power;
+        S2 conic;
+        if (surfel) {
+            // project_forward.rs:128-147: bin by the ellipse covering the cutoff
+            // footprint and the low-pass disk; no 2-D blur compensation.
+            if (!(fl.opac >= 1.0f / 255.0f)) continue;
+            power = logf_c(fl.opac * 255.0f);
+            const SurfelProj sp = surfel_project(fl.scale, q, mean_c, u, power);
+            if (!sp.valid) continue;
+            conic = sp.bin_conic; mx = sp.bin_x; my = sp.bin_y;
+        } else {
+            float filter_comp;
+            const S2 cov = compensate_cov2d(calc_cov2d(fl.scale, q, mean_c, u), mip, filter_comp);
+            const float opac = fl.opac * filter_comp;
+            if (!s2_finite(cov)) continue;
+            project(mean_c, u, mx, my);
+            if (!(opac >= 1.0f / 255.0f)) continue;
+            power = logf_c(opac * 255.0f);
+            conic = s2_inverse(cov);
+        }
         float ex, ey;
         bbox_extent(conic, power, ex, ey);
         if (!(ex >= 0.0f && ey >= 0.0f)) continue;
@@ -1001,7 +1089,8 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
 
     // ---- project_visible, kernels/project_visible.rs:97-174 / 182-312 ----------
     f->projected.assign((size_t)V * 9, 0.0f);
-    if (geometry) f->aux.assign((size_t)V * 4, 0.0f);
+    if (geometry && !surfel) f->aux.assign((size_t)V * 4, 0.0f);
+    if (surfel) f->surf.assign((size_t)V * SURFEL_AUX, 0.0f);
     #pragma omp parallel for schedule(static) num_threads(nthreads)
     for (int64_t ci = 0; ci < (int64_t)V; ++ci) {
         const uint32_t c = (uint32_t)ci;
@@ -1030,6 +1119,20 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
             col = splat_color(sh + (size_t)g * K * 3, degree, mean, u);
         }
         float* row = &f->projected[(size_t)c * 9];
+        if (surfel) {
+            // project_visible.rs:231-273: the row carries the binning ellipse and
+            // the floored opacity; the coverage reads the aux row.
+            const SurfelProj sp = surfel_project(fl.scale, q, mean_c, u, logf_c(fl.opac * 255.0f));
+            const V3 nrm = surfel_normal(q, mean_c, u);
+            float* a = &f->surf[(size_t)c * SURFEL_AUX];
+            a[0] = sp.r0.x; a[1] = sp.r0.y; a[2] = sp.r0.z; a[3] = sp.r1.x; a[4] = sp.r1.y; a[5] = sp.r1.z;
+            a[6] = sp.r2.x; a[7] = sp.r2.y; a[8] = sp.r2.z;
+            project_pinhole(mean_c, u, a[9], a[10]);
+            a[11] = nrm.x; a[12] = nrm.y; a[13] = nrm.z;
+            row[0] = sp.bin_x; row[1] = sp.bin_y; row[2] = sp.bin_conic.c00; row[3] = sp.bin_conic.c01;
+            row[4] = sp.bin_conic.c11; row[5] = fl.opac; row[6] = col.x; row[7] = col.y; row[8] = col.z;
+            continue;
+        }
         row[0] = mx; row[1] = my; row[2] = conic.c00; row[3] = conic.c01; row[4] = conic.c11;
         row[5] = opac; row[6] = col.x; row[7] = col.y; row[8] = col.z;
         if (geometry) {
@@ -1132,7 +1235,9 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
             s.A = 0.5f * row[2]; s.B = row[3]; s.C = 0.5f * row[4];
             s.opac = row[5]; s.r = row[6]; s.g = row[7]; s.b = row[8];
             s.gid = f->global_from_compact[c];
-            if (geometry) { const float* a = &f->aux[(size_t)c * 4]; s.z = a[0]; s.nx = a[1]; s.ny = a[2]; s.nz = a[3]; }
+            s.surf = surfel ? &f->surf[(size_t)c * SURFEL_AUX] : nullptr;
+            if (surfel) { s.z = 0.0f; s.nx = s.surf[11]; s.ny = s.surf[12]; s.nz = s.surf[13]; }
+            else if (geometry) { const float* a = &f->aux[(size_t)c * 4]; s.z = a[0]; s.nx = a[1]; s.ny = a[2]; s.nz = a[3]; }
             else { s.z = s.nx = s.ny = s.nz = 0.0f; }
             list[i - lo] = s;
         }
@@ -1145,11 +1250,21 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
                 float depth_acc = 0.0f, median = 0.0f, dist_b = 0.0f, dist_c = 0.0f, nx = 0.0f, ny = 0.0f, nz = 0.0f;
                 uint32_t median_id = 0xFFFFFFFFu;
                 uint32_t last_useful = lo;
+                float surf_o = 0.0f;
+                bool surf_found = false;
                 for (uint32_t i = lo; i < hi; ++i) {
                     const RasterSplat& s = list[i - lo];
                     ++evals_total;
-                    const float dx = pcx - s.x, dy = pcy - s.y;
-                    const float sigma = std::fma(std::fma(s.A, dx, s.B * dy), dx, (s.C * dy) * dy);
+                    float sigma, z = s.z;
+                    if (surfel) {
+                        const SurfelHit hit = surfel_hit(s.surf, pcx, pcy);
+                        if (!hit.valid) continue;          // no intersection in front of the near limit
+                        sigma = hit.sigma;
+                        z = hit.z;
+                    } else {
+                        const float dx = pcx - s.x, dy = pcy - s.y;
+                        sigma = std::fma(std::fma(s.A, dx, s.B * dy), dx, (s.C * dy) * dy);
+                    }
                     const float G = expf_c(-sigma);
                     const float alpha = fmin_(0.999f, s.opac * G);
                     const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
@@ -1163,9 +1278,17 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
                     cg = std::fma(fmax_(s.g, 0.0f), vis, cg);
                     cb = std::fma(fmax_(s.b, 0.0f), vis, cb);
                     if (geometry) {
-                        depth_acc = std::fma(s.z, vis, depth_acc);
-                        if (T > 0.5f) { median = s.z; median_id = i; }
-                        const float m = dist_depth(s.z);
+                        depth_acc = std::fma(z, vis, depth_acc);
+                        if (surf_crit) {
+                            // unbiased-depth surface criterion (rasterize.rs:346-354)
+                            surf_o += alpha_eff + 0.1f * G;
+                            if (!surf_found && (surf_o > 0.6f || T > 0.5f)) {
+                                median = z; median_id = i; surf_found = surf_o > 0.6f;
+                            }
+                        } else if (T > 0.5f) {
+                            median = z; median_id = i;
+                        }
+                        const float m = dist_depth(z);
                         dist_b = std::fma(m, vis, dist_b);
                         dist_c = std::fma(m * m, vis, dist_c);
                         nx = std::fma(s.nx, vis, nx);
@@ -1235,6 +1358,7 @@ extern "C" int or_fwd_get(const or_fwd* f, int field, void* dst) {
     case OR_F_TILE_OFFSETS_SHRUNK: return cp(f->tile_offsets_shrunk);
     case OR_F_VISIBLE: return cp(f->visible);
     case OR_F_OUT_IMG: return (f->flags & OR_FLAG_BWD_INFO) ? cp(f->out_img) : cp(f->out_packed);
+    case OR_F_SURFEL_AUX: return cp(f->surf);
     default: return 1;
     }
 }
@@ -1260,7 +1384,8 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
         const uint32_t lo = f->tile_offsets_shrunk[(size_t)t * 2], hi = f->tile_offsets_shrunk[(size_t)t * 2 + 1];
         row_of[t + 1] = row_of[t] + (hi > lo ? hi - lo : 0);
     }
-    std::vector<double> part((size_t)row_of[f->T] * 10, 0.0);
+    const int NG = f->surfel ? SURFEL_GRADS : 10;     // gradient components per splat
+    std::vector<double> part((size_t)row_of[f->T] * NG, 0.0);
     const float img_w = (float)W, img_h = (float)H;
 
     // ---- raster VJP, bwd/kernels/rasterize_backwards_planes.rs:112-682 ----------
@@ -1284,6 +1409,81 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
                 const float v_t = (v_out[base + 3] - (f->bg[0] * vr + f->bg[1] * vg + f->bg[2] * vb)) * t_final;
                 const float refine_scale = 1.0f / fmax_(final_a, 1.0e-5f);
                 const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+                if (f->surfel) {
+                    // rasterize_backwards_planes.rs:266-480: the surfel replay, with the
+                    // geometry channels composited like colours without a background.
+                    double sz = f->out_img[base + 4], snx = f->out_img[base + 6], sny = f->out_img[base + 7];
+                    double snz = f->out_img[base + 8], sdb = f->out_img[base + 9], sdc = f->out_img[base + 10];
+                    double srd = sr, sgd = sg, sbd = sb;
+                    const uint32_t med_id = f2u(f->out_img[base + 11]);
+                    const double vz = v_out[base + 4], vmed = v_out[base + 5], vnx = v_out[base + 6];
+                    const double vny = v_out[base + 7], vnz = v_out[base + 8], vdb = v_out[base + 9], vdc = v_out[base + 10];
+                    for (uint32_t i = lo; i < hi && T > 1.0e-4f; ++i) {
+                        const uint32_t c = f->isect_cid[i];
+                        const float* row = &f->projected[(size_t)c * 9];
+                        const float* a = &f->surf[(size_t)c * SURFEL_AUX];
+                        const float opac = row[5], cr = row[6], cgc = row[7], cbc = row[8];
+                        const SurfelHit h = surfel_hit(a, pcx, pcy);
+                        if (!h.valid) continue;
+                        const float sigma = h.sigma;
+                        const float G = expf_c(-sigma);
+                        const float alpha = fmin_(0.999f, opac * G);
+                        const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
+                        if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
+                        const float alpha_eff = alpha * w_cut;
+                        const float next_t = T * (1.0f - alpha_eff);
+                        if (next_t <= 1.0e-4f) { T = 0.0f; break; }
+                        const float vis = alpha_eff * T;
+                        double* p = &part[(size_t)(row_of[tile] + (i - lo)) * NG];
+                        const double clr = fmax_(cr, 0.0f), clg = fmax_(cgc, 0.0f), clb = fmax_(cbc, 0.0f);
+                        const double z = h.z, nx = a[11], ny = a[12], nz = a[13];
+                        const double m = dist_depth(h.z);
+                        const double dm_dz = (h.z > DIST_NEAR) ? (double)DIST_FAR / (DIST_FAR - DIST_NEAR) * DIST_NEAR / (z * z) : 0.0;
+                        if (cr >= 0.0f) p[12] += (double)vis * vr;
+                        if (cgc >= 0.0f) p[13] += (double)vis * vg;
+                        if (cbc >= 0.0f) p[14] += (double)vis * vb;
+                        p[9] += vis * vnx; p[10] += vis * vny; p[11] += vis * vnz;
+                        const double Td = T;
+                        const double ra = 1.0 / (1.0 - (double)alpha_eff);
+                        const double dot = ((Td * clr - srd) * vr + (Td * clg - sgd) * vg + (Td * clb - sbd) * vb +
+                                            (Td * z - sz) * vz + (Td * nx - snx) * vnx + (Td * ny - sny) * vny +
+                                            (Td * nz - snz) * vnz + (Td * m - sdb) * vdb + (Td * m * m - sdc) * vdc) * ra;
+                        const double v_alpha_eff = dot + (double)v_t * ra;
+                        const double v_alpha = smooth ? v_alpha_eff * ((double)w_cut + (double)alpha * alpha_cutoff_weight_deriv(alpha)) : v_alpha_eff;
+                        const double v_z = (double)vis * (vz + (vdb + 2.0 * m * vdc) * dm_dz) + (i == med_id ? vmed : 0.0);
+                        const bool unsat = opac * G <= 0.999f;
+                        const double v_sigma = unsat ? -(double)alpha * v_alpha : 0.0;
+                        if (unsat) p[15] += v_alpha * (double)G;
+                        const bool use_3d = h.s3d <= h.s2d;
+                        const double su = h.su, sv = h.sv;
+                        const double v_su = (use_3d ? v_sigma * su : 0.0) + v_z * a[6];
+                        const double v_sv = (use_3d ? v_sigma * sv : 0.0) + v_z * a[7];
+                        const double v_cx = use_3d ? 0.0 : -2.0 * v_sigma * h.dxs;
+                        const double v_cy = use_3d ? 0.0 : -2.0 * v_sigma * h.dys;
+                        const double inv_qz = 1.0 / (double)h.qz;
+                        const double vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * su + v_sv * sv) * inv_qz;
+                        // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
+                        const double vhux = h.hvy * vqz - h.hvz * vqy, vhuy = h.hvz * vqx - h.hvx * vqz, vhuz = h.hvx * vqy - h.hvy * vqx;
+                        const double vhvx = vqy * h.huz - vqz * h.huy, vhvy = vqz * h.hux - vqx * h.huz, vhvz = vqx * h.huy - vqy * h.hux;
+                        const double inv_r2z = 1.0 / (double)a[8];
+                        const double g0 = vhux, g1 = vhuy, g2 = vhuz + v_cx * inv_r2z;
+                        const double g3 = vhvx, g4 = vhvy, g5 = vhvz + v_cy * inv_r2z;
+                        const double g6 = v_z * su - pcx * vhux - pcy * vhvx;
+                        const double g7 = v_z * sv - pcx * vhuy - pcy * vhvy;
+                        const double g8 = v_z - pcx * vhuz - pcy * vhvz - (v_cx * a[9] + v_cy * a[10]) * inv_r2z;
+                        p[0] += g0; p[1] += g1; p[2] += g2; p[3] += g3; p[4] += g4; p[5] += g5;
+                        p[6] += g6; p[7] += g7; p[8] += g8;
+                        // refine weight: the gradient of a screen-space shift of the surfel (M -> T M)
+                        const double shx = g0 * a[6] + g1 * a[7] + g2 * a[8];
+                        const double shy = g3 * a[6] + g4 * a[7] + g5 * a[8];
+                        p[16] += std::sqrt(shx * img_w * shx * img_w + shy * img_h * shy * img_h) * (double)refine_scale;
+                        srd -= vis * clr; sgd -= vis * clg; sbd -= vis * clb;
+                        sz -= vis * z; snx -= vis * nx; sny -= vis * ny; snz -= vis * nz;
+                        sdb -= vis * m; sdc -= vis * m * m;
+                        T = next_t;
+                    }
+                    continue;
+                }
                 for (uint32_t i = lo; i < hi && T > 1.0e-4f; ++i) {
                     const float* row = &f->projected[(size_t)f->isect_cid[i] * 9];
                     const float x = row[0], y = row[1], c00 = row[2], c01 = row[3], c11 = row[4];
@@ -1298,7 +1498,7 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
                     const float next_t = T * (1.0f - alpha_eff);
                     if (next_t <= 1.0e-4f) { T = 0.0f; break; }
                     const float vis = alpha_eff * T;
-                    double* p = &part[(size_t)(row_of[tile] + (i - lo)) * 10];
+                    double* p = &part[(size_t)(row_of[tile] + (i - lo)) * NG];
                     const float clr = fmax_(cr, 0.0f), clg = fmax_(cgc, 0.0f), clb = fmax_(cbc, 0.0f);
                     if (cr >= 0.0f) p[5] += (double)vis * vr;
                     if (cgc >= 0.0f) p[6] += (double)vis * vg;
@@ -1329,17 +1529,17 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
         }
     }
     // Per-splat sums in sorted-intersection order.
-    std::vector<double> vc((size_t)N * 10, 0.0);
+    std::vector<double> vc((size_t)N * NG, 0.0);
     for (uint32_t t = 0; t < f->T; ++t) {
         const uint32_t lo = f->tile_offsets_shrunk[(size_t)t * 2], hi = f->tile_offsets_shrunk[(size_t)t * 2 + 1];
         for (uint32_t i = lo; i < hi; ++i) {
             const uint32_t g = f->global_from_compact[f->isect_cid[i]];
-            const double* p = &part[(size_t)(row_of[t] + (i - lo)) * 10];
-            for (int k = 0; k < 10; ++k) vc[(size_t)g * 10 + k] += p[k];
+            const double* p = &part[(size_t)(row_of[t] + (i - lo)) * NG];
+            for (int k = 0; k < NG; ++k) vc[(size_t)g * NG + k] += p[k];
         }
     }
-    std::vector<float> vcf((size_t)N * 10);
-    for (size_t i = 0; i < (size_t)N * 10; ++i) vcf[i] = (float)vc[i];
+    std::vector<float> vcf((size_t)N * NG);
+    for (size_t i = 0; i < (size_t)N * NG; ++i) vcf[i] = (float)vc[i];
     if (v_combined_out) std::memcpy(v_combined_out, vcf.data(), sizeof(float) * vcf.size());
     return project_vjp(f, vcf.data(), nthreads, v_transforms, v_sh, v_raw_opac, v_refine);
 }
@@ -1401,6 +1601,60 @@ static SplatVjp splat_vjp(const or_fwd* f, uint32_t g, const float* t, float raw
     return r;
 }
 
+// surfel_backwards (project_backwards.rs:426-570) of global splat g from its
+// 17 raster gradients [M rows (9), normal (3), rgb (3), alpha, refine]:
+// M = K [s_u W R e0, s_v W R e1, W p + t], n = +-W R e2.
+static void surfel_vjp(const or_fwd* f, uint32_t g, const float* rg, float* v_transforms, float* v_sh,
+                       float* v_raw_opac, float* v_refine) {
+    const or_camera& u = f->cam;
+    const uint32_t K = f->K, degree = f->degree;
+    const float* t = f->transforms + (size_t)g * 10;
+    const float* cb = f->sh + (size_t)g * K * 3;
+    const V3 mean = v3(t[0], t[1], t[2]);
+    const V3 sc_raw = v3(expf_c(t[7] + f->lso), expf_c(t[8] + f->lso), expf_c(t[9] + f->lso));
+    const Q4 qu{t[3], t[4], t[5], t[6]};
+    const Q4 q = qnormalize(qu);
+    const float opac_sig = sigmoid(f->raw_opac[g]);
+    const ScaleFloor fl = apply_scale_floor(sc_raw, opac_sig, f->min_scale, g);
+    const V3 sc = fl.scale;
+    const V3 vc0{rg[0], rg[3], rg[6]}, vc1{rg[1], rg[4], rg[7]}, vc2{rg[2], rg[5], rg[8]};
+    const V3 v_n{rg[9], rg[10], rg[11]}, v_color{rg[12], rg[13], rg[14]};
+    const V3 u_world = sub(mean, V3{u.cam_pos[0], u.cam_pos[1], u.cam_pos[2]});
+    const float u_len = length(u_world);
+    const V3 vdir = scale(u_world, 1.0f / u_len);
+    if (v_sh) {
+        float Y[25];
+        const int n = sh_basis(degree, vdir, Y);
+        float* o = v_sh + (size_t)g * K * 3;
+        for (int k = 0; k < n; ++k) { o[3 * k] = v_color.x * Y[k]; o[3 * k + 1] = v_color.y * Y[k]; o[3 * k + 2] = v_color.z * Y[k]; }
+    }
+    const V3 v_v_sh = sh_viewdir_vjp(cb, degree, vdir, v_color);
+    const V3 v_mean_sh = scale(sub(v_v_sh, scale(vdir, dot(vdir, v_v_sh))), 1.0f / u_len);
+    const float v_opac_base = fl.opac_open ? rg[15] : 0.0f;         // no 2-D blur compensation
+    if (v_raw_opac) v_raw_opac[g] = v_opac_base * fl.coef * opac_sig * (1.0f - opac_sig);
+    if (v_refine) v_refine[g] = clampf(is_finite(rg[16]) ? rg[16] : 0.0f, 0.0f, 1.0e32f);
+    // M = K X  =>  v_X = K^T v_M, column by column
+    const V3 v_a{u.fx * vc0.x, u.fy * vc0.y, u.cx * vc0.x + u.cy * vc0.y + vc0.z};
+    const V3 v_b{u.fx * vc1.x, u.fy * vc1.y, u.cx * vc1.x + u.cy * vc1.y + vc1.z};
+    const V3 v_c{u.fx * vc2.x, u.fy * vc2.y, u.cx * vc2.x + u.cy * vc2.y + vc2.z};
+    const M3 W = view_rot(u);
+    const M3 wr = mul_mat3(W, quat_to_mat3(q));
+    const V3 mean_c = world_to_cam(mean, u);
+    const float v_su = dot(wr.c0, v_a), v_sv = dot(wr.c1, v_b);
+    const float flip = dot(wr.c2, mean_c) > 0.0f ? -1.0f : 1.0f;
+    const M3 v_r{scale(tmul_vec3(W, v_a), sc.x), scale(tmul_vec3(W, v_b), sc.y), scale(tmul_vec3(W, v_n), flip)};
+    const Q4 v_q = apply_normalize_vjp(qu, quat_to_mat_vjp(q, v_r));
+    const V3 v_mean = add(tmul_vec3(W, v_c), v_mean_sh);
+    if (v_transforms) {
+        float* o = v_transforms + (size_t)g * 10;
+        o[0] = v_mean.x; o[1] = v_mean.y; o[2] = v_mean.z;
+        o[3] = v_q.w; o[4] = v_q.x; o[5] = v_q.y; o[6] = v_q.z;
+        o[7] = v_su * sc.x * fl.ratio_sq.x + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.x);
+        o[8] = v_sv * sc.y * fl.ratio_sq.y + v_opac_base * fl.opac * (1.0f - fl.ratio_sq.y);
+        o[9] = v_opac_base * fl.opac * (1.0f - fl.ratio_sq.z);
+    }
+}
+
 // Dense per-splat gradients from the raster VJP's v_combined [N,10]; rows of
 // splats that were culled, or whose v_combined row is all zero, stay zero
 // (bwd/kernels/project_backwards.rs:311-382).
@@ -1415,6 +1669,13 @@ static int project_vjp(const or_fwd* f, const float* vcf, int nthreads, float* v
     #pragma omp parallel for schedule(static) num_threads(nthreads)
     for (int64_t ci = 0; ci < (int64_t)f->V; ++ci) {
         const uint32_t g = f->global_from_compact[(size_t)ci];
+        if (f->surfel) {
+            const float* rs = vcf + (size_t)g * SURFEL_GRADS;
+            bool any_s = false;
+            for (int k = 0; k < SURFEL_GRADS; ++k) any_s = any_s || rs[k] != 0.0f;
+            if (any_s) surfel_vjp(f, g, rs, v_transforms, v_sh, v_raw_opac, v_refine);
+            continue;
+        }
         float rg[10];
         bool any = false;
         for (int k = 0; k < 10; ++k) { rg[k] = vcf[(size_t)g * 10 + k]; any = any || rg[k] != 0.0f; }

@@ -43,6 +43,9 @@ enum {
     OR_FLAG_BRUTE_FORCE = 8,    /* composite every pixel over the whole depth-sorted
                                    visible list instead of its tile's list (checks binning) */
     OR_FLAG_MIP = 16,           /* SplatRenderMode::Mip: 0.1 blur with opacity compensation */
+    OR_FLAG_SURFEL = 32,        /* SplatRenderMode::Surfel (2DGS, pinhole): ray-plane coverage; with
+                                   BWD_INFO the image carries the 12 geometry channels */
+    OR_FLAG_SURFACE = 64,       /* surfels outside training: median by the surface criterion */
 };
 
 typedef struct or_fwd or_fwd;
@@ -78,6 +81,7 @@ enum {
     OR_F_TILE_OFFSETS_SHRUNK = 10, /* u32 [T,2] after it */
     OR_F_VISIBLE = 11,          /* f32 [N] */
     OR_F_OUT_IMG = 12,          /* f32 [H,W,C] (C=4 or 12) or u32 [H,W] packed */
+    OR_F_SURFEL_AUX = 13,       /* f32 [V,14] surfels: M rows (9), low-pass centre (2), normal (3) */
 };
 int or_fwd_get(const or_fwd* f, int field, void* dst);
 void or_fwd_free(or_fwd* f);
