@@ -153,9 +153,29 @@ def measure_next_rows(va, wl, cam, t, s, o, gt, dev, reps: int = 10) -> dict:
         neural_step()
     st_ms = ctx.stage_times()
     ctx.enable_timing(False)
+
+    # surfels (SplatRenderMode::Surfel): the same view and splats as 2DGS
+    # disks, 12-channel training render, L1 cotangent on the colour, the
+    # 17-component raster backward and the surfel projection VJP.
+    def surfel_step():
+        o3 = va.render(cam, wl.img_size, t, s, o, pass_=va.RasterPass.BACKWARD, render_mode=va.SplatRenderMode.SURFEL)
+        v3 = va.l1_cotangent(o3.out_img, gt, (0.0, 0.0), 0.0)
+        va.render_backward(o3, t, s, o, v3)
+        o3.state.free()
+    sf_ms = timed(surfel_step)
+    ctx.enable_timing(True, stages=["raster_fwd", "raster_bwd", "project_bwd"])
+    ctx.stage_times()
+    for _ in range(reps):
+        surfel_step()
+    sf_st = ctx.stage_times()
+    ctx.enable_timing(False)
     return {"neural_appearance": {"view_ms": round(n_ms, 4), "band": 3,
                                   "project_ms": round(st_ms["project_ms"] / reps, 4),
                                   "project_bwd_with_neural_ms": round(st_ms["project_bwd_ms"] / reps, 4)},
+            "surfel": {"view_ms": round(sf_ms, 4), "channels": 12,
+                       "raster_fwd_ms": round(sf_st["raster_fwd_ms"] / reps, 4),
+                       "raster_bwd_ms": round(sf_st["raster_bwd_ms"] / reps, 4),
+                       "project_bwd_ms": round(sf_st["project_bwd_ms"] / reps, 4)},
             "image_loss_l1_ssim": {"img": [w, h], "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
                                    "fwd_alg_GBs": round(56 * px / (f_ms * 1e-3) / 1e9, 1),
                                    "bwd_alg_GBs": round(72 * px / (b_ms * 1e-3) / 1e9, 1)},

@@ -109,9 +109,17 @@ typedef enum vs_pass {
     VS_PASS_GEOMETRY = 4,           /* float [H,W,12]: RGBA, sum(w z), median z, normal, distortion, median id */
 } vs_pass;
 
-/* SplatRenderMode, gaussian_splats.rs:19-26.  DEFAULT (+0.3 2-D blur) and MIP
- * (+0.1 blur with opacity compensation, kernels/helpers.rs:227-245) are
- * built; SURFEL returns VS_ERR_UNSUPPORTED. */
+/* SplatRenderMode, gaussian_splats.rs:19-26: DEFAULT (+0.3 2-D blur), MIP
+ * (+0.1 blur with opacity compensation, kernels/helpers.rs:227-245) and
+ * SURFEL (2DGS: each splat is the disk of its first two scaled axes, covered
+ * by the pixel ray's intersection with its plane and a screen-space low-pass,
+ * kernels/helpers.rs:316-423, kernels/rasterize.rs:267-301).  Surfels are
+ * pinhole-only (a lens camera renders as the pinhole with its focal length)
+ * and take SH colour; every pass but FORWARD writes the 12 geometry channels
+ * (RGBA, sum(w z), median z, normal, distortion moments, median id; the
+ * median by the surface criterion except in VS_PASS_BACKWARD), and the
+ * backward's v_combined rows have 17 components [M rows (9), normal (3),
+ * rgb (3), alpha, refine]. */
 typedef enum vs_render_mode { VS_MODE_DEFAULT = 0, VS_MODE_MIP = 1, VS_MODE_SURFEL = 2 } vs_render_mode;
 
 /* Forward outputs (RenderAux, crates/splat-train-render/src/render_aux.rs:74-100).
@@ -133,7 +141,7 @@ typedef struct vs_grads {
     float* v_sh_coeffs;             /* [N,(d+1)^2,3], or the neural rows [N,4,3] */
     float* v_raw_opacities;         /* [N] */
     float* v_refine_weight;         /* [N] screen-space refine weight, clamped [0,1e32] */
-    float* v_combined;              /* [N,10] raster gradient rows (xy, conic, rgb, alpha, refine) */
+    float* v_combined;              /* [N,10] raster gradient rows (xy, conic, rgb, alpha, refine); surfels [N,17] */
     float* v_decoder;               /* [816] neural appearance: decoder gradient summed over splats */
     float* v_coeffs_sq;             /* [N] neural appearance: mean square of each row's gradient */
 } vs_grads;
@@ -243,6 +251,8 @@ typedef struct vs_state_view {
     const float* proj_b;            /* [N] b */
     const float* proj_aux;          /* [N,4] z, nx, ny, nz (GEOMETRY) or NULL */
     const uint32_t* tile_ranges;    /* [T,2] before the forward shrank the ends */
+    const float* proj_surf;         /* [N,16] surfels: M rows (9), low-pass centre (2), normal (3), 2 pad;
+                                       else NULL */
 } vs_state_view;
 vs_status vs_fwd_state_view(const vs_fwd_state* state, vs_state_view* out);
 

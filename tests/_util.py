@@ -71,4 +71,5 @@ def gpu_state_arrays(out):
         "proj_c": dev_to_numpy(v.proj_b, (n,), np.float32),
         "proj_aux": dev_to_numpy(v.proj_aux, (n, 4), np.float32) if v.proj_aux else None,
         "ranges": dev_to_numpy(v.tile_ranges, (v.tile_bh, v.tile_bw, 2), np.uint32),
+        "proj_surf": dev_to_numpy(v.proj_surf, (n, 16), np.float32) if v.proj_surf else None,
     }

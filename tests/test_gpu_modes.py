@@ -71,8 +71,8 @@ def test_mode_errors():
     w = scenes.workload("c1", 500)
     cam = w.cameras[0].uniforms(w.img_size)
     t, s, o = to_gpu(w.scene)
-    with pytest.raises(va.VsError):
-        va.render(cam, w.img_size, t, s, o, render_mode=va.SplatRenderMode.SURFEL)
+    with pytest.raises(ValueError):                 # not a SplatRenderMode
+        va.render(cam, w.img_size, t, s, o, render_mode=7)
     out = va.render(cam, w.img_size, t, s, o, min_scale=torch.full((500,), 0.01, device="cuda"))
     v = torch.zeros_like(out.out_img)
     with pytest.raises(va.VsError):                 # the backward must see the forward's floor

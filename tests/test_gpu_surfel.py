@@ -1,0 +1,149 @@
+"""GPU parity of the surfel (2DGS) render mode (kernels/helpers.rs:316-423,
+kernels/rasterize.rs:267-301, bwd/kernels/rasterize_backwards_planes.rs:266-480,
+bwd/kernels/project_backwards.rs:426-570) against the CPU oracle: counts, key
+order, projected rows and the surfel rows (M, low-pass centre, normal) bit for
+bit; the 12-channel image (colour, alpha, depth, normal and the median channels
+under the training rule or the surface criterion) bit for bit in every float
+pass and the packed pass; the 17 raster gradient components and the parameter
+gradients at the contract bar (1e-3 relative / 1e-5 absolute), the projection
+stage on its own against the oracle's VJP of the GPU's raster gradients; and
+the entry points that reject surfels."""
+import numpy as np
+import pytest
+import torch
+
+import vauss_amd as va
+from oracle import pyoracle as po
+from tests._util import circle_mask, gpu_state_arrays, l1_cotangent_np, to_gpu
+from tests.test_gpu_parity import _check_forward, _check_grads, ill_conditioned_rows
+from vauss_amd import scenes
+
+pytestmark = pytest.mark.gpu
+
+SURFEL = va.SplatRenderMode.SURFEL
+
+
+def _flags(pass_):
+    f = po.FLAG_SURFEL
+    if pass_.bwd_info():
+        f |= po.FLAG_BWD_INFO
+    if pass_ == va.RasterPass.GEOMETRY:
+        f |= po.FLAG_GEOMETRY
+    if pass_ == va.RasterPass.BACKWARD_SMOOTH_CUTOFF:
+        f |= po.FLAG_SMOOTH_CUTOFF
+    if pass_ != va.RasterPass.BACKWARD:          # every pass but the training one takes the surface criterion
+        f |= po.FLAG_SURFACE
+    return f
+
+
+def _surfel_both(cfg, n, view, pass_=va.RasterPass.BACKWARD):
+    w = scenes.workload(cfg, n)
+    cam = w.cameras[view].uniforms(w.img_size)
+    t, s, o = to_gpu(w.scene)
+    print(f"[case] surfel {cfg} n={w.scene.num_splats} view={view} pass={pass_.name}", flush=True)
+    out = va.render(cam, w.img_size, t, s, o, pass_=pass_, render_mode=SURFEL)
+    ref = po.render_forward(cam, w.img_size, w.scene.transforms, w.scene.sh_coeffs, w.scene.raw_opacities,
+                            flags=_flags(pass_))
+    return w, (t, s, o), out, ref
+
+
+def _check_surfel_rows(out, ref):
+    gpu = gpu_state_arrays(out)
+    _check_forward(out, ref, gpu)
+    gfc = ref.get(po.F_GLOBAL_FROM_COMPACT)
+    rows = gpu["proj_surf"][gfc, :14]
+    np.testing.assert_array_equal(rows.view(np.uint32), ref.get(po.F_SURFEL_AUX).view(np.uint32))
+
+
+PASSES = [va.RasterPass.BACKWARD, va.RasterPass.FLOAT, va.RasterPass.GEOMETRY, va.RasterPass.BACKWARD_SMOOTH_CUTOFF]
+
+
+@pytest.mark.parametrize("pass_", PASSES, ids=[p.name for p in PASSES])
+def test_surfel_forward_passes(pass_):
+    w, _, out, ref = _surfel_both("c1", None, 0, pass_)
+    _check_surfel_rows(out, ref)
+    img = out.out_img.cpu().numpy()
+    rimg = ref.get(po.F_OUT_IMG)
+    assert img.shape == rimg.shape == (256, 256, 12)
+    assert np.abs(img[..., :11] - rimg[..., :11]).max() <= 1e-4
+    np.testing.assert_array_equal(img.view(np.uint32), rimg.view(np.uint32))
+    assert img[..., 3].max() > 0.5 and np.count_nonzero(img[..., 4]) > 1000
+    out.state.free()
+
+
+def test_surfel_packed_forward():
+    w, _, out, ref = _surfel_both("c1", None, 0, va.RasterPass.FORWARD)
+    np.testing.assert_array_equal(out.out_img.cpu().numpy().view(np.uint32), ref.get(po.F_OUT_IMG))
+    assert out.state is None
+
+
+@pytest.mark.parametrize("cfg,n,view", [("c1", None, 0), ("c2", 20_000, 0), ("c3", 20_000, 2)])
+def test_surfel_forward_bit_exact(cfg, n, view):
+    w, _, out, ref = _surfel_both(cfg, n, view)
+    _check_surfel_rows(out, ref)
+    np.testing.assert_array_equal(out.out_img.cpu().numpy().view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))
+    out.state.free()
+
+
+def _check_surfel_grads(g, rg, ref, vc):
+    for sl, name in ((slice(0, 9), "v_M"), (slice(9, 12), "v_normal"), (slice(12, 15), "v_rgb"),
+                     (15, "v_alpha"), (16, "v_refine")):
+        _check_grads(vc[:, sl], rg["v_combined"][:, sl], name)
+    vt = g.v_transforms.cpu().numpy()
+    vs = g.v_coeffs.cpu().numpy().reshape(len(vt), -1)
+    vo = g.v_raw_opac.cpu().numpy()
+    vr = g.v_refine_weight.cpu().numpy()
+    assert np.isfinite(vt).all() and np.isfinite(vs).all()
+    keep = ~ill_conditioned_rows(ref, vc)
+    for got, want, name in ((vt, rg["v_transforms"], "v_transforms"), (vo, rg["v_raw_opac"], "v_raw_opacity"),
+                            (vs, rg["v_sh"].reshape(len(vt), -1), "v_sh"), (vr, rg["v_refine"], "v_refine_weight")):
+        _check_grads(got[keep], want[keep], name, group_rtol=None)
+    pg = ref.project_backward(vc)
+    for got, want, name in ((vt, pg["v_transforms"], "v_transforms (projection stage)"),
+                            (vo, pg["v_raw_opac"], "v_raw_opacity (projection stage)"),
+                            (vs, pg["v_sh"].reshape(len(vt), -1), "v_sh (projection stage)"),
+                            (vr, pg["v_refine"], "v_refine_weight (projection stage)")):
+        _check_grads(got, want, name, rtol=1e-5, atol=0.0, group_rtol=1e-3)
+
+
+@pytest.mark.parametrize("cfg,n,view,pass_", [("c1", None, 0, va.RasterPass.BACKWARD),
+                                              ("c2", 20_000, 0, va.RasterPass.BACKWARD),
+                                              ("c3", 20_000, 2, va.RasterPass.BACKWARD),
+                                              ("c1", None, 0, va.RasterPass.BACKWARD_SMOOTH_CUTOFF)],
+                         ids=["c1", "c2", "c3", "c1-smooth"])
+def test_surfel_backward_parity(cfg, n, view, pass_):
+    w, (t, s, o), out, ref = _surfel_both(cfg, n, view, pass_)
+    img = out.out_img.cpu().numpy()
+    mask = circle_mask(w.img_size, w.mask_center, w.mask_radius) if w.mask_radius > 0 else None
+    v_rgb = l1_cotangent_np(img[..., :4], scenes.loss_target(w.img_size), mask)
+    rng = np.random.default_rng(7)
+    v_out = np.zeros_like(img)
+    v_out[..., :4] = v_rgb
+    # depth and normal channels carry a small loss too; the median channels are not differentiable
+    v_out[..., 4:8] = (rng.standard_normal(img[..., 4:8].shape) * 0.1 / img[..., 0].size).astype(np.float32)
+    g = va.render_backward(out, t, s, o, torch.from_numpy(v_out).cuda())
+    rg = ref.backward(v_out)
+    vc = g.v_combined.cpu().numpy()
+    assert vc.shape == (w.scene.num_splats, 17)
+    assert np.count_nonzero(np.any(vc != 0, axis=1)) > 100
+    _check_surfel_grads(g, rg, ref, vc)
+    out.state.free()
+
+
+def test_surfel_rejections():
+    w = scenes.workload("c1", 500)
+    cam = w.cameras[0].uniforms(w.img_size)
+    t, s, o = to_gpu(w.scene)
+    out = va.render(cam, w.img_size, t, s, o, render_mode=SURFEL)
+    with pytest.raises(va.VsError):                 # the camera gradient is built for gaussians
+        va.pose_backward(out, t, s, o, torch.zeros((500, 10), device="cuda"))
+    adam = va.FusedAdam.at_step(1, lr_opac=0.05)
+    with pytest.raises(va.VsError):                 # surfels train unfused
+        va.project_update(out, t.clone(), s, o.clone(), torch.zeros((500, 10), device="cuda"),
+                          torch.zeros((500, 10), dtype=torch.int32, device="cuda"),
+                          torch.full((10,), 1e-3, device="cuda"), torch.zeros(500, dtype=torch.int32, device="cuda"),
+                          adam)
+    out.state.free()
+    rows = torch.zeros((500, 4, 3), device="cuda")
+    with pytest.raises(va.VsError):                 # surfels take SH colour
+        va.render(cam, w.img_size, t, rows, o, render_mode=SURFEL, decoder=torch.zeros(816, device="cuda"))

@@ -74,7 +74,7 @@ class VsStateView(C.Structure):
                 ("isect_tiles", C.c_void_p), ("isect_gids", C.c_void_p), ("intersect_counts", C.c_void_p),
                 ("depth_bits", C.c_void_p), ("compact_from_global", C.c_void_p),
                 ("proj_xy_conic", C.c_void_p), ("proj_c11_opac_rg", C.c_void_p), ("proj_b", C.c_void_p),
-                ("proj_aux", C.c_void_p), ("tile_ranges", C.c_void_p)]
+                ("proj_aux", C.c_void_p), ("tile_ranges", C.c_void_p), ("proj_surf", C.c_void_p)]
 
 
 class VsLossCfg(C.Structure):

@@ -64,6 +64,7 @@ struct vs_ctx {
                      size_t limit = 0; bool live = false; };
     std::map<CapacityKey, Pending> pending;
     uint64_t lagged_renders = 0, lagged_overflows = 0;
+    uint64_t surfel_lens_dropped = 0;   // surfel renders whose camera had lens distortion (rendered as pinhole)
     hipEvent_t take() {
         if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
         hipEvent_t e = nullptr;
@@ -75,7 +76,7 @@ struct vs_ctx {
 struct vs_fwd_state {
     vs_ctx* ctx = nullptr;
     vs_camera cam{};
-    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0, sh_half = 0, mip = 0, neural = 0;
+    uint32_t W = 0, H = 0, N = 0, degree = 0, K = 0, sh_half = 0, mip = 0, neural = 0, surfel = 0;
     const float* min_scale = nullptr;   // the forward's scale floor (borrowed), or null
     float lso = 0.0f;
     float bg[3] = {0, 0, 0};
@@ -90,6 +91,7 @@ struct vs_fwd_state {
     float4* proj_b = nullptr;
     float* proj_c = nullptr;
     float4* proj_aux = nullptr;
+    float4* proj_surf = nullptr;  // [N][4] surfels: M rows, low-pass centre, normal
     float* opacities = nullptr;
     float* max_radius = nullptr;
     float* visible = nullptr;
@@ -306,13 +308,15 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     if (state_out) *state_out = nullptr;
     if (!ctx || !cam || !out || !background) return fail(VS_ERR_INVALID, "null argument");
     if (W == 0 || H == 0) return fail(VS_ERR_INVALID, "Can't render images with 0 size.");
-    if (mode != VS_MODE_DEFAULT && mode != VS_MODE_MIP)
-        return fail(VS_ERR_UNSUPPORTED, "the Surfel render mode is not built (Default and Mip are)");
+    if (mode != VS_MODE_DEFAULT && mode != VS_MODE_MIP && mode != VS_MODE_SURFEL)
+        return fail(VS_ERR_INVALID, "unknown render mode");
     if ((int)pass < 0 || (int)pass > (int)VS_PASS_GEOMETRY) return fail(VS_ERR_INVALID, "unknown pass");
     if (cam->model < VS_CAMERA_PINHOLE || cam->model > VS_CAMERA_TPF)
         return fail(VS_ERR_INVALID, "unknown camera model");
     vs_status vst = check_splats(sp);
     if (vst != VS_OK) return vst;
+    if (mode == VS_MODE_SURFEL && sp->decoder)
+        return fail(VS_ERR_UNSUPPORTED, "surfels take SH colour (no neural appearance)");
     if (!out->out_img) return fail(VS_ERR_INVALID, "out_img is null");
     if (pass_bwd_info(pass) && ((uintptr_t)out->out_img & 15u)) return fail(VS_ERR_INVALID, "out_img must be 16-byte aligned");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
@@ -328,6 +332,14 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->K = sp->decoder ? 4u : (sp->sh_degree + 1) * (sp->sh_degree + 1);
     st->sh_half = sp->sh_dtype == VS_SH_F16 ? 1u : 0u;
     st->mip = mode == VS_MODE_MIP ? 1u : 0u;
+    st->surfel = mode == VS_MODE_SURFEL ? 1u : 0u;
+    if (st->surfel && st->cam.model != VS_CAMERA_PINHOLE) {
+        // render.rs:451-469: surfel ray-plane coverage is pinhole-only; a lens
+        // camera renders as the pinhole with its focal length and principal point.
+        if (ctx->surfel_lens_dropped++ == 0)
+            std::fprintf(stderr, "vsplat: surfel (2DGS) rendering is pinhole-only: lens distortion ignored\n");
+        st->cam.model = VS_CAMERA_PINHOLE;
+    }
     st->min_scale = sp->min_scale;
     st->lso = sp->log_scale_offset;
     st->bg[0] = background[0]; st->bg[1] = background[1]; st->bg[2] = background[2];
@@ -339,7 +351,9 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->T = (uint32_t)T64;
     const uint32_t N = st->N, T = st->T;
     const bool bwd_info = pass_bwd_info(pass);
-    const bool geometry = pass == VS_PASS_GEOMETRY;
+    const bool surfel = st->surfel != 0u;
+    // Surfel renders with backward state always carry the geometry channels (render.rs:471-473).
+    const bool geometry = pass == VS_PASS_GEOMETRY || (surfel && bwd_info);
     const bool smooth = pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF;
     const uint32_t nblocks = (N + 255) / 256;
 
@@ -365,7 +379,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
     const size_t o_counts = take((size_t)N * 4), o_depth = take((size_t)N * 4), o_compact = take((size_t)N * 4);
     const size_t o_pa = take((size_t)N * 16), o_pb = take((size_t)N * 16), o_pc = take((size_t)N * 4);
-    const size_t o_aux = geometry ? take((size_t)N * 16) : 0;
+    const size_t o_aux = (geometry && !surfel) ? take((size_t)N * 16) : 0;
+    const size_t o_surf = surfel ? take((size_t)N * 64) : 0;
     const size_t o_opac = out->opacities ? 0 : take((size_t)N * 4);
     const size_t o_rad = out->max_radius ? 0 : take((size_t)N * 4);
     const size_t o_vis = (bwd_info && !out->visible) ? take((size_t)N * 4) : 0;
@@ -380,7 +395,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->proj_a = reinterpret_cast<float4*>(base + o_pa);
     st->proj_b = reinterpret_cast<float4*>(base + o_pb);
     st->proj_c = reinterpret_cast<float*>(base + o_pc);
-    st->proj_aux = geometry ? reinterpret_cast<float4*>(base + o_aux) : nullptr;
+    st->proj_aux = (geometry && !surfel) ? reinterpret_cast<float4*>(base + o_aux) : nullptr;
+    st->proj_surf = surfel ? reinterpret_cast<float4*>(base + o_surf) : nullptr;
     st->opacities = out->opacities ? out->opacities : reinterpret_cast<float*>(base + o_opac);
     st->max_radius = out->max_radius ? out->max_radius : reinterpret_cast<float*>(base + o_rad);
     st->visible = bwd_info ? (out->visible ? out->visible : reinterpret_cast<float*>(base + o_vis)) : nullptr;
@@ -399,7 +415,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.min_scale = st->min_scale; pa.mip = st->mip; pa.decoder = sp->decoder; pa.raw_opac = sp->raw_opacities;
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
-        pa.proj_aux = st->proj_aux; pa.compact = st->compact; pa.block_stats = st->block_stats;
+        pa.proj_aux = st->proj_aux; pa.proj_surf = st->proj_surf; pa.compact = st->compact; pa.block_stats = st->block_stats;
         VS_HIP(launch_project(pa, s), "project kernel");
         VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, isect_cap, s), "projection counts");
         if (bwd_info) VS_HIP(launch_fill_f32(st->visible, 0.0f, N, s), "zero visible");
@@ -506,6 +522,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
         ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;
         ra.proj_a = st->proj_a; ra.proj_b = st->proj_b; ra.proj_c = st->proj_c; ra.proj_aux = st->proj_aux;
+        // surfels outside training take the median by the surface criterion (gaussian_splats.rs:100-106)
+        ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass != VS_PASS_BACKWARD) ? 1u : 0u;
         ra.out = out->out_img; ra.visible = st->visible;
         VS_HIP(launch_raster_fwd(ra, bwd_info, geometry, smooth, s), "raster forward");
     }
@@ -561,13 +579,14 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     const uint32_t N = st->N;
     float* vc = grads->v_combined;
     void* vc_alloc = nullptr;
+    const uint32_t n_grads = st->surfel ? 17u : 10u;      // raster gradient components per splat
     if (!vc && N > 0) {
-        VS_HIP(hipMallocAsync(&vc_alloc, (size_t)N * 40, s), "hipMallocAsync(v_combined)");
+        VS_HIP(hipMallocAsync(&vc_alloc, (size_t)N * n_grads * 4, s), "hipMallocAsync(v_combined)");
         vc = static_cast<float*>(vc_alloc);
     }
     if (vc && ((uintptr_t)vc & 7u)) return fail(VS_ERR_INVALID, "v_combined must be 8-byte aligned");
     {
-        VS_HIP(launch_fill_f32(vc, 0.0f, (uint64_t)N * 10, s), "zero v_combined");
+        VS_HIP(launch_fill_f32(vc, 0.0f, (uint64_t)N * n_grads, s), "zero v_combined");
         StageTimer tm(ctx, ST_RASTER_BWD);
         if (st->I > 0) {
             RasterBwdArgs rb{};
@@ -575,7 +594,9 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             rb.bg_r = st->bg[0]; rb.bg_g = st->bg[1]; rb.bg_b = st->bg[2];
             rb.gids = st->gids; rb.ranges = st->ranges_shrunk;
             rb.proj_a = st->proj_a; rb.proj_b = st->proj_b; rb.proj_c = st->proj_c;
-            rb.out_img = out_img; rb.v_out = v_out; rb.channels = (st->pass == VS_PASS_GEOMETRY) ? 12u : 4u;
+            rb.out_img = out_img; rb.v_out = v_out;
+            rb.channels = (st->pass == VS_PASS_GEOMETRY || st->surfel) ? 12u : 4u;
+            rb.proj_surf = st->proj_surf;
             rb.v_combined = vc;
             VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s), "raster backward");
         }
@@ -590,7 +611,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
         ProjectBwdArgs pb{};
         pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = sp->log_scale_offset;
         pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.sh_half = st->sh_half; pb.min_scale = sp->min_scale; pb.mip = st->mip; pb.raw_opac = sp->raw_opacities;
-        pb.decoder = sp->decoder;
+        pb.decoder = sp->decoder; pb.surfel = st->surfel;
         pb.counts = st->counts; pb.v_combined = vc;
         pb.v_transforms = grads->v_transforms; pb.v_sh = grads->v_sh_coeffs;
         pb.v_raw_opac = grads->v_raw_opacities; pb.v_refine = grads->v_refine_weight;
@@ -620,6 +641,7 @@ extern "C" vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_sp
     if (!ctx || !st || !v_combined || !v_pose) return fail(VS_ERR_INVALID, "null argument");
     if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
     if (st->neural) return fail(VS_ERR_UNSUPPORTED, "the camera gradient follows the SH colour path (no neural appearance)");
+    if (st->surfel) return fail(VS_ERR_UNSUPPORTED, "the camera gradient is built for gaussians (not surfels)");
     vs_status vst = check_splats(sp);
     if (vst != VS_OK) return vst;
     if (sp->num_splats != st->N || sp->sh_degree != st->degree || (sp->sh_dtype == VS_SH_F16) != (st->sh_half != 0))
@@ -651,6 +673,7 @@ extern "C" vs_status vs_project_update(vs_ctx* ctx, vs_fwd_state* st, float* tra
     if (!ctx || !st || !adam || !out) return fail(VS_ERR_INVALID, "null argument");
     if (!pass_bwd_info(st->pass)) return fail(VS_ERR_INVALID, "the forward pass kept no backward state");
     if (st->neural) return fail(VS_ERR_UNSUPPORTED, "the fused update takes SH colour (neural appearance trains unfused)");
+    if (st->surfel) return fail(VS_ERR_UNSUPPORTED, "the fused update is built for gaussians (surfels train unfused)");
     const uint32_t N = st->N;
     if (N > 0 && (!transforms || !sh_coeffs || !raw_opacities || !v_combined || !w_t || !lr_scale || !w_o))
         return fail(VS_ERR_INVALID, "parameter, gradient or moment pointer is null");
@@ -769,6 +792,7 @@ extern "C" vs_status vs_fwd_state_view(const vs_fwd_state* st, vs_state_view* o)
     o->proj_c11_opac_rg = reinterpret_cast<const float*>(st->proj_b);
     o->proj_b = st->proj_c;
     o->proj_aux = reinterpret_cast<const float*>(st->proj_aux);
+    o->proj_surf = reinterpret_cast<const float*>(st->proj_surf);
     o->tile_ranges = st->ranges;
     return VS_OK;
 }

@@ -18,6 +18,7 @@
 #include "vs_camera.h"
 #include "vs_sh.h"
 #include "vs_neural.h"
+#include "vs_surfel.h"
 #include "vs_internal.h"
 
 namespace vs {
@@ -234,7 +235,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             const F3 mean{t01.x, t01.y, t23.x};
             const F3 mc = world_to_cam(mean, u);
             if (!(finite(mc) && mc.z <= 1.0e10f)) break;
-            if constexpr (MODEL == VS_CAMERA_PINHOLE) {
+            if constexpr (MODEL == VS_CAMERA_PINHOLE || MODEL == SURFEL_MODEL) {
                 if (mc.z < 0.01f) break;
             } else {
                 const float r = __builtin_sqrtf(mc.x * mc.x + mc.y * mc.y);
@@ -250,15 +251,30 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             const Qt q = normalize(qu);
             const ScaleFloor fl = apply_scale_floor(scl, sigmoid(raw_op), a.min_scale, g);
             opac_out = fl.opac;
-            float filter_comp;
-            const S2 cov = compensate_cov2d(cov2d_raw<MODEL>(fl.scale, q, mc, u), a.mip != 0u, filter_comp);
-            const float opac = fl.opac * filter_comp;
-            fscl = fl.scale;
-            if (!finite(cov)) break;
-            project_point<MODEL>(mc, u, px, py);
-            if (!(opac >= 1.0f / 255.0f)) break;
-            power = logf_c(opac * 255.0f);
-            conic = inverse(cov);
+            float opac;
+            SurfelProj sp{};
+            if constexpr (MODEL == SURFEL_MODEL) {
+                // project_forward.rs:128-147: bin by the ellipse covering the
+                // cutoff footprint and the low-pass disk; no 2-D blur compensation.
+                opac = fl.opac;
+                if (!(opac >= 1.0f / 255.0f)) break;
+                power = logf_c(opac * 255.0f);
+                sp = surfel_project(fl.scale, q, mc, u, power);
+                if (!sp.valid) break;
+                conic = sp.bin_conic;
+                px = sp.bin_x;
+                py = sp.bin_y;
+            } else {
+                float filter_comp;
+                const S2 cov = compensate_cov2d(cov2d_raw<MODEL>(fl.scale, q, mc, u), a.mip != 0u, filter_comp);
+                opac = fl.opac * filter_comp;
+                fscl = fl.scale;
+                if (!finite(cov)) break;
+                project_point<MODEL>(mc, u, px, py);
+                if (!(opac >= 1.0f / 255.0f)) break;
+                power = logf_c(opac * 255.0f);
+                conic = inverse(cov);
+            }
             float ex, ey;
             bbox_extent(conic, power, ex, ey);
             if (!(ex >= 0.0f && ey >= 0.0f)) break;
@@ -284,6 +300,18 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             a.proj_a[g] = make_float4(px, py, conic.c00, conic.c01);
             a.proj_b[g] = make_float4(conic.c11, opac, col.x, col.y);
             a.proj_c[g] = col.z;
+            if constexpr (MODEL == SURFEL_MODEL) {
+                // project_visible.rs:231-273: M rows, the low-pass centre (the
+                // pinhole projection of the centre) and the camera-facing normal
+                float cx_, cy_;
+                project_point<VS_CAMERA_PINHOLE>(mc, u, cx_, cy_);
+                const F3 nrm = surfel_normal(q, mc, u);
+                float4* o = a.proj_surf + (size_t)g * 4;
+                o[0] = make_float4(sp.r0.x, sp.r0.y, sp.r0.z, sp.r1.x);
+                o[1] = make_float4(sp.r1.y, sp.r1.z, sp.r2.x, sp.r2.y);
+                o[2] = make_float4(sp.r2.z, cx_, cy_, nrm.x);
+                o[3] = make_float4(nrm.y, nrm.z, 0.0f, 0.0f);
+            }
             if constexpr (GEOM) {
                 // kernels/project_visible.rs:271-289
                 const M3 rot = mul(view_rot(u), to_mat3(q));
@@ -485,6 +513,10 @@ static void launch_project_type(const ProjectArgs& a, dim3 grid, hipStream_t s, 
 }
 template <int DEG>
 static void launch_project_model(const ProjectArgs& a, dim3 grid, hipStream_t s, bool geom) {
+    if (a.proj_surf) {                       // surfels: pinhole camera, no gaussian geometry normal
+        launch_project_type<DEG, SURFEL_MODEL>(a, grid, s, false);
+        return;
+    }
     switch (a.cam.model) {
     case VS_CAMERA_KB4: launch_project_type<DEG, VS_CAMERA_KB4>(a, grid, s, geom); break;
     case VS_CAMERA_RT8: launch_project_type<DEG, VS_CAMERA_RT8>(a, grid, s, geom); break;

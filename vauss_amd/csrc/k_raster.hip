@@ -25,6 +25,7 @@
 // permlane swaps and DPP (no LDS traffic), so each (tile, splat) pair issues
 // one atomic instruction of at most ten lanes.
 #include "vs_device.h"
+#include "vs_surfel.h"
 #include "vs_internal.h"
 
 namespace vs {
@@ -119,12 +120,16 @@ VS_DEV uint32_t compact_bits_16(uint32_t v) {
 
 constexpr int FWD_BLOCK = 256;
 
-template <bool BWD, bool GEOM, bool SMOOTH>
+// SURF: surfels (2DGS): coverage by the pixel ray's sample of the surfel's
+// plane (vs_surfel.h), depth from the intersection, the normal from the row;
+// no quadrant culling (the binning ellipse, not the coverage, is an ellipse).
+template <bool BWD, bool GEOM, bool SMOOTH, bool SURF>
 __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
     __shared__ float4 s_a[FWD_BLOCK];    // x, y, c00/2, c01
     __shared__ float4 s_b[FWD_BLOCK];    // c11/2, opacity, max(r,0), max(g,0)
     __shared__ float s_c[FWD_BLOCK];     // max(b,0)
-    __shared__ float4 s_d[GEOM ? FWD_BLOCK : 1];
+    __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BLOCK : 1];
+    __shared__ float4 s_s[SURF ? FWD_BLOCK * 4 : 1];
     __shared__ uint32_t s_gid[BWD ? FWD_BLOCK : 1];
     __shared__ uint32_t s_hit[BWD ? FWD_BLOCK : 1];
     __shared__ uint8_t s_list[4][FWD_BLOCK];       // per-quadrant live batch slots
@@ -148,6 +153,8 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
     float depth_acc = 0.0f, median = 0.0f, dist_b = 0.0f, dist_c = 0.0f, nx = 0.0f, ny = 0.0f, nz = 0.0f;
     uint32_t median_id = 0xFFFFFFFFu;
+    float surf_o = 0.0f;
+    bool surf_found = false;
     bool done = !inside;
     uint32_t last = lo;
 
@@ -166,9 +173,16 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
             s_a[l] = sa;
             s_b[l] = sb;
             s_c[l] = mx(a.proj_c[gid], 0.0f);
-            if constexpr (GEOM) s_d[l] = a.proj_aux[gid];
+            if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
             if constexpr (BWD) { s_gid[l] = gid; s_hit[l] = 0u; }
-            qmask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
+            if constexpr (SURF) {
+                const float4* ps = a.proj_surf + (size_t)gid * 4;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) s_s[4 * l + k] = ps[k];
+                qmask = 0xFu;
+            } else {
+                qmask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
+            }
         }
         // Per-quadrant compaction of the live slots, in slot (= depth) order.
         uint32_t below[4];
@@ -192,10 +206,18 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
         const uint8_t* list = s_list[wave];
         for (uint32_t j = 0; j < count && !done; ++j) {
             const uint32_t t = list[j];
-            const float4 sa = s_a[t];
             const float4 sb = s_b[t];
-            const float dx = pcx - sa.x, dy = pcy - sa.y;
-            const float sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);
+            float sigma, zs = 0.0f;
+            if constexpr (SURF) {
+                const SurfelHit hit = surfel_hit(s_s[4 * t], s_s[4 * t + 1], s_s[4 * t + 2], pcx, pcy);
+                if (!hit.valid) continue;       // the ray misses the plane or meets it before the near limit
+                sigma = hit.sigma;
+                zs = hit.z;
+            } else {
+                const float4 sa = s_a[t];
+                const float dx = pcx - sa.x, dy = pcy - sa.y;
+                sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);
+            }
             const float G = expf_neg(-sigma);
             // min(0.999, .) of a product that is NaN only when sigma is
             // (then the sigma test below rejects the pair): same value as mn().
@@ -213,9 +235,23 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
                     cg = __builtin_fmaf(sb.w, vis, cg);
                     cb = __builtin_fmaf(s_c[t], vis, cb);
                     if constexpr (GEOM) {
-                        const float4 d = s_d[t];
+                        float4 d;
+                        if constexpr (SURF) {
+                            const float4 s2 = s_s[4 * t + 2], s3 = s_s[4 * t + 3];
+                            d = make_float4(zs, s2.w, s3.x, s3.y);
+                        } else {
+                            d = s_d[t];
+                        }
                         depth_acc = __builtin_fmaf(d.x, vis, depth_acc);
-                        if (T > 0.5f) { median = d.x; median_id = start + t; }
+                        if (SURF && a.surf_crit) {
+                            // unbiased-depth surface criterion (rasterize.rs:181-187, 346-354)
+                            surf_o += ae + 0.1f * G;
+                            if (!surf_found && (surf_o > 0.6f || T > 0.5f)) {
+                                median = d.x; median_id = start + t; surf_found = surf_o > 0.6f;
+                            }
+                        } else if (T > 0.5f) {
+                            median = d.x; median_id = start + t;
+                        }
                         const float m = dist_depth(d.x);
                         dist_b = __builtin_fmaf(m, vis, dist_b);
                         dist_c = __builtin_fmaf(m * m, vis, dist_c);
@@ -464,6 +500,173 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     }
 }
 
+// Surfel (2DGS) backward, bwd/kernels/rasterize_backwards_planes.rs:266-480:
+// one 64-lane wavefront per tile, lane L owning pixel (L % 8, L / 8) of each
+// 8x8 quadrant.  Each pixel replays the forward with the remaining colour,
+// depth, normal and distortion sums and their cotangents (the geometry
+// channels composite like colours without a background), and a lane adds its
+// pixels' 17 gradient components [M rows, normal, rgb, alpha, refine] per
+// splat; the wavefront sums each component once per (tile, splat) and 17
+// lanes add the sums to v_combined [N,17].
+template <bool SMOOTH>
+__global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) {
+    __shared__ float4 s_s[BWD_BATCH * 4];   // M rows, centre, normal (vs_surfel.h layout)
+    __shared__ float4 s_b[BWD_BATCH];       // opacity, r, g, b (raw colours: the gates need the sign)
+    __shared__ uint32_t s_gid[BWD_BATCH];
+
+    const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
+    if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
+    const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
+    if (lo >= hi) return;   // uniform per tile
+    const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
+    const uint32_t lane = threadIdx.x;
+    const float img_w = (float)a.img_w, img_h = (float)a.img_h;
+
+    float pcx[BWD_PX], pcy[BWD_PX], T[BWD_PX], rscale[BWD_PX];
+    float sr[BWD_PX], sg[BWD_PX], sb[BWD_PX], sz[BWD_PX], snx[BWD_PX], sny[BWD_PX], snz[BWD_PX], sdb[BWD_PX], sdc[BWD_PX];
+    float vr[BWD_PX], vg[BWD_PX], vb[BWD_PX], vt[BWD_PX], vz[BWD_PX], vmed[BWD_PX], vnx[BWD_PX], vny[BWD_PX], vnz[BWD_PX];
+    float vdb[BWD_PX], vdc[BWD_PX];
+    uint32_t med[BWD_PX];
+#pragma unroll
+    for (int k = 0; k < BWD_PX; ++k) {
+        const uint32_t px = tx * TILE_W + 8 * (k & 1) + (lane & 7);
+        const uint32_t py = ty * TILE_W + 8 * (k >> 1) + (lane >> 3);
+        pcx[k] = (float)px + 0.5f;
+        pcy[k] = (float)py + 0.5f;
+        T[k] = rscale[k] = 0.0f;
+        sr[k] = sg[k] = sb[k] = sz[k] = snx[k] = sny[k] = snz[k] = sdb[k] = sdc[k] = 0.0f;
+        vr[k] = vg[k] = vb[k] = vt[k] = vz[k] = vmed[k] = vnx[k] = vny[k] = vnz[k] = vdb[k] = vdc[k] = 0.0f;
+        med[k] = 0xFFFFFFFFu;
+        if (px < a.img_w && py < a.img_h) {
+            const size_t base = ((size_t)py * a.img_w + px) * a.channels;
+            const float4 o0 = *reinterpret_cast<const float4*>(a.out_img + base);
+            const float4 o1 = *reinterpret_cast<const float4*>(a.out_img + base + 4);
+            const float4 o2 = *reinterpret_cast<const float4*>(a.out_img + base + 8);
+            const float4 v0 = *reinterpret_cast<const float4*>(a.v_out + base);
+            const float4 v1 = *reinterpret_cast<const float4*>(a.v_out + base + 4);
+            const float4 v2 = *reinterpret_cast<const float4*>(a.v_out + base + 8);
+            const float t_final = 1.0f - o0.w;
+            sr[k] = o0.x - t_final * a.bg_r;
+            sg[k] = o0.y - t_final * a.bg_g;
+            sb[k] = o0.z - t_final * a.bg_b;
+            T[k] = 1.0f;
+            vr[k] = v0.x; vg[k] = v0.y; vb[k] = v0.z;
+            vt[k] = (v0.w - (a.bg_r * v0.x + a.bg_g * v0.y + a.bg_b * v0.z)) * t_final;
+            rscale[k] = 1.0f / mx(o0.w, 1.0e-5f);
+            sz[k] = o1.x; snx[k] = o1.z; sny[k] = o1.w; snz[k] = o2.x; sdb[k] = o2.y; sdc[k] = o2.z;
+            med[k] = as_u(o2.w);
+            vz[k] = v1.x; vmed[k] = v1.y; vnx[k] = v1.z; vny[k] = v1.w; vnz[k] = v2.x; vdb[k] = v2.y; vdc[k] = v2.z;
+        }
+    }
+    const float cut_lo = ALPHA_MID - 0.5f * ALPHA_BAND;
+
+    for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
+        bool any_alive = false;
+#pragma unroll
+        for (int k = 0; k < BWD_PX; ++k) any_alive = any_alive || T[k] > T_STOP;
+        if (__ballot(any_alive) == 0ull) break;              // every pixel of the tile is done
+        const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
+        __syncthreads();
+        if (lane < rem) {
+            const uint32_t gid = a.gids[start + lane];
+            const float4* ps = a.proj_surf + (size_t)gid * 4;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) s_s[4 * lane + k] = ps[k];
+            const float4 pb = a.proj_b[gid];
+            s_b[lane] = make_float4(pb.y, pb.z, pb.w, a.proj_c[gid]);
+            s_gid[lane] = gid;
+        }
+        __syncthreads();
+        for (uint32_t t = 0; t < rem; ++t) {
+            const float4 m0 = s_s[4 * t], m1 = s_s[4 * t + 1], m2 = s_s[4 * t + 2], m3 = s_s[4 * t + 3];
+            const float4 cb = s_b[t];
+            const float opac = cb.x, col_r = cb.y, col_g = cb.z, col_b = cb.w;
+            const float cl_r = mx(col_r, 0.0f), cl_g = mx(col_g, 0.0f), cl_b = mx(col_b, 0.0f);
+            const float r2x = m1.z, r2y = m1.w, r2z = m2.x, cen_x = m2.y, cen_y = m2.z;
+            const float nrm_x = m2.w, nrm_y = m3.x, nrm_z = m3.y;
+            const float inv_r2z = 1.0f / r2z;
+            const float sigma_max = logf_c(opac / cut_lo) + 1.0e-3f;   // alpha below the cutoff band beyond it
+            const uint32_t isect = start + t;
+            float gs[SURFEL_GRADS];
+#pragma unroll
+            for (int i = 0; i < SURFEL_GRADS; ++i) gs[i] = 0.0f;
+            bool contrib = false;
+#pragma unroll
+            for (int k = 0; k < BWD_PX; ++k) {
+                if (!(T[k] > T_STOP)) continue;
+                const SurfelHit h = surfel_hit(m0, m1, m2, pcx[k], pcy[k]);
+                if (!(h.valid && h.sigma <= sigma_max)) continue;
+                const float G = expf_neg(-h.sigma);
+                const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);
+                const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
+                if (!(h.sigma >= 0.0f && w_cut > 0.0f)) continue;
+                const float ae = alpha * w_cut;
+                const float nt = T[k] * (1.0f - ae);
+                if (nt <= T_STOP) { T[k] = 0.0f; continue; }
+                contrib = true;
+                const float z = h.z;
+                const float m = dist_depth(z);
+                const float dm_dz = (z > 0.2f) ? 100.0f / (100.0f - 0.2f) * 0.2f / (z * z) : 0.0f;
+                const float Tk = T[k];
+                const float vis = ae * Tk;
+                gs[12] += (col_r >= 0.0f) ? vis * vr[k] : 0.0f;
+                gs[13] += (col_g >= 0.0f) ? vis * vg[k] : 0.0f;
+                gs[14] += (col_b >= 0.0f) ? vis * vb[k] : 0.0f;
+                gs[9] += vis * vnx[k];
+                gs[10] += vis * vny[k];
+                gs[11] += vis * vnz[k];
+                const float ra = 1.0f / (1.0f - ae);
+                const float dot_ = ((Tk * cl_r - sr[k]) * vr[k] + (Tk * cl_g - sg[k]) * vg[k] + (Tk * cl_b - sb[k]) * vb[k] +
+                                    (Tk * z - sz[k]) * vz[k] + (Tk * nrm_x - snx[k]) * vnx[k] +
+                                    (Tk * nrm_y - sny[k]) * vny[k] + (Tk * nrm_z - snz[k]) * vnz[k] +
+                                    (Tk * m - sdb[k]) * vdb[k] + (Tk * m * m - sdc[k]) * vdc[k]) * ra;
+                const float v_ae = dot_ + vt[k] * ra;
+                const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+                const float v_z = vis * (vz[k] + (vdb[k] + 2.0f * m * vdc[k]) * dm_dz) + ((isect == med[k]) ? vmed[k] : 0.0f);
+                const bool unsat = opac * G <= ALPHA_CAP;
+                const float v_sigma = unsat ? -alpha * v_alpha : 0.0f;
+                if (unsat) gs[15] += v_alpha * G;
+                const bool use_3d = h.s3d <= h.s2d;
+                const float v_su = (use_3d ? v_sigma * h.su : 0.0f) + v_z * r2x;
+                const float v_sv = (use_3d ? v_sigma * h.sv : 0.0f) + v_z * r2y;
+                const float v_cx = use_3d ? 0.0f : -2.0f * v_sigma * h.dxs;
+                const float v_cy = use_3d ? 0.0f : -2.0f * v_sigma * h.dys;
+                const float inv_qz = 1.0f / h.qz;
+                const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * h.su + v_sv * h.sv) * inv_qz;
+                // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
+                const float vhux = h.hvy * vqz - h.hvz * vqy, vhuy = h.hvz * vqx - h.hvx * vqz, vhuz = h.hvx * vqy - h.hvy * vqx;
+                const float vhvx = vqy * h.huz - vqz * h.huy, vhvy = vqz * h.hux - vqx * h.huz, vhvz = vqx * h.huy - vqy * h.hux;
+                const float g0 = vhux, g1 = vhuy, g2 = vhuz + v_cx * inv_r2z;
+                const float g3 = vhvx, g4 = vhvy, g5 = vhvz + v_cy * inv_r2z;
+                gs[0] += g0; gs[1] += g1; gs[2] += g2; gs[3] += g3; gs[4] += g4; gs[5] += g5;
+                gs[6] += v_z * h.su - pcx[k] * vhux - pcy[k] * vhvx;
+                gs[7] += v_z * h.sv - pcx[k] * vhuy - pcy[k] * vhvy;
+                gs[8] += v_z - pcx[k] * vhuz - pcy[k] * vhvz - (v_cx * cen_x + v_cy * cen_y) * inv_r2z;
+                // refine weight: this pixel's gradient of a screen-space shift of the surfel (M -> T M)
+                const float shx = g0 * r2x + g1 * r2y + g2 * r2z;
+                const float shy = g3 * r2x + g4 * r2y + g5 * r2z;
+                const float ux = shx * img_w, uy = shy * img_h;
+                gs[16] += __builtin_sqrtf(ux * ux + uy * uy) * rscale[k];
+                sr[k] -= vis * cl_r; sg[k] -= vis * cl_g; sb[k] -= vis * cl_b;
+                sz[k] -= vis * z; snx[k] -= vis * nrm_x; sny[k] -= vis * nrm_y; snz[k] -= vis * nrm_z;
+                sdb[k] -= vis * m; sdc[k] -= vis * m * m;
+                T[k] = nt;
+            }
+            if (__ballot(contrib) == 0ull) continue;          // uniform: gs is zero in every lane
+            float mine = 0.0f;
+#pragma unroll
+            for (int c = 0; c < SURFEL_GRADS; ++c) {
+                float v = gs[c];
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+                if ((int)lane == c) mine = v;
+            }
+            if (lane < (uint32_t)SURFEL_GRADS && mine != 0.0f)
+                atomicAdd(&a.v_combined[(size_t)s_gid[t] * SURFEL_GRADS + lane], mine);
+        }
+    }
+}
+
 __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, const float* __restrict__ gt, uint32_t w,
                                     uint32_t h, float mcx, float mcy, float mr, float inv_count, float* __restrict__ v) {
     const uint32_t pid = blockIdx.x * blockDim.x + threadIdx.x;
@@ -494,17 +697,24 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s) {
     if (a.num_tiles == 0) return hipSuccess;
     const dim3 grid(xcd_grid(a.num_tiles));
-    if (!bwd_info) raster_fwd_kernel<false, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
-    else if (geometry) raster_fwd_kernel<true, true, false><<<grid, FWD_BLOCK, 0, s>>>(a);
-    else if (smooth) raster_fwd_kernel<true, false, true><<<grid, FWD_BLOCK, 0, s>>>(a);
-    else raster_fwd_kernel<true, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
+    if (a.proj_surf) {           // surfels: every bwd-info pass carries the geometry channels
+        if (!bwd_info) raster_fwd_kernel<false, false, false, true><<<grid, FWD_BLOCK, 0, s>>>(a);
+        else if (smooth) raster_fwd_kernel<true, true, true, true><<<grid, FWD_BLOCK, 0, s>>>(a);
+        else raster_fwd_kernel<true, true, false, true><<<grid, FWD_BLOCK, 0, s>>>(a);
+    } else if (!bwd_info) raster_fwd_kernel<false, false, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
+    else if (geometry) raster_fwd_kernel<true, true, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
+    else if (smooth) raster_fwd_kernel<true, false, true, false><<<grid, FWD_BLOCK, 0, s>>>(a);
+    else raster_fwd_kernel<true, false, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
 
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s) {
     if (a.num_tiles == 0) return hipSuccess;
     const dim3 grid(xcd_grid(a.num_tiles));
-    if (smooth) raster_bwd_kernel<true><<<grid, 64, 0, s>>>(a);
+    if (a.proj_surf) {
+        if (smooth) raster_bwd_surfel_kernel<true><<<grid, 64, 0, s>>>(a);
+        else raster_bwd_surfel_kernel<false><<<grid, 64, 0, s>>>(a);
+    } else if (smooth) raster_bwd_kernel<true><<<grid, 64, 0, s>>>(a);
     else raster_bwd_kernel<false><<<grid, 64, 0, s>>>(a);
     return hipGetLastError();
 }

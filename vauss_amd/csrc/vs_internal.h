@@ -57,6 +57,7 @@ struct ProjectArgs {
     float4* proj_b;             // [N] c11, opacity, r, g
     float* proj_c;              // [N] b
     float4* proj_aux;           // [N] z, nx, ny, nz (geometry) or null
+    float4* proj_surf;          // [N][4] surfels: M rows, low-pass centre, normal (vs_surfel.h layout), or null
     uint32_t* compact;          // [N] g + 1 for splats past every cull, else 0 (compact_from_global)
     uint32_t* block_stats;      // [BS_ROWS][ceil(N/256)]
 };
@@ -92,6 +93,8 @@ struct RasterArgs {
     const float4* proj_b;
     const float* proj_c;
     const float4* proj_aux;
+    const float4* proj_surf;         // [N][4] surfels (vs_surfel.h layout) or null
+    uint32_t surf_crit;              // surfels outside training: median by the surface criterion
     void* out;                       // f32 [H,W,C] or u32 [H,W]
     float* visible;                  // [N] or null
 };
@@ -104,10 +107,11 @@ struct RasterBwdArgs {
     const float4* proj_a;
     const float4* proj_b;
     const float* proj_c;
+    const float4* proj_surf;         // [N][4] surfels, or null
     const float* out_img;            // [H,W,C]
     const float* v_out;              // [H,W,C]
     uint32_t channels;
-    float* v_combined;               // [N,10]
+    float* v_combined;               // [N,10], surfels [N,17]
 };
 
 struct ProjectBwdArgs {
@@ -120,6 +124,7 @@ struct ProjectBwdArgs {
     const float* min_scale;          // [N] scale floor (apply_scale_floor) or null
     uint32_t mip;                    // SplatRenderMode::Mip
     const float* decoder;            // neural appearance: no SH term here (the neural backward adds it)
+    uint32_t surfel;                 // surfels: v_combined rows of 17 (surfel_backwards)
     const float* raw_opac;
     const uint32_t* counts;          // visible <=> counts defined; culled rows get zeros
     const float* v_combined;         // [N,10]

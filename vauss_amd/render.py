@@ -40,12 +40,17 @@ class RasterPass(enum.IntEnum):
     def bwd_info(self) -> bool:
         return self is not RasterPass.FORWARD
 
-    def out_channels(self) -> int:
-        return 12 if self is RasterPass.GEOMETRY else (4 if self.bwd_info() else 1)
+    def out_channels(self, surfel: bool = False) -> int:
+        """Image channels: 12 for the geometry pass and every surfel pass with
+        backward state (render.rs:471-473), 4 for other float passes, 1 packed."""
+        if self is RasterPass.GEOMETRY or (surfel and self.bwd_info()):
+            return 12
+        return 4 if self.bwd_info() else 1
 
 
 class SplatRenderMode(enum.IntEnum):
-    """SplatRenderMode (gaussian_splats.rs:19-26); DEFAULT and MIP are built, SURFEL raises VsError."""
+    """SplatRenderMode (gaussian_splats.rs:19-26): DEFAULT, MIP, and SURFEL (2DGS, pinhole-only,
+    SH colour; v_combined rows of 17 in the backward)."""
     DEFAULT = _lib.MODE_DEFAULT
     MIP = _lib.MODE_MIP
     SURFEL = _lib.MODE_SURFEL
@@ -287,7 +292,7 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     ctx = Context.get(dev)
     cam = camera.uniforms((w, h)) if isinstance(camera, Camera) else camera
     tbw, tbh = (w + 15) // 16, (h + 15) // 16
-    ch = pass_.out_channels()
+    ch = pass_.out_channels(SplatRenderMode(render_mode) is SplatRenderMode.SURFEL)
     if ch == 1:
         out_img = torch.empty((h, w), dtype=torch.int32, device=dev)
     else:
@@ -312,6 +317,7 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     state = ForwardState(st, ctx, pass_, n, degree) if st.value else None
     if state is not None:
         state.keep = min_scale          # the state borrows the floor for project_update
+        state.surfel = SplatRenderMode(render_mode) is SplatRenderMode.SURFEL
     return RenderOutput(out_img, aux, state, cam, tuple(float(v) for v in background))
 
 
@@ -342,14 +348,15 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     ctx = output.state.ctx
     Context.get(dev)
     k = 4 if decoder is not None else (degree + 1) ** 2
+    n_grads = 17 if getattr(output.state, "surfel", False) else 10     # surfel rows: M, normal, rgb, alpha, refine
     if fused:
-        g = SplatGrads(None, None, None, None, torch.empty((n, 10), dtype=torch.float32, device=dev))
+        g = SplatGrads(None, None, None, None, torch.empty((n, n_grads), dtype=torch.float32, device=dev))
     else:
         g = SplatGrads(torch.empty((n, 10), dtype=torch.float32, device=dev),
                        torch.empty((n, k, 3), dtype=torch.float32, device=dev),
                        torch.empty(n, dtype=torch.float32, device=dev),
                        torch.empty(n, dtype=torch.float32, device=dev),
-                       torch.empty((n, 10), dtype=torch.float32, device=dev))
+                       torch.empty((n, n_grads), dtype=torch.float32, device=dev))
         if decoder is not None:
             g.v_decoder = torch.empty(NEURAL_DECODER_LEN, dtype=torch.float32, device=dev)
             g.v_coeffs_sq = torch.empty(n, dtype=torch.float32, device=dev)
