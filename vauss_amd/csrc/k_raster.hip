@@ -352,6 +352,40 @@ VS_DEV float reduce_scatter10(const float v[10], uint32_t lane) {
     return z;
 }
 
+// 17-component reduce-scatter on the same data paths (surfel gradients):
+// bit 5 pairs component i with i + 9, bit 4 pairs 5 apart, bit 3 pairs 3
+// apart, bit 2 pairs 2 apart, bit 1 pairs neighbours, bit 0 completes the
+// sum.  Lane L then holds the wave sum of component
+// 9*b5 + 5*b4 + 3*b3 + 2*b2 + b1 unless a sub-index is padding
+// (scatter_component17 < 0); lanes with L & 1 == 0 write it.
+VS_DEV int scatter_component17(uint32_t lane) {
+    const int k = ((lane & 4) ? 2 : 0) + ((lane & 2) ? 1 : 0);      // 3 = padding
+    const int j = ((lane & 8) ? 3 : 0) + k;                          // 5 = padding
+    const int i = ((lane & 16) ? 5 : 0) + j;                         // 9 = padding
+    const int c = ((lane & 32) ? 9 : 0) + i;                         // 17 = padding
+    return (k < 3 && j < 5 && i < 9 && c < 17) ? c : -1;
+}
+
+VS_DEV float reduce_scatter17(const float v[17], uint32_t lane) {
+    float w[9];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = swap32_sum(v[i], v[i + 9]);
+    w[8] = swap32_sum(v[8], 0.0f);
+    float x[5];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = swap16_sum(w[j], w[j + 5]);
+    x[4] = swap16_sum(w[4], 0.0f);
+    const bool h8 = lane & 8, h4 = lane & 4, h2 = lane & 2;
+    const float y0 = (h8 ? x[3] : x[0]) + dpp<DPP_ROW_ROR8>(h8 ? x[0] : x[3]);
+    const float y1 = (h8 ? x[4] : x[1]) + dpp<DPP_ROW_ROR8>(h8 ? x[1] : x[4]);
+    const float y2 = (h8 ? 0.0f : x[2]) + dpp<DPP_ROW_ROR8>(h8 ? x[2] : 0.0f);
+    const float z0 = (h4 ? y2 : y0) + dpp<DPP_ROW_HALF_MIRROR>(h4 ? y0 : y2);
+    const float z1 = (h4 ? 0.0f : y1) + dpp<DPP_ROW_HALF_MIRROR>(h4 ? y1 : 0.0f);
+    float u = (h2 ? z1 : z0) + dpp<DPP_QUAD_XOR2>(h2 ? z0 : z1);
+    u += dpp<DPP_QUAD_XOR1>(u);
+    return u;
+}
+
 // One 64-lane wavefront per tile; lane L owns pixel (L % 8, L / 8) of each
 // 8x8 quadrant k (k = 0..3), so the quadrant masks turn into uniform branches.
 // A lane sums its pixels' contributions in registers and the wavefront
@@ -506,8 +540,9 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
 // depth, normal and distortion sums and their cotangents (the geometry
 // channels composite like colours without a background), and a lane adds its
 // pixels' 17 gradient components [M rows, normal, rgb, alpha, refine] per
-// splat; the wavefront sums each component once per (tile, splat) and 17
-// lanes add the sums to v_combined [N,17].
+// splat; a 17-component reduce-scatter (reduce_scatter17) leaves each
+// component's wave sum in one lane, and those 17 lanes add the sums to
+// v_combined [N,17].
 template <bool SMOOTH>
 __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) {
     __shared__ float4 s_s[BWD_BATCH * 4];   // M rows, centre, normal (vs_surfel.h layout)
@@ -559,6 +594,7 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
         }
     }
     const float cut_lo = ALPHA_MID - 0.5f * ALPHA_BAND;
+    const int comp = (lane & 1u) ? -1 : scatter_component17(lane);   // the gradient component this lane adds
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
         bool any_alive = false;
@@ -653,16 +689,9 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
                 T[k] = nt;
             }
             if (__ballot(contrib) == 0ull) continue;          // uniform: gs is zero in every lane
-            float mine = 0.0f;
-#pragma unroll
-            for (int c = 0; c < SURFEL_GRADS; ++c) {
-                float v = gs[c];
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-                if ((int)lane == c) mine = v;
-            }
-            if (lane < (uint32_t)SURFEL_GRADS && mine != 0.0f)
-                atomicAdd(&a.v_combined[(size_t)s_gid[t] * SURFEL_GRADS + lane], mine);
+            const float mine = reduce_scatter17(gs, lane);
+            if (comp >= 0 && mine != 0.0f)
+                atomicAdd(&a.v_combined[(size_t)s_gid[t] * SURFEL_GRADS + comp], mine);
         }
     }
 }
