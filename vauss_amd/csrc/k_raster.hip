@@ -642,7 +642,9 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
                 contrib = true;
                 const float z = h.z;
                 const float m = dist_depth(z);
-                const float dm_dz = (z > 0.2f) ? 100.0f / (100.0f - 0.2f) * 0.2f / (z * z) : 0.0f;
+                // gradient-only quotients and roots take the hardware reciprocal and
+                // square root (1 ulp); the replayed forward above keeps IEEE division
+                const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
                 const float Tk = T[k];
                 const float vis = ae * Tk;
                 gs[12] += (col_r >= 0.0f) ? vis * vr[k] : 0.0f;
@@ -667,7 +669,7 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
                 const float v_sv = (use_3d ? v_sigma * h.sv : 0.0f) + v_z * r2y;
                 const float v_cx = use_3d ? 0.0f : -2.0f * v_sigma * h.dxs;
                 const float v_cy = use_3d ? 0.0f : -2.0f * v_sigma * h.dys;
-                const float inv_qz = 1.0f / h.qz;
+                const float inv_qz = __builtin_amdgcn_rcpf(h.qz);
                 const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * h.su + v_sv * h.sv) * inv_qz;
                 // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
                 const float vhux = h.hvy * vqz - h.hvz * vqy, vhuy = h.hvz * vqx - h.hvx * vqz, vhuz = h.hvx * vqy - h.hvy * vqx;
@@ -682,7 +684,7 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
                 const float shx = g0 * r2x + g1 * r2y + g2 * r2z;
                 const float shy = g3 * r2x + g4 * r2y + g5 * r2z;
                 const float ux = shx * img_w, uy = shy * img_h;
-                gs[16] += __builtin_sqrtf(ux * ux + uy * uy) * rscale[k];
+                gs[16] += __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale[k];
                 sr[k] -= vis * cl_r; sg[k] -= vis * cl_g; sb[k] -= vis * cl_b;
                 sz[k] -= vis * z; snx[k] -= vis * nrm_x; sny[k] -= vis * nrm_y; snz[k] -= vis * nrm_z;
                 sdb[k] -= vis * m; sdc[k] -= vis * m * m;
