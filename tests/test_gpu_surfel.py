@@ -147,3 +147,29 @@ def test_surfel_rejections():
     rows = torch.zeros((500, 4, 3), device="cuda")
     with pytest.raises(va.VsError):                 # surfels take SH colour
         va.render(cam, w.img_size, t, rows, o, render_mode=SURFEL, decoder=torch.zeros(816, device="cuda"))
+
+
+def test_surfel_floor_background_f16():
+    """Surfels under the scale floor, a background (colour composites over it,
+    the geometry channels do not) and f16 SH rows."""
+    w = scenes.workload("c2", 20_000)
+    sc = w.scene
+    cam = w.cameras[0].uniforms(w.img_size)
+    t, _, o = to_gpu(sc)
+    sh16 = sc.sh_coeffs.astype(np.float16)
+    s = torch.from_numpy(sh16).cuda()
+    floor = np.random.default_rng(23).uniform(0.0, 0.02, sc.num_splats).astype(np.float32)
+    floor_gpu = torch.from_numpy(floor).cuda()
+    bg = (0.7, 0.3, 0.1)
+    print("[case] surfel c2 floor + background + f16", flush=True)
+    out = va.render(cam, w.img_size, t, s, o, background=bg, render_mode=SURFEL, min_scale=floor_gpu)
+    ref = po.render_forward(cam, w.img_size, sc.transforms, sh16.astype(np.float32), sc.raw_opacities,
+                            background=bg, flags=_flags(va.RasterPass.BACKWARD), min_scale=floor)
+    _check_surfel_rows(out, ref)
+    img = out.out_img.cpu().numpy()
+    np.testing.assert_array_equal(img.view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))
+    v_out = l1_cotangent_np(img, scenes.loss_target(w.img_size))
+    g = va.render_backward(out, t, s, o, torch.from_numpy(v_out).cuda(), min_scale=floor_gpu)
+    rg = ref.backward(v_out)
+    _check_surfel_grads(g, rg, ref, g.v_combined.cpu().numpy())
+    out.state.free()
