@@ -328,7 +328,9 @@ def main() -> int:
     roofline = {"bound": "hbm", "kernel": dom.replace("_ms", ""), "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "traffic_source": traffic_note, "alg_bytes_per_launch": dom_bytes,
-                "ms_per_launch": round(dom_ms, 4)}
+                "ms_per_launch": round(dom_ms, 4),
+                # the same kernel's event time in the exact-count stage pass (one view at a time)
+                "ms_per_launch_exact_pass": round(per_launch[dom], 4)}
     # The raster kernels are bound by VALU instruction issue, not HBM: their
     # wave instructions per launch (counter summary) over the live launch
     # time, against MI355X's FP32 issue rate (256 CUs x 4 SIMDs x 2.4 GHz / 4

@@ -587,7 +587,8 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     if (vc && ((uintptr_t)vc & 7u)) return fail(VS_ERR_INVALID, "v_combined must be 8-byte aligned");
     {
         VS_HIP(launch_fill_f32(vc, 0.0f, (uint64_t)N * n_grads, s), "zero v_combined");
-        StageTimer tm(ctx, ST_RASTER_BWD);
+        // The raster backward's stage time is its kernel's own execution: the
+        // launch records the two events around the dispatch.
         if (st->I > 0) {
             RasterBwdArgs rb{};
             rb.img_w = st->W; rb.img_h = st->H; rb.tile_bw = st->tbw; rb.tile_bh = st->tbh; rb.num_tiles = st->T;
@@ -598,7 +599,10 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             rb.channels = (st->pass == VS_PASS_GEOMETRY || st->surfel) ? 12u : 4u;
             rb.proj_surf = st->proj_surf;
             rb.v_combined = vc;
-            VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s), "raster backward");
+            hipEvent_t eb = nullptr, ee = nullptr;
+            if (ctx->timing & (1u << ST_RASTER_BWD)) { eb = ctx->take(); ee = ctx->take(); }
+            VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s, eb, ee), "raster backward");
+            if (eb) ctx->recs.push_back(vs_ctx::Rec{(int)ST_RASTER_BWD, eb, ee});
         }
     }
     // With no dense gradient requested the backward stops at the raster

@@ -24,6 +24,7 @@
 // components in registers, and the wavefront reduce-scatters them with
 // permlane swaps and DPP (no LDS traffic), so each (tile, splat) pair issues
 // one atomic instruction of at most ten lanes.
+#include <hip/hip_ext.h>
 #include "vs_device.h"
 #include "vs_surfel.h"
 #include "vs_internal.h"
@@ -739,14 +740,14 @@ hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, 
     return hipGetLastError();
 }
 
-hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s) {
+hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
     if (a.num_tiles == 0) return hipSuccess;
     const dim3 grid(xcd_grid(a.num_tiles));
-    if (a.proj_surf) {
-        if (smooth) raster_bwd_surfel_kernel<true><<<grid, 64, 0, s>>>(a);
-        else raster_bwd_surfel_kernel<false><<<grid, 64, 0, s>>>(a);
-    } else if (smooth) raster_bwd_kernel<true><<<grid, 64, 0, s>>>(a);
-    else raster_bwd_kernel<false><<<grid, 64, 0, s>>>(a);
+    void (*k)(RasterBwdArgs);
+    if (a.proj_surf) k = smooth ? raster_bwd_surfel_kernel<true> : raster_bwd_surfel_kernel<false>;
+    else k = smooth ? raster_bwd_kernel<true> : raster_bwd_kernel<false>;
+    if (start) hipExtLaunchKernelGGL(k, grid, dim3(64), 0, s, start, stop, 0u, a);
+    else k<<<grid, 64, 0, s>>>(a);
     return hipGetLastError();
 }
 

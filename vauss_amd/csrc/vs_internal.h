@@ -240,7 +240,10 @@ hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
 hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
                               const uint32_t* n_dev = nullptr);
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
-hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s);
+// With `start` and `stop` set, the kernel is launched by hipExtLaunchKernelGGL,
+// which records the two events around the kernel's own execution.
+hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s, hipEvent_t start = nullptr,
+                             hipEvent_t stop = nullptr);
 hipError_t launch_project_bwd(const ProjectBwdArgs& a, hipStream_t s);
 hipError_t launch_project_update(const ProjectUpdateArgs& a, hipStream_t s);
 // Camera gradient: per-splat rows summed per 256-splat block, then the blocks (in order).
