@@ -251,7 +251,8 @@ typedef struct vs_state_view {
     const float* proj_b;            /* [N] b */
     const float* proj_aux;          /* [N,4] z, nx, ny, nz (GEOMETRY) or NULL */
     const uint32_t* tile_ranges;    /* [T,2] before the forward shrank the ends */
-    const float* proj_surf;         /* [N,16] surfels: M rows (9), low-pass centre (2), normal (3), 2 pad;
+    const float* proj_surf;         /* [N,16] surfels: M rows (9), low-pass centre (2), normal (3),
+                                       the raster's footprint bound on sigma, 1 pad;
                                        else NULL */
 } vs_state_view;
 vs_status vs_fwd_state_view(const vs_fwd_state* state, vs_state_view* out);

@@ -310,7 +310,10 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
                 o[0] = make_float4(sp.r0.x, sp.r0.y, sp.r0.z, sp.r1.x);
                 o[1] = make_float4(sp.r1.y, sp.r1.z, sp.r2.x, sp.r2.y);
                 o[2] = make_float4(sp.r2.z, cx_, cy_, nrm.x);
-                o[3] = make_float4(nrm.y, nrm.z, 0.0f, 0.0f);
+                // the raster kernels' footprint bound: sigma beyond it leaves alpha
+                // below the lowest cutoff (ALPHA_MID - ALPHA_BAND / 2) by a factor e^-1e-3
+                const float smax = logf_c(opac / (ALPHA_MID - 0.5f * ALPHA_BAND)) + 1.0e-3f;
+                o[3] = make_float4(nrm.y, nrm.z, smax, 0.0f);
             }
             if constexpr (GEOM) {
                 // kernels/project_visible.rs:271-289

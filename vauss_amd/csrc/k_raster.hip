@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
             const float4 sb = s_b[t];
             float sigma, zs = 0.0f;
             if constexpr (SURF) {
-                const SurfelHit hit = surfel_hit(s_s[4 * t], s_s[4 * t + 1], s_s[4 * t + 2], pcx, pcy);
+                const SurfelHit hit = surfel_hit(s_s[4 * t], s_s[4 * t + 1], s_s[4 * t + 2], s_s[4 * t + 3].z, pcx, pcy);
                 if (!hit.valid) continue;       // the ray misses the plane or meets it before the near limit
                 sigma = hit.sigma;
                 zs = hit.z;
@@ -631,7 +631,7 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
 #pragma unroll
             for (int k = 0; k < BWD_PX; ++k) {
                 if (!(T[k] > T_STOP)) continue;
-                const SurfelHit h = surfel_hit(m0, m1, m2, pcx[k], pcy[k]);
+                const SurfelHit h = surfel_hit(m0, m1, m2, m3.z, pcx[k], pcy[k]);
                 if (!(h.valid && h.sigma <= sigma_max)) continue;
                 const float G = expf_neg(-h.sigma);
                 const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);

@@ -70,9 +70,14 @@ VS_DEV F3 surfel_normal(Qt q, F3 mc, const vs_camera& u) {
 // h_v = M1 - y M2, q = h_u x h_v, (u, v) = (q.x, q.y) / q.z, depth
 // z = M2 . (u, v, 1); the low-pass offsets from the projected centre; sigma =
 // min(u^2 + v^2, 2 |pixel - centre|^2) / 2.  `m` is the staged row: M rows
-// (m0.xyzw, m1.xyzw, m2.x), centre (m2.yz), normal (m2.w, m3.xy).
+// (m0.xyzw, m1.xyzw, m2.x), centre (m2.yz), normal (m2.w, m3.xy); `smax`
+// (m3.z) bounds the footprint.  A pixel whose two sigma candidates both
+// certainly exceed smax (u^2 + v^2 tested as q.x^2 + q.y^2 against
+// 2 smax q.z^2 with a 2e-4 margin, far above the few ulp of the divided
+// form) comes back invalid before the divisions: such a pair has alpha below
+// every cutoff, so skipping it changes no result.
 struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
-VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float px, float py) {
+VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float px, float py) {
     SurfelHit h;
     const float m20 = m1.z, m21 = m1.w, m22 = m2.x;
     h.hux = m0.x - px * m20; h.huy = m0.y - px * m21; h.huz = m0.z - px * m22;
@@ -80,13 +85,15 @@ VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float px, float py)
     const float qx = h.huy * h.hvz - h.huz * h.hvy;
     const float qy = h.huz * h.hvx - h.hux * h.hvz;
     h.qz = h.hux * h.hvy - h.huy * h.hvx;
+    h.dxs = px - m2.y;
+    h.dys = py - m2.z;
+    h.s2d = 2.0f * (h.dxs * h.dxs + h.dys * h.dys);
+    h.valid = false;
+    if (0.5f * h.s2d > smax && qx * qx + qy * qy > (2.0004f * smax) * (h.qz * h.qz)) return h;
     h.su = qx / h.qz;
     h.sv = qy / h.qz;
     h.s3d = h.su * h.su + h.sv * h.sv;
     h.z = m20 * h.su + m21 * h.sv + m22;
-    h.dxs = px - m2.y;
-    h.dys = py - m2.z;
-    h.s2d = 2.0f * (h.dxs * h.dxs + h.dys * h.dys);
     h.sigma = 0.5f * mn(h.s3d, h.s2d);
     h.valid = finite(h.z) && h.z >= SURFEL_NEAR;
     return h;
