@@ -79,6 +79,94 @@ def test_tile_hit_test_is_conservative(name, scene, img, model):
     np.testing.assert_array_equal(np.bincount(f.get(po.F_ISECT_GID), minlength=scene.num_splats), counts)
 
 
+def _rect_min_sigma(mx, my, a, b, c, x0, y0, x1, y1):
+    """float64 minimum of sigma = (a dx^2 + c dy^2)/2 + b dx dy (d = p - mean) over
+    the rectangle [x0, x1] x [y0, y1], for positive-definite conics: 0 when the
+    mean lies inside, otherwise the least of the four edges' minima (sigma is
+    convex along each edge, so each edge minimum is its clamped stationary
+    point).  All arguments broadcast."""
+    def edge(u, lo, hi, p, q, r):
+        # sigma(u, t) = p u^2 / 2 + q u t + r t^2 / 2 on t in [lo, hi]
+        t = np.clip(-q * u / r, lo, hi)
+        return 0.5 * p * u * u + q * u * t + 0.5 * r * t * t
+    ux0, ux1, uy0, uy1 = x0 - mx, x1 - mx, y0 - my, y1 - my
+    m = np.minimum.reduce([edge(ux0, uy0, uy1, a, b, c), edge(ux1, uy0, uy1, a, b, c),
+                           edge(uy0, ux0, ux1, c, b, a), edge(uy1, ux0, ux1, c, b, a)])
+    inside = (ux0 <= 0) & (ux1 >= 0) & (uy0 <= 0) & (uy1 >= 0)
+    return np.where(inside, 0.0, m)
+
+
+def _view_z64(cam, transforms):
+    """float64 view-space z of every splat mean: row 2 of the 3x4 world-to-camera
+    matrix (column-major in vs_camera.viewmat) applied to (x, y, z, 1)."""
+    vm = np.array(cam.viewmat, np.float64).reshape(4, 3).T
+    means = transforms[:, 0:3].astype(np.float64)
+    return means @ vm[2, :3] + vm[2, 3]
+
+
+def _pin_cases():
+    return _cases() + [("c1", scenes.scene_c1(), (256, 256), None)]
+
+
+@pytest.mark.parametrize("name,scene,img,model", _pin_cases(), ids=[c[0] for c in _pin_cases()])
+def test_tile_hits_equal_exact_rectangle_test(name, scene, img, model):
+    """Each (tile, splat) pair the oracle emits, and each it does not, against a
+    float64 exact ellipse-rectangle test: the minimum of sigma over the tile's
+    pixel rectangle [16 tx, 16 tx + 16] x [16 ty, 16 ty + 16] against
+    ln(255 opacity) (kernels/helpers.rs:254-314 decide the same set).  Pairs whose
+    minimum lies within 1e-4 (relative) of the threshold may go either way."""
+    if name == "c1":
+        cam = scenes.workload("c1").cameras[0].uniforms(img)
+    else:
+        cam = scenes.test_camera(img, fov=0.5, model=model).uniforms(img)
+    f = _render(scene, cam, img)
+    proj = f.get(po.F_PROJECTED).astype(np.float64)
+    gfc = f.get(po.F_GLOBAL_FROM_COMPACT).astype(np.int64)
+    tbw, tbh = (img[0] + 15) // 16, (img[1] + 15) // 16
+    tx, ty = np.meshgrid(np.arange(tbw), np.arange(tbh))
+    tx, ty = tx.ravel().astype(np.float64), ty.ravel().astype(np.float64)
+    x, y, c00, c01, c11, op = (proj[:, i:i + 1] for i in range(6))
+    power = np.log(255.0 * op)
+    smin = _rect_min_sigma(x, y, c00, c01, c11, 16 * tx[None], 16 * ty[None], 16 * tx[None] + 16, 16 * ty[None] + 16)
+    exact = smin <= power                                           # [V, T]
+    emitted = np.zeros_like(exact)
+    comp_of = np.full(scene.num_splats, -1, np.int64)
+    comp_of[gfc] = np.arange(len(gfc))
+    emitted[comp_of[f.get(po.F_ISECT_GID).astype(np.int64)], f.get(po.F_ISECT_TILE).astype(np.int64)] = True
+    boundary = np.abs(smin - power) <= 1e-4 * np.maximum(np.abs(power), 1.0)
+    wrong = (exact != emitted) & ~boundary
+    assert emitted.sum() > 1000 and (exact & ~emitted).sum() + (emitted & ~exact).sum() <= boundary.sum()
+    assert not wrong.any(), [(int(gfc[c]), int(t), bool(emitted[c, t])) for c, t in zip(*np.nonzero(wrong))][:10]
+    # and every splat's count is its number of emitted tiles
+    counts = f.get(po.F_INTERSECT_COUNTS)
+    np.testing.assert_array_equal(counts[gfc], emitted.sum(axis=1))
+
+
+@pytest.mark.parametrize("name,scene,img,model", _pin_cases(), ids=[c[0] for c in _pin_cases()])
+def test_depth_keys_are_view_z(name, scene, img, model):
+    """The depth key (render.rs:689-694) is view-space z: each visible splat's
+    key is within 2 ulp of the f32 rounding of the float64 (W x + t).z, and the
+    sorted list is ordered by it within every tile."""
+    if name == "c1":
+        cam = scenes.workload("c1").cameras[0].uniforms(img)
+    else:
+        cam = scenes.test_camera(img, fov=0.5, model=model).uniforms(img)
+    f = _render(scene, cam, img)
+    gfc = f.get(po.F_GLOBAL_FROM_COMPACT).astype(np.int64)
+    z64 = _view_z64(cam, scene.transforms)
+    key = f.get(po.F_DEPTHS)
+    ref = z64[gfc].astype(np.float32)
+    ulp = np.spacing(np.abs(ref))
+    assert (ref > 0).all()
+    np.testing.assert_array_less(np.abs(key.astype(np.float64) - ref.astype(np.float64)), 2.0 * ulp + 1e-30)
+    tile = f.get(po.F_ISECT_TILE).astype(np.int64)
+    zs = z64[f.get(po.F_ISECT_GID).astype(np.int64)]
+    same = tile[1:] == tile[:-1]
+    dz = zs[1:] - zs[:-1]
+    tol = 4.0 * np.spacing(np.abs(zs[1:]).astype(np.float32)).astype(np.float64)
+    assert (dz[same] >= -tol[same]).all()
+
+
 def test_composite_matches_float64_over():
     img = (40, 32)
     scene = scenes.rng_scene(60, 0.9, (-2.3, -1.0), (-1.0, 2.0), 0x5151)
@@ -90,7 +178,11 @@ def test_composite_matches_float64_over():
     f = _render(scene, cam, img, background=bg)
     out = f.get(po.F_OUT_IMG).reshape(-1, 4).astype(np.float64)
     proj = f.get(po.F_PROJECTED).astype(np.float64)
-    order = np.lexsort((f.get(po.F_GLOBAL_FROM_COMPACT), f.get(po.F_DEPTHS)))
+    # front to back by float64 view z (not the oracle's own keys), ties by id
+    gfc = f.get(po.F_GLOBAL_FROM_COMPACT)
+    z64 = _view_z64(cam, scene.transforms)[gfc.astype(np.int64)]
+    assert len(np.unique(z64)) == len(z64)
+    order = np.lexsort((gfc, z64))
     sig, alpha = _pixel_sigma_alpha(proj[order], img)
     assert (proj[:, 6:9] < 0).any()
     rgb = np.maximum(proj[order][:, 6:9], 0.0)
