@@ -27,7 +27,7 @@ FP32_VALU_PEAK_TFLOPS = 157.3    # MI355X vector fp32 (packed) peak
 VALU_ISSUE_PEAK_G = 256 * 4 * 2.4 / 4   # G wave64 VALU instructions/s without packed fp32 (614.4)
 SIMD_CYCLES_G = 256 * 4 * 2.4           # G SIMD cycles/s across the chip
 # Cycles per wave64 instruction by counter class, relative to FP32 add at 4,
-# as vauss_amd/valu_rates measures them on gfx950: FP32 add/mul/fma 4,
+# as the probe vauss_amd/probes/valu_rates.hip measures them on gfx950: FP32 add/mul/fma 4,
 # int32 2, conversions 4, transcendentals 8.  The remainder (moves 2;
 # max/min, compares, selects 4) is bracketed by its two rates.
 VALU_CLASS_CYCLES = {"SQ_INSTS_VALU_ADD_F32": 4, "SQ_INSTS_VALU_MUL_F32": 4, "SQ_INSTS_VALU_FMA_F32": 4,

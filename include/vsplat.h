@@ -200,6 +200,16 @@ vs_status vs_ctx_set_lagged_counts(vs_ctx* ctx, int enable);
  * them overflowed their capacity (either pointer may be NULL). */
 vs_status vs_ctx_settle_lagged_counts(vs_ctx* ctx, uint64_t* renders, uint64_t* overflows);
 
+/* Bound on a one-sweep radix pass's wait for its predecessors' digit counts
+ * (the decoupled look-back): after `polls` polls of an unpublished
+ * predecessor the pass gives up, its output is wrong, and the call that ran
+ * the sort returns VS_ERR_HIP (vs_radix_argsort_*, exact renders; a lagged
+ * render's sorts are reported by the next lagged render at its size or by
+ * vs_ctx_settle_lagged_counts).  0xFFFFFFFF restores the default (2^18).  The
+ * reference's sort has no bounded wait (crates/splat-train-sort/src/lib.rs);
+ * a small limit lets tests drive the give-up path with every kernel exiting. */
+vs_status vs_ctx_set_sort_spin_limit(vs_ctx* ctx, uint32_t polls);
+
 /* ---- camera host math --------------------------------------------------------- */
 
 /* camera.rs:99-116 fov_to_focal / :118-134 focal_to_fov (host, f64).
@@ -363,7 +373,9 @@ vs_status vs_sh_step(vs_ctx* ctx, uint16_t* sh_coeffs, uint32_t num_splats, uint
 /* radix_argsort_skip_low_with_count (crates/splat-train-sort/src/lib.rs:40-189):
  * stable LSD sort of (key, value) pairs by key bits [skip, skip+8*ceil(bits/8)).
  * `n_dev` (device, may be NULL) holds the active count <= n; entries past it
- * are not read or written.  Outputs must not alias inputs. */
+ * are not read or written.  Outputs must not alias inputs.  The call waits
+ * for the sort to finish, so that a pass that gave up (see
+ * vs_ctx_set_sort_spin_limit) is reported here. */
 vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, const uint32_t* vals, uint32_t n,
                                const uint32_t* n_dev, uint32_t skip_bits, uint32_t sorting_bits,
                                uint32_t* out_keys, uint32_t* out_vals);

@@ -140,3 +140,45 @@ def test_empty_inputs():
     assert va.prefix_sum(e).numel() == 0
     k, v = va.radix_argsort(e, e, 32)
     assert k.numel() == 0 and v.numel() == 0
+
+
+def test_lookback_give_up_is_reported_by_the_call():
+    """A one-sweep pass whose look-back gives up (forced from the host with a
+    poll limit of 0: every wait ends at its first unpublished predecessor, and
+    every kernel exits) makes the sort call fail; the flag is cleared, so the
+    next sort with the default limit is correct."""
+    ctx = va.Context.get(torch.device("cuda"))
+    rng = SplitMix64(0x5717)
+    keys = rng.next_u64(30_000_000).astype(np.uint32)
+    vals = np.arange(keys.size, dtype=np.uint32)
+    print(f"[case] sort give-up n={keys.size} spin_limit=0", flush=True)
+    ctx.set_sort_spin_limit(0)
+    try:
+        with pytest.raises(va.VsError, match="gave up"):
+            _sort(keys, vals, 32)
+    finally:
+        ctx.set_sort_spin_limit(None)
+    gk, gv = _sort(keys[:2_000_000], vals[:2_000_000], 32)
+    ek, ev = _expected(keys[:2_000_000], vals[:2_000_000], 32)
+    np.testing.assert_array_equal(gk, ek)
+    np.testing.assert_array_equal(gv, ev)
+
+
+def test_exact_render_reports_a_sort_give_up():
+    """An exact render whose depth or tile sort gave up fails in the same call."""
+    from vauss_amd import scenes
+    wl = scenes.workload("c2")
+    sc = wl.scene
+    t = torch.from_numpy(sc.transforms).cuda()
+    s = torch.from_numpy(sc.sh_coeffs).cuda()
+    o = torch.from_numpy(sc.raw_opacities).cuda()
+    ctx = va.Context.get(t.device)
+    print("[case] c2 exact render with spin_limit=0", flush=True)
+    ctx.set_sort_spin_limit(0)
+    try:
+        with pytest.raises(va.VsError, match="gave up"):
+            va.render(wl.cameras[0], wl.img_size, t, s, o, pass_=va.RasterPass.FLOAT)
+    finally:
+        ctx.set_sort_spin_limit(None)
+    out = va.render(wl.cameras[0], wl.img_size, t, s, o, pass_=va.RasterPass.FLOAT)
+    assert out.aux.num_intersections > 1_000_000

@@ -50,6 +50,7 @@ struct vs_ctx {
     uint32_t* host_counters = nullptr;    // pinned readback of the projection counters (+ CTX_FLAGS words)
     uint32_t* dev_flags = nullptr;        // device: [0] set when a sort look-back gave up waiting
     uint32_t timing = 0;                  // bitmask of timed stages (VS_TIME_*)
+    uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT;   // look-back polls before a one-sweep pass gives up
     // Stage event pairs recorded since the last vs_ctx_stage_times(); the
     // pool is reused, so timing many renders needs no extra synchronisation.
     struct Rec { int stage; hipEvent_t b, e; };
@@ -124,6 +125,27 @@ struct StageTimer {
 
 bool pass_bwd_info(vs_pass p) { return p != VS_PASS_FORWARD; }
 
+const char* const SORT_STALL_MSG =
+    "a radix sort's look-back gave up waiting for a predecessor's counts; its output is wrong";
+
+// The sort-stall flag as copied to ctx->host_counters[CNT_COUNT + ...] behind
+// the last readback: report it (and clear the device word) if set.
+vs_status take_sort_flag(vs_ctx* c) {
+    if (c->host_counters[CNT_COUNT + FLAG_SORT_STALL] == 0u) return VS_OK;
+    c->host_counters[CNT_COUNT + FLAG_SORT_STALL] = 0u;
+    VS_HIP(launch_fill_u32(c->dev_flags, 0u, CTX_FLAGS, c->stream), "flag reset");
+    return fail(VS_ERR_HIP, SORT_STALL_MSG);
+}
+
+// Copy the device flags behind everything enqueued so far and wait for them:
+// a sort that gave up is reported by the call that ran it.
+vs_status sync_sort_flag(vs_ctx* c) {
+    VS_HIP(hipMemcpyAsync(c->host_counters + CNT_COUNT, c->dev_flags, CTX_FLAGS * 4, hipMemcpyDeviceToHost, c->stream),
+           "flag readback");
+    VS_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return take_sort_flag(c);
+}
+
 vs_status check_splats(const vs_splats* sp) {
     if (!sp) return fail(VS_ERR_INVALID, "splats is null");
     if (sp->sh_degree > 4) return fail(VS_ERR_INVALID, "SH degree must be 0..4 (1, 4, 9, 16 or 25 coefficients)");
@@ -194,6 +216,12 @@ extern "C" vs_status vs_ctx_set_stream(vs_ctx* c, void* hip_stream) {
     return VS_OK;
 }
 
+extern "C" vs_status vs_ctx_set_sort_spin_limit(vs_ctx* c, uint32_t polls) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    c->spin_limit = polls == 0xFFFFFFFFu ? SORT_SPIN_LIMIT_DEFAULT : polls;
+    return VS_OK;
+}
+
 extern "C" vs_status vs_ctx_enable_timing(vs_ctx* c, uint32_t stages) {
     if (!c) return fail(VS_ERR_INVALID, "ctx is null");
     if (stages & ~(uint32_t)VS_TIME_ALL) return fail(VS_ERR_INVALID, "unknown stage bit in the timing mask");
@@ -244,8 +272,9 @@ vs_status settle(vs_ctx* ctx, const CapacityKey& k, bool& have, uint32_t& vis, u
     p.live = false;
     const uint32_t* hc = p.host;
     if (hc[CNT_COUNT + FLAG_SORT_STALL] != 0u) {
+        // the lagged render's own sorts: reported by the next call at its key
         VS_HIP(launch_fill_u32(ctx->dev_flags, 0u, CTX_FLAGS, ctx->stream), "flag reset");
-        return fail(VS_ERR_HIP, "an earlier radix sort on this context gave up waiting in its look-back; its output was wrong");
+        return fail(VS_ERR_HIP, std::string("the previous lagged render at this size: ") + SORT_STALL_MSG);
     }
     uint64_t I64 = 0;
     std::memcpy(&I64, hc + CNT_ISECT64, 8);
@@ -432,10 +461,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
                "flag readback");
         VS_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
         const uint32_t* hc = ctx->host_counters;
-        if (hc[CNT_COUNT + FLAG_SORT_STALL] != 0u) {
-            VS_HIP(launch_fill_u32(ctx->dev_flags, 0u, CTX_FLAGS, s), "flag reset");
-            return fail(VS_ERR_HIP, "an earlier radix sort on this context gave up waiting in its look-back; its output was wrong");
-        }
+        vs_status fe = take_sort_flag(ctx);   // a lagged render's sorts, enqueued earlier on this context
+        if (fe != VS_OK) return fe;
         st->V = hc[CNT_VISIBLE];
         st->M = hc[CNT_EMITTERS];
         uint64_t I64 = 0;
@@ -455,6 +482,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         i_dev = st->counters + CNT_BOUNDED;
     }
     const uint32_t I = st->I, M = st->M;
+    hipEvent_t sort_done = nullptr;   // exact renders: the sorts' flag readback
+    struct EventBack { vs_ctx* c; hipEvent_t& e; ~EventBack() { if (e) c->pool.push_back(e); } } sort_done_back{ctx, sort_done};
 
     // ---- binning: compaction, depth sort, slot scan, emission, tile sort ------------
     if (I > 0) {
@@ -490,12 +519,12 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         {
             StageTimer tm(ctx, ST_SORT);
             VS_HIP(radix_sort_pairs(dkeys, dvals, dkeys_sorted, order, M, m_dev, false, 0, depth_bits, ib + o_tmp,
-                                    err, s),
+                                    err, s, ctx->spin_limit),
                    "depth sort");
         }
         {
             StageTimer tm(ctx, ST_EMIT);
-            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order, m_dev), "slot scan");
+            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order, m_dev, N), "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
             ea.counts = st->counts; ea.slot_base = slot_base;
@@ -505,8 +534,17 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         {
             StageTimer tm(ctx, ST_SORT);
             VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, i_dev, false, 0, tile_bits, ib + o_tmp,
-                                    err, s),
+                                    err, s, ctx->spin_limit),
                    "tile sort");
+        }
+        if (!lagged) {
+            // An exact render reports a sort that gave up before it returns: the
+            // flag follows the sorts, and the host waits for it after the raster
+            // is enqueued (the raster still runs behind the wait).
+            VS_HIP(hipMemcpyAsync(ctx->host_counters + CNT_COUNT, ctx->dev_flags, CTX_FLAGS * 4, hipMemcpyDeviceToHost, s),
+                   "flag readback");
+            sort_done = ctx->take();
+            VS_HIP(hipEventRecord(sort_done, s), "hipEventRecord(sorts)");
         }
         {
             StageTimer tm(ctx, ST_RANGES);
@@ -518,7 +556,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     {
         StageTimer tm(ctx, ST_RASTER_FWD);
         RasterArgs ra{};
-        ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T;
+        ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T; ra.num_splats = N;
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
         ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;
         ra.proj_a = st->proj_a; ra.proj_b = st->proj_b; ra.proj_c = st->proj_c; ra.proj_aux = st->proj_aux;
@@ -526,6 +564,11 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass != VS_PASS_BACKWARD) ? 1u : 0u;
         ra.out = out->out_img; ra.visible = st->visible;
         VS_HIP(launch_raster_fwd(ra, bwd_info, geometry, smooth, s), "raster forward");
+    }
+    if (sort_done) {
+        VS_HIP(hipEventSynchronize(sort_done), "hipEventSynchronize(sorts)");
+        vs_status fe = take_sort_flag(ctx);
+        if (fe != VS_OK) return fe;
     }
     if (out->tile_offsets) {
         const uint32_t* src = bwd_info ? st->ranges_shrunk : st->ranges;
@@ -592,6 +635,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
         if (st->I > 0) {
             RasterBwdArgs rb{};
             rb.img_w = st->W; rb.img_h = st->H; rb.tile_bw = st->tbw; rb.tile_bh = st->tbh; rb.num_tiles = st->T;
+            rb.num_splats = N;
             rb.bg_r = st->bg[0]; rb.bg_g = st->bg[1]; rb.bg_b = st->bg[2];
             rb.gids = st->gids; rb.ranges = st->ranges_shrunk;
             rb.proj_a = st->proj_a; rb.proj_b = st->proj_b; rb.proj_c = st->proj_c;
@@ -814,10 +858,10 @@ extern "C" vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, con
     VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, false), ctx->stream), "hipMallocAsync(sort tmp)");
     StageTimer tm(ctx, ST_OTHER);
     hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, n_dev, false, skip_bits, skip_bits + sorting_bits,
-                                    tmp, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream);
+                                    tmp, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream, ctx->spin_limit);
     hipFreeAsync(tmp, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
-    return VS_OK;
+    return sync_sort_flag(ctx);
 }
 
 extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, const uint32_t* vals, uint32_t n,
@@ -832,10 +876,10 @@ extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, con
     VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, true), ctx->stream), "hipMallocAsync(sort tmp)");
     StageTimer tm(ctx, ST_OTHER);
     hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, nullptr, true, 0, sorting_bits, tmp,
-                                    ctx->dev_flags + FLAG_SORT_STALL, ctx->stream);
+                                    ctx->dev_flags + FLAG_SORT_STALL, ctx->stream, ctx->spin_limit);
     hipFreeAsync(tmp, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
-    return VS_OK;
+    return sync_sort_flag(ctx);
 }
 
 extern "C" vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {

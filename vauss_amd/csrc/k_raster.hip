@@ -165,8 +165,11 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
         if (__syncthreads_count(!done) == 0) break;
         const uint32_t rem = min((uint32_t)FWD_BLOCK, hi - start);
         uint32_t qmask = 0;
-        if (l < rem) {
-            const uint32_t gid = a.gids[start + l];
+        const uint32_t gid = (l < rem) ? a.gids[start + l] : 0xFFFFFFFFu;
+        if constexpr (BWD) {
+            if (l < rem) { s_gid[l] = 0u; s_hit[l] = 0u; }
+        }
+        if (gid < a.num_splats) {   // else: past the batch, or a corrupt id (dead slot)
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
             const float4 sa = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
@@ -175,7 +178,7 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
             s_b[l] = sb;
             s_c[l] = mx(a.proj_c[gid], 0.0f);
             if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
-            if constexpr (BWD) { s_gid[l] = gid; s_hit[l] = 0u; }
+            if constexpr (BWD) s_gid[l] = gid;
             if constexpr (SURF) {
                 const float4* ps = a.proj_surf + (size_t)gid * 4;
 #pragma unroll
@@ -458,8 +461,9 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
         if (alive == 0) break;                              // every pixel of the tile is done
         const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
         __syncthreads();
-        if (lane < rem) {
-            const uint32_t gid = a.gids[start + lane];
+        const uint32_t gid = (lane < rem) ? a.gids[start + lane] : 0xFFFFFFFFu;
+        if (lane < rem && gid >= a.num_splats) s_mask[lane] = 0u;   // a corrupt id: no quadrant
+        if (gid < a.num_splats) {
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
             const float4 sa = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
@@ -606,12 +610,19 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
         __syncthreads();
         if (lane < rem) {
             const uint32_t gid = a.gids[start + lane];
-            const float4* ps = a.proj_surf + (size_t)gid * 4;
+            if (gid < a.num_splats) {
+                const float4* ps = a.proj_surf + (size_t)gid * 4;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) s_s[4 * lane + k] = ps[k];
-            const float4 pb = a.proj_b[gid];
-            s_b[lane] = make_float4(pb.y, pb.z, pb.w, a.proj_c[gid]);
-            s_gid[lane] = gid;
+                for (int k = 0; k < 4; ++k) s_s[4 * lane + k] = ps[k];
+                const float4 pb = a.proj_b[gid];
+                s_b[lane] = make_float4(pb.y, pb.z, pb.w, a.proj_c[gid]);
+                s_gid[lane] = gid;
+            } else {   // a corrupt id: zero opacity never reaches the cutoff
+#pragma unroll
+                for (int k = 0; k < 4; ++k) s_s[4 * lane + k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                s_b[lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                s_gid[lane] = 0u;
+            }
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {

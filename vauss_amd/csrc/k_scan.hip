@@ -44,10 +44,14 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t& excl, 
 }
 
 // With a permutation `perm`, element i of the scanned sequence is in[perm[i]]
-// and its result is written to out[perm[i]].
+// and its result is written to out[perm[i]].  Entries at or past
+// `perm_bound` (only a corrupt permutation holds them) read as 0 and are not
+// written, so a bad permutation cannot index out of bounds.
 __device__ __forceinline__ uint32_t scan_load(const uint32_t* __restrict__ in, const uint32_t* __restrict__ perm,
-                                              uint64_t idx) {
-    return perm ? in[perm[idx]] : in[idx];
+                                              uint64_t idx, uint32_t perm_bound) {
+    if (!perm) return in[idx];
+    const uint32_t j = perm[idx];
+    return j < perm_bound ? in[j] : 0u;
 }
 
 // Element count: n, or min(*n_dev, n) when a device count is given.
@@ -58,14 +62,14 @@ __device__ __forceinline__ uint64_t scan_count(uint64_t n, const uint32_t* __res
 __global__ void __launch_bounds__(SCAN_BLOCK) scan_reduce_kernel(const uint32_t* __restrict__ in, uint64_t n_cap,
                                                                  uint32_t* __restrict__ sums,
                                                                  const uint32_t* __restrict__ perm,
-                                                                 const uint32_t* __restrict__ n_dev) {
+                                                                 const uint32_t* __restrict__ n_dev, uint32_t perm_bound) {
     const uint64_t n = scan_count(n_cap, n_dev);
     const uint64_t base = (uint64_t)blockIdx.x * SCAN_TILE;
     uint32_t acc = 0;
 #pragma unroll
     for (int i = 0; i < SCAN_ITEMS; ++i) {
         const uint64_t idx = base + (uint64_t)i * SCAN_BLOCK + threadIdx.x;
-        if (idx < n) acc += scan_load(in, perm, idx);
+        if (idx < n) acc += scan_load(in, perm, idx, perm_bound);
     }
     __shared__ uint32_t s_w[48];
     uint32_t excl;
@@ -76,7 +80,7 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_reduce_kernel(const uint32_t*
 __global__ void __launch_bounds__(SCAN_BLOCK) scan_block_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
                                                                 uint64_t n_cap, const uint32_t* __restrict__ offsets,
                                                                 int inclusive, const uint32_t* __restrict__ perm,
-                                                                const uint32_t* __restrict__ n_dev) {
+                                                                const uint32_t* __restrict__ n_dev, uint32_t perm_bound) {
     const uint64_t n = scan_count(n_cap, n_dev);
     __shared__ uint32_t s_data[SCAN_TILE];
     __shared__ uint32_t s_w[48];
@@ -85,7 +89,7 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_block_kernel(const uint32_t* 
     for (int i = 0; i < SCAN_ITEMS; ++i) {
         const uint32_t li = i * SCAN_BLOCK + threadIdx.x;
         const uint64_t idx = base + li;
-        s_data[li] = (idx < n) ? scan_load(in, perm, idx) : 0u;
+        s_data[li] = (idx < n) ? scan_load(in, perm, idx, perm_bound) : 0u;
     }
     __syncthreads();
     uint32_t v[SCAN_ITEMS];
@@ -106,7 +110,10 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_block_kernel(const uint32_t* 
     for (int i = 0; i < SCAN_ITEMS; ++i) {
         const uint32_t li = i * SCAN_BLOCK + threadIdx.x;
         const uint64_t idx = base + li;
-        if (idx < n) out[perm ? perm[idx] : idx] = s_data[li];
+        if (idx < n) {
+            const uint64_t j = perm ? (uint64_t)perm[idx] : idx;
+            if (!perm || j < perm_bound) out[j] = s_data[li];
+        }
     }
 }
 
@@ -138,28 +145,29 @@ hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_
 }
 
 hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
-                    uint32_t* total_out, hipStream_t s, const uint32_t* perm, const uint32_t* n_dev) {
+                    uint32_t* total_out, hipStream_t s, const uint32_t* perm, const uint32_t* n_dev,
+                    uint32_t perm_bound) {
     if (n == 0) {
         if (total_out) return scan_single_block(tmp, 0, false, total_out, s);
         return hipSuccess;
     }
     const uint64_t blocks = (n + SCAN_TILE - 1) / SCAN_TILE;
     if (blocks == 1) {
-        scan_block_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, out, n, nullptr, inclusive ? 1 : 0, perm, n_dev);
+        scan_block_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, out, n, nullptr, inclusive ? 1 : 0, perm, n_dev, perm_bound);
         if (total_out) {
-            scan_reduce_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm, n_dev);
+            scan_reduce_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm, n_dev, perm_bound);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
             return scan_single_block(tmp, 1, true, total_out, s);
         }
         return hipGetLastError();
     }
-    scan_reduce_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm, n_dev);
+    scan_reduce_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm, n_dev, perm_bound);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     e = scan_single_block(tmp, (uint32_t)blocks, false, total_out, s);
     if (e != hipSuccess) return e;
-    scan_block_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, tmp, inclusive ? 1 : 0, perm, n_dev);
+    scan_block_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, tmp, inclusive ? 1 : 0, perm, n_dev, perm_bound);
     return hipGetLastError();
 }
 

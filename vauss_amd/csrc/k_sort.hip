@@ -250,7 +250,6 @@ constexpr uint32_t ONESWEEP_MAX_KEYS = 1u << 30;       // counts fit the 30-bit 
 constexpr uint32_t OS_AGGREGATE = 1u << 30;            // status: this tile's own count
 constexpr uint32_t OS_PREFIX = 2u << 30;               // status: count of this tile and all before it
 constexpr uint32_t OS_VALUE = (1u << 30) - 1u;
-constexpr uint32_t OS_SPIN_LIMIT = 1u << 18;           // polls before a look-back gives up
 constexpr int MAX_PASSES = 8;
 constexpr int LOOKBACK = VS_LOOKBACK;                  // predecessor statuses read per look-back step
 constexpr uint32_t HIST_BLOCKS = VS_HIST_BLOCKS;
@@ -306,7 +305,7 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
                                                                    K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
                                                                    uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
                                                                    const uint32_t* __restrict__ ghist, uint32_t* status,
-                                                                   uint32_t* err) {
+                                                                   uint32_t* err, uint32_t spin_limit) {
     constexpr uint32_t TILE = BLOCK * ITEMS;
     __shared__ uint32_t wave_hist[BLOCK / 64][256];
     __shared__ uint32_t digit_start[256];
@@ -357,7 +356,7 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
                 if (found) break;
                 j -= used;
                 if (stalled) {
-                    if (++spins > OS_SPIN_LIMIT) { atomicOr(err, 1u); break; }
+                    if (++spins > spin_limit) { atomicOr(err, 1u); break; }
                     __builtin_amdgcn_s_sleep(1);
                 }
             }
@@ -417,7 +416,7 @@ size_t sort_tmp_bytes(uint64_t n, bool key64) {
 template <typename K>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_out, uint32_t* vals_out, uint32_t n,
                             const uint32_t* n_dev, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t* err,
-                            hipStream_t s) {
+                            hipStream_t s, uint32_t spin_limit) {
     if (n == 0) return hipSuccess;
     const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
     const uint32_t passes = (bits + 7) / 8;
@@ -460,10 +459,10 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         if (onesweep) {
             if (small)
                 sort_onesweep_kernel<K, OS_SMALL_BLOCK, OS_SMALL_ITEMS><<<os_tiles, OS_SMALL_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err);
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err, spin_limit);
             else
                 sort_onesweep_kernel<K, OS_BLOCK, OS_ITEMS><<<os_tiles, OS_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err);
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err, spin_limit);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         } else {
@@ -484,12 +483,12 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
 
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
-                            void* tmp, uint32_t* err, hipStream_t s) {
+                            void* tmp, uint32_t* err, hipStream_t s, uint32_t spin_limit) {
     if (key64)
         return sort_impl<uint64_t>(static_cast<const uint64_t*>(keys_in), vals_in, static_cast<uint64_t*>(keys_out),
-                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s);
+                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit);
     return sort_impl<uint32_t>(static_cast<const uint32_t*>(keys_in), vals_in, static_cast<uint32_t*>(keys_out),
-                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s);
+                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit);
 }
 
 } // namespace vs

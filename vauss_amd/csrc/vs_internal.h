@@ -85,6 +85,7 @@ struct EmitArgs {
 
 struct RasterArgs {
     uint32_t img_w, img_h, tile_bw, tile_bh, num_tiles;
+    uint32_t num_splats;             // ids at or past it (only a corrupt list holds them) are skipped
     float bg_r, bg_g, bg_b;
     const uint32_t* gids;            // sorted intersections -> global splat id
     const uint32_t* ranges;          // [T,2]
@@ -101,6 +102,7 @@ struct RasterArgs {
 
 struct RasterBwdArgs {
     uint32_t img_w, img_h, tile_bw, tile_bh, num_tiles;
+    uint32_t num_splats;             // ids at or past it are skipped
     float bg_r, bg_g, bg_b;
     const uint32_t* gids;
     const uint32_t* ranges;          // shrunk ranges
@@ -268,22 +270,27 @@ hipError_t launch_b8_zero_rows(uint32_t* codes, uint32_t n, const uint32_t* rows
 hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float mr, uint32_t* out, hipStream_t s);
 
 // Scans.  `tmp` needs scan_tmp_words(n) u32 words.  With a permutation `perm`
-// (n distinct indices) the scan runs along it: element i of the sequence is
-// in[perm[i]] and its result goes to out[perm[i]].
+// (n distinct indices below `perm_bound`, the length of `in` and `out`) the
+// scan runs along it: element i of the sequence is in[perm[i]] and its
+// result goes to out[perm[i]]; an index at or past perm_bound reads 0 and
+// writes nothing.
 size_t scan_tmp_words(uint64_t n);
 // `n_dev` (device, may be null): only the first min(*n_dev, n) elements are
 // scanned, read and written.
 hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
                     uint32_t* total_out, hipStream_t s, const uint32_t* perm = nullptr,
-                    const uint32_t* n_dev = nullptr);
+                    const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu);
 hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_t* total_out, hipStream_t s);
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
 size_t sort_tmp_bytes(uint64_t n, bool key64);
 // `err` (device word, may be null: then the one-sweep schedule is not used)
-// is or-ed with 1 if a one-sweep look-back gave up waiting.
+// is or-ed with 1 if a one-sweep look-back gave up waiting: after
+// `spin_limit` polls of a predecessor that has not published its counts.
+constexpr uint32_t SORT_SPIN_LIMIT_DEFAULT = 1u << 18;
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
-                            void* tmp, uint32_t* err, hipStream_t s);
+                            void* tmp, uint32_t* err, hipStream_t s,
+                            uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT);
 
 } // namespace vs

@@ -104,6 +104,12 @@ class Context:
         _lib.check(self.lib.vs_ctx_stage_times(self.handle, C.byref(t)))
         return {name: getattr(t, name) for name, _ in _lib.VsStageTimes._fields_}
 
+    def set_sort_spin_limit(self, polls: Optional[int] = None) -> None:
+        """Polls of an unpublished predecessor before a one-sweep radix pass
+        gives up (None: the default).  A pass that gives up makes the call that
+        ran it fail with VS_ERR_HIP."""
+        _lib.check(self.lib.vs_ctx_set_sort_spin_limit(self.handle, 0xFFFFFFFF if polls is None else int(polls)))
+
     def set_lagged_counts(self, on: bool = True) -> None:
         """Training renders (RasterPass.BACKWARD) at an already-seen image size
         run on a capacity hint and device counts without waiting for the GPU;
