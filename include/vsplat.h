@@ -100,14 +100,29 @@ typedef struct vs_splats {
                                        decoder's direction band, 0..3. */
 } vs_splats;
 
-/* RasterPass, crates/splat-train-render/src/gaussian_splats.rs:32-107. */
+/* RasterPass, crates/splat-train-render/src/gaussian_splats.rs:32-107.
+ * Every pass but FORWARD writes a float image and keeps backward state.
+ * Training passes (BACKWARD, BACKWARD_DENSE, EXPOSURE, BACKWARD_FUSED_UPDATE)
+ * use lagged counts when the context enables them (vs_ctx_set_lagged_counts).
+ * BACKWARD_DENSE and EXPOSURE carry the reference's `slot` (RasterPass::
+ * BackwardDense { slot }, Exposure { slot }) in bits 8..15 of the value,
+ * written VS_PASS_SLOT(pass, slot): a render settles the lagged counts of the
+ * previous render at its (width, height, slot), so a step's several renders
+ * at one size keep their capacity hints and pending counts apart
+ * (render.rs:741-747).  Other passes take slot 0. */
 typedef enum vs_pass {
     VS_PASS_FORWARD = 0,            /* packed RGBA8 image [H,W] u32, no backward state */
-    VS_PASS_BACKWARD = 1,           /* float RGBA [H,W,4] + backward state */
+    VS_PASS_BACKWARD = 1,           /* float RGBA [H,W,4] + backward state (training) */
     VS_PASS_FLOAT = 2,              /* float RGBA [H,W,4], exact counts, not differentiated */
     VS_PASS_BACKWARD_SMOOTH_CUTOFF = 3, /* Backward with the C^1 alpha cutoff (gradient checks) */
     VS_PASS_GEOMETRY = 4,           /* float [H,W,12]: RGBA, sum(w z), median z, normal, distortion, median id */
+    VS_PASS_BACKWARD_DENSE = 5,     /* Backward whose dense gradients several renders of a step sum (training, slot) */
+    VS_PASS_EXPOSURE = 6,           /* a training-time forward with no gradient, e.g. exposure sub-renders (slot) */
+    VS_PASS_BACKWARD_FUSED_UPDATE = 7, /* Backward whose vs_render_backward stops at v_combined for vs_project_update */
+    VS_PASS_GEOMETRY_TRAIN_DEPTH = 8,  /* GEOMETRY with the training median (T > 1/2) for surfels too */
+    VS_PASS_SLOT_MASK = 0xFF00      /* bits of the count slot (BACKWARD_DENSE, EXPOSURE) */
 } vs_pass;
+#define VS_PASS_SLOT(pass, slot) ((vs_pass)((uint32_t)(pass) | (((uint32_t)(slot) & 0xFFu) << 8)))
 
 /* SplatRenderMode, gaussian_splats.rs:19-26: DEFAULT (+0.3 2-D blur), MIP
  * (+0.1 blur with opacity compensation, kernels/helpers.rs:227-245) and
@@ -117,7 +132,8 @@ typedef enum vs_pass {
  * pinhole-only (a lens camera renders as the pinhole with its focal length)
  * and take SH colour; every pass but FORWARD writes the 12 geometry channels
  * (RGBA, sum(w z), median z, normal, distortion moments, median id; the
- * median by the surface criterion except in VS_PASS_BACKWARD), and the
+ * median by the surface criterion except in training passes and
+ * VS_PASS_GEOMETRY_TRAIN_DEPTH, gaussian_splats.rs:100-106), and the
  * backward's v_combined rows have 17 components [M rows (9), normal (3),
  * rgb (3), alpha, refine]. */
 typedef enum vs_render_mode { VS_MODE_DEFAULT = 0, VS_MODE_MIP = 1, VS_MODE_SURFEL = 2 } vs_render_mode;
@@ -181,12 +197,13 @@ vs_status vs_ctx_enable_timing(vs_ctx* ctx, uint32_t stages);
 vs_status vs_ctx_stage_times(vs_ctx* ctx, vs_stage_times* out);
 
 /* Lagged counts for training renders (render.rs:38-304, 741-768, 887-915).
- * With `enable` set, a VS_PASS_BACKWARD forward at an image size this context
- * has already rendered sizes its intersection arena from a capacity hint kept
- * per (width, height) and runs every stage after projection on device-resident
- * counts: it never waits for the GPU.  Its vs_render_out counts are then the
- * previous lagged render's at that size (0, 0 for the first), and its own are
- * read by the next one.  A render needing more intersections than the hint
+ * With `enable` set, a training-pass forward (VS_PASS_BACKWARD,
+ * _BACKWARD_DENSE, _EXPOSURE, _BACKWARD_FUSED_UPDATE) at an image size and
+ * count slot this context has already rendered sizes its intersection arena
+ * from a capacity hint kept per (width, height, slot) and runs every stage
+ * after projection on device-resident counts: it never waits for the GPU.
+ * Its vs_fwd_out counts are then the previous lagged render's at that key
+ * (0, 0 for the first), and its own are read by the next one.  A render needing more intersections than the hint
  * keeps the first `capacity` of the depth-ordered list (the farthest splats'
  * tiles are dropped), logs to stderr and grows the hint.  The hint follows
  * the reference's policy: 200-render windows sized to the p99 intersections

@@ -209,3 +209,59 @@ def test_lagged_surfel_render_matches_exact(lagged_ctx):
     assert lagged_ctx.settle_lagged_counts()[1] == 0
     for x in (r0, r1, e1):
         x.state.free()
+
+
+def test_count_slots_keep_renders_apart(lagged_ctx):
+    """Two training renders per step at one size in different count slots
+    (RasterPass::BackwardDense { slot }, Exposure { slot }; render.rs:741-747):
+    each slot keeps its own capacity hint and pending counts.  Slot 1 renders
+    a small-scale cloud, slot 2 the full one: slot 2's lagged render fits its
+    own hint (a single shared hint from slot 1 would overflow it), every lagged
+    render is bit-identical to the exact render, and each reports its own
+    slot's previous counts."""
+    w = scenes.workload("c2", 20_000)
+    sc = w.scene
+    small = sc.transforms.copy()
+    small[:, 7:10] -= 1.0
+    cam = w.cameras[0].uniforms(w.img_size)
+    t, s, o = to_gpu(sc)
+    ts = torch.from_numpy(small).cuda()
+    dense, expo = va.RasterPass.BACKWARD_DENSE, va.RasterPass.EXPOSURE
+    print("[case] c2 n=20000 view 0, slots 1 (small scales) and 2 (full), lagged", flush=True)
+
+    def render(x, pass_, slot, lagged=True):
+        lagged_ctx.set_lagged_counts(lagged)
+        try:
+            return va.render(cam, w.img_size, x, s, o, pass_=pass_, count_slot=slot)
+        finally:
+            lagged_ctx.set_lagged_counts(True)
+
+    a0 = render(ts, dense, 1)                      # exact: seeds slot 1 with the small count
+    b0 = render(t, expo, 2)                        # exact: seeds slot 2 with the full count
+    ea = render(ts, va.RasterPass.BACKWARD, 0, lagged=False)
+    eb = render(t, va.RasterPass.BACKWARD, 0, lagged=False)
+    assert ea.aux.num_intersections * 2 < eb.aux.num_intersections
+    a1 = render(ts, dense, 1)
+    b1 = render(t, expo, 2)
+    assert (a1.aux.num_visible, a1.aux.num_intersections) == (0, 0)
+    assert (b1.aux.num_visible, b1.aux.num_intersections) == (0, 0)
+    cap_a, cap_b = a1.state.view().num_intersections, b1.state.view().num_intersections
+    assert ea.aux.num_intersections <= cap_a < eb.aux.num_intersections <= cap_b, (cap_a, cap_b)
+    for lag, ex in ((a1, ea), (b1, eb)):
+        np.testing.assert_array_equal(lag.out_img.cpu().numpy().view(np.uint32), ex.out_img.cpu().numpy().view(np.uint32))
+        lt, lg, lr, _ = _list(lag)
+        et, eg, er, _ = _list(ex)
+        np.testing.assert_array_equal(lr, er)
+        np.testing.assert_array_equal(lg, eg)
+    a2 = render(ts, dense, 1)                      # reports a1's counts
+    b2 = render(t, expo, 2)                        # reports b1's counts
+    assert (a2.aux.num_visible, a2.aux.num_intersections) == (ea.aux.num_visible, ea.aux.num_intersections)
+    assert (b2.aux.num_visible, b2.aux.num_intersections) == (eb.aux.num_visible, eb.aux.num_intersections)
+    assert lagged_ctx.settle_lagged_counts() == (4, 0)
+    # the fused-update pass is a training pass of slot 0 whose backward stops at the raster gradients
+    f = render(t, va.RasterPass.BACKWARD_FUSED_UPDATE, 0)
+    v_out = torch.from_numpy(l1_cotangent_np(eb.out_img.cpu().numpy(), scenes.loss_target(w.img_size))).cuda()
+    g = va.render_backward(f, t, s, o, v_out)
+    assert g.v_transforms is None and g.v_combined is not None
+    for x in (a0, b0, ea, eb, a1, b1, a2, b2, f):
+        x.state.free()

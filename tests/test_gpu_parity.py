@@ -30,7 +30,7 @@ def _render_both(cfg, n, view, pass_=va.RasterPass.BACKWARD, background=(0.0, 0.
     print(f"[case] {cfg} n={w.scene.num_splats} view={view} pass={pass_.name}", flush=True)
     out = va.render(cam, w.img_size, t, s, o, background=background, pass_=pass_)
     flags = po.FLAG_BWD_INFO if pass_.bwd_info() else 0
-    if pass_ == va.RasterPass.GEOMETRY:
+    if pass_.geometry():
         flags |= po.FLAG_GEOMETRY
     if pass_ == va.RasterPass.BACKWARD_SMOOTH_CUTOFF:
         flags |= po.FLAG_SMOOTH_CUTOFF
@@ -142,8 +142,11 @@ def test_backward_parity(cfg, n, view):
     _check_param_grads(g, rg, ref, vc)
 
 
-def test_geometry_pass_parity():
-    w, _, out, ref = _render_both("c1", None, 0, pass_=va.RasterPass.GEOMETRY)
+@pytest.mark.parametrize("pass_", [va.RasterPass.GEOMETRY, va.RasterPass.GEOMETRY_TRAIN_DEPTH],
+                         ids=["geometry", "geometry_train_depth"])
+def test_geometry_pass_parity(pass_):
+    """Both geometry passes; for gaussians they agree (the surface criterion is surfels' only)."""
+    w, _, out, ref = _render_both("c1", None, 0, pass_=pass_)
     gpu = gpu_state_arrays(out)
     _check_forward(out, ref, gpu)
     gfc = ref.get(po.F_GLOBAL_FROM_COMPACT)

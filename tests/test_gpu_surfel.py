@@ -27,11 +27,11 @@ def _flags(pass_):
     f = po.FLAG_SURFEL
     if pass_.bwd_info():
         f |= po.FLAG_BWD_INFO
-    if pass_ == va.RasterPass.GEOMETRY:
+    if pass_.geometry():
         f |= po.FLAG_GEOMETRY
     if pass_ == va.RasterPass.BACKWARD_SMOOTH_CUTOFF:
         f |= po.FLAG_SMOOTH_CUTOFF
-    if pass_ != va.RasterPass.BACKWARD:          # every pass but the training one takes the surface criterion
+    if pass_.surface_criterion():                # inference passes but GEOMETRY_TRAIN_DEPTH (gaussian_splats.rs:100-106)
         f |= po.FLAG_SURFACE
     return f
 
@@ -55,7 +55,9 @@ def _check_surfel_rows(out, ref):
     np.testing.assert_array_equal(rows.view(np.uint32), ref.get(po.F_SURFEL_AUX).view(np.uint32))
 
 
-PASSES = [va.RasterPass.BACKWARD, va.RasterPass.FLOAT, va.RasterPass.GEOMETRY, va.RasterPass.BACKWARD_SMOOTH_CUTOFF]
+PASSES = [va.RasterPass.BACKWARD, va.RasterPass.FLOAT, va.RasterPass.GEOMETRY, va.RasterPass.BACKWARD_SMOOTH_CUTOFF,
+          va.RasterPass.GEOMETRY_TRAIN_DEPTH, va.RasterPass.EXPOSURE, va.RasterPass.BACKWARD_DENSE,
+          va.RasterPass.BACKWARD_FUSED_UPDATE]
 
 
 @pytest.mark.parametrize("pass_", PASSES, ids=[p.name for p in PASSES])
@@ -69,6 +71,18 @@ def test_surfel_forward_passes(pass_):
     np.testing.assert_array_equal(img.view(np.uint32), rimg.view(np.uint32))
     assert img[..., 3].max() > 0.5 and np.count_nonzero(img[..., 4]) > 1000
     out.state.free()
+
+
+def test_surfel_train_depth_rule_differs_from_the_surface_criterion():
+    """GEOMETRY_TRAIN_DEPTH keeps the training median where GEOMETRY takes the
+    surface criterion: the median channels differ, colour and alpha do not."""
+    _, _, a, _ = _surfel_both("c1", None, 0, va.RasterPass.GEOMETRY)
+    _, _, b, _ = _surfel_both("c1", None, 0, va.RasterPass.GEOMETRY_TRAIN_DEPTH)
+    ia, ib = a.out_img.cpu().numpy(), b.out_img.cpu().numpy()
+    np.testing.assert_array_equal(ia[..., :5].view(np.uint32), ib[..., :5].view(np.uint32))
+    assert (ia[..., 5] != ib[..., 5]).mean() > 0.01
+    a.state.free()
+    b.state.free()
 
 
 def test_surfel_packed_forward():

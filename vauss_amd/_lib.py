@@ -20,7 +20,13 @@ STATUS_NAMES = ["VS_OK", "VS_ERR_INVALID", "VS_ERR_HIP", "VS_ERR_OOM", "VS_ERR_U
                 "VS_ERR_CAPACITY", "VS_ERR_NONFINITE"]
 
 CAMERA_PINHOLE, CAMERA_KB4, CAMERA_RT8, CAMERA_TPF = 0, 1, 2, 3
-PASS_FORWARD, PASS_BACKWARD, PASS_FLOAT, PASS_BACKWARD_SMOOTH_CUTOFF, PASS_GEOMETRY = range(5)
+(PASS_FORWARD, PASS_BACKWARD, PASS_FLOAT, PASS_BACKWARD_SMOOTH_CUTOFF, PASS_GEOMETRY, PASS_BACKWARD_DENSE,
+ PASS_EXPOSURE, PASS_BACKWARD_FUSED_UPDATE, PASS_GEOMETRY_TRAIN_DEPTH) = range(9)
+
+
+def pass_with_slot(pass_: int, slot: int) -> int:
+    """VS_PASS_SLOT: the count slot in bits 8..15 of a vs_pass value."""
+    return int(pass_) | ((int(slot) & 0xFF) << 8)
 MODE_DEFAULT, MODE_MIP, MODE_SURFEL = range(3)
 # stage bits of vs_ctx_enable_timing, in vs_stage_times field order
 TIME_STAGES = ("project", "emit", "sort", "ranges", "raster_fwd", "raster_bwd", "project_bwd", "other")

@@ -123,7 +123,17 @@ struct StageTimer {
     }
 };
 
+// RasterPass predicates, gaussian_splats.rs:60-107 (on the pass kind, the
+// value's low byte).
 bool pass_bwd_info(vs_pass p) { return p != VS_PASS_FORWARD; }
+bool pass_training(vs_pass p) {
+    return p == VS_PASS_BACKWARD || p == VS_PASS_BACKWARD_DENSE || p == VS_PASS_EXPOSURE ||
+           p == VS_PASS_BACKWARD_FUSED_UPDATE;
+}
+bool pass_has_slot(vs_pass p) { return p == VS_PASS_BACKWARD_DENSE || p == VS_PASS_EXPOSURE; }
+bool pass_geometry(vs_pass p) { return p == VS_PASS_GEOMETRY || p == VS_PASS_GEOMETRY_TRAIN_DEPTH; }
+// Surfel depth by the surface criterion: every inference pass but GEOMETRY_TRAIN_DEPTH.
+bool pass_surface_criterion(vs_pass p) { return !pass_training(p) && p != VS_PASS_GEOMETRY_TRAIN_DEPTH; }
 
 const char* const SORT_STALL_MSG =
     "a radix sort's look-back gave up waiting for a predecessor's counts; its output is wrong";
@@ -339,7 +349,13 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     if (W == 0 || H == 0) return fail(VS_ERR_INVALID, "Can't render images with 0 size.");
     if (mode != VS_MODE_DEFAULT && mode != VS_MODE_MIP && mode != VS_MODE_SURFEL)
         return fail(VS_ERR_INVALID, "unknown render mode");
-    if ((int)pass < 0 || (int)pass > (int)VS_PASS_GEOMETRY) return fail(VS_ERR_INVALID, "unknown pass");
+    const uint32_t pass_value = (uint32_t)pass;
+    if (pass_value > 0xFFFFu || (pass_value & 0xFFu) > (uint32_t)VS_PASS_GEOMETRY_TRAIN_DEPTH)
+        return fail(VS_ERR_INVALID, "unknown pass");
+    const uint32_t count_slot = pass_value >> 8;
+    pass = static_cast<vs_pass>(pass_value & 0xFFu);
+    if (count_slot != 0 && !pass_has_slot(pass))
+        return fail(VS_ERR_INVALID, "only VS_PASS_BACKWARD_DENSE and VS_PASS_EXPOSURE take a count slot");
     if (cam->model < VS_CAMERA_PINHOLE || cam->model > VS_CAMERA_TPF)
         return fail(VS_ERR_INVALID, "unknown camera model");
     vs_status vst = check_splats(sp);
@@ -382,7 +398,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     const bool bwd_info = pass_bwd_info(pass);
     const bool surfel = st->surfel != 0u;
     // Surfel renders with backward state always carry the geometry channels (render.rs:471-473).
-    const bool geometry = pass == VS_PASS_GEOMETRY || (surfel && bwd_info);
+    const bool geometry = pass_geometry(pass) || (surfel && bwd_info);
     const bool smooth = pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF;
     const uint32_t nblocks = (N + 255) / 256;
 
@@ -390,9 +406,9 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     // A training render at a size with a capacity hint sizes its intersection
     // arena from it and does not wait for its own counts; it reports the
     // previous training render's at this size.  Other renders stay exact.
-    const CapacityKey key{W, H, 0u};
+    const CapacityKey key{W, H, count_slot};
     const size_t limit = (size_t)std::max<uint64_t>(std::min<uint64_t>((uint64_t)N * T, 0xFFFFFFFFull), 1);
-    const bool training = pass == VS_PASS_BACKWARD;
+    const bool training = pass_training(pass);
     bool have_lag = false;
     uint32_t lag_vis = 0, lag_isects = 0;
     if (ctx->lagged && training) {
@@ -561,7 +577,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;
         ra.proj_a = st->proj_a; ra.proj_b = st->proj_b; ra.proj_c = st->proj_c; ra.proj_aux = st->proj_aux;
         // surfels outside training take the median by the surface criterion (gaussian_splats.rs:100-106)
-        ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass != VS_PASS_BACKWARD) ? 1u : 0u;
+        ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass_surface_criterion(pass)) ? 1u : 0u;
         ra.out = out->out_img; ra.visible = st->visible;
         VS_HIP(launch_raster_fwd(ra, bwd_info, geometry, smooth, s), "raster forward");
     }
@@ -617,6 +633,11 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
         return fail(VS_ERR_INVALID, "neural row gradients must be 16-byte aligned");
     if (((uintptr_t)out_img & 15u) || ((uintptr_t)v_out & 15u)) return fail(VS_ERR_INVALID, "images must be 16-byte aligned");
     if (grads->v_transforms && ((uintptr_t)grads->v_transforms & 7u)) return fail(VS_ERR_INVALID, "v_transforms must be 8-byte aligned");
+    const bool dense = grads->v_transforms || grads->v_sh_coeffs || grads->v_raw_opacities || grads->v_refine_weight ||
+                       grads->v_decoder || grads->v_coeffs_sq;
+    if (st->pass == VS_PASS_BACKWARD_FUSED_UPDATE && (dense || !grads->v_combined))
+        return fail(VS_ERR_INVALID, "a BACKWARD_FUSED_UPDATE render's backward stops at v_combined: pass only "
+                                    "v_combined (gaussian_splats.rs:83-86)");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     hipStream_t s = ctx->stream;
     const uint32_t N = st->N;
@@ -640,7 +661,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             rb.gids = st->gids; rb.ranges = st->ranges_shrunk;
             rb.proj_a = st->proj_a; rb.proj_b = st->proj_b; rb.proj_c = st->proj_c;
             rb.out_img = out_img; rb.v_out = v_out;
-            rb.channels = (st->pass == VS_PASS_GEOMETRY || st->surfel) ? 12u : 4u;
+            rb.channels = (pass_geometry(st->pass) || st->surfel) ? 12u : 4u;
             rb.proj_surf = st->proj_surf;
             rb.v_combined = vc;
             hipEvent_t eb = nullptr, ee = nullptr;
@@ -652,8 +673,6 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     // With no dense gradient requested the backward stops at the raster
     // gradients (the reference's BackwardFusedUpdate pass: vs_project_update
     // then takes v_combined).
-    const bool dense = grads->v_transforms || grads->v_sh_coeffs || grads->v_raw_opacities || grads->v_refine_weight ||
-                       grads->v_decoder || grads->v_coeffs_sq;
     if (dense) {
         StageTimer tm(ctx, ST_PROJECT_BWD);
         ProjectBwdArgs pb{};

@@ -30,20 +30,40 @@ from .camera import Camera
 
 
 class RasterPass(enum.IntEnum):
-    """RasterPass (gaussian_splats.rs:32-107) -- the passes built here."""
+    """RasterPass (gaussian_splats.rs:32-107).  BACKWARD_DENSE and EXPOSURE
+    take the reference's `slot` as render()'s `count_slot`."""
     FORWARD = _lib.PASS_FORWARD
     BACKWARD = _lib.PASS_BACKWARD
     FLOAT = _lib.PASS_FLOAT
     BACKWARD_SMOOTH_CUTOFF = _lib.PASS_BACKWARD_SMOOTH_CUTOFF
     GEOMETRY = _lib.PASS_GEOMETRY
+    BACKWARD_DENSE = _lib.PASS_BACKWARD_DENSE
+    EXPOSURE = _lib.PASS_EXPOSURE
+    BACKWARD_FUSED_UPDATE = _lib.PASS_BACKWARD_FUSED_UPDATE
+    GEOMETRY_TRAIN_DEPTH = _lib.PASS_GEOMETRY_TRAIN_DEPTH
 
     def bwd_info(self) -> bool:
         return self is not RasterPass.FORWARD
 
+    def training(self) -> bool:
+        """Training renders, which use lagged counts when the context enables them."""
+        return self in (RasterPass.BACKWARD, RasterPass.BACKWARD_DENSE, RasterPass.EXPOSURE,
+                        RasterPass.BACKWARD_FUSED_UPDATE)
+
+    def has_slot(self) -> bool:
+        return self in (RasterPass.BACKWARD_DENSE, RasterPass.EXPOSURE)
+
+    def geometry(self) -> bool:
+        return self in (RasterPass.GEOMETRY, RasterPass.GEOMETRY_TRAIN_DEPTH)
+
+    def surface_criterion(self) -> bool:
+        """Surfel depth by the unbiased surface criterion rather than the training median."""
+        return not self.training() and self is not RasterPass.GEOMETRY_TRAIN_DEPTH
+
     def out_channels(self, surfel: bool = False) -> int:
-        """Image channels: 12 for the geometry pass and every surfel pass with
+        """Image channels: 12 for the geometry passes and every surfel pass with
         backward state (render.rs:471-473), 4 for other float passes, 1 packed."""
-        if self is RasterPass.GEOMETRY or (surfel and self.bwd_info()):
+        if self.geometry() or (surfel and self.bwd_info()):
             return 12
         return 4 if self.bwd_info() else 1
 
@@ -111,9 +131,10 @@ class Context:
         _lib.check(self.lib.vs_ctx_set_sort_spin_limit(self.handle, 0xFFFFFFFF if polls is None else int(polls)))
 
     def set_lagged_counts(self, on: bool = True) -> None:
-        """Training renders (RasterPass.BACKWARD) at an already-seen image size
-        run on a capacity hint and device counts without waiting for the GPU;
-        their aux counts are the previous such render's (render.rs:741-768)."""
+        """Training renders (RasterPass.training()) at an already-seen image size
+        and count slot run on a capacity hint and device counts without waiting
+        for the GPU; their aux counts are the previous such render's at that
+        (size, slot) (render.rs:741-768)."""
         _lib.check(self.lib.vs_ctx_set_lagged_counts(self.handle, 1 if on else 0))
 
     def settle_lagged_counts(self) -> tuple:
@@ -270,13 +291,17 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
            raw_opacities: torch.Tensor, background=(0.0, 0.0, 0.0), pass_: RasterPass = RasterPass.BACKWARD,
            render_mode: SplatRenderMode = SplatRenderMode.DEFAULT, log_scale_offset: float = 0.0,
            validate: bool = False, min_scale: Optional[torch.Tensor] = None,
-           decoder: Optional[torch.Tensor] = None, neural_degree: int = 0) -> RenderOutput:
+           decoder: Optional[torch.Tensor] = None, neural_degree: int = 0, count_slot: int = 0) -> RenderOutput:
     """SplatOps::render (SplatOps::render_neural with `decoder`).  `camera` is
     a Camera or ready-made vs_camera uniforms.  `render_mode` DEFAULT or MIP;
     `min_scale` [N] is the scale floor (render's min_scale with
     has_min_scale), None for none.  With `decoder` [816] the colour comes from
     the compact neural appearance: `sh_coeffs` holds [N,4,3] rows (base,
     latent, pad) and `neural_degree` (0..3) is its direction band.
+
+    `count_slot` (0..255) is the slot of a BACKWARD_DENSE or EXPOSURE pass
+    (RasterPass::BackwardDense { slot }): its lagged counts stay apart from
+    the step's other renders at the same size.
 
     Returns the image ([H,W,C] f32, or [H,W] int32-packed RGBA8 for
     FORWARD), the aux outputs and, for every pass but FORWARD, the state the
@@ -285,6 +310,10 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     if w <= 0 or h <= 0:
         raise ValueError("Can't render images with 0 size.")
     pass_ = RasterPass(pass_)
+    if count_slot and not pass_.has_slot():
+        raise ValueError("only BACKWARD_DENSE and EXPOSURE passes take a count slot")
+    if not 0 <= int(count_slot) <= 255:
+        raise ValueError("count_slot must be 0..255")
     transforms = transforms.contiguous()
     sh_coeffs = sh_coeffs.contiguous()
     raw_opacities = raw_opacities.contiguous()
@@ -317,8 +346,9 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale, decoder)
     bg = (C.c_float * 3)(*[float(v) for v in background])
     st = C.c_void_p()
-    _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg, int(pass_),
-                                         int(render_mode), C.byref(out), C.byref(st)))
+    _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg,
+                                         _lib.pass_with_slot(pass_, count_slot), int(render_mode), C.byref(out),
+                                         C.byref(st)))
     aux = RenderAux(out.num_visible, out.num_intersections, visible, max_radius, opacities, tile_offsets, (w, h))
     state = ForwardState(st, ctx, pass_, n, degree) if st.value else None
     if state is not None:
@@ -341,6 +371,8 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     [N] are filled."""
     if output.state is None or output.state.handle is None:
         raise ValueError("the forward pass kept no backward state (use a bwd-info pass)")
+    # a BACKWARD_FUSED_UPDATE render's backward always stops at the raster gradients
+    fused = fused or output.state.pass_ is RasterPass.BACKWARD_FUSED_UPDATE
     transforms = transforms.contiguous()
     sh_coeffs = sh_coeffs.contiguous()
     raw_opacities = raw_opacities.contiguous()
