@@ -227,6 +227,26 @@ vs_status vs_ctx_settle_lagged_counts(vs_ctx* ctx, uint64_t* renders, uint64_t* 
  * a small limit lets tests drive the give-up path with every kernel exiting. */
 vs_status vs_ctx_set_sort_spin_limit(vs_ctx* ctx, uint32_t polls);
 
+/* Validation readbacks (crates/splat-train-render/src/validation.rs:1-140;
+ * Splats::validate_values / bwd_validate, gaussian_splats.rs:417-509).  With
+ * `enable` set, vs_render_forward first scans the splat parameters (means,
+ * rotations, log-scales, SH coefficients, raw opacities, the floor and the
+ * decoder when given) and vs_render_backward the gradients it wrote; a NaN or
+ * Inf fails the call with VS_ERR_NONFINITE naming the tensor and its first
+ * bad element (the reference panics), values outside the reference's ranges
+ * (log-scales [-10, 10], SH [-5, 5], raw opacity [-20, 20]) are logged to
+ * stderr.  Each scan synchronises the stream.  Off by default, as in the
+ * reference's release builds; without it, non-finite splats are culled. */
+vs_status vs_ctx_set_validation(vs_ctx* ctx, int enable);
+
+/* Fill every buffer the library allocates for this context with the f32
+ * pattern of -12345.0 before first use, as the reference's test builds
+ * initialise fresh tensors (crates/splat-train-cube/src/host.rs:23-36), so a
+ * kernel reading a slot it never wrote shows up as a wrong result.  A debug
+ * aid; also switched on for new contexts by the environment variable
+ * VSPLAT_POISON=1. */
+vs_status vs_ctx_set_poison(vs_ctx* ctx, int enable);
+
 /* ---- camera host math --------------------------------------------------------- */
 
 /* camera.rs:99-116 fov_to_focal / :118-134 focal_to_fov (host, f64).

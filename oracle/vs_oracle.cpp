@@ -1339,7 +1339,7 @@ extern "C" void or_fwd_get_info(const or_fwd* f, or_fwd_info* info) {
 }
 
 extern "C" int or_fwd_get(const or_fwd* f, int field, void* dst) {
-    auto cp = [&](const auto& v) { std::memcpy(dst, v.data(), v.size() * sizeof(v[0])); return 0; };
+    auto cp = [&](const auto& v) { if (!v.empty()) std::memcpy(dst, v.data(), v.size() * sizeof(v[0])); return 0; };
     switch (field) {
     case OR_F_INTERSECT_COUNTS: return cp(f->intersect_counts);
     case OR_F_MAX_RADIUS: return cp(f->max_radius);

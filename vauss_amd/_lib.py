@@ -105,6 +105,8 @@ SIGNATURES = {
     "vs_last_error": (C.c_char_p, []),
     "vs_version": (C.c_char_p, []),
     "vs_ctx_set_sort_spin_limit": (C.c_int, [C.c_void_p, C.c_uint32]),
+    "vs_ctx_set_validation": (C.c_int, [C.c_void_p, C.c_int]),
+    "vs_ctx_set_poison": (C.c_int, [C.c_void_p, C.c_int]),
     "vs_ctx_enable_timing": (C.c_int, [C.c_void_p, C.c_uint32]),
     "vs_ctx_stage_times": (C.c_int, [C.c_void_p, C.POINTER(VsStageTimes)]),
     "vs_ctx_set_lagged_counts": (C.c_int, [C.c_void_p, C.c_int]),

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <new>
@@ -51,6 +52,10 @@ struct vs_ctx {
     uint32_t* dev_flags = nullptr;        // device: [0] set when a sort look-back gave up waiting
     uint32_t timing = 0;                  // bitmask of timed stages (VS_TIME_*)
     uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT;   // look-back polls before a one-sweep pass gives up
+    bool validate = false;                // scan inputs and gradients for NaN / Inf (vs_ctx_set_validation)
+    bool poison = false;                  // fill every library allocation with POISON_WORD first
+    uint32_t* dev_val = nullptr;          // device: validation counters, VALIDATE_WORDS per check
+    uint32_t* host_val = nullptr;         // pinned mirror of dev_val
     // Stage event pairs recorded since the last vs_ctx_stage_times(); the
     // pool is reused, so timing many renders needs no extra synchronisation.
     struct Rec { int stage; hipEvent_t b, e; };
@@ -156,6 +161,90 @@ vs_status sync_sort_flag(vs_ctx* c) {
     return take_sort_flag(c);
 }
 
+// The f32 bit pattern of -12345.0, the value the reference's test builds add to
+// every fresh tensor (crates/splat-train-cube/src/host.rs:23-36): a kernel that
+// reads a slot it never wrote then sees a value far from any real one.
+constexpr uint32_t POISON_WORD = 0xC640E400u;
+
+// Every buffer the library allocates for itself: stream-ordered, and filled
+// with POISON_WORD first when the context asks for it.
+hipError_t lib_alloc(vs_ctx* c, void** p, size_t bytes, hipStream_t s) {
+    hipError_t e = hipMallocAsync(p, bytes, s);
+    if (e != hipSuccess || !c->poison || bytes < 4) return e;
+    return launch_fill_u32(static_cast<uint32_t*>(*p), POISON_WORD, bytes / 4, s);
+}
+
+// validate_tensor_val (validation.rs:60-140): NaN and Inf are errors, values
+// outside [lo, hi] are logged.
+struct Check {
+    const char* name;
+    const void* p;
+    bool half;
+    uint64_t n;
+    uint32_t row, col0, col1;
+    float lo, hi;
+};
+constexpr int MAX_CHECKS = 8;
+
+vs_status run_checks(vs_ctx* c, const Check* checks, int count) {
+    hipStream_t s = c->stream;
+    for (int i = 0; i < count; ++i) {
+        uint32_t* h = c->host_val + i * VALIDATE_WORDS;
+        for (int w = 0; w < VALIDATE_WORDS; ++w) h[w] = 0u;
+        h[VAL_FIRST_NAN] = h[VAL_FIRST_INF] = 0xFFFFFFFFu;
+    }
+    VS_HIP(hipMemcpyAsync(c->dev_val, c->host_val, (size_t)count * VALIDATE_WORDS * 4, hipMemcpyHostToDevice, s),
+           "validation reset");
+    for (int i = 0; i < count; ++i) {
+        const Check& k = checks[i];
+        VS_HIP(launch_validate(k.p, k.half, k.n, k.row, k.col0, k.col1, k.lo, k.hi, c->dev_val + i * VALIDATE_WORDS, s),
+               "validation scan");
+    }
+    VS_HIP(hipMemcpyAsync(c->host_val, c->dev_val, (size_t)count * VALIDATE_WORDS * 4, hipMemcpyDeviceToHost, s),
+           "validation readback");
+    VS_HIP(hipStreamSynchronize(s), "hipStreamSynchronize(validation)");
+    std::string bad;
+    for (int i = 0; i < count; ++i) {
+        const Check& k = checks[i];
+        const uint32_t* h = c->host_val + i * VALIDATE_WORDS;
+        const uint64_t total = k.n / k.row * (k.col1 - k.col0);
+        if (h[VAL_BELOW])
+            std::fprintf(stderr, "vsplat: tensor '%s': %u values < %g of %llu\n", k.name, h[VAL_BELOW], (double)k.lo,
+                         (unsigned long long)total);
+        if (h[VAL_ABOVE])
+            std::fprintf(stderr, "vsplat: tensor '%s': %u values > %g of %llu\n", k.name, h[VAL_ABOVE], (double)k.hi,
+                         (unsigned long long)total);
+        if (h[VAL_NAN] || h[VAL_INF]) {
+            char msg[256];
+            std::snprintf(msg, sizeof msg, "%stensor '%s' has %u NaN (first @ element %lld), %u Inf (first @ element %lld)",
+                          bad.empty() ? "" : "; ", k.name, h[VAL_NAN],
+                          h[VAL_NAN] ? (long long)h[VAL_FIRST_NAN] : -1LL, h[VAL_INF],
+                          h[VAL_INF] ? (long long)h[VAL_FIRST_INF] : -1LL);
+            bad += msg;
+        }
+    }
+    if (!bad.empty()) return fail(VS_ERR_NONFINITE, bad);
+    return VS_OK;
+}
+
+// Splats::validate_values (gaussian_splats.rs:417-470) on the inputs of a render.
+vs_status validate_splats(vs_ctx* c, const vs_splats* sp) {
+    const uint64_t N = sp->num_splats;
+    if (N == 0) return VS_OK;
+    const uint64_t K = sp->decoder ? 4u : (uint64_t)(sp->sh_degree + 1) * (sp->sh_degree + 1);
+    const float inf = __builtin_inff();
+    Check ch[MAX_CHECKS];
+    int n = 0;
+    ch[n++] = Check{"means", sp->transforms, false, N * 10, 10, 0, 3, -inf, inf};
+    ch[n++] = Check{"rotations", sp->transforms, false, N * 10, 10, 3, 7, -inf, inf};
+    ch[n++] = Check{"log_scales", sp->transforms, false, N * 10, 10, 7, 10, -10.0f, 10.0f};
+    ch[n++] = Check{"sh_coeffs", sp->sh_coeffs, sp->sh_dtype == VS_SH_F16, N * K * 3, 1, 0, 1, -5.0f, 5.0f};
+    ch[n++] = Check{"raw_opacity", sp->raw_opacities, false, N, 1, 0, 1, -20.0f, 20.0f};
+    if (sp->min_scale) ch[n++] = Check{"min_scale", sp->min_scale, false, N, 1, 0, 1, -inf, inf};
+    if (sp->decoder) ch[n++] = Check{"decoder", sp->decoder, false, 816, 1, 0, 1, -inf, inf};
+    return run_checks(c, ch, n);
+}
+
 vs_status check_splats(const vs_splats* sp) {
     if (!sp) return fail(VS_ERR_INVALID, "splats is null");
     if (sp->sh_degree > 4) return fail(VS_ERR_INVALID, "SH degree must be 0..4 (1, 4, 9, 16 or 25 coefficients)");
@@ -194,7 +283,20 @@ extern "C" vs_status vs_ctx_create(int device, void* hip_stream, vs_ctx** out) {
     if (e != hipSuccess) { delete c; return hip_fail(e, "hipHostMalloc"); }
     e = hipMalloc(reinterpret_cast<void**>(&c->dev_flags), CTX_FLAGS * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->dev_flags, 0, CTX_FLAGS * sizeof(uint32_t));
-    if (e != hipSuccess) { hipHostFree(c->host_counters); if (c->dev_flags) hipFree(c->dev_flags); delete c; return hip_fail(e, "context flags"); }
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->dev_val), MAX_CHECKS * VALIDATE_WORDS * sizeof(uint32_t));
+    if (e == hipSuccess)
+        e = hipHostMalloc(reinterpret_cast<void**>(&c->host_val), MAX_CHECKS * VALIDATE_WORDS * sizeof(uint32_t),
+                          hipHostMallocDefault);
+    if (e != hipSuccess) {
+        hipHostFree(c->host_counters);
+        if (c->dev_flags) hipFree(c->dev_flags);
+        if (c->dev_val) hipFree(c->dev_val);
+        delete c;
+        return hip_fail(e, "context buffers");
+    }
+    // VSPLAT_POISON=1 poisons every allocation of this context (a debug aid for test runs).
+    const char* poison_env = std::getenv("VSPLAT_POISON");
+    c->poison = poison_env && poison_env[0] == '1';
     // Keep freed stream-ordered allocations in the pool between renders.
     hipMemPool_t pool;
     if (hipDeviceGetDefaultMemPool(&pool, device) == hipSuccess) {
@@ -216,13 +318,27 @@ extern "C" void vs_ctx_destroy(vs_ctx* c) {
         if (kv.second.host) hipHostFree(kv.second.host);
     }
     hipHostFree(c->host_counters);
+    hipHostFree(c->host_val);
     hipFree(c->dev_flags);
+    hipFree(c->dev_val);
     delete c;
 }
 
 extern "C" vs_status vs_ctx_set_stream(vs_ctx* c, void* hip_stream) {
     if (!c) return fail(VS_ERR_INVALID, "ctx is null");
     c->stream = static_cast<hipStream_t>(hip_stream);
+    return VS_OK;
+}
+
+extern "C" vs_status vs_ctx_set_validation(vs_ctx* c, int enable) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    c->validate = enable != 0;
+    return VS_OK;
+}
+
+extern "C" vs_status vs_ctx_set_poison(vs_ctx* c, int enable) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    c->poison = enable != 0;
     return VS_OK;
 }
 
@@ -366,6 +482,10 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     if (pass_bwd_info(pass) && ((uintptr_t)out->out_img & 15u)) return fail(VS_ERR_INVALID, "out_img must be 16-byte aligned");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     hipStream_t s = ctx->stream;
+    if (ctx->validate) {
+        vs_status ve = validate_splats(ctx, sp);
+        if (ve != VS_OK) return ve;
+    }
 
     vs_fwd_state* st = new (std::nothrow) vs_fwd_state();
     if (!st) return fail(VS_ERR_OOM, "state allocation");
@@ -432,7 +552,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     const size_t o_bs = take((size_t)std::max(nblocks, 1u) * 4 * BS_ROWS);
     const size_t o_cnt = take(CNT_COUNT * 4);
     const size_t o_rng = take((size_t)T * 8), o_rngs = take((size_t)T * 8);
-    VS_HIP(hipMallocAsync(&st->arena, off, s), "hipMallocAsync(splat arena)");
+    VS_HIP(lib_alloc(ctx, &st->arena, off, s), "hipMallocAsync(splat arena)");
     char* base = static_cast<char*>(st->arena);
     st->counts = reinterpret_cast<uint32_t*>(base + o_counts);
     st->depth_bits = reinterpret_cast<uint32_t*>(base + o_depth);
@@ -511,7 +631,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)N * 4);
         const size_t o_scan = itake(scan_tmp_words(M) * 4);
         const size_t o_tmp = itake(sort_tmp_bytes(std::max(I, M), false));   // serves both sorts
-        VS_HIP(hipMallocAsync(&st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
+        VS_HIP(lib_alloc(ctx, &st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
         char* ib = static_cast<char*>(st->isect_arena);
         uint32_t* tiles_u = reinterpret_cast<uint32_t*>(ib + o_tu);
         uint32_t* vals_u = reinterpret_cast<uint32_t*>(ib + o_vu);
@@ -645,7 +765,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     void* vc_alloc = nullptr;
     const uint32_t n_grads = st->surfel ? 17u : 10u;      // raster gradient components per splat
     if (!vc && N > 0) {
-        VS_HIP(hipMallocAsync(&vc_alloc, (size_t)N * n_grads * 4, s), "hipMallocAsync(v_combined)");
+        VS_HIP(lib_alloc(ctx, &vc_alloc, (size_t)N * n_grads * 4, s), "hipMallocAsync(v_combined)");
         vc = static_cast<float*>(vc_alloc);
     }
     if (vc && ((uintptr_t)vc & 7u)) return fail(VS_ERR_INVALID, "v_combined must be 8-byte aligned");
@@ -691,7 +811,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             nb.v_transforms = grads->v_transforms; nb.v_rows = grads->v_sh_coeffs; nb.v_rows_sq = grads->v_coeffs_sq;
             nb.v_decoder = grads->v_decoder;
             void* part = nullptr;
-            VS_HIP(hipMallocAsync(&part, (size_t)neural_bwd_blocks(N) * 816 * sizeof(float), s),
+            VS_HIP(lib_alloc(ctx, &part, (size_t)neural_bwd_blocks(N) * 816 * sizeof(float), s),
                    "hipMallocAsync(decoder partials)");
             nb.partials = static_cast<float*>(part);
             const hipError_t e = launch_neural_bwd(nb, s);
@@ -699,8 +819,22 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             VS_HIP(e, "neural backward");
         }
     }
+    vs_status ve = VS_OK;
+    if (ctx->validate && N > 0) {
+        // bwd_validate (gaussian_splats.rs:475-509): the parameter gradients, or
+        // the raster gradients when the backward stops there
+        const uint32_t K = st->neural ? 4u : (st->degree + 1) * (st->degree + 1);
+        const float inf = __builtin_inff();
+        Check ch[MAX_CHECKS];
+        int n = 0;
+        if (grads->v_transforms) ch[n++] = Check{"gradient_transforms", grads->v_transforms, false, (uint64_t)N * 10, 1, 0, 1, -inf, inf};
+        if (grads->v_sh_coeffs) ch[n++] = Check{"gradient_sh_coeffs", grads->v_sh_coeffs, false, (uint64_t)N * K * 3, 1, 0, 1, -inf, inf};
+        if (grads->v_raw_opacities) ch[n++] = Check{"gradient_raw_opacities", grads->v_raw_opacities, false, N, 1, 0, 1, -inf, inf};
+        if (!dense) ch[n++] = Check{"gradient_v_combined", vc, false, (uint64_t)N * n_grads, 1, 0, 1, -inf, inf};
+        ve = run_checks(ctx, ch, n);
+    }
     if (vc_alloc) VS_HIP(hipFreeAsync(vc_alloc, s), "hipFreeAsync(v_combined)");
-    return VS_OK;
+    return ve;
 }
 
 extern "C" vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_splats* sp, const float* v_combined,
@@ -725,7 +859,7 @@ extern "C" vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_sp
     pa.mip = st->mip; pa.raw_opac = sp->raw_opacities; pa.v_combined = v_combined; pa.v_pose = v_pose;
     void* part = nullptr;
     const uint32_t nb = pose_bwd_blocks(st->N);
-    if (nb > 0) VS_HIP(hipMallocAsync(&part, (size_t)nb * 12 * sizeof(float), s), "hipMallocAsync(pose partials)");
+    if (nb > 0) VS_HIP(lib_alloc(ctx, &part, (size_t)nb * 12 * sizeof(float), s), "hipMallocAsync(pose partials)");
     pa.partials = static_cast<float*>(part);
     const hipError_t e = launch_pose_bwd(pa, s);
     if (part) hipFreeAsync(part, s);
@@ -874,7 +1008,7 @@ extern "C" vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, con
     if (keys == out_keys || vals == out_vals) return fail(VS_ERR_INVALID, "outputs must not alias inputs");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     void* tmp = nullptr;
-    VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, false), ctx->stream), "hipMallocAsync(sort tmp)");
+    VS_HIP(lib_alloc(ctx, &tmp, sort_tmp_bytes(n, false), ctx->stream), "hipMallocAsync(sort tmp)");
     StageTimer tm(ctx, ST_OTHER);
     hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, n_dev, false, skip_bits, skip_bits + sorting_bits,
                                     tmp, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream, ctx->spin_limit);
@@ -892,7 +1026,7 @@ extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, con
     if (keys == out_keys || vals == out_vals) return fail(VS_ERR_INVALID, "outputs must not alias inputs");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     void* tmp = nullptr;
-    VS_HIP(hipMallocAsync(&tmp, sort_tmp_bytes(n, true), ctx->stream), "hipMallocAsync(sort tmp)");
+    VS_HIP(lib_alloc(ctx, &tmp, sort_tmp_bytes(n, true), ctx->stream), "hipMallocAsync(sort tmp)");
     StageTimer tm(ctx, ST_OTHER);
     hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, nullptr, true, 0, sorting_bits, tmp,
                                     ctx->dev_flags + FLAG_SORT_STALL, ctx->stream, ctx->spin_limit);
@@ -907,7 +1041,7 @@ extern "C" vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t
     if (!in || !out) return fail(VS_ERR_INVALID, "null buffer");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     void* tmp = nullptr;
-    VS_HIP(hipMallocAsync(&tmp, scan_tmp_words(n) * 4, ctx->stream), "hipMallocAsync(scan tmp)");
+    VS_HIP(lib_alloc(ctx, &tmp, scan_tmp_words(n) * 4, ctx->stream), "hipMallocAsync(scan tmp)");
     hipError_t e = scan_u32(in, out, n, true, static_cast<uint32_t*>(tmp), nullptr, ctx->stream);
     hipFreeAsync(tmp, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "prefix sum");
@@ -979,7 +1113,7 @@ extern "C" vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint
     if (!coeffs) {
         // No stored coefficients: the forward recomputes them (the reference's
         // recomputing backward blurs the same quantities in the same order).
-        VS_HIP(hipMallocAsync(&tmp, (size_t)9 * img_w * img_h * 4, s), "hipMallocAsync(loss coefficients)");
+        VS_HIP(lib_alloc(ctx, &tmp, (size_t)9 * img_w * img_h * 4, s), "hipMallocAsync(loss coefficients)");
         LossArgs f = a;
         f.coeffs = static_cast<float*>(tmp);
         hipError_t e = launch_loss_forward(f, s);

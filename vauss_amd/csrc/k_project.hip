@@ -14,6 +14,7 @@
 // global-id order) writes one u32 tile id per hit tile into that range.  A
 // stable sort by tile id then yields each tile's list in (depth bits, global
 // id) order.
+#include <algorithm>
 #include "vs_device.h"
 #include "vs_camera.h"
 #include "vs_sh.h"
@@ -555,6 +556,38 @@ hipError_t launch_compact(const CompactArgs& a, hipStream_t s) {
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s) {
     if (a.num_splats == 0) return hipSuccess;
     emit_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+// One lane per element, per-wavefront ballots before the global atomics.
+template <bool HALF>
+__global__ void __launch_bounds__(256) validate_kernel(const void* __restrict__ p, uint64_t n, uint32_t row,
+                                                       uint32_t col0, uint32_t col1, float lo, float hi,
+                                                       uint32_t* __restrict__ stats) {
+    uint32_t nan = 0, inf = 0, below = 0, above = 0, first_nan = 0xFFFFFFFFu, first_inf = 0xFFFFFFFFu;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint32_t col = (uint32_t)(i % row);
+        if (col < col0 || col >= col1) continue;
+        const float v = HALF ? h2f(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+        if (v != v) { ++nan; first_nan = min(first_nan, (uint32_t)min(i, (uint64_t)0xFFFFFFFEu)); }
+        else if (!finite(v)) { ++inf; first_inf = min(first_inf, (uint32_t)min(i, (uint64_t)0xFFFFFFFEu)); }
+        else { below += v < lo; above += v > hi; }
+    }
+    const uint64_t any = __ballot(nan | inf | below | above);
+    if (any == 0ull) return;
+    if (nan) { atomicAdd(&stats[VAL_NAN], nan); atomicMin(&stats[VAL_FIRST_NAN], first_nan); }
+    if (inf) { atomicAdd(&stats[VAL_INF], inf); atomicMin(&stats[VAL_FIRST_INF], first_inf); }
+    if (below) atomicAdd(&stats[VAL_BELOW], below);
+    if (above) atomicAdd(&stats[VAL_ABOVE], above);
+}
+
+hipError_t launch_validate(const void* p, bool half, uint64_t n, uint32_t row, uint32_t col0, uint32_t col1, float lo,
+                           float hi, uint32_t* stats, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>((n + 255) / 256, 4096);
+    if (half) validate_kernel<true><<<grid, 256, 0, s>>>(p, n, row, col0, col1, lo, hi, stats);
+    else validate_kernel<false><<<grid, 256, 0, s>>>(p, n, row, col0, col1, lo, hi, stats);
     return hipGetLastError();
 }
 

@@ -238,6 +238,15 @@ hipError_t launch_compact(const CompactArgs& a, hipStream_t s);
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
+
+// Validation scan (the reference's validate_tensor_val, validation.rs:60-140):
+// over the elements of an [n / row, row] array whose column lies in
+// [col0, col1), count NaN, Inf, finite values below `lo` and above `hi`, and
+// keep the first NaN and first Inf element index.  `stats` holds
+// VALIDATE_WORDS u32: counts, then the two indices (start at 0xFFFFFFFF).
+enum { VAL_NAN = 0, VAL_INF = 1, VAL_BELOW = 2, VAL_ABOVE = 3, VAL_FIRST_NAN = 4, VAL_FIRST_INF = 5, VALIDATE_WORDS = 8 };
+hipError_t launch_validate(const void* p, bool half, uint64_t n, uint32_t row, uint32_t col0, uint32_t col1, float lo,
+                           float hi, uint32_t* stats, hipStream_t s);
 // Ranges of the first min(*n_dev, n) sorted tile ids (all n when n_dev is null).
 hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
                               const uint32_t* n_dev = nullptr);

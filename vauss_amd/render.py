@@ -99,6 +99,7 @@ class Context:
         _lib.check(self.lib.vs_ctx_create(device, None, C.byref(h)))
         self.handle = h
         self.device = device
+        self.validation = False
 
     @classmethod
     def get(cls, device: torch.device) -> "Context":
@@ -123,6 +124,16 @@ class Context:
         t = _lib.VsStageTimes()
         _lib.check(self.lib.vs_ctx_stage_times(self.handle, C.byref(t)))
         return {name: getattr(t, name) for name, _ in _lib.VsStageTimes._fields_}
+
+    def set_validation(self, on: bool = True) -> None:
+        """Validation readbacks (validation.rs): renders scan their inputs and
+        backwards their gradients; NaN / Inf raise VsError(VS_ERR_NONFINITE)."""
+        _lib.check(self.lib.vs_ctx_set_validation(self.handle, 1 if on else 0))
+        self.validation = bool(on)
+
+    def set_poison(self, on: bool = True) -> None:
+        """Fill every library allocation with -12345.0 before first use (a debug aid)."""
+        _lib.check(self.lib.vs_ctx_set_poison(self.handle, 1 if on else 0))
 
     def set_sort_spin_limit(self, polls: Optional[int] = None) -> None:
         """Polls of an unpublished predecessor before a one-sweep radix pass
@@ -319,10 +330,6 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     raw_opacities = raw_opacities.contiguous()
     decoder = _check_decoder(decoder, neural_degree)
     n, degree = _check_splats(transforms, sh_coeffs, raw_opacities, None if decoder is None else neural_degree)
-    if validate:
-        for name, t in (("transforms", transforms), ("sh_coeffs", sh_coeffs), ("raw_opacities", raw_opacities)):
-            if not bool(torch.isfinite(t).all()):
-                raise _lib.VsError(_lib.VS_ERR_NONFINITE, f"{name} holds NaN or Inf")
     dev = transforms.device
     ctx = Context.get(dev)
     cam = camera.uniforms((w, h)) if isinstance(camera, Camera) else camera
@@ -346,9 +353,16 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, min_scale, decoder)
     bg = (C.c_float * 3)(*[float(v) for v in background])
     st = C.c_void_p()
-    _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg,
-                                         _lib.pass_with_slot(pass_, count_slot), int(render_mode), C.byref(out),
-                                         C.byref(st)))
+    was_validating = ctx.validation
+    if validate and not was_validating:
+        ctx.set_validation(True)
+    try:
+        _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg,
+                                             _lib.pass_with_slot(pass_, count_slot), int(render_mode), C.byref(out),
+                                             C.byref(st)))
+    finally:
+        if validate and not was_validating:
+            ctx.set_validation(False)
     aux = RenderAux(out.num_visible, out.num_intersections, visible, max_radius, opacities, tile_offsets, (w, h))
     state = ForwardState(st, ctx, pass_, n, degree) if st.value else None
     if state is not None:
