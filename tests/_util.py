@@ -43,7 +43,7 @@ def l1_cotangent_np(img: np.ndarray, gt: np.ndarray, mask=None) -> np.ndarray:
     d = img[..., :3] - gt
     s = np.sign(d).astype(np.float32) * np.float32(1.0 / (3.0 * count))
     if mask is not None:
-        s = s * mask[..., None]
+        s = np.where(mask[..., None] > 0, s, np.float32(0.0))     # masked pixels are +0
     v[..., :3] = s
     return v
 

@@ -86,3 +86,30 @@ def test_loss_parity_rendered_1080p():
     gt = va.pack_rgba8(torch.from_numpy(gt_rgba)).numpy().view(np.uint32)
     _check(pred, gt, dict(alpha_weight=0.0), "scalar")
     out.state.free()
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c5"])
+def test_l1_cotangent_matches_closed_form(cfg):
+    """vs_l1_cotangent (crates/splat-train-loss/src/lib.rs:786-811 sign,
+    :1297-1300 weights) at the workload's full image size, with C5's circular
+    mask of r = 940 px: bit-equal to sign(pred - gt) / (3 count) on rgb, 0 on
+    alpha and on every masked pixel; ties (pred == gt) give 0.  Repeated calls
+    (the mask count is cached) give the same result."""
+    from tests._util import circle_mask, l1_cotangent_np
+    w = scenes.workload(cfg, 1000)
+    W, H = w.img_size
+    rng = np.random.default_rng(7)
+    gt = scenes.loss_target(w.img_size)
+    pred = rng.uniform(0, 1, (H, W, 4)).astype(np.float32)
+    pred[::7, ::5, :3] = gt[::7, ::5]                                 # exact ties
+    mask = circle_mask(w.img_size, w.mask_center, w.mask_radius) if w.mask_radius > 0 else None
+    print(f"[case] l1 cotangent {cfg} {W}x{H} mask_radius={w.mask_radius}", flush=True)
+    p, g = torch.from_numpy(pred).cuda(), torch.from_numpy(gt).cuda()
+    for _ in range(2):
+        got = va.l1_cotangent(p, g, w.mask_center, w.mask_radius).cpu().numpy()
+        want = l1_cotangent_np(pred, gt, mask)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert (got[..., 3] == 0).all() and (got[..., :3][pred[..., :3] == gt] == 0).all()
+    if mask is not None:
+        assert 0 < mask.mean() < 1 and (got[mask == 0].view(np.uint32) == 0).all()
+        assert (got[mask == 1][:, :3] != 0).mean() > 0.9

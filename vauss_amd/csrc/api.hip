@@ -52,6 +52,9 @@ struct vs_ctx {
     uint32_t* dev_flags = nullptr;        // device: [0] set when a sort look-back gave up waiting
     uint32_t timing = 0;                  // bitmask of timed stages (VS_TIME_*)
     uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT;   // look-back polls before a one-sweep pass gives up
+    // the unmasked pixel count of the last circular L1 mask (vs_l1_cotangent)
+    struct MaskKey { uint32_t w, h; float cx, cy, r; } l1_mask{0, 0, 0.0f, 0.0f, 0.0f};
+    uint64_t l1_mask_count = 0;
     bool validate = false;                // scan inputs and gradients for NaN / Inf (vs_ctx_set_validation)
     bool poison = false;                  // fill every library allocation with POISON_WORD first
     uint32_t* dev_val = nullptr;          // device: validation counters, VALIDATE_WORDS per check
@@ -1136,12 +1139,20 @@ extern "C" vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t ch
     if (channels < 3) return fail(VS_ERR_INVALID, "prediction needs at least 3 channels");
     uint64_t count = (uint64_t)w * h;
     if (mr > 0.0f) {
-        count = 0;
-        for (uint32_t y = 0; y < h; ++y)
-            for (uint32_t x = 0; x < w; ++x) {
-                const float dx = (float)x + 0.5f - mcx, dy = (float)y + 0.5f - mcy;
-                if (dx * dx + dy * dy <= mr * mr) ++count;
-            }
+        // The pixels the kernel keeps, counted with its own f32 test once per
+        // mask (a training loop passes the same mask every step).
+        const vs_ctx::MaskKey& k = ctx->l1_mask;
+        if (!(k.w == w && k.h == h && k.cx == mcx && k.cy == mcy && k.r == mr)) {
+            count = 0;
+            for (uint32_t y = 0; y < h; ++y)
+                for (uint32_t x = 0; x < w; ++x) {
+                    const float dx = (float)x + 0.5f - mcx, dy = (float)y + 0.5f - mcy;
+                    if (dx * dx + dy * dy <= mr * mr) ++count;
+                }
+            ctx->l1_mask = vs_ctx::MaskKey{w, h, mcx, mcy, mr};
+            ctx->l1_mask_count = count;
+        }
+        count = ctx->l1_mask_count;
     }
     const float inv = count ? 1.0f / (3.0f * (float)count) : 0.0f;
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
