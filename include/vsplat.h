@@ -416,6 +416,21 @@ vs_status vs_sh_step(vs_ctx* ctx, uint16_t* sh_coeffs, uint32_t num_splats, uint
 vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, const uint32_t* vals, uint32_t n,
                                const uint32_t* n_dev, uint32_t skip_bits, uint32_t sorting_bits,
                                uint32_t* out_keys, uint32_t* out_vals);
+/* vs_radix_argsort_u32 without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Its scratch is one device array of 40 MiB per GPU, held by the library
+ * until the process ends, so n <= VS_NOALLOC_SORT_MAX_KEYS (else
+ * VS_ERR_CAPACITY).  Every call on a GPU uses that GPU's one array, so calls
+ * that overlap on one GPU (from any context or stream) race.  Stream-ordered
+ * and does not wait: a one-sweep pass that gave up (vs_ctx_set_sort_spin_limit)
+ * is reported by the context's next synchronising call (vs_radix_argsort_u32,
+ * an exact render, vs_ctx_settle_lagged_counts).  Same arguments and result
+ * as vs_radix_argsort_u32. */
+#define VS_NOALLOC_SORT_MAX_KEYS 4194304u
+vs_status vs_radix_argsort_u32_noalloc(vs_ctx* ctx, const uint32_t* keys, const uint32_t* vals, uint32_t n,
+                                       const uint32_t* n_dev, uint32_t skip_bits, uint32_t sorting_bits,
+                                       uint32_t* out_keys, uint32_t* out_vals);
 /* The same sort on 64-bit keys, bits [0, sorting_bits) with sorting_bits <= 64
  * (e.g. a packed (tile, depth) key).  No reference counterpart: the
  * reference's sort crate takes u32 keys only. */

@@ -136,6 +136,8 @@ SIGNATURES = {
                              C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(VsShStepParams)]),
     "vs_radix_argsort_u32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32,
                                        C.c_uint32, C.c_void_p, C.c_void_p]),
+    "vs_radix_argsort_u32_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
+                                               C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p]),
     "vs_radix_argsort_u64": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
                                        C.c_void_p]),
     "vs_prefix_sum_u32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]),

@@ -6,6 +6,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -267,6 +268,41 @@ vs_status check_splats(const vs_splats* sp) {
 
 } // namespace
 
+// ---- allocation-free sort scratch --------------------------------------------
+// One array per GPU, used by vs_radix_argsort_u32_noalloc in place of the
+// per-call allocation of vs_radix_argsort_u32.  In host code `scratch` names
+// a host-side stand-in, not device memory: the device address of each GPU's
+// copy comes from hipGetSymbolAddress, taken once per device (with that device
+// current) when the first context on it is created, and only that address is
+// ever handed to kernels.
+constexpr uint32_t NOALLOC_SORT_MAX_KEYS = 1u << 22;
+constexpr size_t SCRATCH_BYTES = (size_t)40 << 20;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Set-up, called with `device` current.
+vs_status init_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return fail(VS_ERR_INVALID, "device index beyond the library's table");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device]) return VS_OK;
+    if (sort_tmp_bytes(NOALLOC_SORT_MAX_KEYS, false) + 256 > SCRATCH_BYTES)
+        return fail(VS_ERR_INVALID, "the sort scratch array is smaller than its maximum sort needs");
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[device] = ptr;
+    return VS_OK;
+}
+void* scratch_ptr(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    return (device >= 0 && device < MAX_DEVICES) ? g_scratch_ptr[device] : nullptr;
+}
+} // namespace
+
 extern "C" const char* vs_last_error(void) { return g_last_error.c_str(); }
 extern "C" const char* vs_version(void) { return "vsplat-gfx950 0.1"; }
 
@@ -296,6 +332,17 @@ extern "C" vs_status vs_ctx_create(int device, void* hip_stream, vs_ctx** out) {
         if (c->dev_val) hipFree(c->dev_val);
         delete c;
         return hip_fail(e, "context buffers");
+    }
+    {
+        const vs_status se = init_scratch(device);
+        if (se != VS_OK) {
+            hipHostFree(c->host_counters);
+            hipHostFree(c->host_val);
+            hipFree(c->dev_flags);
+            hipFree(c->dev_val);
+            delete c;
+            return se;
+        }
     }
     // VSPLAT_POISON=1 poisons every allocation of this context (a debug aid for test runs).
     const char* poison_env = std::getenv("VSPLAT_POISON");
@@ -1018,6 +1065,28 @@ extern "C" vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, con
     hipFreeAsync(tmp, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
     return sync_sort_flag(ctx);
+}
+
+extern "C" vs_status vs_radix_argsort_u32_noalloc(vs_ctx* ctx, const uint32_t* keys, const uint32_t* vals, uint32_t n,
+                                                  const uint32_t* n_dev, uint32_t skip_bits, uint32_t sorting_bits,
+                                                  uint32_t* out_keys, uint32_t* out_vals) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (skip_bits + sorting_bits > 32) return fail(VS_ERR_INVALID, "Can only sort up to 32 bits");
+    if (n > NOALLOC_SORT_MAX_KEYS)
+        return fail(VS_ERR_CAPACITY, "vs_radix_argsort_u32_noalloc sorts at most 4194304 keys (its scratch array's size)");
+    if (n == 0) return VS_OK;
+    if (!keys || !vals || !out_keys || !out_vals) return fail(VS_ERR_INVALID, "null buffer");
+    if (keys == out_keys || vals == out_vals) return fail(VS_ERR_INVALID, "outputs must not alias inputs");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    void* tmp = scratch_ptr(ctx->device);
+    if (!tmp) return fail(VS_ERR_INVALID, "no scratch address for this device (no context was created on it)");
+    // Stream-ordered, no wait: a pass that gave up sets the context's flag,
+    // which the next synchronising call on the context reports.
+    const hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, n_dev, false, skip_bits,
+                                          skip_bits + sorting_bits, tmp, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream,
+                                          ctx->spin_limit);
+    if (e != hipSuccess) return hip_fail(e, "radix sort");
+    return VS_OK;
 }
 
 extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, const uint32_t* vals, uint32_t n,
