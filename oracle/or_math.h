@@ -48,6 +48,27 @@ static inline float expf_c(float x) {
     return std::ldexp(p, (int)n);
 }
 
+// exp2n: 2^x for the compositing loops, whose argument is -sigma in base-2
+//      units (sigma log2 e, never positive for a pair that can contribute):
+//      x = min(max(x, -127), 128) (NaN -> -127), n = rint(x), f = x - n in
+//      [-1/2, 1/2] (exact), 2^f = 1 + f P(f) with P of degree 4 fitted for
+//      least maximum relative error on [-1/2, 1/2] (Lawson iterations),
+//      result ldexp(p, n); relative error <= 2.1 ulp on [-126, 0].
+static inline float exp2n_c(float x) {
+    x = std::fmin(std::fmax(x, -127.0f), 128.0f);
+    const float n = std::rint(x);
+    const float f = x - n;
+    float p = std::fma(1.326472731e-03f, f, 9.671512991e-03f);
+    p = std::fma(p, f, 5.550733581e-02f);
+    p = std::fma(p, f, 2.402224243e-01f);
+    p = std::fma(p, f, 6.931470037e-01f);
+    p = std::fma(p, f, 1.0f);
+    return std::ldexp(p, (int)n);
+}
+// log2(e) rounded to f32: the compositing loops scale the conic by it so
+// sigma comes out in base-2 units.
+constexpr float LOG2E_F = 1.44269502f;
+
 // log: x = m 2^e with m in [sqrt(1/2), sqrt(2)); s = (m-1)/(m+1);
 //      ln m = 2 atanh(s) = 2s + s * s^2 (2/3 + 2/5 s^2 + 2/7 s^4 + 2/9 s^6)
 //      (Taylor terms of atanh; |s| <= 0.1716 so the tail is < 3e-9).

@@ -130,6 +130,7 @@ def load() -> C.CDLL:
     lib.or_atan2f.restype = C.c_float
     lib.or_atan2f.argtypes = [C.c_float, C.c_float]
     lib.or_expf_n.argtypes = [_F, _F, C.c_uint64]
+    lib.or_exp2n_n.argtypes = [_F, _F, C.c_uint64]
     lib.or_logf_n.argtypes = [_F, _F, C.c_uint64]
     lib.or_atan2f_n.argtypes = [_F, _F, _F, C.c_uint64]
     lib.or_sh_basis.argtypes = [C.c_uint32, _F, _F]
@@ -348,6 +349,14 @@ def expf(x):
     a = np.ascontiguousarray(x, np.float32)
     out = np.empty_like(a)
     load().or_expf_n(_fp(a), _fp(out), a.size)
+    return out
+
+
+def exp2n(x):
+    """The compositing loops' 2^x (or_math.h exp2n_c)."""
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    load().or_exp2n_n(_fp(a), _fp(out), a.size)
     return out
 
 

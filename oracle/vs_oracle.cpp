@@ -27,12 +27,15 @@
 // independently):
 //  * projection-side math: the reference's operation order, no contraction;
 //  * exp/log/atan2: the portable evaluations of or_math.h;
-//  * compositing: dx = px - x, dy = py - y,
-//      sigma = fma(fma(A, dx, B*dy), dx, (C*dy)*dy)   A = c00/2, B = c01, C = c11/2
-//    (equal to the reference's 0.5(c00 dx^2 + c11 dy^2) + c01 dx dy up to the
-//    contraction the reference's shader compiler is also free to apply),
-//    G = exp(-sigma), alpha = min(0.999, opac G), T' = T (1 - alpha),
+//  * compositing: dx = px - x, dy = py - y, and sigma in base-2 units
+//      s2 = fma(fma(A, dx, B*dy), dx, (C*dy)*dy),
+//      A = (c00/2) L, B = c01 L, C = (c11/2) L, L = log2(e) in f32
+//    (the reference's 0.5(c00 dx^2 + c11 dy^2) + c01 dx dy times log2 e, up to
+//    rounding and the contraction its shader compiler is also free to apply;
+//    s2 >= 0 exactly when sigma >= 0), G = exp2n(-s2) (or_math.h),
+//    alpha = min(0.999, opac G), T' = T (1 - alpha),
 //    colour += max(c,0) * (alpha T) as an fma, final = fma(T, bg, colour).
+//    Surfels: G = exp2n(-(sigma L)) of their ray-plane sigma.
 #include "vs_oracle.h"
 #include "or_math.h"
 
@@ -1232,7 +1235,7 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
             const float* row = &f->projected[(size_t)c * 9];
             RasterSplat s;
             s.x = row[0]; s.y = row[1]; s.c00 = row[2]; s.c01 = row[3]; s.c11 = row[4];
-            s.A = 0.5f * row[2]; s.B = row[3]; s.C = 0.5f * row[4];
+            s.A = (0.5f * row[2]) * LOG2E_F; s.B = row[3] * LOG2E_F; s.C = (0.5f * row[4]) * LOG2E_F;
             s.opac = row[5]; s.r = row[6]; s.g = row[7]; s.b = row[8];
             s.gid = f->global_from_compact[c];
             s.surf = surfel ? &f->surf[(size_t)c * SURFEL_AUX] : nullptr;
@@ -1255,17 +1258,18 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
                 for (uint32_t i = lo; i < hi; ++i) {
                     const RasterSplat& s = list[i - lo];
                     ++evals_total;
-                    float sigma, z = s.z;
+                    float sigma, z = s.z, G;
                     if (surfel) {
                         const SurfelHit hit = surfel_hit(s.surf, pcx, pcy);
                         if (!hit.valid) continue;          // no intersection in front of the near limit
                         sigma = hit.sigma;
                         z = hit.z;
+                        G = exp2n_c(-(sigma * LOG2E_F));
                     } else {
                         const float dx = pcx - s.x, dy = pcy - s.y;
-                        sigma = std::fma(std::fma(s.A, dx, s.B * dy), dx, (s.C * dy) * dy);
+                        sigma = std::fma(std::fma(s.A, dx, s.B * dy), dx, (s.C * dy) * dy);   // base 2
+                        G = exp2n_c(-sigma);
                     }
-                    const float G = expf_c(-sigma);
                     const float alpha = fmin_(0.999f, s.opac * G);
                     const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
                     if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -1426,7 +1430,7 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
                         const SurfelHit h = surfel_hit(a, pcx, pcy);
                         if (!h.valid) continue;
                         const float sigma = h.sigma;
-                        const float G = expf_c(-sigma);
+                        const float G = exp2n_c(-(sigma * LOG2E_F));
                         const float alpha = fmin_(0.999f, opac * G);
                         const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
                         if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -1489,8 +1493,9 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
                     const float x = row[0], y = row[1], c00 = row[2], c01 = row[3], c11 = row[4];
                     const float opac = row[5], cr = row[6], cgc = row[7], cbc = row[8];
                     const float dx = pcx - x, dy = pcy - y;
-                    const float sigma = std::fma(std::fma(0.5f * c00, dx, c01 * dy), dx, ((0.5f * c11) * dy) * dy);
-                    const float G = expf_c(-sigma);
+                    const float sigma = std::fma(std::fma((0.5f * c00) * LOG2E_F, dx, (c01 * LOG2E_F) * dy), dx,
+                                                 (((0.5f * c11) * LOG2E_F) * dy) * dy);   // base 2, as the forward's
+                    const float G = exp2n_c(-sigma);
                     const float alpha = fmin_(0.999f, opac * G);
                     const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
                     if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -2176,6 +2181,9 @@ extern "C" void or_prefix_sum_u32(const uint32_t* in, uint32_t* out, uint32_t n)
 
 // ---- exported math -------------------------------------------------------------
 extern "C" float or_expf(float x) { return expf_c(x); }
+extern "C" void or_exp2n_n(const float* x, float* y, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) y[i] = exp2n_c(x[i]);
+}
 extern "C" float or_logf(float x) { return logf_c(x); }
 extern "C" float or_atan2f(float y, float x) { return atan2f_c(y, x); }
 extern "C" void or_expf_n(const float* x, float* y, uint64_t n) {

@@ -196,6 +196,8 @@ float or_expf(float x);
 float or_logf(float x);
 float or_atan2f(float y, float x);
 void or_expf_n(const float* x, float* y, uint64_t n);
+/* The compositing loops' 2^x (exp2n). */
+void or_exp2n_n(const float* x, float* y, uint64_t n);
 void or_logf_n(const float* x, float* y, uint64_t n);
 void or_atan2f_n(const float* y, const float* x, float* r, uint64_t n);
 

@@ -1,8 +1,8 @@
 """Pins the oracle's scalar math against what mathematics fixes, independently of
 the oracle's own formulas:
 
-* exp / log / atan2 against numpy's float64 functions (error in f32 ulps)
-  and the C99 special values;
+* exp / exp2n / log / atan2 against numpy's float64 functions (error in f32
+  ulps) and the C99 special values;
 * the real spherical-harmonic basis (kernels/sh.rs:8-140, Sloan's
   convention) against scipy's complex spherical harmonics, and its
   orthonormality over the sphere by Gauss-Legendre quadrature;
@@ -38,6 +38,32 @@ def test_expf_special_values():
     assert y[5] == 0.0 and y[6] == 0.0          # flushed below -87.33654: results are never subnormal
     assert y[7] == np.inf
     assert abs(float(y[8]) - np.e) <= np.spacing(np.float32(np.e))
+
+
+def test_exp2n_within_2_1_ulp():
+    """The compositing exp (2^x of -sigma in base-2 units) against numpy's
+    float64 exp2: <= 2.1 ulp on [-126, 0] (the contributing pairs' sigma lies in
+    [0, 8]), every grid point of 2^-12 on [-12, 0] included."""
+    rng = np.random.default_rng(21)
+    x = np.concatenate([rng.uniform(-126.0, 0.0, 1_000_000), rng.uniform(-12.0, 0.0, 1_000_000),
+                        -np.arange(0.0, 12.0, 2.0 ** -12), rng.uniform(-1e-3, 0.0, 50_000)]).astype(np.float32)
+    err = _ulp_err(po.exp2n(x), np.exp2(x.astype(np.float64)))
+    assert err.max() <= 2.1, err.max()
+    # e^-sigma through the base-2 conic: exp2n(-sigma log2 e) within 1e-6 relative of
+    # float64 e^-sigma on the live range (the conic's own rounding adds an ulp of sigma)
+    sig = rng.uniform(0.0, 6.0, 200_000).astype(np.float32)
+    g = po.exp2n(-(sig * np.float32(1.44269502)))
+    np.testing.assert_allclose(g, np.exp(-sig.astype(np.float64)), rtol=1e-6, atol=0)
+
+
+def test_exp2n_special_values():
+    x = np.array([0.0, -0.0, -1.0, -10.0, -np.inf, np.nan, -1e30, -127.0, -200.0, 1.0, 5.0, 1e30, np.inf],
+                 np.float32)
+    y = po.exp2n(x)
+    assert y[0] == 1.0 and y[1] == 1.0 and y[2] == 0.5 and y[3] == np.float32(2.0 ** -10)
+    # arguments below -127 (and NaN) clamp to -127: 2^-127, a subnormal, never above the cutoffs
+    assert (y[4:9] == np.float32(2.0 ** -127)).all()
+    assert y[9] == 2.0 and y[10] == 32.0 and y[11] == np.inf and y[12] == np.inf
 
 
 def test_logf_within_two_ulp():

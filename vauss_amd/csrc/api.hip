@@ -109,6 +109,7 @@ struct vs_fwd_state {
     uint32_t* counters = nullptr;
     uint32_t* ranges = nullptr;
     uint32_t* ranges_shrunk = nullptr;
+    uint32_t* tile_order = nullptr;   // [8 ceil(T/8)] raster dispatch order
     float* v_combined = nullptr;
     uint32_t* tiles = nullptr;    // [I] sorted tile ids
     uint32_t* gids = nullptr;     // [I] sorted global ids
@@ -602,6 +603,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     const size_t o_bs = take((size_t)std::max(nblocks, 1u) * 4 * BS_ROWS);
     const size_t o_cnt = take(CNT_COUNT * 4);
     const size_t o_rng = take((size_t)T * 8), o_rngs = take((size_t)T * 8);
+    const size_t o_ord = take((size_t)8 * ((T + 7) / 8) * 4);
     VS_HIP(lib_alloc(ctx, &st->arena, off, s), "hipMallocAsync(splat arena)");
     char* base = static_cast<char*>(st->arena);
     st->counts = reinterpret_cast<uint32_t*>(base + o_counts);
@@ -619,6 +621,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->counters = reinterpret_cast<uint32_t*>(base + o_cnt);
     st->ranges = reinterpret_cast<uint32_t*>(base + o_rng);
     st->ranges_shrunk = reinterpret_cast<uint32_t*>(base + o_rngs);
+    st->tile_order = reinterpret_cast<uint32_t*>(base + o_ord);
 
     // ---- projection --------------------------------------------------------------
     {
@@ -743,6 +746,9 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         StageTimer tm(ctx, ST_RASTER_FWD);
         RasterArgs ra{};
         ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T; ra.num_splats = N;
+        // longest lists first within each XCD's band (the forward's cost grows with its list)
+        VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s), "tile order");
+        ra.order = st->tile_order;
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
         ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;
         ra.proj_a = st->proj_a; ra.proj_b = st->proj_b; ra.proj_c = st->proj_c; ra.proj_aux = st->proj_aux;
@@ -827,6 +833,9 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             RasterBwdArgs rb{};
             rb.img_w = st->W; rb.img_h = st->H; rb.tile_bw = st->tbw; rb.tile_bh = st->tbh; rb.num_tiles = st->T;
             rb.num_splats = N;
+            // the backward walks the shrunk ranges: order by their lengths
+            VS_HIP(launch_tile_order(st->ranges_shrunk, st->T, st->tile_order, s), "tile order");
+            rb.order = st->tile_order;
             rb.bg_r = st->bg[0]; rb.bg_g = st->bg[1]; rb.bg_b = st->bg[2];
             rb.gids = st->gids; rb.ranges = st->ranges_shrunk;
             rb.proj_a = st->proj_a; rb.proj_b = st->proj_b; rb.proj_c = st->proj_c;

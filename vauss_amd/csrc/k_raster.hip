@@ -57,6 +57,70 @@ VS_DEV uint32_t xcd_tile(uint32_t block, uint32_t num_tiles) {
 }
 static uint32_t xcd_grid(uint32_t num_tiles) { return 8 * ((num_tiles + 7) / 8); }
 
+// Tile of workgroup `block`: order[block] when a dispatch order is given
+// (tile_order_kernel; entries past the tiles hold 0xFFFFFFFF), else the
+// banded mapping above.
+VS_DEV uint32_t block_tile(const uint32_t* order, uint32_t block, uint32_t num_tiles) {
+    return order ? order[block] : xcd_tile(block, num_tiles);
+}
+
+// Dispatch order of the raster kernels.  Each XCD starts its workgroups in
+// increasing index order as slots free up, so a long tile dealt out late
+// ends the launch alone (the backward runs one wavefront per tile and holds
+// about 1.6 tiles per slot at C3).  XCD k keeps its contiguous band of tiles
+// [k per, (k + 1) per) (neighbouring tiles share splats, whose rows then stay
+// in one L2) but takes them longest list first: block i * 8 + k gets the
+// i-th longest tile of band k.  One workgroup per band counts its tiles into
+// ORDER_BINS bins of 8 sqrt(list length) (LDS atomics: the order inside a
+// bin is arbitrary, which changes no result) and scatters them by bin,
+// longest bin first.
+constexpr int ORDER_BLOCK = 1024;
+constexpr int ORDER_BINS = 2048;
+static_assert(ORDER_BINS == 2 * ORDER_BLOCK, "each thread of the order scan owns two bins");
+
+VS_DEV uint32_t order_bin(const uint32_t* __restrict__ ranges, uint32_t t) {
+    const uint32_t lo = ranges[2 * t], hi = ranges[2 * t + 1];
+    const float len = (float)(hi > lo ? hi - lo : 0u);
+    const uint32_t key = min((uint32_t)(__builtin_sqrtf(len) * 8.0f), (uint32_t)ORDER_BINS - 1u);
+    return (uint32_t)ORDER_BINS - 1u - key;   // ascending bin = descending length
+}
+
+__global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(const uint32_t* __restrict__ ranges, uint32_t num_tiles,
+                                                                 uint32_t* __restrict__ order) {
+    __shared__ uint32_t s_bin[ORDER_BINS];
+    __shared__ uint32_t s_wave[ORDER_BLOCK / 64];
+    const uint32_t per = (num_tiles + 7) / 8;
+    const uint32_t band = blockIdx.x;
+    const uint32_t t0 = band * per, t1 = min(num_tiles, t0 + per);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (uint32_t i = tid; i < ORDER_BINS; i += ORDER_BLOCK) s_bin[i] = 0u;
+    __syncthreads();
+    for (uint32_t t = t0 + tid; t < t1; t += ORDER_BLOCK) atomicAdd(&s_bin[order_bin(ranges, t)], 1u);
+    __syncthreads();
+    // exclusive scan of the bins: each thread owns bins 2 tid and 2 tid + 1
+    const uint32_t c0 = s_bin[2 * tid], c1 = s_bin[2 * tid + 1];
+    uint32_t incl = c0 + c1;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o);
+        if ((int)lane >= o) incl += v;
+    }
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (uint32_t w = 0; w < wave; ++w) before += s_wave[w];
+    const uint32_t excl = before + incl - (c0 + c1);
+    __syncthreads();                      // every count is read before the offsets replace them
+    s_bin[2 * tid] = excl;
+    s_bin[2 * tid + 1] = excl + c0;
+    __syncthreads();
+    for (uint32_t t = t0 + tid; t < t1; t += ORDER_BLOCK) {
+        const uint32_t pos = atomicAdd(&s_bin[order_bin(ranges, t)], 1u);
+        order[(size_t)pos * 8 + band] = t;
+    }
+    for (uint32_t i = (t1 > t0 ? t1 - t0 : 0u) + tid; i < per; i += ORDER_BLOCK) order[(size_t)i * 8 + band] = 0xFFFFFFFFu;
+}
+
 // ---- quadrant culling -------------------------------------------------------
 // A tile is four 8x8 quadrants.  For each staged splat the kernels compute a
 // 4-bit mask of the quadrants in which some pixel centre may pass the alpha
@@ -67,9 +131,10 @@ static uint32_t xcd_grid(uint32_t num_tiles) { return 8 * ((num_tiles + 7) / 8);
 // accumulator untouched.
 //
 // alpha = min(0.999, opac e^-sigma) is below the cutoff c whenever
-// sigma > ln(opac / c).  A quadrant is dead when the minimum of
-// sigma = A dx^2 + B dx dy + C dy^2 over the rectangle spanned by its pixel
-// centres exceeds 1.01 ln(opac / c) + 0.01.  The 1% + 0.01 margin dwarfs the
+// sigma > ln(opac / c).  The kernels hold the conic in base-2 units
+// (s2 = sigma log2 e = A dx^2 + B dx dy + C dy^2 with the staged A, B, C), so a
+// quadrant is dead when the minimum of s2 over the rectangle spanned by its
+// pixel centres exceeds (1.01 ln(opac / c) + 0.01) log2 e.  The 1% + 0.01 margin dwarfs the
 // f32 rounding of both this minimum and the per-pixel sigma, which is at most
 // a few ulp of (A dx^2 + |B dx dy| + C dy^2) <= 2 sigma / (1 - rho) with
 // rho = |B| / (2 sqrt(AC)); splats with 1 - rho^2 <= 0.01 (and any
@@ -90,7 +155,7 @@ VS_DEV float edge_min(float a, float b, float c, float k, float u, float lo, flo
 VS_DEV uint32_t quadrant_mask(float x0, float y0, float mx_, float my_, float A, float B, float C, float opac,
                               bool smooth) {
     const float cut = smooth ? (ALPHA_MID - 0.5f * ALPHA_BAND) : ALPHA_MID;
-    const float thr = QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS;
+    const float thr = (QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS) * LOG2E_F;
     const float four_ac = 4.0f * A * C;
     if (!(A > 0.0f && C > 0.0f && four_ac - B * B > QUAD_MIN_DECORR * four_ac && thr < 3.0e38f)) return 0xFu;
     const float kx = -B / (2.0f * C);   // vertical edges: dy* = kx dx
@@ -126,18 +191,20 @@ constexpr int FWD_BLOCK = 256;
 // no quadrant culling (the binning ellipse, not the coverage, is an ellipse).
 template <bool BWD, bool GEOM, bool SMOOTH, bool SURF>
 __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
-    __shared__ float4 s_a[FWD_BLOCK];    // x, y, c00/2, c01
-    __shared__ float4 s_b[FWD_BLOCK];    // c11/2, opacity, max(r,0), max(g,0)
-    __shared__ float s_c[FWD_BLOCK];     // max(b,0)
+    // Every per-splat array has 16-byte slots, so one LDS address, the slot's
+    // byte offset kept in the per-quadrant lists, serves all reads of a splat.
+    __shared__ float4 s_a[FWD_BLOCK];    // x, y, A, B (the conic in base-2 units)
+    __shared__ float4 s_b[FWD_BLOCK];    // C, opacity, max(r,0), max(g,0)
+    __shared__ float4 s_c[FWD_BLOCK];    // max(b,0), -, -, -
     __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BLOCK : 1];
     __shared__ float4 s_s[SURF ? FWD_BLOCK * 4 : 1];
     __shared__ uint32_t s_gid[BWD ? FWD_BLOCK : 1];
-    __shared__ uint32_t s_hit[BWD ? FWD_BLOCK : 1];
-    __shared__ uint8_t s_list[4][FWD_BLOCK];       // per-quadrant live batch slots
+    __shared__ uint4 s_hit[BWD ? FWD_BLOCK : 1];   // .x = 1 once the slot blended a pixel
+    __shared__ uint16_t s_list[4][FWD_BLOCK];      // per-quadrant live slots as byte offsets (slot * 16)
     __shared__ uint32_t s_qcnt[4][4];                 // [wavefront][quadrant] live-slot counts
     __shared__ uint32_t s_last;
 
-    const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
+    const uint32_t tile = block_tile(a.order, blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
     const uint32_t l = threadIdx.x;
@@ -158,6 +225,11 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
     bool surf_found = false;
     bool done = !inside;
     uint32_t last = lo;
+    const char* const lds_a = reinterpret_cast<const char*>(s_a);
+    const char* const lds_b = reinterpret_cast<const char*>(s_b);
+    const char* const lds_c = reinterpret_cast<const char*>(s_c);
+    const char* const lds_d = reinterpret_cast<const char*>(s_d);
+    const char* const lds_s = reinterpret_cast<const char*>(s_s);
 
     for (uint32_t start = lo; start < hi; start += FWD_BLOCK) {
         // Barrier + vote: protects the previous batch's LDS reads and ends the
@@ -167,16 +239,17 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
         uint32_t qmask = 0;
         const uint32_t gid = (l < rem) ? a.gids[start + l] : 0xFFFFFFFFu;
         if constexpr (BWD) {
-            if (l < rem) { s_gid[l] = 0u; s_hit[l] = 0u; }
+            if (l < rem) { s_gid[l] = 0u; s_hit[l].x = 0u; }
         }
         if (gid < a.num_splats) {   // else: past the batch, or a corrupt id (dead slot)
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
-            const float4 sa = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
-            const float4 sb = make_float4(0.5f * pb.x, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
+            // the conic in base-2 units: sigma log2 e comes out of the same fma chain
+            const float4 sa = make_float4(pa.x, pa.y, (0.5f * pa.z) * LOG2E_F, pa.w * LOG2E_F);
+            const float4 sb = make_float4((0.5f * pb.x) * LOG2E_F, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
             s_a[l] = sa;
             s_b[l] = sb;
-            s_c[l] = mx(a.proj_c[gid], 0.0f);
+            s_c[l].x = mx(a.proj_c[gid], 0.0f);
             if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
             if constexpr (BWD) s_gid[l] = gid;
             if constexpr (SURF) {
@@ -203,49 +276,57 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
             uint32_t off = below[q];
 #pragma unroll
             for (uint32_t w = 0; w < 3; ++w) off += (w < wave) ? s_qcnt[w][q] : 0u;
-            if ((qmask >> q) & 1u) s_list[q][off] = (uint8_t)l;
+            if ((qmask >> q) & 1u) s_list[q][off] = (uint16_t)(l * 16u);
             count += (q == (int)wave) ? s_qcnt[0][q] + s_qcnt[1][q] + s_qcnt[2][q] + s_qcnt[3][q] : 0u;
         }
         __syncthreads();
-        const uint8_t* list = s_list[wave];
-        for (uint32_t j = 0; j < count && !done; ++j) {
-            const uint32_t t = list[j];
-            const float4 sb = s_b[t];
-            float sigma, zs = 0.0f;
+        const uint16_t* list = s_list[wave];
+        const uint32_t nlist = __builtin_amdgcn_readfirstlane(count);   // the same for the whole wavefront
+        uint32_t last_off = 0xFFFFFFFFu;                                  // byte offset of the last slot blended
+        for (uint32_t j = 0; j < nlist; ++j) {
+            if (done) break;
+            const uint32_t off = list[j];
+            const float4 sb = *reinterpret_cast<const float4*>(lds_b + off);
+            float sigma, zs = 0.0f, G;
             if constexpr (SURF) {
-                const SurfelHit hit = surfel_hit(s_s[4 * t], s_s[4 * t + 1], s_s[4 * t + 2], s_s[4 * t + 3].z, pcx, pcy);
+                const float4* ss = reinterpret_cast<const float4*>(lds_s + off * 4u);
+                const SurfelHit hit = surfel_hit(ss[0], ss[1], ss[2], ss[3].z, pcx, pcy);
                 if (!hit.valid) continue;       // the ray misses the plane or meets it before the near limit
                 sigma = hit.sigma;
                 zs = hit.z;
+                G = exp2n(-(sigma * LOG2E_F));
             } else {
-                const float4 sa = s_a[t];
+                const float4 sa = *reinterpret_cast<const float4*>(lds_a + off);
                 const float dx = pcx - sa.x, dy = pcy - sa.y;
-                sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);
+                sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);   // base 2
+                G = exp2n(-sigma);
             }
-            const float G = expf_neg(-sigma);
             // min(0.999, .) of a product that is NaN only when sigma is
             // (then the sigma test below rejects the pair): same value as mn().
             const float alpha = __builtin_fminf(ALPHA_CAP, sb.y * G);
             const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
             if (sigma >= 0.0f && w_cut > 0.0f) {
-                const float ae = alpha * w_cut;
+                const float ae = SMOOTH ? alpha * w_cut : alpha;
                 const float nt = T * (1.0f - ae);
                 if (nt <= T_STOP) {
                     done = true;
                 } else {
-                    if constexpr (BWD) s_hit[t] = 1u;
+                    if constexpr (BWD) reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_hit) + off)->x = 1u;
                     const float vis = ae * T;
+                    const float cbv = reinterpret_cast<const float4*>(lds_c + off)->x;
                     cr = __builtin_fmaf(sb.z, vis, cr);
                     cg = __builtin_fmaf(sb.w, vis, cg);
-                    cb = __builtin_fmaf(s_c[t], vis, cb);
+                    cb = __builtin_fmaf(cbv, vis, cb);
                     if constexpr (GEOM) {
                         float4 d;
                         if constexpr (SURF) {
-                            const float4 s2 = s_s[4 * t + 2], s3 = s_s[4 * t + 3];
+                            const float4* ss = reinterpret_cast<const float4*>(lds_s + off * 4u);
+                            const float4 s2 = ss[2], s3 = ss[3];
                             d = make_float4(zs, s2.w, s3.x, s3.y);
                         } else {
-                            d = s_d[t];
+                            d = *reinterpret_cast<const float4*>(lds_d + off);
                         }
+                        const uint32_t t = off >> 4;
                         depth_acc = __builtin_fmaf(d.x, vis, depth_acc);
                         if (SURF && a.surf_crit) {
                             // unbiased-depth surface criterion (rasterize.rs:181-187, 346-354)
@@ -264,13 +345,15 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
                         nz = __builtin_fmaf(d.w, vis, nz);
                     }
                     T = nt;
-                    last = start + t + 1;
+                    last_off = off;
                 }
             }
         }
+        // slots blend in increasing order, so the batch's last blend is the lane's last so far
+        if (last_off != 0xFFFFFFFFu) last = start + (last_off >> 4) + 1u;
         if constexpr (BWD) {
             __syncthreads();
-            if (l < rem && s_hit[l]) a.visible[s_gid[l]] = 1.0f;
+            if (l < rem && s_hit[l].x) a.visible[s_gid[l]] = 1.0f;
         }
     }
 
@@ -400,13 +483,15 @@ template <bool SMOOTH>
 __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     // Per-splat values are formed once at staging, where one instruction
     // serves the 64 splats of a batch, not per (splat, wavefront) in the loop.
-    __shared__ float4 s_a[BWD_BATCH];       // x, y, c00/2, c01
-    __shared__ float4 s_b[BWD_BATCH];       // c11/2, opacity, max(r,0), max(g,0)
+    __shared__ float4 s_a[BWD_BATCH];       // x, y, A, B (the forward's conic in base-2 units)
+    __shared__ float4 s_b[BWD_BATCH];       // C, opacity, max(r,0), max(g,0)
     __shared__ float4 s_c[BWD_BATCH];       // max(b,0), c00, c11, colour gates (bits r,g,b >= 0, bit 3 set)
+    __shared__ float4 s_d[BWD_BATCH];       // the conic's rows scaled to pixels: c00 W, c01 W, c01 H, c11 H
+    __shared__ float s_c01[BWD_BATCH];      // c01
     __shared__ uint32_t s_gid[BWD_BATCH];
     __shared__ uint32_t s_mask[BWD_BATCH];  // live quadrants
 
-    const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
+    const uint32_t tile = block_tile(a.order, blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
     if (lo >= hi) return;   // uniform per tile
@@ -466,14 +551,18 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
         if (gid < a.num_splats) {
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
-            const float4 sa = make_float4(pa.x, pa.y, 0.5f * pa.z, pa.w);
+            // the forward's base-2 conic for the replay; c00, c01, c11 for the gradients
+            const float4 sa = make_float4(pa.x, pa.y, (0.5f * pa.z) * LOG2E_F, pa.w * LOG2E_F);
+            const float c2 = (0.5f * pb.x) * LOG2E_F;
             const float cb = a.proj_c[gid];
             const uint32_t gates = (pb.z >= 0.0f ? 1u : 0u) | (pb.w >= 0.0f ? 2u : 0u) | (cb >= 0.0f ? 4u : 0u) | 8u;
             s_a[lane] = sa;
-            s_b[lane] = make_float4(0.5f * pb.x, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
+            s_b[lane] = make_float4(c2, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
             s_c[lane] = make_float4(mx(cb, 0.0f), pa.z, pb.x, as_f(gates));
+            s_d[lane] = make_float4(pa.z * img_w, pa.w * img_w, pa.w * img_h, pb.x * img_h);
+            s_c01[lane] = pa.w;
             s_gid[lane] = gid;
-            s_mask[lane] = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, 0.5f * pb.x, pb.y, SMOOTH);
+            s_mask[lane] = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, c2, pb.y, SMOOTH);
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {
@@ -482,53 +571,61 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             const float4 sa = s_a[t];
             const float4 sbv = s_b[t];
             const float4 scv = s_c[t];
+            const float4 sdv = s_d[t];
             const float opac = sbv.y;
-            const float c00 = scv.y, c01 = sa.w, c11 = scv.z;
             const float cl_r = sbv.z, cl_g = sbv.w, cl_b = scv.x;
             bool contrib = false;
 #pragma unroll
             for (int k = 0; k < BWD_PX; ++k) {
                 if (!((live >> k) & 1u)) continue;          // uniform
-                if (!(T[k] > T_STOP)) continue;
+                const float Tk = T[k];
+                if (!(Tk > T_STOP)) continue;
                 const float dx = pcx[k] - sa.x, dy = pcy[k] - sa.y;
-                const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);
-                const float G = expf_neg(-sigma);
+                const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);   // base 2, as the forward's
+                const float G = exp2n(-sigma);
                 const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);   // == mn(): see the forward
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
                 if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
-                const float ae = alpha * w_cut;
+                const float ae = SMOOTH ? alpha * w_cut : alpha;
                 const float one_m = 1.0f - ae;
-                const float nt = T[k] * one_m;
-                if (nt <= T_STOP) { T[k] = 0.0f; continue; }
+                const float nt = Tk * one_m;
+                T[k] = (nt <= T_STOP) ? 0.0f : nt;
+                if (nt <= T_STOP) continue;
                 contrib = true;
-                const float vis = ae * T[k];
+                const float vis = ae * Tk;
                 // colour: the c >= 0 gate is per splat, applied after the reduction
                 g[5] = __builtin_fmaf(vis, vr[k], g[5]);
                 g[6] = __builtin_fmaf(vis, vg[k], g[6]);
                 g[7] = __builtin_fmaf(vis, vb[k], g[7]);
                 const float cv = __builtin_fmaf(cl_b, vb[k], __builtin_fmaf(cl_g, vg[k], cl_r * vr[k]));
                 const float ra = __builtin_amdgcn_rcpf(one_m);
-                const float v_ae = (__builtin_fmaf(T[k], cv, -D[k]) + vt[k]) * ra;
+                const float v_ae = (__builtin_fmaf(Tk, cv, -D[k]) + vt[k]) * ra;
                 const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+                D[k] = __builtin_fmaf(-vis, cv, D[k]);
                 if (opac * G <= ALPHA_CAP) {
                     const float nv = alpha * v_alpha;                // = -v_sigma
-                    const float u = __builtin_fmaf(c01, dy, c00 * dx);
-                    const float w = __builtin_fmaf(c11, dy, c01 * dx);
-                    const float vx = nv * u, vy = nv * w;            // v_xy with dx = mean - pixel
-                    g[0] += vx;
-                    g[1] += vy;
-                    const float tx_ = nv * dx, ty_ = nv * dy;
+                    const float tx_ = nv * dx, ty_ = nv * dy;        // nv (pixel - mean)
+                    // the mean gradient is conic . sum nv (pixel - mean): the conic is
+                    // applied once per splat below; here only the sums
+                    g[0] += tx_;
+                    g[1] += ty_;
                     g[2] = __builtin_fmaf(tx_, dx, g[2]);
                     g[3] = __builtin_fmaf(tx_, dy, g[3]);
                     g[4] = __builtin_fmaf(ty_, dy, g[4]);
                     g[8] = __builtin_fmaf(v_alpha, G, g[8]);
-                    const float ux = vx * img_w, uy = vy * img_h;
+                    // this pixel's mean gradient in pixels: (W (c00 tx + c01 ty), H (c01 tx + c11 ty))
+                    const float ux = __builtin_fmaf(sdv.y, ty_, sdv.x * tx_);
+                    const float uy = __builtin_fmaf(sdv.w, ty_, sdv.z * tx_);
                     g[9] = __builtin_fmaf(__builtin_amdgcn_sqrtf(__builtin_fmaf(ux, ux, uy * uy)), rscale[k], g[9]);
                 }
-                D[k] = __builtin_fmaf(-vis, cv, D[k]);
-                T[k] = nt;
             }
             if (__ballot(contrib) == 0ull) continue;          // g is still all zero
+            {
+                const float c00 = scv.y, c01 = s_c01[t], c11 = scv.z;
+                const float sx = g[0], sy = g[1];
+                g[0] = __builtin_fmaf(c01, sy, c00 * sx);
+                g[1] = __builtin_fmaf(c11, sy, c01 * sx);
+            }
             float val = reduce_scatter10(g, lane);
 #pragma unroll
             for (int i = 0; i < 10; ++i) g[i] = 0.0f;
@@ -554,7 +651,7 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
     __shared__ float4 s_b[BWD_BATCH];       // opacity, r, g, b (raw colours: the gates need the sign)
     __shared__ uint32_t s_gid[BWD_BATCH];
 
-    const uint32_t tile = xcd_tile(blockIdx.x, a.num_tiles);
+    const uint32_t tile = block_tile(a.order, blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
     if (lo >= hi) return;   // uniform per tile
@@ -644,7 +741,7 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
                 if (!(T[k] > T_STOP)) continue;
                 const SurfelHit h = surfel_hit(m0, m1, m2, m3.z, pcx[k], pcy[k]);
                 if (!(h.valid && h.sigma <= sigma_max)) continue;
-                const float G = expf_neg(-h.sigma);
+                const float G = exp2n(-(h.sigma * LOG2E_F));
                 const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
                 if (!(h.sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -734,6 +831,12 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
                               const uint32_t* n_dev) {
     if (n == 0) return hipSuccess;
     tile_ranges_kernel<<<(n + 255) / 256, 256, 0, s>>>(tiles, n, num_tiles, ranges, n_dev);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s) {
+    if (num_tiles == 0) return hipSuccess;
+    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order);
     return hipGetLastError();
 }
 

@@ -57,21 +57,26 @@ VS_DEV float expf_c(float x) {
     return __builtin_ldexpf(p, (int)n);
 }
 
-// exp for the compositing loops, where the argument is -sigma with sigma >= 0
-// already tested by the caller's cutoff: the same operation sequence as
-// expf_c for every x <= 88.7 (NaN excluded by the callers' sigma >= 0 test).
-VS_DEV float expf_neg(float x) {
-    const float n = __builtin_rintf(x * 1.44269502f);
-    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
-    r = __builtin_fmaf(-n, 1.42860677e-06f, r);
-    float q = __builtin_fmaf(0.00137514074f, r, 0.00836891588f);
-    q = __builtin_fmaf(q, r, 0.0416695327f);
-    q = __builtin_fmaf(q, r, 0.166665182f);
-    q = __builtin_fmaf(q, r, 0.499999881f);
-    const float r2 = r * r;
-    const float p = __builtin_fmaf(r2, q, r) + 1.0f;
-    const float v = __builtin_ldexpf(p, (int)n);
-    return (x < -87.33654f) ? 0.0f : v;
+// exp2 for the compositing loops, whose argument is -sigma in base-2 units
+// (the conic is staged pre-scaled by LOG2E_F): x = max(x, -127) (NaN ->
+// -127), n = rint(x), f = x - n in [-1/2, 1/2] (exact), 2^f = 1 + f P(f)
+// with P of degree 4 (least maximum relative error on [-1/2, 1/2]), result
+// ldexp(p, n): <= 2.1 ulp on [-126, 0]; v_max, v_rndne, v_sub, five FMAs,
+// v_cvt, v_ldexp.  The CPU restatement also clamps x at 128 to keep its int
+// conversion defined; the results agree for every x: above 128 both give
+// +inf (here the conversion saturates), and a positive x comes only from a
+// pair the sigma >= 0 test rejects.
+constexpr float LOG2E_F = 1.44269502f;
+VS_DEV float exp2n(float x) {
+    x = __builtin_fmaxf(x, -127.0f);
+    const float n = __builtin_rintf(x);
+    const float f = x - n;
+    float p = __builtin_fmaf(1.326472731e-03f, f, 9.671512991e-03f);
+    p = __builtin_fmaf(p, f, 5.550733581e-02f);
+    p = __builtin_fmaf(p, f, 2.402224243e-01f);
+    p = __builtin_fmaf(p, f, 6.931470037e-01f);
+    p = __builtin_fmaf(p, f, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
 }
 
 // log: m = x 2^-e in [sqrt(1/2), sqrt(2)), s = (m-1)/(m+1),
@@ -282,7 +287,8 @@ VS_DEV float calc_sigma(float px, float py, S2 c, float x, float y) {
     return 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
 }
 
-// Compositing form of sigma (contract): A = c00/2, B = c01, C = c11/2.
+// Compositing form of sigma (contract), in base-2 units with the staged
+// A = (c00/2) log2 e, B = c01 log2 e, C = (c11/2) log2 e.
 VS_DEV float raster_sigma(float A, float B, float C, float dx, float dy) {
     return __builtin_fmaf(__builtin_fmaf(A, dx, B * dy), dx, (C * dy) * dy);
 }

@@ -86,6 +86,7 @@ struct EmitArgs {
 struct RasterArgs {
     uint32_t img_w, img_h, tile_bw, tile_bh, num_tiles;
     uint32_t num_splats;             // ids at or past it (only a corrupt list holds them) are skipped
+    const uint32_t* order;           // [8 ceil(T/8)] tile of each workgroup (launch_tile_order), or null
     float bg_r, bg_g, bg_b;
     const uint32_t* gids;            // sorted intersections -> global splat id
     const uint32_t* ranges;          // [T,2]
@@ -103,6 +104,7 @@ struct RasterArgs {
 struct RasterBwdArgs {
     uint32_t img_w, img_h, tile_bw, tile_bh, num_tiles;
     uint32_t num_splats;             // ids at or past it are skipped
+    const uint32_t* order;           // [8 ceil(T/8)] tile of each workgroup, or null
     float bg_r, bg_g, bg_b;
     const uint32_t* gids;
     const uint32_t* ranges;          // shrunk ranges
@@ -250,6 +252,9 @@ hipError_t launch_validate(const void* p, bool half, uint64_t n, uint32_t row, u
 // Ranges of the first min(*n_dev, n) sorted tile ids (all n when n_dev is null).
 hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
                               const uint32_t* n_dev = nullptr);
+// Dispatch order of the raster kernels from tile ranges [T,2]: XCD bands,
+// longest list first within each (order holds 8 ceil(T/8) entries).
+hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s);
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
 // With `start` and `stop` set, the kernel is launched by hipExtLaunchKernelGGL,
 // which records the two events around the kernel's own execution.
