@@ -747,7 +747,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         RasterArgs ra{};
         ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T; ra.num_splats = N;
         // longest lists first within each XCD's band (the forward's cost grows with its list)
-        VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s), "tile order");
+        VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s, bwd_info ? st->ranges_shrunk : nullptr),
+               "tile order");
         ra.order = st->tile_order;
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
         ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;

@@ -86,7 +86,8 @@ VS_DEV uint32_t order_bin(const uint32_t* __restrict__ ranges, uint32_t t) {
 }
 
 __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(const uint32_t* __restrict__ ranges, uint32_t num_tiles,
-                                                                 uint32_t* __restrict__ order) {
+                                                                 uint32_t* __restrict__ order,
+                                                                 uint32_t* __restrict__ shrunk_init) {
     __shared__ uint32_t s_bin[ORDER_BINS];
     __shared__ uint32_t s_wave[ORDER_BLOCK / 64];
     const uint32_t per = (num_tiles + 7) / 8;
@@ -95,7 +96,14 @@ __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(const uint32_t*
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (uint32_t i = tid; i < ORDER_BINS; i += ORDER_BLOCK) s_bin[i] = 0u;
     __syncthreads();
-    for (uint32_t t = t0 + tid; t < t1; t += ORDER_BLOCK) atomicAdd(&s_bin[order_bin(ranges, t)], 1u);
+    for (uint32_t t = t0 + tid; t < t1; t += ORDER_BLOCK) {
+        atomicAdd(&s_bin[order_bin(ranges, t)], 1u);
+        if (shrunk_init) {   // the forward's shrunk ranges start empty at the range start
+            const uint32_t lo = ranges[2 * t];
+            shrunk_init[2 * t] = lo;
+            shrunk_init[2 * t + 1] = lo;
+        }
+    }
     __syncthreads();
     // exclusive scan of the bins: each thread owns bins 2 tid and 2 tid + 1
     const uint32_t c0 = s_bin[2 * tid], c1 = s_bin[2 * tid + 1];
@@ -173,8 +181,26 @@ VS_DEV uint32_t quadrant_mask(float x0, float y0, float mx_, float my_, float A,
     return mask;
 }
 
-// kernels/helpers.rs:105-113: pixel of lane l in a 256-lane tile in Morton
-// order, so wavefront w = l / 64 owns the 8x8 quadrant w.
+// The same test for one quadrant whose first pixel centre is (x0, y0): true
+// when some pixel of its 8 x 8 block may pass the cutoff.
+VS_DEV bool quadrant_live(float x0, float y0, float mx_, float my_, float A, float B, float C, float opac, bool smooth) {
+    const float cut = smooth ? (ALPHA_MID - 0.5f * ALPHA_BAND) : ALPHA_MID;
+    const float thr = (QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS) * LOG2E_F;
+    const float four_ac = 4.0f * A * C;
+    if (!(A > 0.0f && C > 0.0f && four_ac - B * B > QUAD_MIN_DECORR * four_ac && thr < 3.0e38f)) return true;
+    const float kx = -B / (2.0f * C);
+    const float ky = -B / (2.0f * A);
+    const float a0 = x0 - mx_, a1 = a0 + 7.0f;
+    const float b0 = y0 - my_, b1 = b0 + 7.0f;
+    const bool inside = a0 <= 0.0f && a1 >= 0.0f && b0 <= 0.0f && b1 >= 0.0f;
+    float m = __builtin_fminf(edge_min(A, B, C, kx, a0, b0, b1), edge_min(A, B, C, kx, a1, b0, b1));
+    m = __builtin_fminf(m, __builtin_fminf(edge_min(C, B, A, ky, b0, a0, a1), edge_min(C, B, A, ky, b1, a0, a1)));
+    return inside || !(m > thr);
+}
+
+// Morton order of the 64 lanes over an 8 x 8 quadrant (kernels/helpers.rs:
+// 105-113 lay a tile out the same way): lane l holds pixel
+// (even bits of l, odd bits of l).
 VS_DEV uint32_t compact_bits_16(uint32_t v) {
     uint32_t x = v & 0x55555555u;
     x = (x | (x >> 1)) & 0x33333333u;
@@ -184,39 +210,46 @@ VS_DEV uint32_t compact_bits_16(uint32_t v) {
     return x;
 }
 
-constexpr int FWD_BLOCK = 256;
+constexpr int FWD_BATCH = 64;
 
-// SURF: surfels (2DGS): coverage by the pixel ray's sample of the surfel's
-// plane (vs_surfel.h), depth from the intersection, the normal from the row;
-// no quadrant culling (the binning ellipse, not the coverage, is an ellipse).
+// Forward, kernels/rasterize.rs:109-420.  One 64-lane wavefront, its own
+// workgroup, per 8 x 8 quadrant of a 16 x 16 tile, one pixel per lane.  The
+// four quadrant workgroups of a tile are dealt to one XCD one after another
+// (XCD b % 8 starts its blocks in index order; its i-th is quadrant i % 4 of
+// the tile in dispatch slot i / 4), so the tile's splat rows are shared in
+// one L2, yet no quadrant waits on another: each stages the tile's
+// depth-sorted splats 64 at a time into its LDS, keeps in a compacted list
+// those that may reach the quadrant (quadrant_live; surfels keep all), walks
+// the list, and leaves as soon as its 64 pixels are done.  The tile's shrunk
+// range end (one past its last blended intersection) is the maximum over its
+// quadrants, kept with an atomic max on an end the dispatch-order pass set
+// to the range start.
 template <bool BWD, bool GEOM, bool SMOOTH, bool SURF>
-__global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
+__global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
     // Every per-splat array has 16-byte slots, so one LDS address, the slot's
-    // byte offset kept in the per-quadrant lists, serves all reads of a splat.
-    __shared__ float4 s_a[FWD_BLOCK];    // x, y, A, B (the conic in base-2 units)
-    __shared__ float4 s_b[FWD_BLOCK];    // C, opacity, max(r,0), max(g,0)
-    __shared__ float4 s_c[FWD_BLOCK];    // max(b,0), -, -, -
-    __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BLOCK : 1];
-    __shared__ float4 s_s[SURF ? FWD_BLOCK * 4 : 1];
-    __shared__ uint32_t s_gid[BWD ? FWD_BLOCK : 1];
-    __shared__ uint4 s_hit[BWD ? FWD_BLOCK : 1];   // .x = 1 once the slot blended a pixel
-    __shared__ uint16_t s_list[4][FWD_BLOCK];      // per-quadrant live slots as byte offsets (slot * 16)
-    __shared__ uint32_t s_qcnt[4][4];                 // [wavefront][quadrant] live-slot counts
-    __shared__ uint32_t s_last;
+    // byte offset kept in the list, serves all reads of a splat.
+    __shared__ float4 s_a[FWD_BATCH];    // x, y, A, B (the conic in base-2 units)
+    __shared__ float4 s_b[FWD_BATCH];    // C, opacity, max(r,0), max(g,0)
+    __shared__ float4 s_c[FWD_BATCH];    // max(b,0), -, -, -
+    __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BATCH : 1];
+    __shared__ float4 s_s[SURF ? FWD_BATCH * 4 : 1];
+    __shared__ uint4 s_hit[BWD ? FWD_BATCH : 1];   // .x = 1 once the slot blended a pixel
+    __shared__ uint16_t s_list[FWD_BATCH];         // live slots as byte offsets (slot * 16)
 
-    const uint32_t tile = block_tile(a.order, blockIdx.x, a.num_tiles);
-    if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
+    const uint32_t xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
+    const uint32_t q = idx % 4;
+    const uint32_t slot = (idx / 4) * 8 + xcd;
+    const uint32_t tile = block_tile(a.order, slot, a.num_tiles);
+    if (tile >= a.num_tiles) return;   // uniform: padding of the dispatch order
     const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
     const uint32_t l = threadIdx.x;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(l >> 6);   // Morton order: wavefront w owns quadrant w
-    const uint64_t lt_mask = (1ull << (l & 63)) - 1ull;
-    const uint32_t px = tx * TILE_W + compact_bits_16(l);
-    const uint32_t py = ty * TILE_W + compact_bits_16(l >> 1);
+    const uint32_t qx0 = tx * TILE_W + 8u * (q & 1u), qy0 = ty * TILE_W + 8u * (q >> 1);
+    const uint32_t px = qx0 + compact_bits_16(l);
+    const uint32_t py = qy0 + compact_bits_16(l >> 1);
     const bool inside = px < a.img_w && py < a.img_h;
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
-    const float x0 = (float)(tx * TILE_W) + 0.5f, y0 = (float)(ty * TILE_W) + 0.5f;
+    const float x0 = (float)qx0 + 0.5f, y0 = (float)qy0 + 0.5f;   // the quadrant's first pixel centre
     const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
-    if (BWD && l == 0) s_last = lo;
 
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
     float depth_acc = 0.0f, median = 0.0f, dist_b = 0.0f, dist_c = 0.0f, nx = 0.0f, ny = 0.0f, nz = 0.0f;
@@ -231,16 +264,13 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
     const char* const lds_d = reinterpret_cast<const char*>(s_d);
     const char* const lds_s = reinterpret_cast<const char*>(s_s);
 
-    for (uint32_t start = lo; start < hi; start += FWD_BLOCK) {
-        // Barrier + vote: protects the previous batch's LDS reads and ends the
-        // tile once every pixel is done.
-        if (__syncthreads_count(!done) == 0) break;
-        const uint32_t rem = min((uint32_t)FWD_BLOCK, hi - start);
-        uint32_t qmask = 0;
+    for (uint32_t start = lo; start < hi; start += FWD_BATCH) {
+        if (__ballot(!done) == 0ull) break;           // every pixel of the quadrant is done
+        const uint32_t rem = min((uint32_t)FWD_BATCH, hi - start);
         const uint32_t gid = (l < rem) ? a.gids[start + l] : 0xFFFFFFFFu;
-        if constexpr (BWD) {
-            if (l < rem) { s_gid[l] = 0u; s_hit[l].x = 0u; }
-        }
+        bool live = false;
+        __syncthreads();                              // the previous batch's LDS reads are complete
+        if constexpr (BWD) s_hit[l].x = 0u;
         if (gid < a.num_splats) {   // else: past the batch, or a corrupt id (dead slot)
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
@@ -251,41 +281,25 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
             s_b[l] = sb;
             s_c[l].x = mx(a.proj_c[gid], 0.0f);
             if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
-            if constexpr (BWD) s_gid[l] = gid;
             if constexpr (SURF) {
                 const float4* ps = a.proj_surf + (size_t)gid * 4;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) s_s[4 * l + k] = ps[k];
-                qmask = 0xFu;
+                live = true;
             } else {
-                qmask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
+                live = quadrant_live(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
             }
         }
-        // Per-quadrant compaction of the live slots, in slot (= depth) order.
-        uint32_t below[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint64_t b = __ballot((qmask >> q) & 1u);
-            below[q] = (uint32_t)__popcll(b & lt_mask);
-            if ((l & 63) == 0) s_qcnt[wave][q] = (uint32_t)__popcll(b);
-        }
+        // the live slots, compacted in slot (= depth) order
+        const uint64_t lm = __ballot(live);
+        if (live) s_list[__builtin_amdgcn_mbcnt_hi((uint32_t)(lm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lm, 0u))] =
+            (uint16_t)(l * 16u);
         __syncthreads();
-        uint32_t count = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t off = below[q];
-#pragma unroll
-            for (uint32_t w = 0; w < 3; ++w) off += (w < wave) ? s_qcnt[w][q] : 0u;
-            if ((qmask >> q) & 1u) s_list[q][off] = (uint16_t)(l * 16u);
-            count += (q == (int)wave) ? s_qcnt[0][q] + s_qcnt[1][q] + s_qcnt[2][q] + s_qcnt[3][q] : 0u;
-        }
-        __syncthreads();
-        const uint16_t* list = s_list[wave];
-        const uint32_t nlist = __builtin_amdgcn_readfirstlane(count);   // the same for the whole wavefront
+        const uint32_t nlist = (uint32_t)__popcll(lm);
         uint32_t last_off = 0xFFFFFFFFu;                                  // byte offset of the last slot blended
         for (uint32_t j = 0; j < nlist; ++j) {
             if (done) break;
-            const uint32_t off = list[j];
+            const uint32_t off = s_list[j];
             const float4 sb = *reinterpret_cast<const float4*>(lds_b + off);
             float sigma, zs = 0.0f, G;
             if constexpr (SURF) {
@@ -353,7 +367,7 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
         if (last_off != 0xFFFFFFFFu) last = start + (last_off >> 4) + 1u;
         if constexpr (BWD) {
             __syncthreads();
-            if (l < rem && s_hit[l].x) a.visible[s_gid[l]] = 1.0f;
+            if (gid < a.num_splats && s_hit[l].x) a.visible[gid] = 1.0f;
         }
     }
 
@@ -379,13 +393,9 @@ __global__ void __launch_bounds__(FWD_BLOCK) raster_fwd_kernel(RasterArgs a) {
         }
     }
     if constexpr (BWD) {
-        __syncthreads();
-        atomicMax(&s_last, last);
-        __syncthreads();
-        if (l == 0) {
-            a.ranges_shrunk[tile * 2] = lo;
-            a.ranges_shrunk[tile * 2 + 1] = s_last;
-        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) last = max(last, (uint32_t)__shfl_xor((int)last, o));
+        if (l == 0 && last > lo) atomicMax(&a.ranges_shrunk[tile * 2 + 1], last);
     }
 }
 
@@ -807,6 +817,12 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
     }
 }
 
+// sign(pred - gt) * inv_count on rgb, 0 on the other channels and outside
+// the mask.  The 4-channel image (the training render's) is read and written
+// as one float4 per pixel.
+VS_DEV float l1_sign(float p, float g, float inv) { const float d = p - g; return (d > 0.0f) ? inv : ((d < 0.0f) ? -inv : 0.0f); }
+
+template <bool RGBA>
 __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, const float* __restrict__ gt, uint32_t w,
                                     uint32_t h, float mcx, float mcy, float mr, float inv_count, float* __restrict__ v) {
     const uint32_t pid = blockIdx.x * blockDim.x + threadIdx.x;
@@ -817,13 +833,17 @@ __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, 
         const float dx = (float)x + 0.5f - mcx, dy = (float)y + 0.5f - mcy;
         in_mask = dx * dx + dy * dy <= mr * mr;
     }
-    for (uint32_t c = 0; c < C; ++c) {
-        float g = 0.0f;
-        if (c < 3 && in_mask) {
-            const float d = pred[(size_t)pid * C + c] - gt[(size_t)pid * 3 + c];
-            g = (d > 0.0f) ? inv_count : ((d < 0.0f) ? -inv_count : 0.0f);
-        }
-        v[(size_t)pid * C + c] = g;
+    const float inv = in_mask ? inv_count : 0.0f;
+    const float g0 = gt[(size_t)pid * 3], g1 = gt[(size_t)pid * 3 + 1], g2 = gt[(size_t)pid * 3 + 2];
+    if constexpr (RGBA) {
+        const float4 p = reinterpret_cast<const float4*>(pred)[pid];
+        reinterpret_cast<float4*>(v)[pid] =
+            in_mask ? make_float4(l1_sign(p.x, g0, inv), l1_sign(p.y, g1, inv), l1_sign(p.z, g2, inv), 0.0f)
+                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+        const float gg[3] = {g0, g1, g2};
+        for (uint32_t c = 0; c < C; ++c)
+            v[(size_t)pid * C + c] = (c < 3 && in_mask) ? l1_sign(pred[(size_t)pid * C + c], gg[c], inv) : 0.0f;
     }
 }
 
@@ -834,23 +854,24 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
     return hipGetLastError();
 }
 
-hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s) {
+hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
+                             uint32_t* shrunk_init) {
     if (num_tiles == 0) return hipSuccess;
-    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order);
+    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init);
     return hipGetLastError();
 }
 
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s) {
     if (a.num_tiles == 0) return hipSuccess;
-    const dim3 grid(xcd_grid(a.num_tiles));
+    const dim3 grid(4 * xcd_grid(a.num_tiles));   // four quadrant workgroups per dispatch slot
     if (a.proj_surf) {           // surfels: every bwd-info pass carries the geometry channels
-        if (!bwd_info) raster_fwd_kernel<false, false, false, true><<<grid, FWD_BLOCK, 0, s>>>(a);
-        else if (smooth) raster_fwd_kernel<true, true, true, true><<<grid, FWD_BLOCK, 0, s>>>(a);
-        else raster_fwd_kernel<true, true, false, true><<<grid, FWD_BLOCK, 0, s>>>(a);
-    } else if (!bwd_info) raster_fwd_kernel<false, false, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
-    else if (geometry) raster_fwd_kernel<true, true, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
-    else if (smooth) raster_fwd_kernel<true, false, true, false><<<grid, FWD_BLOCK, 0, s>>>(a);
-    else raster_fwd_kernel<true, false, false, false><<<grid, FWD_BLOCK, 0, s>>>(a);
+        if (!bwd_info) raster_fwd_kernel<false, false, false, true><<<grid, FWD_BATCH, 0, s>>>(a);
+        else if (smooth) raster_fwd_kernel<true, true, true, true><<<grid, FWD_BATCH, 0, s>>>(a);
+        else raster_fwd_kernel<true, true, false, true><<<grid, FWD_BATCH, 0, s>>>(a);
+    } else if (!bwd_info) raster_fwd_kernel<false, false, false, false><<<grid, FWD_BATCH, 0, s>>>(a);
+    else if (geometry) raster_fwd_kernel<true, true, false, false><<<grid, FWD_BATCH, 0, s>>>(a);
+    else if (smooth) raster_fwd_kernel<true, false, true, false><<<grid, FWD_BATCH, 0, s>>>(a);
+    else raster_fwd_kernel<true, false, false, false><<<grid, FWD_BATCH, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -869,7 +890,9 @@ hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float
                                float mcy, float mr, float inv_count, float* v_out, hipStream_t s) {
     const uint32_t n = w * h;
     if (n == 0) return hipSuccess;
-    l1_cotangent_kernel<<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    const bool rgba = channels == 4 && ((uintptr_t)pred & 15u) == 0 && ((uintptr_t)v_out & 15u) == 0;
+    if (rgba) l1_cotangent_kernel<true><<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    else l1_cotangent_kernel<false><<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
     return hipGetLastError();
 }
 

@@ -253,8 +253,11 @@ hipError_t launch_validate(const void* p, bool half, uint64_t n, uint32_t row, u
 hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
                               const uint32_t* n_dev = nullptr);
 // Dispatch order of the raster kernels from tile ranges [T,2]: XCD bands,
-// longest list first within each (order holds 8 ceil(T/8) entries).
-hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s);
+// longest list first within each (order holds 8 ceil(T/8) entries).  With
+// `shrunk_init`, every tile's entry there is set to (start, start): the
+// forward's shrunk ranges, whose ends it raises.
+hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
+                             uint32_t* shrunk_init = nullptr);
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
 // With `start` and `stop` set, the kernel is launched by hipExtLaunchKernelGGL,
 // which records the two events around the kernel's own execution.
