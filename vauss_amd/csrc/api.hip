@@ -563,7 +563,9 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->tbw = (W + TILE_W_HOST_ - 1) / TILE_W_HOST_;
     st->tbh = (H + TILE_W_HOST_ - 1) / TILE_W_HOST_;
     const uint64_t T64 = (uint64_t)st->tbw * st->tbh;
-    if (T64 >= 0x7FFFFFFFull) return fail(VS_ERR_INVALID, "image too large");
+    // 2^24 tiles (a 65536 x 65536 image): a wavefront's 64 bounding boxes hold
+    // under 2^30 tiles, and tile rows and offsets stay exact in f32.
+    if (T64 > (1ull << 24)) return fail(VS_ERR_INVALID, "image too large (more than 2^24 tiles)");
     st->T = (uint32_t)T64;
     const uint32_t N = st->N, T = st->T;
     const bool bwd_info = pass_bwd_info(pass);
@@ -681,7 +683,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const size_t o_tu = itake((size_t)I * 4), o_vu = itake((size_t)I * 4);
         const size_t o_t = itake((size_t)I * 4), o_v = itake((size_t)I * 4);
         const size_t o_dk = itake((size_t)M * 4), o_dv = itake((size_t)M * 4);
-        const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)N * 4);
+        const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)M * 4);
+        const size_t o_base_g = itake((size_t)N * 4);
         const size_t o_scan = itake(scan_tmp_words(M) * 4);
         const size_t o_tmp = itake(sort_tmp_bytes(std::max(I, M), false));   // serves both sorts
         VS_HIP(lib_alloc(ctx, &st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
@@ -694,7 +697,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         uint32_t* dvals = reinterpret_cast<uint32_t*>(ib + o_dv);
         uint32_t* dkeys_sorted = reinterpret_cast<uint32_t*>(ib + o_dks);
         uint32_t* order = reinterpret_cast<uint32_t*>(ib + o_ord);
-        uint32_t* slot_base = reinterpret_cast<uint32_t*>(ib + o_base);   // written for splats with hits only
+        uint32_t* slot_base = reinterpret_cast<uint32_t*>(ib + o_base);   // [M], nearest emitter first
+        uint32_t* slot_base_g = reinterpret_cast<uint32_t*>(ib + o_base_g);   // [N], written for emitters only
         uint32_t* scan_tmp = reinterpret_cast<uint32_t*>(ib + o_scan);
         uint32_t* err = ctx->dev_flags + FLAG_SORT_STALL;
         {
@@ -713,10 +717,12 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         }
         {
             StageTimer tm(ctx, ST_EMIT);
-            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order, m_dev, N), "slot scan");
+            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order, m_dev, N, true, slot_base_g),
+                   "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
-            ea.counts = st->counts; ea.slot_base = slot_base;
+            ea.num_emitters = M; ea.m_dev = m_dev; ea.order = order;
+            ea.counts = st->counts; ea.slot_base = slot_base; ea.slot_base_g = slot_base_g;
             ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u; ea.capacity = I;
             VS_HIP(launch_emit(ea, s), "emit kernel");
         }

@@ -10,10 +10,10 @@
 // smaller keys: the splats that hit a tile are compacted in global-id order
 // with their depth bits (less the minimum) as u32 keys, a stable radix sort
 // puts them in depth order (ties in global-id order), a scan of their tile
-// counts in that order gives each one its slot range, and emission (in
-// global-id order) writes one u32 tile id per hit tile into that range.  A
-// stable sort by tile id then yields each tile's list in (depth bits, global
-// id) order.
+// counts in that order gives each one its slot range, and emission writes one
+// u32 tile id per hit tile into that range.  A stable sort by tile id then
+// yields each tile's list in (depth bits, global id) order.  Counting and
+// emission test only the tiles near the ellipse's boundary (see walk_rows).
 #include <algorithm>
 #include "vs_device.h"
 #include "vs_camera.h"
@@ -25,10 +25,6 @@
 namespace vs {
 
 constexpr int PROJ_BLOCK = 256;
-// Bounding boxes up to this many tiles are walked by their own lane; larger
-// ones by the whole wavefront (kernels/map_gaussians.rs:17-19 uses 16 for the
-// same split).
-constexpr uint32_t SMALL_BBOX = 16;
 
 struct TileBox { uint32_t x0, y0, x1, y1; };
 
@@ -72,6 +68,225 @@ VS_DEV bool will_contribute(uint32_t tx, uint32_t ty, float mx_, float my_, S2 c
 VS_DEV uint32_t lane_id() { return __lane_id(); }
 VS_DEV float rl(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
 VS_DEV uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+
+// ---- tile walk: exact ranges per tile row, tests only at the boundary --------
+// The reference tests every tile of a box, a small box per thread and a large
+// one per subgroup (kernels/map_gaussians.rs:17-19, project_forward.rs:198-247).
+// Here each tile row of a box is split, from the ellipse's chords in double
+// precision, into
+//   * tiles outside an outer range, which the test cannot pass: they lie
+//     outside the ellipse sigma <= P (1 + 4e-3) + 1e-4 with half a pixel to
+//     spare, while the test evaluates sigma at a point of the tile (within
+//     5e-4 px of it) in f32, within 5 ulp x (1 + rho) / (1 - rho) = 1.3e-3
+//     relative for the conics admitted below (rho = |c01| / sqrt(c00 c11));
+//   * tiles inside an interior range, which it must pass: they lie inside
+//     sigma <= P (1 - 4e-3) - 1e-4 with 0.05 px to spare;
+//   * the rest, on which will_contribute runs as the reference's does.
+// Conics with c01^2 > 0.999 c00 c11 (f32 sigma too inexact to rely on) test
+// every tile of the box.  All of it is load-balanced over the wavefront: its
+// box rows are laid end to end and walked 64 at a time, and each step's
+// boundary tiles (and, for emission, interior tiles) likewise.  The set of
+// tiles that pass is exactly the reference's; emission writes a splat's tiles
+// in an order of its own, which the stable tile sort makes irrelevant (a
+// splat has one entry per tile, and entries of one tile keep slot order).
+constexpr float BAND_OUT = 0.5f;      // px of slack around the outer range
+constexpr float BAND_IN = 0.05f;      // px of slack inside the interior range
+
+struct RowLds {
+    float4 geo[64];       // per splat: px, py, c00, c01
+    float2 geo2[64];      // c11, power
+    uint4 box[64];        // x0, x1, y0, exact ranges (1) or every tile (0)
+    uint4 word[64];       // caller words: slot base, global id, count
+    uint32_t acc[64];     // per splat: tiles that passed (count) / slots taken (emission)
+    uint32_t mark[64];    // per step: lane whose run starts at this position
+    uint32_t mark2[64];
+    uint4 row[64];        // per row of the step: owner, ty, oa, ia
+    uint4 row2[64];       // ib, ob, first interior slot, -
+    uint32_t tmp[64];
+};
+
+VS_DEV void wave_sync() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront"); __builtin_amdgcn_wave_barrier();
+                          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront"); }
+
+// One step of an enumeration over per-lane runs of n items, laid end to end.
+struct EnumStep {
+    bool active, head;    // head: first lane of its run within the step
+    uint32_t owner;       // lane whose run holds this lane's item
+    uint32_t idx;         // the item's index within that run
+    uint64_t seg;         // lanes of the step holding items of the same run
+};
+// Every lane calls this together; `visit(EnumStep)` runs once per step on
+// every lane.  `mark` is the wavefront's 64-word LDS scratch for the step.
+template <typename Visit>
+VS_DEV void wave_enum(uint32_t* mark, uint32_t n, Visit&& visit) {
+    const uint32_t lane = __lane_id();
+    uint32_t incl = n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o);
+        if ((int)lane >= o) incl += t;
+    }
+    const uint32_t excl = incl - n;
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    const uint64_t le = (lane == 63) ? ~0ull : ((2ull << lane) - 1ull);
+    for (uint32_t c0 = 0; c0 < total; c0 += 64) {
+        mark[lane] = 0xFFFFFFFFu;
+        wave_sync();
+        if (n > 0 && excl >= c0 && excl - c0 < 64u) mark[excl - c0] = lane;
+        wave_sync();
+        const uint64_t starts = __ballot(mark[lane] != 0xFFFFFFFFu);
+        const uint64_t carry = __ballot(n > 0 && excl < c0 && incl > c0);   // run begun in an earlier step
+        const uint64_t below = starts & le;
+        const uint32_t seg_lo = below ? 63u - (uint32_t)__builtin_clzll(below) : 0u;
+        EnumStep st;
+        st.owner = below ? mark[seg_lo] : (carry ? (uint32_t)__builtin_ctzll(carry) : 0u);
+        st.active = c0 + lane < total;
+        st.idx = c0 + lane - (uint32_t)__shfl((int)excl, (int)st.owner);
+        const uint64_t above = starts & ~le;
+        const uint32_t seg_hi = above ? (uint32_t)__builtin_ctzll(above) : 64u;
+        st.seg = (~0ull << seg_lo) & (seg_hi == 64u ? ~0ull : ((1ull << seg_hi) - 1ull));
+        st.head = st.active && lane == seg_lo;
+        visit(st);
+        wave_sync();
+    }
+}
+VS_DEV uint32_t lanes_below(uint64_t m) {
+    const uint32_t lane = __lane_id();
+    return (uint32_t)__popcll(m & (lane == 0 ? 0ull : (~0ull >> (64 - lane))));
+}
+
+// Ellipse chord at height dy (sigma = 0.5 (a dx^2 + c dy^2) + b dx dy <= P):
+// [l, r], or false when the line misses it (`touch`: a line at the ellipse's
+// top or bottom, where rounding may leave the discriminant just below 0,
+// still gets its one point).
+VS_DEV bool chord(double a, double b, double det, double inva, double two_a_p, double dy, double& l, double& r,
+                  bool touch = false) {
+    double disc = two_a_p - det * dy * dy;
+    if (touch) disc = fmax(disc, 0.0);
+    if (!(disc >= 0.0)) return false;
+    const double s = sqrt(disc);
+    l = (-b * dy - s) * inva;
+    r = (-b * dy + s) * inva;
+    return true;
+}
+
+// Tile-x ranges of row ty of a splat's box: [oa, ob) may pass, [ia, ib) must.
+VS_DEV void row_ranges(float px, float py, S2 cf, float power, uint4 box, uint32_t ty, uint32_t& oa, uint32_t& ia,
+                       uint32_t& ib, uint32_t& ob) {
+    const uint32_t x0 = box.x, x1 = box.y;
+    oa = x0; ob = x1; ia = ib = x1;
+    if (!box.w) return;
+    const double a = cf.c00, b = cf.c01, c = cf.c11, P = power;
+    const double det = a * c - b * b, inva = 1.0 / a;
+    const double mx_ = px, my_ = py;
+    const double p_out = P * 1.004 + 1e-4;
+    const double ex = sqrt(2.0 * c * p_out / det), ey = sqrt(2.0 * a * p_out / det);
+    // outer: the ellipse's x-extent over the row band (widened by BAND_OUT);
+    // its rightmost point is at dy = -b ex / c, its leftmost at +b ex / c
+    const double d0 = (double)(ty * TILE_W) - my_ - BAND_OUT, d1 = d0 + (double)TILE_W + 2.0 * BAND_OUT;
+    const double lo = fmax(d0, -ey), hi = fmin(d1, ey);
+    if (!(lo <= hi)) { oa = ob = x0; ia = ib = x0; return; }
+    double l, r, t;
+    chord(a, b, det, inva, 2.0 * a * p_out, fmin(fmax(b * ex / c, lo), hi), l, t, true);
+    chord(a, b, det, inva, 2.0 * a * p_out, fmin(fmax(-b * ex / c, lo), hi), t, r, true);
+    const double fo = floor((mx_ + l - BAND_OUT) / TILE_W), fe = floor((mx_ + r + BAND_OUT) / TILE_W) + 1.0;
+    oa = (uint32_t)fmin(fmax(fo, (double)x0), (double)x1);
+    ob = (uint32_t)fmin(fmax(fe, (double)oa), (double)x1);
+    ia = ib = ob;
+    // interior: tiles whose corners (widened by BAND_IN) lie inside the shrunk ellipse
+    const double p_in = P * 0.996 - 1e-4;
+    if (!(p_in > 0.0)) return;
+    const double e0 = (double)(ty * TILE_W) - my_ - BAND_IN, e1 = e0 + (double)TILE_W + 2.0 * BAND_IN;
+    double l0, r0, l1, r1;
+    if (!chord(a, b, det, inva, 2.0 * a * p_in, e0, l0, r0) || !chord(a, b, det, inva, 2.0 * a * p_in, e1, l1, r1)) return;
+    const double fi = ceil((mx_ + fmax(l0, l1) + BAND_IN) / TILE_W), fj = floor((mx_ + fmin(r0, r1) - BAND_IN) / TILE_W);
+    const double ci = fmin(fmax(fi, (double)oa), (double)ob), cj = fmin(fmax(fj, (double)oa), (double)ob);
+    if (ci < cj) { ia = (uint32_t)ci; ib = (uint32_t)cj; }
+}
+
+// Whether a conic admits the exact ranges (positive definite, |corr| <= sqrt(0.999)).
+VS_DEV uint32_t ranges_ok(S2 c, float power) {
+    const double a = c.c00, b = c.c01, cc = c.c11;
+    return (a > 0.0 && cc > 0.0 && b * b <= 0.999 * a * cc && power >= 0.0f && finite(c) && finite(power)) ? 1u : 0u;
+}
+
+// Walks the boxes of the wavefront (every lane calls it; nb == 0: no box).
+// EMIT: writes each passing tile id (and the global id) into the splat's slot
+// range [word0, word0 + count), at most `count` of them and below `capacity`;
+// otherwise counts them.  On return acc[lane] holds the lane's tiles.
+template <bool EMIT>
+VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf, float power, uint32_t base,
+                      uint32_t gid, uint32_t cnt, uint32_t tile_bw, uint32_t* tiles, uint32_t* vals, uint32_t capacity) {
+    const uint32_t lane = __lane_id();
+    L.geo[lane] = make_float4(px, py, cf.c00, cf.c01);
+    L.geo2[lane] = make_float2(cf.c11, power);
+    L.box[lane] = make_uint4(bb.x0, bb.x1, bb.y0, has ? ranges_ok(cf, power) : 0u);
+    L.word[lane] = make_uint4(base, gid, cnt, 0u);
+    L.acc[lane] = 0u;
+    const uint32_t rows = has ? bb.y1 - bb.y0 : 0u;
+    wave_enum(L.mark, rows, [&](const EnumStep& rs) {
+        // this lane's row: ranges, then a walk over the step's boundary tiles
+        const uint32_t o = rs.owner;
+        uint32_t oa = 0, ia = 0, ib = 0, ob = 0, ty = 0;
+        const float4 g = L.geo[o];
+        const float2 g2 = L.geo2[o];
+        const S2 oc{g.z, g.w, g2.x};
+        if (rs.active) {
+            const uint4 bx = L.box[o];
+            ty = bx.z + rs.idx;
+            row_ranges(g.x, g.y, oc, g2.y, bx, ty, oa, ia, ib, ob);
+        }
+        const uint32_t n_in = ib - ia;
+        uint32_t first_in = 0;
+        if (rs.active && n_in) {
+            if (EMIT) first_in = atomicAdd(&L.acc[o], n_in);
+            else atomicAdd(&L.acc[o], n_in);
+        }
+        L.row[lane] = make_uint4(o, ty, oa, ia);
+        L.row2[lane] = make_uint4(ib, ob, first_in, 0u);
+        wave_sync();
+        const uint32_t n_bd = rs.active ? (ia - oa) + (ob - ib) : 0u;
+        wave_enum(L.mark2, n_bd, [&](const EnumStep& bs) {
+            const uint4 rw = L.row[bs.owner];
+            const uint4 rw2 = L.row2[bs.owner];
+            const uint32_t left = rw.w - rw.z;
+            const uint32_t tx = bs.idx < left ? rw.z + bs.idx : rw2.x + (bs.idx - left);
+            const float4 sg = L.geo[rw.x];
+            const float2 sg2 = L.geo2[rw.x];
+            const bool hit = bs.active && will_contribute(tx, rw.y, sg.x, sg.y, S2{sg.z, sg.w, sg2.x}, sg2.y);
+            const uint64_t hm = __ballot(hit);
+            const uint32_t seg_hits = (uint32_t)__popcll(hm & bs.seg);
+            if (!EMIT) {
+                if (bs.head && seg_hits) atomicAdd(&L.acc[rw.x], seg_hits);
+            } else {
+                if (bs.head) L.tmp[lane] = seg_hits ? atomicAdd(&L.acc[rw.x], seg_hits) : 0u;
+                wave_sync();
+                if (hit) {
+                    const uint32_t seg_lo = (uint32_t)__builtin_ctzll(bs.seg);
+                    const uint32_t k = L.tmp[seg_lo] + lanes_below(hm & bs.seg);
+                    const uint4 w = L.word[rw.x];
+                    if (k < w.z && w.x + k < capacity) {
+                        tiles[w.x + k] = tx + rw.y * tile_bw;
+                        vals[w.x + k] = w.y;
+                    }
+                }
+            }
+        });
+        if (EMIT) {
+            wave_enum(L.mark2, rs.active ? n_in : 0u, [&](const EnumStep& is) {
+                if (!is.active) return;
+                const uint4 rw = L.row[is.owner];
+                const uint4 rw2 = L.row2[is.owner];
+                const uint4 w = L.word[rw.x];
+                const uint32_t k = rw2.z + is.idx;
+                if (k < w.z && w.x + k < capacity) {
+                    tiles[w.x + k] = rw.w + is.idx + rw.y * tile_bw;
+                    vals[w.x + k] = w.y;
+                }
+            });
+        }
+    });
+}
 
 VS_DEV uint32_t wave_sum(uint32_t v) {
 #pragma unroll
@@ -328,34 +543,13 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
         } while (false);
     }
 
-    // Tile counting (kernels/helpers.rs:253-273; wave-cooperative walk for
-    // big boxes as kernels/project_forward.rs:198-247 does per subgroup).
-    const uint32_t bw = bb.x1 - bb.x0;
-    const uint32_t nb = visible ? (bb.y1 - bb.y0) * bw : 0u;
-    uint32_t hits = 0;
-    if (visible && nb <= SMALL_BBOX) {
-        for (uint32_t i = 0; i < nb; ++i) {
-            const uint32_t tx = i % bw + bb.x0, ty = i / bw + bb.y0;
-            if (will_contribute(tx, ty, px, py, conic, power)) ++hits;
-        }
-    }
-    uint64_t pending = __ballot(visible && nb > SMALL_BBOX);
+    // Tile counting (kernels/helpers.rs:253-273): the StopThePop test on every
+    // tile of the box, in a load-balanced walk over the wavefront's boxes.
+    __shared__ RowLds s_walk[PROJ_BLOCK / 64];
     const uint32_t lane = lane_id();
-    while (pending) {
-        const int leader = __builtin_ctzll(pending);
-        const float lx = rl(px, leader), ly = rl(py, leader);
-        const S2 lc{rl(conic.c00, leader), rl(conic.c01, leader), rl(conic.c11, leader)};
-        const float lp = rl(power, leader);
-        const uint32_t lx0 = rl(bb.x0, leader), ly0 = rl(bb.y0, leader), lw = rl(bw, leader), ln = rl(nb, leader);
-        uint32_t total = 0;
-        for (uint32_t t0 = 0; t0 < ln; t0 += 64) {
-            const uint32_t t = t0 + lane;
-            const bool hit = t < ln && will_contribute(t % lw + lx0, t / lw + ly0, lx, ly, lc, lp);
-            total += (uint32_t)__popcll(__ballot(hit));
-        }
-        if ((int)lane == leader) hits = total;
-        pending &= pending - 1;
-    }
+    RowLds& L = s_walk[threadIdx.x / 64];
+    walk_rows<false>(L, visible, bb, px, py, conic, power, 0u, 0u, 0u, a.tile_bw, nullptr, nullptr, 0u);
+    const uint32_t hits = L.acc[lane];
 
     if (g < a.num_splats) {
         a.opacities[g] = opac_out;
@@ -414,18 +608,39 @@ __global__ void __launch_bounds__(PROJ_BLOCK) compact_kernel(CompactArgs a) {
     }
 }
 
-// Emission (kernels/map_gaussians.rs:23-174), one lane per splat in global-id
-// order so the projected rows are read coalesced: a splat with hits owns the
-// slots [slot_base, slot_base + count), which a scan in depth order assigned,
-// and writes there the ids of the tiles that pass the tile test, in row-major
-// box order; if the recomputed test finds fewer tiles than the projection
-// counted, the rest of its slots get the sentinel tile id T, which sorts last
-// and owns no range.
+// Emission (kernels/map_gaussians.rs:23-174): a splat with hits owns the
+// slots [base, base + count), which the scan in depth order assigned, and
+// writes there the ids of the tiles that pass the tile test, in row-major box
+// order.  One launch, two kinds of blocks:
+//  * the first EMIT_BIG_BLOCKS(N) blocks walk the splats whose box exceeds
+//    EMIT_SMALL_BOX tiles, one lane per splat in global-id order, where large
+//    boxes are spread evenly over the wavefronts (in depth order the nearest,
+//    largest ones would share the first wavefronts);
+//  * the rest walk the other splats in depth order, one lane per emitter:
+//    neighbouring lanes own neighbouring slot ranges, so a wavefront's stores
+//    fill one contiguous stretch of the list.
+// If the recomputed test finds fewer tiles than the projection counted, the
+// rest of a splat's slots get the sentinel tile id T, which sorts last and
+// owns no range.
+constexpr uint32_t EMIT_SMALL_BOX = 32;
+VS_DEV uint32_t emit_big_blocks(uint32_t n) { return (n + PROJ_BLOCK - 1) / PROJ_BLOCK; }
+
 __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
-    const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
     const uint32_t lane = lane_id();
-    const uint32_t cnt = (g < a.num_splats) ? a.counts[g] : 0u;
-    const uint32_t base = (cnt > 0) ? a.slot_base[g] : 0u;
+    const uint32_t big_blocks = emit_big_blocks(a.num_splats);
+    const bool big = blockIdx.x < big_blocks;
+    uint32_t g = 0xFFFFFFFFu, base = 0u;
+    if (big) {
+        g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+    } else {
+        const uint32_t j = (blockIdx.x - big_blocks) * PROJ_BLOCK + threadIdx.x;
+        const uint32_t m = a.m_dev ? min(*a.m_dev, a.num_emitters) : a.num_emitters;
+        if (j < m) {
+            g = a.order[j];
+            base = a.slot_base[j];
+        }
+    }
+    uint32_t cnt = (g < a.num_splats) ? a.counts[g] : 0u;
     float px = 0.0f, py = 0.0f, power = 0.0f;
     S2 conic{0.0f, 0.0f, 0.0f};
     TileBox bb{0, 0, 0, 0};
@@ -440,50 +655,18 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
         bbox_extent(conic, power, ex, ey);
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
     }
-    const uint32_t bw = bb.x1 - bb.x0;
-    const uint32_t nb = (cnt > 0) ? (bb.y1 - bb.y0) * bw : 0u;
+    const uint32_t nb = (cnt > 0) ? (bb.y1 - bb.y0) * (bb.x1 - bb.x0) : 0u;
+    if (big != (nb > EMIT_SMALL_BOX)) cnt = 0u;     // the other kind of block emits it
+    if (big && cnt > 0) base = a.slot_base_g[g];
+    __shared__ RowLds s_walk[PROJ_BLOCK / 64];
+    RowLds& L = s_walk[threadIdx.x / 64];
+    // a splat's count bounds its slots; slots past the arena are dropped
+    walk_rows<true>(L, cnt > 0, bb, px, py, conic, power, base, g, cnt, a.tile_bw, a.tiles, a.vals, a.capacity);
+    const uint32_t emitted = L.acc[lane];
     const uint32_t sentinel = a.tile_bw * a.tile_bh;
-    if (cnt > 0 && nb <= SMALL_BBOX) {
-        uint32_t k = 0;
-        for (uint32_t i = 0; i < nb; ++i) {
-            const uint32_t tx = i % bw + bb.x0, ty = i / bw + bb.y0;
-            if (k < cnt && will_contribute(tx, ty, px, py, conic, power)) {
-                if (base + k < a.capacity) {
-                    a.tiles[base + k] = tx + ty * a.tile_bw;
-                    a.vals[base + k] = g;
-                }
-                ++k;
-            }
-        }
-        for (; k < cnt && base + k < a.capacity; ++k) { a.tiles[base + k] = sentinel; a.vals[base + k] = g; }
-    }
-    uint64_t pending = __ballot(cnt > 0 && nb > SMALL_BBOX);
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    while (pending) {
-        const int leader = __builtin_ctzll(pending);
-        const float lx = rl(px, leader), ly = rl(py, leader);
-        const S2 lc{rl(conic.c00, leader), rl(conic.c01, leader), rl(conic.c11, leader)};
-        const float lp = rl(power, leader);
-        const uint32_t lx0 = rl(bb.x0, leader), ly0 = rl(bb.y0, leader), lw = rl(bw, leader), ln = rl(nb, leader);
-        const uint32_t lbase = rl(base, leader), lcnt = rl(cnt, leader), lg = rl(g, leader);
-        uint32_t emitted = 0;
-        for (uint32_t t0 = 0; t0 < ln; t0 += 64) {
-            const uint32_t t = t0 + lane;
-            const uint32_t tx = t % lw + lx0, ty = t / lw + ly0;
-            const bool hit = t < ln && will_contribute(tx, ty, lx, ly, lc, lp);
-            const uint64_t m = __ballot(hit);
-            const uint32_t slot = emitted + (uint32_t)__popcll(m & lt_mask);
-            if (hit && slot < lcnt && lbase + slot < a.capacity) {
-                a.tiles[lbase + slot] = tx + ty * a.tile_bw;
-                a.vals[lbase + slot] = lg;
-            }
-            emitted += (uint32_t)__popcll(m);
-        }
-        for (uint32_t p = (emitted < lcnt ? emitted : lcnt) + lane; p < lcnt && lbase + p < a.capacity; p += 64) {
-            a.tiles[lbase + p] = sentinel;
-            a.vals[lbase + p] = lg;
-        }
-        pending &= pending - 1;
+    for (uint32_t k = emitted; k < cnt && base + k < a.capacity; ++k) {
+        a.tiles[base + k] = sentinel;
+        a.vals[base + k] = g;
     }
 }
 
@@ -554,8 +737,9 @@ hipError_t launch_compact(const CompactArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s) {
-    if (a.num_splats == 0) return hipSuccess;
-    emit_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
+    if (a.num_emitters == 0 || a.num_splats == 0) return hipSuccess;
+    const uint32_t big_blocks = (a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK;   // emit_big_blocks
+    emit_kernel<<<big_blocks + (a.num_emitters + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -34,15 +34,35 @@ namespace vs {
 constexpr int BWD_BATCH = 64;
 
 // get_tile_offset.rs:11-59: [start, end) of each tile in the sorted ids.
-__global__ void tile_ranges_kernel(const uint32_t* __restrict__ tiles, uint32_t n_cap, uint32_t num_tiles,
-                                   uint32_t* __restrict__ ranges, const uint32_t* __restrict__ n_dev) {
+// Four sorted entries per thread (one 16-byte load): a tile's range starts
+// where its id differs from the entry before and ends where it differs from
+// the entry after.
+__global__ void __launch_bounds__(256) tile_ranges_kernel(const uint32_t* __restrict__ tiles, uint32_t n_cap,
+                                                          uint32_t num_tiles, uint32_t* __restrict__ ranges,
+                                                          const uint32_t* __restrict__ n_dev) {
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const uint32_t tile = tiles[i];
-    if (tile >= num_tiles) return;   // sentinel rows sort last and own no tile
-    if (i == 0 || tiles[i - 1] != tile) ranges[tile * 2] = i;
-    if (i + 1 == n || tiles[i + 1] != tile) ranges[tile * 2 + 1] = i + 1;
+    const uint64_t i0 = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    uint32_t v[5];
+    if (i0 + 4 <= n) {
+        const uint4 q = reinterpret_cast<const uint4*>(tiles)[i0 / 4];
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = (i0 + k < n) ? tiles[i0 + k] : 0xFFFFFFFFu;
+    }
+    v[4] = (i0 + 4 < n) ? tiles[i0 + 4] : 0xFFFFFFFFu;
+    uint32_t prev = i0 ? tiles[i0 - 1] : 0xFFFFFFFFu;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint64_t i = i0 + k;
+        const uint32_t tile = v[k];
+        if (i < n && tile < num_tiles) {   // sentinel rows sort last and own no tile
+            if (prev != tile) ranges[tile * 2] = (uint32_t)i;
+            if (v[k + 1] != tile) ranges[tile * 2 + 1] = (uint32_t)i + 1;
+        }
+        prev = tile;
+    }
 }
 
 // DIST_NEAR / DIST_FAR depth map, kernels/helpers.rs:91-103.
@@ -850,7 +870,7 @@ __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, 
 hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
                               const uint32_t* n_dev) {
     if (n == 0) return hipSuccess;
-    tile_ranges_kernel<<<(n + 255) / 256, 256, 0, s>>>(tiles, n, num_tiles, ranges, n_dev);
+    tile_ranges_kernel<<<(uint32_t)(((uint64_t)n + 1023) / 1024), 256, 0, s>>>(tiles, n, num_tiles, ranges, n_dev);
     return hipGetLastError();
 }
 

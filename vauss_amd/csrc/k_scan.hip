@@ -44,9 +44,10 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t& excl, 
 }
 
 // With a permutation `perm`, element i of the scanned sequence is in[perm[i]]
-// and its result is written to out[perm[i]].  Entries at or past
-// `perm_bound` (only a corrupt permutation holds them) read as 0 and are not
-// written, so a bad permutation cannot index out of bounds.
+// and its result is written to out[perm[i]] (out[i] with `in_order`, and then
+// also to out2[perm[i]] when out2 is given).  Entries at or past `perm_bound`
+// (only a corrupt permutation holds them) read as 0 and are not scattered, so
+// a bad permutation cannot index out of bounds.
 __device__ __forceinline__ uint32_t scan_load(const uint32_t* __restrict__ in, const uint32_t* __restrict__ perm,
                                               uint64_t idx, uint32_t perm_bound) {
     if (!perm) return in[idx];
@@ -80,7 +81,8 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_reduce_kernel(const uint32_t*
 __global__ void __launch_bounds__(SCAN_BLOCK) scan_block_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
                                                                 uint64_t n_cap, const uint32_t* __restrict__ offsets,
                                                                 int inclusive, const uint32_t* __restrict__ perm,
-                                                                const uint32_t* __restrict__ n_dev, uint32_t perm_bound) {
+                                                                const uint32_t* __restrict__ n_dev, uint32_t perm_bound,
+                                                                int in_order, uint32_t* __restrict__ out2) {
     const uint64_t n = scan_count(n_cap, n_dev);
     __shared__ uint32_t s_data[SCAN_TILE];
     __shared__ uint32_t s_w[48];
@@ -111,8 +113,12 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_block_kernel(const uint32_t* 
         const uint32_t li = i * SCAN_BLOCK + threadIdx.x;
         const uint64_t idx = base + li;
         if (idx < n) {
-            const uint64_t j = perm ? (uint64_t)perm[idx] : idx;
-            if (!perm || j < perm_bound) out[j] = s_data[li];
+            const uint64_t j = (perm && !in_order) ? (uint64_t)perm[idx] : idx;
+            if (!perm || in_order || j < perm_bound) out[j] = s_data[li];
+            if (out2) {
+                const uint32_t k = perm[idx];
+                if (k < perm_bound) out2[k] = s_data[li];
+            }
         }
     }
 }
@@ -146,14 +152,16 @@ hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_
 
 hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
                     uint32_t* total_out, hipStream_t s, const uint32_t* perm, const uint32_t* n_dev,
-                    uint32_t perm_bound) {
+                    uint32_t perm_bound, bool out_in_order, uint32_t* out_scattered) {
+    const int in_order = out_in_order ? 1 : 0;
+    uint32_t* out2 = (perm && out_in_order) ? out_scattered : nullptr;
     if (n == 0) {
         if (total_out) return scan_single_block(tmp, 0, false, total_out, s);
         return hipSuccess;
     }
     const uint64_t blocks = (n + SCAN_TILE - 1) / SCAN_TILE;
     if (blocks == 1) {
-        scan_block_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, out, n, nullptr, inclusive ? 1 : 0, perm, n_dev, perm_bound);
+        scan_block_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, out, n, nullptr, inclusive ? 1 : 0, perm, n_dev, perm_bound, in_order, out2);
         if (total_out) {
             scan_reduce_kernel<<<1, SCAN_BLOCK, 0, s>>>(in, n, tmp, perm, n_dev, perm_bound);
             hipError_t e = hipGetLastError();
@@ -167,7 +175,7 @@ hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusiv
     if (e != hipSuccess) return e;
     e = scan_single_block(tmp, (uint32_t)blocks, false, total_out, s);
     if (e != hipSuccess) return e;
-    scan_block_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, tmp, inclusive ? 1 : 0, perm, n_dev, perm_bound);
+    scan_block_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, tmp, inclusive ? 1 : 0, perm, n_dev, perm_bound, in_order, out2);
     return hipGetLastError();
 }
 

@@ -74,8 +74,12 @@ struct CompactArgs {
 
 struct EmitArgs {
     uint32_t num_splats, tile_bw, tile_bh;
+    uint32_t num_emitters;           // M: length of `order` (a capacity when m_dev is set)
+    const uint32_t* m_dev;           // device count of emitters (lagged renders), or null
+    const uint32_t* order;           // [M] global ids of the emitters, nearest first
     const uint32_t* counts;          // [N]
-    const uint32_t* slot_base;       // [N] first slot of each splat with hits (scan in depth order)
+    const uint32_t* slot_base;       // [M] first slot of the j-th nearest emitter (exclusive scan)
+    const uint32_t* slot_base_g;     // [N] the same, at the global id (emitters only)
     const float4* proj_a;
     const float4* proj_b;
     uint32_t* tiles;                 // [capacity] tile id (T = sentinel)
@@ -287,16 +291,18 @@ hipError_t launch_b8_zero_rows(uint32_t* codes, uint32_t n, const uint32_t* rows
 hipError_t launch_count_mask(uint32_t w, uint32_t h, float mcx, float mcy, float mr, uint32_t* out, hipStream_t s);
 
 // Scans.  `tmp` needs scan_tmp_words(n) u32 words.  With a permutation `perm`
-// (n distinct indices below `perm_bound`, the length of `in` and `out`) the
-// scan runs along it: element i of the sequence is in[perm[i]] and its
-// result goes to out[perm[i]]; an index at or past perm_bound reads 0 and
-// writes nothing.
+// (n distinct indices below `perm_bound`, the length of `in`) the scan runs
+// along it: element i of the sequence is in[perm[i]] and its result goes to
+// out[perm[i]], or to out[i] when `out_in_order` is set, in which case
+// `out_scattered` (if given) also receives it at [perm[i]]; an index at or
+// past perm_bound reads 0 (and is not scattered).
 size_t scan_tmp_words(uint64_t n);
 // `n_dev` (device, may be null): only the first min(*n_dev, n) elements are
 // scanned, read and written.
 hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusive, uint32_t* tmp,
                     uint32_t* total_out, hipStream_t s, const uint32_t* perm = nullptr,
-                    const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu);
+                    const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu, bool out_in_order = false,
+                    uint32_t* out_scattered = nullptr);
 hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_t* total_out, hipStream_t s);
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
