@@ -187,3 +187,75 @@ def test_surfel_floor_background_f16():
     rg = ref.backward(v_out)
     _check_surfel_grads(g, rg, ref, g.v_combined.cpu().numpy())
     out.state.free()
+
+
+def _grazing_scene(n, rng):
+    """Surfels whose normal lies within 10 degrees of perpendicular to the ray from
+    the camera at (0, 0, -5): the disk is seen almost edge-on."""
+    mean = rng.uniform([-1.2, -0.9, -1.5], [1.2, 0.9, 2.0], (n, 3))
+    view = mean - np.array([0.0, 0.0, -5.0])
+    view /= np.linalg.norm(view, axis=1, keepdims=True)
+    w = rng.standard_normal((n, 3))
+    w -= (w * view).sum(1, keepdims=True) * view
+    w /= np.linalg.norm(w, axis=1, keepdims=True)
+    tilt = np.radians(rng.uniform(-10.0, 10.0, (n, 1)))
+    nrm = np.cos(tilt) * w + np.sin(tilt) * view
+    a = np.cross(nrm, rng.standard_normal((n, 3)))
+    a /= np.linalg.norm(a, axis=1, keepdims=True)
+    b = np.cross(nrm, a)
+    rot = np.stack([a, b, nrm], axis=2)                       # columns: disk axes, normal
+    # rotation matrix -> quaternion (w, x, y, z), the largest-component branch per row
+    q = np.zeros((n, 4))
+    for i in range(n):
+        m = rot[i]
+        tr = np.trace(m)
+        if tr > 0:
+            s = np.sqrt(tr + 1.0) * 2
+            q[i] = [0.25 * s, (m[2, 1] - m[1, 2]) / s, (m[0, 2] - m[2, 0]) / s, (m[1, 0] - m[0, 1]) / s]
+        else:
+            k = int(np.argmax(np.diag(m)))
+            j, l = (k + 1) % 3, (k + 2) % 3
+            s = np.sqrt(1.0 + m[k, k] - m[j, j] - m[l, l]) * 2
+            v = np.zeros(3)
+            v[k] = 0.25 * s
+            v[j] = (m[j, k] + m[k, j]) / s
+            v[l] = (m[l, k] + m[k, l]) / s
+            q[i] = [(m[l, j] - m[j, l]) / s, *v]
+    t = np.zeros((n, 10), np.float32)
+    t[:, 0:3] = mean
+    t[:, 3:7] = q
+    t[:, 7:9] = rng.uniform(-3.0, 0.0, (n, 2))
+    t[:, 9] = -6.0
+    sh = rng.uniform(0.0, 1.0, (n, 1, 3)).astype(np.float32)
+    o = rng.uniform(-1.0, 4.0, n).astype(np.float32)
+    return t, sh, o
+
+
+@pytest.mark.parametrize("pass_", [va.RasterPass.BACKWARD, va.RasterPass.BACKWARD_SMOOTH_CUTOFF],
+                         ids=["hard", "smooth"])
+def test_surfel_grazing_bit_exact(pass_):
+    """Nearly edge-on surfels, where the ray-plane footprint is ill-conditioned
+    and the raster's quadrant culling (surfel_quadrant_live) rests on its
+    rounding bound: the image stays bit-exact and the raster gradients at the
+    contract bar."""
+    rng = np.random.default_rng(11)
+    t, sh, o = _grazing_scene(3000, rng)
+    img = (256, 192)
+    cam = scenes.test_camera(img, fov=0.6).uniforms(img)
+    print(f"[case] surfel grazing pass={pass_.name}", flush=True)
+    args = [torch.from_numpy(x).cuda() for x in (t, sh, o)]
+    out = va.render(cam, img, *args, pass_=pass_, render_mode=SURFEL)
+    ref = po.render_forward(cam, img, t, sh, o, flags=_flags(pass_))
+    assert ref.info.num_visible > 1000
+    _check_surfel_rows(out, ref)
+    got = out.out_img.cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), ref.get(po.F_OUT_IMG).view(np.uint32))
+    v_out = np.zeros_like(got)
+    v_out[..., :4] = l1_cotangent_np(got[..., :4], np.full(got.shape[:2] + (3,), 0.5, np.float32))
+    g = va.render_backward(out, *args, torch.from_numpy(v_out).cuda())
+    rg = ref.backward(v_out)
+    vc = g.v_combined.cpu().numpy()
+    assert np.count_nonzero(np.any(vc != 0, axis=1)) > 100
+    for sl, name in ((slice(0, 9), "v_M"), (slice(9, 12), "v_normal"), (slice(12, 15), "v_rgb"), (15, "v_alpha")):
+        _check_grads(vc[:, sl], rg["v_combined"][:, sl], name)
+    out.state.free()

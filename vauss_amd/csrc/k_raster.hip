@@ -230,6 +230,60 @@ VS_DEV uint32_t compact_bits_16(uint32_t v) {
     return x;
 }
 
+// Surfel quadrant culling.  A surfel's pixel sigma is
+// 0.5 min(u^2 + v^2, 2 |pixel - centre|^2) (surfel_hit), and alpha is below
+// the cutoff c whenever sigma > ln(opac / c); with s = 1.01 ln(opac / c) +
+// 0.01 a quadrant is dead when, over its pixel centres, both
+//   * the low-pass disk misses: |pixel - centre|^2 > s, and
+//   * the ray-plane disk misses: u^2 + v^2 > 2 s (1 + 1e-3).
+// q = h_u x h_v = R0 x R1 + x (R1 x R2) - y (R0 x R2) is affine in the pixel
+// (x, y) (R0, R1, R2 the rows of M), and (u, v) = (q.x, q.y) / q.z.  Over the
+// quadrant the exact q lies in the box of its four corner values, and the
+// f32 q of surfel_hit within E of it at every pixel, E = 16 ulp of the sum of
+// the magnitudes the cross product multiplies (its inputs bounded as
+// |R0| + |x| |R2|, |R1| + |y| |R2|), so every pixel's q is in the corner box
+// widened by 2E.  If q.z keeps one sign across that box, u and v lie in its
+// interval quotients, and the plane test uses the box they span.  Anything
+// else (q.z near 0, non-finite rows) keeps the quadrant.
+VS_DEV bool surfel_quadrant_live(float x0, float y0, float4 m0, float4 m1, float4 m2, float opac, bool smooth) {
+    const float cut = smooth ? (ALPHA_MID - 0.5f * ALPHA_BAND) : ALPHA_MID;
+    const float s = QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS;
+    if (!(s < 3.0e38f)) return true;
+    // low-pass disk around the projected centre (m2.y, m2.z)
+    const float a0 = x0 - m2.y, a1 = a0 + 7.0f, b0 = y0 - m2.z, b1 = b0 + 7.0f;
+    const float nx_ = __builtin_fminf(__builtin_fmaxf(0.0f, a0), a1), ny_ = __builtin_fminf(__builtin_fmaxf(0.0f, b0), b1);
+    if (!(nx_ * nx_ + ny_ * ny_ > s)) return true;
+    const F3 r0{m0.x, m0.y, m0.z}, r1{m0.w, m1.x, m1.y}, r2{m1.z, m1.w, m2.x};
+    float lo[3] = {3.0e38f, 3.0e38f, 3.0e38f}, hi[3] = {-3.0e38f, -3.0e38f, -3.0e38f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float x = x0 + ((c & 1) ? 7.0f : 0.0f), y = y0 + ((c & 2) ? 7.0f : 0.0f);
+        const float hux = r0.x - x * r2.x, huy = r0.y - x * r2.y, huz = r0.z - x * r2.z;
+        const float hvx = r1.x - y * r2.x, hvy = r1.y - y * r2.y, hvz = r1.z - y * r2.z;
+        const float q[3] = {huy * hvz - huz * hvy, huz * hvx - hux * hvz, hux * hvy - huy * hvx};
+#pragma unroll
+        for (int i = 0; i < 3; ++i) { lo[i] = __builtin_fminf(lo[i], q[i]); hi[i] = __builtin_fmaxf(hi[i], q[i]); }
+    }
+    const float xm = __builtin_fmaxf(fabsf(x0), fabsf(x0 + 7.0f)), ym = __builtin_fmaxf(fabsf(y0), fabsf(y0 + 7.0f));
+    const float Hx = fabsf(r0.x) + xm * fabsf(r2.x), Hy = fabsf(r0.y) + xm * fabsf(r2.y), Hz = fabsf(r0.z) + xm * fabsf(r2.z);
+    const float Vx = fabsf(r1.x) + ym * fabsf(r2.x), Vy = fabsf(r1.y) + ym * fabsf(r2.y), Vz = fabsf(r1.z) + ym * fabsf(r2.z);
+    const float mag = Hy * Vz + Hz * Vy + Hz * Vx + Hx * Vz + Hx * Vy + Hy * Vx;
+    const float e2 = 2.0f * 16.0f * 5.9604645e-8f * mag;      // 2E
+    float zl = lo[2] - e2, zh = hi[2] + e2;
+    float xl = lo[0] - e2, xh = hi[0] + e2, yl = lo[1] - e2, yh = hi[1] + e2;
+    if (!(zl > 0.0f)) {
+        if (!(zh < 0.0f)) return true;                     // q.z may vanish (or is not finite)
+        const float t0 = -zh, t1 = -zl; zl = t0; zh = t1;  // flip q: (u, v) unchanged
+        const float u0 = -xh, u1 = -xl; xl = u0; xh = u1;
+        const float v0 = -yh, v1 = -yl; yl = v0; yh = v1;
+    }
+    // u = q.x / q.z over the box: extremes at the corners of the quotient
+    const float ul = __builtin_fminf(xl / zl, xl / zh), uh = __builtin_fmaxf(xh / zl, xh / zh);
+    const float vl = __builtin_fminf(yl / zl, yl / zh), vh = __builtin_fmaxf(yh / zl, yh / zh);
+    const float nu = __builtin_fminf(__builtin_fmaxf(0.0f, ul), uh), nv = __builtin_fminf(__builtin_fmaxf(0.0f, vl), vh);
+    return !(nu * nu + nv * nv > 2.0f * s * 1.001f);
+}
+
 constexpr int FWD_BATCH = 64;
 
 // Forward, kernels/rasterize.rs:109-420.  One 64-lane wavefront, its own
@@ -239,7 +293,7 @@ constexpr int FWD_BATCH = 64;
 // the tile in dispatch slot i / 4), so the tile's splat rows are shared in
 // one L2, yet no quadrant waits on another: each stages the tile's
 // depth-sorted splats 64 at a time into its LDS, keeps in a compacted list
-// those that may reach the quadrant (quadrant_live; surfels keep all), walks
+// those that may reach the quadrant (quadrant_live, surfel_quadrant_live), walks
 // the list, and leaves as soon as its 64 pixels are done.  The tile's shrunk
 // range end (one past its last blended intersection) is the maximum over its
 // quadrants, kept with an atomic max on an end the dispatch-order pass set
@@ -303,9 +357,10 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
             if constexpr (SURF) {
                 const float4* ps = a.proj_surf + (size_t)gid * 4;
+                float4 r[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) s_s[4 * l + k] = ps[k];
-                live = true;
+                for (int k = 0; k < 4; ++k) { r[k] = ps[k]; s_s[4 * l + k] = r[k]; }
+                live = surfel_quadrant_live(x0, y0, r[0], r[1], r[2], pb.y, SMOOTH);
             } else {
                 live = quadrant_live(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
             }
@@ -667,139 +722,141 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
 }
 
 // Surfel (2DGS) backward, bwd/kernels/rasterize_backwards_planes.rs:266-480:
-// one 64-lane wavefront per tile, lane L owning pixel (L % 8, L / 8) of each
-// 8x8 quadrant.  Each pixel replays the forward with the remaining colour,
-// depth, normal and distortion sums and their cotangents (the geometry
-// channels composite like colours without a background), and a lane adds its
-// pixels' 17 gradient components [M rows, normal, rgb, alpha, refine] per
-// splat; a 17-component reduce-scatter (reduce_scatter17) leaves each
-// component's wave sum in one lane, and those 17 lanes add the sums to
-// v_combined [N,17].
+// a 256-thread workgroup per tile, one 64-lane wavefront per 8x8 quadrant and
+// one pixel per lane.  Each pixel replays the forward with the remaining
+// colour, depth, normal and distortion sums and their cotangents (the
+// geometry channels composite like colours without a background).  Per batch
+// of 64 splats, each wavefront walks the splats that may reach its quadrant
+// (surfel_quadrant_live, the forward's test), reduce-scatters its pixels' 17
+// gradient components [M rows, normal, rgb, alpha, refine] per splat
+// (reduce_scatter17) and adds the 17 wave sums into the batch's LDS
+// accumulator; after the batch the workgroup adds each splat's nonzero sums
+// to v_combined [N,17], one atomic per component and tile.
+constexpr int SURF_BWD_BLOCK = 256;
 template <bool SMOOTH>
-__global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) {
+__global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(RasterBwdArgs a) {
     __shared__ float4 s_s[BWD_BATCH * 4];   // M rows, centre, normal (vs_surfel.h layout)
     __shared__ float4 s_b[BWD_BATCH];       // opacity, r, g, b (raw colours: the gates need the sign)
     __shared__ uint32_t s_gid[BWD_BATCH];
+    __shared__ float s_acc[BWD_BATCH * SURFEL_GRADS];
 
     const uint32_t tile = block_tile(a.order, blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
     if (lo >= hi) return;   // uniform per tile
     const uint32_t tx = tile % a.tile_bw, ty = tile / a.tile_bw;
-    const uint32_t lane = threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63u, q = threadIdx.x >> 6;
     const float img_w = (float)a.img_w, img_h = (float)a.img_h;
+    const uint32_t qx0 = tx * TILE_W + 8u * (q & 1u), qy0 = ty * TILE_W + 8u * (q >> 1);
+    const float x0 = (float)qx0 + 0.5f, y0 = (float)qy0 + 0.5f;   // the quadrant's first pixel centre
 
-    float pcx[BWD_PX], pcy[BWD_PX], T[BWD_PX], rscale[BWD_PX];
-    float sr[BWD_PX], sg[BWD_PX], sb[BWD_PX], sz[BWD_PX], snx[BWD_PX], sny[BWD_PX], snz[BWD_PX], sdb[BWD_PX], sdc[BWD_PX];
-    float vr[BWD_PX], vg[BWD_PX], vb[BWD_PX], vt[BWD_PX], vz[BWD_PX], vmed[BWD_PX], vnx[BWD_PX], vny[BWD_PX], vnz[BWD_PX];
-    float vdb[BWD_PX], vdc[BWD_PX];
-    uint32_t med[BWD_PX];
-#pragma unroll
-    for (int k = 0; k < BWD_PX; ++k) {
-        const uint32_t px = tx * TILE_W + 8 * (k & 1) + (lane & 7);
-        const uint32_t py = ty * TILE_W + 8 * (k >> 1) + (lane >> 3);
-        pcx[k] = (float)px + 0.5f;
-        pcy[k] = (float)py + 0.5f;
-        T[k] = rscale[k] = 0.0f;
-        sr[k] = sg[k] = sb[k] = sz[k] = snx[k] = sny[k] = snz[k] = sdb[k] = sdc[k] = 0.0f;
-        vr[k] = vg[k] = vb[k] = vt[k] = vz[k] = vmed[k] = vnx[k] = vny[k] = vnz[k] = vdb[k] = vdc[k] = 0.0f;
-        med[k] = 0xFFFFFFFFu;
-        if (px < a.img_w && py < a.img_h) {
-            const size_t base = ((size_t)py * a.img_w + px) * a.channels;
-            const float4 o0 = *reinterpret_cast<const float4*>(a.out_img + base);
-            const float4 o1 = *reinterpret_cast<const float4*>(a.out_img + base + 4);
-            const float4 o2 = *reinterpret_cast<const float4*>(a.out_img + base + 8);
-            const float4 v0 = *reinterpret_cast<const float4*>(a.v_out + base);
-            const float4 v1 = *reinterpret_cast<const float4*>(a.v_out + base + 4);
-            const float4 v2 = *reinterpret_cast<const float4*>(a.v_out + base + 8);
-            const float t_final = 1.0f - o0.w;
-            sr[k] = o0.x - t_final * a.bg_r;
-            sg[k] = o0.y - t_final * a.bg_g;
-            sb[k] = o0.z - t_final * a.bg_b;
-            T[k] = 1.0f;
-            vr[k] = v0.x; vg[k] = v0.y; vb[k] = v0.z;
-            vt[k] = (v0.w - (a.bg_r * v0.x + a.bg_g * v0.y + a.bg_b * v0.z)) * t_final;
-            rscale[k] = 1.0f / mx(o0.w, 1.0e-5f);
-            sz[k] = o1.x; snx[k] = o1.z; sny[k] = o1.w; snz[k] = o2.x; sdb[k] = o2.y; sdc[k] = o2.z;
-            med[k] = as_u(o2.w);
-            vz[k] = v1.x; vmed[k] = v1.y; vnx[k] = v1.z; vny[k] = v1.w; vnz[k] = v2.x; vdb[k] = v2.y; vdc[k] = v2.z;
-        }
+    const uint32_t px = qx0 + (lane & 7u), py = qy0 + (lane >> 3);
+    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+    float T = 0.0f, rscale = 0.0f;
+    float sr = 0.0f, sg = 0.0f, sb = 0.0f, sz = 0.0f, snx = 0.0f, sny = 0.0f, snz = 0.0f, sdb = 0.0f, sdc = 0.0f;
+    float vr = 0.0f, vg = 0.0f, vb = 0.0f, vt = 0.0f, vz = 0.0f, vmed = 0.0f, vnx = 0.0f, vny = 0.0f, vnz = 0.0f;
+    float vdb = 0.0f, vdc = 0.0f;
+    uint32_t med = 0xFFFFFFFFu;
+    if (px < a.img_w && py < a.img_h) {
+        const size_t base = ((size_t)py * a.img_w + px) * a.channels;
+        const float4 o0 = *reinterpret_cast<const float4*>(a.out_img + base);
+        const float4 o1 = *reinterpret_cast<const float4*>(a.out_img + base + 4);
+        const float4 o2 = *reinterpret_cast<const float4*>(a.out_img + base + 8);
+        const float4 v0 = *reinterpret_cast<const float4*>(a.v_out + base);
+        const float4 v1 = *reinterpret_cast<const float4*>(a.v_out + base + 4);
+        const float4 v2 = *reinterpret_cast<const float4*>(a.v_out + base + 8);
+        const float t_final = 1.0f - o0.w;
+        sr = o0.x - t_final * a.bg_r;
+        sg = o0.y - t_final * a.bg_g;
+        sb = o0.z - t_final * a.bg_b;
+        T = 1.0f;
+        vr = v0.x; vg = v0.y; vb = v0.z;
+        vt = (v0.w - (a.bg_r * v0.x + a.bg_g * v0.y + a.bg_b * v0.z)) * t_final;
+        rscale = 1.0f / mx(o0.w, 1.0e-5f);
+        sz = o1.x; snx = o1.z; sny = o1.w; snz = o2.x; sdb = o2.y; sdc = o2.z;
+        med = as_u(o2.w);
+        vz = v1.x; vmed = v1.y; vnx = v1.z; vny = v1.w; vnz = v2.x; vdb = v2.y; vdc = v2.z;
     }
-    const float cut_lo = ALPHA_MID - 0.5f * ALPHA_BAND;
     const int comp = (lane & 1u) ? -1 : scatter_component17(lane);   // the gradient component this lane adds
+    for (uint32_t i = threadIdx.x; i < BWD_BATCH * SURFEL_GRADS; i += SURF_BWD_BLOCK) s_acc[i] = 0.0f;
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
-        bool any_alive = false;
-#pragma unroll
-        for (int k = 0; k < BWD_PX; ++k) any_alive = any_alive || T[k] > T_STOP;
-        if (__ballot(any_alive) == 0ull) break;              // every pixel of the tile is done
+        // every pixel of the tile is done: the whole workgroup leaves together
+        if (!__syncthreads_or(T > T_STOP ? 1 : 0)) break;
         const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
-        __syncthreads();
+        // wavefront q stages row q of each splat's surfel record; wavefront 0 the rest
         if (lane < rem) {
             const uint32_t gid = a.gids[start + lane];
             if (gid < a.num_splats) {
-                const float4* ps = a.proj_surf + (size_t)gid * 4;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) s_s[4 * lane + k] = ps[k];
-                const float4 pb = a.proj_b[gid];
-                s_b[lane] = make_float4(pb.y, pb.z, pb.w, a.proj_c[gid]);
-                s_gid[lane] = gid;
+                float4 row = a.proj_surf[(size_t)gid * 4 + q];
+                if (q == 3) row.w = 1.0f / a.proj_surf[(size_t)gid * 4 + 2].x;   // 1 / M[2][2] in the pad slot
+                s_s[4 * lane + q] = row;
+                if (q == 0) {
+                    const float4 pb = a.proj_b[gid];
+                    s_b[lane] = make_float4(pb.y, pb.z, pb.w, a.proj_c[gid]);
+                    s_gid[lane] = gid;
+                }
             } else {   // a corrupt id: zero opacity never reaches the cutoff
-#pragma unroll
-                for (int k = 0; k < 4; ++k) s_s[4 * lane + k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                s_b[lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                s_gid[lane] = 0u;
+                s_s[4 * lane + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (q == 0) { s_b[lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f); s_gid[lane] = 0u; }
             }
         }
         __syncthreads();
-        for (uint32_t t = 0; t < rem; ++t) {
+        // the batch's splats that may reach this quadrant, in depth order
+        const bool live_t = lane < rem && surfel_quadrant_live(x0, y0, s_s[4 * lane], s_s[4 * lane + 1],
+                                                                s_s[4 * lane + 2], s_b[lane].x, SMOOTH);
+        uint64_t live = __ballot(live_t);
+        if (__ballot(T > T_STOP) == 0ull) live = 0ull;       // this quadrant is done
+        while (live) {
+            const uint32_t t = (uint32_t)__builtin_ctzll(live);
+            live &= live - 1ull;
             const float4 m0 = s_s[4 * t], m1 = s_s[4 * t + 1], m2 = s_s[4 * t + 2], m3 = s_s[4 * t + 3];
             const float4 cb = s_b[t];
             const float opac = cb.x, col_r = cb.y, col_g = cb.z, col_b = cb.w;
             const float cl_r = mx(col_r, 0.0f), cl_g = mx(col_g, 0.0f), cl_b = mx(col_b, 0.0f);
             const float r2x = m1.z, r2y = m1.w, r2z = m2.x, cen_x = m2.y, cen_y = m2.z;
             const float nrm_x = m2.w, nrm_y = m3.x, nrm_z = m3.y;
-            const float inv_r2z = 1.0f / r2z;
-            const float sigma_max = logf_c(opac / cut_lo) + 1.0e-3f;   // alpha below the cutoff band beyond it
+            const float inv_r2z = m3.w;
+            // the projection's logf(opac / (1/255 - 5e-4)) + 1e-3: alpha is below the cutoff band beyond it
+            const float sigma_max = m3.z;
             const uint32_t isect = start + t;
             float gs[SURFEL_GRADS];
 #pragma unroll
             for (int i = 0; i < SURFEL_GRADS; ++i) gs[i] = 0.0f;
             bool contrib = false;
-#pragma unroll
-            for (int k = 0; k < BWD_PX; ++k) {
-                if (!(T[k] > T_STOP)) continue;
-                const SurfelHit h = surfel_hit(m0, m1, m2, m3.z, pcx[k], pcy[k]);
-                if (!(h.valid && h.sigma <= sigma_max)) continue;
+            do {
+                if (!(T > T_STOP)) break;
+                const SurfelHit h = surfel_hit(m0, m1, m2, m3.z, pcx, pcy);
+                if (!(h.valid && h.sigma <= sigma_max)) break;
                 const float G = exp2n(-(h.sigma * LOG2E_F));
                 const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
-                if (!(h.sigma >= 0.0f && w_cut > 0.0f)) continue;
+                if (!(h.sigma >= 0.0f && w_cut > 0.0f)) break;
                 const float ae = alpha * w_cut;
-                const float nt = T[k] * (1.0f - ae);
-                if (nt <= T_STOP) { T[k] = 0.0f; continue; }
+                const float nt = T * (1.0f - ae);
+                if (nt <= T_STOP) { T = 0.0f; break; }
                 contrib = true;
                 const float z = h.z;
                 const float m = dist_depth(z);
                 // gradient-only quotients and roots take the hardware reciprocal and
                 // square root (1 ulp); the replayed forward above keeps IEEE division
                 const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
-                const float Tk = T[k];
+                const float Tk = T;
                 const float vis = ae * Tk;
-                gs[12] += (col_r >= 0.0f) ? vis * vr[k] : 0.0f;
-                gs[13] += (col_g >= 0.0f) ? vis * vg[k] : 0.0f;
-                gs[14] += (col_b >= 0.0f) ? vis * vb[k] : 0.0f;
-                gs[9] += vis * vnx[k];
-                gs[10] += vis * vny[k];
-                gs[11] += vis * vnz[k];
-                const float ra = 1.0f / (1.0f - ae);
-                const float dot_ = ((Tk * cl_r - sr[k]) * vr[k] + (Tk * cl_g - sg[k]) * vg[k] + (Tk * cl_b - sb[k]) * vb[k] +
-                                    (Tk * z - sz[k]) * vz[k] + (Tk * nrm_x - snx[k]) * vnx[k] +
-                                    (Tk * nrm_y - sny[k]) * vny[k] + (Tk * nrm_z - snz[k]) * vnz[k] +
-                                    (Tk * m - sdb[k]) * vdb[k] + (Tk * m * m - sdc[k]) * vdc[k]) * ra;
-                const float v_ae = dot_ + vt[k] * ra;
+                gs[12] += (col_r >= 0.0f) ? vis * vr : 0.0f;
+                gs[13] += (col_g >= 0.0f) ? vis * vg : 0.0f;
+                gs[14] += (col_b >= 0.0f) ? vis * vb : 0.0f;
+                gs[9] += vis * vnx;
+                gs[10] += vis * vny;
+                gs[11] += vis * vnz;
+                const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+                const float dot_ = ((Tk * cl_r - sr) * vr + (Tk * cl_g - sg) * vg + (Tk * cl_b - sb) * vb +
+                                    (Tk * z - sz) * vz + (Tk * nrm_x - snx) * vnx +
+                                    (Tk * nrm_y - sny) * vny + (Tk * nrm_z - snz) * vnz +
+                                    (Tk * m - sdb) * vdb + (Tk * m * m - sdc) * vdc) * ra;
+                const float v_ae = dot_ + vt * ra;
                 const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
-                const float v_z = vis * (vz[k] + (vdb[k] + 2.0f * m * vdc[k]) * dm_dz) + ((isect == med[k]) ? vmed[k] : 0.0f);
+                const float v_z = vis * (vz + (vdb + 2.0f * m * vdc) * dm_dz) + ((isect == med) ? vmed : 0.0f);
                 const bool unsat = opac * G <= ALPHA_CAP;
                 const float v_sigma = unsat ? -alpha * v_alpha : 0.0f;
                 if (unsat) gs[15] += v_alpha * G;
@@ -816,23 +873,30 @@ __global__ void __launch_bounds__(64) raster_bwd_surfel_kernel(RasterBwdArgs a) 
                 const float g0 = vhux, g1 = vhuy, g2 = vhuz + v_cx * inv_r2z;
                 const float g3 = vhvx, g4 = vhvy, g5 = vhvz + v_cy * inv_r2z;
                 gs[0] += g0; gs[1] += g1; gs[2] += g2; gs[3] += g3; gs[4] += g4; gs[5] += g5;
-                gs[6] += v_z * h.su - pcx[k] * vhux - pcy[k] * vhvx;
-                gs[7] += v_z * h.sv - pcx[k] * vhuy - pcy[k] * vhvy;
-                gs[8] += v_z - pcx[k] * vhuz - pcy[k] * vhvz - (v_cx * cen_x + v_cy * cen_y) * inv_r2z;
+                gs[6] += v_z * h.su - pcx * vhux - pcy * vhvx;
+                gs[7] += v_z * h.sv - pcx * vhuy - pcy * vhvy;
+                gs[8] += v_z - pcx * vhuz - pcy * vhvz - (v_cx * cen_x + v_cy * cen_y) * inv_r2z;
                 // refine weight: this pixel's gradient of a screen-space shift of the surfel (M -> T M)
                 const float shx = g0 * r2x + g1 * r2y + g2 * r2z;
                 const float shy = g3 * r2x + g4 * r2y + g5 * r2z;
                 const float ux = shx * img_w, uy = shy * img_h;
-                gs[16] += __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale[k];
-                sr[k] -= vis * cl_r; sg[k] -= vis * cl_g; sb[k] -= vis * cl_b;
-                sz[k] -= vis * z; snx[k] -= vis * nrm_x; sny[k] -= vis * nrm_y; snz[k] -= vis * nrm_z;
-                sdb[k] -= vis * m; sdc[k] -= vis * m * m;
-                T[k] = nt;
-            }
+                gs[16] += __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale;
+                sr -= vis * cl_r; sg -= vis * cl_g; sb -= vis * cl_b;
+                sz -= vis * z; snx -= vis * nrm_x; sny -= vis * nrm_y; snz -= vis * nrm_z;
+                sdb -= vis * m; sdc -= vis * m * m;
+                T = nt;
+            } while (false);
             if (__ballot(contrib) == 0ull) continue;          // uniform: gs is zero in every lane
             const float mine = reduce_scatter17(gs, lane);
-            if (comp >= 0 && mine != 0.0f)
-                atomicAdd(&a.v_combined[(size_t)s_gid[t] * SURFEL_GRADS + comp], mine);
+            if (comp >= 0 && mine != 0.0f) atomicAdd(&s_acc[t * SURFEL_GRADS + comp], mine);
+        }
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < rem * SURFEL_GRADS; i += SURF_BWD_BLOCK) {
+            const float v = s_acc[i];
+            if (v != 0.0f) {
+                atomicAdd(&a.v_combined[(size_t)s_gid[i / SURFEL_GRADS] * SURFEL_GRADS + i % SURFEL_GRADS], v);
+                s_acc[i] = 0.0f;
+            }
         }
     }
 }
@@ -899,10 +963,15 @@ hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s,
     if (a.num_tiles == 0) return hipSuccess;
     const dim3 grid(xcd_grid(a.num_tiles));
     void (*k)(RasterBwdArgs);
-    if (a.proj_surf) k = smooth ? raster_bwd_surfel_kernel<true> : raster_bwd_surfel_kernel<false>;
-    else k = smooth ? raster_bwd_kernel<true> : raster_bwd_kernel<false>;
-    if (start) hipExtLaunchKernelGGL(k, grid, dim3(64), 0, s, start, stop, 0u, a);
-    else k<<<grid, 64, 0, s>>>(a);
+    uint32_t block = 64;
+    if (a.proj_surf) {
+        k = smooth ? raster_bwd_surfel_kernel<true> : raster_bwd_surfel_kernel<false>;
+        block = SURF_BWD_BLOCK;
+    } else {
+        k = smooth ? raster_bwd_kernel<true> : raster_bwd_kernel<false>;
+    }
+    if (start) hipExtLaunchKernelGGL(k, grid, dim3(block), 0, s, start, stop, 0u, a);
+    else k<<<grid, block, 0, s>>>(a);
     return hipGetLastError();
 }
 
