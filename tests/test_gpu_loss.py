@@ -113,3 +113,9 @@ def test_l1_cotangent_matches_closed_form(cfg):
     if mask is not None:
         assert 0 < mask.mean() < 1 and (got[mask == 0].view(np.uint32) == 0).all()
         assert (got[mask == 1][:, :3] != 0).mean() > 0.9
+    # the 12-channel geometry render (surfel training): rgb as above, the other 9 channels 0
+    pred12 = np.concatenate([pred, rng.uniform(0, 1, (H, W, 8)).astype(np.float32)], axis=-1)
+    got12 = va.l1_cotangent(torch.from_numpy(pred12).cuda(), g, w.mask_center, w.mask_radius).cpu().numpy()
+    want12 = np.zeros_like(pred12)
+    want12[..., :4] = want
+    np.testing.assert_array_equal(got12.view(np.uint32), want12.view(np.uint32))

@@ -111,8 +111,11 @@ struct vs_fwd_state {
     uint32_t* ranges_shrunk = nullptr;
     uint32_t* tile_order = nullptr;   // [8 ceil(T/8)] raster dispatch order
     float* v_combined = nullptr;
-    uint32_t* tiles = nullptr;    // [I] sorted tile ids
+    uint32_t* tiles = nullptr;    // [I] sorted tile ids (written on demand, see tiles_pending)
     uint32_t* gids = nullptr;     // [I] sorted global ids
+    // the tile sort produced the ranges and skipped the sorted ids: the state
+    // view rebuilds them from the ranges
+    mutable bool tiles_pending = false;
 };
 
 namespace {
@@ -639,7 +642,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         VS_HIP(launch_project(pa, s), "project kernel");
         VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, isect_cap, s), "projection counts");
         if (bwd_info) VS_HIP(launch_fill_f32(st->visible, 0.0f, N, s), "zero visible");
-        VS_HIP(launch_fill_u32(st->ranges, 0u, (uint64_t)T * 2, s), "zero ranges");
+        VS_HIP(launch_ranges_init(st->ranges, T, s), "range init");
     }
     const uint32_t tile_bits = bit_length(T);     // the sentinel tile id T must fit too
     uint32_t depth_bits = 32;
@@ -726,11 +729,13 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
             ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u; ea.capacity = I;
             VS_HIP(launch_emit(ea, s), "emit kernel");
         }
+        TileRangesOut tro{st->ranges, T, false};   // the tile sort's last pass finds the ranges
         {
             StageTimer tm(ctx, ST_SORT);
             VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, i_dev, false, 0, tile_bits, ib + o_tmp,
-                                    err, s, ctx->spin_limit),
+                                    err, s, ctx->spin_limit, &tro),
                    "tile sort");
+            st->tiles_pending = tro.done;
         }
         if (!lagged) {
             // An exact render reports a sort that gave up before it returns: the
@@ -741,7 +746,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
             sort_done = ctx->take();
             VS_HIP(hipEventRecord(sort_done, s), "hipEventRecord(sorts)");
         }
-        {
+        if (!tro.done) {
             StageTimer tm(ctx, ST_RANGES);
             VS_HIP(launch_tile_ranges(st->tiles, I, T, st->ranges, s, i_dev), "tile ranges");
         }
@@ -753,7 +758,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         RasterArgs ra{};
         ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T; ra.num_splats = N;
         // longest lists first within each XCD's band (the forward's cost grows with its list)
-        VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s, bwd_info ? st->ranges_shrunk : nullptr),
+        VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s, bwd_info ? st->ranges_shrunk : nullptr, true),
                "tile order");
         ra.order = st->tile_order;
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
@@ -1050,6 +1055,13 @@ extern "C" vs_status vs_geo_zero_rows(vs_ctx* ctx, uint32_t* words, uint64_t num
 
 extern "C" vs_status vs_fwd_state_view(const vs_fwd_state* st, vs_state_view* o) {
     if (!st || !o) return fail(VS_ERR_INVALID, "null argument");
+    if (st->tiles_pending && st->I > 0) {
+        vs_ctx* ctx = st->ctx;
+        VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+        VS_HIP(launch_tiles_from_ranges(st->ranges, st->T, st->I, st->tiles, ctx->stream), "tile ids from ranges");
+        VS_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        st->tiles_pending = false;
+    }
     o->num_splats = st->N; o->num_visible = st->V; o->num_intersections = st->I; o->num_tiles = st->T;
     o->tile_bw = st->tbw; o->tile_bh = st->tbh;
     o->isect_tiles = st->tiles; o->isect_gids = st->gids; o->intersect_counts = st->counts;

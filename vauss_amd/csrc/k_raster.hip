@@ -98,16 +98,15 @@ constexpr int ORDER_BLOCK = 1024;
 constexpr int ORDER_BINS = 2048;
 static_assert(ORDER_BINS == 2 * ORDER_BLOCK, "each thread of the order scan owns two bins");
 
-VS_DEV uint32_t order_bin(const uint32_t* __restrict__ ranges, uint32_t t) {
-    const uint32_t lo = ranges[2 * t], hi = ranges[2 * t + 1];
+VS_DEV uint32_t order_bin(uint32_t lo, uint32_t hi) {
     const float len = (float)(hi > lo ? hi - lo : 0u);
     const uint32_t key = min((uint32_t)(__builtin_sqrtf(len) * 8.0f), (uint32_t)ORDER_BINS - 1u);
     return (uint32_t)ORDER_BINS - 1u - key;   // ascending bin = descending length
 }
 
-__global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(const uint32_t* __restrict__ ranges, uint32_t num_tiles,
+__global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(uint32_t* ranges, uint32_t num_tiles,
                                                                  uint32_t* __restrict__ order,
-                                                                 uint32_t* __restrict__ shrunk_init) {
+                                                                 uint32_t* __restrict__ shrunk_init, int fix_empty) {
     __shared__ uint32_t s_bin[ORDER_BINS];
     __shared__ uint32_t s_wave[ORDER_BLOCK / 64];
     const uint32_t per = (num_tiles + 7) / 8;
@@ -117,9 +116,14 @@ __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(const uint32_t*
     for (uint32_t i = tid; i < ORDER_BINS; i += ORDER_BLOCK) s_bin[i] = 0u;
     __syncthreads();
     for (uint32_t t = t0 + tid; t < t1; t += ORDER_BLOCK) {
-        atomicAdd(&s_bin[order_bin(ranges, t)], 1u);
+        uint32_t lo = ranges[2 * t];
+        const uint32_t hi = ranges[2 * t + 1];
+        if (fix_empty && lo == 0xFFFFFFFFu) {   // a tile the sort's range pass never saw: empty, (0, 0)
+            lo = 0u;
+            ranges[2 * t] = 0u;
+        }
+        atomicAdd(&s_bin[order_bin(lo, hi)], 1u);
         if (shrunk_init) {   // the forward's shrunk ranges start empty at the range start
-            const uint32_t lo = ranges[2 * t];
             shrunk_init[2 * t] = lo;
             shrunk_init[2 * t + 1] = lo;
         }
@@ -143,7 +147,7 @@ __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(const uint32_t*
     s_bin[2 * tid + 1] = excl + c0;
     __syncthreads();
     for (uint32_t t = t0 + tid; t < t1; t += ORDER_BLOCK) {
-        const uint32_t pos = atomicAdd(&s_bin[order_bin(ranges, t)], 1u);
+        const uint32_t pos = atomicAdd(&s_bin[order_bin(ranges[2 * t], ranges[2 * t + 1])], 1u);
         order[(size_t)pos * 8 + band] = t;
     }
     for (uint32_t i = (t1 > t0 ? t1 - t0 : 0u) + tid; i < per; i += ORDER_BLOCK) order[(size_t)i * 8 + band] = 0xFFFFFFFFu;
@@ -902,11 +906,12 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
 }
 
 // sign(pred - gt) * inv_count on rgb, 0 on the other channels and outside
-// the mask.  The 4-channel image (the training render's) is read and written
-// as one float4 per pixel.
+// the mask.  Images whose channel count is a multiple of 4 (RGBA, the
+// 12-channel geometry render) are read and written as float4s: the first
+// holds rgb, the rest are zero.
 VS_DEV float l1_sign(float p, float g, float inv) { const float d = p - g; return (d > 0.0f) ? inv : ((d < 0.0f) ? -inv : 0.0f); }
 
-template <bool RGBA>
+template <bool VEC4>
 __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, const float* __restrict__ gt, uint32_t w,
                                     uint32_t h, float mcx, float mcy, float mr, float inv_count, float* __restrict__ v) {
     const uint32_t pid = blockIdx.x * blockDim.x + threadIdx.x;
@@ -919,16 +924,46 @@ __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, 
     }
     const float inv = in_mask ? inv_count : 0.0f;
     const float g0 = gt[(size_t)pid * 3], g1 = gt[(size_t)pid * 3 + 1], g2 = gt[(size_t)pid * 3 + 2];
-    if constexpr (RGBA) {
-        const float4 p = reinterpret_cast<const float4*>(pred)[pid];
-        reinterpret_cast<float4*>(v)[pid] =
-            in_mask ? make_float4(l1_sign(p.x, g0, inv), l1_sign(p.y, g1, inv), l1_sign(p.z, g2, inv), 0.0f)
-                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (VEC4) {
+        const uint32_t q4 = C / 4;
+        const float4 p = reinterpret_cast<const float4*>(pred)[(size_t)pid * q4];
+        float4* o = reinterpret_cast<float4*>(v) + (size_t)pid * q4;
+        o[0] = in_mask ? make_float4(l1_sign(p.x, g0, inv), l1_sign(p.y, g1, inv), l1_sign(p.z, g2, inv), 0.0f)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t k = 1; k < q4; ++k) o[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     } else {
         const float gg[3] = {g0, g1, g2};
         for (uint32_t c = 0; c < C; ++c)
             v[(size_t)pid * C + c] = (c < 3 && in_mask) ? l1_sign(pred[(size_t)pid * C + c], gg[c], inv) : 0.0f;
     }
+}
+
+// Every tile's range starts as (0xFFFFFFFF, 0): the sort's range pass
+// lowers starts and raises ends.
+__global__ void ranges_init_kernel(uint32_t* __restrict__ ranges, uint32_t num_tiles) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < num_tiles) reinterpret_cast<uint2*>(ranges)[t] = make_uint2(0xFFFFFFFFu, 0u);
+}
+hipError_t launch_ranges_init(uint32_t* ranges, uint32_t num_tiles, hipStream_t s) {
+    if (num_tiles == 0) return hipSuccess;
+    ranges_init_kernel<<<(num_tiles + 255) / 256, 256, 0, s>>>(ranges, num_tiles);
+    return hipGetLastError();
+}
+
+// The sorted tile ids, rebuilt from the ranges (one workgroup per tile; the
+// caller fills the list with the sentinel first).
+__global__ void tiles_from_ranges_kernel(const uint32_t* __restrict__ ranges, uint32_t n, uint32_t* __restrict__ tiles) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t lo = ranges[2 * t], hi = min(ranges[2 * t + 1], n);
+    for (uint32_t i = lo + threadIdx.x; i < hi; i += blockDim.x) tiles[i] = t;
+}
+hipError_t launch_tiles_from_ranges(const uint32_t* ranges, uint32_t num_tiles, uint32_t n, uint32_t* tiles,
+                                    hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipError_t e = launch_fill_u32(tiles, num_tiles, n, s);
+    if (e != hipSuccess || num_tiles == 0) return e;
+    tiles_from_ranges_kernel<<<num_tiles, 256, 0, s>>>(ranges, n, tiles);
+    return hipGetLastError();
 }
 
 hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_tiles, uint32_t* ranges, hipStream_t s,
@@ -938,10 +973,10 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
     return hipGetLastError();
 }
 
-hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
-                             uint32_t* shrunk_init) {
+hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
+                             uint32_t* shrunk_init, bool fix_empty) {
     if (num_tiles == 0) return hipSuccess;
-    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init);
+    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init, fix_empty ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -979,8 +1014,8 @@ hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float
                                float mcy, float mr, float inv_count, float* v_out, hipStream_t s) {
     const uint32_t n = w * h;
     if (n == 0) return hipSuccess;
-    const bool rgba = channels == 4 && ((uintptr_t)pred & 15u) == 0 && ((uintptr_t)v_out & 15u) == 0;
-    if (rgba) l1_cotangent_kernel<true><<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    const bool vec4 = channels >= 4 && channels % 4 == 0 && ((uintptr_t)pred & 15u) == 0 && ((uintptr_t)v_out & 15u) == 0;
+    if (vec4) l1_cotangent_kernel<true><<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
     else l1_cotangent_kernel<false><<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
     return hipGetLastError();
 }

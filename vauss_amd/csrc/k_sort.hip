@@ -305,7 +305,8 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
                                                                    K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
                                                                    uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
                                                                    const uint32_t* __restrict__ ghist, uint32_t* status,
-                                                                   uint32_t* err, uint32_t spin_limit) {
+                                                                   uint32_t* err, uint32_t spin_limit,
+                                                                   uint32_t* __restrict__ ranges, uint32_t num_tiles) {
     constexpr uint32_t TILE = BLOCK * ITEMS;
     __shared__ uint32_t wave_hist[BLOCK / 64][256];
     __shared__ uint32_t digit_start[256];
@@ -390,8 +391,18 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
         const uint32_t dd = digit_of(k, shift);
         const uint32_t gpos = s_gstart[dd] + (i - digit_start[dd]);
         if (gpos < n) {   // always true for consistent counts; keeps a bad count from writing out of bounds
-            keys_out[gpos] = k;
+            if (!ranges) keys_out[gpos] = k;
             vals_out[gpos] = s_vals[i];
+            if (ranges && (uint64_t)k < num_tiles) {
+                // The last pass: within a digit's run of this tile the keys are
+                // sorted (earlier passes sorted the lower bits), so a key change
+                // inside the run is a range bound; a run's first and last keys
+                // may continue in another tile's run and meet there by min / max.
+                const uint32_t t = (uint32_t)k;
+                const uint32_t run_lo = digit_start[dd], run_hi = dd < 255 ? digit_start[dd + 1] : count;
+                if (i == run_lo || s_keys[i - 1] != k) atomicMin(&ranges[2 * t], gpos);
+                if (i + 1 == run_hi || s_keys[i + 1] != k) atomicMax(&ranges[2 * t + 1], gpos + 1);
+            }
         }
     }
 }
@@ -416,7 +427,7 @@ size_t sort_tmp_bytes(uint64_t n, bool key64) {
 template <typename K>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_out, uint32_t* vals_out, uint32_t n,
                             const uint32_t* n_dev, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t* err,
-                            hipStream_t s, uint32_t spin_limit) {
+                            hipStream_t s, uint32_t spin_limit, TileRangesOut* tr) {
     if (n == 0) return hipSuccess;
     const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
     const uint32_t passes = (bits + 7) / 8;
@@ -455,14 +466,20 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         K* dk = to_out ? keys_out : tk;
         uint32_t* dv = to_out ? vals_out : tv;
         const uint32_t shift = first_bit + 8 * pass;
+        // the last pass of a tile sort derives the tile ranges instead of writing the keys
+        uint32_t* rng = (tr && pass + 1 == passes) ? tr->ranges : nullptr;
+        const uint32_t nt = tr ? tr->num_tiles : 0u;
         hipError_t e;
         if (onesweep) {
             if (small)
                 sort_onesweep_kernel<K, OS_SMALL_BLOCK, OS_SMALL_ITEMS><<<os_tiles, OS_SMALL_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err, spin_limit);
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err,
+                    spin_limit, rng, nt);
             else
                 sort_onesweep_kernel<K, OS_BLOCK, OS_ITEMS><<<os_tiles, OS_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err, spin_limit);
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err,
+                    spin_limit, rng, nt);
+            if (rng) tr->done = true;
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         } else {
@@ -483,12 +500,13 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
 
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
-                            void* tmp, uint32_t* err, hipStream_t s, uint32_t spin_limit) {
+                            void* tmp, uint32_t* err, hipStream_t s, uint32_t spin_limit, TileRangesOut* tr) {
+    if (tr) tr->done = false;
     if (key64)
         return sort_impl<uint64_t>(static_cast<const uint64_t*>(keys_in), vals_in, static_cast<uint64_t*>(keys_out),
-                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit);
+                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, nullptr);
     return sort_impl<uint32_t>(static_cast<const uint32_t*>(keys_in), vals_in, static_cast<uint32_t*>(keys_out),
-                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit);
+                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, tr);
 }
 
 } // namespace vs

@@ -260,8 +260,12 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 // longest list first within each (order holds 8 ceil(T/8) entries).  With
 // `shrunk_init`, every tile's entry there is set to (start, start): the
 // forward's shrunk ranges, whose ends it raises.
-hipError_t launch_tile_order(const uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
-                             uint32_t* shrunk_init = nullptr);
+// `fix_empty`: ranges left at (0xFFFFFFFF, 0) by the sort become (0, 0).
+hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
+                             uint32_t* shrunk_init = nullptr, bool fix_empty = false);
+hipError_t launch_ranges_init(uint32_t* ranges, uint32_t num_tiles, hipStream_t s);
+hipError_t launch_tiles_from_ranges(const uint32_t* ranges, uint32_t num_tiles, uint32_t n, uint32_t* tiles,
+                                    hipStream_t s);
 hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, bool smooth, hipStream_t s);
 // With `start` and `stop` set, the kernel is launched by hipExtLaunchKernelGGL,
 // which records the two events around the kernel's own execution.
@@ -311,9 +315,19 @@ size_t sort_tmp_bytes(uint64_t n, bool key64);
 // is or-ed with 1 if a one-sweep look-back gave up waiting: after
 // `spin_limit` polls of a predecessor that has not published its counts.
 constexpr uint32_t SORT_SPIN_LIMIT_DEFAULT = 1u << 18;
+// A u32 sort of tile ids may produce the tiles' [start, end) ranges itself:
+// `ranges` [num_tiles, 2] must hold (0xFFFFFFFF, 0) beforehand (tiles left so
+// are empty; launch_tile_order turns them into (0, 0)).  When the sort does
+// so (its last pass is a one-sweep pass) it sets `done` and does not write
+// the sorted keys; otherwise the caller finds the ranges (launch_tile_ranges).
+struct TileRangesOut {
+    uint32_t* ranges;
+    uint32_t num_tiles;
+    bool done;
+};
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
                             void* tmp, uint32_t* err, hipStream_t s,
-                            uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT);
+                            uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT, TileRangesOut* tr = nullptr);
 
 } // namespace vs
