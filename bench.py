@@ -279,17 +279,25 @@ def main() -> int:
 
     # Stage breakdown: one pass over the views with every stage bracketed by
     # HIP events (each bracket adds a few microseconds of stream time, so this
-    # pass is not the timed one), on exact counts so each view's counts are its own.
-    ctx.set_lagged_counts(False)
-    ctx.enable_timing(True)
-    ctx.stage_times()                # drop anything recorded before
-    counts = []
+    # pass is not the timed one), on exact counts so each view's counts are its
+    # own.  It runs once before the timed region (to pick the dominant stage)
+    # and once after it, when clocks and caches are at their steady state as
+    # in the timed steps: the second pass gives the per-launch times.
     nb = len(cams)
-    for i in range(nb):
-        _, aux = step(i % len(cams), list_histogram=(i == 0), used=True)
-        counts.append(aux)
-    stages = ctx.stage_times()
-    per_launch = {name: ms / nb for name, ms in stages.items()}
+
+    def stage_pass(first: bool):
+        ctx.set_lagged_counts(False)
+        ctx.enable_timing(True)
+        ctx.stage_times()                # drop anything recorded before
+        counts = []
+        for i in range(nb):
+            _, aux = step(i % len(cams), list_histogram=first and i == 0, used=True)
+            counts.append(aux)
+        stages = ctx.stage_times()
+        ctx.enable_timing(False)
+        return counts, {name: ms / nb for name, ms in stages.items()}
+
+    counts, per_launch = stage_pass(True)
     dom = max(("raster_bwd_ms", "raster_fwd_ms", "project_ms", "project_bwd_ms", "sort_ms"), key=lambda x: per_launch[x])
 
     # Timed region: K steps; only the dominant kernel's stage is bracketed by
@@ -318,6 +326,7 @@ def main() -> int:
 
     ms_per_step, dom_ms = timed_steps(lagged)
     other_ms = timed_steps(not lagged)[0]
+    counts, per_launch = stage_pass(False)
     print(f"[bench] {args.steps} steps, {ms_per_step:.3f} ms/view ({'lagged' if lagged else 'exact'} counts; "
           f"{other_ms:.3f} with {'exact' if lagged else 'lagged'} counts)", file=sys.stderr, flush=True)
 

@@ -283,7 +283,10 @@ void vs_fwd_state_free(vs_fwd_state* state);
 
 /* Read-only view of the forward's intermediate buffers (device pointers owned
  * by the state), for parity checks of each stage against the reference
- * semantics.  Projected rows are indexed by global splat id. */
+ * semantics.  Projected rows are indexed by global splat id.  The render does
+ * not keep the sorted tile ids (its tile sort derives the ranges instead):
+ * the first view of a state rebuilds them from the ranges on the context's
+ * stream and waits for that. */
 typedef struct vs_state_view {
     uint32_t num_splats, num_visible, num_intersections, num_tiles, tile_bw, tile_bh;
     const uint32_t* isect_tiles;    /* [I] sorted tile ids (T = sentinel, sorts last) */
