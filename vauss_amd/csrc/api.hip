@@ -594,6 +594,18 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     size_t hint = 0;
     const bool lagged = ctx->lagged && training && N > 0 && ctx->caps.hint(key, N, limit, hint);
     const uint32_t isect_cap = lagged ? (uint32_t)std::min(hint, isect_ceiling(hint, limit)) : 0xFFFFFFFFu;
+    // A lagged render's counts and flags go straight to the key's pinned slot
+    // (the projection's counter kernel and the forward's tile-order kernel
+    // write them there), read by the next training render at this key.
+    vs_ctx::Pending* lag_slot = nullptr;
+    if (lagged) {
+        lag_slot = &ctx->pending[key];
+        if (!lag_slot->host) {
+            VS_HIP(hipHostMalloc(reinterpret_cast<void**>(&lag_slot->host), (CNT_COUNT + CTX_FLAGS) * sizeof(uint32_t),
+                                 hipHostMallocDefault), "hipHostMalloc(lagged counts)");
+            VS_HIP(hipEventCreateWithFlags(&lag_slot->ev, hipEventDisableTiming), "hipEventCreate(lagged counts)");
+        }
+    }
 
     // ---- per-splat arena -----------------------------------------------------
     size_t off = 0;
@@ -639,10 +651,12 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
         pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
         pa.proj_aux = st->proj_aux; pa.proj_surf = st->proj_surf; pa.compact = st->compact; pa.block_stats = st->block_stats;
+        pa.visible = bwd_info ? st->visible : nullptr;   // cleared by the projection
+        pa.ranges = st->ranges; pa.num_tiles = T;         // initialised by the projection
         VS_HIP(launch_project(pa, s), "project kernel");
-        VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, isect_cap, s), "projection counts");
-        if (bwd_info) VS_HIP(launch_fill_f32(st->visible, 0.0f, N, s), "zero visible");
-        VS_HIP(launch_ranges_init(st->ranges, T, s), "range init");
+        VS_HIP(launch_finalize_counts(st->block_stats, nblocks, st->counters, isect_cap, s,
+                                      lag_slot ? lag_slot->host : nullptr), "projection counts");
+        if (N == 0) VS_HIP(launch_ranges_init(st->ranges, T, s), "range init");
     }
     const uint32_t tile_bits = bit_length(T);     // the sentinel tile id T must fit too
     uint32_t depth_bits = 32;
@@ -704,18 +718,24 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         uint32_t* slot_base_g = reinterpret_cast<uint32_t*>(ib + o_base_g);   // [N], written for emitters only
         uint32_t* scan_tmp = reinterpret_cast<uint32_t*>(ib + o_scan);
         uint32_t* err = ctx->dev_flags + FLAG_SORT_STALL;
+        // the sorts' one-sweep state (shared scratch) is cleared by the kernel
+        // before each sort: compaction for the depth sort, emission for the tile sort
+        const SortZeroSpan depth_zero = sort_zero_span(M, 0, depth_bits, ib + o_tmp);
+        const SortZeroSpan tile_zero = (M > 0 && N > 0) ? sort_zero_span(I, 0, tile_bits, ib + o_tmp)
+                                                         : SortZeroSpan{nullptr, 0};
         {
             StageTimer tm(ctx, ST_EMIT);
             CompactArgs ca{};
             ca.num_splats = N; ca.counts = st->counts; ca.depth_bits = st->depth_bits;
             ca.block_offsets = st->block_stats + (size_t)BS_EMIT * nblocks; ca.counters = st->counters;
             ca.keys = dkeys; ca.vals = dvals;
+            ca.zero = depth_zero.ptr; ca.zero_words = depth_zero.words;   // the depth sort's one-sweep state
             VS_HIP(launch_compact(ca, s), "compaction");
         }
         {
             StageTimer tm(ctx, ST_SORT);
             VS_HIP(radix_sort_pairs(dkeys, dvals, dkeys_sorted, order, M, m_dev, false, 0, depth_bits, ib + o_tmp,
-                                    err, s, ctx->spin_limit),
+                                    err, s, ctx->spin_limit, nullptr, depth_zero.ptr != nullptr),
                    "depth sort");
         }
         {
@@ -726,6 +746,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
             ea.num_emitters = M; ea.m_dev = m_dev; ea.order = order;
             ea.counts = st->counts; ea.slot_base = slot_base; ea.slot_base_g = slot_base_g;
+            ea.zero = tile_zero.ptr; ea.zero_words = tile_zero.words;      // the tile sort's one-sweep state
             ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u; ea.capacity = I;
             VS_HIP(launch_emit(ea, s), "emit kernel");
         }
@@ -733,7 +754,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         {
             StageTimer tm(ctx, ST_SORT);
             VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, i_dev, false, 0, tile_bits, ib + o_tmp,
-                                    err, s, ctx->spin_limit, &tro),
+                                    err, s, ctx->spin_limit, &tro, tile_zero.ptr != nullptr),
                    "tile sort");
             st->tiles_pending = tro.done;
         }
@@ -758,7 +779,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         RasterArgs ra{};
         ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T; ra.num_splats = N;
         // longest lists first within each XCD's band (the forward's cost grows with its list)
-        VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s, bwd_info ? st->ranges_shrunk : nullptr, true),
+        VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s, bwd_info ? st->ranges_shrunk : nullptr, true,
+                                 ctx->dev_flags, lag_slot ? lag_slot->host + CNT_COUNT : nullptr, CTX_FLAGS),
                "tile order");
         ra.order = st->tile_order;
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
@@ -781,15 +803,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     if (lagged) {
         // Counts leave behind an event; the next training render at this size
         // (or vs_ctx_settle_lagged_counts) reads them.
-        vs_ctx::Pending& p = ctx->pending[key];
-        if (!p.host) {
-            VS_HIP(hipHostMalloc(reinterpret_cast<void**>(&p.host), (CNT_COUNT + CTX_FLAGS) * sizeof(uint32_t),
-                                 hipHostMallocDefault), "hipHostMalloc(lagged counts)");
-            VS_HIP(hipEventCreateWithFlags(&p.ev, hipEventDisableTiming), "hipEventCreate(lagged counts)");
-        }
-        VS_HIP(hipMemcpyAsync(p.host, st->counters, CNT_COUNT * 4, hipMemcpyDeviceToHost, s), "lagged counter copy");
-        VS_HIP(hipMemcpyAsync(p.host + CNT_COUNT, ctx->dev_flags, CTX_FLAGS * 4, hipMemcpyDeviceToHost, s),
-               "lagged flag copy");
+        vs_ctx::Pending& p = *lag_slot;
         VS_HIP(hipEventRecord(p.ev, s), "hipEventRecord(lagged counts)");
         p.capacity = isect_cap; p.splats = N; p.limit = limit; p.live = true;
         out->num_visible = have_lag ? std::min(lag_vis, N) : 0u;

@@ -311,7 +311,7 @@ VS_DEV uint32_t wave_max(uint32_t v) {
 constexpr int FIN_BLOCK = 1024;
 __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __restrict__ stats, uint32_t nb,
                                                                    uint32_t* __restrict__ counters,
-                                                                   uint32_t isect_capacity) {
+                                                                   uint32_t isect_capacity, uint32_t* host_copy) {
     __shared__ uint32_t s_w[FIN_BLOCK / 64];
     __shared__ uint32_t s_vis[FIN_BLOCK / 64], s_min[FIN_BLOCK / 64], s_max[FIN_BLOCK / 64];
     __shared__ unsigned long long s_hits[FIN_BLOCK / 64];
@@ -361,13 +361,17 @@ __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __
         for (int w = 0; w < FIN_BLOCK / 64; ++w) {
             tv += s_vis[w]; tmn = min(tmn, s_min[w]); tmx = max(tmx, s_max[w]); th += s_hits[w];
         }
-        counters[CNT_VISIBLE] = tv;
-        counters[CNT_DEPTH_MIN] = tmn;
-        counters[CNT_DEPTH_MAX] = tmx;
-        counters[CNT_EMITTERS] = carry;
-        counters[CNT_ISECT64] = (uint32_t)th;
-        counters[CNT_ISECT64 + 1] = (uint32_t)(th >> 32);
-        counters[CNT_BOUNDED] = th < (unsigned long long)isect_capacity ? (uint32_t)th : isect_capacity;
+        uint32_t c[CNT_COUNT] = {};
+        c[CNT_VISIBLE] = tv;
+        c[CNT_DEPTH_MIN] = tmn;
+        c[CNT_DEPTH_MAX] = tmx;
+        c[CNT_EMITTERS] = carry;
+        c[CNT_ISECT64] = (uint32_t)th;
+        c[CNT_ISECT64 + 1] = (uint32_t)(th >> 32);
+        c[CNT_BOUNDED] = th < (unsigned long long)isect_capacity ? (uint32_t)th : isect_capacity;
+        for (int i = 0; i < CNT_COUNT; ++i) counters[i] = c[i];
+        if (host_copy)
+            for (int i = 0; i < CNT_COUNT; ++i) host_copy[i] = c[i];
     }
 }
 
@@ -557,7 +561,12 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
         a.counts[g] = hits;
         a.depth_bits[g] = dbits;
         a.compact[g] = visible ? g + 1u : 0u;
+        if (a.visible) a.visible[g] = 0.0f;
     }
+    // every tile's range starts as (0xFFFFFFFF, 0): the tile sort's range pass
+    // lowers starts and raises ends
+    for (uint32_t t = g; t < a.num_tiles; t += gridDim.x * PROJ_BLOCK)
+        reinterpret_cast<uint2*>(a.ranges)[t] = make_uint2(0xFFFFFFFFu, 0u);
 
     // Block statistics, reduced by finalize_counts_kernel (no global atomics:
     // a same-address atomic from every wave serialises across the XCDs).
@@ -606,6 +615,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) compact_kernel(CompactArgs a) {
         a.keys[o] = a.depth_bits[g] - a.counters[CNT_DEPTH_MIN];
         a.vals[o] = g;
     }
+    for (uint64_t i = g; i < a.zero_words; i += (uint64_t)gridDim.x * PROJ_BLOCK) a.zero[i] = 0u;
 }
 
 // Emission (kernels/map_gaussians.rs:23-174): a splat with hits owns the
@@ -668,6 +678,8 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
         a.tiles[base + k] = sentinel;
         a.vals[base + k] = g;
     }
+    for (uint64_t i = (uint64_t)blockIdx.x * PROJ_BLOCK + threadIdx.x; i < a.zero_words; i += (uint64_t)gridDim.x * PROJ_BLOCK)
+        a.zero[i] = 0u;
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n) {
@@ -683,8 +695,8 @@ static uint32_t fill_grid(uint64_t n) {
 }
 
 hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, uint32_t isect_capacity,
-                                  hipStream_t s) {
-    finalize_counts_kernel<<<1, FIN_BLOCK, 0, s>>>(block_stats, nblocks, counters, isect_capacity);
+                                  hipStream_t s, uint32_t* host_copy) {
+    finalize_counts_kernel<<<1, FIN_BLOCK, 0, s>>>(block_stats, nblocks, counters, isect_capacity, host_copy);
     return hipGetLastError();
 }
 

@@ -106,7 +106,10 @@ VS_DEV uint32_t order_bin(uint32_t lo, uint32_t hi) {
 
 __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(uint32_t* ranges, uint32_t num_tiles,
                                                                  uint32_t* __restrict__ order,
-                                                                 uint32_t* __restrict__ shrunk_init, int fix_empty) {
+                                                                 uint32_t* __restrict__ shrunk_init, int fix_empty,
+                                                                 const uint32_t* __restrict__ flags_from,
+                                                                 uint32_t* flags_to, uint32_t nflags) {
+    if (blockIdx.x == 0 && threadIdx.x < nflags) flags_to[threadIdx.x] = flags_from[threadIdx.x];
     __shared__ uint32_t s_bin[ORDER_BINS];
     __shared__ uint32_t s_wave[ORDER_BLOCK / 64];
     const uint32_t per = (num_tiles + 7) / 8;
@@ -974,9 +977,12 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 }
 
 hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
-                             uint32_t* shrunk_init, bool fix_empty) {
+                             uint32_t* shrunk_init, bool fix_empty, const uint32_t* flags_from, uint32_t* flags_to,
+                             uint32_t nflags) {
     if (num_tiles == 0) return hipSuccess;
-    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init, fix_empty ? 1 : 0);
+    if (!flags_to) nflags = 0;
+    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init, fix_empty ? 1 : 0, flags_from,
+                                                flags_to, nflags);
     return hipGetLastError();
 }
 

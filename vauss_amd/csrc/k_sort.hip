@@ -427,7 +427,7 @@ size_t sort_tmp_bytes(uint64_t n, bool key64) {
 template <typename K>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_out, uint32_t* vals_out, uint32_t n,
                             const uint32_t* n_dev, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t* err,
-                            hipStream_t s, uint32_t spin_limit, TileRangesOut* tr) {
+                            hipStream_t s, uint32_t spin_limit, TileRangesOut* tr, bool state_zeroed) {
     if (n == 0) return hipSuccess;
     const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
     const uint32_t passes = (bits + 7) / 8;
@@ -449,7 +449,8 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
     uint32_t* ghist = reinterpret_cast<uint32_t*>(p);          // [passes][256]
     uint32_t* status = ghist + passes * 256 + 16;              // [passes][os_tiles][256]
     if (onesweep) {
-        hipError_t e = launch_fill_u32(ghist, 0u, (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
+        hipError_t e = hipSuccess;
+        if (!state_zeroed) e = launch_fill_u32(ghist, 0u, (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
         if (e != hipSuccess) return e;
         // ~4k keys per block up to HIST_BLOCKS blocks: each block ends with
         // passes x 256 global atomics, so a grid much wider than the data
@@ -500,13 +501,31 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
 
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
-                            void* tmp, uint32_t* err, hipStream_t s, uint32_t spin_limit, TileRangesOut* tr) {
+                            void* tmp, uint32_t* err, hipStream_t s, uint32_t spin_limit, TileRangesOut* tr,
+                            bool state_zeroed) {
     if (tr) tr->done = false;
     if (key64)
         return sort_impl<uint64_t>(static_cast<const uint64_t*>(keys_in), vals_in, static_cast<uint64_t*>(keys_out),
-                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, nullptr);
+                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, nullptr, false);
     return sort_impl<uint32_t>(static_cast<const uint32_t*>(keys_in), vals_in, static_cast<uint32_t*>(keys_out),
-                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, tr);
+                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, tr, state_zeroed);
+}
+
+SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, void* tmp) {
+    // the layout of sort_impl<uint32_t>: ping-pong keys, values, digit table, scan scratch, then the
+    // one-sweep histograms and status
+    const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
+    const uint32_t passes = (bits + 7) / 8;
+    if (n == 0 || passes == 0 || !(n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS)) return SortZeroSpan{nullptr, 0};
+    const uint32_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;
+    char* p = reinterpret_cast<char*>(align_up(reinterpret_cast<uintptr_t>(tmp), 256));
+    p += align_up((size_t)n * 4, 256);
+    p += align_up((size_t)n * 4, 256);
+    p += align_up((size_t)nblocks * 256 * 4, 256);
+    p += align_up(scan_tmp_words((uint64_t)nblocks * 256) * 4, 256);
+    const uint32_t os_tile = n < OS_SMALL_N ? OS_SMALL_TILE : OS_TILE;
+    const uint64_t os_tiles = (n + os_tile - 1) / os_tile;
+    return SortZeroSpan{reinterpret_cast<uint32_t*>(p), (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256};
 }
 
 } // namespace vs

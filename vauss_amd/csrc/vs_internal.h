@@ -60,6 +60,9 @@ struct ProjectArgs {
     float4* proj_surf;          // [N][4] surfels: M rows, low-pass centre, normal (vs_surfel.h layout), or null
     uint32_t* compact;          // [N] g + 1 for splats past every cull, else 0 (compact_from_global)
     uint32_t* block_stats;      // [BS_ROWS][ceil(N/256)]
+    float* visible;             // [N] cleared to 0 (the forward marks the splats it blends), or null
+    uint32_t* ranges;           // [num_tiles, 2] set to (0xFFFFFFFF, 0) for the tile sort's range pass
+    uint32_t num_tiles;
 };
 
 struct CompactArgs {
@@ -70,6 +73,8 @@ struct CompactArgs {
     const uint32_t* counters;        // device counters (CNT_DEPTH_MIN)
     uint32_t* keys;                  // [M] depth bits - min
     uint32_t* vals;                  // [M] global ids
+    uint32_t* zero;                  // [zero_words] cleared (the depth sort's one-sweep state), or null
+    uint64_t zero_words;
 };
 
 struct EmitArgs {
@@ -85,6 +90,8 @@ struct EmitArgs {
     uint32_t* tiles;                 // [capacity] tile id (T = sentinel)
     uint32_t* vals;                  // [capacity] global id
     uint32_t capacity;               // slots at or past it are dropped (the farthest splats' pairs)
+    uint32_t* zero;                  // [zero_words] cleared (the tile sort's one-sweep state), or null
+    uint64_t zero_words;
 };
 
 struct RasterArgs {
@@ -236,10 +243,11 @@ struct ShStepArgs {
 
 // ---- launchers (return hipError_t of the launch) -------------------------------
 hipError_t launch_project(const ProjectArgs& a, hipStream_t s);
-// Reduces the projection's block stats into `counters` and turns the block
-// emitter counts (row BS_EMIT) into exclusive offsets in place.
+// Reduces the projection's block stats into `counters` (and a copy at
+// `host_copy`, a pinned readback slot, if given) and turns the block emitter
+// counts (row BS_EMIT) into exclusive offsets in place.
 hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint32_t* counters, uint32_t isect_capacity,
-                                  hipStream_t s);
+                                  hipStream_t s, uint32_t* host_copy = nullptr);
 hipError_t launch_compact(const CompactArgs& a, hipStream_t s);
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
@@ -261,8 +269,11 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 // `shrunk_init`, every tile's entry there is set to (start, start): the
 // forward's shrunk ranges, whose ends it raises.
 // `fix_empty`: ranges left at (0xFFFFFFFF, 0) by the sort become (0, 0).
+// `flags_to` (optional): copies nflags words of flags_from there (the
+// lagged render's pinned readback slot).
 hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
-                             uint32_t* shrunk_init = nullptr, bool fix_empty = false);
+                             uint32_t* shrunk_init = nullptr, bool fix_empty = false,
+                             const uint32_t* flags_from = nullptr, uint32_t* flags_to = nullptr, uint32_t nflags = 0);
 hipError_t launch_ranges_init(uint32_t* ranges, uint32_t num_tiles, hipStream_t s);
 hipError_t launch_tiles_from_ranges(const uint32_t* ranges, uint32_t num_tiles, uint32_t n, uint32_t* tiles,
                                     hipStream_t s);
@@ -328,6 +339,13 @@ struct TileRangesOut {
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
                             void* tmp, uint32_t* err, hipStream_t s,
-                            uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT, TileRangesOut* tr = nullptr);
+                            uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT, TileRangesOut* tr = nullptr,
+                            bool state_zeroed = false);
+// The words of `tmp` that a u32-key sort of n keys over [first_bit, end_bit)
+// needs cleared before it runs (its one-sweep histograms and tile status):
+// a caller that clears them in a kernel of its own passes state_zeroed and
+// the sort skips its fill.  {nullptr, 0} when the sort would not use them.
+struct SortZeroSpan { uint32_t* ptr; uint64_t words; };
+SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, void* tmp);
 
 } // namespace vs
