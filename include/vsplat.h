@@ -218,10 +218,11 @@ vs_status vs_ctx_set_lagged_counts(vs_ctx* ctx, int enable);
 vs_status vs_ctx_settle_lagged_counts(vs_ctx* ctx, uint64_t* renders, uint64_t* overflows);
 
 /* Bound on a one-sweep radix pass's wait for its predecessors' digit counts
- * (the decoupled look-back): after `polls` polls of an unpublished
- * predecessor the pass gives up, its output is wrong, and the call that ran
- * the sort returns VS_ERR_HIP (vs_radix_argsort_*, exact renders; a lagged
- * render's sorts are reported by the next lagged render at its size or by
+ * (the decoupled look-back), and on the render's slot scan's wait for its
+ * predecessors' sums: after `polls` polls of an unpublished predecessor the
+ * pass gives up, its output is wrong, and the call that ran it returns
+ * VS_ERR_HIP (vs_radix_argsort_*, exact renders; a lagged render's are
+ * reported by the next lagged render at its size or by
  * vs_ctx_settle_lagged_counts).  0xFFFFFFFF restores the default (2^18).  The
  * reference's sort has no bounded wait (crates/splat-train-sort/src/lib.rs);
  * a small limit lets tests drive the give-up path with every kernel exiting. */

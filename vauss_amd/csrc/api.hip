@@ -50,7 +50,7 @@ struct vs_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     uint32_t* host_counters = nullptr;    // pinned readback of the projection counters (+ CTX_FLAGS words)
-    uint32_t* dev_flags = nullptr;        // device: [0] set when a sort look-back gave up waiting
+    uint32_t* dev_flags = nullptr;        // device: [0] set when a sort or scan look-back gave up waiting
     uint32_t timing = 0;                  // bitmask of timed stages (VS_TIME_*)
     uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT;   // look-back polls before a one-sweep pass gives up
     // the unmasked pixel count of the last circular L1 mask (vs_l1_cotangent)
@@ -149,7 +149,7 @@ bool pass_geometry(vs_pass p) { return p == VS_PASS_GEOMETRY || p == VS_PASS_GEO
 bool pass_surface_criterion(vs_pass p) { return !pass_training(p) && p != VS_PASS_GEOMETRY_TRAIN_DEPTH; }
 
 const char* const SORT_STALL_MSG =
-    "a radix sort's look-back gave up waiting for a predecessor's counts; its output is wrong";
+    "a one-sweep look-back (radix sort or slot scan) gave up waiting for a predecessor's counts; its output is wrong";
 
 // The sort-stall flag as copied to ctx->host_counters[CNT_COUNT + ...] behind
 // the last readback: report it (and clear the device word) if set.
@@ -702,7 +702,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const size_t o_dk = itake((size_t)M * 4), o_dv = itake((size_t)M * 4);
         const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)M * 4);
         const size_t o_base_g = itake((size_t)N * 4);
-        const size_t o_scan = itake(scan_tmp_words(M) * 4);
+        const size_t o_scan = itake(scan_lookback_status_words(M) * 4);
         const size_t o_tmp = itake(sort_tmp_bytes(std::max(I, M), false));   // serves both sorts
         VS_HIP(lib_alloc(ctx, &st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
         char* ib = static_cast<char*>(st->isect_arena);
@@ -730,6 +730,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
             ca.block_offsets = st->block_stats + (size_t)BS_EMIT * nblocks; ca.counters = st->counters;
             ca.keys = dkeys; ca.vals = dvals;
             ca.zero = depth_zero.ptr; ca.zero_words = depth_zero.words;   // the depth sort's one-sweep state
+            ca.zero2 = scan_tmp; ca.zero2_words = scan_lookback_status_words(M);   // the slot scan's status
             VS_HIP(launch_compact(ca, s), "compaction");
         }
         {
@@ -740,7 +741,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         }
         {
             StageTimer tm(ctx, ST_EMIT);
-            VS_HIP(scan_u32(st->counts, slot_base, M, false, scan_tmp, nullptr, s, order, m_dev, N, true, slot_base_g),
+            VS_HIP(scan_u32_lookback(st->counts, slot_base, M, scan_tmp, err, s, ctx->spin_limit, order, m_dev, N,
+                                     slot_base_g),
                    "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;

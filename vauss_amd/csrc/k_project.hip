@@ -616,6 +616,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) compact_kernel(CompactArgs a) {
         a.vals[o] = g;
     }
     for (uint64_t i = g; i < a.zero_words; i += (uint64_t)gridDim.x * PROJ_BLOCK) a.zero[i] = 0u;
+    for (uint64_t i = g; i < a.zero2_words; i += (uint64_t)gridDim.x * PROJ_BLOCK) a.zero2[i] = 0u;
 }
 
 // Emission (kernels/map_gaussians.rs:23-174): a splat with hits owns the

@@ -139,6 +139,112 @@ __global__ void __launch_bounds__(SINGLE_BLOCK) scan_single_kernel(uint32_t* __r
     if (total_out && threadIdx.x == 0) *total_out = carry;
 }
 
+// Single-pass scan with decoupled look-back: each block scans its tile,
+// publishes its total, and finds the sum of every earlier tile by reading
+// its predecessors' published totals 64 at a time (one per lane of the first
+// wavefront) back to the nearest full prefix.  A block only waits on
+// lower-indexed blocks, which are dispatched first and publish before they
+// wait, so the chain drains; a wait past `spin_limit` polls sets *err and
+// proceeds (the result is then wrong and reported).  Status words are 64-bit:
+// two flag bits over a 62-bit sum.
+constexpr uint64_t LB_AGG = 1ull << 62, LB_PREFIX = 2ull << 62, LB_VAL = (1ull << 62) - 1ull;
+
+__global__ void __launch_bounds__(SCAN_BLOCK) scan_lookback_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
+                                                                   uint64_t n_cap, const uint32_t* __restrict__ perm,
+                                                                   const uint32_t* __restrict__ n_dev, uint32_t perm_bound,
+                                                                   uint32_t* __restrict__ out2,
+                                                                   unsigned long long* status, uint32_t* err,
+                                                                   uint32_t spin_limit) {
+    const uint64_t n = scan_count(n_cap, n_dev);
+    const uint64_t base = (uint64_t)blockIdx.x * SCAN_TILE;
+    if (base >= n) return;   // uniform: no later block has elements either
+    __shared__ uint32_t s_data[SCAN_TILE];
+    __shared__ uint32_t s_w[48];
+    __shared__ unsigned long long s_prefix;
+#pragma unroll
+    for (int i = 0; i < SCAN_ITEMS; ++i) {
+        const uint32_t li = i * SCAN_BLOCK + threadIdx.x;
+        const uint64_t idx = base + li;
+        s_data[li] = (idx < n) ? scan_load(in, perm, idx, perm_bound) : 0u;
+    }
+    __syncthreads();
+    uint32_t v[SCAN_ITEMS];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < SCAN_ITEMS; ++i) { v[i] = s_data[threadIdx.x * SCAN_ITEMS + i]; acc += v[i]; }
+    uint32_t excl;
+    const uint32_t total = block_excl_scan<SCAN_BLOCK>(acc, excl, s_w);
+    if (threadIdx.x < 64) {
+        const uint32_t lane = threadIdx.x;
+        const int b = (int)blockIdx.x;
+        if (lane == 0)
+            __hip_atomic_store(&status[b], (b == 0 ? LB_PREFIX : LB_AGG) | (unsigned long long)total, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        unsigned long long prefix = 0;
+        if (b > 0) {
+            int top = b - 1;           // the window is [top - 63, top], lane i reads top - i
+            uint32_t spins = 0;
+            while (true) {
+                const int j = top - (int)lane;
+                const unsigned long long st =
+                    j >= 0 ? __hip_atomic_load(&status[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : LB_PREFIX;
+                const unsigned long long flag = st & ~LB_VAL;
+                const uint64_t pref = __ballot(flag == LB_PREFIX), unpub = __ballot(flag == 0ull);
+                const uint32_t last = pref ? (uint32_t)__builtin_ctzll(pref) : 63u;   // the lanes this window needs
+                const uint64_t need = last == 63u ? ~0ull : ((2ull << last) - 1ull);
+                if (unpub & need) {   // a needed predecessor has not published yet
+                    if (++spins > spin_limit) { if (lane == 0) atomicOr(err, 1u); break; }
+                    __builtin_amdgcn_s_sleep(1);
+                    continue;
+                }
+                unsigned long long part = ((need >> lane) & 1ull) ? (st & LB_VAL) : 0ull;
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+                prefix += part;
+                if (pref) break;
+                top -= 64;
+            }
+            if (lane == 0)
+                __hip_atomic_store(&status[b], LB_PREFIX | (prefix + total), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane == 0) s_prefix = prefix;
+    }
+    __syncthreads();
+    uint32_t run = excl + (uint32_t)s_prefix;
+#pragma unroll
+    for (int i = 0; i < SCAN_ITEMS; ++i) {
+        s_data[threadIdx.x * SCAN_ITEMS + i] = run;
+        run += v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < SCAN_ITEMS; ++i) {
+        const uint32_t li = i * SCAN_BLOCK + threadIdx.x;
+        const uint64_t idx = base + li;
+        if (idx < n) {
+            out[idx] = s_data[li];
+            if (out2) {
+                const uint32_t k = perm[idx];
+                if (k < perm_bound) out2[k] = s_data[li];
+            }
+        }
+    }
+}
+
+uint64_t scan_lookback_status_words(uint64_t n) { return 2 * ((n + SCAN_TILE - 1) / SCAN_TILE); }
+
+hipError_t scan_u32_lookback(const uint32_t* in, uint32_t* out, uint64_t n, uint32_t* status, uint32_t* err,
+                             hipStream_t s, uint32_t spin_limit, const uint32_t* perm, const uint32_t* n_dev,
+                             uint32_t perm_bound, uint32_t* out_scattered) {
+    if (n == 0) return hipSuccess;
+    const uint64_t blocks = (n + SCAN_TILE - 1) / SCAN_TILE;
+    scan_lookback_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, perm, n_dev, perm_bound,
+                                                                 perm ? out_scattered : nullptr,
+                                                                 reinterpret_cast<unsigned long long*>(status), err,
+                                                                 spin_limit);
+    return hipGetLastError();
+}
+
 size_t scan_tmp_words(uint64_t n) {
     const uint64_t blocks = (n + SCAN_TILE - 1) / SCAN_TILE;
     return (size_t)(blocks ? blocks : 1) + 64;

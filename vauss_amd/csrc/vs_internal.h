@@ -75,6 +75,8 @@ struct CompactArgs {
     uint32_t* vals;                  // [M] global ids
     uint32_t* zero;                  // [zero_words] cleared (the depth sort's one-sweep state), or null
     uint64_t zero_words;
+    uint32_t* zero2;                 // [zero2_words] cleared (the slot scan's look-back status), or null
+    uint64_t zero2_words;
 };
 
 struct EmitArgs {
@@ -319,6 +321,15 @@ hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusiv
                     const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu, bool out_in_order = false,
                     uint32_t* out_scattered = nullptr);
 hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_t* total_out, hipStream_t s);
+// The same exclusive scan in one kernel by decoupled look-back, written in
+// sequence order (out[i]; `out_scattered[perm[i]]` too when both are given).
+// `status` needs scan_lookback_status_words(n) words, zero on entry; a
+// look-back that waits past `spin_limit` polls sets *err.
+uint64_t scan_lookback_status_words(uint64_t n);
+hipError_t scan_u32_lookback(const uint32_t* in, uint32_t* out, uint64_t n, uint32_t* status, uint32_t* err,
+                             hipStream_t s, uint32_t spin_limit, const uint32_t* perm = nullptr,
+                             const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu,
+                             uint32_t* out_scattered = nullptr);
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
 size_t sort_tmp_bytes(uint64_t n, bool key64);
