@@ -253,7 +253,7 @@ constexpr uint32_t OS_VALUE = (1u << 30) - 1u;
 constexpr int MAX_PASSES = 8;
 constexpr int LOOKBACK = VS_LOOKBACK;                  // predecessor statuses read per look-back step
 constexpr uint32_t HIST_BLOCKS = VS_HIST_BLOCKS;
-constexpr int HIST_ITEMS = 4;
+constexpr int HIST_ITEMS = 16;       // keys per lane in flight per chunk (the kernel is latency-bound below that)
 
 // Digit histograms of every pass in one read: ghist[p][d] (zeroed by the caller).
 // Each wavefront takes chunks of HIST_ITEMS x 64 consecutive keys.
