@@ -242,16 +242,40 @@ VS_DEV uint32_t compact_bits_16(uint32_t v) {
 // the cutoff c whenever sigma > ln(opac / c); with s = 1.01 ln(opac / c) +
 // 0.01 a quadrant is dead when, over its pixel centres, both
 //   * the low-pass disk misses: |pixel - centre|^2 > s, and
-//   * the ray-plane disk misses: u^2 + v^2 > 2 s (1 + 1e-3).
-// q = h_u x h_v = R0 x R1 + x (R1 x R2) - y (R0 x R2) is affine in the pixel
-// (x, y) (R0, R1, R2 the rows of M), and (u, v) = (q.x, q.y) / q.z.  Over the
-// quadrant the exact q lies in the box of its four corner values, and the
-// f32 q of surfel_hit within E of it at every pixel, E = 16 ulp of the sum of
-// the magnitudes the cross product multiplies (its inputs bounded as
-// |R0| + |x| |R2|, |R1| + |y| |R2|), so every pixel's q is in the corner box
-// widened by 2E.  If q.z keeps one sign across that box, u and v lie in its
-// interval quotients, and the plane test uses the box they span.  Anything
-// else (q.z near 0, non-finite rows) keeps the quadrant.
+//   * the ray-plane disk misses: q.x^2 + q.y^2 > 2 s q.z^2,
+// where q = h_u x h_v and (u, v) = (q.x, q.y) / q.z (a pixel with q.z = 0
+// gets a non-finite depth and is no hit; the 1 % of s covers the rounding of
+// the quotients).  The exact q is affine in the pixel:
+// q(x, y) = R0 x R1 + x (R1 x R2) - y (R0 x R2) (R0, R1, R2 the rows of M), so
+// over the quadrant it is P + t1 A + t2 B, t in [0, 1]^2, with P the q at its
+// first pixel centre, A = 7 (R1 x R2) and B = -7 (R0 x R2).  Per component,
+// the f32 q of surfel_hit at any of its pixels is within
+// E = 6.5 ulp (H_y V_z + H_z V_y) (and so on) of the exact q (h_u within
+// 2 ulp of H = |R0| + |x| |R2|, h_v of V = |R1| + |y| |R2|, one rounding of
+// each product and of the difference), and the model built from the f32 P, A
+// and B within E + 4.1 ulp of 7 (|.| |.| + |.| |.|) of the exact q; d is the
+// sum.  f = q.x^2 + q.y^2 - 2 s q.z^2 is then a quadratic in t, a pixel's f is
+// at least the model's minus 2 (|q.x| d.x + |q.y| d.y) + 2 s (2 |q.z| + d.z)
+// d.z, and the f32 evaluation of the model's minimum errs by far less than
+// 1e-4 of (|q.x| + |q.y|)^2 + 2 s q.z^2.  The minimum is at a corner, at the
+// vertex of an edge parabola (value f - k^2 / h), or at the interior critical
+// point when the Hessian is positive definite: then q.xy = 0 at some point of
+// the pixel plane, the unconstrained minimum is <= 0, and a critical point
+// inside the square keeps the quadrant.  Non-finite or huge values keep the
+// quadrant.
+VS_DEV float3 surf_q(float4 m0, float4 m1, float4 m2, float px, float py) {
+    const float hux = m0.x - px * m1.z, huy = m0.y - px * m1.w, huz = m0.z - px * m2.x;
+    const float hvx = m0.w - py * m1.z, hvy = m1.x - py * m1.w, hvz = m1.y - py * m2.x;
+    return make_float3(huy * hvz - huz * hvy, huz * hvx - hux * hvz, hux * hvy - huy * hvx);
+}
+VS_DEV float surf_f(float3 p, float s2) { return p.x * p.x + p.y * p.y - s2 * (p.z * p.z); }
+VS_DEV float surf_dot(float3 p, float3 d, float s2) { return p.x * d.x + p.y * d.y - s2 * (p.z * d.z); }
+// Minimum over t in [0, 1] of f + 2 k t + h t^2 is below thr (the ends are
+// tested separately): only a vertex inside the edge matters.
+VS_DEV bool surf_edge_low(float f, float k, float h, float thr) {
+    return h > 0.0f && k < 0.0f && -k < h && !(f - k * (k * __builtin_amdgcn_rcpf(h)) > thr);
+}
+
 VS_DEV bool surfel_quadrant_live(float x0, float y0, float4 m0, float4 m1, float4 m2, float opac, bool smooth) {
     const float cut = smooth ? (ALPHA_MID - 0.5f * ALPHA_BAND) : ALPHA_MID;
     const float s = QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS;
@@ -260,35 +284,51 @@ VS_DEV bool surfel_quadrant_live(float x0, float y0, float4 m0, float4 m1, float
     const float a0 = x0 - m2.y, a1 = a0 + 7.0f, b0 = y0 - m2.z, b1 = b0 + 7.0f;
     const float nx_ = __builtin_fminf(__builtin_fmaxf(0.0f, a0), a1), ny_ = __builtin_fminf(__builtin_fmaxf(0.0f, b0), b1);
     if (!(nx_ * nx_ + ny_ * ny_ > s)) return true;
-    const F3 r0{m0.x, m0.y, m0.z}, r1{m0.w, m1.x, m1.y}, r2{m1.z, m1.w, m2.x};
-    float lo[3] = {3.0e38f, 3.0e38f, 3.0e38f}, hi[3] = {-3.0e38f, -3.0e38f, -3.0e38f};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const float x = x0 + ((c & 1) ? 7.0f : 0.0f), y = y0 + ((c & 2) ? 7.0f : 0.0f);
-        const float hux = r0.x - x * r2.x, huy = r0.y - x * r2.y, huz = r0.z - x * r2.z;
-        const float hvx = r1.x - y * r2.x, hvy = r1.y - y * r2.y, hvz = r1.z - y * r2.z;
-        const float q[3] = {huy * hvz - huz * hvy, huz * hvx - hux * hvz, hux * hvy - huy * hvx};
-#pragma unroll
-        for (int i = 0; i < 3; ++i) { lo[i] = __builtin_fminf(lo[i], q[i]); hi[i] = __builtin_fmaxf(hi[i], q[i]); }
-    }
+    // pixel centres x0 + i, y0 + j exact in f32
+    if (!(fabsf(x0) < 4.0e6f && fabsf(y0) < 4.0e6f)) return true;
+    const float r0x = m0.x, r0y = m0.y, r0z = m0.z, r1x = m0.w, r1y = m1.x, r1z = m1.y;
+    const float r2x = m1.z, r2y = m1.w, r2z = m2.x;
     const float xm = __builtin_fmaxf(fabsf(x0), fabsf(x0 + 7.0f)), ym = __builtin_fmaxf(fabsf(y0), fabsf(y0 + 7.0f));
-    const float Hx = fabsf(r0.x) + xm * fabsf(r2.x), Hy = fabsf(r0.y) + xm * fabsf(r2.y), Hz = fabsf(r0.z) + xm * fabsf(r2.z);
-    const float Vx = fabsf(r1.x) + ym * fabsf(r2.x), Vy = fabsf(r1.y) + ym * fabsf(r2.y), Vz = fabsf(r1.z) + ym * fabsf(r2.z);
-    const float mag = Hy * Vz + Hz * Vy + Hz * Vx + Hx * Vz + Hx * Vy + Hy * Vx;
-    const float e2 = 2.0f * 16.0f * 5.9604645e-8f * mag;      // 2E
-    float zl = lo[2] - e2, zh = hi[2] + e2;
-    float xl = lo[0] - e2, xh = hi[0] + e2, yl = lo[1] - e2, yh = hi[1] + e2;
-    if (!(zl > 0.0f)) {
-        if (!(zh < 0.0f)) return true;                     // q.z may vanish (or is not finite)
-        const float t0 = -zh, t1 = -zl; zl = t0; zh = t1;  // flip q: (u, v) unchanged
-        const float u0 = -xh, u1 = -xl; xl = u0; xh = u1;
-        const float v0 = -yh, v1 = -yl; yl = v0; yh = v1;
+    const float Hx = fabsf(r0x) + xm * fabsf(r2x), Hy = fabsf(r0y) + xm * fabsf(r2y), Hz = fabsf(r0z) + xm * fabsf(r2z);
+    const float Vx = fabsf(r1x) + ym * fabsf(r2x), Vy = fabsf(r1y) + ym * fabsf(r2y), Vz = fabsf(r1z) + ym * fabsf(r2z);
+    constexpr float ULP = 5.9604645e-8f;
+    const float3 A = make_float3(7.0f * (r1y * r2z - r1z * r2y), 7.0f * (r1z * r2x - r1x * r2z), 7.0f * (r1x * r2y - r1y * r2x));
+    const float3 B = make_float3(7.0f * (r0z * r2y - r0y * r2z), 7.0f * (r0x * r2z - r0z * r2x), 7.0f * (r0y * r2x - r0x * r2y));
+    const float ax_ = fabsf(r2x), ay_ = fabsf(r2y), az_ = fabsf(r2z);
+    const float dx = (13.0f * ULP) * (Hy * Vz + Hz * Vy) +
+                     (28.7f * ULP) * ((fabsf(r1y) + fabsf(r0y)) * az_ + (fabsf(r1z) + fabsf(r0z)) * ay_);
+    const float dy = (13.0f * ULP) * (Hz * Vx + Hx * Vz) +
+                     (28.7f * ULP) * ((fabsf(r1z) + fabsf(r0z)) * ax_ + (fabsf(r1x) + fabsf(r0x)) * az_);
+    const float dz = (13.0f * ULP) * (Hx * Vy + Hy * Vx) +
+                     (28.7f * ULP) * ((fabsf(r1x) + fabsf(r0x)) * ay_ + (fabsf(r1y) + fabsf(r0y)) * ax_);
+    const float3 p00 = surf_q(m0, m1, m2, x0, y0);
+    const float3 p10 = make_float3(p00.x + A.x, p00.y + A.y, p00.z + A.z);
+    const float3 p01 = make_float3(p00.x + B.x, p00.y + B.y, p00.z + B.z);
+    const float3 p11 = make_float3(p10.x + B.x, p10.y + B.y, p10.z + B.z);
+    const float s2 = 2.0f * s;
+    const float qx = __builtin_fmaxf(__builtin_fmaxf(fabsf(p00.x), fabsf(p10.x)), __builtin_fmaxf(fabsf(p01.x), fabsf(p11.x)));
+    const float qy = __builtin_fmaxf(__builtin_fmaxf(fabsf(p00.y), fabsf(p10.y)), __builtin_fmaxf(fabsf(p01.y), fabsf(p11.y)));
+    const float qz = __builtin_fmaxf(__builtin_fmaxf(fabsf(p00.z), fabsf(p10.z)), __builtin_fmaxf(fabsf(p01.z), fabsf(p11.z)));
+    const float qxy = qx + qy;
+    const float M = qxy * qxy + s2 * (qz * qz);
+    if (!(M < 1.0e36f)) return true;
+    const float thr = 2.0f * (qx * dx + qy * dy) + s2 * ((2.0f * qz + dz) * dz) + 1.0e-4f * M;
+    const float f00 = surf_f(p00, s2), f10 = surf_f(p10, s2), f01 = surf_f(p01, s2), f11 = surf_f(p11, s2);
+    if (!(f00 > thr && f10 > thr && f01 > thr && f11 > thr)) return true;
+    const float hA = surf_f(A, s2), hB = surf_f(B, s2), hAB = surf_dot(A, B, s2);
+    const float g1 = surf_dot(p00, A, s2), g2 = surf_dot(p00, B, s2);
+    if (surf_edge_low(f00, g1, hA, thr) || surf_edge_low(f01, surf_dot(p01, A, s2), hA, thr) ||
+        surf_edge_low(f00, g2, hB, thr) || surf_edge_low(f10, surf_dot(p10, B, s2), hB, thr))
+        return true;
+    // interior critical point of a positive definite Hessian (scaled by 1/M)
+    const float c = __builtin_amdgcn_rcpf(M);
+    const float ha = hA * c, hb = hB * c, hab = hAB * c, ga = g1 * c, gb = g2 * c;
+    const float det = ha * hb - hab * hab;
+    if (ha > 0.0f && det > 0.0f) {
+        const float n1 = hab * gb - hb * ga, n2 = hab * ga - ha * gb, lo = -1.0e-3f * det, hi = 1.001f * det;
+        if (n1 >= lo && n1 <= hi && n2 >= lo && n2 <= hi) return true;
     }
-    // u = q.x / q.z over the box: extremes at the corners of the quotient
-    const float ul = __builtin_fminf(xl / zl, xl / zh), uh = __builtin_fmaxf(xh / zl, xh / zh);
-    const float vl = __builtin_fminf(yl / zl, yl / zh), vh = __builtin_fmaxf(yh / zl, yh / zh);
-    const float nu = __builtin_fminf(__builtin_fmaxf(0.0f, ul), uh), nv = __builtin_fminf(__builtin_fmaxf(0.0f, vl), vh);
-    return !(nu * nu + nv * nv > 2.0f * s * 1.001f);
+    return false;
 }
 
 constexpr int FWD_BATCH = 64;
