@@ -240,6 +240,23 @@ vs_status vs_ctx_set_sort_spin_limit(vs_ctx* ctx, uint32_t polls);
  * reference's release builds; without it, non-finite splats are culled. */
 vs_status vs_ctx_set_validation(vs_ctx* ctx, int enable);
 
+/* Depth cutoff for renders whose tiles are listed far more splats than
+ * their pixels can blend (no reference counterpart: the reference lists and
+ * sorts every intersection).  From the opacity each splat lays over the
+ * whole of a tile (its cores at 0.4 and 0.8 of its opacity), a tile's list
+ * stops at the depth bin (64 bins over the frame's depth range) by which
+ * every pixel of the tile has provably reached the raster's stopping
+ * transmittance; the splats it drops are never evaluated there, so images,
+ * consumed ranges and gradients are those of the full list.  Gaussian modes
+ * only.  VS_CUTOFF_AUTO (the default) applies it when a render lists at
+ * least 2048 intersections per tile on average (the exact count, or a lagged
+ * render's capacity); ON applies it to every gaussian render, OFF never.
+ * num_intersections still reports every intersection; the state view gives
+ * the listed ones, which the geometry render's median-id channel indexes
+ * (the same position within its tile's list as in the full list). */
+typedef enum vs_cutoff_mode { VS_CUTOFF_AUTO = 0, VS_CUTOFF_OFF = 1, VS_CUTOFF_ON = 2 } vs_cutoff_mode;
+vs_status vs_ctx_set_depth_cutoff(vs_ctx* ctx, vs_cutoff_mode mode);
+
 /* Fill every buffer the library allocates for this context with the f32
  * pattern of -12345.0 before first use, as the reference's test builds
  * initialise fresh tensors (crates/splat-train-cube/src/host.rs:23-36), so a
@@ -305,6 +322,11 @@ typedef struct vs_state_view {
     const float* proj_surf;         /* [N,16] surfels: M rows (9), low-pass centre (2), normal (3),
                                        the raster's footprint bound on sigma, 1 pad;
                                        else NULL */
+    uint32_t listed_intersections;  /* length of isect_tiles / isect_gids: num_intersections, or
+                                       under the depth cutoff the pairs each tile's list keeps */
+    uint32_t depth_cutoff;          /* 1: every tile's list is the front of its full list */
+    const uint32_t* listed_counts;  /* [N] pairs of each splat in the lists (intersect_counts
+                                       without the depth cutoff) */
 } vs_state_view;
 vs_status vs_fwd_state_view(const vs_fwd_state* state, vs_state_view* out);
 

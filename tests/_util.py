@@ -59,13 +59,14 @@ def circle_mask(img_size, center, radius) -> np.ndarray:
 def gpu_state_arrays(out):
     """Intermediate buffers of a GPU forward as numpy arrays keyed like the oracle's."""
     v = out.state.view()
-    n, i = v.num_splats, v.num_intersections
+    n, i = v.num_splats, v.listed_intersections
     return {
         "view": v,
         "tile": dev_to_numpy(v.isect_tiles, (i,), np.uint32),
         "depth_bits": dev_to_numpy(v.depth_bits, (n,), np.uint32),
         "gid": dev_to_numpy(v.isect_gids, (i,), np.uint32),
         "counts": dev_to_numpy(v.intersect_counts, (n,), np.uint32),
+        "listed_counts": dev_to_numpy(v.listed_counts, (n,), np.uint32),
         "proj_a": dev_to_numpy(v.proj_xy_conic, (n, 4), np.float32),
         "proj_b": dev_to_numpy(v.proj_c11_opac_rg, (n, 4), np.float32),
         "proj_c": dev_to_numpy(v.proj_b, (n,), np.float32),

@@ -14,7 +14,11 @@ inputs, then checks:
     sorted list, the list is ordered by (tile, depth bits, splat id), and the
     backward is linear in the image cotangent.
 The 3M-splat heavy-tailed case has 3.6e8 intersections; the oracle's render
-of it takes ~20 s on the host's cores.
+of it takes ~20 s on the host's cores.  These checks run on the full lists
+(depth cutoff off); the same view is then rendered with the depth cutoff on
+and checked against the same oracle render: every tile's list is the front of
+the full one and covers what the tile consumes, and the image, consumed
+ranges and gradients are unchanged.
 """
 import time
 
@@ -25,6 +29,7 @@ import torch
 import vauss_amd as va
 from oracle import pyoracle as po
 from tests._util import circle_mask, gpu_state_arrays, l1_cotangent_np, to_gpu
+from tests.test_gpu_cutoff import _check_cut_lists, _consumed
 from tests.test_gpu_parity import _check_forward, _check_grads, _check_param_grads
 from vauss_amd import scenes
 
@@ -63,8 +68,13 @@ def test_full_size_parity(cfg, view):
     cam = w.cameras[view].uniforms(w.img_size)
     t, s, o = to_gpu(w.scene)
     _log(f"{cfg}: GPU render of {n} splats at {w.img_size}")
-    out = va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
-    torch.cuda.synchronize()
+    ctx = va.Context.get(torch.device("cuda", 0))
+    ctx.set_depth_cutoff(ctx.CUTOFF_OFF)
+    try:
+        out = va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_depth_cutoff(ctx.CUTOFF_AUTO)
     gpu = gpu_state_arrays(out)
     _log(f"{cfg}: {out.aux.num_visible} visible, {out.aux.num_intersections} intersections; oracle forward")
     ref = po.render_forward(cam, w.img_size, w.scene.transforms, w.scene.sh_coeffs, w.scene.raw_opacities,
@@ -98,5 +108,23 @@ def test_full_size_parity(cfg, view):
     # linearity in the cotangent: doubling it doubles every raster gradient
     # (exact per term; only the atomic summation order may differ)
     _check_grads(g2.v_combined.cpu().numpy(), 2.0 * vc, "v_combined under a doubled cotangent")
-    _log(f"{cfg}: done")
     out.state.free()
+
+    _log(f"{cfg}: depth cutoff on")
+    ctx.set_depth_cutoff(ctx.CUTOFF_ON)
+    try:
+        cut = va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_depth_cutoff(ctx.CUTOFF_AUTO)
+    gc = gpu_state_arrays(cut)
+    t_count = gc["ranges"].shape[0] * gc["ranges"].shape[1]
+    listed, full = _check_cut_lists(gc, ref, t_count)
+    _log(f"{cfg}: {listed} of {full} pairs listed under the cutoff")
+    del gc
+    assert np.array_equal(cut.out_img.cpu().numpy().view(np.uint32), rimg.view(np.uint32))
+    np.testing.assert_array_equal(_consumed(cut.aux.tile_offsets.cpu().numpy()), _consumed(ref.get(po.F_TILE_OFFSETS_SHRUNK)))
+    gcut = va.render_backward(cut, t, s, o, v_dev)
+    _check_grads(gcut.v_combined.cpu().numpy(), vc, "v_combined (cutoff vs full lists)")
+    cut.state.free()
+    _log(f"{cfg}: done")

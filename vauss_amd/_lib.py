@@ -80,7 +80,8 @@ class VsStateView(C.Structure):
                 ("isect_tiles", C.c_void_p), ("isect_gids", C.c_void_p), ("intersect_counts", C.c_void_p),
                 ("depth_bits", C.c_void_p), ("compact_from_global", C.c_void_p),
                 ("proj_xy_conic", C.c_void_p), ("proj_c11_opac_rg", C.c_void_p), ("proj_b", C.c_void_p),
-                ("proj_aux", C.c_void_p), ("tile_ranges", C.c_void_p), ("proj_surf", C.c_void_p)]
+                ("proj_aux", C.c_void_p), ("tile_ranges", C.c_void_p), ("proj_surf", C.c_void_p),
+                ("listed_intersections", C.c_uint32), ("depth_cutoff", C.c_uint32), ("listed_counts", C.c_void_p)]
 
 
 class VsLossCfg(C.Structure):
@@ -106,6 +107,7 @@ SIGNATURES = {
     "vs_version": (C.c_char_p, []),
     "vs_ctx_set_sort_spin_limit": (C.c_int, [C.c_void_p, C.c_uint32]),
     "vs_ctx_set_validation": (C.c_int, [C.c_void_p, C.c_int]),
+    "vs_ctx_set_depth_cutoff": (C.c_int, [C.c_void_p, C.c_int]),
     "vs_ctx_set_poison": (C.c_int, [C.c_void_p, C.c_int]),
     "vs_ctx_enable_timing": (C.c_int, [C.c_void_p, C.c_uint32]),
     "vs_ctx_stage_times": (C.c_int, [C.c_void_p, C.POINTER(VsStageTimes)]),

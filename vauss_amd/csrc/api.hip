@@ -56,6 +56,7 @@ struct vs_ctx {
     // the unmasked pixel count of the last circular L1 mask (vs_l1_cotangent)
     struct MaskKey { uint32_t w, h; float cx, cy, r; } l1_mask{0, 0, 0.0f, 0.0f, 0.0f};
     uint64_t l1_mask_count = 0;
+    vs_cutoff_mode depth_cutoff = VS_CUTOFF_AUTO;   // vs_ctx_set_depth_cutoff
     bool validate = false;                // scan inputs and gradients for NaN / Inf (vs_ctx_set_validation)
     bool poison = false;                  // fill every library allocation with POISON_WORD first
     uint32_t* dev_val = nullptr;          // device: validation counters, VALIDATE_WORDS per check
@@ -116,6 +117,10 @@ struct vs_fwd_state {
     // the tile sort produced the ranges and skipped the sorted ids: the state
     // view rebuilds them from the ranges
     mutable bool tiles_pending = false;
+    // depth cutoff: the lists' length (device) and each splat's listed pairs
+    bool cutoff = false;
+    uint32_t* listed = nullptr;
+    uint32_t* kept_counts = nullptr;
 };
 
 namespace {
@@ -381,6 +386,14 @@ extern "C" void vs_ctx_destroy(vs_ctx* c) {
 extern "C" vs_status vs_ctx_set_stream(vs_ctx* c, void* hip_stream) {
     if (!c) return fail(VS_ERR_INVALID, "ctx is null");
     c->stream = static_cast<hipStream_t>(hip_stream);
+    return VS_OK;
+}
+
+extern "C" vs_status vs_ctx_set_depth_cutoff(vs_ctx* c, vs_cutoff_mode mode) {
+    if (!c) return fail(VS_ERR_INVALID, "ctx is null");
+    if (mode != VS_CUTOFF_AUTO && mode != VS_CUTOFF_OFF && mode != VS_CUTOFF_ON)
+        return fail(VS_ERR_INVALID, "unknown depth cutoff mode");
+    c->depth_cutoff = mode;
     return VS_OK;
 }
 
@@ -690,6 +703,14 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         i_dev = st->counters + CNT_BOUNDED;
     }
     const uint32_t I = st->I, M = st->M;
+    // Depth cutoff (gaussian modes): per-tile tables of (bh x CUT_BINS x (bw + 1))
+    // u32 masses and u16 prefix counts, at most 256 MiB.
+    const uint64_t cut_words = (uint64_t)st->tbh * CUT_BINS * ((uint64_t)st->tbw + 1u);
+    bool cutoff = false;
+    if (!surfel && N > 0 && I > 0 && st->tbw <= CUT_MAX_BW && cut_words * 6u <= (256ull << 20) &&
+        ctx->depth_cutoff != VS_CUTOFF_OFF)
+        cutoff = ctx->depth_cutoff == VS_CUTOFF_ON || (uint64_t)I >= (uint64_t)CUT_AUTO_PER_TILE * T;
+    st->cutoff = cutoff;
     hipEvent_t sort_done = nullptr;   // exact renders: the sorts' flag readback
     struct EventBack { vs_ctx* c; hipEvent_t& e; ~EventBack() { if (e) c->pool.push_back(e); } } sort_done_back{ctx, sort_done};
 
@@ -703,6 +724,9 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)M * 4);
         const size_t o_base_g = itake((size_t)N * 4);
         const size_t o_scan = itake(scan_lookback_status_words(M) * 4);
+        const size_t o_mass = cutoff ? itake(cut_words * 4) : 0, o_allow = cutoff ? itake(cut_words * 2) : 0;
+        const size_t o_cut = cutoff ? itake(T) : 0, o_kept = cutoff ? itake((size_t)N * 4) : 0;
+        const size_t o_listed = cutoff ? itake(4) : 0;
         const size_t o_tmp = itake(sort_tmp_bytes(std::max(I, M), false));   // serves both sorts
         VS_HIP(lib_alloc(ctx, &st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
         char* ib = static_cast<char*>(st->isect_arena);
@@ -723,6 +747,30 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const SortZeroSpan depth_zero = sort_zero_span(M, 0, depth_bits, ib + o_tmp);
         const SortZeroSpan tile_zero = (M > 0 && N > 0) ? sort_zero_span(I, 0, tile_bits, ib + o_tmp)
                                                          : SortZeroSpan{nullptr, 0};
+        uint32_t* cut_mass = cutoff ? reinterpret_cast<uint32_t*>(ib + o_mass) : nullptr;
+        uint16_t* cut_allow = cutoff ? reinterpret_cast<uint16_t*>(ib + o_allow) : nullptr;
+        uint8_t* cut_tile = cutoff ? reinterpret_cast<uint8_t*>(ib + o_cut) : nullptr;
+        st->kept_counts = cutoff ? reinterpret_cast<uint32_t*>(ib + o_kept) : nullptr;
+        st->listed = cutoff ? reinterpret_cast<uint32_t*>(ib + o_listed) : nullptr;
+        if (cutoff) {
+            // each tile's cutoff bin, then each splat's pairs under it
+            StageTimer tm(ctx, ST_EMIT);
+            CutArgs ka{};
+            ka.num_splats = N; ka.tile_bw = st->tbw; ka.tile_bh = st->tbh;
+            ka.counts = st->counts; ka.depth_bits = st->depth_bits; ka.counters = st->counters;
+            ka.proj_a = st->proj_a; ka.proj_b = st->proj_b;
+            ka.mass = cut_mass; ka.cut = cut_tile; ka.allow = cut_allow;
+            VS_HIP(launch_fill_u32(cut_mass, 0u, cut_words, s), "zero cutoff masses");
+            VS_HIP(launch_cut_mass(ka, s), "cutoff masses");
+            VS_HIP(launch_cut_rows(ka, s), "cutoff bins");
+            EmitArgs ca{};
+            ca.num_splats = N; ca.tile_bw = st->tbw; ca.tile_bh = st->tbh;
+            ca.counts = st->counts; ca.proj_a = st->proj_a; ca.proj_b = st->proj_b;
+            ca.cut = cut_tile; ca.allow = cut_allow; ca.depth_bits = st->depth_bits; ca.counters = st->counters;
+            ca.counts_out = st->kept_counts;
+            VS_HIP(launch_count_kept(ca, s), "cutoff counts");
+        }
+        const uint32_t* slot_counts = cutoff ? st->kept_counts : st->counts;
         {
             StageTimer tm(ctx, ST_EMIT);
             CompactArgs ca{};
@@ -741,22 +789,26 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         }
         {
             StageTimer tm(ctx, ST_EMIT);
-            VS_HIP(scan_u32_lookback(st->counts, slot_base, M, scan_tmp, err, s, ctx->spin_limit, order, m_dev, N,
+            VS_HIP(scan_u32_lookback(slot_counts, slot_base, M, scan_tmp, err, s, ctx->spin_limit, order, m_dev, N,
                                      slot_base_g),
                    "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;
             ea.num_emitters = M; ea.m_dev = m_dev; ea.order = order;
-            ea.counts = st->counts; ea.slot_base = slot_base; ea.slot_base_g = slot_base_g;
+            ea.counts = slot_counts; ea.slot_base = slot_base; ea.slot_base_g = slot_base_g;
             ea.zero = tile_zero.ptr; ea.zero_words = tile_zero.words;      // the tile sort's one-sweep state
             ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u; ea.capacity = I;
+            if (cutoff) {
+                ea.cut = cut_tile; ea.allow = cut_allow; ea.depth_bits = st->depth_bits; ea.counters = st->counters;
+                ea.listed = st->listed;
+            }
             VS_HIP(launch_emit(ea, s), "emit kernel");
         }
         TileRangesOut tro{st->ranges, T, false};   // the tile sort's last pass finds the ranges
         {
             StageTimer tm(ctx, ST_SORT);
-            VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, i_dev, false, 0, tile_bits, ib + o_tmp,
-                                    err, s, ctx->spin_limit, &tro, tile_zero.ptr != nullptr),
+            VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, cutoff ? st->listed : i_dev, false, 0,
+                                    tile_bits, ib + o_tmp, err, s, ctx->spin_limit, &tro, tile_zero.ptr != nullptr),
                    "tile sort");
             st->tiles_pending = tro.done;
         }
@@ -771,7 +823,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         }
         if (!tro.done) {
             StageTimer tm(ctx, ST_RANGES);
-            VS_HIP(launch_tile_ranges(st->tiles, I, T, st->ranges, s, i_dev), "tile ranges");
+            VS_HIP(launch_tile_ranges(st->tiles, I, T, st->ranges, s, cutoff ? st->listed : i_dev), "tile ranges");
         }
     }
 
@@ -1089,6 +1141,17 @@ extern "C" vs_status vs_fwd_state_view(const vs_fwd_state* st, vs_state_view* o)
     o->proj_aux = reinterpret_cast<const float*>(st->proj_aux);
     o->proj_surf = reinterpret_cast<const float*>(st->proj_surf);
     o->tile_ranges = st->ranges;
+    o->listed_intersections = st->I;
+    o->depth_cutoff = st->cutoff ? 1u : 0u;
+    o->listed_counts = st->cutoff ? st->kept_counts : st->counts;
+    if (st->cutoff && st->listed) {
+        vs_ctx* ctx = st->ctx;
+        VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+        uint32_t listed = 0;
+        VS_HIP(hipMemcpyAsync(&listed, st->listed, 4, hipMemcpyDeviceToHost, ctx->stream), "listed count readback");
+        VS_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        o->listed_intersections = std::min(listed, st->I);
+    }
     return VS_OK;
 }
 

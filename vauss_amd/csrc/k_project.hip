@@ -170,6 +170,24 @@ VS_DEV bool chord(double a, double b, double det, double inva, double two_a_p, d
     return true;
 }
 
+// Tiles [ia, ib) of row ty, within [lo, hi), whose corners (widened by
+// BAND_IN) lie inside the ellipse sigma <= P (1 - 4e-3) - 1e-4; ia and ib are
+// left alone when there are none.
+VS_DEV void row_interior(float px, float py, S2 cf, double P, uint32_t ty, uint32_t lo, uint32_t hi, uint32_t& ia,
+                         uint32_t& ib) {
+    const double a = cf.c00, b = cf.c01, c = cf.c11;
+    const double det = a * c - b * b, inva = 1.0 / a;
+    const double mx_ = px, my_ = py;
+    const double p_in = P * 0.996 - 1e-4;
+    if (!(p_in > 0.0)) return;
+    const double e0 = (double)(ty * TILE_W) - my_ - BAND_IN, e1 = e0 + (double)TILE_W + 2.0 * BAND_IN;
+    double l0, r0, l1, r1;
+    if (!chord(a, b, det, inva, 2.0 * a * p_in, e0, l0, r0) || !chord(a, b, det, inva, 2.0 * a * p_in, e1, l1, r1)) return;
+    const double fi = ceil((mx_ + fmax(l0, l1) + BAND_IN) / TILE_W), fj = floor((mx_ + fmin(r0, r1) - BAND_IN) / TILE_W);
+    const double ci = fmin(fmax(fi, (double)lo), (double)hi), cj = fmin(fmax(fj, (double)lo), (double)hi);
+    if (ci < cj) { ia = (uint32_t)ci; ib = (uint32_t)cj; }
+}
+
 // Tile-x ranges of row ty of a splat's box: [oa, ob) may pass, [ia, ib) must.
 VS_DEV void row_ranges(float px, float py, S2 cf, float power, uint4 box, uint32_t ty, uint32_t& oa, uint32_t& ia,
                        uint32_t& ib, uint32_t& ob) {
@@ -193,15 +211,7 @@ VS_DEV void row_ranges(float px, float py, S2 cf, float power, uint4 box, uint32
     oa = (uint32_t)fmin(fmax(fo, (double)x0), (double)x1);
     ob = (uint32_t)fmin(fmax(fe, (double)oa), (double)x1);
     ia = ib = ob;
-    // interior: tiles whose corners (widened by BAND_IN) lie inside the shrunk ellipse
-    const double p_in = P * 0.996 - 1e-4;
-    if (!(p_in > 0.0)) return;
-    const double e0 = (double)(ty * TILE_W) - my_ - BAND_IN, e1 = e0 + (double)TILE_W + 2.0 * BAND_IN;
-    double l0, r0, l1, r1;
-    if (!chord(a, b, det, inva, 2.0 * a * p_in, e0, l0, r0) || !chord(a, b, det, inva, 2.0 * a * p_in, e1, l1, r1)) return;
-    const double fi = ceil((mx_ + fmax(l0, l1) + BAND_IN) / TILE_W), fj = floor((mx_ + fmin(r0, r1) - BAND_IN) / TILE_W);
-    const double ci = fmin(fmax(fi, (double)oa), (double)ob), cj = fmin(fmax(fj, (double)oa), (double)ob);
-    if (ci < cj) { ia = (uint32_t)ci; ib = (uint32_t)cj; }
+    row_interior(px, py, cf, P, ty, oa, ob, ia, ib);
 }
 
 // Whether a conic admits the exact ranges (positive definite, |corr| <= sqrt(0.999)).
@@ -210,18 +220,34 @@ VS_DEV uint32_t ranges_ok(S2 c, float power) {
     return (a > 0.0 && cc > 0.0 && b * b <= 0.999 * a * cc && power >= 0.0f && finite(c) && finite(power)) ? 1u : 0u;
 }
 
+// The depth cutoff's per-tile tables (null cut: no cutoff).
+struct CutFilter {
+    const uint8_t* cut;       // [T] last depth bin the tile keeps
+    const uint16_t* allow;    // [bh][CUT_BINS][bw + 1] tiles before x in row ty keeping bin b
+};
+// Depth bin of raw depth bits in [dmin, dmax]: equal spans of the bits, so
+// about equal ratios of depth (monotone, as the depth order is).
+VS_DEV uint32_t cut_bin(uint32_t dbits, uint32_t dmin, uint32_t dmax) {
+    const uint64_t span = (uint64_t)(dmax - dmin) + 1ull;
+    return (uint32_t)min(((uint64_t)(dbits - dmin) * CUT_BINS) / span, (uint64_t)(CUT_BINS - 1u));
+}
+
 // Walks the boxes of the wavefront (every lane calls it; nb == 0: no box).
 // EMIT: writes each passing tile id (and the global id) into the splat's slot
 // range [word0, word0 + count), at most `count` of them and below `capacity`;
 // otherwise counts them.  On return acc[lane] holds the lane's tiles.
-template <bool EMIT>
+// FILTER: only tiles whose cutoff bin is at least the splat's depth bin
+// (`bin`) count: interior runs by the row's prefix counts of such tiles (the
+// k-th found by bisection when emitting), boundary tiles before their test.
+template <bool EMIT, bool FILTER = false>
 VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf, float power, uint32_t base,
-                      uint32_t gid, uint32_t cnt, uint32_t tile_bw, uint32_t* tiles, uint32_t* vals, uint32_t capacity) {
+                      uint32_t gid, uint32_t cnt, uint32_t tile_bw, uint32_t* tiles, uint32_t* vals, uint32_t capacity,
+                      CutFilter cutf = CutFilter{nullptr, nullptr}, uint32_t bin = 0u) {
     const uint32_t lane = __lane_id();
     L.geo[lane] = make_float4(px, py, cf.c00, cf.c01);
     L.geo2[lane] = make_float2(cf.c11, power);
     L.box[lane] = make_uint4(bb.x0, bb.x1, bb.y0, has ? ranges_ok(cf, power) : 0u);
-    L.word[lane] = make_uint4(base, gid, cnt, 0u);
+    L.word[lane] = make_uint4(base, gid, cnt, bin);
     L.acc[lane] = 0u;
     const uint32_t rows = has ? bb.y1 - bb.y0 : 0u;
     wave_enum(L.mark, rows, [&](const EnumStep& rs) {
@@ -236,14 +262,18 @@ VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf
             ty = bx.z + rs.idx;
             row_ranges(g.x, g.y, oc, g2.y, bx, ty, oa, ia, ib, ob);
         }
-        const uint32_t n_in = ib - ia;
+        uint32_t n_in = ib - ia;
+        if (FILTER && rs.active && n_in) {
+            const uint16_t* ar = cutf.allow + ((size_t)ty * CUT_BINS + L.word[o].w) * (tile_bw + 1u);
+            n_in = (uint32_t)ar[ib] - (uint32_t)ar[ia];
+        }
         uint32_t first_in = 0;
         if (rs.active && n_in) {
             if (EMIT) first_in = atomicAdd(&L.acc[o], n_in);
             else atomicAdd(&L.acc[o], n_in);
         }
         L.row[lane] = make_uint4(o, ty, oa, ia);
-        L.row2[lane] = make_uint4(ib, ob, first_in, 0u);
+        L.row2[lane] = make_uint4(ib, ob, first_in, n_in);
         wave_sync();
         const uint32_t n_bd = rs.active ? (ia - oa) + (ob - ib) : 0u;
         wave_enum(L.mark2, n_bd, [&](const EnumStep& bs) {
@@ -253,7 +283,8 @@ VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf
             const uint32_t tx = bs.idx < left ? rw.z + bs.idx : rw2.x + (bs.idx - left);
             const float4 sg = L.geo[rw.x];
             const float2 sg2 = L.geo2[rw.x];
-            const bool hit = bs.active && will_contribute(tx, rw.y, sg.x, sg.y, S2{sg.z, sg.w, sg2.x}, sg2.y);
+            const bool kept = !FILTER || (bs.active && (uint32_t)cutf.cut[rw.y * tile_bw + tx] >= L.word[rw.x].w);
+            const bool hit = bs.active && kept && will_contribute(tx, rw.y, sg.x, sg.y, S2{sg.z, sg.w, sg2.x}, sg2.y);
             const uint64_t hm = __ballot(hit);
             const uint32_t seg_hits = (uint32_t)__popcll(hm & bs.seg);
             if (!EMIT) {
@@ -279,8 +310,20 @@ VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf
                 const uint4 rw2 = L.row2[is.owner];
                 const uint4 w = L.word[rw.x];
                 const uint32_t k = rw2.z + is.idx;
+                uint32_t tx = rw.w + is.idx;
+                if (FILTER) {
+                    // the idx-th kept tile of [ia, ib): the first x with ar[x + 1] > ar[ia] + idx
+                    const uint16_t* ar = cutf.allow + ((size_t)rw.y * CUT_BINS + w.w) * (tile_bw + 1u);
+                    const uint32_t target = (uint32_t)ar[rw.w] + is.idx;
+                    uint32_t lo = rw.w, hi = rw2.x - 1u;
+                    while (lo < hi) {
+                        const uint32_t mid = (lo + hi) >> 1;
+                        if ((uint32_t)ar[mid + 1u] > target) hi = mid; else lo = mid + 1u;
+                    }
+                    tx = lo;
+                }
                 if (k < w.z && w.x + k < capacity) {
-                    tiles[w.x + k] = rw.w + is.idx + rw.y * tile_bw;
+                    tiles[w.x + k] = tx + rw.y * tile_bw;
                     vals[w.x + k] = w.y;
                 }
             });
@@ -636,6 +679,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) compact_kernel(CompactArgs a) {
 constexpr uint32_t EMIT_SMALL_BOX = 32;
 VS_DEV uint32_t emit_big_blocks(uint32_t n) { return (n + PROJ_BLOCK - 1) / PROJ_BLOCK; }
 
+template <bool FILTER>
 __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     const uint32_t lane = lane_id();
     const uint32_t big_blocks = emit_big_blocks(a.num_splats);
@@ -655,6 +699,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     float px = 0.0f, py = 0.0f, power = 0.0f;
     S2 conic{0.0f, 0.0f, 0.0f};
     TileBox bb{0, 0, 0, 0};
+    uint32_t bin = 0u;
     if (cnt > 0) {
         // Recompute the box from the projected row as kernels/map_gaussians.rs:61-66 does.
         const float4 pa = a.proj_a[g];
@@ -665,6 +710,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
         float ex, ey;
         bbox_extent(conic, power, ex, ey);
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
+        if (FILTER) bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
     }
     const uint32_t nb = (cnt > 0) ? (bb.y1 - bb.y0) * (bb.x1 - bb.x0) : 0u;
     if (big != (nb > EMIT_SMALL_BOX)) cnt = 0u;     // the other kind of block emits it
@@ -672,7 +718,8 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     __shared__ RowLds s_walk[PROJ_BLOCK / 64];
     RowLds& L = s_walk[threadIdx.x / 64];
     // a splat's count bounds its slots; slots past the arena are dropped
-    walk_rows<true>(L, cnt > 0, bb, px, py, conic, power, base, g, cnt, a.tile_bw, a.tiles, a.vals, a.capacity);
+    walk_rows<true, FILTER>(L, cnt > 0, bb, px, py, conic, power, base, g, cnt, a.tile_bw, a.tiles, a.vals, a.capacity,
+                            CutFilter{a.cut, a.allow}, bin);
     const uint32_t emitted = L.acc[lane];
     const uint32_t sentinel = a.tile_bw * a.tile_bh;
     for (uint32_t k = emitted; k < cnt && base + k < a.capacity; ++k) {
@@ -681,6 +728,179 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     }
     for (uint64_t i = (uint64_t)blockIdx.x * PROJ_BLOCK + threadIdx.x; i < a.zero_words; i += (uint64_t)gridDim.x * PROJ_BLOCK)
         a.zero[i] = 0u;
+    // the list's length: the last emitter's slot range ends it
+    if (a.listed && blockIdx.x == 0 && threadIdx.x == 0) {
+        const uint32_t m = a.m_dev ? min(*a.m_dev, a.num_emitters) : a.num_emitters;
+        *a.listed = m ? a.slot_base[m - 1] + a.counts[a.order[m - 1]] : 0u;
+    }
+}
+
+// ---- depth cutoff ---------------------------------------------------------------
+// A splat's alpha at a pixel is min(ALPHA_CAP, opac G) with G = exp(-sigma).
+// Inside its core ellipse sigma <= ln(opac / a_k), a_k = f_k min(opac,
+// ALPHA_CAP) (f = CUT_LEVEL_LO, CUT_LEVEL_HI), every pixel of a tile that
+// row_interior places inside (0.4 % of sigma and 0.05 px to spare against
+// the f32 evaluation) gets alpha >= a_k, and a_k >= CUT_MIN_ALPHA lies above
+// the cutoff band, so a pixel that still runs blends the splat with
+// (1 - alpha) <= (1 - a_k).  Such a tile lists the splat (its core lies inside
+// the footprint the tile test passes).  The fixed-point masses
+// floor(-ln(1 - a_k) CUT_SCALE 0.999) of the cores covering a tile, summed
+// over the depth bins up to b, bound -ln T at every pixel after the tile's
+// splats of bins <= b from below; once they reach CUT_NEED, ln(1 / T_STOP)
+// + 0.25 nats (the margin covers the f32 rounding of T over two million
+// blends), every pixel has stopped by the end of bin b, and splats of later
+// bins are never evaluated there.  The rasterised image, the ranges a
+// forward consumes and everything downstream are those of the full list.
+constexpr float CUT_LEVEL_LO = 0.4f, CUT_LEVEL_HI = 0.8f;
+constexpr float CUT_MIN_ALPHA = 0.01f;
+constexpr uint32_t CUT_NEED = 38750;   // ceil((ln(1e4) + 0.25) * CUT_SCALE)
+
+// Per splat with tiles: the mass of its two cores added to the difference
+// rows of its depth bin, +m at the first interior tile, -m past the last
+// (u32 arithmetic wraps; the prefix sums recover the masses).
+__global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
+    const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+    const uint32_t lane = lane_id();
+    bool has = g < a.num_splats && a.counts[g] > 0u;
+    float px = 0.0f, py = 0.0f, p_lo = 0.0f, p_hi = 0.0f;
+    S2 cf{0.0f, 0.0f, 0.0f};
+    uint32_t m_lo = 0u, m_hi = 0u, bin = 0u;
+    TileBox bb{0, 0, 0, 0};
+    if (has) {
+        const float4 pa = a.proj_a[g];
+        const float4 pb = a.proj_b[g];
+        px = pa.x; py = pa.y;
+        cf = S2{pa.z, pa.w, pb.x};
+        const float opac = pb.y, a0 = __builtin_fminf(opac, ALPHA_CAP);
+        const float alo = CUT_LEVEL_LO * a0, ahi = CUT_LEVEL_HI * a0;
+        p_lo = logf_c(opac / alo);
+        p_hi = logf_c(opac / ahi);
+        const float fm_lo = floorf(-logf_c(1.0f - alo) * (CUT_SCALE * 0.999f));
+        const float fm_hi = floorf(-logf_c(1.0f - ahi) * (CUT_SCALE * 0.999f));
+        has = alo >= CUT_MIN_ALPHA && p_lo > 0.0f && p_hi > 0.0f && ranges_ok(cf, p_lo) && fm_lo >= 0.0f &&
+              fm_hi >= fm_lo && fm_hi < 1.0e6f;
+        if (has) {
+            m_lo = (uint32_t)fm_lo;
+            m_hi = (uint32_t)fm_hi;
+            float ex, ey;
+            bbox_extent(cf, p_lo, ex, ey);
+            bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
+            bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
+        }
+    }
+    __shared__ RowLds s_walk[PROJ_BLOCK / 64];
+    RowLds& L = s_walk[threadIdx.x / 64];
+    L.geo[lane] = make_float4(px, py, cf.c00, cf.c01);
+    L.geo2[lane] = make_float2(cf.c11, p_lo);
+    L.box[lane] = make_uint4(bb.x0, bb.x1, bb.y0, __float_as_uint(p_hi));
+    L.word[lane] = make_uint4(m_lo, m_hi - m_lo, bin, 0u);
+    const uint32_t rows = has ? bb.y1 - bb.y0 : 0u;
+    wave_enum(L.mark, rows, [&](const EnumStep& rs) {
+        if (!rs.active) return;
+        const uint32_t o = rs.owner;
+        const float4 g4 = L.geo[o];
+        const float2 g2 = L.geo2[o];
+        const uint4 bx = L.box[o];
+        const uint4 w = L.word[o];
+        const S2 oc{g4.z, g4.w, g2.x};
+        const uint32_t ty = bx.z + rs.idx;
+        uint32_t* row = a.mass + ((size_t)ty * CUT_BINS + w.z) * (a.tile_bw + 1u);
+        uint32_t ia = bx.y, ib = bx.y;
+        row_interior(g4.x, g4.y, oc, g2.y, ty, bx.x, bx.y, ia, ib);
+        if (ia < ib) {
+            atomicAdd(&row[ia], w.x);
+            atomicAdd(&row[ib], 0u - w.x);
+            uint32_t ja = ib, jb = ib;   // the inner core lies inside the outer one
+            row_interior(g4.x, g4.y, oc, __uint_as_float(bx.w), ty, ia, ib, ja, jb);
+            if (ja < jb && w.y) {
+                atomicAdd(&row[ja], w.y);
+                atomicAdd(&row[jb], 0u - w.y);
+            }
+        }
+    });
+}
+
+// One workgroup per tile row: the masses per (bin, tile) by prefix sums of
+// the differences (in place), each tile's cutoff bin (the first whose
+// cumulative mass reaches CUT_NEED; the last bin when none does), and per
+// bin the prefix counts of the row's tiles that keep it.
+constexpr int CUT_ROW_BLOCK = 256;
+__global__ void __launch_bounds__(CUT_ROW_BLOCK) cut_rows_kernel(CutArgs a) {
+    __shared__ uint8_t s_cut[CUT_MAX_BW];
+    const uint32_t ty = blockIdx.x, bw = a.tile_bw, lane = lane_id(), wave = threadIdx.x / 64;
+    const size_t w1 = (size_t)bw + 1u;
+    uint32_t* mrow = a.mass + (size_t)ty * CUT_BINS * w1;
+    for (uint32_t b = wave; b < CUT_BINS; b += CUT_ROW_BLOCK / 64) {
+        uint32_t* r = mrow + b * w1;
+        uint32_t carry = 0u;
+        for (uint32_t x0 = 0; x0 < bw; x0 += 64) {
+            const uint32_t x = x0 + lane;
+            uint32_t v = x < bw ? r[x] : 0u;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_up(v, o);
+                if ((int)lane >= o) v += t;
+            }
+            if (x < bw) r[x] = v + carry;
+            carry += (uint32_t)__shfl((int)v, 63);
+        }
+    }
+    __syncthreads();
+    for (uint32_t x = threadIdx.x; x < bw; x += CUT_ROW_BLOCK) {
+        uint64_t cum = 0;
+        uint32_t c = CUT_BINS - 1u;
+        for (uint32_t b = 0; b < CUT_BINS; ++b) {
+            cum += mrow[b * w1 + x];
+            if (cum >= CUT_NEED) { c = b; break; }
+        }
+        s_cut[x] = (uint8_t)c;
+        a.cut[(size_t)ty * bw + x] = (uint8_t)c;
+    }
+    __syncthreads();
+    for (uint32_t b = wave; b < CUT_BINS; b += CUT_ROW_BLOCK / 64) {
+        uint16_t* r = a.allow + ((size_t)ty * CUT_BINS + b) * w1;
+        uint32_t carry = 0u;
+        for (uint32_t x0 = 0; x0 < bw; x0 += 64) {
+            const uint32_t x = x0 + lane;
+            const uint32_t k = (x < bw && (uint32_t)s_cut[x] >= b) ? 1u : 0u;
+            uint32_t v = k;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_up(v, o);
+                if ((int)lane >= o) v += t;
+            }
+            if (x < bw) r[x] = (uint16_t)(carry + v - k);
+            carry += (uint32_t)__shfl((int)v, 63);
+        }
+        if (lane == 0) r[bw] = (uint16_t)carry;
+    }
+}
+
+// Per splat with tiles: the tiles it keeps under the cutoff (the emission's walk).
+__global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
+    const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t cnt = (g < a.num_splats) ? a.counts[g] : 0u;
+    float px = 0.0f, py = 0.0f, power = 0.0f;
+    S2 conic{0.0f, 0.0f, 0.0f};
+    TileBox bb{0, 0, 0, 0};
+    uint32_t bin = 0u;
+    if (cnt > 0) {
+        const float4 pa = a.proj_a[g];
+        const float4 pb = a.proj_b[g];
+        px = pa.x; py = pa.y;
+        conic = S2{pa.z, pa.w, pb.x};
+        power = logf_c(pb.y * 255.0f);
+        float ex, ey;
+        bbox_extent(conic, power, ex, ey);
+        bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
+        bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
+    }
+    __shared__ RowLds s_walk[PROJ_BLOCK / 64];
+    RowLds& L = s_walk[threadIdx.x / 64];
+    walk_rows<false, true>(L, cnt > 0, bb, px, py, conic, power, 0u, 0u, 0u, a.tile_bw, nullptr, nullptr, 0u,
+                           CutFilter{a.cut, a.allow}, bin);
+    if (g < a.num_splats) a.counts_out[g] = L.acc[lane];
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n) {
@@ -752,7 +972,26 @@ hipError_t launch_compact(const CompactArgs& a, hipStream_t s) {
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s) {
     if (a.num_emitters == 0 || a.num_splats == 0) return hipSuccess;
     const uint32_t big_blocks = (a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK;   // emit_big_blocks
-    emit_kernel<<<big_blocks + (a.num_emitters + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
+    const uint32_t grid = big_blocks + (a.num_emitters + PROJ_BLOCK - 1) / PROJ_BLOCK;
+    if (a.cut) emit_kernel<true><<<grid, PROJ_BLOCK, 0, s>>>(a);
+    else emit_kernel<false><<<grid, PROJ_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_cut_mass(const CutArgs& a, hipStream_t s) {
+    if (a.num_splats == 0) return hipSuccess;
+    cut_mass_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+hipError_t launch_cut_rows(const CutArgs& a, hipStream_t s) {
+    if (a.tile_bh == 0 || a.tile_bw == 0) return hipSuccess;
+    if (a.tile_bw > CUT_MAX_BW) return hipErrorInvalidValue;
+    cut_rows_kernel<<<a.tile_bh, CUT_ROW_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+hipError_t launch_count_kept(const EmitArgs& a, hipStream_t s) {
+    if (a.num_splats == 0) return hipSuccess;
+    count_kept_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
 

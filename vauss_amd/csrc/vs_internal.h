@@ -94,6 +94,33 @@ struct EmitArgs {
     uint32_t capacity;               // slots at or past it are dropped (the farthest splats' pairs)
     uint32_t* zero;                  // [zero_words] cleared (the tile sort's one-sweep state), or null
     uint64_t zero_words;
+    // depth cutoff (null cut: every tile keeps every splat)
+    const uint8_t* cut;              // [T] last depth bin each tile keeps
+    const uint16_t* allow;           // [bh][CUT_BINS][bw + 1] tiles before x in row ty keeping bin b
+    const uint32_t* depth_bits;      // [N] raw depth bits (the splat's bin)
+    const uint32_t* counters;        // the projection's counters (depth range)
+    uint32_t* counts_out;            // count pass: [N] tiles kept per splat
+    uint32_t* listed;                // emission: the list's length (slots the scan handed out), or null
+};
+
+// Depth cutoff: a lower bound on the opacity that splats of each depth bin
+// lay over the whole of a tile gives the bin by which every pixel of the tile
+// has reached the raster's stopping transmittance; later bins never reach
+// the tile's pixels and are not listed for it.
+constexpr uint32_t CUT_BINS = 64;         // depth bins, equal spans of the raw depth bits
+constexpr float CUT_SCALE = 4096.0f;      // fixed-point units per nat of -ln(1 - alpha)
+constexpr uint32_t CUT_MAX_BW = 4096;     // tile columns the row kernel holds in LDS
+constexpr uint32_t CUT_AUTO_PER_TILE = 2048;   // VS_CUTOFF_AUTO: listed pairs per tile that turn it on
+struct CutArgs {
+    uint32_t num_splats, tile_bw, tile_bh;
+    const uint32_t* counts;          // [N] tiles per splat (0: not listed anywhere)
+    const uint32_t* depth_bits;      // [N]
+    const uint32_t* counters;        // depth range
+    const float4* proj_a;
+    const float4* proj_b;
+    uint32_t* mass;                  // [bh][CUT_BINS][bw + 1] fixed-point mass differences along each row
+    uint8_t* cut;                    // [T]
+    uint16_t* allow;                 // [bh][CUT_BINS][bw + 1]
 };
 
 struct RasterArgs {
@@ -252,6 +279,12 @@ hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint3
                                   hipStream_t s, uint32_t* host_copy = nullptr);
 hipError_t launch_compact(const CompactArgs& a, hipStream_t s);
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
+// Depth cutoff: the opacity mass of every splat's core (mass zeroed by the
+// caller), each tile's cutoff bin and the rows' kept-tile prefix counts, then
+// each splat's kept tiles (EmitArgs: counts = the projection's, counts_out).
+hipError_t launch_cut_mass(const CutArgs& a, hipStream_t s);
+hipError_t launch_cut_rows(const CutArgs& a, hipStream_t s);
+hipError_t launch_count_kept(const EmitArgs& a, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
 

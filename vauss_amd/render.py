@@ -131,6 +131,15 @@ class Context:
         _lib.check(self.lib.vs_ctx_set_validation(self.handle, 1 if on else 0))
         self.validation = bool(on)
 
+    CUTOFF_AUTO, CUTOFF_OFF, CUTOFF_ON = 0, 1, 2
+
+    def set_depth_cutoff(self, mode: int) -> None:
+        """Depth cutoff of the tile lists (vs_ctx_set_depth_cutoff): CUTOFF_AUTO
+        (the default: renders listing at least 2048 pairs per tile), CUTOFF_OFF
+        or CUTOFF_ON (every gaussian render).  Images and gradients are the
+        full list's either way."""
+        _lib.check(self.lib.vs_ctx_set_depth_cutoff(self.handle, int(mode)))
+
     def set_poison(self, on: bool = True) -> None:
         """Fill every library allocation with -12345.0 before first use (a debug aid)."""
         _lib.check(self.lib.vs_ctx_set_poison(self.handle, 1 if on else 0))
