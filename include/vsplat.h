@@ -243,7 +243,7 @@ vs_status vs_ctx_set_validation(vs_ctx* ctx, int enable);
 /* Depth cutoff for renders whose tiles are listed far more splats than
  * their pixels can blend (no reference counterpart: the reference lists and
  * sorts every intersection).  From the opacity each splat lays over the
- * whole of a tile (its cores at 0.4 and 0.8 of its opacity), a tile's list
+ * whole of a tile (its core at half its opacity), a tile's list
  * stops at the depth bin (64 bins over the frame's depth range) by which
  * every pixel of the tile has provably reached the raster's stopping
  * transmittance; the splats it drops are never evaluated there, so images,

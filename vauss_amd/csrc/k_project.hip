@@ -257,16 +257,17 @@ VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf
         const float4 g = L.geo[o];
         const float2 g2 = L.geo2[o];
         const S2 oc{g.z, g.w, g2.x};
+        const uint16_t* ar = nullptr;   // FILTER: the row's prefix counts of tiles keeping the splat's bin
         if (rs.active) {
             const uint4 bx = L.box[o];
             ty = bx.z + rs.idx;
-            row_ranges(g.x, g.y, oc, g2.y, bx, ty, oa, ia, ib, ob);
+            if (FILTER) ar = cutf.allow + ((size_t)ty * CUT_BINS + L.word[o].w) * (tile_bw + 1u);
+            // a row of the box without such a tile is skipped whole
+            if (!FILTER || ar[bx.y] != ar[bx.x]) row_ranges(g.x, g.y, oc, g2.y, bx, ty, oa, ia, ib, ob);
+            if (FILTER && ar[ob] == ar[oa]) oa = ia = ib = ob;
         }
         uint32_t n_in = ib - ia;
-        if (FILTER && rs.active && n_in) {
-            const uint16_t* ar = cutf.allow + ((size_t)ty * CUT_BINS + L.word[o].w) * (tile_bw + 1u);
-            n_in = (uint32_t)ar[ib] - (uint32_t)ar[ia];
-        }
+        if (FILTER && rs.active && n_in) n_in = (uint32_t)ar[ib] - (uint32_t)ar[ia];
         uint32_t first_in = 0;
         if (rs.active && n_in) {
             if (EMIT) first_in = atomicAdd(&L.acc[o], n_in);
@@ -737,53 +738,49 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
 
 // ---- depth cutoff ---------------------------------------------------------------
 // A splat's alpha at a pixel is min(ALPHA_CAP, opac G) with G = exp(-sigma).
-// Inside its core ellipse sigma <= ln(opac / a_k), a_k = f_k min(opac,
-// ALPHA_CAP) (f = CUT_LEVEL_LO, CUT_LEVEL_HI), every pixel of a tile that
-// row_interior places inside (0.4 % of sigma and 0.05 px to spare against
-// the f32 evaluation) gets alpha >= a_k, and a_k >= CUT_MIN_ALPHA lies above
-// the cutoff band, so a pixel that still runs blends the splat with
-// (1 - alpha) <= (1 - a_k).  Such a tile lists the splat (its core lies inside
-// the footprint the tile test passes).  The fixed-point masses
-// floor(-ln(1 - a_k) CUT_SCALE 0.999) of the cores covering a tile, summed
+// Inside its core ellipse sigma <= ln(opac / a), a = CUT_LEVEL min(opac,
+// ALPHA_CAP), every pixel of a tile that row_interior places inside (0.4 %
+// of sigma and 0.05 px to spare against the f32 evaluation) gets alpha >= a,
+// and a >= CUT_MIN_ALPHA lies above the cutoff band, so a pixel that still
+// runs blends the splat with (1 - alpha) <= (1 - a).  Such a tile lists the
+// splat (its core lies inside the footprint the tile test passes).  The
+// fixed-point masses floor(-ln(1 - a) CUT_SCALE 0.999) of the cores covering a tile, summed
 // over the depth bins up to b, bound -ln T at every pixel after the tile's
 // splats of bins <= b from below; once they reach CUT_NEED, ln(1 / T_STOP)
 // + 0.25 nats (the margin covers the f32 rounding of T over two million
 // blends), every pixel has stopped by the end of bin b, and splats of later
 // bins are never evaluated there.  The rasterised image, the ranges a
 // forward consumes and everything downstream are those of the full list.
-constexpr float CUT_LEVEL_LO = 0.4f, CUT_LEVEL_HI = 0.8f;
+constexpr float CUT_LEVEL = 0.5f;
 constexpr float CUT_MIN_ALPHA = 0.01f;
 constexpr uint32_t CUT_NEED = 38750;   // ceil((ln(1e4) + 0.25) * CUT_SCALE)
 
-// Per splat with tiles: the mass of its two cores added to the difference
-// rows of its depth bin, +m at the first interior tile, -m past the last
-// (u32 arithmetic wraps; the prefix sums recover the masses).
+// Per splat with tiles: the mass of its core added to the difference rows of
+// its depth bin, +m at the first interior tile, -m past the last (u32
+// arithmetic wraps; the prefix sums recover the masses; the row's entry bw
+// is never read).  A core narrower than a tile covers none.
 __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
     const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
     const uint32_t lane = lane_id();
     bool has = g < a.num_splats && a.counts[g] > 0u;
-    float px = 0.0f, py = 0.0f, p_lo = 0.0f, p_hi = 0.0f;
+    float px = 0.0f, py = 0.0f, pc = 0.0f;
     S2 cf{0.0f, 0.0f, 0.0f};
-    uint32_t m_lo = 0u, m_hi = 0u, bin = 0u;
+    uint32_t m = 0u, bin = 0u;
     TileBox bb{0, 0, 0, 0};
     if (has) {
         const float4 pa = a.proj_a[g];
         const float4 pb = a.proj_b[g];
         px = pa.x; py = pa.y;
         cf = S2{pa.z, pa.w, pb.x};
-        const float opac = pb.y, a0 = __builtin_fminf(opac, ALPHA_CAP);
-        const float alo = CUT_LEVEL_LO * a0, ahi = CUT_LEVEL_HI * a0;
-        p_lo = logf_c(opac / alo);
-        p_hi = logf_c(opac / ahi);
-        const float fm_lo = floorf(-logf_c(1.0f - alo) * (CUT_SCALE * 0.999f));
-        const float fm_hi = floorf(-logf_c(1.0f - ahi) * (CUT_SCALE * 0.999f));
-        has = alo >= CUT_MIN_ALPHA && p_lo > 0.0f && p_hi > 0.0f && ranges_ok(cf, p_lo) && fm_lo >= 0.0f &&
-              fm_hi >= fm_lo && fm_hi < 1.0e6f;
+        const float opac = pb.y, ac = CUT_LEVEL * __builtin_fminf(opac, ALPHA_CAP);
+        pc = logf_c(opac / ac);
+        const float fm = floorf(-logf_c(1.0f - ac) * (CUT_SCALE * 0.999f));
+        has = ac >= CUT_MIN_ALPHA && pc > 0.0f && ranges_ok(cf, pc) && fm >= 1.0f && fm < 1.0e6f;
         if (has) {
-            m_lo = (uint32_t)fm_lo;
-            m_hi = (uint32_t)fm_hi;
+            m = (uint32_t)fm;
             float ex, ey;
-            bbox_extent(cf, p_lo, ex, ey);
+            bbox_extent(cf, pc, ex, ey);
+            has = ex >= 0.5f * TILE_W && ey >= 0.5f * TILE_W;
             bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
             bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
         }
@@ -791,9 +788,9 @@ __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
     __shared__ RowLds s_walk[PROJ_BLOCK / 64];
     RowLds& L = s_walk[threadIdx.x / 64];
     L.geo[lane] = make_float4(px, py, cf.c00, cf.c01);
-    L.geo2[lane] = make_float2(cf.c11, p_lo);
-    L.box[lane] = make_uint4(bb.x0, bb.x1, bb.y0, __float_as_uint(p_hi));
-    L.word[lane] = make_uint4(m_lo, m_hi - m_lo, bin, 0u);
+    L.geo2[lane] = make_float2(cf.c11, pc);
+    L.box[lane] = make_uint4(bb.x0, bb.x1, bb.y0, 0u);
+    L.word[lane] = make_uint4(m, bin, 0u, 0u);
     const uint32_t rows = has ? bb.y1 - bb.y0 : 0u;
     wave_enum(L.mark, rows, [&](const EnumStep& rs) {
         if (!rs.active) return;
@@ -802,20 +799,13 @@ __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
         const float2 g2 = L.geo2[o];
         const uint4 bx = L.box[o];
         const uint4 w = L.word[o];
-        const S2 oc{g4.z, g4.w, g2.x};
         const uint32_t ty = bx.z + rs.idx;
-        uint32_t* row = a.mass + ((size_t)ty * CUT_BINS + w.z) * (a.tile_bw + 1u);
         uint32_t ia = bx.y, ib = bx.y;
-        row_interior(g4.x, g4.y, oc, g2.y, ty, bx.x, bx.y, ia, ib);
+        row_interior(g4.x, g4.y, S2{g4.z, g4.w, g2.x}, g2.y, ty, bx.x, bx.y, ia, ib);
         if (ia < ib) {
+            uint32_t* row = a.mass + ((size_t)ty * CUT_BINS + w.y) * (a.tile_bw + 1u);
             atomicAdd(&row[ia], w.x);
-            atomicAdd(&row[ib], 0u - w.x);
-            uint32_t ja = ib, jb = ib;   // the inner core lies inside the outer one
-            row_interior(g4.x, g4.y, oc, __uint_as_float(bx.w), ty, ia, ib, ja, jb);
-            if (ja < jb && w.y) {
-                atomicAdd(&row[ja], w.y);
-                atomicAdd(&row[jb], 0u - w.y);
-            }
+            if (ib < a.tile_bw) atomicAdd(&row[ib], 0u - w.x);
         }
     });
 }
