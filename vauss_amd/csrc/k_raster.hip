@@ -867,73 +867,74 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             // the projection's logf(opac / (1/255 - 5e-4)) + 1e-3: alpha is below the cutoff band beyond it
             const float sigma_max = m3.z;
             const uint32_t isect = start + t;
+            // the replayed forward: which lanes blend this splat (every field of the
+            // hit is computed, so the gradient below runs on every lane and one
+            // select per component keeps the blending lanes' values)
+            const SurfelHit h = surfel_hit<false>(m0, m1, m2, m3.z, pcx, pcy);
+            const float G = exp2n(-(h.sigma * LOG2E_F));
+            const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);
+            const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
+            const float ae = alpha * w_cut;
+            const float nt = T * (1.0f - ae);
+            const bool blend = T > T_STOP && h.valid && h.sigma <= sigma_max && h.sigma >= 0.0f && w_cut > 0.0f;
+            const bool stop = blend && nt <= T_STOP;
+            const bool contrib = blend && !stop;
+            if (stop) T = 0.0f;
+            if (__ballot(contrib) == 0ull) continue;          // uniform: no lane blends it
+            const float z = h.z;
+            const float m = dist_depth(z);
+            // gradient-only quotients and roots take the hardware reciprocal and
+            // square root (1 ulp); the replayed forward above keeps IEEE division
+            const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
+            const float Tk = T;
+            const float vis = ae * Tk;
             float gs[SURFEL_GRADS];
+            gs[12] = (col_r >= 0.0f) ? vis * vr : 0.0f;
+            gs[13] = (col_g >= 0.0f) ? vis * vg : 0.0f;
+            gs[14] = (col_b >= 0.0f) ? vis * vb : 0.0f;
+            gs[9] = vis * vnx;
+            gs[10] = vis * vny;
+            gs[11] = vis * vnz;
+            const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
+            const float dot_ = ((Tk * cl_r - sr) * vr + (Tk * cl_g - sg) * vg + (Tk * cl_b - sb) * vb +
+                                (Tk * z - sz) * vz + (Tk * nrm_x - snx) * vnx +
+                                (Tk * nrm_y - sny) * vny + (Tk * nrm_z - snz) * vnz +
+                                (Tk * m - sdb) * vdb + (Tk * m * m - sdc) * vdc) * ra;
+            const float v_ae = dot_ + vt * ra;
+            const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+            const float v_z = vis * (vz + (vdb + 2.0f * m * vdc) * dm_dz) + ((isect == med) ? vmed : 0.0f);
+            const bool unsat = opac * G <= ALPHA_CAP;
+            const float v_sigma = unsat ? -alpha * v_alpha : 0.0f;
+            gs[15] = unsat ? v_alpha * G : 0.0f;
+            const bool use_3d = h.s3d <= h.s2d;
+            const float v_su = (use_3d ? v_sigma * h.su : 0.0f) + v_z * r2x;
+            const float v_sv = (use_3d ? v_sigma * h.sv : 0.0f) + v_z * r2y;
+            const float v_cx = use_3d ? 0.0f : -2.0f * v_sigma * h.dxs;
+            const float v_cy = use_3d ? 0.0f : -2.0f * v_sigma * h.dys;
+            const float inv_qz = __builtin_amdgcn_rcpf(h.qz);
+            const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * h.su + v_sv * h.sv) * inv_qz;
+            // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
+            const float vhux = h.hvy * vqz - h.hvz * vqy, vhuy = h.hvz * vqx - h.hvx * vqz, vhuz = h.hvx * vqy - h.hvy * vqx;
+            const float vhvx = vqy * h.huz - vqz * h.huy, vhvy = vqz * h.hux - vqx * h.huz, vhvz = vqx * h.huy - vqy * h.hux;
+            const float g0 = vhux, g1 = vhuy, g2 = vhuz + v_cx * inv_r2z;
+            const float g3 = vhvx, g4 = vhvy, g5 = vhvz + v_cy * inv_r2z;
+            gs[0] = g0; gs[1] = g1; gs[2] = g2; gs[3] = g3; gs[4] = g4; gs[5] = g5;
+            gs[6] = v_z * h.su - pcx * vhux - pcy * vhvx;
+            gs[7] = v_z * h.sv - pcx * vhuy - pcy * vhvy;
+            gs[8] = v_z - pcx * vhuz - pcy * vhvz - (v_cx * cen_x + v_cy * cen_y) * inv_r2z;
+            // refine weight: this pixel's gradient of a screen-space shift of the surfel (M -> T M)
+            const float shx = g0 * r2x + g1 * r2y + g2 * r2z;
+            const float shy = g3 * r2x + g4 * r2y + g5 * r2z;
+            const float ux = shx * img_w, uy = shy * img_h;
+            gs[16] = __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale;
 #pragma unroll
-            for (int i = 0; i < SURFEL_GRADS; ++i) gs[i] = 0.0f;
-            bool contrib = false;
-            do {
-                if (!(T > T_STOP)) break;
-                const SurfelHit h = surfel_hit(m0, m1, m2, m3.z, pcx, pcy);
-                if (!(h.valid && h.sigma <= sigma_max)) break;
-                const float G = exp2n(-(h.sigma * LOG2E_F));
-                const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);
-                const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
-                if (!(h.sigma >= 0.0f && w_cut > 0.0f)) break;
-                const float ae = alpha * w_cut;
-                const float nt = T * (1.0f - ae);
-                if (nt <= T_STOP) { T = 0.0f; break; }
-                contrib = true;
-                const float z = h.z;
-                const float m = dist_depth(z);
-                // gradient-only quotients and roots take the hardware reciprocal and
-                // square root (1 ulp); the replayed forward above keeps IEEE division
-                const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
-                const float Tk = T;
-                const float vis = ae * Tk;
-                gs[12] += (col_r >= 0.0f) ? vis * vr : 0.0f;
-                gs[13] += (col_g >= 0.0f) ? vis * vg : 0.0f;
-                gs[14] += (col_b >= 0.0f) ? vis * vb : 0.0f;
-                gs[9] += vis * vnx;
-                gs[10] += vis * vny;
-                gs[11] += vis * vnz;
-                const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
-                const float dot_ = ((Tk * cl_r - sr) * vr + (Tk * cl_g - sg) * vg + (Tk * cl_b - sb) * vb +
-                                    (Tk * z - sz) * vz + (Tk * nrm_x - snx) * vnx +
-                                    (Tk * nrm_y - sny) * vny + (Tk * nrm_z - snz) * vnz +
-                                    (Tk * m - sdb) * vdb + (Tk * m * m - sdc) * vdc) * ra;
-                const float v_ae = dot_ + vt * ra;
-                const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
-                const float v_z = vis * (vz + (vdb + 2.0f * m * vdc) * dm_dz) + ((isect == med) ? vmed : 0.0f);
-                const bool unsat = opac * G <= ALPHA_CAP;
-                const float v_sigma = unsat ? -alpha * v_alpha : 0.0f;
-                if (unsat) gs[15] += v_alpha * G;
-                const bool use_3d = h.s3d <= h.s2d;
-                const float v_su = (use_3d ? v_sigma * h.su : 0.0f) + v_z * r2x;
-                const float v_sv = (use_3d ? v_sigma * h.sv : 0.0f) + v_z * r2y;
-                const float v_cx = use_3d ? 0.0f : -2.0f * v_sigma * h.dxs;
-                const float v_cy = use_3d ? 0.0f : -2.0f * v_sigma * h.dys;
-                const float inv_qz = __builtin_amdgcn_rcpf(h.qz);
-                const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * h.su + v_sv * h.sv) * inv_qz;
-                // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
-                const float vhux = h.hvy * vqz - h.hvz * vqy, vhuy = h.hvz * vqx - h.hvx * vqz, vhuz = h.hvx * vqy - h.hvy * vqx;
-                const float vhvx = vqy * h.huz - vqz * h.huy, vhvy = vqz * h.hux - vqx * h.huz, vhvz = vqx * h.huy - vqy * h.hux;
-                const float g0 = vhux, g1 = vhuy, g2 = vhuz + v_cx * inv_r2z;
-                const float g3 = vhvx, g4 = vhvy, g5 = vhvz + v_cy * inv_r2z;
-                gs[0] += g0; gs[1] += g1; gs[2] += g2; gs[3] += g3; gs[4] += g4; gs[5] += g5;
-                gs[6] += v_z * h.su - pcx * vhux - pcy * vhvx;
-                gs[7] += v_z * h.sv - pcx * vhuy - pcy * vhvy;
-                gs[8] += v_z - pcx * vhuz - pcy * vhvz - (v_cx * cen_x + v_cy * cen_y) * inv_r2z;
-                // refine weight: this pixel's gradient of a screen-space shift of the surfel (M -> T M)
-                const float shx = g0 * r2x + g1 * r2y + g2 * r2z;
-                const float shy = g3 * r2x + g4 * r2y + g5 * r2z;
-                const float ux = shx * img_w, uy = shy * img_h;
-                gs[16] += __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale;
+            for (int i = 0; i < SURFEL_GRADS; ++i) gs[i] = contrib ? gs[i] : 0.0f;
+            if (contrib) {
                 sr -= vis * cl_r; sg -= vis * cl_g; sb -= vis * cl_b;
                 sz -= vis * z; snx -= vis * nrm_x; sny -= vis * nrm_y; snz -= vis * nrm_z;
                 sdb -= vis * m; sdc -= vis * m * m;
                 T = nt;
-            } while (false);
-            if (__ballot(contrib) == 0ull) continue;          // uniform: gs is zero in every lane
+            }
             const float mine = reduce_scatter17(gs, lane);
             if (comp >= 0 && mine != 0.0f) atomicAdd(&s_acc[t * SURFEL_GRADS + comp], mine);
         }

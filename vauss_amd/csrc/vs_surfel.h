@@ -77,6 +77,10 @@ VS_DEV F3 surfel_normal(Qt q, F3 mc, const vs_camera& u) {
 // form) comes back invalid before the divisions: such a pair has alpha below
 // every cutoff, so skipping it changes no result.
 struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
+// EARLY: a pixel far outside both the plane disk and the low-pass disk
+// returns at once (invalid, the other fields unset); otherwise every field is
+// computed and such a pixel is marked invalid all the same.
+template <bool EARLY = true>
 VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float px, float py) {
     SurfelHit h;
     const float m20 = m1.z, m21 = m1.w, m22 = m2.x;
@@ -89,13 +93,14 @@ VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float p
     h.dys = py - m2.z;
     h.s2d = 2.0f * (h.dxs * h.dxs + h.dys * h.dys);
     h.valid = false;
-    if (0.5f * h.s2d > smax && qx * qx + qy * qy > (2.0004f * smax) * (h.qz * h.qz)) return h;
+    const bool far = 0.5f * h.s2d > smax && qx * qx + qy * qy > (2.0004f * smax) * (h.qz * h.qz);
+    if (EARLY && far) return h;
     h.su = qx / h.qz;
     h.sv = qy / h.qz;
     h.s3d = h.su * h.su + h.sv * h.sv;
     h.z = m20 * h.su + m21 * h.sv + m22;
     h.sigma = 0.5f * mn(h.s3d, h.s2d);
-    h.valid = finite(h.z) && h.z >= SURFEL_NEAR;
+    h.valid = !far && finite(h.z) && h.z >= SURFEL_NEAR;
     return h;
 }
 
