@@ -824,6 +824,9 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
         med = as_u(o2.w);
         vz = v1.x; vmed = v1.y; vnx = v1.z; vny = v1.w; vnz = v2.x; vdb = v2.y; vdc = v2.z;
     }
+    // S.v: the channels still to come behind the current splat, dotted with the
+    // cotangent (the only use of those sums); each blend takes vis (c.v) off it
+    float sv_rest = sr * vr + sg * vg + sb * vb + sz * vz + snx * vnx + sny * vny + snz * vnz + sdb * vdb + sdc * vdc;
     const int comp = (lane & 1u) ? -1 : scatter_component17(lane);   // the gradient component this lane adds
     for (uint32_t i = threadIdx.x; i < BWD_BATCH * SURFEL_GRADS; i += SURF_BWD_BLOCK) s_acc[i] = 0.0f;
 
@@ -896,10 +899,10 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             gs[10] = vis * vny;
             gs[11] = vis * vnz;
             const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
-            const float dot_ = ((Tk * cl_r - sr) * vr + (Tk * cl_g - sg) * vg + (Tk * cl_b - sb) * vb +
-                                (Tk * z - sz) * vz + (Tk * nrm_x - snx) * vnx +
-                                (Tk * nrm_y - sny) * vny + (Tk * nrm_z - snz) * vnz +
-                                (Tk * m - sdb) * vdb + (Tk * m * m - sdc) * vdc) * ra;
+            // this splat's channels at the pixel, dotted with the cotangent
+            const float cv = cl_r * vr + cl_g * vg + cl_b * vb + z * vz + nrm_x * vnx + nrm_y * vny + nrm_z * vnz +
+                             m * vdb + (m * m) * vdc;
+            const float dot_ = (Tk * cv - sv_rest) * ra;
             const float v_ae = dot_ + vt * ra;
             const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
             const float v_z = vis * (vz + (vdb + 2.0f * m * vdc) * dm_dz) + ((isect == med) ? vmed : 0.0f);
@@ -930,9 +933,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
 #pragma unroll
             for (int i = 0; i < SURFEL_GRADS; ++i) gs[i] = contrib ? gs[i] : 0.0f;
             if (contrib) {
-                sr -= vis * cl_r; sg -= vis * cl_g; sb -= vis * cl_b;
-                sz -= vis * z; snx -= vis * nrm_x; sny -= vis * nrm_y; snz -= vis * nrm_z;
-                sdb -= vis * m; sdc -= vis * m * m;
+                sv_rest -= vis * cv;
                 T = nt;
             }
             const float mine = reduce_scatter17(gs, lane);
