@@ -783,7 +783,8 @@ constexpr int SURF_BWD_BLOCK = 256;
 template <bool SMOOTH>
 __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(RasterBwdArgs a) {
     __shared__ float4 s_s[BWD_BATCH * 4];   // M rows, centre, normal (vs_surfel.h layout)
-    __shared__ float4 s_b[BWD_BATCH];       // opacity, r, g, b (raw colours: the gates need the sign)
+    __shared__ float4 s_b[BWD_BATCH];       // opacity, max(r, 0), max(g, 0), max(b, 0)
+    __shared__ uint32_t s_gate[BWD_BATCH];  // bit c: colour channel c is >= 0 (its gradient passes the clamp)
     __shared__ uint32_t s_gid[BWD_BATCH];
     __shared__ float s_acc[BWD_BATCH * SURFEL_GRADS];
 
@@ -828,6 +829,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
     // cotangent (the only use of those sums); each blend takes vis (c.v) off it
     float sv_rest = sr * vr + sg * vg + sb * vb + sz * vz + snx * vnx + sny * vny + snz * vnz + sdb * vdb + sdc * vdc;
     const int comp = (lane & 1u) ? -1 : scatter_component17(lane);   // the gradient component this lane adds
+    const int gate_bit = (comp >= 12 && comp <= 14) ? comp - 12 : -1;  // rgb components: their clamp's gate
     for (uint32_t i = threadIdx.x; i < BWD_BATCH * SURFEL_GRADS; i += SURF_BWD_BLOCK) s_acc[i] = 0.0f;
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
@@ -843,12 +845,14 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
                 s_s[4 * lane + q] = row;
                 if (q == 0) {
                     const float4 pb = a.proj_b[gid];
-                    s_b[lane] = make_float4(pb.y, pb.z, pb.w, a.proj_c[gid]);
+                    const float cb_ = a.proj_c[gid];
+                    s_b[lane] = make_float4(pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f), mx(cb_, 0.0f));
+                    s_gate[lane] = (pb.z >= 0.0f ? 1u : 0u) | (pb.w >= 0.0f ? 2u : 0u) | (cb_ >= 0.0f ? 4u : 0u);
                     s_gid[lane] = gid;
                 }
             } else {   // a corrupt id: zero opacity never reaches the cutoff
                 s_s[4 * lane + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (q == 0) { s_b[lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f); s_gid[lane] = 0u; }
+                if (q == 0) { s_b[lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f); s_gate[lane] = 0u; s_gid[lane] = 0u; }
             }
         }
         __syncthreads();
@@ -862,8 +866,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             live &= live - 1ull;
             const float4 m0 = s_s[4 * t], m1 = s_s[4 * t + 1], m2 = s_s[4 * t + 2], m3 = s_s[4 * t + 3];
             const float4 cb = s_b[t];
-            const float opac = cb.x, col_r = cb.y, col_g = cb.z, col_b = cb.w;
-            const float cl_r = mx(col_r, 0.0f), cl_g = mx(col_g, 0.0f), cl_b = mx(col_b, 0.0f);
+            const float opac = cb.x, cl_r = cb.y, cl_g = cb.z, cl_b = cb.w;
             const float r2x = m1.z, r2y = m1.w, r2z = m2.x, cen_x = m2.y, cen_y = m2.z;
             const float nrm_x = m2.w, nrm_y = m3.x, nrm_z = m3.y;
             const float inv_r2z = m3.w;
@@ -892,9 +895,9 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             const float Tk = T;
             const float vis = ae * Tk;
             float gs[SURFEL_GRADS];
-            gs[12] = (col_r >= 0.0f) ? vis * vr : 0.0f;
-            gs[13] = (col_g >= 0.0f) ? vis * vg : 0.0f;
-            gs[14] = (col_b >= 0.0f) ? vis * vb : 0.0f;
+            gs[12] = vis * vr;      // the colour clamps' gates apply to the wave sums below
+            gs[13] = vis * vg;
+            gs[14] = vis * vb;
             gs[9] = vis * vnx;
             gs[10] = vis * vny;
             gs[11] = vis * vnz;
@@ -936,7 +939,8 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
                 sv_rest -= vis * cv;
                 T = nt;
             }
-            const float mine = reduce_scatter17(gs, lane);
+            float mine = reduce_scatter17(gs, lane);
+            if (gate_bit >= 0 && !((s_gate[t] >> gate_bit) & 1u)) mine = 0.0f;
             if (comp >= 0 && mine != 0.0f) atomicAdd(&s_acc[t * SURFEL_GRADS + comp], mine);
         }
         __syncthreads();
