@@ -908,7 +908,10 @@ static V3 surfel_normal(Q4 q, V3 mc, const or_camera& u) {
 }
 // The ray-plane sample of a pixel (rasterize.rs:267-301): (u, v), the
 // intersection depth z, the low-pass offsets and sigma = min(s3d, s2d) / 2;
-// false when the ray misses or meets the plane before the near limit.
+// false when the ray misses or meets the plane before the near limit.  The
+// quotients q.x / q.z and q.y / q.z are taken as products with the correctly
+// rounded 1 / q.z (one division for both; each within one rounding of the
+// quotient), as the kernels do.
 struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
 static SurfelHit surfel_hit(const float* a, float px, float py) {
     SurfelHit h;
@@ -918,8 +921,9 @@ static SurfelHit surfel_hit(const float* a, float px, float py) {
     const float qx = h.huy * h.hvz - h.huz * h.hvy;
     const float qy = h.huz * h.hvx - h.hux * h.hvz;
     h.qz = h.hux * h.hvy - h.huy * h.hvx;
-    h.su = qx / h.qz;
-    h.sv = qy / h.qz;
+    const float rq = 1.0f / h.qz;
+    h.su = qx * rq;
+    h.sv = qy * rq;
     h.s3d = h.su * h.su + h.sv * h.sv;
     h.z = m20 * h.su + m21 * h.sv + m22;
     h.dxs = px - a[9]; h.dys = py - a[10];

@@ -95,8 +95,10 @@ VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float p
     h.valid = false;
     const bool far = 0.5f * h.s2d > smax && qx * qx + qy * qy > (2.0004f * smax) * (h.qz * h.qz);
     if (EARLY && far) return h;
-    h.su = qx / h.qz;
-    h.sv = qy / h.qz;
+    // the quotients as products with the correctly rounded 1 / q.z (the oracle's form)
+    const float rq = 1.0f / h.qz;
+    h.su = qx * rq;
+    h.sv = qy * rq;
     h.s3d = h.su * h.su + h.sv * h.sv;
     h.z = m20 * h.su + m21 * h.sv + m22;
     h.sigma = 0.5f * mn(h.s3d, h.s2d);
