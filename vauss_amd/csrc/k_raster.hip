@@ -638,6 +638,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     // that sum, so a lane carries D per pixel: D -= vis (max(c,0) . v).
     float pcx[BWD_PX], pcy[BWD_PX], D[BWD_PX], T[BWD_PX];
     float vr[BWD_PX], vg[BWD_PX], vb[BWD_PX], vt[BWD_PX], rscale[BWD_PX];
+    bool cot = false;   // a pixel of the lane has a nonzero (or non-finite) cotangent
 #pragma unroll
     for (int k = 0; k < BWD_PX; ++k) {
         const uint32_t px = tx * TILE_W + 8 * (k & 1) + (lane & 7);
@@ -649,6 +650,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             const size_t base = ((size_t)py * a.img_w + px) * a.channels;
             const float4 o = *reinterpret_cast<const float4*>(a.out_img + base);
             const float4 v = *reinterpret_cast<const float4*>(a.v_out + base);
+            cot = cot || v.x != 0.0f || v.y != 0.0f || v.z != 0.0f || v.w != 0.0f;
             const float t_final = 1.0f - o.w;
             const float sr = o.x - t_final * a.bg_r;
             const float sg = o.y - t_final * a.bg_g;
@@ -660,6 +662,9 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             rscale[k] = __builtin_amdgcn_rcpf(mx(o.w, 1.0e-5f));
         }
     }
+    // every gradient term is linear in the cotangent: a tile whose pixels all
+    // have a zero one (outside a loss mask) adds nothing
+    if (__ballot(cot) == 0ull) return;
     const int comp = scatter_component(lane);
     // Per-lane factor applied to the reduced sum: the conic sums are carried
     // as sum nv dx^2, nv dx dy, nv dy^2 with nv = alpha v_alpha = -v_sigma,
@@ -805,6 +810,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
     float vr = 0.0f, vg = 0.0f, vb = 0.0f, vt = 0.0f, vz = 0.0f, vmed = 0.0f, vnx = 0.0f, vny = 0.0f, vnz = 0.0f;
     float vdb = 0.0f, vdc = 0.0f;
     uint32_t med = 0xFFFFFFFFu;
+    bool cot = false;   // the pixel has a nonzero (or non-finite) cotangent
     if (px < a.img_w && py < a.img_h) {
         const size_t base = ((size_t)py * a.img_w + px) * a.channels;
         const float4 o0 = *reinterpret_cast<const float4*>(a.out_img + base);
@@ -813,6 +819,8 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
         const float4 v0 = *reinterpret_cast<const float4*>(a.v_out + base);
         const float4 v1 = *reinterpret_cast<const float4*>(a.v_out + base + 4);
         const float4 v2 = *reinterpret_cast<const float4*>(a.v_out + base + 8);
+        cot = v0.x != 0.0f || v0.y != 0.0f || v0.z != 0.0f || v0.w != 0.0f || v1.x != 0.0f || v1.y != 0.0f ||
+              v1.z != 0.0f || v1.w != 0.0f || v2.x != 0.0f || v2.y != 0.0f || v2.z != 0.0f || v2.w != 0.0f;
         const float t_final = 1.0f - o0.w;
         sr = o0.x - t_final * a.bg_r;
         sg = o0.y - t_final * a.bg_g;
@@ -828,6 +836,9 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
     // S.v: the channels still to come behind the current splat, dotted with the
     // cotangent (the only use of those sums); each blend takes vis (c.v) off it
     float sv_rest = sr * vr + sg * vg + sb * vb + sz * vz + snx * vnx + sny * vny + snz * vnz + sdb * vdb + sdc * vdc;
+    // every gradient term is linear in the cotangent: a tile whose pixels all
+    // have a zero one (outside a loss mask) adds nothing
+    if (!__syncthreads_or(cot ? 1 : 0)) return;
     const int comp = (lane & 1u) ? -1 : scatter_component17(lane);   // the gradient component this lane adds
     const int gate_bit = (comp >= 12 && comp <= 14) ? comp - 12 : -1;  // rgb components: their clamp's gate
     for (uint32_t i = threadIdx.x; i < BWD_BATCH * SURFEL_GRADS; i += SURF_BWD_BLOCK) s_acc[i] = 0.0f;
