@@ -608,10 +608,14 @@ VS_DEV float reduce_scatter17(const float v[17], uint32_t lane) {
 // One 64-lane wavefront per tile; lane L owns pixel (L % 8, L / 8) of each
 // 8x8 quadrant k (k = 0..3), so the quadrant masks turn into uniform branches.
 // A lane sums its pixels' contributions in registers and the wavefront
-// reduces each splat once.
+// reduces each splat once.  PX = 1: images of fewer than BWD_QUAD_TILES
+// tiles, which leave most SIMDs idle with one wavefront per tile, take one
+// wavefront per quadrant instead (the four of a tile on one XCD, as in the
+// forward); each reduces and adds its own sums.
 constexpr int BWD_PX = 4;
+constexpr uint32_t BWD_QUAD_TILES = 2048;
 
-template <bool SMOOTH>
+template <bool SMOOTH, int PX>
 __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     // Per-splat values are formed once at staging, where one instruction
     // serves the 64 splats of a batch, not per (splat, wavefront) in the loop.
@@ -623,7 +627,13 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     __shared__ uint32_t s_gid[BWD_BATCH];
     __shared__ uint32_t s_mask[BWD_BATCH];  // live quadrants
 
-    const uint32_t tile = block_tile(a.order, blockIdx.x, a.num_tiles);
+    uint32_t slot = blockIdx.x, q0 = 0u;      // q0: the first quadrant the wavefront owns
+    if constexpr (PX == 1) {
+        const uint32_t xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
+        q0 = idx % 4;
+        slot = (idx / 4) * 8 + xcd;
+    }
+    const uint32_t tile = block_tile(a.order, slot, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
     const uint32_t lo = a.ranges[tile * 2], hi = a.ranges[tile * 2 + 1];
     if (lo >= hi) return;   // uniform per tile
@@ -636,13 +646,14 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     // The reference carries the remaining colour S (3 channels) to form
     // sum_c (T max(c,0) - S_c) v_c; only its projection D = S . v enters
     // that sum, so a lane carries D per pixel: D -= vis (max(c,0) . v).
-    float pcx[BWD_PX], pcy[BWD_PX], D[BWD_PX], T[BWD_PX];
-    float vr[BWD_PX], vg[BWD_PX], vb[BWD_PX], vt[BWD_PX], rscale[BWD_PX];
+    float pcx[PX], pcy[PX], D[PX], T[PX];
+    float vr[PX], vg[PX], vb[PX], vt[PX], rscale[PX];
     bool cot = false;   // a pixel of the lane has a nonzero (or non-finite) cotangent
 #pragma unroll
-    for (int k = 0; k < BWD_PX; ++k) {
-        const uint32_t px = tx * TILE_W + 8 * (k & 1) + (lane & 7);
-        const uint32_t py = ty * TILE_W + 8 * (k >> 1) + (lane >> 3);
+    for (int k = 0; k < PX; ++k) {
+        const uint32_t qk = q0 + (uint32_t)k;
+        const uint32_t px = tx * TILE_W + 8 * (qk & 1) + (lane & 7);
+        const uint32_t py = ty * TILE_W + 8 * (qk >> 1) + (lane >> 3);
         pcx[k] = (float)px + 0.5f;
         pcy[k] = (float)py + 0.5f;
         D[k] = T[k] = vr[k] = vg[k] = vb[k] = vt[k] = rscale[k] = 0.0f;
@@ -679,7 +690,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
         uint32_t alive = 0;   // quadrants with a pixel still above T_STOP (uniform)
 #pragma unroll
-        for (int k = 0; k < BWD_PX; ++k) alive |= (__ballot(T[k] > T_STOP) != 0ull) ? (1u << k) : 0u;
+        for (int k = 0; k < PX; ++k) alive |= (__ballot(T[k] > T_STOP) != 0ull) ? (1u << k) : 0u;
         if (alive == 0) break;                              // every pixel of the tile is done
         const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
         __syncthreads();
@@ -703,7 +714,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {
-            const uint32_t live = __builtin_amdgcn_readfirstlane(s_mask[t]) & alive;
+            const uint32_t live = (__builtin_amdgcn_readfirstlane(s_mask[t]) >> q0) & alive;
             if (live == 0) continue;                        // uniform: no quadrant reaches the cutoff
             const float4 sa = s_a[t];
             const float4 sbv = s_b[t];
@@ -713,7 +724,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             const float cl_r = sbv.z, cl_g = sbv.w, cl_b = scv.x;
             bool contrib = false;
 #pragma unroll
-            for (int k = 0; k < BWD_PX; ++k) {
+            for (int k = 0; k < PX; ++k) {
                 if (!((live >> k) & 1u)) continue;          // uniform
                 const float Tk = T[k];
                 if (!(Tk > T_STOP)) continue;
@@ -1059,14 +1070,17 @@ hipError_t launch_raster_fwd(const RasterArgs& a, bool bwd_info, bool geometry, 
 
 hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
     if (a.num_tiles == 0) return hipSuccess;
-    const dim3 grid(xcd_grid(a.num_tiles));
+    dim3 grid(xcd_grid(a.num_tiles));
     void (*k)(RasterBwdArgs);
     uint32_t block = 64;
     if (a.proj_surf) {
         k = smooth ? raster_bwd_surfel_kernel<true> : raster_bwd_surfel_kernel<false>;
         block = SURF_BWD_BLOCK;
+    } else if (a.num_tiles < BWD_QUAD_TILES) {
+        k = smooth ? raster_bwd_kernel<true, 1> : raster_bwd_kernel<false, 1>;
+        grid = dim3(4 * xcd_grid(a.num_tiles));   // four quadrant wavefronts per dispatch slot
     } else {
-        k = smooth ? raster_bwd_kernel<true> : raster_bwd_kernel<false>;
+        k = smooth ? raster_bwd_kernel<true, BWD_PX> : raster_bwd_kernel<false, BWD_PX>;
     }
     if (start) hipExtLaunchKernelGGL(k, grid, dim3(block), 0, s, start, stop, 0u, a);
     else k<<<grid, block, 0, s>>>(a);
