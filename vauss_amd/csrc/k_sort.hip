@@ -28,7 +28,7 @@ namespace vs {
 #define VS_SORT_ITEMS 8
 #endif
 #ifndef VS_ONESWEEP_MIN
-#define VS_ONESWEEP_MIN (1u << 16)
+#define VS_ONESWEEP_MIN (1u << 12)   // below it the input is one block of the three-kernel schedule
 #endif
 constexpr int SORT_BLOCK = 256;
 constexpr int SORT_ITEMS = VS_SORT_ITEMS;
