@@ -355,7 +355,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
     __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BATCH : 1];
     __shared__ float4 s_s[SURF ? FWD_BATCH * 4 : 1];
     __shared__ uint4 s_hit[BWD ? FWD_BATCH : 1];   // .x = 1 once the slot blended a pixel
-    __shared__ uint16_t s_list[FWD_BATCH];         // live slots as byte offsets (slot * 16)
+    __shared__ uint32_t s_list[FWD_BATCH];         // live slots as byte offsets (slot * 16)
 
     const uint32_t xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
     const uint32_t q = idx % 4;
@@ -412,22 +412,31 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                 live = quadrant_live(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
             }
         }
-        // the live slots, compacted in slot (= depth) order
+        // the live slots in slot (= depth) order: the mask is walked in
+        // scalar registers, lowest set bit first
         const uint64_t lm = __ballot(live);
         if (live) s_list[__builtin_amdgcn_mbcnt_hi((uint32_t)(lm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lm, 0u))] =
-            (uint16_t)(l * 16u);
+            l * 16u;
         __syncthreads();
         const uint32_t nlist = (uint32_t)__popcll(lm);
-        uint32_t last_off = 0xFFFFFFFFu;                                  // byte offset of the last slot blended
-        for (uint32_t j = 0; j < nlist; ++j) {
-            if (done) break;
+        uint32_t done_v = done ? 1u : 0u;   // carried in a vector register through the loop
+        // A uniform loop over the list: every lane evaluates every pair and a
+        // done lane only fails the blend test.  One divergent branch per pair
+        // (the blend) keeps the scalar exec-mask work per pair small; the
+        // scalar unit is shared by the CU's four SIMDs, and a per-lane loop
+        // exit or a guard around the whole body costs it more per pair than
+        // the vector work the masked lanes would skip.
+        for (uint32_t j0 = 0; j0 < nlist; j0 += 8u) {
+          const uint32_t jn = min(j0 + 8u, nlist);
+          for (uint32_t j = j0; j < jn; ++j) {
             const uint32_t off = s_list[j];
             const float4 sb = *reinterpret_cast<const float4*>(lds_b + off);
             float sigma, zs = 0.0f, G;
+            bool valid = true;
             if constexpr (SURF) {
                 const float4* ss = reinterpret_cast<const float4*>(lds_s + off * 4u);
                 const SurfelHit hit = surfel_hit(ss[0], ss[1], ss[2], ss[3].z, pcx, pcy);
-                if (!hit.valid) continue;       // the ray misses the plane or meets it before the near limit
+                valid = hit.valid;              // the ray misses the plane or meets it before the near limit
                 sigma = hit.sigma;
                 zs = hit.z;
                 G = exp2n(-(sigma * LOG2E_F));
@@ -441,12 +450,13 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             // (then the sigma test below rejects the pair): same value as mn().
             const float alpha = __builtin_fminf(ALPHA_CAP, sb.y * G);
             const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
-            if (sigma >= 0.0f && w_cut > 0.0f) {
-                const float ae = SMOOTH ? alpha * w_cut : alpha;
-                const float nt = T * (1.0f - ae);
-                if (nt <= T_STOP) {
-                    done = true;
-                } else {
+            const float ae = SMOOTH ? alpha * w_cut : alpha;
+            const float nt = T * (1.0f - ae);
+            const bool pass = done_v == 0u && valid && sigma >= 0.0f && w_cut > 0.0f;
+            const bool stop = nt <= T_STOP;
+            done_v = (pass && stop) ? 1u : done_v;
+            {
+                if (pass && !stop) {
                     if constexpr (BWD) reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_hit) + off)->x = 1u;
                     const float vis = ae * T;
                     const float cbv = reinterpret_cast<const float4*>(lds_c + off)->x;
@@ -481,15 +491,20 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                         nz = __builtin_fmaf(d.w, vis, nz);
                     }
                     T = nt;
-                    last_off = off;
                 }
             }
+          }
+          if (__ballot(done_v == 0u) == 0ull) break;   // every pixel of the quadrant is done (uniform)
         }
-        // slots blend in increasing order, so the batch's last blend is the lane's last so far
-        if (last_off != 0xFFFFFFFFu) last = start + (last_off >> 4) + 1u;
+        done = done_v != 0u;
         if constexpr (BWD) {
             __syncthreads();
-            if (gid < a.num_splats && s_hit[l].x) a.visible[gid] = 1.0f;
+            const bool hit = gid < a.num_splats && s_hit[l].x;
+            if (hit) a.visible[gid] = 1.0f;
+            // batches run in increasing order, so the batch's last blended
+            // slot is the quadrant's last so far
+            const uint64_t hm = __ballot(hit);
+            if (hm != 0ull) last = start + 64u - (uint32_t)__builtin_clzll(hm);
         }
     }
 
@@ -515,8 +530,6 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         }
     }
     if constexpr (BWD) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) last = max(last, (uint32_t)__shfl_xor((int)last, o));
         if (l == 0 && last > lo) atomicMax(&a.ranges_shrunk[tile * 2 + 1], last);
     }
 }
@@ -553,6 +566,9 @@ VS_DEV int scatter_component(uint32_t lane) {
     const int i5 = ((lane & 16) ? 3 : 0) + i3;                      // 5 = padding
     return (i3 < 3 && i5 < 5) ? ((lane & 32) ? 5 : 0) + i5 : -1;
 }
+
+// Sets a register to +0 where it lives.
+VS_DEV void zero_in_place(float& x) { asm volatile("v_mov_b32 %0, 0" : "=v"(x)); }
 
 VS_DEV float reduce_scatter10(const float v[10], uint32_t lane) {
     float w[5];
@@ -624,8 +640,6 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
     __shared__ float4 s_c[BWD_BATCH];       // max(b,0), c00, c11, colour gates (bits r,g,b >= 0, bit 3 set)
     __shared__ float4 s_d[BWD_BATCH];       // the conic's rows scaled to pixels: c00 W, c01 W, c01 H, c11 H
     __shared__ float s_c01[BWD_BATCH];      // c01
-    __shared__ uint32_t s_gid[BWD_BATCH];
-    __shared__ uint32_t s_mask[BWD_BATCH];  // live quadrants
 
     uint32_t slot = blockIdx.x, q0 = 0u;      // q0: the first quadrant the wavefront owns
     if constexpr (PX == 1) {
@@ -692,10 +706,14 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
 #pragma unroll
         for (int k = 0; k < PX; ++k) alive |= (__ballot(T[k] > T_STOP) != 0ull) ? (1u << k) : 0u;
         if (alive == 0) break;                              // every pixel of the tile is done
-        const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
+        // uniform; kept in a scalar register so the splat loop counts in SALU
+        const uint32_t rem = __builtin_amdgcn_readfirstlane(min((uint32_t)BWD_BATCH, hi - start));
         __syncthreads();
         const uint32_t gid = (lane < rem) ? a.gids[start + lane] : 0xFFFFFFFFu;
-        if (lane < rem && gid >= a.num_splats) s_mask[lane] = 0u;   // a corrupt id: no quadrant
+        // Lane t stages splat t: its live-quadrant mask and id stay in this
+        // lane's registers and reach the splat loop by readlane (a corrupt id
+        // keeps mask 0: no quadrant).
+        uint32_t mask = 0u;
         if (gid < a.num_splats) {
             const float4 pa = a.proj_a[gid];
             const float4 pb = a.proj_b[gid];
@@ -709,12 +727,11 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             s_c[lane] = make_float4(mx(cb, 0.0f), pa.z, pb.x, as_f(gates));
             s_d[lane] = make_float4(pa.z * img_w, pa.w * img_w, pa.w * img_h, pb.x * img_h);
             s_c01[lane] = pa.w;
-            s_gid[lane] = gid;
-            s_mask[lane] = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, c2, pb.y, SMOOTH);
+            mask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, c2, pb.y, SMOOTH);
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {
-            const uint32_t live = (__builtin_amdgcn_readfirstlane(s_mask[t]) >> q0) & alive;
+            const uint32_t live = (__builtin_amdgcn_readlane(mask, t) >> q0) & alive;
             if (live == 0) continue;                        // uniform: no quadrant reaches the cutoff
             const float4 sa = s_a[t];
             const float4 sbv = s_b[t];
@@ -775,11 +792,15 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 g[1] = __builtin_fmaf(c11, sy, c01 * sx);
             }
             float val = reduce_scatter10(g, lane);
+            // the sums restart at zero for the next splat, cleared in their own
+            // registers (a plain assignment makes the compiler rebuild the
+            // zeros at every branch of the next splat's quadrant loop)
 #pragma unroll
-            for (int i = 0; i < 10; ++i) g[i] = 0.0f;
+            for (int i = 0; i < 10; ++i) zero_in_place(g[i]);
             val = ((as_u(scv.w) >> gate_shift) & 1u) ? val * comp_scale : 0.0f;
+            const uint32_t gid_t = __builtin_amdgcn_readlane(gid, t);
             if ((lane & 3) == 0 && comp >= 0 && val != 0.0f)
-                atomicAdd(&a.v_combined[(size_t)s_gid[t] * 10 + comp], val);
+                atomicAdd(&a.v_combined[(size_t)gid_t * 10 + comp], val);
         }
     }
 }
