@@ -82,6 +82,25 @@ struct vs_ctx {
         hipEventCreate(&e);
         return e;
     }
+    // Stage-timing events: recorded without the system-scope fence (a cache
+    // write-back and invalidate that stalls the stream for several
+    // microseconds); they are only read by vs_ctx_stage_times after a stream
+    // synchronisation.
+    std::vector<hipEvent_t> tpool;
+    hipEvent_t take_timing() {
+        if (!tpool.empty()) { hipEvent_t e = tpool.back(); tpool.pop_back(); return e; }
+        hipEvent_t e = nullptr;
+        hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
+        return e;
+    }
+    // Library allocations freed by the last renders, reused in stream order:
+    // every library buffer lives on `stream`, so a block freed behind earlier
+    // work is free for any later work on it, and a render that takes one
+    // leaves no allocator packet in the stream.
+    struct Block { void* p; size_t bytes; };
+    std::vector<Block> cache;
+    std::map<void*, size_t> live;      // size of each library allocation in use
+    size_t cached_bytes = 0;
 };
 
 struct vs_fwd_state {
@@ -130,11 +149,11 @@ struct StageTimer {
     Stage s;
     hipEvent_t b = nullptr;
     StageTimer(vs_ctx* ctx, Stage st) : c(ctx), s(st) {
-        if (c->timing & (1u << s)) { b = c->take(); hipEventRecord(b, c->stream); }
+        if (c->timing & (1u << s)) { b = c->take_timing(); hipEventRecord(b, c->stream); }
     }
     ~StageTimer() {
         if (b) {
-            hipEvent_t e = c->take();
+            hipEvent_t e = c->take_timing();
             hipEventRecord(e, c->stream);
             c->recs.push_back(vs_ctx::Rec{(int)s, b, e});
         }
@@ -181,10 +200,57 @@ constexpr uint32_t POISON_WORD = 0xC640E400u;
 
 // Every buffer the library allocates for itself: stream-ordered, and filled
 // with POISON_WORD first when the context asks for it.
+constexpr size_t CACHE_MAX_BLOCKS = 8;
+constexpr size_t CACHE_MAX_BYTES = size_t(4) << 30;
+
+// A library buffer of at least `bytes` on the context's stream: the smallest
+// cached block that fits (and is at most twice the request), else a new
+// stream-ordered allocation.
 hipError_t lib_alloc(vs_ctx* c, void** p, size_t bytes, hipStream_t s) {
-    hipError_t e = hipMallocAsync(p, bytes, s);
-    if (e != hipSuccess || !c->poison || bytes < 4) return e;
+    bytes = std::max<size_t>(align256(bytes), 256);
+    size_t best = c->cache.size();
+    for (size_t i = 0; i < c->cache.size(); ++i) {
+        const size_t b = c->cache[i].bytes;
+        if (b >= bytes && b <= 2 * bytes && (best == c->cache.size() || b < c->cache[best].bytes)) best = i;
+    }
+    hipError_t e = hipSuccess;
+    if (best < c->cache.size()) {
+        *p = c->cache[best].p;
+        c->cached_bytes -= c->cache[best].bytes;
+        bytes = c->cache[best].bytes;
+        c->cache.erase(c->cache.begin() + (ptrdiff_t)best);
+    } else {
+        e = hipMallocAsync(p, bytes, s);
+        if (e != hipSuccess) return e;
+    }
+    c->live[*p] = bytes;
+    if (!c->poison || bytes < 4) return hipSuccess;
     return launch_fill_u32(static_cast<uint32_t*>(*p), POISON_WORD, bytes / 4, s);
+}
+
+// Returns a lib_alloc buffer to the cache behind the work already enqueued on
+// the context's stream; the oldest cached blocks beyond the cache's bounds
+// go back to the stream-ordered allocator.
+void lib_free(vs_ctx* c, void* p) {
+    if (!p) return;
+    auto it = c->live.find(p);
+    if (it == c->live.end()) { hipFreeAsync(p, c->stream); return; }
+    c->cache.push_back(vs_ctx::Block{p, it->second});
+    c->cached_bytes += it->second;
+    c->live.erase(it);
+    while (!c->cache.empty() && (c->cache.size() > CACHE_MAX_BLOCKS || c->cached_bytes > CACHE_MAX_BYTES)) {
+        hipFreeAsync(c->cache.front().p, c->stream);
+        c->cached_bytes -= c->cache.front().bytes;
+        c->cache.erase(c->cache.begin());
+    }
+}
+
+// Hands every cached block back to the allocator (on a stream change, where
+// stream order no longer covers reuse, and at context destruction).
+void drain_cache(vs_ctx* c) {
+    for (auto& b : c->cache) hipFreeAsync(b.p, c->stream);
+    c->cache.clear();
+    c->cached_bytes = 0;
 }
 
 // validate_tensor_val (validation.rs:60-140): NaN and Inf are errors, values
@@ -369,9 +435,11 @@ extern "C" vs_status vs_ctx_create(int device, void* hip_stream, vs_ctx** out) {
 extern "C" void vs_ctx_destroy(vs_ctx* c) {
     if (!c) return;
     hipSetDevice(c->device);
+    drain_cache(c);
     hipStreamSynchronize(c->stream);
     for (auto& r : c->recs) { hipEventDestroy(r.b); hipEventDestroy(r.e); }
     for (auto e : c->pool) hipEventDestroy(e);
+    for (auto e : c->tpool) hipEventDestroy(e);
     for (auto& kv : c->pending) {
         if (kv.second.ev) hipEventDestroy(kv.second.ev);
         if (kv.second.host) hipHostFree(kv.second.host);
@@ -385,7 +453,13 @@ extern "C" void vs_ctx_destroy(vs_ctx* c) {
 
 extern "C" vs_status vs_ctx_set_stream(vs_ctx* c, void* hip_stream) {
     if (!c) return fail(VS_ERR_INVALID, "ctx is null");
-    c->stream = static_cast<hipStream_t>(hip_stream);
+    hipStream_t ns = static_cast<hipStream_t>(hip_stream);
+    if (ns != c->stream) {
+        // cached blocks were freed in the old stream's order: return them there
+        drain_cache(c);
+        VS_HIP(hipStreamSynchronize(c->stream), "hipStreamSynchronize(old stream)");
+    }
+    c->stream = ns;
     return VS_OK;
 }
 
@@ -429,8 +503,8 @@ extern "C" vs_status vs_ctx_stage_times(vs_ctx* c, vs_stage_times* out) {
     for (auto& r : c->recs) {
         float v = 0.0f;
         if (hipEventElapsedTime(&v, r.b, r.e) == hipSuccess) ms[r.stage] += v;
-        c->pool.push_back(r.b);
-        c->pool.push_back(r.e);
+        c->tpool.push_back(r.b);
+        c->tpool.push_back(r.e);
     }
     c->recs.clear();
     out->project_ms = ms[ST_PROJECT];
@@ -447,8 +521,8 @@ extern "C" vs_status vs_ctx_stage_times(vs_ctx* c, vs_stage_times* out) {
 extern "C" void vs_fwd_state_free(vs_fwd_state* st) {
     if (!st) return;
     hipSetDevice(st->ctx->device);
-    if (st->isect_arena) hipFreeAsync(st->isect_arena, st->ctx->stream);
-    if (st->arena) hipFreeAsync(st->arena, st->ctx->stream);
+    lib_free(st->ctx, st->isect_arena);
+    lib_free(st->ctx, st->arena);
     delete st;
 }
 
@@ -833,12 +907,16 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         RasterArgs ra{};
         ra.img_w = W; ra.img_h = H; ra.tile_bw = st->tbw; ra.tile_bh = st->tbh; ra.num_tiles = T; ra.num_splats = N;
         // longest lists first within each XCD's band (the forward's cost grows with its list)
+        // the caller's tile offsets are written by this pass and the forward
+        // (no copy behind the forward)
         VS_HIP(launch_tile_order(st->ranges, T, st->tile_order, s, bwd_info ? st->ranges_shrunk : nullptr, true,
-                                 ctx->dev_flags, lag_slot ? lag_slot->host + CNT_COUNT : nullptr, CTX_FLAGS),
+                                 ctx->dev_flags, lag_slot ? lag_slot->host + CNT_COUNT : nullptr, CTX_FLAGS,
+                                 out->tile_offsets),
                "tile order");
         ra.order = st->tile_order;
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
         ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;
+        ra.aux_ranges = bwd_info ? out->tile_offsets : nullptr;
         ra.proj_a = st->proj_a; ra.proj_b = st->proj_b; ra.proj_c = st->proj_c; ra.proj_aux = st->proj_aux;
         // surfels outside training take the median by the surface criterion (gaussian_splats.rs:100-106)
         ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass_surface_criterion(pass)) ? 1u : 0u;
@@ -849,10 +927,6 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         VS_HIP(hipEventSynchronize(sort_done), "hipEventSynchronize(sorts)");
         vs_status fe = take_sort_flag(ctx);
         if (fe != VS_OK) return fe;
-    }
-    if (out->tile_offsets) {
-        const uint32_t* src = bwd_info ? st->ranges_shrunk : st->ranges;
-        VS_HIP(hipMemcpyAsync(out->tile_offsets, src, (size_t)T * 8, hipMemcpyDeviceToDevice, s), "tile offsets copy");
     }
     if (lagged) {
         // Counts leave behind an event; the next training render at this size
@@ -924,7 +998,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             rb.proj_surf = st->proj_surf;
             rb.v_combined = vc;
             hipEvent_t eb = nullptr, ee = nullptr;
-            if (ctx->timing & (1u << ST_RASTER_BWD)) { eb = ctx->take(); ee = ctx->take(); }
+            if (ctx->timing & (1u << ST_RASTER_BWD)) { eb = ctx->take_timing(); ee = ctx->take_timing(); }
             VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s, eb, ee), "raster backward");
             if (eb) ctx->recs.push_back(vs_ctx::Rec{(int)ST_RASTER_BWD, eb, ee});
         }
@@ -954,7 +1028,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
                    "hipMallocAsync(decoder partials)");
             nb.partials = static_cast<float*>(part);
             const hipError_t e = launch_neural_bwd(nb, s);
-            hipFreeAsync(part, s);
+            lib_free(ctx, part);
             VS_HIP(e, "neural backward");
         }
     }
@@ -972,7 +1046,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
         if (!dense) ch[n++] = Check{"gradient_v_combined", vc, false, (uint64_t)N * n_grads, 1, 0, 1, -inf, inf};
         ve = run_checks(ctx, ch, n);
     }
-    if (vc_alloc) VS_HIP(hipFreeAsync(vc_alloc, s), "hipFreeAsync(v_combined)");
+    if (vc_alloc) lib_free(ctx, vc_alloc);
     return ve;
 }
 
@@ -1001,7 +1075,7 @@ extern "C" vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_sp
     if (nb > 0) VS_HIP(lib_alloc(ctx, &part, (size_t)nb * 12 * sizeof(float), s), "hipMallocAsync(pose partials)");
     pa.partials = static_cast<float*>(part);
     const hipError_t e = launch_pose_bwd(pa, s);
-    if (part) hipFreeAsync(part, s);
+    if (part) lib_free(ctx, part);
     VS_HIP(e, "pose backward");
     return VS_OK;
 }
@@ -1169,7 +1243,7 @@ extern "C" vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, con
     StageTimer tm(ctx, ST_OTHER);
     hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, n_dev, false, skip_bits, skip_bits + sorting_bits,
                                     tmp, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream, ctx->spin_limit);
-    hipFreeAsync(tmp, ctx->stream);
+    lib_free(ctx, tmp);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
     return sync_sort_flag(ctx);
 }
@@ -1209,7 +1283,7 @@ extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, con
     StageTimer tm(ctx, ST_OTHER);
     hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, nullptr, true, 0, sorting_bits, tmp,
                                     ctx->dev_flags + FLAG_SORT_STALL, ctx->stream, ctx->spin_limit);
-    hipFreeAsync(tmp, ctx->stream);
+    lib_free(ctx, tmp);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
     return sync_sort_flag(ctx);
 }
@@ -1222,7 +1296,7 @@ extern "C" vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t
     void* tmp = nullptr;
     VS_HIP(lib_alloc(ctx, &tmp, scan_tmp_words(n) * 4, ctx->stream), "hipMallocAsync(scan tmp)");
     hipError_t e = scan_u32(in, out, n, true, static_cast<uint32_t*>(tmp), nullptr, ctx->stream);
-    hipFreeAsync(tmp, ctx->stream);
+    lib_free(ctx, tmp);
     if (e != hipSuccess) return hip_fail(e, "prefix sum");
     return VS_OK;
 }
@@ -1296,7 +1370,7 @@ extern "C" vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint
         LossArgs f = a;
         f.coeffs = static_cast<float*>(tmp);
         hipError_t e = launch_loss_forward(f, s);
-        if (e != hipSuccess) { hipFreeAsync(tmp, s); return hip_fail(e, "image loss coefficients"); }
+        if (e != hipSuccess) { lib_free(ctx, tmp); return hip_fail(e, "image loss coefficients"); }
         coeffs = static_cast<const float*>(tmp);
     }
     LossBwdArgs b{};
@@ -1304,7 +1378,7 @@ extern "C" vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint
     b.dl = dl_dpartials; b.coeffs = coeffs; b.dl_dpred = dl_dpred; b.rgb_weight = a.rgb_weight;
     b.alpha_weight = a.alpha_weight;
     hipError_t e = launch_loss_backward(b, dl_count == 1, s);
-    if (tmp) hipFreeAsync(tmp, s);
+    if (tmp) lib_free(ctx, tmp);
     if (e != hipSuccess) return hip_fail(e, "image loss backward");
     return VS_OK;
 }

@@ -108,7 +108,8 @@ __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(uint32_t* range
                                                                  uint32_t* __restrict__ order,
                                                                  uint32_t* __restrict__ shrunk_init, int fix_empty,
                                                                  const uint32_t* __restrict__ flags_from,
-                                                                 uint32_t* flags_to, uint32_t nflags) {
+                                                                 uint32_t* flags_to, uint32_t nflags,
+                                                                 uint32_t* __restrict__ aux_out) {
     if (blockIdx.x == 0 && threadIdx.x < nflags) flags_to[threadIdx.x] = flags_from[threadIdx.x];
     __shared__ uint32_t s_bin[ORDER_BINS];
     __shared__ uint32_t s_wave[ORDER_BLOCK / 64];
@@ -129,6 +130,10 @@ __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(uint32_t* range
         if (shrunk_init) {   // the forward's shrunk ranges start empty at the range start
             shrunk_init[2 * t] = lo;
             shrunk_init[2 * t + 1] = lo;
+        }
+        if (aux_out) {
+            aux_out[2 * t] = lo;
+            aux_out[2 * t + 1] = shrunk_init ? lo : hi;
         }
     }
     __syncthreads();
@@ -530,7 +535,10 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         }
     }
     if constexpr (BWD) {
-        if (l == 0 && last > lo) atomicMax(&a.ranges_shrunk[tile * 2 + 1], last);
+        if (l == 0 && last > lo) {
+            atomicMax(&a.ranges_shrunk[tile * 2 + 1], last);
+            if (a.aux_ranges) atomicMax(&a.aux_ranges[tile * 2 + 1], last);
+        }
     }
 }
 
@@ -1067,11 +1075,11 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 
 hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
                              uint32_t* shrunk_init, bool fix_empty, const uint32_t* flags_from, uint32_t* flags_to,
-                             uint32_t nflags) {
+                             uint32_t nflags, uint32_t* aux_out) {
     if (num_tiles == 0) return hipSuccess;
     if (!flags_to) nflags = 0;
     tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init, fix_empty ? 1 : 0, flags_from,
-                                                flags_to, nflags);
+                                                flags_to, nflags, aux_out);
     return hipGetLastError();
 }
 

@@ -131,6 +131,7 @@ struct RasterArgs {
     const uint32_t* gids;            // sorted intersections -> global splat id
     const uint32_t* ranges;          // [T,2]
     uint32_t* ranges_shrunk;         // [T,2] written by bwd-info passes (may alias nothing else)
+    uint32_t* aux_ranges;            // [T,2] the caller's copy of the shrunk ranges (bwd-info passes), or null
     const float4* proj_a;
     const float4* proj_b;
     const float* proj_c;
@@ -306,9 +307,13 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 // `fix_empty`: ranges left at (0xFFFFFFFF, 0) by the sort become (0, 0).
 // `flags_to` (optional): copies nflags words of flags_from there (the
 // lagged render's pinned readback slot).
+// `aux_out` (optional): the caller's tile offsets, set like `shrunk_init`
+// when that is given (the forward raises their ends too), else to the
+// (fixed) ranges.
 hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
                              uint32_t* shrunk_init = nullptr, bool fix_empty = false,
-                             const uint32_t* flags_from = nullptr, uint32_t* flags_to = nullptr, uint32_t nflags = 0);
+                             const uint32_t* flags_from = nullptr, uint32_t* flags_to = nullptr, uint32_t nflags = 0,
+                             uint32_t* aux_out = nullptr);
 hipError_t launch_ranges_init(uint32_t* ranges, uint32_t num_tiles, hipStream_t s);
 hipError_t launch_tiles_from_ranges(const uint32_t* ranges, uint32_t num_tiles, uint32_t n, uint32_t* tiles,
                                     hipStream_t s);
