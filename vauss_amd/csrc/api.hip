@@ -795,7 +795,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const size_t o_tu = itake((size_t)I * 4), o_vu = itake((size_t)I * 4);
         const size_t o_t = itake((size_t)I * 4), o_v = itake((size_t)I * 4);
         const size_t o_dk = itake((size_t)M * 4), o_dv = itake((size_t)M * 4);
-        const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)M * 4);
+        const size_t o_dks = itake((size_t)M * 4), o_ord = itake((size_t)M * 4), o_base = itake((size_t)(M + 1) * 4);
         const size_t o_base_g = itake((size_t)N * 4);
         const size_t o_scan = itake(scan_lookback_status_words(M) * 4);
         const size_t o_mass = cutoff ? itake(cut_words * 4) : 0, o_allow = cutoff ? itake(cut_words * 2) : 0;
@@ -812,7 +812,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         uint32_t* dvals = reinterpret_cast<uint32_t*>(ib + o_dv);
         uint32_t* dkeys_sorted = reinterpret_cast<uint32_t*>(ib + o_dks);
         uint32_t* order = reinterpret_cast<uint32_t*>(ib + o_ord);
-        uint32_t* slot_base = reinterpret_cast<uint32_t*>(ib + o_base);   // [M], nearest emitter first
+        uint32_t* slot_base = reinterpret_cast<uint32_t*>(ib + o_base);   // [M + 1], nearest emitter first, then the total
         uint32_t* slot_base_g = reinterpret_cast<uint32_t*>(ib + o_base_g);   // [N], written for emitters only
         uint32_t* scan_tmp = reinterpret_cast<uint32_t*>(ib + o_scan);
         uint32_t* err = ctx->dev_flags + FLAG_SORT_STALL;
@@ -864,7 +864,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         {
             StageTimer tm(ctx, ST_EMIT);
             VS_HIP(scan_u32_lookback(slot_counts, slot_base, M, scan_tmp, err, s, ctx->spin_limit, order, m_dev, N,
-                                     slot_base_g),
+                                     slot_base_g, true),
                    "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;

@@ -685,18 +685,21 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     const uint32_t lane = lane_id();
     const uint32_t big_blocks = emit_big_blocks(a.num_splats);
     const bool big = blockIdx.x < big_blocks;
-    uint32_t g = 0xFFFFFFFFu, base = 0u;
+    uint32_t g = 0xFFFFFFFFu, base = 0u, cnt = 0u;
     if (big) {
         g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+        cnt = (g < a.num_splats) ? a.counts[g] : 0u;
     } else {
         const uint32_t j = (blockIdx.x - big_blocks) * PROJ_BLOCK + threadIdx.x;
         const uint32_t m = a.m_dev ? min(*a.m_dev, a.num_emitters) : a.num_emitters;
         if (j < m) {
             g = a.order[j];
             base = a.slot_base[j];
+            // the count from the slot bases in depth order (slot_base[m] is the
+            // total) rather than a gather from the counts in id order
+            cnt = (g < a.num_splats) ? a.slot_base[j + 1] - base : 0u;
         }
     }
-    uint32_t cnt = (g < a.num_splats) ? a.counts[g] : 0u;
     float px = 0.0f, py = 0.0f, power = 0.0f;
     S2 conic{0.0f, 0.0f, 0.0f};
     TileBox bb{0, 0, 0, 0};
@@ -732,7 +735,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     // the list's length: the last emitter's slot range ends it
     if (a.listed && blockIdx.x == 0 && threadIdx.x == 0) {
         const uint32_t m = a.m_dev ? min(*a.m_dev, a.num_emitters) : a.num_emitters;
-        *a.listed = m ? a.slot_base[m - 1] + a.counts[a.order[m - 1]] : 0u;
+        *a.listed = m ? a.slot_base[m] : 0u;
     }
 }
 

@@ -154,7 +154,7 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_lookback_kernel(const uint32_
                                                                    const uint32_t* __restrict__ n_dev, uint32_t perm_bound,
                                                                    uint32_t* __restrict__ out2,
                                                                    unsigned long long* status, uint32_t* err,
-                                                                   uint32_t spin_limit) {
+                                                                   uint32_t spin_limit, int write_end) {
     const uint64_t n = scan_count(n_cap, n_dev);
     const uint64_t base = (uint64_t)blockIdx.x * SCAN_TILE;
     if (base >= n) return;   // uniform: no later block has elements either
@@ -216,6 +216,12 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_lookback_kernel(const uint32_
         s_data[threadIdx.x * SCAN_ITEMS + i] = run;
         run += v[i];
     }
+    // out[n]: the total, from the thread holding element n - 1 (the elements
+    // past it loaded as zero)
+    if (write_end) {
+        const uint64_t first = base + (uint64_t)threadIdx.x * SCAN_ITEMS;
+        if (first < n && n <= first + SCAN_ITEMS) out[n] = run;
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < SCAN_ITEMS; ++i) {
@@ -235,13 +241,13 @@ uint64_t scan_lookback_status_words(uint64_t n) { return 2 * ((n + SCAN_TILE - 1
 
 hipError_t scan_u32_lookback(const uint32_t* in, uint32_t* out, uint64_t n, uint32_t* status, uint32_t* err,
                              hipStream_t s, uint32_t spin_limit, const uint32_t* perm, const uint32_t* n_dev,
-                             uint32_t perm_bound, uint32_t* out_scattered) {
+                             uint32_t perm_bound, uint32_t* out_scattered, bool write_end) {
     if (n == 0) return hipSuccess;
     const uint64_t blocks = (n + SCAN_TILE - 1) / SCAN_TILE;
     scan_lookback_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, perm, n_dev, perm_bound,
                                                                  perm ? out_scattered : nullptr,
                                                                  reinterpret_cast<unsigned long long*>(status), err,
-                                                                 spin_limit);
+                                                                 spin_limit, write_end ? 1 : 0);
     return hipGetLastError();
 }
 

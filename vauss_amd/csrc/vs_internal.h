@@ -85,7 +85,7 @@ struct EmitArgs {
     const uint32_t* m_dev;           // device count of emitters (lagged renders), or null
     const uint32_t* order;           // [M] global ids of the emitters, nearest first
     const uint32_t* counts;          // [N]
-    const uint32_t* slot_base;       // [M] first slot of the j-th nearest emitter (exclusive scan)
+    const uint32_t* slot_base;       // [M + 1] first slot of the j-th nearest emitter (exclusive scan), then the total
     const uint32_t* slot_base_g;     // [N] the same, at the global id (emitters only)
     const float4* proj_a;
     const float4* proj_b;
@@ -362,12 +362,13 @@ hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_
 // The same exclusive scan in one kernel by decoupled look-back, written in
 // sequence order (out[i]; `out_scattered[perm[i]]` too when both are given).
 // `status` needs scan_lookback_status_words(n) words, zero on entry; a
-// look-back that waits past `spin_limit` polls sets *err.
+// look-back that waits past `spin_limit` polls sets *err.  With `write_end`,
+// out[n] (out holds n + 1 words) receives the total.
 uint64_t scan_lookback_status_words(uint64_t n);
 hipError_t scan_u32_lookback(const uint32_t* in, uint32_t* out, uint64_t n, uint32_t* status, uint32_t* err,
                              hipStream_t s, uint32_t spin_limit, const uint32_t* perm = nullptr,
                              const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu,
-                             uint32_t* out_scattered = nullptr);
+                             uint32_t* out_scattered = nullptr, bool write_end = false);
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
 size_t sort_tmp_bytes(uint64_t n, bool key64);
