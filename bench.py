@@ -437,6 +437,19 @@ STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "r
                    ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
 
 
+def stage_of_kernel(k: str) -> str:
+    """The bench stage of a (short) kernel name; the surfel and neural render
+    modes' kernels (bench rows of their own) are kept apart from the gaussian
+    SH stages they share names with."""
+    if k.startswith("raster_bwd_surfel") or (k.startswith("raster_fwd_kernel") and k.endswith(", true>")):
+        return "surfel"
+    if k.startswith(("project_kernel<-1", "project_bwd_kernel<-1")):
+        return "surfel"
+    if k.startswith(("project_kernel<3, 16", "project_bwd_kernel<3, 16")):
+        return "neural"
+    return next((st for pat, st in STAGE_OF_KERNEL if pat in k), k)
+
+
 # what the markdown summary lists (the traffic file keeps every kernel)
 SUMMARY_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VALU_TRANS_F32",
                     "SQ_LDS_BANK_CONFLICT", "SQ_THREAD_CYCLES_VALU", "SQ_ACTIVE_INST_VALU", "TCC_ATOMIC_sum",
@@ -544,7 +557,8 @@ def summarize(args) -> int:
         def per_run(v):        # dispatches of one run (the same counter may come from two runs)
             runs = {key[0] for key in v}
             return max(sum(1 for key in v if key[0] == r) for r in runs) if v else 0
-        nbwd = max(1, per_run(per.get("raster_bwd_kernel<false>", {}).get("FETCH_SIZE", {})))
+        # steps of the profiled run: launches of the gaussian raster backward
+        nbwd = max([1] + [per_run(v.get("FETCH_SIZE", {})) for k, v in per.items() if k.startswith("raster_bwd_kernel<")])
         for k, cs in sorted(per.items()):
             n = max(per_run(v) for v in cs.values())
             mean = {c: sum(v.values()) / len(v) for c, v in cs.items()}
@@ -561,7 +575,7 @@ def summarize(args) -> int:
                     derived = f"{mean[c] * 1024 * w_scale / 1e6:.1f} MB calibrated"
                 lines.append(f"| `{k}` | {n} | {c} | {mean[c]:.5g} | {derived} |")
             if f_scale and "FETCH_SIZE" in mean and "WRITE_SIZE" in mean:
-                stage = next((st for pat, st in STAGE_OF_KERNEL if pat in k), k)
+                stage = stage_of_kernel(k)
                 if stage in ("copy", "torch", "fill"):
                     continue
                 e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "valu_insts": 0.0,

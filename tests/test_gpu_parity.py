@@ -81,7 +81,11 @@ def _check_grads(got, want, name, rtol=1e-3, atol=1e-5, group_rtol=1e-3):
     want = np.asarray(want, np.float64)
     err = np.abs(got - want)
     bad = err > atol + rtol * np.abs(want)
-    assert not bad.any(), f"{name}: {bad.sum()} entries exceed {rtol:g} rel / {atol:g} abs (max err {err.max():.3e})"
+    if bad.any():
+        flat = np.argsort(-(err / (atol + rtol * np.abs(want))).ravel())[:4]
+        worst = [(np.unravel_index(i, err.shape), float(got.ravel()[i]), float(want.ravel()[i])) for i in flat]
+        raise AssertionError(f"{name}: {bad.sum()} entries exceed {rtol:g} rel / {atol:g} abs (max err {err.max():.3e}); "
+                             f"worst (index, gpu, oracle): {worst}")
     if group_rtol is None:
         return
     scale = np.abs(want).max(axis=0, keepdims=True) if want.ndim > 1 else np.abs(want).max()
