@@ -577,6 +577,14 @@ VS_DEV int scatter_component(uint32_t lane) {
 
 // Sets a register to +0 where it lives.
 VS_DEV void zero_in_place(float& x) { asm volatile("v_mov_b32 %0, 0" : "=v"(x)); }
+// Sets a register pair to +0 with one 64-bit move.
+VS_DEV void zero_pair(float& x, float& y) {
+    double z;
+    asm volatile("v_mov_b64 %0, 0" : "=v"(z));
+    const unsigned long long u = (unsigned long long)__double_as_longlong(z);
+    x = __uint_as_float((uint32_t)u);
+    y = __uint_as_float((uint32_t)(u >> 32));
+}
 
 VS_DEV float reduce_scatter10(const float v[10], uint32_t lane) {
     float w[5];
@@ -804,7 +812,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             // registers (a plain assignment makes the compiler rebuild the
             // zeros at every branch of the next splat's quadrant loop)
 #pragma unroll
-            for (int i = 0; i < 10; ++i) zero_in_place(g[i]);
+            for (int i = 0; i < 10; i += 2) zero_pair(g[i], g[i + 1]);
             val = ((as_u(scv.w) >> gate_shift) & 1u) ? val * comp_scale : 0.0f;
             const uint32_t gid_t = __builtin_amdgcn_readlane(gid, t);
             if ((lane & 3) == 0 && comp >= 0 && val != 0.0f)
