@@ -360,7 +360,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
     __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BATCH : 1];
     __shared__ float4 s_s[SURF ? FWD_BATCH * 4 : 1];
     __shared__ uint4 s_hit[BWD ? FWD_BATCH : 1];   // .x = 1 once the slot blended a pixel
-    __shared__ uint32_t s_list[FWD_BATCH];         // live slots as byte offsets (slot * 16)
+    __shared__ __align__(16) uint32_t s_list[FWD_BATCH];   // live slots as byte offsets (slot * 16)
 
     const uint32_t xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
     const uint32_t q = idx % 4;
@@ -433,8 +433,16 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         // the vector work the masked lanes would skip.
         for (uint32_t j0 = 0; j0 < nlist; j0 += 8u) {
           const uint32_t jn = min(j0 + 8u, nlist);
-          for (uint32_t j = j0; j < jn; ++j) {
-            const uint32_t off = s_list[j];
+          // the group's eight list entries in two 16-byte reads (entries past
+          // the list are never used)
+          const uint4 la = *reinterpret_cast<const uint4*>(&s_list[j0]);
+          const uint4 lb = *reinterpret_cast<const uint4*>(&s_list[j0 + 4u]);
+          const uint32_t offs[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
+#pragma unroll
+          for (uint32_t jj = 0; jj < 8u; ++jj) {
+            const uint32_t j = j0 + jj;
+            if (j >= jn) break;                       // uniform
+            const uint32_t off = offs[jj];
             const float4 sb = *reinterpret_cast<const float4*>(lds_b + off);
             float sigma, zs = 0.0f, G;
             bool valid = true;
