@@ -51,7 +51,7 @@ def test_camera_model_parity(cfg, view, model, mip):
     # take thin-prism terms in 1/z^3 and 1/z^4: their end-to-end gradients
     # amplify atomic-order noise beyond any bar, so only the projection stage
     # (every row, 1e-5) checks them.
-    bad = ill_conditioned_rows(ref, vc)
+    bad = ill_conditioned_rows(ref, vc, rg["v_combined"])
     assert bad.mean() < 0.01
     _check_param_grads(g, rg, ref, vc, exclude=bad)
 

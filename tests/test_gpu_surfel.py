@@ -108,7 +108,7 @@ def _check_surfel_grads(g, rg, ref, vc):
     vo = g.v_raw_opac.cpu().numpy()
     vr = g.v_refine_weight.cpu().numpy()
     assert np.isfinite(vt).all() and np.isfinite(vs).all()
-    keep = ~ill_conditioned_rows(ref, vc)
+    keep = ~ill_conditioned_rows(ref, vc, rg["v_combined"])
     for got, want, name in ((vt, rg["v_transforms"], "v_transforms"), (vo, rg["v_raw_opac"], "v_raw_opacity"),
                             (vs, rg["v_sh"].reshape(len(vt), -1), "v_sh"), (vr, rg["v_refine"], "v_refine_weight")):
         _check_grads(got[keep], want[keep], name, group_rtol=None)

@@ -682,10 +682,11 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
 
     // Pixel replay state, bwd/kernels/rasterize_backwards_planes.rs:194-209.
     // The reference carries the remaining colour S (3 channels) to form
-    // sum_c (T max(c,0) - S_c) v_c; only its projection D = S . v enters
-    // that sum, so a lane carries D per pixel: D -= vis (max(c,0) . v).
+    // v_alpha = (sum_c (T max(c,0) - S_c) v_c + v_t) / (1 - alpha); only
+    // D = S . v - v_t enters it, so a lane carries that per pixel:
+    // v_alpha = (T (max(c,0) . v) - D) / (1 - alpha), D -= vis (max(c,0) . v).
     float pcx[PX], pcy[PX], D[PX], T[PX];
-    float vr[PX], vg[PX], vb[PX], vt[PX], rscale[PX];
+    float vr[PX], vg[PX], vb[PX], rscale[PX];
     bool cot = false;   // a pixel of the lane has a nonzero (or non-finite) cotangent
 #pragma unroll
     for (int k = 0; k < PX; ++k) {
@@ -694,7 +695,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
         const uint32_t py = ty * TILE_W + 8 * (qk >> 1) + (lane >> 3);
         pcx[k] = (float)px + 0.5f;
         pcy[k] = (float)py + 0.5f;
-        D[k] = T[k] = vr[k] = vg[k] = vb[k] = vt[k] = rscale[k] = 0.0f;
+        D[k] = T[k] = vr[k] = vg[k] = vb[k] = rscale[k] = 0.0f;
         if (px < a.img_w && py < a.img_h) {
             const size_t base = ((size_t)py * a.img_w + px) * a.channels;
             const float4 o = *reinterpret_cast<const float4*>(a.out_img + base);
@@ -704,10 +705,10 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             const float sr = o.x - t_final * a.bg_r;
             const float sg = o.y - t_final * a.bg_g;
             const float sb = o.z - t_final * a.bg_b;
-            D[k] = sr * v.x + sg * v.y + sb * v.z;
+            const float vt = (v.w - (a.bg_r * v.x + a.bg_g * v.y + a.bg_b * v.z)) * t_final;
+            D[k] = (sr * v.x + sg * v.y + sb * v.z) - vt;
             T[k] = 1.0f;
             vr[k] = v.x; vg[k] = v.y; vb[k] = v.z;
-            vt[k] = (v.w - (a.bg_r * v.x + a.bg_g * v.y + a.bg_b * v.z)) * t_final;
             rscale[k] = __builtin_amdgcn_rcpf(mx(o.w, 1.0e-5f));
         }
     }
@@ -788,7 +789,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 g[7] = __builtin_fmaf(vis, vb[k], g[7]);
                 const float cv = __builtin_fmaf(cl_b, vb[k], __builtin_fmaf(cl_g, vg[k], cl_r * vr[k]));
                 const float ra = __builtin_amdgcn_rcpf(one_m);
-                const float v_ae = (__builtin_fmaf(Tk, cv, -D[k]) + vt[k]) * ra;
+                const float v_ae = __builtin_fmaf(Tk, cv, -D[k]) * ra;
                 const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
                 D[k] = __builtin_fmaf(-vis, cv, D[k]);
                 if (opac * G <= ALPHA_CAP) {
