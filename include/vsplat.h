@@ -305,6 +305,7 @@ void vs_fwd_state_free(vs_fwd_state* state);
  * not keep the sorted tile ids (its tile sort derives the ranges instead):
  * the first view of a state rebuilds them from the ranges on the context's
  * stream and waits for that. */
+#define VS_PROJ_ROW_FLOATS 16u   /* stride of the projected rows, in floats */
 typedef struct vs_state_view {
     uint32_t num_splats, num_visible, num_intersections, num_tiles, tile_bw, tile_bh;
     const uint32_t* isect_tiles;    /* [I] sorted tile ids (T = sentinel, sorts last) */
@@ -314,9 +315,11 @@ typedef struct vs_state_view {
     const uint32_t* compact_from_global; /* [N] g + 1 for splats past every cull, 0 if culled
                                        (RenderOutput state, render_aux.rs:36-41: the rows of
                                        vs_project_update's color_dir) */
-    const float* proj_xy_conic;     /* [N,4] x, y, c00, c01 (valid for visible splats) */
-    const float* proj_c11_opac_rg;  /* [N,4] c11, opacity, r, g */
-    const float* proj_b;            /* [N] b */
+    /* The projected rows: N rows of VS_PROJ_ROW_FLOATS floats (64 bytes), valid
+       for visible splats; the three pointers below point into row 0. */
+    const float* proj_xy_conic;     /* x, y, c00, c01 (floats 0-3 of each row) */
+    const float* proj_c11_opac_rg;  /* c11, opacity, r, g (floats 4-7) */
+    const float* proj_b;            /* b (float 8; float 9 holds logf(255 opacity)) */
     const float* proj_aux;          /* [N,4] z, nx, ny, nz (GEOMETRY) or NULL */
     const uint32_t* tile_ranges;    /* [T,2] before the forward shrank the ends */
     const float* proj_surf;         /* [N,16] surfels: M rows (9), low-pass centre (2), normal (3),

@@ -5,6 +5,8 @@ import ctypes as C
 
 import numpy as np
 
+from vauss_amd._lib import PROJ_ROW_FLOATS
+
 _HIP = None
 
 
@@ -60,6 +62,7 @@ def gpu_state_arrays(out):
     """Intermediate buffers of a GPU forward as numpy arrays keyed like the oracle's."""
     v = out.state.view()
     n, i = v.num_splats, v.listed_intersections
+    rows = dev_to_numpy(v.proj_xy_conic, (n, PROJ_ROW_FLOATS), np.float32)
     return {
         "view": v,
         "tile": dev_to_numpy(v.isect_tiles, (i,), np.uint32),
@@ -67,9 +70,11 @@ def gpu_state_arrays(out):
         "gid": dev_to_numpy(v.isect_gids, (i,), np.uint32),
         "counts": dev_to_numpy(v.intersect_counts, (n,), np.uint32),
         "listed_counts": dev_to_numpy(v.listed_counts, (n,), np.uint32),
-        "proj_a": dev_to_numpy(v.proj_xy_conic, (n, 4), np.float32),
-        "proj_b": dev_to_numpy(v.proj_c11_opac_rg, (n, 4), np.float32),
-        "proj_c": dev_to_numpy(v.proj_b, (n,), np.float32),
+        # the projected rows are 16 floats apart; the three views start inside row 0
+        "proj_a": rows[:, 0:4].copy(),
+        "proj_b": rows[:, 4:8].copy(),
+        "proj_c": rows[:, 8].copy(),
+        "proj_power": rows[:, 9].copy(),
         "proj_aux": dev_to_numpy(v.proj_aux, (n, 4), np.float32) if v.proj_aux else None,
         "ranges": dev_to_numpy(v.tile_ranges, (v.tile_bh, v.tile_bw, 2), np.uint32),
         "proj_surf": dev_to_numpy(v.proj_surf, (n, 16), np.float32) if v.proj_surf else None,

@@ -196,3 +196,10 @@ def test_rust_binding_declares_every_entry_point():
     assert set(rust) == set(header), (set(header) - set(rust), set(rust) - set(header))
     for name, n in header.items():
         assert rust[name] == n, (name, rust[name], n)
+
+
+def test_header_constants_match_the_bindings():
+    """The state view's projected-row stride, which a binding has to repeat."""
+    text = HEADER.read_text()
+    stride = int(re.search(r"#define VS_PROJ_ROW_FLOATS (\d+)u", text).group(1))
+    assert stride == _lib.PROJ_ROW_FLOATS == 16

@@ -55,6 +55,9 @@ def _check_forward(out, ref, gpu):
     got = np.concatenate([gpu["proj_a"][gfc], gpu["proj_b"][gfc], gpu["proj_c"][gfc, None]], axis=1)
     got = got[:, [0, 1, 2, 3, 4, 5, 6, 7, 8]]
     np.testing.assert_array_equal(got.view(np.uint32), proj.view(np.uint32))
+    # the row's footprint exponent, logf(255 opacity), which emission reads back
+    np.testing.assert_array_equal(gpu["proj_power"][gfc].view(np.uint32),
+                                  po.logf(proj[:, 5] * np.float32(255.0)).view(np.uint32))
     # the depth key of every visible splat is its raw view-z bits
     np.testing.assert_array_equal(gpu["depth_bits"][gfc], ref.get(po.F_DEPTHS).view(np.uint32))
     # aux outputs

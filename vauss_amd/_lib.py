@@ -31,6 +31,7 @@ MODE_DEFAULT, MODE_MIP, MODE_SURFEL = range(3)
 # stage bits of vs_ctx_enable_timing, in vs_stage_times field order
 TIME_STAGES = ("project", "emit", "sort", "ranges", "raster_fwd", "raster_bwd", "project_bwd", "other")
 TIME_ALL = (1 << len(TIME_STAGES)) - 1
+PROJ_ROW_FLOATS = 16   # VS_PROJ_ROW_FLOATS: stride of the state view's projected rows
 
 
 class VsCamera(C.Structure):

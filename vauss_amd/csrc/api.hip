@@ -117,9 +117,7 @@ struct vs_fwd_state {
     uint32_t* counts = nullptr;
     uint32_t* depth_bits = nullptr;
     uint32_t* compact = nullptr;  // [N] g + 1 past every cull, else 0
-    float4* proj_a = nullptr;
-    float4* proj_b = nullptr;
-    float* proj_c = nullptr;
+    float4* proj = nullptr;          // [N][PROJ_Q] projected rows
     float4* proj_aux = nullptr;
     float4* proj_surf = nullptr;  // [N][4] surfels: M rows, low-pass centre, normal
     float* opacities = nullptr;
@@ -698,7 +696,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
     const size_t o_counts = take((size_t)N * 4), o_depth = take((size_t)N * 4), o_compact = take((size_t)N * 4);
-    const size_t o_pa = take((size_t)N * 16), o_pb = take((size_t)N * 16), o_pc = take((size_t)N * 4);
+    const size_t o_proj = take((size_t)N * PROJ_Q * 16);
     const size_t o_aux = (geometry && !surfel) ? take((size_t)N * 16) : 0;
     const size_t o_surf = surfel ? take((size_t)N * 64) : 0;
     const size_t o_opac = out->opacities ? 0 : take((size_t)N * 4);
@@ -713,9 +711,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
     st->counts = reinterpret_cast<uint32_t*>(base + o_counts);
     st->depth_bits = reinterpret_cast<uint32_t*>(base + o_depth);
     st->compact = reinterpret_cast<uint32_t*>(base + o_compact);
-    st->proj_a = reinterpret_cast<float4*>(base + o_pa);
-    st->proj_b = reinterpret_cast<float4*>(base + o_pb);
-    st->proj_c = reinterpret_cast<float*>(base + o_pc);
+    st->proj = reinterpret_cast<float4*>(base + o_proj);
     st->proj_aux = (geometry && !surfel) ? reinterpret_cast<float4*>(base + o_aux) : nullptr;
     st->proj_surf = surfel ? reinterpret_cast<float4*>(base + o_surf) : nullptr;
     st->opacities = out->opacities ? out->opacities : reinterpret_cast<float*>(base + o_opac);
@@ -736,7 +732,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         pa.num_splats = N; pa.sh_degree = sp->sh_degree; pa.log_scale_offset = sp->log_scale_offset;
         pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.min_scale = st->min_scale; pa.mip = st->mip; pa.decoder = sp->decoder; pa.raw_opac = sp->raw_opacities;
         pa.opacities = st->opacities; pa.max_radius = st->max_radius; pa.counts = st->counts;
-        pa.depth_bits = st->depth_bits; pa.proj_a = st->proj_a; pa.proj_b = st->proj_b; pa.proj_c = st->proj_c;
+        pa.depth_bits = st->depth_bits; pa.proj = st->proj;
         pa.proj_aux = st->proj_aux; pa.proj_surf = st->proj_surf; pa.compact = st->compact; pa.block_stats = st->block_stats;
         pa.visible = bwd_info ? st->visible : nullptr;   // cleared by the projection
         pa.ranges = st->ranges; pa.num_tiles = T;         // initialised by the projection
@@ -832,14 +828,14 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
             CutArgs ka{};
             ka.num_splats = N; ka.tile_bw = st->tbw; ka.tile_bh = st->tbh;
             ka.counts = st->counts; ka.depth_bits = st->depth_bits; ka.counters = st->counters;
-            ka.proj_a = st->proj_a; ka.proj_b = st->proj_b;
+            ka.proj = st->proj;
             ka.mass = cut_mass; ka.cut = cut_tile; ka.allow = cut_allow;
             VS_HIP(launch_fill_u32(cut_mass, 0u, cut_words, s), "zero cutoff masses");
             VS_HIP(launch_cut_mass(ka, s), "cutoff masses");
             VS_HIP(launch_cut_rows(ka, s), "cutoff bins");
             EmitArgs ca{};
             ca.num_splats = N; ca.tile_bw = st->tbw; ca.tile_bh = st->tbh;
-            ca.counts = st->counts; ca.proj_a = st->proj_a; ca.proj_b = st->proj_b;
+            ca.counts = st->counts; ca.proj = st->proj;
             ca.cut = cut_tile; ca.allow = cut_allow; ca.depth_bits = st->depth_bits; ca.counters = st->counters;
             ca.counts_out = st->kept_counts;
             VS_HIP(launch_count_kept(ca, s), "cutoff counts");
@@ -871,7 +867,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
             ea.num_emitters = M; ea.m_dev = m_dev; ea.order = order;
             ea.counts = slot_counts; ea.slot_base = slot_base; ea.slot_base_g = slot_base_g;
             ea.zero = tile_zero.ptr; ea.zero_words = tile_zero.words;      // the tile sort's one-sweep state
-            ea.proj_a = st->proj_a; ea.proj_b = st->proj_b; ea.tiles = tiles_u; ea.vals = vals_u; ea.capacity = I;
+            ea.proj = st->proj; ea.tiles = tiles_u; ea.vals = vals_u; ea.capacity = I;
             if (cutoff) {
                 ea.cut = cut_tile; ea.allow = cut_allow; ea.depth_bits = st->depth_bits; ea.counters = st->counters;
                 ea.listed = st->listed;
@@ -917,7 +913,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         ra.bg_r = background[0]; ra.bg_g = background[1]; ra.bg_b = background[2];
         ra.gids = st->gids; ra.ranges = st->ranges; ra.ranges_shrunk = st->ranges_shrunk;
         ra.aux_ranges = bwd_info ? out->tile_offsets : nullptr;
-        ra.proj_a = st->proj_a; ra.proj_b = st->proj_b; ra.proj_c = st->proj_c; ra.proj_aux = st->proj_aux;
+        ra.proj = st->proj; ra.proj_aux = st->proj_aux;
         // surfels outside training take the median by the surface criterion (gaussian_splats.rs:100-106)
         ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass_surface_criterion(pass)) ? 1u : 0u;
         ra.out = out->out_img; ra.visible = st->visible;
@@ -992,7 +988,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             rb.order = st->tile_order;
             rb.bg_r = st->bg[0]; rb.bg_g = st->bg[1]; rb.bg_b = st->bg[2];
             rb.gids = st->gids; rb.ranges = st->ranges_shrunk;
-            rb.proj_a = st->proj_a; rb.proj_b = st->proj_b; rb.proj_c = st->proj_c;
+            rb.proj = st->proj;
             rb.out_img = out_img; rb.v_out = v_out;
             rb.channels = (pass_geometry(st->pass) || st->surfel) ? 12u : 4u;
             rb.proj_surf = st->proj_surf;
@@ -1209,9 +1205,10 @@ extern "C" vs_status vs_fwd_state_view(const vs_fwd_state* st, vs_state_view* o)
     o->isect_tiles = st->tiles; o->isect_gids = st->gids; o->intersect_counts = st->counts;
     o->depth_bits = st->depth_bits;
     o->compact_from_global = st->compact;
-    o->proj_xy_conic = reinterpret_cast<const float*>(st->proj_a);
-    o->proj_c11_opac_rg = reinterpret_cast<const float*>(st->proj_b);
-    o->proj_b = st->proj_c;
+    // views into the 64-byte rows (VS_PROJ_ROW_FLOATS floats apart)
+    o->proj_xy_conic = reinterpret_cast<const float*>(st->proj);
+    o->proj_c11_opac_rg = reinterpret_cast<const float*>(st->proj) + 4;
+    o->proj_b = reinterpret_cast<const float*>(st->proj) + 8;
     o->proj_aux = reinterpret_cast<const float*>(st->proj_aux);
     o->proj_surf = reinterpret_cast<const float*>(st->proj_surf);
     o->tile_ranges = st->ranges;

@@ -561,9 +561,10 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
             } else {
                 col = load_color<DEG>(static_cast<const SHT*>(a.sh), g, mean, u);
             }
-            a.proj_a[g] = make_float4(px, py, conic.c00, conic.c01);
-            a.proj_b[g] = make_float4(conic.c11, opac, col.x, col.y);
-            a.proj_c[g] = col.z;
+            float4* row = a.proj + (size_t)g * PROJ_Q;
+            row[0] = make_float4(px, py, conic.c00, conic.c01);
+            row[1] = make_float4(conic.c11, opac, col.x, col.y);
+            row[2] = make_float4(col.z, power, 0.0f, 0.0f);
             if constexpr (MODEL == SURFEL_MODEL) {
                 // project_visible.rs:231-273: M rows, the low-pass centre (the
                 // pinhole projection of the centre) and the camera-facing normal
@@ -705,12 +706,14 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     TileBox bb{0, 0, 0, 0};
     uint32_t bin = 0u;
     if (cnt > 0) {
-        // Recompute the box from the projected row as kernels/map_gaussians.rs:61-66 does.
-        const float4 pa = a.proj_a[g];
-        const float4 pb = a.proj_b[g];
+        // Recompute the box from the projected row as kernels/map_gaussians.rs:61-66 does
+        // (power = logf(255 opacity) as the projection computed it).
+        const float4* row = a.proj + (size_t)g * PROJ_Q;
+        const float4 pa = row[0];
+        const float c11 = row[1].x;
+        power = row[2].y;
         px = pa.x; py = pa.y;
-        conic = S2{pa.z, pa.w, pb.x};
-        power = logf_c(pb.y * 255.0f);
+        conic = S2{pa.z, pa.w, c11};
         float ex, ey;
         bbox_extent(conic, power, ex, ey);
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
@@ -771,8 +774,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
     uint32_t m = 0u, bin = 0u;
     TileBox bb{0, 0, 0, 0};
     if (has) {
-        const float4 pa = a.proj_a[g];
-        const float4 pb = a.proj_b[g];
+        const float4 pa = a.proj[(size_t)g * PROJ_Q], pb = a.proj[(size_t)g * PROJ_Q + 1];
         px = pa.x; py = pa.y;
         cf = S2{pa.z, pa.w, pb.x};
         const float opac = pb.y, ac = CUT_LEVEL * __builtin_fminf(opac, ALPHA_CAP);
@@ -879,11 +881,11 @@ __global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
     TileBox bb{0, 0, 0, 0};
     uint32_t bin = 0u;
     if (cnt > 0) {
-        const float4 pa = a.proj_a[g];
-        const float4 pb = a.proj_b[g];
+        const float4* row = a.proj + (size_t)g * PROJ_Q;
+        const float4 pa = row[0];
         px = pa.x; py = pa.y;
-        conic = S2{pa.z, pa.w, pb.x};
-        power = logf_c(pb.y * 255.0f);
+        conic = S2{pa.z, pa.w, row[1].x};
+        power = row[2].y;
         float ex, ey;
         bbox_extent(conic, power, ex, ey);
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);

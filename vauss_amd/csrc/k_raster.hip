@@ -398,14 +398,16 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         __syncthreads();                              // the previous batch's LDS reads are complete
         if constexpr (BWD) s_hit[l].x = 0u;
         if (gid < a.num_splats) {   // else: past the batch, or a corrupt id (dead slot)
-            const float4 pa = a.proj_a[gid];
-            const float4 pb = a.proj_b[gid];
+            const float4* row = a.proj + (size_t)gid * PROJ_Q;
+            const float4 pa = row[0];
+            const float4 pb = row[1];
+            const float cb = row[2].x;
             // the conic in base-2 units: sigma log2 e comes out of the same fma chain
             const float4 sa = make_float4(pa.x, pa.y, (0.5f * pa.z) * LOG2E_F, pa.w * LOG2E_F);
             const float4 sb = make_float4((0.5f * pb.x) * LOG2E_F, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
             s_a[l] = sa;
             s_b[l] = sb;
-            s_c[l].x = mx(a.proj_c[gid], 0.0f);
+            s_c[l].x = mx(cb, 0.0f);
             if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
             if constexpr (SURF) {
                 const float4* ps = a.proj_surf + (size_t)gid * 4;
@@ -457,7 +459,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                 const float4 sa = *reinterpret_cast<const float4*>(lds_a + off);
                 const float dx = pcx - sa.x, dy = pcy - sa.y;
                 sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);   // base 2
-                G = exp2n(-sigma);
+                G = exp2n_live(-sigma);
             }
             // min(0.999, .) of a product that is NaN only when sigma is
             // (then the sigma test below rejects the pair): same value as mn().
@@ -740,12 +742,13 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
         // keeps mask 0: no quadrant).
         uint32_t mask = 0u;
         if (gid < a.num_splats) {
-            const float4 pa = a.proj_a[gid];
-            const float4 pb = a.proj_b[gid];
+            const float4* row = a.proj + (size_t)gid * PROJ_Q;
+            const float4 pa = row[0];
+            const float4 pb = row[1];
+            const float cb = row[2].x;
             // the forward's base-2 conic for the replay; c00, c01, c11 for the gradients
             const float4 sa = make_float4(pa.x, pa.y, (0.5f * pa.z) * LOG2E_F, pa.w * LOG2E_F);
             const float c2 = (0.5f * pb.x) * LOG2E_F;
-            const float cb = a.proj_c[gid];
             const uint32_t gates = (pb.z >= 0.0f ? 1u : 0u) | (pb.w >= 0.0f ? 2u : 0u) | (cb >= 0.0f ? 4u : 0u) | 8u;
             s_a[lane] = sa;
             s_b[lane] = make_float4(c2, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
@@ -772,7 +775,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 if (!(Tk > T_STOP)) continue;
                 const float dx = pcx[k] - sa.x, dy = pcy[k] - sa.y;
                 const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);   // base 2, as the forward's
-                const float G = exp2n(-sigma);
+                const float G = exp2n_live(-sigma);
                 const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);   // == mn(): see the forward
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
                 if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -912,8 +915,8 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
                 if (q == 3) row.w = 1.0f / a.proj_surf[(size_t)gid * 4 + 2].x;   // 1 / M[2][2] in the pad slot
                 s_s[4 * lane + q] = row;
                 if (q == 0) {
-                    const float4 pb = a.proj_b[gid];
-                    const float cb_ = a.proj_c[gid];
+                    const float4 pb = a.proj[(size_t)gid * PROJ_Q + 1];
+                    const float cb_ = a.proj[(size_t)gid * PROJ_Q + 2].x;
                     s_b[lane] = make_float4(pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f), mx(cb_, 0.0f));
                     s_gate[lane] = (pb.z >= 0.0f ? 1u : 0u) | (pb.w >= 0.0f ? 2u : 0u) | (cb_ >= 0.0f ? 4u : 0u);
                     s_gid[lane] = gid;

@@ -79,6 +79,27 @@ VS_DEV float exp2n(float x) {
     return __builtin_ldexpf(p, (int)n);
 }
 
+// exp2n without the clamp at -127, for the gaussian compositing loops.  There
+// x = -sigma is finite: the conic is the inverse of a 2-D covariance that
+// carries the low-pass term on its diagonal (0.3 px^2, 0.1 with the Mip
+// filter), so its entries are at most 10 in magnitude, and a listed pair's
+// pixel lies within the splat's extent of its centre, so no product in sigma
+// overflows.  For x >= -127 both functions
+// compute the same bits.  Below -127 both return less than 2^-126, so
+// opacity x G stays under every cutoff (1/255 - 5e-4 at the lowest) and the
+// pair is rejected by either function.  What a pixel composites is
+// therefore unchanged.
+VS_DEV float exp2n_live(float x) {
+    const float n = __builtin_rintf(x);
+    const float f = x - n;
+    float p = __builtin_fmaf(1.326472731e-03f, f, 9.671512991e-03f);
+    p = __builtin_fmaf(p, f, 5.550733581e-02f);
+    p = __builtin_fmaf(p, f, 2.402224243e-01f);
+    p = __builtin_fmaf(p, f, 6.931470037e-01f);
+    p = __builtin_fmaf(p, f, 1.0f);
+    return __builtin_ldexpf(p, (int)n);
+}
+
 // log: m = x 2^-e in [sqrt(1/2), sqrt(2)), s = (m-1)/(m+1),
 // ln m = 2s + s^3 (2/3 + 2/5 s^2 + 2/7 s^4 + 2/9 s^6), ln x = e ln2 + ln m.
 VS_DEV float logf_c(float x) {

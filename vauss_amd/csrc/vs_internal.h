@@ -36,6 +36,13 @@ enum : uint32_t {
     CTX_FLAGS = 4,
 };
 
+// A projected splat's row: four float4, one aligned 64-byte segment, so the
+// emission and raster gathers touch one segment per splat (three planes of
+// 16 + 16 + 4 bytes touched three):
+//   q0 = x, y, c00, c01    q1 = c11, opacity, r, g    q2 = b, power, 0, 0    q3 unused
+// power = logf(255 opacity), the exponent bound of the tile footprint.
+constexpr uint32_t PROJ_Q = 4;
+
 struct ProjectArgs {
     vs_camera cam;
     uint32_t img_w, img_h, tile_bw, tile_bh;
@@ -53,9 +60,7 @@ struct ProjectArgs {
     float* max_radius;          // [N]
     uint32_t* counts;           // [N] tiles hit
     uint32_t* depth_bits;       // [N] raw f32 bits of view z
-    float4* proj_a;             // [N] x, y, c00, c01
-    float4* proj_b;             // [N] c11, opacity, r, g
-    float* proj_c;              // [N] b
+    float4* proj;               // [N][PROJ_Q] projected rows (layout above)
     float4* proj_aux;           // [N] z, nx, ny, nz (geometry) or null
     float4* proj_surf;          // [N][4] surfels: M rows, low-pass centre, normal (vs_surfel.h layout), or null
     uint32_t* compact;          // [N] g + 1 for splats past every cull, else 0 (compact_from_global)
@@ -87,8 +92,7 @@ struct EmitArgs {
     const uint32_t* counts;          // [N]
     const uint32_t* slot_base;       // [M + 1] first slot of the j-th nearest emitter (exclusive scan), then the total
     const uint32_t* slot_base_g;     // [N] the same, at the global id (emitters only)
-    const float4* proj_a;
-    const float4* proj_b;
+    const float4* proj;              // [N][PROJ_Q] projected rows
     uint32_t* tiles;                 // [capacity] tile id (T = sentinel)
     uint32_t* vals;                  // [capacity] global id
     uint32_t capacity;               // slots at or past it are dropped (the farthest splats' pairs)
@@ -116,8 +120,7 @@ struct CutArgs {
     const uint32_t* counts;          // [N] tiles per splat (0: not listed anywhere)
     const uint32_t* depth_bits;      // [N]
     const uint32_t* counters;        // depth range
-    const float4* proj_a;
-    const float4* proj_b;
+    const float4* proj;              // [N][PROJ_Q] projected rows
     uint32_t* mass;                  // [bh][CUT_BINS][bw + 1] fixed-point mass differences along each row
     uint8_t* cut;                    // [T]
     uint16_t* allow;                 // [bh][CUT_BINS][bw + 1]
@@ -132,9 +135,7 @@ struct RasterArgs {
     const uint32_t* ranges;          // [T,2]
     uint32_t* ranges_shrunk;         // [T,2] written by bwd-info passes (may alias nothing else)
     uint32_t* aux_ranges;            // [T,2] the caller's copy of the shrunk ranges (bwd-info passes), or null
-    const float4* proj_a;
-    const float4* proj_b;
-    const float* proj_c;
+    const float4* proj;              // [N][PROJ_Q] projected rows
     const float4* proj_aux;
     const float4* proj_surf;         // [N][4] surfels (vs_surfel.h layout) or null
     uint32_t surf_crit;              // surfels outside training: median by the surface criterion
@@ -149,9 +150,7 @@ struct RasterBwdArgs {
     float bg_r, bg_g, bg_b;
     const uint32_t* gids;
     const uint32_t* ranges;          // shrunk ranges
-    const float4* proj_a;
-    const float4* proj_b;
-    const float* proj_c;
+    const float4* proj;              // [N][PROJ_Q] projected rows
     const float4* proj_surf;         // [N][4] surfels, or null
     const float* out_img;            // [H,W,C]
     const float* v_out;              // [H,W,C]
