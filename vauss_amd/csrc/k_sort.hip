@@ -250,21 +250,25 @@ constexpr uint32_t ONESWEEP_MAX_KEYS = 1u << 30;       // counts fit the 30-bit 
 constexpr uint32_t OS_AGGREGATE = 1u << 30;            // status: this tile's own count
 constexpr uint32_t OS_PREFIX = 2u << 30;               // status: count of this tile and all before it
 constexpr uint32_t OS_VALUE = (1u << 30) - 1u;
-constexpr int MAX_PASSES = 8;
 constexpr int LOOKBACK = VS_LOOKBACK;                  // predecessor statuses read per look-back step
 constexpr uint32_t HIST_BLOCKS = VS_HIST_BLOCKS;
 constexpr int HIST_ITEMS = 16;       // keys per lane in flight per chunk (the kernel is latency-bound below that)
 
-// Digit histograms of every pass in one read: ghist[p][d] (zeroed by the caller).
-// Each wavefront takes chunks of HIST_ITEMS x 64 consecutive keys.
+// Digit histograms of every pass in one read: ghist[x][p][d] (zeroed by the
+// caller), one copy per XCD x = block index mod 8 (the XCD the block runs on),
+// so the blocks' closing atomics spread over eight sets of addresses; a pass
+// sums the eight copies of a digit.  Each wavefront takes chunks of
+// HIST_ITEMS x 64 consecutive keys.
+constexpr uint32_t HIST_COPIES = 8;
 template <typename K>
 __global__ void __launch_bounds__(SORT_BLOCK) sort_histogram_kernel(const K* __restrict__ keys, uint32_t n_cap,
                                                                     const uint32_t* __restrict__ n_dev, uint32_t first_bit,
                                                                     uint32_t passes, uint32_t* __restrict__ ghist) {
-    __shared__ uint32_t h[SORT_WAVES][MAX_PASSES][256];
+    constexpr int HP = sizeof(K);           // passes of 8-bit digits a key can need
+    __shared__ uint32_t h[SORT_WAVES][HP][256];
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (uint32_t i = threadIdx.x; i < SORT_WAVES * MAX_PASSES * 256; i += SORT_BLOCK) (&h[0][0][0])[i] = 0;
+    for (uint32_t i = threadIdx.x; i < SORT_WAVES * HP * 256; i += SORT_BLOCK) (&h[0][0][0])[i] = 0;
     __syncthreads();
     const uint64_t stride = (uint64_t)gridDim.x * SORT_WAVES * 64 * HIST_ITEMS;
     for (uint64_t c = ((uint64_t)blockIdx.x * SORT_WAVES + wave) * 64 * HIST_ITEMS; c < n; c += stride) {
@@ -283,11 +287,12 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_histogram_kernel(const K* __r
         }
     }
     __syncthreads();
+    uint32_t* mine = ghist + (size_t)(blockIdx.x % HIST_COPIES) * passes * 256;
     for (uint32_t i = threadIdx.x; i < passes * 256; i += SORT_BLOCK) {
         uint32_t c = 0;
 #pragma unroll
         for (int w = 0; w < SORT_WAVES; ++w) c += (&h[w][0][0])[i];
-        if (c) atomicAdd(&ghist[i], c);
+        if (c) atomicAdd(&mine[i], c);
     }
 }
 
@@ -304,7 +309,8 @@ template <typename K, int BLOCK, int ITEMS>
 __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                                                                    K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
                                                                    uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
-                                                                   const uint32_t* __restrict__ ghist, uint32_t* status,
+                                                                   const uint32_t* __restrict__ ghist, uint32_t ghist_copy_stride,
+                                                                   uint32_t* status,
                                                                    uint32_t* err, uint32_t spin_limit,
                                                                    uint32_t* __restrict__ ranges, uint32_t num_tiles) {
     constexpr uint32_t TILE = BLOCK * ITEMS;
@@ -368,7 +374,11 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
     // global exclusive start of digit d: sum of ghist[0..d) (block scan over 256)
     {
         const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const uint32_t c = d < 256 ? ghist[d] : 0u;
+        uint32_t c = 0u;
+        if (d < 256) {
+#pragma unroll
+            for (uint32_t x = 0; x < HIST_COPIES; ++x) c += ghist[(size_t)x * ghist_copy_stride + d];
+        }
         uint32_t incl = c;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -420,7 +430,7 @@ size_t sort_tmp_bytes(uint64_t n, bool key64) {
     b += align_up(scan_tmp_words(nblocks * 256) * 4, 256);
     // one-sweep: histograms and per-pass tile status
     const uint64_t os_tiles = (n + OS_MIN_TILE - 1) / OS_MIN_TILE;
-    b += align_up((size_t)max_passes * 256 * 4 + 64 + (size_t)max_passes * os_tiles * 256 * 4, 256);
+    b += align_up((size_t)HIST_COPIES * max_passes * 256 * 4 + 64 + (size_t)max_passes * os_tiles * 256 * 4, 256);
     return b + 256;
 }
 
@@ -446,11 +456,12 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
     const bool small = n < OS_SMALL_N;
     const uint32_t os_tile = small ? OS_SMALL_TILE : OS_TILE;
     const uint32_t os_tiles = (n + os_tile - 1) / os_tile;
-    uint32_t* ghist = reinterpret_cast<uint32_t*>(p);          // [passes][256]
-    uint32_t* status = ghist + passes * 256 + 16;              // [passes][os_tiles][256]
+    uint32_t* ghist = reinterpret_cast<uint32_t*>(p);          // [HIST_COPIES][passes][256]
+    uint32_t* status = ghist + HIST_COPIES * passes * 256 + 16; // [passes][os_tiles][256]
     if (onesweep) {
         hipError_t e = hipSuccess;
-        if (!state_zeroed) e = launch_fill_u32(ghist, 0u, (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
+        if (!state_zeroed)
+            e = launch_fill_u32(ghist, 0u, (uint64_t)HIST_COPIES * passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
         if (e != hipSuccess) return e;
         // ~4k keys per block up to HIST_BLOCKS blocks: each block ends with
         // passes x 256 global atomics, so a grid much wider than the data
@@ -474,11 +485,11 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         if (onesweep) {
             if (small)
                 sort_onesweep_kernel<K, OS_SMALL_BLOCK, OS_SMALL_ITEMS><<<os_tiles, OS_SMALL_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err,
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, passes * 256, status + (size_t)pass * os_tiles * 256, err,
                     spin_limit, rng, nt);
             else
                 sort_onesweep_kernel<K, OS_BLOCK, OS_ITEMS><<<os_tiles, OS_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, status + (size_t)pass * os_tiles * 256, err,
+                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, passes * 256, status + (size_t)pass * os_tiles * 256, err,
                     spin_limit, rng, nt);
             if (rng) tr->done = true;
             e = hipGetLastError();
@@ -525,7 +536,8 @@ SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, vo
     p += align_up(scan_tmp_words((uint64_t)nblocks * 256) * 4, 256);
     const uint32_t os_tile = n < OS_SMALL_N ? OS_SMALL_TILE : OS_TILE;
     const uint64_t os_tiles = (n + os_tile - 1) / os_tile;
-    return SortZeroSpan{reinterpret_cast<uint32_t*>(p), (uint64_t)passes * 256 + 16 + (uint64_t)passes * os_tiles * 256};
+    return SortZeroSpan{reinterpret_cast<uint32_t*>(p),
+                        (uint64_t)HIST_COPIES * passes * 256 + 16 + (uint64_t)passes * os_tiles * 256};
 }
 
 } // namespace vs
