@@ -190,12 +190,21 @@ VS_DEV float edge_min(float a, float b, float c, float k, float u, float lo, flo
     return (a * u + b * t) * u + c * t * t;
 }
 
+// The dead-quadrant bound (1.01 ln(opac / c) + 0.01) log2 e from the row's
+// power = ln(255 opac): ln(opac / c) = power for c = 1/255 (up to a few ulp,
+// far inside the 0.01 margin) and power + ln(1 / (255 c)) = power + 0.13640
+// for the smooth cutoff's c = 1/255 - 5e-4 (0.1365 rounds that up).
+constexpr float QUAD_SMOOTH_SHIFT = 0.1365f;
+VS_DEV float quad_threshold(float power, bool smooth) {
+    return (QUAD_MARGIN_REL * (smooth ? power + QUAD_SMOOTH_SHIFT : power) + QUAD_MARGIN_ABS) * LOG2E_F;
+}
+
 // Bit q (q = qy * 2 + qx) set when quadrant q of the tile whose first pixel
-// centre is (x0, y0) may hold a pixel that passes the cutoff.
-VS_DEV uint32_t quadrant_mask(float x0, float y0, float mx_, float my_, float A, float B, float C, float opac,
+// centre is (x0, y0) may hold a pixel that passes the cutoff (power: the
+// row's ln(255 opacity)).
+VS_DEV uint32_t quadrant_mask(float x0, float y0, float mx_, float my_, float A, float B, float C, float power,
                               bool smooth) {
-    const float cut = smooth ? (ALPHA_MID - 0.5f * ALPHA_BAND) : ALPHA_MID;
-    const float thr = (QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS) * LOG2E_F;
+    const float thr = quad_threshold(power, smooth);
     const float four_ac = 4.0f * A * C;
     if (!(A > 0.0f && C > 0.0f && four_ac - B * B > QUAD_MIN_DECORR * four_ac && thr < 3.0e38f)) return 0xFu;
     const float kx = -B / (2.0f * C);   // vertical edges: dy* = kx dx
@@ -215,9 +224,8 @@ VS_DEV uint32_t quadrant_mask(float x0, float y0, float mx_, float my_, float A,
 
 // The same test for one quadrant whose first pixel centre is (x0, y0): true
 // when some pixel of its 8 x 8 block may pass the cutoff.
-VS_DEV bool quadrant_live(float x0, float y0, float mx_, float my_, float A, float B, float C, float opac, bool smooth) {
-    const float cut = smooth ? (ALPHA_MID - 0.5f * ALPHA_BAND) : ALPHA_MID;
-    const float thr = (QUAD_MARGIN_REL * logf_c(opac / cut) + QUAD_MARGIN_ABS) * LOG2E_F;
+VS_DEV bool quadrant_live(float x0, float y0, float mx_, float my_, float A, float B, float C, float power, bool smooth) {
+    const float thr = quad_threshold(power, smooth);
     const float four_ac = 4.0f * A * C;
     if (!(A > 0.0f && C > 0.0f && four_ac - B * B > QUAD_MIN_DECORR * four_ac && thr < 3.0e38f)) return true;
     const float kx = -B / (2.0f * C);
@@ -401,7 +409,8 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             const float4* row = a.proj + (size_t)gid * PROJ_Q;
             const float4 pa = row[0];
             const float4 pb = row[1];
-            const float cb = row[2].x;
+            const float4 pc = row[2];
+            const float cb = pc.x;
             // the conic in base-2 units: sigma log2 e comes out of the same fma chain
             const float4 sa = make_float4(pa.x, pa.y, (0.5f * pa.z) * LOG2E_F, pa.w * LOG2E_F);
             const float4 sb = make_float4((0.5f * pb.x) * LOG2E_F, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
@@ -416,7 +425,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                 for (int k = 0; k < 4; ++k) { r[k] = ps[k]; s_s[4 * l + k] = r[k]; }
                 live = surfel_quadrant_live(x0, y0, r[0], r[1], r[2], pb.y, SMOOTH);
             } else {
-                live = quadrant_live(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, SMOOTH);
+                live = quadrant_live(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, pc.y, SMOOTH);
             }
         }
         // the live slots in slot (= depth) order: the mask is walked in
@@ -745,7 +754,8 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             const float4* row = a.proj + (size_t)gid * PROJ_Q;
             const float4 pa = row[0];
             const float4 pb = row[1];
-            const float cb = row[2].x;
+            const float4 pc = row[2];
+            const float cb = pc.x;
             // the forward's base-2 conic for the replay; c00, c01, c11 for the gradients
             const float4 sa = make_float4(pa.x, pa.y, (0.5f * pa.z) * LOG2E_F, pa.w * LOG2E_F);
             const float c2 = (0.5f * pb.x) * LOG2E_F;
@@ -755,7 +765,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             s_c[lane] = make_float4(mx(cb, 0.0f), pa.z, pb.x, as_f(gates));
             s_d[lane] = make_float4(pa.z * img_w, pa.w * img_w, pa.w * img_h, pb.x * img_h);
             s_c01[lane] = pa.w;
-            mask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, c2, pb.y, SMOOTH);
+            mask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, c2, pc.y, SMOOTH);
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {
