@@ -188,30 +188,55 @@ VS_DEV void row_interior(float px, float py, S2 cf, double P, uint32_t ty, uint3
     if (ci < cj) { ia = (uint32_t)ci; ib = (uint32_t)cj; }
 }
 
-// Tile-x ranges of row ty of a splat's box: [oa, ob) may pass, [ia, ib) must.
-VS_DEV void row_ranges(float px, float py, S2 cf, float power, uint4 box, uint32_t ty, uint32_t& oa, uint32_t& ia,
-                       uint32_t& ib, uint32_t& ob) {
+// The per-splat terms of the row ranges, formed once per splat and handed to
+// the lanes that walk its rows.
+struct RangeK { double det, inva, two_a_pout, ey, kx, two_a_pin; };
+VS_DEV RangeK range_consts(S2 cf, float power) {
+    const double a = cf.c00, b = cf.c01, c = cf.c11, P = power;
+    RangeK k;
+    k.det = a * c - b * b;
+    k.inva = 1.0 / a;
+    const double p_out = P * 1.004 + 1e-4;
+    const double ex = sqrt(2.0 * c * p_out / k.det);
+    k.ey = sqrt(2.0 * a * p_out / k.det);
+    k.two_a_pout = 2.0 * a * p_out;
+    k.kx = b * ex / c;                  // -b ex / c is its exact negation
+    const double p_in = P * 0.996 - 1e-4;
+    k.two_a_pin = (p_in > 0.0) ? 2.0 * a * p_in : __builtin_nan("");   // NaN: no interior chord
+    return k;
+}
+VS_DEV RangeK shfl_k(const RangeK& k, uint32_t src) {
+    const int s = (int)src;
+    return RangeK{__shfl(k.det, s), __shfl(k.inva, s), __shfl(k.two_a_pout, s), __shfl(k.ey, s), __shfl(k.kx, s),
+                  __shfl(k.two_a_pin, s)};
+}
+
+// Tile-x ranges of row ty of a splat's box: [oa, ob) may pass, [ia, ib) must
+// (b = c01, k: the splat's range_consts).
+VS_DEV void row_ranges_k(float px, float py, double b, const RangeK& k, uint4 box, uint32_t ty, uint32_t& oa,
+                         uint32_t& ia, uint32_t& ib, uint32_t& ob) {
     const uint32_t x0 = box.x, x1 = box.y;
     oa = x0; ob = x1; ia = ib = x1;
     if (!box.w) return;
-    const double a = cf.c00, b = cf.c01, c = cf.c11, P = power;
-    const double det = a * c - b * b, inva = 1.0 / a;
     const double mx_ = px, my_ = py;
-    const double p_out = P * 1.004 + 1e-4;
-    const double ex = sqrt(2.0 * c * p_out / det), ey = sqrt(2.0 * a * p_out / det);
-    // outer: the ellipse's x-extent over the row band (widened by BAND_OUT);
-    // its rightmost point is at dy = -b ex / c, its leftmost at +b ex / c
     const double d0 = (double)(ty * TILE_W) - my_ - BAND_OUT, d1 = d0 + (double)TILE_W + 2.0 * BAND_OUT;
-    const double lo = fmax(d0, -ey), hi = fmin(d1, ey);
+    const double lo = fmax(d0, -k.ey), hi = fmin(d1, k.ey);
     if (!(lo <= hi)) { oa = ob = x0; ia = ib = x0; return; }
     double l, r, t;
-    chord(a, b, det, inva, 2.0 * a * p_out, fmin(fmax(b * ex / c, lo), hi), l, t, true);
-    chord(a, b, det, inva, 2.0 * a * p_out, fmin(fmax(-b * ex / c, lo), hi), t, r, true);
+    chord(0.0, b, k.det, k.inva, k.two_a_pout, fmin(fmax(k.kx, lo), hi), l, t, true);
+    chord(0.0, b, k.det, k.inva, k.two_a_pout, fmin(fmax(-k.kx, lo), hi), t, r, true);
     const double fo = floor((mx_ + l - BAND_OUT) / TILE_W), fe = floor((mx_ + r + BAND_OUT) / TILE_W) + 1.0;
     oa = (uint32_t)fmin(fmax(fo, (double)x0), (double)x1);
     ob = (uint32_t)fmin(fmax(fe, (double)oa), (double)x1);
     ia = ib = ob;
-    row_interior(px, py, cf, P, ty, oa, ob, ia, ib);
+    // the interior range (row_interior)
+    const double e0 = (double)(ty * TILE_W) - my_ - BAND_IN, e1 = e0 + (double)TILE_W + 2.0 * BAND_IN;
+    double l0, r0, l1, r1;
+    if (!chord(0.0, b, k.det, k.inva, k.two_a_pin, e0, l0, r0) || !chord(0.0, b, k.det, k.inva, k.two_a_pin, e1, l1, r1))
+        return;
+    const double fi = ceil((mx_ + fmax(l0, l1) + BAND_IN) / TILE_W), fj = floor((mx_ + fmin(r0, r1) - BAND_IN) / TILE_W);
+    const double ci = fmin(fmax(fi, (double)oa), (double)ob), cj = fmin(fmax(fj, (double)oa), (double)ob);
+    if (ci < cj) { ia = (uint32_t)ci; ib = (uint32_t)cj; }
 }
 
 // Whether a conic admits the exact ranges (positive definite, |corr| <= sqrt(0.999)).
@@ -250,20 +275,20 @@ VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf
     L.word[lane] = make_uint4(base, gid, cnt, bin);
     L.acc[lane] = 0u;
     const uint32_t rows = has ? bb.y1 - bb.y0 : 0u;
+    const RangeK myk = range_consts(cf, power);
     wave_enum(L.mark, rows, [&](const EnumStep& rs) {
         // this lane's row: ranges, then a walk over the step's boundary tiles
         const uint32_t o = rs.owner;
         uint32_t oa = 0, ia = 0, ib = 0, ob = 0, ty = 0;
         const float4 g = L.geo[o];
-        const float2 g2 = L.geo2[o];
-        const S2 oc{g.z, g.w, g2.x};
+        const RangeK ok = shfl_k(myk, o);   // every lane, before any branch
         const uint16_t* ar = nullptr;   // FILTER: the row's prefix counts of tiles keeping the splat's bin
         if (rs.active) {
             const uint4 bx = L.box[o];
             ty = bx.z + rs.idx;
             if (FILTER) ar = cutf.allow + ((size_t)ty * CUT_BINS + L.word[o].w) * (tile_bw + 1u);
             // a row of the box without such a tile is skipped whole
-            if (!FILTER || ar[bx.y] != ar[bx.x]) row_ranges(g.x, g.y, oc, g2.y, bx, ty, oa, ia, ib, ob);
+            if (!FILTER || ar[bx.y] != ar[bx.x]) row_ranges_k(g.x, g.y, (double)g.w, ok, bx, ty, oa, ia, ib, ob);
             if (FILTER && ar[ob] == ar[oa]) oa = ia = ib = ob;
         }
         uint32_t n_in = ib - ia;
