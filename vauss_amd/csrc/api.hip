@@ -976,15 +976,17 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     }
     if (vc && ((uintptr_t)vc & 7u)) return fail(VS_ERR_INVALID, "v_combined must be 8-byte aligned");
     {
-        VS_HIP(launch_fill_f32(vc, 0.0f, (uint64_t)N * n_grads, s), "zero v_combined");
         // The raster backward's stage time is its kernel's own execution: the
         // launch records the two events around the dispatch.
         if (st->I > 0) {
             RasterBwdArgs rb{};
             rb.img_w = st->W; rb.img_h = st->H; rb.tile_bw = st->tbw; rb.tile_bh = st->tbh; rb.num_tiles = st->T;
             rb.num_splats = N;
-            // the backward walks the shrunk ranges: order by their lengths
-            VS_HIP(launch_tile_order(st->ranges_shrunk, st->T, st->tile_order, s), "tile order");
+            // the backward walks the shrunk ranges: order by their lengths; the
+            // same launch clears v_combined
+            VS_HIP(launch_tile_order(st->ranges_shrunk, st->T, st->tile_order, s, nullptr, false, nullptr, nullptr, 0,
+                                     nullptr, vc, (uint64_t)N * n_grads),
+                   "tile order and v_combined clear");
             rb.order = st->tile_order;
             rb.bg_r = st->bg[0]; rb.bg_g = st->bg[1]; rb.bg_b = st->bg[2];
             rb.gids = st->gids; rb.ranges = st->ranges_shrunk;
@@ -997,6 +999,8 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             if (ctx->timing & (1u << ST_RASTER_BWD)) { eb = ctx->take_timing(); ee = ctx->take_timing(); }
             VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s, eb, ee), "raster backward");
             if (eb) ctx->recs.push_back(vs_ctx::Rec{(int)ST_RASTER_BWD, eb, ee});
+        } else {
+            VS_HIP(launch_fill_f32(vc, 0.0f, (uint64_t)N * n_grads, s), "zero v_combined");
         }
     }
     // With no dense gradient requested the backward stops at the raster

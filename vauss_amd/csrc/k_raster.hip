@@ -109,7 +109,18 @@ __global__ void __launch_bounds__(ORDER_BLOCK) tile_order_kernel(uint32_t* range
                                                                  uint32_t* __restrict__ shrunk_init, int fix_empty,
                                                                  const uint32_t* __restrict__ flags_from,
                                                                  uint32_t* flags_to, uint32_t nflags,
-                                                                 uint32_t* __restrict__ aux_out) {
+                                                                 uint32_t* __restrict__ aux_out,
+                                                                 float* __restrict__ zero, uint64_t zero_floats) {
+    // Blocks past the eight bands clear `zero` (8-byte aligned; the backward's
+    // gradient rows), which would otherwise take a launch of its own.
+    if (blockIdx.x >= 8u) {
+        const uint64_t stride = (uint64_t)(gridDim.x - 8u) * ORDER_BLOCK, pairs = zero_floats / 2;
+        const uint64_t first = (uint64_t)(blockIdx.x - 8u) * ORDER_BLOCK + threadIdx.x;
+        float2* z2 = reinterpret_cast<float2*>(zero);
+        for (uint64_t i = first; i < pairs; i += stride) z2[i] = make_float2(0.0f, 0.0f);
+        if (first == 0 && (zero_floats & 1u)) zero[zero_floats - 1] = 0.0f;
+        return;
+    }
     if (blockIdx.x == 0 && threadIdx.x < nflags) flags_to[threadIdx.x] = flags_from[threadIdx.x];
     __shared__ uint32_t s_bin[ORDER_BINS];
     __shared__ uint32_t s_wave[ORDER_BLOCK / 64];
@@ -1105,11 +1116,17 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 
 hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
                              uint32_t* shrunk_init, bool fix_empty, const uint32_t* flags_from, uint32_t* flags_to,
-                             uint32_t nflags, uint32_t* aux_out) {
+                             uint32_t nflags, uint32_t* aux_out, float* zero, uint64_t zero_floats) {
     if (num_tiles == 0) return hipSuccess;
     if (!flags_to) nflags = 0;
-    tile_order_kernel<<<8, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init, fix_empty ? 1 : 0, flags_from,
-                                                flags_to, nflags, aux_out);
+    // the clearing blocks store float2
+    if (zero && ((uintptr_t)zero & 7u)) return hipErrorInvalidValue;
+    if (!zero) zero_floats = 0;
+    const uint64_t pairs = zero_floats / 2;
+    const uint32_t fill_blocks =
+        zero_floats ? (uint32_t)std::min<uint64_t>((pairs + ORDER_BLOCK * 4 - 1) / (ORDER_BLOCK * 4) + 1, 2048) : 0u;
+    tile_order_kernel<<<8 + fill_blocks, ORDER_BLOCK, 0, s>>>(ranges, num_tiles, order, shrunk_init, fix_empty ? 1 : 0,
+                                                              flags_from, flags_to, nflags, aux_out, zero, zero_floats);
     return hipGetLastError();
 }
 

@@ -312,7 +312,7 @@ hipError_t launch_tile_ranges(const uint32_t* tiles, uint32_t n, uint32_t num_ti
 hipError_t launch_tile_order(uint32_t* ranges, uint32_t num_tiles, uint32_t* order, hipStream_t s,
                              uint32_t* shrunk_init = nullptr, bool fix_empty = false,
                              const uint32_t* flags_from = nullptr, uint32_t* flags_to = nullptr, uint32_t nflags = 0,
-                             uint32_t* aux_out = nullptr);
+                             uint32_t* aux_out = nullptr, float* zero = nullptr, uint64_t zero_floats = 0);
 hipError_t launch_ranges_init(uint32_t* ranges, uint32_t num_tiles, hipStream_t s);
 hipError_t launch_tiles_from_ranges(const uint32_t* ranges, uint32_t num_tiles, uint32_t n, uint32_t* tiles,
                                     hipStream_t s);
