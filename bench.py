@@ -27,7 +27,7 @@ FP32_VALU_PEAK_TFLOPS = 157.3    # MI355X vector fp32 (packed) peak
 VALU_ISSUE_PEAK_G = 256 * 4 * 2.4 / 4   # G wave64 VALU instructions/s without packed fp32 (614.4)
 SIMD_CYCLES_G = 256 * 4 * 2.4           # G SIMD cycles/s across the chip
 # Cycles per wave64 instruction by counter class, relative to FP32 add at 4,
-# as the probe vauss_amd/probes/valu_rates.hip measures them on gfx950: FP32 add/mul/fma 4,
+# as a one-off per-class issue probe measured them on gfx950: FP32 add/mul/fma 4,
 # int32 2, conversions 4, transcendentals 8.  The remainder (moves 2;
 # max/min, compares, selects 4) is bracketed by its two rates.
 VALU_CLASS_CYCLES = {"SQ_INSTS_VALU_ADD_F32": 4, "SQ_INSTS_VALU_MUL_F32": 4, "SQ_INSTS_VALU_FMA_F32": 4,
@@ -213,6 +213,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--depth-cutoff", choices=("off", "on", "auto"), default="off",
+                    help="depth cutoff of the tile lists (vs_ctx_set_depth_cutoff; off, as the reference lists "
+                         "every pair, unless opted in)")
     ap.add_argument("--exact-counts", action="store_true",
                     help="time training renders that wait for their own counts (the default times lagged counts, "
                          "as the reference's training renders run)")
@@ -271,6 +274,7 @@ def main() -> int:
         return g, aux
 
     ctx = va.Context.get(dev)
+    ctx.set_depth_cutoff({"off": ctx.CUTOFF_OFF, "on": ctx.CUTOFF_ON, "auto": ctx.CUTOFF_AUTO}[args.depth_cutoff])
     lagged = not args.exact_counts
     ctx.set_lagged_counts(lagged)
     for i in range(args.warmup):
@@ -402,7 +406,7 @@ def main() -> int:
         "config": {"workload": f"{args.workload}: {WORKLOAD_DESC[args.workload]}", "num_splats": n,
                    "sh_degree": sc.sh_degree, "img": [w, h], "tile": 16, "views": len(cams),
                    "mean_visible": round(V), "mean_intersections": round(I),
-                   "counts": "lagged" if lagged else "exact"},
+                   "counts": "lagged" if lagged else "exact", "depth_cutoff": args.depth_cutoff},
         ("ms_per_view_exact_counts" if lagged else "ms_per_view_lagged_counts"): round(other_ms, 4),
         "fwd_ms": round(fwd_ms, 4),
         "bwd_ms": round(bwd_ms, 4),

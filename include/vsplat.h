@@ -248,12 +248,18 @@ vs_status vs_ctx_set_validation(vs_ctx* ctx, int enable);
  * every pixel of the tile has provably reached the raster's stopping
  * transmittance; the splats it drops are never evaluated there, so images,
  * consumed ranges and gradients are those of the full list.  Gaussian modes
- * only.  VS_CUTOFF_AUTO (the default) applies it when a render lists at
- * least 2048 intersections per tile on average (the exact count, or a lagged
- * render's capacity); ON applies it to every gaussian render, OFF never.
+ * only.  VS_CUTOFF_OFF (the default) lists every intersection, as the
+ * reference does; ON applies the cutoff to every gaussian render, AUTO when a
+ * render lists at least 2048 intersections per tile on average (the exact
+ * count, or a lagged render's capacity).  Opt in knowing what it changes:
+ * outputs that index the intersection list then index the shortened one.
+ * vs_fwd_out.tile_offsets (RenderAux.tile_offsets, render_aux.rs:84,100)
+ * holds for each tile a range of the same length over the same pairs as the
+ * full list's shrunk range, but starting at the tile's offset in the
+ * shortened list, and the geometry render's median-id channel is an index
+ * into that list (the same position within its tile's list).
  * num_intersections still reports every intersection; the state view gives
- * the listed ones, which the geometry render's median-id channel indexes
- * (the same position within its tile's list as in the full list). */
+ * the listed ones. */
 typedef enum vs_cutoff_mode { VS_CUTOFF_AUTO = 0, VS_CUTOFF_OFF = 1, VS_CUTOFF_ON = 2 } vs_cutoff_mode;
 vs_status vs_ctx_set_depth_cutoff(vs_ctx* ctx, vs_cutoff_mode mode);
 
@@ -290,7 +296,9 @@ vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* 
 /* SplatBwdOps::rasterize_bwd + project_bwd (bwd/burn_glue.rs:70-111;
  * bwd/render_bwd.rs:27-155 and 295-447).  `out_img` is the image the
  * forward wrote (f32, C channels), `v_out` its cotangent [H,W,C].  The
- * splat parameters must be the ones the forward saw.  When every dense
+ * splat parameters must be the ones the forward saw; splats->log_scale_offset
+ * is not read: the forward's is used, as the reference's ProjectUniforms
+ * carry it from the forward to project_bwd.  When every dense
  * output of `grads` is NULL the call stops at the raster gradients
  * (grads->v_combined), as the reference's BackwardFusedUpdate pass does
  * (gaussian_splats.rs:95); vs_project_update then consumes them. */
@@ -364,7 +372,8 @@ typedef struct vs_update_out {
  * b], summed over the splats with position, conic or colour gradients in
  * `v_combined` [N,10] (vs_render_backward's raster rows for `state`).  A
  * rigid twist [rho, w] is A = [w]x, b = rho.  `splats` must be the forward's
- * (same floor).  Stream-ordered; the sum is deterministic. */
+ * (same floor); the log-scale offset is the forward's, as in
+ * vs_render_backward.  Stream-ordered; the sum is deterministic. */
 vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* state, const vs_splats* splats, const float* v_combined,
                            float* v_pose);
 
@@ -450,9 +459,14 @@ vs_status vs_radix_argsort_u32(vs_ctx* ctx, const uint32_t* keys, const uint32_t
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Its scratch is one device array of 40 MiB per GPU, held by the library
  * until the process ends, so n <= VS_NOALLOC_SORT_MAX_KEYS (else
- * VS_ERR_CAPACITY).  Every call on a GPU uses that GPU's one array, so calls
- * that overlap on one GPU (from any context or stream) race.  Stream-ordered
- * and does not wait: a one-sweep pass that gave up (vs_ctx_set_sort_spin_limit)
+ * VS_ERR_CAPACITY).  Every call on a GPU uses that GPU's one array: calls on
+ * one stream are ordered by it, and a call on another stream than the array's
+ * last user first makes its stream wait for that user's sort (an event, no
+ * allocation), so calls from several contexts or streams serialise on the
+ * GPU.  Host threads are serialised by a lock while they enqueue.  If the
+ * array's address could not be taken when the device's first context was
+ * created, this call returns VS_ERR_INVALID (the context itself is usable).
+ * Stream-ordered and does not wait: a one-sweep pass that gave up (vs_ctx_set_sort_spin_limit)
  * is reported by the context's next synchronising call (vs_radix_argsort_u32,
  * an exact render, vs_ctx_settle_lagged_counts).  Same arguments and result
  * as vs_radix_argsort_u32. */

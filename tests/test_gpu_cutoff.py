@@ -32,7 +32,7 @@ pytestmark = pytest.mark.gpu
 def ctx():
     c = va.Context.get(torch.device("cuda", 0))
     yield c
-    c.set_depth_cutoff(c.CUTOFF_AUTO)
+    c.set_depth_cutoff(c.CUTOFF_OFF)
     c.set_lagged_counts(False)
 
 
@@ -64,6 +64,20 @@ def _check_cut_lists(gpu, ref, t_count):
     np.testing.assert_array_equal(np.bincount(gpu["gid"][gi], minlength=gpu["listed_counts"].shape[0]),
                                   gpu["listed_counts"])
     return int(glen.sum()), int(olen.sum())
+
+
+def _check_cut_offsets(tile_offsets, gpu_ranges, ref):
+    """The aux tile offsets of a cut render, bit for bit: each tile's shrunk
+    range of the full list (the oracle's RenderAux.tile_offsets) moved to the
+    tile's start in the shortened list; tiles with an empty full list keep the
+    full list's entry."""
+    got = np.asarray(tile_offsets).reshape(-1, 2).view(np.uint32).astype(np.int64)
+    r = np.asarray(gpu_ranges).reshape(-1, 2).astype(np.int64)
+    o = ref.get(po.F_TILE_OFFSETS).reshape(-1, 2).astype(np.int64)
+    sh = ref.get(po.F_TILE_OFFSETS_SHRUNK).reshape(-1, 2).astype(np.int64)
+    nonempty = (o[:, 1] - o[:, 0]) > 0
+    want = np.where(nonempty[:, None], sh - o[:, :1] + r[:, :1], sh)
+    np.testing.assert_array_equal(got, want)
 
 
 def _check_median_ids(got, want, ranges, ref_ranges):
@@ -121,6 +135,7 @@ def test_cutoff_lists_are_fronts_of_the_full_lists(ctx, cfg, n, view, pass_name,
     assert np.array_equal(img_cmp.view(np.uint32), rimg_cmp.view(np.uint32)), f"{(img_cmp != rimg_cmp).sum()} channels differ"
     np.testing.assert_array_equal(out.aux.visible.cpu().numpy(), ref.get(po.F_VISIBLE))
     np.testing.assert_array_equal(_consumed(out.aux.tile_offsets.cpu().numpy()), _consumed(ref.get(po.F_TILE_OFFSETS_SHRUNK)))
+    _check_cut_offsets(out.aux.tile_offsets.cpu().numpy(), gpu["ranges"], ref)
     del gpu
     if pass_.geometry():
         out.state.free()
@@ -194,7 +209,7 @@ def test_cutoff_forward_pass_packs_the_same_image(ctx):
 def test_cutoff_auto_turns_on_for_long_lists(ctx):
     """AUTO lists every pair of a short-list render and cuts a render with
     thousands of pairs per tile."""
-    ctx.set_depth_cutoff(ctx.CUTOFF_AUTO)
+    ctx.set_depth_cutoff(ctx.CUTOFF_OFF)
     for cfg, n, want in (("c3", 100_000, 0), ("c4", 3_000_000, 1)):
         w = scenes.workload(cfg, n)
         cam = w.cameras[0].uniforms(w.img_size)

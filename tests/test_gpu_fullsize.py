@@ -15,10 +15,12 @@ inputs, then checks:
     backward is linear in the image cotangent.
 The 3M-splat heavy-tailed case has 3.6e8 intersections; the oracle's render
 of it takes ~20 s on the host's cores.  These checks run on the full lists
-(depth cutoff off); the same view is then rendered with the depth cutoff on
-and checked against the same oracle render: every tile's list is the front of
-the full one and covers what the tile consumes, and the image, consumed
-ranges and gradients are unchanged.
+(the depth cutoff is off by default); the same view is then rendered with the
+depth cutoff opted in and checked against the same oracle render: every
+tile's list is the front of the full one and covers what the tile consumes,
+the image, consumed ranges and gradients are unchanged, and the aux tile
+offsets are the full list's shrunk ranges moved to each tile's start in the
+shortened list.
 """
 import time
 
@@ -29,7 +31,7 @@ import torch
 import vauss_amd as va
 from oracle import pyoracle as po
 from tests._util import circle_mask, gpu_state_arrays, l1_cotangent_np, to_gpu
-from tests.test_gpu_cutoff import _check_cut_lists, _consumed
+from tests.test_gpu_cutoff import _check_cut_lists, _check_cut_offsets, _consumed
 from tests.test_gpu_parity import _check_forward, _check_grads, _check_param_grads
 from vauss_amd import scenes
 
@@ -74,7 +76,7 @@ def test_full_size_parity(cfg, view):
         out = va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
         torch.cuda.synchronize()
     finally:
-        ctx.set_depth_cutoff(ctx.CUTOFF_AUTO)
+        ctx.set_depth_cutoff(ctx.CUTOFF_OFF)
     gpu = gpu_state_arrays(out)
     _log(f"{cfg}: {out.aux.num_visible} visible, {out.aux.num_intersections} intersections; oracle forward")
     ref = po.render_forward(cam, w.img_size, w.scene.transforms, w.scene.sh_coeffs, w.scene.raw_opacities,
@@ -116,14 +118,17 @@ def test_full_size_parity(cfg, view):
         cut = va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
         torch.cuda.synchronize()
     finally:
-        ctx.set_depth_cutoff(ctx.CUTOFF_AUTO)
+        ctx.set_depth_cutoff(ctx.CUTOFF_OFF)
     gc = gpu_state_arrays(cut)
     t_count = gc["ranges"].shape[0] * gc["ranges"].shape[1]
     listed, full = _check_cut_lists(gc, ref, t_count)
     _log(f"{cfg}: {listed} of {full} pairs listed under the cutoff")
-    del gc
     assert np.array_equal(cut.out_img.cpu().numpy().view(np.uint32), rimg.view(np.uint32))
     np.testing.assert_array_equal(_consumed(cut.aux.tile_offsets.cpu().numpy()), _consumed(ref.get(po.F_TILE_OFFSETS_SHRUNK)))
+    # with the cutoff opted in, the aux offsets index the shortened list: the
+    # full list's shrunk ranges moved to each tile's start in it
+    _check_cut_offsets(cut.aux.tile_offsets.cpu().numpy(), gc["ranges"], ref)
+    del gc
     gcut = va.render_backward(cut, t, s, o, v_dev)
     _check_grads(gcut.v_combined.cpu().numpy(), vc, "v_combined (cutoff vs full lists)")
     cut.state.free()

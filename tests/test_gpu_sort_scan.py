@@ -79,18 +79,36 @@ def test_sort_with_device_count():
     np.testing.assert_array_equal(gk[31_337:], keys[31_337:])   # the inactive tail is untouched
 
 
-def test_sort_permutation_above_block_sizes():
-    # lib.rs:366-403 shuffles 0..70M with SplitMix64; 2M keeps the CPU side quick
-    n = 2_000_000
-    keys = np.arange(n, dtype=np.uint32)
-    r = SplitMix64(0xD15EA5E).next_u64(n - 1)
-    for i, j in zip(range(n - 1, 0, -1), (r % np.arange(n, 1, -1, dtype=np.uint64)).astype(np.int64)):
-        keys[i], keys[j] = keys[j], keys[i]
+def test_sorting_large():
+    """lib.rs:308-356: 30M keys drawn from [0, 1M), values 0..n-1, all 32 bits:
+    sorted, and every value points at an input with its key (checked in full
+    against numpy's stable argsort, not only at the reference's sample)."""
+    n = 30_000_000
+    rng = np.random.default_rng(0x30)
+    keys = rng.integers(0, 1_000_000, n, dtype=np.uint32)
     vals = np.arange(n, dtype=np.uint32)
+    print(f"[case] sort n={n} keys < 1e6", flush=True)
+    gk, gv = _sort(keys, vals, 32)
+    assert (np.diff(gk.astype(np.int64)) >= 0).all()
+    for idx in (0, 1000, 10_000, 100_000, 1_000_000, 10_000_000, 19_999_999):
+        assert keys[gv[idx]] == gk[idx]
+    idx = np.argsort(keys, kind="stable")
+    np.testing.assert_array_equal(gk, keys[idx])
+    np.testing.assert_array_equal(gv, idx.astype(np.uint32))
+
+
+def test_sorting_above_scan_block_size():
+    """lib.rs:358-403: a random permutation of 0..70M (the reference shuffles
+    with SplitMix64 Fisher-Yates; any uniform permutation serves, so numpy
+    draws it): sorted keys are 0..n-1 and each value is its key's position."""
+    n = 70_000_000
+    keys = np.random.default_rng(0xD15EA5E).permutation(n).astype(np.uint32)
+    vals = np.arange(n, dtype=np.uint32)
+    print(f"[case] sort permutation n={n}", flush=True)
     gk, gv = _sort(keys, vals, 32)
     np.testing.assert_array_equal(gk, np.arange(n, dtype=np.uint32))
     expected = np.empty(n, np.uint32)
-    expected[keys] = np.arange(n, dtype=np.uint32)
+    expected[keys] = vals
     np.testing.assert_array_equal(gv, expected)
 
 

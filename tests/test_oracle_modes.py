@@ -145,3 +145,32 @@ def test_vjp_matches_central_differences(mip, use_floor):
             assert np.all(np.abs(got[grp] - num[grp]) <= tol), (gi, grp, got[grp], num[grp])
         checked += 1
     assert checked >= 10
+
+
+@pytest.mark.parametrize("mip,use_floor", [(False, False), (False, True), (True, False), (True, True)])
+def test_log_scale_offset_matches_materialized(mip, use_floor):
+    """tests/mod.rs:287-382 (viewer_scale_matches_materialized_transforms) on
+    the oracle: an offset of ln(s) renders exactly like log-scales shifted by
+    ln(s) in f32 beforehand (counts, lists, aux, image, every dense gradient),
+    and ln(2) visibly changes the render."""
+    cam = scenes.test_camera(IMG, fov=0.9, position=(0.0, 0.0, -4.0)).uniforms(IMG)
+    t, sh, op, floor = _scene(300, 11)
+    flags = po.FLAG_BWD_INFO | (po.FLAG_MIP if mip else 0)
+    fl = floor if use_floor else None
+    base = po.render_forward(cam, IMG, t, sh, op, flags=flags, min_scale=fl)
+    for scale in (0.5, 2.0):
+        lso = np.float32(np.log(scale))
+        tm = t.copy()
+        tm[:, 7:10] = tm[:, 7:10] + lso
+        a = po.render_forward(cam, IMG, t, sh, op, flags=flags, min_scale=fl, log_scale_offset=float(lso))
+        b = po.render_forward(cam, IMG, tm, sh, op, flags=flags, min_scale=fl)
+        assert a.info.num_visible == b.info.num_visible and a.info.num_intersections == b.info.num_intersections
+        for field in (po.F_INTERSECT_COUNTS, po.F_ISECT_GID, po.F_TILE_OFFSETS_SHRUNK, po.F_MAX_RADIUS,
+                      po.F_OPACITIES, po.F_PROJECTED, po.F_OUT_IMG):
+            np.testing.assert_array_equal(a.get(field).view(np.uint32), b.get(field).view(np.uint32))
+        assert not np.array_equal(a.get(po.F_OUT_IMG), base.get(po.F_OUT_IMG))
+        v_out = (np.random.default_rng(4).standard_normal(a.get(po.F_OUT_IMG).shape) * 1e-3).astype(np.float32)
+        ga, gb = a.backward(v_out), b.backward(v_out)
+        for key in ("v_combined", "v_transforms", "v_sh", "v_raw_opac", "v_refine"):
+            np.testing.assert_array_equal(ga[key].view(np.uint32), gb[key].view(np.uint32))
+        assert np.abs(ga["v_transforms"][:, 7:10]).max() > 0

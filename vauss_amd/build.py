@@ -65,25 +65,6 @@ def build(verbose: bool = True) -> Path:
     return LIB
 
 
-VALU_RATES = ROOT / "_build" / "valu_rates"
-
-
-def build_valu_rates(verbose: bool = True) -> Path:
-    """The VALU issue-rate calibration probe (probes/valu_rates.hip), a
-    measurement tool outside the library: `python -m vauss_amd.build
-    --valu-rates` builds _build/valu_rates, which prints the rate of each
-    instruction class, the ceiling bench.py's instruction-issue roofline is
-    built on."""
-    VALU_RATES.parent.mkdir(parents=True, exist_ok=True)
-    cmd = [HIPCC, "-O3", "-std=c++17", *DEVICE, "-o", str(VALU_RATES), str(PKG / "probes" / "valu_rates.hip")]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"compiling valu_rates failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    if verbose:
-        print(f"built {VALU_RATES}", file=sys.stderr)
-    return VALU_RATES
-
-
 def build_oracle(verbose: bool = True) -> None:
     """Compile the CPU oracle (test infrastructure) with its own Makefile."""
     res = subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], capture_output=True, text=True)
@@ -94,7 +75,4 @@ def build_oracle(verbose: bool = True) -> None:
 
 
 if __name__ == "__main__":
-    if "--valu-rates" in sys.argv[1:]:
-        build_valu_rates()
-    else:
-        build()
+    build()

@@ -56,7 +56,7 @@ struct vs_ctx {
     // the unmasked pixel count of the last circular L1 mask (vs_l1_cotangent)
     struct MaskKey { uint32_t w, h; float cx, cy, r; } l1_mask{0, 0, 0.0f, 0.0f, 0.0f};
     uint64_t l1_mask_count = 0;
-    vs_cutoff_mode depth_cutoff = VS_CUTOFF_AUTO;   // vs_ctx_set_depth_cutoff
+    vs_cutoff_mode depth_cutoff = VS_CUTOFF_OFF;    // vs_ctx_set_depth_cutoff (opt-in)
     bool validate = false;                // scan inputs and gradients for NaN / Inf (vs_ctx_set_validation)
     bool poison = false;                  // fill every library allocation with POISON_WORD first
     uint32_t* dev_val = nullptr;          // device: validation counters, VALIDATE_WORDS per check
@@ -347,32 +347,55 @@ vs_status check_splats(const vs_splats* sp) {
 // a host-side stand-in, not device memory: the device address of each GPU's
 // copy comes from hipGetSymbolAddress, taken once per device (with that device
 // current) when the first context on it is created, and only that address is
-// ever handed to kernels.
+// ever handed to kernels.  A failed lookup leaves the context usable; only the
+// allocation-free sort then reports it.
+//
+// Calls on one stream are ordered by the stream.  A call on another stream
+// than the array's last user first waits (hipStreamWaitEvent, no allocation)
+// on an event recorded after that user's sort, so sorts from different
+// contexts or streams never overlap in the array.
 constexpr uint32_t NOALLOC_SORT_MAX_KEYS = 1u << 22;
 constexpr size_t SCRATCH_BYTES = (size_t)40 << 20;
 static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 
 namespace {
 constexpr int MAX_DEVICES = 64;
+struct ScratchSlot {
+    bool tried = false;
+    void* ptr = nullptr;             // the array's device address on this GPU
+    hipEvent_t done = nullptr;       // recorded after the last sort that used it
+    bool used = false;
+    hipStream_t last = nullptr;      // that sort's stream
+    std::string error;               // why `ptr` is missing
+};
 std::mutex g_scratch_mutex;
-void* g_scratch_ptr[MAX_DEVICES] = {};
+ScratchSlot g_scratch[MAX_DEVICES];
 
-// Set-up, called with `device` current.
-vs_status init_scratch(int device) {
-    if (device < 0 || device >= MAX_DEVICES) return fail(VS_ERR_INVALID, "device index beyond the library's table");
+// Set-up, called with `device` current.  Never fails the caller: a missing
+// address is recorded and reported by the allocation-free sort.
+void init_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return;
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    if (g_scratch_ptr[device]) return VS_OK;
-    if (sort_tmp_bytes(NOALLOC_SORT_MAX_KEYS, false) + 256 > SCRATCH_BYTES)
-        return fail(VS_ERR_INVALID, "the sort scratch array is smaller than its maximum sort needs");
+    ScratchSlot& sl = g_scratch[device];
+    if (sl.tried) return;
+    sl.tried = true;
+    if (sort_tmp_bytes(NOALLOC_SORT_MAX_KEYS, false) + 256 > SCRATCH_BYTES) {
+        sl.error = "the scratch array is smaller than its maximum sort needs";
+        return;
+    }
     void* ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
-    g_scratch_ptr[device] = ptr;
-    return VS_OK;
-}
-void* scratch_ptr(int device) {
-    std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    return (device >= 0 && device < MAX_DEVICES) ? g_scratch_ptr[device] : nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        sl.error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e != hipSuccess ? e : hipErrorInvalidSymbol);
+        return;
+    }
+    e = hipEventCreateWithFlags(&sl.done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        sl.done = nullptr;
+        sl.error = std::string("hipEventCreateWithFlags: ") + hipGetErrorString(e);
+        return;
+    }
+    sl.ptr = ptr;
 }
 } // namespace
 
@@ -406,17 +429,7 @@ extern "C" vs_status vs_ctx_create(int device, void* hip_stream, vs_ctx** out) {
         delete c;
         return hip_fail(e, "context buffers");
     }
-    {
-        const vs_status se = init_scratch(device);
-        if (se != VS_OK) {
-            hipHostFree(c->host_counters);
-            hipHostFree(c->host_val);
-            hipFree(c->dev_flags);
-            hipFree(c->dev_val);
-            delete c;
-            return se;
-        }
-    }
+    init_scratch(device);
     // VSPLAT_POISON=1 poisons every allocation of this context (a debug aid for test runs).
     const char* poison_env = std::getenv("VSPLAT_POISON");
     c->poison = poison_env && poison_env[0] == '1';
@@ -1009,7 +1022,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
     if (dense) {
         StageTimer tm(ctx, ST_PROJECT_BWD);
         ProjectBwdArgs pb{};
-        pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = sp->log_scale_offset;
+        pb.cam = st->cam; pb.num_splats = N; pb.sh_degree = st->degree; pb.log_scale_offset = st->lso;
         pb.transforms = sp->transforms; pb.sh = sp->sh_coeffs; pb.sh_half = st->sh_half; pb.min_scale = sp->min_scale; pb.mip = st->mip; pb.raw_opac = sp->raw_opacities;
         pb.decoder = sp->decoder; pb.surfel = st->surfel;
         pb.counts = st->counts; pb.v_combined = vc;
@@ -1067,7 +1080,7 @@ extern "C" vs_status vs_pose_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_sp
     hipStream_t s = ctx->stream;
     StageTimer tm(ctx, ST_PROJECT_BWD);
     PoseBwdArgs pa{};
-    pa.cam = st->cam; pa.num_splats = st->N; pa.sh_degree = st->degree; pa.log_scale_offset = sp->log_scale_offset;
+    pa.cam = st->cam; pa.num_splats = st->N; pa.sh_degree = st->degree; pa.log_scale_offset = st->lso;
     pa.transforms = sp->transforms; pa.sh = sp->sh_coeffs; pa.sh_half = st->sh_half; pa.min_scale = sp->min_scale;
     pa.mip = st->mip; pa.raw_opac = sp->raw_opacities; pa.v_combined = v_combined; pa.v_pose = v_pose;
     void* part = nullptr;
@@ -1260,14 +1273,24 @@ extern "C" vs_status vs_radix_argsort_u32_noalloc(vs_ctx* ctx, const uint32_t* k
     if (!keys || !vals || !out_keys || !out_vals) return fail(VS_ERR_INVALID, "null buffer");
     if (keys == out_keys || vals == out_vals) return fail(VS_ERR_INVALID, "outputs must not alias inputs");
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
-    void* tmp = scratch_ptr(ctx->device);
-    if (!tmp) return fail(VS_ERR_INVALID, "no scratch address for this device (no context was created on it)");
+    if (ctx->device < 0 || ctx->device >= MAX_DEVICES) return fail(VS_ERR_INVALID, "device index beyond the library's table");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ScratchSlot& sl = g_scratch[ctx->device];
+    if (!sl.ptr)
+        return fail(VS_ERR_INVALID, "the allocation-free sort's scratch array is unavailable on this device: " +
+                                        (sl.tried ? sl.error : std::string("no context was created on it")));
+    // Order this sort behind the array's last user on another stream.
+    if (sl.used && sl.last != ctx->stream)
+        VS_HIP(hipStreamWaitEvent(ctx->stream, sl.done, 0), "hipStreamWaitEvent(scratch)");
     // Stream-ordered, no wait: a pass that gave up sets the context's flag,
     // which the next synchronising call on the context reports.
     const hipError_t e = radix_sort_pairs(keys, vals, out_keys, out_vals, n, n_dev, false, skip_bits,
-                                          skip_bits + sorting_bits, tmp, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream,
+                                          skip_bits + sorting_bits, sl.ptr, ctx->dev_flags + FLAG_SORT_STALL, ctx->stream,
                                           ctx->spin_limit);
     if (e != hipSuccess) return hip_fail(e, "radix sort");
+    VS_HIP(hipEventRecord(sl.done, ctx->stream), "hipEventRecord(scratch)");
+    sl.used = true;
+    sl.last = ctx->stream;
     return VS_OK;
 }
 

@@ -134,10 +134,13 @@ class Context:
     CUTOFF_AUTO, CUTOFF_OFF, CUTOFF_ON = 0, 1, 2
 
     def set_depth_cutoff(self, mode: int) -> None:
-        """Depth cutoff of the tile lists (vs_ctx_set_depth_cutoff): CUTOFF_AUTO
-        (the default: renders listing at least 2048 pairs per tile), CUTOFF_OFF
-        or CUTOFF_ON (every gaussian render).  Images and gradients are the
-        full list's either way."""
+        """Depth cutoff of the tile lists (vs_ctx_set_depth_cutoff): CUTOFF_OFF
+        (the default: every pair listed, as the reference does), CUTOFF_ON
+        (every gaussian render) or CUTOFF_AUTO (renders listing at least 2048
+        pairs per tile).  Images, visibility, consumed tile ranges and
+        gradients are the full list's either way; with the cutoff applied
+        the aux tile_offsets index the shortened list (same range lengths,
+        other starts)."""
         _lib.check(self.lib.vs_ctx_set_depth_cutoff(self.handle, int(mode)))
 
     def set_poison(self, on: bool = True) -> None:
@@ -381,11 +384,13 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
 
 
 def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
-                    raw_opacities: torch.Tensor, v_output: torch.Tensor, log_scale_offset: float = 0.0,
+                    raw_opacities: torch.Tensor, v_output: torch.Tensor,
                     fused: bool = False, min_scale: Optional[torch.Tensor] = None,
                     decoder: Optional[torch.Tensor] = None) -> SplatGrads:
     """rasterize_bwd followed by project_bwd (project_bwd_neural with
-    `decoder`, the forward's), returning dense gradients.
+    `decoder`, the forward's), returning dense gradients.  The log-scale
+    offset is the forward's (the reference's ProjectUniforms carry it from the
+    forward to project_bwd).
 
     With `fused` the backward stops at the raster gradients (the
     BackwardFusedUpdate pass): only `v_combined` is filled, for
@@ -429,15 +434,14 @@ def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: t
     grads.v_combined = _ptr(g.v_combined)
     grads.v_decoder = _ptr(g.v_decoder)
     grads.v_coeffs_sq = _ptr(g.v_coeffs_sq)
-    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, _min_scale(min_scale, n),
-                            decoder)
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, 0.0, _min_scale(min_scale, n), decoder)
     _lib.check(ctx.lib.vs_render_backward(ctx.handle, output.state.handle, C.byref(splats), _ptr(output.out_img),
                                           _ptr(v_output), C.byref(grads)))
     return g
 
 
 def pose_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
-                  raw_opacities: torch.Tensor, v_combined: torch.Tensor, log_scale_offset: float = 0.0,
+                  raw_opacities: torch.Tensor, v_combined: torch.Tensor,
                   min_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """pose_bwd (bwd/render_bwd.rs:224-288): the camera gradient [12] =
     d loss / d [A (row-major 3x3), b] of x_c' = (I + A) x_c + b, from the raster
@@ -455,7 +459,7 @@ def pose_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: tor
     ctx = output.state.ctx
     Context.get(dev)
     v_pose = torch.empty(12, dtype=torch.float32, device=dev)
-    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, log_scale_offset, _min_scale(min_scale, n))
+    splats = _splats_struct(transforms, sh_coeffs, raw_opacities, degree, 0.0, _min_scale(min_scale, n))
     _lib.check(ctx.lib.vs_pose_backward(ctx.handle, output.state.handle, C.byref(splats), _ptr(v_combined),
                                         _ptr(v_pose)))
     return v_pose
