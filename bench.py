@@ -213,6 +213,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-next-rows", action="store_true",
+                    help="skip the timings of the rows after the render (loss, update, SH step, pose, neural, surfel)")
     ap.add_argument("--depth-cutoff", choices=("off", "on", "auto"), default="off",
                     help="depth cutoff of the tile lists (vs_ctx_set_depth_cutoff; off, as the reference lists "
                          "every pair, unless opted in)")
@@ -384,7 +386,7 @@ def main() -> int:
         print(f"[bench] copy calibration: {args.copy_calib} MiB read + {args.copy_calib} MiB written per copy",
               file=sys.stderr, flush=True)
 
-    next_rows = measure_next_rows(va, wl, cams[0], t, s, o, gt, dev)
+    next_rows = None if args.no_next_rows else measure_next_rows(va, wl, cams[0], t, s, o, gt, dev)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -209,7 +209,7 @@ def test_cutoff_forward_pass_packs_the_same_image(ctx):
 def test_cutoff_auto_turns_on_for_long_lists(ctx):
     """AUTO lists every pair of a short-list render and cuts a render with
     thousands of pairs per tile."""
-    ctx.set_depth_cutoff(ctx.CUTOFF_OFF)
+    ctx.set_depth_cutoff(ctx.CUTOFF_AUTO)
     for cfg, n, want in (("c3", 100_000, 0), ("c4", 3_000_000, 1)):
         w = scenes.workload(cfg, n)
         cam = w.cameras[0].uniforms(w.img_size)

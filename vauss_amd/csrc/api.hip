@@ -131,6 +131,8 @@ struct vs_fwd_state {
     float* v_combined = nullptr;
     uint32_t* tiles = nullptr;    // [I] sorted tile ids (written on demand, see tiles_pending)
     uint32_t* gids = nullptr;     // [I] sorted global ids
+    uint32_t* qpass = nullptr;    // [I] bwd-info passes: the forward's quadrant pass bytes (the emission's
+                                  // tile-id buffer, free once the tile sort has read it)
     // the tile sort produced the ranges and skipped the sorted ids: the state
     // view rebuilds them from the ranges
     mutable bool tiles_pending = false;
@@ -895,6 +897,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
                    "tile sort");
             st->tiles_pending = tro.done;
         }
+        if (bwd_info) st->qpass = tiles_u;
         if (!lagged) {
             // An exact render reports a sort that gave up before it returns: the
             // flag follows the sorts, and the host waits for it after the raster
@@ -930,6 +933,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         // surfels outside training take the median by the surface criterion (gaussian_splats.rs:100-106)
         ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass_surface_criterion(pass)) ? 1u : 0u;
         ra.out = out->out_img; ra.visible = st->visible;
+        ra.qpass = reinterpret_cast<uint8_t*>(st->qpass);
         VS_HIP(launch_raster_fwd(ra, bwd_info, geometry, smooth, s), "raster forward");
     }
     if (sort_done) {
@@ -1008,6 +1012,7 @@ extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_
             rb.channels = (pass_geometry(st->pass) || st->surfel) ? 12u : 4u;
             rb.proj_surf = st->proj_surf;
             rb.v_combined = vc;
+            rb.qpass = st->qpass;
             hipEvent_t eb = nullptr, ee = nullptr;
             if (ctx->timing & (1u << ST_RASTER_BWD)) { eb = ctx->take_timing(); ee = ctx->take_timing(); }
             VS_HIP(launch_raster_bwd(rb, st->pass == VS_PASS_BACKWARD_SMOOTH_CUTOFF, s, eb, ee), "raster backward");

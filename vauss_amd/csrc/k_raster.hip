@@ -378,7 +378,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
     __shared__ float4 s_c[FWD_BATCH];    // max(b,0), -, -, -
     __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BATCH : 1];
     __shared__ float4 s_s[SURF ? FWD_BATCH * 4 : 1];
-    __shared__ uint4 s_hit[BWD ? FWD_BATCH : 1];   // .x = 1 once the slot blended a pixel
+    __shared__ uint4 s_hit[BWD ? FWD_BATCH : 1];   // .x = 1 once the slot blended a pixel, .y once it stopped one
     __shared__ __align__(16) uint32_t s_list[FWD_BATCH];   // live slots as byte offsets (slot * 16)
 
     const uint32_t xcd = blockIdx.x % 8, idx = blockIdx.x / 8;
@@ -415,7 +415,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         const uint32_t gid = (l < rem) ? a.gids[start + l] : 0xFFFFFFFFu;
         bool live = false;
         __syncthreads();                              // the previous batch's LDS reads are complete
-        if constexpr (BWD) s_hit[l].x = 0u;
+        if constexpr (BWD) *reinterpret_cast<uint2*>(&s_hit[l]) = make_uint2(0u, 0u);
         if (gid < a.num_splats) {   // else: past the batch, or a corrupt id (dead slot)
             const float4* row = a.proj + (size_t)gid * PROJ_Q;
             const float4 pa = row[0];
@@ -447,6 +447,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         __syncthreads();
         const uint32_t nlist = (uint32_t)__popcll(lm);
         uint32_t done_v = done ? 1u : 0u;   // carried in a vector register through the loop
+        uint32_t stop_off = 0xFFFFFFFFu;    // the slot at which the lane's pixel stopped in this batch
         // A uniform loop over the list: every lane evaluates every pair and a
         // done lane only fails the blend test.  One divergent branch per pair
         // (the blend) keeps the scalar exec-mask work per pair small; the
@@ -490,6 +491,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             const bool pass = done_v == 0u && valid && sigma >= 0.0f && w_cut > 0.0f;
             const bool stop = nt <= T_STOP;
             done_v = (pass && stop) ? 1u : done_v;
+            if constexpr (BWD) stop_off = (pass && stop) ? off : stop_off;
             {
                 if (pass && !stop) {
                     if constexpr (BWD) reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_hit) + off)->x = 1u;
@@ -533,9 +535,15 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         }
         done = done_v != 0u;
         if constexpr (BWD) {
+            // A slot passes in this quadrant when one of its pixels blended it
+            // or stopped at it (the backward's replay changes a pixel's state
+            // only there), recorded per list entry for the backward.
+            if (stop_off != 0xFFFFFFFFu) reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_hit) + stop_off)->y = 1u;
             __syncthreads();
-            const bool hit = gid < a.num_splats && s_hit[l].x;
+            const uint2 h = *reinterpret_cast<const uint2*>(&s_hit[l]);
+            const bool hit = gid < a.num_splats && h.x;
             if (hit) a.visible[gid] = 1.0f;
+            if (l < rem && a.qpass) a.qpass[(size_t)(start + l) * 4 + q] = (h.x | h.y) ? (uint8_t)(1u << q) : (uint8_t)0u;
             // batches run in increasing order, so the batch's last blended
             // slot is the quadrant's last so far
             const uint64_t hm = __ballot(hit);
@@ -776,7 +784,14 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             s_c[lane] = make_float4(mx(cb, 0.0f), pa.z, pb.x, as_f(gates));
             s_d[lane] = make_float4(pa.z * img_w, pa.w * img_w, pa.w * img_h, pb.x * img_h);
             s_c01[lane] = pa.w;
-            mask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, c2, pc.y, SMOOTH);
+            if (a.qpass) {
+                // the quadrants where the forward's replay passed this entry:
+                // the others' pixels neither blend nor stop there
+                const uint32_t w = a.qpass[start + lane];
+                mask = (w | (w >> 8) | (w >> 16) | (w >> 24)) & 0xFu;
+            } else {
+                mask = quadrant_mask(x0, y0, sa.x, sa.y, sa.z, sa.w, c2, pc.y, SMOOTH);
+            }
         }
         __syncthreads();
         for (uint32_t t = 0; t < rem; ++t) {
@@ -948,9 +963,15 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             }
         }
         __syncthreads();
-        // the batch's splats that may reach this quadrant, in depth order
-        const bool live_t = lane < rem && surfel_quadrant_live(x0, y0, s_s[4 * lane], s_s[4 * lane + 1],
-                                                                s_s[4 * lane + 2], s_b[lane].x, SMOOTH);
+        // the batch's splats that may reach this quadrant, in depth order: with
+        // the forward's pass bytes, exactly those at which a pixel of the
+        // quadrant blended or stopped (the others change no pixel's state)
+        bool live_t = false;
+        if (lane < rem) {
+            live_t = a.qpass ? ((a.qpass[start + lane] >> (8u * q)) & 0xFFu) != 0u
+                             : surfel_quadrant_live(x0, y0, s_s[4 * lane], s_s[4 * lane + 1], s_s[4 * lane + 2],
+                                                    s_b[lane].x, SMOOTH);
+        }
         uint64_t live = __ballot(live_t);
         if (__ballot(T > T_STOP) == 0ull) live = 0ull;       // this quadrant is done
         while (live) {

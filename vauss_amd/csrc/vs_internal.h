@@ -141,6 +141,8 @@ struct RasterArgs {
     uint32_t surf_crit;              // surfels outside training: median by the surface criterion
     void* out;                       // f32 [H,W,C] or u32 [H,W]
     float* visible;                  // [N] or null
+    uint8_t* qpass;                  // [I][4] bwd-info passes: byte q = 1 << q when a pixel of quadrant q
+                                     // passed (blended or stopped) at that list entry, or null
 };
 
 struct RasterBwdArgs {
@@ -156,6 +158,7 @@ struct RasterBwdArgs {
     const float* v_out;              // [H,W,C]
     uint32_t channels;
     float* v_combined;               // [N,10], surfels [N,17]
+    const uint32_t* qpass;           // [I] the forward's quadrant pass bytes (RasterArgs::qpass), or null
 };
 
 struct ProjectBwdArgs {
