@@ -1000,13 +1000,18 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             const bool contrib = blend && !stop;
             if (stop) T = 0.0f;
             if (__ballot(contrib) == 0ull) continue;          // uniform: no lane blends it
-            const float z = h.z;
+            // Lanes that do not blend this splat must add exact zeros: every
+            // component below is a product with vis, v_alpha or v_z, or with the
+            // ray-plane terms su, sv, 1/q.z, and those (the only ones that can
+            // be non-finite off the disk) are zeroed on such lanes, so each
+            // gradient component is 0 there without a select of its own.
+            const float z = contrib ? h.z : 0.0f;
             const float m = dist_depth(z);
             // gradient-only quotients and roots take the hardware reciprocal and
             // square root (1 ulp); the replayed forward above keeps IEEE division
             const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
             const float Tk = T;
-            const float vis = ae * Tk;
+            const float vis = contrib ? ae * Tk : 0.0f;
             float gs[SURFEL_GRADS];
             gs[12] = vis * vr;      // the colour clamps' gates apply to the wave sums below
             gs[13] = vis * vg;
@@ -1020,34 +1025,34 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
                              m * vdb + (m * m) * vdc;
             const float dot_ = (Tk * cv - sv_rest) * ra;
             const float v_ae = dot_ + vt * ra;
-            const float v_alpha = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
-            const float v_z = vis * (vz + (vdb + 2.0f * m * vdc) * dm_dz) + ((isect == med) ? vmed : 0.0f);
-            const bool unsat = opac * G <= ALPHA_CAP;
-            const float v_sigma = unsat ? -alpha * v_alpha : 0.0f;
-            gs[15] = unsat ? v_alpha * G : 0.0f;
+            const float v_alpha_c = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
+            const bool unsat = contrib && opac * G <= ALPHA_CAP;
+            const float v_alpha = unsat ? v_alpha_c : 0.0f;
+            const float v_z = vis * (vz + (vdb + 2.0f * m * vdc) * dm_dz) + ((contrib && isect == med) ? vmed : 0.0f);
+            const float v_sigma = -alpha * v_alpha;
+            gs[15] = v_alpha * G;
+            const float su = contrib ? h.su : 0.0f, sv = contrib ? h.sv : 0.0f;
             const bool use_3d = h.s3d <= h.s2d;
-            const float v_su = (use_3d ? v_sigma * h.su : 0.0f) + v_z * r2x;
-            const float v_sv = (use_3d ? v_sigma * h.sv : 0.0f) + v_z * r2y;
+            const float v_su = (use_3d ? v_sigma * su : 0.0f) + v_z * r2x;
+            const float v_sv = (use_3d ? v_sigma * sv : 0.0f) + v_z * r2y;
             const float v_cx = use_3d ? 0.0f : -2.0f * v_sigma * h.dxs;
             const float v_cy = use_3d ? 0.0f : -2.0f * v_sigma * h.dys;
-            const float inv_qz = __builtin_amdgcn_rcpf(h.qz);
-            const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * h.su + v_sv * h.sv) * inv_qz;
+            const float inv_qz = contrib ? __builtin_amdgcn_rcpf(h.qz) : 0.0f;
+            const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * su + v_sv * sv) * inv_qz;
             // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
             const float vhux = h.hvy * vqz - h.hvz * vqy, vhuy = h.hvz * vqx - h.hvx * vqz, vhuz = h.hvx * vqy - h.hvy * vqx;
             const float vhvx = vqy * h.huz - vqz * h.huy, vhvy = vqz * h.hux - vqx * h.huz, vhvz = vqx * h.huy - vqy * h.hux;
             const float g0 = vhux, g1 = vhuy, g2 = vhuz + v_cx * inv_r2z;
             const float g3 = vhvx, g4 = vhvy, g5 = vhvz + v_cy * inv_r2z;
             gs[0] = g0; gs[1] = g1; gs[2] = g2; gs[3] = g3; gs[4] = g4; gs[5] = g5;
-            gs[6] = v_z * h.su - pcx * vhux - pcy * vhvx;
-            gs[7] = v_z * h.sv - pcx * vhuy - pcy * vhvy;
+            gs[6] = v_z * su - pcx * vhux - pcy * vhvx;
+            gs[7] = v_z * sv - pcx * vhuy - pcy * vhvy;
             gs[8] = v_z - pcx * vhuz - pcy * vhvz - (v_cx * cen_x + v_cy * cen_y) * inv_r2z;
             // refine weight: this pixel's gradient of a screen-space shift of the surfel (M -> T M)
             const float shx = g0 * r2x + g1 * r2y + g2 * r2z;
             const float shy = g3 * r2x + g4 * r2y + g5 * r2z;
             const float ux = shx * img_w, uy = shy * img_h;
             gs[16] = __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale;
-#pragma unroll
-            for (int i = 0; i < SURFEL_GRADS; ++i) gs[i] = contrib ? gs[i] : 0.0f;
             if (contrib) {
                 sv_rest -= vis * cv;
                 T = nt;
