@@ -45,20 +45,24 @@ WORKLOAD_DESC = {
 }
 
 
-def algorithmic_bytes(stage: str, n: int, v: int, i: int, t: int, p: int, k: int, used: int | None = None) -> int:
+def algorithmic_bytes(stage: str, n: int, v: int, i: int, t: int, p: int, k: int, used: int | None = None,
+                      graded: int | None = None) -> int:
     """Compulsory HBM bytes of one launch (4-byte words).  The raster kernels
     are charged for the intersections they consume, the shrunk tile ranges
     (`used`: every pair past a tile's last blended one is never needed), not
-    for the whole list."""
+    for the whole list; the projection backward reads parameters and SH rows
+    only of the splats with a nonzero raster-gradient row (`graded`; the
+    others get zero rows, bwd/kernels/project_backwards.rs:311-382)."""
     u = i if used is None else used
+    c = v if graded is None else graded
     if stage == "raster_bwd_ms":      # ranges, ids + 36 B rows per used intersection, RGBA + cotangent, 40 B/visible grads
         return 8 * t + 40 * u + 32 * p + 40 * v
     if stage == "raster_fwd_ms":      # ranges in/out, ids + rows, RGBA out, visible marks
         return 16 * t + 40 * u + 16 * p + 4 * n
     if stage == "project_ms":         # 44 B params for all, SH for visible, 16 B out + 36 B row per visible
         return 44 * n + 16 * n + v * (12 * k + 36)
-    if stage == "project_bwd_ms":     # 40 B raster grads, params + SH for visible, dense grads out
-        return 40 * n + v * (44 + 12 * k) + n * (48 + 12 * k)
+    if stage == "project_bwd_ms":     # 40 B raster grads, params + SH of graded rows, dense grads out
+        return 40 * n + c * (44 + 12 * k) + n * (48 + 12 * k)
     if stage == "sort_ms":            # one read + one write of the 8 B (key, id) pairs: depth sort + tile sort
         return 16 * v + 16 * i
     if stage == "emit_ms":            # compaction (8N in, 8V out), slot scan (12V), emission (4N + 36V in, 8I out)
@@ -269,7 +273,8 @@ def main() -> int:
         aux = (out.aux.num_visible, out.aux.num_intersections)
         if used:      # intersections the raster kernels consume: the shrunk tile ranges
             r = out.aux.tile_offsets.reshape(-1, 2).to(torch.int64) & 0xFFFFFFFF
-            aux = aux + (int((r[:, 1] - r[:, 0]).clamp(min=0).sum().item()),)
+            aux = aux + (int((r[:, 1] - r[:, 0]).clamp(min=0).sum().item()),
+                         int((g.v_combined != 0).any(dim=1).sum().item()))
         if list_histogram:
             tile_lists = list_length_histogram(out.state.tile_ranges(dev))
         out.state.free()
@@ -339,9 +344,10 @@ def main() -> int:
     V = float(np.mean([c[0] for c in counts]))
     I = float(np.mean([c[1] for c in counts]))
     U = float(np.mean([c[2] for c in counts]))      # intersections inside the shrunk ranges
+    Cg = float(np.mean([c[3] for c in counts]))     # splats with a nonzero raster-gradient row
     kernels = {}
     for name, ms in per_launch.items():
-        b = algorithmic_bytes(name, n, int(V), int(I), T, P, k, int(U))
+        b = algorithmic_bytes(name, n, int(V), int(I), T, P, k, int(U), int(Cg))
         kernels[name.replace("_ms", "")] = {"ms": round(ms, 4),
                                              "alg_GBs": round(b / (ms * 1e-3) / 1e9, 1) if ms > 0 and b else None}
     # The roofline's denominator is the dominant kernel's dispatch time: the
@@ -350,7 +356,7 @@ def main() -> int:
     # rocprofv3's per-dispatch average for the kernel.  The same kernel's
     # events inside the back-to-back timed region also carry dispatch-queue
     # time and are reported beside it.
-    dom_bytes = algorithmic_bytes(dom, n, int(V), int(I), T, P, k, int(U))
+    dom_bytes = algorithmic_bytes(dom, n, int(V), int(I), T, P, k, int(U), int(Cg))
     disp_ms = per_launch[dom]
     achieved = dom_bytes / (disp_ms * 1e-3) / 1e9
     traffic, traffic_note = measured_traffic(args.workload, dom.replace("_ms", ""))
@@ -378,13 +384,19 @@ def main() -> int:
     bwd_ms = per_launch["raster_bwd_ms"] + per_launch["project_bwd_ms"]
 
     if args.copy_calib:
-        src = torch.empty(args.copy_calib * (1 << 20) // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        # kernels of known traffic for the memory counters: a device copy, and
+        # the library's streaming read and write kernels (16- and 4-byte words)
+        nbytes = args.copy_calib * (1 << 20)
+        src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
+        for mode in (0, 1, 2, 3):
+            for _ in range(3):
+                va._lib.check(ctx.lib.vs_stream_probe(ctx.handle, dst.data_ptr(), nbytes, mode))
         torch.cuda.synchronize()
-        print(f"[bench] copy calibration: {args.copy_calib} MiB read + {args.copy_calib} MiB written per copy",
-              file=sys.stderr, flush=True)
+        print(f"[bench] counter calibration: {args.copy_calib} MiB per copy (read + write), streaming read and write "
+              f"(16- and 4-byte words)", file=sys.stderr, flush=True)
 
     next_rows = None if args.no_next_rows else measure_next_rows(va, wl, cams[0], t, s, o, gt, dev)
 
@@ -407,7 +419,7 @@ def main() -> int:
         "data": "synthetic (seeded SplitMix64 cloud, random-init parameters)",
         "config": {"workload": f"{args.workload}: {WORKLOAD_DESC[args.workload]}", "num_splats": n,
                    "sh_degree": sc.sh_degree, "img": [w, h], "tile": 16, "views": len(cams),
-                   "mean_visible": round(V), "mean_intersections": round(I),
+                   "mean_visible": round(V), "mean_intersections": round(I), "mean_graded_rows": round(Cg),
                    "counts": "lagged" if lagged else "exact", "depth_cutoff": args.depth_cutoff},
         ("ms_per_view_exact_counts" if lagged else "ms_per_view_lagged_counts"): round(other_ms, 4),
         "fwd_ms": round(fwd_ms, 4),
@@ -440,7 +452,7 @@ STAGE_OF_KERNEL = [("raster_bwd_kernel", "raster_bwd"), ("raster_fwd_kernel", "r
                    ("l1_cotangent", "loss"), ("loss_", "image_loss"), ("project_update", "project_update"),
                    ("sh_step", "sh_step"), ("sh_variance", "sh_step"), ("b8_", "sh_step"),
                    ("pose_", "pose_backward"), ("neural_", "neural"),
-                   ("fill", "fill"), ("copyBuffer", "copy"), ("elementwise", "torch")]
+                   ("fill", "fill"), ("copyBuffer", "copy"), ("stream_", "calib"), ("elementwise", "torch")]
 
 
 def stage_of_kernel(k: str) -> str:
@@ -460,9 +472,12 @@ def stage_of_kernel(k: str) -> str:
 SUMMARY_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VALU_TRANS_F32",
                     "SQ_LDS_BANK_CONFLICT", "SQ_THREAD_CYCLES_VALU", "SQ_ACTIVE_INST_VALU", "TCC_ATOMIC_sum",
                     "TCC_EA0_ATOMIC_sum", "TCC_HIT_sum", "TCC_MISS_sum", "FETCH_SIZE", "WRITE_SIZE",
+                    "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_sum",
+                    "TCC_EA0_RDREQ_DRAM_sum", "TCC_EA0_WRREQ_DRAM_sum",
                     "SQ_INSTS_VALU_ADD_F32", "SQ_INSTS_VALU_MUL_F32", "SQ_INSTS_VALU_FMA_F32", "SQ_INSTS_VALU_INT32",
                     "SQ_INSTS_VALU_CVT", "SQ_INSTS_VALU_INT64")
-SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "pose_", "neural_", "copyBuffer")
+SUMMARY_KERNELS = ("raster_", "project_", "emit", "sort_", "loss_", "sh_step", "pose_", "neural_", "copyBuffer",
+                   "stream_")
 
 
 def source_digest() -> str:
@@ -548,48 +563,98 @@ def summarize(args) -> int:
                         per[k][r["Counter_Name"]][key] += float(r["Counter_Value"])
                         durs.setdefault(k, {})[key] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
         dur = {k: sum(v.values()) / len(v) for k, v in durs.items()}
-        copy = per.get("__amd_rocclr_copyBuffer", {})
+
+        def mean_of(cs, c):
+            v = cs.get(c)
+            return sum(v.values()) / len(v) if v else None
+
+        def read_bytes(cs):
+            """L2->memory read bytes per dispatch from the request-size counters
+            (32, 64 and 128-byte requests), or None when a pass is missing."""
+            r32, r64, r128 = (mean_of(cs, f"TCC_EA0_RDREQ_{w}B_sum") for w in (32, 64, 128))
+            if r32 is None or r64 is None or r128 is None:
+                return None
+            return 32.0 * r32 + 64.0 * r64 + 128.0 * r128
+
+        def write_bytes(cs):
+            """Write bytes per dispatch: WRITE_SIZE, whose expression counts the
+            32- and 64-byte write requests (atomics travel as 32-byte ones)."""
+            w = mean_of(cs, "WRITE_SIZE")
+            return None if w is None else w * 1024.0
+
+        # Calibration: kernels whose traffic is known exactly (each byte of an
+        # N-byte buffer read and/or written once).
         calib = args.copy_calib * (1 << 20) if args.copy_calib else 0
-        f_scale = w_scale = None
-        if calib and copy.get("FETCH_SIZE") and copy.get("WRITE_SIZE"):
+        known = {"__amd_rocclr_copyBuffer": ("device copy", calib, calib),
+                 "stream_read_kernel<16>": ("streaming read, 16-byte words", calib, 0),
+                 "stream_read_kernel<4>": ("streaming read, 4-byte words", calib, 0),
+                 "stream_write_kernel<16>": ("streaming write, 16-byte words", 0, calib),
+                 "stream_write_kernel<4>": ("streaming write, 4-byte words", 0, calib)}
+        cal = {}
+        if calib:
+            lines += ["", f"Calibration ({args.copy_calib} MiB buffers): counter bytes per dispatch / known bytes", "",
+                      "| kernel | known read | known write | requests read / known | FETCH_SIZE / known | "
+                      "WRITE_SIZE / known |", "|---|---|---|---|---|---|"]
+            for k, (desc, kr, kw) in known.items():
+                cs = per.get(k)
+                if not cs:
+                    continue
+                if k == "__amd_rocclr_copyBuffer":      # the largest of the run's copies is the calibration copy
+                    cs = {c: {0: max(v.values())} for c, v in cs.items()}
+                rb, wb = read_bytes(cs), write_bytes(cs)
+                fs = mean_of(cs, "FETCH_SIZE")
+                cal[k] = {"read": rb / kr if (rb is not None and kr) else None,
+                          "fetch_size": fs * 1024.0 / kr if (fs is not None and kr) else None,
+                          "write": wb / kw if (wb is not None and kw) else None}
+                fmt = lambda x: "-" if x is None else f"{x:.3f}"
+                lines.append(f"| `{k}` ({desc}) | {kr >> 20} MiB | {kw >> 20} MiB | {fmt(cal[k]['read'])} | "
+                             f"{fmt(cal[k]['fetch_size'])} | {fmt(cal[k]['write'])} |")
+        # Reads: the request-size counters, exact where the streaming reads
+        # show it (ratio 1); FETCH_SIZE's expression, which counts a 128-byte
+        # request as 64 bytes, is kept only as a fallback scaled by the copy.
+        copy = per.get("__amd_rocclr_copyBuffer", {})
+        f_scale = None
+        if calib and mean_of(copy, "FETCH_SIZE"):
             f_scale = calib / (max(copy["FETCH_SIZE"].values()) * 1024.0)
-            w_scale = calib / (max(copy["WRITE_SIZE"].values()) * 1024.0)
-        lines += ["", f"Copy calibration ({args.copy_calib} MiB read + written): FETCH_SIZE x "
-                      f"{f_scale if f_scale is None else round(f_scale, 3)}, WRITE_SIZE x "
-                      f"{w_scale if w_scale is None else round(w_scale, 3)}", ""]
-        lines += ["| kernel | dispatches | counter | mean per dispatch | derived |", "|---|---|---|---|---|"]
-        traffic = {"source_digest": source_digest(), "calibration_mib": args.copy_calib,
-                   "fetch_scale": f_scale, "write_scale": w_scale, "kernels": {}}
+        lines += ["", "| kernel | dispatches | counter | mean per dispatch | derived |", "|---|---|---|---|---|"]
+        traffic = {"source_digest": source_digest(), "calibration_mib": args.copy_calib, "calibration": cal,
+                   "read_method": "32 RDREQ_32B + 64 RDREQ_64B + 128 RDREQ_128B",
+                   "write_method": "WRITE_SIZE (32- and 64-byte write requests)",
+                   "fetch_size_scale": f_scale, "kernels": {}}
         def per_run(v):        # dispatches of one run (the same counter may come from two runs)
             runs = {key[0] for key in v}
             return max(sum(1 for key in v if key[0] == r) for r in runs) if v else 0
         # steps of the profiled run: launches of the gaussian raster backward
-        nbwd = max([1] + [per_run(v.get("FETCH_SIZE", {})) for k, v in per.items() if k.startswith("raster_bwd_kernel<")])
+        nbwd = max([1] + [max(per_run(c) for c in v.values()) for k, v in per.items()
+                          if k.startswith("raster_bwd_kernel<")])
         for k, cs in sorted(per.items()):
             n = max(per_run(v) for v in cs.values())
             mean = {c: sum(v.values()) / len(v) for c, v in cs.items()}
             dur_ns = dur.get(k)
+            rb, wb = read_bytes(cs), write_bytes(cs)
+            if rb is None and f_scale and "FETCH_SIZE" in mean:
+                rb = mean["FETCH_SIZE"] * 1024.0 * f_scale
             for c in sorted(mean):
                 if c not in SUMMARY_COUNTERS or not any(x in k for x in SUMMARY_KERNELS):
                     continue
                 derived = ""
                 if c == "SQ_INSTS_VALU" and dur_ns:
                     derived = f"{mean[c] / dur_ns:.0f} G wave-instr/s over {dur_ns / 1e3:.1f} us"
-                elif c == "FETCH_SIZE" and f_scale:
-                    derived = f"{mean[c] * 1024 * f_scale / 1e6:.1f} MB calibrated"
-                elif c == "WRITE_SIZE" and w_scale:
-                    derived = f"{mean[c] * 1024 * w_scale / 1e6:.1f} MB calibrated"
+                elif c == "TCC_EA0_RDREQ_128B_sum" and rb is not None:
+                    derived = f"{rb / 1e6:.1f} MB read (32/64/128-byte requests)"
+                elif c == "WRITE_SIZE" and wb is not None:
+                    derived = f"{wb / 1e6:.1f} MB written"
                 lines.append(f"| `{k}` | {n} | {c} | {mean[c]:.5g} | {derived} |")
-            if f_scale and "FETCH_SIZE" in mean and "WRITE_SIZE" in mean:
+            if rb is not None and wb is not None:
                 stage = stage_of_kernel(k)
-                if stage in ("copy", "torch", "fill"):
+                if stage in ("copy", "torch", "fill", "calib"):
                     continue
                 e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "valu_insts": 0.0,
                                                           "valu_classes": {}, "kernels": []})
                 # per step: a kernel launched several times a step (sort passes) adds up
                 reps = n / nbwd
-                e["fetch_bytes"] += mean["FETCH_SIZE"] * 1024.0 * f_scale * reps
-                e["write_bytes"] += mean["WRITE_SIZE"] * 1024.0 * w_scale * reps
+                e["fetch_bytes"] += rb * reps
+                e["write_bytes"] += wb * reps
                 e["valu_insts"] += mean.get("SQ_INSTS_VALU", 0.0) * reps
                 for c in VALU_CLASS_CYCLES:
                     if c in mean:

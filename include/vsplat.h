@@ -531,6 +531,20 @@ vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint32_t channe
                                  const float* dl_dpartials, uint32_t dl_count, const float* coeffs,
                                  float* dl_dpred);
 
+/* ---- measurement aid ------------------------------------------------------------ */
+
+/* Streaming kernels of known memory traffic, for calibrating the memory
+ * counters that turn a profiled kernel's requests into HBM bytes (bench.py
+ * --copy-calib).  No counterpart in the reference.  Reads (VS_PROBE_READ*)
+ * or writes (VS_PROBE_WRITE*) each byte of `buf` [bytes] exactly once, in
+ * fully coalesced 16- or 4-byte words per lane; `buf` aligned to the word
+ * width and `bytes` a multiple of it.  Stream-ordered; written contents are
+ * a fixed pattern. */
+typedef enum vs_probe_mode {
+    VS_PROBE_READ16 = 0, VS_PROBE_WRITE16 = 1, VS_PROBE_READ4 = 2, VS_PROBE_WRITE4 = 3
+} vs_probe_mode;
+vs_status vs_stream_probe(vs_ctx* ctx, void* buf, uint64_t bytes, int32_t mode);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,7 +32,7 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
           "-fno-gpu-rdc", "-munsafe-fp-atomics"]
 
 SOURCES = ["k_project.hip", "k_project_bwd.hip", "k_project_update.hip", "k_raster.hip", "k_loss.hip", "k_sh_step.hip", "k_pose.hip", "k_neural.hip",
-           "k_scan.hip", "k_sort.hip", "api.hip", "camera.cpp"]
+           "k_scan.hip", "k_sort.hip", "k_calib.hip", "api.hip", "camera.cpp"]
 HEADERS = ["vs_device.h", "vs_camera.h", "vs_sh.h", "vs_vjp.h", "vs_adam.h", "vs_neural.h", "vs_surfel.h",
            "vs_internal.h"]
 

@@ -1317,6 +1317,22 @@ extern "C" vs_status vs_radix_argsort_u64(vs_ctx* ctx, const uint64_t* keys, con
     return sync_sort_flag(ctx);
 }
 
+extern "C" vs_status vs_stream_probe(vs_ctx* ctx, void* buf, uint64_t bytes, int32_t mode) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (mode < 0 || mode > 3) return fail(VS_ERR_INVALID, "mode must be 0..3 (vs_probe_mode)");
+    const uint64_t width = (mode & 2) ? 4u : 16u;
+    if (!buf || ((uintptr_t)buf & (width - 1)) || bytes % width)
+        return fail(VS_ERR_INVALID, "buf must be non-null and aligned, bytes a multiple of the word width");
+    if (bytes == 0) return VS_OK;
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    void* sink = nullptr;
+    if ((mode & 1) == 0) VS_HIP(lib_alloc(ctx, &sink, (size_t)calib_sink_words() * 4, ctx->stream), "hipMallocAsync(sink)");
+    const hipError_t e = launch_stream_probe(buf, bytes, mode, static_cast<uint32_t*>(sink), ctx->stream);
+    if (sink) lib_free(ctx, sink);
+    if (e != hipSuccess) return hip_fail(e, "stream probe");
+    return VS_OK;
+}
+
 extern "C" vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {
     if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
     if (n == 0) return VS_OK;

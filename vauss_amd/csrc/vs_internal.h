@@ -336,6 +336,11 @@ hipError_t launch_geo_encode(const float* m, const float* v, uint32_t n, float e
 hipError_t launch_geo_decode(const uint32_t* words, uint32_t n, float epsilon, float* m, float* v, hipStream_t s);
 hipError_t launch_geo_zero_rows(uint32_t* words, const uint32_t* rows, uint32_t num_rows, uint32_t row_width,
                                 uint64_t num_words, hipStream_t s);
+// Streaming kernels of known traffic for memory-counter calibration
+// (k_calib.hip): mode bit 0 = write (else read), bit 1 = 4-byte words (else
+// 16-byte); `sink` holds calib_sink_words() u32 for the read kernels.
+hipError_t launch_stream_probe(void* buf, uint64_t bytes, int mode, uint32_t* sink, hipStream_t s);
+uint32_t calib_sink_words();
 hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float* gt, uint32_t w, uint32_t h,
                                float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
 hipError_t launch_loss_forward(const LossArgs& a, hipStream_t s);
