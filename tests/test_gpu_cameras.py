@@ -2,8 +2,9 @@
 (kernels/camera_model/{radial_tangential_8,thin_prism_fisheye}.rs) against the
 CPU oracle: forward bit for bit (counts, sorted order, projected rows, image),
 dense gradients at the contract bar with the projection stage checked on its
-own (end to end, rows the oracle itself cannot reproduce under 1e-6 noise in
-v_combined are left to the stage check), and the fused update bit for bit."""
+own (end to end, the few rows the oracle itself cannot reproduce under 1e-6
+noise in v_combined are counted, capped per case and checked at a bar scaled
+to their measured condition), and the fused update bit for bit."""
 import dataclasses
 
 import numpy as np
@@ -13,7 +14,7 @@ import torch
 import vauss_amd as va
 from oracle import pyoracle as po
 from tests._util import circle_mask, gpu_state_arrays, l1_cotangent_np, to_gpu
-from tests.test_gpu_parity import _check_forward, _check_grads, _check_param_grads, ill_conditioned_rows
+from tests.test_gpu_parity import _check_forward, _check_grads, _check_param_grads, check_ill_conditioned_rows, row_sensitivity
 from vauss_amd import scenes
 
 pytestmark = pytest.mark.gpu
@@ -22,9 +23,14 @@ RT8 = va.RadialTangential8(-0.15, 0.06, -0.01, 0.05, 0.02, -0.005, 0.03, -0.02)
 TPF = va.ThinPrismFisheye(va.KannalaBrandt4(0.03, -0.02, 0.01, -0.005), 0.02, -0.015, 0.01, -0.01)
 
 
-@pytest.mark.parametrize("cfg,view,model,mip", [("c2", 0, RT8, False), ("c3", 2, RT8, True), ("c5", 0, TPF, False),
-                                                ("c3", 5, TPF, False)], ids=["c2-rt8", "c3-rt8-mip", "c5-tpf", "c3-tpf"])
-def test_camera_model_parity(cfg, view, model, mip):
+# the largest share of visible rows each case may leave to the condition-scaled bar
+ILL_CAP = {"c2-rt8": 0.0005, "c3-rt8-mip": 0.0005, "c5-tpf": 0.003, "c3-tpf": 0.0005}
+
+
+@pytest.mark.parametrize("cfg,view,model,mip,case", [("c2", 0, RT8, False, "c2-rt8"), ("c3", 2, RT8, True, "c3-rt8-mip"),
+                                                     ("c5", 0, TPF, False, "c5-tpf"), ("c3", 5, TPF, False, "c3-tpf")],
+                         ids=["c2-rt8", "c3-rt8-mip", "c5-tpf", "c3-tpf"])
+def test_camera_model_parity(cfg, view, model, mip, case):
     w = scenes.workload(cfg, 20_000)
     sc = w.scene
     cam_obj = dataclasses.replace(w.cameras[view], model=model)
@@ -49,11 +55,18 @@ def test_camera_model_parity(cfg, view, model, mip):
     _check_grads(vc[:, 5:9], rg["v_combined"][:, 5:9], "v_rgb_opacity")
     # Splats a few millimetres from the camera plane of the wide fisheye (C5)
     # take thin-prism terms in 1/z^3 and 1/z^4: their end-to-end gradients
-    # amplify atomic-order noise beyond any bar, so only the projection stage
-    # (every row, 1e-5) checks them.
-    bad = ill_conditioned_rows(ref, vc, rg["v_combined"])
-    assert bad.mean() < 0.01
+    # amplify atomic-order noise beyond the contract bar, so they are checked
+    # at a bar scaled to their measured condition (and the projection stage,
+    # every row at 1e-5, checks them exactly).
+    bad, sens = row_sensitivity(ref, vc, rg["v_combined"])
+    visible = int((ref.get(po.F_INTERSECT_COUNTS) > 0).sum())
+    print(f"[ill-conditioned] {case}: {int(bad.sum())} of {visible} visible rows", flush=True)
+    assert bad.sum() <= ILL_CAP[case] * visible, (case, int(bad.sum()), visible)
     _check_param_grads(g, rg, ref, vc, exclude=bad)
+    vt = g.v_transforms.cpu().numpy()
+    for got, want, name in ((vt, rg["v_transforms"], "v_transforms"), (g.v_raw_opac.cpu().numpy(), rg["v_raw_opac"], "v_raw_opacity"),
+                            (g.v_coeffs.cpu().numpy(), rg["v_sh"], "v_sh")):
+        check_ill_conditioned_rows(got, want, vc, rg["v_combined"], bad, sens, name)
 
     nn = sc.num_splats
     rng = np.random.default_rng(4)
