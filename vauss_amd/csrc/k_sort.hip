@@ -84,72 +84,86 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_upsweep_kernel(const K* __res
     table[(size_t)d * nblocks + blockIdx.x] = c;
 }
 
-// Block-level ranking of one tile of up to BLOCK * ITEMS keys.  On return the tile
-// sits digit-ordered (and stable) in s_keys/s_vals, digit_start[d] is the
-// first LDS slot of digit d and d_count[d] (thread d) its count in the tile.
+// Block-level ranking of one tile of up to BLOCK * ITEMS keys, in two
+// phases so that a one-sweep pass can publish its digit counts (and look back)
+// between them:
+//  * count(): loads the tile, ranks every key among the equal digits of its
+//    wavefront (ballot matching), and turns the per-wave digit histograms into
+//    each wave's exclusive offset within its digit; returns, in thread d < 256,
+//    the tile's count of digit d;
+//  * place(): from those counts, digit_start[d] (the first LDS slot of digit d)
+//    and the digit-ordered (stable) tile in s_keys / s_vals.
 template <typename K, int BLOCK, int ITEMS>
-__device__ __forceinline__ uint32_t rank_tile(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
-                                              uint32_t base, uint32_t n, uint32_t shift,
-                                              uint32_t (*wave_hist)[256], uint32_t* digit_start, uint32_t* s_tot,
-                                              K* s_keys, uint32_t* s_vals) {
+struct TileRanker {
     static_assert(BLOCK >= 256 && BLOCK % 64 == 0, "one thread per digit");
-    constexpr int WAVES = BLOCK / 64;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // Issue every load of the tile before any ranking step, so a wavefront
-    // waits for memory once rather than once per step.
+    static constexpr int WAVES = BLOCK / 64;
     K key[ITEMS];
     uint32_t val[ITEMS], dig[ITEMS], rank[ITEMS];
-    const uint32_t wbase = base + wave * (64 * ITEMS);
-#pragma unroll
-    for (int s = 0; s < ITEMS; ++s) {
-        const uint32_t idx = wbase + s * 64 + lane;
-        key[s] = idx < n ? keys_in[idx] : (K)0;
-    }
-#pragma unroll
-    for (int s = 0; s < ITEMS; ++s) {
-        const uint32_t idx = wbase + s * 64 + lane;
-        val[s] = idx < n ? vals_in[idx] : 0u;
-    }
-    for (uint32_t i = threadIdx.x; i < WAVES * 256; i += BLOCK) (&wave_hist[0][0])[i] = 0;
-    __syncthreads();
-
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-#pragma unroll
-    for (int s = 0; s < ITEMS; ++s) {
-        const uint32_t idx = wbase + s * 64 + lane;
-        const bool valid = idx < n;
-        const uint32_t d = digit_of(key[s], shift);
-        dig[s] = valid ? d : 256u;
-        uint64_t peers = __ballot(valid);
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const uint64_t bal = __ballot((d >> b) & 1u);
-            peers &= ((d >> b) & 1u) ? bal : ~bal;
-        }
-        uint32_t r = 0;
-        if (valid) {
-            const uint32_t before = wave_hist[wave][d];
-            r = before + (uint32_t)__popcll(peers & lt_mask);
-            if ((peers & lt_mask) == 0) wave_hist[wave][d] = before + (uint32_t)__popcll(peers);
-        }
-        rank[s] = r;
-        __builtin_amdgcn_wave_barrier();
-    }
-    __syncthreads();
-    // Per-digit totals, wave offsets and the block's digit starts (threads 0..255, one digit each).
     uint32_t run = 0;
-    {
+
+    __device__ __forceinline__ uint32_t count(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+                                              uint32_t base, uint32_t n, uint32_t shift, uint32_t (*wave_hist)[256]) {
+        const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        // Issue every load of the tile before any ranking step, so a wavefront
+        // waits for memory once rather than once per step.
+        const uint32_t wbase = base + wave * (64 * ITEMS);
+#pragma unroll
+        for (int s = 0; s < ITEMS; ++s) {
+            const uint32_t idx = wbase + s * 64 + lane;
+            key[s] = idx < n ? keys_in[idx] : (K)0;
+        }
+#pragma unroll
+        for (int s = 0; s < ITEMS; ++s) {
+            const uint32_t idx = wbase + s * 64 + lane;
+            val[s] = idx < n ? vals_in[idx] : 0u;
+        }
+        for (uint32_t i = threadIdx.x; i < WAVES * 256; i += BLOCK) (&wave_hist[0][0])[i] = 0;
+        __syncthreads();
+
+        const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+        for (int s = 0; s < ITEMS; ++s) {
+            const uint32_t idx = wbase + s * 64 + lane;
+            const bool valid = idx < n;
+            const uint32_t d = digit_of(key[s], shift);
+            dig[s] = valid ? d : 256u;
+            uint64_t peers = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const uint64_t bal = __ballot((d >> b) & 1u);
+                peers &= ((d >> b) & 1u) ? bal : ~bal;
+            }
+            uint32_t r = 0;
+            if (valid) {
+                const uint32_t before = wave_hist[wave][d];
+                r = before + (uint32_t)__popcll(peers & lt_mask);
+                if ((peers & lt_mask) == 0) wave_hist[wave][d] = before + (uint32_t)__popcll(peers);
+            }
+            rank[s] = r;
+            __builtin_amdgcn_wave_barrier();
+        }
+        __syncthreads();
+        // per-digit totals; each wave's count becomes its exclusive offset within the digit
+        run = 0;
         const uint32_t d = threadIdx.x;
-        uint32_t incl = 0;
         if (d < 256) {
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) {
                 const uint32_t c = wave_hist[w][d];
-                wave_hist[w][d] = run;     // becomes the wave's exclusive offset within digit d
+                wave_hist[w][d] = run;
                 run += c;
             }
-            // exclusive scan of run over the 256 digits
-            incl = run;
+        }
+        return run;
+    }
+
+    __device__ __forceinline__ void place(uint32_t (*wave_hist)[256], uint32_t* digit_start, uint32_t* s_tot,
+                                          K* s_keys, uint32_t* s_vals) {
+        const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const uint32_t d = threadIdx.x;
+        // exclusive scan of the digit counts over the 256 digits
+        uint32_t incl = run;
+        if (d < 256) {
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const uint32_t t = __shfl_up(incl, o);
@@ -163,19 +177,18 @@ __device__ __forceinline__ uint32_t rank_tile(const K* __restrict__ keys_in, con
             for (uint32_t w = 0; w < wave; ++w) wo += s_tot[w];
             digit_start[d] = wo + incl - run;
         }
-    }
-    __syncthreads();
+        __syncthreads();
 #pragma unroll
-    for (int s = 0; s < ITEMS; ++s) {
-        if (dig[s] < 256u) {
-            const uint32_t pos = digit_start[dig[s]] + wave_hist[wave][dig[s]] + rank[s];
-            s_keys[pos] = key[s];
-            s_vals[pos] = val[s];
+        for (int s = 0; s < ITEMS; ++s) {
+            if (dig[s] < 256u) {
+                const uint32_t pos = digit_start[dig[s]] + wave_hist[wave][dig[s]] + rank[s];
+                s_keys[pos] = key[s];
+                s_vals[pos] = val[s];
+            }
         }
+        __syncthreads();
     }
-    __syncthreads();
-    return run;
-}
+};
 
 template <typename K>
 __global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
@@ -193,7 +206,11 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_scatter_kernel(const K* __res
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
     const uint32_t base = blockIdx.x * SORT_TILE;
     if (base >= n) return;   // uniform per block
-    rank_tile<K, SORT_BLOCK, SORT_ITEMS>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
+    {
+        TileRanker<K, SORT_BLOCK, SORT_ITEMS> rk;
+        rk.count(keys_in, vals_in, base, n, shift, wave_hist);
+        rk.place(wave_hist, digit_start, s_tot, s_keys, s_vals);
+    }
     if (threadIdx.x < 256) s_gstart[threadIdx.x] = offsets[(size_t)threadIdx.x * nblocks + blockIdx.x];
     __syncthreads();
     const uint32_t count = min(SORT_TILE, n - base);
@@ -331,13 +348,22 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
     const uint32_t base = tile * TILE;
     // A tile past the end has no successor with keys.
     if (base >= n) return;
-    const uint32_t cnt = rank_tile<K, BLOCK, ITEMS>(keys_in, vals_in, base, n, shift, wave_hist, digit_start, s_tot, s_keys, s_vals);
-
     const uint32_t d = threadIdx.x;
+    // The pass's global digit counts (the sum of the eight histogram copies)
+    // are loaded first, so their latency overlaps the tile's.
+    uint32_t gh[HIST_COPIES];
+#pragma unroll
+    for (uint32_t x = 0; x < HIST_COPIES; ++x) gh[x] = d < 256 ? ghist[(size_t)x * ghist_copy_stride + d] : 0u;
+    TileRanker<K, BLOCK, ITEMS> rk;
+    const uint32_t cnt = rk.count(keys_in, vals_in, base, n, shift, wave_hist);
+
+    // The tile's digit counts are published as soon as they are known, and
+    // the look-back runs before the tile is reordered in LDS, so the tile's
+    // prefix reaches its successors as early as it can.
+    uint32_t excl = 0;
     if (d < 256) {
         uint32_t* my = status + (size_t)tile * 256 + d;
         status_store(my, (tile == 0 ? OS_PREFIX : OS_AGGREGATE) | cnt);
-        uint32_t excl = 0;
         if (tile > 0) {
             // Look back over predecessors LOOKBACK at a time (independent loads),
             // newest first, summing aggregates until a prefix; a not-yet-published
@@ -369,29 +395,26 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
             }
             status_store(my, OS_PREFIX | (excl + cnt));
         }
-        s_gstart[d] = excl;
     }
+    rk.place(wave_hist, digit_start, s_tot, s_keys, s_vals);
     // global exclusive start of digit d: sum of ghist[0..d) (block scan over 256)
     {
         const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         uint32_t c = 0u;
-        if (d < 256) {
 #pragma unroll
-            for (uint32_t x = 0; x < HIST_COPIES; ++x) c += ghist[(size_t)x * ghist_copy_stride + d];
-        }
+        for (uint32_t x = 0; x < HIST_COPIES; ++x) c += gh[x];
         uint32_t incl = c;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const uint32_t t = __shfl_up(incl, o);
             if ((int)lane >= o) incl += t;
         }
-        __syncthreads();                    // s_tot is reused
-        if (lane == 63 && d < 256) s_tot[wave] = incl;
+        if (lane == 63 && d < 256) s_tot[wave] = incl;   // place() has finished with s_tot
         __syncthreads();
         if (d < 256) {
             uint32_t wo = 0;
             for (uint32_t w = 0; w < wave; ++w) wo += s_tot[w];
-            s_gstart[d] += wo + incl - c;
+            s_gstart[d] = excl + wo + incl - c;
         }
     }
     __syncthreads();
