@@ -632,9 +632,13 @@ def summarize(args) -> int:
         def per_run(v):        # dispatches of one run (the same counter may come from two runs)
             runs = {key[0] for key in v}
             return max(sum(1 for key in v if key[0] == r) for r in runs) if v else 0
-        # steps of the profiled run: launches of the gaussian raster backward
-        nbwd = max([1] + [max(per_run(c) for c in v.values()) for k, v in per.items()
-                          if k.startswith("raster_bwd_kernel<")])
+        # per render: the forward stages' kernels (sort passes, histograms,
+        # compaction, scan ...) add up over the gaussian training renders of
+        # the run (launches of the bwd-info gaussian raster forward); the two
+        # backward kernels are taken per launch (some of the run's backwards
+        # stop at the raster gradients)
+        nrender = max([1] + [max(per_run(c) for c in v.values()) for k, v in per.items()
+                             if k.startswith("raster_fwd_kernel<true, false, false, false>")])
         for k, cs in sorted(per.items()):
             n = max(per_run(v) for v in cs.values())
             mean = {c: sum(v.values()) / len(v) for c, v in cs.items()}
@@ -659,8 +663,8 @@ def summarize(args) -> int:
                     continue
                 e = traffic["kernels"].setdefault(stage, {"fetch_bytes": 0.0, "write_bytes": 0.0, "valu_insts": 0.0,
                                                           "valu_classes": {}, "kernels": []})
-                # per step: a kernel launched several times a step (sort passes) adds up
-                reps = n / nbwd
+                # per render: a kernel launched several times a render (sort passes) adds up
+                reps = 1.0 if stage in ("raster_bwd", "project_bwd") else n / nrender
                 e["fetch_bytes"] += rb * reps
                 e["write_bytes"] += wb * reps
                 e["valu_insts"] += mean.get("SQ_INSTS_VALU", 0.0) * reps
