@@ -390,34 +390,40 @@ __global__ void __launch_bounds__(FIN_BLOCK) finalize_counts_kernel(uint32_t* __
     const uint32_t* dmin = stats + (size_t)BS_DMIN * nb;
     const uint32_t* dmax = stats + (size_t)BS_DMAX * nb;
     uint32_t* emit = stats + (size_t)BS_EMIT * nb;
-    uint32_t carry = 0;
+    // Each thread takes a contiguous chunk of the blocks: one read of every
+    // row (the chunk's loads in flight together), one block scan of the
+    // chunks' emitter counts, then the chunk's offsets written from a second
+    // (L2-resident) read of its counts.
+    const uint32_t per = (nb + FIN_BLOCK - 1) / FIN_BLOCK;
+    const uint32_t b0 = min(nb, threadIdx.x * per), b1 = min(nb, b0 + per);
     unsigned long long h_acc = 0;
-    uint32_t v_acc = 0, mn_acc = 0xFFFFFFFFu, mx_acc = 0u;
-    for (uint32_t start = 0; start < nb; start += FIN_BLOCK) {
-        const uint32_t i = start + threadIdx.x;
-        const uint32_t x = (i < nb) ? emit[i] : 0u;
-        if (i < nb) {
-            h_acc += hits[i];
-            v_acc += vis[i];
-            mn_acc = min(mn_acc, dmin[i]);
-            mx_acc = max(mx_acc, dmax[i]);
-        }
-        uint32_t incl = x;
+    uint32_t v_acc = 0, mn_acc = 0xFFFFFFFFu, mx_acc = 0u, e_acc = 0;
+#pragma unroll 4
+    for (uint32_t i = b0; i < b1; ++i) {
+        e_acc += emit[i];
+        h_acc += hits[i];
+        v_acc += vis[i];
+        mn_acc = min(mn_acc, dmin[i]);
+        mx_acc = max(mx_acc, dmax[i]);
+    }
+    uint32_t incl = e_acc;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t t = __shfl_up(incl, o);
-            if ((int)lane >= o) incl += t;
-        }
-        if (lane == 63) s_w[wave] = incl;
-        __syncthreads();
-        uint32_t before = 0, chunk = 0;
-        for (uint32_t w = 0; w < FIN_BLOCK / 64; ++w) {
-            if (w < wave) before += s_w[w];
-            chunk += s_w[w];
-        }
-        if (i < nb) emit[i] = carry + before + incl - x;
-        carry += chunk;
-        __syncthreads();
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o);
+        if ((int)lane >= o) incl += t;
+    }
+    if (lane == 63) s_w[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, carry = 0;
+    for (uint32_t w = 0; w < FIN_BLOCK / 64; ++w) {
+        if (w < wave) before += s_w[w];
+        carry += s_w[w];
+    }
+    uint32_t run = before + incl - e_acc;
+    for (uint32_t i = b0; i < b1; ++i) {
+        const uint32_t x = emit[i];
+        emit[i] = run;
+        run += x;
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) h_acc += __shfl_xor(h_acc, o);

@@ -67,6 +67,11 @@ __global__ void __launch_bounds__(256) tile_ranges_kernel(const uint32_t* __rest
 
 // DIST_NEAR / DIST_FAR depth map, kernels/helpers.rs:91-103.
 VS_DEV float dist_depth(float z) { return 100.0f / (100.0f - 0.2f) * (1.0f - 0.2f / mx(z, 0.2f)); }
+// The same map for the backward's gradient terms only, with the hardware
+// reciprocal (1 ulp) in place of the correctly rounded division.
+VS_DEV float dist_depth_grad(float z) {
+    return 100.0f / (100.0f - 0.2f) * (1.0f - 0.2f * __builtin_amdgcn_rcpf(mx(z, 0.2f)));
+}
 
 // Workgroups are dealt to the 8 XCDs round-robin; give XCD k the contiguous
 // band of tiles [k*per, (k+1)*per) so neighbouring tiles, which share most of
@@ -1006,7 +1011,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             // be non-finite off the disk) are zeroed on such lanes, so each
             // gradient component is 0 there without a select of its own.
             const float z = contrib ? h.z : 0.0f;
-            const float m = dist_depth(z);
+            const float m = dist_depth_grad(z);
             // gradient-only quotients and roots take the hardware reciprocal and
             // square root (1 ulp); the replayed forward above keeps IEEE division
             const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
