@@ -257,6 +257,8 @@ def main() -> int:
     o = torch.from_numpy(sc.raw_opacities).to(dev)
     cams = [c.uniforms(wl.img_size) for c in wl.cameras]
     gt = torch.from_numpy(scenes.loss_target(wl.img_size)).to(dev)
+    # the training target as the reference's loss reads it: u32 RGBA8 per pixel
+    gt_packed = va.pack_rgba8(torch.cat([gt, torch.ones_like(gt[..., :1])], dim=-1).cpu()).to(dev)
     mc, mr = wl.mask_center, wl.mask_radius
     n = sc.num_splats
     k = (sc.sh_degree + 1) ** 2
@@ -269,7 +271,7 @@ def main() -> int:
     def step(view: int, list_histogram: bool = False, used: bool = False):
         nonlocal tile_lists
         out = va.render(cams[view], wl.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
-        v = va.l1_cotangent(out.out_img, gt, mc, mr)
+        v = va.l1_cotangent(out.out_img, gt_packed, mc, mr)
         g = va.render_backward(out, t, s, o, v)
         aux = (out.aux.num_visible, out.aux.num_intersections)
         if used:      # intersections the raster kernels consume: the shrunk tile ranges

@@ -495,6 +495,13 @@ vs_status vs_scan_in_place_u32(vs_ctx* ctx, uint32_t* data, uint32_t n);
 vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const float* gt,
                           uint32_t img_w, uint32_t img_h, float mask_cx, float mask_cy,
                           float mask_radius, float* v_out);
+/* vs_l1_cotangent with the ground truth as the reference's training loss
+ * takes it (crates/splat-train-loss/src/lib.rs, header and :93,1042-1044):
+ * gt_packed [H,W] u32 RGBA8, r in the low byte, each channel byte x (1/255)
+ * in f32. */
+vs_status vs_l1_cotangent_packed(vs_ctx* ctx, const float* pred, uint32_t channels, const uint32_t* gt_packed,
+                                 uint32_t img_w, uint32_t img_h, float mask_cx, float mask_cy,
+                                 float mask_radius, float* v_out);
 
 /* ---- image loss: L1 + SSIM ------------------------------------------------------- */
 

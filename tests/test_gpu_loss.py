@@ -119,3 +119,33 @@ def test_l1_cotangent_matches_closed_form(cfg):
     want12 = np.zeros_like(pred12)
     want12[..., :4] = want
     np.testing.assert_array_equal(got12.view(np.uint32), want12.view(np.uint32))
+
+
+def test_l1_cotangent_packed_target_matches_unpacked():
+    """vs_l1_cotangent_packed reads the reference's u32 RGBA8 target
+    (crates/splat-train-loss/src/lib.rs:93,1042-1044: byte x (1/255) in f32):
+    bit-equal to vs_l1_cotangent on the float target byte * float32(1/255) and
+    to the closed form, with ties at every 7th row, at C5's image size and
+    mask, for 4- and 3-channel predictions."""
+    from tests._util import circle_mask, l1_cotangent_np
+    w = scenes.workload("c5", 1000)
+    W, H = w.img_size
+    rng = np.random.default_rng(11)
+    rgba8 = rng.integers(0, 256, (H, W, 4), dtype=np.uint8)
+    gt = rgba8[..., :3].astype(np.float32) * np.float32(1.0 / 255.0)
+    pred = rng.uniform(0, 1, (H, W, 4)).astype(np.float32)
+    pred[::7, :, :3] = gt[::7]                                         # exact ties
+    mask = circle_mask(w.img_size, w.mask_center, w.mask_radius)
+    print(f"[case] l1 cotangent packed {W}x{H} mask_radius={w.mask_radius}", flush=True)
+    gtp = va.pack_rgba8(torch.from_numpy(rgba8)).cuda()
+    assert gtp.dtype == torch.int32 and tuple(gtp.shape) == (H, W)
+    want = l1_cotangent_np(pred, gt, mask)
+    for c in (4, 3):
+        p = torch.from_numpy(np.ascontiguousarray(pred[..., :c])).cuda()
+        got = va.l1_cotangent(p, gtp, w.mask_center, w.mask_radius).cpu().numpy()
+        ref = va.l1_cotangent(p, torch.from_numpy(gt).cuda(), w.mask_center, w.mask_radius).cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+        np.testing.assert_array_equal(got.view(np.uint32), want[..., :c].view(np.uint32))
+    assert (got[::7][..., :3] == 0).all()
+    with pytest.raises(ValueError):
+        va.l1_cotangent(p, gtp[:, :-1], w.mask_center, w.mask_radius)

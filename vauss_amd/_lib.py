@@ -152,6 +152,8 @@ SIGNATURES = {
                                          C.POINTER(VsLossCfg), C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
     "vs_l1_cotangent": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
                                   C.c_float, C.c_float, C.c_float, C.c_void_p]),
+    "vs_l1_cotangent_packed": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
+                                         C.c_float, C.c_float, C.c_float, C.c_void_p]),
 }
 
 _LIB = None

@@ -1428,8 +1428,8 @@ extern "C" vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint
     return VS_OK;
 }
 
-extern "C" vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const float* gt, uint32_t w,
-                                     uint32_t h, float mcx, float mcy, float mr, float* v_out) {
+static vs_status l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const void* gt, bool packed, uint32_t w,
+                              uint32_t h, float mcx, float mcy, float mr, float* v_out) {
     if (!ctx || !pred || !gt || !v_out) return fail(VS_ERR_INVALID, "null argument");
     if (channels < 3) return fail(VS_ERR_INVALID, "prediction needs at least 3 channels");
     uint64_t count = (uint64_t)w * h;
@@ -1451,6 +1451,16 @@ extern "C" vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t ch
     }
     const float inv = count ? 1.0f / (3.0f * (float)count) : 0.0f;
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
-    VS_HIP(launch_l1_cotangent(pred, channels, gt, w, h, mcx, mcy, mr, inv, v_out, ctx->stream), "l1 cotangent");
+    VS_HIP(launch_l1_cotangent(pred, channels, gt, packed, w, h, mcx, mcy, mr, inv, v_out, ctx->stream), "l1 cotangent");
     return VS_OK;
+}
+
+extern "C" vs_status vs_l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const float* gt, uint32_t w,
+                                     uint32_t h, float mcx, float mcy, float mr, float* v_out) {
+    return l1_cotangent(ctx, pred, channels, gt, false, w, h, mcx, mcy, mr, v_out);
+}
+
+extern "C" vs_status vs_l1_cotangent_packed(vs_ctx* ctx, const float* pred, uint32_t channels, const uint32_t* gt_packed,
+                                            uint32_t w, uint32_t h, float mcx, float mcy, float mr, float* v_out) {
+    return l1_cotangent(ctx, pred, channels, gt_packed, true, w, h, mcx, mcy, mr, v_out);
 }

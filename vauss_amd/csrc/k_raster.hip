@@ -1080,11 +1080,14 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
 // sign(pred - gt) * inv_count on rgb, 0 on the other channels and outside
 // the mask.  Images whose channel count is a multiple of 4 (RGBA, the
 // 12-channel geometry render) are read and written as float4s: the first
-// holds rgb, the rest are zero.
+// holds rgb, the rest are zero.  A PACKED target is [H,W] RGBA8 (r in the
+// low byte), each channel byte x (1/255) in f32 as the reference's loss
+// kernels unpack it (crates/splat-train-loss/src/lib.rs:93,1042-1044).
 VS_DEV float l1_sign(float p, float g, float inv) { const float d = p - g; return (d > 0.0f) ? inv : ((d < 0.0f) ? -inv : 0.0f); }
+constexpr float L1_INV_255 = 1.0f / 255.0f;
 
-template <bool VEC4>
-__global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, const float* __restrict__ gt, uint32_t w,
+template <bool VEC4, bool PACKED>
+__global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, const void* __restrict__ gt_in, uint32_t w,
                                     uint32_t h, float mcx, float mcy, float mr, float inv_count, float* __restrict__ v) {
     const uint32_t pid = blockIdx.x * blockDim.x + threadIdx.x;
     if (pid >= w * h) return;
@@ -1095,7 +1098,16 @@ __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, 
         in_mask = dx * dx + dy * dy <= mr * mr;
     }
     const float inv = in_mask ? inv_count : 0.0f;
-    const float g0 = gt[(size_t)pid * 3], g1 = gt[(size_t)pid * 3 + 1], g2 = gt[(size_t)pid * 3 + 2];
+    float g0, g1, g2;
+    if constexpr (PACKED) {
+        const uint32_t q = static_cast<const uint32_t*>(gt_in)[pid];
+        g0 = (float)(q & 0xFFu) * L1_INV_255;
+        g1 = (float)((q >> 8) & 0xFFu) * L1_INV_255;
+        g2 = (float)((q >> 16) & 0xFFu) * L1_INV_255;
+    } else {
+        const float* gt = static_cast<const float*>(gt_in);
+        g0 = gt[(size_t)pid * 3]; g1 = gt[(size_t)pid * 3 + 1]; g2 = gt[(size_t)pid * 3 + 2];
+    }
     if constexpr (VEC4) {
         const uint32_t q4 = C / 4;
         const float4 p = reinterpret_cast<const float4*>(pred)[(size_t)pid * q4];
@@ -1194,13 +1206,16 @@ hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s,
     return hipGetLastError();
 }
 
-hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const float* gt, uint32_t w, uint32_t h, float mcx,
-                               float mcy, float mr, float inv_count, float* v_out, hipStream_t s) {
+hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const void* gt, bool packed, uint32_t w, uint32_t h,
+                               float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s) {
     const uint32_t n = w * h;
     if (n == 0) return hipSuccess;
     const bool vec4 = channels >= 4 && channels % 4 == 0 && ((uintptr_t)pred & 15u) == 0 && ((uintptr_t)v_out & 15u) == 0;
-    if (vec4) l1_cotangent_kernel<true><<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
-    else l1_cotangent_kernel<false><<<(n + 255) / 256, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    const dim3 grid((n + 255) / 256);
+    if (vec4 && packed) l1_cotangent_kernel<true, true><<<grid, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    else if (vec4) l1_cotangent_kernel<true, false><<<grid, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    else if (packed) l1_cotangent_kernel<false, true><<<grid, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
+    else l1_cotangent_kernel<false, false><<<grid, 256, 0, s>>>(pred, channels, gt, w, h, mcx, mcy, mr, inv_count, v_out);
     return hipGetLastError();
 }
 

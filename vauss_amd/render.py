@@ -663,14 +663,24 @@ def scan_in_place(x: torch.Tensor) -> None:
 
 
 def l1_cotangent(pred: torch.Tensor, gt: torch.Tensor, mask_center=(0.0, 0.0), mask_radius: float = 0.0) -> torch.Tensor:
-    """d(mean L1 over rgb)/d pred for an [H,W,C] prediction and [H,W,3] target."""
+    """d(mean L1 over rgb)/d pred for an [H,W,C] prediction and an [H,W,3]
+    float32 target, or an [H,W] int32 packed RGBA8 target (the reference's
+    u8 ground truth, unpacked as byte x (1/255))."""
     pred = pred.contiguous()
     gt = gt.contiguous()
     h, w, c = pred.shape
     ctx = Context.get(pred.device)
     v = torch.empty_like(pred)
-    _lib.check(ctx.lib.vs_l1_cotangent(ctx.handle, _ptr(pred), c, _ptr(gt), w, h, float(mask_center[0]),
-                                       float(mask_center[1]), float(mask_radius), _ptr(v)))
+    if gt.dtype == torch.int32:
+        if tuple(gt.shape) != (h, w):
+            raise ValueError(f"a packed target must be int32 [{h}, {w}], got {tuple(gt.shape)}")
+        fn = ctx.lib.vs_l1_cotangent_packed
+    else:
+        if gt.dtype != torch.float32 or tuple(gt.shape) != (h, w, 3):
+            raise ValueError(f"a float target must be float32 [{h}, {w}, 3], got {gt.dtype} {tuple(gt.shape)}")
+        fn = ctx.lib.vs_l1_cotangent
+    _lib.check(fn(ctx.handle, _ptr(pred), c, _ptr(gt), w, h, float(mask_center[0]), float(mask_center[1]),
+                  float(mask_radius), _ptr(v)))
     return v
 
 
