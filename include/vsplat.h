@@ -552,6 +552,13 @@ typedef enum vs_probe_mode {
 } vs_probe_mode;
 vs_status vs_stream_probe(vs_ctx* ctx, void* buf, uint64_t bytes, int32_t mode);
 
+/* The compositing kernels' 2^x (the G = 2^(-sigma log2 e) of every forward
+ * and backward raster pass, the hardware's exp2 instruction), for checking:
+ * out[i] = G(x) for the f32 x whose bit pattern is first_bits + i, i < count.
+ * No counterpart in the reference, whose compositing exp is its shader's.
+ * VS_ERR_INVALID when the range passes bit pattern 0xFFFFFFFF.  Stream-ordered. */
+vs_status vs_compositing_exp2(vs_ctx* ctx, uint32_t first_bits, uint64_t count, float* out);
+
 #ifdef __cplusplus
 }
 #endif

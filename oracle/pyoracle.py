@@ -131,6 +131,7 @@ def load() -> C.CDLL:
     lib.or_atan2f.argtypes = [C.c_float, C.c_float]
     lib.or_expf_n.argtypes = [_F, _F, C.c_uint64]
     lib.or_exp2n_n.argtypes = [_F, _F, C.c_uint64]
+    lib.or_set_comp_exp2_table.argtypes = [C.c_void_p, C.c_uint32, C.c_uint64]
     lib.or_logf_n.argtypes = [_F, _F, C.c_uint64]
     lib.or_atan2f_n.argtypes = [_F, _F, _F, C.c_uint64]
     lib.or_sh_basis.argtypes = [C.c_uint32, _F, _F]
@@ -352,8 +353,26 @@ def expf(x):
     return out
 
 
+_COMP_EXP2 = None   # the installed table; the library holds its pointer
+
+
+def set_comp_exp2_table(tab, first_bits: int = 0x80000000):
+    """Makes the compositing loops take G = 2^x from `tab` (float32, tab[i] for
+    the f32 x whose bit pattern is first_bits + i) wherever it covers x, as the
+    GPU kernels' exp2 instruction gives it; None restores exp2n everywhere."""
+    global _COMP_EXP2
+    lib = load()
+    if tab is None:
+        lib.or_set_comp_exp2_table(None, 0, 0)
+        _COMP_EXP2 = None
+        return
+    a = np.ascontiguousarray(tab, np.float32)
+    lib.or_set_comp_exp2_table(C.c_void_p(a.ctypes.data), int(first_bits), int(a.size))
+    _COMP_EXP2 = a
+
+
 def exp2n(x):
-    """The compositing loops' 2^x (or_math.h exp2n_c)."""
+    """The compositing loops' default 2^x (or_math.h exp2n_c)."""
     a = np.ascontiguousarray(x, np.float32)
     out = np.empty_like(a)
     load().or_exp2n_n(_fp(a), _fp(out), a.size)

@@ -32,10 +32,11 @@
 //      A = (c00/2) L, B = c01 L, C = (c11/2) L, L = log2(e) in f32
 //    (the reference's 0.5(c00 dx^2 + c11 dy^2) + c01 dx dy times log2 e, up to
 //    rounding and the contraction its shader compiler is also free to apply;
-//    s2 >= 0 exactly when sigma >= 0), G = exp2n(-s2) (or_math.h),
-//    alpha = min(0.999, opac G), T' = T (1 - alpha),
+//    s2 >= 0 exactly when sigma >= 0), G = 2^(-s2) (comp_exp2_c below: the
+//    GPU's exp2 instruction from an installed table of its values, else
+//    exp2n of or_math.h), alpha = min(0.999, opac G), T' = T (1 - alpha),
 //    colour += max(c,0) * (alpha T) as an fma, final = fma(T, bg, colour).
-//    Surfels: G = exp2n(-(sigma L)) of their ray-plane sigma.
+//    Surfels: G = 2^(-(sigma L)) of their ray-plane sigma.
 #include "vs_oracle.h"
 #include "or_math.h"
 
@@ -52,6 +53,28 @@
 using namespace orc;
 
 namespace {
+
+// G = 2^x of the compositing loops.  The GPU kernels take it from the
+// hardware's exp2 instruction, whose bits no CPU routine reproduces; a caller
+// that holds that instruction's values for a range of f32 bit patterns
+// (normally every x from -0 down to -128) installs them with
+// or_set_comp_exp2_table and the loops composite with the same G.  Outside
+// the table, and with none installed, G is exp2n_c (or_math.h).  That covers
+// x < -128, where both give less than 2^-127 and every cutoff rejects the
+// pair; a NaN x, whose sigma the sigma >= 0 test rejects; and +0, which takes
+// the value of -0 (both are 1).
+const float* g_exp2_tab = nullptr;
+uint32_t g_exp2_first = 0;
+uint64_t g_exp2_count = 0;
+inline float comp_exp2_c(float x) {
+    if (g_exp2_tab) {
+        uint32_t b;
+        std::memcpy(&b, &x, 4);
+        if (b == 0u) b = 0x80000000u;
+        if (b >= g_exp2_first && (uint64_t)(b - g_exp2_first) < g_exp2_count) return g_exp2_tab[b - g_exp2_first];
+    }
+    return exp2n_c(x);
+}
 
 constexpr uint32_t TILE_W = 16;                 // kernels/helpers.rs:15-16
 constexpr float ALPHA_CUTOFF_MID = 1.0f / 255.0f;   // kernels/helpers.rs:23
@@ -1268,11 +1291,11 @@ extern "C" int or_render_forward(const or_camera* cam_in, uint32_t W, uint32_t H
                         if (!hit.valid) continue;          // no intersection in front of the near limit
                         sigma = hit.sigma;
                         z = hit.z;
-                        G = exp2n_c(-(sigma * LOG2E_F));
+                        G = comp_exp2_c(-(sigma * LOG2E_F));
                     } else {
                         const float dx = pcx - s.x, dy = pcy - s.y;
                         sigma = std::fma(std::fma(s.A, dx, s.B * dy), dx, (s.C * dy) * dy);   // base 2
-                        G = exp2n_c(-sigma);
+                        G = comp_exp2_c(-sigma);
                     }
                     const float alpha = fmin_(0.999f, s.opac * G);
                     const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
@@ -1434,7 +1457,7 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
                         const SurfelHit h = surfel_hit(a, pcx, pcy);
                         if (!h.valid) continue;
                         const float sigma = h.sigma;
-                        const float G = exp2n_c(-(sigma * LOG2E_F));
+                        const float G = comp_exp2_c(-(sigma * LOG2E_F));
                         const float alpha = fmin_(0.999f, opac * G);
                         const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
                         if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -1499,7 +1522,7 @@ extern "C" int or_render_backward(const or_fwd* f, const float* v_out, int threa
                     const float dx = pcx - x, dy = pcy - y;
                     const float sigma = std::fma(std::fma((0.5f * c00) * LOG2E_F, dx, (c01 * LOG2E_F) * dy), dx,
                                                  (((0.5f * c11) * LOG2E_F) * dy) * dy);   // base 2, as the forward's
-                    const float G = exp2n_c(-sigma);
+                    const float G = comp_exp2_c(-sigma);
                     const float alpha = fmin_(0.999f, opac * G);
                     const float w_cut = smooth ? alpha_cutoff_weight(alpha) : ((alpha >= ALPHA_CUTOFF_MID) ? 1.0f : 0.0f);
                     if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -2187,6 +2210,11 @@ extern "C" void or_prefix_sum_u32(const uint32_t* in, uint32_t* out, uint32_t n)
 extern "C" float or_expf(float x) { return expf_c(x); }
 extern "C" void or_exp2n_n(const float* x, float* y, uint64_t n) {
     for (uint64_t i = 0; i < n; ++i) y[i] = exp2n_c(x[i]);
+}
+extern "C" void or_set_comp_exp2_table(const float* tab, uint32_t first_bits, uint64_t count) {
+    g_exp2_tab = (tab && count) ? tab : nullptr;
+    g_exp2_first = first_bits;
+    g_exp2_count = g_exp2_tab ? count : 0;
 }
 extern "C" float or_logf(float x) { return logf_c(x); }
 extern "C" float or_atan2f(float y, float x) { return atan2f_c(y, x); }

@@ -196,8 +196,12 @@ float or_expf(float x);
 float or_logf(float x);
 float or_atan2f(float y, float x);
 void or_expf_n(const float* x, float* y, uint64_t n);
-/* The compositing loops' 2^x (exp2n). */
+/* The compositing loops' default 2^x (exp2n). */
 void or_exp2n_n(const float* x, float* y, uint64_t n);
+/* The compositing loops' 2^x taken from a table: tab[i] is G for the f32 x
+ * whose bit pattern is first_bits + i (i < count); other x keep exp2n.  The
+ * table is not copied and must outlive its use; tab = NULL restores exp2n. */
+void or_set_comp_exp2_table(const float* tab, uint32_t first_bits, uint64_t count);
 void or_logf_n(const float* x, float* y, uint64_t n);
 void or_atan2f_n(const float* y, const float* x, float* r, uint64_t n);
 

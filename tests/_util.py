@@ -31,6 +31,44 @@ def dev_to_numpy(ptr, shape, dtype) -> np.ndarray:
     return out
 
 
+# The compositing kernels' G = 2^x is the GPU's exp2 instruction; the oracle
+# composites with its values for every f32 x from -0 (bit pattern 0x80000000)
+# down to -128 (0xC3000000).
+EXP2_FIRST = 0x80000000
+EXP2_COUNT = 0xC3000000 - 0x80000000 + 1
+_EXP2_TABLE = None
+
+
+def device_comp_exp2_table() -> np.ndarray:
+    """The device's compositing 2^x over EXP2_FIRST .. + EXP2_COUNT (4.5 GB, built once)."""
+    global _EXP2_TABLE
+    if _EXP2_TABLE is None:
+        import torch
+        import vauss_amd as va
+        print(f"[case] compositing exp2 table, {EXP2_COUNT} inputs", flush=True)
+        d = va.compositing_exp2(EXP2_FIRST, EXP2_COUNT)
+        _EXP2_TABLE = d.cpu().numpy()
+        del d
+        torch.cuda.empty_cache()
+    return _EXP2_TABLE
+
+
+def use_device_comp_exp2() -> None:
+    """Makes the oracle composite with the device's 2^x (a no-op once installed)."""
+    from oracle import pyoracle as po
+    tab = device_comp_exp2_table()
+    if po._COMP_EXP2 is not tab:
+        po.set_comp_exp2_table(tab, EXP2_FIRST)
+
+
+def use_default_comp_exp2() -> None:
+    """Restores the oracle's own exp2n (CPU tests and golden vectors)."""
+    import sys
+    po = sys.modules.get("oracle.pyoracle")
+    if po is not None and po._COMP_EXP2 is not None:
+        po.set_comp_exp2_table(None)
+
+
 def to_gpu(scene):
     import torch
     return (torch.from_numpy(scene.transforms).cuda(), torch.from_numpy(scene.sh_coeffs).cuda(),

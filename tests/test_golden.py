@@ -2,8 +2,11 @@
 
 The CPU tests check that the oracle still reproduces every fixture bit for
 bit; the GPU tests check the HIP path against the fixtures with the parity
-bars (integer outputs and RGBA bit for bit, gradients within 1e-3 relative /
-1e-5 absolute of each entry, or 1e-3 of the group's largest gradient)."""
+bars: integer outputs bit for bit, RGBA within 1e-4 absolute (the fixtures
+composite with the oracle's exp2n, the kernels with the GPU's exp2
+instruction, both within 2.1 ulp of 2^x) and bit for bit against the oracle
+re-run with the GPU's exp2 values, gradients within 1e-3 relative / 1e-5
+absolute of each entry, or 1e-3 of the group's largest gradient."""
 import ctypes as C
 import glob
 import os
@@ -89,7 +92,12 @@ def test_gpu_matches_fixture(path):
     np.testing.assert_array_equal(gpu["tile"], fx["isect_tile"])
     np.testing.assert_array_equal(gpu["gid"], fx["isect_gid"])
     np.testing.assert_array_equal(gpu["ranges"], fx["tile_offsets"])
-    np.testing.assert_array_equal(out.out_img.cpu().numpy().view(np.uint32), fx["out_img"].view(np.uint32))
+    got_img = out.out_img.cpu().numpy()
+    assert float(np.abs(got_img - fx["out_img"]).max()) <= 1e-4
+    from oracle import pyoracle as po
+    f = po.render_forward(po.OrCamera.from_buffer_copy(_camera_bytes(fx)), img, fx["transforms"], fx["sh_coeffs"],
+                          fx["raw_opacities"], background=tuple(fx["background"]), flags=int(fx["flags"]))
+    np.testing.assert_array_equal(got_img.view(np.uint32), f.get(po.F_OUT_IMG).view(np.uint32))
     np.testing.assert_array_equal(out.aux.visible.cpu().numpy(), fx["visible"])
     g = va.render_backward(out, t, s, o, torch.from_numpy(fx["v_out"]).cuda())
     vc = g.v_combined.cpu().numpy()

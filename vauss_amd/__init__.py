@@ -15,7 +15,7 @@ from .camera import (  # noqa: F401
 )
 from .render import (  # noqa: F401
     Block8Moment, Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput,
-    ShStepState, SplatGrads, SplatRenderMode, adam_bias_corrections, geo_decode, geo_encode, geo_zero_rows,
+    ShStepState, SplatGrads, SplatRenderMode, adam_bias_corrections, compositing_exp2, geo_decode, geo_encode, geo_zero_rows,
     l1_cotangent, pose_backward, prefix_sum, project_update, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
     radix_argsort_with_count, render, render_backward, scan_in_place, sh_degree_from_coeffs, sh_step, unpack_rgba8,
 )
@@ -26,7 +26,7 @@ __all__ = [
     "Camera", "KannalaBrandt4", "RadialTangential8", "ThinPrismFisheye", "PINHOLE", "fov_to_focal", "focal_to_fov", "max_render_theta",
     "Block8Moment", "ShStepState", "adam_bias_corrections", "sh_step",
     "Context", "ForwardState", "FusedAdam", "ProjectUpdateResult", "RasterPass", "RenderAux", "RenderOutput",
-    "SplatGrads", "SplatRenderMode", "VsError", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",
+    "SplatGrads", "SplatRenderMode", "VsError", "compositing_exp2", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",
     "pose_backward", "prefix_sum", "project_update", "radix_argsort", "radix_argsort_skip_low_with_count",
     "radix_argsort_u64", "radix_argsort_with_count", "render", "render_backward", "scan_in_place",
     "sh_degree_from_coeffs", "unpack_rgba8",

@@ -1333,6 +1333,16 @@ extern "C" vs_status vs_stream_probe(vs_ctx* ctx, void* buf, uint64_t bytes, int
     return VS_OK;
 }
 
+extern "C" vs_status vs_compositing_exp2(vs_ctx* ctx, uint32_t first_bits, uint64_t count, float* out) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (count > (1ull << 32) - first_bits) return fail(VS_ERR_INVALID, "the range passes bit pattern 0xFFFFFFFF");
+    if (count == 0) return VS_OK;
+    if (!out) return fail(VS_ERR_INVALID, "out is null");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_exp2_range(first_bits, count, out, ctx->stream), "compositing exp2");
+    return VS_OK;
+}
+
 extern "C" vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {
     if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
     if (n == 0) return VS_OK;

@@ -480,12 +480,12 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                 valid = hit.valid;              // the ray misses the plane or meets it before the near limit
                 sigma = hit.sigma;
                 zs = hit.z;
-                G = exp2n(-(sigma * LOG2E_F));
+                G = comp_exp2(-(sigma * LOG2E_F));
             } else {
                 const float4 sa = *reinterpret_cast<const float4*>(lds_a + off);
                 const float dx = pcx - sa.x, dy = pcy - sa.y;
                 sigma = raster_sigma(sa.z, sa.w, sb.x, dx, dy);   // base 2
-                G = exp2n_live(-sigma);
+                G = comp_exp2(-sigma);
             }
             // min(0.999, .) of a product that is NaN only when sigma is
             // (then the sigma test below rejects the pair): same value as mn().
@@ -816,7 +816,7 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 if (!(Tk > T_STOP)) continue;
                 const float dx = pcx[k] - sa.x, dy = pcy[k] - sa.y;
                 const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);   // base 2, as the forward's
-                const float G = exp2n_live(-sigma);
+                const float G = comp_exp2(-sigma);
                 const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);   // == mn(): see the forward
                 const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
                 if (!(sigma >= 0.0f && w_cut > 0.0f)) continue;
@@ -995,7 +995,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             // hit is computed, so the gradient below runs on every lane and one
             // select per component keeps the blending lanes' values)
             const SurfelHit h = surfel_hit<false>(m0, m1, m2, m3.z, pcx, pcy);
-            const float G = exp2n(-(h.sigma * LOG2E_F));
+            const float G = comp_exp2(-(h.sigma * LOG2E_F));
             const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);
             const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
             const float ae = alpha * w_cut;
@@ -1203,6 +1203,20 @@ hipError_t launch_raster_bwd(const RasterBwdArgs& a, bool smooth, hipStream_t s,
     }
     if (start) hipExtLaunchKernelGGL(k, grid, dim3(block), 0, s, start, stop, 0u, a);
     else k<<<grid, block, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+// out[i] = comp_exp2(x) for the f32 x whose bit pattern is first_bits + i.
+__global__ void __launch_bounds__(256) exp2_range_kernel(uint32_t first_bits, uint64_t count, float* __restrict__ out) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < count; i += stride)
+        out[i] = comp_exp2(__uint_as_float(first_bits + (uint32_t)i));
+}
+
+hipError_t launch_exp2_range(uint32_t first_bits, uint64_t count, float* out, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>(16384u, (count + 255u) / 256u);
+    exp2_range_kernel<<<grid, 256, 0, s>>>(first_bits, count, out);
     return hipGetLastError();
 }
 

@@ -57,48 +57,16 @@ VS_DEV float expf_c(float x) {
     return __builtin_ldexpf(p, (int)n);
 }
 
-// exp2 for the compositing loops, whose argument is -sigma in base-2 units
-// (the conic is staged pre-scaled by LOG2E_F): x = max(x, -127) (NaN ->
-// -127), n = rint(x), f = x - n in [-1/2, 1/2] (exact), 2^f = 1 + f P(f)
-// with P of degree 4 (least maximum relative error on [-1/2, 1/2]), result
-// ldexp(p, n): <= 2.1 ulp on [-126, 0]; v_max, v_rndne, v_sub, five FMAs,
-// v_cvt, v_ldexp.  The CPU restatement also clamps x at 128 to keep its int
-// conversion defined; the results agree for every x: above 128 both give
-// +inf (here the conversion saturates), and a positive x comes only from a
-// pair the sigma >= 0 test rejects.
+// 2^x for the compositing loops, whose argument is -sigma in base-2 units
+// (the conic is staged pre-scaled by LOG2E_F): the hardware's v_exp_f32, one
+// transcendental instruction (the degree-5 polynomial it replaced took nine
+// VALU instructions per pixel and splat).  On [-126, 0] it is within 1 ulp of
+// 2^x; below -126 it returns less than 2^-126 (or 0), so opacity x G stays
+// under every cutoff (1/255 - 5e-4 at the lowest) and the pair is rejected.
+// A NaN argument (a NaN sigma) gives NaN, and the sigma >= 0 test rejects the
+// pair.  vs_compositing_exp2 returns this function's values for checking.
 constexpr float LOG2E_F = 1.44269502f;
-VS_DEV float exp2n(float x) {
-    x = __builtin_fmaxf(x, -127.0f);
-    const float n = __builtin_rintf(x);
-    const float f = x - n;
-    float p = __builtin_fmaf(1.326472731e-03f, f, 9.671512991e-03f);
-    p = __builtin_fmaf(p, f, 5.550733581e-02f);
-    p = __builtin_fmaf(p, f, 2.402224243e-01f);
-    p = __builtin_fmaf(p, f, 6.931470037e-01f);
-    p = __builtin_fmaf(p, f, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
-}
-
-// exp2n without the clamp at -127, for the gaussian compositing loops.  There
-// x = -sigma is finite: the conic is the inverse of a 2-D covariance that
-// carries the low-pass term on its diagonal (0.3 px^2, 0.1 with the Mip
-// filter), so its entries are at most 10 in magnitude, and a listed pair's
-// pixel lies within the splat's extent of its centre, so no product in sigma
-// overflows.  For x >= -127 both functions
-// compute the same bits.  Below -127 both return less than 2^-126, so
-// opacity x G stays under every cutoff (1/255 - 5e-4 at the lowest) and the
-// pair is rejected by either function.  What a pixel composites is
-// therefore unchanged.
-VS_DEV float exp2n_live(float x) {
-    const float n = __builtin_rintf(x);
-    const float f = x - n;
-    float p = __builtin_fmaf(1.326472731e-03f, f, 9.671512991e-03f);
-    p = __builtin_fmaf(p, f, 5.550733581e-02f);
-    p = __builtin_fmaf(p, f, 2.402224243e-01f);
-    p = __builtin_fmaf(p, f, 6.931470037e-01f);
-    p = __builtin_fmaf(p, f, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
-}
+VS_DEV float comp_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // log: m = x 2^-e in [sqrt(1/2), sqrt(2)), s = (m-1)/(m+1),
 // ln m = 2s + s^3 (2/3 + 2/5 s^2 + 2/7 s^4 + 2/9 s^6), ln x = e ln2 + ln m.

@@ -341,6 +341,7 @@ hipError_t launch_geo_zero_rows(uint32_t* words, const uint32_t* rows, uint32_t 
 // 16-byte); `sink` holds calib_sink_words() u32 for the read kernels.
 hipError_t launch_stream_probe(void* buf, uint64_t bytes, int mode, uint32_t* sink, hipStream_t s);
 uint32_t calib_sink_words();
+hipError_t launch_exp2_range(uint32_t first_bits, uint64_t count, float* out, hipStream_t s);
 hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const void* gt, bool packed, uint32_t w, uint32_t h,
                                float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
 hipError_t launch_loss_forward(const LossArgs& a, hipStream_t s);

@@ -662,6 +662,17 @@ def scan_in_place(x: torch.Tensor) -> None:
     _lib.check(ctx.lib.vs_scan_in_place_u32(ctx.handle, _ptr(x), x.shape[0]))
 
 
+def compositing_exp2(first_bits: int, count: int, device=None) -> torch.Tensor:
+    """The compositing kernels' 2^x for the f32 inputs whose bit patterns are
+    first_bits .. first_bits + count - 1, as a float32 tensor on the device
+    (vs_compositing_exp2)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    out = torch.empty(int(count), dtype=torch.float32, device=dev)
+    ctx = Context.get(dev)
+    _lib.check(ctx.lib.vs_compositing_exp2(ctx.handle, int(first_bits), int(count), _ptr(out) if count else None))
+    return out
+
+
 def l1_cotangent(pred: torch.Tensor, gt: torch.Tensor, mask_center=(0.0, 0.0), mask_radius: float = 0.0) -> torch.Tensor:
     """d(mean L1 over rgb)/d pred for an [H,W,C] prediction and an [H,W,3]
     float32 target, or an [H,W] int32 packed RGBA8 target (the reference's
