@@ -812,8 +812,10 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
 #pragma unroll
             for (int k = 0; k < PX; ++k) {
                 if (!((live >> k) & 1u)) continue;          // uniform
+                // a done pixel (T = 0, as is a pixel outside the image) fails
+                // the stop test below; a per-pixel guard here costs more than
+                // the arithmetic it would mask
                 const float Tk = T[k];
-                if (!(Tk > T_STOP)) continue;
                 const float dx = pcx[k] - sa.x, dy = pcy[k] - sa.y;
                 const float sigma = raster_sigma(sa.z, sa.w, sbv.x, dx, dy);   // base 2, as the forward's
                 const float G = comp_exp2(-sigma);
