@@ -197,6 +197,10 @@ vs_status sync_sort_flag(vs_ctx* c) {
 // every fresh tensor (crates/splat-train-cube/src/host.rs:23-36): a kernel that
 // reads a slot it never wrote then sees a value far from any real one.
 constexpr uint32_t POISON_WORD = 0xC640E400u;
+// The depth sort's digits: 9 bits, so three passes cover the 25-27 bits a
+// view's depth keys (depth bits - minimum) span.
+constexpr uint32_t DEPTH_RADIX_BITS = 9;
+static_assert(CNT_DEPTH_MAX == CNT_DEPTH_MIN + 1, "the depth sort reads [min, max] as a pair");
 
 // Every buffer the library allocates for itself: stream-ordered, and filled
 // with POISON_WORD first when the context asks for it.
@@ -812,7 +816,8 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         const size_t o_mass = cutoff ? itake(cut_words * 4) : 0, o_allow = cutoff ? itake(cut_words * 2) : 0;
         const size_t o_cut = cutoff ? itake(T) : 0, o_kept = cutoff ? itake((size_t)N * 4) : 0;
         const size_t o_listed = cutoff ? itake(4) : 0;
-        const size_t o_tmp = itake(sort_tmp_bytes(std::max(I, M), false));   // serves both sorts
+        // serves both sorts: the depth sort on 9-bit digits, the tile sort on 8-bit ones
+        const size_t o_tmp = itake(std::max(sort_tmp_bytes(I, false), sort_tmp_bytes(M, false, DEPTH_RADIX_BITS)));
         VS_HIP(lib_alloc(ctx, &st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
         char* ib = static_cast<char*>(st->isect_arena);
         uint32_t* tiles_u = reinterpret_cast<uint32_t*>(ib + o_tu);
@@ -829,7 +834,7 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         uint32_t* err = ctx->dev_flags + FLAG_SORT_STALL;
         // the sorts' one-sweep state (shared scratch) is cleared by the kernel
         // before each sort: compaction for the depth sort, emission for the tile sort
-        const SortZeroSpan depth_zero = sort_zero_span(M, 0, depth_bits, ib + o_tmp);
+        const SortZeroSpan depth_zero = sort_zero_span(M, 0, depth_bits, ib + o_tmp, DEPTH_RADIX_BITS);
         const SortZeroSpan tile_zero = (M > 0 && N > 0) ? sort_zero_span(I, 0, tile_bits, ib + o_tmp)
                                                          : SortZeroSpan{nullptr, 0};
         uint32_t* cut_mass = cutoff ? reinterpret_cast<uint32_t*>(ib + o_mass) : nullptr;
@@ -868,8 +873,11 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         }
         {
             StageTimer tm(ctx, ST_SORT);
+            // lagged counts sort over 32 bits: a pass above the view's depth
+            // span (max - min of the visible depth bits) copies its input
             VS_HIP(radix_sort_pairs(dkeys, dvals, dkeys_sorted, order, M, m_dev, false, 0, depth_bits, ib + o_tmp,
-                                    err, s, ctx->spin_limit, nullptr, depth_zero.ptr != nullptr),
+                                    err, s, ctx->spin_limit, nullptr, depth_zero.ptr != nullptr, DEPTH_RADIX_BITS,
+                                    lagged ? st->counters + CNT_DEPTH_MIN : nullptr),
                    "depth sort");
         }
         {

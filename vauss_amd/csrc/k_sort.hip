@@ -1,5 +1,5 @@
-// k_sort.hip -- stable LSD radix sort of (key, u32 value) pairs, 8-bit digits,
-// u32 or u64 keys.
+// k_sort.hip -- stable LSD radix sort of (key, u32 value) pairs, 8-bit digits
+// (9-bit for the render's depth sort, see sort_impl), u32 or u64 keys.
 //
 // Replaces crates/splat-train-sort (radix_argsort*, lib.rs:15-189;
 // kernels.rs:35-341).  Two schedules share one block-level ranking step, in
@@ -37,6 +37,9 @@ constexpr int SORT_WAVES = SORT_BLOCK / 64;
 
 template <typename K>
 __device__ __forceinline__ uint32_t digit_of(K k, uint32_t shift) { return (uint32_t)(k >> shift) & 0xFFu; }
+// A digit of RB bits (RB = 8 or 9).
+template <int RB, typename K>
+__device__ __forceinline__ uint32_t digit_rb(K k, uint32_t shift) { return (uint32_t)(k >> shift) & ((1u << RB) - 1u); }
 
 // Adds the digits of 64 consecutive keys (one per lane, the first `nvalid`
 // valid) to a wavefront's LDS histogram: only the first lane of each run of
@@ -89,20 +92,21 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_upsweep_kernel(const K* __res
 // between them:
 //  * count(): loads the tile, ranks every key among the equal digits of its
 //    wavefront (ballot matching), and turns the per-wave digit histograms into
-//    each wave's exclusive offset within its digit; returns, in thread d < 256,
-//    the tile's count of digit d;
+//    each wave's exclusive offset within its digit; returns, in thread
+//    d < 2^RB, the tile's count of digit d;
 //  * place(): from those counts, digit_start[d] (the first LDS slot of digit d)
 //    and the digit-ordered (stable) tile in s_keys / s_vals.
-template <typename K, int BLOCK, int ITEMS>
+template <typename K, int BLOCK, int ITEMS, int RB = 8>
 struct TileRanker {
-    static_assert(BLOCK >= 256 && BLOCK % 64 == 0, "one thread per digit");
+    static constexpr uint32_t R = 1u << RB;   // digits
+    static_assert(BLOCK >= (int)R && BLOCK % 64 == 0, "one thread per digit");
     static constexpr int WAVES = BLOCK / 64;
     K key[ITEMS];
     uint32_t val[ITEMS], dig[ITEMS], rank[ITEMS];
     uint32_t run = 0;
 
     __device__ __forceinline__ uint32_t count(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
-                                              uint32_t base, uint32_t n, uint32_t shift, uint32_t (*wave_hist)[256]) {
+                                              uint32_t base, uint32_t n, uint32_t shift, uint32_t (*wave_hist)[R]) {
         const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         // Issue every load of the tile before any ranking step, so a wavefront
         // waits for memory once rather than once per step.
@@ -117,7 +121,7 @@ struct TileRanker {
             const uint32_t idx = wbase + s * 64 + lane;
             val[s] = idx < n ? vals_in[idx] : 0u;
         }
-        for (uint32_t i = threadIdx.x; i < WAVES * 256; i += BLOCK) (&wave_hist[0][0])[i] = 0;
+        for (uint32_t i = threadIdx.x; i < WAVES * R; i += BLOCK) (&wave_hist[0][0])[i] = 0;
         __syncthreads();
 
         const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -125,11 +129,11 @@ struct TileRanker {
         for (int s = 0; s < ITEMS; ++s) {
             const uint32_t idx = wbase + s * 64 + lane;
             const bool valid = idx < n;
-            const uint32_t d = digit_of(key[s], shift);
-            dig[s] = valid ? d : 256u;
+            const uint32_t d = digit_rb<RB>(key[s], shift);
+            dig[s] = valid ? d : R;
             uint64_t peers = __ballot(valid);
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
+            for (int b = 0; b < RB; ++b) {
                 const uint64_t bal = __ballot((d >> b) & 1u);
                 peers &= ((d >> b) & 1u) ? bal : ~bal;
             }
@@ -146,7 +150,7 @@ struct TileRanker {
         // per-digit totals; each wave's count becomes its exclusive offset within the digit
         run = 0;
         const uint32_t d = threadIdx.x;
-        if (d < 256) {
+        if (d < R) {
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) {
                 const uint32_t c = wave_hist[w][d];
@@ -157,13 +161,13 @@ struct TileRanker {
         return run;
     }
 
-    __device__ __forceinline__ void place(uint32_t (*wave_hist)[256], uint32_t* digit_start, uint32_t* s_tot,
+    __device__ __forceinline__ void place(uint32_t (*wave_hist)[R], uint32_t* digit_start, uint32_t* s_tot,
                                           K* s_keys, uint32_t* s_vals) {
         const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         const uint32_t d = threadIdx.x;
-        // exclusive scan of the digit counts over the 256 digits
+        // exclusive scan of the digit counts over the R digits
         uint32_t incl = run;
-        if (d < 256) {
+        if (d < R) {
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const uint32_t t = __shfl_up(incl, o);
@@ -172,7 +176,7 @@ struct TileRanker {
             if (lane == 63) s_tot[wave] = incl;
         }
         __syncthreads();
-        if (d < 256) {
+        if (d < R) {
             uint32_t wo = 0;
             for (uint32_t w = 0; w < wave; ++w) wo += s_tot[w];
             digit_start[d] = wo + incl - run;
@@ -180,7 +184,7 @@ struct TileRanker {
         __syncthreads();
 #pragma unroll
         for (int s = 0; s < ITEMS; ++s) {
-            if (dig[s] < 256u) {
+            if (dig[s] < R) {
                 const uint32_t pos = digit_start[dig[s]] + wave_hist[wave][dig[s]] + rank[s];
                 s_keys[pos] = key[s];
                 s_vals[pos] = val[s];
@@ -275,17 +279,18 @@ constexpr int HIST_ITEMS = 16;       // keys per lane in flight per chunk (the k
 // caller), one copy per XCD x = block index mod 8 (the XCD the block runs on),
 // so the blocks' closing atomics spread over eight sets of addresses; a pass
 // sums the eight copies of a digit.  Each wavefront takes chunks of
-// HIST_ITEMS x 64 consecutive keys.
+// HIST_ITEMS x 64 consecutive keys.  Digits of RB bits.
 constexpr uint32_t HIST_COPIES = 8;
-template <typename K>
+template <typename K, int RB = 8>
 __global__ void __launch_bounds__(SORT_BLOCK) sort_histogram_kernel(const K* __restrict__ keys, uint32_t n_cap,
                                                                     const uint32_t* __restrict__ n_dev, uint32_t first_bit,
                                                                     uint32_t passes, uint32_t* __restrict__ ghist) {
-    constexpr int HP = sizeof(K);           // passes of 8-bit digits a key can need
-    __shared__ uint32_t h[SORT_WAVES][HP][256];
+    constexpr uint32_t R = 1u << RB;
+    constexpr int HP = (8 * (int)sizeof(K) + RB - 1) / RB;   // passes a key can need
+    __shared__ uint32_t h[SORT_WAVES][HP][R];
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (uint32_t i = threadIdx.x; i < SORT_WAVES * HP * 256; i += SORT_BLOCK) (&h[0][0][0])[i] = 0;
+    for (uint32_t i = threadIdx.x; i < SORT_WAVES * HP * R; i += SORT_BLOCK) (&h[0][0][0])[i] = 0;
     __syncthreads();
     const uint64_t stride = (uint64_t)gridDim.x * SORT_WAVES * 64 * HIST_ITEMS;
     for (uint64_t c = ((uint64_t)blockIdx.x * SORT_WAVES + wave) * 64 * HIST_ITEMS; c < n; c += stride) {
@@ -300,12 +305,12 @@ __global__ void __launch_bounds__(SORT_BLOCK) sort_histogram_kernel(const K* __r
             const uint64_t b = c + (uint64_t)s * 64;
             if (b >= n) break;                                   // uniform across the wavefront
             const uint32_t nvalid = (uint32_t)min((uint64_t)64, (uint64_t)n - b);
-            for (uint32_t p = 0; p < passes; ++p) hist_add_runs(h[wave][p], digit_of(k[s], first_bit + 8 * p), lane, nvalid);
+            for (uint32_t p = 0; p < passes; ++p) hist_add_runs(h[wave][p], digit_rb<RB>(k[s], first_bit + RB * p), lane, nvalid);
         }
     }
     __syncthreads();
-    uint32_t* mine = ghist + (size_t)(blockIdx.x % HIST_COPIES) * passes * 256;
-    for (uint32_t i = threadIdx.x; i < passes * 256; i += SORT_BLOCK) {
+    uint32_t* mine = ghist + (size_t)(blockIdx.x % HIST_COPIES) * passes * R;
+    for (uint32_t i = threadIdx.x; i < passes * R; i += SORT_BLOCK) {
         uint32_t c = 0;
 #pragma unroll
         for (int w = 0; w < SORT_WAVES; ++w) c += (&h[w][0][0])[i];
@@ -320,21 +325,26 @@ __device__ __forceinline__ void status_store(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One pass: rank a tile, find its digits' global offsets by look-back, scatter.
-// `status` is [nblocks][256], zeroed before the pass.
-template <typename K, int BLOCK, int ITEMS>
+// One pass over digits of RB bits: rank a tile, find its digits' global
+// offsets by look-back, scatter.  `status` is [nblocks][2^RB], zeroed before
+// the pass.  key_span (null: unused) is the [min, max] of values whose
+// differences the keys are: a pass whose digit lies above every key's
+// highest set bit is the identity, and copies its tile.
+template <typename K, int BLOCK, int ITEMS, int RB = 8>
 __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
                                                                    K* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
                                                                    uint32_t n_cap, const uint32_t* __restrict__ n_dev, uint32_t shift,
                                                                    const uint32_t* __restrict__ ghist, uint32_t ghist_copy_stride,
                                                                    uint32_t* status,
                                                                    uint32_t* err, uint32_t spin_limit,
-                                                                   uint32_t* __restrict__ ranges, uint32_t num_tiles) {
+                                                                   uint32_t* __restrict__ ranges, uint32_t num_tiles,
+                                                                   const uint32_t* __restrict__ key_span) {
     constexpr uint32_t TILE = BLOCK * ITEMS;
-    __shared__ uint32_t wave_hist[BLOCK / 64][256];
-    __shared__ uint32_t digit_start[256];
+    constexpr uint32_t R = 1u << RB;
+    __shared__ uint32_t wave_hist[BLOCK / 64][R];
+    __shared__ uint32_t digit_start[R];
     __shared__ uint32_t s_tot[BLOCK / 64];
-    __shared__ uint32_t s_gstart[256];      // where this tile's digit d starts in the output
+    __shared__ uint32_t s_gstart[R];        // where this tile's digit d starts in the output
     __shared__ K s_keys[TILE];
     __shared__ uint32_t s_vals[TILE];
 
@@ -348,21 +358,34 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
     const uint32_t base = tile * TILE;
     // A tile past the end has no successor with keys.
     if (base >= n) return;
+    if (key_span) {
+        // every key is below 2^bits: a digit above that is 0 for all (uniform)
+        const uint32_t span = key_span[1] - key_span[0];
+        const uint32_t bits = span ? 32u - (uint32_t)__builtin_clz(span) : 0u;
+        if (shift >= bits) {
+            const uint32_t count = min(TILE, n - base);
+            for (uint32_t i = threadIdx.x; i < count; i += BLOCK) {
+                keys_out[base + i] = keys_in[base + i];
+                vals_out[base + i] = vals_in[base + i];
+            }
+            return;
+        }
+    }
     const uint32_t d = threadIdx.x;
     // The pass's global digit counts (the sum of the eight histogram copies)
     // are loaded first, so their latency overlaps the tile's.
     uint32_t gh[HIST_COPIES];
 #pragma unroll
-    for (uint32_t x = 0; x < HIST_COPIES; ++x) gh[x] = d < 256 ? ghist[(size_t)x * ghist_copy_stride + d] : 0u;
-    TileRanker<K, BLOCK, ITEMS> rk;
+    for (uint32_t x = 0; x < HIST_COPIES; ++x) gh[x] = d < R ? ghist[(size_t)x * ghist_copy_stride + d] : 0u;
+    TileRanker<K, BLOCK, ITEMS, RB> rk;
     const uint32_t cnt = rk.count(keys_in, vals_in, base, n, shift, wave_hist);
 
     // The tile's digit counts are published as soon as they are known, and
     // the look-back runs before the tile is reordered in LDS, so the tile's
     // prefix reaches its successors as early as it can.
     uint32_t excl = 0;
-    if (d < 256) {
-        uint32_t* my = status + (size_t)tile * 256 + d;
+    if (d < R) {
+        uint32_t* my = status + (size_t)tile * R + d;
         status_store(my, (tile == 0 ? OS_PREFIX : OS_AGGREGATE) | cnt);
         if (tile > 0) {
             // Look back over predecessors LOOKBACK at a time (independent loads),
@@ -374,7 +397,7 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
                 uint32_t st[LOOKBACK];
     #pragma unroll
                 for (int i = 0; i < LOOKBACK; ++i)
-                    st[i] = (j - i >= 0) ? status_load(status + (size_t)(j - i) * 256 + d) : OS_PREFIX;
+                    st[i] = (j - i >= 0) ? status_load(status + (size_t)(j - i) * R + d) : OS_PREFIX;
                 int used = 0;
                 bool found = false, stalled = false;
     #pragma unroll
@@ -397,7 +420,7 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
         }
     }
     rk.place(wave_hist, digit_start, s_tot, s_keys, s_vals);
-    // global exclusive start of digit d: sum of ghist[0..d) (block scan over 256)
+    // global exclusive start of digit d: sum of ghist[0..d) (block scan over R)
     {
         const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         uint32_t c = 0u;
@@ -409,9 +432,9 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
             const uint32_t t = __shfl_up(incl, o);
             if ((int)lane >= o) incl += t;
         }
-        if (lane == 63 && d < 256) s_tot[wave] = incl;   // place() has finished with s_tot
+        if (lane == 63 && d < R) s_tot[wave] = incl;   // place() has finished with s_tot
         __syncthreads();
-        if (d < 256) {
+        if (d < R) {
             uint32_t wo = 0;
             for (uint32_t w = 0; w < wave; ++w) wo += s_tot[w];
             s_gstart[d] = excl + wo + incl - c;
@@ -421,7 +444,7 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
     const uint32_t count = min(TILE, n - base);
     for (uint32_t i = threadIdx.x; i < count; i += BLOCK) {
         const K k = s_keys[i];
-        const uint32_t dd = digit_of(k, shift);
+        const uint32_t dd = digit_rb<RB>(k, shift);
         const uint32_t gpos = s_gstart[dd] + (i - digit_start[dd]);
         if (gpos < n) {   // always true for consistent counts; keeps a bad count from writing out of bounds
             if (!ranges) keys_out[gpos] = k;
@@ -432,7 +455,7 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
                 // inside the run is a range bound; a run's first and last keys
                 // may continue in another tile's run and meet there by min / max.
                 const uint32_t t = (uint32_t)k;
-                const uint32_t run_lo = digit_start[dd], run_hi = dd < 255 ? digit_start[dd + 1] : count;
+                const uint32_t run_lo = digit_start[dd], run_hi = dd < R - 1 ? digit_start[dd + 1] : count;
                 if (i == run_lo || s_keys[i - 1] != k) atomicMin(&ranges[2 * t], gpos);
                 if (i + 1 == run_hi || s_keys[i + 1] != k) atomicMax(&ranges[2 * t + 1], gpos + 1);
             }
@@ -442,10 +465,11 @@ __global__ void __launch_bounds__(BLOCK) sort_onesweep_kernel(const K* __restric
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-size_t sort_tmp_bytes(uint64_t n, bool key64) {
+size_t sort_tmp_bytes(uint64_t n, bool key64, uint32_t radix_bits) {
     const uint64_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;
     const size_t ks = key64 ? 8 : 4;
-    const int max_passes = key64 ? 8 : 4;
+    const uint32_t rb = radix_bits == 9 ? 9u : 8u;
+    const uint64_t max_passes = (8 * ks + rb - 1) / rb, R = 1ull << rb;
     size_t b = 0;
     b += align_up(n * ks, 256);                 // ping-pong keys
     b += align_up(n * 4, 256);                  // ping-pong values
@@ -453,44 +477,67 @@ size_t sort_tmp_bytes(uint64_t n, bool key64) {
     b += align_up(scan_tmp_words(nblocks * 256) * 4, 256);
     // one-sweep: histograms and per-pass tile status
     const uint64_t os_tiles = (n + OS_MIN_TILE - 1) / OS_MIN_TILE;
-    b += align_up((size_t)HIST_COPIES * max_passes * 256 * 4 + 64 + (size_t)max_passes * os_tiles * 256 * 4, 256);
+    b += align_up((size_t)(HIST_COPIES * max_passes * R * 4 + 64 + max_passes * os_tiles * R * 4), 256);
     return b + 256;
 }
 
+template <typename K, int RB>
+static void launch_onesweep_pass(bool small, uint32_t os_tiles, const K* src_k, const uint32_t* src_v, K* dk,
+                                 uint32_t* dv, uint32_t n, const uint32_t* n_dev, uint32_t shift, const uint32_t* gh,
+                                 uint32_t gh_stride, uint32_t* status, uint32_t* err, uint32_t spin_limit,
+                                 uint32_t* rng, uint32_t nt, const uint32_t* key_span, hipStream_t s) {
+    if (small)
+        sort_onesweep_kernel<K, OS_SMALL_BLOCK, OS_SMALL_ITEMS, RB><<<os_tiles, OS_SMALL_BLOCK, 0, s>>>(
+            src_k, src_v, dk, dv, n, n_dev, shift, gh, gh_stride, status, err, spin_limit, rng, nt, key_span);
+    else
+        sort_onesweep_kernel<K, OS_BLOCK, OS_ITEMS, RB><<<os_tiles, OS_BLOCK, 0, s>>>(
+            src_k, src_v, dk, dv, n, n_dev, shift, gh, gh_stride, status, err, spin_limit, rng, nt, key_span);
+}
+
+// Digits of 8 bits, or of 9 (radix_bits = 9, u32 keys, one-sweep schedule
+// only): three passes then cover 27 bits, the span of a view's depth keys.
 template <typename K>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_out, uint32_t* vals_out, uint32_t n,
                             const uint32_t* n_dev, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t* err,
-                            hipStream_t s, uint32_t spin_limit, TileRangesOut* tr, bool state_zeroed) {
+                            hipStream_t s, uint32_t spin_limit, TileRangesOut* tr, bool state_zeroed,
+                            uint32_t radix_bits, const uint32_t* key_span) {
     if (n == 0) return hipSuccess;
     const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
-    const uint32_t passes = (bits + 7) / 8;
-    if (passes == 0) {
+    if (bits == 0) {
         hipError_t e = hipMemcpyAsync(keys_out, keys_in, (size_t)n * sizeof(K), hipMemcpyDeviceToDevice, s);
         if (e != hipSuccess) return e;
         return hipMemcpyAsync(vals_out, vals_in, (size_t)n * 4, hipMemcpyDeviceToDevice, s);
     }
+    const bool onesweep = n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS && err != nullptr;
+    const uint32_t rb = (onesweep && sizeof(K) == 4 && radix_bits == 9) ? 9u : 8u;
+    const uint32_t R = 1u << rb;
+    const uint32_t passes = (bits + rb - 1) / rb;
     const uint32_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;
     char* p = reinterpret_cast<char*>(align_up(reinterpret_cast<uintptr_t>(tmp), 256));
     K* tk = reinterpret_cast<K*>(p); p += align_up((size_t)n * sizeof(K), 256);
     uint32_t* tv = reinterpret_cast<uint32_t*>(p); p += align_up((size_t)n * 4, 256);
     uint32_t* table = reinterpret_cast<uint32_t*>(p); p += align_up((size_t)nblocks * 256 * 4, 256);
     uint32_t* stmp = reinterpret_cast<uint32_t*>(p); p += align_up(scan_tmp_words((uint64_t)nblocks * 256) * 4, 256);
-    const bool onesweep = n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS && err != nullptr;
     const bool small = n < OS_SMALL_N;
     const uint32_t os_tile = small ? OS_SMALL_TILE : OS_TILE;
     const uint32_t os_tiles = (n + os_tile - 1) / os_tile;
-    uint32_t* ghist = reinterpret_cast<uint32_t*>(p);          // [HIST_COPIES][passes][256]
-    uint32_t* status = ghist + HIST_COPIES * passes * 256 + 16; // [passes][os_tiles][256]
+    uint32_t* ghist = reinterpret_cast<uint32_t*>(p);          // [HIST_COPIES][passes][R]
+    uint32_t* status = ghist + HIST_COPIES * passes * R + 16; // [passes][os_tiles][R]
     if (onesweep) {
         hipError_t e = hipSuccess;
         if (!state_zeroed)
-            e = launch_fill_u32(ghist, 0u, (uint64_t)HIST_COPIES * passes * 256 + 16 + (uint64_t)passes * os_tiles * 256, s);
+            e = launch_fill_u32(ghist, 0u, (uint64_t)HIST_COPIES * passes * R + 16 + (uint64_t)passes * os_tiles * R, s);
         if (e != hipSuccess) return e;
         // ~4k keys per block up to HIST_BLOCKS blocks: each block ends with
-        // passes x 256 global atomics, so a grid much wider than the data
+        // passes x R global atomics, so a grid much wider than the data
         // only adds atomics (16k keys per block starves short inputs).
         const uint32_t hist_blocks = (uint32_t)max((uint64_t)1, min((uint64_t)HIST_BLOCKS, ((uint64_t)n + 4095) / 4096));
-        sort_histogram_kernel<K><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+        if constexpr (sizeof(K) == 4) {
+            if (rb == 9) sort_histogram_kernel<K, 9><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+            else sort_histogram_kernel<K, 8><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+        } else {
+            sort_histogram_kernel<K, 8><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+        }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -500,20 +547,25 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         const bool to_out = ((passes - 1 - pass) % 2) == 0;
         K* dk = to_out ? keys_out : tk;
         uint32_t* dv = to_out ? vals_out : tv;
-        const uint32_t shift = first_bit + 8 * pass;
+        const uint32_t shift = first_bit + rb * pass;
         // the last pass of a tile sort derives the tile ranges instead of writing the keys
         uint32_t* rng = (tr && pass + 1 == passes) ? tr->ranges : nullptr;
         const uint32_t nt = tr ? tr->num_tiles : 0u;
         hipError_t e;
         if (onesweep) {
-            if (small)
-                sort_onesweep_kernel<K, OS_SMALL_BLOCK, OS_SMALL_ITEMS><<<os_tiles, OS_SMALL_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, passes * 256, status + (size_t)pass * os_tiles * 256, err,
-                    spin_limit, rng, nt);
-            else
-                sort_onesweep_kernel<K, OS_BLOCK, OS_ITEMS><<<os_tiles, OS_BLOCK, 0, s>>>(
-                    src_k, src_v, dk, dv, n, n_dev, shift, ghist + pass * 256, passes * 256, status + (size_t)pass * os_tiles * 256, err,
-                    spin_limit, rng, nt);
+            const uint32_t* gh = ghist + pass * R;
+            uint32_t* st = status + (size_t)pass * os_tiles * R;
+            if constexpr (sizeof(K) == 4) {
+                if (rb == 9)
+                    launch_onesweep_pass<K, 9>(small, os_tiles, src_k, src_v, dk, dv, n, n_dev, shift, gh, passes * R, st,
+                                               err, spin_limit, rng, nt, key_span, s);
+                else
+                    launch_onesweep_pass<K, 8>(small, os_tiles, src_k, src_v, dk, dv, n, n_dev, shift, gh, passes * R, st,
+                                               err, spin_limit, rng, nt, key_span, s);
+            } else {
+                launch_onesweep_pass<K, 8>(small, os_tiles, src_k, src_v, dk, dv, n, n_dev, shift, gh, passes * R, st, err,
+                                           spin_limit, rng, nt, nullptr, s);
+            }
             if (rng) tr->done = true;
             e = hipGetLastError();
             if (e != hipSuccess) return e;
@@ -536,21 +588,26 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
 hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* keys_out, uint32_t* vals_out,
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
                             void* tmp, uint32_t* err, hipStream_t s, uint32_t spin_limit, TileRangesOut* tr,
-                            bool state_zeroed) {
+                            bool state_zeroed, uint32_t radix_bits, const uint32_t* key_span) {
     if (tr) tr->done = false;
+    if (tr && key_span) return hipErrorInvalidValue;   // a range pass never skips
     if (key64)
         return sort_impl<uint64_t>(static_cast<const uint64_t*>(keys_in), vals_in, static_cast<uint64_t*>(keys_out),
-                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, nullptr, false);
+                                   vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, nullptr, false, 8u,
+                                   nullptr);
     return sort_impl<uint32_t>(static_cast<const uint32_t*>(keys_in), vals_in, static_cast<uint32_t*>(keys_out),
-                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, tr, state_zeroed);
+                               vals_out, n, n_dev, first_bit, end_bit, tmp, err, s, spin_limit, tr, state_zeroed,
+                               radix_bits, key_span);
 }
 
-SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, void* tmp) {
+SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t radix_bits) {
     // the layout of sort_impl<uint32_t>: ping-pong keys, values, digit table, scan scratch, then the
     // one-sweep histograms and status
     const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
-    const uint32_t passes = (bits + 7) / 8;
-    if (n == 0 || passes == 0 || !(n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS)) return SortZeroSpan{nullptr, 0};
+    if (n == 0 || bits == 0 || !(n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS)) return SortZeroSpan{nullptr, 0};
+    const uint32_t rb = radix_bits == 9 ? 9u : 8u;
+    const uint64_t R = 1ull << rb;
+    const uint32_t passes = (bits + rb - 1) / rb;
     const uint32_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;
     char* p = reinterpret_cast<char*>(align_up(reinterpret_cast<uintptr_t>(tmp), 256));
     p += align_up((size_t)n * 4, 256);
@@ -559,8 +616,7 @@ SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, vo
     p += align_up(scan_tmp_words((uint64_t)nblocks * 256) * 4, 256);
     const uint32_t os_tile = n < OS_SMALL_N ? OS_SMALL_TILE : OS_TILE;
     const uint64_t os_tiles = (n + os_tile - 1) / os_tile;
-    return SortZeroSpan{reinterpret_cast<uint32_t*>(p),
-                        (uint64_t)HIST_COPIES * passes * 256 + 16 + (uint64_t)passes * os_tiles * 256};
+    return SortZeroSpan{reinterpret_cast<uint32_t*>(p), (uint64_t)HIST_COPIES * passes * R + 16 + (uint64_t)passes * os_tiles * R};
 }
 
 } // namespace vs

@@ -378,8 +378,8 @@ hipError_t scan_u32_lookback(const uint32_t* in, uint32_t* out, uint64_t n, uint
                              const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu,
                              uint32_t* out_scattered = nullptr, bool write_end = false);
 
-// Radix sort.  `tmp` needs sort_tmp_bytes(n) bytes.
-size_t sort_tmp_bytes(uint64_t n, bool key64);
+// Radix sort.  `tmp` needs sort_tmp_bytes(n, key64, radix_bits) bytes.
+size_t sort_tmp_bytes(uint64_t n, bool key64, uint32_t radix_bits = 8);
 // `err` (device word, may be null: then the one-sweep schedule is not used)
 // is or-ed with 1 if a one-sweep look-back gave up waiting: after
 // `spin_limit` polls of a predecessor that has not published its counts.
@@ -398,12 +398,17 @@ hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* 
                             uint32_t n, const uint32_t* n_dev, bool key64, uint32_t first_bit, uint32_t end_bit,
                             void* tmp, uint32_t* err, hipStream_t s,
                             uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT, TileRangesOut* tr = nullptr,
-                            bool state_zeroed = false);
+                            bool state_zeroed = false, uint32_t radix_bits = 8,
+                            const uint32_t* key_span = nullptr);
+// radix_bits = 9: digits of 9 bits (u32 keys of the one-sweep schedule; 8
+// elsewhere).  key_span (device [min, max], or null): the keys are values
+// minus min, so no key has a bit at or above bitlen(max - min), and a pass
+// whose digit lies there copies its input (not with a range pass).
 // The words of `tmp` that a u32-key sort of n keys over [first_bit, end_bit)
 // needs cleared before it runs (its one-sweep histograms and tile status):
 // a caller that clears them in a kernel of its own passes state_zeroed and
 // the sort skips its fill.  {nullptr, 0} when the sort would not use them.
 struct SortZeroSpan { uint32_t* ptr; uint64_t words; };
-SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, void* tmp);
+SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t radix_bits = 8);
 
 } // namespace vs
