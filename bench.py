@@ -3,8 +3,9 @@
 Workload (default): 1,000,000 SH-degree-3 Gaussians at 1920x1080 (fx=fy=1600,
 16x16 tiles) seen from 8 seeded poses on a radius-6 orbit; one step = one
 view's full training render: forward (projection, tile binning, sort,
-compositing), L1 loss cotangent, raster backward and projection backward to
-dense parameter gradients.  Inputs are resident in HBM before timing.
+compositing, with the L1 loss cotangent written by the compositing pass),
+raster backward and projection backward to dense parameter gradients.
+Inputs are resident in HBM before timing.
 
 Prints one JSON line (contract: metric/value/unit/.../roofline/cpu_baseline).
 
@@ -150,9 +151,9 @@ def measure_next_rows(va, wl, cam, t, s, o, gt, dev, reps: int = 10) -> dict:
     dec = torch.randn(816, generator=gen, device=dev) * 0.35
 
     def neural_step():
-        o2 = va.render(cam, wl.img_size, t, nrows, o, pass_=va.RasterPass.BACKWARD, decoder=dec, neural_degree=3)
-        v2 = va.l1_cotangent(o2.out_img, gt, (0.0, 0.0), 0.0)
-        va.render_backward(o2, t, nrows, o, v2, decoder=dec)
+        o2 = va.render(cam, wl.img_size, t, nrows, o, pass_=va.RasterPass.BACKWARD, decoder=dec, neural_degree=3,
+                       l1_target=gtp)
+        va.render_backward(o2, t, nrows, o, o2.v_l1, decoder=dec)
         o2.state.free()
     n_ms = timed(neural_step)
     ctx = va.Context.get(dev)
@@ -270,9 +271,10 @@ def main() -> int:
 
     def step(view: int, list_histogram: bool = False, used: bool = False):
         nonlocal tile_lists
-        out = va.render(cams[view], wl.img_size, t, s, o, pass_=va.RasterPass.BACKWARD)
-        v = va.l1_cotangent(out.out_img, gt_packed, mc, mr)
-        g = va.render_backward(out, t, s, o, v)
+        # the L1 cotangent is written by the raster pass with the image
+        out = va.render(cams[view], wl.img_size, t, s, o, pass_=va.RasterPass.BACKWARD, l1_target=gt_packed,
+                        l1_mask_center=mc, l1_mask_radius=mr)
+        g = va.render_backward(out, t, s, o, out.v_l1)
         aux = (out.aux.num_visible, out.aux.num_intersections)
         if used:      # intersections the raster kernels consume: the shrunk tile ranges
             r = out.aux.tile_offsets.reshape(-1, 2).to(torch.int64) & 0xFFFFFFFF

@@ -293,6 +293,21 @@ vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* 
                             vs_pass pass, vs_render_mode mode,
                             vs_fwd_out* out, vs_fwd_state** state);
 
+/* vs_render_forward followed by vs_l1_cotangent_packed of its image, with the
+ * cotangent written by the raster pass itself (no second read of the image;
+ * one launch fewer): for a pass with a float RGBA image (every pass but
+ * VS_PASS_FORWARD and the geometry passes; not surfels).  gt_packed
+ * [H,W] RGBA8 as the reference's loss reads it (crates/splat-train-loss/src/
+ * lib.rs:93,1042-1044), the circle mask as vs_l1_cotangent's, v_out [H,W,4]
+ * f32, 16-byte aligned: bit for bit what vs_l1_cotangent_packed writes for
+ * the same image.  No counterpart in the reference, whose loss is a separate
+ * pass (lib.rs:786-811). */
+vs_status vs_render_forward_l1(vs_ctx* ctx, const vs_camera* cam, const vs_splats* splats,
+                               uint32_t img_w, uint32_t img_h, const float background[3],
+                               vs_pass pass, vs_render_mode mode,
+                               const uint32_t* gt_packed, float mask_cx, float mask_cy, float mask_radius,
+                               float* v_out, vs_fwd_out* out, vs_fwd_state** state);
+
 /* SplatBwdOps::rasterize_bwd + project_bwd (bwd/burn_glue.rs:70-111;
  * bwd/render_bwd.rs:27-155 and 295-447).  `out_img` is the image the
  * forward wrote (f32, C channels), `v_out` its cotangent [H,W,C].  The

@@ -149,3 +149,55 @@ def test_l1_cotangent_packed_target_matches_unpacked():
     assert (got[::7][..., :3] == 0).all()
     with pytest.raises(ValueError):
         va.l1_cotangent(p, gtp[:, :-1], w.mask_center, w.mask_radius)
+
+
+@pytest.mark.parametrize("cfg,pass_", [("c3", "BACKWARD"), ("c5", "BACKWARD"), ("c1", "BACKWARD_SMOOTH_CUTOFF")])
+def test_forward_fused_l1_cotangent(cfg, pass_):
+    """vs_render_forward_l1: the raster pass writes the L1 cotangent of its own
+    image (crates/splat-train-loss/src/lib.rs:786-811) bit for bit as
+    vs_l1_cotangent_packed computes it from that image, at the workload's full
+    size and mask (C5: r = 940), and the image, aux outputs and gradients of
+    the render are those of a plain render."""
+    w = scenes.workload(cfg, 1000 if cfg == "c1" else 200_000)
+    W, H = w.img_size
+    rng = np.random.default_rng(5)
+    rgba8 = rng.integers(0, 256, (H, W, 4), dtype=np.uint8)
+    gtp = va.pack_rgba8(torch.from_numpy(rgba8)).cuda()
+    cam = w.cameras[0].uniforms(w.img_size)
+    t, s, o = to_gpu(w.scene)
+    p = va.RasterPass[pass_]
+    print(f"[case] fused l1 {cfg} {W}x{H} {pass_} mask_radius={w.mask_radius}", flush=True)
+    fused = va.render(cam, w.img_size, t, s, o, pass_=p, l1_target=gtp, l1_mask_center=w.mask_center,
+                      l1_mask_radius=w.mask_radius)
+    plain = va.render(cam, w.img_size, t, s, o, pass_=p)
+    np.testing.assert_array_equal(fused.out_img.cpu().numpy().view(np.uint32), plain.out_img.cpu().numpy().view(np.uint32))
+    for name in ("visible", "max_radius", "opacities", "tile_offsets"):
+        np.testing.assert_array_equal(getattr(fused.aux, name).cpu().numpy(), getattr(plain.aux, name).cpu().numpy(),
+                                      err_msg=name)
+    want = va.l1_cotangent(plain.out_img, gtp, w.mask_center, w.mask_radius)
+    got = fused.v_l1
+    assert got.shape == (H, W, 4)
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32))
+    assert (got[..., :3] != 0).float().mean().item() > 0.5
+    g1 = va.render_backward(fused, t, s, o, got)
+    g2 = va.render_backward(plain, t, s, o, want)
+    a, b = g1.v_transforms.cpu().numpy(), g2.v_transforms.cpu().numpy()
+    assert (np.abs(a - b) <= 1e-5 + 1e-3 * np.abs(b)).all()
+    fused.state.free()
+    plain.state.free()
+
+
+def test_forward_fused_l1_rejects_other_passes():
+    w = scenes.workload("c1", 500)
+    W, H = w.img_size
+    gtp = torch.zeros((H, W), dtype=torch.int32, device="cuda")
+    cam = w.cameras[0].uniforms(w.img_size)
+    t, s, o = to_gpu(w.scene)
+    for p in (va.RasterPass.FORWARD, va.RasterPass.GEOMETRY):
+        with pytest.raises(ValueError):
+            va.render(cam, w.img_size, t, s, o, pass_=p, l1_target=gtp)
+    with pytest.raises(ValueError):
+        va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD, l1_target=gtp[:, :-1])
+    with pytest.raises(ValueError):
+        va.render(cam, w.img_size, t, s, o, pass_=va.RasterPass.BACKWARD, l1_target=gtp,
+                  render_mode=va.SplatRenderMode.SURFEL)

@@ -615,9 +615,17 @@ extern "C" vs_status vs_ctx_settle_lagged_counts(vs_ctx* c, uint64_t* renders, u
     return VS_OK;
 }
 
-extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* sp, uint32_t W, uint32_t H,
-                                       const float background[3], vs_pass pass, vs_render_mode mode, vs_fwd_out* out,
-                                       vs_fwd_state** state_out) {
+// The L1 cotangent a forward may write with its image (vs_render_forward_l1).
+struct L1Fuse {
+    const uint32_t* gt;
+    float mcx, mcy, mr;
+    float* v_out;
+};
+static float l1_inv_count(vs_ctx* ctx, uint32_t w, uint32_t h, float mcx, float mcy, float mr);
+
+static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* sp, uint32_t W, uint32_t H,
+                                const float background[3], vs_pass pass, vs_render_mode mode, vs_fwd_out* out,
+                                vs_fwd_state** state_out, const L1Fuse* l1) {
     if (state_out) *state_out = nullptr;
     if (!ctx || !cam || !out || !background) return fail(VS_ERR_INVALID, "null argument");
     if (W == 0 || H == 0) return fail(VS_ERR_INVALID, "Can't render images with 0 size.");
@@ -942,6 +950,11 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         ra.proj_surf = st->proj_surf; ra.surf_crit = (surfel && pass_surface_criterion(pass)) ? 1u : 0u;
         ra.out = out->out_img; ra.visible = st->visible;
         ra.qpass = reinterpret_cast<uint8_t*>(st->qpass);
+        if (l1) {
+            ra.l1_gt = l1->gt; ra.l1_v = l1->v_out;
+            ra.l1_mcx = l1->mcx; ra.l1_mcy = l1->mcy; ra.l1_mr = l1->mr;
+            ra.l1_inv = l1_inv_count(ctx, W, H, l1->mcx, l1->mcy, l1->mr);
+        }
         VS_HIP(launch_raster_fwd(ra, bwd_info, geometry, smooth, s), "raster forward");
     }
     if (sort_done) {
@@ -966,6 +979,26 @@ extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const 
         st = nullptr;   // ownership passes to the caller
     }
     return VS_OK;
+}
+
+extern "C" vs_status vs_render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_splats* sp, uint32_t W, uint32_t H,
+                                       const float background[3], vs_pass pass, vs_render_mode mode, vs_fwd_out* out,
+                                       vs_fwd_state** state_out) {
+    return render_forward(ctx, cam, sp, W, H, background, pass, mode, out, state_out, nullptr);
+}
+
+extern "C" vs_status vs_render_forward_l1(vs_ctx* ctx, const vs_camera* cam, const vs_splats* sp, uint32_t W,
+                                          uint32_t H, const float background[3], vs_pass pass, vs_render_mode mode,
+                                          const uint32_t* gt_packed, float mask_cx, float mask_cy, float mask_radius,
+                                          float* v_out, vs_fwd_out* out, vs_fwd_state** state_out) {
+    if (state_out) *state_out = nullptr;
+    const vs_pass base = static_cast<vs_pass>((uint32_t)pass & 0xFFu);
+    if (!pass_bwd_info(base) || pass_geometry(base) || mode == VS_MODE_SURFEL)
+        return fail(VS_ERR_INVALID, "the fused L1 cotangent takes an RGBA training pass (no geometry channels, no surfels)");
+    if (!gt_packed || !v_out) return fail(VS_ERR_INVALID, "null argument");
+    if ((uintptr_t)v_out & 15u) return fail(VS_ERR_INVALID, "v_out must be 16-byte aligned");
+    const L1Fuse l1{gt_packed, mask_cx, mask_cy, mask_radius, v_out};
+    return render_forward(ctx, cam, sp, W, H, background, pass, mode, out, state_out, &l1);
 }
 
 extern "C" vs_status vs_render_backward(vs_ctx* ctx, vs_fwd_state* st, const vs_splats* sp, const float* out_img,
@@ -1446,14 +1479,12 @@ extern "C" vs_status vs_image_loss_backward(vs_ctx* ctx, const float* pred, uint
     return VS_OK;
 }
 
-static vs_status l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const void* gt, bool packed, uint32_t w,
-                              uint32_t h, float mcx, float mcy, float mr, float* v_out) {
-    if (!ctx || !pred || !gt || !v_out) return fail(VS_ERR_INVALID, "null argument");
-    if (channels < 3) return fail(VS_ERR_INVALID, "prediction needs at least 3 channels");
+// 1 / (3 x the pixels the L1 term averages over): the whole image, or the
+// pixels inside the circle mask, counted with the kernels' own f32 test once
+// per mask (a training loop passes the same mask every step).
+static float l1_inv_count(vs_ctx* ctx, uint32_t w, uint32_t h, float mcx, float mcy, float mr) {
     uint64_t count = (uint64_t)w * h;
     if (mr > 0.0f) {
-        // The pixels the kernel keeps, counted with its own f32 test once per
-        // mask (a training loop passes the same mask every step).
         const vs_ctx::MaskKey& k = ctx->l1_mask;
         if (!(k.w == w && k.h == h && k.cx == mcx && k.cy == mcy && k.r == mr)) {
             count = 0;
@@ -1467,7 +1498,14 @@ static vs_status l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels,
         }
         count = ctx->l1_mask_count;
     }
-    const float inv = count ? 1.0f / (3.0f * (float)count) : 0.0f;
+    return count ? 1.0f / (3.0f * (float)count) : 0.0f;
+}
+
+static vs_status l1_cotangent(vs_ctx* ctx, const float* pred, uint32_t channels, const void* gt, bool packed, uint32_t w,
+                              uint32_t h, float mcx, float mcy, float mr, float* v_out) {
+    if (!ctx || !pred || !gt || !v_out) return fail(VS_ERR_INVALID, "null argument");
+    if (channels < 3) return fail(VS_ERR_INVALID, "prediction needs at least 3 channels");
+    const float inv = l1_inv_count(ctx, w, h, mcx, mcy, mr);
     VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
     VS_HIP(launch_l1_cotangent(pred, channels, gt, packed, w, h, mcx, mcy, mr, inv, v_out, ctx->stream), "l1 cotangent");
     return VS_OK;

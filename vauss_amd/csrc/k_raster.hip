@@ -374,6 +374,20 @@ constexpr int FWD_BATCH = 64;
 // range end (one past its last blended intersection) is the maximum over its
 // quadrants, kept with an atomic max on an end the dispatch-order pass set
 // to the range start.
+// The L1 term's cotangent at pixel (x, y) (crates/splat-train-loss/src/lib.rs:
+// 786-811): sign(pred - gt) * inv_count on rgb inside the circle mask of
+// radius mr about (mcx, mcy) (none for mr <= 0), 0 on alpha and outside; a
+// packed target channel is its byte x (1/255) in f32 (lib.rs:93,1042-1044).
+// l1_cotangent_kernel and the forward's fused epilogue both use these.
+constexpr float L1_INV_255 = 1.0f / 255.0f;
+VS_DEV float l1_sign(float p, float g, float inv) { const float d = p - g; return (d > 0.0f) ? inv : ((d < 0.0f) ? -inv : 0.0f); }
+VS_DEV bool l1_in_mask(uint32_t x, uint32_t y, float mcx, float mcy, float mr) {
+    if (!(mr > 0.0f)) return true;
+    const float dx = (float)x + 0.5f - mcx, dy = (float)y + 0.5f - mcy;
+    return dx * dx + dy * dy <= mr * mr;
+}
+VS_DEV float l1_unpack(uint32_t q, int c) { return (float)((q >> (8 * c)) & 0xFFu) * L1_INV_255; }
+
 template <bool BWD, bool GEOM, bool SMOOTH, bool SURF>
 __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
     // Every per-splat array has 16-byte slots, so one LDS address, the slot's
@@ -569,6 +583,15 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             o[2] = make_float4(nz, dist_b, dist_c, as_f(median_id));
         } else if constexpr (BWD) {
             reinterpret_cast<float4*>(a.out)[pid] = make_float4(fr, fg, fb, fa);
+            if (a.l1_v) {   // uniform: the L1 cotangent of this image (vs_render_forward_l1)
+                const uint32_t q = a.l1_gt[pid];
+                const float inv = a.l1_inv;
+                reinterpret_cast<float4*>(a.l1_v)[pid] =
+                    l1_in_mask(px, py, a.l1_mcx, a.l1_mcy, a.l1_mr)
+                        ? make_float4(l1_sign(fr, l1_unpack(q, 0), inv), l1_sign(fg, l1_unpack(q, 1), inv),
+                                      l1_sign(fb, l1_unpack(q, 2), inv), 0.0f)
+                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
         } else {
             const uint32_t r8 = f2u_sat(clampf(fr * 255.0f, 0.0f, 255.0f));
             const uint32_t g8 = f2u_sat(clampf(fg * 255.0f, 0.0f, 255.0f));
@@ -1080,13 +1103,10 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
 }
 
 // sign(pred - gt) * inv_count on rgb, 0 on the other channels and outside
-// the mask.  Images whose channel count is a multiple of 4 (RGBA, the
-// 12-channel geometry render) are read and written as float4s: the first
-// holds rgb, the rest are zero.  A PACKED target is [H,W] RGBA8 (r in the
-// low byte), each channel byte x (1/255) in f32 as the reference's loss
-// kernels unpack it (crates/splat-train-loss/src/lib.rs:93,1042-1044).
-VS_DEV float l1_sign(float p, float g, float inv) { const float d = p - g; return (d > 0.0f) ? inv : ((d < 0.0f) ? -inv : 0.0f); }
-constexpr float L1_INV_255 = 1.0f / 255.0f;
+// the mask (l1_sign, l1_in_mask).  Images whose channel count is a multiple
+// of 4 (RGBA, the 12-channel geometry render) are read and written as
+// float4s: the first holds rgb, the rest are zero.  A PACKED target is [H,W]
+// RGBA8 (r in the low byte, l1_unpack).
 
 template <bool VEC4, bool PACKED>
 __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, const void* __restrict__ gt_in, uint32_t w,
@@ -1094,18 +1114,14 @@ __global__ void l1_cotangent_kernel(const float* __restrict__ pred, uint32_t C, 
     const uint32_t pid = blockIdx.x * blockDim.x + threadIdx.x;
     if (pid >= w * h) return;
     const uint32_t x = pid % w, y = pid / w;
-    bool in_mask = true;
-    if (mr > 0.0f) {
-        const float dx = (float)x + 0.5f - mcx, dy = (float)y + 0.5f - mcy;
-        in_mask = dx * dx + dy * dy <= mr * mr;
-    }
+    const bool in_mask = l1_in_mask(x, y, mcx, mcy, mr);
     const float inv = in_mask ? inv_count : 0.0f;
     float g0, g1, g2;
     if constexpr (PACKED) {
         const uint32_t q = static_cast<const uint32_t*>(gt_in)[pid];
-        g0 = (float)(q & 0xFFu) * L1_INV_255;
-        g1 = (float)((q >> 8) & 0xFFu) * L1_INV_255;
-        g2 = (float)((q >> 16) & 0xFFu) * L1_INV_255;
+        g0 = l1_unpack(q, 0);
+        g1 = l1_unpack(q, 1);
+        g2 = l1_unpack(q, 2);
     } else {
         const float* gt = static_cast<const float*>(gt_in);
         g0 = gt[(size_t)pid * 3]; g1 = gt[(size_t)pid * 3 + 1]; g2 = gt[(size_t)pid * 3 + 2];

@@ -143,6 +143,11 @@ struct RasterArgs {
     float* visible;                  // [N] or null
     uint8_t* qpass;                  // [I][4] bwd-info passes: byte q = 1 << q when a pixel of quadrant q
                                      // passed (blended or stopped) at that list entry, or null
+    // The L1 term's cotangent of the RGBA image written with it (null l1_v: none):
+    // target [H,W] packed RGBA8, circle mask (l1_mr <= 0: none), 1 / (3 masked pixels)
+    const uint32_t* l1_gt;
+    float* l1_v;                     // [H,W,4]
+    float l1_mcx, l1_mcy, l1_mr, l1_inv;
 };
 
 struct RasterBwdArgs {

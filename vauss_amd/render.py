@@ -235,6 +235,7 @@ class RenderOutput:
     state: Optional[ForwardState]
     camera_uniforms: _lib.VsCamera
     background: tuple
+    v_l1: Optional[torch.Tensor] = None     # the L1 cotangent written with the image (render's l1_target)
 
 
 @dataclass
@@ -314,7 +315,9 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
            raw_opacities: torch.Tensor, background=(0.0, 0.0, 0.0), pass_: RasterPass = RasterPass.BACKWARD,
            render_mode: SplatRenderMode = SplatRenderMode.DEFAULT, log_scale_offset: float = 0.0,
            validate: bool = False, min_scale: Optional[torch.Tensor] = None,
-           decoder: Optional[torch.Tensor] = None, neural_degree: int = 0, count_slot: int = 0) -> RenderOutput:
+           decoder: Optional[torch.Tensor] = None, neural_degree: int = 0, count_slot: int = 0,
+           l1_target: Optional[torch.Tensor] = None, l1_mask_center=(0.0, 0.0),
+           l1_mask_radius: float = 0.0) -> RenderOutput:
     """SplatOps::render (SplatOps::render_neural with `decoder`).  `camera` is
     a Camera or ready-made vs_camera uniforms.  `render_mode` DEFAULT or MIP;
     `min_scale` [N] is the scale floor (render's min_scale with
@@ -325,6 +328,11 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     `count_slot` (0..255) is the slot of a BACKWARD_DENSE or EXPOSURE pass
     (RasterPass::BackwardDense { slot }): its lagged counts stay apart from
     the step's other renders at the same size.
+
+    `l1_target` ([H,W] int32 packed RGBA8) makes the raster pass also write
+    the L1 term's cotangent of its image (vs_render_forward_l1, the values of
+    l1_cotangent with that target and circle mask) into `v_l1`: a float RGBA
+    pass, not surfels.
 
     Returns the image ([H,W,C] f32, or [H,W] int32-packed RGBA8 for
     FORWARD), the aux outputs and, for every pass but FORWARD, the state the
@@ -368,10 +376,26 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     was_validating = ctx.validation
     if validate and not was_validating:
         ctx.set_validation(True)
+    v_l1 = None
+    if l1_target is not None:
+        if ch != 4 or SplatRenderMode(render_mode) is SplatRenderMode.SURFEL:
+            raise ValueError("the fused L1 cotangent takes a float RGBA pass (no geometry channels, no surfels)")
+        l1_target = l1_target.contiguous()
+        if l1_target.dtype != torch.int32 or tuple(l1_target.shape) != (h, w):
+            raise ValueError(f"l1_target must be int32 [{h}, {w}] packed RGBA8, got {l1_target.dtype} "
+                             f"{tuple(l1_target.shape)}")
+        v_l1 = torch.empty((h, w, 4), dtype=torch.float32, device=dev)
     try:
-        _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg,
-                                             _lib.pass_with_slot(pass_, count_slot), int(render_mode), C.byref(out),
-                                             C.byref(st)))
+        if v_l1 is None:
+            _lib.check(ctx.lib.vs_render_forward(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg,
+                                                 _lib.pass_with_slot(pass_, count_slot), int(render_mode),
+                                                 C.byref(out), C.byref(st)))
+        else:
+            _lib.check(ctx.lib.vs_render_forward_l1(ctx.handle, C.byref(cam), C.byref(splats), w, h, bg,
+                                                    _lib.pass_with_slot(pass_, count_slot), int(render_mode),
+                                                    _ptr(l1_target), float(l1_mask_center[0]),
+                                                    float(l1_mask_center[1]), float(l1_mask_radius), _ptr(v_l1),
+                                                    C.byref(out), C.byref(st)))
     finally:
         if validate and not was_validating:
             ctx.set_validation(False)
@@ -380,7 +404,7 @@ def render(camera, img_size: Sequence[int], transforms: torch.Tensor, sh_coeffs:
     if state is not None:
         state.keep = min_scale          # the state borrows the floor for project_update
         state.surfel = SplatRenderMode(render_mode) is SplatRenderMode.SURFEL
-    return RenderOutput(out_img, aux, state, cam, tuple(float(v) for v in background))
+    return RenderOutput(out_img, aux, state, cam, tuple(float(v) for v in background), v_l1)
 
 
 def render_backward(output: RenderOutput, transforms: torch.Tensor, sh_coeffs: torch.Tensor,
