@@ -201,6 +201,15 @@ constexpr uint32_t POISON_WORD = 0xC640E400u;
 // view's depth keys (depth bits - minimum) span.
 constexpr uint32_t DEPTH_RADIX_BITS = 9;
 static_assert(CNT_DEPTH_MAX == CNT_DEPTH_MIN + 1, "the depth sort reads [min, max] as a pair");
+// The tile sort's digits: the narrowest of 7, 8 and 9 bits that sorts `bits`
+// in as few passes as 9-bit digits would (7 for the 13-14 bits of tile ids
+// up to 2560 x 1440 images: two passes of 128-digit look-back).
+static uint32_t tile_radix_bits(uint32_t bits) {
+    const uint32_t passes = (bits + 8) / 9;
+    for (uint32_t rb = 7; rb < 9; ++rb)
+        if ((bits + rb - 1) / rb <= passes) return rb;
+    return 9;
+}
 
 // Every buffer the library allocates for itself: stream-ordered, and filled
 // with POISON_WORD first when the context asks for it.
@@ -824,8 +833,9 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
         const size_t o_mass = cutoff ? itake(cut_words * 4) : 0, o_allow = cutoff ? itake(cut_words * 2) : 0;
         const size_t o_cut = cutoff ? itake(T) : 0, o_kept = cutoff ? itake((size_t)N * 4) : 0;
         const size_t o_listed = cutoff ? itake(4) : 0;
-        // serves both sorts: the depth sort on 9-bit digits, the tile sort on 8-bit ones
-        const size_t o_tmp = itake(std::max(sort_tmp_bytes(I, false), sort_tmp_bytes(M, false, DEPTH_RADIX_BITS)));
+        // serves both sorts (the depth sort on 9-bit digits, the tile sort on tile_rb-bit ones)
+        const uint32_t tile_rb = tile_radix_bits(tile_bits);
+        const size_t o_tmp = itake(std::max(sort_tmp_bytes(I, false, tile_rb), sort_tmp_bytes(M, false, DEPTH_RADIX_BITS)));
         VS_HIP(lib_alloc(ctx, &st->isect_arena, ioff, s), "hipMallocAsync(intersection arena)");
         char* ib = static_cast<char*>(st->isect_arena);
         uint32_t* tiles_u = reinterpret_cast<uint32_t*>(ib + o_tu);
@@ -843,7 +853,7 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
         // the sorts' one-sweep state (shared scratch) is cleared by the kernel
         // before each sort: compaction for the depth sort, emission for the tile sort
         const SortZeroSpan depth_zero = sort_zero_span(M, 0, depth_bits, ib + o_tmp, DEPTH_RADIX_BITS);
-        const SortZeroSpan tile_zero = (M > 0 && N > 0) ? sort_zero_span(I, 0, tile_bits, ib + o_tmp)
+        const SortZeroSpan tile_zero = (M > 0 && N > 0) ? sort_zero_span(I, 0, tile_bits, ib + o_tmp, tile_rb)
                                                          : SortZeroSpan{nullptr, 0};
         uint32_t* cut_mass = cutoff ? reinterpret_cast<uint32_t*>(ib + o_mass) : nullptr;
         uint16_t* cut_allow = cutoff ? reinterpret_cast<uint16_t*>(ib + o_allow) : nullptr;
@@ -909,7 +919,8 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
         {
             StageTimer tm(ctx, ST_SORT);
             VS_HIP(radix_sort_pairs(tiles_u, vals_u, st->tiles, st->gids, I, cutoff ? st->listed : i_dev, false, 0,
-                                    tile_bits, ib + o_tmp, err, s, ctx->spin_limit, &tro, tile_zero.ptr != nullptr),
+                                    tile_bits, ib + o_tmp, err, s, ctx->spin_limit, &tro, tile_zero.ptr != nullptr,
+                                    tile_rb),
                    "tile sort");
             st->tiles_pending = tro.done;
         }

@@ -1,5 +1,5 @@
 // k_sort.hip -- stable LSD radix sort of (key, u32 value) pairs, 8-bit digits
-// (9-bit for the render's depth sort, see sort_impl), u32 or u64 keys.
+// (7 or 9 bits for the render's sorts, see sort_impl), u32 or u64 keys.
 //
 // Replaces crates/splat-train-sort (radix_argsort*, lib.rs:15-189;
 // kernels.rs:35-341).  Two schedules share one block-level ranking step, in
@@ -468,7 +468,7 @@ static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 size_t sort_tmp_bytes(uint64_t n, bool key64, uint32_t radix_bits) {
     const uint64_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;
     const size_t ks = key64 ? 8 : 4;
-    const uint32_t rb = radix_bits == 9 ? 9u : 8u;
+    const uint32_t rb = (radix_bits == 7 || radix_bits == 9) ? radix_bits : 8u;
     const uint64_t max_passes = (8 * ks + rb - 1) / rb, R = 1ull << rb;
     size_t b = 0;
     b += align_up(n * ks, 256);                 // ping-pong keys
@@ -494,8 +494,10 @@ static void launch_onesweep_pass(bool small, uint32_t os_tiles, const K* src_k, 
             src_k, src_v, dk, dv, n, n_dev, shift, gh, gh_stride, status, err, spin_limit, rng, nt, key_span);
 }
 
-// Digits of 8 bits, or of 9 (radix_bits = 9, u32 keys, one-sweep schedule
-// only): three passes then cover 27 bits, the span of a view's depth keys.
+// Digits of 8 bits, or of 7 or 9 (radix_bits, u32 keys, one-sweep schedule
+// only): 9-bit digits cover a view's depth span (27 bits) in three passes,
+// 7-bit ones a tile id of up to 14 bits in two, with a quarter of the
+// look-back and one ballot fewer per key than 8-bit ones.
 template <typename K>
 static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_out, uint32_t* vals_out, uint32_t n,
                             const uint32_t* n_dev, uint32_t first_bit, uint32_t end_bit, void* tmp, uint32_t* err,
@@ -509,7 +511,7 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         return hipMemcpyAsync(vals_out, vals_in, (size_t)n * 4, hipMemcpyDeviceToDevice, s);
     }
     const bool onesweep = n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS && err != nullptr;
-    const uint32_t rb = (onesweep && sizeof(K) == 4 && radix_bits == 9) ? 9u : 8u;
+    const uint32_t rb = (onesweep && sizeof(K) == 4 && (radix_bits == 7 || radix_bits == 9)) ? radix_bits : 8u;
     const uint32_t R = 1u << rb;
     const uint32_t passes = (bits + rb - 1) / rb;
     const uint32_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;
@@ -534,6 +536,7 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         const uint32_t hist_blocks = (uint32_t)max((uint64_t)1, min((uint64_t)HIST_BLOCKS, ((uint64_t)n + 4095) / 4096));
         if constexpr (sizeof(K) == 4) {
             if (rb == 9) sort_histogram_kernel<K, 9><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+            else if (rb == 7) sort_histogram_kernel<K, 7><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
             else sort_histogram_kernel<K, 8><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
         } else {
             sort_histogram_kernel<K, 8><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
@@ -556,7 +559,10 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
             const uint32_t* gh = ghist + pass * R;
             uint32_t* st = status + (size_t)pass * os_tiles * R;
             if constexpr (sizeof(K) == 4) {
-                if (rb == 9)
+                if (rb == 7)
+                    launch_onesweep_pass<K, 7>(small, os_tiles, src_k, src_v, dk, dv, n, n_dev, shift, gh, passes * R, st,
+                                               err, spin_limit, rng, nt, key_span, s);
+                else if (rb == 9)
                     launch_onesweep_pass<K, 9>(small, os_tiles, src_k, src_v, dk, dv, n, n_dev, shift, gh, passes * R, st,
                                                err, spin_limit, rng, nt, key_span, s);
                 else
@@ -605,7 +611,7 @@ SortZeroSpan sort_zero_span(uint32_t n, uint32_t first_bit, uint32_t end_bit, vo
     // one-sweep histograms and status
     const uint32_t bits = end_bit > first_bit ? end_bit - first_bit : 0;
     if (n == 0 || bits == 0 || !(n >= ONESWEEP_MIN && n < ONESWEEP_MAX_KEYS)) return SortZeroSpan{nullptr, 0};
-    const uint32_t rb = radix_bits == 9 ? 9u : 8u;
+    const uint32_t rb = (radix_bits == 7 || radix_bits == 9) ? radix_bits : 8u;
     const uint64_t R = 1ull << rb;
     const uint32_t passes = (bits + rb - 1) / rb;
     const uint32_t nblocks = (n + SORT_TILE - 1) / SORT_TILE;

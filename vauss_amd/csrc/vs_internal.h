@@ -405,8 +405,8 @@ hipError_t radix_sort_pairs(const void* keys_in, const uint32_t* vals_in, void* 
                             uint32_t spin_limit = SORT_SPIN_LIMIT_DEFAULT, TileRangesOut* tr = nullptr,
                             bool state_zeroed = false, uint32_t radix_bits = 8,
                             const uint32_t* key_span = nullptr);
-// radix_bits = 9: digits of 9 bits (u32 keys of the one-sweep schedule; 8
-// elsewhere).  key_span (device [min, max], or null): the keys are values
+// radix_bits = 7 or 9: digits of that width (u32 keys of the one-sweep
+// schedule; 8 elsewhere).  key_span (device [min, max], or null): the keys are values
 // minus min, so no key has a bit at or above bitlen(max - min), and a pass
 // whose digit lies there copies its input (not with a range pass).
 // The words of `tmp` that a u32-key sort of n keys over [first_bit, end_bit)
