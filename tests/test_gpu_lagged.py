@@ -265,3 +265,51 @@ def test_count_slots_keep_renders_apart(lagged_ctx):
     assert g.v_transforms is None and g.v_combined is not None
     for x in (a0, b0, ea, eb, a1, b1, a2, b2, f):
         x.state.free()
+
+
+def test_lagged_depth_sort_over_the_full_key_width(lagged_ctx):
+    """A wide Kannala-Brandt camera with splats on both sides of its camera
+    plane: the visible depth bits span more than 27 bits (negative z sorts
+    after every positive one by raw bits, render.rs:689-694), so the depth
+    sort's fourth 9-bit pass ranks instead of copying, in the lagged render
+    (32-bit keys) and the exact one (bitlen of the span).  Both lists, images
+    and gradients agree bit for bit / at the contract bar, and each tile's list
+    is the stable order of (raw depth bits, id) of its splats."""
+    from vauss_amd import camera as vcam
+    img = (256, 256)
+    model = vcam.KannalaBrandt4(0.01, -0.004, 0.001, -0.0002)
+    cam = vcam.Camera.from_focal(40.0, 40.0, img, model=model).uniforms(img)
+    rng = np.random.default_rng(78)
+    n = 30_000
+    d = rng.standard_normal((n, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    r = rng.uniform(2.0, 4.0, n)
+    tr = np.concatenate([d * r[:, None], rng.standard_normal((n, 4)), rng.uniform(-3.2, -2.4, (n, 3))],
+                        1).astype(np.float32)
+    sc = scenes.Scene(tr, rng.uniform(0, 1, (n, 1, 3)).astype(np.float32), rng.uniform(0.0, 3.0, n).astype(np.float32))
+    t, s, o = to_gpu(sc)
+    print(f"[case] kb4 wide n={n} {img}, both sides of the camera plane, lagged", flush=True)
+    r0 = _render(lagged_ctx, cam, img, t, s, o)          # seeds the hint
+    r1 = _render(lagged_ctx, cam, img, t, s, o)          # lagged
+    e1 = _render(lagged_ctx, cam, img, t, s, o, lagged=False)
+    lt, lg, lr, la = _list(r1)
+    et, eg, er, ea = _list(e1)
+    db = ea["depth_bits"]
+    vis = ea["counts"] > 0
+    assert vis.sum() >= 4096                             # the one-sweep schedule, where 9-bit digits apply
+    span = int(db[vis].max()) - int(db[vis].min())
+    assert span.bit_length() > 27 and (db[vis] >= 0x80000000).sum() >= 100
+    np.testing.assert_array_equal(lr, er)
+    np.testing.assert_array_equal(lt, et)
+    np.testing.assert_array_equal(lg, eg)
+    np.testing.assert_array_equal(r1.out_img.cpu().numpy().view(np.uint32), e1.out_img.cpu().numpy().view(np.uint32))
+    # each tile's entries in (raw depth bits, id) order
+    key = (et.astype(np.uint64) << np.uint64(52)) | (db[eg].astype(np.uint64) << np.uint64(20)) | eg.astype(np.uint64)
+    assert eg.max() < (1 << 20) and et.max() < (1 << 11)
+    assert (key[1:] > key[:-1]).all()
+    v_out = torch.from_numpy(l1_cotangent_np(e1.out_img.cpu().numpy(), np.full(img[::-1] + (3,), 0.5, np.float32))).cuda()
+    gl = va.render_backward(r1, t, s, o, v_out)
+    ge = va.render_backward(e1, t, s, o, v_out)
+    _check_grads(gl.v_transforms.cpu().numpy(), ge.v_transforms.cpu().numpy(), "v_transforms")
+    for x in (r0, r1, e1):
+        x.state.free()
