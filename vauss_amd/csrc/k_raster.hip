@@ -480,11 +480,8 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
           const uint4 la = *reinterpret_cast<const uint4*>(&s_list[j0]);
           const uint4 lb = *reinterpret_cast<const uint4*>(&s_list[j0 + 4u]);
           const uint32_t offs[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
-#pragma unroll
-          for (uint32_t jj = 0; jj < 8u; ++jj) {
-            const uint32_t j = j0 + jj;
-            if (j >= jn) break;                       // uniform
-            const uint32_t off = offs[jj];
+          // one list entry: the slot at LDS byte offset `off`
+          auto entry = [&](uint32_t off) {
             const float4 sb = *reinterpret_cast<const float4*>(lds_b + off);
             float sigma, zs = 0.0f, G;
             bool valid = true;
@@ -548,6 +545,18 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                     }
                     T = nt;
                 }
+            }
+          };
+          if (j0 + 8u <= nlist) {
+            // a full group runs without a bound test per entry (scalar
+            // compare-and-branch work the CU's shared scalar unit would do)
+#pragma unroll
+            for (uint32_t jj = 0; jj < 8u; ++jj) entry(offs[jj]);
+          } else {
+#pragma unroll
+            for (uint32_t jj = 0; jj < 8u; ++jj) {
+              if (j0 + jj >= jn) break;                 // uniform
+              entry(offs[jj]);
             }
           }
           if (__ballot(done_v == 0u) == 0ull) break;   // every pixel of the quadrant is done (uniform)
