@@ -901,7 +901,7 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
         {
             StageTimer tm(ctx, ST_EMIT);
             VS_HIP(scan_u32_lookback(slot_counts, slot_base, M, scan_tmp, err, s, ctx->spin_limit, order, m_dev, N,
-                                     slot_base_g, true),
+                                     slot_base_g, true, EMIT_SMALL_LIST),
                    "slot scan");
             EmitArgs ea{};
             ea.num_splats = N; ea.tile_bw = st->tbw; ea.tile_bh = st->tbh;

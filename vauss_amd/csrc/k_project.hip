@@ -712,17 +712,18 @@ __global__ void __launch_bounds__(PROJ_BLOCK) compact_kernel(CompactArgs a) {
 // slots [base, base + count), which the scan in depth order assigned, and
 // writes there the ids of the tiles that pass the tile test, in row-major box
 // order.  One launch, two kinds of blocks:
-//  * the first EMIT_BIG_BLOCKS(N) blocks walk the splats whose box exceeds
-//    EMIT_SMALL_BOX tiles, one lane per splat in global-id order, where large
-//    boxes are spread evenly over the wavefronts (in depth order the nearest,
-//    largest ones would share the first wavefronts);
+//  * the first emit_big_blocks(N) blocks walk the splats of more than
+//    EMIT_SMALL_LIST slots, one lane per splat in global-id order, where long
+//    lists are spread evenly over the wavefronts (in depth order the nearest,
+//    largest ones would share the first wavefronts); their slot bases come
+//    from the scan's copy by global id, which it writes for them alone;
 //  * the rest walk the other splats in depth order, one lane per emitter:
 //    neighbouring lanes own neighbouring slot ranges, so a wavefront's stores
 //    fill one contiguous stretch of the list.
-// If the recomputed test finds fewer tiles than the projection counted, the
-// rest of a splat's slots get the sentinel tile id T, which sorts last and
-// owns no range.
-constexpr uint32_t EMIT_SMALL_BOX = 32;
+// Both kinds know a splat's count before reading its row, so each reads only
+// the rows it emits.  If the recomputed test finds fewer tiles than the
+// projection counted, the rest of a splat's slots get the sentinel tile id T,
+// which sorts last and owns no range.
 VS_DEV uint32_t emit_big_blocks(uint32_t n) { return (n + PROJ_BLOCK - 1) / PROJ_BLOCK; }
 
 template <bool FILTER>
@@ -734,6 +735,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     if (big) {
         g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
         cnt = (g < a.num_splats) ? a.counts[g] : 0u;
+        if (cnt <= EMIT_SMALL_LIST) cnt = 0u;         // the depth-order blocks emit it
     } else {
         const uint32_t j = (blockIdx.x - big_blocks) * PROJ_BLOCK + threadIdx.x;
         const uint32_t m = a.m_dev ? min(*a.m_dev, a.num_emitters) : a.num_emitters;
@@ -743,6 +745,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
             // the count from the slot bases in depth order (slot_base[m] is the
             // total) rather than a gather from the counts in id order
             cnt = (g < a.num_splats) ? a.slot_base[j + 1] - base : 0u;
+            if (cnt > EMIT_SMALL_LIST) cnt = 0u;      // the global-id blocks emit it
         }
     }
     float px = 0.0f, py = 0.0f, power = 0.0f;
@@ -763,8 +766,6 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
         if (FILTER) bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
     }
-    const uint32_t nb = (cnt > 0) ? (bb.y1 - bb.y0) * (bb.x1 - bb.x0) : 0u;
-    if (big != (nb > EMIT_SMALL_BOX)) cnt = 0u;     // the other kind of block emits it
     if (big && cnt > 0) base = a.slot_base_g[g];
     __shared__ RowLds s_walk[PROJ_BLOCK / 64];
     RowLds& L = s_walk[threadIdx.x / 64];

@@ -1,7 +1,7 @@
 // k_scan.hip -- device-wide u32 prefix sums.
 //
 // Replaces crates/splat-train-scan (prefix_sum, lib.rs:24-83; scan_in_place,
-// lib.rs:85-96).  Reduce-then-scan over 4096-element blocks: a reduce kernel
+// lib.rs:85-96).  Reduce-then-scan over 1024-element blocks: a reduce kernel
 // writes block totals, one workgroup scans the totals, and a scan kernel
 // re-reads its block through LDS (coalesced loads, blocked per-thread
 // sequential scan, wave shuffles) and adds the block offset.
@@ -10,8 +10,8 @@
 namespace vs {
 
 constexpr int SCAN_BLOCK = 256;
-constexpr int SCAN_ITEMS = 16;
-constexpr uint32_t SCAN_TILE = SCAN_BLOCK * SCAN_ITEMS;   // 4096
+constexpr int SCAN_ITEMS = 4;
+constexpr uint32_t SCAN_TILE = SCAN_BLOCK * SCAN_ITEMS;   // 1024: over 600 blocks for 616k elements
 constexpr int SINGLE_BLOCK = 1024;
 
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, uint32_t lane) {
@@ -152,7 +152,7 @@ constexpr uint64_t LB_AGG = 1ull << 62, LB_PREFIX = 2ull << 62, LB_VAL = (1ull <
 __global__ void __launch_bounds__(SCAN_BLOCK) scan_lookback_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
                                                                    uint64_t n_cap, const uint32_t* __restrict__ perm,
                                                                    const uint32_t* __restrict__ n_dev, uint32_t perm_bound,
-                                                                   uint32_t* __restrict__ out2,
+                                                                   uint32_t* __restrict__ out2, uint32_t out2_above,
                                                                    unsigned long long* status, uint32_t* err,
                                                                    uint32_t spin_limit, int write_end) {
     const uint64_t n = scan_count(n_cap, n_dev);
@@ -214,6 +214,12 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_lookback_kernel(const uint32_
 #pragma unroll
     for (int i = 0; i < SCAN_ITEMS; ++i) {
         s_data[threadIdx.x * SCAN_ITEMS + i] = run;
+        // the scattered copy, for the few elements above the threshold (an
+        // element past n loaded as 0, which is never above it)
+        if (out2 && v[i] > out2_above) {
+            const uint32_t k = perm[base + (uint64_t)threadIdx.x * SCAN_ITEMS + i];
+            if (k < perm_bound) out2[k] = run;
+        }
         run += v[i];
     }
     // out[n]: the total, from the thread holding element n - 1 (the elements
@@ -227,13 +233,7 @@ __global__ void __launch_bounds__(SCAN_BLOCK) scan_lookback_kernel(const uint32_
     for (int i = 0; i < SCAN_ITEMS; ++i) {
         const uint32_t li = i * SCAN_BLOCK + threadIdx.x;
         const uint64_t idx = base + li;
-        if (idx < n) {
-            out[idx] = s_data[li];
-            if (out2) {
-                const uint32_t k = perm[idx];
-                if (k < perm_bound) out2[k] = s_data[li];
-            }
-        }
+        if (idx < n) out[idx] = s_data[li];
     }
 }
 
@@ -241,11 +241,11 @@ uint64_t scan_lookback_status_words(uint64_t n) { return 2 * ((n + SCAN_TILE - 1
 
 hipError_t scan_u32_lookback(const uint32_t* in, uint32_t* out, uint64_t n, uint32_t* status, uint32_t* err,
                              hipStream_t s, uint32_t spin_limit, const uint32_t* perm, const uint32_t* n_dev,
-                             uint32_t perm_bound, uint32_t* out_scattered, bool write_end) {
+                             uint32_t perm_bound, uint32_t* out_scattered, bool write_end, uint32_t scatter_above) {
     if (n == 0) return hipSuccess;
     const uint64_t blocks = (n + SCAN_TILE - 1) / SCAN_TILE;
     scan_lookback_kernel<<<(uint32_t)blocks, SCAN_BLOCK, 0, s>>>(in, out, n, perm, n_dev, perm_bound,
-                                                                 perm ? out_scattered : nullptr,
+                                                                 perm ? out_scattered : nullptr, scatter_above,
                                                                  reinterpret_cast<unsigned long long*>(status), err,
                                                                  spin_limit, write_end ? 1 : 0);
     return hipGetLastError();

@@ -84,6 +84,10 @@ struct CompactArgs {
     uint64_t zero2_words;
 };
 
+// Emission splits the emitters by slot count: up to EMIT_SMALL_LIST slots
+// in depth order, more in global-id order (their slot bases scattered by id).
+constexpr uint32_t EMIT_SMALL_LIST = 64;
+
 struct EmitArgs {
     uint32_t num_splats, tile_bw, tile_bh;
     uint32_t num_emitters;           // M: length of `order` (a capacity when m_dev is set)
@@ -91,7 +95,7 @@ struct EmitArgs {
     const uint32_t* order;           // [M] global ids of the emitters, nearest first
     const uint32_t* counts;          // [N]
     const uint32_t* slot_base;       // [M + 1] first slot of the j-th nearest emitter (exclusive scan), then the total
-    const uint32_t* slot_base_g;     // [N] the same, at the global id (emitters only)
+    const uint32_t* slot_base_g;     // [N] the same, at the global id (emitters of more than EMIT_SMALL_LIST slots only)
     const float4* proj;              // [N][PROJ_Q] projected rows
     uint32_t* tiles;                 // [capacity] tile id (T = sentinel)
     uint32_t* vals;                  // [capacity] global id
@@ -373,15 +377,16 @@ hipError_t scan_u32(const uint32_t* in, uint32_t* out, uint64_t n, bool inclusiv
                     uint32_t* out_scattered = nullptr);
 hipError_t scan_single_block(uint32_t* data, uint32_t n, bool inclusive, uint32_t* total_out, hipStream_t s);
 // The same exclusive scan in one kernel by decoupled look-back, written in
-// sequence order (out[i]; `out_scattered[perm[i]]` too when both are given).
-// `status` needs scan_lookback_status_words(n) words, zero on entry; a
-// look-back that waits past `spin_limit` polls sets *err.  With `write_end`,
-// out[n] (out holds n + 1 words) receives the total.
+// sequence order (out[i]; with both `perm` and `out_scattered`, also
+// out_scattered[perm[i]] for the elements whose input exceeds
+// `scatter_above`).  `status` needs scan_lookback_status_words(n) words, zero
+// on entry; a look-back that waits past `spin_limit` polls sets *err.  With
+// `write_end`, out[n] (out holds n + 1 words) receives the total.
 uint64_t scan_lookback_status_words(uint64_t n);
 hipError_t scan_u32_lookback(const uint32_t* in, uint32_t* out, uint64_t n, uint32_t* status, uint32_t* err,
                              hipStream_t s, uint32_t spin_limit, const uint32_t* perm = nullptr,
                              const uint32_t* n_dev = nullptr, uint32_t perm_bound = 0xFFFFFFFFu,
-                             uint32_t* out_scattered = nullptr, bool write_end = false);
+                             uint32_t* out_scattered = nullptr, bool write_end = false, uint32_t scatter_above = 0u);
 
 // Radix sort.  `tmp` needs sort_tmp_bytes(n, key64, radix_bits) bytes.
 size_t sort_tmp_bytes(uint64_t n, bool key64, uint32_t radix_bits = 8);
