@@ -472,16 +472,9 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         // (the blend) keeps the scalar exec-mask work per pair small; the
         // scalar unit is shared by the CU's four SIMDs, and a per-lane loop
         // exit or a guard around the whole body costs it more per pair than
-        // the vector work the masked lanes would skip.
-        for (uint32_t j0 = 0; j0 < nlist; j0 += 8u) {
-          const uint32_t jn = min(j0 + 8u, nlist);
-          // the group's eight list entries in two 16-byte reads (entries past
-          // the list are never used)
-          const uint4 la = *reinterpret_cast<const uint4*>(&s_list[j0]);
-          const uint4 lb = *reinterpret_cast<const uint4*>(&s_list[j0 + 4u]);
-          const uint32_t offs[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
-          // one list entry: the slot at LDS byte offset `off`
-          auto entry = [&](uint32_t off) {
+        // the vector work the masked lanes would skip.  One list entry: the
+        // slot at LDS byte offset `off`.
+        auto entry = [&](uint32_t off) {
             const float4 sb = *reinterpret_cast<const float4*>(lds_b + off);
             float sigma, zs = 0.0f, G;
             bool valid = true;
@@ -546,20 +539,31 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                     T = nt;
                 }
             }
-          };
-          if (j0 + 8u <= nlist) {
-            // a full group runs without a bound test per entry (scalar
-            // compare-and-branch work the CU's shared scalar unit would do)
-#pragma unroll
-            for (uint32_t jj = 0; jj < 8u; ++jj) entry(offs[jj]);
-          } else {
+        };
+        // Full groups of eight entries (two 16-byte list reads each) run
+        // without a bound test per entry (scalar compare-and-branch work the
+        // CU's shared scalar unit would do); the last, partial group has its
+        // own loop, so no entry is shared between the two paths (a shared
+        // first entry made the compiler copy the accumulators there).
+        uint32_t j0 = 0;
+        for (; j0 + 8u <= nlist; j0 += 8u) {
+            const uint4 la = *reinterpret_cast<const uint4*>(&s_list[j0]);
+            const uint4 lb = *reinterpret_cast<const uint4*>(&s_list[j0 + 4u]);
+            entry(la.x); entry(la.y); entry(la.z); entry(la.w);
+            entry(lb.x); entry(lb.y); entry(lb.z); entry(lb.w);
+            if (__ballot(done_v == 0u) == 0ull) break;   // every pixel of the quadrant is done (uniform)
+        }
+        // after a break every pixel is done and the ballot skips the rest
+        if (j0 < nlist && __ballot(done_v == 0u) != 0ull) {
+            // j0 <= 56: both reads stay inside the 64-entry list
+            const uint4 la = *reinterpret_cast<const uint4*>(&s_list[j0]);
+            const uint4 lb = *reinterpret_cast<const uint4*>(&s_list[j0 + 4u]);
+            const uint32_t offs[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
 #pragma unroll
             for (uint32_t jj = 0; jj < 8u; ++jj) {
-              if (j0 + jj >= jn) break;                 // uniform
-              entry(offs[jj]);
+                if (j0 + jj >= nlist) break;                 // uniform
+                entry(offs[jj]);
             }
-          }
-          if (__ballot(done_v == 0u) == 0ull) break;   // every pixel of the quadrant is done (uniform)
         }
         done = done_v != 0u;
         if constexpr (BWD) {
