@@ -844,7 +844,6 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             const float4 sdv = s_d[t];
             const float opac = sbv.y;
             const float cl_r = sbv.z, cl_g = sbv.w, cl_b = scv.x;
-            bool contrib = false;
 #pragma unroll
             for (int k = 0; k < PX; ++k) {
                 if (!((live >> k) & 1u)) continue;          // uniform
@@ -863,7 +862,6 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                 const float nt = Tk * one_m;
                 T[k] = (nt <= T_STOP) ? 0.0f : nt;
                 if (nt <= T_STOP) continue;
-                contrib = true;
                 const float vis = ae * Tk;
                 // colour: the c >= 0 gate is per splat, applied after the reduction
                 g[5] = __builtin_fmaf(vis, vr[k], g[5]);
@@ -891,7 +889,10 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
                     g[9] = __builtin_fmaf(__builtin_amdgcn_sqrtf(__builtin_fmaf(ux, ux, uy * uy)), rscale[k], g[9]);
                 }
             }
-            if (__ballot(contrib) == 0ull) continue;          // g is still all zero
+            // Every live splat is reduced: one whose live quadrants hold no
+            // blending pixel (the forward only stopped pixels there) sums
+            // zeros and adds nothing, and is rare enough that a ballot to
+            // skip it (materialised from the exec masks per splat) cost more.
             {
                 const float c00 = scv.y, c01 = s_c01[t], c11 = scv.z;
                 const float sx = g[0], sy = g[1];
@@ -904,7 +905,9 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
             // zeros at every branch of the next splat's quadrant loop)
 #pragma unroll
             for (int i = 0; i < 10; i += 2) zero_pair(g[i], g[i + 1]);
-            val = ((as_u(scv.w) >> gate_shift) & 1u) ? val * comp_scale : 0.0f;
+            // the gate bit sign-extended to a mask: +0 where the gate is off
+            val = __uint_as_float(__float_as_uint(val * comp_scale) &
+                                  (uint32_t)__builtin_amdgcn_sbfe((int)as_u(scv.w), gate_shift, 1u));
             const uint32_t gid_t = __builtin_amdgcn_readlane(gid, t);
             if ((lane & 3) == 0 && comp >= 0 && val != 0.0f)
                 atomicAdd(&a.v_combined[(size_t)gid_t * 10 + comp], val);
