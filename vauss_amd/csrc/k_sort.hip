@@ -281,39 +281,49 @@ constexpr int HIST_ITEMS = 16;       // keys per lane in flight per chunk (the k
 // sums the eight copies of a digit.  Each wavefront takes chunks of
 // HIST_ITEMS x 64 consecutive keys.  Digits of RB bits.
 constexpr uint32_t HIST_COPIES = 8;
-template <typename K, int RB = 8>
-__global__ void __launch_bounds__(SORT_BLOCK) sort_histogram_kernel(const K* __restrict__ keys, uint32_t n_cap,
-                                                                    const uint32_t* __restrict__ n_dev, uint32_t first_bit,
-                                                                    uint32_t passes, uint32_t* __restrict__ ghist) {
+// NT threads per block, ITEMS keys per lane and chunk.  256-thread blocks
+// keep one LDS histogram per wavefront; wider blocks share one (the same
+// keys per block in a quarter of the chunks per wavefront: a shorter chain
+// of dependent LDS adds, and the same closing global atomics).
+constexpr int HIST_NT = 1024;
+constexpr int HIST_NT_ITEMS = 4;
+static_assert(HIST_NT * HIST_NT_ITEMS == 4096, "a block's first chunks cover the 4096 keys per block of its grid");
+template <typename K, int RB = 8, int NT = SORT_BLOCK, int ITEMS = HIST_ITEMS>
+__global__ void __launch_bounds__(NT) sort_histogram_kernel(const K* __restrict__ keys, uint32_t n_cap,
+                                                            const uint32_t* __restrict__ n_dev, uint32_t first_bit,
+                                                            uint32_t passes, uint32_t* __restrict__ ghist) {
     constexpr uint32_t R = 1u << RB;
     constexpr int HP = (8 * (int)sizeof(K) + RB - 1) / RB;   // passes a key can need
-    __shared__ uint32_t h[SORT_WAVES][HP][R];
+    constexpr int W = NT / 64;
+    constexpr int COPIES = (NT == SORT_BLOCK) ? W : 1;
+    __shared__ uint32_t h[COPIES][HP][R];
     const uint32_t n = n_dev ? min(*n_dev, n_cap) : n_cap;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (uint32_t i = threadIdx.x; i < SORT_WAVES * HP * R; i += SORT_BLOCK) (&h[0][0][0])[i] = 0;
+    for (uint32_t i = threadIdx.x; i < COPIES * HP * R; i += NT) (&h[0][0][0])[i] = 0;
     __syncthreads();
-    const uint64_t stride = (uint64_t)gridDim.x * SORT_WAVES * 64 * HIST_ITEMS;
-    for (uint64_t c = ((uint64_t)blockIdx.x * SORT_WAVES + wave) * 64 * HIST_ITEMS; c < n; c += stride) {
-        K k[HIST_ITEMS];
+    const uint64_t stride = (uint64_t)gridDim.x * W * 64 * ITEMS;
+    for (uint64_t c = ((uint64_t)blockIdx.x * W + wave) * 64 * ITEMS; c < n; c += stride) {
+        K k[ITEMS];
 #pragma unroll
-        for (int s = 0; s < HIST_ITEMS; ++s) {
+        for (int s = 0; s < ITEMS; ++s) {
             const uint64_t idx = c + (uint64_t)s * 64 + lane;
             k[s] = idx < n ? keys[idx] : (K)0;
         }
 #pragma unroll
-        for (int s = 0; s < HIST_ITEMS; ++s) {
+        for (int s = 0; s < ITEMS; ++s) {
             const uint64_t b = c + (uint64_t)s * 64;
             if (b >= n) break;                                   // uniform across the wavefront
             const uint32_t nvalid = (uint32_t)min((uint64_t)64, (uint64_t)n - b);
-            for (uint32_t p = 0; p < passes; ++p) hist_add_runs(h[wave][p], digit_rb<RB>(k[s], first_bit + RB * p), lane, nvalid);
+            for (uint32_t p = 0; p < passes; ++p)
+                hist_add_runs(h[COPIES == 1 ? 0 : wave][p], digit_rb<RB>(k[s], first_bit + RB * p), lane, nvalid);
         }
     }
     __syncthreads();
     uint32_t* mine = ghist + (size_t)(blockIdx.x % HIST_COPIES) * passes * R;
-    for (uint32_t i = threadIdx.x; i < passes * R; i += SORT_BLOCK) {
+    for (uint32_t i = threadIdx.x; i < passes * R; i += NT) {
         uint32_t c = 0;
 #pragma unroll
-        for (int w = 0; w < SORT_WAVES; ++w) c += (&h[w][0][0])[i];
+        for (int w = 0; w < COPIES; ++w) c += (&h[w][0][0])[i];
         if (c) atomicAdd(&mine[i], c);
     }
 }
@@ -535,9 +545,12 @@ static hipError_t sort_impl(const K* keys_in, const uint32_t* vals_in, K* keys_o
         // only adds atomics (16k keys per block starves short inputs).
         const uint32_t hist_blocks = (uint32_t)max((uint64_t)1, min((uint64_t)HIST_BLOCKS, ((uint64_t)n + 4095) / 4096));
         if constexpr (sizeof(K) == 4) {
-            if (rb == 9) sort_histogram_kernel<K, 9><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
-            else if (rb == 7) sort_histogram_kernel<K, 7><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
-            else sort_histogram_kernel<K, 8><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+            if (rb == 9)
+                sort_histogram_kernel<K, 9, HIST_NT, HIST_NT_ITEMS><<<hist_blocks, HIST_NT, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+            else if (rb == 7)
+                sort_histogram_kernel<K, 7, HIST_NT, HIST_NT_ITEMS><<<hist_blocks, HIST_NT, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
+            else
+                sort_histogram_kernel<K, 8, HIST_NT, HIST_NT_ITEMS><<<hist_blocks, HIST_NT, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
         } else {
             sort_histogram_kernel<K, 8><<<hist_blocks, SORT_BLOCK, 0, s>>>(keys_in, n, n_dev, first_bit, passes, ghist);
         }
