@@ -641,8 +641,11 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(ProjectArgs a) {
     __shared__ RowLds s_walk[PROJ_BLOCK / 64];
     const uint32_t lane = lane_id();
     RowLds& L = s_walk[threadIdx.x / 64];
-    walk_rows<false>(L, visible, bb, px, py, conic, power, 0u, 0u, 0u, a.tile_bw, nullptr, nullptr, 0u);
-    const uint32_t hits = L.acc[lane];
+    uint32_t hits = 0u;
+    if (__ballot(visible) != 0ull) {   // a wavefront without a visible splat skips the walk
+        walk_rows<false>(L, visible, bb, px, py, conic, power, 0u, 0u, 0u, a.tile_bw, nullptr, nullptr, 0u);
+        hits = L.acc[lane];
+    }
 
     if (g < a.num_splats) {
         a.opacities[g] = opac_out;
@@ -769,10 +772,15 @@ __global__ void __launch_bounds__(PROJ_BLOCK) emit_kernel(EmitArgs a) {
     if (big && cnt > 0) base = a.slot_base_g[g];
     __shared__ RowLds s_walk[PROJ_BLOCK / 64];
     RowLds& L = s_walk[threadIdx.x / 64];
-    // a splat's count bounds its slots; slots past the arena are dropped
-    walk_rows<true, FILTER>(L, cnt > 0, bb, px, py, conic, power, base, g, cnt, a.tile_bw, a.tiles, a.vals, a.capacity,
-                            CutFilter{a.cut, a.allow}, bin);
-    const uint32_t emitted = L.acc[lane];
+    // a splat's count bounds its slots; slots past the arena are dropped.  A
+    // wavefront with nothing to emit (most of the global-id blocks' ones)
+    // skips the walk and its per-lane setup (the walk is wavefront-local).
+    uint32_t emitted = 0u;
+    if (__ballot(cnt > 0) != 0ull) {
+        walk_rows<true, FILTER>(L, cnt > 0, bb, px, py, conic, power, base, g, cnt, a.tile_bw, a.tiles, a.vals,
+                                a.capacity, CutFilter{a.cut, a.allow}, bin);
+        emitted = L.acc[lane];
+    }
     const uint32_t sentinel = a.tile_bw * a.tile_bh;
     for (uint32_t k = emitted; k < cnt && base + k < a.capacity; ++k) {
         a.tiles[base + k] = sentinel;
