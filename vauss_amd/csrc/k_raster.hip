@@ -1051,10 +1051,13 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             // ray-plane terms su, sv, 1/q.z, and those (the only ones that can
             // be non-finite off the disk) are zeroed on such lanes, so each
             // gradient component is 0 there without a select of its own.
+            // The gradient terms below are not part of the replay: they take
+            // fused multiply-adds (the build contracts nothing by itself, so
+            // that the replay above rounds as the forward does), and the
+            // hardware reciprocal and square root (1 ulp) where the replay
+            // keeps IEEE division.
             const float z = contrib ? h.z : 0.0f;
             const float m = dist_depth_grad(z);
-            // gradient-only quotients and roots take the hardware reciprocal and
-            // square root (1 ulp); the replayed forward above keeps IEEE division
             const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
             const float Tk = T;
             const float vis = contrib ? ae * Tk : 0.0f;
@@ -1067,40 +1070,47 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             gs[11] = vis * vnz;
             const float ra = __builtin_amdgcn_rcpf(1.0f - ae);
             // this splat's channels at the pixel, dotted with the cotangent
-            const float cv = cl_r * vr + cl_g * vg + cl_b * vb + z * vz + nrm_x * vnx + nrm_y * vny + nrm_z * vnz +
-                             m * vdb + (m * m) * vdc;
-            const float dot_ = (Tk * cv - sv_rest) * ra;
-            const float v_ae = dot_ + vt * ra;
+            float cv = cl_r * vr;
+            cv = __builtin_fmaf(cl_g, vg, cv);
+            cv = __builtin_fmaf(cl_b, vb, cv);
+            cv = __builtin_fmaf(z, vz, cv);
+            cv = __builtin_fmaf(nrm_x, vnx, cv);
+            cv = __builtin_fmaf(nrm_y, vny, cv);
+            cv = __builtin_fmaf(nrm_z, vnz, cv);
+            cv = __builtin_fmaf(m, __builtin_fmaf(m, vdc, vdb), cv);
+            const float v_ae = __builtin_fmaf(vt, ra, __builtin_fmaf(Tk, cv, -sv_rest) * ra);
             const float v_alpha_c = SMOOTH ? v_ae * (w_cut + alpha * cutoff_weight_deriv(alpha)) : v_ae;
             const bool unsat = contrib && opac * G <= ALPHA_CAP;
             const float v_alpha = unsat ? v_alpha_c : 0.0f;
-            const float v_z = vis * (vz + (vdb + 2.0f * m * vdc) * dm_dz) + ((contrib && isect == med) ? vmed : 0.0f);
+            const float v_z = __builtin_fmaf(vis, __builtin_fmaf(__builtin_fmaf(m + m, vdc, vdb), dm_dz, vz), (contrib && isect == med) ? vmed : 0.0f);
             const float v_sigma = -alpha * v_alpha;
             gs[15] = v_alpha * G;
             const float su = contrib ? h.su : 0.0f, sv = contrib ? h.sv : 0.0f;
             const bool use_3d = h.s3d <= h.s2d;
-            const float v_su = (use_3d ? v_sigma * su : 0.0f) + v_z * r2x;
-            const float v_sv = (use_3d ? v_sigma * sv : 0.0f) + v_z * r2y;
-            const float v_cx = use_3d ? 0.0f : -2.0f * v_sigma * h.dxs;
-            const float v_cy = use_3d ? 0.0f : -2.0f * v_sigma * h.dys;
+            const float v_su = __builtin_fmaf(v_z, r2x, use_3d ? v_sigma * su : 0.0f);
+            const float v_sv = __builtin_fmaf(v_z, r2y, use_3d ? v_sigma * sv : 0.0f);
+            const float v_s2 = use_3d ? 0.0f : -2.0f * v_sigma;
+            const float v_cx = v_s2 * h.dxs, v_cy = v_s2 * h.dys;
             const float inv_qz = contrib ? __builtin_amdgcn_rcpf(h.qz) : 0.0f;
-            const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -(v_su * su + v_sv * sv) * inv_qz;
+            const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -__builtin_fmaf(v_su, su, v_sv * sv) * inv_qz;
             // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
-            const float vhux = h.hvy * vqz - h.hvz * vqy, vhuy = h.hvz * vqx - h.hvx * vqz, vhuz = h.hvx * vqy - h.hvy * vqx;
-            const float vhvx = vqy * h.huz - vqz * h.huy, vhvy = vqz * h.hux - vqx * h.huz, vhvz = vqx * h.huy - vqy * h.hux;
-            const float g0 = vhux, g1 = vhuy, g2 = vhuz + v_cx * inv_r2z;
-            const float g3 = vhvx, g4 = vhvy, g5 = vhvz + v_cy * inv_r2z;
+            const float vhux = __builtin_fmaf(h.hvy, vqz, -(h.hvz * vqy)), vhuy = __builtin_fmaf(h.hvz, vqx, -(h.hvx * vqz));
+            const float vhuz = __builtin_fmaf(h.hvx, vqy, -(h.hvy * vqx));
+            const float vhvx = __builtin_fmaf(vqy, h.huz, -(vqz * h.huy)), vhvy = __builtin_fmaf(vqz, h.hux, -(vqx * h.huz));
+            const float vhvz = __builtin_fmaf(vqx, h.huy, -(vqy * h.hux));
+            const float g0 = vhux, g1 = vhuy, g2 = __builtin_fmaf(v_cx, inv_r2z, vhuz);
+            const float g3 = vhvx, g4 = vhvy, g5 = __builtin_fmaf(v_cy, inv_r2z, vhvz);
             gs[0] = g0; gs[1] = g1; gs[2] = g2; gs[3] = g3; gs[4] = g4; gs[5] = g5;
-            gs[6] = v_z * su - pcx * vhux - pcy * vhvx;
-            gs[7] = v_z * sv - pcx * vhuy - pcy * vhvy;
-            gs[8] = v_z - pcx * vhuz - pcy * vhvz - (v_cx * cen_x + v_cy * cen_y) * inv_r2z;
+            gs[6] = __builtin_fmaf(v_z, su, -__builtin_fmaf(pcx, vhux, pcy * vhvx));
+            gs[7] = __builtin_fmaf(v_z, sv, -__builtin_fmaf(pcx, vhuy, pcy * vhvy));
+            gs[8] = v_z - __builtin_fmaf(pcx, vhuz, __builtin_fmaf(pcy, vhvz, __builtin_fmaf(v_cx, cen_x, v_cy * cen_y) * inv_r2z));
             // refine weight: this pixel's gradient of a screen-space shift of the surfel (M -> T M)
-            const float shx = g0 * r2x + g1 * r2y + g2 * r2z;
-            const float shy = g3 * r2x + g4 * r2y + g5 * r2z;
+            const float shx = __builtin_fmaf(g0, r2x, __builtin_fmaf(g1, r2y, g2 * r2z));
+            const float shy = __builtin_fmaf(g3, r2x, __builtin_fmaf(g4, r2y, g5 * r2z));
             const float ux = shx * img_w, uy = shy * img_h;
-            gs[16] = __builtin_amdgcn_sqrtf(ux * ux + uy * uy) * rscale;
+            gs[16] = __builtin_amdgcn_sqrtf(__builtin_fmaf(ux, ux, uy * uy)) * rscale;
             if (contrib) {
-                sv_rest -= vis * cv;
+                sv_rest = __builtin_fmaf(-vis, cv, sv_rest);
                 T = nt;
             }
             float mine = reduce_scatter17(gs, lane);
