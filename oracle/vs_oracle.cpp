@@ -934,23 +934,24 @@ static V3 surfel_normal(Q4 q, V3 mc, const or_camera& u) {
 // false when the ray misses or meets the plane before the near limit.  The
 // quotients q.x / q.z and q.y / q.z are taken as products with the correctly
 // rounded 1 / q.z (one division for both; each within one rounding of the
-// quotient), as the kernels do.
+// quotient), and the products that feed a sum or a difference are fused
+// multiply-adds where written, as the kernels do.
 struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
 static SurfelHit surfel_hit(const float* a, float px, float py) {
     SurfelHit h;
     const float m20 = a[6], m21 = a[7], m22 = a[8];
-    h.hux = a[0] - px * m20; h.huy = a[1] - px * m21; h.huz = a[2] - px * m22;
-    h.hvx = a[3] - py * m20; h.hvy = a[4] - py * m21; h.hvz = a[5] - py * m22;
-    const float qx = h.huy * h.hvz - h.huz * h.hvy;
-    const float qy = h.huz * h.hvx - h.hux * h.hvz;
-    h.qz = h.hux * h.hvy - h.huy * h.hvx;
+    h.hux = std::fmaf(-px, m20, a[0]); h.huy = std::fmaf(-px, m21, a[1]); h.huz = std::fmaf(-px, m22, a[2]);
+    h.hvx = std::fmaf(-py, m20, a[3]); h.hvy = std::fmaf(-py, m21, a[4]); h.hvz = std::fmaf(-py, m22, a[5]);
+    const float qx = std::fmaf(h.huy, h.hvz, -(h.huz * h.hvy));
+    const float qy = std::fmaf(h.huz, h.hvx, -(h.hux * h.hvz));
+    h.qz = std::fmaf(h.hux, h.hvy, -(h.huy * h.hvx));
     const float rq = 1.0f / h.qz;
     h.su = qx * rq;
     h.sv = qy * rq;
-    h.s3d = h.su * h.su + h.sv * h.sv;
-    h.z = m20 * h.su + m21 * h.sv + m22;
+    h.s3d = std::fmaf(h.su, h.su, h.sv * h.sv);
+    h.z = std::fmaf(m20, h.su, std::fmaf(m21, h.sv, m22));
     h.dxs = px - a[9]; h.dys = py - a[10];
-    h.s2d = 2.0f * (h.dxs * h.dxs + h.dys * h.dys);
+    h.s2d = 2.0f * std::fmaf(h.dxs, h.dxs, h.dys * h.dys);
     h.sigma = 0.5f * fmin_(h.s3d, h.s2d);
     h.valid = is_finite(h.z) && h.z >= SURFEL_NEAR;
     return h;

@@ -82,25 +82,28 @@ struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, su, sv, s3d, z, dxs, 
 // computed and such a pixel is marked invalid all the same.
 template <bool EARLY = true>
 VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float px, float py) {
+    // Fused multiply-adds where written (the oracle fuses the same ones; each
+    // rounds once where the unfused form rounded twice, so the culling's
+    // rounding bounds on q still hold).
     SurfelHit h;
     const float m20 = m1.z, m21 = m1.w, m22 = m2.x;
-    h.hux = m0.x - px * m20; h.huy = m0.y - px * m21; h.huz = m0.z - px * m22;
-    h.hvx = m0.w - py * m20; h.hvy = m1.x - py * m21; h.hvz = m1.y - py * m22;
-    const float qx = h.huy * h.hvz - h.huz * h.hvy;
-    const float qy = h.huz * h.hvx - h.hux * h.hvz;
-    h.qz = h.hux * h.hvy - h.huy * h.hvx;
+    h.hux = __builtin_fmaf(-px, m20, m0.x); h.huy = __builtin_fmaf(-px, m21, m0.y); h.huz = __builtin_fmaf(-px, m22, m0.z);
+    h.hvx = __builtin_fmaf(-py, m20, m0.w); h.hvy = __builtin_fmaf(-py, m21, m1.x); h.hvz = __builtin_fmaf(-py, m22, m1.y);
+    const float qx = __builtin_fmaf(h.huy, h.hvz, -(h.huz * h.hvy));
+    const float qy = __builtin_fmaf(h.huz, h.hvx, -(h.hux * h.hvz));
+    h.qz = __builtin_fmaf(h.hux, h.hvy, -(h.huy * h.hvx));
     h.dxs = px - m2.y;
     h.dys = py - m2.z;
-    h.s2d = 2.0f * (h.dxs * h.dxs + h.dys * h.dys);
+    h.s2d = 2.0f * __builtin_fmaf(h.dxs, h.dxs, h.dys * h.dys);
     h.valid = false;
-    const bool far = 0.5f * h.s2d > smax && qx * qx + qy * qy > (2.0004f * smax) * (h.qz * h.qz);
+    const bool far = 0.5f * h.s2d > smax && __builtin_fmaf(qx, qx, qy * qy) > (2.0004f * smax) * (h.qz * h.qz);
     if (EARLY && far) return h;
     // the quotients as products with the correctly rounded 1 / q.z (the oracle's form)
     const float rq = 1.0f / h.qz;
     h.su = qx * rq;
     h.sv = qy * rq;
-    h.s3d = h.su * h.su + h.sv * h.sv;
-    h.z = m20 * h.su + m21 * h.sv + m22;
+    h.s3d = __builtin_fmaf(h.su, h.su, h.sv * h.sv);
+    h.z = __builtin_fmaf(m20, h.su, __builtin_fmaf(m21, h.sv, m22));
     h.sigma = 0.5f * mn(h.s3d, h.s2d);
     h.valid = !far && finite(h.z) && h.z >= SURFEL_NEAR;
     return h;
