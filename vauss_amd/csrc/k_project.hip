@@ -79,9 +79,11 @@ VS_DEV uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_rea
 //     spare, while the test evaluates sigma at a point of the tile (within
 //     5e-4 px of it) in f32, within 5 ulp x (1 + rho) / (1 - rho) = 1.3e-3
 //     relative for the conics admitted below (rho = |c01| / sqrt(c00 c11));
-//   * tiles inside an interior range, which it must pass: they lie inside
-//     sigma <= P (1 - 4e-3) - 1e-4 with 0.05 px to spare;
-//   * the rest, on which will_contribute runs as the reference's does.
+//   * tiles inside an interior (certain) range, which it must pass: each
+//     holds, 0.05 px inside its edges, a point with sigma <= P (1 - 4e-3)
+//     - 1e-4 (the range spans the x extent of that ellipse over the row);
+//   * the rest, on which will_contribute runs as the reference's does: at
+//     most a tile or two at each end of a row.
 // Conics with c01^2 > 0.999 c00 c11 (f32 sigma too inexact to rely on) test
 // every tile of the box.  All of it is load-balanced over the wavefront: its
 // box rows are laid end to end and walked 64 at a time, and each step's
@@ -202,8 +204,10 @@ VS_DEV void row_interior(float px, float py, S2 cf, double P, uint32_t ty, uint3
 }
 
 // The per-splat terms of the row ranges, formed once per splat and handed to
-// the lanes that walk its rows.
-struct RangeK { double det, inva, two_a_pout, ey, kx, two_a_pin; };
+// the lanes that walk its rows: the outer ellipse sigma <= p_out (y extent ey,
+// leftmost point at dy = kx) and the inner one sigma <= p_in (ey_in, kx_in;
+// NaN when p_in <= 0: no certain tiles).
+struct RangeK { double det, inva, two_a_pout, ey, kx, two_a_pin, ey_in, kx_in; };
 VS_DEV RangeK range_consts(S2 cf, float power) {
     const double a = cf.c00, b = cf.c01, c = cf.c11, P = power;
     RangeK k;
@@ -216,12 +220,17 @@ VS_DEV RangeK range_consts(S2 cf, float power) {
     k.kx = b * ex / c;                  // -b ex / c is its exact negation
     const double p_in = P * 0.996 - 1e-4;
     k.two_a_pin = (p_in > 0.0) ? 2.0 * a * p_in : __builtin_nan("");   // NaN: no interior chord
+    // both ellipses share their axes: the inner extents are the outer ones
+    // scaled by sqrt(p_in / p_out)
+    const double s_in = sqrt(p_in / p_out);
+    k.ey_in = k.ey * s_in;
+    k.kx_in = k.kx * s_in;
     return k;
 }
 VS_DEV RangeK shfl_k(const RangeK& k, uint32_t src) {
     const int s = (int)src;
     return RangeK{__shfl(k.det, s), __shfl(k.inva, s), __shfl(k.two_a_pout, s), __shfl(k.ey, s), __shfl(k.kx, s),
-                  __shfl(k.two_a_pin, s)};
+                  __shfl(k.two_a_pin, s), __shfl(k.ey_in, s), __shfl(k.kx_in, s)};
 }
 
 // Tile-x ranges of row ty of a splat's box: [oa, ob) may pass, [ia, ib) must
@@ -242,12 +251,23 @@ VS_DEV void row_ranges_k(float px, float py, double b, const RangeK& k, uint4 bo
     oa = (uint32_t)fmin(fmax(fo, (double)x0), (double)x1);
     ob = (uint32_t)fmin(fmax(fe, (double)oa), (double)x1);
     ia = ib = ob;
-    // the interior range (row_interior)
-    const double e0 = (double)(ty * TILE_W) - my_ - BAND_IN, e1 = e0 + (double)TILE_W + 2.0 * BAND_IN;
-    double l0, r0, l1, r1;
-    if (!chord(0.0, b, k.det, k.inva, k.two_a_pin, e0, l0, r0) || !chord(0.0, b, k.det, k.inva, k.two_a_pin, e1, l1, r1))
-        return;
-    const double fi = ceil((mx_ + fmax(l0, l1) + BAND_IN) / TILE_W), fj = floor((mx_ + fmin(r0, r1) - BAND_IN) / TILE_W);
+    // The certain range: tiles whose x span overlaps, by BAND_IN, the x extent
+    // of the inner ellipse over the row band shrunk by BAND_IN.  The ellipse
+    // meets the band in a convex set, so each such tile holds a point of the
+    // band with sigma <= p_in, and the exact minimum of sigma over the tile
+    // (which the StopThePop test evaluates) is no larger: the test passes with
+    // the p_in margin (0.4 % of sigma + 1e-4, 0.05 px) to spare against its f32
+    // rounding, as for a tile wholly inside.  The leftmost point of the set is
+    // at dy = kx_in clamped to the band (the left chord end is convex in dy),
+    // the rightmost at -kx_in.
+    const double f0 = (double)(ty * TILE_W) - my_ + BAND_IN, f1 = f0 + (double)TILE_W - 2.0 * BAND_IN;
+    const double lo_i = fmax(f0, -k.ey_in), hi_i = fmin(f1, k.ey_in);
+    if (!(lo_i <= hi_i)) return;
+    double li, ri;
+    if (!chord(0.0, b, k.det, k.inva, k.two_a_pin, fmin(fmax(k.kx_in, lo_i), hi_i), li, t) ||
+        !chord(0.0, b, k.det, k.inva, k.two_a_pin, fmin(fmax(-k.kx_in, lo_i), hi_i), t, ri))
+        return;   // also for a NaN inner ellipse (p_in <= 0)
+    const double fi = floor((mx_ + li + BAND_IN) / TILE_W), fj = ceil((mx_ + ri - BAND_IN) / TILE_W);
     const double ci = fmin(fmax(fi, (double)oa), (double)ob), cj = fmin(fmax(fj, (double)oa), (double)ob);
     if (ci < cj) { ia = (uint32_t)ci; ib = (uint32_t)cj; }
 }
