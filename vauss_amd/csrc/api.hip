@@ -810,7 +810,7 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
     }
     const uint32_t I = st->I, M = st->M;
     // Depth cutoff (gaussian modes): per-tile tables of (bh x CUT_BINS x (bw + 1))
-    // u32 masses and u16 prefix counts, at most 256 MiB.
+    // u32 masses (then their sums over rows) and u16 prefix counts, at most 256 MiB.
     const uint64_t cut_words = (uint64_t)st->tbh * CUT_BINS * ((uint64_t)st->tbw + 1u);
     bool cutoff = false;
     if (!surfel && N > 0 && I > 0 && st->tbw <= CUT_MAX_BW && cut_words * 6u <= (256ull << 20) &&
@@ -868,14 +868,16 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
             ka.counts = st->counts; ka.depth_bits = st->depth_bits; ka.counters = st->counters;
             ka.proj = st->proj;
             ka.mass = cut_mass; ka.cut = cut_tile; ka.allow = cut_allow;
+            ka.sat = cut_mass;   // the masses are spent once the bins are known
             VS_HIP(launch_fill_u32(cut_mass, 0u, cut_words, s), "zero cutoff masses");
             VS_HIP(launch_cut_mass(ka, s), "cutoff masses");
             VS_HIP(launch_cut_rows(ka, s), "cutoff bins");
+            VS_HIP(launch_cut_sat(ka, s), "cutoff box counts");
             EmitArgs ca{};
             ca.num_splats = N; ca.tile_bw = st->tbw; ca.tile_bh = st->tbh;
             ca.counts = st->counts; ca.proj = st->proj;
             ca.cut = cut_tile; ca.allow = cut_allow; ca.depth_bits = st->depth_bits; ca.counters = st->counters;
-            ca.counts_out = st->kept_counts;
+            ca.counts_out = st->kept_counts; ca.sat = ka.sat;
             VS_HIP(launch_count_kept(ca, s), "cutoff counts");
         }
         const uint32_t* slot_counts = cutoff ? st->kept_counts : st->counts;

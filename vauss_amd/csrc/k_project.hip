@@ -944,7 +944,40 @@ __global__ void __launch_bounds__(CUT_ROW_BLOCK) cut_rows_kernel(CutArgs a) {
     }
 }
 
-// Per splat with tiles: the tiles it keeps under the cutoff (the emission's walk).
+// The kept-tile prefix counts summed over rows: sat[ty][b][x] = the tiles of
+// rows 0..ty left of column x that keep bin b.  One thread per (bin, column)
+// runs down the rows.
+constexpr int CUT_SAT_BLOCK = 256;
+__global__ void __launch_bounds__(CUT_SAT_BLOCK) cut_sat_kernel(CutArgs a) {
+    const uint32_t w1 = a.tile_bw + 1u;
+    const uint32_t i = blockIdx.x * CUT_SAT_BLOCK + threadIdx.x;
+    if (i >= CUT_BINS * w1) return;
+    const size_t stride = (size_t)CUT_BINS * w1;
+    const uint16_t* __restrict__ src = a.allow + i;   // (bin, column) i of row 0: [b * w1 + x]
+    uint32_t* __restrict__ dst = a.sat + i;
+    uint32_t sum = 0u;
+#pragma unroll 8
+    for (uint32_t y = 0; y < a.tile_bh; ++y) {
+        sum += src[y * stride];
+        dst[y * stride] = sum;
+    }
+}
+
+// Tiles of the box [x0, x1) x [y0, y1) that keep bin b (the box is not empty).
+VS_DEV uint32_t box_keeps(const uint32_t* sat, uint32_t tile_bw, TileBox bb, uint32_t b) {
+    const size_t w1 = (size_t)tile_bw + 1u;
+    const uint32_t* hi = sat + ((size_t)(bb.y1 - 1u) * CUT_BINS + b) * w1;
+    uint32_t k = hi[bb.x1] - hi[bb.x0];
+    if (bb.y0 > 0u) {
+        const uint32_t* lo = sat + ((size_t)(bb.y0 - 1u) * CUT_BINS + b) * w1;
+        k -= lo[bb.x1] - lo[bb.x0];
+    }
+    return k;
+}
+
+// Per splat with tiles: the tiles it keeps under the cutoff (the emission's
+// walk).  A splat whose box holds no tile keeping its depth bin (at C4 all
+// but a few thousand of the listed splats) keeps none, without a walk.
 __global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
     const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
     const uint32_t lane = lane_id();
@@ -953,6 +986,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
     S2 conic{0.0f, 0.0f, 0.0f};
     TileBox bb{0, 0, 0, 0};
     uint32_t bin = 0u;
+    bool has = false;
     if (cnt > 0) {
         const float4* row = a.proj + (size_t)g * PROJ_Q;
         const float4 pa = row[0];
@@ -963,12 +997,17 @@ __global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
         bbox_extent(conic, power, ex, ey);
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
         bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
+        has = bb.x1 > bb.x0 && bb.y1 > bb.y0 && box_keeps(a.sat, a.tile_bw, bb, bin) > 0u;
     }
-    __shared__ RowLds s_walk[PROJ_BLOCK / 64];
-    RowLds& L = s_walk[threadIdx.x / 64];
-    walk_rows<false, true>(L, cnt > 0, bb, px, py, conic, power, 0u, 0u, 0u, a.tile_bw, nullptr, nullptr, 0u,
-                           CutFilter{a.cut, a.allow}, bin);
-    if (g < a.num_splats) a.counts_out[g] = L.acc[lane];
+    uint32_t kept = 0u;
+    if (__ballot(has) != 0ull) {   // a wavefront with nothing to walk skips the walk
+        __shared__ RowLds s_walk[PROJ_BLOCK / 64];
+        RowLds& L = s_walk[threadIdx.x / 64];
+        walk_rows<false, true>(L, has, bb, px, py, conic, power, 0u, 0u, 0u, a.tile_bw, nullptr, nullptr, 0u,
+                               CutFilter{a.cut, a.allow}, bin);
+        kept = L.acc[lane];
+    }
+    if (g < a.num_splats) a.counts_out[g] = kept;
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n) {
@@ -1057,8 +1096,15 @@ hipError_t launch_cut_rows(const CutArgs& a, hipStream_t s) {
     cut_rows_kernel<<<a.tile_bh, CUT_ROW_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
+hipError_t launch_cut_sat(const CutArgs& a, hipStream_t s) {
+    if (a.tile_bh == 0 || a.tile_bw == 0) return hipSuccess;
+    const uint32_t cols = CUT_BINS * (a.tile_bw + 1u);
+    cut_sat_kernel<<<(cols + CUT_SAT_BLOCK - 1) / CUT_SAT_BLOCK, CUT_SAT_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
 hipError_t launch_count_kept(const EmitArgs& a, hipStream_t s) {
     if (a.num_splats == 0) return hipSuccess;
+    if (!a.sat) return hipErrorInvalidValue;
     count_kept_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }

@@ -108,6 +108,7 @@ struct EmitArgs {
     const uint32_t* depth_bits;      // [N] raw depth bits (the splat's bin)
     const uint32_t* counters;        // the projection's counters (depth range)
     uint32_t* counts_out;            // count pass: [N] tiles kept per splat
+    const uint32_t* sat;             // count pass: [bh][CUT_BINS][bw + 1] allow summed over rows 0..ty
     uint32_t* listed;                // emission: the list's length (slots the scan handed out), or null
 };
 
@@ -128,6 +129,7 @@ struct CutArgs {
     uint32_t* mass;                  // [bh][CUT_BINS][bw + 1] fixed-point mass differences along each row
     uint8_t* cut;                    // [T]
     uint16_t* allow;                 // [bh][CUT_BINS][bw + 1]
+    uint32_t* sat;                   // [bh][CUT_BINS][bw + 1] allow summed over rows 0..ty (may alias mass)
 };
 
 struct RasterArgs {
@@ -292,10 +294,12 @@ hipError_t launch_finalize_counts(uint32_t* block_stats, uint32_t nblocks, uint3
 hipError_t launch_compact(const CompactArgs& a, hipStream_t s);
 hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 // Depth cutoff: the opacity mass of every splat's core (mass zeroed by the
-// caller), each tile's cutoff bin and the rows' kept-tile prefix counts, then
-// each splat's kept tiles (EmitArgs: counts = the projection's, counts_out).
+// caller), each tile's cutoff bin and the rows' kept-tile prefix counts, their
+// sums over rows (sat, which may reuse the masses' memory), then each splat's
+// kept tiles (EmitArgs: counts = the projection's, counts_out, sat).
 hipError_t launch_cut_mass(const CutArgs& a, hipStream_t s);
 hipError_t launch_cut_rows(const CutArgs& a, hipStream_t s);
+hipError_t launch_cut_sat(const CutArgs& a, hipStream_t s);
 hipError_t launch_count_kept(const EmitArgs& a, hipStream_t s);
 hipError_t launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 hipError_t launch_fill_f32(float* p, float value, uint64_t n, hipStream_t s);
