@@ -434,7 +434,9 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
         const uint32_t gid = (l < rem) ? a.gids[start + l] : 0xFFFFFFFFu;
         bool live = false;
         __syncthreads();                              // the previous batch's LDS reads are complete
-        if constexpr (BWD) *reinterpret_cast<uint2*>(&s_hit[l]) = make_uint2(0u, 0u);
+        // whole 16-byte slots: lanes write consecutive addresses (a narrower
+        // store at the 16-byte stride puts eight lanes on each bank)
+        if constexpr (BWD) s_hit[l] = make_uint4(0u, 0u, 0u, 0u);
         if (gid < a.num_splats) {   // else: past the batch, or a corrupt id (dead slot)
             const float4* row = a.proj + (size_t)gid * PROJ_Q;
             const float4 pa = row[0];
@@ -446,7 +448,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             const float4 sb = make_float4((0.5f * pb.x) * LOG2E_F, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
             s_a[l] = sa;
             s_b[l] = sb;
-            s_c[l].x = mx(cb, 0.0f);
+            s_c[l] = make_float4(mx(cb, 0.0f), 0.0f, 0.0f, 0.0f);
             if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
             if constexpr (SURF) {
                 const float4* ps = a.proj_surf + (size_t)gid * 4;
@@ -572,7 +574,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             // only there), recorded per list entry for the backward.
             if (stop_off != 0xFFFFFFFFu) reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_hit) + stop_off)->y = 1u;
             __syncthreads();
-            const uint2 h = *reinterpret_cast<const uint2*>(&s_hit[l]);
+            const uint4 h = s_hit[l];
             const bool hit = gid < a.num_splats && h.x;
             if (hit) a.visible[gid] = 1.0f;
             if (l < rem && a.qpass) a.qpass[(size_t)(start + l) * 4 + q] = (h.x | h.y) ? (uint8_t)(1u << q) : (uint8_t)0u;
