@@ -67,11 +67,6 @@ __global__ void __launch_bounds__(256) tile_ranges_kernel(const uint32_t* __rest
 
 // DIST_NEAR / DIST_FAR depth map, kernels/helpers.rs:91-103.
 VS_DEV float dist_depth(float z) { return 100.0f / (100.0f - 0.2f) * (1.0f - 0.2f / mx(z, 0.2f)); }
-// The same map for the backward's gradient terms only, with the hardware
-// reciprocal (1 ulp) in place of the correctly rounded division.
-VS_DEV float dist_depth_grad(float z) {
-    return 100.0f / (100.0f - 0.2f) * (1.0f - 0.2f * __builtin_amdgcn_rcpf(mx(z, 0.2f)));
-}
 
 // Workgroups are dealt to the 8 XCDs round-robin; give XCD k the contiguous
 // band of tiles [k*per, (k+1)*per) so neighbouring tiles, which share most of
@@ -1059,8 +1054,12 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             // hardware reciprocal and square root (1 ulp) where the replay
             // keeps IEEE division.
             const float z = contrib ? h.z : 0.0f;
-            const float m = dist_depth_grad(z);
-            const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * __builtin_amdgcn_rcpf(z * z) : 0.0f;
+            // the distortion map and its slope from one hardware reciprocal
+            // r = 1 / max(z, 0.2) (1 ulp): m = K (1 - 0.2 r), dm/dz = 0.2 K r^2
+            // above z = 0.2 (m is flat below)
+            const float rz = __builtin_amdgcn_rcpf(mx(z, 0.2f));
+            const float m = 100.0f / (100.0f - 0.2f) * (1.0f - 0.2f * rz);
+            const float dm_dz = (z > 0.2f) ? (100.0f / (100.0f - 0.2f) * 0.2f) * (rz * rz) : 0.0f;
             const float Tk = T;
             const float vis = contrib ? ae * Tk : 0.0f;
             float gs[SURFEL_GRADS];
@@ -1093,7 +1092,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             const float v_sv = __builtin_fmaf(v_z, r2y, use_3d ? v_sigma * sv : 0.0f);
             const float v_s2 = use_3d ? 0.0f : -2.0f * v_sigma;
             const float v_cx = v_s2 * h.dxs, v_cy = v_s2 * h.dys;
-            const float inv_qz = contrib ? __builtin_amdgcn_rcpf(h.qz) : 0.0f;
+            const float inv_qz = contrib ? h.rq : 0.0f;   // the replay's 1 / q.z
             const float vqx = v_su * inv_qz, vqy = v_sv * inv_qz, vqz = -__builtin_fmaf(v_su, su, v_sv * sv) * inv_qz;
             // q = h_u x h_v: v_hu = h_v x v_q, v_hv = v_q x h_u
             const float vhux = __builtin_fmaf(h.hvy, vqz, -(h.hvz * vqy)), vhuy = __builtin_fmaf(h.hvz, vqx, -(h.hvx * vqz));

@@ -76,7 +76,7 @@ VS_DEV F3 surfel_normal(Qt q, F3 mc, const vs_camera& u) {
 // 2 smax q.z^2 with a 2e-4 margin, far above the few ulp of the divided
 // form) comes back invalid before the divisions: such a pair has alpha below
 // every cutoff, so skipping it changes no result.
-struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
+struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, rq, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
 // EARLY: a pixel far outside both the plane disk and the low-pass disk
 // returns at once (invalid, the other fields unset); otherwise every field is
 // computed and such a pixel is marked invalid all the same.
@@ -99,9 +99,9 @@ VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float p
     const bool far = 0.5f * h.s2d > smax && __builtin_fmaf(qx, qx, qy * qy) > (2.0004f * smax) * (h.qz * h.qz);
     if (EARLY && far) return h;
     // the quotients as products with the correctly rounded 1 / q.z (the oracle's form)
-    const float rq = 1.0f / h.qz;
-    h.su = qx * rq;
-    h.sv = qy * rq;
+    h.rq = 1.0f / h.qz;
+    h.su = qx * h.rq;
+    h.sv = qy * h.rq;
     h.s3d = __builtin_fmaf(h.su, h.su, h.sv * h.sv);
     h.z = __builtin_fmaf(m20, h.su, __builtin_fmaf(m21, h.sv, m22));
     h.sigma = 0.5f * mn(h.s3d, h.s2d);
