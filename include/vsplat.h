@@ -574,6 +574,18 @@ vs_status vs_stream_probe(vs_ctx* ctx, void* buf, uint64_t bytes, int32_t mode);
  * VS_ERR_INVALID when the range passes bit pattern 0xFFFFFFFF.  Stream-ordered. */
 vs_status vs_compositing_exp2(vs_ctx* ctx, uint32_t first_bits, uint64_t count, float* out);
 
+/* The raster kernels' refined quotient a / b, which must round as the
+ * division does (the surfel backward replays the forward's ray-plane sample
+ * with its 1 / q.z: a reciprocal refined in six instructions for
+ * 2^-100 <= |b| <= 2^100, the division for other b), for checking.  No counterpart in the reference.
+ * vs_raster_division: out[i] = the quotient for the f32 b whose bit pattern is
+ * bits[i], i < count (device arrays).  vs_raster_division_mismatches:
+ * *mismatches (device memory, one u64) = the number of the 2^32 bit patterns b
+ * at which the quotient and the IEEE division a / b differ (two NaNs agree).
+ * Stream-ordered. */
+vs_status vs_raster_division(vs_ctx* ctx, float a, const uint32_t* bits, uint64_t count, float* out);
+vs_status vs_raster_division_mismatches(vs_ctx* ctx, float a, uint64_t* mismatches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,8 @@ from .render import (  # noqa: F401
     Block8Moment, Context, ForwardState, FusedAdam, ProjectUpdateResult, RasterPass, RenderAux, RenderOutput,
     ShStepState, SplatGrads, SplatRenderMode, adam_bias_corrections, compositing_exp2, geo_decode, geo_encode, geo_zero_rows,
     l1_cotangent, pose_backward, prefix_sum, project_update, radix_argsort, radix_argsort_skip_low_with_count, radix_argsort_u64,
-    radix_argsort_with_count, render, render_backward, scan_in_place, sh_degree_from_coeffs, sh_step, unpack_rgba8,
+    radix_argsort_with_count, raster_division, raster_division_mismatches, render, render_backward, scan_in_place,
+    sh_degree_from_coeffs, sh_step, unpack_rgba8,
 )
 
 __all__ = [
@@ -28,6 +29,6 @@ __all__ = [
     "Context", "ForwardState", "FusedAdam", "ProjectUpdateResult", "RasterPass", "RenderAux", "RenderOutput",
     "SplatGrads", "SplatRenderMode", "VsError", "compositing_exp2", "geo_decode", "geo_encode", "geo_zero_rows", "l1_cotangent", "load",
     "pose_backward", "prefix_sum", "project_update", "radix_argsort", "radix_argsort_skip_low_with_count",
-    "radix_argsort_u64", "radix_argsort_with_count", "render", "render_backward", "scan_in_place",
+    "radix_argsort_u64", "radix_argsort_with_count", "raster_division", "raster_division_mismatches", "render", "render_backward", "scan_in_place",
     "sh_degree_from_coeffs", "unpack_rgba8",
 ]

@@ -146,6 +146,8 @@ SIGNATURES = {
     "vs_prefix_sum_u32": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]),
     "vs_stream_probe": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_int32]),
     "vs_compositing_exp2": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p]),
+    "vs_raster_division": (C.c_int, [C.c_void_p, C.c_float, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "vs_raster_division_mismatches": (C.c_int, [C.c_void_p, C.c_float, C.c_void_p]),
     "vs_render_forward_l1": (C.c_int, [C.c_void_p, C.POINTER(VsCamera), C.POINTER(VsSplats), C.c_uint32, C.c_uint32,
                                        C.POINTER(C.c_float), C.c_int, C.c_int, C.c_void_p, C.c_float, C.c_float,
                                        C.c_float, C.c_void_p, C.POINTER(VsFwdOut), C.POINTER(C.c_void_p)]),

@@ -1397,6 +1397,24 @@ extern "C" vs_status vs_compositing_exp2(vs_ctx* ctx, uint32_t first_bits, uint6
     return VS_OK;
 }
 
+extern "C" vs_status vs_raster_division(vs_ctx* ctx, float a, const uint32_t* bits, uint64_t count, float* out) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (count == 0) return VS_OK;
+    if (!bits || !out) return fail(VS_ERR_INVALID, "null buffer");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_division_values(a, bits, count, out, ctx->stream), "raster division");
+    return VS_OK;
+}
+
+extern "C" vs_status vs_raster_division_mismatches(vs_ctx* ctx, float a, uint64_t* mismatches) {
+    if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
+    if (!mismatches) return fail(VS_ERR_INVALID, "mismatches is null");
+    VS_HIP(hipSetDevice(ctx->device), "hipSetDevice");
+    VS_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(mismatches), 0u, 2u, ctx->stream), "zero mismatch count");
+    VS_HIP(launch_division_check(a, reinterpret_cast<unsigned long long*>(mismatches), ctx->stream), "raster division check");
+    return VS_OK;
+}
+
 extern "C" vs_status vs_prefix_sum_u32(vs_ctx* ctx, const uint32_t* in, uint32_t* out, uint32_t n) {
     if (!ctx) return fail(VS_ERR_INVALID, "ctx is null");
     if (n == 0) return VS_OK;

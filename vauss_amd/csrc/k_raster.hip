@@ -1032,7 +1032,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             // the replayed forward: which lanes blend this splat (every field of the
             // hit is computed, so the gradient below runs on every lane and one
             // select per component keeps the blending lanes' values)
-            const SurfelHit h = surfel_hit<false>(m0, m1, m2, m3.z, pcx, pcy);
+            const SurfelHit h = surfel_hit<false, true>(m0, m1, m2, m3.z, pcx, pcy);
             const float G = comp_exp2(-(h.sigma * LOG2E_F));
             const float alpha = __builtin_fminf(ALPHA_CAP, opac * G);
             const float w_cut = SMOOTH ? cutoff_weight(alpha) : ((alpha >= ALPHA_MID) ? 1.0f : 0.0f);
@@ -1256,6 +1256,42 @@ __global__ void __launch_bounds__(256) exp2_range_kernel(uint32_t first_bits, ui
     const uint64_t stride = (uint64_t)gridDim.x * 256u;
     for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < count; i += stride)
         out[i] = comp_exp2(__uint_as_float(first_bits + (uint32_t)i));
+}
+
+// out[i] = div_cr(a, b) for the f32 b whose bit pattern is bits[i].
+__global__ void __launch_bounds__(256) division_values_kernel(float a, const uint32_t* __restrict__ bits, uint64_t count,
+                                                              float* __restrict__ out) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < count; i += stride)
+        out[i] = div_cr(a, __uint_as_float(bits[i]));
+}
+// *mismatches += the bit patterns b, of all 2^32, at which div_cr(a, b) and the
+// division a / b differ (two NaNs agree); each thread takes 256 consecutive b.
+constexpr uint32_t DIV_CHECK_PER_THREAD = 256;
+__global__ void __launch_bounds__(256) division_check_kernel(float a, unsigned long long* __restrict__ mismatches) {
+    const uint64_t base = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * DIV_CHECK_PER_THREAD;
+    uint32_t bad = 0;
+    for (uint32_t k = 0; k < DIV_CHECK_PER_THREAD; ++k) {
+        const float b = __uint_as_float((uint32_t)(base + k));
+        const float x = div_cr(a, b), y = a / b;
+        bad += (__float_as_uint(x) != __float_as_uint(y) && !(x != x && y != y)) ? 1u : 0u;
+    }
+    uint32_t wave_bad = bad;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) wave_bad += (uint32_t)__shfl_xor((int)wave_bad, o);
+    if ((threadIdx.x & 63u) == 0u && wave_bad) atomicAdd(mismatches, (unsigned long long)wave_bad);
+}
+
+hipError_t launch_division_values(float a, const uint32_t* bits, uint64_t count, float* out, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>(16384u, (count + 255u) / 256u);
+    division_values_kernel<<<grid, 256, 0, s>>>(a, bits, count, out);
+    return hipGetLastError();
+}
+hipError_t launch_division_check(float a, unsigned long long* mismatches, hipStream_t s) {
+    // 2^32 patterns: 65536 blocks x 256 threads x 256 patterns
+    division_check_kernel<<<(uint32_t)((1ull << 32) / (256ull * DIV_CHECK_PER_THREAD)), 256, 0, s>>>(a, mismatches);
+    return hipGetLastError();
 }
 
 hipError_t launch_exp2_range(uint32_t first_bits, uint64_t count, float* out, hipStream_t s) {

@@ -68,6 +68,24 @@ VS_DEV float expf_c(float x) {
 constexpr float LOG2E_F = 1.44269502f;
 VS_DEV float comp_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// a / b with the IEEE division's result, in six instructions for the
+// divisors that matter: for 2^-100 <= |b| <= 2^100 the hardware reciprocal
+// (1 ulp), one Newton step on it and one remainder correction of a times it
+// (Markstein's sequence) give the correctly rounded quotient, for a = 1 and
+// a = 0.2 at every such b (all 2^32 bit patterns are compared with the
+// division by vs_raster_division_mismatches); any other b takes the
+// division itself.  The surfel backward's replay takes the ray-plane
+// sample's 1 / q.z from it (the forward divides: the range branch costs its
+// busier scalar unit more than the division).
+VS_DEV float div_cr(float a, float b) {
+    const float ab = __builtin_fabsf(b);
+    if (!(ab >= 0x1p-100f && ab <= 0x1p100f)) return a / b;
+    const float r0 = __builtin_amdgcn_rcpf(b);
+    const float r1 = __builtin_fmaf(__builtin_fmaf(-b, r0, 1.0f), r0, r0);
+    const float q0 = a * r1;
+    return __builtin_fmaf(__builtin_fmaf(-b, q0, a), r1, q0);
+}
+
 // log: m = x 2^-e in [sqrt(1/2), sqrt(2)), s = (m-1)/(m+1),
 // ln m = 2s + s^3 (2/3 + 2/5 s^2 + 2/7 s^4 + 2/9 s^6), ln x = e ln2 + ln m.
 VS_DEV float logf_c(float x) {

@@ -355,6 +355,10 @@ hipError_t launch_geo_zero_rows(uint32_t* words, const uint32_t* rows, uint32_t 
 hipError_t launch_stream_probe(void* buf, uint64_t bytes, int mode, uint32_t* sink, hipStream_t s);
 uint32_t calib_sink_words();
 hipError_t launch_exp2_range(uint32_t first_bits, uint64_t count, float* out, hipStream_t s);
+// div_cr's quotients for given divisor bit patterns, and its mismatches with
+// the division over all 2^32 divisors (mismatches zeroed by the caller).
+hipError_t launch_division_values(float a, const uint32_t* bits, uint64_t count, float* out, hipStream_t s);
+hipError_t launch_division_check(float a, unsigned long long* mismatches, hipStream_t s);
 hipError_t launch_l1_cotangent(const float* pred, uint32_t channels, const void* gt, bool packed, uint32_t w, uint32_t h,
                                float mcx, float mcy, float mr, float inv_count, float* v_out, hipStream_t s);
 hipError_t launch_loss_forward(const LossArgs& a, hipStream_t s);

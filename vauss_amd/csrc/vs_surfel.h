@@ -79,8 +79,10 @@ VS_DEV F3 surfel_normal(Qt q, F3 mc, const vs_camera& u) {
 struct SurfelHit { float hux, huy, huz, hvx, hvy, hvz, qz, rq, su, sv, s3d, z, dxs, dys, s2d, sigma; bool valid; };
 // EARLY: a pixel far outside both the plane disk and the low-pass disk
 // returns at once (invalid, the other fields unset); otherwise every field is
-// computed and such a pixel is marked invalid all the same.
-template <bool EARLY = true>
+// computed and such a pixel is marked invalid all the same.  REFINED: 1 / q.z
+// from div_cr (the same bits as the division; cheaper where the caller's
+// scalar unit has room for its range branch: the backward's replay).
+template <bool EARLY = true, bool REFINED = false>
 VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float px, float py) {
     // Fused multiply-adds where written (the oracle fuses the same ones; each
     // rounds once where the unfused form rounded twice, so the culling's
@@ -99,7 +101,7 @@ VS_DEV SurfelHit surfel_hit(float4 m0, float4 m1, float4 m2, float smax, float p
     const bool far = 0.5f * h.s2d > smax && __builtin_fmaf(qx, qx, qy * qy) > (2.0004f * smax) * (h.qz * h.qz);
     if (EARLY && far) return h;
     // the quotients as products with the correctly rounded 1 / q.z (the oracle's form)
-    h.rq = 1.0f / h.qz;
+    h.rq = REFINED ? div_cr(1.0f, h.qz) : 1.0f / h.qz;
     h.su = qx * h.rq;
     h.sv = qy * h.rq;
     h.s3d = __builtin_fmaf(h.su, h.su, h.sv * h.sv);

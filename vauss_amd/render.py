@@ -697,6 +697,30 @@ def compositing_exp2(first_bits: int, count: int, device=None) -> torch.Tensor:
     return out
 
 
+def raster_division(a: float, bits: torch.Tensor) -> torch.Tensor:
+    """The raster kernels' quotient a / b for the f32 divisors whose bit
+    patterns `bits` holds (a uint32 or int32 device tensor), as a float32
+    tensor (vs_raster_division)."""
+    b = bits.contiguous()
+    if b.dtype not in (torch.int32, torch.uint32) or not b.is_cuda:
+        raise ValueError("bits must be a 32-bit integer device tensor")
+    out = torch.empty(b.shape, dtype=torch.float32, device=b.device)
+    ctx = Context.get(b.device)
+    _lib.check(ctx.lib.vs_raster_division(ctx.handle, float(a), _ptr(b) if b.numel() else None, b.numel(),
+                                          _ptr(out) if b.numel() else None))
+    return out
+
+
+def raster_division_mismatches(a: float, device=None) -> int:
+    """How many of the 2^32 f32 divisors b give a raster-kernel quotient a / b
+    that differs from the IEEE division (vs_raster_division_mismatches)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    count = torch.zeros(1, dtype=torch.int64, device=dev)
+    ctx = Context.get(dev)
+    _lib.check(ctx.lib.vs_raster_division_mismatches(ctx.handle, float(a), _ptr(count)))
+    return int(count.item())
+
+
 def l1_cotangent(pred: torch.Tensor, gt: torch.Tensor, mask_center=(0.0, 0.0), mask_radius: float = 0.0) -> torch.Tensor:
     """d(mean L1 over rgb)/d pred for an [H,W,C] prediction and an [H,W,3]
     float32 target, or an [H,W] int32 packed RGBA8 target (the reference's
