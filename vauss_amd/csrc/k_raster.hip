@@ -391,7 +391,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
     __shared__ float4 s_b[FWD_BATCH];    // C, opacity, max(r,0), max(g,0)
     __shared__ float4 s_c[FWD_BATCH];    // max(b,0), -, -, -
     __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BATCH : 1];
-    __shared__ float4 s_s[SURF ? FWD_BATCH * 4 : 1];
+    __shared__ float4 s_s[SURF ? FWD_BATCH * 4 : 1];   // row k of slot t at s_s[k * FWD_BATCH + t]
     __shared__ uint4 s_hit[BWD ? FWD_BATCH : 1];   // .x = 1 once the slot blended a pixel, .y once it stopped one
     __shared__ __align__(16) uint32_t s_list[FWD_BATCH];   // live slots as byte offsets (slot * 16)
 
@@ -449,7 +449,7 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                 const float4* ps = a.proj_surf + (size_t)gid * 4;
                 float4 r[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) { r[k] = ps[k]; s_s[4 * l + k] = r[k]; }
+                for (int k = 0; k < 4; ++k) { r[k] = ps[k]; s_s[k * FWD_BATCH + l] = r[k]; }
                 live = surfel_quadrant_live(x0, y0, r[0], r[1], r[2], pb.y, SMOOTH);
             } else {
                 live = quadrant_live(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, pc.y, SMOOTH);
@@ -476,8 +476,8 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             float sigma, zs = 0.0f, G;
             bool valid = true;
             if constexpr (SURF) {
-                const float4* ss = reinterpret_cast<const float4*>(lds_s + off * 4u);
-                const SurfelHit hit = surfel_hit(ss[0], ss[1], ss[2], ss[3].z, pcx, pcy);
+                const float4* ss = reinterpret_cast<const float4*>(lds_s + off);
+                const SurfelHit hit = surfel_hit(ss[0], ss[FWD_BATCH], ss[2 * FWD_BATCH], ss[3 * FWD_BATCH].z, pcx, pcy);
                 valid = hit.valid;              // the ray misses the plane or meets it before the near limit
                 sigma = hit.sigma;
                 zs = hit.z;
@@ -509,8 +509,8 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                     if constexpr (GEOM) {
                         float4 d;
                         if constexpr (SURF) {
-                            const float4* ss = reinterpret_cast<const float4*>(lds_s + off * 4u);
-                            const float4 s2 = ss[2], s3 = ss[3];
+                            const float4* ss = reinterpret_cast<const float4*>(lds_s + off);
+                            const float4 s2 = ss[2 * FWD_BATCH], s3 = ss[3 * FWD_BATCH];
                             d = make_float4(zs, s2.w, s3.x, s3.y);
                         } else {
                             d = *reinterpret_cast<const float4*>(lds_d + off);
@@ -926,11 +926,15 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
 constexpr int SURF_BWD_BLOCK = 256;
 template <bool SMOOTH>
 __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(RasterBwdArgs a) {
-    __shared__ float4 s_s[BWD_BATCH * 4];   // M rows, centre, normal (vs_surfel.h layout)
+    __shared__ float4 s_s[BWD_BATCH * 4];   // M rows, centre, normal (vs_surfel.h layout): row k of splat t at
+                                            // s_s[k * BWD_BATCH + t], so each wavefront's staging store is consecutive
     __shared__ float4 s_b[BWD_BATCH];       // opacity, max(r, 0), max(g, 0), max(b, 0)
     __shared__ uint32_t s_gate[BWD_BATCH];  // bit c: colour channel c is >= 0 (its gradient passes the clamp)
     __shared__ uint32_t s_gid[BWD_BATCH];
     __shared__ float s_acc[BWD_BATCH * SURFEL_GRADS];
+    // per wavefront: whether any lane holds a nonzero cotangent / a pixel still
+    // running (a ballot and one barrier in place of a workgroup OR-reduction)
+    __shared__ uint4 s_any_cot, s_any_run;
 
     const uint32_t tile = block_tile(a.order, blockIdx.x, a.num_tiles);
     if (tile >= a.num_tiles) return;   // uniform: padding blocks of the XCD mapping
@@ -977,14 +981,27 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
     float sv_rest = sr * vr + sg * vg + sb * vb + sz * vz + snx * vnx + sny * vny + snz * vnz + sdb * vdb + sdc * vdc;
     // every gradient term is linear in the cotangent: a tile whose pixels all
     // have a zero one (outside a loss mask) adds nothing
-    if (!__syncthreads_or(cot ? 1 : 0)) return;
+    {
+        const bool w = __ballot(cot) != 0ull;
+        if (lane == 0) reinterpret_cast<uint32_t*>(&s_any_cot)[q] = w ? 1u : 0u;
+        __syncthreads();
+        const uint4 f = s_any_cot;
+        if ((f.x | f.y | f.z | f.w) == 0u) return;
+    }
     const int comp = (lane & 1u) ? -1 : scatter_component17(lane);   // the gradient component this lane adds
     const int gate_bit = (comp >= 12 && comp <= 14) ? comp - 12 : -1;  // rgb components: their clamp's gate
     for (uint32_t i = threadIdx.x; i < BWD_BATCH * SURFEL_GRADS; i += SURF_BWD_BLOCK) s_acc[i] = 0.0f;
 
     for (uint32_t start = lo; start < hi; start += BWD_BATCH) {
         // every pixel of the tile is done: the whole workgroup leaves together
-        if (!__syncthreads_or(T > T_STOP ? 1 : 0)) break;
+        // (the previous batch's reads of s_any_run are behind its two barriers)
+        {
+            const bool w = __ballot(T > T_STOP) != 0ull;
+            if (lane == 0) reinterpret_cast<uint32_t*>(&s_any_run)[q] = w ? 1u : 0u;
+            __syncthreads();
+            const uint4 f = s_any_run;
+            if ((f.x | f.y | f.z | f.w) == 0u) break;
+        }
         const uint32_t rem = min((uint32_t)BWD_BATCH, hi - start);
         // wavefront q stages row q of each splat's surfel record; wavefront 0 the rest
         if (lane < rem) {
@@ -992,7 +1009,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
             if (gid < a.num_splats) {
                 float4 row = a.proj_surf[(size_t)gid * 4 + q];
                 if (q == 3) row.w = 1.0f / a.proj_surf[(size_t)gid * 4 + 2].x;   // 1 / M[2][2] in the pad slot
-                s_s[4 * lane + q] = row;
+                s_s[q * BWD_BATCH + lane] = row;
                 if (q == 0) {
                     const float4 pb = a.proj[(size_t)gid * PROJ_Q + 1];
                     const float cb_ = a.proj[(size_t)gid * PROJ_Q + 2].x;
@@ -1001,7 +1018,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
                     s_gid[lane] = gid;
                 }
             } else {   // a corrupt id: zero opacity never reaches the cutoff
-                s_s[4 * lane + q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                s_s[q * BWD_BATCH + lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (q == 0) { s_b[lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f); s_gate[lane] = 0u; s_gid[lane] = 0u; }
             }
         }
@@ -1012,7 +1029,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
         bool live_t = false;
         if (lane < rem) {
             live_t = a.qpass ? ((a.qpass[start + lane] >> (8u * q)) & 0xFFu) != 0u
-                             : surfel_quadrant_live(x0, y0, s_s[4 * lane], s_s[4 * lane + 1], s_s[4 * lane + 2],
+                             : surfel_quadrant_live(x0, y0, s_s[lane], s_s[BWD_BATCH + lane], s_s[2 * BWD_BATCH + lane],
                                                     s_b[lane].x, SMOOTH);
         }
         uint64_t live = __ballot(live_t);
@@ -1020,7 +1037,7 @@ __global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(Raste
         while (live) {
             const uint32_t t = (uint32_t)__builtin_ctzll(live);
             live &= live - 1ull;
-            const float4 m0 = s_s[4 * t], m1 = s_s[4 * t + 1], m2 = s_s[4 * t + 2], m3 = s_s[4 * t + 3];
+            const float4 m0 = s_s[t], m1 = s_s[BWD_BATCH + t], m2 = s_s[2 * BWD_BATCH + t], m3 = s_s[3 * BWD_BATCH + t];
             const float4 cb = s_b[t];
             const float opac = cb.x, cl_r = cb.y, cl_g = cb.z, cl_b = cb.w;
             const float r2x = m1.z, r2y = m1.w, r2z = m2.x, cen_x = m2.y, cen_y = m2.z;
