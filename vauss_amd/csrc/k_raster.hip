@@ -387,9 +387,12 @@ template <bool BWD, bool GEOM, bool SMOOTH, bool SURF>
 __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
     // Every per-splat array has 16-byte slots, so one LDS address, the slot's
     // byte offset kept in the list, serves all reads of a splat.
-    __shared__ float4 s_a[FWD_BATCH];    // x, y, A, B (the conic in base-2 units)
+    // (surfels read neither the conic nor s_c: their blue channel rides in the
+    // pad word of the fourth surfel row, and the smaller LDS footprint lets a
+    // sixth wavefront onto each SIMD)
+    __shared__ float4 s_a[SURF ? 1 : FWD_BATCH];    // x, y, A, B (the conic in base-2 units)
     __shared__ float4 s_b[FWD_BATCH];    // C, opacity, max(r,0), max(g,0)
-    __shared__ float4 s_c[FWD_BATCH];    // max(b,0), -, -, -
+    __shared__ float4 s_c[SURF ? 1 : FWD_BATCH];    // max(b,0), -, -, -
     __shared__ float4 s_d[(GEOM && !SURF) ? FWD_BATCH : 1];
     __shared__ float4 s_s[SURF ? FWD_BATCH * 4 : 1];   // row k of slot t at s_s[k * FWD_BATCH + t]
     __shared__ uint4 s_hit[BWD ? FWD_BATCH : 1];   // .x = 1 once the slot blended a pixel, .y once it stopped one
@@ -441,15 +444,20 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
             // the conic in base-2 units: sigma log2 e comes out of the same fma chain
             const float4 sa = make_float4(pa.x, pa.y, (0.5f * pa.z) * LOG2E_F, pa.w * LOG2E_F);
             const float4 sb = make_float4((0.5f * pb.x) * LOG2E_F, pb.y, mx(pb.z, 0.0f), mx(pb.w, 0.0f));
-            s_a[l] = sa;
+            if constexpr (!SURF) {
+                s_a[l] = sa;
+                s_c[l] = make_float4(mx(cb, 0.0f), 0.0f, 0.0f, 0.0f);
+            }
             s_b[l] = sb;
-            s_c[l] = make_float4(mx(cb, 0.0f), 0.0f, 0.0f, 0.0f);
             if constexpr (GEOM && !SURF) s_d[l] = a.proj_aux[gid];
             if constexpr (SURF) {
                 const float4* ps = a.proj_surf + (size_t)gid * 4;
                 float4 r[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) { r[k] = ps[k]; s_s[k * FWD_BATCH + l] = r[k]; }
+                for (int k = 0; k < 4; ++k) r[k] = ps[k];
+                r[3].w = mx(cb, 0.0f);   // the pad word
+#pragma unroll
+                for (int k = 0; k < 4; ++k) s_s[k * FWD_BATCH + l] = r[k];
                 live = surfel_quadrant_live(x0, y0, r[0], r[1], r[2], pb.y, SMOOTH);
             } else {
                 live = quadrant_live(x0, y0, sa.x, sa.y, sa.z, sa.w, sb.x, pc.y, SMOOTH);
@@ -502,7 +510,8 @@ __global__ void __launch_bounds__(FWD_BATCH) raster_fwd_kernel(RasterArgs a) {
                 if (pass && !stop) {
                     if constexpr (BWD) reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_hit) + off)->x = 1u;
                     const float vis = ae * T;
-                    const float cbv = reinterpret_cast<const float4*>(lds_c + off)->x;
+                    const float cbv = SURF ? reinterpret_cast<const float4*>(lds_s + off)[3 * FWD_BATCH].w
+                                           : reinterpret_cast<const float4*>(lds_c + off)->x;
                     cr = __builtin_fmaf(sb.z, vis, cr);
                     cg = __builtin_fmaf(sb.w, vis, cg);
                     cb = __builtin_fmaf(cbv, vis, cb);
@@ -923,9 +932,12 @@ __global__ void __launch_bounds__(64) raster_bwd_kernel(RasterBwdArgs a) {
 // (reduce_scatter17) and adds the 17 wave sums into the batch's LDS
 // accumulator; after the batch the workgroup adds each splat's nonzero sums
 // to v_combined [N,17], one atomic per component and tile.
+// Six waves per SIMD (80 VGPRs, five values spilled) instead of the 89
+// registers' five: 1.61 -> 1.56 ms at C3 (the loop is issue-bound, and a
+// sixth wave hides more of its LDS and transcendental latency).
 constexpr int SURF_BWD_BLOCK = 256;
 template <bool SMOOTH>
-__global__ void __launch_bounds__(SURF_BWD_BLOCK) raster_bwd_surfel_kernel(RasterBwdArgs a) {
+__global__ void __launch_bounds__(SURF_BWD_BLOCK) __attribute__((amdgpu_waves_per_eu(6))) raster_bwd_surfel_kernel(RasterBwdArgs a) {
     __shared__ float4 s_s[BWD_BATCH * 4];   // M rows, centre, normal (vs_surfel.h layout): row k of splat t at
                                             // s_s[k * BWD_BATCH + t], so each wavefront's staging store is consecutive
     __shared__ float4 s_b[BWD_BATCH];       // opacity, max(r, 0), max(g, 0), max(b, 0)
