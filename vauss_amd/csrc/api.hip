@@ -833,6 +833,7 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
         const size_t o_mass = cutoff ? itake(cut_words * 4) : 0, o_allow = cutoff ? itake(cut_words * 2) : 0;
         const size_t o_cut = cutoff ? itake(T) : 0, o_kept = cutoff ? itake((size_t)N * 4) : 0;
         const size_t o_listed = cutoff ? itake(4) : 0;
+        const size_t o_pend = cutoff ? itake((size_t)st->tbh * ((size_t)st->tbw + 1u) * 4) : 0;
         // serves both sorts (the depth sort on 9-bit digits, the tile sort on tile_rb-bit ones)
         const uint32_t tile_rb = tile_radix_bits(tile_bits);
         const size_t o_tmp = itake(std::max(sort_tmp_bytes(I, false, tile_rb), sort_tmp_bytes(M, false, DEPTH_RADIX_BITS)));
@@ -869,8 +870,11 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
             ka.proj = st->proj;
             ka.mass = cut_mass; ka.cut = cut_tile; ka.allow = cut_allow;
             ka.sat = cut_mass;   // the masses are spent once the bins are known
+            ka.pend = reinterpret_cast<uint32_t*>(ib + o_pend);
             VS_HIP(launch_fill_u32(cut_mass, 0u, cut_words, s), "zero cutoff masses");
-            VS_HIP(launch_cut_mass(ka, s), "cutoff masses");
+            VS_HIP(launch_cut_mass(ka, false, s), "cutoff masses (front bins)");
+            VS_HIP(launch_cut_pending(ka, s), "cutoff pending tiles");
+            VS_HIP(launch_cut_mass(ka, true, s), "cutoff masses (back bins)");
             VS_HIP(launch_cut_rows(ka, s), "cutoff bins");
             VS_HIP(launch_cut_sat(ka, s), "cutoff box counts");
             EmitArgs ca{};

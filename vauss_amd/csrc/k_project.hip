@@ -838,6 +838,16 @@ constexpr uint32_t CUT_NEED = 38750;   // ceil((ln(1e4) + 0.25) * CUT_SCALE)
 // its depth bin, +m at the first interior tile, -m past the last (u32
 // arithmetic wraps; the prefix sums recover the masses; the row's entry bw
 // is never read).  A core narrower than a tile covers none.
+//
+// Two passes.  The front one adds the splats of bins < CUT_FRONT; a tile
+// whose masses over those bins reach CUT_NEED has its cutoff bin among them
+// (cut_pending_kernel marks the others pending).  The back one adds the
+// splats of later bins whose box holds a pending tile: a box without one
+// lies over tiles whose cutoff bins all precede the splat's bin, where its
+// mass would only raise bins past the cutoff, which decide nothing.  The
+// cutoff bins are those of every mass added (a heavy-tailed view 2560 x 1440
+// has every cutoff bin below 8 while all but 0.5 % of 2.7 M cores lie behind).
+template <bool BACK>
 __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
     const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
     const uint32_t lane = lane_id();
@@ -846,6 +856,10 @@ __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
     S2 cf{0.0f, 0.0f, 0.0f};
     uint32_t m = 0u, bin = 0u;
     TileBox bb{0, 0, 0, 0};
+    if (has) {
+        bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
+        has = BACK ? bin >= CUT_FRONT : bin < CUT_FRONT;
+    }
     if (has) {
         const float4 pa = a.proj[(size_t)g * PROJ_Q], pb = a.proj[(size_t)g * PROJ_Q + 1];
         px = pa.x; py = pa.y;
@@ -860,8 +874,17 @@ __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
             bbox_extent(cf, pc, ex, ey);
             has = ex >= 0.5f * TILE_W && ey >= 0.5f * TILE_W;
             bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
-            bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
         }
+    }
+    if (BACK && has) {
+        // summed over every row of the box: with an exit at the first pending
+        // row the loop's flag came out of the last iteration's compare, which
+        // clears it for lanes that left earlier
+        const size_t w1 = (size_t)a.tile_bw + 1u;
+        const uint32_t* p = a.pend + (size_t)bb.y0 * w1;
+        uint32_t k = 0u;
+        for (uint32_t y = bb.y0; y < bb.y1; ++y, p += w1) k += p[bb.x1] - p[bb.x0];
+        has = k > 0u;
     }
     __shared__ RowLds s_walk[PROJ_BLOCK / 64];
     RowLds& L = s_walk[threadIdx.x / 64];
@@ -886,6 +909,50 @@ __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
             if (ib < a.tile_bw) atomicAdd(&row[ib], 0u - w.x);
         }
     });
+}
+
+// After the front pass, one wavefront per tile row: each tile's masses over
+// the front bins (prefix sums of their difference rows, which stay as they
+// are) and
+// pend[ty][x] = the row's tiles left of x where they stay below CUT_NEED
+// (pend[ty][bw]: all of them).
+constexpr int CUT_PEND_BLOCK = 64;
+__global__ void __launch_bounds__(CUT_PEND_BLOCK) cut_pending_kernel(CutArgs a) {
+    const uint32_t ty = blockIdx.x, bw = a.tile_bw, lane = lane_id();
+    const size_t w1 = (size_t)bw + 1u;
+    const uint32_t* mrow = a.mass + (size_t)ty * CUT_BINS * w1;
+    uint32_t* p = a.pend + (size_t)ty * w1;
+    uint32_t carry[CUT_FRONT];
+#pragma unroll
+    for (uint32_t b = 0; b < CUT_FRONT; ++b) carry[b] = 0u;
+    uint32_t pc = 0u;
+    for (uint32_t x0 = 0; x0 < bw; x0 += 64) {
+        const uint32_t x = x0 + lane;
+        uint32_t v[CUT_FRONT];
+#pragma unroll
+        for (uint32_t b = 0; b < CUT_FRONT; ++b) v[b] = x < bw ? mrow[b * w1 + x] : 0u;
+        uint64_t cum = 0;
+#pragma unroll
+        for (uint32_t b = 0; b < CUT_FRONT; ++b) {
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_up(v[b], o);
+                if ((int)lane >= o) v[b] += t;
+            }
+            cum += v[b] + carry[b];
+            carry[b] += (uint32_t)__shfl((int)v[b], 63);
+        }
+        const uint32_t k = (x < bw && cum < CUT_NEED) ? 1u : 0u;
+        uint32_t c = k;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(c, o);
+            if ((int)lane >= o) c += t;
+        }
+        if (x < bw) p[x] = pc + c - k;
+        pc += (uint32_t)__shfl((int)c, 63);
+    }
+    if (lane == 0) p[bw] = pc;
 }
 
 // One workgroup per tile row: the masses per (bin, tile) by prefix sums of
@@ -1085,9 +1152,18 @@ hipError_t launch_emit(const EmitArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_cut_mass(const CutArgs& a, hipStream_t s) {
+hipError_t launch_cut_mass(const CutArgs& a, bool back, hipStream_t s) {
     if (a.num_splats == 0) return hipSuccess;
-    cut_mass_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
+    if (back && !a.pend) return hipErrorInvalidValue;
+    const uint32_t grid = (a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK;
+    if (back) cut_mass_kernel<true><<<grid, PROJ_BLOCK, 0, s>>>(a);
+    else cut_mass_kernel<false><<<grid, PROJ_BLOCK, 0, s>>>(a);
+    return hipGetLastError();
+}
+hipError_t launch_cut_pending(const CutArgs& a, hipStream_t s) {
+    if (a.tile_bh == 0 || a.tile_bw == 0) return hipSuccess;
+    if (a.tile_bw > CUT_MAX_BW || !a.pend) return hipErrorInvalidValue;
+    cut_pending_kernel<<<a.tile_bh, CUT_PEND_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
 hipError_t launch_cut_rows(const CutArgs& a, hipStream_t s) {

@@ -118,6 +118,7 @@ struct EmitArgs {
 // the tile's pixels and are not listed for it.
 constexpr uint32_t CUT_BINS = 64;         // depth bins, equal spans of the raw depth bits
 constexpr float CUT_SCALE = 4096.0f;      // fixed-point units per nat of -ln(1 - alpha)
+constexpr uint32_t CUT_FRONT = 16;        // front bins, whose masses every splat adds
 constexpr uint32_t CUT_MAX_BW = 4096;     // tile columns the row kernel holds in LDS
 constexpr uint32_t CUT_AUTO_PER_TILE = 2048;   // VS_CUTOFF_AUTO: listed pairs per tile that turn it on
 struct CutArgs {
@@ -130,6 +131,8 @@ struct CutArgs {
     uint8_t* cut;                    // [T]
     uint16_t* allow;                 // [bh][CUT_BINS][bw + 1]
     uint32_t* sat;                   // [bh][CUT_BINS][bw + 1] allow summed over rows 0..ty (may alias mass)
+    uint32_t* pend;                  // [bh][bw + 1] per row, the tiles left of x whose front bins' masses
+                                     // stay below the stopping mass
 };
 
 struct RasterArgs {
@@ -297,7 +300,10 @@ hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 // caller), each tile's cutoff bin and the rows' kept-tile prefix counts, their
 // sums over rows (sat, which may reuse the masses' memory), then each splat's
 // kept tiles (EmitArgs: counts = the projection's, counts_out, sat).
-hipError_t launch_cut_mass(const CutArgs& a, hipStream_t s);
+// back: the splats of bins >= CUT_FRONT whose box holds a pending tile
+// (a.pend from launch_cut_pending); otherwise the splats of the front bins
+hipError_t launch_cut_mass(const CutArgs& a, bool back, hipStream_t s);
+hipError_t launch_cut_pending(const CutArgs& a, hipStream_t s);
 hipError_t launch_cut_rows(const CutArgs& a, hipStream_t s);
 hipError_t launch_cut_sat(const CutArgs& a, hipStream_t s);
 hipError_t launch_count_kept(const EmitArgs& a, hipStream_t s);
