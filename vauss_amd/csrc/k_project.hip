@@ -370,8 +370,9 @@ VS_DEV void walk_rows(RowLds& L, bool has, TileBox bb, float px, float py, S2 cf
                 const uint4 w = L.word[rw.x];
                 const uint32_t k = rw2.z + is.idx;
                 uint32_t tx = rw.w + is.idx;
-                if (FILTER) {
-                    // the idx-th kept tile of [ia, ib): the first x with ar[x + 1] > ar[ia] + idx
+                if (FILTER && rw2.w != rw2.x - rw.w) {
+                    // the idx-th kept tile of [ia, ib) (a run that keeps every
+                    // tile needs no search): the first x with ar[x + 1] > ar[ia] + idx
                     const uint16_t* ar = cutf.allow + ((size_t)rw.y * CUT_BINS + w.w) * (tile_bw + 1u);
                     const uint32_t target = (uint32_t)ar[rw.w] + is.idx;
                     uint32_t lo = rw.w, hi = rw2.x - 1u;
