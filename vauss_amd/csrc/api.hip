@@ -834,6 +834,7 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
         const size_t o_cut = cutoff ? itake(T) : 0, o_kept = cutoff ? itake((size_t)N * 4) : 0;
         const size_t o_listed = cutoff ? itake(4) : 0;
         const size_t o_pend = cutoff ? itake((size_t)st->tbh * ((size_t)st->tbw + 1u) * 4) : 0;
+        const size_t o_kblk = cutoff ? itake((size_t)nblocks * 4) : 0;
         // serves both sorts (the depth sort on 9-bit digits, the tile sort on tile_rb-bit ones)
         const uint32_t tile_rb = tile_radix_bits(tile_bits);
         const size_t o_tmp = itake(std::max(sort_tmp_bytes(I, false, tile_rb), sort_tmp_bytes(M, false, DEPTH_RADIX_BITS)));
@@ -882,14 +883,20 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
             ca.counts = st->counts; ca.proj = st->proj;
             ca.cut = cut_tile; ca.allow = cut_allow; ca.depth_bits = st->depth_bits; ca.counters = st->counters;
             ca.counts_out = st->kept_counts; ca.sat = ka.sat;
+            ca.kept_blocks = reinterpret_cast<uint32_t*>(ib + o_kblk);
             VS_HIP(launch_count_kept(ca, s), "cutoff counts");
+            // the emitters are the splats that keep a pair: their count stays on the device
+            VS_HIP(launch_scan_blocks(ca.kept_blocks, nblocks, st->counters + CNT_KEPT, s), "cutoff emitter offsets");
+            m_dev = st->counters + CNT_KEPT;
         }
         const uint32_t* slot_counts = cutoff ? st->kept_counts : st->counts;
         {
             StageTimer tm(ctx, ST_EMIT);
             CompactArgs ca{};
-            ca.num_splats = N; ca.counts = st->counts; ca.depth_bits = st->depth_bits;
-            ca.block_offsets = st->block_stats + (size_t)BS_EMIT * nblocks; ca.counters = st->counters;
+            ca.num_splats = N; ca.counts = slot_counts; ca.depth_bits = st->depth_bits;
+            ca.block_offsets = cutoff ? reinterpret_cast<const uint32_t*>(ib + o_kblk)
+                                      : st->block_stats + (size_t)BS_EMIT * nblocks;
+            ca.counters = st->counters;
             ca.keys = dkeys; ca.vals = dvals;
             ca.zero = depth_zero.ptr; ca.zero_words = depth_zero.words;   // the depth sort's one-sweep state
             ca.zero2 = scan_tmp; ca.zero2_words = scan_lookback_status_words(M);   // the slot scan's status

@@ -1076,6 +1076,47 @@ __global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
         kept = L.acc[lane];
     }
     if (g < a.num_splats) a.counts_out[g] = kept;
+    // the block's splats that keep a pair: the compaction takes them alone
+    __shared__ uint32_t s_k[PROJ_BLOCK / 64];
+    const uint64_t km = __ballot(kept > 0u);
+    if (lane == 0) s_k[threadIdx.x / 64] = (uint32_t)__popcll(km);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int w = 0; w < PROJ_BLOCK / 64; ++w) t += s_k[w];
+        a.kept_blocks[blockIdx.x] = t;
+    }
+}
+
+// One workgroup: v[0, n) scanned in place (exclusive), the sum to *total.
+// Each thread scans a contiguous chunk after the workgroup's scan of the
+// chunk sums.
+constexpr int SCAN_BLOCKS_BLOCK = 1024;
+__global__ void __launch_bounds__(SCAN_BLOCKS_BLOCK) scan_blocks_kernel(uint32_t* v, uint32_t n, uint32_t* total) {
+    __shared__ uint32_t s_w[SCAN_BLOCKS_BLOCK / 64];
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t per = (n + SCAN_BLOCKS_BLOCK - 1) / SCAN_BLOCKS_BLOCK;
+    const uint32_t lo = (uint32_t)min((uint64_t)t * per, (uint64_t)n), hi = (uint32_t)min((uint64_t)lo + per, (uint64_t)n);
+    uint32_t sum = 0u;
+    for (uint32_t i = lo; i < hi; ++i) sum += v[i];
+    uint32_t incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = __shfl_up(incl, o);
+        if ((int)lane >= o) incl += u;
+    }
+    if (lane == 63u) s_w[wave] = incl;
+    __syncthreads();
+    uint32_t wbase = 0u;
+    for (uint32_t w = 0; w < wave; ++w) wbase += s_w[w];
+    uint32_t run = wbase + incl - sum;
+    for (uint32_t i = lo; i < hi; ++i) {
+        const uint32_t x = v[i];
+        v[i] = run;
+        run += x;
+    }
+    if (t == SCAN_BLOCKS_BLOCK - 1) *total = wbase + incl;
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, uint64_t n) {
@@ -1179,9 +1220,14 @@ hipError_t launch_cut_sat(const CutArgs& a, hipStream_t s) {
     cut_sat_kernel<<<(cols + CUT_SAT_BLOCK - 1) / CUT_SAT_BLOCK, CUT_SAT_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }
+hipError_t launch_scan_blocks(uint32_t* v, uint32_t n, uint32_t* total, hipStream_t s) {
+    if (!v || !total) return hipErrorInvalidValue;
+    scan_blocks_kernel<<<1, SCAN_BLOCKS_BLOCK, 0, s>>>(v, n, total);
+    return hipGetLastError();
+}
 hipError_t launch_count_kept(const EmitArgs& a, hipStream_t s) {
     if (a.num_splats == 0) return hipSuccess;
-    if (!a.sat) return hipErrorInvalidValue;
+    if (!a.sat || !a.kept_blocks) return hipErrorInvalidValue;
     count_kept_kernel<<<(a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK, PROJ_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }

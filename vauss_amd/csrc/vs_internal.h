@@ -17,6 +17,7 @@ enum : uint32_t {
     CNT_EMITTERS = 3,     // splats that hit at least one tile
     CNT_ISECT64 = 4,      // words 4..5: total intersections as a u64
     CNT_BOUNDED = 6,      // min(total intersections, the arena's capacity): the pairs emitted
+    CNT_KEPT = 7,         // depth cutoff: splats keeping at least one pair (the emitters)
     CNT_COUNT = 8,
 };
 
@@ -109,6 +110,7 @@ struct EmitArgs {
     const uint32_t* counters;        // the projection's counters (depth range)
     uint32_t* counts_out;            // count pass: [N] tiles kept per splat
     const uint32_t* sat;             // count pass: [bh][CUT_BINS][bw + 1] allow summed over rows 0..ty
+    uint32_t* kept_blocks;           // count pass: [ceil(N / PROJ_BLOCK)] splats per block keeping a pair
     uint32_t* listed;                // emission: the list's length (slots the scan handed out), or null
 };
 
@@ -304,6 +306,8 @@ hipError_t launch_emit(const EmitArgs& a, hipStream_t s);
 // (a.pend from launch_cut_pending); otherwise the splats of the front bins
 hipError_t launch_cut_mass(const CutArgs& a, bool back, hipStream_t s);
 hipError_t launch_cut_pending(const CutArgs& a, hipStream_t s);
+// Exclusive scan of v[0, n) in place (one workgroup); *total = the sum.
+hipError_t launch_scan_blocks(uint32_t* v, uint32_t n, uint32_t* total, hipStream_t s);
 hipError_t launch_cut_rows(const CutArgs& a, hipStream_t s);
 hipError_t launch_cut_sat(const CutArgs& a, hipStream_t s);
 hipError_t launch_count_kept(const EmitArgs& a, hipStream_t s);
