@@ -835,6 +835,7 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
         const size_t o_listed = cutoff ? itake(4) : 0;
         const size_t o_pend = cutoff ? itake((size_t)st->tbh * ((size_t)st->tbw + 1u) * 4) : 0;
         const size_t o_kblk = cutoff ? itake((size_t)nblocks * 4) : 0;
+        const size_t o_ptot = cutoff ? itake(4) : 0;
         // serves both sorts (the depth sort on 9-bit digits, the tile sort on tile_rb-bit ones)
         const uint32_t tile_rb = tile_radix_bits(tile_bits);
         const size_t o_tmp = itake(std::max(sort_tmp_bytes(I, false, tile_rb), sort_tmp_bytes(M, false, DEPTH_RADIX_BITS)));
@@ -872,6 +873,7 @@ static vs_status render_forward(vs_ctx* ctx, const vs_camera* cam, const vs_spla
             ka.mass = cut_mass; ka.cut = cut_tile; ka.allow = cut_allow;
             ka.sat = cut_mass;   // the masses are spent once the bins are known
             ka.pend = reinterpret_cast<uint32_t*>(ib + o_pend);
+            ka.pend_total = reinterpret_cast<uint32_t*>(ib + o_ptot);
             VS_HIP(launch_fill_u32(cut_mass, 0u, cut_words, s), "zero cutoff masses");
             VS_HIP(launch_cut_mass(ka, false, s), "cutoff masses (front bins)");
             VS_HIP(launch_cut_pending(ka, s), "cutoff pending tiles");

@@ -852,6 +852,8 @@ template <bool BACK>
 __global__ void __launch_bounds__(PROJ_BLOCK) cut_mass_kernel(CutArgs a) {
     const uint32_t g = blockIdx.x * PROJ_BLOCK + threadIdx.x;
     const uint32_t lane = lane_id();
+    if (BACK && *a.pend_total == 0u) return;   // every cutoff bin lies among the front bins
+    if (!BACK && g == 0u) *a.pend_total = 0u;   // cut_pending_kernel sums it next
     bool has = g < a.num_splats && a.counts[g] > 0u;
     float px = 0.0f, py = 0.0f, pc = 0.0f;
     S2 cf{0.0f, 0.0f, 0.0f};
@@ -953,7 +955,10 @@ __global__ void __launch_bounds__(CUT_PEND_BLOCK) cut_pending_kernel(CutArgs a) 
         if (x < bw) p[x] = pc + c - k;
         pc += (uint32_t)__shfl((int)c, 63);
     }
-    if (lane == 0) p[bw] = pc;
+    if (lane == 0) {
+        p[bw] = pc;
+        if (pc) atomicAdd(a.pend_total, pc);
+    }
 }
 
 // One workgroup per tile row: the masses per (bin, tile) by prefix sums of
@@ -1056,6 +1061,13 @@ __global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
     uint32_t bin = 0u;
     bool has = false;
     if (cnt > 0) {
+        bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
+        // the image's tiles keeping the bin (the summed table's last row, past
+        // its last column): none, and the projected row is never read
+        const size_t w1 = (size_t)a.tile_bw + 1u;
+        has = a.sat[((size_t)(a.tile_bh - 1u) * CUT_BINS + bin) * w1 + a.tile_bw] > 0u;
+    }
+    if (has) {
         const float4* row = a.proj + (size_t)g * PROJ_Q;
         const float4 pa = row[0];
         px = pa.x; py = pa.y;
@@ -1064,7 +1076,6 @@ __global__ void __launch_bounds__(PROJ_BLOCK) count_kept_kernel(EmitArgs a) {
         float ex, ey;
         bbox_extent(conic, power, ex, ey);
         bb = tile_box(px, py, ex, ey, a.tile_bw, a.tile_bh);
-        bin = cut_bin(a.depth_bits[g], a.counters[CNT_DEPTH_MIN], a.counters[CNT_DEPTH_MAX]);
         has = bb.x1 > bb.x0 && bb.y1 > bb.y0 && box_keeps(a.sat, a.tile_bw, bb, bin) > 0u;
     }
     uint32_t kept = 0u;
@@ -1196,7 +1207,7 @@ hipError_t launch_emit(const EmitArgs& a, hipStream_t s) {
 
 hipError_t launch_cut_mass(const CutArgs& a, bool back, hipStream_t s) {
     if (a.num_splats == 0) return hipSuccess;
-    if (back && !a.pend) return hipErrorInvalidValue;
+    if (!a.pend_total || (back && !a.pend)) return hipErrorInvalidValue;
     const uint32_t grid = (a.num_splats + PROJ_BLOCK - 1) / PROJ_BLOCK;
     if (back) cut_mass_kernel<true><<<grid, PROJ_BLOCK, 0, s>>>(a);
     else cut_mass_kernel<false><<<grid, PROJ_BLOCK, 0, s>>>(a);
@@ -1204,7 +1215,7 @@ hipError_t launch_cut_mass(const CutArgs& a, bool back, hipStream_t s) {
 }
 hipError_t launch_cut_pending(const CutArgs& a, hipStream_t s) {
     if (a.tile_bh == 0 || a.tile_bw == 0) return hipSuccess;
-    if (a.tile_bw > CUT_MAX_BW || !a.pend) return hipErrorInvalidValue;
+    if (a.tile_bw > CUT_MAX_BW || !a.pend || !a.pend_total) return hipErrorInvalidValue;
     cut_pending_kernel<<<a.tile_bh, CUT_PEND_BLOCK, 0, s>>>(a);
     return hipGetLastError();
 }

@@ -135,6 +135,7 @@ struct CutArgs {
     uint32_t* sat;                   // [bh][CUT_BINS][bw + 1] allow summed over rows 0..ty (may alias mass)
     uint32_t* pend;                  // [bh][bw + 1] per row, the tiles left of x whose front bins' masses
                                      // stay below the stopping mass
+    uint32_t* pend_total;            // the tiles still short of it after the front bins (all rows)
 };
 
 struct RasterArgs {
